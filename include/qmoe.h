@@ -1,0 +1,173 @@
+/*
+ * qmoe — C ABI of the MI355X (gfx950) quantized-GEMM / fused-MoE library.
+ *
+ * Every entry point takes raw device pointers, sizes and a hipStream_t, is
+ * asynchronous on that stream, allocates nothing, and returns a status:
+ *   0 QMOE_OK, 1 QMOE_ERR_ARG (bad shape / unsupported combination),
+ *   2 QMOE_ERR_WORKSPACE (workspace too small), 3 QMOE_ERR_LAUNCH.
+ * Layouts (all row-major):
+ *   activations  [rows, K]            bf16 (uint16 bit patterns) or 1-byte codes
+ *   weights      [G][N][K]            N-major: each output channel's K contiguous
+ *                                     (e2m1: [G][N][K/2], low nibble = even k)
+ *   scales       per-channel f32 [G][N]; block f32 [G][N/bn][K/128];
+ *                MX e8m0 bytes [G][N][K/32]
+ * Reference paths below are relative to the reference plugin's
+ * src/vllm_torchtpu/.
+ */
+#ifndef QMOE_H_
+#define QMOE_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* qmoe_stream_t; /* == hipStream_t */
+
+/* GEMM kinds (qmoe_gemm_desc.kind) */
+enum {
+  QMOE_W8A8_PC = 0,  /* A e4m3|int8 + per-row f32 scale; W same dtype + per-channel f32 scale */
+  QMOE_W8A8_BLK = 1, /* A e4m3 + per-(row,128) scale; W e4m3 + per-(n/bn, 128) scale */
+  QMOE_W8A16_PC = 2, /* A bf16; W e4m3 + per-channel scale */
+  QMOE_W4A16_MX = 3, /* A bf16; W e2m1 + e8m0 scale per 32 k */
+  QMOE_W16A16 = 4    /* A bf16; W bf16 */
+};
+
+/* Fused gate/up activations (qmoe_gemm_desc.act) */
+enum {
+  QMOE_ACT_NONE = 0,
+  QMOE_ACT_SILU = 1,
+  QMOE_ACT_SWIGLUOAI = 2, /* p0 = alpha (1.702), p1 = limit (7.0) */
+  QMOE_ACT_GELU_TANH = 3,
+  QMOE_ACT_SILU_CLAMP = 4, /* p0 = limit (10.0) */
+  QMOE_ACT_SITU = 5        /* p0 = beta, p1 = linear_beta (<= 0: none) */
+};
+
+/*
+ * Grouped GEMM problem. For each group g (one group when group_offs is NULL)
+ * and compact row R in [group_offs[g], group_offs[g+1]):
+ *   acc[R, n] = sum_k A[a_rows ? a_rows[R] : R, k] * W[g, n, k]
+ *   v = scales(acc) (+ bias[g, n]); with act: out[n] = act(v[n], v[n + N/2])
+ *   out *= row_weight[R] (bf16, optional)
+ *   Y[y_rows ? y_rows[R] : R, n] = bf16(out)
+ */
+typedef struct qmoe_gemm_desc {
+  int32_t kind;           /* QMOE_W8A8_PC ... */
+  int32_t wfmt;           /* QMOE_W8A8_PC only: 0 e4m3, 1 int8 */
+  const void* a;          /* activation codes or bf16 */
+  int64_t lda;            /* elements */
+  const float* a_scale;   /* W8A8: [rows] or [rows, lds_a] */
+  int64_t lds_a;
+  const int32_t* a_rows;  /* optional gather map [M] */
+  const void* w;
+  int64_t ldw;            /* bytes per weight row */
+  int64_t w_gstride;      /* bytes per group */
+  const void* w_scale;
+  int64_t ldws;           /* elements per scale row */
+  int64_t ws_gstride;     /* elements per group */
+  int32_t ws_bn;          /* W8A8_BLK: weight rows per scale row (1 or 128) */
+  const float* bias;      /* optional [G, N] */
+  int64_t bias_gstride;
+  const int32_t* group_offs; /* optional [G+1] */
+  const int32_t* active;     /* optional slot -> group list (non-empty groups) */
+  const int32_t* num_active; /* device scalar, valid slots in `active` */
+  int32_t slots;          /* number of groups (or capacity of `active`) */
+  int32_t max_rows;       /* host bound on rows of any one group */
+  int32_t M;              /* total compact rows */
+  int32_t N;              /* weight rows (2*I with a fused activation) */
+  int32_t K;
+  int32_t act;
+  float act_p0, act_p1;
+  const uint16_t* row_weight; /* optional bf16 [M] */
+  void* y;                /* bf16 output */
+  int64_t ldy;
+  const int32_t* y_rows;  /* optional scatter map [M] */
+} qmoe_gemm_desc;
+
+/* ABI revision of this header (bumped on any layout change). */
+int qmoe_abi_version(void);
+
+/*
+ * Row quantizer: rows of x (bf16, or f32 when in_f32) -> 1-byte codes q and
+ * f32 scales (one per row, or per (row, 128 columns) when block == 128).
+ *   qdtype 0 e4m3fn, 1 int8.
+ *   mode 0: runtime activation quant, replaces the reference's
+ *           `kernels/quantized_matmul/util.py:47-64` quantize_tensor /
+ *           `:294-318` quantize_block (fp8 in f32, int8 in bf16 arithmetic);
+ *   mode 1: load-time weight quant, replaces
+ *           `layers/core/quantization.py:232-318` quantize_tensor
+ *           (reciprocal-multiply scale, zero rows keep scale 0).
+ */
+int qmoe_row_quant(const void* x, int64_t ldx, int in_f32, int64_t M, int64_t K, int qdtype,
+                   int mode, int block, void* q, int64_t ldq, float* scales, int64_t lds,
+                   qmoe_stream_t stream);
+
+/* Workspace bytes qmoe_gemm needs for this problem (split-K partials). */
+int qmoe_gemm_workspace_size(const qmoe_gemm_desc* d, int64_t* bytes);
+
+/*
+ * Quantized (grouped) GEMM. One group replaces the dense runtime matmul of
+ * `layers/adapter/linear_common.py:69-128` (_quantized_matmul_jax ->
+ * `kernels/quantized_matmul/util.py:80-124` xla_quantized_matmul, and the
+ * single-group gmm_v2 call for rank-4 scales) and `:188-209`
+ * (_quantized_matmul_fp4_jax). Several groups replace the grouped matmul
+ * `kernels/megablox/gmm_v2.py:1280-1443` (gmm_v2, incl. its fused
+ * activation epilogue `:84-122`). The workspace's first bytes are counters
+ * that must be zero before the first call; every call leaves them zero.
+ */
+int qmoe_gemm(const qmoe_gemm_desc* d, void* workspace, int64_t ws_bytes, qmoe_stream_t stream);
+
+/*
+ * MoE routing for T tokens over E experts: scores, top-k, renormalize and
+ * scale; weights written as bf16 (or f32 with weights_f32), ids int32 [T, k].
+ * Replaces `layers/adapter/moe_routing.py:232-323` (select_experts) with the
+ * sort-free top-k of `layers/core/rowmax_topk.py:28-61` (ties -> lowest id;
+ * a row with no score above -3e38 gets NaN weights and ids 0..k-1).
+ *   logits   : bf16 [T, E] (logits_f32 = 0) or f32 [T, E] (logits_f32 = 1)
+ *   scoring  : 0 softmax, 1 sigmoid, 2 sqrtsoftplus, 3 none (logits are the
+ *              scores: the reference's `layers/adapter/router_topk.py:42-50`
+ *              rowmax_select)
+ *   bias     : optional f32 [E] (choice = score + bias, weight = score)
+ *   num_group/topk_group > 1: grouped selection (sum of top-2 per group with
+ *   a bias, max without), the DeepSeek-V3 rule; upstream vLLM grouped_topk,
+ *   called at `moe_routing.py:276-299`.
+ */
+int qmoe_moe_route(const void* logits, int logits_f32, int64_t T, int E, int topk, int scoring,
+                   const float* bias, int renormalize, float routed_scaling_factor, int num_group,
+                   int topk_group, void* topk_weights, int weights_f32, int32_t* topk_ids,
+                   qmoe_stream_t stream);
+
+/*
+ * Token permutation by expert, replaces `layers/core/fused_moe_gmm.py:288-408`
+ * (prepare_routed_gmm_inputs, non-EP): stable order by (expert, flat route
+ * index t*k + slot); invalid routes (id < 0, or weight == 0 with
+ * skip_padded) sort last. Outputs (int32):
+ *   sorted_idx [T*k]  flat route index of each sorted row
+ *   revert     [T*k]  sorted position of each flat route (inverse permutation)
+ *   token_sorted [T*k] token of each sorted row (sorted_idx / k)
+ *   group_offs [E+1]  row offsets per expert (group_sizes = diff)
+ *   active     [min(E, T*k)] ids of experts with rows, ascending; num_active [1]
+ *   sorted_weight [T*k] bf16 routing weight of each sorted row
+ * One workgroup; histogram + exclusive scan + stable scatter in LDS.
+ */
+int qmoe_moe_dispatch(const int32_t* topk_ids, const uint16_t* topk_weights, int64_t T, int topk,
+                      int E, int skip_padded, int32_t* sorted_idx, int32_t* revert,
+                      int32_t* token_sorted, int32_t* group_offs, int32_t* active,
+                      int32_t* num_active, uint16_t* sorted_weight, qmoe_stream_t stream);
+
+/*
+ * Weighted unpermute, replaces `layers/core/fused_moe_gmm.py:572-577`:
+ * out[t] = bf16( sum over valid slots j of rows[t*k + j] ), where `rows`
+ * holds the already weighted down-projection rows in flat route order
+ * (written by qmoe_gemm with row_weight and y_rows = sorted_idx).
+ */
+int qmoe_moe_combine(const uint16_t* rows, const int32_t* topk_ids, const uint16_t* topk_weights,
+                     int64_t T, int topk, int64_t H, int skip_padded, uint16_t* out, int64_t ldo,
+                     qmoe_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QMOE_H_ */

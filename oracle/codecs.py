@@ -1,0 +1,145 @@
+"""Bit-level codecs: bf16 rounding, OCP e4m3fn, e2m1 (fp4), e8m0.
+
+Written from the format definitions (OCP 8-bit floating point spec v1.0 for
+E4M3 "fn"; OCP MX spec v1.0 for E2M1 and E8M0). Test infrastructure only.
+"""
+
+import numpy as np
+
+# ---------------------------------------------------------------- bfloat16
+
+
+def bf16_round(x) -> np.ndarray:
+    """Round float32 values to bfloat16 (round-to-nearest-even), return f32.
+
+    NaN stays NaN (quiet). This is the rounding every bf16 cast in the
+    reference performs (torch `.to(bfloat16)`, jnp `.astype(bfloat16)`).
+    """
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    u = x.view(np.uint32).astype(np.uint64)
+    lsb = (u >> 16) & 1
+    r = ((u + 0x7FFF + lsb) >> 16) << 16
+    out = r.astype(np.uint32).view(np.float32).copy()
+    nan = np.isnan(x)
+    if nan.any():
+        out[nan] = np.float32("nan")
+    return out
+
+
+def bf16_bits(x) -> np.ndarray:
+    """bf16 bit patterns (uint16) of float32 values after RNE rounding."""
+    r = bf16_round(x)
+    return (r.view(np.uint32) >> 16).astype(np.uint16)
+
+
+def bf16_from_bits(b) -> np.ndarray:
+    b = np.asarray(b, dtype=np.uint16).astype(np.uint32) << 16
+    return b.view(np.float32)
+
+
+# ---------------------------------------------------------------- e4m3fn
+
+E4M3_MAX = 448.0
+E4M3_NAN = 0x7F
+
+
+def e4m3_decode(codes) -> np.ndarray:
+    """uint8 e4m3fn codes -> float32 values (exact).
+
+    Layout S.EEEE.MMM, bias 7, no infinities, S.1111.111 is NaN.
+    """
+    c = np.asarray(codes, dtype=np.uint8).astype(np.int64)
+    s = np.where((c >> 7) & 1, -1.0, 1.0)
+    e = (c >> 3) & 0xF
+    m = c & 0x7
+    val = np.where(e == 0, m * 2.0 ** -9, (1.0 + m / 8.0) * np.exp2(e - 7.0))
+    val = s * val
+    val = np.where((e == 0xF) & (m == 0x7), np.nan, val)
+    return val.astype(np.float32)
+
+
+def e4m3_encode(x) -> np.ndarray:
+    """float32 -> uint8 e4m3fn codes, round-to-nearest-even.
+
+    Magnitudes that round above 448 and NaN inputs encode as NaN (0x7F/0xFF),
+    as torch's float8_e4m3fn cast does; every caller in the reference clips to
+    +-448 first, so only NaN reaches that branch on the hot path.
+    """
+    x = np.asarray(x, dtype=np.float32)
+    a = np.abs(x).astype(np.float64)
+    sign = np.signbit(x).astype(np.int64) << 7
+    _, ex = np.frexp(a)  # a = f * 2**ex, f in [0.5, 1)
+    e = ex.astype(np.int64) - 1  # a in [2**e, 2**(e+1))
+    e = np.maximum(e, -6)  # subnormal binade shares the 2**-9 quantum
+    q = np.exp2((e - 3).astype(np.float64))
+    r = np.rint(a / q)  # exact quotient (a is f32, q a power of 2); RNE
+    v = r * q  # the rounded magnitude, exactly representable
+    code = np.zeros(a.shape, dtype=np.int64)
+    nz = v > 0
+    _, ev = np.frexp(np.where(nz, v, 1.0))
+    ev = ev.astype(np.int64) - 1
+    sub = nz & (ev < -6)
+    code = np.where(sub, np.rint(v / 2.0 ** -9).astype(np.int64), code)
+    norm = nz & ~sub
+    mant = np.rint(v / np.exp2((ev - 3).astype(np.float64))).astype(np.int64) - 8
+    code = np.where(norm, ((ev + 7) << 3) | mant, code)
+    code = np.where(np.isnan(x) | (v > E4M3_MAX), E4M3_NAN, code)
+    return (code | sign).astype(np.uint8)
+
+
+# ---------------------------------------------------------------- e2m1 / e8m0
+
+# Value of each 4-bit e2m1 code: S.EE.M, bias 1; E==0 is subnormal (0, 0.5).
+FP4_VALUES = np.array(
+    [0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0,
+     -0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0],
+    dtype=np.float32,
+)
+
+
+def fp4_decode(nibbles) -> np.ndarray:
+    """4-bit codes -> float32 (`layers/core/quantization.py:145-175`)."""
+    return FP4_VALUES[np.asarray(nibbles, dtype=np.int64) & 0xF]
+
+
+def unpack_fp4(packed) -> np.ndarray:
+    """uint8 [..., K/2] -> 4-bit codes [..., K], low nibble first.
+
+    `layers/core/quantization.py:131-179` (`unpack_uint8_to_fp4`): element 2i
+    is the low nibble of byte i, element 2i+1 the high nibble.
+    """
+    p = np.asarray(packed, dtype=np.uint8)
+    lo = p & 0xF
+    hi = (p >> 4) & 0xF
+    return np.stack([lo, hi], axis=-1).reshape(*p.shape[:-1], -1)
+
+
+def pack_fp4(codes) -> np.ndarray:
+    """4-bit codes [..., K] -> uint8 [..., K/2] (`quantization.py:445-468`)."""
+    c = np.asarray(codes, dtype=np.uint8) & 0xF
+    c = c.reshape(*c.shape[:-1], -1, 2)
+    return (c[..., 0] | (c[..., 1] << 4)).astype(np.uint8)
+
+
+def e8m0_decode(u8) -> np.ndarray:
+    """e8m0 byte -> float32 2**(b-127) (`layers/core/quantization.py:105-128`).
+
+    The reference computes `ldexp(1, b-127)` in float32, so b == 255 gives
+    +inf (not NaN) and b == 0 gives the subnormal 2**-127.
+    """
+    b = np.asarray(u8, dtype=np.uint8).astype(np.int64)
+    return np.ldexp(np.float32(1.0), b - 127).astype(np.float32)
+
+
+def dequant_mxfp4(packed, scales_u8) -> np.ndarray:
+    """MXFP4 [N, K/2] codes + e8m0 [N, K/32] -> float32 [N, K].
+
+    `layers/core/quantization.py:321-345` (`dequantize_mxfp4_packed`): LUT
+    value times the block's power of two; every product is exact in f32.
+    """
+    vals = fp4_decode(unpack_fp4(packed))
+    s = e8m0_decode(scales_u8)
+    n, k = vals.shape[-2], vals.shape[-1]
+    blk = k // s.shape[-1]
+    out = vals.reshape(*vals.shape[:-1], s.shape[-1], blk) * s[..., None]
+    return out.reshape(*vals.shape[:-2], n, k).astype(np.float32)

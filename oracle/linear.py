@@ -1,0 +1,95 @@
+"""Dense quantized linear references (dequantize-then-matmul, fp32).
+
+Weights are held N-major ``[N, K]`` here (the checkpoint layout); the
+reference's runtime contraction over its K-major ``[K, N]`` copy computes the
+same sums. Test infrastructure only.
+"""
+
+import numpy as np
+
+from oracle.codecs import bf16_round, dequant_mxfp4, e4m3_decode
+from oracle.quant import dequant_codes, quantize_act
+
+
+def _mm(a, b_nk) -> np.ndarray:
+    """float32 [M, K] @ [N, K]^T with float32 accumulation (BLAS sgemm)."""
+    return np.matmul(np.asarray(a, np.float32), np.asarray(b_nk, np.float32).T)
+
+
+def w8a8_per_channel(x, wq, ws, qdtype):
+    """`kernels/quantized_matmul/util.py:80-124` (`xla_quantized_matmul`).
+
+    ``xq, sx = quantize_tensor(x)`` per token; ``dot(xq, wq)`` accumulated in
+    int32 (int8) or float32 (fp8); ``.astype(f32) * sx``; ``* ws[None, :]``;
+    cast to bf16. For int8 the integer dot is exact (computed in float64,
+    exact below 2**53), so the float32 epilogue, done in the reference's
+    operation order, reproduces the reference's output bit for bit.
+
+    Returns (y as bf16-valued f32 [M, N], xq, sx).
+    """
+    xq, sx = quantize_act(x, qdtype)
+    if qdtype == "int8":
+        acc = np.matmul(xq.astype(np.float64), np.asarray(wq, np.int8).astype(np.float64).T)
+        out = acc.astype(np.float32)
+    else:
+        out = _mm(e4m3_decode(xq), e4m3_decode(wq))
+    out = (out * sx[:, None]).astype(np.float32)
+    out = (out * np.asarray(ws, np.float32)[None, :]).astype(np.float32)
+    return bf16_round(out), xq, sx
+
+
+def w8a16_per_channel(x, wq, ws, qdtype="fp8"):
+    """`util.py:116-124` (``quantize_activation=False``): bf16 x times the
+    weight codes, f32 accumulation, ``* ws``, bf16 out."""
+    out = _mm(x, dequant_codes(wq, qdtype))
+    out = (out * np.asarray(ws, np.float32)[None, :]).astype(np.float32)
+    return bf16_round(out)
+
+
+def w8a8_blockwise(x, wq, ws_blocks, block=128):
+    """`tests/kernels/test_quantized_matmul_kernel.py:66-94`
+    (`reference_block_quantized_matmul`), the oracle of the blockwise kernel
+    `kernels/quantized_matmul/blockwise_kernel.py:197-247`.
+
+    x is quantized per (token, block) to e4m3 in float32 (`util.quantize_block`
+    on ``x.reshape(M, K/B, B)``); for each K block the f32 dot of codes is
+    multiplied by ``x_s`` and ``w_s`` and the blocks are summed.
+
+    ``ws_blocks`` is the per-(n, K-block) scale ``[N, K/B]`` (a 128x128 tile
+    scale repeated along N is the DeepSeek-V3 case). Returns (y, xq, xs).
+    """
+    m, k = x.shape
+    n = wq.shape[0]
+    xq, xs = quantize_act(x, "fp8", block=block)
+    xv = e4m3_decode(xq).reshape(m, k // block, block)
+    wv = e4m3_decode(wq).reshape(n, k // block, block)
+    out = np.zeros((m, n), np.float32)
+    for b in range(k // block):
+        d = _mm(xv[:, b, :], wv[:, b, :])
+        out += (d * xs[:, b:b + 1]).astype(np.float32) * ws_blocks[None, :, b]
+    return bf16_round(out), xq, xs
+
+
+def tile_scales_to_blocks(scale_tiles, n, tile=128):
+    """[N/128, K/128] tile scales -> per-(n, K-block) [N, K/128]."""
+    return np.repeat(np.asarray(scale_tiles, np.float32), tile, axis=0)[:n]
+
+
+def w4a16_mxfp4(x, packed, scales_u8, bias=None):
+    """MXFP4 weight x bf16 activation (`adapter/linear_common.py:188-209` ->
+    `kernels/megablox/gmm_v2.py:452-462`: block 32 < MXU width, so the rhs is
+    dequantized (exactly) in the activation dtype and bf16 x stays unquantized,
+    f32 accumulation, bf16 out)."""
+    w = dequant_mxfp4(packed, scales_u8)
+    out = _mm(x, w)
+    if bias is not None:
+        out = out + np.asarray(bias, np.float32)[None, :]
+    return bf16_round(out)
+
+
+def w16a16(x, w, bias=None):
+    """Unquantized bf16 linear with f32 accumulation."""
+    out = _mm(x, w)
+    if bias is not None:
+        out = out + np.asarray(bias, np.float32)[None, :]
+    return bf16_round(out)

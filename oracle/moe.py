@@ -1,0 +1,182 @@
+"""Fused-MoE references: permutation metadata, activations, full layer.
+
+Test infrastructure only.
+"""
+
+import numpy as np
+
+from oracle.codecs import bf16_round, dequant_mxfp4, e4m3_decode
+from oracle.linear import _mm
+from oracle.quant import quantize_act
+
+
+def prepare_routed(topk_ids, topk_weights=None, num_experts=None, skip_padded_tokens=False):
+    """`layers/core/fused_moe_gmm.py:288-408` (`prepare_routed_gmm_inputs`,
+    non-EP, non-SparseCore branch).
+
+    Flattens ``[T, k]`` ids to ``T*k`` routes; a route is valid when its id is
+    >= 0 (and, with ``skip_padded_tokens``, its weight is non-zero,
+    `:314-320`); invalid routes sort after every expert (key ``E``). The sort
+    is a STABLE argsort of the keys (`:337-378`; the single packed sort of
+    `:272-285` orders equal keys by flat position, which is the same thing).
+
+    Returns dict(sorted_idx, revert, group_sizes, token_sorted, valid).
+    """
+    ids = np.asarray(topk_ids, np.int64)
+    t, k = ids.shape
+    flat = ids.reshape(-1)
+    valid = flat >= 0
+    if skip_padded_tokens:
+        valid &= np.asarray(topk_weights, np.float32).reshape(-1) != 0
+    keys = np.where(valid, flat, num_experts)
+    sorted_idx = np.argsort(keys, kind="stable").astype(np.int32)
+    revert = np.argsort(sorted_idx, kind="stable").astype(np.int32)
+    group_sizes = np.bincount(flat[valid], minlength=num_experts).astype(np.int32)
+    return dict(
+        sorted_idx=sorted_idx,
+        revert=revert,
+        group_sizes=group_sizes,
+        token_sorted=(sorted_idx // k).astype(np.int32),
+        valid=valid,
+    )
+
+
+def _sigmoid(x):
+    return (1.0 / (1.0 + np.exp(-x.astype(np.float64)))).astype(np.float32)
+
+
+def _gelu_tanh(x):
+    x = x.astype(np.float64)
+    return (0.5 * x * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (x + 0.044715 * x ** 3)))).astype(np.float32)
+
+
+def act_fn(gate, up, activation):
+    """`kernels/megablox/gmm_v2.py:30-58, 84-122` (`apply_act_fn`).
+
+    ``gelu`` is jax.nn.gelu with its default ``approximate=True``, i.e. the
+    same tanh form as ``gelu_tanh``.
+    """
+    g = np.asarray(gate, np.float32)
+    u = np.asarray(up, np.float32)
+    if activation == "silu":
+        return g * _sigmoid(g) * u
+    if activation in ("gelu", "gelu_tanh"):
+        return _gelu_tanh(g) * u
+    if activation == "swigluoai":
+        g = np.minimum(g, np.float32(7.0))
+        u = np.clip(u, np.float32(-7.0), np.float32(7.0))
+        return (u + np.float32(1.0)) * (g * _sigmoid(np.float32(1.702) * g))
+    if activation == "silu_and_mul_with_clamp":
+        g = np.minimum(g, np.float32(10.0))
+        u = np.clip(u, np.float32(-10.0), np.float32(10.0))
+        return g * _sigmoid(g) * u
+    if activation.startswith("situ:"):
+        _, beta, lin = activation.split(":")
+        beta = float(beta)
+        gg = (beta * np.tanh(g.astype(np.float64) / beta) * _sigmoid(g)).astype(np.float32)
+        if lin != "none":
+            lb = float(lin)
+            u = (lb * np.tanh(u.astype(np.float64) / lb)).astype(np.float32)
+        return gg * u
+    raise NotImplementedError(f"Unsupported activation function: {activation}")
+
+
+class ExpertWeights:
+    """Dequantized view of one expert format, for the reference loops.
+
+    fmt:
+      "mxfp4": w13 packed u8 [E, 2I, H/2] + e8m0 [E, 2I, H/32]; w2 [E, H, I/2] + [E, H, I/32]
+      "fp8_block": w13 e4m3 [E, 2I, H] + tile scale_inv [E, 2I/128, H/128]; w2 likewise
+      "bf16": w13 [E, 2I, H] f32 (bf16 values); w2 [E, H, I]
+    Activations: bf16 for mxfp4/bf16 (W4A16 / W16A16); per-(row, 128) e4m3 for
+    fp8_block (the blockwise W8A8 recipe of config 4).
+    """
+
+    def __init__(self, fmt, w13, w13_scale, w2, w2_scale, b13=None, b2=None):
+        self.fmt, self.w13, self.s13, self.w2, self.s2 = fmt, w13, w13_scale, w2, w2_scale
+        self.b13, self.b2 = b13, b2
+        self._cache = {}
+
+    def dense(self, which, e):
+        key = (which, e)
+        if key not in self._cache:
+            w = self.w13[e] if which == 13 else self.w2[e]
+            s = None
+            if self.fmt != "bf16":
+                s = self.s13[e] if which == 13 else self.s2[e]
+            if self.fmt == "mxfp4":
+                d = dequant_mxfp4(w, s)
+            elif self.fmt == "fp8_block":
+                d = e4m3_decode(w)
+            else:
+                d = np.asarray(w, np.float32)
+            self._cache[key] = d
+        return self._cache[key]
+
+    def linear(self, which, e, x):
+        """x bf16-valued [R, K] -> f32 [R, N] for expert e."""
+        if self.fmt != "fp8_block":
+            out = _mm(x, self.dense(which, e))
+        else:
+            s = self.s13[e] if which == 13 else self.s2[e]
+            wv = self.dense(which, e)
+            n, k = wv.shape
+            xq, xs = quantize_act(x, "fp8", block=128)
+            xv = e4m3_decode(xq)
+            out = np.zeros((x.shape[0], n), np.float32)
+            sb = np.repeat(s, 128, axis=0)[:n]  # [N, K/128]
+            for b in range(k // 128):
+                sl = slice(b * 128, (b + 1) * 128)
+                d = _mm(xv[:, sl], wv[:, sl])
+                out += (d * xs[:, b:b + 1]).astype(np.float32) * sb[None, :, b]
+        bias = self.b13 if which == 13 else self.b2
+        if bias is not None:
+            out = out + np.asarray(bias[e], np.float32)[None, :]
+        return out.astype(np.float32)
+
+
+def fused_moe(hidden, weights: ExpertWeights, topk_weights, topk_ids, activation,
+              skip_padded_tokens=False):
+    """Grouped form of `layers/core/fused_moe_gmm.py:592-728` (non-EP):
+
+    permute by expert (`prepare_routed`), gmm1 with the fused activation and a
+    bf16 result (gmm_v2's output dtype is the lhs dtype, `:441-453`), gmm2,
+    then the weighted unpermute ``sum_k w[t,k] * y[revert[t*k+k']]`` over valid
+    routes (`:572-577`). Accumulation is kept in float32 up to the final bf16
+    cast; the reference's intermediate bf16 roundings after gmm2 are within
+    the tolerance the parity tests state.
+
+    Also returns the intermediate (post-activation, bf16) rows in sorted order
+    for kernel-level checks.
+    """
+    x = np.asarray(hidden, np.float32)
+    t, h = x.shape
+    ids = np.asarray(topk_ids)
+    k = ids.shape[1]
+    num_experts = weights.w13.shape[0]
+    meta = prepare_routed(ids, topk_weights, num_experts, skip_padded_tokens)
+    w = bf16_round(np.asarray(topk_weights, np.float32))  # `:653` weights -> bf16
+    gs = meta["group_sizes"]
+    offs = np.concatenate([[0], np.cumsum(gs)])
+    n_valid = int(offs[-1])
+    inter_rows = None
+    y_sorted = np.zeros((t * k, h), np.float32)
+    for e in range(num_experts):
+        lo, hi = int(offs[e]), int(offs[e + 1])
+        if lo == hi:
+            continue
+        rows = x[meta["token_sorted"][lo:hi]]
+        gu = weights.linear(13, e, rows)
+        i = gu.shape[1] // 2
+        a = bf16_round(act_fn(gu[:, :i], gu[:, i:], activation))
+        if inter_rows is None:
+            inter_rows = np.zeros((t * k, i), np.float32)
+        inter_rows[lo:hi] = a
+        y_sorted[lo:hi] = weights.linear(2, e, a)
+    out = np.zeros((t, h), np.float32)
+    flat_w = w.reshape(-1)
+    for r in range(t * k):
+        pos = meta["revert"][r]
+        if pos < n_valid and meta["valid"][r]:
+            out[r // k] += flat_w[r] * y_sorted[pos]
+    return bf16_round(out), meta, inter_rows

@@ -1,0 +1,143 @@
+"""Quantizers of the reference, restated in numpy.
+
+Two different quantizers exist in the reference and they round differently:
+
+* runtime activation quantization, `kernels/quantized_matmul/util.py:294-318`
+  (`quantize_block`): ``scale = absmax / qmax`` (a DIVISION), codes
+  ``x / scale``. JAX type promotion decides the arithmetic precision: for a
+  float target, ``get_max_min`` returns a NumPy float32 scalar, which is not
+  weakly typed, so a bf16 ``x`` is promoted and everything runs in float32;
+  for an int8 target it returns a Python int, which IS weakly typed, so the
+  whole computation stays in bf16 (every intermediate rounded to bf16).
+* load-time weight quantization, `layers/core/quantization.py:232-318`
+  (`quantize_tensor`): ``scale = absmax * f32(1/qmax)`` (a RECIPROCAL
+  MULTIPLY), ``inv = where(scale == 0, 0, 1/scale)``, codes
+  ``clamp(x * inv)``; integer targets round half-to-even first.
+
+Test infrastructure only.
+"""
+
+import numpy as np
+
+from oracle.codecs import bf16_round, e4m3_decode, e4m3_encode
+
+FP8_MAX = np.float32(448.0)
+
+
+def _absmax(x, axis):
+    return np.max(np.abs(x), axis=axis, keepdims=True)
+
+
+def quantize_block_fp8(x, axis=-1):
+    """`util.py:303-318` with a float8_e4m3fn target (float32 arithmetic).
+
+    ``x`` holds bf16 values as float32. Returns (uint8 e4m3 codes, f32 scale
+    with the reduced axis kept).
+    """
+    x = np.asarray(x, dtype=np.float32)
+    scale = (_absmax(x, axis) / FP8_MAX).astype(np.float32)
+    scale = np.where(scale == 0, np.float32(1.0), scale).astype(np.float32)
+    q = np.clip((x / scale).astype(np.float32), -FP8_MAX, FP8_MAX)
+    return e4m3_encode(q), scale
+
+
+def quantize_block_int8(x, axis=-1):
+    """`util.py:303-318` with an int8 target (bf16 arithmetic).
+
+    Every intermediate is rounded to bf16 because ``qmax`` (127) is a weakly
+    typed Python int: ``scale = bf16(absmax / 127)``, ``q = round_half_even(
+    bf16(x / scale))``. A float32 division followed by one bf16 rounding equals
+    the correctly rounded bf16 quotient (24 >= 2*8+2 bits, so the double
+    rounding is innocuous). Returns (int8 codes, f32 scale = f32(bf16 scale)).
+
+    parity unpinned: the bf16 quotient can reach 127.5, which rounds to 128;
+    the reference then casts with XLA's float->int8 convert, assumed
+    saturating here (128 -> 127).
+    """
+    x = bf16_round(np.asarray(x, dtype=np.float32))
+    scale = bf16_round(_absmax(x, axis) / np.float32(127.0))
+    scale = np.where(scale == 0, np.float32(1.0), scale).astype(np.float32)
+    with np.errstate(invalid="ignore"):
+        q = np.rint(bf16_round(x / scale))
+    q = np.where(np.isnan(q), 0, np.clip(q, -128, 127)).astype(np.int8)  # NaN -> 0
+    return q, scale
+
+
+def quantize_act(x, qdtype, block=None):
+    """Per-token (``block=None``) or per-(token, block) activation quant.
+
+    ``qdtype`` is "fp8" or "int8". Returns codes [M, K] and scales [M] or
+    [M, K/block] (float32).
+    """
+    x = np.asarray(x, dtype=np.float32)
+    m, k = x.shape
+    fn = quantize_block_fp8 if qdtype == "fp8" else quantize_block_int8
+    if block is None:
+        q, s = fn(x, axis=-1)
+        return q, s[:, 0]
+    q, s = fn(x.reshape(m, k // block, block), axis=-1)
+    return q.reshape(m, k), s[..., 0]
+
+
+def dequant_codes(q, qdtype) -> np.ndarray:
+    if qdtype == "fp8":
+        return e4m3_decode(q)
+    return np.asarray(q, dtype=np.int8).astype(np.float32)
+
+
+def quantize_tensor(w, qdtype, block=None):
+    """Load-time quantizer, `layers/core/quantization.py:232-318` (no ue8m0).
+
+    Quantizes along the last axis; ``block=None`` means the whole axis.
+    Returns (codes, scale) with scale shaped [..., K/block] (squeezed to [...]
+    for the whole-axis case, as the reference's ``squeeze(-1)`` does).
+    """
+    w = np.asarray(w, dtype=np.float32)
+    k = w.shape[-1]
+    block = block or k
+    if k % block:
+        raise ValueError("Quantization expects the requested axis to be divisible by block_size")
+    qmax = 448.0 if qdtype == "fp8" else 127.0
+    qmin = -448.0 if qdtype == "fp8" else -128.0
+    blocked = w.reshape(*w.shape[:-1], k // block, block)
+    recip = np.float32(1.0 / qmax)
+    scale = (_absmax(blocked, -1) * recip).astype(np.float32)
+    with np.errstate(divide="ignore"):
+        inv = np.where(scale == 0, np.float32(0.0), (np.float32(1.0) / scale)).astype(np.float32)
+    q = np.clip((blocked * inv).astype(np.float32), qmin, qmax)
+    if qdtype == "fp8":
+        codes = e4m3_encode(q)
+    else:
+        codes = np.where(np.isnan(q), 0, np.rint(q)).astype(np.int8)
+    codes = codes.reshape(w.shape)
+    scale = scale[..., 0]
+    if block == k:
+        scale = scale[..., 0]
+    return codes, scale
+
+
+def quantize_fp8_tiles(w, tile=128):
+    """DeepSeek-V3 checkpoint form of a weight: one f32 scale per 128x128 tile.
+
+    ``scale_inv = amax(tile) / 448`` (the checkpoint's ``weight_scale_inv``),
+    codes = RNE e4m3 of ``w / scale_inv`` clipped to +-448. This generates the
+    BASELINE config-2/4 inputs; it is not a reference function.
+    """
+    w = np.asarray(w, dtype=np.float32)
+    n, k = w.shape
+    t = w.reshape(n // tile, tile, k // tile, tile)
+    s = (np.max(np.abs(t), axis=(1, 3)) / FP8_MAX).astype(np.float32)
+    s = np.where(s == 0, np.float32(1.0), s).astype(np.float32)
+    q = np.clip(t / s[:, None, :, None], -FP8_MAX, FP8_MAX).astype(np.float32)
+    return e4m3_encode(q).reshape(n, k), s
+
+
+def dequant_tiles(codes, scale_inv, tile=128) -> np.ndarray:
+    """f32 weights from e4m3 codes [N, K] and tile scales [N/tile, K/tile].
+
+    `adapter/quantization/fp8.py:132-182` (`_dequantize_fp8_linear`, block
+    branch): code value times the scale of its tile.
+    """
+    n, k = codes.shape
+    v = e4m3_decode(codes).reshape(n // tile, tile, k // tile, tile)
+    return (v * scale_inv[:, None, :, None]).reshape(n, k).astype(np.float32)

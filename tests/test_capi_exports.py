@@ -1,0 +1,78 @@
+"""The C-ABI library loads (no GPU needed) and exports every function that
+include/qmoe.h declares; host-side argument validation rejects bad input
+before any launch."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared():
+    src = open(os.path.join(ROOT, "include", "qmoe.h")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"^\s*int(?:64_t)?\s+(qmoe_\w+)\s*\(", src, flags=re.M)))
+
+
+def test_header_declares_the_abi():
+    names = _declared()
+    assert "qmoe_gemm" in names and "qmoe_moe_dispatch" in names
+    assert len(names) >= 7
+
+
+def test_library_exports_every_declared_symbol():
+    from qmoe import _capi
+
+    for name in _declared():
+        assert hasattr(_capi.lib, name), name
+    assert set(_capi.EXPORTED) == set(_declared())
+    assert _capi.lib.qmoe_abi_version() == _capi.ABI_VERSION
+
+
+def test_gemm_desc_layout_matches_header_fields():
+    from qmoe import _capi
+
+    src = open(os.path.join(ROOT, "include", "qmoe.h")).read()
+    body = src[src.index("typedef struct qmoe_gemm_desc"):src.index("} qmoe_gemm_desc;")]
+    body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
+    fields = []
+    for decl in body.split("{", 1)[1].split(";"):
+        decl = decl.strip()
+        if not decl:
+            continue
+        names = decl.replace("*", " ").split()
+        tail = decl.split()[-1]
+        # "float act_p0, act_p1" declares two fields
+        for part in decl.split(","):
+            fields.append(part.replace("*", " ").split()[-1])
+    assert [f for f, _ in _capi.GemmDesc._fields_] == fields
+
+
+def test_invalid_descriptor_is_rejected_without_launch():
+    from qmoe import _capi
+
+    d = _capi.GemmDesc()
+    d.kind = 99
+    d.slots = 1
+    n = ctypes.c_int64(0)
+    assert _capi.lib.qmoe_gemm_workspace_size(ctypes.byref(d), ctypes.byref(n)) == 1
+    assert _capi.lib.qmoe_gemm(ctypes.byref(d), None, 0, None) == 1
+    # row quant: K not a multiple of 8
+    assert _capi.lib.qmoe_row_quant(None, 0, 0, 1, 12, 0, 0, 0, None, 0, None, 0, None) == 1
+    # router: topk > E
+    assert _capi.lib.qmoe_moe_route(None, 0, 1, 4, 8, 0, None, 1, 1.0, 1, 1, None, 0, None, None) == 1
+    # dispatch: too many experts
+    assert _capi.lib.qmoe_moe_dispatch(None, None, 1, 1, 4096, 0, None, None, None, None, None, None,
+                                       None, None) == 1
+
+
+def test_product_path_has_no_cpu_fallback():
+    import torch
+
+    from qmoe import ops
+
+    with pytest.raises(ValueError, match="device tensors"):
+        ops.row_quant(torch.zeros(2, 16, dtype=torch.bfloat16))

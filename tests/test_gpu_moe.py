@@ -1,0 +1,168 @@
+"""GPU parity of the MoE path: router (ids bit-exact), dispatch (bit-exact),
+combine, and the whole fused layer for each weight format."""
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_close_rows
+from oracle import codecs, moe as omoe, quant, routing
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(a, dev, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    return t.to(dtype) if dtype is not None else t
+
+
+@pytest.mark.parametrize("T,E,k", [(1, 128, 4), (37, 128, 4), (1000, 256, 8), (64, 512, 10)])
+def test_route_softmax_renorm(dev, T, E, k):
+    from qmoe import ops
+
+    print(f"route softmax T={T} E={E} k={k}", flush=True)
+    rng = np.random.default_rng(T + E)
+    logits = codecs.bf16_round(rng.standard_normal((T, E)).astype(np.float32))
+    if T > 3:
+        logits[1, :] = 0.0                  # all tied -> ids 0..k-1
+        logits[2, 10:20] = 5.0              # tie across the k boundary
+        logits[3, :] = np.nan               # poisoned row
+    w_ref, ids_ref = routing.select_experts(logits, k, True, "softmax")
+    w, ids = ops.moe_route(_t(logits, dev, torch.bfloat16), k, "softmax", True)
+    np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
+    wg = w.float().cpu().numpy()
+    np.testing.assert_array_equal(np.isnan(wg), np.isnan(w_ref))
+    ok = ~np.isnan(w_ref)
+    np.testing.assert_allclose(wg[ok], w_ref[ok], rtol=8e-3, atol=1e-6)
+
+
+@pytest.mark.parametrize("grouped", [False, True])
+@pytest.mark.parametrize("T", [1, 8, 513])
+def test_route_sigmoid_bias(dev, grouped, T):
+    """DeepSeek-V3 routing: sigmoid, correction bias, (grouped) top-8,
+    renormalize, routed_scaling_factor 2.5."""
+    from qmoe import ops
+
+    print(f"route sigmoid grouped={grouped} T={T}", flush=True)
+    E, k = 256, 8
+    rng = np.random.default_rng(T * 3 + grouped)
+    logits = codecs.bf16_round(rng.standard_normal((T, E)).astype(np.float32))
+    bias = (rng.standard_normal(E) * 0.1).astype(np.float32)
+    if grouped:
+        w_ref, ids_ref = routing.grouped_topk(logits, k, True, 8, 4, "sigmoid", bias, 2.5)
+    else:
+        w_ref, ids_ref = routing.select_experts(logits, k, True, "sigmoid", bias, 2.5)
+    w, ids = ops.moe_route(_t(logits, dev, torch.bfloat16), k, "sigmoid", True, bias=_t(bias, dev),
+                           routed_scaling_factor=2.5, num_expert_group=8 if grouped else 1,
+                           topk_group=4 if grouped else 1)
+    np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
+    np.testing.assert_allclose(w.float().cpu().numpy(), w_ref, rtol=8e-3, atol=1e-6)
+
+
+def test_rowmax_select_nan_and_sentinel_rows(dev):
+    # tests/kernels/test_router_topk.py:101-135 (NaN, -inf, -FLT_MAX rows)
+    from qmoe.layers.moe_routing import rowmax_select
+
+    E, k = 512, 10
+    for bad in (np.nan, -np.inf, np.finfo(np.float32).min):
+        s = np.full((3, E), bad, np.float32)
+        v, i = rowmax_select(_t(s, dev), k)
+        assert np.isnan(v.cpu().numpy()).all()
+        for row in i.cpu().numpy():
+            assert sorted(row.tolist()) == list(range(k))
+    rng = np.random.default_rng(5)
+    s = rng.random((37, E), dtype=np.float32)
+    s[:, :5] = np.nan
+    v, i = rowmax_select(_t(s, dev), k)
+    ref_v, ref_i = routing.rowmax_topk(s, k)
+    np.testing.assert_array_equal(i.cpu().numpy(), ref_i)
+    np.testing.assert_array_equal(v.cpu().numpy(), ref_v)
+
+
+@pytest.mark.parametrize("T,k,E", [(3, 2, 2), (1, 8, 256), (64, 8, 256), (4096, 8, 256),
+                                   (8192, 4, 128), (100, 10, 512)])
+@pytest.mark.parametrize("skip_padded", [False, True])
+def test_dispatch_bit_exact(dev, T, k, E, skip_padded):
+    from qmoe import ops
+
+    print(f"dispatch T={T} k={k} E={E} skip={skip_padded}", flush=True)
+    rng = np.random.default_rng(T + k + E)
+    ids = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
+    w = codecs.bf16_round(rng.random((T, k)).astype(np.float32))
+    if T >= 3:
+        ids[1, -1] = -1
+        w[2, :] = 0.0
+    if T == 3 and k == 2:  # test_fused_moe_gmm.py:430-467 known answer
+        ids = np.array([[1, 0], [0, -1], [1, 0]], np.int32)
+        w = codecs.bf16_round(np.float32([[0.1, 0.2], [0.3, 0.0], [0.4, 0.5]]))
+    ref = omoe.prepare_routed(ids, w, E, skip_padded)
+    meta = ops.moe_dispatch(_t(ids, dev), _t(w, dev, torch.bfloat16), E, skip_padded)
+    np.testing.assert_array_equal(meta["sorted_idx"].cpu().numpy(), ref["sorted_idx"])
+    np.testing.assert_array_equal(meta["revert"].cpu().numpy(), ref["revert"])
+    np.testing.assert_array_equal(meta["token_sorted"].cpu().numpy(), ref["token_sorted"])
+    offs = meta["group_offs"].cpu().numpy()
+    np.testing.assert_array_equal(np.diff(offs), ref["group_sizes"])
+    na = int(meta["num_active"].cpu().item())
+    np.testing.assert_array_equal(meta["active"].cpu().numpy()[:na], np.nonzero(ref["group_sizes"])[0])
+    if T == 3 and k == 2 and not skip_padded:
+        np.testing.assert_array_equal(ref["group_sizes"], [3, 2])
+
+
+def _moe_case(fmt, E, k, H, I, T, seed, bias=False):
+    rng = np.random.default_rng(seed)
+    if fmt == "mxfp4":
+        w13 = rng.integers(0, 256, (E, 2 * I, H // 2), dtype=np.uint8)
+        s13 = (127 + rng.integers(-8, 1, (E, 2 * I, H // 32))).astype(np.uint8)
+        w2 = rng.integers(0, 256, (E, H, I // 2), dtype=np.uint8)
+        s2 = (127 + rng.integers(-8, 1, (E, H, I // 32))).astype(np.uint8)
+    elif fmt == "fp8_block":
+        w13f = (rng.standard_normal((E, 2 * I, H)) * 0.02).astype(np.float32)
+        w2f = (rng.standard_normal((E, H, I)) * 0.02).astype(np.float32)
+        q13 = [quant.quantize_fp8_tiles(w13f[e]) for e in range(E)]
+        q2 = [quant.quantize_fp8_tiles(w2f[e]) for e in range(E)]
+        w13, s13 = np.stack([q[0] for q in q13]), np.stack([q[1] for q in q13])
+        w2, s2 = np.stack([q[0] for q in q2]), np.stack([q[1] for q in q2])
+    else:  # bf16
+        w13 = codecs.bf16_round((rng.standard_normal((E, 2 * I, H)) * 0.05).astype(np.float32))
+        w2 = codecs.bf16_round((rng.standard_normal((E, H, I)) * 0.05).astype(np.float32))
+        s13 = s2 = None
+    b13 = (rng.standard_normal((E, 2 * I)) * 0.1).astype(np.float32) if bias else None
+    b2 = (rng.standard_normal((E, H)) * 0.1).astype(np.float32) if bias else None
+    hid = codecs.bf16_round(rng.standard_normal((T, H)).astype(np.float32))
+    ids = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
+    tw = codecs.bf16_round(rng.random((T, k)).astype(np.float32))
+    return w13, s13, w2, s2, b13, b2, hid, ids, tw
+
+
+@pytest.mark.parametrize("fmt,act,E,k,H,I,T,bias", [
+    ("mxfp4", "swigluoai", 8, 2, 256, 256, 1, False),
+    ("mxfp4", "swigluoai", 16, 4, 512, 384, 40, True),
+    ("mxfp4", "swigluoai", 16, 4, 512, 256, 300, True),   # tiled path (T > 64)
+    ("fp8_block", "silu", 8, 2, 512, 256, 5, False),
+    ("fp8_block", "silu", 16, 4, 512, 256, 200, False),   # tiled path
+    ("bf16", "silu", 8, 2, 256, 128, 9, False),
+    ("bf16", "gelu_tanh", 8, 3, 256, 128, 100, True),
+])
+def test_fused_moe_layer(dev, fmt, act, E, k, H, I, T, bias):
+    from qmoe.layers.fused_moe import fused_moe_gmm
+
+    print(f"fused moe {fmt} {act} E={E} k={k} H={H} I={I} T={T} bias={bias}", flush=True)
+    w13, s13, w2, s2, b13, b2, hid, ids, tw = _moe_case(fmt, E, k, H, I, T, seed=E + T + H)
+    ref, _, _ = omoe.fused_moe(hid, omoe.ExpertWeights(fmt if fmt != "bf16" else "bf16", w13, s13, w2, s2,
+                                                      b13, b2), tw, ids, act)
+    wdt = torch.float8_e4m3fn if fmt == "fp8_block" else (torch.bfloat16 if fmt == "bf16" else None)
+
+    def wt(a):
+        t = _t(a, dev)
+        if wdt is torch.float8_e4m3fn:
+            return t.view(torch.float8_e4m3fn)
+        return t.to(wdt) if wdt is not None else t
+
+    got = fused_moe_gmm(
+        _t(hid, dev, torch.bfloat16), wt(w13), wt(w2),
+        _t(s13, dev) if s13 is not None else None, _t(s2, dev) if s2 is not None else None,
+        _t(b13, dev) if b13 is not None else None, _t(b2, dev) if b2 is not None else None,
+        _t(tw, dev, torch.bfloat16), _t(ids, dev), None, k, act,
+        weight_format=fmt,
+    )
+    assert_close_rows(got.float().cpu().numpy(), ref, f"moe {fmt}")

@@ -1,0 +1,195 @@
+"""GPU parity: row quantizer (bit-exact codes) and the grouped GEMM kinds
+(skinny and tiled paths) against the CPU oracle."""
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_close_rows
+from oracle import codecs, linear, quant
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(a, dev, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    return t.to(dtype) if dtype is not None else t
+
+
+def _bf16(rng, shape, scale=1.0):
+    return codecs.bf16_round((rng.standard_normal(shape) * scale).astype(np.float32))
+
+
+@pytest.mark.parametrize("qdtype", ["fp8", "int8"])
+@pytest.mark.parametrize("block", [None, 128])
+@pytest.mark.parametrize("M,K", [(1, 4096), (7, 2048), (64, 7168), (300, 1024)])
+def test_row_quant_runtime_bit_exact(dev, qdtype, block, M, K):
+    if qdtype == "int8" and block is not None:
+        pytest.skip("int8 activations are quantized per token only")
+    from qmoe import ops
+
+    print(f"row_quant {qdtype} block={block} M={M} K={K}", flush=True)
+    rng = np.random.default_rng(M * 7 + K)
+    x = _bf16(rng, (M, K), 3.0)
+    x[0, :] = 0.0  # zero row -> scale 1
+    if M > 2:
+        x[2, 5] = 1e4  # large outlier
+    x = codecs.bf16_round(x)  # the device sees bf16 values
+    q_ref, s_ref = quant.quantize_act(x, qdtype, block=block)
+    q, s = ops.row_quant(_t(x, dev, torch.bfloat16), qdtype, block=block)
+    np.testing.assert_array_equal(q.view(torch.uint8).cpu().numpy(), q_ref.view(np.uint8))
+    np.testing.assert_array_equal(s.cpu().numpy(), s_ref)
+
+
+@pytest.mark.parametrize("qdtype", ["fp8", "int8"])
+def test_row_quant_load_time_bit_exact(dev, qdtype):
+    from qmoe import ops
+
+    print(f"row_quant load {qdtype}", flush=True)
+    rng = np.random.default_rng(11)
+    w = (rng.standard_normal((96, 1024)) * 0.02).astype(np.float32)
+    w[5] = 0.0
+    q_ref, s_ref = quant.quantize_tensor(w, qdtype)
+    q, s = ops.row_quant(_t(w, dev), qdtype, mode="load")
+    np.testing.assert_array_equal(q.view(torch.uint8).cpu().numpy(), q_ref.view(np.uint8))
+    np.testing.assert_array_equal(s.cpu().numpy(), s_ref)
+    assert s_ref[5] == 0.0
+
+
+def test_e4m3_device_encoder_sweep(dev):
+    """Every e4m3 rounding boundary (+-1 ulp) through the device encoder."""
+    from qmoe import ops
+
+    vals = codecs.e4m3_decode(np.arange(256, dtype=np.uint8))
+    fin = np.unique(vals[np.isfinite(vals)].astype(np.float64))
+    mids = ((fin[:-1] + fin[1:]) / 2).astype(np.float32)
+    x = np.concatenate([fin.astype(np.float32), mids, np.nextafter(mids, np.float32(1e9)),
+                        np.nextafter(mids, np.float32(-1e9))]).astype(np.float32)
+    x = x[np.abs(x) <= 448]
+    n = (x.size + 127) // 128 * 128
+    row = np.zeros(n, np.float32)
+    row[: x.size] = x
+    row[-1] = 448.0  # absmax 448 -> load-time scale = 448 * f32(1/448) ~ 1
+    xm = row.reshape(1, -1)
+    q_ref, s_ref = quant.quantize_tensor(xm, "fp8")
+    q, s = ops.row_quant(_t(xm, dev), "fp8", mode="load")
+    np.testing.assert_array_equal(q.view(torch.uint8).cpu().numpy(), q_ref)
+
+
+# ------------------------------------------------------------------ GEMM
+
+SHAPES_SKINNY = [(1, 512, 384), (8, 1024, 640), (16, 2048, 256), (33, 512, 4096), (64, 4096, 1024)]
+SHAPES_TILED = [(65, 512, 384), (200, 1024, 1000), (512, 2048, 2048), (300, 1536, 2304)]
+
+
+@pytest.mark.parametrize("M,K,N", SHAPES_SKINNY + SHAPES_TILED)
+def test_w8a8_fp8_per_channel(dev, M, K, N):
+    from qmoe import _capi, ops
+
+    print(f"w8a8 fp8 pc M={M} K={K} N={N}", flush=True)
+    rng = np.random.default_rng(M + K + N)
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    wq, ws = quant.quantize_tensor(w, "fp8")
+    x = _bf16(rng, (M, K))
+    ref, xq_ref, xs_ref = linear.w8a8_per_channel(x, wq, ws, "fp8")
+    xq, xs = ops.row_quant(_t(x, dev, torch.bfloat16), "fp8")
+    np.testing.assert_array_equal(xq.view(torch.uint8).cpu().numpy(), xq_ref)
+    y = ops.gemm(_capi.W8A8_PC, xq.view(torch.uint8), _t(wq, dev), a_scale=xs, w_scale=_t(ws, dev))
+    assert_close_rows(y.float().cpu().numpy(), ref, f"fp8 pc {M}x{K}x{N}")
+
+
+@pytest.mark.parametrize("M,K,N", SHAPES_SKINNY + SHAPES_TILED)
+def test_w8a8_int8_per_channel_bit_exact(dev, M, K, N):
+    """int32 accumulation is exact, so the f32 epilogue in the reference's
+    operation order reproduces the oracle bit for bit."""
+    from qmoe import _capi, ops
+
+    print(f"w8a8 int8 pc M={M} K={K} N={N}", flush=True)
+    rng = np.random.default_rng(M * 3 + K + N)
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    wq, ws = quant.quantize_tensor(w, "int8")
+    x = _bf16(rng, (M, K))
+    ref, xq_ref, _ = linear.w8a8_per_channel(x, wq, ws, "int8")
+    xq, xs = ops.row_quant(_t(x, dev, torch.bfloat16), "int8")
+    np.testing.assert_array_equal(xq.cpu().numpy(), xq_ref)
+    y = ops.gemm(_capi.W8A8_PC, xq.view(torch.uint8), _t(wq.view(np.uint8), dev), a_scale=xs,
+                 w_scale=_t(ws, dev), wfmt=1)
+    np.testing.assert_array_equal(y.float().cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 1024, 512), (32, 2048, 768), (130, 1024, 640), (256, 2048, 1024)])
+@pytest.mark.parametrize("tile_scales", [True, False])
+def test_w8a8_fp8_block(dev, M, K, N, tile_scales):
+    from qmoe import _capi, ops
+
+    print(f"w8a8 blk M={M} K={K} N={N} tiles={tile_scales}", flush=True)
+    rng = np.random.default_rng(M + 2 * K + N)
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    if tile_scales:
+        wq, st = quant.quantize_fp8_tiles(w)
+        sblk, bn, s_dev = linear.tile_scales_to_blocks(st, N), 128, st
+    else:
+        wq, sblk = quant.quantize_tensor(w, "fp8", block=128)
+        bn, s_dev = 1, sblk
+    x = _bf16(rng, (M, K))
+    ref, xq_ref, _ = linear.w8a8_blockwise(x, wq, sblk)
+    xq, xs = ops.row_quant(_t(x, dev, torch.bfloat16), "fp8", block=128)
+    np.testing.assert_array_equal(xq.view(torch.uint8).cpu().numpy(), xq_ref)
+    y = ops.gemm(_capi.W8A8_BLK, xq.view(torch.uint8), _t(wq, dev), a_scale=xs,
+                 w_scale=_t(s_dev, dev), ws_bn=bn)
+    assert_close_rows(y.float().cpu().numpy(), ref, f"fp8 blk {M}x{K}x{N}")
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 2880, 5760), (16, 2880, 5760), (128, 2880, 1440),
+                                   (5, 512, 200), (90, 1024, 96)])
+def test_w4a16_mxfp4(dev, M, K, N):
+    from qmoe import _capi, ops
+
+    print(f"w4a16 mx M={M} K={K} N={N}", flush=True)
+    rng = np.random.default_rng(M + K + 3 * N)
+    packed = rng.integers(0, 256, (N, K // 2), dtype=np.uint8)
+    sc = (127 + rng.integers(-8, 1, (N, K // 32))).astype(np.uint8)
+    x = _bf16(rng, (M, K))
+    bias = (rng.standard_normal(N) * 0.1).astype(np.float32)
+    ref = linear.w4a16_mxfp4(x, packed, sc, bias)
+    y = ops.gemm(_capi.W4A16_MX, _t(x, dev, torch.bfloat16), _t(packed, dev), w_scale=_t(sc, dev),
+                 bias=_t(bias, dev))
+    assert_close_rows(y.float().cpu().numpy(), ref, f"mxfp4 {M}x{K}x{N}")
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 1024, 512), (48, 512, 384), (100, 1024, 512)])
+def test_w8a16_and_w16a16(dev, M, K, N):
+    from qmoe import _capi, ops
+
+    print(f"w8a16/w16a16 M={M} K={K} N={N}", flush=True)
+    rng = np.random.default_rng(M + K + 5 * N)
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    wq, ws = quant.quantize_tensor(w, "fp8")
+    x = _bf16(rng, (M, K))
+    xt = _t(x, dev, torch.bfloat16)
+    ref = linear.w8a16_per_channel(x, wq, ws)
+    y = ops.gemm(_capi.W8A16_PC, xt, _t(wq, dev), w_scale=_t(ws, dev))
+    assert_close_rows(y.float().cpu().numpy(), ref, "w8a16")
+    wb = codecs.bf16_round(w)
+    ref = linear.w16a16(x, wb)
+    y = ops.gemm(_capi.W16A16, xt, _t(wb, dev, torch.bfloat16))
+    assert_close_rows(y.float().cpu().numpy(), ref, "w16a16")
+
+
+def test_split_k_deterministic_and_reusable(dev):
+    """Split-K (last-workgroup reduction) gives identical results on repeat
+    calls, i.e. the counters are left at zero."""
+    from qmoe import _capi, ops
+
+    rng = np.random.default_rng(21)
+    K, N = 14336, 1024
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    wq, ws = quant.quantize_tensor(w, "fp8")
+    x = _bf16(rng, (4, K))
+    ref, _, _ = linear.w8a8_per_channel(x, wq, ws, "fp8")
+    xq, xs = ops.row_quant(_t(x, dev, torch.bfloat16), "fp8")
+    wt, wst = _t(wq, dev), _t(ws, dev)
+    outs = [ops.gemm(_capi.W8A8_PC, xq.view(torch.uint8), wt, a_scale=xs, w_scale=wst) for _ in range(3)]
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0])
+    assert_close_rows(outs[0].float().cpu().numpy(), ref, "split-k")

@@ -1,0 +1,110 @@
+"""Pins the oracle's codecs (CPU).
+
+Known answers are the reference's own test vectors
+(`tests/layers/core/test_mxfp4_requantization.py`); e4m3 / bf16 rounding is
+pinned against torch's float8_e4m3fn / bfloat16 casts (library routines)
+over dense sweeps that include every rounding boundary.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import codecs
+
+
+@pytest.mark.parametrize(
+    "u8,expected",
+    # test_mxfp4_requantization.py:194-209 values; 2**(b-127) in f32, 255 -> inf
+    [(0, 2.0 ** -127), (1, 2.0 ** -126), (127, 1.0), (128, 2.0), (253, 2.0 ** 126),
+     (254, 2.0 ** 127), (255, np.inf)],
+)
+def test_e8m0_known_values(u8, expected):
+    got = codecs.e8m0_decode(np.array([u8], np.uint8))[0]
+    assert got == np.float32(expected)
+
+
+@pytest.mark.parametrize("byte_val", [0, 1, 15, 16, 128, 255])
+def test_unpack_specific_bytes(byte_val):
+    # test_mxfp4_requantization.py:230-239: low nibble first
+    lut = [0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0, -0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0]
+    got = codecs.fp4_decode(codecs.unpack_fp4(np.array([[byte_val]], np.uint8)))
+    np.testing.assert_array_equal(got, [[lut[byte_val & 15], lut[byte_val >> 4]]])
+
+
+def test_unpack_all_bytes_is_the_e2m1_format():
+    # every code against the E2M1 definition: S.EE.M, bias 1, E=0 subnormal
+    for c in range(16):
+        s, e, m = c >> 3, (c >> 1) & 3, c & 1
+        v = (m * 0.5) if e == 0 else (1 + m / 2) * 2.0 ** (e - 1)
+        assert codecs.fp4_decode(np.array([c]))[0] == np.float32(-v if s else v)
+
+
+@pytest.mark.parametrize("lo,hi", [(0, 0), (15, 15), (1, 0), (0, 1), (5, 10)])
+def test_pack_specific_values(lo, hi):
+    # test_mxfp4_requantization.py:371-387
+    assert codecs.pack_fp4(np.array([[lo, hi]]))[0, 0] == (lo | (hi << 4))
+
+
+def test_pack_unpack_roundtrip():
+    rng = np.random.default_rng(42)
+    idx = rng.integers(0, 16, (4, 64, 512))
+    np.testing.assert_array_equal(codecs.unpack_fp4(codecs.pack_fp4(idx)), idx)
+
+
+def test_dequant_mxfp4_blocks_scale_each_32():
+    rng = np.random.default_rng(1)
+    packed = rng.integers(0, 256, (8, 64), dtype=np.uint8)
+    sc = rng.integers(100, 140, (8, 4), dtype=np.uint8)
+    d = codecs.dequant_mxfp4(packed, sc)
+    vals = codecs.fp4_decode(codecs.unpack_fp4(packed))
+    for n in range(8):
+        for k in range(128):
+            assert d[n, k] == vals[n, k] * np.float32(2.0 ** (int(sc[n, k // 32]) - 127))
+
+
+def _e4m3_sweep():
+    # all codes' values, the midpoints between neighbours, and +-1 ulp around
+    # each midpoint (the RNE tie and both sides), plus random values
+    vals = codecs.e4m3_decode(np.arange(256, dtype=np.uint8))
+    fin = np.unique(vals[np.isfinite(vals)].astype(np.float64))
+    mids = (fin[:-1] + fin[1:]) / 2
+    mids32 = mids.astype(np.float32)
+    up = np.nextafter(mids32, np.float32(np.inf))
+    dn = np.nextafter(mids32, np.float32(-np.inf))
+    rnd = np.random.default_rng(0).uniform(-448, 448, 200000).astype(np.float32)
+    tiny = np.random.default_rng(1).uniform(-2 ** -6, 2 ** -6, 50000).astype(np.float32)
+    return np.concatenate([fin.astype(np.float32), mids32, up, dn, rnd, tiny,
+                           np.float32([0.0, -0.0, 448.0, -448.0])])
+
+
+def test_e4m3_encode_matches_torch_cast():
+    x = _e4m3_sweep()
+    x = x[np.abs(x) <= 448]
+    ours = codecs.e4m3_encode(x)
+    ref = torch.from_numpy(x).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    np.testing.assert_array_equal(ours, ref)
+
+
+def test_e4m3_decode_matches_torch():
+    codes = np.arange(256, dtype=np.uint8)
+    ref = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+    np.testing.assert_array_equal(codecs.e4m3_decode(codes), ref)
+
+
+def test_e4m3_known_values():
+    assert codecs.e4m3_encode(np.float32([448.0]))[0] == 0x7E
+    assert codecs.e4m3_encode(np.float32([2 ** -9]))[0] == 0x01
+    assert codecs.e4m3_encode(np.float32([2 ** -6]))[0] == 0x08
+    assert codecs.e4m3_encode(np.float32([np.nan]))[0] & 0x7F == 0x7F
+    assert codecs.e4m3_encode(np.float32([-1.0]))[0] == 0xB8
+
+
+def test_bf16_round_matches_torch():
+    rng = np.random.default_rng(3)
+    x = np.concatenate([rng.standard_normal(100000).astype(np.float32) * 10.0 ** rng.integers(-30, 30, 100000),
+                        # exact ties at bf16 granularity
+                        (rng.integers(0, 2 ** 16, 5000).astype(np.uint32) << 16 | 0x8000).view(np.float32)])
+    x = x[np.isfinite(x)]
+    ref = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    np.testing.assert_array_equal(codecs.bf16_round(x), ref)

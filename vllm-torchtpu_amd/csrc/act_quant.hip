@@ -1,0 +1,185 @@
+// Row quantizer: bf16/f32 rows -> e4m3 or int8 codes + float32 scales.
+//
+// One kernel covers the two quantizers of the reference, which round
+// differently (both restated from the reference source):
+//  * RUNTIME activation quant, kernels/quantized_matmul/util.py:294-318
+//    (quantize_block): scale = absmax / qmax (a division), codes x / scale.
+//    fp8 target: float32 arithmetic; int8 target: bf16 arithmetic (the
+//    reference's qmax is a weakly typed Python int, so JAX stays in bf16):
+//    scale = bf16(absmax / 127), codes = rint(bf16(x / scale)). A zero scale
+//    becomes 1.
+//  * LOAD-TIME weight quant, layers/core/quantization.py:232-318
+//    (quantize_tensor): scale = absmax * f32(1/qmax) (reciprocal multiply),
+//    inv = scale == 0 ? 0 : 1/scale, codes clamp(x * inv); int rounds half to
+//    even. A zero scale stays 0.
+// Granularity: one scale per row, or per (row, 128-column block).
+//
+// Launch: one 256-thread workgroup per row; thread t owns 8 consecutive
+// columns per 2048-column stride, so a 128-column block is exactly 16
+// adjacent lanes of one wavefront (reduced with shuffles, no LDS).
+
+#include "qmoe_common.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+
+struct Row8 {
+  float v[8];
+};
+
+template <bool kInF32>
+__device__ __forceinline__ Row8 load8(const void* base, int64_t idx) {
+  Row8 r;
+  if (kInF32) {
+    const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(base) + idx);
+    float4 a = p[0], b = p[1];
+    r.v[0] = a.x; r.v[1] = a.y; r.v[2] = a.z; r.v[3] = a.w;
+    r.v[4] = b.x; r.v[5] = b.y; r.v[6] = b.z; r.v[7] = b.w;
+  } else {
+    uint4 q = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + idx);
+    uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      r.v[2 * i] = bits_f32(w[i] << 16);
+      r.v[2 * i + 1] = bits_f32(w[i] & 0xffff0000u);
+    }
+  }
+  return r;
+}
+
+// mode: 0 runtime (division), 1 load-time (reciprocal multiply)
+// qdt : 0 e4m3fn, 1 int8
+template <int kQdt, int kMode>
+__device__ __forceinline__ float make_scale(float amax) {
+  if (kMode == 0) {
+    if (kQdt == 0) {
+      float s = amax / 448.0f;
+      return s == 0.0f ? 1.0f : s;
+    }
+    float s = bf16_round(amax / 127.0f);
+    return s == 0.0f ? 1.0f : s;
+  }
+  const float recip = kQdt == 0 ? (float)(1.0 / 448.0) : (float)(1.0 / 127.0);
+  return amax * recip;
+}
+
+template <int kQdt, int kMode>
+__device__ __forceinline__ uint32_t quant1(float x, float scale, float inv) {
+  if (kMode == 0) {
+    if (kQdt == 0) {
+      float d = x / scale;
+      float q = d != d ? d : fminf(fmaxf(d, -448.0f), 448.0f);  // clip keeps NaN
+      return f32_to_e4m3(q);
+    }
+    float q = rintf(bf16_round(x / scale));
+    q = q != q ? 0.0f : fminf(fmaxf(q, -128.0f), 127.0f);  // NaN -> 0, saturate
+    return (uint32_t)(int32_t)q & 0xffu;
+  }
+  float q = x * inv;
+  if (kQdt == 0) {
+    float c = fminf(fmaxf(q, -448.0f), 448.0f);
+    if (q != q) c = q;
+    return f32_to_e4m3(c);
+  }
+  float c = q != q ? 0.0f : fminf(fmaxf(q, -128.0f), 127.0f);
+  return (uint32_t)(int32_t)rintf(c) & 0xffu;
+}
+
+template <int kQdt, int kMode>
+__device__ __forceinline__ void store8(uint8_t* dst, const Row8& r, float scale) {
+  float inv = 0.0f;
+  if (kMode == 1) inv = scale == 0.0f ? 0.0f : 1.0f / scale;
+  uint32_t lo = 0, hi = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) lo |= quant1<kQdt, kMode>(r.v[i], scale, inv) << (8 * i);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) hi |= quant1<kQdt, kMode>(r.v[4 + i], scale, inv) << (8 * i);
+  *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
+}
+
+// max that keeps NaN sticky, like a jnp/np reduction (fmaxf drops NaN)
+__device__ __forceinline__ float nanmax(float a, float b) {
+  float r = fmaxf(a, b);
+  return a != a ? a : (b != b ? b : r);
+}
+
+__device__ __forceinline__ float amax8(const Row8& r) {
+  float m = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) m = nanmax(m, fabsf(r.v[i]));
+  return m;
+}
+
+template <int kQdt, int kMode, bool kInF32, bool kBlock>
+__global__ __launch_bounds__(kThreads) void row_quant_kernel(
+    const void* __restrict__ x, int64_t ldx, int64_t K, uint8_t* __restrict__ q,
+    int64_t ldq, float* __restrict__ scales, int64_t lds) {
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int64_t xbase = row * ldx;
+  uint8_t* qrow = q + row * ldq;
+  if (kBlock) {
+    // 16 lanes per 128-column block
+    for (int64_t c = (int64_t)tid * 8; c < K; c += kThreads * 8) {
+      Row8 r = load8<kInF32>(x, xbase + c);
+      float m = amax8(r);
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) m = nanmax(m, __shfl_xor(m, o, 64));
+      float s = make_scale<kQdt, kMode>(m);
+      store8<kQdt, kMode>(qrow + c, r, s);
+      if ((tid & 15) == 0) scales[row * lds + c / 128] = s;
+    }
+    return;
+  }
+  __shared__ float red[kThreads / 64];
+  float m = 0.0f;
+  for (int64_t c = (int64_t)tid * 8; c < K; c += kThreads * 8)
+    m = nanmax(m, amax8(load8<kInF32>(x, xbase + c)));
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) m = nanmax(m, __shfl_xor(m, o, 64));
+  if ((tid & 63) == 0) red[tid >> 6] = m;
+  __syncthreads();
+  m = nanmax(nanmax(red[0], red[1]), nanmax(red[2], red[3]));
+  float s = make_scale<kQdt, kMode>(m);
+  for (int64_t c = (int64_t)tid * 8; c < K; c += kThreads * 8)
+    store8<kQdt, kMode>(qrow + c, load8<kInF32>(x, xbase + c), s);
+  if (tid == 0) scales[row * lds] = s;
+}
+
+template <int kQdt, int kMode, bool kInF32, bool kBlock>
+void launch_rq(const void* x, int64_t ldx, int64_t M, int64_t K, uint8_t* q, int64_t ldq,
+               float* s, int64_t lds, hipStream_t st) {
+  hipLaunchKernelGGL((row_quant_kernel<kQdt, kMode, kInF32, kBlock>), dim3((unsigned)M),
+                     dim3(kThreads), 0, st, x, ldx, K, q, ldq, s, lds);
+}
+
+}  // namespace
+
+// See include/qmoe.h for the contract.
+extern "C" int qmoe_row_quant(const void* x, int64_t ldx, int in_f32, int64_t M, int64_t K,
+                              int qdtype, int mode, int block, void* q, int64_t ldq,
+                              float* scales, int64_t lds, hipStream_t stream) {
+  if (M < 0 || K <= 0 || (K % 8) != 0) return QMOE_ERR_ARG;
+  if (qdtype != 0 && qdtype != 1) return QMOE_ERR_ARG;
+  if (mode != 0 && mode != 1) return QMOE_ERR_ARG;
+  if (block != 0 && block != 128) return QMOE_ERR_ARG;
+  if (block == 128 && (K % 128) != 0) return QMOE_ERR_ARG;
+  if (in_f32 && mode == 0) return QMOE_ERR_ARG;  // runtime path takes bf16 activations
+  if (M == 0) return QMOE_OK;
+  uint8_t* qq = static_cast<uint8_t*>(q);
+  const bool blk = block == 128;
+#define QMOE_RQ(QD, MD, F32, BLK) launch_rq<QD, MD, F32, BLK>(x, ldx, M, K, qq, ldq, scales, lds, stream)
+  if (mode == 0) {
+    if (qdtype == 0) { if (blk) QMOE_RQ(0, 0, false, true); else QMOE_RQ(0, 0, false, false); }
+    else { if (blk) QMOE_RQ(1, 0, false, true); else QMOE_RQ(1, 0, false, false); }
+  } else if (in_f32) {
+    if (qdtype == 0) { if (blk) QMOE_RQ(0, 1, true, true); else QMOE_RQ(0, 1, true, false); }
+    else { if (blk) QMOE_RQ(1, 1, true, true); else QMOE_RQ(1, 1, true, false); }
+  } else {
+    if (qdtype == 0) { if (blk) QMOE_RQ(0, 1, false, true); else QMOE_RQ(0, 1, false, false); }
+    else { if (blk) QMOE_RQ(1, 1, false, true); else QMOE_RQ(1, 1, false, false); }
+  }
+#undef QMOE_RQ
+  return hipGetLastError() == hipSuccess ? QMOE_OK : QMOE_ERR_LAUNCH;
+}

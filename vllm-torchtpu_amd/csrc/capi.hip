@@ -1,0 +1,116 @@
+// C ABI of the grouped GEMM: validates the descriptor and picks the skinny
+// (weight-streaming, <= 64 rows per group) or the tiled (LDS/MFMA) kernel.
+
+#include <algorithm>
+
+#include "../../include/qmoe.h"
+#include "gemm_common.h"
+
+// defined in gemm_skinny.hip / gemm_tiled.hip
+void qmoe_skinny_plan(int64_t M, int64_t N, int64_t K, int act, int slots, int ksplit_hint,
+                      int* ksplit_out, int64_t* ws_bytes);
+int qmoe_skinny_launch(int kind, GemmParams p, int max_rows, int slots, void* workspace,
+                       int64_t ws_bytes, int ksplit_hint, hipStream_t st);
+int qmoe_tiled_launch(int kind, GemmParams p, hipStream_t st);
+
+namespace {
+
+constexpr int kSkinnyMaxRows = 64;
+
+int to_params(const qmoe_gemm_desc* d, GemmParams* p) {
+  if (!d) return QMOE_ERR_ARG;
+  if (d->kind < QMOE_W8A8_PC || d->kind > QMOE_W16A16) return QMOE_ERR_ARG;
+  if (d->kind == QMOE_W8A8_PC && d->wfmt != 0 && d->wfmt != 1) return QMOE_ERR_ARG;
+  if (d->act < QMOE_ACT_NONE || d->act > QMOE_ACT_SITU) return QMOE_ERR_ARG;
+  if (d->M < 0 || d->N <= 0 || d->K <= 0 || d->slots <= 0) return QMOE_ERR_ARG;
+  if (!d->a || !d->w || !d->y) return QMOE_ERR_ARG;
+  if ((d->kind == QMOE_W8A8_PC || d->kind == QMOE_W8A8_BLK) && !d->a_scale) return QMOE_ERR_ARG;
+  if (d->kind != QMOE_W16A16 && !d->w_scale) return QMOE_ERR_ARG;
+  if (d->kind == QMOE_W8A8_BLK && (d->ws_bn <= 0 || (d->K % 128) != 0)) return QMOE_ERR_ARG;
+  if (d->act != QMOE_ACT_NONE && (d->N % 2) != 0) return QMOE_ERR_ARG;
+  if (d->active && (!d->num_active || !d->group_offs)) return QMOE_ERR_ARG;
+  if (!d->group_offs && d->slots != 1) return QMOE_ERR_ARG;
+  // 16-byte loads along K
+  const int wbytes = d->kind == QMOE_W4A16_MX ? d->K / 2 : (d->kind == QMOE_W16A16 ? 2 * d->K : d->K);
+  if (d->ldw < wbytes || (d->ldw % 16) != 0 || (d->K % 32) != 0) return QMOE_ERR_ARG;
+  const bool abf16 = d->kind == QMOE_W8A16_PC || d->kind == QMOE_W4A16_MX || d->kind == QMOE_W16A16;
+  if (d->lda < d->K || ((d->lda * (abf16 ? 2 : 1)) % 16) != 0) return QMOE_ERR_ARG;
+  const int nout = d->act != QMOE_ACT_NONE ? d->N / 2 : d->N;
+  if (d->ldy < nout) return QMOE_ERR_ARG;
+  *p = GemmParams{};
+  p->a = d->a;
+  p->lda = d->lda;
+  p->a_scale = d->a_scale;
+  p->lds_a = d->lds_a;
+  p->a_rows = d->a_rows;
+  p->w = static_cast<const uint8_t*>(d->w);
+  p->ldw = d->ldw;
+  p->w_gstride = d->w_gstride;
+  p->w_scale = d->w_scale;
+  p->ldws = d->ldws;
+  p->ws_gstride = d->ws_gstride;
+  p->ws_bn = d->ws_bn > 0 ? d->ws_bn : 1;
+  p->bias = d->bias;
+  p->bias_gstride = d->bias_gstride;
+  p->group_offs = d->group_offs;
+  p->active = d->active;
+  p->num_active = d->num_active;
+  p->slots = d->slots;
+  p->M = d->M;
+  p->N = d->N;
+  p->K = d->K;
+  p->wfmt = d->wfmt;
+  p->act = d->act;
+  p->act_p0 = d->act_p0;
+  p->act_p1 = d->act_p1;
+  p->row_weight = d->row_weight;
+  p->y = static_cast<uint16_t*>(d->y);
+  p->ldy = d->ldy;
+  p->y_rows = d->y_rows;
+  p->ksplit = 1;
+  return QMOE_OK;
+}
+
+// Grid depth of the skinny kernel: every group, or -- with an active list --
+// at most one slot per row (a listed group has at least one row).
+int skinny_slots(const qmoe_gemm_desc* d) {
+  return d->active ? std::max(1, std::min(d->slots, d->M)) : d->slots;
+}
+
+bool use_skinny(const qmoe_gemm_desc* d) {
+  const int rows = d->group_offs ? d->max_rows : d->M;
+  return rows <= kSkinnyMaxRows;
+}
+
+}  // namespace
+
+extern "C" int qmoe_abi_version(void) { return 1; }
+
+extern "C" int qmoe_gemm_workspace_size(const qmoe_gemm_desc* d, int64_t* bytes) {
+  GemmParams p;
+  const int st = to_params(d, &p);
+  if (st != QMOE_OK) return st;
+  *bytes = 0;
+  if (use_skinny(d)) {
+    int ks = 1;
+    qmoe_skinny_plan(d->M, d->N, d->K, d->act, skinny_slots(d), 0, &ks, bytes);
+  }
+  return QMOE_OK;
+}
+
+extern "C" int qmoe_gemm(const qmoe_gemm_desc* d, void* workspace, int64_t ws_bytes,
+                         hipStream_t stream) {
+  GemmParams p;
+  const int st = to_params(d, &p);
+  if (st != QMOE_OK) return st;
+  if (d->M == 0) return QMOE_OK;
+  if (use_skinny(d)) {
+    const int rows = d->group_offs ? std::max(1, std::min(d->max_rows, d->M)) : d->M;
+    return qmoe_skinny_launch(d->kind, p, rows, skinny_slots(d), workspace, ws_bytes, 0, stream);
+  }
+  // the tiled kernel enumerates m-tiles over all groups; the active list is
+  // a skinny-path device (it bounds the grid by the number of routed experts)
+  p.active = nullptr;
+  p.num_active = nullptr;
+  return qmoe_tiled_launch(d->kind, p, stream);
+}

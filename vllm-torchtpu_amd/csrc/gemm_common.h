@@ -1,0 +1,103 @@
+// Problem description shared by the skinny (decode) and tiled (prefill)
+// grouped GEMM kernels.
+//
+// A grouped GEMM computes, for every group g and every compact row R in
+// [group_offs[g], group_offs[g+1]):
+//     acc[R, n] = sum_k A[arow(R), k] * W[g, n, k]          (n < N)
+// then the epilogue applies the format's scales, the optional bias, the
+// optional fused gate/up activation (gate = column n, up = column
+// n + N/2, output column n < N/2), the optional per-row routing weight, and
+// stores bf16 at Y[yrow(R), n_out].
+// A dense linear is the one-group case (group_offs == nullptr, rows [0, M)).
+#pragma once
+
+#include "qmoe_common.h"
+
+enum QmoeKind {
+  QK_W8A8_PC = 0,   // A e4m3/int8 codes + per-row f32 scale; W codes + per-channel f32 scale
+  QK_W8A8_BLK = 1,  // A e4m3 + per-(row,128) f32 scale; W e4m3 + per-(n/bn, 128) f32 scale
+  QK_W8A16_PC = 2,  // A bf16; W e4m3 + per-channel f32 scale
+  QK_W4A16_MX = 3,  // A bf16; W e2m1 (2 per byte, low nibble = even k) + e8m0 per 32 k
+  QK_W16A16 = 4,    // A bf16; W bf16
+};
+
+enum QmoeAct {
+  QA_NONE = 0,
+  QA_SILU = 1,
+  QA_SWIGLUOAI = 2,  // alpha = p0 (1.702), limit = p1 (7.0)
+  QA_GELU_TANH = 3,
+  QA_SILU_CLAMP = 4,  // limit = p0 (10.0)
+  QA_SITU = 5,        // beta = p0, linear_beta = p1 (<= 0: none)
+};
+
+struct GemmParams {
+  // A operand
+  const void* a;           // codes (1 byte) or bf16, row-major
+  int64_t lda;             // row stride in elements
+  const float* a_scale;    // W8A8: per-row [rows] or per-(row,kb) [rows, lds_a]
+  int64_t lds_a;           // row stride of a_scale (1 for per-row)
+  const int32_t* a_rows;   // optional gather: physical A row of compact row R
+  // W operand, group g at w + g * w_gstride (bytes); row n at + n * ldw
+  const uint8_t* w;
+  int64_t ldw;             // bytes per weight row
+  int64_t w_gstride;
+  const void* w_scale;     // f32 [N] | f32 [N/bn, ldws] | u8 [N, ldws]
+  int64_t ldws;            // row stride of w_scale (elements)
+  int64_t ws_gstride;      // group stride of w_scale (elements)
+  int32_t ws_bn;           // rows of W sharing one block-scale row (1 or 128)
+  const float* bias;       // optional f32 [G, N]
+  int64_t bias_gstride;
+  // rows / groups
+  const int32_t* group_offs;  // [G+1] compact row offsets, or nullptr (one group)
+  const int32_t* active;      // optional list of non-empty groups (slot -> group)
+  const int32_t* num_active;  // device scalar: number of valid slots in `active`
+  int32_t slots;              // number of groups (or capacity of `active`)
+  int32_t M;                  // total compact rows
+  int32_t N;                  // weight rows (2*I when an activation is fused)
+  int32_t K;
+  int32_t wfmt;               // QK_W8A8_PC only: 0 e4m3, 1 int8
+  // epilogue
+  int32_t act;
+  float act_p0, act_p1;
+  const uint16_t* row_weight;  // optional bf16 per compact row
+  uint16_t* y;
+  int64_t ldy;
+  const int32_t* y_rows;       // optional scatter: destination row of compact row R
+  // split-K workspace (skinny kernel only)
+  float* partial;
+  uint32_t* counters;
+  int32_t ksplit;
+};
+
+__device__ __forceinline__ float qmoe_sigmoid(float x) { return 1.0f / (1.0f + __expf(-x)); }
+
+// Fused gate/up activations, `kernels/megablox/gmm_v2.py:30-58, 84-122` of the
+// reference (gelu is jax.nn.gelu's default tanh approximation).
+__device__ __forceinline__ float qmoe_act(int act, float g, float u, float p0, float p1) {
+  switch (act) {
+    case QA_SILU:
+      return g * qmoe_sigmoid(g) * u;
+    case QA_SWIGLUOAI: {
+      g = fminf(g, p1);
+      u = fminf(fmaxf(u, -p1), p1);
+      return (u + 1.0f) * (g * qmoe_sigmoid(p0 * g));
+    }
+    case QA_GELU_TANH: {
+      const float c = 0.7978845608028654f;  // sqrt(2/pi)
+      float t = tanhf(c * (g + 0.044715f * g * g * g));
+      return 0.5f * g * (1.0f + t) * u;
+    }
+    case QA_SILU_CLAMP: {
+      g = fminf(g, p0);
+      u = fminf(fmaxf(u, -p0), p0);
+      return g * qmoe_sigmoid(g) * u;
+    }
+    case QA_SITU: {
+      float gg = p0 * tanhf(g / p0) * qmoe_sigmoid(g);
+      if (p1 > 0.0f) u = p1 * tanhf(u / p1);
+      return gg * u;
+    }
+    default:
+      return g;
+  }
+}

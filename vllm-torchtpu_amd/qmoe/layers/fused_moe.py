@@ -1,0 +1,109 @@
+"""Fused-MoE entry point (the reference's `fused_moe_gmm` bridge).
+
+Mirrors `layers/adapter/fused_moe.py:241-293` (``fused_moe_gmm``) and the
+non-EP body of `layers/core/fused_moe_gmm.py:592-728` (``fused_moe_func``):
+permute routes by expert, grouped GEMM gate_up with the activation fused in
+its epilogue, grouped GEMM down with the routing weight fused in its epilogue
+(scattering each row to its flat route slot), then the per-token sum.
+
+Weight formats (this package's runtime layouts, produced by the MoE methods'
+`process_weights_after_loading`; all N-major, K contiguous):
+
+====================  ==========================  ====================================
+format                w1 [E, 2I, H...] / w2        scales
+====================  ==========================  ====================================
+``mxfp4``             uint8 packed e2m1 [., ., K/2]  e8m0 uint8 [E, N, K/32]
+``fp8_block``         float8_e4m3fn [E, N, K]      f32 tile scales [E, N/128, K/128]
+``fp8`` / ``int8``    float8_e4m3fn / int8         f32 per-channel [E, N]
+``bf16``              bfloat16                      none
+====================  ==========================  ====================================
+
+w1's N axis is ``[gate | up]`` (gate rows first), as in the reference
+(`kernels/megablox/gmm_v2.py:894-901`).
+"""
+
+import torch
+
+from qmoe import _capi, ops
+
+
+def infer_weight_format(w1: torch.Tensor, w1_scale) -> str:
+    if w1.dtype == torch.bfloat16:
+        return "bf16"
+    if w1.dtype == torch.int8:
+        return "int8"
+    if w1.dtype == torch.float8_e4m3fn:
+        if w1_scale is not None and w1_scale.dim() == 3 and w1_scale.shape[-1] * 128 == w1.shape[-1]:
+            return "fp8_block"
+        return "fp8"
+    if w1.dtype == torch.uint8 or "float4" in str(w1.dtype):
+        return "mxfp4"
+    raise ValueError(f"unsupported MoE weight dtype {w1.dtype}")
+
+
+def fused_moe_gmm(hidden_states, w1, w2, w1_scale, w2_scale, w1_bias, w2_bias, topk_weights,
+                  topk_ids, experts_start, topk, activation, rhs_quant_dtype=None,
+                  skip_padded_tokens=None, weight_format=None):
+    """Routed-expert MoE forward (`fused_moe.py:241-293`). Returns bf16 [T, H].
+
+    ``experts_start`` is the reference's expert-parallel offset; this build
+    runs the whole expert set on one GPU, so it must be None or 0.
+    ``rhs_quant_dtype`` (packed int4 carriers) is not supported.
+    """
+    if experts_start is not None and int(experts_start) != 0:
+        raise NotImplementedError("expert parallelism is out of scope: experts_start must be 0")
+    if rhs_quant_dtype is not None:
+        raise NotImplementedError("packed int4 rhs_quant_dtype is not supported")
+    fmt = weight_format or infer_weight_format(w1, w1_scale)
+    T, H = hidden_states.shape
+    E = w1.shape[0]
+    if topk_weights.shape != (T, topk) or topk_ids.shape != (T, topk):
+        raise ValueError(f"topk tensors must be [{T}, {topk}]")
+    x = hidden_states if hidden_states.dtype == torch.bfloat16 else hidden_states.to(torch.bfloat16)
+    x = x.contiguous()
+    # `fused_moe_gmm.py:653`: routing weights take the hidden dtype
+    tw = topk_weights.to(torch.bfloat16).contiguous()
+    skip = bool(skip_padded_tokens)
+    meta = ops.moe_dispatch(topk_ids, tw, E, skip)
+    M = T * topk
+    common = dict(group_offs=meta["group_offs"], active=meta["active"],
+                  num_active=meta["num_active"], slots=E, max_rows=T, M=M)
+
+    b1 = w1_bias.float().reshape(E, -1).contiguous() if w1_bias is not None else None
+    b2 = w2_bias.float().reshape(E, -1).contiguous() if w2_bias is not None else None
+    u8 = lambda t: t.view(torch.uint8)  # noqa: E731
+
+    if fmt == "mxfp4":
+        inter = ops.gemm(_capi.W4A16_MX, x, u8(w1), w_scale=u8(w1_scale), bias=b1,
+                         a_rows=meta["token_sorted"], activation=activation, **common)
+        a2, a2_scale, kind, wf, bn = inter, None, _capi.W4A16_MX, 0, 1
+        w2k, w2s = u8(w2), u8(w2_scale)
+    elif fmt == "bf16":
+        inter = ops.gemm(_capi.W16A16, x, w1, bias=b1, a_rows=meta["token_sorted"],
+                         activation=activation, **common)
+        a2, a2_scale, kind, wf, bn = inter, None, _capi.W16A16, 0, 1
+        w2k, w2s = w2, None
+    elif fmt == "fp8_block":
+        xq, xs = ops.row_quant(x, "fp8", block=128)
+        inter = ops.gemm(_capi.W8A8_BLK, u8(xq), u8(w1), a_scale=xs, w_scale=w1_scale, ws_bn=128,
+                         bias=b1, a_rows=meta["token_sorted"], activation=activation, **common)
+        a2q, a2_scale = ops.row_quant(inter, "fp8", block=128)
+        a2, kind, wf, bn = u8(a2q), _capi.W8A8_BLK, 0, 128
+        w2k, w2s = u8(w2), w2_scale
+    elif fmt in ("fp8", "int8"):
+        qd = "fp8" if fmt == "fp8" else "int8"
+        wf = 0 if fmt == "fp8" else 1
+        xq, xs = ops.row_quant(x, qd)
+        inter = ops.gemm(_capi.W8A8_PC, u8(xq), u8(w1), a_scale=xs,
+                         w_scale=w1_scale.float().reshape(E, -1).contiguous(), wfmt=wf, bias=b1,
+                         a_rows=meta["token_sorted"], activation=activation, **common)
+        a2q, a2_scale = ops.row_quant(inter, qd)
+        a2, kind, bn = u8(a2q), _capi.W8A8_PC, 1
+        w2k, w2s = u8(w2), w2_scale.float().reshape(E, -1).contiguous()
+    else:
+        raise ValueError(f"unknown MoE weight format {fmt!r}")
+
+    routed = torch.empty((M, H), dtype=torch.bfloat16, device=x.device)
+    ops.gemm(kind, a2, w2k, a_scale=a2_scale, w_scale=w2s, wfmt=wf, ws_bn=bn, bias=b2,
+             row_weight=meta["sorted_weight"], y_rows=meta["sorted_idx"], out=routed, **common)
+    return ops.moe_combine(routed, topk_ids, tw, skip)

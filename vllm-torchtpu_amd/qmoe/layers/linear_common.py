@@ -1,0 +1,145 @@
+"""Dense quantized-matmul entry points (the reference's `linear_common`).
+
+Mirrors `layers/adapter/linear_common.py` of the reference plugin:
+``quantized_matmul(x, w_q, w_s, w8a16_max_rows=0)`` (`:162-185`, dispatch
+`:69-128`) and ``quantized_matmul_fp4(x, w_q, w_s)`` (`:242-255`). Same
+argument meaning and the same ValueError texts; the computation runs in the
+qmoe HIP kernels.
+
+Weight layout: the reference's runtime weight is the canonical (k, n)
+``[n_in, n_out]`` array. Here ``w_q`` has that same logical shape but must be
+the transposed VIEW of an N-major ``[n_out, n_in]`` buffer (stride
+``(1, n_in)``), which is what this package's `process_weights_after_loading`
+produces: each output channel's K values stay contiguous for 16-byte HBM
+loads. A K-major contiguous ``[n_in, n_out]`` tensor is rejected rather than
+transposed per call.
+"""
+
+import torch
+
+from qmoe import _capi, ops
+
+
+def _weight_nk(w_q: torch.Tensor) -> torch.Tensor:
+    """[K, N] logical weight -> the N-major [N, K] buffer it views."""
+    if w_q.dim() != 2:
+        raise ValueError(f"weight must be 2-D [n_in, n_out], got {tuple(w_q.shape)}")
+    w_nk = w_q.t()
+    if not w_nk.is_contiguous():
+        raise ValueError(
+            "qmoe expects w_q as the [n_in, n_out] view of an N-major [n_out, n_in] "
+            "buffer (stride (1, n_in)); keep the checkpoint layout and pass weight.t()"
+        )
+    return w_nk
+
+
+def _scale_blocks(w_s: torch.Tensor, k_dim: int, n_out: int):
+    """Block scales -> (f32 [N/bn, K/128] tensor, bn).
+
+    Accepts the reference's rank-4 ``[1, K/B, 1, N]`` (B must be 128; per
+    (K-block, n)) or the native compact ``[N/bn, K/128]`` form (bn = 1 or a
+    128x128 tile scale with bn = 128).
+    """
+    if w_s.dim() == 4:
+        _, sharded_num_blocks, mid, scale_n_out = w_s.shape
+        if mid != 1:
+            raise ValueError(f"Blockwise weight scale axis 2 must be 1, got {w_s.shape=}")
+        if scale_n_out != n_out:
+            raise ValueError(
+                f"Blockwise weight scale output dim {scale_n_out} must match "
+                f"weight output dim {n_out}."
+            )
+        if sharded_num_blocks <= 0 or k_dim % sharded_num_blocks != 0:
+            raise ValueError(
+                f"Input hidden dim {k_dim} must be divisible by block scale "
+                f"count {sharded_num_blocks}."
+            )
+        if k_dim // sharded_num_blocks != 128:
+            raise ValueError("qmoe blockwise kernels take 128-wide K blocks")
+        return w_s[0, :, 0, :].t().contiguous().float(), 1
+    if w_s.dim() == 2:
+        if w_s.shape[1] * 128 != k_dim:
+            raise ValueError(f"block scale has {w_s.shape[1]} K blocks, expected {k_dim // 128}")
+        if w_s.shape[0] == n_out:
+            return w_s.float().contiguous(), 1
+        if w_s.shape[0] == (n_out + 127) // 128:
+            return w_s.float().contiguous(), 128
+        raise ValueError(f"block scale rows {w_s.shape[0]} match neither {n_out} nor {n_out // 128}")
+    raise ValueError(f"unsupported weight scale shape {tuple(w_s.shape)}")
+
+
+def quantized_matmul(x: torch.Tensor, w_q: torch.Tensor, w_s: torch.Tensor,
+                     w8a16_max_rows: int = 0) -> torch.Tensor:
+    """Runtime quantized dense linear, `linear_common.py:162-185` + `:69-128`.
+
+    * ``w_s`` 1-D ``[n_out]``: per-channel. e4m3 weights with
+      ``0 < rows <= w8a16_max_rows`` keep bf16 activations (W8A16); otherwise
+      activations are quantized per token (e4m3 in f32 / int8 in bf16
+      arithmetic, `kernels/quantized_matmul/util.py:80-124`) -- W8A8.
+    * block scales (rank-4 reference form or compact 2-D): e4m3 weights with
+      128-wide K blocks; activations quantized per (token, 128 columns) in
+      f32 -- the blockwise W8A8 recipe
+      (`kernels/quantized_matmul/blockwise_kernel.py:197-247`).
+    """
+    if x.shape[-1] != w_q.shape[0]:
+        raise ValueError(
+            f"Input hidden dim {x.shape[-1]} must match weight hidden dim "
+            f"{w_q.shape[0]}."
+        )
+    orig_out_shape = (*x.shape[:-1], w_q.shape[-1])
+    x2 = x.reshape(-1, x.shape[-1])
+    if x2.dtype != torch.bfloat16:
+        x2 = x2.to(torch.bfloat16)
+    w_nk = _weight_nk(w_q)
+    k_dim, n_out = w_q.shape
+    rows = x2.shape[0]
+    if w_s.dim() == 1:
+        if w_s.shape[0] != n_out:
+            raise ValueError(f"per-channel scale has {w_s.shape[0]} entries, expected {n_out}")
+        ws = w_s.float().contiguous()
+        if w_nk.dtype == torch.int8:
+            xq, xs = ops.row_quant(x2, "int8")
+            out = ops.gemm(_capi.W8A8_PC, xq.view(torch.uint8), w_nk.view(torch.uint8),
+                           a_scale=xs, w_scale=ws, wfmt=1)
+        elif w_nk.dtype == torch.float8_e4m3fn:
+            if 0 < rows <= w8a16_max_rows:
+                out = ops.gemm(_capi.W8A16_PC, x2, w_nk.view(torch.uint8), w_scale=ws)
+            else:
+                xq, xs = ops.row_quant(x2, "fp8")
+                out = ops.gemm(_capi.W8A8_PC, xq.view(torch.uint8), w_nk.view(torch.uint8),
+                               a_scale=xs, w_scale=ws, wfmt=0)
+        else:
+            raise ValueError(f"Unsupported quantized dtype: {w_nk.dtype}")
+    else:
+        if w_nk.dtype != torch.float8_e4m3fn:
+            raise ValueError(f"blockwise kernels take float8_e4m3fn weights, got {w_nk.dtype}")
+        sb, bn = _scale_blocks(w_s, k_dim, n_out)
+        xq, xs = ops.row_quant(x2, "fp8", block=128)
+        out = ops.gemm(_capi.W8A8_BLK, xq.view(torch.uint8), w_nk.view(torch.uint8),
+                       a_scale=xs, w_scale=sb, ws_bn=bn)
+    return out.reshape(orig_out_shape)
+
+
+def quantized_matmul_fp4(x: torch.Tensor, w_q: torch.Tensor, w_s: torch.Tensor,
+                         bias: torch.Tensor | None = None) -> torch.Tensor:
+    """MXFP4 W4A16 dense linear, `linear_common.py:188-209, 242-255`.
+
+    ``w_q``: packed e2m1 codes, N-major ``[n_out, n_in/2]`` uint8 (the
+    checkpoint layout; low nibble = even k); ``w_s``: e8m0 bytes
+    ``[n_out, n_in/32]``. bf16 activations stay unquantized (block 32 is
+    below the reference's dequantize-after-matmul threshold), f32 accumulate.
+    """
+    if w_q.dim() != 2 or w_s.dim() != 2:
+        raise ValueError("quantized_matmul_fp4 expects w_q [n_out, n_in/2] and w_s [n_out, n_in/32]")
+    n_out = w_s.shape[0]
+    k_dim = x.shape[-1]
+    if w_q.shape != (n_out, k_dim // 2) or w_s.shape[1] * 32 != k_dim:
+        raise ValueError(
+            f"MXFP4 weight {tuple(w_q.shape)} / scale {tuple(w_s.shape)} do not match input dim {k_dim}"
+        )
+    x2 = x.reshape(-1, k_dim)
+    if x2.dtype != torch.bfloat16:
+        x2 = x2.to(torch.bfloat16)
+    out = ops.gemm(_capi.W4A16_MX, x2, w_q.view(torch.uint8).contiguous(),
+                   w_scale=w_s.view(torch.uint8).contiguous(), bias=bias)
+    return out.reshape(*x.shape[:-1], n_out)

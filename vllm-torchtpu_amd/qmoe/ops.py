@@ -1,0 +1,265 @@
+"""Torch-facing wrappers of the qmoe C ABI.
+
+Every function here takes device tensors (HIP), validates shapes / dtypes /
+layouts on the host, and launches the HIP kernels on the current stream via
+`_capi`. There is no CPU path: a CPU tensor is a ValueError.
+"""
+
+import ctypes
+import threading
+
+import torch
+
+from qmoe import _capi
+from qmoe._capi import GemmDesc, check, lib
+
+FP8 = torch.float8_e4m3fn
+
+_ACT_CODES = {
+    None: (_capi.ACT_NONE, 0.0, 0.0),
+    "silu": (_capi.ACT_SILU, 0.0, 0.0),
+    "swigluoai": (_capi.ACT_SWIGLUOAI, 1.702, 7.0),
+    "gelu": (_capi.ACT_GELU_TANH, 0.0, 0.0),  # jax.nn.gelu defaults to tanh form
+    "gelu_tanh": (_capi.ACT_GELU_TANH, 0.0, 0.0),
+    "silu_and_mul_with_clamp": (_capi.ACT_SILU_CLAMP, 10.0, 0.0),
+}
+
+
+def act_code(activation):
+    """Activation string (`kernels/megablox/gmm_v2.py:101-122`) -> code."""
+    if activation in _ACT_CODES:
+        return _ACT_CODES[activation]
+    if isinstance(activation, str) and activation.startswith("situ:"):
+        _, beta, lin = activation.split(":")
+        return _capi.ACT_SITU, float(beta), (-1.0 if lin == "none" else float(lin))
+    raise NotImplementedError(f"Unsupported activation function: {activation}")
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _stream(dev):
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _require_gpu(*ts):
+    for t in ts:
+        if t is not None and t.device.type != "cuda":
+            raise ValueError(f"qmoe kernels need device tensors, got a {t.device} tensor")
+
+
+def _bytes_view(t):
+    """1-byte code tensors (float8 / int8 / uint8 / packed fp4) as uint8."""
+    if t.element_size() != 1:
+        raise ValueError(f"expected a 1-byte code tensor, got {t.dtype}")
+    return t.view(torch.uint8)
+
+
+# ---------------------------------------------------------------- workspace
+
+_ws_lock = threading.Lock()
+_ws = {}
+
+
+def _workspace(dev, nbytes):
+    """Per-device zero-initialised workspace; its counter area stays zero
+    between calls (every kernel that uses it resets its counters)."""
+    if nbytes <= 0:
+        return None, 0
+    key = (dev.type, dev.index)
+    with _ws_lock:
+        cur = _ws.get(key)
+        if cur is None or cur.numel() < nbytes:
+            cur = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
+            _ws[key] = cur
+    return cur, cur.numel()
+
+
+# ---------------------------------------------------------------- row quant
+
+
+def row_quant(x, qdtype="fp8", block=None, mode="runtime"):
+    """Quantize rows of ``x`` ([M, K] bf16, or f32 for mode="load").
+
+    mode "runtime": `kernels/quantized_matmul/util.py:294-318` semantics
+    (scale = absmax / qmax; fp8 in f32, int8 in bf16 arithmetic; zero scale
+    -> 1). mode "load": `layers/core/quantization.py:232-318` (reciprocal
+    multiply; zero rows keep scale 0). Returns (codes [M, K] float8_e4m3fn or
+    int8, scales f32 [M] or [M, K/128]).
+    """
+    _require_gpu(x)
+    if x.dim() != 2:
+        raise ValueError(f"row_quant expects a 2-D tensor, got {tuple(x.shape)}")
+    if x.stride(-1) != 1:
+        x = x.contiguous()
+    M, K = x.shape
+    in_f32 = x.dtype == torch.float32
+    if not in_f32 and x.dtype != torch.bfloat16:
+        raise ValueError(f"row_quant expects bf16 (or f32 at load time), got {x.dtype}")
+    qd = {"fp8": 0, "int8": 1}[qdtype]
+    md = {"runtime": 0, "load": 1}[mode]
+    blk = 0 if block is None else int(block)
+    q = torch.empty((M, K), dtype=FP8 if qd == 0 else torch.int8, device=x.device)
+    ns = 1 if blk == 0 else K // blk
+    s = torch.empty((M, ns), dtype=torch.float32, device=x.device)
+    if M:
+        check(lib.qmoe_row_quant(_ptr(x), x.stride(0), int(in_f32), M, K, qd, md, blk, _ptr(q), K,
+                                 _ptr(s), ns, _stream(x.device)), "row_quant")
+    return q, (s[:, 0] if blk == 0 else s)
+
+
+# ---------------------------------------------------------------- GEMM
+
+
+def gemm(kind, a, w, *, a_scale=None, w_scale=None, bias=None, wfmt=0, ws_bn=1,
+         group_offs=None, active=None, num_active=None, slots=1, max_rows=None, a_rows=None,
+         activation=None, row_weight=None, out=None, y_rows=None, M=None):
+    """Run one (grouped) quantized GEMM through `qmoe_gemm`.
+
+    a        : [rows, K] activation codes (1 byte) or bf16
+    w        : [G, N, K] / [N, K] weights (1 byte codes, packed e2m1 [.., K/2], bf16)
+    w_scale  : per-channel f32 [G, N] | block f32 [G, N/bn, K/128] | e8m0 u8 [G, N, K/32]
+    Returns ``out`` ([M, N or N/2] bf16 unless given).
+    """
+    _require_gpu(a, w)
+    dev = a.device
+    if w.dim() == 2:
+        w = w.unsqueeze(0)
+    G, N, wcols = w.shape
+    if a.stride(-1) != 1 or w.stride(-1) != 1 or w.stride(1) != wcols:
+        raise ValueError("qmoe gemm needs K-contiguous activations and N-major [G, N, K] weights")
+    abf16 = kind in (_capi.W8A16_PC, _capi.W4A16_MX, _capi.W16A16)
+    K = a.shape[1]
+    if kind == _capi.W4A16_MX:
+        if wcols * 2 != K:
+            raise ValueError(f"packed e2m1 weight has {wcols} bytes per row, expected K/2 = {K // 2}")
+    elif wcols != K:
+        raise ValueError(f"Input hidden dim {K} must match weight hidden dim {wcols}.")
+    if abf16 and a.dtype != torch.bfloat16:
+        raise ValueError(f"this kind takes bf16 activations, got {a.dtype}")
+    if M is None:
+        M = a.shape[0] if a_rows is None else a_rows.shape[0]
+    act, p0, p1 = act_code(activation)
+    nout = N // 2 if act != _capi.ACT_NONE else N
+    if out is None:
+        out = torch.empty((M, nout), dtype=torch.bfloat16, device=dev)
+    d = GemmDesc()
+    d.kind = kind
+    d.wfmt = wfmt
+    d.a = a.data_ptr()
+    d.lda = a.stride(0)
+    if a_scale is not None:
+        d.a_scale = a_scale.data_ptr()
+        d.lds_a = a_scale.stride(0) if a_scale.dim() == 2 else 1
+    d.a_rows = a_rows.data_ptr() if a_rows is not None else None
+    d.w = w.data_ptr()
+    d.ldw = w.stride(1) * w.element_size()
+    d.w_gstride = w.stride(0) * w.element_size()
+    if w_scale is not None:
+        ws = w_scale
+        if kind in (_capi.W8A8_PC, _capi.W8A16_PC):
+            ws = ws.reshape(G, N)
+            d.ldws, d.ws_gstride = 1, ws.stride(0)
+        else:
+            if ws.dim() == 2:
+                ws = ws.unsqueeze(0)
+            d.ldws, d.ws_gstride = ws.stride(1), ws.stride(0)
+        d.w_scale = ws.data_ptr()
+    d.ws_bn = ws_bn
+    if bias is not None:
+        b = bias.reshape(G, N)
+        if b.dtype != torch.float32:
+            raise ValueError("bias must be float32 [G, N]")
+        d.bias, d.bias_gstride = b.data_ptr(), b.stride(0)
+    d.group_offs = group_offs.data_ptr() if group_offs is not None else None
+    d.active = active.data_ptr() if active is not None else None
+    d.num_active = num_active.data_ptr() if num_active is not None else None
+    d.slots = slots
+    d.max_rows = max_rows if max_rows is not None else M
+    d.M, d.N, d.K = M, N, K
+    d.act, d.act_p0, d.act_p1 = act, p0, p1
+    d.row_weight = row_weight.data_ptr() if row_weight is not None else None
+    d.y = out.data_ptr()
+    d.ldy = out.stride(0)
+    d.y_rows = y_rows.data_ptr() if y_rows is not None else None
+    need = ctypes.c_int64(0)
+    check(lib.qmoe_gemm_workspace_size(ctypes.byref(d), ctypes.byref(need)), "gemm (plan)")
+    ws_t, ws_n = _workspace(dev, need.value)
+    check(lib.qmoe_gemm(ctypes.byref(d), _ptr(ws_t), ws_n, _stream(dev)), "gemm")
+    return out
+
+
+# ---------------------------------------------------------------- MoE
+
+
+_SCORING = {"softmax": 0, "sigmoid": 1, "sqrtsoftplus": 2, "none": 3}
+
+
+def moe_route(router_logits, topk, scoring_func="softmax", renormalize=True, bias=None,
+              routed_scaling_factor=1.0, num_expert_group=1, topk_group=1, weights_f32=False):
+    """Router on the GPU: (bf16 (or f32) weights [T, k], int32 ids [T, k]).
+
+    scoring_func "none" takes the input as scores (rowmax top-k only)."""
+    _require_gpu(router_logits, bias)
+    if scoring_func not in _SCORING:
+        raise NotImplementedError(f"FusedMoE does not support {scoring_func} scoring function for TPU.")
+    x = router_logits.reshape(-1, router_logits.shape[-1])
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        x = x.float()
+    x = x.contiguous()
+    T, E = x.shape
+    if topk > E:
+        raise ValueError(f"topk k={topk} exceeds the expert count {E}")
+    w = torch.empty((T, topk), dtype=torch.float32 if weights_f32 else torch.bfloat16,
+                    device=x.device)
+    ids = torch.empty((T, topk), dtype=torch.int32, device=x.device)
+    b = bias.float().contiguous() if bias is not None else None
+    check(lib.qmoe_moe_route(_ptr(x), int(x.dtype == torch.float32), T, E, topk,
+                             _SCORING[scoring_func], _ptr(b), int(bool(renormalize)),
+                             float(routed_scaling_factor), int(num_expert_group or 1),
+                             int(topk_group or 1), _ptr(w), int(bool(weights_f32)), _ptr(ids),
+                             _stream(x.device)),
+          "moe_route")
+    return w, ids
+
+
+def moe_dispatch(topk_ids, topk_weights, num_experts, skip_padded_tokens=False):
+    """Permutation metadata (see include/qmoe.h `qmoe_moe_dispatch`)."""
+    _require_gpu(topk_ids, topk_weights)
+    T, k = topk_ids.shape
+    dev = topk_ids.device
+    ids = topk_ids.to(torch.int32).contiguous()
+    wts = topk_weights.to(torch.bfloat16).contiguous()
+    nf = T * k
+    i32 = dict(dtype=torch.int32, device=dev)
+    meta = dict(
+        sorted_idx=torch.empty(nf, **i32),
+        revert=torch.empty(nf, **i32),
+        token_sorted=torch.empty(nf, **i32),
+        group_offs=torch.empty(num_experts + 1, **i32),
+        active=torch.empty(max(1, min(num_experts, nf)), **i32),
+        num_active=torch.empty(1, **i32),
+        sorted_weight=torch.empty(nf, dtype=torch.bfloat16, device=dev),
+    )
+    check(lib.qmoe_moe_dispatch(_ptr(ids), _ptr(wts), T, k, num_experts, int(bool(skip_padded_tokens)),
+                                _ptr(meta["sorted_idx"]), _ptr(meta["revert"]),
+                                _ptr(meta["token_sorted"]), _ptr(meta["group_offs"]),
+                                _ptr(meta["active"]), _ptr(meta["num_active"]),
+                                _ptr(meta["sorted_weight"]), _stream(dev)), "moe_dispatch")
+    return meta
+
+
+def moe_combine(rows, topk_ids, topk_weights, skip_padded_tokens=False, out=None):
+    """Sum each token's k weighted route rows ([T*k, H] bf16) -> [T, H] bf16."""
+    _require_gpu(rows, topk_ids, topk_weights)
+    T, k = topk_ids.shape
+    H = rows.shape[1]
+    if out is None:
+        out = torch.empty((T, H), dtype=torch.bfloat16, device=rows.device)
+    ids = topk_ids.to(torch.int32).contiguous()
+    wts = topk_weights.to(torch.bfloat16).contiguous()
+    check(lib.qmoe_moe_combine(_ptr(rows), _ptr(ids), _ptr(wts), T, k, H,
+                               int(bool(skip_padded_tokens)), _ptr(out), out.stride(0),
+                               _stream(rows.device)), "moe_combine")
+    return out
