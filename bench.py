@@ -54,13 +54,19 @@ def parse():
 # ------------------------------------------------------------------ timing
 
 
-def graph_time_us(fn, iters=50, warm=3):
-    """Median device time (us) of fn() replayed from a CUDA (HIP) graph."""
+def graph_time_us(fn, iters=20, warm=3, target_us=2000.0, max_reps=64):
+    """Device time (us) per call of fn(): `reps` back-to-back calls are
+    captured in ONE HIP graph (so per-launch host cost and graph-launch
+    latency are amortised away, inter-kernel gaps inside the graph are kept),
+    the graph is replayed `iters` times, and the median replay time / reps is
+    returned (with p10 / p90)."""
     import torch
 
     for _ in range(warm):
         fn()
     torch.cuda.synchronize()
+    est = event_time_us(fn, iters=3, warm=0)[0]
+    reps = int(max(1, min(max_reps, target_us / max(est, 1.0))))
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     g = torch.cuda.CUDAGraph()
@@ -68,18 +74,20 @@ def graph_time_us(fn, iters=50, warm=3):
         fn()  # allocations of the first call happen outside the capture
         torch.cuda.synchronize()
         with torch.cuda.graph(g, stream=s):
-            fn()
+            for _ in range(reps):
+                fn()
+    torch.cuda.synchronize()
+    g.replay()
     torch.cuda.synchronize()
     times = []
     st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    reps = max(1, min(20, int(2000 / max(1, iters))))
     for _ in range(iters):
         st.record()
-        for _ in range(reps):
-            g.replay()
+        g.replay()
         en.record()
         en.synchronize()
         times.append(st.elapsed_time(en) * 1e3 / reps)
+    del g
     return float(np.median(times)), float(np.percentile(times, 10)), float(np.percentile(times, 90))
 
 

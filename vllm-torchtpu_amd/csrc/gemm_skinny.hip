@@ -1,27 +1,33 @@
-// Skinny (decode) grouped GEMM: at most 64 rows per group, weights streamed
-// from HBM exactly once.
+// Skinny (decode) grouped GEMM: few rows per group, weights streamed from HBM
+// exactly once.
 //
 // Small-M linears and decode MoE are weight-bandwidth bound, so the design
 // goal is to keep enough 16-byte weight loads in flight to saturate HBM3E:
 //  * workgroup = 4 wavefronts; it owns 32 weight rows (two 16-row MFMA
 //    B tiles, or one 16-column gate tile + the matching up tile when an
 //    activation is fused) and a slice of K;
-//  * K is cut into 128-wide steps; the steps of the workgroup's slice are
-//    dealt out to its 4 wavefronts, and further across `ksplit` workgroups
-//    (a split-K reduction through a float32 workspace, finished by the last
-//    workgroup to arrive, in a fixed order, so results are deterministic);
-//  * in a step, lane l reads 32 consecutive k values of weight row (l & 15)
-//    (32 B of e4m3/int8, 16 B of e2m1, 64 B of bf16) and 32 k values of
-//    activation row (l & 15) of each 16-row M tile, and issues the matching
-//    MFMA(s): one v_mfma_scale_f32_16x16x128_f8f6f4 (e4m3), two
-//    v_mfma_i32_16x16x64_i8 (int8) or four v_mfma_f32_16x16x32_bf16 (bf16
-//    activations; e2m1 weights are expanded with v_cvt_scalef32_pk_bf16_fp4,
-//    which also applies the e8m0 block scale, e4m3 with v_cvt_pk_f32_fp8).
-//    A and W use the same lane -> k assignment, so the products pair up
-//    correctly whatever order the MFMA unit walks k in.
-// Rows beyond the group's count and k beyond K are fed as zeros.
+//  * K is cut into 128-wide steps; the workgroup's steps are dealt out to its
+//    4 wavefronts, and further across `ksplit` workgroups (grid.y);
+//  * a wavefront issues the loads of U steps back to back, unconditionally
+//    (weight rows past N and activation rows past the group are clamped to
+//    valid rows -- they only feed outputs that are never stored), and only
+//    then waits and issues the MFMAs, so U steps of weights are in flight
+//    per wavefront. Only a K tail (K % 128 != 0) uses masked loads;
+//  * in a step, lane l holds 32 consecutive k values of weight row (l & 15)
+//    (32 B of e4m3/int8, 16 B of e2m1, 64 B of bf16) and of activation row
+//    (l & 15) of each 16-row M tile, and issues the matching MFMA(s): one
+//    v_mfma_scale_f32_16x16x128_f8f6f4 (e4m3), two v_mfma_i32_16x16x64_i8
+//    (int8) or four v_mfma_f32_16x16x32_bf16 (bf16 activations; e2m1 weights
+//    are expanded with v_cvt_scalef32_pk_bf16_fp4, which also applies the e8m0
+//    block scale; e4m3 with v_cvt_pk_f32_fp8). A and W use the same
+//    lane -> k assignment, so products pair up whatever order the MFMA walks k;
+//  * the 4 wavefronts' sums are added in LDS in a fixed order; with
+//    ksplit > 1 each workgroup stores its raw sums to a float32 workspace and
+//    a second kernel adds the slices in order and runs the epilogue (kernel
+//    boundaries order the memory traffic, so no cache-flushing fence runs).
 
 #include <algorithm>
+#include <cstdlib>
 #include <type_traits>
 
 #include "gemm_common.h"
@@ -40,17 +46,27 @@ template <int KIND, int WF>
 struct Traits {
   static constexpr bool kAbf16 = KIND == QK_W8A16_PC || KIND == QK_W4A16_MX || KIND == QK_W16A16;
   static constexpr bool kInt = KIND == QK_W8A8_PC && WF == 1;
-  // weight bytes per lane per 128-k step (32 k values)
+  // bytes per lane per 128-k step (32 k values)
   static constexpr int kWBytes = KIND == QK_W4A16_MX ? 16 : (KIND == QK_W16A16 ? 64 : 32);
   static constexpr int kABytes = kAbf16 ? 64 : 32;
 };
 
+// 128-k steps per pipeline chunk (two chunks are in flight per wavefront)
+int default_unroll(int kind, int ms) {
+  if (ms > 1) return 1;
+  return kind == QK_W16A16 ? 1 : 2;
+}
+
 template <int NB>
-__device__ __forceinline__ void load_frag(Frag& f, const uint8_t* p, bool ok) {
+__device__ __forceinline__ void ld(Frag& f, const uint8_t* p) {
 #pragma unroll
-  for (int i = 0; i < NB / 16; ++i) {
-    f.v[i] = ok ? reinterpret_cast<const uint4*>(p)[i] : make_uint4(0, 0, 0, 0);
-  }
+  for (int i = 0; i < NB / 16; ++i) f.v[i] = reinterpret_cast<const uint4*>(p)[i];
+}
+
+template <int NB>
+__device__ __forceinline__ void ld_masked(Frag& f, const uint8_t* p, bool ok) {
+#pragma unroll
+  for (int i = 0; i < NB / 16; ++i) f.v[i] = ok ? reinterpret_cast<const uint4*>(p)[i] : make_uint4(0, 0, 0, 0);
 }
 
 __device__ __forceinline__ i32x8 as_i32x8(const Frag& f) {
@@ -73,15 +89,14 @@ __device__ __forceinline__ bf16x8 as_bf16x8(const uint4& u) {
 }
 
 // 8 e2m1 codes (one dword, low nibble first) -> 8 bf16 times 2^(e-127)
-__device__ __forceinline__ bf16x8 fp4x8_to_bf16(uint32_t d, float scale) {
+__device__ __forceinline__ uint4 fp4x8_to_bf16(uint32_t d, float scale) {
   bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, scale, 0);
   bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, scale, 1);
   bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, scale, 2);
   bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, scale, 3);
-  bf16x8 r;
-  r[0] = p0[0]; r[1] = p0[1]; r[2] = p1[0]; r[3] = p1[1];
-  r[4] = p2[0]; r[5] = p2[1]; r[6] = p3[0]; r[7] = p3[1];
-  return r;
+  union { bf16x2 b; uint32_t u; } c0, c1, c2, c3;
+  c0.b = p0; c1.b = p1; c2.b = p2; c3.b = p3;
+  return make_uint4(c0.u, c1.u, c2.u, c3.u);
 }
 
 // 4 e4m3 codes (one dword) -> 4 bf16 bit patterns packed in two dwords
@@ -101,7 +116,79 @@ struct Acc {
   T v[MS][kNSub];
 };
 
-__device__ __forceinline__ float ldf(const float* p) { return *p; }
+// Per-step side data: per-(row, block) and per-(n, block) scales (W8A8_BLK),
+// e8m0 block scale of the lane's weight row (W4A16_MX).
+template <int MS>
+struct StepScales {
+  float sa[MS][4];
+  float sb[kNSub];
+};
+
+// One 128-k step of MFMAs for all (M tile, weight tile) pairs.
+template <int KIND, int WF, int MS>
+__device__ __forceinline__ void mma_step(Acc<KIND, WF, MS>& acc, const Frag (&fa)[MS],
+                                         const Frag (&bw)[kNSub], const StepScales<MS>& sc) {
+  if constexpr (KIND == QK_W8A8_PC && WF == 0) {
+#pragma unroll
+    for (int ms = 0; ms < MS; ++ms)
+#pragma unroll
+      for (int s = 0; s < kNSub; ++s)
+        acc.v[ms][s] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+            as_i32x8(fa[ms]), as_i32x8(bw[s]), acc.v[ms][s], 0, 0, 0, 127, 0, 127);
+  } else if constexpr (KIND == QK_W8A8_PC && WF == 1) {
+#pragma unroll
+    for (int ms = 0; ms < MS; ++ms)
+#pragma unroll
+      for (int s = 0; s < kNSub; ++s) {
+        acc.v[ms][s] = __builtin_amdgcn_mfma_i32_16x16x64_i8(as_i32x4(fa[ms].v[0]), as_i32x4(bw[s].v[0]),
+                                                             acc.v[ms][s], 0, 0, 0);
+        acc.v[ms][s] = __builtin_amdgcn_mfma_i32_16x16x64_i8(as_i32x4(fa[ms].v[1]), as_i32x4(bw[s].v[1]),
+                                                             acc.v[ms][s], 0, 0, 0);
+      }
+  } else if constexpr (KIND == QK_W8A8_BLK) {
+    // one 128-k step == one scale block: scale the block's dot, then add
+#pragma unroll
+    for (int ms = 0; ms < MS; ++ms)
+#pragma unroll
+      for (int s = 0; s < kNSub; ++s) {
+        f32x4 d = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(as_i32x8(fa[ms]), as_i32x8(bw[s]),
+                                                                   f32x4{0, 0, 0, 0}, 0, 0, 0, 127, 0, 127);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc.v[ms][s][r] += d[r] * (sc.sa[ms][r] * sc.sb[s]);
+      }
+  } else {
+    // bf16 activations: expand the weight fragment to 4 x 8 bf16
+    uint4 wb[kNSub][4];
+#pragma unroll
+    for (int s = 0; s < kNSub; ++s) {
+      if constexpr (KIND == QK_W16A16) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) wb[s][q] = bw[s].v[q];
+      } else if constexpr (KIND == QK_W8A16_PC) {
+        const uint32_t d[8] = {bw[s].v[0].x, bw[s].v[0].y, bw[s].v[0].z, bw[s].v[0].w,
+                               bw[s].v[1].x, bw[s].v[1].y, bw[s].v[1].z, bw[s].v[1].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint2 lo = fp8x4_to_bf16(d[2 * q]);
+          const uint2 hi = fp8x4_to_bf16(d[2 * q + 1]);
+          wb[s][q] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+        }
+      } else {  // QK_W4A16_MX
+        const uint32_t d[4] = {bw[s].v[0].x, bw[s].v[0].y, bw[s].v[0].z, bw[s].v[0].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) wb[s][q] = fp4x8_to_bf16(d[q], sc.sb[s]);
+      }
+    }
+#pragma unroll
+    for (int ms = 0; ms < MS; ++ms)
+#pragma unroll
+      for (int s = 0; s < kNSub; ++s)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          acc.v[ms][s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(fa[ms].v[q]), as_bf16x8(wb[s][q]),
+                                                                 acc.v[ms][s], 0, 0, 0);
+  }
+}
 
 // Per-format scale + bias for one accumulator element (before activation).
 template <int KIND>
@@ -122,47 +209,30 @@ __device__ __forceinline__ void store_out(const GemmParams& p, int g, int R, int
                                           int n0, int n1, float v0, float v1) {
   float out;
   if (ACT) {
-    float gte = finish_elem<KIND>(p, v0, arow, g, n0);
-    float up = finish_elem<KIND>(p, v1, arow, g, n1);
+    const float gte = finish_elem<KIND>(p, v0, arow, g, n0);
+    const float up = finish_elem<KIND>(p, v1, arow, g, n1);
     out = qmoe_act(p.act, gte, up, p.act_p0, p.act_p1);
   } else {
     out = finish_elem<KIND>(p, v0, arow, g, n0);
   }
   if (p.row_weight) out *= bf16_to_f32(p.row_weight[R]);
-  int64_t yr = p.y_rows ? p.y_rows[R] : R;
+  const int64_t yr = p.y_rows ? p.y_rows[R] : R;
   p.y[yr * p.ldy + ncol_out] = f32_to_bf16(out);
 }
 
-template <int KIND, int WF, int MS, bool ACT>
-__device__ __forceinline__ void epilogue_pass(const GemmParams& p, const Acc<KIND, WF, MS>& acc, int g,
-                                              int row0, int rows, int mp, int kg, int col, int tile,
-                                              const int (&nw)[kNSub], const bool (&nok)[kNSub]) {
-#pragma unroll
-  for (int ms = 0; ms < MS; ++ms)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int rr = mp + ms * 16 + kg * 4 + r;
-      if (rr >= rows) continue;
-      const int R = row0 + rr;
-      const int ar = p.a_rows ? p.a_rows[R] : R;
-      float v0, v1;
-      if constexpr (Traits<KIND, WF>::kInt) {
-        v0 = (float)acc.v[ms][0][r];
-        v1 = (float)acc.v[ms][1][r];
-      } else {
-        v0 = acc.v[ms][0][r];
-        v1 = acc.v[ms][1][r];
-      }
-      if (ACT) {
-        if (nok[0]) store_out<KIND, true>(p, g, R, ar, tile * 16 + col, nw[0], nw[1], v0, v1);
-      } else {
-        if (nok[0]) store_out<KIND, false>(p, g, R, ar, nw[0], nw[0], 0, v0, 0.0f);
-        if (nok[1]) store_out<KIND, false>(p, g, R, ar, nw[1], nw[1], 0, v1, 0.0f);
-      }
-    }
+// group of this workgroup's slot; false if the slot is empty
+__device__ __forceinline__ bool slot_group(const GemmParams& p, int slot, int& g, int& row0, int& rows) {
+  g = slot;
+  if (p.active) {
+    if (slot >= *p.num_active) return false;
+    g = p.active[slot];
+  }
+  row0 = p.group_offs ? p.group_offs[g] : 0;
+  rows = p.group_offs ? p.group_offs[g + 1] - row0 : p.M;
+  return rows > 0;
 }
 
-template <int KIND, int WF, int MS, bool ACT>
+template <int KIND, int WF, int MS, bool ACT, int U>
 __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(const GemmParams p) {
   using Tr = Traits<KIND, WF>;
   const int lane = threadIdx.x & 63;
@@ -170,37 +240,43 @@ __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(const GemmParams 
   const int col = lane & 15;
   const int kg = lane >> 4;
 
-  const int slot = blockIdx.z;
-  int g = slot;
-  if (p.active) {
-    if (slot >= *p.num_active) return;
-    g = p.active[slot];
-  }
-  const int row0 = p.group_offs ? p.group_offs[g] : 0;
-  const int rows = p.group_offs ? p.group_offs[g + 1] - row0 : p.M;
-  if (rows <= 0) return;
+  int g, row0, rows;
+  if (!slot_group(p, blockIdx.z, g, row0, rows)) return;
 
-  // weight rows of the two B tiles
+  // weight rows of the two B tiles (clamped copies feed the loads)
   const int tile = blockIdx.x;
+  const int nlim = ACT ? (p.N >> 1) : p.N;
   int nw[kNSub];
+  bool nok[kNSub];
   if (ACT) {
-    nw[0] = tile * 16 + col;
-    nw[1] = (p.N >> 1) + tile * 16 + col;
+    const int c = tile * 16 + col;
+    nok[0] = nok[1] = c < nlim;
+    nw[0] = c;
+    nw[1] = (p.N >> 1) + c;
   } else {
     nw[0] = tile * 32 + col;
     nw[1] = tile * 32 + 16 + col;
+    nok[0] = nw[0] < nlim;
+    nok[1] = nw[1] < nlim;
   }
-  const int nlim = ACT ? (p.N >> 1) : p.N;
-  bool nok[kNSub];
-  nok[0] = (ACT ? tile * 16 + col : nw[0]) < nlim;
-  nok[1] = ACT ? nok[0] : nw[1] < nlim;
-
   const uint8_t* wg = p.w + (int64_t)g * p.w_gstride;
-  const int KS = (p.K + 127) >> 7;
+  const uint8_t* wrow[kNSub];
+  int nclamp[kNSub];
+#pragma unroll
+  for (int s = 0; s < kNSub; ++s) {
+    nclamp[s] = nok[s] ? nw[s] : (ACT ? (s == 0 ? nlim - 1 : p.N - 1) : p.N - 1);
+    wrow[s] = wg + (int64_t)nclamp[s] * p.ldw + kg * Tr::kWBytes;
+  }
+
+  // K steps: KSF full 128-wide steps, plus a tail step when K % 128 != 0
+  const int KSF = p.K >> 7;
+  const bool tail = (p.K & 127) != 0;
+  const int KS = KSF + (tail ? 1 : 0);
   const int nsl = p.ksplit * kWaves;
   const int sl = blockIdx.y * kWaves + wave;
   const int ks0 = (int)((int64_t)KS * sl / nsl);
   const int ks1 = (int)((int64_t)KS * (sl + 1) / nsl);
+  const int kf1 = min(ks1, KSF);
 
   const uint8_t* abase = static_cast<const uint8_t*>(p.a);
   const int64_t lda_b = p.lda * (Tr::kAbf16 ? 2 : 1);
@@ -211,15 +287,22 @@ __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(const GemmParams 
   // Rows are taken 16*MS at a time (one pass when the host's row bound
   // holds; more passes re-read this workgroup's weight slice from cache).
   for (int mp = 0; mp < rows; mp += 16 * MS) {
-    // activation rows of this lane, per M tile
-    int arow[MS];
-    bool aok[MS];
+    const uint8_t* arowp[MS];
+    int arow4[MS][4];  // physical A rows of the 4 accumulator rows (block scales)
 #pragma unroll
     for (int ms = 0; ms < MS; ++ms) {
       const int r = mp + ms * 16 + col;
-      aok[ms] = r < rows;
-      const int R = row0 + (aok[ms] ? r : 0);
-      arow[ms] = p.a_rows ? p.a_rows[R] : R;
+      const int R = row0 + (r < rows ? r : 0);
+      const int ar = p.a_rows ? p.a_rows[R] : R;
+      arowp[ms] = abase + (int64_t)ar * lda_b + kg * Tr::kABytes;
+      if constexpr (KIND == QK_W8A8_BLK) {
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const int rr = mp + ms * 16 + kg * 4 + r4;
+          const int R2 = row0 + (rr < rows ? rr : 0);
+          arow4[ms][r4] = p.a_rows ? p.a_rows[R2] : R2;
+        }
+      }
     }
 
     Acc<KIND, WF, MS> acc;
@@ -228,110 +311,83 @@ __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(const GemmParams 
 #pragma unroll
       for (int s = 0; s < kNSub; ++s) acc.v[ms][s] = {0, 0, 0, 0};
 
-    for (int ks = ks0; ks < ks1; ++ks) {
-      const int k0 = ks * 128 + kg * 32;
-      const bool kok = k0 < p.K;
-      Frag bw[kNSub];
+    auto load_scales = [&](int ks, StepScales<MS>& sc) {
+      if constexpr (KIND == QK_W8A8_BLK) {
 #pragma unroll
-      for (int s = 0; s < kNSub; ++s) {
-        const int64_t off = (int64_t)nw[s] * p.ldw + (int64_t)k0 * Tr::kWBytes / 32;
-        load_frag<Tr::kWBytes>(bw[s], wg + off, kok && nok[s]);
-      }
-      Frag fa[MS];
+        for (int s = 0; s < kNSub; ++s)
+          sc.sb[s] = static_cast<const float*>(p.w_scale)[(int64_t)g * p.ws_gstride +
+                                                          (int64_t)(nclamp[s] / p.ws_bn) * p.ldws + ks];
 #pragma unroll
-      for (int ms = 0; ms < MS; ++ms) {
-        const int64_t off = (int64_t)arow[ms] * lda_b + (int64_t)k0 * Tr::kABytes / 32;
-        load_frag<Tr::kABytes>(fa[ms], abase + off, kok && aok[ms]);
+        for (int ms = 0; ms < MS; ++ms)
+#pragma unroll
+          for (int r4 = 0; r4 < 4; ++r4) sc.sa[ms][r4] = p.a_scale[(int64_t)arow4[ms][r4] * p.lds_a + ks];
+      } else if constexpr (KIND == QK_W4A16_MX) {
+#pragma unroll
+        for (int s = 0; s < kNSub; ++s)
+          sc.sb[s] = e8m0_to_f32(static_cast<const uint8_t*>(p.w_scale)[(int64_t)g * p.ws_gstride +
+                                                                        (int64_t)nclamp[s] * p.ldws + ks * 4 + kg]);
       }
+    };
 
-      if constexpr (KIND == QK_W8A8_PC && WF == 0) {
+    // Full steps, U at a time, double-buffered: the loads of chunk c+1 are
+    // issued before the MFMAs of chunk c, so 1-2 chunks are always in flight.
+    // Step indices past the slice are clamped to its last step (the
+    // duplicate loads hit cache; their MFMAs are skipped).
+    struct Chunk {
+      Frag bw[U][kNSub];
+      Frag fa[U][MS];
+      StepScales<MS> sc[U];
+    };
+    auto issue = [&](int ks, Chunk& c) {
 #pragma unroll
-        for (int ms = 0; ms < MS; ++ms)
+      for (int u = 0; u < U; ++u) {
+        const int kk = min(ks + u, kf1 - 1);
 #pragma unroll
-          for (int s = 0; s < kNSub; ++s)
-            acc.v[ms][s] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-                as_i32x8(fa[ms]), as_i32x8(bw[s]), acc.v[ms][s], 0, 0, 0, 127, 0, 127);
-      } else if constexpr (KIND == QK_W8A8_PC && WF == 1) {
+        for (int s = 0; s < kNSub; ++s) ld<Tr::kWBytes>(c.bw[u][s], wrow[s] + (int64_t)kk * (4 * Tr::kWBytes));
 #pragma unroll
-        for (int ms = 0; ms < MS; ++ms)
+        for (int ms = 0; ms < MS; ++ms) ld<Tr::kABytes>(c.fa[u][ms], arowp[ms] + (int64_t)kk * (4 * Tr::kABytes));
+        load_scales(kk, c.sc[u]);
+      }
+    };
+    auto consume = [&](int ks, const Chunk& c) {
 #pragma unroll
-          for (int s = 0; s < kNSub; ++s) {
-            acc.v[ms][s] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
-                as_i32x4(fa[ms].v[0]), as_i32x4(bw[s].v[0]), acc.v[ms][s], 0, 0, 0);
-            acc.v[ms][s] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
-                as_i32x4(fa[ms].v[1]), as_i32x4(bw[s].v[1]), acc.v[ms][s], 0, 0, 0);
-          }
-      } else if constexpr (KIND == QK_W8A8_BLK) {
-        // one 128-k step == one scale block: scale the block's dot, then add
-        const int kb = ks;
-        float sb[kNSub];
-#pragma unroll
-        for (int s = 0; s < kNSub; ++s) {
-          const int nn = nok[s] ? nw[s] : 0;
-          sb[s] = static_cast<const float*>(p.w_scale)[(int64_t)g * p.ws_gstride +
-                                                       (int64_t)(nn / p.ws_bn) * p.ldws + kb];
-        }
-#pragma unroll
-        for (int ms = 0; ms < MS; ++ms) {
-          float sa[4];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int rr = mp + ms * 16 + kg * 4 + r;
-            const int R = row0 + (rr < rows ? rr : 0);
-            const int ar = p.a_rows ? p.a_rows[R] : R;
-            sa[r] = p.a_scale[(int64_t)ar * p.lds_a + kb];
-          }
-#pragma unroll
-          for (int s = 0; s < kNSub; ++s) {
-            f32x4 d = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-                as_i32x8(fa[ms]), as_i32x8(bw[s]), f32x4{0, 0, 0, 0}, 0, 0, 0, 127, 0, 127);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) acc.v[ms][s][r] += d[r] * (sa[r] * sb[s]);
-          }
-        }
-      } else {
-        // bf16 activations: expand the weight fragment to 4 x 8 bf16
-        uint4 wb[kNSub][4];
-#pragma unroll
-        for (int s = 0; s < kNSub; ++s) {
-          if constexpr (KIND == QK_W16A16) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) wb[s][q] = bw[s].v[q];
-          } else if constexpr (KIND == QK_W8A16_PC) {
-            uint32_t d[8] = {bw[s].v[0].x, bw[s].v[0].y, bw[s].v[0].z, bw[s].v[0].w,
-                             bw[s].v[1].x, bw[s].v[1].y, bw[s].v[1].z, bw[s].v[1].w};
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              uint2 lo = fp8x4_to_bf16(d[2 * q]);
-              uint2 hi = fp8x4_to_bf16(d[2 * q + 1]);
-              wb[s][q] = make_uint4(lo.x, lo.y, hi.x, hi.y);
-            }
-          } else {  // QK_W4A16_MX
-            const int nn = nok[s] ? nw[s] : 0;
-            const uint8_t* sp = static_cast<const uint8_t*>(p.w_scale) + (int64_t)g * p.ws_gstride +
-                                (int64_t)nn * p.ldws + (kok ? (k0 >> 5) : 0);
-            const float scl = e8m0_to_f32(*sp);
-            uint32_t d[4] = {bw[s].v[0].x, bw[s].v[0].y, bw[s].v[0].z, bw[s].v[0].w};
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              union { bf16x8 b; uint4 u; } c;
-              c.b = fp4x8_to_bf16(d[q], scl);
-              wb[s][q] = c.u;
-            }
-          }
-        }
-#pragma unroll
-        for (int ms = 0; ms < MS; ++ms)
-#pragma unroll
-          for (int s = 0; s < kNSub; ++s)
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-              acc.v[ms][s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                  as_bf16x8(fa[ms].v[q]), as_bf16x8(wb[s][q]), acc.v[ms][s], 0, 0, 0);
+      for (int u = 0; u < U; ++u)
+        if (ks + u < kf1) mma_step<KIND, WF, MS>(acc, c.fa[u], c.bw[u], c.sc[u]);
+    };
+    if (ks0 < kf1) {
+      Chunk ca, cb;
+      issue(ks0, ca);
+      for (int ks = ks0; ks < kf1; ks += 2 * U) {
+        const bool more = ks + U < kf1;
+        if (more) issue(ks + U, cb);
+        consume(ks, ca);
+        if (!more) break;
+        if (ks + 2 * U < kf1) issue(ks + 2 * U, ca);
+        consume(ks + U, cb);
       }
     }
+    // K tail: lanes whose 32 k values start past K feed zeros
+    if (tail && ks1 == KS && ks0 < ks1) {
+      const int kk = KSF;
+      const bool kok = kk * 128 + kg * 32 < p.K;
+      Frag bw[kNSub];
+      Frag fa[MS];
+      StepScales<MS> sc;
+#pragma unroll
+      for (int s = 0; s < kNSub; ++s) ld_masked<Tr::kWBytes>(bw[s], wrow[s] + (int64_t)kk * (4 * Tr::kWBytes), kok);
+#pragma unroll
+      for (int ms = 0; ms < MS; ++ms) ld_masked<Tr::kABytes>(fa[ms], arowp[ms] + (int64_t)kk * (4 * Tr::kABytes), kok);
+      if constexpr (KIND == QK_W4A16_MX) {
+#pragma unroll
+        for (int s = 0; s < kNSub; ++s)
+          sc.sb[s] = kok ? e8m0_to_f32(static_cast<const uint8_t*>(p.w_scale)[(int64_t)g * p.ws_gstride +
+                                                                              (int64_t)nclamp[s] * p.ldws + kk * 4 + kg])
+                         : 1.0f;
+      }
+      mma_step<KIND, WF, MS>(acc, fa, bw, sc);
+    }
 
-    // ---- reduce the 4 wavefronts' partial sums (fixed order) ----
+    // ---- reduce the 4 wavefronts' sums (fixed order) ----
     __syncthreads();  // the previous pass has finished reading `red`
     if (wave > 0) {
 #pragma unroll
@@ -347,83 +403,110 @@ __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(const GemmParams 
           }
     }
     __syncthreads();
-    if (wave == 0) {
+    if (wave != 0) continue;
 #pragma unroll
-      for (int w = 0; w < kWaves - 1; ++w)
+    for (int w = 0; w < kWaves - 1; ++w)
 #pragma unroll
-        for (int ms = 0; ms < MS; ++ms)
+      for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
-          for (int s = 0; s < kNSub; ++s)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              float v = red[w][(ms * kNSub + s) * 4 + r][lane];
-              if constexpr (Tr::kInt) acc.v[ms][s][r] += __float_as_int(v);
-              else acc.v[ms][s][r] += v;
-            }
-      if (p.ksplit > 1) {
-        // publish this slice's partial sums
-#pragma unroll
-        for (int ms = 0; ms < MS; ++ms)
+        for (int s = 0; s < kNSub; ++s)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const int rr = mp + ms * 16 + kg * 4 + r;
-            if (rr >= rows) continue;
-            const int64_t base = (int64_t)blockIdx.y * plane + (int64_t)(row0 + rr) * p.N;
-#pragma unroll
-            for (int s = 0; s < kNSub; ++s) {
-              if (!nok[s]) continue;
-              float v;
-              if constexpr (Tr::kInt) v = __int_as_float(acc.v[ms][s][r]);
-              else v = acc.v[ms][s][r];
-              p.partial[base + nw[s]] = v;
-            }
+            const float v = red[w][(ms * kNSub + s) * 4 + r][lane];
+            if constexpr (Tr::kInt) acc.v[ms][s][r] += __float_as_int(v);
+            else acc.v[ms][s][r] += v;
           }
-      } else {
-        epilogue_pass<KIND, WF, MS, ACT>(p, acc, g, row0, rows, mp, kg, col, tile, nw, nok);
-      }
-    }
-  }
-  if (wave > 0 || p.ksplit <= 1) return;
-
-  // ---- split-K: the last workgroup to arrive sums the slices in order ----
-  __threadfence();
-  uint32_t* ctr = p.counters + (int64_t)slot * gridDim.x + tile;
-  uint32_t prev = 0;
-  if (lane == 0) prev = atomicAdd(ctr, 1u);
-  prev = __shfl(prev, 0, 64);
-  if (prev != (uint32_t)(p.ksplit - 1)) return;
-  __threadfence();
-  for (int mp = 0; mp < rows; mp += 16 * MS) {
-    Acc<KIND, WF, MS> acc;
 #pragma unroll
     for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int rr = mp + ms * 16 + kg * 4 + r;
-        const int64_t rowoff = (int64_t)(row0 + (rr < rows ? rr : 0)) * p.N;
-#pragma unroll
-        for (int s = 0; s < kNSub; ++s) {
-          const int64_t idx = rowoff + (nok[s] ? nw[s] : 0);
-          if constexpr (Tr::kInt) {
-            int t = 0;
-            for (int j = 0; j < p.ksplit; ++j)
-              t += __float_as_int(__builtin_nontemporal_load(&p.partial[j * plane + idx]));
-            acc.v[ms][s][r] = t;
-          } else {
-            float t = 0.0f;
-            for (int j = 0; j < p.ksplit; ++j) t += __builtin_nontemporal_load(&p.partial[j * plane + idx]);
-            acc.v[ms][s][r] = t;
-          }
+        if (rr >= rows) continue;
+        const int R = row0 + rr;
+        float v0, v1;
+        if constexpr (Tr::kInt) {
+          v0 = __int_as_float(acc.v[ms][0][r]);
+          v1 = __int_as_float(acc.v[ms][1][r]);
+        } else {
+          v0 = acc.v[ms][0][r];
+          v1 = acc.v[ms][1][r];
+        }
+        if (p.ksplit > 1) {
+          // raw sums (int32 bit patterns for int8) for the reduce kernel
+          float* dst = p.partial + (int64_t)blockIdx.y * plane + (int64_t)R * p.N;
+          if (nok[0]) dst[nw[0]] = v0;
+          if (nok[1]) dst[nw[1]] = v1;
+          continue;
+        }
+        if constexpr (Tr::kInt) {
+          v0 = (float)acc.v[ms][0][r];
+          v1 = (float)acc.v[ms][1][r];
+        }
+        const int ar = p.a_rows ? p.a_rows[R] : R;
+        if (ACT) {
+          if (nok[0]) store_out<KIND, true>(p, g, R, ar, tile * 16 + col, nw[0], nw[1], v0, v1);
+        } else {
+          if (nok[0]) store_out<KIND, false>(p, g, R, ar, nw[0], nw[0], 0, v0, 0.0f);
+          if (nok[1]) store_out<KIND, false>(p, g, R, ar, nw[1], nw[1], 0, v1, 0.0f);
         }
       }
-    epilogue_pass<KIND, WF, MS, ACT>(p, acc, g, row0, rows, mp, kg, col, tile, nw, nok);
   }
-  if (lane == 0) *ctr = 0u;  // leave the counter ready for the next call
+}
+
+// Split-K finish: sum the ksplit slices in order, then the epilogue.
+// grid = (ceil(nout / 64), 1, slots); thread = one output column, rows
+// strided over the 4 wavefronts.
+template <int KIND, int WF, bool ACT>
+__global__ __launch_bounds__(kThreads) void skinny_reduce_kernel(const GemmParams p) {
+  using Tr = Traits<KIND, WF>;
+  int g, row0, rows;
+  if (!slot_group(p, blockIdx.z, g, row0, rows)) return;
+  const int nout = ACT ? p.N / 2 : p.N;
+  const int c = blockIdx.x * 64 + (threadIdx.x & 63);
+  if (c >= nout) return;
+  const int64_t plane = (int64_t)p.M * p.N;
+  for (int r = threadIdx.x >> 6; r < rows; r += kWaves) {
+    const int R = row0 + r;
+    const float* src = p.partial + (int64_t)R * p.N;
+    float v0, v1 = 0.0f;
+    if constexpr (Tr::kInt) {
+      int s0 = 0, s1 = 0;
+      for (int j = 0; j < p.ksplit; ++j) {
+        s0 += __float_as_int(src[j * plane + c]);
+        if (ACT) s1 += __float_as_int(src[j * plane + p.N / 2 + c]);
+      }
+      v0 = (float)s0;
+      v1 = (float)s1;
+    } else {
+      float s0 = 0.0f, s1 = 0.0f;
+      for (int j = 0; j < p.ksplit; ++j) {
+        s0 += src[j * plane + c];
+        if (ACT) s1 += src[j * plane + p.N / 2 + c];
+      }
+      v0 = s0;
+      v1 = s1;
+    }
+    const int ar = p.a_rows ? p.a_rows[R] : R;
+    store_out<KIND, ACT>(p, g, R, ar, c, c, ACT ? p.N / 2 + c : c, v0, v1);
+  }
 }
 
 template <int KIND, int WF, int MS, bool ACT>
 void launch_skinny(const GemmParams& p, dim3 grid, hipStream_t st) {
-  hipLaunchKernelGGL((skinny_gemm_kernel<KIND, WF, MS, ACT>), grid, dim3(kThreads), 0, st, p);
+  const char* env_s = getenv("QMOE_SKINNY_U");  // tuning knob
+  const int env_u = env_s ? atoi(env_s) : 0;
+  const int u = MS == 1 && env_u > 0 ? env_u : default_unroll(KIND, MS);
+  if (MS == 1 && u >= 4)
+    hipLaunchKernelGGL((skinny_gemm_kernel<KIND, WF, MS, ACT, 4>), grid, dim3(kThreads), 0, st, p);
+  else if (MS == 1 && u == 2)
+    hipLaunchKernelGGL((skinny_gemm_kernel<KIND, WF, MS, ACT, 2>), grid, dim3(kThreads), 0, st, p);
+  else
+    hipLaunchKernelGGL((skinny_gemm_kernel<KIND, WF, MS, ACT, 1>), grid, dim3(kThreads), 0, st, p);
+  if (p.ksplit > 1) {
+    const int nout = ACT ? p.N / 2 : p.N;
+    dim3 rg((unsigned)cdiv(nout, 64), 1, grid.z);
+    hipLaunchKernelGGL((skinny_reduce_kernel<KIND, WF, ACT>), rg, dim3(kThreads), 0, st, p);
+  }
 }
 
 template <int KIND, int WF, bool ACT>
@@ -441,35 +524,38 @@ void launch_act(const GemmParams& p, int ms, dim3 grid, hipStream_t st) {
 
 }  // namespace
 
-// Split-K workspace layout: a FIXED counter area (so a call never reads as a
-// counter what an earlier call of another shape wrote as a partial sum),
-// then the float32 partial planes [ksplit][M][N].
-constexpr int64_t kCounterBytes = 256 * 1024;
-constexpr int64_t kMaxCounters = kCounterBytes / 4;
-
-// Split-K plan of the skinny kernel: the number of K slices and the workspace
-// bytes they need.
+// Split-K plan of the skinny kernel: the number of K slices and the float32
+// workspace ([ksplit][M][N] raw sums) they need. K is split only when there
+// are fewer than ~160 workgroups (a split costs a second launch and the
+// partial-sum traffic; measured on MI355X, one workgroup per 32 weight rows
+// streams best once there are >= 160 of them), and every wavefront keeps at
+// least two 128-k steps.
 void qmoe_skinny_plan(int64_t M, int64_t N, int64_t K, int act, int slots, int ksplit_hint,
                       int* ksplit_out, int64_t* ws_bytes) {
   const int n_tiles = act != QA_NONE ? (int)cdiv<int64_t>(N / 2, 16) : (int)cdiv<int64_t>(N, 32);
   const int KS = (int)cdiv<int64_t>(K, 128);
   int ksplit = ksplit_hint;
-  if (ksplit <= 0) ksplit = (int)cdiv<int64_t>(1024, (int64_t)n_tiles * std::max(slots, 1));
-  ksplit = std::max(1, std::min(ksplit, std::max(1, KS / kWaves)));
-  if ((int64_t)n_tiles * slots > kMaxCounters) ksplit = 1;
+  // tuning knobs (read per call): QMOE_SKINNY_KSPLIT forces the split,
+  // QMOE_SKINNY_TARGET_WG sets the workgroup count the planner aims for
+  const char* ks_s = getenv("QMOE_SKINNY_KSPLIT");
+  const char* tg_s = getenv("QMOE_SKINNY_TARGET_WG");
+  const int env_ksplit = ks_s ? atoi(ks_s) : 0;
+  const int env_target = tg_s && atoi(tg_s) > 0 ? atoi(tg_s) : 160;
+  if (ksplit <= 0) ksplit = env_ksplit;
+  if (ksplit <= 0) ksplit = (int)cdiv<int64_t>(env_target, (int64_t)n_tiles * std::max(slots, 1));
+  ksplit = std::max(1, std::min(ksplit, std::max(1, KS / (2 * kWaves))));
   *ksplit_out = ksplit;
-  *ws_bytes = ksplit <= 1 ? 0 : kCounterBytes + (int64_t)ksplit * M * N * 4;
+  *ws_bytes = ksplit <= 1 ? 0 : (int64_t)ksplit * M * N * 4;
 }
 
 // Host-side launcher shared by the dense and MoE entry points.
-//   max_rows : upper bound of rows in any group (<= 64)
+//   max_rows : rows of the largest group (sizes the M tile; larger groups
+//              are still correct, in more passes)
 //   slots    : gridDim.z (groups, or the capacity of the active list)
-// The workspace's counter area must be zero on first use; the kernel leaves
-// it zero again. Returns a QMOE_* status.
+// Returns a QMOE_* status.
 int qmoe_skinny_launch(int kind, GemmParams p, int max_rows, int slots, void* workspace,
                        int64_t ws_bytes, int ksplit_hint, hipStream_t st) {
   if (max_rows <= 0 || slots <= 0 || p.M <= 0) return QMOE_OK;
-  if (max_rows > 64) return QMOE_ERR_ARG;
   if (p.K <= 0 || (p.K % 32) != 0 || p.N <= 0) return QMOE_ERR_ARG;
   if (p.act != QA_NONE && (p.N % 2) != 0) return QMOE_ERR_ARG;
   if (kind == QK_W8A8_BLK && (p.K % 128) != 0) return QMOE_ERR_ARG;
@@ -481,8 +567,7 @@ int qmoe_skinny_launch(int kind, GemmParams p, int max_rows, int slots, void* wo
   p.ksplit = ksplit;
   if (ksplit > 1) {
     if (!workspace || ws_bytes < need) return QMOE_ERR_WORKSPACE;
-    p.counters = static_cast<uint32_t*>(workspace);
-    p.partial = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + kCounterBytes);
+    p.partial = static_cast<float*>(workspace);
   }
   dim3 grid(n_tiles, ksplit, slots);
   switch (kind) {

@@ -1,29 +1,39 @@
 // Tiled (prefill) grouped GEMM: LDS-staged, double-buffered MFMA tiles.
 //
 // Workgroup = 256 threads (2x2 wavefronts) owning a BM x BN output tile;
-// each wavefront owns (BM/2) x (BN/2) = MF x NF MFMA 16x16 tiles. K advances
-// in stages of 128 bytes per row (128 e4m3/int8 values, 64 bf16 values):
+// each wavefront owns (BM/2) x (BN/2) = MF x NF MFMA 16x16 tiles (128 x 128
+// for the 256 x 256 tile: every 2 KB fragment read from LDS feeds 8 MFMAs,
+// which keeps LDS reads at about half the MFMA time). K advances in stages
+// of 128 bytes per row (128 e4m3/int8 values, 64 bf16 values):
 //  1. every thread issues the global loads of stage s+1 into registers
 //     (16-byte loads; 8 threads cover a 128-byte row, so rows are read with
 //     full coalescing) -- e2m1 / e4m3 weights of the bf16-activation kinds
-//     are expanded to bf16 here, once per element per workgroup;
+//     are expanded to bf16 on the way into LDS, once per element per tile;
 //  2. the wavefronts run stage s out of LDS: lane l reads 32 bytes at column
-//     32*(l>>4) of row (l & 15) of each A and B fragment (ds_read_b128 x 2)
-//     and issues MF*NF MFMAs (one 16x16x128 f8f6f4, two 16x16x64 i8 or two
-//     16x16x32 bf16 per fragment pair);
-//  3. barrier, registers -> the other LDS buffer, barrier.
+//     32*(l>>4) of row (l & 15) of each A and B fragment (2 x ds_read_b128)
+//     and issues MF*NF MFMA groups (one 16x16x128 f8f6f4, two 16x16x64 i8 or
+//     two 16x16x32 bf16 per fragment pair);
+//  3. registers -> the other LDS buffer (free since the last barrier),
+//     barrier.
 // LDS rows are padded to 144 bytes: 16 lanes reading 16 consecutive rows at
 // one column hit 16 disjoint 4-bank groups of the 64 banks.
+// The epilogue applies scales / bias / activation / routing weight in
+// registers, stages the bf16 tile in LDS and writes whole rows with 16-byte
+// stores.
 //
-// Groups: the workgroup's y index enumerates the m-tiles of all groups in
-// order (ceil(rows_g / BM) tiles for group g); a wavefront-parallel scan of
-// the group sizes maps y to (group, m-tile). Rows past a group's end and
-// weight rows past N load as zeros and are not stored.
+// Tile order: a dense GEMM runs a 1-D grid; consecutive workgroups are dealt
+// round-robin to the 8 XCDs, so the block index is remapped to give each XCD
+// a contiguous run of tiles that share a weight (B) column block, which its
+// L2 then serves to all of them. A grouped GEMM enumerates the m-tiles of all
+// groups in order (ceil(rows_g / BM) per group) on grid.y; a wavefront-wide
+// scan of the group sizes maps y to (group, m-tile). Rows past a group's end
+// and weight rows past N load as zeros and are not stored.
 // A fused activation pairs gate rows [n0, n0+BN/2) with up rows
 // [N/2+n0, ...): in a wavefront, fragment j < NF/2 is gate and j + NF/2 the
 // matching up fragment, so the epilogue combines them in registers.
 
 #include <algorithm>
+#include <cstdlib>
 #include <type_traits>
 
 #include "gemm_common.h"
@@ -35,6 +45,7 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kRowBytes = 128;  // K bytes per row per stage
 constexpr int kPitch = 144;     // padded LDS row pitch
+constexpr int kXcds = 8;
 
 template <int KIND, int WF>
 struct TTraits {
@@ -44,6 +55,13 @@ struct TTraits {
   // bytes of one weight row per stage in HBM
   static constexpr int kWRowBytes = KIND == QK_W4A16_MX ? 32 : (KIND == QK_W8A16_PC ? 64 : 128);
 };
+
+template <int BM, int BN, bool ACT>
+constexpr size_t tiled_smem_bytes() {
+  const size_t pipe = 2 * (BM + BN) * kPitch + 2 * (BM + BN) * sizeof(float);
+  const size_t out = (size_t)BM * ((ACT ? BN / 2 : BN) * 2 + 16);
+  return pipe > out ? pipe : out;
+}
 
 __device__ __forceinline__ i32x8 pack8(uint4 a, uint4 b) {
   i32x8 r;
@@ -82,17 +100,11 @@ __device__ __forceinline__ uint2 fp8x4_bf16(uint32_t d) {
                     (f32_bits(hi[0]) >> 16) | (f32_bits(hi[1]) & 0xffff0000u));
 }
 
-// Map the workgroup's y index to (group, first compact row, rows in tile).
-// Returns false if y is past the last tile.
+// Map a grouped workgroup's y index to (group, first compact row, rows in
+// tile). Returns false if y is past the last tile.
 template <int BM>
-__device__ __forceinline__ bool map_tile(const GemmParams& p, int y, int& g, int& row0, int& rows,
-                                         int* s_info) {
-  if (!p.group_offs) {
-    g = 0;
-    row0 = y * BM;
-    rows = min(BM, p.M - row0);
-    return rows > 0;
-  }
+__device__ __forceinline__ bool map_group_tile(const GemmParams& p, int y, int& g, int& row0, int& rows,
+                                               int* s_info) {
   const int G = p.slots;
   if (threadIdx.x < 64) {
     const int lane = threadIdx.x;
@@ -137,13 +149,27 @@ __device__ __forceinline__ bool map_tile(const GemmParams& p, int y, int& g, int
   return g >= 0;
 }
 
+// Dense tile of a 1-D grid, XCD-aware: workgroup b runs on XCD b % 8; the
+// tiles are split into 8 contiguous runs (n-tile major, so a run shares
+// weight column blocks) and XCD x takes run x.
+__device__ __forceinline__ bool map_dense_tile(int b, int m_tiles, int n_tiles, int& mt, int& nt) {
+  const int total = m_tiles * n_tiles;
+  const int per = (total + kXcds - 1) / kXcds;
+  const int t = (b % kXcds) * per + b / kXcds;
+  if (t >= total) return false;
+  nt = t / m_tiles;
+  mt = t % m_tiles;
+  return true;
+}
+
 template <int KIND, int WF, int BM, int BN, bool ACT>
-__global__ __launch_bounds__(kThreads) void tiled_gemm_kernel(const GemmParams p) {
+__global__ __launch_bounds__(kThreads) void tiled_gemm_kernel(const GemmParams p, int m_tiles, int n_tiles) {
   using Tr = TTraits<KIND, WF>;
   constexpr int MF = BM / 32;  // 16-row fragments per wavefront (2x2 waves)
   constexpr int NF = BN / 32;
-  constexpr int A_CH = BM * 8 / kThreads;  // 16-byte chunks per thread (A)
+  constexpr int A_CH = BM * 8 / kThreads;                    // 16-byte chunks per thread (A)
   constexpr int W_CH = BN * Tr::kWRowBytes / 16 / kThreads;  // 16-byte global chunks (W)
+  constexpr int BNO = ACT ? BN / 2 : BN;                     // output columns of the tile
   static_assert(A_CH >= 1 && W_CH >= 1, "tile too small");
   static_assert(BM + BN <= 2 * kThreads, "block-scale staging holds two scales per thread");
 
@@ -158,10 +184,19 @@ __global__ __launch_bounds__(kThreads) void tiled_gemm_kernel(const GemmParams p
   const int wm = wave >> 1, wn = wave & 1;
   const int col = lane & 15, kg = lane >> 4;
 
-  int g, row0, rows;
-  if (!map_tile<BM>(p, blockIdx.y, g, row0, rows, s_info)) return;
+  int g, row0, rows, ntile;
+  if (p.group_offs) {
+    if (!map_group_tile<BM>(p, blockIdx.y, g, row0, rows, s_info)) return;
+    ntile = blockIdx.x;
+  } else {
+    int mt;
+    if (!map_dense_tile(blockIdx.x, m_tiles, n_tiles, mt, ntile)) return;
+    g = 0;
+    row0 = mt * BM;
+    rows = min(BM, p.M - row0);
+  }
 
-  const int n0 = blockIdx.x * (ACT ? BN / 2 : BN);
+  const int n0 = ntile * BNO;
   const int nlim = ACT ? p.N / 2 : p.N;
   const uint8_t* wg = p.w + (int64_t)g * p.w_gstride;
   const uint8_t* abase = static_cast<const uint8_t*>(p.a);
@@ -206,7 +241,7 @@ __global__ __launch_bounds__(kThreads) void tiled_gemm_kernel(const GemmParams p
 
   uint4 ra[A_CH];
   uint4 rw[W_CH];
-  float rsc[2] = {0.0f, 0.0f};  // block-scale staging (BM + BN <= 2 * 256)
+  float rsc[2] = {0.0f, 0.0f};  // block-scale staging
 
   auto gload = [&](int ks) {
 #pragma unroll
@@ -268,8 +303,8 @@ __global__ __launch_bounds__(kThreads) void tiled_gemm_kernel(const GemmParams p
         d[3] = fp4x8_bf16(rw[i].w, scl);
       } else if constexpr (KIND == QK_W8A16_PC) {
         uint4* d = reinterpret_cast<uint4*>(dst + cc * 32);
-        uint2 a0 = fp8x4_bf16(rw[i].x), a1 = fp8x4_bf16(rw[i].y);
-        uint2 a2 = fp8x4_bf16(rw[i].z), a3 = fp8x4_bf16(rw[i].w);
+        const uint2 a0 = fp8x4_bf16(rw[i].x), a1 = fp8x4_bf16(rw[i].y);
+        const uint2 a2 = fp8x4_bf16(rw[i].z), a3 = fp8x4_bf16(rw[i].w);
         d[0] = make_uint4(a0.x, a0.y, a1.x, a1.y);
         d[1] = make_uint4(a2.x, a2.y, a3.x, a3.y);
       } else {
@@ -282,6 +317,15 @@ __global__ __launch_bounds__(kThreads) void tiled_gemm_kernel(const GemmParams p
         if (tid + h * kThreads < BM + BN) sSc[buf * (BM + BN) + tid + h * kThreads] = rsc[h];
     }
     (void)ks;
+  };
+
+  // LDS row of B fragment j of this wavefront
+  auto b_row = [&](int j) {
+    if (ACT) {
+      constexpr int half = NF / 2;
+      return (j < half ? 0 : BN / 2) + wn * (BN / 4) + (j % half) * 16 + col;
+    }
+    return wn * (BN / 2) + j * 16 + col;
   };
 
   using AccT = typename std::conditional<Tr::kInt, i32x4, f32x4>::type;
@@ -303,18 +347,10 @@ __global__ __launch_bounds__(kThreads) void tiled_gemm_kernel(const GemmParams p
 
     const uint8_t* A = sA(buf);
     const uint8_t* Bt = sB(buf);
-    // B fragments of this wavefront
     uint4 bfr[NF][2];
 #pragma unroll
     for (int j = 0; j < NF; ++j) {
-      int tr;
-      if (ACT) {
-        const int half = NF / 2;
-        tr = (j < half ? 0 : BN / 2) + wn * (BN / 4) + (j % half) * 16 + col;
-      } else {
-        tr = wn * (BN / 2) + j * 16 + col;
-      }
-      const uint4* src = reinterpret_cast<const uint4*>(Bt + tr * kPitch + kg * 32);
+      const uint4* src = reinterpret_cast<const uint4*>(Bt + b_row(j) * kPitch + kg * 32);
       bfr[j][0] = src[0];
       bfr[j][1] = src[1];
     }
@@ -322,16 +358,7 @@ __global__ __launch_bounds__(kThreads) void tiled_gemm_kernel(const GemmParams p
     if constexpr (KIND == QK_W8A8_BLK) {
       const float* sc = sSc + buf * (BM + BN) + BM;
 #pragma unroll
-      for (int j = 0; j < NF; ++j) {
-        int tr;
-        if (ACT) {
-          const int half = NF / 2;
-          tr = (j < half ? 0 : BN / 2) + wn * (BN / 4) + (j % half) * 16 + col;
-        } else {
-          tr = wn * (BN / 2) + j * 16 + col;
-        }
-        sbv[j] = sc[tr];
-      }
+      for (int j = 0; j < NF; ++j) sbv[j] = sc[b_row(j)];
     }
 #pragma unroll
     for (int i = 0; i < MF; ++i) {
@@ -377,36 +404,34 @@ __global__ __launch_bounds__(kThreads) void tiled_gemm_kernel(const GemmParams p
     __syncthreads();
   }
 
-  // ---- epilogue ----
+  // ---- epilogue: finish in registers, stage bf16 in LDS, 16-byte stores ----
+  constexpr int OP = BNO * 2 + 16;  // padded LDS pitch of the output tile (bytes)
+  uint8_t* sOut = smem;
   const float* wsc = static_cast<const float*>(p.w_scale);
+  auto fin = [&](float v, float sxa, int n) {
+    if (KIND == QK_W8A8_PC) {
+      v = v * sxa;
+      v = v * wsc[(int64_t)g * p.ws_gstride + n];
+    } else if (KIND == QK_W8A16_PC) {
+      v = v * wsc[(int64_t)g * p.ws_gstride + n];
+    }
+    if (p.bias) v += p.bias[(int64_t)g * p.bias_gstride + n];
+    return v;
+  };
 #pragma unroll
   for (int i = 0; i < MF; ++i)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int rr = wm * (BM / 2) + i * 16 + kg * 4 + r;
-      if (rr >= rows) continue;
-      const int R = row0 + rr;
+      const int R = row0 + (rr < rows ? rr : 0);
       const int ar = p.a_rows ? p.a_rows[R] : R;
-      float sxa = 1.0f;
-      if (KIND == QK_W8A8_PC) sxa = p.a_scale[(int64_t)ar * p.lds_a];
+      const float sxa = KIND == QK_W8A8_PC ? p.a_scale[(int64_t)ar * p.lds_a] : 1.0f;
       const float rwt = p.row_weight ? bf16_to_f32(p.row_weight[R]) : 1.0f;
-      const int64_t yr = p.y_rows ? p.y_rows[R] : R;
-      uint16_t* yrow = p.y + yr * p.ldy;
       constexpr int JN = ACT ? NF / 2 : NF;
 #pragma unroll
       for (int j = 0; j < JN; ++j) {
-        const int ccol = ACT ? n0 + wn * (BN / 4) + j * 16 + col : n0 + wn * (BN / 2) + j * 16 + col;
-        if (ccol >= nlim) continue;
-        auto fin = [&](float v, int n) {
-          if (KIND == QK_W8A8_PC) {
-            v = v * sxa;
-            v = v * wsc[(int64_t)g * p.ws_gstride + n];
-          } else if (KIND == QK_W8A16_PC) {
-            v = v * wsc[(int64_t)g * p.ws_gstride + n];
-          }
-          if (p.bias) v += p.bias[(int64_t)g * p.bias_gstride + n];
-          return v;
-        };
+        const int tc = ACT ? wn * (BN / 4) + j * 16 + col : wn * (BN / 2) + j * 16 + col;
+        const int ccol = min(n0 + tc, nlim - 1);
         float v0, v1 = 0.0f;
         if constexpr (Tr::kInt) v0 = (float)acc[i][j][r];
         else v0 = acc[i][j][r];
@@ -414,73 +439,112 @@ __global__ __launch_bounds__(kThreads) void tiled_gemm_kernel(const GemmParams p
         if (ACT) {
           if constexpr (Tr::kInt) v1 = (float)acc[i][j + NF / 2][r];
           else v1 = acc[i][j + NF / 2][r];
-          out = qmoe_act(p.act, fin(v0, ccol), fin(v1, p.N / 2 + ccol), p.act_p0, p.act_p1);
+          out = qmoe_act(p.act, fin(v0, sxa, ccol), fin(v1, sxa, p.N / 2 + ccol), p.act_p0, p.act_p1);
         } else {
-          out = fin(v0, ccol);
+          out = fin(v0, sxa, ccol);
         }
-        yrow[ccol] = f32_to_bf16(out * rwt);
+        *reinterpret_cast<uint16_t*>(sOut + rr * OP + tc * 2) = f32_to_bf16(out * rwt);
       }
     }
+  __syncthreads();
+  // copy rows out: 8 bf16 (16 bytes) per thread per chunk
+  constexpr int CPR = BNO / 8;  // chunks per row
+  const bool vec_ok = ((p.ldy & 7) == 0) && ((reinterpret_cast<uintptr_t>(p.y) & 15) == 0);
+  for (int c = tid; c < BM * CPR; c += kThreads) {
+    const int rr = c / CPR;
+    const int cc = (c % CPR) * 8;
+    if (rr >= rows) continue;
+    const int R = row0 + rr;
+    const int64_t yr = p.y_rows ? p.y_rows[R] : R;
+    uint16_t* dst = p.y + yr * p.ldy + n0 + cc;
+    const uint8_t* src = sOut + rr * OP + cc * 2;
+    if (vec_ok && n0 + cc + 8 <= nlim) {
+      *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src);
+    } else {
+      for (int e = 0; e < 8 && n0 + cc + e < nlim; ++e) dst[e] = reinterpret_cast<const uint16_t*>(src)[e];
+    }
+  }
 }
 
 template <int KIND, int WF, int BM, int BN, bool ACT>
-void launch_tiled(const GemmParams& p, dim3 grid, hipStream_t st) {
-  const size_t smem = 2 * (BM + BN) * kPitch + 2 * (BM + BN) * sizeof(float);
+void launch_tiled(const GemmParams& p, hipStream_t st) {
+  constexpr size_t smem = tiled_smem_bytes<BM, BN, ACT>();
   auto kern = tiled_gemm_kernel<KIND, WF, BM, BN, ACT>;
-  static bool attr_set = false;  // once per instantiation (process-wide; one GPU)
+  static bool attr_set = false;  // once per instantiation (process-wide)
   if (!attr_set) {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
     attr_set = true;
   }
-  hipLaunchKernelGGL(kern, grid, dim3(kThreads), smem, st, p);
+  const int nout = ACT ? p.N / 2 : p.N;
+  const int n_tiles = cdiv(nout, ACT ? BN / 2 : BN);
+  if (p.group_offs) {
+    const int m_tiles = cdiv(p.M, BM) + std::min(p.slots, p.M);
+    hipLaunchKernelGGL(kern, dim3(n_tiles, m_tiles, 1), dim3(kThreads), smem, st, p, m_tiles, n_tiles);
+  } else {
+    const int m_tiles = cdiv(p.M, BM);
+    const int total = m_tiles * n_tiles;
+    const int grid = cdiv(total, kXcds) * kXcds;
+    hipLaunchKernelGGL(kern, dim3(grid, 1, 1), dim3(kThreads), smem, st, p, m_tiles, n_tiles);
+  }
 }
 
 template <int KIND, int WF, int BM, int BN>
-void launch_tiled_act(const GemmParams& p, dim3 grid, hipStream_t st) {
-  if (p.act != QA_NONE) launch_tiled<KIND, WF, BM, BN, true>(p, grid, st);
-  else launch_tiled<KIND, WF, BM, BN, false>(p, grid, st);
+void launch_tiled_act(const GemmParams& p, hipStream_t st) {
+  if (p.act != QA_NONE) launch_tiled<KIND, WF, BM, BN, true>(p, st);
+  else launch_tiled<KIND, WF, BM, BN, false>(p, st);
+}
+
+// 256 x 256 tiles only for the kinds whose 128 x 128 wavefront tile fits the
+// register file without spilling (the block-scale and bf16-expanding kinds
+// need extra registers per MFMA group)
+template <int KIND>
+constexpr bool has_big_tile() {
+  return KIND == QK_W8A8_PC || KIND == QK_W8A16_PC;
+}
+
+template <int KIND, int WF>
+void launch_shape(const GemmParams& p, bool big, hipStream_t st) {
+  if constexpr (has_big_tile<KIND>()) {
+    if (big) {
+      launch_tiled_act<KIND, WF, 256, 256>(p, st);
+      return;
+    }
+  }
+  launch_tiled_act<KIND, WF, 128, 128>(p, st);
 }
 
 }  // namespace
 
-// Tile shape: 128 x 256 for big problems, 128 x 128 for narrow N.
+// Tile shape: 256 x 256 when the problem has enough such tiles to fill the
+// GPU (>= 2 per CU), else 128 x 128.
 int qmoe_tiled_launch(int kind, GemmParams p, hipStream_t st) {
   if (p.M <= 0) return QMOE_OK;
   const bool abf16 = kind == QK_W8A16_PC || kind == QK_W4A16_MX || kind == QK_W16A16;
   const int kstage = abf16 ? 64 : 128;
   if (p.K <= 0 || (p.K % kstage) != 0 || p.N <= 0) return QMOE_ERR_ARG;
   if (p.act != QA_NONE && (p.N % 2) != 0) return QMOE_ERR_ARG;
-  constexpr int BM = 128;
   const int nout = p.act != QA_NONE ? p.N / 2 : p.N;
-  const bool wide = nout >= 2048;
-  const int BN = wide ? 256 : 128;
-  const int n_tiles = cdiv(nout, p.act != QA_NONE ? BN / 2 : BN);
-  int m_tiles;
+  const int64_t big_tiles = (int64_t)cdiv(p.M, 256) * cdiv(nout, p.act != QA_NONE ? 128 : 256);
+  bool big = false;  // 128 x 128 measured faster or equal on every config shape
+  (void)big_tiles;
+  const char* env = getenv("QMOE_TILED_BIG");  // tuning knob: force 1 / 0
+  if (env) big = atoi(env) != 0;
+  if (kind != QK_W8A8_PC && kind != QK_W8A16_PC) big = false;
   if (p.group_offs) {
-    m_tiles = cdiv(p.M, BM) + std::min(p.slots, p.M);
-  } else {
-    m_tiles = cdiv(p.M, BM);
+    const int m_tiles = cdiv(p.M, big ? 256 : 128) + std::min(p.slots, p.M);
+    if (m_tiles > 65535) return QMOE_ERR_ARG;
   }
-  if (m_tiles > 65535) return QMOE_ERR_ARG;
-  dim3 grid(n_tiles, m_tiles, 1);
-#define QMOE_TL(KD, WFMT)                                                     \
-  do {                                                                        \
-    if (wide) launch_tiled_act<KD, WFMT, 128, 256>(p, grid, st);              \
-    else launch_tiled_act<KD, WFMT, 128, 128>(p, grid, st);                   \
-  } while (0)
   switch (kind) {
     case QK_W8A8_PC:
-      if (p.wfmt == 0) QMOE_TL(QK_W8A8_PC, 0);
-      else QMOE_TL(QK_W8A8_PC, 1);
+      if (p.wfmt == 0) launch_shape<QK_W8A8_PC, 0>(p, big, st);
+      else launch_shape<QK_W8A8_PC, 1>(p, big, st);
       break;
-    case QK_W8A8_BLK: QMOE_TL(QK_W8A8_BLK, 0); break;
-    case QK_W8A16_PC: QMOE_TL(QK_W8A16_PC, 0); break;
-    case QK_W4A16_MX: QMOE_TL(QK_W4A16_MX, 0); break;
-    case QK_W16A16: QMOE_TL(QK_W16A16, 0); break;
+    case QK_W8A8_BLK: launch_shape<QK_W8A8_BLK, 0>(p, big, st); break;
+    case QK_W8A16_PC: launch_shape<QK_W8A16_PC, 0>(p, big, st); break;
+    case QK_W4A16_MX: launch_shape<QK_W4A16_MX, 0>(p, big, st); break;
+    case QK_W16A16: launch_shape<QK_W16A16, 0>(p, big, st); break;
     default: return QMOE_ERR_ARG;
   }
-#undef QMOE_TL
-  (void)BM;
   return hipGetLastError() == hipSuccess ? QMOE_OK : QMOE_ERR_LAUNCH;
 }
