@@ -1,0 +1,166 @@
+"""GPU parity of the quant-method layer: checkpoint -> process_weights_after_loading
+-> apply / apply_monolithic, against the oracle's restatement of the same
+load-time transforms and forward."""
+
+import types
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_close_rows
+from oracle import codecs, linear, moe as omoe, quant, routing
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(a, dev, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    return t.to(dtype) if dtype is not None else t
+
+
+def _fp8(a, dev):
+    return _t(a, dev).view(torch.float8_e4m3fn)
+
+
+def _linear_layer(method, n, k, ckpt_codes, ckpt_scale_inv, dev):
+    layer = torch.nn.Module()
+    method.create_weights(layer, k, [n], k, n, torch.bfloat16)
+    layer.weight.data = _fp8(ckpt_codes, dev)
+    layer.weight_scale_inv.data = _t(ckpt_scale_inv, dev)
+    method.process_weights_after_loading(layer)
+    return layer
+
+
+@pytest.mark.parametrize("mode", ["per_channel", "native_tiles", "int8"])
+def test_fp8_linear_from_block_checkpoint(dev, monkeypatch, mode):
+    from qmoe.layers import quantization as q
+
+    print(f"fp8 linear method {mode}", flush=True)
+    for v in ("ENABLE_QUANTIZED_MATMUL_KERNEL", "REQUANTIZE_BLOCK_SIZE", "REQUANTIZE_WEIGHT_DTYPE"):
+        monkeypatch.delenv(v, raising=False)
+    if mode == "native_tiles":
+        monkeypatch.setenv("ENABLE_QUANTIZED_MATMUL_KERNEL", "1")
+        monkeypatch.setenv("REQUANTIZE_BLOCK_SIZE", "128")
+    if mode == "int8":
+        monkeypatch.setenv("REQUANTIZE_WEIGHT_DTYPE", "int8")
+    rng = np.random.default_rng(3)
+    N, K, M = 384, 512, 6
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    codes, s_inv = quant.quantize_fp8_tiles(w)
+    method = q.Fp8LinearMethod(q.Fp8Config(weight_block_size=[128, 128]))
+    layer = _linear_layer(method, N, K, codes, s_inv, dev)
+    x = codecs.bf16_round(rng.standard_normal((M, K)).astype(np.float32))
+    bias = codecs.bf16_round(rng.standard_normal(N).astype(np.float32))
+    got = method.apply(layer, _t(x, dev, torch.bfloat16), _t(bias, dev, torch.bfloat16)).float().cpu().numpy()
+    w_deq = quant.dequant_tiles(codes, s_inv)
+    if mode == "native_tiles":
+        np.testing.assert_array_equal(layer.weight.view(torch.uint8).cpu().numpy(), codes)
+        ref, _, _ = linear.w8a8_blockwise(x, codes, linear.tile_scales_to_blocks(s_inv, N))
+    else:
+        qd = "int8" if mode == "int8" else "fp8"
+        wq, ws = quant.quantize_tensor(w_deq, qd)  # `fp8.py:297-348`: dequant -> requant per channel
+        np.testing.assert_array_equal(layer.weight.view(torch.uint8).cpu().numpy(), wq.view(np.uint8))
+        np.testing.assert_array_equal(layer.weight_scale.cpu().numpy(), ws)
+        ref, _, _ = linear.w8a8_per_channel(x, wq, ws, qd)
+    ref = codecs.bf16_round(ref + bias[None, :])
+    if mode == "int8":
+        np.testing.assert_array_equal(got, ref)
+    else:
+        assert_close_rows(got, ref, f"fp8 linear {mode}")
+
+
+def test_fp8_apply_known_answer(dev):
+    """`tests/layers/adapter/quantization/test_fp8.py:1208-1238`: all-ones
+    weight, scale and input -> every output equals in_dim (128)."""
+    from qmoe.layers import quantization as q
+
+    method = q.Fp8LinearMethod(q.Fp8Config(weight_block_size=[128, 128]))
+    layer = torch.nn.Module()
+    layer.weight = torch.nn.Parameter(torch.ones(64, 128, device=dev).to(torch.float8_e4m3fn),
+                                      requires_grad=False)
+    layer.weight_scale = torch.nn.Parameter(torch.ones(64, device=dev), requires_grad=False)
+    out = method.apply(layer, torch.ones(4, 128, device=dev, dtype=torch.bfloat16))
+    assert out.shape == (4, 64)
+    assert torch.all(out.float() == 128.0)
+
+
+def _moe_layer(k, act, renormalize=True, scoring="softmax", bias=None, grouped=None, rsf=1.0):
+    layer = torch.nn.Module()
+    layer.moe_config = types.SimpleNamespace(experts_per_token=k, has_bias=True)
+    layer.renormalize = renormalize
+    layer.scoring_func = scoring
+    layer.e_score_correction_bias = bias
+    layer.use_grouped_topk = grouped is not None
+    layer.num_expert_group, layer.topk_group = grouped if grouped else (None, None)
+    layer.routed_scaling_factor = rsf
+    layer.custom_routing_function = None
+    layer.activation = act
+    return layer
+
+
+def test_fp8_moe_block_checkpoint_sigmoid_grouped(dev):
+    """DeepSeek-V3-form layer: 128x128 FP8 experts, sigmoid + bias, grouped
+    top-k, routed_scaling_factor; native tiles stay resident."""
+    from qmoe.layers import quantization as q
+
+    print("fp8 moe method", flush=True)
+    rng = np.random.default_rng(7)
+    E, H, I, k, T = 16, 256, 256, 4, 9
+    cfg = q.Fp8Config(weight_block_size=[128, 128])
+    bias = (rng.standard_normal(E) * 0.1).astype(np.float32)
+    layer = _moe_layer(k, "silu", scoring="sigmoid", bias=_t(bias, dev), grouped=(4, 2), rsf=2.5)
+    method = q.Fp8MoEMethod(cfg, layer.moe_config)
+    method.create_weights(layer, E, H, I, torch.bfloat16)
+    w13f = (rng.standard_normal((E, 2 * I, H)) * 0.02).astype(np.float32)
+    w2f = (rng.standard_normal((E, H, I)) * 0.02).astype(np.float32)
+    t13 = [quant.quantize_fp8_tiles(w13f[e]) for e in range(E)]
+    t2 = [quant.quantize_fp8_tiles(w2f[e]) for e in range(E)]
+    c13, s13 = np.stack([a for a, _ in t13]), np.stack([b for _, b in t13])
+    c2, s2 = np.stack([a for a, _ in t2]), np.stack([b for _, b in t2])
+    layer.w13_weight.data = _fp8(c13, dev)
+    layer.w2_weight.data = _fp8(c2, dev)
+    layer.w13_weight_scale_inv.data = _t(s13, dev)
+    layer.w2_weight_scale_inv.data = _t(s2, dev)
+    method.process_weights_after_loading(layer)
+    x = codecs.bf16_round(rng.standard_normal((T, H)).astype(np.float32))
+    logits = codecs.bf16_round(rng.standard_normal((T, E)).astype(np.float32))
+    got = method.apply_monolithic(layer, _t(x, dev, torch.bfloat16), _t(logits, dev, torch.bfloat16))
+    tw, ids = routing.grouped_topk(logits, k, True, 4, 2, "sigmoid", bias, 2.5)
+    ref, _, _ = omoe.fused_moe(x, omoe.ExpertWeights("fp8_block", c13, s13, c2, s2), tw, ids, "silu")
+    assert_close_rows(got.float().cpu().numpy(), ref, "fp8 moe method")
+
+
+def test_mxfp4_moe_interleaved_checkpoint_swigluoai(dev):
+    """GPT-OSS-form layer: MXFP4 experts with interleaved gate/up rows and
+    biases, softmax top-k, swigluoai."""
+    from qmoe.layers import quantization as q
+
+    print("mxfp4 moe method", flush=True)
+    rng = np.random.default_rng(11)
+    E, H, I, k, T = 8, 256, 192, 2, 7
+    layer = _moe_layer(k, "swigluoai")
+    method = q.Mxfp4MoEMethod(layer.moe_config)
+    method.create_weights(layer, E, H, I, torch.bfloat16)
+    c13 = rng.integers(0, 256, (E, 2 * I, H // 2), dtype=np.uint8)
+    s13 = (127 + rng.integers(-8, 1, (E, 2 * I, H // 32))).astype(np.uint8)
+    c2 = rng.integers(0, 256, (E, H, I // 2), dtype=np.uint8)
+    s2 = (127 + rng.integers(-8, 1, (E, H, I // 32))).astype(np.uint8)
+    b13 = codecs.bf16_round((rng.standard_normal((E, 2 * I)) * 0.1).astype(np.float32))
+    b2 = codecs.bf16_round((rng.standard_normal((E, H)) * 0.1).astype(np.float32))
+    layer.w13_weight.data = _t(c13, dev)
+    layer.w13_weight_scale.data = _t(s13, dev)
+    layer.w2_weight.data = _t(c2, dev)
+    layer.w2_weight_scale.data = _t(s2, dev)
+    layer.w13_bias.data = _t(b13, dev, torch.bfloat16)
+    layer.w2_bias.data = _t(b2, dev, torch.bfloat16)
+    method.process_weights_after_loading(layer)
+    x = codecs.bf16_round(rng.standard_normal((T, H)).astype(np.float32))
+    logits = codecs.bf16_round(rng.standard_normal((T, E)).astype(np.float32))
+    got = method.apply_monolithic(layer, _t(x, dev, torch.bfloat16), _t(logits, dev, torch.bfloat16))
+    tw, ids = routing.select_experts(logits, k, True, "softmax")
+    # the reference de-interleaves gate (even) / up (odd) rows at load (`mxfp4.py:257-262`)
+    dei = lambda a: np.concatenate([a[:, 0::2], a[:, 1::2]], axis=1)  # noqa: E731
+    ref, _, _ = omoe.fused_moe(x, omoe.ExpertWeights("mxfp4", dei(c13), dei(s13), c2, s2, dei(b13), b2),
+                               tw, ids, "swigluoai")
+    assert_close_rows(got.float().cpu().numpy(), ref, "mxfp4 moe method")

@@ -1,0 +1,89 @@
+"""Host-side behaviour of the quant-method layer (no GPU): env-gate
+validation with the reference's error texts (`fp8.py:241-259`), method
+dispatch, and the checkpoint parameter shapes `create_weights` registers."""
+
+import types
+
+import pytest
+import torch
+
+from qmoe.layers import quantization as q
+
+
+def _moe_layer(**kw):
+    layer = torch.nn.Module()
+    layer.moe_config = types.SimpleNamespace(experts_per_token=kw.get("k", 2), has_bias=True)
+    return layer
+
+
+def test_blockwise_kernel_requires_block_size(monkeypatch):
+    monkeypatch.setenv("ENABLE_QUANTIZED_MATMUL_KERNEL", "1")
+    monkeypatch.delenv("REQUANTIZE_BLOCK_SIZE", raising=False)
+    with pytest.raises(ValueError, match="REQUANTIZE_BLOCK_SIZE"):
+        q.Fp8LinearMethod(q.Fp8Config())
+
+
+def test_block_size_requires_blockwise_kernel(monkeypatch):
+    monkeypatch.delenv("ENABLE_QUANTIZED_MATMUL_KERNEL", raising=False)
+    monkeypatch.setenv("REQUANTIZE_BLOCK_SIZE", "128")
+    with pytest.raises(ValueError, match="Blockwise quantization is supported by quantized matmul kernel"):
+        q.Fp8LinearMethod(q.Fp8Config())
+
+
+def test_unsupported_requant_dtype(monkeypatch):
+    monkeypatch.setenv("REQUANTIZE_WEIGHT_DTYPE", "float8_e5m2fnuz")
+    with pytest.raises(ValueError, match="Unsupported REQUANTIZE_WEIGHT_DTYPE"):
+        q.Fp8LinearMethod(q.Fp8Config())
+
+
+def test_negative_w8a16_rows_rejected(monkeypatch):
+    monkeypatch.setenv("TPU_FP8_LINEAR_W8A16_MAX_ROWS", "-1")
+    with pytest.raises(ValueError):
+        q.Fp8LinearMethod(q.Fp8Config())
+
+
+def test_config_dispatch():
+    cfg = q.Fp8Config.from_config({"quant_method": "fp8", "weight_block_size": [128, 128]})
+    assert cfg.is_checkpoint_fp8_serialized and cfg.weight_block_size == [128, 128]
+    assert isinstance(cfg.get_quant_method(torch.nn.Module()), q.Fp8LinearMethod)
+    assert isinstance(cfg.get_quant_method(_moe_layer()), q.Fp8MoEMethod)
+    m = q.Mxfp4Config()
+    assert isinstance(m.get_quant_method(torch.nn.Module()), q.UnquantizedLinearMethod)
+    assert isinstance(m.get_quant_method(_moe_layer()), q.Mxfp4MoEMethod)
+    assert q.get_quantization_config("fp8") is q.Fp8Config
+    with pytest.raises(ValueError):
+        q.get_quantization_config("gptq")
+    with pytest.raises(ValueError):
+        q.Fp8Config(activation_scheme="static")
+
+
+def test_fp8_create_weights_shapes():
+    cfg = q.Fp8Config(weight_block_size=[128, 128])
+    layer = torch.nn.Module()
+    q.Fp8LinearMethod(cfg).create_weights(layer, 512, [256, 128], 512, 384, torch.bfloat16)
+    assert layer.weight.shape == (384, 512) and layer.weight.dtype == torch.float8_e4m3fn
+    assert layer.weight_scale_inv.shape == (3, 4)
+    moe = _moe_layer()
+    q.Fp8MoEMethod(cfg).create_weights(moe, 4, 256, 384, torch.bfloat16)
+    assert moe.w13_weight.shape == (4, 768, 256) and moe.w2_weight.shape == (4, 256, 384)
+    assert moe.w13_weight_scale_inv.shape == (4, 6, 2) and moe.w2_weight_scale_inv.shape == (4, 2, 3)
+
+
+def test_mxfp4_create_weights_shapes():
+    moe = _moe_layer()
+    q.Mxfp4MoEMethod().create_weights(moe, 8, 2880, 2880, torch.bfloat16)
+    assert moe.w13_weight.shape == (8, 5760, 1440) and moe.w13_weight.dtype == torch.uint8
+    assert moe.w13_weight_scale.shape == (8, 5760, 90)
+    assert moe.w2_weight.shape == (8, 2880, 1440) and moe.w2_weight_scale.shape == (8, 2880, 90)
+    assert moe.w13_bias.shape == (8, 5760) and moe.w2_bias.shape == (8, 2880)
+    with pytest.raises(ValueError):
+        q.Mxfp4MoEMethod().create_weights(_moe_layer(), 8, 2880, 2890, torch.bfloat16)
+
+
+def test_activation_codes():
+    from qmoe import ops
+
+    assert ops.act_code("gelu") == ops.act_code("gelu_tanh")  # jax.nn.gelu is approximate
+    assert ops.act_code("situ:2.0:none")[2] < 0
+    with pytest.raises(NotImplementedError):
+        ops.act_code("relu")

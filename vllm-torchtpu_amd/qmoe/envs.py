@@ -1,0 +1,54 @@
+"""Hot-path flags, read from the environment (names and meanings follow the
+reference plugin's `envs.py`, `:43-97, 503-535, 725-750`).
+
+Values are read when accessed (``envs.NAME``), so tests can monkeypatch the
+environment; the quant methods read them at construction / load time, never
+inside a forward call.
+"""
+
+import os
+
+
+def _bool(name, default=False):
+    v = os.getenv(name)
+    if v is None:
+        return default
+    return v.strip().lower() in ("1", "true", "yes", "on")
+
+
+def _opt_int(name):
+    v = os.getenv(name)
+    return int(v) if v not in (None, "") else None
+
+
+def _nonneg_int(name, default):
+    v = os.getenv(name)
+    if v in (None, ""):
+        return default
+    iv = int(v)
+    if iv < 0:
+        raise ValueError(f"{name} must be >= 0, got {iv}")
+    return iv
+
+
+_READERS = {
+    # dense linears: blockwise runtime kernel + its K block (both or neither)
+    "ENABLE_QUANTIZED_MATMUL_KERNEL": lambda: _bool("ENABLE_QUANTIZED_MATMUL_KERNEL"),
+    "REQUANTIZE_BLOCK_SIZE": lambda: _opt_int("REQUANTIZE_BLOCK_SIZE"),
+    # dense linears: runtime weight dtype ("float8_e4m3fn" or "int8")
+    "REQUANTIZE_WEIGHT_DTYPE": lambda: os.getenv("REQUANTIZE_WEIGHT_DTYPE", "float8_e4m3fn"),
+    # FP8 dense linears keep bf16 activations for steps of at most this many rows
+    "TPU_FP8_LINEAR_W8A16_MAX_ROWS": lambda: _nonneg_int("TPU_FP8_LINEAR_W8A16_MAX_ROWS", 0),
+    # MoE: routes with a zero routing weight are padding and skipped
+    "TPU_MOE_SKIP_PADDED_TOKENS": lambda: _bool("TPU_MOE_SKIP_PADDED_TOKENS"),
+}
+
+
+def __getattr__(name):
+    if name in _READERS:
+        return _READERS[name]()
+    raise AttributeError(name)
+
+
+def __dir__():
+    return list(_READERS)

@@ -14,6 +14,7 @@ format                w1 [E, 2I, H...] / w2        scales
 ====================  ==========================  ====================================
 ``mxfp4``             uint8 packed e2m1 [., ., K/2]  e8m0 uint8 [E, N, K/32]
 ``fp8_block``         float8_e4m3fn [E, N, K]      f32 tile scales [E, N/128, K/128]
+``fp8_block_rows``    float8_e4m3fn [E, N, K]      f32 per-(row, 128) scales [E, N, K/128]
 ``fp8`` / ``int8``    float8_e4m3fn / int8         f32 per-channel [E, N]
 ``bf16``              bfloat16                      none
 ====================  ==========================  ====================================
@@ -34,7 +35,7 @@ def infer_weight_format(w1: torch.Tensor, w1_scale) -> str:
         return "int8"
     if w1.dtype == torch.float8_e4m3fn:
         if w1_scale is not None and w1_scale.dim() == 3 and w1_scale.shape[-1] * 128 == w1.shape[-1]:
-            return "fp8_block"
+            return "fp8_block_rows" if w1_scale.shape[1] == w1.shape[1] else "fp8_block"
         return "fp8"
     if w1.dtype == torch.uint8 or "float4" in str(w1.dtype):
         return "mxfp4"
@@ -83,12 +84,13 @@ def fused_moe_gmm(hidden_states, w1, w2, w1_scale, w2_scale, w1_bias, w2_bias, t
                          activation=activation, **common)
         a2, a2_scale, kind, wf, bn = inter, None, _capi.W16A16, 0, 1
         w2k, w2s = w2, None
-    elif fmt == "fp8_block":
+    elif fmt in ("fp8_block", "fp8_block_rows"):
+        bn = 128 if fmt == "fp8_block" else 1
         xq, xs = ops.row_quant(x, "fp8", block=128)
-        inter = ops.gemm(_capi.W8A8_BLK, u8(xq), u8(w1), a_scale=xs, w_scale=w1_scale, ws_bn=128,
+        inter = ops.gemm(_capi.W8A8_BLK, u8(xq), u8(w1), a_scale=xs, w_scale=w1_scale, ws_bn=bn,
                          bias=b1, a_rows=meta["token_sorted"], activation=activation, **common)
         a2q, a2_scale = ops.row_quant(inter, "fp8", block=128)
-        a2, kind, wf, bn = u8(a2q), _capi.W8A8_BLK, 0, 128
+        a2, kind, wf = u8(a2q), _capi.W8A8_BLK, 0
         w2k, w2s = u8(w2), w2_scale
     elif fmt in ("fp8", "int8"):
         qd = "fp8" if fmt == "fp8" else "int8"
