@@ -48,6 +48,8 @@ def parse():
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="", help="comma list of sweep configs to run (0-4)")
+    ap.add_argument("--profile", action="store_true",
+                    help="only run the headline kernel + a copy calibration (for rocprofv3)")
     return ap.parse_args()
 
 
@@ -369,8 +371,35 @@ def cpu_baseline():
                 f"{dt * 1e3:.1f} ms each, numpy fp32 BLAS, {cpu_model}")
 
 
+def profile_target(args):
+    """Short run for rocprofv3 (kernel trace / counters): the dominant kernel
+    of the headline step (FP8 W8A8 tiled GEMM, up projection, M=args.m), 10
+    launches, plus a plain 256 MiB device copy (10 launches) whose known byte
+    count calibrates FETCH_SIZE / WRITE_SIZE."""
+    import torch
+
+    from qmoe import _capi, ops
+
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    M = args.m
+    w_up, s_up = fp8_weights(14336, 4096, gen)
+    x1 = torch.randn((M, 4096), device="cuda", generator=gen).to(torch.bfloat16)
+    xq, xs = ops.row_quant(x1, "fp8")
+    for _ in range(10):
+        ops.gemm(_capi.W8A8_PC, xq.view(torch.uint8), w_up.view(torch.uint8), a_scale=xs, w_scale=s_up)
+    src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"profile target done: gemm M={M} x10, copy 256MiB x10")
+
+
 def main():
     args = parse()
+    if args.profile:
+        profile_target(args)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (got --gpus {args.gpus}); "
               "the multi-GPU sharding design is documented in DESIGN.md", file=sys.stderr)

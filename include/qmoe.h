@@ -113,8 +113,10 @@ int qmoe_gemm_workspace_size(const qmoe_gemm_desc* d, int64_t* bytes);
  * single-group gmm_v2 call for rank-4 scales) and `:188-209`
  * (_quantized_matmul_fp4_jax). Several groups replace the grouped matmul
  * `kernels/megablox/gmm_v2.py:1280-1443` (gmm_v2, incl. its fused
- * activation epilogue `:84-122`). The workspace's first bytes are counters
- * that must be zero before the first call; every call leaves them zero.
+ * activation epilogue `:84-122`). The workspace holds split-K partial sums
+ * of the small-M path; every call writes before it reads, so it needs no
+ * initialisation, and calls that share one workspace must be ordered on one
+ * stream.
  */
 int qmoe_gemm(const qmoe_gemm_desc* d, void* workspace, int64_t ws_bytes, qmoe_stream_t stream);
 

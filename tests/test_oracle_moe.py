@@ -1,0 +1,146 @@
+"""Pins the MoE oracle (`oracle/moe.py`): permutation metadata against the
+reference's known answer and its single-sort procedure, activations against
+closed forms, and the grouped layer against a per-token loop. CPU only."""
+
+import numpy as np
+import pytest
+
+from oracle import codecs, moe
+
+
+def test_prepare_routed_known_answer():
+    """`tests/layers/core/test_fused_moe_gmm.py:430-467`, answers written out:
+    ids [[1,0],[0,-1],[1,0]] -> keys [1,0,0,2,1,0]."""
+    meta = moe.prepare_routed(np.array([[1, 0], [0, -1], [1, 0]]), num_experts=2)
+    assert meta["sorted_idx"].tolist() == [1, 2, 5, 0, 4, 3]
+    assert meta["revert"].tolist() == [3, 0, 1, 5, 4, 2]
+    assert meta["token_sorted"].tolist() == [0, 1, 2, 0, 2, 1]
+    assert meta["group_sizes"].tolist() == [3, 2]
+    assert meta["valid"].tolist() == [True, True, True, False, True, True]
+
+
+def _single_sort(keys, k):
+    """`layers/core/fused_moe_gmm.py:272-285`: one sort of the packed unique
+    integers key << flat_bits | flat position (any sort order of unique keys
+    is the same), unpacked into (sorted_idx, revert, token_sorted)."""
+    n = keys.shape[0]
+    bits = max(1, (n - 1).bit_length())
+    packed = np.sort((keys.astype(np.int64) << bits) | np.arange(n))
+    sorted_idx = packed & ((1 << bits) - 1)
+    revert = np.empty(n, np.int64)
+    revert[sorted_idx] = np.arange(n)
+    return sorted_idx, revert, sorted_idx // k
+
+
+@pytest.mark.parametrize("T,k,E", [(1, 8, 256), (4, 10, 64), (204, 10, 64), (16, 1, 8), (33, 4, 128)])
+def test_prepare_routed_matches_packed_single_sort(T, k, E):
+    """Invariants of `tests/layers/adapter/test_moe_single_sort.py:35-119`:
+    the stable argsort and the packed single sort agree (incl. invalid
+    routes, all-equal keys and k = 1)."""
+    rng = np.random.default_rng(T * 100 + k)
+    ids = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
+    ids[rng.random(ids.shape) < 0.1] = -1
+    meta = moe.prepare_routed(ids, num_experts=E)
+    keys = np.where(ids.reshape(-1) >= 0, ids.reshape(-1), E)
+    si, rv, ts = _single_sort(keys, k)
+    np.testing.assert_array_equal(meta["sorted_idx"], si)
+    np.testing.assert_array_equal(meta["revert"], rv)
+    np.testing.assert_array_equal(meta["token_sorted"], ts)
+    np.testing.assert_array_equal(meta["group_sizes"], np.bincount(keys, minlength=E + 1)[:E])
+
+
+def test_all_equal_keys_keep_flat_order():
+    meta = moe.prepare_routed(np.zeros((16, 1), np.int32), num_experts=4)
+    assert meta["sorted_idx"].tolist() == list(range(16))
+
+
+def test_skip_padded_routes_sort_last():
+    """`fused_moe_gmm.py:314-320`: a zero routing weight makes a route
+    invalid when skip_padded_tokens is set."""
+    ids = np.array([[0, 1], [1, 0]], np.int32)
+    w = np.array([[0.5, 0.0], [0.25, 0.75]], np.float32)
+    meta = moe.prepare_routed(ids, w, 2, skip_padded_tokens=True)
+    assert meta["group_sizes"].tolist() == [2, 1]
+    assert meta["sorted_idx"].tolist() == [0, 3, 2, 1]
+
+
+def test_swigluoai_closed_form():
+    """`gmm_v2.py:30-38`: g = min(g, 7), u = clip(u, -7, 7),
+    (u + 1) * g * sigmoid(1.702 g)."""
+    g = np.array([8.0, -2.0, 0.5], np.float32)
+    u = np.array([-9.0, 9.0, 0.25], np.float32)
+    got = moe.act_fn(g, u, "swigluoai")
+    sig = lambda x: 1 / (1 + np.exp(-x))  # noqa: E731
+    want = [(-7 + 1) * 7 * sig(1.702 * 7), (7 + 1) * -2 * sig(-3.404), 1.25 * 0.5 * sig(0.851)]
+    np.testing.assert_allclose(got, want, rtol=1e-6)
+
+
+@pytest.mark.parametrize("linear_beta", ["none", "25.0"])
+def test_situ_known_form(linear_beta):
+    """`tests/kernels/test_gmm_v2.py:57-68`."""
+    g = np.array([-3.0, 0.5, 7.0], np.float32)
+    u = np.array([-30.0, 2.0, 40.0], np.float32)
+    eg = 4.0 * np.tanh(g / 4.0) / (1 + np.exp(-g))
+    eu = u if linear_beta == "none" else 25.0 * np.tanh(u / 25.0)
+    np.testing.assert_allclose(moe.act_fn(g, u, f"situ:4.0:{linear_beta}"), eg * eu, rtol=1e-5, atol=1e-5)
+
+
+def test_silu_and_clamp_and_gelu_points():
+    g = np.array([0.0, 12.0, -1.0], np.float32)
+    u = np.array([3.0, -20.0, 2.0], np.float32)
+    sig = lambda x: 1 / (1 + np.exp(-x))  # noqa: E731
+    np.testing.assert_allclose(moe.act_fn(g, u, "silu"), g * sig(g) * u, rtol=1e-6)
+    np.testing.assert_allclose(moe.act_fn(g, u, "silu_and_mul_with_clamp"),
+                               [0.0, 10 * sig(10.0) * -10, -sig(-1.0) * 2], rtol=1e-6)
+    # gelu(0) = 0, gelu(x) -> x for large x, gelu(-1) (tanh form) = -0.15880801
+    np.testing.assert_allclose(moe.act_fn(np.array([0.0, 6.0, -1.0], np.float32), np.ones(3, np.float32),
+                                          "gelu_tanh"), [0.0, 6.0, -0.15880801], rtol=1e-5, atol=1e-6)
+
+
+def test_combine_exact_arithmetic():
+    """`test_fused_moe_gmm.py:322-384` in spirit: bf16 integer-valued experts,
+    inputs and weights 0.125 make every step exact, so the grouped layer must
+    equal the per-token loop bit for bit."""
+    rng = np.random.default_rng(0)
+    T, H, I, E, k = 9, 32, 16, 5, 3
+    x = rng.integers(-2, 3, (T, H)).astype(np.float32)
+    w13 = rng.integers(-1, 2, (E, 2 * I, H)).astype(np.float32)
+    w2 = rng.integers(-1, 2, (E, H, I)).astype(np.float32)
+    ids = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
+    ids[2, 1] = -1
+    tw = np.full((T, k), 0.125, np.float32)
+    ew = moe.ExpertWeights("bf16", w13, None, w2, None)
+    got, _, _ = moe.fused_moe(x, ew, tw, ids, "silu_and_mul_with_clamp")
+    want = np.zeros((T, H), np.float32)
+    for t in range(T):
+        for j in range(k):
+            e = ids[t, j]
+            if e < 0:
+                continue
+            gu = w13[e] @ x[t]
+            a = codecs.bf16_round(moe.act_fn(gu[:I], gu[I:], "silu_and_mul_with_clamp"))
+            want[t] += 0.125 * (w2[e] @ a)
+    np.testing.assert_allclose(got, codecs.bf16_round(want), rtol=8e-3, atol=1e-6)
+
+
+def test_grouped_layer_matches_per_token_loop():
+    """`_reference_fused_moe`, `test_fused_moe_gmm.py:387-427`: per token and
+    slot, skip id < 0, accumulate w * expert(x). Random bf16 data."""
+    rng = np.random.default_rng(3)
+    T, H, I, E, k = 11, 64, 32, 6, 2
+    x = codecs.bf16_round(rng.standard_normal((T, H)).astype(np.float32))
+    w13 = codecs.bf16_round((rng.standard_normal((E, 2 * I, H)) * 0.1).astype(np.float32))
+    w2 = codecs.bf16_round((rng.standard_normal((E, H, I)) * 0.1).astype(np.float32))
+    ids = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
+    ids[0, 0] = -1
+    tw = codecs.bf16_round(rng.random((T, k)).astype(np.float32))
+    got, _, _ = moe.fused_moe(x, moe.ExpertWeights("bf16", w13, None, w2, None), tw, ids, "silu")
+    want = np.zeros((T, H), np.float64)
+    for t in range(T):
+        for j in range(k):
+            e = ids[t, j]
+            if e >= 0:
+                gu = w13[e].astype(np.float64) @ x[t]
+                a = codecs.bf16_round(moe.act_fn(gu[:I].astype(np.float32), gu[I:].astype(np.float32), "silu"))
+                want[t] += tw[t, j] * (w2[e].astype(np.float64) @ a)
+    np.testing.assert_allclose(got, want, rtol=1e-2, atol=2e-2 * np.abs(want).max())

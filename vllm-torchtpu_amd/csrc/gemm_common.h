@@ -65,7 +65,6 @@ struct GemmParams {
   const int32_t* y_rows;       // optional scatter: destination row of compact row R
   // split-K workspace (skinny kernel only)
   float* partial;
-  uint32_t* counters;
   int32_t ksplit;
 };
 

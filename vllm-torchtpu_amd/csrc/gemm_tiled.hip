@@ -149,16 +149,25 @@ __device__ __forceinline__ bool map_group_tile(const GemmParams& p, int y, int& 
   return g >= 0;
 }
 
-// Dense tile of a 1-D grid, XCD-aware: workgroup b runs on XCD b % 8; the
-// tiles are split into 8 contiguous runs (n-tile major, so a run shares
-// weight column blocks) and XCD x takes run x.
+// Dense tile of a 1-D grid, XCD-aware: workgroup b runs on XCD b % 8, and
+// the 8 XCDs each take one contiguous run of the tile order. The order walks
+// groups of kGroupM m-tiles column by column (n-tile after n-tile), so the
+// ~64 workgroups an XCD runs at once cover about 8 m-tiles x 8 n-tiles:
+// each A row block and each weight column block fetched into that XCD's L2
+// is then shared by ~8 tiles instead of being re-fetched per tile.
+constexpr int kGroupM = 8;
+
 __device__ __forceinline__ bool map_dense_tile(int b, int m_tiles, int n_tiles, int& mt, int& nt) {
   const int total = m_tiles * n_tiles;
   const int per = (total + kXcds - 1) / kXcds;
   const int t = (b % kXcds) * per + b / kXcds;
   if (t >= total) return false;
-  nt = t / m_tiles;
-  mt = t % m_tiles;
+  const int group = t / (kGroupM * n_tiles);
+  const int first_m = group * kGroupM;
+  const int gm = min(kGroupM, m_tiles - first_m);
+  const int in = t - group * kGroupM * n_tiles;
+  mt = first_m + in % gm;
+  nt = in / gm;
   return true;
 }
 

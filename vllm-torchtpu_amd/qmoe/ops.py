@@ -63,15 +63,16 @@ _ws = {}
 
 
 def _workspace(dev, nbytes):
-    """Per-device zero-initialised workspace; its counter area stays zero
-    between calls (every kernel that uses it resets its counters)."""
+    """Per-device workspace for split-K partial sums, grown on demand. The
+    kernels write every partial before reading it, so it needs no clearing;
+    calls are ordered by the current stream."""
     if nbytes <= 0:
         return None, 0
     key = (dev.type, dev.index)
     with _ws_lock:
         cur = _ws.get(key)
         if cur is None or cur.numel() < nbytes:
-            cur = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
+            cur = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
             _ws[key] = cur
     return cur, cur.numel()
 
