@@ -2,16 +2,18 @@
 // (weight-streaming, <= 64 rows per group) or the tiled (LDS/MFMA) kernel.
 
 #include <algorithm>
+#include <cstdlib>
 
 #include "../../include/qmoe.h"
 #include "gemm_common.h"
 
-// defined in gemm_skinny.hip / gemm_tiled.hip
+// defined in gemm_skinny.hip / gemm_tiled.hip / gemm_f8.hip
 void qmoe_skinny_plan(int64_t M, int64_t N, int64_t K, int act, int slots, int ksplit_hint,
                       int* ksplit_out, int64_t* ws_bytes);
 int qmoe_skinny_launch(int kind, GemmParams p, int max_rows, int slots, void* workspace,
                        int64_t ws_bytes, int ksplit_hint, hipStream_t st);
 int qmoe_tiled_launch(int kind, GemmParams p, hipStream_t st);
+int qmoe_f8_launch(GemmParams p, hipStream_t st);
 
 namespace {
 
@@ -112,5 +114,11 @@ extern "C" int qmoe_gemm(const qmoe_gemm_desc* d, void* workspace, int64_t ws_by
   // a skinny-path device (it bounds the grid by the number of routed experts)
   p.active = nullptr;
   p.num_active = nullptr;
+  if (d->kind == QMOE_W8A8_PC && !getenv("QMOE_F8_OFF")) {  // tuning knob: generic kernel only
+    // 1-byte x 1-byte kernel; it declines (QMOE_ERR_ARG) problems outside its
+    // envelope (K % 128, 16-byte alignment), which the generic kernel takes
+    const int rc = qmoe_f8_launch(p, stream);
+    if (rc != QMOE_ERR_ARG) return rc;
+  }
   return qmoe_tiled_launch(d->kind, p, stream);
 }
