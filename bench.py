@@ -333,6 +333,26 @@ def sweep_moe(only):
     return out
 
 
+def profiled_traffic(m):
+    """HBM bytes per launch of the headline kernel from the committed
+    rocprofv3 counters (profiles/, collected with `bench.py --profile`):
+    FETCH_SIZE and WRITE_SIZE, each scaled by what it reads for a plain copy
+    of known size in the same run. None when no profile matches the
+    workload."""
+    path = os.path.join(ROOT, "profiles", "tiled_gemm_fp8_w8a8_M4096_K4096_N14336.json")
+    try:
+        d = json.load(open(path))
+    except (OSError, ValueError):
+        return None
+    if d.get("workload", {}).get("M") != m:
+        return None
+    cal = d["copy_calibration"]
+    c = d["counters_kib_per_dispatch"]
+    rd = c["FETCH_SIZE"] * cal["bytes"] / cal["FETCH_SIZE_kib"]
+    wr = c["WRITE_SIZE"] * cal["bytes"] / cal["WRITE_SIZE_kib"]
+    return int(rd + wr)
+
+
 # ------------------------------------------------------------------ CPU baseline
 
 
@@ -430,7 +450,7 @@ def main():
                    "M": args.m, "parallelism": "single GPU"},
         "roofline": {"kernel": "tiled W8A8 FP8 GEMM (up projection)", "bound": "mfma",
                      "achieved": round(k_tf, 2), "peak": PEAK["fp8"] / 1e12, "unit": "TFLOP/s",
-                     "frac": round(k_tf / (PEAK["fp8"] / 1e12), 4), "traffic": None,
+                     "frac": round(k_tf / (PEAK["fp8"] / 1e12), 4), "traffic": profiled_traffic(args.m),
                      "us_per_launch": round(h["k_us"], 2),
                      "algorithmic_bytes": h["k_bytes"]},
     }

@@ -79,9 +79,20 @@ int skinny_slots(const qmoe_gemm_desc* d) {
   return d->active ? std::max(1, std::min(d->slots, d->M)) : d->slots;
 }
 
+// Rows the skinny kernel's M tile is sized for: all rows of a dense
+// problem; for a grouped one the average rows per routed group (groups
+// above it take extra 16-row passes over their weight slice, from cache).
+int skinny_rows(const qmoe_gemm_desc* d) {
+  if (!d->group_offs) return d->M;
+  const int groups = std::max(1, std::min(skinny_slots(d), d->M));
+  const int avg = (d->M + groups - 1) / groups;
+  return std::max(1, std::min(std::min(d->max_rows, d->M), avg));
+}
+
 bool use_skinny(const qmoe_gemm_desc* d) {
-  const int rows = d->group_offs ? d->max_rows : d->M;
-  return rows <= kSkinnyMaxRows;
+  const char* env = getenv("QMOE_SKINNY_MAX_ROWS");  // tuning knob
+  const int lim = env ? atoi(env) : kSkinnyMaxRows;
+  return skinny_rows(d) <= lim;
 }
 
 }  // namespace
@@ -107,8 +118,7 @@ extern "C" int qmoe_gemm(const qmoe_gemm_desc* d, void* workspace, int64_t ws_by
   if (st != QMOE_OK) return st;
   if (d->M == 0) return QMOE_OK;
   if (use_skinny(d)) {
-    const int rows = d->group_offs ? std::max(1, std::min(d->max_rows, d->M)) : d->M;
-    return qmoe_skinny_launch(d->kind, p, rows, skinny_slots(d), workspace, ws_bytes, 0, stream);
+    return qmoe_skinny_launch(d->kind, p, skinny_rows(d), skinny_slots(d), workspace, ws_bytes, 0, stream);
   }
   // the tiled kernel enumerates m-tiles over all groups; the active list is
   // a skinny-path device (it bounds the grid by the number of routed experts)

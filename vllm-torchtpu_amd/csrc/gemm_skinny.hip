@@ -51,9 +51,11 @@ struct Traits {
   static constexpr int kABytes = kAbf16 ? 64 : 32;
 };
 
-// 128-k steps per pipeline chunk (two chunks are in flight per wavefront)
-int default_unroll(int kind, int ms) {
-  if (ms > 1) return 1;
+// 128-k steps per pipeline chunk (two chunks are in flight per wavefront);
+// measured on MI355X: two for dense decode, one for grouped (MoE) problems,
+// whose per-wavefront K slices are short
+int default_unroll(int kind, int ms, bool grouped) {
+  if (grouped || ms > 1) return 1;
   return kind == QK_W16A16 ? 1 : 2;
 }
 
@@ -495,10 +497,10 @@ template <int KIND, int WF, int MS, bool ACT>
 void launch_skinny(const GemmParams& p, dim3 grid, hipStream_t st) {
   const char* env_s = getenv("QMOE_SKINNY_U");  // tuning knob
   const int env_u = env_s ? atoi(env_s) : 0;
-  const int u = MS == 1 && env_u > 0 ? env_u : default_unroll(KIND, MS);
-  if (MS == 1 && u >= 4)
+  const int u = env_u > 0 ? env_u : default_unroll(KIND, MS, p.group_offs != nullptr);
+  if (u >= 4)
     hipLaunchKernelGGL((skinny_gemm_kernel<KIND, WF, MS, ACT, 4>), grid, dim3(kThreads), 0, st, p);
-  else if (MS == 1 && u == 2)
+  else if (u == 2)
     hipLaunchKernelGGL((skinny_gemm_kernel<KIND, WF, MS, ACT, 2>), grid, dim3(kThreads), 0, st, p);
   else
     hipLaunchKernelGGL((skinny_gemm_kernel<KIND, WF, MS, ACT, 1>), grid, dim3(kThreads), 0, st, p);
@@ -559,7 +561,9 @@ int qmoe_skinny_launch(int kind, GemmParams p, int max_rows, int slots, void* wo
   if (p.K <= 0 || (p.K % 32) != 0 || p.N <= 0) return QMOE_ERR_ARG;
   if (p.act != QA_NONE && (p.N % 2) != 0) return QMOE_ERR_ARG;
   if (kind == QK_W8A8_BLK && (p.K % 128) != 0) return QMOE_ERR_ARG;
-  const int ms = max_rows <= 16 ? 1 : (max_rows <= 32 ? 2 : 4);
+  int ms = max_rows <= 16 ? 1 : (max_rows <= 32 ? 2 : 4);
+  const char* env_ms = getenv("QMOE_SKINNY_MS");  // tuning knob: 1, 2 or 4
+  if (env_ms && (atoi(env_ms) == 1 || atoi(env_ms) == 2 || atoi(env_ms) == 4)) ms = atoi(env_ms);
   const int n_tiles = p.act != QA_NONE ? cdiv(p.N / 2, 16) : cdiv(p.N, 32);
   int ksplit = 1;
   int64_t need = 0;
