@@ -7,6 +7,7 @@ import torch
 
 from conftest import assert_close_rows
 from oracle import codecs, linear, quant
+from oracle import moe as omoe
 
 pytestmark = pytest.mark.gpu
 
@@ -79,7 +80,9 @@ def test_e4m3_device_encoder_sweep(dev):
 # ------------------------------------------------------------------ GEMM
 
 SHAPES_SKINNY = [(1, 512, 384), (8, 1024, 640), (16, 2048, 256), (33, 512, 4096), (64, 4096, 1024)]
-SHAPES_TILED = [(65, 512, 384), (200, 1024, 1000), (512, 2048, 2048), (300, 1536, 2304)]
+# the last two split K across workgroups (few tiles, long K)
+SHAPES_TILED = [(65, 512, 384), (200, 1024, 1000), (512, 2048, 2048), (300, 1536, 2304), (130, 8192, 512),
+                (96, 14336, 768)]
 
 
 @pytest.mark.parametrize("M,K,N", SHAPES_SKINNY + SHAPES_TILED)
@@ -177,8 +180,8 @@ def test_w8a16_and_w16a16(dev, M, K, N):
 
 
 def test_split_k_deterministic_and_reusable(dev):
-    """Split-K (last-workgroup reduction) gives identical results on repeat
-    calls, i.e. the counters are left at zero."""
+    """Split-K (slices summed in a fixed order by a second kernel) gives
+    identical results on repeat calls that share the workspace."""
     from qmoe import _capi, ops
 
     rng = np.random.default_rng(21)
@@ -193,3 +196,26 @@ def test_split_k_deterministic_and_reusable(dev):
     for o in outs[1:]:
         assert torch.equal(o, outs[0])
     assert_close_rows(outs[0].float().cpu().numpy(), ref, "split-k")
+
+
+@pytest.mark.parametrize("act", ["silu", "swigluoai"])
+def test_tiled_split_k_fused_activation(dev, act):
+    """Tiled FP8 GEMM with a K split and the gate/up activation applied by
+    the split-K finishing kernel."""
+    from qmoe import _capi, ops
+
+    print(f"tiled split-k act {act}", flush=True)
+    rng = np.random.default_rng(5)
+    M, K, I = 100, 8192, 320
+    w = (rng.standard_normal((2 * I, K)) * 0.02).astype(np.float32)
+    wq, ws = quant.quantize_tensor(w, "fp8")
+    x = _bf16(rng, (M, K))
+    xq_ref, sx = quant.quantize_act(x, "fp8")
+    acc = codecs.e4m3_decode(xq_ref).astype(np.float64) @ codecs.e4m3_decode(wq).astype(np.float64).T
+    gu = ((acc.astype(np.float32) * sx[:, None]).astype(np.float32) * ws[None, :]).astype(np.float32)
+    ref = codecs.bf16_round(omoe.act_fn(gu[:, :I], gu[:, I:], act))
+    xq, xs = ops.row_quant(_t(x, dev, torch.bfloat16), "fp8")
+    y = ops.gemm(_capi.W8A8_PC, xq.view(torch.uint8), _t(wq, dev), a_scale=xs, w_scale=_t(ws, dev),
+                 activation=act)
+    assert_close_rows(y.float().cpu().numpy(), ref, f"split-k {act}")
+

@@ -13,11 +13,14 @@ void qmoe_skinny_plan(int64_t M, int64_t N, int64_t K, int act, int slots, int k
 int qmoe_skinny_launch(int kind, GemmParams p, int max_rows, int slots, void* workspace,
                        int64_t ws_bytes, int ksplit_hint, hipStream_t st);
 int qmoe_tiled_launch(int kind, GemmParams p, hipStream_t st);
-int qmoe_f8_launch(GemmParams p, hipStream_t st);
+bool qmoe_f8_plan(const GemmParams& p, int* bm_out, int* ksplit_out, int64_t* ws_bytes);
+int qmoe_f8_launch(GemmParams p, void* workspace, int64_t ws_bytes, hipStream_t st);
 
 namespace {
 
 constexpr int kSkinnyMaxRows = 64;
+constexpr int kSkinnyMaxGroupRows = 8;
+constexpr int kSkinnyMaxRowsW8A8 = 32;
 
 int to_params(const qmoe_gemm_desc* d, GemmParams* p) {
   if (!d) return QMOE_ERR_ARG;
@@ -89,10 +92,20 @@ int skinny_rows(const qmoe_gemm_desc* d) {
   return std::max(1, std::min(std::min(d->max_rows, d->M), avg));
 }
 
+// Dense problems take the skinny kernel up to 64 rows (32 for W8A8, whose
+// tiled kernel is faster from there on); grouped ones while the routed
+// experts average at most 8 rows (measured on MI355X: beyond that the tiled
+// kernel's weight reuse across rows wins).
 bool use_skinny(const qmoe_gemm_desc* d) {
   const char* env = getenv("QMOE_SKINNY_MAX_ROWS");  // tuning knob
-  const int lim = env ? atoi(env) : kSkinnyMaxRows;
+  int lim = d->group_offs ? kSkinnyMaxGroupRows : kSkinnyMaxRows;
+  if (!d->group_offs && d->kind == QMOE_W8A8_PC) lim = kSkinnyMaxRowsW8A8;
+  if (env) lim = atoi(env);
   return skinny_rows(d) <= lim;
+}
+
+bool use_f8(const qmoe_gemm_desc* d) {
+  return d->kind == QMOE_W8A8_PC && !getenv("QMOE_F8_OFF");  // tuning knob: generic kernel only
 }
 
 }  // namespace
@@ -107,6 +120,11 @@ extern "C" int qmoe_gemm_workspace_size(const qmoe_gemm_desc* d, int64_t* bytes)
   if (use_skinny(d)) {
     int ks = 1;
     qmoe_skinny_plan(d->M, d->N, d->K, d->act, skinny_slots(d), 0, &ks, bytes);
+  } else if (use_f8(d)) {
+    p.active = nullptr;
+    p.num_active = nullptr;
+    int bm = 0, ks = 1;
+    if (!qmoe_f8_plan(p, &bm, &ks, bytes)) *bytes = 0;
   }
   return QMOE_OK;
 }
@@ -124,10 +142,10 @@ extern "C" int qmoe_gemm(const qmoe_gemm_desc* d, void* workspace, int64_t ws_by
   // a skinny-path device (it bounds the grid by the number of routed experts)
   p.active = nullptr;
   p.num_active = nullptr;
-  if (d->kind == QMOE_W8A8_PC && !getenv("QMOE_F8_OFF")) {  // tuning knob: generic kernel only
+  if (use_f8(d)) {
     // 1-byte x 1-byte kernel; it declines (QMOE_ERR_ARG) problems outside its
-    // envelope (K % 128, 16-byte alignment), which the generic kernel takes
-    const int rc = qmoe_f8_launch(p, stream);
+    // envelope (K % 256, 16-byte alignment), which the generic kernel takes
+    const int rc = qmoe_f8_launch(p, workspace, ws_bytes, stream);
     if (rc != QMOE_ERR_ARG) return rc;
   }
   return qmoe_tiled_launch(d->kind, p, stream);

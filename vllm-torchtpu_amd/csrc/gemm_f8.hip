@@ -36,6 +36,7 @@
 
 #include "gemm_common.h"
 
+
 namespace {
 
 constexpr int kThreads = 256;
@@ -283,8 +284,14 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
   // The row terms pass through an empty asm so that the compiler forms the
   // 64-bit addresses at each copy instead of keeping them alive across the
   // MFMA loop.
+  // split-K: this workgroup's K range, in units of 256 bytes (two 128-byte
+  // or four 64-byte stages, so every pipeline below runs whole loops)
+  const int NU = p.K / 256;
+  const int u0 = (int)((int64_t)NU * blockIdx.z / p.ksplit);
+  const int u1 = (int)((int64_t)NU * (blockIdx.z + 1) / p.ksplit);
+  const uint32_t kbase = (uint32_t)u0 * 256u;
   auto copy_stage = [&](uint8_t* dW, uint8_t* dX, int ks) {
-    const uint32_t kb = (uint32_t)ks * (uint32_t)KB;
+    const uint32_t kb = kbase + (uint32_t)ks * (uint32_t)KB;
 #pragma unroll
     for (int j = 0; j < WI; ++j) {
       uint32_t o = woff[j];
@@ -360,7 +367,7 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
   constexpr int NM = NI * MJ * (INT ? 2 : 1);  // MFMAs per k-step
   constexpr int NR = 2 * (NI + MJ);            // LDS operand reads per k-step
   if constexpr (KB == 64) {
-    // ---- four stages of one k-step (KS = K / 64, KS % 4 == 0) ----
+    // ---- four stages of one k-step (KS % 4 == 0) ----
     // Stage s lives in LDS buffer s % 4 and is copied four stages ahead.
     // Stage s: wait for the own copy of stage s+1 -> barrier (every copy of
     // stage s+1 has landed, and every wavefront holds the operands of stage
@@ -370,7 +377,7 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
     // among the rest. The copy is unconditional (past the end it refetches
     // the last stage into a consumed buffer, which is never read again), so
     // the loop body has no branch.
-    const int KS = p.K / 64;
+    const int KS = (u1 - u0) * 4;
     copy_stage(sW0, sX0, 0);
     copy_stage(sW1, sX1, 1);
     copy_stage(sW2, sX2, 2);
@@ -393,14 +400,14 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
       stage(sW3, sX3, sW0, sX0, s + 3, 1);
     }
   } else {
-    // ---- two stages of two k-steps (KS = K / 128, KS % 2 == 0) ----
+    // ---- two stages of two k-steps (KS % 2 == 0) ----
     // Stage s lives in LDS buffer s % 2. Its first half runs the MFMAs of
     // k-step 0 while k-step 1 is read; then: wait for the own copy of stage
     // s+1 -> barrier (stage s+1 has landed everywhere, and stage s has been
     // read everywhere, so its buffer is free) -> copy stage s+2 into it ->
     // MFMAs of k-step 1 while k-step 0 of stage s+1 is read. A copy has one
     // stage (two k-steps of MFMAs) to land.
-    const int KS = p.K / 128;
+    const int KS = (u1 - u0) * 2;
     copy_stage(sW0, sX0, 0);
     copy_stage(sW1, sX1, 1);
     wait_copies_upto<CPS>();
@@ -421,6 +428,43 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
       stage(sW0, sX0, sW1, sX1, s);
       stage(sW1, sX1, sW0, sX0, s + 1);
     }
+  }
+
+  // ---- split-K: raw sums (int32 bit patterns for INT8) to the f32
+  // workspace [ksplit][M][N]; the reduce kernel adds the slices in order and
+  // runs the epilogue. A lane holds 4 consecutive weight rows of one token.
+  if (p.ksplit > 1) {
+    float* plane = p.partial + (int64_t)blockIdx.z * p.M * p.N;
+#pragma unroll
+    for (int j = 0; j < MJ; ++j) {
+      const int tr = wm * TM + j * 32 + rl;
+      if (tr >= rows) continue;
+      float* dst = plane + (int64_t)(row0 + tr) * p.N;
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int lr = wrow(i) + q * 8 + kh * 4;  // tile weight row of the quad
+          int n;
+          if (ACT) n = (lr < BN / 2 ? n0 + lr : p.N / 2 + n0 + (lr - BN / 2));
+          else n = n0 + lr;
+          const int nl = ACT ? (lr < BN / 2 ? n0 + lr : n0 + (lr - BN / 2)) : n;  // output column
+          float v[4];
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            if constexpr (INT) v[t] = __int_as_float(acc[i][j][q * 4 + t]);
+            else v[t] = acc[i][j][q * 4 + t];
+          }
+          if (nl + 4 <= nlim && (p.N & 3) == 0) {
+            *reinterpret_cast<float4*>(dst + n) = make_float4(v[0], v[1], v[2], v[3]);
+          } else {
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+              if (nl + t < nlim) dst[n + t] = v[t];
+          }
+        }
+    }
+    return;
   }
 
   // ---- epilogue ----
@@ -533,6 +577,106 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
   }
 }
 
+// Split-K finish for the tiled kernel: one lane = 8 consecutive output
+// channels of one compact row; a wavefront covers 512 channels of a row, a
+// workgroup 4 rows. The slices are added in slice order (deterministic),
+// then scales, bias, activation and routing weight are applied as in the
+// single-pass epilogue. A grouped problem finds the row's group by binary
+// search over group_offs.
+template <bool INT, bool ACT>
+__global__ __launch_bounds__(kThreads) void f8_splitk_finish_kernel(const GemmParams p) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int R = blockIdx.y * 4 + wave;
+  if (R >= p.M) return;
+  const int nlim = ACT ? p.N / 2 : p.N;
+  const int c0 = (blockIdx.x * 64 + lane) * 8;
+  if (c0 >= nlim) return;
+  int g = 0;
+  if (p.group_offs) {
+    int lo = 0, hi = p.slots;  // group_offs[lo] <= R < group_offs[hi]
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (p.group_offs[mid] <= R) lo = mid;
+      else hi = mid;
+    }
+    g = lo;
+  }
+  const int ar = p.a_rows ? p.a_rows[R] : R;
+  const float sxa = p.a_scale[(int64_t)ar * p.lds_a];
+  const float rwt = p.row_weight ? bf16_to_f32(p.row_weight[R]) : 1.0f;
+  const float* wsc = static_cast<const float*>(p.w_scale) + (int64_t)g * p.ws_gstride;
+  const float* bias = p.bias ? p.bias + (int64_t)g * p.bias_gstride : nullptr;
+  const int64_t plane = (int64_t)p.M * p.N;
+  const float* src = p.partial + (int64_t)R * p.N;
+  const bool vec = (p.N & 3) == 0 && c0 + 8 <= nlim;
+  float vg[8], vu[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) vg[k] = vu[k] = 0.0f;
+  int ig[8], iu[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) ig[k] = iu[k] = 0;
+  for (int j = 0; j < p.ksplit; ++j) {
+    const float* sj = src + j * plane;
+    float a[8], b[8];
+    if (vec) {
+      const float4 a0 = *reinterpret_cast<const float4*>(sj + c0);
+      const float4 a1 = *reinterpret_cast<const float4*>(sj + c0 + 4);
+      a[0] = a0.x; a[1] = a0.y; a[2] = a0.z; a[3] = a0.w; a[4] = a1.x; a[5] = a1.y; a[6] = a1.z; a[7] = a1.w;
+      if (ACT) {
+        const float4 b0 = *reinterpret_cast<const float4*>(sj + p.N / 2 + c0);
+        const float4 b1 = *reinterpret_cast<const float4*>(sj + p.N / 2 + c0 + 4);
+        b[0] = b0.x; b[1] = b0.y; b[2] = b0.z; b[3] = b0.w; b[4] = b1.x; b[5] = b1.y; b[6] = b1.z; b[7] = b1.w;
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int c = min(c0 + k, nlim - 1);
+        a[k] = sj[c];
+        b[k] = ACT ? sj[p.N / 2 + c] : 0.0f;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      if constexpr (INT) {
+        ig[k] += __float_as_int(a[k]);
+        if (ACT) iu[k] += __float_as_int(b[k]);
+      } else {
+        vg[k] += a[k];
+        if (ACT) vu[k] += b[k];
+      }
+    }
+  }
+  uint32_t packed[4];
+#pragma unroll
+  for (int k = 0; k < 8; k += 2) {
+    float o2[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int n = min(c0 + k + h, nlim - 1);
+      float v = INT ? (float)ig[k + h] : vg[k + h];
+      v = v * sxa;
+      v = v * wsc[n];
+      if (bias) v += bias[n];
+      if (ACT) {
+        float u = INT ? (float)iu[k + h] : vu[k + h];
+        u = u * sxa;
+        u = u * wsc[p.N / 2 + n];
+        if (bias) u += bias[p.N / 2 + n];
+        v = qmoe_act(p.act, v, u, p.act_p0, p.act_p1);
+      }
+      o2[h] = v * rwt;
+    }
+    packed[k / 2] = (uint32_t)f32_to_bf16(o2[0]) | ((uint32_t)f32_to_bf16(o2[1]) << 16);
+  }
+  const int64_t yr = p.y_rows ? p.y_rows[R] : R;
+  uint16_t* dst = p.y + yr * p.ldy + c0;
+  if (c0 + 8 <= nlim && ((p.ldy & 7) == 0) && ((reinterpret_cast<uintptr_t>(p.y) & 15) == 0)) {
+    *reinterpret_cast<uint4*>(dst) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+  } else {
+    for (int k = 0; k < 8 && c0 + k < nlim; ++k) dst[k] = (uint16_t)(packed[k / 2] >> ((k & 1) * 16));
+  }
+}
+
 template <bool INT, int BM, int BN, bool ACT>
 void f8_launch_shape(const GemmParams& p, hipStream_t st) {
   const char* env = getenv("QMOE_F8_KB");  // tuning knob: K bytes per LDS stage
@@ -540,13 +684,14 @@ void f8_launch_shape(const GemmParams& p, hipStream_t st) {
   auto kern = kb == 64 ? f8_gemm_kernel<INT, BM, BN, ACT, 64> : f8_gemm_kernel<INT, BM, BN, ACT, 128>;
   const int nout = ACT ? p.N / 2 : p.N;
   const int n_tiles = cdiv(nout, ACT ? BN / 2 : BN);
+  const unsigned ks = (unsigned)std::max(1, p.ksplit);
   if (p.group_offs) {
     const int m_tiles = cdiv(p.M, BM) + std::min(p.slots, p.M);
-    hipLaunchKernelGGL(kern, dim3(n_tiles, m_tiles, 1), dim3(kThreads), 0, st, p, m_tiles, n_tiles);
+    hipLaunchKernelGGL(kern, dim3(n_tiles, m_tiles, ks), dim3(kThreads), 0, st, p, m_tiles, n_tiles);
   } else {
     const int m_tiles = cdiv(p.M, BM);
     const int grid = cdiv(m_tiles * n_tiles, kXcds) * kXcds;
-    hipLaunchKernelGGL(kern, dim3(grid, 1, 1), dim3(kThreads), 0, st, p, m_tiles, n_tiles);
+    hipLaunchKernelGGL(kern, dim3(grid, 1, ks), dim3(kThreads), 0, st, p, m_tiles, n_tiles);
   }
 }
 
@@ -591,25 +736,63 @@ static int f8_pick_bm(const GemmParams& p) {
   return 32;
 }
 
-// Returns QMOE_ERR_ARG when the problem is outside this kernel's envelope
-// (K % 256, 16-byte alignment, weights < 4 GiB per group); the caller then
-// uses the generic tiled kernel.
-int qmoe_f8_launch(GemmParams p, hipStream_t st) {
-  if (p.M <= 0) return QMOE_OK;
-  if (p.K <= 0 || (p.K % 256) != 0 || p.N <= 0) return QMOE_ERR_ARG;
-  if (p.act != QA_NONE && (p.N % 2) != 0) return QMOE_ERR_ARG;
-  if ((p.lda % 16) != 0 || (p.ldw % 16) != 0) return QMOE_ERR_ARG;
+// Whether this kernel takes the problem (K % 256, 16-byte alignment,
+// weights < 4 GiB per group), and its plan: token-tile height, K split and
+// the f32 workspace the split needs ([ksplit][M][N]).
+bool qmoe_f8_plan(const GemmParams& p, int* bm_out, int* ksplit_out, int64_t* ws_bytes) {
+  if (p.M <= 0 || p.K <= 0 || (p.K % 256) != 0 || p.N <= 0) return false;
+  if (p.act != QA_NONE && (p.N % 2) != 0) return false;
+  if ((p.lda % 16) != 0 || (p.ldw % 16) != 0) return false;
   if ((reinterpret_cast<uintptr_t>(p.a) & 15) || (reinterpret_cast<uintptr_t>(p.w) & 15) ||
       (p.w_gstride % 16) != 0)
-    return QMOE_ERR_ARG;
-  // 32-bit per-lane weight offsets within a group
-  if ((int64_t)p.ldw * p.N >= ((int64_t)1 << 32)) return QMOE_ERR_ARG;
-  const int bm = f8_pick_bm(p);
-  if (p.group_offs) {
-    const int m_tiles = cdiv(p.M, bm) + std::min(p.slots, p.M);
-    if (m_tiles > 65535) return QMOE_ERR_ARG;
+    return false;
+  if ((int64_t)p.ldw * p.N >= ((int64_t)1 << 32)) return false;
+  int bm = f8_pick_bm(p);
+  const int m_tiles = p.group_offs ? cdiv(p.M, bm) + std::min(p.slots, p.M) : cdiv(p.M, bm);
+  if (p.group_offs && m_tiles > 65535) return false;
+  // Dense problems whose largest CU-filling tile is small (tall-K, few
+  // tokens) are split over K, with the tile and split that measured best on
+  // MI355X: (32 rows, 4 slices) up to 256 tokens, (128, 4) up to 512,
+  // (128, 2) above.
+  int ksplit = 1;
+  const bool env_bm = getenv("QMOE_F8_BM") != nullptr;
+  if (!p.group_offs && bm <= 64 && p.K >= 8192 && !env_bm) {
+    if (p.M <= 256) { bm = 32; ksplit = 4; }
+    else if (p.M <= 512) { bm = 128; ksplit = 4; }
+    else { bm = 128; ksplit = 2; }
+  }
+  const char* env = getenv("QMOE_F8_KSPLIT");  // tuning knob
+  if (env && atoi(env) > 0) ksplit = std::max(1, std::min(atoi(env), p.K / 256));
+  *bm_out = bm;
+  *ksplit_out = ksplit;
+  *ws_bytes = ksplit > 1 ? (int64_t)ksplit * p.M * p.N * 4 : 0;
+  return true;
+}
+
+// Launch per the plan (the caller checked qmoe_f8_plan and sized the
+// workspace); with a K split the reduce kernel finishes the epilogue.
+int qmoe_f8_launch(GemmParams p, void* workspace, int64_t ws_bytes, hipStream_t st) {
+  int bm = 0, ksplit = 1;
+  int64_t need = 0;
+  if (!qmoe_f8_plan(p, &bm, &ksplit, &need)) return QMOE_ERR_ARG;
+  p.ksplit = ksplit;
+  if (ksplit > 1) {
+    if (!workspace || ws_bytes < need) return QMOE_ERR_WORKSPACE;
+    p.partial = static_cast<float*>(workspace);
   }
   if (p.wfmt == 1) f8_launch_bm<true>(p, bm, st);
   else f8_launch_bm<false>(p, bm, st);
+  if (ksplit > 1) {
+    const int nout = p.act != QA_NONE ? p.N / 2 : p.N;
+    const dim3 rg((unsigned)cdiv(nout, 512), (unsigned)cdiv(p.M, 4), 1);
+    const bool act = p.act != QA_NONE;
+    if (p.wfmt == 1) {
+      if (act) hipLaunchKernelGGL((f8_splitk_finish_kernel<true, true>), rg, dim3(kThreads), 0, st, p);
+      else hipLaunchKernelGGL((f8_splitk_finish_kernel<true, false>), rg, dim3(kThreads), 0, st, p);
+    } else {
+      if (act) hipLaunchKernelGGL((f8_splitk_finish_kernel<false, true>), rg, dim3(kThreads), 0, st, p);
+      else hipLaunchKernelGGL((f8_splitk_finish_kernel<false, false>), rg, dim3(kThreads), 0, st, p);
+    }
+  }
   return hipGetLastError() == hipSuccess ? QMOE_OK : QMOE_ERR_LAUNCH;
 }
