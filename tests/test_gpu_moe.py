@@ -138,6 +138,7 @@ def _moe_case(fmt, E, k, H, I, T, seed, bias=False):
     ("mxfp4", "swigluoai", 8, 2, 256, 256, 1, False),
     ("mxfp4", "swigluoai", 16, 4, 512, 384, 40, True),
     ("mxfp4", "swigluoai", 16, 4, 512, 256, 300, True),   # tiled path (T > 64)
+    ("mxfp4", "swigluoai", 8, 2, 288, 160, 6, False),     # K % 256 != 0 in both GEMMs
     ("fp8_block", "silu", 8, 2, 512, 256, 5, False),
     ("fp8_block", "silu", 16, 4, 512, 256, 200, False),   # tiled path
     ("bf16", "silu", 8, 2, 256, 128, 9, False),

@@ -8,8 +8,8 @@
 #include "gemm_common.h"
 
 // defined in gemm_skinny.hip / gemm_tiled.hip / gemm_f8.hip
-void qmoe_skinny_plan(int64_t M, int64_t N, int64_t K, int act, int slots, int ksplit_hint,
-                      int* ksplit_out, int64_t* ws_bytes);
+void qmoe_skinny_plan(int kind, int64_t M, int64_t N, int64_t K, int act, int slots, int rows,
+                      int ksplit_hint, int* ksplit_out, int64_t* ws_bytes);
 int qmoe_skinny_launch(int kind, GemmParams p, int max_rows, int slots, void* workspace,
                        int64_t ws_bytes, int ksplit_hint, hipStream_t st);
 int qmoe_tiled_launch(int kind, GemmParams p, hipStream_t st);
@@ -119,7 +119,7 @@ extern "C" int qmoe_gemm_workspace_size(const qmoe_gemm_desc* d, int64_t* bytes)
   *bytes = 0;
   if (use_skinny(d)) {
     int ks = 1;
-    qmoe_skinny_plan(d->M, d->N, d->K, d->act, skinny_slots(d), 0, &ks, bytes);
+    qmoe_skinny_plan(d->kind, d->M, d->N, d->K, d->act, skinny_slots(d), skinny_rows(d), 0, &ks, bytes);
   } else if (use_f8(d)) {
     p.active = nullptr;
     p.num_active = nullptr;
@@ -136,7 +136,13 @@ extern "C" int qmoe_gemm(const qmoe_gemm_desc* d, void* workspace, int64_t ws_by
   if (st != QMOE_OK) return st;
   if (d->M == 0) return QMOE_OK;
   if (use_skinny(d)) {
-    return qmoe_skinny_launch(d->kind, p, skinny_rows(d), skinny_slots(d), workspace, ws_bytes, 0, stream);
+    // the skinny kernel declines (QMOE_ERR_ARG) operands of 2 GiB or more,
+    // which the generic tiled kernel takes
+    const int rc = qmoe_skinny_launch(d->kind, p, skinny_rows(d), skinny_slots(d), workspace, ws_bytes, 0, stream);
+    if (rc != QMOE_ERR_ARG) return rc;
+    p.active = nullptr;
+    p.num_active = nullptr;
+    return qmoe_tiled_launch(d->kind, p, stream);
   }
   // the tiled kernel enumerates m-tiles over all groups; the active list is
   // a skinny-path device (it bounds the grid by the number of routed experts)

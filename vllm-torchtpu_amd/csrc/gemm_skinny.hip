@@ -3,9 +3,10 @@
 //
 // Small-M linears and decode MoE are weight-bandwidth bound, so the design
 // goal is to keep enough 16-byte weight loads in flight to saturate HBM3E:
-//  * workgroup = 4 wavefronts; it owns 32 weight rows (two 16-row MFMA
-//    B tiles, or one 16-column gate tile + the matching up tile when an
-//    activation is fused) and a slice of K;
+//  * workgroup = 4 wavefronts; it owns NS 16-row MFMA B tiles of weight
+//    rows (NS/2 gate tiles + the matching up tiles when an activation is
+//    fused) and a slice of K. NS = 2 (4 is kept for e2m1 weights as a tuning
+//    option);
 //  * K is cut into 128-wide steps; the workgroup's steps are dealt out to its
 //    4 wavefronts, and further across `ksplit` workgroups (grid.y);
 //  * a wavefront issues the loads of U steps back to back, unconditionally
@@ -36,7 +37,6 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
-constexpr int kNSub = 2;  // 16-row weight tiles per workgroup
 
 struct Frag {
   uint4 v[4];
@@ -59,16 +59,38 @@ int default_unroll(int kind, int ms, bool grouped) {
   return kind == QK_W16A16 ? 1 : 2;
 }
 
-template <int NB>
-__device__ __forceinline__ void ld(Frag& f, const uint8_t* p) {
+// Operands are read with buffer loads: a wave-uniform resource (base and
+// extent in SGPRs), a 32-bit per-lane offset fixed for the whole K loop, and
+// the step's byte offset as a scalar. This keeps one VGPR per stream instead
+// of a 64-bit address per load; the host keeps every operand below 2 GiB.
+using rsrc_t = __amdgpu_buffer_rsrc_t;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, int64_t bytes) {
+  const int n = bytes >= 0x7fffffff ? 0x7fffffff : (int)bytes;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
+}
+
+// cache-policy bits of the weight stream's loads (read once per launch)
+constexpr int kWeightAux = 0;
+
+template <int NB, int AUX = 0>
+__device__ __forceinline__ void ldb(Frag& f, rsrc_t r, uint32_t voff, uint32_t soff) {
 #pragma unroll
-  for (int i = 0; i < NB / 16; ++i) f.v[i] = reinterpret_cast<const uint4*>(p)[i];
+  for (int i = 0; i < NB / 16; ++i) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff + i * 16, soff, AUX);
+    f.v[i] = make_uint4(v[0], v[1], v[2], v[3]);
+  }
 }
 
 template <int NB>
-__device__ __forceinline__ void ld_masked(Frag& f, const uint8_t* p, bool ok) {
+__device__ __forceinline__ void zero_unless(Frag& f, bool ok) {
 #pragma unroll
-  for (int i = 0; i < NB / 16; ++i) f.v[i] = ok ? reinterpret_cast<const uint4*>(p)[i] : make_uint4(0, 0, 0, 0);
+  for (int i = 0; i < NB / 16; ++i)
+    if (!ok) f.v[i] = make_uint4(0, 0, 0, 0);
+}
+
+__device__ __forceinline__ float ldb_f32(rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
 }
 
 __device__ __forceinline__ i32x8 as_i32x8(const Frag& f) {
@@ -112,36 +134,37 @@ __device__ __forceinline__ uint2 fp8x4_to_bf16(uint32_t d) {
   return make_uint2(a, b);
 }
 
-template <int KIND, int WF, int MS>
+template <int KIND, int WF, int MS, int NS>
 struct Acc {
   using T = typename std::conditional<Traits<KIND, WF>::kInt, i32x4, f32x4>::type;
-  T v[MS][kNSub];
+  T v[MS][NS];
 };
 
 // Per-step side data: per-(row, block) and per-(n, block) scales (W8A8_BLK),
 // e8m0 block scale of the lane's weight row (W4A16_MX).
-template <int MS>
+template <int MS, int NS>
 struct StepScales {
   float sa[MS][4];
-  float sb[kNSub];
+  float sb[NS];
+  uint32_t eb[NS];  // raw e8m0 bytes, decoded where they are used
 };
 
 // One 128-k step of MFMAs for all (M tile, weight tile) pairs.
-template <int KIND, int WF, int MS>
-__device__ __forceinline__ void mma_step(Acc<KIND, WF, MS>& acc, const Frag (&fa)[MS],
-                                         const Frag (&bw)[kNSub], const StepScales<MS>& sc) {
+template <int KIND, int WF, int MS, int NS>
+__device__ __forceinline__ void mma_step(Acc<KIND, WF, MS, NS>& acc, const Frag (&fa)[MS],
+                                         const Frag (&bw)[NS], const StepScales<MS, NS>& sc) {
   if constexpr (KIND == QK_W8A8_PC && WF == 0) {
 #pragma unroll
     for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
-      for (int s = 0; s < kNSub; ++s)
+      for (int s = 0; s < NS; ++s)
         acc.v[ms][s] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
             as_i32x8(fa[ms]), as_i32x8(bw[s]), acc.v[ms][s], 0, 0, 0, 127, 0, 127);
   } else if constexpr (KIND == QK_W8A8_PC && WF == 1) {
 #pragma unroll
     for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
-      for (int s = 0; s < kNSub; ++s) {
+      for (int s = 0; s < NS; ++s) {
         acc.v[ms][s] = __builtin_amdgcn_mfma_i32_16x16x64_i8(as_i32x4(fa[ms].v[0]), as_i32x4(bw[s].v[0]),
                                                              acc.v[ms][s], 0, 0, 0);
         acc.v[ms][s] = __builtin_amdgcn_mfma_i32_16x16x64_i8(as_i32x4(fa[ms].v[1]), as_i32x4(bw[s].v[1]),
@@ -152,20 +175,21 @@ __device__ __forceinline__ void mma_step(Acc<KIND, WF, MS>& acc, const Frag (&fa
 #pragma unroll
     for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
-      for (int s = 0; s < kNSub; ++s) {
+      for (int s = 0; s < NS; ++s) {
         f32x4 d = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(as_i32x8(fa[ms]), as_i32x8(bw[s]),
                                                                    f32x4{0, 0, 0, 0}, 0, 0, 0, 127, 0, 127);
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc.v[ms][s][r] += d[r] * (sc.sa[ms][r] * sc.sb[s]);
       }
   } else {
-    // bf16 activations: expand the weight fragment to 4 x 8 bf16
-    uint4 wb[kNSub][4];
+    // bf16 activations: expand each weight fragment to 4 x 8 bf16 right
+    // before its MFMAs (one tile's expansion live at a time)
 #pragma unroll
-    for (int s = 0; s < kNSub; ++s) {
+    for (int s = 0; s < NS; ++s) {
+      uint4 wb[4];
       if constexpr (KIND == QK_W16A16) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) wb[s][q] = bw[s].v[q];
+        for (int q = 0; q < 4; ++q) wb[q] = bw[s].v[q];
       } else if constexpr (KIND == QK_W8A16_PC) {
         const uint32_t d[8] = {bw[s].v[0].x, bw[s].v[0].y, bw[s].v[0].z, bw[s].v[0].w,
                                bw[s].v[1].x, bw[s].v[1].y, bw[s].v[1].z, bw[s].v[1].w};
@@ -173,22 +197,21 @@ __device__ __forceinline__ void mma_step(Acc<KIND, WF, MS>& acc, const Frag (&fa
         for (int q = 0; q < 4; ++q) {
           const uint2 lo = fp8x4_to_bf16(d[2 * q]);
           const uint2 hi = fp8x4_to_bf16(d[2 * q + 1]);
-          wb[s][q] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+          wb[q] = make_uint4(lo.x, lo.y, hi.x, hi.y);
         }
       } else {  // QK_W4A16_MX
         const uint32_t d[4] = {bw[s].v[0].x, bw[s].v[0].y, bw[s].v[0].z, bw[s].v[0].w};
+        const float scale = e8m0_to_f32(sc.eb[s]);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) wb[s][q] = fp4x8_to_bf16(d[q], sc.sb[s]);
+        for (int q = 0; q < 4; ++q) wb[q] = fp4x8_to_bf16(d[q], scale);
       }
-    }
 #pragma unroll
-    for (int ms = 0; ms < MS; ++ms)
-#pragma unroll
-      for (int s = 0; s < kNSub; ++s)
+      for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-          acc.v[ms][s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(fa[ms].v[q]), as_bf16x8(wb[s][q]),
+          acc.v[ms][s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(fa[ms].v[q]), as_bf16x8(wb[q]),
                                                                  acc.v[ms][s], 0, 0, 0);
+    }
   }
 }
 
@@ -234,40 +257,64 @@ __device__ __forceinline__ bool slot_group(const GemmParams& p, int slot, int& g
   return rows > 0;
 }
 
-template <int KIND, int WF, int MS, bool ACT, int U>
+template <int KIND, int WF, int MS, bool ACT, int U, int NS>
 __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(const GemmParams p) {
   using Tr = Traits<KIND, WF>;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  // wave-uniform in an SGPR, so K-slice bounds and loop tests are scalar
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int col = lane & 15;
   const int kg = lane >> 4;
 
   int g, row0, rows;
   if (!slot_group(p, blockIdx.z, g, row0, rows)) return;
 
-  // weight rows of the two B tiles (clamped copies feed the loads)
+  // weight rows of the NS B tiles (clamped copies feed the loads); with an
+  // activation, tile s < NS/2 holds gate rows and tile s + NS/2 the
+  // matching up rows
+  constexpr int NH = NS / 2;
   const int tile = blockIdx.x;
   const int nlim = ACT ? (p.N >> 1) : p.N;
-  int nw[kNSub];
-  bool nok[kNSub];
+  int nw[NS];
+  bool nok[NS];
   if (ACT) {
-    const int c = tile * 16 + col;
-    nok[0] = nok[1] = c < nlim;
-    nw[0] = c;
-    nw[1] = (p.N >> 1) + c;
-  } else {
-    nw[0] = tile * 32 + col;
-    nw[1] = tile * 32 + 16 + col;
-    nok[0] = nw[0] < nlim;
-    nok[1] = nw[1] < nlim;
-  }
-  const uint8_t* wg = p.w + (int64_t)g * p.w_gstride;
-  const uint8_t* wrow[kNSub];
-  int nclamp[kNSub];
 #pragma unroll
-  for (int s = 0; s < kNSub; ++s) {
-    nclamp[s] = nok[s] ? nw[s] : (ACT ? (s == 0 ? nlim - 1 : p.N - 1) : p.N - 1);
-    wrow[s] = wg + (int64_t)nclamp[s] * p.ldw + kg * Tr::kWBytes;
+    for (int s = 0; s < NH; ++s) {
+      const int c = tile * (16 * NH) + s * 16 + col;
+      nok[s] = nok[s + NH] = c < nlim;
+      nw[s] = c;
+      nw[s + NH] = (p.N >> 1) + c;
+    }
+  } else {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      nw[s] = tile * (16 * NS) + s * 16 + col;
+      nok[s] = nw[s] < nlim;
+    }
+  }
+  g = __builtin_amdgcn_readfirstlane(g);
+  const rsrc_t wres = make_rsrc(p.w + (int64_t)g * p.w_gstride, (int64_t)p.N * p.ldw);
+  uint32_t woff[NS];
+  int nclamp[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    nclamp[s] = nok[s] ? nw[s] : (ACT ? (s < NH ? nlim - 1 : p.N - 1) : p.N - 1);
+    woff[s] = (uint32_t)(nclamp[s] * p.ldw + kg * Tr::kWBytes);
+  }
+  // per-step scale streams: e8m0 bytes [N][K/32] (W4A16), f32 [N/bn][K/128]
+  // weight blocks and [rows][K/128] activation blocks (W8A8_BLK)
+  rsrc_t sres = wres, ares = wres;  // placeholders for kinds without scale streams
+  uint32_t soffw[NS];
+  if constexpr (KIND == QK_W4A16_MX) {
+    sres = make_rsrc(static_cast<const uint8_t*>(p.w_scale) + (int64_t)g * p.ws_gstride, (int64_t)p.N * p.ldws);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) soffw[s] = (uint32_t)(nclamp[s] * p.ldws + kg);
+  } else if constexpr (KIND == QK_W8A8_BLK) {
+    sres = make_rsrc(static_cast<const float*>(p.w_scale) + (int64_t)g * p.ws_gstride,
+                     (int64_t)cdiv(p.N, p.ws_bn) * p.ldws * 4);
+    ares = make_rsrc(p.a_scale, (int64_t)p.M * p.lds_a * 4);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) soffw[s] = (uint32_t)((nclamp[s] / p.ws_bn) * p.ldws * 4);
   }
 
   // K steps: KSF full 128-wide steps, plus a tail step when K % 128 != 0
@@ -280,54 +327,50 @@ __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(const GemmParams 
   const int ks1 = (int)((int64_t)KS * (sl + 1) / nsl);
   const int kf1 = min(ks1, KSF);
 
-  const uint8_t* abase = static_cast<const uint8_t*>(p.a);
   const int64_t lda_b = p.lda * (Tr::kAbf16 ? 2 : 1);
-  constexpr int NV = MS * kNSub * 4;
+  const rsrc_t xres = make_rsrc(p.a, (int64_t)p.M * lda_b);
+  constexpr int NV = MS * NS * 4;
   __shared__ float red[kWaves - 1][NV][64];
   const int64_t plane = (int64_t)p.M * p.N;
 
   // Rows are taken 16*MS at a time (one pass when the host's row bound
   // holds; more passes re-read this workgroup's weight slice from cache).
   for (int mp = 0; mp < rows; mp += 16 * MS) {
-    const uint8_t* arowp[MS];
-    int arow4[MS][4];  // physical A rows of the 4 accumulator rows (block scales)
+    uint32_t aoff[MS];
+    uint32_t soffa[MS][4];  // scale offsets of the 4 accumulator rows (block scales)
 #pragma unroll
     for (int ms = 0; ms < MS; ++ms) {
       const int r = mp + ms * 16 + col;
       const int R = row0 + (r < rows ? r : 0);
       const int ar = p.a_rows ? p.a_rows[R] : R;
-      arowp[ms] = abase + (int64_t)ar * lda_b + kg * Tr::kABytes;
+      aoff[ms] = (uint32_t)(ar * lda_b + kg * Tr::kABytes);
       if constexpr (KIND == QK_W8A8_BLK) {
 #pragma unroll
         for (int r4 = 0; r4 < 4; ++r4) {
           const int rr = mp + ms * 16 + kg * 4 + r4;
           const int R2 = row0 + (rr < rows ? rr : 0);
-          arow4[ms][r4] = p.a_rows ? p.a_rows[R2] : R2;
+          soffa[ms][r4] = (uint32_t)((p.a_rows ? p.a_rows[R2] : R2) * p.lds_a * 4);
         }
       }
     }
 
-    Acc<KIND, WF, MS> acc;
+    Acc<KIND, WF, MS, NS> acc;
 #pragma unroll
     for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
-      for (int s = 0; s < kNSub; ++s) acc.v[ms][s] = {0, 0, 0, 0};
+      for (int s = 0; s < NS; ++s) acc.v[ms][s] = {0, 0, 0, 0};
 
-    auto load_scales = [&](int ks, StepScales<MS>& sc) {
+    auto load_scales = [&](int ks, StepScales<MS, NS>& sc) {
       if constexpr (KIND == QK_W8A8_BLK) {
 #pragma unroll
-        for (int s = 0; s < kNSub; ++s)
-          sc.sb[s] = static_cast<const float*>(p.w_scale)[(int64_t)g * p.ws_gstride +
-                                                          (int64_t)(nclamp[s] / p.ws_bn) * p.ldws + ks];
+        for (int s = 0; s < NS; ++s) sc.sb[s] = ldb_f32(sres, soffw[s], (uint32_t)ks * 4);
 #pragma unroll
         for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
-          for (int r4 = 0; r4 < 4; ++r4) sc.sa[ms][r4] = p.a_scale[(int64_t)arow4[ms][r4] * p.lds_a + ks];
+          for (int r4 = 0; r4 < 4; ++r4) sc.sa[ms][r4] = ldb_f32(ares, soffa[ms][r4], (uint32_t)ks * 4);
       } else if constexpr (KIND == QK_W4A16_MX) {
 #pragma unroll
-        for (int s = 0; s < kNSub; ++s)
-          sc.sb[s] = e8m0_to_f32(static_cast<const uint8_t*>(p.w_scale)[(int64_t)g * p.ws_gstride +
-                                                                        (int64_t)nclamp[s] * p.ldws + ks * 4 + kg]);
+        for (int s = 0; s < NS; ++s) sc.eb[s] = __builtin_amdgcn_raw_buffer_load_b8(sres, soffw[s], (uint32_t)ks * 4, 0);
       }
     };
 
@@ -336,57 +379,74 @@ __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(const GemmParams 
     // Step indices past the slice are clamped to its last step (the
     // duplicate loads hit cache; their MFMAs are skipped).
     struct Chunk {
-      Frag bw[U][kNSub];
+      Frag bw[U][NS];
       Frag fa[U][MS];
-      StepScales<MS> sc[U];
+      StepScales<MS, NS> sc[U];
     };
     auto issue = [&](int ks, Chunk& c) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int kk = min(ks + u, kf1 - 1);
 #pragma unroll
-        for (int s = 0; s < kNSub; ++s) ld<Tr::kWBytes>(c.bw[u][s], wrow[s] + (int64_t)kk * (4 * Tr::kWBytes));
+        for (int s = 0; s < NS; ++s)
+          ldb<Tr::kWBytes, kWeightAux>(c.bw[u][s], wres, woff[s], (uint32_t)kk * (4 * Tr::kWBytes));
 #pragma unroll
-        for (int ms = 0; ms < MS; ++ms) ld<Tr::kABytes>(c.fa[u][ms], arowp[ms] + (int64_t)kk * (4 * Tr::kABytes));
+        for (int ms = 0; ms < MS; ++ms) ldb<Tr::kABytes>(c.fa[u][ms], xres, aoff[ms], (uint32_t)kk * (4 * Tr::kABytes));
         load_scales(kk, c.sc[u]);
       }
     };
     auto consume = [&](int ks, const Chunk& c) {
 #pragma unroll
       for (int u = 0; u < U; ++u)
-        if (ks + u < kf1) mma_step<KIND, WF, MS>(acc, c.fa[u], c.bw[u], c.sc[u]);
+        if (ks + u < kf1) mma_step<KIND, WF, MS, NS>(acc, c.fa[u], c.bw[u], c.sc[u]);
     };
+    // Issues are unconditional (clamped step indices): a load issued only on
+    // some paths would make the wait before the next MFMAs assume the
+    // shorter path and drain the chunk just issued as well. The scheduling
+    // barriers keep the compiler from sinking a chunk's loads below the
+    // MFMAs of the previous one.
     if (ks0 < kf1) {
       Chunk ca, cb;
       issue(ks0, ca);
       for (int ks = ks0; ks < kf1; ks += 2 * U) {
-        const bool more = ks + U < kf1;
-        if (more) issue(ks + U, cb);
+        issue(ks + U, cb);
+        __builtin_amdgcn_sched_barrier(0);
         consume(ks, ca);
-        if (!more) break;
-        if (ks + 2 * U < kf1) issue(ks + 2 * U, ca);
+        __builtin_amdgcn_sched_barrier(0);
+        issue(ks + 2 * U, ca);
+        __builtin_amdgcn_sched_barrier(0);
         consume(ks + U, cb);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
-    // K tail: lanes whose 32 k values start past K feed zeros
+    // K tail: lanes whose 32 k values start past K feed zeros; they load the
+    // step's first 32 values instead (always in range), so no load leaves
+    // the row
     if (tail && ks1 == KS && ks0 < ks1) {
       const int kk = KSF;
       const bool kok = kk * 128 + kg * 32 < p.K;
-      Frag bw[kNSub];
+      const uint32_t kshift = kok ? 0u : (uint32_t)kg;
+      Frag bw[NS];
       Frag fa[MS];
-      StepScales<MS> sc;
+      StepScales<MS, NS> sc;
 #pragma unroll
-      for (int s = 0; s < kNSub; ++s) ld_masked<Tr::kWBytes>(bw[s], wrow[s] + (int64_t)kk * (4 * Tr::kWBytes), kok);
+      for (int s = 0; s < NS; ++s) {
+        ldb<Tr::kWBytes>(bw[s], wres, woff[s] - kshift * Tr::kWBytes, (uint32_t)kk * (4 * Tr::kWBytes));
+        zero_unless<Tr::kWBytes>(bw[s], kok);
+      }
 #pragma unroll
-      for (int ms = 0; ms < MS; ++ms) ld_masked<Tr::kABytes>(fa[ms], arowp[ms] + (int64_t)kk * (4 * Tr::kABytes), kok);
+      for (int ms = 0; ms < MS; ++ms) {
+        ldb<Tr::kABytes>(fa[ms], xres, aoff[ms] - kshift * Tr::kABytes, (uint32_t)kk * (4 * Tr::kABytes));
+        zero_unless<Tr::kABytes>(fa[ms], kok);
+      }
       if constexpr (KIND == QK_W4A16_MX) {
 #pragma unroll
-        for (int s = 0; s < kNSub; ++s)
-          sc.sb[s] = kok ? e8m0_to_f32(static_cast<const uint8_t*>(p.w_scale)[(int64_t)g * p.ws_gstride +
-                                                                              (int64_t)nclamp[s] * p.ldws + kk * 4 + kg])
-                         : 1.0f;
+        for (int s = 0; s < NS; ++s) {
+          const uint32_t b = __builtin_amdgcn_raw_buffer_load_b8(sres, soffw[s] - kshift, (uint32_t)kk * 4, 0);
+          sc.eb[s] = kok ? b : 127u;
+        }
       }
-      mma_step<KIND, WF, MS>(acc, fa, bw, sc);
+      mma_step<KIND, WF, MS, NS>(acc, fa, bw, sc);
     }
 
     // ---- reduce the 4 wavefronts' sums (fixed order) ----
@@ -395,13 +455,13 @@ __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(const GemmParams 
 #pragma unroll
       for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
-        for (int s = 0; s < kNSub; ++s)
+        for (int s = 0; s < NS; ++s)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             float v;
             if constexpr (Tr::kInt) v = __int_as_float(acc.v[ms][s][r]);
             else v = acc.v[ms][s][r];
-            red[wave - 1][(ms * kNSub + s) * 4 + r][lane] = v;
+            red[wave - 1][(ms * NS + s) * 4 + r][lane] = v;
           }
     }
     __syncthreads();
@@ -411,10 +471,10 @@ __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(const GemmParams 
 #pragma unroll
       for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
-        for (int s = 0; s < kNSub; ++s)
+        for (int s = 0; s < NS; ++s)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const float v = red[w][(ms * kNSub + s) * 4 + r][lane];
+            const float v = red[w][(ms * NS + s) * 4 + r][lane];
             if constexpr (Tr::kInt) acc.v[ms][s][r] += __float_as_int(v);
             else acc.v[ms][s][r] += v;
           }
@@ -425,31 +485,33 @@ __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(const GemmParams 
         const int rr = mp + ms * 16 + kg * 4 + r;
         if (rr >= rows) continue;
         const int R = row0 + rr;
-        float v0, v1;
-        if constexpr (Tr::kInt) {
-          v0 = __int_as_float(acc.v[ms][0][r]);
-          v1 = __int_as_float(acc.v[ms][1][r]);
-        } else {
-          v0 = acc.v[ms][0][r];
-          v1 = acc.v[ms][1][r];
+        float v[NS];
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+          if constexpr (Tr::kInt) v[s] = __int_as_float(acc.v[ms][s][r]);
+          else v[s] = acc.v[ms][s][r];
         }
         if (p.ksplit > 1) {
           // raw sums (int32 bit patterns for int8) for the reduce kernel
           float* dst = p.partial + (int64_t)blockIdx.y * plane + (int64_t)R * p.N;
-          if (nok[0]) dst[nw[0]] = v0;
-          if (nok[1]) dst[nw[1]] = v1;
+#pragma unroll
+          for (int s = 0; s < NS; ++s)
+            if (nok[s]) dst[nw[s]] = v[s];
           continue;
         }
         if constexpr (Tr::kInt) {
-          v0 = (float)acc.v[ms][0][r];
-          v1 = (float)acc.v[ms][1][r];
+#pragma unroll
+          for (int s = 0; s < NS; ++s) v[s] = (float)acc.v[ms][s][r];
         }
         const int ar = p.a_rows ? p.a_rows[R] : R;
         if (ACT) {
-          if (nok[0]) store_out<KIND, true>(p, g, R, ar, tile * 16 + col, nw[0], nw[1], v0, v1);
+#pragma unroll
+          for (int s = 0; s < NH; ++s)
+            if (nok[s]) store_out<KIND, true>(p, g, R, ar, nw[s], nw[s], nw[s + NH], v[s], v[s + NH]);
         } else {
-          if (nok[0]) store_out<KIND, false>(p, g, R, ar, nw[0], nw[0], 0, v0, 0.0f);
-          if (nok[1]) store_out<KIND, false>(p, g, R, ar, nw[1], nw[1], 0, v1, 0.0f);
+#pragma unroll
+          for (int s = 0; s < NS; ++s)
+            if (nok[s]) store_out<KIND, false>(p, g, R, ar, nw[s], nw[s], 0, v[s], 0.0f);
         }
       }
   }
@@ -493,17 +555,17 @@ __global__ __launch_bounds__(kThreads) void skinny_reduce_kernel(const GemmParam
   }
 }
 
-template <int KIND, int WF, int MS, bool ACT>
+template <int KIND, int WF, int MS, bool ACT, int NS>
 void launch_skinny(const GemmParams& p, dim3 grid, hipStream_t st) {
   const char* env_s = getenv("QMOE_SKINNY_U");  // tuning knob
   const int env_u = env_s ? atoi(env_s) : 0;
   const int u = env_u > 0 ? env_u : default_unroll(KIND, MS, p.group_offs != nullptr);
   if (u >= 4)
-    hipLaunchKernelGGL((skinny_gemm_kernel<KIND, WF, MS, ACT, 4>), grid, dim3(kThreads), 0, st, p);
+    hipLaunchKernelGGL((skinny_gemm_kernel<KIND, WF, MS, ACT, 4, NS>), grid, dim3(kThreads), 0, st, p);
   else if (u == 2)
-    hipLaunchKernelGGL((skinny_gemm_kernel<KIND, WF, MS, ACT, 2>), grid, dim3(kThreads), 0, st, p);
+    hipLaunchKernelGGL((skinny_gemm_kernel<KIND, WF, MS, ACT, 2, NS>), grid, dim3(kThreads), 0, st, p);
   else
-    hipLaunchKernelGGL((skinny_gemm_kernel<KIND, WF, MS, ACT, 1>), grid, dim3(kThreads), 0, st, p);
+    hipLaunchKernelGGL((skinny_gemm_kernel<KIND, WF, MS, ACT, 1, NS>), grid, dim3(kThreads), 0, st, p);
   if (p.ksplit > 1) {
     const int nout = ACT ? p.N / 2 : p.N;
     dim3 rg((unsigned)cdiv(nout, 64), 1, grid.z);
@@ -512,16 +574,47 @@ void launch_skinny(const GemmParams& p, dim3 grid, hipStream_t st) {
 }
 
 template <int KIND, int WF, bool ACT>
-void launch_ms(const GemmParams& p, int ms, dim3 grid, hipStream_t st) {
-  if (ms == 1) launch_skinny<KIND, WF, 1, ACT>(p, grid, st);
-  else if (ms == 2) launch_skinny<KIND, WF, 2, ACT>(p, grid, st);
-  else launch_skinny<KIND, WF, 4, ACT>(p, grid, st);
+void launch_ms(const GemmParams& p, int ms, int ns, dim3 grid, hipStream_t st) {
+  if (ms == 1) {
+    if constexpr (KIND == QK_W4A16_MX) {
+      if (ns == 4) {
+        launch_skinny<KIND, WF, 1, ACT, 4>(p, grid, st);
+        return;
+      }
+    }
+    launch_skinny<KIND, WF, 1, ACT, 2>(p, grid, st);
+  } else if (ms == 2) {
+    launch_skinny<KIND, WF, 2, ACT, 2>(p, grid, st);
+  } else {
+    launch_skinny<KIND, WF, 4, ACT, 2>(p, grid, st);
+  }
 }
 
 template <int KIND, int WF>
-void launch_act(const GemmParams& p, int ms, dim3 grid, hipStream_t st) {
-  if (p.act != QA_NONE) launch_ms<KIND, WF, true>(p, ms, grid, st);
-  else launch_ms<KIND, WF, false>(p, ms, grid, st);
+void launch_act(const GemmParams& p, int ms, int ns, dim3 grid, hipStream_t st) {
+  if (p.act != QA_NONE) launch_ms<KIND, WF, true>(p, ms, ns, grid, st);
+  else launch_ms<KIND, WF, false>(p, ms, ns, grid, st);
+}
+
+// 16-row M tiles per pass for a problem whose groups hold `rows` rows
+int skinny_ms(int rows) {
+  int ms = rows <= 16 ? 1 : (rows <= 32 ? 2 : 4);
+  const char* env_ms = getenv("QMOE_SKINNY_MS");  // tuning knob: 1, 2 or 4
+  if (env_ms && (atoi(env_ms) == 1 || atoi(env_ms) == 2 || atoi(env_ms) == 4)) ms = atoi(env_ms);
+  return ms;
+}
+
+// 16-row weight tiles per workgroup: 2 (measured on MI355X: 4 tiles for
+// e2m1 weights gain a few percent on grouped decode and lose a third on
+// dense decode, where the workgroup count halves)
+int skinny_ns(int kind, int ms) {
+  if (kind != QK_W4A16_MX || ms != 1) return 2;
+  const char* env = getenv("QMOE_SKINNY_NS");  // tuning knob: 2 or 4
+  return env && atoi(env) == 4 ? 4 : 2;
+}
+
+int skinny_tiles(int64_t N, int act, int ns) {
+  return act != QA_NONE ? (int)cdiv<int64_t>(N / 2, 8 * ns) : (int)cdiv<int64_t>(N, 16 * ns);
 }
 
 }  // namespace
@@ -532,9 +625,9 @@ void launch_act(const GemmParams& p, int ms, dim3 grid, hipStream_t st) {
 // partial-sum traffic; measured on MI355X, one workgroup per 32 weight rows
 // streams best once there are >= 160 of them), and every wavefront keeps at
 // least two 128-k steps.
-void qmoe_skinny_plan(int64_t M, int64_t N, int64_t K, int act, int slots, int ksplit_hint,
-                      int* ksplit_out, int64_t* ws_bytes) {
-  const int n_tiles = act != QA_NONE ? (int)cdiv<int64_t>(N / 2, 16) : (int)cdiv<int64_t>(N, 32);
+void qmoe_skinny_plan(int kind, int64_t M, int64_t N, int64_t K, int act, int slots, int rows,
+                      int ksplit_hint, int* ksplit_out, int64_t* ws_bytes) {
+  const int n_tiles = skinny_tiles(N, act, skinny_ns(kind, skinny_ms(rows)));
   const int KS = (int)cdiv<int64_t>(K, 128);
   int ksplit = ksplit_hint;
   // tuning knobs (read per call): QMOE_SKINNY_KSPLIT forces the split,
@@ -551,8 +644,8 @@ void qmoe_skinny_plan(int64_t M, int64_t N, int64_t K, int act, int slots, int k
 }
 
 // Host-side launcher shared by the dense and MoE entry points.
-//   max_rows : rows of the largest group (sizes the M tile; larger groups
-//              are still correct, in more passes)
+//   max_rows : rows the M tile is sized for (groups with more rows are
+//              still correct, in more passes)
 //   slots    : gridDim.z (groups, or the capacity of the active list)
 // Returns a QMOE_* status.
 int qmoe_skinny_launch(int kind, GemmParams p, int max_rows, int slots, void* workspace,
@@ -561,13 +654,20 @@ int qmoe_skinny_launch(int kind, GemmParams p, int max_rows, int slots, void* wo
   if (p.K <= 0 || (p.K % 32) != 0 || p.N <= 0) return QMOE_ERR_ARG;
   if (p.act != QA_NONE && (p.N % 2) != 0) return QMOE_ERR_ARG;
   if (kind == QK_W8A8_BLK && (p.K % 128) != 0) return QMOE_ERR_ARG;
-  int ms = max_rows <= 16 ? 1 : (max_rows <= 32 ? 2 : 4);
-  const char* env_ms = getenv("QMOE_SKINNY_MS");  // tuning knob: 1, 2 or 4
-  if (env_ms && (atoi(env_ms) == 1 || atoi(env_ms) == 2 || atoi(env_ms) == 4)) ms = atoi(env_ms);
-  const int n_tiles = p.act != QA_NONE ? cdiv(p.N / 2, 16) : cdiv(p.N, 32);
+  // 32-bit buffer offsets: every operand stream stays below 2 GiB
+  const bool abf16 = kind == QK_W8A16_PC || kind == QK_W4A16_MX || kind == QK_W16A16;
+  constexpr int64_t kLim = 0x7fffffff;
+  if ((int64_t)p.N * p.ldw > kLim || p.M * p.lda * (abf16 ? 2 : 1) > kLim) return QMOE_ERR_ARG;
+  if (kind == QK_W4A16_MX && (int64_t)p.N * p.ldws > kLim) return QMOE_ERR_ARG;
+  if (kind == QK_W8A8_BLK &&
+      ((int64_t)cdiv(p.N, p.ws_bn) * p.ldws * 4 > kLim || p.M * p.lds_a * 4 > kLim))
+    return QMOE_ERR_ARG;
+  const int ms = skinny_ms(max_rows);
+  const int ns = skinny_ns(kind, ms);
+  const int n_tiles = skinny_tiles(p.N, p.act, ns);
   int ksplit = 1;
   int64_t need = 0;
-  qmoe_skinny_plan(p.M, p.N, p.K, p.act, slots, ksplit_hint, &ksplit, &need);
+  qmoe_skinny_plan(kind, p.M, p.N, p.K, p.act, slots, max_rows, ksplit_hint, &ksplit, &need);
   p.ksplit = ksplit;
   if (ksplit > 1) {
     if (!workspace || ws_bytes < need) return QMOE_ERR_WORKSPACE;
@@ -576,13 +676,13 @@ int qmoe_skinny_launch(int kind, GemmParams p, int max_rows, int slots, void* wo
   dim3 grid(n_tiles, ksplit, slots);
   switch (kind) {
     case QK_W8A8_PC:
-      if (p.wfmt == 0) launch_act<QK_W8A8_PC, 0>(p, ms, grid, st);
-      else launch_act<QK_W8A8_PC, 1>(p, ms, grid, st);
+      if (p.wfmt == 0) launch_act<QK_W8A8_PC, 0>(p, ms, ns, grid, st);
+      else launch_act<QK_W8A8_PC, 1>(p, ms, ns, grid, st);
       break;
-    case QK_W8A8_BLK: launch_act<QK_W8A8_BLK, 0>(p, ms, grid, st); break;
-    case QK_W8A16_PC: launch_act<QK_W8A16_PC, 0>(p, ms, grid, st); break;
-    case QK_W4A16_MX: launch_act<QK_W4A16_MX, 0>(p, ms, grid, st); break;
-    case QK_W16A16: launch_act<QK_W16A16, 0>(p, ms, grid, st); break;
+    case QK_W8A8_BLK: launch_act<QK_W8A8_BLK, 0>(p, ms, ns, grid, st); break;
+    case QK_W8A16_PC: launch_act<QK_W8A16_PC, 0>(p, ms, ns, grid, st); break;
+    case QK_W4A16_MX: launch_act<QK_W4A16_MX, 0>(p, ms, ns, grid, st); break;
+    case QK_W16A16: launch_act<QK_W16A16, 0>(p, ms, ns, grid, st); break;
     default: return QMOE_ERR_ARG;
   }
   return hipGetLastError() == hipSuccess ? QMOE_OK : QMOE_ERR_LAUNCH;

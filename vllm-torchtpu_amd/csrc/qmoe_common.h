@@ -87,10 +87,11 @@ QMOE_HD float e4m3_to_f32(uint32_t c) {
 
 // e8m0 byte -> float32 2^(b-127). b == 0 is the f32 subnormal 2^-127 and
 // b == 255 is +inf, matching the reference's ldexp-based decoder.
+// Branch-free: 255 << 23 is already the +inf pattern, and every b >= 1
+// gives a pattern above the subnormal's, so one unsigned max covers b == 0.
 QMOE_HD float e8m0_to_f32(uint32_t b) {
-  if (b == 0) return bits_f32(0x00400000u);
-  if (b == 255) return bits_f32(0x7f800000u);
-  return bits_f32(b << 23);
+  const uint32_t bits = (b & 0xffu) << 23;
+  return bits_f32(bits > 0x00400000u ? bits : 0x00400000u);
 }
 
 // ----------------------------------------------------------------- misc
