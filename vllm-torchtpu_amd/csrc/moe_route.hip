@@ -10,6 +10,11 @@
 // Scores are evaluated in float64 and rounded once to float32 (the correctly
 // rounded score), so that a bias-corrected choice score -- compared exactly
 // -- is reproducible on any host that evaluates the same definition.
+//
+// The kernel is instantiated per (slots, scoring rule, grouped): a decode
+// step runs it on one CU with a cold instruction cache, so its time is
+// mostly instruction fetch, and each instantiation carries only the code of
+// its own rule.
 
 #include "qmoe_common.h"
 
@@ -18,13 +23,28 @@ namespace {
 constexpr int kMaxSlots = 8;  // E <= 512
 constexpr float kNeg = -3.0e38f;
 
-__device__ __forceinline__ float score_of(float x, int scoring) {
-  if (scoring == 3) return x;  // scores given
-  double d = (double)x;
-  if (scoring == 1) return (float)(1.0 / (1.0 + exp(-d)));
-  // sqrtsoftplus: sqrt(log(1 + e^x)), evaluated stably
-  double sp = d > 0.0 ? d + log1p(exp(-d)) : log1p(exp(d));
-  return (float)sqrt(sp);
+// scoring rules: 0 softmax (over the row), 1 sigmoid, 2 sqrtsoftplus,
+// 3 scores given
+template <int SCORING>
+__device__ __forceinline__ float score_of(float x) {
+  if constexpr (SCORING == 3) {
+    return x;
+  } else if constexpr (SCORING == 1) {
+    return (float)(1.0 / (1.0 + exp(-(double)x)));
+  } else {
+    // sqrtsoftplus: sqrt(log(1 + e^x)), evaluated stably
+    const double d = (double)x;
+    const double sp = d > 0.0 ? d + log1p(exp(-d)) : log1p(exp(d));
+    return (float)sqrt(sp);
+  }
+}
+
+// (largest, second largest) of two pairs, duplicates counted
+__device__ __forceinline__ void top2_merge(float& m1, float& m2, float o1, float o2) {
+  const float hi = fmaxf(m1, o1);
+  const float lo = fmaxf(fminf(m1, o1), fmaxf(m2, o2));
+  m1 = hi;
+  m2 = lo;
 }
 
 // Make this wavefront's LDS writes visible to its own later LDS reads.
@@ -34,17 +54,64 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
 
-// (value, index) argmax over the wavefront: largest value, lowest index.
+// Cross-lane reductions without LDS round trips: DPP moves inside each
+// 16-lane row (xor-1 and xor-2 inside quads, then the half-row and row
+// mirrors; each step pairs lanes holding disjoint partial results, so every
+// lane of a row ends with the row's result), then the four row results read
+// into scalars. The results are wave-uniform.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ float lane_f(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+__device__ __forceinline__ float wave_max_u(float v) {
+  v = fmaxf(v, dpp_f<0xB1>(v));
+  v = fmaxf(v, dpp_f<0x4E>(v));
+  v = fmaxf(v, dpp_f<0x141>(v));
+  v = fmaxf(v, dpp_f<0x140>(v));
+  return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
+}
+
+__device__ __forceinline__ int wave_min_u(int v) {
+  v = min(v, dpp_i<0xB1>(v));
+  v = min(v, dpp_i<0x4E>(v));
+  v = min(v, dpp_i<0x141>(v));
+  v = min(v, dpp_i<0x140>(v));
+  return min(min(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+             min(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+
+__device__ __forceinline__ float wave_sum_u(float v) {
+  v = v + dpp_f<0xB1>(v);
+  v = v + dpp_f<0x4E>(v);
+  v = v + dpp_f<0x141>(v);
+  v = v + dpp_f<0x140>(v);
+  return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
+}
+
+// (value, index) argmax over the wavefront: largest value, lowest index
+// among the lanes holding it (values are never NaN here). Uniform result.
 __device__ __forceinline__ void wave_argmax(float& v, int& i) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    float ov = __shfl_xor(v, o, 64);
-    int oi = __shfl_xor(i, o, 64);
-    if (ov > v || (ov == v && oi < i)) {
-      v = ov;
-      i = oi;
-    }
-  }
+  const float m = wave_max_u(v);
+  i = wave_min_u(v == m ? i : 0x7fffffff);
+  v = m;
+}
+
+// Top-2 all-reduce inside aligned groups of G = 2^n <= 64 lanes.
+__device__ __forceinline__ void group_top2(float& m1, float& m2, int G) {
+  if (G > 1) top2_merge(m1, m2, dpp_f<0xB1>(m1), dpp_f<0xB1>(m2));
+  if (G > 2) top2_merge(m1, m2, dpp_f<0x4E>(m1), dpp_f<0x4E>(m2));
+  if (G > 4) top2_merge(m1, m2, dpp_f<0x141>(m1), dpp_f<0x141>(m2));
+  if (G > 8) top2_merge(m1, m2, dpp_f<0x140>(m1), dpp_f<0x140>(m2));
+  if (G > 16) top2_merge(m1, m2, __shfl_xor(m1, 16, 64), __shfl_xor(m2, 16, 64));
+  if (G > 32) top2_merge(m1, m2, __shfl_xor(m1, 32, 64), __shfl_xor(m2, 32, 64));
 }
 
 // One rowmax pass over the lane's slots (values already clamped to >= kNeg,
@@ -69,18 +136,17 @@ __device__ __forceinline__ void rowmax_pass(const float (&cur)[kMaxSlots], int l
   mi = idx;
 }
 
-template <int S>
+template <int S, int SCORING, bool GROUPED>
 __global__ __launch_bounds__(256) void route_kernel(const void* __restrict__ logits, int logits_f32,
-                                                    int64_t T, int E, int topk, int scoring,
+                                                    int64_t T, int E, int topk,
                                                     const float* __restrict__ bias, int renormalize,
                                                     float rsf, int num_group, int topk_group,
                                                     void* __restrict__ out_w, int w_f32,
                                                     int32_t* __restrict__ out_ids) {
   const int lane = threadIdx.x & 63;
   const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  __shared__ float choice_lds[4][kMaxSlots * 64];
+  __shared__ float choice_lds[GROUPED ? 4 : 1][GROUPED ? kMaxSlots * 64 : 1];
   if (t >= T) return;
-  float* ch = choice_lds[threadIdx.x >> 6];
 
   float x[kMaxSlots];
 #pragma unroll
@@ -94,7 +160,7 @@ __global__ __launch_bounds__(256) void route_kernel(const void* __restrict__ log
     x[j] = v;
   }
   float s[kMaxSlots];
-  if (scoring == 0) {  // softmax in float64
+  if constexpr (SCORING == 0) {  // softmax in float64
     float mx = -__builtin_inff();
     bool nan = false;
 #pragma unroll
@@ -103,7 +169,7 @@ __global__ __launch_bounds__(256) void route_kernel(const void* __restrict__ log
         nan |= x[j] != x[j];
         mx = fmaxf(mx, x[j]);
       }
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    mx = wave_max_u(mx);
     double ex[kMaxSlots];
     double sum = 0.0;
 #pragma unroll
@@ -117,7 +183,7 @@ __global__ __launch_bounds__(256) void route_kernel(const void* __restrict__ log
     for (int j = 0; j < S; ++j) s[j] = anynan ? __builtin_nanf("") : (float)(ex[j] / sum);
   } else {
 #pragma unroll
-    for (int j = 0; j < S; ++j) s[j] = score_of(x[j], scoring);
+    for (int j = 0; j < S; ++j) s[j] = score_of<SCORING>(x[j]);
   }
 
   // choice scores
@@ -132,25 +198,41 @@ __global__ __launch_bounds__(256) void route_kernel(const void* __restrict__ log
 #pragma unroll
   for (int j = 0; j < S; ++j) cur[j] = c[j] > kNeg ? c[j] : kNeg;
 
-  if (num_group > 1 && topk_group < num_group) {
+  if constexpr (GROUPED) {
     const int gsize = E / num_group;
-#pragma unroll
-    for (int j = 0; j < S; ++j)
-      if (j * 64 + lane < E) ch[j * 64 + lane] = cur[j];
-    wave_lds_sync();
+    // group score: the top choice score, or the sum of the top two when a
+    // correction bias is given
     float gs = -3.402823466e38f;
-    if (lane < num_group) {
-      float m1 = -__builtin_inff(), m2 = -__builtin_inff();
-      for (int i = 0; i < gsize; ++i) {
-        const float v = ch[lane * gsize + i];
-        if (v > m1) {
-          m2 = m1;
-          m1 = v;
-        } else if (v > m2) {
-          m2 = v;
-        }
+    if (gsize <= 64 && (gsize & (gsize - 1)) == 0) {
+      // power-of-two groups inside a slot: top-2 by a butterfly over the
+      // group's lanes, then lane g fetches group g's result
+      float res[S];
+#pragma unroll
+      for (int j = 0; j < S; ++j) {
+        float m1 = j * 64 + lane < E ? cur[j] : -__builtin_inff();
+        float m2 = -__builtin_inff();
+        group_top2(m1, m2, gsize);
+        res[j] = bias ? (gsize >= 2 ? m1 + m2 : m1) : m1;
       }
-      gs = bias ? (gsize >= 2 ? m1 + m2 : m1) : m1;
+      const int first = (lane < num_group ? lane : 0) * gsize;  // group's first expert
+      float v = 0.0f;
+#pragma unroll
+      for (int j = 0; j < S; ++j) {
+        const float r = __shfl(res[j], first & 63, 64);
+        if (j == (first >> 6)) v = r;
+      }
+      if (lane < num_group) gs = v;
+    } else {
+      float* ch = choice_lds[threadIdx.x >> 6];
+#pragma unroll
+      for (int j = 0; j < S; ++j)
+        if (j * 64 + lane < E) ch[j * 64 + lane] = cur[j];
+      wave_lds_sync();
+      if (lane < num_group) {
+        float m1 = -__builtin_inff(), m2 = -__builtin_inff();
+        for (int i = 0; i < gsize; ++i) top2_merge(m1, m2, ch[lane * gsize + i], -__builtin_inff());
+        gs = bias ? (gsize >= 2 ? m1 + m2 : m1) : m1;
+      }
     }
     // top `topk_group` groups (rowmax order over group scores)
     float gcur = lane < num_group ? (gs > kNeg ? gs : kNeg) : -3.402823466e38f;
@@ -164,47 +246,45 @@ __global__ __launch_bounds__(256) void route_kernel(const void* __restrict__ log
         gcur = -3.402823466e38f;
       }
     }
-    const int keep_i = keep ? 1 : 0;
+    const uint64_t kept_groups = __ballot(keep);
 #pragma unroll
     for (int j = 0; j < S; ++j) {
       const int e = j * 64 + lane;
-      const int kept = __shfl(keep_i, e < E ? e / gsize : 0, 64);
-      if (e < E && !kept) cur[j] = kNeg;
+      if (e < E && !((kept_groups >> (e / gsize)) & 1)) cur[j] = kNeg;
     }
   }
-  const bool gather = bias != nullptr || (num_group > 1 && topk_group < num_group);
+  const bool gather = bias != nullptr || GROUPED;
 
   float first = 0.0f;
   float myw = 0.0f;
+  int myid = 0;
   for (int p = 0; p < topk; ++p) {
     float mv;
     int mi;
-    rowmax_pass<S>(cur, lane, E, mv, mi);
+    rowmax_pass<S>(cur, lane, E, mv, mi);  // wave-uniform results
     if (p == 0) first = mv;
     // weight: the pass value for plain top-k, the unbiased score otherwise
     float w = mv;
     if (gather) {
-      const int src_lane = mi & 63;
       const int src_slot = mi >> 6;
       float sv = 0.0f;
 #pragma unroll
       for (int j = 0; j < S; ++j)
         if (j == src_slot) sv = s[j];
-      w = __shfl(sv, src_lane, 64);
+      w = lane_f(sv, mi & 63);
     }
     if (lane == p) {
-      out_ids[t * topk + p] = mi;
+      myid = mi;
       myw = w;
     }
 #pragma unroll
     for (int j = 0; j < S; ++j)
       if (j * 64 + lane == mi) cur[j] = -3.402823466e38f;
   }
+  if (lane < topk) out_ids[t * topk + lane] = myid;
   // a plain top-k row with no score above the sentinel is poisoned (NaN)
   if (!gather && first <= kNeg) myw = __builtin_nanf("");
-  float sum = lane < topk ? myw : 0.0f;
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+  const float sum = wave_sum_u(lane < topk ? myw : 0.0f);
   if (lane < topk) {
     float v = myw;
     if (renormalize) v = v / (sum != sum ? sum : fmaxf(sum, 1e-20f));
@@ -212,6 +292,33 @@ __global__ __launch_bounds__(256) void route_kernel(const void* __restrict__ log
     if (w_f32) static_cast<float*>(out_w)[t * topk + lane] = v;
     else static_cast<uint16_t*>(out_w)[t * topk + lane] = f32_to_bf16(v);
   }
+}
+
+template <int S, int SCORING, bool GROUPED, typename... A>
+void launch_route3(dim3 grid, hipStream_t st, A... a) {
+  hipLaunchKernelGGL((route_kernel<S, SCORING, GROUPED>), grid, dim3(256), 0, st, a...);
+}
+
+template <int S, typename... A>
+void launch_route2(int scoring, bool grouped, dim3 grid, hipStream_t st, A... a) {
+  switch (scoring * 2 + (grouped ? 1 : 0)) {
+    case 0: launch_route3<S, 0, false>(grid, st, a...); break;
+    case 1: launch_route3<S, 0, true>(grid, st, a...); break;
+    case 2: launch_route3<S, 1, false>(grid, st, a...); break;
+    case 3: launch_route3<S, 1, true>(grid, st, a...); break;
+    case 4: launch_route3<S, 2, false>(grid, st, a...); break;
+    case 5: launch_route3<S, 2, true>(grid, st, a...); break;
+    case 6: launch_route3<S, 3, false>(grid, st, a...); break;
+    default: launch_route3<S, 3, true>(grid, st, a...); break;
+  }
+}
+
+template <typename... A>
+void launch_route(int S, int scoring, bool grouped, dim3 grid, hipStream_t st, A... a) {
+  if (S == 1) launch_route2<1>(scoring, grouped, grid, st, a...);
+  else if (S == 2) launch_route2<2>(scoring, grouped, grid, st, a...);
+  else if (S == 4) launch_route2<4>(scoring, grouped, grid, st, a...);
+  else launch_route2<8>(scoring, grouped, grid, st, a...);
 }
 
 }  // namespace
@@ -230,15 +337,8 @@ extern "C" int qmoe_moe_route(const void* logits, int logits_f32, int64_t T, int
   }
   if (T == 0) return QMOE_OK;
   const int S = (E + 63) / 64;
-  dim3 grid((unsigned)((T + 3) / 4));
-#define QMOE_ROUTE(SS)                                                                              \
-  hipLaunchKernelGGL((route_kernel<SS>), grid, dim3(256), 0, stream, logits, logits_f32, T, E, topk, \
-                     scoring, bias, renormalize, routed_scaling_factor, num_group, topk_group,      \
-                     topk_weights, weights_f32, topk_ids)
-  if (S <= 1) QMOE_ROUTE(1);
-  else if (S <= 2) QMOE_ROUTE(2);
-  else if (S <= 4) QMOE_ROUTE(4);
-  else QMOE_ROUTE(8);
-#undef QMOE_ROUTE
+  launch_route(S <= 1 ? 1 : (S <= 2 ? 2 : (S <= 4 ? 4 : 8)), scoring, grouped, dim3((unsigned)((T + 3) / 4)),
+               stream, logits, logits_f32, T, E, topk, bias, renormalize, routed_scaling_factor, num_group,
+               topk_group, topk_weights, weights_f32, topk_ids);
   return hipGetLastError() == hipSuccess ? QMOE_OK : QMOE_ERR_LAUNCH;
 }
