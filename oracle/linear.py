@@ -46,7 +46,7 @@ def w8a16_per_channel(x, wq, ws, qdtype="fp8"):
     return bf16_round(out)
 
 
-def w8a8_blockwise(x, wq, ws_blocks, block=128):
+def w8a8_blockwise(x, wq, ws_blocks, block=128, round_out=True):
     """`tests/kernels/test_quantized_matmul_kernel.py:66-94`
     (`reference_block_quantized_matmul`), the oracle of the blockwise kernel
     `kernels/quantized_matmul/blockwise_kernel.py:197-247`.
@@ -56,7 +56,9 @@ def w8a8_blockwise(x, wq, ws_blocks, block=128):
     multiplied by ``x_s`` and ``w_s`` and the blocks are summed.
 
     ``ws_blocks`` is the per-(n, K-block) scale ``[N, K/B]`` (a 128x128 tile
-    scale repeated along N is the DeepSeek-V3 case). Returns (y, xq, xs).
+    scale repeated along N is the DeepSeek-V3 case). Returns (y, xq, xs); y is
+    the bf16-rounded output, or the float32 sums with ``round_out=False`` (the
+    input of a fused activation).
     """
     m, k = x.shape
     n = wq.shape[0]
@@ -67,7 +69,7 @@ def w8a8_blockwise(x, wq, ws_blocks, block=128):
     for b in range(k // block):
         d = _mm(xv[:, b, :], wv[:, b, :])
         out += (d * xs[:, b:b + 1]).astype(np.float32) * ws_blocks[None, :, b]
-    return bf16_round(out), xq, xs
+    return (bf16_round(out) if round_out else out), xq, xs
 
 
 def tile_scales_to_blocks(scale_tiles, n, tile=128):

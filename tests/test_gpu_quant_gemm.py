@@ -120,7 +120,10 @@ def test_w8a8_int8_per_channel_bit_exact(dev, M, K, N):
     np.testing.assert_array_equal(y.float().cpu().numpy(), ref)
 
 
-@pytest.mark.parametrize("M,K,N", [(1, 1024, 512), (32, 2048, 768), (130, 1024, 640), (256, 2048, 1024)])
+@pytest.mark.parametrize("M,K,N", [(1, 1024, 512), (32, 2048, 768), (130, 1024, 640), (256, 2048, 1024),
+                                   # tiled block-scaled kernel: ragged tiles, 32/64/128-token tiles,
+                                   # a K split (tall K, few tokens)
+                                   (300, 2048, 1280), (70, 1536, 384), (400, 1024, 2304), (96, 8192, 512)])
 @pytest.mark.parametrize("tile_scales", [True, False])
 def test_w8a8_fp8_block(dev, M, K, N, tile_scales):
     from qmoe import _capi, ops
@@ -198,6 +201,25 @@ def test_split_k_deterministic_and_reusable(dev):
     for o in outs[1:]:
         assert torch.equal(o, outs[0])
     assert_close_rows(outs[0].float().cpu().numpy(), ref, "split-k")
+
+
+@pytest.mark.parametrize("M,K,I", [(200, 1024, 384), (96, 8192, 256)])
+def test_w8a8_fp8_block_fused_activation(dev, M, K, I):
+    """Block-scaled FP8 GEMM with the gate/up SwiGLU fused (DeepSeek shared
+    expert form), with and without a K split."""
+    from qmoe import _capi, ops
+
+    print(f"w8a8 blk act M={M} K={K} I={I}", flush=True)
+    rng = np.random.default_rng(M + K + I)
+    w = (rng.standard_normal((2 * I, K)) * 0.02).astype(np.float32)
+    wq, st = quant.quantize_fp8_tiles(w)
+    x = _bf16(rng, (M, K))
+    gu, _, _ = linear.w8a8_blockwise(x, wq, linear.tile_scales_to_blocks(st, 2 * I), round_out=False)
+    ref = codecs.bf16_round(omoe.act_fn(gu[:, :I].astype(np.float32), gu[:, I:].astype(np.float32), "silu"))
+    xq, xs = ops.row_quant(_t(x, dev, torch.bfloat16), "fp8", block=128)
+    y = ops.gemm(_capi.W8A8_BLK, xq.view(torch.uint8), _t(wq, dev), a_scale=xs, w_scale=_t(st, dev),
+                 ws_bn=128, activation="silu")
+    assert_close_rows(y.float().cpu().numpy(), ref, f"fp8 blk silu {M}x{K}x{I}")
 
 
 @pytest.mark.parametrize("act", ["silu", "swigluoai"])

@@ -13,8 +13,8 @@ void qmoe_skinny_plan(int kind, int64_t M, int64_t N, int64_t K, int act, int sl
 int qmoe_skinny_launch(int kind, GemmParams p, int max_rows, int slots, void* workspace,
                        int64_t ws_bytes, int ksplit_hint, hipStream_t st);
 int qmoe_tiled_launch(int kind, GemmParams p, hipStream_t st);
-bool qmoe_f8_plan(const GemmParams& p, int* bm_out, int* ksplit_out, int64_t* ws_bytes);
-int qmoe_f8_launch(GemmParams p, void* workspace, int64_t ws_bytes, hipStream_t st);
+bool qmoe_f8_plan(const GemmParams& p, bool blk, int* bm_out, int* ksplit_out, int64_t* ws_bytes);
+int qmoe_f8_launch(GemmParams p, bool blk, void* workspace, int64_t ws_bytes, hipStream_t st);
 
 namespace {
 
@@ -105,7 +105,8 @@ bool use_skinny(const qmoe_gemm_desc* d) {
 }
 
 bool use_f8(const qmoe_gemm_desc* d) {
-  return d->kind == QMOE_W8A8_PC && !getenv("QMOE_F8_OFF");  // tuning knob: generic kernel only
+  if (getenv("QMOE_F8_OFF")) return false;  // tuning knob: generic kernel only
+  return d->kind == QMOE_W8A8_PC || (d->kind == QMOE_W8A8_BLK && !getenv("QMOE_F8_BLK_OFF"));
 }
 
 }  // namespace
@@ -124,7 +125,7 @@ extern "C" int qmoe_gemm_workspace_size(const qmoe_gemm_desc* d, int64_t* bytes)
     p.active = nullptr;
     p.num_active = nullptr;
     int bm = 0, ks = 1;
-    if (!qmoe_f8_plan(p, &bm, &ks, bytes)) *bytes = 0;
+    if (!qmoe_f8_plan(p, d->kind == QMOE_W8A8_BLK, &bm, &ks, bytes)) *bytes = 0;
   }
   return QMOE_OK;
 }
@@ -151,7 +152,7 @@ extern "C" int qmoe_gemm(const qmoe_gemm_desc* d, void* workspace, int64_t ws_by
   if (use_f8(d)) {
     // 1-byte x 1-byte kernel; it declines (QMOE_ERR_ARG) problems outside its
     // envelope (K % 256, 16-byte alignment), which the generic kernel takes
-    const int rc = qmoe_f8_launch(p, workspace, ws_bytes, stream);
+    const int rc = qmoe_f8_launch(p, d->kind == QMOE_W8A8_BLK, workspace, ws_bytes, stream);
     if (rc != QMOE_ERR_ARG) return rc;
   }
   return qmoe_tiled_launch(d->kind, p, stream);

@@ -181,9 +181,11 @@ __device__ __forceinline__ bool f8_dense_tile(int b, int m_tiles, int n_tiles, i
   return true;
 }
 
-template <bool INT, int BM, int BN, bool ACT, int KB>
+template <bool INT, int BM, int BN, bool ACT, int KB, bool BLK>
 __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, int m_tiles, int n_tiles) {
   static_assert(KB == 64 || KB == 128, "K bytes per LDS stage");
+  // BLK: 128x128 block scales (W8A8_BLK): one 128-byte stage is one K block
+  static_assert(!BLK || (KB == 128 && !INT && BN == 256), "block scales: FP8, 128-byte stages, 256-row tiles");
   using S = F8Shape<BM, BN>;
   constexpr int NI = S::NI, MJ = S::MJ, TN = S::TN, TM = S::TM;
   constexpr int BNO = ACT ? BN / 2 : BN;  // output channels per tile
@@ -192,12 +194,20 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
 
   // LDS stages, each operand of each stage in its own array: four stages of
   // 64 K-bytes (KB = 64) or two of 128 (KB = 128; arrays 2 and 3 unused)
+  // (KB = 128 with tiles of at most 128 tokens: three stages fit in LDS,
+  // array 2 holds the third)
+  constexpr bool TRI = KB == 128 && BM <= 128;
   constexpr int XRS = KB == 64 ? S::XR : BM;  // activation rows per stage array
-  constexpr int U2 = KB == 64 ? 1 : 0;        // arrays 2, 3 in use
-  __shared__ __align__(1024) uint8_t sW0[BN * KB], sW1[BN * KB], sW2[U2 ? BN * 64 : 16], sW3[U2 ? BN * 64 : 16];
-  __shared__ __align__(1024) uint8_t sX0[XRS * KB], sX1[XRS * KB], sX2[U2 ? XRS * 64 : 16], sX3[U2 ? XRS * 64 : 16];
+  constexpr int B2 = KB == 64 ? 64 : (TRI ? 128 : 0);  // bytes per row of array 2
+  constexpr int B3 = KB == 64 ? 64 : 0;                // and of array 3
+  __shared__ __align__(1024) uint8_t sW0[BN * KB], sW1[BN * KB], sW2[B2 ? BN * B2 : 16], sW3[B3 ? BN * B3 : 16];
+  __shared__ __align__(1024) uint8_t sX0[XRS * KB], sX1[XRS * KB], sX2[B2 ? XRS * B2 : 16], sX3[B3 ? XRS * B3 : 16];
   __shared__ int s_info[4];
   __shared__ float s_sx[BM], s_rw[BM], s_ws[BN], s_bs[BN];
+  // BLK: per-stage scales, one 64-float slot per wavefront: [0, BM) token
+  // scales of the stage's K block, [BM, BM + 2) the scales of the tile's two
+  // 128-row weight blocks (LDS rows 0..127 and 128..255), the rest unused
+  __shared__ __align__(16) float sS0[BLK ? 256 : 1], sS1[BLK ? 256 : 1], sS2[BLK && TRI ? 256 : 1];
   __shared__ int s_yr[BM];
 
   const int tid = threadIdx.x;
@@ -227,7 +237,7 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
   if (tid < BM) {
     const int R = row0 + min(tid, rows - 1);
     const int ar = p.a_rows ? p.a_rows[R] : R;
-    e_sx = p.a_scale[(int64_t)ar * p.lds_a];
+    e_sx = BLK ? 1.0f : p.a_scale[(int64_t)ar * p.lds_a];
     if (p.row_weight) e_rw = bf16_to_f32(p.row_weight[R]);
     e_yr = p.y_rows ? p.y_rows[R] : R;
   }
@@ -239,7 +249,7 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
     } else {
       n = min(n0 + tid, nlim - 1);
     }
-    e_ws = static_cast<const float*>(p.w_scale)[(int64_t)g * p.ws_gstride + n];
+    e_ws = BLK ? 1.0f : static_cast<const float*>(p.w_scale)[(int64_t)g * p.ws_gstride + n];
     if (p.bias) e_bs = p.bias[(int64_t)g * p.bias_gstride + n];
   }
 
@@ -281,6 +291,23 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
     }
     woff[j] = (uint32_t)n * (uint32_t)p.ldw + chunk_of(r);
   }
+  // BLK: this lane's source for the per-stage scale copy (4 bytes; the K
+  // block index is added per stage): LDS slot wave*64 + lane holds token
+  // scale `slot` for slot < BM, the scale of LDS weight rows
+  // [(slot-BM)*128, +128) for slot < BM + 2, a duplicate elsewhere
+  const float* sc_src = p.a_scale;
+  if constexpr (BLK) {
+    const int slot = wave * 64 + lane;
+    if (slot >= BM && slot < BM + 2) {
+      const int b = slot - BM;
+      const int n = ACT ? (b == 0 ? 0 : p.N / 2) + min(n0, nlim - 1) : min(n0 + b * 128, nlim - 1);
+      sc_src = static_cast<const float*>(p.w_scale) + (int64_t)g * p.ws_gstride + (int64_t)(n / 128) * p.ldws;
+    } else {
+      const int R = row0 + min(slot < BM ? slot : 0, rows - 1);
+      const int ar = p.a_rows ? p.a_rows[R] : R;
+      sc_src = p.a_scale + (int64_t)ar * p.lds_a;
+    }
+  }
   // The row terms pass through an empty asm so that the compiler forms the
   // 64-bit addresses at each copy instead of keeping them alive across the
   // MFMA loop.
@@ -290,8 +317,10 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
   const int u0 = (int)((int64_t)NU * blockIdx.z / p.ksplit);
   const int u1 = (int)((int64_t)NU * (blockIdx.z + 1) / p.ksplit);
   const uint32_t kbase = (uint32_t)u0 * 256u;
-  auto copy_stage = [&](uint8_t* dW, uint8_t* dX, int ks) {
+  auto copy_stage = [&](uint8_t* dW, uint8_t* dX, float* dS, int ks) {
     const uint32_t kb = kbase + (uint32_t)ks * (uint32_t)KB;
+    if constexpr (BLK)
+      __builtin_amdgcn_global_load_lds(sc_src + kb / 128, QMOE_LDS(dS + wave * 64), 4, 0, 0);
 #pragma unroll
     for (int j = 0; j < WI; ++j) {
       uint32_t o = woff[j];
@@ -348,12 +377,31 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
 
+  // BLK: the stage's block sums go to tmp, then acc += tmp * (sx * sw)
+  f32x16 tmp[BLK ? NI : 1][BLK ? MJ : 1];
+  float scl[BLK ? NI : 1][BLK ? MJ : 1];
+  auto read_scales = [&](const float* sS) {
+    if constexpr (BLK) {
+      float sx[MJ];
+#pragma unroll
+      for (int j = 0; j < MJ; ++j) sx[j] = sS[wm * TM + j * 32 + rl];
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const float sw = sS[BM + wrow(i) / 128];
+#pragma unroll
+        for (int j = 0; j < MJ; ++j) scl[i][j] = sx[j] * sw;
+      }
+    }
+  };
   auto mma = [&](int t) {
 #pragma unroll
     for (int i = 0; i < NI; ++i)
 #pragma unroll
       for (int j = 0; j < MJ; ++j) {
-        if constexpr (INT) {
+        if constexpr (BLK) {
+          const f32x16 c = t == 0 ? f32x16{} : tmp[i][j];
+          tmp[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[t][i], xf[t][j], c, 0, 0, 0, 127, 0, 127);
+        } else if constexpr (INT) {
           acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(lo4(wf[t][i]), lo4(xf[t][j]), acc[i][j], 0, 0, 0);
           acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(hi4(wf[t][i]), hi4(xf[t][j]), acc[i][j], 0, 0, 0);
         } else {
@@ -363,7 +411,18 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
       }
   };
 
-  constexpr int CPS = WI + XI;  // copy instructions per wavefront per stage
+  auto apply_scales = [&]() {
+    if constexpr (BLK) {
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+#pragma unroll
+        for (int j = 0; j < MJ; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[i][j][r] += tmp[i][j][r] * scl[i][j];
+    }
+  };
+
+  constexpr int CPS = WI + XI + (BLK ? 1 : 0);  // copy instructions per wavefront per stage
   constexpr int NM = NI * MJ * (INT ? 2 : 1);  // MFMAs per k-step
   constexpr int NR = 2 * (NI + MJ);            // LDS operand reads per k-step
   if constexpr (KB == 64) {
@@ -378,17 +437,17 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
     // the last stage into a consumed buffer, which is never read again), so
     // the loop body has no branch.
     const int KS = (u1 - u0) * 4;
-    copy_stage(sW0, sX0, 0);
-    copy_stage(sW1, sX1, 1);
-    copy_stage(sW2, sX2, 2);
-    copy_stage(sW3, sX3, 3);
+    copy_stage(sW0, sX0, sS0, 0);
+    copy_stage(sW1, sX1, sS0, 1);
+    copy_stage(sW2, sX2, sS0, 2);
+    copy_stage(sW3, sX3, sS0, 3);
     wait_copies_upto<3 * CPS>();
     __syncthreads();
     read_frags(sW0, sX0, 0, 0);
     auto stage = [&](uint8_t* fW, uint8_t* fX, uint8_t* nW, uint8_t* nX, int s, int t) {
       wait_copies_upto<2 * CPS>();  // copies issued after stage s+1's: s+2, s+3
       stage_barrier();
-      copy_stage(fW, fX, min(s + 4, KS - 1));
+      copy_stage(fW, fX, sS0, min(s + 4, KS - 1));
       mma(t);
       read_frags(nW, nX, 0, t ^ 1);
       interleave<0, NM, NR, CPS>();
@@ -407,26 +466,45 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
     // read everywhere, so its buffer is free) -> copy stage s+2 into it ->
     // MFMAs of k-step 1 while k-step 0 of stage s+1 is read. A copy has one
     // stage (two k-steps of MFMAs) to land.
+    // BLK: the stage's scales are read with its second k-step (before the
+    // barrier that frees its buffer) and applied after the k-step's MFMAs.
+    // With three buffers (TRI) the buffer freed at stage s's barrier takes
+    // stage s+3, so a copy has two stages to land.
     const int KS = (u1 - u0) * 2;
-    copy_stage(sW0, sX0, 0);
-    copy_stage(sW1, sX1, 1);
-    wait_copies_upto<CPS>();
-    __syncthreads();
-    read_frags(sW0, sX0, 0, 0);
-    auto stage = [&](uint8_t* cW, uint8_t* cX, uint8_t* nW, uint8_t* nX, int s) {
+    constexpr int AHEAD = TRI ? 3 : 2;
+    auto stage = [&](uint8_t* cW, uint8_t* cX, float* cS, uint8_t* nW, uint8_t* nX, int s) {
       mma(0);
       read_frags(cW, cX, 1, 1);
-      interleave<0, NM, NR, 0>();
-      wait_copies_upto<0>();
+      read_scales(cS);
+      interleave<0, NM, NR + (BLK ? MJ + NI : 0), 0>();
+      wait_copies_upto<(AHEAD - 2) * CPS>();  // stage s+1 has landed
       stage_barrier();
-      copy_stage(cW, cX, min(s + 2, KS - 1));
+      copy_stage(cW, cX, cS, min(s + AHEAD, KS - 1));
       mma(1);
+      apply_scales();
       read_frags(nW, nX, 0, 0);
       interleave<0, NM, NR, CPS>();
     };
-    for (int s = 0; s < KS; s += 2) {
-      stage(sW0, sX0, sW1, sX1, s);
-      stage(sW1, sX1, sW0, sX0, s + 1);
+    copy_stage(sW0, sX0, sS0, 0);
+    copy_stage(sW1, sX1, sS1, 1);
+    if constexpr (TRI) copy_stage(sW2, sX2, sS2, min(2, KS - 1));
+    wait_copies_upto<(AHEAD - 1) * CPS>();
+    __syncthreads();
+    read_frags(sW0, sX0, 0, 0);
+    if constexpr (TRI) {
+      int s = 0;
+      for (; s + 3 <= KS; s += 3) {
+        stage(sW0, sX0, sS0, sW1, sX1, s);
+        stage(sW1, sX1, sS1, sW2, sX2, s + 1);
+        stage(sW2, sX2, sS2, sW0, sX0, s + 2);
+      }
+      if (s < KS) stage(sW0, sX0, sS0, sW1, sX1, s);
+      if (s + 1 < KS) stage(sW1, sX1, sS1, sW2, sX2, s + 1);
+    } else {
+      for (int s = 0; s < KS; s += 2) {
+        stage(sW0, sX0, sS0, sW1, sX1, s);
+        stage(sW1, sX1, sS1, sW0, sX0, s + 1);
+      }
     }
   }
 
@@ -583,7 +661,7 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
 // then scales, bias, activation and routing weight are applied as in the
 // single-pass epilogue. A grouped problem finds the row's group by binary
 // search over group_offs.
-template <bool INT, bool ACT>
+template <bool INT, bool ACT, bool BLK>
 __global__ __launch_bounds__(kThreads) void f8_splitk_finish_kernel(const GemmParams p) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int R = blockIdx.y * 4 + wave;
@@ -602,7 +680,8 @@ __global__ __launch_bounds__(kThreads) void f8_splitk_finish_kernel(const GemmPa
     g = lo;
   }
   const int ar = p.a_rows ? p.a_rows[R] : R;
-  const float sxa = p.a_scale[(int64_t)ar * p.lds_a];
+  // block-scaled partials already carry their scales
+  const float sxa = BLK ? 1.0f : p.a_scale[(int64_t)ar * p.lds_a];
   const float rwt = p.row_weight ? bf16_to_f32(p.row_weight[R]) : 1.0f;
   const float* wsc = static_cast<const float*>(p.w_scale) + (int64_t)g * p.ws_gstride;
   const float* bias = p.bias ? p.bias + (int64_t)g * p.bias_gstride : nullptr;
@@ -655,12 +734,12 @@ __global__ __launch_bounds__(kThreads) void f8_splitk_finish_kernel(const GemmPa
       const int n = min(c0 + k + h, nlim - 1);
       float v = INT ? (float)ig[k + h] : vg[k + h];
       v = v * sxa;
-      v = v * wsc[n];
+      if (!BLK) v = v * wsc[n];
       if (bias) v += bias[n];
       if (ACT) {
         float u = INT ? (float)iu[k + h] : vu[k + h];
         u = u * sxa;
-        u = u * wsc[p.N / 2 + n];
+        if (!BLK) u = u * wsc[p.N / 2 + n];
         if (bias) u += bias[p.N / 2 + n];
         v = qmoe_act(p.act, v, u, p.act_p0, p.act_p1);
       }
@@ -677,11 +756,12 @@ __global__ __launch_bounds__(kThreads) void f8_splitk_finish_kernel(const GemmPa
   }
 }
 
-template <bool INT, int BM, int BN, bool ACT>
+template <bool INT, int BM, int BN, bool ACT, bool BLK>
 void f8_launch_shape(const GemmParams& p, hipStream_t st) {
   const char* env = getenv("QMOE_F8_KB");  // tuning knob: K bytes per LDS stage
-  const int kb = env ? atoi(env) : 128;
-  auto kern = kb == 64 ? f8_gemm_kernel<INT, BM, BN, ACT, 64> : f8_gemm_kernel<INT, BM, BN, ACT, 128>;
+  const int kb = BLK ? 128 : (env ? atoi(env) : 128);
+  auto kern = kb == 64 ? f8_gemm_kernel<INT, BM, BN, ACT, BLK ? 128 : 64, BLK>
+                       : f8_gemm_kernel<INT, BM, BN, ACT, 128, BLK>;
   const int nout = ACT ? p.N / 2 : p.N;
   const int n_tiles = cdiv(nout, ACT ? BN / 2 : BN);
   const unsigned ks = (unsigned)std::max(1, p.ksplit);
@@ -695,19 +775,29 @@ void f8_launch_shape(const GemmParams& p, hipStream_t st) {
   }
 }
 
-template <bool INT, int BM, int BN>
+template <bool INT, int BM, int BN, bool BLK>
 void f8_launch_act(const GemmParams& p, hipStream_t st) {
-  if (p.act != QA_NONE) f8_launch_shape<INT, BM, BN, true>(p, st);
-  else f8_launch_shape<INT, BM, BN, false>(p, st);
+  if (p.act != QA_NONE) f8_launch_shape<INT, BM, BN, true, BLK>(p, st);
+  else f8_launch_shape<INT, BM, BN, false, BLK>(p, st);
 }
 
 template <bool INT>
 void f8_launch_bm(const GemmParams& p, int bm, hipStream_t st) {
   switch (bm) {
-    case 256: f8_launch_act<INT, 256, 256>(p, st); break;
-    case 128: f8_launch_act<INT, 128, 256>(p, st); break;
-    case 64: f8_launch_act<INT, 64, 256>(p, st); break;
-    default: f8_launch_act<INT, 32, 256>(p, st); break;
+    case 256: f8_launch_act<INT, 256, 256, false>(p, st); break;
+    case 128: f8_launch_act<INT, 128, 256, false>(p, st); break;
+    case 64: f8_launch_act<INT, 64, 256, false>(p, st); break;
+    default: f8_launch_act<INT, 32, 256, false>(p, st); break;
+  }
+}
+
+// block-scaled FP8: tiles of at most 128 tokens (the per-block sums need a
+// second accumulator set)
+void f8_launch_bm_blk(const GemmParams& p, int bm, hipStream_t st) {
+  switch (bm) {
+    case 128: f8_launch_act<false, 128, 256, true>(p, st); break;
+    case 64: f8_launch_act<false, 64, 256, true>(p, st); break;
+    default: f8_launch_act<false, 32, 256, true>(p, st); break;
   }
 }
 
@@ -715,7 +805,7 @@ void f8_launch_bm(const GemmParams& p, int bm, hipStream_t st) {
 
 // Token-tile height: the largest of 256 / 128 / 64 / 32 whose tile count
 // still fills the CUs (dense), or that fits the average group (grouped).
-static int f8_pick_bm(const GemmParams& p) {
+static int f8_pick_bm_any(const GemmParams& p) {
   const char* env = getenv("QMOE_F8_BM");  // tuning knob
   if (env) {
     const int v = atoi(env);
@@ -739,15 +829,22 @@ static int f8_pick_bm(const GemmParams& p) {
 // Whether this kernel takes the problem (K % 256, 16-byte alignment,
 // weights < 4 GiB per group), and its plan: token-tile height, K split and
 // the f32 workspace the split needs ([ksplit][M][N]).
-bool qmoe_f8_plan(const GemmParams& p, int* bm_out, int* ksplit_out, int64_t* ws_bytes) {
+bool qmoe_f8_plan(const GemmParams& p, bool blk, int* bm_out, int* ksplit_out, int64_t* ws_bytes) {
   if (p.M <= 0 || p.K <= 0 || (p.K % 256) != 0 || p.N <= 0) return false;
   if (p.act != QA_NONE && (p.N % 2) != 0) return false;
+  // block scales: 128-row weight blocks aligned with the tile's halves
+  if (blk && (p.ws_bn != 128 || (p.act != QA_NONE && ((p.N / 2) % 128) != 0))) return false;
   if ((p.lda % 16) != 0 || (p.ldw % 16) != 0) return false;
   if ((reinterpret_cast<uintptr_t>(p.a) & 15) || (reinterpret_cast<uintptr_t>(p.w) & 15) ||
       (p.w_gstride % 16) != 0)
     return false;
   if ((int64_t)p.ldw * p.N >= ((int64_t)1 << 32)) return false;
-  int bm = f8_pick_bm(p);
+  int bm = f8_pick_bm_any(p);
+  if (blk && !getenv("QMOE_F8_BM")) {
+    // block-scaled tiles hold at most 128 tokens; measured on MI355X (K 7168,
+    // N 18432): 128-token tiles up to 256 and from 2048 tokens, 64 between
+    bm = p.group_offs ? std::min(bm, 128) : (p.M > 256 && p.M < 2048 ? 64 : 128);
+  }
   const int m_tiles = p.group_offs ? cdiv(p.M, bm) + std::min(p.slots, p.M) : cdiv(p.M, bm);
   if (p.group_offs && m_tiles > 65535) return false;
   // Dense problems whose largest CU-filling tile is small (tall-K, few
@@ -771,27 +868,31 @@ bool qmoe_f8_plan(const GemmParams& p, int* bm_out, int* ksplit_out, int64_t* ws
 
 // Launch per the plan (the caller checked qmoe_f8_plan and sized the
 // workspace); with a K split the reduce kernel finishes the epilogue.
-int qmoe_f8_launch(GemmParams p, void* workspace, int64_t ws_bytes, hipStream_t st) {
+int qmoe_f8_launch(GemmParams p, bool blk, void* workspace, int64_t ws_bytes, hipStream_t st) {
   int bm = 0, ksplit = 1;
   int64_t need = 0;
-  if (!qmoe_f8_plan(p, &bm, &ksplit, &need)) return QMOE_ERR_ARG;
+  if (!qmoe_f8_plan(p, blk, &bm, &ksplit, &need)) return QMOE_ERR_ARG;
   p.ksplit = ksplit;
   if (ksplit > 1) {
     if (!workspace || ws_bytes < need) return QMOE_ERR_WORKSPACE;
     p.partial = static_cast<float*>(workspace);
   }
-  if (p.wfmt == 1) f8_launch_bm<true>(p, bm, st);
+  if (blk) f8_launch_bm_blk(p, bm, st);
+  else if (p.wfmt == 1) f8_launch_bm<true>(p, bm, st);
   else f8_launch_bm<false>(p, bm, st);
   if (ksplit > 1) {
     const int nout = p.act != QA_NONE ? p.N / 2 : p.N;
     const dim3 rg((unsigned)cdiv(nout, 512), (unsigned)cdiv(p.M, 4), 1);
     const bool act = p.act != QA_NONE;
-    if (p.wfmt == 1) {
-      if (act) hipLaunchKernelGGL((f8_splitk_finish_kernel<true, true>), rg, dim3(kThreads), 0, st, p);
-      else hipLaunchKernelGGL((f8_splitk_finish_kernel<true, false>), rg, dim3(kThreads), 0, st, p);
+    if (blk) {
+      if (act) hipLaunchKernelGGL((f8_splitk_finish_kernel<false, true, true>), rg, dim3(kThreads), 0, st, p);
+      else hipLaunchKernelGGL((f8_splitk_finish_kernel<false, false, true>), rg, dim3(kThreads), 0, st, p);
+    } else if (p.wfmt == 1) {
+      if (act) hipLaunchKernelGGL((f8_splitk_finish_kernel<true, true, false>), rg, dim3(kThreads), 0, st, p);
+      else hipLaunchKernelGGL((f8_splitk_finish_kernel<true, false, false>), rg, dim3(kThreads), 0, st, p);
     } else {
-      if (act) hipLaunchKernelGGL((f8_splitk_finish_kernel<false, true>), rg, dim3(kThreads), 0, st, p);
-      else hipLaunchKernelGGL((f8_splitk_finish_kernel<false, false>), rg, dim3(kThreads), 0, st, p);
+      if (act) hipLaunchKernelGGL((f8_splitk_finish_kernel<false, true, false>), rg, dim3(kThreads), 0, st, p);
+      else hipLaunchKernelGGL((f8_splitk_finish_kernel<false, false, false>), rg, dim3(kThreads), 0, st, p);
     }
   }
   return hipGetLastError() == hipSuccess ? QMOE_OK : QMOE_ERR_LAUNCH;
