@@ -149,7 +149,11 @@ def test_w8a8_fp8_block(dev, M, K, N, tile_scales):
 @pytest.mark.parametrize("M,K,N", [(1, 2880, 5760), (16, 2880, 5760), (128, 2880, 1440),
                                    (5, 512, 200), (90, 1024, 96),
                                    # K % 256 = 32, 160 and K < 256: every partial last step pair
-                                   (3, 2848, 200), (1, 416, 70), (7, 96, 130), (2, 160, 64)])
+                                   (3, 2848, 200), (1, 416, 70), (7, 96, 130), (2, 160, 64),
+                                   # tiled kernel: 32/64/128-token tiles, K splits, ragged tiles;
+                                   # K % 64 != 0 takes the generic tiled kernel
+                                   (300, 2880, 768), (520, 1024, 512), (600, 512, 9216), (1200, 512, 9216),
+                                   (70, 2848, 300)])
 def test_w4a16_mxfp4(dev, M, K, N):
     from qmoe import _capi, ops
 

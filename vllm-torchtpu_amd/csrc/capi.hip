@@ -15,6 +15,8 @@ int qmoe_skinny_launch(int kind, GemmParams p, int max_rows, int slots, void* wo
 int qmoe_tiled_launch(int kind, GemmParams p, hipStream_t st);
 bool qmoe_f8_plan(const GemmParams& p, bool blk, int* bm_out, int* ksplit_out, int64_t* ws_bytes);
 int qmoe_f8_launch(GemmParams p, bool blk, void* workspace, int64_t ws_bytes, hipStream_t st);
+bool qmoe_w4_plan(const GemmParams& p, int* bm_out, int* ksplit_out, int64_t* ws_bytes);
+int qmoe_w4_launch(GemmParams p, void* workspace, int64_t ws_bytes, hipStream_t st);
 
 namespace {
 
@@ -104,6 +106,10 @@ bool use_skinny(const qmoe_gemm_desc* d) {
   return skinny_rows(d) <= lim;
 }
 
+bool use_w4(const qmoe_gemm_desc* d) {
+  return d->kind == QMOE_W4A16_MX && !getenv("QMOE_W4_OFF");  // tuning knob: generic kernel only
+}
+
 bool use_f8(const qmoe_gemm_desc* d) {
   if (getenv("QMOE_F8_OFF")) return false;  // tuning knob: generic kernel only
   return d->kind == QMOE_W8A8_PC || (d->kind == QMOE_W8A8_BLK && !getenv("QMOE_F8_BLK_OFF"));
@@ -121,11 +127,13 @@ extern "C" int qmoe_gemm_workspace_size(const qmoe_gemm_desc* d, int64_t* bytes)
   if (use_skinny(d)) {
     int ks = 1;
     qmoe_skinny_plan(d->kind, d->M, d->N, d->K, d->act, skinny_slots(d), skinny_rows(d), 0, &ks, bytes);
-  } else if (use_f8(d)) {
+  } else if (use_f8(d) || use_w4(d)) {
     p.active = nullptr;
     p.num_active = nullptr;
     int bm = 0, ks = 1;
-    if (!qmoe_f8_plan(p, d->kind == QMOE_W8A8_BLK, &bm, &ks, bytes)) *bytes = 0;
+    const bool ok = use_w4(d) ? qmoe_w4_plan(p, &bm, &ks, bytes)
+                              : qmoe_f8_plan(p, d->kind == QMOE_W8A8_BLK, &bm, &ks, bytes);
+    if (!ok) *bytes = 0;
   }
   return QMOE_OK;
 }
@@ -149,11 +157,21 @@ extern "C" int qmoe_gemm(const qmoe_gemm_desc* d, void* workspace, int64_t ws_by
   // a skinny-path device (it bounds the grid by the number of routed experts)
   p.active = nullptr;
   p.num_active = nullptr;
+  // the 1-byte x 1-byte and the bf16 x e2m1 kernels decline (QMOE_ERR_ARG)
+  // problems outside their envelopes (K granule, alignment), which the
+  // generic kernel takes
   if (use_f8(d)) {
-    // 1-byte x 1-byte kernel; it declines (QMOE_ERR_ARG) problems outside its
-    // envelope (K % 256, 16-byte alignment), which the generic kernel takes
     const int rc = qmoe_f8_launch(p, d->kind == QMOE_W8A8_BLK, workspace, ws_bytes, stream);
     if (rc != QMOE_ERR_ARG) return rc;
+  } else if (use_w4(d)) {
+    const int rc = qmoe_w4_launch(p, workspace, ws_bytes, stream);
+    if (rc != QMOE_ERR_ARG) return rc;
   }
-  return qmoe_tiled_launch(d->kind, p, stream);
+  const int rc = qmoe_tiled_launch(d->kind, p, stream);
+  if (rc != QMOE_ERR_ARG) return rc;
+  // K outside the tiled kernels' granule (bf16 activations: K % 64 == 32):
+  // the streaming kernel takes any K % 32 == 0, in passes of 64 rows per group
+  GemmParams q;
+  to_params(d, &q);
+  return qmoe_skinny_launch(d->kind, q, kSkinnyMaxRows, skinny_slots(d), workspace, ws_bytes, 1, stream);
 }

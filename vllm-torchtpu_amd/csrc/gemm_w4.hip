@@ -1,0 +1,399 @@
+// Tiled (prefill) GEMM for bf16 activations x MXFP4 weights (W4A16: e2m1
+// codes, two per byte with the even k in the low nibble, one e8m0 scale per
+// 32 k), dense or grouped.
+//
+// Restates the reference's W4A16 path (`layers/adapter/linear_common.py:
+// 188-209` -> `kernels/megablox/gmm_v2.py:452-462`: the block-32 weights are
+// dequantized to the activation dtype and multiplied in bf16 with f32
+// accumulation). The dequantization is exact in bf16, so expanding the codes
+// on the fly gives the same products as dequantizing the whole matrix first.
+//
+// Design for gfx950 (one workgroup of 4 wavefronts per CU), on the machinery
+// of the 1-byte tiled kernel (gemm_tile.h):
+//  * output tile BM tokens x 256 weight rows of 32 x 32 MFMA blocks (weight
+//    block first, activation block second: v_mfma_f32_32x32x16_bf16);
+//  * a stage is 64 k: 128 bytes of each activation row and 32 bytes of each
+//    weight row, copied straight into a ring of four LDS stages (distinct
+//    arrays) four stages ahead; each lane loads the scale bytes it needs
+//    with the copies (bounded buffer loads into a 4-deep register ring);
+//  * in a stage, lane l (row l % 32, half h = l / 32) feeds k in
+//    [32h, 32h + 32): that is one e8m0 block, 16 contiguous code bytes (one
+//    LDS read for all four 16-k MFMA steps) and one scale byte. Each 16-k
+//    step expands 8 codes to bf16 with the block scale applied
+//    (v_cvt_scalef32_pk_bf16_fp4); activation and weight use the same lane
+//    -> k assignment, so the products pair up whatever order the MFMA sums;
+//  * every operand of stage s+1 is read into the second register set during
+//    the MFMAs of stage s; the activation rows are stored with the 16-byte
+//    chunk c of row r at slot c ^ ((r & 7) ^ ((r >> 3) & 1)) so that the
+//    MFMA operand reads are conflict-free;
+//  * the shared epilogue applies bias, fused activation and routing weight
+//    (the weights carry no other scale).
+
+#include <algorithm>
+#include <cstdlib>
+
+#include "gemm_tile.h"
+
+namespace {
+
+using rsrc_t = __amdgpu_buffer_rsrc_t;
+constexpr int kW4BN = 256;  // weight rows per tile
+
+// The wavefronts split the 256 weight rows (each expands its own 64 rows
+// once per stage and reuses them for all BM tokens); WN = 4 always.
+template <int BM>
+struct W4Shape {
+  static constexpr int WN = 4;                  // wavefronts along weight rows
+  static constexpr int WM = 1;                  // along tokens
+  static constexpr int TN = kW4BN / WN;         // weight rows per wavefront
+  static constexpr int TM = BM / WM;            // tokens per wavefront
+  static constexpr int NI = TN / 32;
+  static constexpr int MJ = TM / 32;
+  static_assert(NI >= 1 && MJ >= 1, "tile too small");
+};
+
+__device__ __forceinline__ int w4_swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
+// 8 e2m1 codes (one dword, low nibble first) -> 8 bf16 times `scale`
+__device__ __forceinline__ bf16x8 w4_expand(uint32_t d, float scale) {
+  union {
+    bf16x2 h[4];
+    bf16x8 v;
+  } u;
+  u.h[0] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, scale, 0);
+  u.h[1] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, scale, 1);
+  u.h[2] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, scale, 2);
+  u.h[3] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, scale, 3);
+  return u.v;
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8_u4(const uint4& x) {
+  union {
+    uint4 u;
+    bf16x8 v;
+  } c;
+  c.u = x;
+  return c.v;
+}
+
+template <int BM, bool ACT>
+__global__ __launch_bounds__(kThreads) void w4_gemm_kernel(const GemmParams p, int m_tiles, int n_tiles) {
+  using S = W4Shape<BM>;
+  constexpr int BN = kW4BN;
+  constexpr int NI = S::NI, MJ = S::MJ, TN = S::TN, TM = S::TM;
+  constexpr int BNO = ACT ? BN / 2 : BN;  // output channels per tile
+  static_assert(!ACT || NI % 2 == 0, "fused activation pairs gate and up blocks");
+
+  // four LDS stages of 64 k: activations [BM][128 B], codes [BN][32 B]
+  __shared__ __align__(1024) uint8_t sA0[BM * 128], sA1[BM * 128], sA2[BM * 128], sA3[BM * 128];
+  __shared__ __align__(1024) uint8_t sW0[BN * 32], sW1[BN * 32], sW2[BN * 32], sW3[BN * 32];
+  __shared__ int s_info[4];
+  __shared__ float s_sx[BM], s_rw[BM], s_ws[BN], s_bs[BN];
+  __shared__ int s_yr[BM];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wn = wave % S::WN, wm = wave / S::WN;
+
+  int g, row0, rows, ntile;
+  if (p.group_offs) {
+    if (!tile_group<BM>(p, blockIdx.y, g, row0, rows, s_info)) return;
+    ntile = blockIdx.x;
+  } else {
+    int mt;
+    if (!tile_dense(blockIdx.x, m_tiles, n_tiles, mt, ntile)) return;
+    g = 0;
+    row0 = mt * BM;
+    rows = min(BM, p.M - row0);
+  }
+  const int n0 = ntile * BNO;
+  const int nlim = ACT ? p.N / 2 : p.N;
+  // global weight row of tile LDS row r (gate rows, then up rows with ACT);
+  // rows past the end are clamped (their outputs are never stored)
+  auto wrow_global = [&](int r) {
+    if (ACT) return (r < BN / 2 ? 0 : p.N / 2) + min(n0 + (r % (BN / 2)), nlim - 1);
+    return min(n0 + r, nlim - 1);
+  };
+
+  // epilogue inputs (loaded now, staged in LDS at the end): token routing
+  // weight and output row; weight-row bias. No activation / channel scales.
+  float e_rw = 1.0f, e_bs = 0.0f;
+  int e_yr = 0;
+  if (tid < BM) {
+    const int R = row0 + min(tid, rows - 1);
+    if (p.row_weight) e_rw = bf16_to_f32(p.row_weight[R]);
+    e_yr = p.y_rows ? p.y_rows[R] : R;
+  }
+  if (tid < BN && p.bias) e_bs = p.bias[(int64_t)g * p.bias_gstride + wrow_global(tid)];
+
+  // ---- LDS copies (16 bytes per lane) ----
+  // activations: one instruction = 8 rows x 128 bytes (lane -> row l >> 3,
+  // slot l & 7, fetching the chunk that the row's swizzle stores there);
+  // codes: 32 rows x 32 bytes (lane -> row l >> 1, half l & 1). Scale bytes:
+  // lane (row l % 32, half h) of weight block i needs byte 2*stage + h of
+  // its row.
+  constexpr int XI = BM / 32;  // activation copies per wavefront
+  constexpr int WI = 2;        // code copies per wavefront
+  const uint8_t* xbase = static_cast<const uint8_t*>(p.a);
+  const uint8_t* wbase = p.w + (int64_t)g * p.w_gstride;
+  const rsrc_t eres = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<void*>(static_cast<const void*>(static_cast<const uint8_t*>(p.w_scale) + (int64_t)g * p.ws_gstride)),
+      (short)0, (int)std::min<int64_t>((int64_t)p.N * p.ldws, 0x7fffffff), 0x00020000);
+  const uint64_t lda_b = (uint64_t)p.lda * 2;
+  uint32_t xrow[XI], woff[WI];
+  int xcx[XI];
+#pragma unroll
+  for (int j = 0; j < XI; ++j) {
+    const int r = (wave + 4 * j) * 8 + (lane >> 3);
+    const int R = row0 + min(r, rows - 1);
+    xrow[j] = (uint32_t)(p.a_rows ? p.a_rows[R] : R);
+    xcx[j] = ((lane & 7) ^ w4_swz(r)) * 16;
+  }
+#pragma unroll
+  for (int j = 0; j < WI; ++j) {
+    const int r = (wave + 4 * j) * 32 + (lane >> 1);
+    woff[j] = (uint32_t)wrow_global(r) * (uint32_t)p.ldw + (lane & 1) * 16;
+  }
+
+  // split-K: this workgroup's K range in 64-k stages
+  const int NU = p.K / 64;
+  const int u0 = (int)((int64_t)NU * blockIdx.z / p.ksplit);
+  const int u1 = (int)((int64_t)NU * (blockIdx.z + 1) / p.ksplit);
+  const int KS = u1 - u0;
+  const int rl = lane & 31, kh = lane >> 5;
+  auto wrow = [&](int i) { return tile_wrow<BN, TN, NI, ACT>(wn, i); };
+  uint32_t eoff[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) eoff[i] = (uint32_t)wrow_global(wrow(i) + rl) * (uint32_t)p.ldws + kh;
+  uint32_t we[4][NI];  // e8m0 bytes of the stages in flight (stage s in set s % 4)
+  auto copy_stage = [&](uint8_t* dA, uint8_t* dW, int e, int ks) {
+    const uint32_t st = (uint32_t)(u0 + ks);
+#pragma unroll
+    for (int j = 0; j < WI; ++j) {
+      uint32_t o = woff[j];
+      asm volatile("" : "+v"(o));
+      __builtin_amdgcn_global_load_lds(wbase + (o + st * 32u), QMOE_LDS(dW + (wave + 4 * j) * 1024), 16, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < XI; ++j) {
+      uint32_t r = xrow[j];
+      asm volatile("" : "+v"(r));
+      const uint8_t* src = xbase + (uint64_t)r * lda_b + (st * 128u + xcx[j]);
+      __builtin_amdgcn_global_load_lds(src, QMOE_LDS(dA + (wave + 4 * j) * 1024), 16, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < NI; ++i) we[e][i] = __builtin_amdgcn_raw_buffer_load_b8(eres, eoff[i], st * 2u, 0);
+  };
+
+  // ---- operands of one stage into register set t ----
+  uint4 wc[2][NI];  // codes: dword q feeds 16-k step q
+  uint4 xa[2][MJ][4];  // activations: [block][16-k step]
+  auto read_stage = [&](const uint8_t* sA, const uint8_t* sW, int t) {
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int r = wrow(i) + rl;
+      wc[t][i] = *reinterpret_cast<const uint4*>(sW + r * 32 + kh * 16);
+    }
+#pragma unroll
+    for (int j = 0; j < MJ; ++j) {
+      const int r = wm * TM + j * 32 + rl;
+      const uint8_t* row = sA + r * 128;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        xa[t][j][q] = *reinterpret_cast<const uint4*>(row + (((kh * 4 + q) ^ w4_swz(r)) * 16));
+    }
+  };
+
+  f32x16 acc[NI][MJ];
+#pragma unroll
+  for (int i = 0; i < NI; ++i)
+#pragma unroll
+    for (int j = 0; j < MJ; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  // k-step outer, blocks inner: consecutive MFMAs go to different
+  // accumulators, and a step's expansions overlap the previous step's MFMAs
+  auto mma_stage = [&](int t, const uint32_t (&eb)[NI]) {
+    float scale[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) scale[i] = e8m0_to_f32(eb[i]);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      bf16x8 wv[NI];
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const uint32_t d = q == 0 ? wc[t][i].x : (q == 1 ? wc[t][i].y : (q == 2 ? wc[t][i].z : wc[t][i].w));
+        wv[i] = w4_expand(d, scale[i]);
+      }
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+#pragma unroll
+        for (int j = 0; j < MJ; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wv[i], as_bf16x8_u4(xa[t][j][q]), acc[i][j], 0, 0, 0);
+    }
+  };
+
+  constexpr int CPS = WI + XI + NI;        // vector-memory loads per wavefront per stage
+  constexpr int NM = NI * MJ * 4;          // MFMAs per stage
+  constexpr int NR = NI + MJ * 4;          // LDS operand reads per stage
+  // Stage s lives in buffer s % 4 and is copied four stages ahead. Stage s:
+  // wait for the own copy of stage s+1 -> barrier (stage s+1 has landed
+  // everywhere, and every wavefront holds stage s in registers, so buffer
+  // s % 4 is free) -> copy stage s+4 into it -> MFMAs of stage s with the
+  // operand reads of stage s+1 among the first half and the copies among
+  // the second. Copies past the end refetch the last stage into a consumed
+  // buffer (never read again).
+  // (stage s's scale bytes are register set s % 4; they are taken before
+  // the set is reloaded with stage s+4)
+  auto stage = [&](uint8_t* fA, uint8_t* fW, const uint8_t* nA, const uint8_t* nW, int e, int s, int t) {
+    wait_copies_upto<2 * CPS>();
+    stage_barrier();
+    uint32_t eb[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) eb[i] = we[e][i];
+    copy_stage(fA, fW, e, min(s + 4, KS - 1));
+    mma_stage(t, eb);
+    read_stage(nA, nW, t ^ 1);
+    interleave<0, NM, NR, CPS>();
+  };
+  if (KS > 0) {
+    copy_stage(sA0, sW0, 0, 0);
+    copy_stage(sA1, sW1, 1, min(1, KS - 1));
+    copy_stage(sA2, sW2, 2, min(2, KS - 1));
+    copy_stage(sA3, sW3, 3, min(3, KS - 1));
+    wait_copies_upto<3 * CPS>();
+    __syncthreads();
+    read_stage(sA0, sW0, 0);
+    int s = 0;
+    for (; s + 4 <= KS; s += 4) {
+      stage(sA0, sW0, sA1, sW1, 0, s, 0);
+      stage(sA1, sW1, sA2, sW2, 1, s + 1, 1);
+      stage(sA2, sW2, sA3, sW3, 2, s + 2, 0);
+      stage(sA3, sW3, sA0, sW0, 3, s + 3, 1);
+    }
+    if (s < KS) stage(sA0, sW0, sA1, sW1, 0, s, 0);
+    if (s + 1 < KS) stage(sA1, sW1, sA2, sW2, 1, s + 1, 1);
+    if (s + 2 < KS) stage(sA2, sW2, sA3, sW3, 2, s + 2, 0);
+  }
+
+  if (p.ksplit > 1) {
+    tile_store_partials<BN, TN, TM, NI, MJ, ACT, false>(p, acc, row0, rows, n0, nlim, wn, wm, lane);
+    return;
+  }
+  wait_copies_upto<0>();
+  __syncthreads();  // every wavefront is done with the stage buffers
+  if (tid < BM) {
+    s_sx[tid] = 1.0f;
+    s_rw[tid] = e_rw;
+    s_yr[tid] = e_yr;
+  }
+  if (tid < BN) {
+    s_ws[tid] = 1.0f;
+    s_bs[tid] = e_bs;
+  }
+  __syncthreads();
+  // a wavefront's f32 region [32 tokens][TN rows]: an activation stage for
+  // 64- and 128-token tiles, a code stage for 32-token tiles
+  static_assert(32 * TN * 4 <= (BM >= 64 ? BM * 128 : BN * 32), "epilogue region");
+  uint8_t* regb;
+  if constexpr (BM >= 64) regb = wave == 0 ? sA0 : wave == 1 ? sA1 : wave == 2 ? sA2 : sA3;
+  else regb = wave == 0 ? sW0 : wave == 1 ? sW1 : wave == 2 ? sW2 : sW3;
+  tile_epilogue<BN, TN, TM, NI, MJ, ACT>(p, acc, reinterpret_cast<float*>(regb), s_sx, s_rw, s_yr, s_ws, s_bs,
+                                        n0, nlim, rows, wn, wm, lane);
+}
+
+template <int BM, bool ACT>
+void w4_launch_shape(const GemmParams& p, hipStream_t st) {
+  const int nout = ACT ? p.N / 2 : p.N;
+  const int n_tiles = cdiv(nout, ACT ? kW4BN / 2 : kW4BN);
+  const unsigned ks = (unsigned)std::max(1, p.ksplit);
+  if (p.group_offs) {
+    const int m_tiles = cdiv(p.M, BM) + std::min(p.slots, p.M);
+    hipLaunchKernelGGL((w4_gemm_kernel<BM, ACT>), dim3(n_tiles, m_tiles, ks), dim3(kThreads), 0, st, p, m_tiles,
+                       n_tiles);
+  } else {
+    const int m_tiles = cdiv(p.M, BM);
+    const int grid = cdiv(m_tiles * n_tiles, kXcds) * kXcds;
+    hipLaunchKernelGGL((w4_gemm_kernel<BM, ACT>), dim3(grid, 1, ks), dim3(kThreads), 0, st, p, m_tiles, n_tiles);
+  }
+}
+
+template <int BM>
+void w4_launch_act(const GemmParams& p, hipStream_t st) {
+  if (p.act != QA_NONE) w4_launch_shape<BM, true>(p, st);
+  else w4_launch_shape<BM, false>(p, st);
+}
+
+}  // namespace
+
+// Whether the W4A16 tiled kernel takes the problem (K % 64, 16-byte aligned
+// rows, even scale rows, codes < 4 GiB per group), and its plan: token-tile
+// height (the largest of 128 / 64 / 32 that still fills the CUs, or that fits
+// the average group), K split (dense problems with few tiles) and the f32
+// workspace the split needs ([ksplit][M][N]).
+bool qmoe_w4_plan(const GemmParams& p, int* bm_out, int* ksplit_out, int64_t* ws_bytes) {
+  if (p.M <= 0 || p.K <= 0 || (p.K % 64) != 0 || p.N <= 0) return false;
+  if (p.act != QA_NONE && (p.N % 2) != 0) return false;
+  if ((p.lda % 8) != 0 || (p.ldw % 16) != 0 || (p.ldws % 2) != 0) return false;
+  if ((reinterpret_cast<uintptr_t>(p.a) & 15) || (reinterpret_cast<uintptr_t>(p.w) & 15) ||
+      (p.w_gstride % 16) != 0 || (reinterpret_cast<uintptr_t>(p.w_scale) & 1) || (p.ws_gstride % 2) != 0)
+    return false;
+  if ((int64_t)p.ldw * p.N >= ((int64_t)1 << 32) || (int64_t)p.ldws * p.N >= ((int64_t)1 << 32)) return false;
+  const int nout = p.act != QA_NONE ? p.N / 2 : p.N;
+  const int n_tiles = cdiv(nout, p.act != QA_NONE ? kW4BN / 2 : kW4BN);
+  int bm = 32;
+  const char* env = getenv("QMOE_W4_BM");  // tuning knob
+  if (env && (atoi(env) == 128 || atoi(env) == 64 || atoi(env) == 32)) {
+    bm = atoi(env);
+  } else if (p.group_offs) {
+    const int avg = std::max(1, p.M / std::max(1, std::min(p.slots, p.M)));
+    bm = avg > 96 ? 128 : (avg > 48 ? 64 : 32);
+  } else {
+    // measured on MI355X (K 2880, N 5760): 128-token tiles once they fill the
+    // CUs, else 64 with a K split (32-token tiles are slower at every M)
+    bm = (int64_t)cdiv(p.M, 128) * n_tiles >= 200 ? 128 : 64;
+  }
+  const int m_tiles = p.group_offs ? cdiv(p.M, bm) + std::min(p.slots, p.M) : cdiv(p.M, bm);
+  if (p.group_offs && m_tiles > 65535) return false;
+  // dense problems with fewer than ~200 tiles split K (every slice keeps at
+  // least 8 stages)
+  int ksplit = 1;
+  if (!p.group_offs) {
+    const int tiles = m_tiles * n_tiles;
+    if (tiles < 200) ksplit = std::min(cdiv(256, tiles), std::max(1, (p.K / 64) / 8));
+  }
+  const char* ks_env = getenv("QMOE_W4_KSPLIT");  // tuning knob
+  if (ks_env && atoi(ks_env) > 0) ksplit = std::max(1, std::min(atoi(ks_env), p.K / 64));
+  *bm_out = bm;
+  *ksplit_out = ksplit;
+  *ws_bytes = ksplit > 1 ? (int64_t)ksplit * p.M * p.N * 4 : 0;
+  return true;
+}
+
+// Launch per the plan (the caller sized the workspace); with a K split the
+// finishing kernel runs the epilogue.
+int qmoe_w4_launch(GemmParams p, void* workspace, int64_t ws_bytes, hipStream_t st) {
+  int bm = 0, ksplit = 1;
+  int64_t need = 0;
+  if (!qmoe_w4_plan(p, &bm, &ksplit, &need)) return QMOE_ERR_ARG;
+  p.ksplit = ksplit;
+  if (ksplit > 1) {
+    if (!workspace || ws_bytes < need) return QMOE_ERR_WORKSPACE;
+    p.partial = static_cast<float*>(workspace);
+  }
+  switch (bm) {
+    case 128: w4_launch_act<128>(p, st); break;
+    case 64: w4_launch_act<64>(p, st); break;
+    default: w4_launch_act<32>(p, st); break;
+  }
+  if (ksplit > 1) {
+    const int nout = p.act != QA_NONE ? p.N / 2 : p.N;
+    const dim3 rg((unsigned)cdiv(nout, 512), (unsigned)cdiv(p.M, 4), 1);
+    if (p.act != QA_NONE)
+      hipLaunchKernelGGL((tile_splitk_finish_kernel<false, true, true>), rg, dim3(kThreads), 0, st, p);
+    else
+      hipLaunchKernelGGL((tile_splitk_finish_kernel<false, false, true>), rg, dim3(kThreads), 0, st, p);
+  }
+  return hipGetLastError() == hipSuccess ? QMOE_OK : QMOE_ERR_LAUNCH;
+}
