@@ -23,7 +23,9 @@ def _bf16(rng, shape, scale=1.0):
 
 @pytest.mark.parametrize("qdtype", ["fp8", "int8"])
 @pytest.mark.parametrize("block", [None, 128])
-@pytest.mark.parametrize("M,K", [(1, 4096), (7, 2048), (64, 7168), (300, 1024)])
+@pytest.mark.parametrize("M,K", [(1, 4096), (7, 2048), (64, 7168), (300, 1024),
+                                 # decode rows on 1024 threads: held in registers, and streamed
+                                 (3, 14336), (2, 40960)])
 def test_row_quant_runtime_bit_exact(dev, qdtype, block, M, K):
     if qdtype == "int8" and block is not None:
         pytest.skip("int8 activations are quantized per token only")

@@ -14,9 +14,12 @@
 //    even. A zero scale stays 0.
 // Granularity: one scale per row, or per (row, 128-column block).
 //
-// Launch: one 256-thread workgroup per row; thread t owns 8 consecutive
-// columns per 2048-column stride, so a 128-column block is exactly 16
-// adjacent lanes of one wavefront (reduced with shuffles, no LDS).
+// Launch: one 256-thread workgroup per row (per-row scale); thread t owns 8
+// consecutive columns per 2048-column stride, so a 128-column block is
+// exactly 16 adjacent lanes of one wavefront (reduced with shuffles, no LDS).
+// Per-block scales need no row-wide reduction, so a row's 2048-column spans
+// go to separate workgroups (grid.y): a decode row is quantized in one
+// memory round trip instead of one per span.
 
 #include "qmoe_common.h"
 
@@ -111,8 +114,8 @@ __device__ __forceinline__ float amax8(const Row8& r) {
   return m;
 }
 
-template <int kQdt, int kMode, bool kInF32, bool kBlock>
-__global__ __launch_bounds__(kThreads) void row_quant_kernel(
+template <int kQdt, int kMode, bool kInF32, bool kBlock, int kNT>
+__global__ __launch_bounds__(kNT) void row_quant_kernel(
     const void* __restrict__ x, int64_t ldx, int64_t K, uint8_t* __restrict__ q,
     int64_t ldq, float* __restrict__ scales, int64_t lds) {
   const int64_t row = blockIdx.x;
@@ -120,8 +123,9 @@ __global__ __launch_bounds__(kThreads) void row_quant_kernel(
   const int64_t xbase = row * ldx;
   uint8_t* qrow = q + row * ldq;
   if (kBlock) {
-    // 16 lanes per 128-column block
-    for (int64_t c = (int64_t)tid * 8; c < K; c += kThreads * 8) {
+    // 16 lanes per 128-column block; this workgroup's 2048-column span
+    const int64_t c = (int64_t)blockIdx.y * (kNT * 8) + (int64_t)tid * 8;
+    if (c < K) {
       Row8 r = load8<kInF32>(x, xbase + c);
       float m = amax8(r);
 #pragma unroll
@@ -132,26 +136,59 @@ __global__ __launch_bounds__(kThreads) void row_quant_kernel(
     }
     return;
   }
-  __shared__ float red[kThreads / 64];
+  __shared__ float red[kNT / 64];
   float m = 0.0f;
-  for (int64_t c = (int64_t)tid * 8; c < K; c += kThreads * 8)
-    m = nanmax(m, amax8(load8<kInF32>(x, xbase + c)));
+  // rows of up to kHeld spans stay in registers: all their loads are in
+  // flight at once and the codes are written from the registers
+  constexpr int kHeld = kNT >= 1024 ? 4 : 8;
+  const bool held = K <= (int64_t)kHeld * kNT * 8;
+  Row8 r[kHeld];
+  if (held) {
+#pragma unroll
+    for (int i = 0; i < kHeld; ++i) {
+      const int64_t c = (int64_t)(i * kNT + tid) * 8;
+      if (c < K) {
+        r[i] = load8<kInF32>(x, xbase + c);
+        m = nanmax(m, amax8(r[i]));
+      }
+    }
+  } else {
+    for (int64_t c = (int64_t)tid * 8; c < K; c += kNT * 8)
+      m = nanmax(m, amax8(load8<kInF32>(x, xbase + c)));
+  }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) m = nanmax(m, __shfl_xor(m, o, 64));
   if ((tid & 63) == 0) red[tid >> 6] = m;
   __syncthreads();
-  m = nanmax(nanmax(red[0], red[1]), nanmax(red[2], red[3]));
+  m = red[0];
+#pragma unroll
+  for (int w = 1; w < kNT / 64; ++w) m = nanmax(m, red[w]);
   float s = make_scale<kQdt, kMode>(m);
-  for (int64_t c = (int64_t)tid * 8; c < K; c += kThreads * 8)
-    store8<kQdt, kMode>(qrow + c, load8<kInF32>(x, xbase + c), s);
+  if (held) {
+#pragma unroll
+    for (int i = 0; i < kHeld; ++i) {
+      const int64_t c = (int64_t)(i * kNT + tid) * 8;
+      if (c < K) store8<kQdt, kMode>(qrow + c, r[i], s);
+    }
+  } else {
+    for (int64_t c = (int64_t)tid * 8; c < K; c += kNT * 8)
+      store8<kQdt, kMode>(qrow + c, load8<kInF32>(x, xbase + c), s);
+  }
   if (tid == 0) scales[row * lds] = s;
 }
 
 template <int kQdt, int kMode, bool kInF32, bool kBlock>
 void launch_rq(const void* x, int64_t ldx, int64_t M, int64_t K, uint8_t* q, int64_t ldq,
                float* s, int64_t lds, hipStream_t st) {
-  hipLaunchKernelGGL((row_quant_kernel<kQdt, kMode, kInF32, kBlock>), dim3((unsigned)M),
-                     dim3(kThreads), 0, st, x, ldx, K, q, ldq, s, lds);
+  const unsigned spans = kBlock ? (unsigned)cdiv<int64_t>(K, kThreads * 8) : 1u;
+  // a few long rows (decode) get 1024 threads per row: 4x the lanes for the
+  // division and encode of each element
+  if (!kBlock && M <= 64 && K > kThreads * 8)
+    hipLaunchKernelGGL((row_quant_kernel<kQdt, kMode, kInF32, kBlock, 1024>), dim3((unsigned)M), dim3(1024), 0,
+                       st, x, ldx, K, q, ldq, s, lds);
+  else
+    hipLaunchKernelGGL((row_quant_kernel<kQdt, kMode, kInF32, kBlock, kThreads>), dim3((unsigned)M, spans),
+                       dim3(kThreads), 0, st, x, ldx, K, q, ldq, s, lds);
 }
 
 }  // namespace
