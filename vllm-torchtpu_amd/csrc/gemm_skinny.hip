@@ -301,14 +301,12 @@ __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(const GemmParams 
     nclamp[s] = nok[s] ? nw[s] : (ACT ? (s < NH ? nlim - 1 : p.N - 1) : p.N - 1);
     woff[s] = (uint32_t)(nclamp[s] * p.ldw + kg * Tr::kWBytes);
   }
-  // per-step scale streams: e8m0 bytes [N][K/32] (W4A16), f32 [N/bn][K/128]
-  // weight blocks and [rows][K/128] activation blocks (W8A8_BLK)
+  // scale streams: e8m0 bytes [N][K/32] (W4A16, staged below), per-step f32
+  // [N/bn][K/128] weight blocks and [rows][K/128] activation blocks (W8A8_BLK)
   rsrc_t sres = wres, ares = wres;  // placeholders for kinds without scale streams
   uint32_t soffw[NS];
   if constexpr (KIND == QK_W4A16_MX) {
     sres = make_rsrc(static_cast<const uint8_t*>(p.w_scale) + (int64_t)g * p.ws_gstride, (int64_t)p.N * p.ldws);
-#pragma unroll
-    for (int s = 0; s < NS; ++s) soffw[s] = (uint32_t)(nclamp[s] * p.ldws + kg);
   } else if constexpr (KIND == QK_W8A8_BLK) {
     sres = make_rsrc(static_cast<const float*>(p.w_scale) + (int64_t)g * p.ws_gstride,
                      (int64_t)cdiv(p.N, p.ws_bn) * p.ldws * 4);
@@ -316,6 +314,34 @@ __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(const GemmParams 
 #pragma unroll
     for (int s = 0; s < NS; ++s) soffw[s] = (uint32_t)((nclamp[s] / p.ws_bn) * p.ldws * 4);
   }
+  // e2m1: the workgroup's NS*16 scale rows (K/32 bytes each; the host keeps
+  // K <= 16384) are staged in LDS once, so the K loop reads a step's byte
+  // from LDS instead of issuing a scattered byte load per tile per step
+  constexpr int kMaxEB = 512;
+  __shared__ uint8_t s_eb[KIND == QK_W4A16_MX ? NS * 16 * kMaxEB : 1];
+  const int KB32 = p.K >> 5;
+  auto row_of = [&](int s, int c) {  // clamped global row of tile s, column c
+    if (ACT) {
+      const int r = min(tile * (16 * NH) + (s % NH) * 16 + c, nlim - 1);
+      return s < NH ? r : (p.N >> 1) + r;
+    }
+    return min(tile * (16 * NS) + s * 16 + c, p.N - 1);
+  };
+  auto stage_scales = [&]() {  // issue: loads of this thread's bytes
+    uint32_t v[16];
+    const int total = NS * 16 * KB32;
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int idx = min(u * kThreads + (int)threadIdx.x, total - 1);
+      const int rr = idx / KB32, b = idx - rr * KB32;
+      v[u] = __builtin_amdgcn_raw_buffer_load_b8(sres, (uint32_t)(row_of(rr >> 4, rr & 15) * p.ldws + b), 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int idx = u * kThreads + (int)threadIdx.x;
+      if (idx < total) s_eb[idx] = (uint8_t)v[u];
+    }
+  };
 
   // K steps: KSF full 128-wide steps, plus a tail step when K % 128 != 0
   const int KSF = p.K >> 7;
@@ -370,7 +396,7 @@ __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(const GemmParams 
           for (int r4 = 0; r4 < 4; ++r4) sc.sa[ms][r4] = ldb_f32(ares, soffa[ms][r4], (uint32_t)ks * 4);
       } else if constexpr (KIND == QK_W4A16_MX) {
 #pragma unroll
-        for (int s = 0; s < NS; ++s) sc.eb[s] = __builtin_amdgcn_raw_buffer_load_b8(sres, soffw[s], (uint32_t)ks * 4, 0);
+        for (int s = 0; s < NS; ++s) sc.eb[s] = s_eb[(s * 16 + col) * KB32 + ks * 4 + kg];
       }
     };
 
@@ -383,7 +409,7 @@ __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(const GemmParams 
       Frag fa[U][MS];
       StepScales<MS, NS> sc[U];
     };
-    auto issue = [&](int ks, Chunk& c) {
+    auto issue_mem = [&](int ks, Chunk& c) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int kk = min(ks + u, kf1 - 1);
@@ -392,8 +418,15 @@ __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(const GemmParams 
           ldb<Tr::kWBytes, kWeightAux>(c.bw[u][s], wres, woff[s], (uint32_t)kk * (4 * Tr::kWBytes));
 #pragma unroll
         for (int ms = 0; ms < MS; ++ms) ldb<Tr::kABytes>(c.fa[u][ms], xres, aoff[ms], (uint32_t)kk * (4 * Tr::kABytes));
-        load_scales(kk, c.sc[u]);
       }
+    };
+    auto issue_sc = [&](int ks, Chunk& c) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) load_scales(min(ks + u, kf1 - 1), c.sc[u]);
+    };
+    auto issue = [&](int ks, Chunk& c) {
+      issue_mem(ks, c);
+      issue_sc(ks, c);
     };
     auto consume = [&](int ks, const Chunk& c) {
 #pragma unroll
@@ -405,9 +438,16 @@ __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(const GemmParams 
     // shorter path and drain the chunk just issued as well. The scheduling
     // barriers keep the compiler from sinking a chunk's loads below the
     // MFMAs of the previous one.
-    if (ks0 < kf1) {
-      Chunk ca, cb;
-      issue(ks0, ca);
+    Chunk ca, cb;
+    const bool run = ks0 < kf1;
+    if (run) issue_mem(ks0, ca);
+    if (KIND == QK_W4A16_MX && mp == 0) {
+      // the scale rows are staged while the first chunk is in flight
+      stage_scales();
+      __syncthreads();
+    }
+    if (run) {
+      issue_sc(ks0, ca);
       for (int ks = ks0; ks < kf1; ks += 2 * U) {
         issue(ks + U, cb);
         __builtin_amdgcn_sched_barrier(0);
@@ -442,7 +482,7 @@ __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(const GemmParams 
       if constexpr (KIND == QK_W4A16_MX) {
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
-          const uint32_t b = __builtin_amdgcn_raw_buffer_load_b8(sres, soffw[s] - kshift, (uint32_t)kk * 4, 0);
+          const uint32_t b = s_eb[(s * 16 + col) * KB32 + kk * 4 + kg - kshift];
           sc.eb[s] = kok ? b : 127u;
         }
       }
@@ -658,7 +698,7 @@ int qmoe_skinny_launch(int kind, GemmParams p, int max_rows, int slots, void* wo
   const bool abf16 = kind == QK_W8A16_PC || kind == QK_W4A16_MX || kind == QK_W16A16;
   constexpr int64_t kLim = 0x7fffffff;
   if ((int64_t)p.N * p.ldw > kLim || p.M * p.lda * (abf16 ? 2 : 1) > kLim) return QMOE_ERR_ARG;
-  if (kind == QK_W4A16_MX && (int64_t)p.N * p.ldws > kLim) return QMOE_ERR_ARG;
+  if (kind == QK_W4A16_MX && ((int64_t)p.N * p.ldws > kLim || p.K > 16384)) return QMOE_ERR_ARG;
   if (kind == QK_W8A8_BLK &&
       ((int64_t)cdiv(p.N, p.ws_bn) * p.ldws * 4 > kLim || p.M * p.lds_a * 4 > kLim))
     return QMOE_ERR_ARG;
