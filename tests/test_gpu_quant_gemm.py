@@ -152,6 +152,8 @@ def test_w8a8_fp8_block(dev, M, K, N, tile_scales):
                                    (5, 512, 200), (90, 1024, 96),
                                    # K % 256 = 32, 160 and K < 256: every partial last step pair
                                    (3, 2848, 200), (1, 416, 70), (7, 96, 130), (2, 160, 64),
+                                   # e8m0 rows longer than one staging batch of the streaming kernel
+                                   (1, 8192, 256), (2, 16384, 64),
                                    # tiled kernel: 32/64/128-token tiles, K splits, ragged tiles;
                                    # K % 64 != 0 takes the generic tiled kernel
                                    (300, 2880, 768), (520, 1024, 512), (600, 512, 9216), (1200, 512, 9216),

@@ -3,12 +3,14 @@
 //
 // Small-M linears and decode MoE are weight-bandwidth bound, so the design
 // goal is to keep enough 16-byte weight loads in flight to saturate HBM3E:
-//  * workgroup = 4 wavefronts; it owns NS 16-row MFMA B tiles of weight
-//    rows (NS/2 gate tiles + the matching up tiles when an activation is
-//    fused) and a slice of K. NS = 2 (4 is kept for e2m1 weights as a tuning
-//    option);
+//  * workgroup = W wavefronts (4, 8 or 16); it owns NS 16-row MFMA B tiles
+//    of weight rows (NS/2 gate tiles + the matching up tiles when an
+//    activation is fused) and a slice of K. NS = 2 (4 is kept for e2m1
+//    weights as a tuning option);
 //  * K is cut into 128-wide steps; the workgroup's steps are dealt out to its
-//    4 wavefronts, and further across `ksplit` workgroups (grid.y);
+//    W wavefronts, and further across `ksplit` workgroups (grid.y). Small
+//    problems get more wavefronts per workgroup rather than a K split, so
+//    they fill the chip without the split's second kernel;
 //  * a wavefront issues the loads of U steps back to back, unconditionally
 //    (weight rows past N and activation rows past the group are clamped to
 //    valid rows -- they only feed outputs that are never stored), and only
@@ -22,7 +24,7 @@
 //    are expanded with v_cvt_scalef32_pk_bf16_fp4, which also applies the e8m0
 //    block scale; e4m3 with v_cvt_pk_f32_fp8). A and W use the same
 //    lane -> k assignment, so products pair up whatever order the MFMA walks k;
-//  * the 4 wavefronts' sums are added in LDS in a fixed order; with
+//  * the W wavefronts' sums are added in LDS in a fixed order; with
 //    ksplit > 1 each workgroup stores its raw sums to a float32 workspace and
 //    a second kernel adds the slices in order and runs the epilogue (kernel
 //    boundaries order the memory traffic, so no cache-flushing fence runs).
@@ -35,7 +37,7 @@
 
 namespace {
 
-constexpr int kWaves = 4;
+constexpr int kWaves = 4;  // wavefronts of the split-K finishing kernel
 constexpr int kThreads = kWaves * 64;
 
 struct Frag {
@@ -52,12 +54,9 @@ struct Traits {
 };
 
 // 128-k steps per pipeline chunk (two chunks are in flight per wavefront);
-// measured on MI355X: two for dense decode, one for grouped (MoE) problems,
-// whose per-wavefront K slices are short
-int default_unroll(int kind, int ms, bool grouped) {
-  if (grouped || ms > 1) return 1;
-  return kind == QK_W16A16 ? 1 : 2;
-}
+// measured on MI355X: one step (deeper chunks add clamped duplicate loads
+// at the end of the short per-wavefront K slices and lose 5-30%)
+int default_unroll() { return 1; }
 
 // Operands are read with buffer loads: a wave-uniform resource (base and
 // extent in SGPRs), a 32-bit per-lane offset fixed for the whole K loop, and
@@ -257,9 +256,10 @@ __device__ __forceinline__ bool slot_group(const GemmParams& p, int slot, int& g
   return rows > 0;
 }
 
-template <int KIND, int WF, int MS, bool ACT, int U, int NS>
-__global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(const GemmParams p) {
+template <int KIND, int WF, int MS, bool ACT, int U, int NS, int W>
+__global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p) {
   using Tr = Traits<KIND, WF>;
+  constexpr int NT = W * 64;
   const int lane = threadIdx.x & 63;
   // wave-uniform in an SGPR, so K-slice bounds and loop tests are scalar
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -327,19 +327,21 @@ __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(const GemmParams 
     }
     return min(tile * (16 * NS) + s * 16 + c, p.N - 1);
   };
-  auto stage_scales = [&]() {  // issue: loads of this thread's bytes
-    uint32_t v[16];
+  auto stage_scales = [&]() {  // 16 byte loads in flight per thread per batch
     const int total = NS * 16 * KB32;
+    for (int b0 = 0; b0 < total; b0 += 16 * NT) {
+      uint32_t v[16];
 #pragma unroll
-    for (int u = 0; u < 16; ++u) {
-      const int idx = min(u * kThreads + (int)threadIdx.x, total - 1);
-      const int rr = idx / KB32, b = idx - rr * KB32;
-      v[u] = __builtin_amdgcn_raw_buffer_load_b8(sres, (uint32_t)(row_of(rr >> 4, rr & 15) * p.ldws + b), 0, 0);
-    }
+      for (int u = 0; u < 16; ++u) {
+        const int idx = min(b0 + u * NT + (int)threadIdx.x, total - 1);
+        const int rr = idx / KB32, b = idx - rr * KB32;
+        v[u] = __builtin_amdgcn_raw_buffer_load_b8(sres, (uint32_t)(row_of(rr >> 4, rr & 15) * p.ldws + b), 0, 0);
+      }
 #pragma unroll
-    for (int u = 0; u < 16; ++u) {
-      const int idx = u * kThreads + (int)threadIdx.x;
-      if (idx < total) s_eb[idx] = (uint8_t)v[u];
+      for (int u = 0; u < 16; ++u) {
+        const int idx = b0 + u * NT + (int)threadIdx.x;
+        if (idx < total) s_eb[idx] = (uint8_t)v[u];
+      }
     }
   };
 
@@ -347,16 +349,19 @@ __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(const GemmParams 
   const int KSF = p.K >> 7;
   const bool tail = (p.K & 127) != 0;
   const int KS = KSF + (tail ? 1 : 0);
-  const int nsl = p.ksplit * kWaves;
-  const int sl = blockIdx.y * kWaves + wave;
-  const int ks0 = (int)((int64_t)KS * sl / nsl);
-  const int ks1 = (int)((int64_t)KS * (sl + 1) / nsl);
-  const int kf1 = min(ks1, KSF);
+  // this wavefront's full steps are sbase + j, j < nj (a contiguous run of
+  // the workgroup's K slice); the wavefront whose run ends at K takes the tail
+  const int nsl = p.ksplit * W;
+  const int sl = blockIdx.y * W + wave;
+  const int sbase = (int)((int64_t)KS * sl / nsl);
+  const int send = (int)((int64_t)KS * (sl + 1) / nsl);
+  const int nj = max(0, min(send, KSF) - sbase);
+  const bool tail_mine = tail && send == KS && sbase < send;
 
   const int64_t lda_b = p.lda * (Tr::kAbf16 ? 2 : 1);
   const rsrc_t xres = make_rsrc(p.a, (int64_t)p.M * lda_b);
   constexpr int NV = MS * NS * 4;
-  __shared__ float red[kWaves - 1][NV][64];
+  __shared__ float red[W - 1][NV][64];
   const int64_t plane = (int64_t)p.M * p.N;
 
   // Rows are taken 16*MS at a time (one pass when the host's row bound
@@ -409,10 +414,10 @@ __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(const GemmParams 
       Frag fa[U][MS];
       StepScales<MS, NS> sc[U];
     };
-    auto issue_mem = [&](int ks, Chunk& c) {
+    auto issue_mem = [&](int j, Chunk& c) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const int kk = min(ks + u, kf1 - 1);
+        const int kk = sbase + min(j + u, nj - 1);
 #pragma unroll
         for (int s = 0; s < NS; ++s)
           ldb<Tr::kWBytes, kWeightAux>(c.bw[u][s], wres, woff[s], (uint32_t)kk * (4 * Tr::kWBytes));
@@ -420,18 +425,18 @@ __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(const GemmParams 
         for (int ms = 0; ms < MS; ++ms) ldb<Tr::kABytes>(c.fa[u][ms], xres, aoff[ms], (uint32_t)kk * (4 * Tr::kABytes));
       }
     };
-    auto issue_sc = [&](int ks, Chunk& c) {
+    auto issue_sc = [&](int j, Chunk& c) {
 #pragma unroll
-      for (int u = 0; u < U; ++u) load_scales(min(ks + u, kf1 - 1), c.sc[u]);
+      for (int u = 0; u < U; ++u) load_scales(sbase + min(j + u, nj - 1), c.sc[u]);
     };
-    auto issue = [&](int ks, Chunk& c) {
-      issue_mem(ks, c);
-      issue_sc(ks, c);
+    auto issue = [&](int j, Chunk& c) {
+      issue_mem(j, c);
+      issue_sc(j, c);
     };
-    auto consume = [&](int ks, const Chunk& c) {
+    auto consume = [&](int j, const Chunk& c) {
 #pragma unroll
       for (int u = 0; u < U; ++u)
-        if (ks + u < kf1) mma_step<KIND, WF, MS, NS>(acc, c.fa[u], c.bw[u], c.sc[u]);
+        if (j + u < nj) mma_step<KIND, WF, MS, NS>(acc, c.fa[u], c.bw[u], c.sc[u]);
     };
     // Issues are unconditional (clamped step indices): a load issued only on
     // some paths would make the wait before the next MFMAs assume the
@@ -439,30 +444,30 @@ __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(const GemmParams 
     // barriers keep the compiler from sinking a chunk's loads below the
     // MFMAs of the previous one.
     Chunk ca, cb;
-    const bool run = ks0 < kf1;
-    if (run) issue_mem(ks0, ca);
+    const bool run = nj > 0;
+    if (run) issue_mem(0, ca);
     if (KIND == QK_W4A16_MX && mp == 0) {
       // the scale rows are staged while the first chunk is in flight
       stage_scales();
       __syncthreads();
     }
     if (run) {
-      issue_sc(ks0, ca);
-      for (int ks = ks0; ks < kf1; ks += 2 * U) {
-        issue(ks + U, cb);
+      issue_sc(0, ca);
+      for (int j = 0; j < nj; j += 2 * U) {
+        issue(j + U, cb);
         __builtin_amdgcn_sched_barrier(0);
-        consume(ks, ca);
+        consume(j, ca);
         __builtin_amdgcn_sched_barrier(0);
-        issue(ks + 2 * U, ca);
+        issue(j + 2 * U, ca);
         __builtin_amdgcn_sched_barrier(0);
-        consume(ks + U, cb);
+        consume(j + U, cb);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
     // K tail: lanes whose 32 k values start past K feed zeros; they load the
     // step's first 32 values instead (always in range), so no load leaves
     // the row
-    if (tail && ks1 == KS && ks0 < ks1) {
+    if (tail_mine) {
       const int kk = KSF;
       const bool kok = kk * 128 + kg * 32 < p.K;
       const uint32_t kshift = kok ? 0u : (uint32_t)kg;
@@ -507,7 +512,7 @@ __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(const GemmParams 
     __syncthreads();
     if (wave != 0) continue;
 #pragma unroll
-    for (int w = 0; w < kWaves - 1; ++w)
+    for (int w = 0; w < W - 1; ++w)
 #pragma unroll
       for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
@@ -595,17 +600,22 @@ __global__ __launch_bounds__(kThreads) void skinny_reduce_kernel(const GemmParam
   }
 }
 
-template <int KIND, int WF, int MS, bool ACT, int NS>
-void launch_skinny(const GemmParams& p, dim3 grid, hipStream_t st) {
-  const char* env_s = getenv("QMOE_SKINNY_U");  // tuning knob
+template <int KIND, int WF, int MS, bool ACT, int NS, int W>
+void launch_skinny_w(const GemmParams& p, dim3 grid, hipStream_t st) {
+  const char* env_s = getenv("QMOE_SKINNY_U");  // tuning knob: 1 or 2
   const int env_u = env_s ? atoi(env_s) : 0;
-  const int u = env_u > 0 ? env_u : default_unroll(KIND, MS, p.group_offs != nullptr);
-  if (u >= 4)
-    hipLaunchKernelGGL((skinny_gemm_kernel<KIND, WF, MS, ACT, 4, NS>), grid, dim3(kThreads), 0, st, p);
-  else if (u == 2)
-    hipLaunchKernelGGL((skinny_gemm_kernel<KIND, WF, MS, ACT, 2, NS>), grid, dim3(kThreads), 0, st, p);
+  const int u = env_u > 0 ? env_u : default_unroll();
+  if (u >= 2)
+    hipLaunchKernelGGL((skinny_gemm_kernel<KIND, WF, MS, ACT, 2, NS, W>), grid, dim3(W * 64), 0, st, p);
   else
-    hipLaunchKernelGGL((skinny_gemm_kernel<KIND, WF, MS, ACT, 1, NS>), grid, dim3(kThreads), 0, st, p);
+    hipLaunchKernelGGL((skinny_gemm_kernel<KIND, WF, MS, ACT, 1, NS, W>), grid, dim3(W * 64), 0, st, p);
+}
+
+template <int KIND, int WF, int MS, bool ACT, int NS>
+void launch_skinny(const GemmParams& p, int waves, dim3 grid, hipStream_t st) {
+  if (MS == 1 && waves >= 16) launch_skinny_w<KIND, WF, MS, ACT, NS, (MS == 1 ? 16 : 4)>(p, grid, st);
+  else if (MS <= 2 && waves >= 8) launch_skinny_w<KIND, WF, MS, ACT, NS, (MS <= 2 ? 8 : 4)>(p, grid, st);
+  else launch_skinny_w<KIND, WF, MS, ACT, NS, 4>(p, grid, st);
   if (p.ksplit > 1) {
     const int nout = ACT ? p.N / 2 : p.N;
     dim3 rg((unsigned)cdiv(nout, 64), 1, grid.z);
@@ -614,26 +624,26 @@ void launch_skinny(const GemmParams& p, dim3 grid, hipStream_t st) {
 }
 
 template <int KIND, int WF, bool ACT>
-void launch_ms(const GemmParams& p, int ms, int ns, dim3 grid, hipStream_t st) {
+void launch_ms(const GemmParams& p, int ms, int ns, int waves, dim3 grid, hipStream_t st) {
   if (ms == 1) {
     if constexpr (KIND == QK_W4A16_MX) {
       if (ns == 4) {
-        launch_skinny<KIND, WF, 1, ACT, 4>(p, grid, st);
+        launch_skinny<KIND, WF, 1, ACT, 4>(p, waves, grid, st);
         return;
       }
     }
-    launch_skinny<KIND, WF, 1, ACT, 2>(p, grid, st);
+    launch_skinny<KIND, WF, 1, ACT, 2>(p, waves, grid, st);
   } else if (ms == 2) {
-    launch_skinny<KIND, WF, 2, ACT, 2>(p, grid, st);
+    launch_skinny<KIND, WF, 2, ACT, 2>(p, waves, grid, st);
   } else {
-    launch_skinny<KIND, WF, 4, ACT, 2>(p, grid, st);
+    launch_skinny<KIND, WF, 4, ACT, 2>(p, waves, grid, st);
   }
 }
 
 template <int KIND, int WF>
-void launch_act(const GemmParams& p, int ms, int ns, dim3 grid, hipStream_t st) {
-  if (p.act != QA_NONE) launch_ms<KIND, WF, true>(p, ms, ns, grid, st);
-  else launch_ms<KIND, WF, false>(p, ms, ns, grid, st);
+void launch_act(const GemmParams& p, int ms, int ns, int waves, dim3 grid, hipStream_t st) {
+  if (p.act != QA_NONE) launch_ms<KIND, WF, true>(p, ms, ns, waves, grid, st);
+  else launch_ms<KIND, WF, false>(p, ms, ns, waves, grid, st);
 }
 
 // 16-row M tiles per pass for a problem whose groups hold `rows` rows
@@ -659,28 +669,49 @@ int skinny_tiles(int64_t N, int act, int ns) {
 
 }  // namespace
 
-// Split-K plan of the skinny kernel: the number of K slices and the float32
-// workspace ([ksplit][M][N] raw sums) they need. K is split only when there
-// are fewer than ~160 workgroups (a split costs a second launch and the
-// partial-sum traffic; measured on MI355X, one workgroup per 32 weight rows
-// streams best once there are >= 160 of them), and every wavefront keeps at
-// least two 128-k steps.
+namespace {
+
+struct SkinnyPlan {
+  int waves;   // wavefronts per workgroup (4, 8 or 16)
+  int ksplit;  // K slices over grid.y
+  int64_t ws_bytes;
+};
+
+int env_int(const char* name, int dflt) {
+  const char* v = getenv(name);
+  return v && atoi(v) > 0 ? atoi(v) : dflt;
+}
+
+// Launch shape of the skinny kernel. Measured on MI355X: 4 wavefronts per
+// workgroup stream best (8 or 16, i.e. shorter K runs per wavefront, lose
+// 10-60%); K is split across workgroups only when there are fewer than ~160
+// workgroups (one per 32 weight rows), which costs a second launch and the
+// [ksplit][M][N] float32 partial sums in the workspace; every wavefront keeps
+// at least two 128-k steps.
+SkinnyPlan skinny_plan(int kind, int64_t M, int64_t N, int64_t K, int act, int slots, int rows,
+                       int ksplit_hint) {
+  const int ms = skinny_ms(rows);
+  const int n_wg = skinny_tiles(N, act, skinny_ns(kind, ms)) * std::max(slots, 1);
+  const int KS = (int)cdiv<int64_t>(K, 128);
+  // tuning knobs (read per call): wavefronts per workgroup, forced K split,
+  // workgroup count the split planner aims for
+  const int wmax = ms == 1 ? 16 : (ms == 2 ? 8 : 4);
+  const int env_w = env_int("QMOE_SKINNY_WAVES", 4);
+  const int w = (env_w == 8 || env_w == 16) ? std::min(env_w, wmax) : 4;
+  int ksplit = ksplit_hint > 0 ? ksplit_hint : env_int("QMOE_SKINNY_KSPLIT", 0);
+  if (ksplit <= 0) ksplit = (int)cdiv<int64_t>(env_int("QMOE_SKINNY_TARGET_WG", 160), n_wg);
+  ksplit = std::max(1, std::min(ksplit, std::max(1, KS / (2 * w))));
+  return SkinnyPlan{w, ksplit, ksplit <= 1 ? 0 : (int64_t)ksplit * M * N * 4};
+}
+
+}  // namespace
+
+// Workspace of the skinny kernel for this problem (see skinny_plan).
 void qmoe_skinny_plan(int kind, int64_t M, int64_t N, int64_t K, int act, int slots, int rows,
                       int ksplit_hint, int* ksplit_out, int64_t* ws_bytes) {
-  const int n_tiles = skinny_tiles(N, act, skinny_ns(kind, skinny_ms(rows)));
-  const int KS = (int)cdiv<int64_t>(K, 128);
-  int ksplit = ksplit_hint;
-  // tuning knobs (read per call): QMOE_SKINNY_KSPLIT forces the split,
-  // QMOE_SKINNY_TARGET_WG sets the workgroup count the planner aims for
-  const char* ks_s = getenv("QMOE_SKINNY_KSPLIT");
-  const char* tg_s = getenv("QMOE_SKINNY_TARGET_WG");
-  const int env_ksplit = ks_s ? atoi(ks_s) : 0;
-  const int env_target = tg_s && atoi(tg_s) > 0 ? atoi(tg_s) : 160;
-  if (ksplit <= 0) ksplit = env_ksplit;
-  if (ksplit <= 0) ksplit = (int)cdiv<int64_t>(env_target, (int64_t)n_tiles * std::max(slots, 1));
-  ksplit = std::max(1, std::min(ksplit, std::max(1, KS / (2 * kWaves))));
-  *ksplit_out = ksplit;
-  *ws_bytes = ksplit <= 1 ? 0 : (int64_t)ksplit * M * N * 4;
+  const SkinnyPlan pl = skinny_plan(kind, M, N, K, act, slots, rows, ksplit_hint);
+  *ksplit_out = pl.ksplit;
+  *ws_bytes = pl.ws_bytes;
 }
 
 // Host-side launcher shared by the dense and MoE entry points.
@@ -705,24 +736,23 @@ int qmoe_skinny_launch(int kind, GemmParams p, int max_rows, int slots, void* wo
   const int ms = skinny_ms(max_rows);
   const int ns = skinny_ns(kind, ms);
   const int n_tiles = skinny_tiles(p.N, p.act, ns);
-  int ksplit = 1;
-  int64_t need = 0;
-  qmoe_skinny_plan(kind, p.M, p.N, p.K, p.act, slots, max_rows, ksplit_hint, &ksplit, &need);
-  p.ksplit = ksplit;
-  if (ksplit > 1) {
-    if (!workspace || ws_bytes < need) return QMOE_ERR_WORKSPACE;
+  const SkinnyPlan pl = skinny_plan(kind, p.M, p.N, p.K, p.act, slots, max_rows, ksplit_hint);
+  const int waves = pl.waves;
+  p.ksplit = pl.ksplit;
+  if (pl.ksplit > 1) {
+    if (!workspace || ws_bytes < pl.ws_bytes) return QMOE_ERR_WORKSPACE;
     p.partial = static_cast<float*>(workspace);
   }
-  dim3 grid(n_tiles, ksplit, slots);
+  dim3 grid(n_tiles, pl.ksplit, slots);
   switch (kind) {
     case QK_W8A8_PC:
-      if (p.wfmt == 0) launch_act<QK_W8A8_PC, 0>(p, ms, ns, grid, st);
-      else launch_act<QK_W8A8_PC, 1>(p, ms, ns, grid, st);
+      if (p.wfmt == 0) launch_act<QK_W8A8_PC, 0>(p, ms, ns, waves, grid, st);
+      else launch_act<QK_W8A8_PC, 1>(p, ms, ns, waves, grid, st);
       break;
-    case QK_W8A8_BLK: launch_act<QK_W8A8_BLK, 0>(p, ms, ns, grid, st); break;
-    case QK_W8A16_PC: launch_act<QK_W8A16_PC, 0>(p, ms, ns, grid, st); break;
-    case QK_W4A16_MX: launch_act<QK_W4A16_MX, 0>(p, ms, ns, grid, st); break;
-    case QK_W16A16: launch_act<QK_W16A16, 0>(p, ms, ns, grid, st); break;
+    case QK_W8A8_BLK: launch_act<QK_W8A8_BLK, 0>(p, ms, ns, waves, grid, st); break;
+    case QK_W8A16_PC: launch_act<QK_W8A16_PC, 0>(p, ms, ns, waves, grid, st); break;
+    case QK_W4A16_MX: launch_act<QK_W4A16_MX, 0>(p, ms, ns, waves, grid, st); break;
+    case QK_W16A16: launch_act<QK_W16A16, 0>(p, ms, ns, waves, grid, st); break;
     default: return QMOE_ERR_ARG;
   }
   return hipGetLastError() == hipSuccess ? QMOE_OK : QMOE_ERR_LAUNCH;
