@@ -51,6 +51,24 @@ struct Traits {
   // bytes per lane per 128-k step (32 k values)
   static constexpr int kWBytes = KIND == QK_W4A16_MX ? 16 : (KIND == QK_W16A16 ? 64 : 32);
   static constexpr int kABytes = kAbf16 ? 64 : 32;
+  // Weight chunk j (16 B) of lane (column c, k-group kg) sits at byte
+  // j*64 + kg*16 of the row's step (4 lanes x 16 B = one 64 B segment per
+  // load instruction and row); the k values of each 16 B activation chunk i
+  // match the weight data they meet in the MFMA:
+  //   1-byte A (e4m3/int8) and bf16 A with bf16 W: byte kg*16 + i*64
+  //   bf16 A with e4m3 W: byte kg*32 + (i/2)*128 + (i%2)*16
+  //   bf16 A with e2m1 W: byte kg*64 + i*16
+  static constexpr int kAOffBase = KIND == QK_W4A16_MX ? 64 : (KIND == QK_W8A16_PC ? 32 : 16);
+  static __device__ __forceinline__ constexpr int a_off(int i) {
+    return KIND == QK_W4A16_MX ? i * 16 : (KIND == QK_W8A16_PC ? (i >> 1) * 128 + (i & 1) * 16 : i * 64);
+  }
+  // first k (within the step) of weight chunk (j, kg) / activation chunk (i, kg)
+  static __device__ __forceinline__ constexpr int w_k0(int j, int kg) {
+    return KIND == QK_W4A16_MX ? kg * 32 : (KIND == QK_W16A16 ? j * 32 + kg * 8 : j * 64 + kg * 16);
+  }
+  static __device__ __forceinline__ constexpr int a_k0(int i, int kg) {
+    return (kg * kAOffBase + a_off(i)) / (kAbf16 ? 2 : 1);
+  }
 };
 
 // 128-k steps per pipeline chunk (two chunks are in flight per wavefront);
@@ -72,20 +90,40 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void* base, int64_t bytes) {
 // cache-policy bits of the weight stream's loads (read once per launch)
 constexpr int kWeightAux = 0;
 
+// NB/16 weight chunks of one step: 16 B at voff + j*64 (the lane's column of
+// 64 B segment j of its load row)
 template <int NB, int AUX = 0>
-__device__ __forceinline__ void ldb(Frag& f, rsrc_t r, uint32_t voff, uint32_t soff) {
+__device__ __forceinline__ void ldw_seg(Frag& f, rsrc_t r, uint32_t voff, uint32_t soff) {
 #pragma unroll
-  for (int i = 0; i < NB / 16; ++i) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff + i * 16, soff, AUX);
+  for (int j = 0; j < NB / 16; ++j) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff + j * 64, soff, AUX);
+    f.v[j] = make_uint4(v[0], v[1], v[2], v[3]);
+  }
+}
+
+// activation chunks of one step at the offsets of Traits::a_off
+template <typename Tr>
+__device__ __forceinline__ void lda_chunks(Frag& f, rsrc_t r, uint32_t voff, uint32_t soff) {
+#pragma unroll
+  for (int i = 0; i < Tr::kABytes / 16; ++i) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff + Tr::a_off(i), soff, 0);
     f.v[i] = make_uint4(v[0], v[1], v[2], v[3]);
   }
 }
 
+// Weight loads put row (l >> 2), column (l & 3) of a 64 B segment in lane l,
+// so the 4 lanes of each 64 B piece are adjacent (the load is coalesced);
+// the MFMA wants row (l & 15), k-group (l >> 4) in lane l. `src` is the
+// byte address of lane 4*(l & 15) + (l >> 4).
 template <int NB>
-__device__ __forceinline__ void zero_unless(Frag& f, bool ok) {
+__device__ __forceinline__ void permute_w(Frag& f, int src) {
 #pragma unroll
-  for (int i = 0; i < NB / 16; ++i)
-    if (!ok) f.v[i] = make_uint4(0, 0, 0, 0);
+  for (int j = 0; j < NB / 16; ++j) {
+    f.v[j].x = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)f.v[j].x);
+    f.v[j].y = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)f.v[j].y);
+    f.v[j].z = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)f.v[j].z);
+    f.v[j].w = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)f.v[j].w);
+  }
 }
 
 __device__ __forceinline__ float ldb_f32(rsrc_t r, uint32_t voff, uint32_t soff) {
@@ -294,13 +332,22 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p)
   }
   g = __builtin_amdgcn_readfirstlane(g);
   const rsrc_t wres = make_rsrc(p.w + (int64_t)g * p.w_gstride, (int64_t)p.N * p.ldw);
+  auto row_of = [&](int s, int c) {  // clamped global row of tile s, column c
+    if (ACT) {
+      const int r = min(tile * (16 * NH) + (s % NH) * 16 + c, nlim - 1);
+      return s < NH ? r : (p.N >> 1) + r;
+    }
+    return min(tile * (16 * NS) + s * 16 + c, p.N - 1);
+  };
+  // weight loads: lane l reads row (l >> 2) of each tile, 16 B column (l & 3)
   uint32_t woff[NS];
   int nclamp[NS];
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
     nclamp[s] = nok[s] ? nw[s] : (ACT ? (s < NH ? nlim - 1 : p.N - 1) : p.N - 1);
-    woff[s] = (uint32_t)(nclamp[s] * p.ldw + kg * Tr::kWBytes);
+    woff[s] = (uint32_t)(row_of(s, lane >> 2) * p.ldw + (lane & 3) * 16);
   }
+  const int perm_src = (4 * col + kg) * 4;
   // scale streams: e8m0 bytes [N][K/32] (W4A16, staged below), per-step f32
   // [N/bn][K/128] weight blocks and [rows][K/128] activation blocks (W8A8_BLK)
   rsrc_t sres = wres, ares = wres;  // placeholders for kinds without scale streams
@@ -320,13 +367,6 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p)
   constexpr int kMaxEB = 512;
   __shared__ uint8_t s_eb[KIND == QK_W4A16_MX ? NS * 16 * kMaxEB : 1];
   const int KB32 = p.K >> 5;
-  auto row_of = [&](int s, int c) {  // clamped global row of tile s, column c
-    if (ACT) {
-      const int r = min(tile * (16 * NH) + (s % NH) * 16 + c, nlim - 1);
-      return s < NH ? r : (p.N >> 1) + r;
-    }
-    return min(tile * (16 * NS) + s * 16 + c, p.N - 1);
-  };
   auto stage_scales = [&]() {  // 16 byte loads in flight per thread per batch
     const int total = NS * 16 * KB32;
     for (int b0 = 0; b0 < total; b0 += 16 * NT) {
@@ -374,7 +414,7 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p)
       const int r = mp + ms * 16 + col;
       const int R = row0 + (r < rows ? r : 0);
       const int ar = p.a_rows ? p.a_rows[R] : R;
-      aoff[ms] = (uint32_t)(ar * lda_b + kg * Tr::kABytes);
+      aoff[ms] = (uint32_t)(ar * lda_b + kg * Tr::kAOffBase);
       if constexpr (KIND == QK_W8A8_BLK) {
 #pragma unroll
         for (int r4 = 0; r4 < 4; ++r4) {
@@ -420,9 +460,9 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p)
         const int kk = sbase + min(j + u, nj - 1);
 #pragma unroll
         for (int s = 0; s < NS; ++s)
-          ldb<Tr::kWBytes, kWeightAux>(c.bw[u][s], wres, woff[s], (uint32_t)kk * (4 * Tr::kWBytes));
+          ldw_seg<Tr::kWBytes, kWeightAux>(c.bw[u][s], wres, woff[s], (uint32_t)kk * (4 * Tr::kWBytes));
 #pragma unroll
-        for (int ms = 0; ms < MS; ++ms) ldb<Tr::kABytes>(c.fa[u][ms], xres, aoff[ms], (uint32_t)kk * (4 * Tr::kABytes));
+        for (int ms = 0; ms < MS; ++ms) lda_chunks<Tr>(c.fa[u][ms], xres, aoff[ms], (uint32_t)kk * (4 * Tr::kABytes));
       }
     };
     auto issue_sc = [&](int j, Chunk& c) {
@@ -433,10 +473,13 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p)
       issue_mem(j, c);
       issue_sc(j, c);
     };
-    auto consume = [&](int j, const Chunk& c) {
+    auto consume = [&](int j, Chunk& c) {
 #pragma unroll
-      for (int u = 0; u < U; ++u)
+      for (int u = 0; u < U; ++u) {
+#pragma unroll
+        for (int s = 0; s < NS; ++s) permute_w<Tr::kWBytes>(c.bw[u][s], perm_src);
         if (j + u < nj) mma_step<KIND, WF, MS, NS>(acc, c.fa[u], c.bw[u], c.sc[u]);
+      }
     };
     // Issues are unconditional (clamped step indices): a load issued only on
     // some paths would make the wait before the next MFMAs assume the
@@ -464,31 +507,45 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p)
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    // K tail: lanes whose 32 k values start past K feed zeros; they load the
-    // step's first 32 values instead (always in range), so no load leaves
-    // the row
+    // K tail (t = K % 128 valid k, a multiple of 32): a chunk whose k values
+    // start past K is loaded from the step's first chunk instead (always in
+    // range, so no load leaves the row) and fed as zeros
     if (tail_mine) {
       const int kk = KSF;
-      const bool kok = kk * 128 + kg * 32 < p.K;
-      const uint32_t kshift = kok ? 0u : (uint32_t)kg;
+      const int t = p.K - KSF * 128;
       Frag bw[NS];
       Frag fa[MS];
       StepScales<MS, NS> sc;
+      const int lc = lane & 3;  // 16 B column of this lane's weight loads
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
-        ldb<Tr::kWBytes>(bw[s], wres, woff[s] - kshift * Tr::kWBytes, (uint32_t)kk * (4 * Tr::kWBytes));
-        zero_unless<Tr::kWBytes>(bw[s], kok);
+#pragma unroll
+        for (int j = 0; j < Tr::kWBytes / 16; ++j) {
+          const uint32_t o = Tr::w_k0(j, lc) < t ? woff[s] + j * 64 : woff[s] - lc * 16;
+          const auto v = __builtin_amdgcn_raw_buffer_load_b128(wres, o, (uint32_t)kk * (4 * Tr::kWBytes), 0);
+          bw[s].v[j] = make_uint4(v[0], v[1], v[2], v[3]);
+        }
+        permute_w<Tr::kWBytes>(bw[s], perm_src);
+#pragma unroll
+        for (int j = 0; j < Tr::kWBytes / 16; ++j)
+          if (Tr::w_k0(j, kg) >= t) bw[s].v[j] = make_uint4(0, 0, 0, 0);
       }
 #pragma unroll
       for (int ms = 0; ms < MS; ++ms) {
-        ldb<Tr::kABytes>(fa[ms], xres, aoff[ms] - kshift * Tr::kABytes, (uint32_t)kk * (4 * Tr::kABytes));
-        zero_unless<Tr::kABytes>(fa[ms], kok);
+#pragma unroll
+        for (int i = 0; i < Tr::kABytes / 16; ++i) {
+          const bool ok = Tr::a_k0(i, kg) < t;
+          const uint32_t o = ok ? aoff[ms] + Tr::a_off(i) : aoff[ms] - kg * Tr::kAOffBase;
+          const auto v = __builtin_amdgcn_raw_buffer_load_b128(xres, o, (uint32_t)kk * (4 * Tr::kABytes), 0);
+          fa[ms].v[i] = ok ? make_uint4(v[0], v[1], v[2], v[3]) : make_uint4(0, 0, 0, 0);
+        }
       }
       if constexpr (KIND == QK_W4A16_MX) {
+        const bool ok = kg * 32 < t;
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
-          const uint32_t b = s_eb[(s * 16 + col) * KB32 + kk * 4 + kg - kshift];
-          sc.eb[s] = kok ? b : 127u;
+          const uint32_t b = s_eb[(s * 16 + col) * KB32 + kk * 4 + (ok ? kg : 0)];
+          sc.eb[s] = ok ? b : 127u;
         }
       }
       mma_step<KIND, WF, MS, NS>(acc, fa, bw, sc);
