@@ -19,7 +19,11 @@
 // exactly 16 adjacent lanes of one wavefront (reduced with shuffles, no LDS).
 // Per-block scales need no row-wide reduction, so a row's 2048-column spans
 // go to separate workgroups (grid.y): a decode row is quantized in one
-// memory round trip instead of one per span.
+// memory round trip instead of one per span. Per-row scales of a few rows
+// (decode) also spread a row's spans over grid.y: every workgroup reads the
+// whole row for the absmax (from L2 after the first) and encodes only its
+// own span, so the per-element division and encode run on S CUs instead of
+// one.
 
 #include "qmoe_common.h"
 
@@ -114,7 +118,7 @@ __device__ __forceinline__ float amax8(const Row8& r) {
   return m;
 }
 
-template <int kQdt, int kMode, bool kInF32, bool kBlock, int kNT>
+template <int kQdt, int kMode, bool kInF32, bool kBlock, int kNT, bool kSpan = false>
 __global__ __launch_bounds__(kNT) void row_quant_kernel(
     const void* __restrict__ x, int64_t ldx, int64_t K, uint8_t* __restrict__ q,
     int64_t ldq, float* __restrict__ scales, int64_t lds) {
@@ -164,6 +168,17 @@ __global__ __launch_bounds__(kNT) void row_quant_kernel(
 #pragma unroll
   for (int w = 1; w < kNT / 64; ++w) m = nanmax(m, red[w]);
   float s = make_scale<kQdt, kMode>(m);
+  if (kSpan) {
+    // held rows only (the host checks); span i of the row is this
+    // workgroup's when i == blockIdx.y
+#pragma unroll
+    for (int i = 0; i < kHeld; ++i) {
+      const int64_t c = (int64_t)(i * kNT + tid) * 8;
+      if (i == (int)blockIdx.y && c < K) store8<kQdt, kMode>(qrow + c, r[i], s);
+    }
+    if (tid == 0 && blockIdx.y == 0) scales[row * lds] = s;
+    return;
+  }
   if (held) {
 #pragma unroll
     for (int i = 0; i < kHeld; ++i) {
@@ -181,9 +196,14 @@ template <int kQdt, int kMode, bool kInF32, bool kBlock>
 void launch_rq(const void* x, int64_t ldx, int64_t M, int64_t K, uint8_t* q, int64_t ldq,
                float* s, int64_t lds, hipStream_t st) {
   const unsigned spans = kBlock ? (unsigned)cdiv<int64_t>(K, kThreads * 8) : 1u;
-  // a few long rows (decode) get 1024 threads per row: 4x the lanes for the
-  // division and encode of each element
-  if (!kBlock && M <= 64 && K > kThreads * 8)
+  // a few long rows (decode): each row's 2048-column spans are encoded by
+  // separate workgroups (rows of up to 8 spans, held in registers), or, for
+  // longer rows, 1024 threads per row
+  if (!kBlock && M <= 256 && K > kThreads * 8 && K <= 8 * kThreads * 8)
+    hipLaunchKernelGGL((row_quant_kernel<kQdt, kMode, kInF32, kBlock, kThreads, true>),
+                       dim3((unsigned)M, (unsigned)cdiv<int64_t>(K, kThreads * 8)), dim3(kThreads), 0, st, x, ldx,
+                       K, q, ldq, s, lds);
+  else if (!kBlock && M <= 64 && K > kThreads * 8)
     hipLaunchKernelGGL((row_quant_kernel<kQdt, kMode, kInF32, kBlock, 1024>), dim3((unsigned)M), dim3(1024), 0,
                        st, x, ldx, K, q, ldq, s, lds);
   else

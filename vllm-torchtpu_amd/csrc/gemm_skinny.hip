@@ -3,22 +3,26 @@
 //
 // Small-M linears and decode MoE are weight-bandwidth bound, so the design
 // goal is to keep enough 16-byte weight loads in flight to saturate HBM3E:
-//  * workgroup = W wavefronts (4, 8 or 16); it owns NS 16-row MFMA B tiles
+//  * workgroup = W wavefronts (4 or 8); it owns NS 16-row MFMA B tiles
 //    of weight rows (NS/2 gate tiles + the matching up tiles when an
 //    activation is fused) and a slice of K. NS = 2 (4 is kept for e2m1
 //    weights as a tuning option);
 //  * K is cut into 128-wide steps; the workgroup's steps are dealt out to its
-//    W wavefronts, and further across `ksplit` workgroups (grid.y). Small
-//    problems get more wavefronts per workgroup rather than a K split, so
-//    they fill the chip without the split's second kernel;
+//    W wavefronts, and further across `ksplit` workgroups (grid.y) when
+//    the grid is small;
 //  * a wavefront issues the loads of U steps back to back, unconditionally
 //    (weight rows past N and activation rows past the group are clamped to
 //    valid rows -- they only feed outputs that are never stored), and only
 //    then waits and issues the MFMAs, so U steps of weights are in flight
 //    per wavefront. Only a K tail (K % 128 != 0) uses masked loads;
-//  * in a step, lane l holds 32 consecutive k values of weight row (l & 15)
-//    (32 B of e4m3/int8, 16 B of e2m1, 64 B of bf16) and of activation row
-//    (l & 15) of each 16-row M tile, and issues the matching MFMA(s): one
+//  * weight loads are coalesced: 4 adjacent lanes read the 4 x 16 B of one
+//    row's 64 B segment (16 rows per load instruction; measured on MI355X,
+//    17% more bandwidth than one row per lane), and ds_bpermute then moves
+//    the data into MFMA fragment order;
+//  * in a step, lane l holds 32 k values of weight row (l & 15)
+//    (32 B of e4m3/int8, 16 B of e2m1, 64 B of bf16) and the same k values of
+//    activation row (l & 15) of each 16-row M tile, and issues the matching
+//    MFMA(s): one
 //    v_mfma_scale_f32_16x16x128_f8f6f4 (e4m3), two v_mfma_i32_16x16x64_i8
 //    (int8) or four v_mfma_f32_16x16x32_bf16 (bf16 activations; e2m1 weights
 //    are expanded with v_cvt_scalef32_pk_bf16_fp4, which also applies the e8m0
@@ -431,14 +435,15 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p)
 #pragma unroll
       for (int s = 0; s < NS; ++s) acc.v[ms][s] = {0, 0, 0, 0};
 
-    auto load_scales = [&](int ks, StepScales<MS, NS>& sc) {
+    auto load_scales = [&](int ks, bool live, StepScales<MS, NS>& sc) {
       if constexpr (KIND == QK_W8A8_BLK) {
+        const uint32_t o = live ? (uint32_t)ks * 4 : 0x80000000u;
 #pragma unroll
-        for (int s = 0; s < NS; ++s) sc.sb[s] = ldb_f32(sres, soffw[s], (uint32_t)ks * 4);
+        for (int s = 0; s < NS; ++s) sc.sb[s] = ldb_f32(sres, soffw[s], o);
 #pragma unroll
         for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
-          for (int r4 = 0; r4 < 4; ++r4) sc.sa[ms][r4] = ldb_f32(ares, soffa[ms][r4], (uint32_t)ks * 4);
+          for (int r4 = 0; r4 < 4; ++r4) sc.sa[ms][r4] = ldb_f32(ares, soffa[ms][r4], o);
       } else if constexpr (KIND == QK_W4A16_MX) {
 #pragma unroll
         for (int s = 0; s < NS; ++s) sc.eb[s] = s_eb[(s * 16 + col) * KB32 + ks * 4 + kg];
@@ -447,27 +452,33 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p)
 
     // Full steps, U at a time, double-buffered: the loads of chunk c+1 are
     // issued before the MFMAs of chunk c, so 1-2 chunks are always in flight.
-    // Step indices past the slice are clamped to its last step (the
-    // duplicate loads hit cache; their MFMAs are skipped).
+    // Steps past the run issue loads that return zeros without a memory
+    // request; their MFMAs are skipped.
     struct Chunk {
       Frag bw[U][NS];
       Frag fa[U][MS];
       StepScales<MS, NS> sc[U];
     };
+    // steps past the run are issued with an offset past every buffer's
+    // extent: the load instructions still count in vmcnt (so every path
+    // waits alike) but return zeros without a memory request
+    constexpr uint32_t kOob = 0x80000000u;
     auto issue_mem = [&](int j, Chunk& c) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const int kk = sbase + min(j + u, nj - 1);
+        const bool live = j + u < nj;
+        const uint32_t kk = (uint32_t)(sbase + j + u);
+        const uint32_t ow = live ? kk * (4 * Tr::kWBytes) : kOob;
+        const uint32_t oa = live ? kk * (4 * Tr::kABytes) : kOob;
 #pragma unroll
-        for (int s = 0; s < NS; ++s)
-          ldw_seg<Tr::kWBytes, kWeightAux>(c.bw[u][s], wres, woff[s], (uint32_t)kk * (4 * Tr::kWBytes));
+        for (int s = 0; s < NS; ++s) ldw_seg<Tr::kWBytes, kWeightAux>(c.bw[u][s], wres, woff[s], ow);
 #pragma unroll
-        for (int ms = 0; ms < MS; ++ms) lda_chunks<Tr>(c.fa[u][ms], xres, aoff[ms], (uint32_t)kk * (4 * Tr::kABytes));
+        for (int ms = 0; ms < MS; ++ms) lda_chunks<Tr>(c.fa[u][ms], xres, aoff[ms], oa);
       }
     };
     auto issue_sc = [&](int j, Chunk& c) {
 #pragma unroll
-      for (int u = 0; u < U; ++u) load_scales(sbase + min(j + u, nj - 1), c.sc[u]);
+      for (int u = 0; u < U; ++u) load_scales(sbase + min(j + u, nj - 1), j + u < nj, c.sc[u]);
     };
     auto issue = [&](int j, Chunk& c) {
       issue_mem(j, c);
@@ -659,10 +670,12 @@ __global__ __launch_bounds__(kThreads) void skinny_reduce_kernel(const GemmParam
 
 template <int KIND, int WF, int MS, bool ACT, int NS, int W>
 void launch_skinny_w(const GemmParams& p, dim3 grid, hipStream_t st) {
-  const char* env_s = getenv("QMOE_SKINNY_U");  // tuning knob: 1 or 2
+  const char* env_s = getenv("QMOE_SKINNY_U");  // tuning knob: 1, 2 or 4
   const int env_u = env_s ? atoi(env_s) : 0;
   const int u = env_u > 0 ? env_u : default_unroll();
-  if (u >= 2)
+  if (u >= 4)
+    hipLaunchKernelGGL((skinny_gemm_kernel<KIND, WF, MS, ACT, 4, NS, W>), grid, dim3(W * 64), 0, st, p);
+  else if (u >= 2)
     hipLaunchKernelGGL((skinny_gemm_kernel<KIND, WF, MS, ACT, 2, NS, W>), grid, dim3(W * 64), 0, st, p);
   else
     hipLaunchKernelGGL((skinny_gemm_kernel<KIND, WF, MS, ACT, 1, NS, W>), grid, dim3(W * 64), 0, st, p);
@@ -670,8 +683,7 @@ void launch_skinny_w(const GemmParams& p, dim3 grid, hipStream_t st) {
 
 template <int KIND, int WF, int MS, bool ACT, int NS>
 void launch_skinny(const GemmParams& p, int waves, dim3 grid, hipStream_t st) {
-  if (MS == 1 && waves >= 16) launch_skinny_w<KIND, WF, MS, ACT, NS, (MS == 1 ? 16 : 4)>(p, grid, st);
-  else if (MS <= 2 && waves >= 8) launch_skinny_w<KIND, WF, MS, ACT, NS, (MS <= 2 ? 8 : 4)>(p, grid, st);
+  if (MS <= 2 && waves >= 8) launch_skinny_w<KIND, WF, MS, ACT, NS, (MS <= 2 ? 8 : 4)>(p, grid, st);
   else launch_skinny_w<KIND, WF, MS, ACT, NS, 4>(p, grid, st);
   if (p.ksplit > 1) {
     const int nout = ACT ? p.N / 2 : p.N;
@@ -729,7 +741,7 @@ int skinny_tiles(int64_t N, int act, int ns) {
 namespace {
 
 struct SkinnyPlan {
-  int waves;   // wavefronts per workgroup (4, 8 or 16)
+  int waves;   // wavefronts per workgroup (4 or 8)
   int ksplit;  // K slices over grid.y
   int64_t ws_bytes;
 };
@@ -741,7 +753,7 @@ int env_int(const char* name, int dflt) {
 
 // Launch shape of the skinny kernel. Measured on MI355X: 4 wavefronts per
 // workgroup stream best (8 or 16, i.e. shorter K runs per wavefront, lose
-// 10-60%); K is split across workgroups only when there are fewer than ~160
+// 10-60%; 8 stays as a tuning option); K is split across workgroups only when there are fewer than ~160
 // workgroups (one per 32 weight rows), which costs a second launch and the
 // [ksplit][M][N] float32 partial sums in the workspace; every wavefront keeps
 // at least two 128-k steps.
@@ -752,9 +764,7 @@ SkinnyPlan skinny_plan(int kind, int64_t M, int64_t N, int64_t K, int act, int s
   const int KS = (int)cdiv<int64_t>(K, 128);
   // tuning knobs (read per call): wavefronts per workgroup, forced K split,
   // workgroup count the split planner aims for
-  const int wmax = ms == 1 ? 16 : (ms == 2 ? 8 : 4);
-  const int env_w = env_int("QMOE_SKINNY_WAVES", 4);
-  const int w = (env_w == 8 || env_w == 16) ? std::min(env_w, wmax) : 4;
+  const int w = ms <= 2 && env_int("QMOE_SKINNY_WAVES", 4) == 8 ? 8 : 4;
   int ksplit = ksplit_hint > 0 ? ksplit_hint : env_int("QMOE_SKINNY_KSPLIT", 0);
   if (ksplit <= 0) ksplit = (int)cdiv<int64_t>(env_int("QMOE_SKINNY_TARGET_WG", 160), n_wg);
   ksplit = std::max(1, std::min(ksplit, std::max(1, KS / (2 * w))));
