@@ -79,6 +79,71 @@ def test_e4m3_device_encoder_sweep(dev):
     np.testing.assert_array_equal(q.view(torch.uint8).cpu().numpy(), q_ref)
 
 
+def _bf16_neighbours(v):
+    """bf16 values one bf16 ulp above and below each f32 value of v."""
+    b = v.astype(np.float32).view(np.uint32) & 0xFFFF0000
+    up = (b + 0x10000).view(np.float32)
+    dn = (b - 0x10000).view(np.float32)
+    return np.concatenate([up, dn])
+
+
+@pytest.mark.parametrize("qdtype", ["fp8", "int8"])
+def test_runtime_encoder_sweep(dev, qdtype):
+    """Runtime activation codes at every e4m3 rounding boundary (exact ties
+    and one bf16 ulp either side), signed zeros and f32-subnormal-scale
+    values, with the row scale exactly 1 (absmax 448 / 127) and 3."""
+    from qmoe import ops
+
+    qmax = 448.0 if qdtype == "fp8" else 127.0
+    vals = codecs.e4m3_decode(np.arange(256, dtype=np.uint8)).astype(np.float64)
+    fin = np.unique(vals[np.isfinite(vals)])
+    mids = (fin[:-1] + fin[1:]) / 2
+    ints = np.arange(-128, 129, dtype=np.float64)
+    halves = ints[:-1] + 0.5
+    base = np.concatenate([fin, mids, ints, halves]).astype(np.float32)
+    base = np.concatenate([base, _bf16_neighbours(base),
+                           np.array([0.0, -0.0, 2.0 ** -10, -(2.0 ** -10), 3 * 2.0 ** -11, 2.0 ** -20,
+                                     2.0 ** -126, -(2.0 ** -133)], np.float32)])
+    rows = []
+    for sc in (1.0, 3.0):
+        x = codecs.bf16_round(base * np.float32(sc))
+        x = x[np.abs(x) <= qmax * sc]
+        n = (x.size + 127) // 128 * 128
+        row = np.zeros(n, np.float32)
+        row[: x.size] = x
+        row[-1] = qmax * sc  # absmax -> scale exactly sc
+        rows.append(row)
+    n = max(r.size for r in rows)
+    xm = np.zeros((len(rows), n), np.float32)
+    for i, r in enumerate(rows):
+        xm[i, : r.size] = r
+        xm[i, -1] = r[-1]
+    q_ref, s_ref = quant.quantize_act(xm, qdtype)
+    q, s = ops.row_quant(_t(xm, dev, torch.bfloat16), qdtype)
+    np.testing.assert_array_equal(s.cpu().numpy(), s_ref)
+    np.testing.assert_array_equal(q.view(torch.uint8).cpu().numpy(), q_ref.view(np.uint8))
+
+
+@pytest.mark.parametrize("qdtype", ["fp8", "int8"])
+def test_runtime_quant_division_stress(dev, qdtype):
+    """Many quotients x / scale with scales that are not powers of two,
+    against the oracle's IEEE division (codes and scales bit-exact)."""
+    from qmoe import ops
+
+    rng = np.random.default_rng(5)
+    M, K = 48, 8192
+    x = codecs.bf16_round((rng.uniform(-1, 1, (M, K)) * rng.uniform(0.01, 1000, (M, 1))).astype(np.float32))
+    q_ref, s_ref = quant.quantize_act(x, qdtype)
+    q, s = ops.row_quant(_t(x, dev, torch.bfloat16), qdtype)
+    np.testing.assert_array_equal(s.cpu().numpy(), s_ref)
+    np.testing.assert_array_equal(q.view(torch.uint8).cpu().numpy(), q_ref.view(np.uint8))
+    if qdtype == "fp8":
+        qb_ref, sb_ref = quant.quantize_act(x, qdtype, block=128)
+        qb, sb = ops.row_quant(_t(x, dev, torch.bfloat16), qdtype, block=128)
+        np.testing.assert_array_equal(sb.cpu().numpy(), sb_ref)
+        np.testing.assert_array_equal(qb.view(torch.uint8).cpu().numpy(), qb_ref.view(np.uint8))
+
+
 # ------------------------------------------------------------------ GEMM
 
 SHAPES_SKINNY = [(1, 512, 384), (8, 1024, 640), (16, 2048, 256), (33, 512, 4096), (64, 4096, 1024)]

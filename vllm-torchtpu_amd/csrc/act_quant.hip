@@ -71,6 +71,18 @@ __device__ __forceinline__ float make_scale(float amax) {
   return amax * recip;
 }
 
+// x / scale rounded to nearest even, from inv = RN(1 / scale): q = RN(x*inv)
+// is within one ulp of the quotient, so r = x - q*scale is exact (one FMA)
+// and RN(q + r*inv) is the correctly rounded quotient (Markstein's theorem;
+// |x / scale| <= qmax rules out overflow, and a quotient in the f32
+// subnormal range encodes to a signed zero whatever its last bits). A zero
+// quotient takes x's sign, as the division gives it.
+__device__ __forceinline__ float div_rn(float x, float scale, float inv) {
+  const float q = x * inv;
+  const float r = __builtin_fmaf(-q, scale, x);
+  return __builtin_copysignf(__builtin_fmaf(r, inv, q), x);
+}
+
 template <int kQdt, int kMode>
 __device__ __forceinline__ uint32_t quant1(float x, float scale, float inv) {
   if (kMode == 0) {
@@ -93,8 +105,39 @@ __device__ __forceinline__ uint32_t quant1(float x, float scale, float inv) {
   return (uint32_t)(int32_t)rintf(c) & 0xffu;
 }
 
+// Runtime codes of 8 values of a row whose scale is finite (so are the
+// values: the absmax is NaN- and inf-sticky): division as div_rn, clip,
+// then the hardware RNE conversion (e4m3 pairs) or rint (int8).
+template <int kQdt>
+__device__ __forceinline__ void store8_fast(uint8_t* dst, const Row8& r, float scale, float inv) {
+  if (kQdt == 0) {
+    float d[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) d[i] = fminf(fmaxf(div_rn(r.v[i], scale, inv), -448.0f), 448.0f);
+    int lo = __builtin_amdgcn_cvt_pk_fp8_f32(d[0], d[1], 0, false);
+    lo = __builtin_amdgcn_cvt_pk_fp8_f32(d[2], d[3], lo, true);
+    int hi = __builtin_amdgcn_cvt_pk_fp8_f32(d[4], d[5], 0, false);
+    hi = __builtin_amdgcn_cvt_pk_fp8_f32(d[6], d[7], hi, true);
+    *reinterpret_cast<uint2*>(dst) = make_uint2((uint32_t)lo, (uint32_t)hi);
+  } else {
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float q = fminf(fmaxf(rintf(bf16_round(div_rn(r.v[i], scale, inv))), -128.0f), 127.0f);
+      const uint32_t c = (uint32_t)(int32_t)q & 0xffu;
+      if (i < 4) lo |= c << (8 * i);
+      else hi |= c << (8 * (i - 4));
+    }
+    *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
+  }
+}
+
 template <int kQdt, int kMode>
 __device__ __forceinline__ void store8(uint8_t* dst, const Row8& r, float scale) {
+  if (kMode == 0 && __builtin_isfinite(scale)) {
+    store8_fast<kQdt>(dst, r, scale, 1.0f / scale);
+    return;
+  }
   float inv = 0.0f;
   if (kMode == 1) inv = scale == 0.0f ? 0.0f : 1.0f / scale;
   uint32_t lo = 0, hi = 0;
