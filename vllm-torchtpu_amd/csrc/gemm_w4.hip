@@ -347,8 +347,11 @@ bool qmoe_w4_plan(const GemmParams& p, int* bm_out, int* ksplit_out, int64_t* ws
   if (env && (atoi(env) == 128 || atoi(env) == 64 || atoi(env) == 32)) {
     bm = atoi(env);
   } else if (p.group_offs) {
+    // measured on MI355X (GPT-OSS MoE, 128 experts): 64-token tiles up to
+    // ~96 rows per routed expert (32-token tiles lose ~25% at 32 rows), 128
+    // above
     const int avg = std::max(1, p.M / std::max(1, std::min(p.slots, p.M)));
-    bm = avg > 96 ? 128 : (avg > 48 ? 64 : 32);
+    bm = avg > 96 ? 128 : 64;
   } else {
     // measured on MI355X (K 2880, N 5760): 128-token tiles once they fill the
     // CUs, else 64 with a K split (32-token tiles are slower at every M)

@@ -21,7 +21,14 @@ format                w1 [E, 2I, H...] / w2        scales
 
 w1's N axis is ``[gate | up]`` (gate rows first), as in the reference
 (`kernels/megablox/gmm_v2.py:894-901`).
+
+The layer body is the torch custom op ``torch.ops.qmoe.fused_moe_gmm`` with a
+fake implementation (output ``[T, H]`` bf16), so ``torch.compile(fullgraph=
+True)`` traces through it; the reference prebuilds one custom op per static
+configuration for the same reason (`layers/adapter/fused_moe.py:146-238`).
 """
+
+from typing import Optional
 
 import torch
 
@@ -51,20 +58,36 @@ def fused_moe_gmm(hidden_states, w1, w2, w1_scale, w2_scale, w1_bias, w2_bias, t
     runs the whole expert set on one GPU, so it must be None or 0.
     ``rhs_quant_dtype`` (packed int4 carriers) is not supported.
     """
-    if experts_start is not None and int(experts_start) != 0:
+    if experts_start is not None and not isinstance(experts_start, torch.Tensor) and int(experts_start) != 0:
         raise NotImplementedError("expert parallelism is out of scope: experts_start must be 0")
     if rhs_quant_dtype is not None:
         raise NotImplementedError("packed int4 rhs_quant_dtype is not supported")
     fmt = weight_format or infer_weight_format(w1, w1_scale)
+    if fmt not in ("mxfp4", "bf16", "fp8_block", "fp8_block_rows", "fp8", "int8"):
+        raise ValueError(f"unknown MoE weight format {fmt!r}")
+    ops.act_code(activation)  # NotImplementedError for an unknown activation string
     T, H = hidden_states.shape
-    E = w1.shape[0]
     if topk_weights.shape != (T, topk) or topk_ids.shape != (T, topk):
         raise ValueError(f"topk tensors must be [{T}, {topk}]")
     x = hidden_states if hidden_states.dtype == torch.bfloat16 else hidden_states.to(torch.bfloat16)
-    x = x.contiguous()
     # `fused_moe_gmm.py:653`: routing weights take the hidden dtype
-    tw = topk_weights.to(torch.bfloat16).contiguous()
-    skip = bool(skip_padded_tokens)
+    tw = topk_weights.to(torch.bfloat16)
+    ids = topk_ids.to(torch.int32)
+    return torch.ops.qmoe.fused_moe_gmm(x, w1, w2, w1_scale, w2_scale, w1_bias, w2_bias, tw, ids, int(topk),
+                                        activation or "", bool(skip_padded_tokens), fmt)
+
+
+@torch.library.custom_op("qmoe::fused_moe_gmm", mutates_args=())
+def _fused_moe_gmm_op(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, w1_scale: Optional[torch.Tensor],
+                      w2_scale: Optional[torch.Tensor], w1_bias: Optional[torch.Tensor],
+                      w2_bias: Optional[torch.Tensor], tw: torch.Tensor, topk_ids: torch.Tensor, topk: int,
+                      activation: str, skip: bool, fmt: str) -> torch.Tensor:
+    """Checked operands: x bf16 [T, H]; tw bf16 / topk_ids int32 [T, topk]."""
+    activation = activation or None
+    T, H = x.shape
+    E = w1.shape[0]
+    x = x.contiguous()
+    tw = tw.contiguous()
     meta = ops.moe_dispatch(topk_ids, tw, E, skip)
     M = T * topk
     common = dict(group_offs=meta["group_offs"], active=meta["active"],
@@ -109,3 +132,8 @@ def fused_moe_gmm(hidden_states, w1, w2, w1_scale, w2_scale, w1_bias, w2_bias, t
     ops.gemm(kind, a2, w2k, a_scale=a2_scale, w_scale=w2s, wfmt=wf, ws_bn=bn, bias=b2,
              row_weight=meta["sorted_weight"], y_rows=meta["sorted_idx"], out=routed, **common)
     return ops.moe_combine(routed, topk_ids, tw, skip)
+
+
+@_fused_moe_gmm_op.register_fake
+def _(x, w1, w2, w1_scale, w2_scale, w1_bias, w2_bias, tw, topk_ids, topk, activation, skip, fmt):
+    return x.new_empty(x.shape, dtype=torch.bfloat16)

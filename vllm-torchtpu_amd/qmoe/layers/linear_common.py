@@ -6,6 +6,13 @@ Mirrors `layers/adapter/linear_common.py` of the reference plugin:
 argument meaning and the same ValueError texts; the computation runs in the
 qmoe HIP kernels.
 
+Both are registered as torch custom ops (``torch.ops.qmoe.quantized_matmul``
+and ``torch.ops.qmoe.quantized_matmul_fp4``) with fake implementations, so a
+model that calls them compiles with ``torch.compile(fullgraph=True)`` (the
+reference builds its ops the same way: custom ops with ``register_fake``,
+`linear_common.py:131-159`). Shape and layout checks run in the Python
+wrappers below, before the op, so they raise at trace time too.
+
 Weight layout: the reference's runtime weight is the canonical (k, n)
 ``[n_in, n_out]`` array. Here ``w_q`` has that same logical shape but must be
 the transposed VIEW of an N-major ``[n_out, n_in]`` buffer (stride
@@ -14,6 +21,8 @@ produces: each output channel's K values stay contiguous for 16-byte HBM
 loads. A K-major contiguous ``[n_in, n_out]`` tensor is rejected rather than
 transposed per call.
 """
+
+from typing import Optional
 
 import torch
 
@@ -92,10 +101,27 @@ def quantized_matmul(x: torch.Tensor, w_q: torch.Tensor, w_s: torch.Tensor,
         x2 = x2.to(torch.bfloat16)
     w_nk = _weight_nk(w_q)
     k_dim, n_out = w_q.shape
-    rows = x2.shape[0]
     if w_s.dim() == 1:
         if w_s.shape[0] != n_out:
             raise ValueError(f"per-channel scale has {w_s.shape[0]} entries, expected {n_out}")
+        if w_nk.dtype not in (torch.int8, torch.float8_e4m3fn):
+            raise ValueError(f"Unsupported quantized dtype: {w_nk.dtype}")
+    else:
+        if w_nk.dtype != torch.float8_e4m3fn:
+            raise ValueError(f"blockwise kernels take float8_e4m3fn weights, got {w_nk.dtype}")
+        w_s, _ = _scale_blocks(w_s, k_dim, n_out)
+    out = torch.ops.qmoe.quantized_matmul(x2, w_nk, w_s, int(w8a16_max_rows))
+    return out.reshape(orig_out_shape)
+
+
+@torch.library.custom_op("qmoe::quantized_matmul", mutates_args=())
+def _quantized_matmul_op(x2: torch.Tensor, w_nk: torch.Tensor, w_s: torch.Tensor,
+                         w8a16_max_rows: int) -> torch.Tensor:
+    """Checked operands: x2 bf16 [rows, K]; w_nk N-major [N, K] codes; w_s
+    per-channel f32 [N] or compact block scales [N/bn, K/128]."""
+    n_out, k_dim = w_nk.shape
+    rows = x2.shape[0]
+    if w_s.dim() == 1:
         ws = w_s.float().contiguous()
         if w_nk.dtype == torch.int8:
             xq, xs = ops.row_quant(x2, "int8")
@@ -111,13 +137,16 @@ def quantized_matmul(x: torch.Tensor, w_q: torch.Tensor, w_s: torch.Tensor,
         else:
             raise ValueError(f"Unsupported quantized dtype: {w_nk.dtype}")
     else:
-        if w_nk.dtype != torch.float8_e4m3fn:
-            raise ValueError(f"blockwise kernels take float8_e4m3fn weights, got {w_nk.dtype}")
         sb, bn = _scale_blocks(w_s, k_dim, n_out)
         xq, xs = ops.row_quant(x2, "fp8", block=128)
         out = ops.gemm(_capi.W8A8_BLK, xq.view(torch.uint8), w_nk.view(torch.uint8),
                        a_scale=xs, w_scale=sb, ws_bn=bn)
-    return out.reshape(orig_out_shape)
+    return out
+
+
+@_quantized_matmul_op.register_fake
+def _(x2, w_nk, w_s, w8a16_max_rows):
+    return x2.new_empty((x2.shape[0], w_nk.shape[0]), dtype=torch.bfloat16)
 
 
 def quantized_matmul_fp4(x: torch.Tensor, w_q: torch.Tensor, w_s: torch.Tensor,
@@ -140,6 +169,16 @@ def quantized_matmul_fp4(x: torch.Tensor, w_q: torch.Tensor, w_s: torch.Tensor,
     x2 = x.reshape(-1, k_dim)
     if x2.dtype != torch.bfloat16:
         x2 = x2.to(torch.bfloat16)
-    out = ops.gemm(_capi.W4A16_MX, x2, w_q.view(torch.uint8).contiguous(),
-                   w_scale=w_s.view(torch.uint8).contiguous(), bias=bias)
+    out = torch.ops.qmoe.quantized_matmul_fp4(x2, w_q.view(torch.uint8), w_s.view(torch.uint8), bias)
     return out.reshape(*x.shape[:-1], n_out)
+
+
+@torch.library.custom_op("qmoe::quantized_matmul_fp4", mutates_args=())
+def _quantized_matmul_fp4_op(x2: torch.Tensor, w_q: torch.Tensor, w_s: torch.Tensor,
+                             bias: Optional[torch.Tensor]) -> torch.Tensor:
+    return ops.gemm(_capi.W4A16_MX, x2, w_q.contiguous(), w_scale=w_s.contiguous(), bias=bias)
+
+
+@_quantized_matmul_fp4_op.register_fake
+def _(x2, w_q, w_s, bias):
+    return x2.new_empty((x2.shape[0], w_s.shape[0]), dtype=torch.bfloat16)

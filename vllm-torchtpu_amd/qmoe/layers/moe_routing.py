@@ -4,12 +4,44 @@
 ``route`` mirrors `:150-186`, and ``rowmax_select`` mirrors
 `layers/adapter/router_topk.py:42-50`. Scores, the sort-free top-k (ties to
 the lowest expert id), grouped selection, renormalization and scaling all run
-in one HIP kernel (`qmoe_moe_route`).
+in one HIP kernel (`qmoe_moe_route`), registered as the torch custom op
+``torch.ops.qmoe.moe_route`` with a fake implementation (the reference
+registers its router op the same way, `layers/adapter/router_topk.py:36-39`).
 """
+
+from typing import Optional, Tuple
 
 import torch
 
 from qmoe import ops
+
+
+@torch.library.custom_op("qmoe::moe_route", mutates_args=())
+def _moe_route_op(logits: torch.Tensor, topk: int, scoring_func: str, renormalize: bool,
+                  bias: Optional[torch.Tensor], routed_scaling_factor: float, num_expert_group: int,
+                  topk_group: int, weights_f32: bool) -> Tuple[torch.Tensor, torch.Tensor]:
+    return ops.moe_route(logits, topk, scoring_func, renormalize, bias, routed_scaling_factor,
+                         num_expert_group, topk_group, weights_f32)
+
+
+@_moe_route_op.register_fake
+def _(logits, topk, scoring_func, renormalize, bias, routed_scaling_factor, num_expert_group, topk_group,
+      weights_f32):
+    T = logits.numel() // logits.shape[-1]
+    w = logits.new_empty((T, topk), dtype=torch.float32 if weights_f32 else torch.bfloat16)
+    return w, logits.new_empty((T, topk), dtype=torch.int32)
+
+
+def _route(logits, topk, scoring_func, renormalize, bias=None, routed_scaling_factor=1.0,
+           num_expert_group=1, topk_group=1, weights_f32=False):
+    """Host-side checks (raised at trace time), then the custom op."""
+    if scoring_func not in ops._SCORING:
+        raise NotImplementedError(f"FusedMoE does not support {scoring_func} scoring function for TPU.")
+    if topk > logits.shape[-1]:
+        raise ValueError(f"topk k={topk} exceeds the expert count {logits.shape[-1]}")
+    return torch.ops.qmoe.moe_route(logits, int(topk), scoring_func, bool(renormalize), bias,
+                                    float(routed_scaling_factor), int(num_expert_group or 1),
+                                    int(topk_group or 1), bool(weights_f32))
 
 
 def rowmax_select(scores: torch.Tensor, topk: int):
@@ -21,8 +53,7 @@ def rowmax_select(scores: torch.Tensor, topk: int):
     n = scores.shape[-1]
     if topk > n:
         raise ValueError(f"topk k={topk} exceeds the expert count {n}")
-    w, ids = ops.moe_route(scores.float(), topk, scoring_func="none", renormalize=False,
-                           weights_f32=True)
+    w, ids = _route(scores.float(), topk, "none", False, weights_f32=True)
     return w.reshape(*scores.shape[:-1], topk), ids.reshape(*scores.shape[:-1], topk)
 
 
@@ -42,9 +73,9 @@ def select_experts(hidden_states, router_logits, *, topk, renormalize, scoring_f
     if (layer is not None and getattr(layer, "use_grouped_topk", False)
             and layer.num_expert_group > 1 and layer.topk_group < layer.num_expert_group):
         ng, tg = layer.num_expert_group, layer.topk_group
-    w, ids = ops.moe_route(router_logits, topk, scoring_func=scoring_fn, renormalize=renormalize,
-                           bias=bias, routed_scaling_factor=rsf if rsf is not None else 1.0,
-                           num_expert_group=ng, topk_group=tg)
+    w, ids = _route(router_logits, topk, scoring_fn, renormalize, bias=bias,
+                    routed_scaling_factor=rsf if rsf is not None else 1.0, num_expert_group=ng,
+                    topk_group=tg)
     return w.to(hidden_states.dtype), ids
 
 
