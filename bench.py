@@ -48,8 +48,10 @@ def parse():
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="", help="comma list of sweep configs to run (0-4)")
-    ap.add_argument("--profile", action="store_true",
-                    help="only run the headline kernel + a copy calibration (for rocprofv3)")
+    ap.add_argument("--profile", nargs="?", const="headline", default=None,
+                    choices=["headline", "decode", "moe"],
+                    help="rocprofv3 targets: the headline kernel + a copy calibration (default), "
+                         "the decode GEMMs (cfg 0/1/2 at M=1), or the MoE layers at T=1 (cfg 3/4)")
     return ap.parse_args()
 
 
@@ -415,10 +417,73 @@ def profile_target(args):
     log(f"profile target done: gemm M={M} x10, copy 256MiB x10")
 
 
+def profile_decode(args):
+    """rocprofv3 target: 20 launches each of the decode linears at M=1 --
+    cfg 0 MXFP4 (K 2880, N 5760), cfg 1 FP8 W8A8 up (K 4096, N 14336, incl.
+    the activation quant), cfg 2 block FP8 (K 7168, N 24576) -- after 3
+    warm-up calls."""
+    import torch
+
+    from qmoe.layers.linear_common import quantized_matmul, quantized_matmul_fp4
+
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    codes, sc = mxfp4_weights((5760, 2880), gen)
+    x0 = torch.randn((1, 2880), device="cuda", generator=gen).to(torch.bfloat16)
+    w1, s1 = fp8_weights(14336, 4096, gen)
+    x1 = torch.randn((1, 4096), device="cuda", generator=gen).to(torch.bfloat16)
+    w2, s2 = fp8_weights(24576, 7168, gen, tiles=True)
+    x2 = torch.randn((1, 7168), device="cuda", generator=gen).to(torch.bfloat16)
+    for fn in (lambda: quantized_matmul_fp4(x0, codes, sc), lambda: quantized_matmul(x1, w1.t(), s1),
+               lambda: quantized_matmul(x2, w2.t(), s2)):
+        for _ in range(23):
+            fn()
+        torch.cuda.synchronize()
+    log("profile target done: cfg0/cfg1/cfg2 M=1 x23 each")
+
+
+def profile_moe(args):
+    """rocprofv3 target: 20 MoE layers at T=1 each for cfg 3 (GPT-OSS,
+    MXFP4) and cfg 4 (DeepSeek-V3 routed experts, 128x128 FP8), after 3
+    warm-up layers."""
+    import torch
+
+    from qmoe import ops
+    from qmoe.layers.fused_moe import fused_moe_gmm
+
+    gen = torch.Generator(device="cuda").manual_seed(2)
+    E, k, H, I = 128, 4, 2880, 2880
+    w13, s13 = mxfp4_weights((E, 2 * I, H), gen)
+    w2, s2 = mxfp4_weights((E, H, I), gen)
+    x = torch.randn((1, H), device="cuda", generator=gen).to(torch.bfloat16)
+    logits = torch.randn((1, E), device="cuda", generator=gen).to(torch.bfloat16)
+    for _ in range(23):
+        w, ids = ops.moe_route(logits, k, "softmax", True)
+        fused_moe_gmm(x, w13, w2, s13, s2, None, None, w, ids, None, k, "swigluoai", weight_format="mxfp4")
+    torch.cuda.synchronize()
+    del w13, s13, w2, s2
+    E, k, H, I = 256, 8, 7168, 2048
+    w13 = torch.empty((E, 2 * I, H), device="cuda", dtype=torch.float8_e4m3fn)
+    s13 = torch.empty((E, 2 * I // 128, H // 128), device="cuda", dtype=torch.float32)
+    w2 = torch.empty((E, H, I), device="cuda", dtype=torch.float8_e4m3fn)
+    s2 = torch.empty((E, H // 128, I // 128), device="cuda", dtype=torch.float32)
+    for e in range(E):
+        w13[e], s13[e] = fp8_weights(2 * I, H, gen, tiles=True)
+        w2[e], s2[e] = fp8_weights(H, I, gen, tiles=True)
+    bias = torch.randn(E, device="cuda", generator=gen) * 0.1
+    x = torch.randn((1, H), device="cuda", generator=gen).to(torch.bfloat16)
+    logits = torch.randn((1, E), device="cuda", generator=gen).to(torch.bfloat16)
+    for _ in range(23):
+        w, ids = ops.moe_route(logits, k, "sigmoid", True, bias=bias, routed_scaling_factor=2.5,
+                               num_expert_group=8, topk_group=4)
+        fused_moe_gmm(x, w13, w2, s13, s2, None, None, w, ids, None, k, "silu", weight_format="fp8_block")
+    torch.cuda.synchronize()
+    log("profile target done: cfg3 / cfg4 MoE T=1 x23 each")
+
+
 def main():
     args = parse()
     if args.profile:
-        profile_target(args)
+        {"headline": profile_target, "decode": profile_decode, "moe": profile_moe}[args.profile](args)
         return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (got --gpus {args.gpus}); "
