@@ -244,11 +244,23 @@ def sweep_linear(only):
     return out
 
 
+def moe_layer_cfg(topk, scoring, activation, bias=None, rsf=1.0, groups=None):
+    """The attributes a MoE method reads from its vLLM layer (routing
+    settings, activation), for `moe_forward`."""
+    from types import SimpleNamespace
+
+    return SimpleNamespace(moe_config=SimpleNamespace(experts_per_token=topk), scoring_func=scoring,
+                           renormalize=True, e_score_correction_bias=bias, routed_scaling_factor=rsf,
+                           use_grouped_topk=groups is not None, num_expert_group=groups[0] if groups else 1,
+                           topk_group=groups[1] if groups else 1, custom_routing_function=None,
+                           _qmoe_activation=activation)
+
+
 def sweep_moe(only):
     import torch
 
     from qmoe import ops
-    from qmoe.layers.fused_moe import fused_moe_gmm
+    from qmoe.layers.fused_moe import moe_forward
 
     gen = torch.Generator(device="cuda").manual_seed(2)
     out = []
@@ -257,14 +269,13 @@ def sweep_moe(only):
         w13, s13 = mxfp4_weights((E, 2 * I, H), gen)
         w2, s2 = mxfp4_weights((E, H, I), gen)
         per_expert = 2 * I * H // 2 + 2 * I * H // 32 + H * I // 2 + H * I // 32
+        lcfg = moe_layer_cfg(k, "softmax", "swigluoai")
         for T in (1, 16, 128, 1024, 8192):
             x = torch.randn((T, H), device="cuda", generator=gen).to(torch.bfloat16)
             logits = torch.randn((T, E), device="cuda", generator=gen).to(torch.bfloat16)
 
             def layer():
-                w, ids = ops.moe_route(logits, k, "softmax", True)
-                return fused_moe_gmm(x, w13, w2, s13, s2, None, None, w, ids, None, k, "swigluoai",
-                                     weight_format="mxfp4")
+                return moe_forward(lcfg, x, logits, w13, w2, s13, s2, None, None, "mxfp4")
 
             us = graph_time_us(layer, iters=20)[0]
             _, ids = ops.moe_route(logits, k, "softmax", True)
@@ -293,6 +304,7 @@ def sweep_moe(only):
         sh13, ss13 = tile_q((2 * I, H))
         sh2, ss2 = tile_q((H, I))
         bias = torch.randn(E, device="cuda", generator=gen) * 0.1
+        lcfg = moe_layer_cfg(k, "sigmoid", "silu", bias=bias, rsf=2.5, groups=(8, 4))
         per_expert = 3 * H * I + 4 * (2 * I // 128) * (H // 128) + 4 * (H // 128) * (I // 128)
         for skew in (False, True):
             for T in (1, 8, 64, 512, 4096):
@@ -306,10 +318,7 @@ def sweep_moe(only):
                 logits = logits.to(torch.bfloat16)
 
                 def routed_part():
-                    w, ids = ops.moe_route(logits, k, "sigmoid", True, bias=bias, routed_scaling_factor=2.5,
-                                           num_expert_group=8, topk_group=4)
-                    return fused_moe_gmm(x, w13, w2, s13, s2, None, None, w, ids, None, k, "silu",
-                                         weight_format="fp8_block")
+                    return moe_forward(lcfg, x, logits, w13, w2, s13, s2, None, None, "fp8_block")
 
                 def shared():
                     from qmoe import _capi
@@ -447,8 +456,7 @@ def profile_moe(args):
     warm-up layers."""
     import torch
 
-    from qmoe import ops
-    from qmoe.layers.fused_moe import fused_moe_gmm
+    from qmoe.layers.fused_moe import moe_forward
 
     gen = torch.Generator(device="cuda").manual_seed(2)
     E, k, H, I = 128, 4, 2880, 2880
@@ -456,9 +464,9 @@ def profile_moe(args):
     w2, s2 = mxfp4_weights((E, H, I), gen)
     x = torch.randn((1, H), device="cuda", generator=gen).to(torch.bfloat16)
     logits = torch.randn((1, E), device="cuda", generator=gen).to(torch.bfloat16)
+    lcfg = moe_layer_cfg(k, "softmax", "swigluoai")
     for _ in range(23):
-        w, ids = ops.moe_route(logits, k, "softmax", True)
-        fused_moe_gmm(x, w13, w2, s13, s2, None, None, w, ids, None, k, "swigluoai", weight_format="mxfp4")
+        moe_forward(lcfg, x, logits, w13, w2, s13, s2, None, None, "mxfp4")
     torch.cuda.synchronize()
     del w13, s13, w2, s2
     E, k, H, I = 256, 8, 7168, 2048
@@ -472,10 +480,9 @@ def profile_moe(args):
     bias = torch.randn(E, device="cuda", generator=gen) * 0.1
     x = torch.randn((1, H), device="cuda", generator=gen).to(torch.bfloat16)
     logits = torch.randn((1, E), device="cuda", generator=gen).to(torch.bfloat16)
+    lcfg = moe_layer_cfg(k, "sigmoid", "silu", bias=bias, rsf=2.5, groups=(8, 4))
     for _ in range(23):
-        w, ids = ops.moe_route(logits, k, "sigmoid", True, bias=bias, routed_scaling_factor=2.5,
-                               num_expert_group=8, topk_group=4)
-        fused_moe_gmm(x, w13, w2, s13, s2, None, None, w, ids, None, k, "silu", weight_format="fp8_block")
+        moe_forward(lcfg, x, logits, w13, w2, s13, s2, None, None, "fp8_block")
     torch.cuda.synchronize()
     log("profile target done: cfg3 / cfg4 MoE T=1 x23 each")
 

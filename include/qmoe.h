@@ -159,6 +159,23 @@ int qmoe_moe_dispatch(const int32_t* topk_ids, const uint16_t* topk_weights, int
                       int32_t* num_active, uint16_t* sorted_weight, qmoe_stream_t stream);
 
 /*
+ * Routing and dispatch of a decode step in one launch (1 <= T <= 16 tokens,
+ * T * topk <= 64 routes, E <= 512): the outputs of qmoe_moe_route (bf16
+ * weights) followed by those of qmoe_moe_dispatch on its routes, written by
+ * one workgroup. Replaces `layers/adapter/moe_routing.py:232-323`
+ * (select_experts) followed by `layers/core/fused_moe_gmm.py:288-408`
+ * (prepare_routed_gmm_inputs), which the reference runs back to back in
+ * its MoE entry (`layers/adapter/quantization/fp8.py:1108-1222`). Returns
+ * QMOE_ERR_ARG outside those bounds (the caller then makes the two calls).
+ */
+int qmoe_moe_route_dispatch(const void* logits, int logits_f32, int64_t T, int E, int topk, int scoring,
+                            const float* bias, int renormalize, float routed_scaling_factor, int num_group,
+                            int topk_group, uint16_t* topk_weights, int32_t* topk_ids, int skip_padded,
+                            int32_t* sorted_idx, int32_t* revert, int32_t* token_sorted,
+                            int32_t* group_offs, int32_t* active, int32_t* num_active,
+                            uint16_t* sorted_weight, qmoe_stream_t stream);
+
+/*
  * Weighted unpermute, replaces `layers/core/fused_moe_gmm.py:572-577`:
  * out[t] = bf16( sum over valid slots j of rows[t*k + j] ), where `rows`
  * holds the already weighted down-projection rows in flat route order

@@ -167,3 +167,47 @@ def test_fused_moe_layer(dev, fmt, act, E, k, H, I, T, bias):
         weight_format=fmt,
     )
     assert_close_rows(got.float().cpu().numpy(), ref, f"moe {fmt}")
+
+
+@pytest.mark.parametrize("T,E,k,scoring,grouped,skip", [
+    (1, 128, 4, "softmax", None, False), (5, 128, 4, "softmax", None, True), (16, 128, 4, "softmax", None, False),
+    (1, 256, 8, "sigmoid", (8, 4), False), (8, 256, 8, "sigmoid", (8, 4), True), (3, 96, 6, "sigmoid", (6, 3), False),
+    (16, 512, 4, "sqrtsoftplus", None, False), (2, 60, 5, "sigmoid", (5, 2), False)])
+def test_route_dispatch_fused_matches_separate(dev, T, E, k, scoring, grouped, skip):
+    """The decode launch that routes and dispatches in one workgroup gives
+    exactly the outputs of the two separate entry points (and the oracle's
+    permutation)."""
+    from qmoe import ops
+
+    print(f"route+dispatch T={T} E={E} k={k} {scoring} grouped={grouped} skip={skip}", flush=True)
+    rng = np.random.default_rng(T * 31 + E + k)
+    logits = codecs.bf16_round(rng.standard_normal((T, E)).astype(np.float32))
+    bias = _t((rng.standard_normal(E) * 0.1).astype(np.float32), dev) if scoring == "sigmoid" else None
+    ng, tg = grouped if grouped else (1, 1)
+    lt = _t(logits, dev, torch.bfloat16)
+    kw = dict(bias=bias, routed_scaling_factor=2.5 if scoring == "sigmoid" else 1.0, num_expert_group=ng,
+              topk_group=tg)
+    w_ref, ids_ref = ops.moe_route(lt, k, scoring, True, **kw)
+    meta_ref = ops.moe_dispatch(ids_ref, w_ref, E, skip)
+    w, ids, meta = ops.moe_route_dispatch(lt, k, scoring, True, skip_padded_tokens=skip, **kw)
+    np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref.cpu().numpy())
+    np.testing.assert_array_equal(w.view(torch.int16).cpu().numpy(), w_ref.view(torch.int16).cpu().numpy())
+    for key in ("sorted_idx", "revert", "token_sorted", "group_offs", "num_active"):
+        np.testing.assert_array_equal(meta[key].cpu().numpy(), meta_ref[key].cpu().numpy(), err_msg=key)
+    na = int(meta["num_active"].item())
+    np.testing.assert_array_equal(meta["active"][:na].cpu().numpy(), meta_ref["active"][:na].cpu().numpy())
+    np.testing.assert_array_equal(meta["sorted_weight"].view(torch.int16).cpu().numpy(),
+                                  meta_ref["sorted_weight"].view(torch.int16).cpu().numpy())
+    p = omoe.prepare_routed(ids.cpu().numpy(), w.float().cpu().numpy(), E, skip)
+    np.testing.assert_array_equal(meta["sorted_idx"].cpu().numpy(), p["sorted_idx"])
+    np.testing.assert_array_equal(np.diff(meta["group_offs"].cpu().numpy()), p["group_sizes"])
+
+
+def test_route_dispatch_rejects_large_batches(dev):
+    from qmoe import ops
+
+    logits = torch.zeros((17, 64), device=dev, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        ops.moe_route_dispatch(logits, 2, "softmax", True)
+    with pytest.raises(ValueError):
+        ops.moe_route_dispatch(logits[:9], 8, "softmax", True)

@@ -366,6 +366,10 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
       read_frags(cW, cX, 1, 1);
       read_scales(cS);
       interleave<0, NM, NR + (BLK ? MJ + NI : 0), 0>();
+      // every MFMA of k-step 0 is issued before the wait (the wait has no
+      // data dependence on them, so the scheduler would otherwise hoist it
+      // above half of them and cut the copies' latency slack)
+      __builtin_amdgcn_sched_barrier(0);
       wait_copies_upto<(AHEAD - 2) * CPS>();  // stage s+1 has landed
       stage_barrier();
       copy_stage(cW, cX, cS, min(s + AHEAD, KS - 1));

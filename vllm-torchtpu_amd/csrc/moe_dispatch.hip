@@ -15,14 +15,14 @@
 // multiplied each row by its routing weight and scattered it to its flat
 // route slot, so out[t] = sum of the token's valid slots.
 
-#include "qmoe_common.h"
+#include "moe_common.h"
 
 namespace {
 
 constexpr int kDT = 1024;
 constexpr int kWaves = kDT / 64;
-constexpr int kMaxE = 512;
-constexpr int kMaxB = kMaxE + 1;  // + the "invalid" bucket
+using qmoe_moe::kMaxB;
+using qmoe_moe::kMaxE;
 
 __device__ __forceinline__ int block_excl_scan(int v, int* tmp, int& total) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -127,84 +127,18 @@ __global__ __launch_bounds__(kDT) void dispatch_kernel(
   }
 }
 
-// Decode form (T*k <= 64): one wavefront, route f in lane f (its barriers
-// are single-wave, they only order the lanes' LDS accesses for the
-// compiler). Bucket counts by LDS atomics; lane l owns buckets 9l..9l+8, whose exclusive prefix gives the
-// group offsets and the active list; a route's rank is its bucket's offset
-// plus the routes of the same bucket in lower lanes (ballot match), i.e. the
-// stable order. Same outputs as dispatch_kernel.
-__device__ __forceinline__ int wave_excl_scan(int v, int lane, int& total) {
-  int x = v;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int y = __shfl_up(x, o, 64);
-    if (lane >= o) x += y;
-  }
-  total = __shfl(x, 63, 64);
-  return x - v;
-}
-
+// Decode form (T*k <= 64): one wavefront, route f in lane f; see
+// qmoe_moe::dispatch_wave. Same outputs as dispatch_kernel.
 __global__ __launch_bounds__(64) void dispatch_small_kernel(
     const int32_t* __restrict__ ids, const uint16_t* __restrict__ wts, int Nf, int topk, int E,
     int skip_padded, int32_t* __restrict__ sorted_idx, int32_t* __restrict__ revert,
     int32_t* __restrict__ token_sorted, int32_t* __restrict__ group_offs,
     int32_t* __restrict__ active, int32_t* __restrict__ num_active,
     uint16_t* __restrict__ sorted_weight) {
-  constexpr int kPer = (kMaxB + 63) / 64;  // buckets per lane
-  __shared__ int cnt[64 * kPer];
-  __shared__ int offs[64 * kPer];
-  const int lane = threadIdx.x;
-  const bool in = lane < Nf;
-  int b = 0;
-  uint16_t w = 0;
-  if (in) {
-    const int id = ids[lane];
-    w = wts[lane];
-    bool ok = id >= 0 && id < E;
-    if (skip_padded && ok) ok = (w & 0x7fffu) != 0;
-    b = ok ? id : E;
-  }
-#pragma unroll
-  for (int j = 0; j < kPer; ++j) cnt[lane * kPer + j] = 0;
-  __syncthreads();
-  if (in) atomicAdd(&cnt[b], 1);
-  __syncthreads();
-  int c[kPer], pre[kPer], t = 0, fa = 0;
-#pragma unroll
-  for (int j = 0; j < kPer; ++j) {
-    c[j] = cnt[lane * kPer + j];
-    pre[j] = t;
-    t += c[j];
-    fa += (lane * kPer + j < E && c[j] > 0) ? 1 : 0;
-  }
-  int total = 0, nact = 0;
-  const int base = wave_excl_scan(t, lane, total);
-  int apos = wave_excl_scan(fa, lane, nact);
-#pragma unroll
-  for (int j = 0; j < kPer; ++j) {
-    const int e = lane * kPer + j;
-    offs[e] = base + pre[j];
-    if (e <= E) group_offs[e] = base + pre[j];  // group_offs[E] = valid routes
-    if (e < E && c[j] > 0) active[apos++] = e;
-  }
-  if (lane == 0) *num_active = nact;
-  __syncthreads();
-  // routes of the same bucket in lower lanes (10 ballots resolve a bucket id)
-  uint64_t m = __ballot(in);
-#pragma unroll
-  for (int bit = 0; bit < 10; ++bit) {
-    const bool s = (b >> bit) & 1;
-    const uint64_t bal = __ballot(s);
-    m &= s ? bal : ~bal;
-  }
-  const uint64_t lower = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-  if (in) {
-    const int rank = offs[b] + __popcll(m & lower);
-    sorted_idx[rank] = lane;
-    revert[lane] = rank;
-    token_sorted[rank] = lane / topk;
-    sorted_weight[rank] = w;
-  }
+  __shared__ int cnt[64 * qmoe_moe::kPer];
+  __shared__ int offs[64 * qmoe_moe::kPer];
+  qmoe_moe::dispatch_wave(ids, wts, Nf, topk, E, skip_padded, sorted_idx, revert, token_sorted, group_offs,
+                          active, num_active, sorted_weight, cnt, offs);
 }
 
 __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict__ rows,

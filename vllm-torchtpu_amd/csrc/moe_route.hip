@@ -16,7 +16,7 @@
 // mostly instruction fetch, and each instantiation carries only the code of
 // its own rule.
 
-#include "qmoe_common.h"
+#include "moe_common.h"
 
 namespace {
 
@@ -47,12 +47,7 @@ __device__ __forceinline__ void top2_merge(float& m1, float& m2, float o1, float
   m2 = lo;
 }
 
-// Make this wavefront's LDS writes visible to its own later LDS reads.
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-}
+using qmoe_moe::wave_lds_sync;
 
 // Cross-lane reductions without LDS round trips: DPP moves inside each
 // 16-lane row (xor-1 and xor-2 inside quads, then the half-row and row
@@ -136,17 +131,17 @@ __device__ __forceinline__ void rowmax_pass(const float (&cur)[kMaxSlots], int l
   mi = idx;
 }
 
+// Routes token t with the calling wavefront (all 64 lanes). `ch` is this
+// wavefront's LDS scratch (kMaxSlots * 64 floats, grouped selection with
+// groups that are not a power of two <= 64). When lds_ids is given, the
+// token's ids and bf16 weights also go to lds_ids / lds_w [t * topk + j].
 template <int S, int SCORING, bool GROUPED>
-__global__ __launch_bounds__(256) void route_kernel(const void* __restrict__ logits, int logits_f32,
-                                                    int64_t T, int E, int topk,
-                                                    const float* __restrict__ bias, int renormalize,
-                                                    float rsf, int num_group, int topk_group,
-                                                    void* __restrict__ out_w, int w_f32,
-                                                    int32_t* __restrict__ out_ids) {
+__device__ __forceinline__ void route_token(const void* __restrict__ logits, int logits_f32, int64_t t, int E,
+                                            int topk, const float* __restrict__ bias, int renormalize, float rsf,
+                                            int num_group, int topk_group, void* __restrict__ out_w, int w_f32,
+                                            int32_t* __restrict__ out_ids, float* ch, int32_t* lds_ids,
+                                            uint16_t* lds_w) {
   const int lane = threadIdx.x & 63;
-  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  __shared__ float choice_lds[GROUPED ? 4 : 1][GROUPED ? kMaxSlots * 64 : 1];
-  if (t >= T) return;
 
   float x[kMaxSlots];
 #pragma unroll
@@ -223,7 +218,6 @@ __global__ __launch_bounds__(256) void route_kernel(const void* __restrict__ log
       }
       if (lane < num_group) gs = v;
     } else {
-      float* ch = choice_lds[threadIdx.x >> 6];
 #pragma unroll
       for (int j = 0; j < S; ++j)
         if (j * 64 + lane < E) ch[j * 64 + lane] = cur[j];
@@ -289,36 +283,98 @@ __global__ __launch_bounds__(256) void route_kernel(const void* __restrict__ log
     float v = myw;
     if (renormalize) v = v / (sum != sum ? sum : fmaxf(sum, 1e-20f));
     if (rsf != 1.0f) v = v * rsf;
-    if (w_f32) static_cast<float*>(out_w)[t * topk + lane] = v;
-    else static_cast<uint16_t*>(out_w)[t * topk + lane] = f32_to_bf16(v);
+    if (w_f32) {
+      static_cast<float*>(out_w)[t * topk + lane] = v;
+    } else {
+      const uint16_t b = f32_to_bf16(v);
+      static_cast<uint16_t*>(out_w)[t * topk + lane] = b;
+      if (lds_w) lds_w[t * topk + lane] = b;
+    }
+    if (lds_ids) lds_ids[t * topk + lane] = myid;
   }
 }
 
-template <int S, int SCORING, bool GROUPED, typename... A>
-void launch_route3(dim3 grid, hipStream_t st, A... a) {
-  hipLaunchKernelGGL((route_kernel<S, SCORING, GROUPED>), grid, dim3(256), 0, st, a...);
+template <int S, int SCORING, bool GROUPED>
+__global__ __launch_bounds__(256) void route_kernel(const void* __restrict__ logits, int logits_f32,
+                                                    int64_t T, int E, int topk,
+                                                    const float* __restrict__ bias, int renormalize,
+                                                    float rsf, int num_group, int topk_group,
+                                                    void* __restrict__ out_w, int w_f32,
+                                                    int32_t* __restrict__ out_ids) {
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  __shared__ float choice_lds[GROUPED ? 4 : 1][GROUPED ? kMaxSlots * 64 : 1];
+  if (t >= T) return;
+  route_token<S, SCORING, GROUPED>(logits, logits_f32, t, E, topk, bias, renormalize, rsf, num_group, topk_group,
+                                   out_w, w_f32, out_ids, choice_lds[GROUPED ? threadIdx.x >> 6 : 0], nullptr,
+                                   nullptr);
 }
 
-template <int S, typename... A>
+// Decode form of routing + dispatch in one launch (T <= 16 tokens, T * topk
+// <= 64 routes): one workgroup, wavefront t routes token t (ids and bf16
+// weights to global and to LDS), then wavefront 0 runs the single-wavefront
+// dispatch on the routes in LDS.
+template <int S, int SCORING, bool GROUPED>
+__global__ __launch_bounds__(1024) void route_dispatch_kernel(
+    const void* __restrict__ logits, int logits_f32, int T, int E, int topk, const float* __restrict__ bias,
+    int renormalize, float rsf, int num_group, int topk_group, uint16_t* __restrict__ out_w,
+    int32_t* __restrict__ out_ids, int skip_padded, int32_t* __restrict__ sorted_idx, int32_t* __restrict__ revert,
+    int32_t* __restrict__ token_sorted, int32_t* __restrict__ group_offs, int32_t* __restrict__ active,
+    int32_t* __restrict__ num_active, uint16_t* __restrict__ sorted_weight) {
+  __shared__ float choice_lds[GROUPED ? 16 : 1][GROUPED ? kMaxSlots * 64 : 1];
+  __shared__ int32_t s_ids[64];
+  __shared__ uint16_t s_w[64];
+  __shared__ int cnt[64 * qmoe_moe::kPer];
+  __shared__ int offs[64 * qmoe_moe::kPer];
+  const int wave = threadIdx.x >> 6;
+  route_token<S, SCORING, GROUPED>(logits, logits_f32, wave, E, topk, bias, renormalize, rsf, num_group, topk_group,
+                                   out_w, 0, out_ids, choice_lds[GROUPED ? wave : 0], s_ids, s_w);
+  __syncthreads();
+  if (wave == 0)
+    qmoe_moe::dispatch_wave(s_ids, s_w, T * topk, topk, E, skip_padded, sorted_idx, revert, token_sorted,
+                            group_offs, active, num_active, sorted_weight, cnt, offs);
+}
+
+// FUSED: the route + dispatch kernel, one workgroup of 64 * grid.x threads
+template <int S, int SCORING, bool GROUPED, bool FUSED = false, typename... A>
+void launch_route3(dim3 grid, hipStream_t st, A... a) {
+  if constexpr (FUSED)
+    hipLaunchKernelGGL((route_dispatch_kernel<S, SCORING, GROUPED>), dim3(1), dim3(64 * grid.x), 0, st, a...);
+  else
+    hipLaunchKernelGGL((route_kernel<S, SCORING, GROUPED>), grid, dim3(256), 0, st, a...);
+}
+
+template <int S, bool FUSED, typename... A>
 void launch_route2(int scoring, bool grouped, dim3 grid, hipStream_t st, A... a) {
   switch (scoring * 2 + (grouped ? 1 : 0)) {
-    case 0: launch_route3<S, 0, false>(grid, st, a...); break;
-    case 1: launch_route3<S, 0, true>(grid, st, a...); break;
-    case 2: launch_route3<S, 1, false>(grid, st, a...); break;
-    case 3: launch_route3<S, 1, true>(grid, st, a...); break;
-    case 4: launch_route3<S, 2, false>(grid, st, a...); break;
-    case 5: launch_route3<S, 2, true>(grid, st, a...); break;
-    case 6: launch_route3<S, 3, false>(grid, st, a...); break;
-    default: launch_route3<S, 3, true>(grid, st, a...); break;
+    case 0: launch_route3<S, 0, false, FUSED>(grid, st, a...); break;
+    case 1: launch_route3<S, 0, true, FUSED>(grid, st, a...); break;
+    case 2: launch_route3<S, 1, false, FUSED>(grid, st, a...); break;
+    case 3: launch_route3<S, 1, true, FUSED>(grid, st, a...); break;
+    case 4: launch_route3<S, 2, false, FUSED>(grid, st, a...); break;
+    case 5: launch_route3<S, 2, true, FUSED>(grid, st, a...); break;
+    case 6: launch_route3<S, 3, false, FUSED>(grid, st, a...); break;
+    default: launch_route3<S, 3, true, FUSED>(grid, st, a...); break;
   }
 }
 
-template <typename... A>
+template <bool FUSED = false, typename... A>
 void launch_route(int S, int scoring, bool grouped, dim3 grid, hipStream_t st, A... a) {
-  if (S == 1) launch_route2<1>(scoring, grouped, grid, st, a...);
-  else if (S == 2) launch_route2<2>(scoring, grouped, grid, st, a...);
-  else if (S == 4) launch_route2<4>(scoring, grouped, grid, st, a...);
-  else launch_route2<8>(scoring, grouped, grid, st, a...);
+  if (S == 1) launch_route2<1, FUSED>(scoring, grouped, grid, st, a...);
+  else if (S == 2) launch_route2<2, FUSED>(scoring, grouped, grid, st, a...);
+  else if (S == 4) launch_route2<4, FUSED>(scoring, grouped, grid, st, a...);
+  else launch_route2<8, FUSED>(scoring, grouped, grid, st, a...);
+}
+
+// argument checks shared by both entry points
+int route_args_ok(int64_t T, int E, int topk, int scoring, int num_group, int topk_group) {
+  if (T < 0 || E <= 0 || E > kMaxSlots * 64 || topk <= 0 || topk > E || topk > 64) return 0;
+  if (scoring < 0 || scoring > 3) return 0;
+  const bool grouped = num_group > 1 && topk_group < num_group;
+  if (grouped) {
+    if (E % num_group != 0 || num_group > 64 || topk_group <= 0) return 0;
+    if (topk > topk_group * (E / num_group)) return 0;
+  }
+  return 1;
 }
 
 }  // namespace
@@ -328,17 +384,30 @@ extern "C" int qmoe_moe_route(const void* logits, int logits_f32, int64_t T, int
                               float routed_scaling_factor, int num_group, int topk_group,
                               void* topk_weights, int weights_f32, int32_t* topk_ids,
                               hipStream_t stream) {
-  if (T < 0 || E <= 0 || E > kMaxSlots * 64 || topk <= 0 || topk > E || topk > 64) return QMOE_ERR_ARG;
-  if (scoring < 0 || scoring > 3) return QMOE_ERR_ARG;
+  if (!route_args_ok(T, E, topk, scoring, num_group, topk_group)) return QMOE_ERR_ARG;
   const bool grouped = num_group > 1 && topk_group < num_group;
-  if (grouped) {
-    if (E % num_group != 0 || num_group > 64 || topk_group <= 0) return QMOE_ERR_ARG;
-    if (topk > topk_group * (E / num_group)) return QMOE_ERR_ARG;
-  }
   if (T == 0) return QMOE_OK;
   const int S = (E + 63) / 64;
   launch_route(S <= 1 ? 1 : (S <= 2 ? 2 : (S <= 4 ? 4 : 8)), scoring, grouped, dim3((unsigned)((T + 3) / 4)),
                stream, logits, logits_f32, T, E, topk, bias, renormalize, routed_scaling_factor, num_group,
                topk_group, topk_weights, weights_f32, topk_ids);
+  return hipGetLastError() == hipSuccess ? QMOE_OK : QMOE_ERR_LAUNCH;
+}
+
+// See include/qmoe.h for the contract.
+extern "C" int qmoe_moe_route_dispatch(const void* logits, int logits_f32, int64_t T, int E, int topk, int scoring,
+                                       const float* bias, int renormalize, float routed_scaling_factor,
+                                       int num_group, int topk_group, uint16_t* topk_weights, int32_t* topk_ids,
+                                       int skip_padded, int32_t* sorted_idx, int32_t* revert,
+                                       int32_t* token_sorted, int32_t* group_offs, int32_t* active,
+                                       int32_t* num_active, uint16_t* sorted_weight, hipStream_t stream) {
+  if (!route_args_ok(T, E, topk, scoring, num_group, topk_group)) return QMOE_ERR_ARG;
+  if (T < 1 || T > 16 || T * topk > 64 || E > qmoe_moe::kMaxE) return QMOE_ERR_ARG;
+  const bool grouped = num_group > 1 && topk_group < num_group;
+  const int S = (E + 63) / 64;
+  launch_route<true>(S <= 1 ? 1 : (S <= 2 ? 2 : (S <= 4 ? 4 : 8)), scoring, grouped, dim3((unsigned)T), stream,
+                     logits, logits_f32, (int)T, E, topk, bias, renormalize, routed_scaling_factor, num_group,
+                     topk_group, topk_weights, topk_ids, skip_padded, sorted_idx, revert, token_sorted,
+                     group_offs, active, num_active, sorted_weight);
   return hipGetLastError() == hipSuccess ? QMOE_OK : QMOE_ERR_LAUNCH;
 }

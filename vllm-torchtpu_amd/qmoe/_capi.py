@@ -89,6 +89,10 @@ def _load():
     lib.qmoe_moe_dispatch.restype = ctypes.c_int
     lib.qmoe_moe_dispatch.argtypes = [_vp, _vp, _i64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                       _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]
+    lib.qmoe_moe_route_dispatch.restype = ctypes.c_int
+    lib.qmoe_moe_route_dispatch.argtypes = [_vp, ctypes.c_int, _i64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                            _vp, ctypes.c_int, _f32, ctypes.c_int, ctypes.c_int, _vp, _vp,
+                                            ctypes.c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]
     lib.qmoe_moe_combine.restype = ctypes.c_int
     lib.qmoe_moe_combine.argtypes = [_vp, _vp, _vp, _i64, ctypes.c_int, _i64, ctypes.c_int, _vp,
                                      _i64, _vp]
@@ -107,6 +111,7 @@ EXPORTED = (
     "qmoe_gemm",
     "qmoe_moe_route",
     "qmoe_moe_dispatch",
+    "qmoe_moe_route_dispatch",
     "qmoe_moe_combine",
 )
 

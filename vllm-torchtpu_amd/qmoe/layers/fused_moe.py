@@ -83,12 +83,67 @@ def _fused_moe_gmm_op(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, w1_sc
                       w2_bias: Optional[torch.Tensor], tw: torch.Tensor, topk_ids: torch.Tensor, topk: int,
                       activation: str, skip: bool, fmt: str) -> torch.Tensor:
     """Checked operands: x bf16 [T, H]; tw bf16 / topk_ids int32 [T, topk]."""
+    tw = tw.contiguous()
+    meta = ops.moe_dispatch(topk_ids, tw, w1.shape[0], skip)
+    return _moe_body(x, w1, w2, w1_scale, w2_scale, w1_bias, w2_bias, tw, topk_ids, topk, activation, skip, fmt,
+                     meta)
+
+
+@torch.library.custom_op("qmoe::routed_moe", mutates_args=())
+def _routed_moe_op(x: torch.Tensor, router_logits: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor,
+                   w1_scale: Optional[torch.Tensor], w2_scale: Optional[torch.Tensor],
+                   w1_bias: Optional[torch.Tensor], w2_bias: Optional[torch.Tensor], topk: int, scoring_func: str,
+                   renormalize: bool, e_bias: Optional[torch.Tensor], routed_scaling_factor: float,
+                   num_expert_group: int, topk_group: int, activation: str, skip: bool,
+                   fmt: str) -> torch.Tensor:
+    """Decode-size layer (1..16 tokens, at most 64 routes): routing and
+    dispatch in one launch (`qmoe_moe_route_dispatch`), then the experts."""
+    tw, ids, meta = ops.moe_route_dispatch(router_logits, topk, scoring_func, renormalize, e_bias,
+                                           routed_scaling_factor, num_expert_group, topk_group, skip)
+    return _moe_body(x, w1, w2, w1_scale, w2_scale, w1_bias, w2_bias, tw, ids, topk, activation, skip, fmt, meta)
+
+
+@_routed_moe_op.register_fake
+def _(x, router_logits, w1, w2, w1_scale, w2_scale, w1_bias, w2_bias, topk, scoring_func, renormalize, e_bias,
+      routed_scaling_factor, num_expert_group, topk_group, activation, skip, fmt):
+    return x.new_empty(x.shape, dtype=torch.bfloat16)
+
+
+def moe_forward(layer, x, router_logits, w1, w2, w1_scale, w2_scale, w1_bias, w2_bias, weight_format,
+                skip_padded_tokens=None, input_ids=None):
+    """Routing + routed experts of a MoE method's `apply_monolithic`
+    (`layers/adapter/quantization/fp8.py:1108-1222`: route, then
+    `fused_moe_gmm`). A decode-size batch (1..16 bf16 tokens, at most 64
+    routes) with the layer's own scoring takes the fused route + dispatch
+    launch; anything else (a model-supplied routing function, hash routing,
+    larger batches) routes first and calls `fused_moe_gmm`."""
+    from qmoe.layers import moe_routing
+
+    topk = layer.moe_config.experts_per_token
+    T = x.shape[0]
+    custom = getattr(layer, "custom_routing_function", None)
+    hashed = getattr(layer, "hash_indices_table", None) is not None and input_ids is not None
+    act = layer._qmoe_activation
+    fusable = (custom is None and not hashed and x.dtype == torch.bfloat16
+               and 1 <= T <= ops.ROUTE_DISPATCH_MAX_TOKENS and T * topk <= ops.ROUTE_DISPATCH_MAX_ROUTES
+               and w1.shape[0] <= 512 and layer.scoring_func in ops._SCORING)
+    if not fusable:
+        topk_weights, topk_ids = moe_routing.route(layer, x, router_logits, input_ids=input_ids)
+        return fused_moe_gmm(x, w1, w2, w1_scale, w2_scale, w1_bias, w2_bias, topk_weights, topk_ids, None, topk,
+                             act, skip_padded_tokens=skip_padded_tokens, weight_format=weight_format)
+    ops.act_code(act)
+    bias, rsf, ng, tg = moe_routing.routing_params(layer)
+    return torch.ops.qmoe.routed_moe(x, router_logits, w1, w2, w1_scale, w2_scale, w1_bias, w2_bias, int(topk),
+                                     layer.scoring_func, bool(layer.renormalize), bias, float(rsf), int(ng),
+                                     int(tg), act or "", bool(skip_padded_tokens), weight_format)
+
+
+def _moe_body(x, w1, w2, w1_scale, w2_scale, w1_bias, w2_bias, tw, topk_ids, topk, activation, skip, fmt, meta):
+    """The experts of a routed layer, given the dispatch metadata."""
     activation = activation or None
     T, H = x.shape
     E = w1.shape[0]
     x = x.contiguous()
-    tw = tw.contiguous()
-    meta = ops.moe_dispatch(topk_ids, tw, E, skip)
     M = T * topk
     common = dict(group_offs=meta["group_offs"], active=meta["active"],
                   num_active=meta["num_active"], slots=E, max_rows=T, M=M)

@@ -57,6 +57,20 @@ def rowmax_select(scores: torch.Tensor, topk: int):
     return w.reshape(*scores.shape[:-1], topk), ids.reshape(*scores.shape[:-1], topk)
 
 
+def routing_params(layer):
+    """The layer's routing settings as `select_experts` reads them: (bias,
+    routed_scaling_factor, num_expert_group, topk_group); grouped selection
+    only when `use_grouped_topk` with num_expert_group > 1 and topk_group <
+    num_expert_group (`moe_routing.py:276-299`)."""
+    bias = getattr(layer, "e_score_correction_bias", None) if layer is not None else None
+    rsf = getattr(layer, "routed_scaling_factor", 1.0) if layer is not None else 1.0
+    ng, tg = 1, 1
+    if (layer is not None and getattr(layer, "use_grouped_topk", False)
+            and layer.num_expert_group > 1 and layer.topk_group < layer.num_expert_group):
+        ng, tg = layer.num_expert_group, layer.topk_group
+    return bias, (rsf if rsf is not None else 1.0), ng, tg
+
+
 def select_experts(hidden_states, router_logits, *, topk, renormalize, scoring_fn, layer=None,
                    input_ids=None):
     """(topk_weights in the hidden dtype, topk_ids int32), `moe_routing.py:232-323`.
@@ -67,15 +81,9 @@ def select_experts(hidden_states, router_logits, *, topk, renormalize, scoring_f
     """
     if layer is not None and getattr(layer, "hash_indices_table", None) is not None and input_ids is not None:
         raise NotImplementedError("hash routing (DeepSeek-V4) is outside this build's scope")
-    bias = getattr(layer, "e_score_correction_bias", None) if layer is not None else None
-    rsf = getattr(layer, "routed_scaling_factor", 1.0) if layer is not None else 1.0
-    ng, tg = 1, 1
-    if (layer is not None and getattr(layer, "use_grouped_topk", False)
-            and layer.num_expert_group > 1 and layer.topk_group < layer.num_expert_group):
-        ng, tg = layer.num_expert_group, layer.topk_group
-    w, ids = _route(router_logits, topk, scoring_fn, renormalize, bias=bias,
-                    routed_scaling_factor=rsf if rsf is not None else 1.0, num_expert_group=ng,
-                    topk_group=tg)
+    bias, rsf, ng, tg = routing_params(layer)
+    w, ids = _route(router_logits, topk, scoring_fn, renormalize, bias=bias, routed_scaling_factor=rsf,
+                    num_expert_group=ng, topk_group=tg)
     return w.to(hidden_states.dtype), ids
 
 

@@ -32,8 +32,7 @@ Requantization runs the library's load-time quantizer kernel
 import torch
 
 from qmoe import envs, ops
-from qmoe.layers import moe_routing
-from qmoe.layers.fused_moe import fused_moe_gmm
+from qmoe.layers.fused_moe import moe_forward
 from qmoe.layers.linear_common import quantized_matmul
 
 FP8 = torch.float8_e4m3fn
@@ -309,26 +308,13 @@ class Fp8MoEMethod:
 
     def apply_monolithic(self, layer, x, router_logits, input_ids=None):
         """`fp8.py:1108-1222` (single-GPU branch): route, then fused MoE."""
-        topk_weights, topk_ids = moe_routing.route(layer, x, router_logits, input_ids=input_ids)
         fmt = layer._qmoe_format
-        if fmt == "fp8_block_rows":
-            # per-(row, 128) scales: the block kernels with one scale row per weight row
-            return _moe_block_rows(layer, x, topk_weights, topk_ids)
-        return fused_moe_gmm(
-            x, layer.w13_weight, layer.w2_weight, layer.w13_weight_scale, layer.w2_weight_scale,
-            None, None, topk_weights, topk_ids, None, layer.moe_config.experts_per_token,
-            layer._qmoe_activation, skip_padded_tokens=envs.TPU_MOE_SKIP_PADDED_TOKENS,
-            weight_format="fp8_block" if fmt == "fp8_block" else "fp8",
-        )
-
-
-def _moe_block_rows(layer, x, topk_weights, topk_ids):
-    return fused_moe_gmm(
-        x, layer.w13_weight, layer.w2_weight, layer.w13_weight_scale, layer.w2_weight_scale,
-        None, None, topk_weights, topk_ids, None, layer.moe_config.experts_per_token,
-        layer._qmoe_activation, skip_padded_tokens=envs.TPU_MOE_SKIP_PADDED_TOKENS,
-        weight_format="fp8_block_rows",
-    )
+        # fp8_block_rows: per-(row, 128) scales, the block kernels with one
+        # scale row per weight row
+        wf = fmt if fmt in ("fp8_block", "fp8_block_rows") else "fp8"
+        return moe_forward(layer, x, router_logits, layer.w13_weight, layer.w2_weight, layer.w13_weight_scale,
+                           layer.w2_weight_scale, None, None, wf,
+                           skip_padded_tokens=envs.TPU_MOE_SKIP_PADDED_TOKENS, input_ids=input_ids)
 
 
 def _activation(layer):

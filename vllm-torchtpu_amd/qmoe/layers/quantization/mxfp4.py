@@ -26,8 +26,7 @@ checkpoint weights are MXFP4.
 import torch
 
 from qmoe import envs
-from qmoe.layers import moe_routing
-from qmoe.layers.fused_moe import fused_moe_gmm
+from qmoe.layers.fused_moe import moe_forward
 from qmoe.layers.linear_common import quantized_matmul_fp4
 from qmoe.layers.quantization.fp8 import _activation, _device, _param
 
@@ -131,10 +130,6 @@ class Mxfp4MoEMethod:
 
     def apply_monolithic(self, layer, x, router_logits, input_ids=None):
         """`mxfp4.py:322-364`: route, then the fused MoE on MXFP4 experts."""
-        topk_weights, topk_ids = moe_routing.route(layer, x, router_logits, input_ids=input_ids)
-        return fused_moe_gmm(
-            x, layer.w13_weight, layer.w2_weight, layer.w13_weight_scale, layer.w2_weight_scale,
-            getattr(layer, "w13_bias", None), getattr(layer, "w2_bias", None), topk_weights, topk_ids,
-            None, layer.moe_config.experts_per_token, layer._qmoe_activation,
-            skip_padded_tokens=envs.TPU_MOE_SKIP_PADDED_TOKENS, weight_format="mxfp4",
-        )
+        return moe_forward(layer, x, router_logits, layer.w13_weight, layer.w2_weight, layer.w13_weight_scale,
+                           layer.w2_weight_scale, getattr(layer, "w13_bias", None), getattr(layer, "w2_bias", None),
+                           "mxfp4", skip_padded_tokens=envs.TPU_MOE_SKIP_PADDED_TOKENS, input_ids=input_ids)

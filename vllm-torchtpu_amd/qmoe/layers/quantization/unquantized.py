@@ -6,8 +6,7 @@ the qmoe grouped GEMM (bf16 MFMA, f32 accumulation)."""
 import torch
 
 from qmoe import _capi, envs, ops
-from qmoe.layers import moe_routing
-from qmoe.layers.fused_moe import fused_moe_gmm
+from qmoe.layers.fused_moe import moe_forward
 from qmoe.layers.quantization.fp8 import _activation, _device, _param
 
 
@@ -65,10 +64,6 @@ class UnquantizedFusedMoEMethod:
         layer._qmoe_processed = True
 
     def apply_monolithic(self, layer, x, router_logits, input_ids=None):
-        topk_weights, topk_ids = moe_routing.route(layer, x, router_logits, input_ids=input_ids)
-        return fused_moe_gmm(
-            x, layer.w13_weight, layer.w2_weight, None, None, getattr(layer, "w13_bias", None),
-            getattr(layer, "w2_bias", None), topk_weights, topk_ids, None,
-            layer.moe_config.experts_per_token, layer._qmoe_activation,
-            skip_padded_tokens=envs.TPU_MOE_SKIP_PADDED_TOKENS, weight_format="bf16",
-        )
+        return moe_forward(layer, x, router_logits, layer.w13_weight, layer.w2_weight, None, None,
+                           getattr(layer, "w13_bias", None), getattr(layer, "w2_bias", None), "bf16",
+                           skip_padded_tokens=envs.TPU_MOE_SKIP_PADDED_TOKENS, input_ids=input_ids)

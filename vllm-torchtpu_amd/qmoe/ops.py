@@ -225,16 +225,9 @@ def moe_route(router_logits, topk, scoring_func="softmax", renormalize=True, bia
     return w, ids
 
 
-def moe_dispatch(topk_ids, topk_weights, num_experts, skip_padded_tokens=False):
-    """Permutation metadata (see include/qmoe.h `qmoe_moe_dispatch`)."""
-    _require_gpu(topk_ids, topk_weights)
-    T, k = topk_ids.shape
-    dev = topk_ids.device
-    ids = topk_ids.to(torch.int32).contiguous()
-    wts = topk_weights.to(torch.bfloat16).contiguous()
-    nf = T * k
+def _dispatch_meta(nf, num_experts, dev):
     i32 = dict(dtype=torch.int32, device=dev)
-    meta = dict(
+    return dict(
         sorted_idx=torch.empty(nf, **i32),
         revert=torch.empty(nf, **i32),
         token_sorted=torch.empty(nf, **i32),
@@ -243,6 +236,52 @@ def moe_dispatch(topk_ids, topk_weights, num_experts, skip_padded_tokens=False):
         num_active=torch.empty(1, **i32),
         sorted_weight=torch.empty(nf, dtype=torch.bfloat16, device=dev),
     )
+
+
+ROUTE_DISPATCH_MAX_TOKENS = 16
+ROUTE_DISPATCH_MAX_ROUTES = 64
+
+
+def moe_route_dispatch(router_logits, topk, scoring_func="softmax", renormalize=True, bias=None,
+                       routed_scaling_factor=1.0, num_expert_group=1, topk_group=1, skip_padded_tokens=False):
+    """Routing + dispatch of a decode step in one launch (1 <= T <= 16,
+    T * topk <= 64): (bf16 weights [T, k], int32 ids [T, k], dispatch
+    metadata as returned by `moe_dispatch`)."""
+    _require_gpu(router_logits, bias)
+    if scoring_func not in _SCORING:
+        raise NotImplementedError(f"FusedMoE does not support {scoring_func} scoring function for TPU.")
+    x = router_logits.reshape(-1, router_logits.shape[-1])
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        x = x.float()
+    x = x.contiguous()
+    T, E = x.shape
+    if not (1 <= T <= ROUTE_DISPATCH_MAX_TOKENS and T * topk <= ROUTE_DISPATCH_MAX_ROUTES):
+        raise ValueError(f"route + dispatch takes 1..16 tokens and at most 64 routes, got T={T}, k={topk}")
+    dev = x.device
+    w = torch.empty((T, topk), dtype=torch.bfloat16, device=dev)
+    ids = torch.empty((T, topk), dtype=torch.int32, device=dev)
+    meta = _dispatch_meta(T * topk, E, dev)
+    b = bias.float().contiguous() if bias is not None else None
+    check(lib.qmoe_moe_route_dispatch(_ptr(x), int(x.dtype == torch.float32), T, E, topk, _SCORING[scoring_func],
+                                      _ptr(b), int(bool(renormalize)), float(routed_scaling_factor),
+                                      int(num_expert_group or 1), int(topk_group or 1), _ptr(w), _ptr(ids),
+                                      int(bool(skip_padded_tokens)), _ptr(meta["sorted_idx"]),
+                                      _ptr(meta["revert"]), _ptr(meta["token_sorted"]),
+                                      _ptr(meta["group_offs"]), _ptr(meta["active"]),
+                                      _ptr(meta["num_active"]), _ptr(meta["sorted_weight"]), _stream(dev)),
+          "moe_route_dispatch")
+    return w, ids, meta
+
+
+def moe_dispatch(topk_ids, topk_weights, num_experts, skip_padded_tokens=False):
+    """Permutation metadata (see include/qmoe.h `qmoe_moe_dispatch`)."""
+    _require_gpu(topk_ids, topk_weights)
+    T, k = topk_ids.shape
+    dev = topk_ids.device
+    ids = topk_ids.to(torch.int32).contiguous()
+    wts = topk_weights.to(torch.bfloat16).contiguous()
+    nf = T * k
+    meta = _dispatch_meta(nf, num_experts, dev)
     check(lib.qmoe_moe_dispatch(_ptr(ids), _ptr(wts), T, k, num_experts, int(bool(skip_padded_tokens)),
                                 _ptr(meta["sorted_idx"]), _ptr(meta["revert"]),
                                 _ptr(meta["token_sorted"]), _ptr(meta["group_offs"]),
