@@ -141,6 +141,21 @@ int qmoe_moe_route(const void* logits, int logits_f32, int64_t T, int E, int top
                    qmoe_stream_t stream);
 
 /*
+ * DeepSeek-V4 hash routing, replaces `layers/adapter/moe_routing.py:204-229`
+ * (_hash_moe_select, taken by select_experts when the layer has a
+ * hash_indices_table and input ids are given, `:259-274`): ids =
+ * hash_table[input_ids[t]] (int32 [table_rows, topk]; input ids int32, or
+ * int64 with ids_i64), weights = the row's scores (scoring as in
+ * qmoe_moe_route, no bias) at those ids, renormalized, scaled, as bf16. An
+ * input id outside the table or a table entry outside [0, E) gives id -1
+ * and a NaN weight.
+ */
+int qmoe_moe_route_hash(const void* logits, int logits_f32, int64_t T, int E, int topk, int scoring,
+                        const int32_t* hash_table, int64_t table_rows, const void* input_ids, int ids_i64,
+                        int renormalize, float routed_scaling_factor, uint16_t* topk_weights, int32_t* topk_ids,
+                        qmoe_stream_t stream);
+
+/*
  * Token permutation by expert, replaces `layers/core/fused_moe_gmm.py:288-408`
  * (prepare_routed_gmm_inputs, non-EP): stable order by (expert, flat route
  * index t*k + slot); invalid routes (id < 0, or weight == 0 with

@@ -124,3 +124,16 @@ def grouped_topk(logits, topk, renormalize, num_expert_group, topk_group,
     _, ids = rowmax_topk(cm, topk)
     w = np.take_along_axis(s, ids.astype(np.int64), axis=-1)
     return _finish(w, renormalize, routed_scaling_factor), ids
+
+
+def hash_select(logits, hash_indices_table, input_ids, renormalize, scoring_func="softmax",
+                routed_scaling_factor=1.0):
+    """`moe_routing.py:204-229` (`_hash_moe_select`, DeepSeek-V4 hash
+    routing, taken by `select_experts` when the layer has a
+    `hash_indices_table` and input ids are given, `:259-274`): expert ids are
+    ``table[input_ids]`` and the weights the row's (unbiased) scores at those
+    ids, renormalized and scaled like every other branch."""
+    s = scores_of(logits, scoring_func)
+    ids = np.asarray(hash_indices_table, np.int64)[np.asarray(input_ids, np.int64).reshape(-1)]
+    w = np.take_along_axis(s, ids, axis=-1)
+    return _finish(w, renormalize, routed_scaling_factor), ids.astype(np.int32)

@@ -211,3 +211,36 @@ def test_route_dispatch_rejects_large_batches(dev):
         ops.moe_route_dispatch(logits, 2, "softmax", True)
     with pytest.raises(ValueError):
         ops.moe_route_dispatch(logits[:9], 8, "softmax", True)
+
+
+@pytest.mark.parametrize("scoring,E,k,T,renorm", [("softmax", 4, 2, 2, False), ("sigmoid", 256, 8, 37, True),
+                                                  ("sqrtsoftplus", 384, 6, 5, True)])
+def test_route_hash_table(dev, scoring, E, k, T, renorm):
+    """DeepSeek-V4 hash routing through select_experts: ids bit-exact, weights
+    vs the oracle; the reference known answer for the first case
+    (`tests/layers/adapter/test_moe_routing.py:237-251`)."""
+    from types import SimpleNamespace
+
+    from qmoe.layers.moe_routing import select_experts
+
+    print(f"route hash {scoring} E={E} k={k} T={T}", flush=True)
+    rng = np.random.default_rng(E + T)
+    if E == 4:
+        logits = np.zeros((T, E), np.float32)
+        table = np.array([[0, 1], [2, 3]], np.int32)
+        inp = np.array([1, 0])
+    else:
+        logits = codecs.bf16_round(rng.standard_normal((T, E)).astype(np.float32))
+        table = rng.integers(0, E, (100, k)).astype(np.int32)
+        inp = rng.integers(0, 100, T)
+    layer = SimpleNamespace(hash_indices_table=_t(table, dev), routed_scaling_factor=2.0,
+                            e_score_correction_bias=None, use_grouped_topk=False)
+    h = torch.zeros((T, 8), device=dev, dtype=torch.bfloat16)
+    w, ids = select_experts(h, _t(logits, dev, torch.bfloat16), topk=k, renormalize=renorm, scoring_fn=scoring,
+                            layer=layer, input_ids=_t(inp, dev))
+    w_ref, ids_ref = routing.hash_select(logits, table, inp, renorm, scoring, 2.0)
+    np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
+    np.testing.assert_allclose(w.float().cpu().numpy(), w_ref, rtol=8e-3, atol=1e-6)
+    if E == 4:
+        assert ids.cpu().tolist() == [[2, 3], [0, 1]]
+        np.testing.assert_array_equal(w.float().cpu().numpy(), np.full((2, 2), 0.5, np.float32))

@@ -144,3 +144,27 @@ def test_grouped_with_all_groups_kept_is_plain_biased_topk():
     wp, ip = routing.select_experts(logits, 6, True, "sigmoid", bias)
     np.testing.assert_array_equal(ig, ip)
     np.testing.assert_array_equal(wg, wp)
+
+
+def test_hash_select_known_answer():
+    """`tests/layers/adapter/test_moe_routing.py:237-251`: uniform logits
+    score every one of 4 experts 0.25; ids come from the table rows of the
+    input ids; without renormalization the factor 2.0 alone shapes the
+    weights."""
+    logits = np.zeros((2, 4), np.float32)
+    w, ids = routing.hash_select(logits, [[0, 1], [2, 3]], [1, 0], False, "softmax", 2.0)
+    assert ids.tolist() == [[2, 3], [0, 1]]
+    np.testing.assert_array_equal(w, np.full((2, 2), 0.5, np.float32))
+
+
+def test_hash_select_gathers_unbiased_scores_and_renormalizes():
+    rng = np.random.default_rng(4)
+    logits = rng.standard_normal((5, 16)).astype(np.float32)
+    table = rng.integers(0, 16, (7, 3))
+    inp = np.array([6, 0, 3, 3, 1])
+    w, ids = routing.hash_select(logits, table, inp, True, "sigmoid", 1.5)
+    s = 1.0 / (1.0 + np.exp(-logits.astype(np.float64)))
+    exp_ids = table[inp]
+    g = np.take_along_axis(s, exp_ids, axis=-1)
+    np.testing.assert_array_equal(ids, exp_ids)
+    np.testing.assert_allclose(w, g / g.sum(-1, keepdims=True) * 1.5, rtol=8e-3)

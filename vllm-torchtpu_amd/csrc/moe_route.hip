@@ -131,18 +131,13 @@ __device__ __forceinline__ void rowmax_pass(const float (&cur)[kMaxSlots], int l
   mi = idx;
 }
 
-// Routes token t with the calling wavefront (all 64 lanes). `ch` is this
-// wavefront's LDS scratch (kMaxSlots * 64 floats, grouped selection with
-// groups that are not a power of two <= 64). When lds_ids is given, the
-// token's ids and bf16 weights also go to lds_ids / lds_w [t * topk + j].
-template <int S, int SCORING, bool GROUPED>
-__device__ __forceinline__ void route_token(const void* __restrict__ logits, int logits_f32, int64_t t, int E,
-                                            int topk, const float* __restrict__ bias, int renormalize, float rsf,
-                                            int num_group, int topk_group, void* __restrict__ out_w, int w_f32,
-                                            int32_t* __restrict__ out_ids, float* ch, int32_t* lds_ids,
-                                            uint16_t* lds_w) {
+// Scores of token t's row, expert e in lane e % 64, slot e / 64 (calling
+// wavefront, all lanes): softmax over the row or the elementwise rule, in
+// float64 rounded once to float32.
+template <int S, int SCORING>
+__device__ __forceinline__ void row_scores(const void* __restrict__ logits, int logits_f32, int64_t t, int E,
+                                           float (&s)[kMaxSlots]) {
   const int lane = threadIdx.x & 63;
-
   float x[kMaxSlots];
 #pragma unroll
   for (int j = 0; j < S; ++j) {
@@ -154,7 +149,6 @@ __device__ __forceinline__ void route_token(const void* __restrict__ logits, int
     }
     x[j] = v;
   }
-  float s[kMaxSlots];
   if constexpr (SCORING == 0) {  // softmax in float64
     float mx = -__builtin_inff();
     bool nan = false;
@@ -180,6 +174,23 @@ __device__ __forceinline__ void route_token(const void* __restrict__ logits, int
 #pragma unroll
     for (int j = 0; j < S; ++j) s[j] = score_of<SCORING>(x[j]);
   }
+
+}
+
+// Routes token t with the calling wavefront (all 64 lanes). `ch` is this
+// wavefront's LDS scratch (kMaxSlots * 64 floats, grouped selection with
+// groups that are not a power of two <= 64). When lds_ids is given, the
+// token's ids and bf16 weights also go to lds_ids / lds_w [t * topk + j].
+template <int S, int SCORING, bool GROUPED>
+__device__ __forceinline__ void route_token(const void* __restrict__ logits, int logits_f32, int64_t t, int E,
+                                            int topk, const float* __restrict__ bias, int renormalize, float rsf,
+                                            int num_group, int topk_group, void* __restrict__ out_w, int w_f32,
+                                            int32_t* __restrict__ out_ids, float* ch, int32_t* lds_ids,
+                                            uint16_t* lds_w) {
+  const int lane = threadIdx.x & 63;
+
+  float s[kMaxSlots];
+  row_scores<S, SCORING>(logits, logits_f32, t, E, s);
 
   // choice scores
   float c[kMaxSlots];
@@ -365,6 +376,65 @@ void launch_route(int S, int scoring, bool grouped, dim3 grid, hipStream_t st, A
   else launch_route2<8, FUSED>(scoring, grouped, grid, st, a...);
 }
 
+// DeepSeek-V4 hash routing, `layers/adapter/moe_routing.py:204-229`
+// (_hash_moe_select): the ids are the table row of the token's input id,
+// the weights the row's scores at those ids (no bias), renormalized and
+// scaled. One wavefront per token; lane j < topk owns route j.
+template <int S, int SCORING>
+__global__ __launch_bounds__(256) void route_hash_kernel(const void* __restrict__ logits, int logits_f32, int64_t T,
+                                                         int E, int topk, const int32_t* __restrict__ table,
+                                                         int64_t table_rows, const void* __restrict__ input_ids,
+                                                         int ids_i64,
+                                                         int renormalize, float rsf, uint16_t* __restrict__ out_w,
+                                                         int32_t* __restrict__ out_ids) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  float s[kMaxSlots];
+  row_scores<S, SCORING>(logits, logits_f32, t, E, s);
+  // an input id outside the table, or a table entry outside [0, E), gives
+  // the invalid route id -1 with a NaN weight (the dispatch sorts it last)
+  int id = 0;
+  bool ok = false;
+  if (lane < topk) {
+    const int64_t row = ids_i64 ? static_cast<const int64_t*>(input_ids)[t] : static_cast<const int32_t*>(input_ids)[t];
+    if (row >= 0 && row < table_rows) {
+      id = table[row * topk + lane];
+      ok = id >= 0 && id < E;
+    }
+  }
+  const int idc = ok ? id : 0;
+  float w = 0.0f;
+#pragma unroll
+  for (int j = 0; j < S; ++j) {
+    const float v = __shfl(s[j], idc & 63, 64);
+    if ((idc >> 6) == j) w = v;
+  }
+  if (!ok) w = __builtin_nanf("");
+  const float sum = wave_sum_u(lane < topk ? w : 0.0f);
+  if (lane < topk) {
+    float v = w;
+    if (renormalize) v = v / (sum != sum ? sum : fmaxf(sum, 1e-20f));
+    if (rsf != 1.0f) v = v * rsf;
+    out_w[t * topk + lane] = f32_to_bf16(v);
+    out_ids[t * topk + lane] = ok ? id : -1;
+  }
+}
+
+template <int S>
+void launch_hash2(int scoring, dim3 grid, hipStream_t st, const void* logits, int logits_f32, int64_t T, int E,
+                  int topk, const int32_t* table, int64_t table_rows, const void* input_ids, int ids_i64,
+                  int renormalize, float rsf, uint16_t* out_w, int32_t* out_ids) {
+#define QMOE_HASH(SC)                                                                                            \
+  hipLaunchKernelGGL((route_hash_kernel<S, SC>), grid, dim3(256), 0, st, logits, logits_f32, T, E, topk, table, \
+                     table_rows, input_ids, ids_i64, renormalize, rsf, out_w, out_ids)
+  if (scoring == 0) QMOE_HASH(0);
+  else if (scoring == 1) QMOE_HASH(1);
+  else if (scoring == 2) QMOE_HASH(2);
+  else QMOE_HASH(3);
+#undef QMOE_HASH
+}
+
 // argument checks shared by both entry points
 int route_args_ok(int64_t T, int E, int topk, int scoring, int num_group, int topk_group) {
   if (T < 0 || E <= 0 || E > kMaxSlots * 64 || topk <= 0 || topk > E || topk > 64) return 0;
@@ -409,5 +479,27 @@ extern "C" int qmoe_moe_route_dispatch(const void* logits, int logits_f32, int64
                      logits, logits_f32, (int)T, E, topk, bias, renormalize, routed_scaling_factor, num_group,
                      topk_group, topk_weights, topk_ids, skip_padded, sorted_idx, revert, token_sorted,
                      group_offs, active, num_active, sorted_weight);
+  return hipGetLastError() == hipSuccess ? QMOE_OK : QMOE_ERR_LAUNCH;
+}
+
+// See include/qmoe.h for the contract.
+extern "C" int qmoe_moe_route_hash(const void* logits, int logits_f32, int64_t T, int E, int topk, int scoring,
+                                   const int32_t* hash_table, int64_t table_rows, const void* input_ids,
+                                   int ids_i64, int renormalize,
+                                   float routed_scaling_factor, uint16_t* topk_weights, int32_t* topk_ids,
+                                   hipStream_t stream) {
+  if (!route_args_ok(T, E, topk, scoring, 1, 1) || !hash_table || !input_ids) return QMOE_ERR_ARG;
+  if (T == 0) return QMOE_OK;
+  const int S = (E + 63) / 64;
+  const dim3 grid((unsigned)((T + 3) / 4));
+  const int Sp = S <= 1 ? 1 : (S <= 2 ? 2 : (S <= 4 ? 4 : 8));
+#define QMOE_HASH_S(SS)                                                                                        \
+  launch_hash2<SS>(scoring, grid, stream, logits, logits_f32, T, E, topk, hash_table, table_rows, input_ids, \
+                   ids_i64, renormalize, routed_scaling_factor, topk_weights, topk_ids)
+  if (Sp == 1) QMOE_HASH_S(1);
+  else if (Sp == 2) QMOE_HASH_S(2);
+  else if (Sp == 4) QMOE_HASH_S(4);
+  else QMOE_HASH_S(8);
+#undef QMOE_HASH_S
   return hipGetLastError() == hipSuccess ? QMOE_OK : QMOE_ERR_LAUNCH;
 }

@@ -93,6 +93,9 @@ def _load():
     lib.qmoe_moe_route_dispatch.argtypes = [_vp, ctypes.c_int, _i64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                             _vp, ctypes.c_int, _f32, ctypes.c_int, ctypes.c_int, _vp, _vp,
                                             ctypes.c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]
+    lib.qmoe_moe_route_hash.restype = ctypes.c_int
+    lib.qmoe_moe_route_hash.argtypes = [_vp, ctypes.c_int, _i64, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp,
+                                        _i64, _vp, ctypes.c_int, ctypes.c_int, _f32, _vp, _vp, _vp]
     lib.qmoe_moe_combine.restype = ctypes.c_int
     lib.qmoe_moe_combine.argtypes = [_vp, _vp, _vp, _i64, ctypes.c_int, _i64, ctypes.c_int, _vp,
                                      _i64, _vp]
@@ -112,6 +115,7 @@ EXPORTED = (
     "qmoe_moe_route",
     "qmoe_moe_dispatch",
     "qmoe_moe_route_dispatch",
+    "qmoe_moe_route_hash",
     "qmoe_moe_combine",
 )
 

@@ -32,6 +32,19 @@ def _(logits, topk, scoring_func, renormalize, bias, routed_scaling_factor, num_
     return w, logits.new_empty((T, topk), dtype=torch.int32)
 
 
+@torch.library.custom_op("qmoe::moe_route_hash", mutates_args=())
+def _moe_route_hash_op(logits: torch.Tensor, topk: int, table: torch.Tensor, input_ids: torch.Tensor,
+                       scoring_func: str, renormalize: bool,
+                       routed_scaling_factor: float) -> Tuple[torch.Tensor, torch.Tensor]:
+    return ops.moe_route_hash(logits, topk, table, input_ids, scoring_func, renormalize, routed_scaling_factor)
+
+
+@_moe_route_hash_op.register_fake
+def _(logits, topk, table, input_ids, scoring_func, renormalize, routed_scaling_factor):
+    T = logits.numel() // logits.shape[-1]
+    return (logits.new_empty((T, topk), dtype=torch.bfloat16), logits.new_empty((T, topk), dtype=torch.int32))
+
+
 def _route(logits, topk, scoring_func, renormalize, bias=None, routed_scaling_factor=1.0,
            num_expert_group=1, topk_group=1, weights_f32=False):
     """Host-side checks (raised at trace time), then the custom op."""
@@ -79,8 +92,16 @@ def select_experts(hidden_states, router_logits, *, topk, renormalize, scoring_f
     and ``topk_group < num_expert_group``) uses the DeepSeek-V3 rule that the
     reference delegates to upstream vLLM (`:276-299`).
     """
-    if layer is not None and getattr(layer, "hash_indices_table", None) is not None and input_ids is not None:
-        raise NotImplementedError("hash routing (DeepSeek-V4) is outside this build's scope")
+    table = getattr(layer, "hash_indices_table", None) if layer is not None else None
+    if table is not None and input_ids is not None:
+        # DeepSeek-V4 hash routing (`moe_routing.py:259-274`): ids from the
+        # table row of each token's input id, weights from its scores
+        rsf = getattr(layer, "routed_scaling_factor", 1.0)
+        if scoring_fn not in ops._SCORING:
+            raise NotImplementedError(f"FusedMoE does not support {scoring_fn} scoring function for TPU.")
+        w, ids = torch.ops.qmoe.moe_route_hash(router_logits, int(topk), table, input_ids, scoring_fn,
+                                               bool(renormalize), float(rsf if rsf is not None else 1.0))
+        return w.to(hidden_states.dtype), ids
     bias, rsf, ng, tg = routing_params(layer)
     w, ids = _route(router_logits, topk, scoring_fn, renormalize, bias=bias, routed_scaling_factor=rsf,
                     num_expert_group=ng, topk_group=tg)

@@ -273,6 +273,36 @@ def moe_route_dispatch(router_logits, topk, scoring_func="softmax", renormalize=
     return w, ids, meta
 
 
+def moe_route_hash(router_logits, topk, hash_indices_table, input_ids, scoring_func="softmax", renormalize=True,
+                   routed_scaling_factor=1.0):
+    """DeepSeek-V4 hash routing on the GPU: (bf16 weights [T, k], int32 ids
+    [T, k]) with ids = hash_indices_table[input_ids]."""
+    _require_gpu(router_logits, hash_indices_table, input_ids)
+    if scoring_func not in _SCORING:
+        raise NotImplementedError(f"FusedMoE does not support {scoring_func} scoring function for TPU.")
+    x = router_logits.reshape(-1, router_logits.shape[-1])
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        x = x.float()
+    x = x.contiguous()
+    T, E = x.shape
+    table = hash_indices_table.to(torch.int32).contiguous()
+    if table.dim() != 2 or table.shape[1] != topk:
+        raise ValueError(f"hash_indices_table must be [vocab, {topk}], got {tuple(table.shape)}")
+    ids_in = input_ids.reshape(-1)
+    if ids_in.numel() != T:
+        raise ValueError(f"{ids_in.numel()} input ids for {T} tokens")
+    if ids_in.dtype not in (torch.int32, torch.int64):
+        ids_in = ids_in.to(torch.int64)
+    ids_in = ids_in.contiguous()
+    w = torch.empty((T, topk), dtype=torch.bfloat16, device=x.device)
+    ids = torch.empty((T, topk), dtype=torch.int32, device=x.device)
+    check(lib.qmoe_moe_route_hash(_ptr(x), int(x.dtype == torch.float32), T, E, topk, _SCORING[scoring_func],
+                                  _ptr(table), table.shape[0], _ptr(ids_in), int(ids_in.dtype == torch.int64),
+                                  int(bool(renormalize)), float(routed_scaling_factor), _ptr(w), _ptr(ids),
+                                  _stream(x.device)), "moe_route_hash")
+    return w, ids
+
+
 def moe_dispatch(topk_ids, topk_weights, num_experts, skip_padded_tokens=False):
     """Permutation metadata (see include/qmoe.h `qmoe_moe_dispatch`)."""
     _require_gpu(topk_ids, topk_weights)
