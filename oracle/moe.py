@@ -87,9 +87,12 @@ class ExpertWeights:
     fmt:
       "mxfp4": w13 packed u8 [E, 2I, H/2] + e8m0 [E, 2I, H/32]; w2 [E, H, I/2] + [E, H, I/32]
       "fp8_block": w13 e4m3 [E, 2I, H] + tile scale_inv [E, 2I/128, H/128]; w2 likewise
+      "fp8": w13 e4m3 [E, 2I, H] + per-channel scale [E, 2I]; w2 [E, H, I] + [E, H]
       "bf16": w13 [E, 2I, H] f32 (bf16 values); w2 [E, H, I]
     Activations: bf16 for mxfp4/bf16 (W4A16 / W16A16); per-(row, 128) e4m3 for
-    fp8_block (the blockwise W8A8 recipe of config 4).
+    fp8_block (the blockwise W8A8 recipe of config 4); per-row e4m3 for fp8
+    (each expert GEMM is `kernels/quantized_matmul/util.py:80-124`, the
+    per-channel W8A8 recipe, restated in ``linear.w8a8_per_channel``).
     """
 
     def __init__(self, fmt, w13, w13_scale, w2, w2_scale, b13=None, b2=None):
@@ -106,7 +109,7 @@ class ExpertWeights:
                 s = self.s13[e] if which == 13 else self.s2[e]
             if self.fmt == "mxfp4":
                 d = dequant_mxfp4(w, s)
-            elif self.fmt == "fp8_block":
+            elif self.fmt in ("fp8_block", "fp8"):
                 d = e4m3_decode(w)
             else:
                 d = np.asarray(w, np.float32)
@@ -115,7 +118,12 @@ class ExpertWeights:
 
     def linear(self, which, e, x):
         """x bf16-valued [R, K] -> f32 [R, N] for expert e."""
-        if self.fmt != "fp8_block":
+        if self.fmt == "fp8":
+            s = self.s13[e] if which == 13 else self.s2[e]
+            xq, xs = quantize_act(x, "fp8")
+            out = (_mm(e4m3_decode(xq), self.dense(which, e)) * xs[:, None]).astype(np.float32)
+            out = (out * np.asarray(s, np.float32)[None, :]).astype(np.float32)
+        elif self.fmt != "fp8_block":
             out = _mm(x, self.dense(which, e))
         else:
             s = self.s13[e] if which == 13 else self.s2[e]

@@ -164,3 +164,55 @@ def test_mxfp4_moe_interleaved_checkpoint_swigluoai(dev):
     ref, _, _ = omoe.fused_moe(x, omoe.ExpertWeights("mxfp4", dei(c13), dei(s13), c2, s2, dei(b13), b2),
                                tw, ids, "swigluoai")
     assert_close_rows(got.float().cpu().numpy(), ref, "mxfp4 moe method")
+
+
+@pytest.mark.parametrize("interleaved", [False, True])
+def test_fp8_moe_requantized_in_expert_chunks(dev, monkeypatch, interleaved):
+    """Per-expert-scale FP8 checkpoint -> the reference's default per-channel
+    requantization (`fp8.py:486-617`), done on the device a few experts at a
+    time (chunk limit patched down to 3 experts), with swigluoai's
+    interleaved gate/up rows de-interleaved on the way; the layer output
+    matches the oracle on the requantized weights."""
+    from qmoe.layers import quantization as q
+    from qmoe.layers.quantization import fp8 as qfp8
+
+    print(f"fp8 moe chunked requant interleaved={interleaved}", flush=True)
+    rng = np.random.default_rng(13)
+    E, H, I, k, T = 8, 256, 128, 2, 5
+    monkeypatch.setattr(qfp8, "REQUANT_CHUNK_BYTES", 4 * 2 * I * H * 3)
+    act = "swigluoai" if interleaved else "silu"
+    layer = _moe_layer(k, act)
+    method = q.Fp8MoEMethod(q.Fp8Config(), layer.moe_config)
+    method.create_weights(layer, E, H, I, torch.bfloat16)
+    w13f = (rng.standard_normal((E, 2 * I, H)) * 0.02).astype(np.float32)
+    w2f = (rng.standard_normal((E, H, I)) * 0.02).astype(np.float32)
+    s13 = (rng.random((E, 2)) * 1e-3 + 1e-4).astype(np.float32)  # one scale per w1 / w3 shard
+    s2 = (rng.random(E) * 1e-3 + 1e-4).astype(np.float32)
+    c13 = codecs.e4m3_encode(np.clip(w13f / np.repeat(s13, I, axis=1)[:, :, None], -448, 448))
+    c2 = codecs.e4m3_encode(np.clip(w2f / s2[:, None, None], -448, 448))
+    layer.w13_weight.data = _fp8(c13, dev)
+    layer.w2_weight.data = _fp8(c2, dev)
+    layer.w13_weight_scale.data = _t(s13, dev)
+    layer.w2_weight_scale.data = _t(s2, dev)
+    method.process_weights_after_loading(layer)
+    # the oracle requantizes the dequantized checkpoint per channel (load-time quantizer)
+    d13 = codecs.e4m3_decode(c13) * np.repeat(s13, I, axis=1)[:, :, None]
+    if interleaved:
+        d13 = np.concatenate([d13[:, 0::2], d13[:, 1::2]], axis=1)
+    d2 = codecs.e4m3_decode(c2) * s2[:, None, None]
+    r13 = [quant.quantize_tensor(d13[e].astype(np.float32), "fp8") for e in range(E)]
+    r2 = [quant.quantize_tensor(d2[e].astype(np.float32), "fp8") for e in range(E)]
+    np.testing.assert_array_equal(layer.w13_weight.data.view(torch.uint8).cpu().numpy(),
+                                  np.stack([a for a, _ in r13]).view(np.uint8))
+    np.testing.assert_array_equal(layer.w2_weight.data.view(torch.uint8).cpu().numpy(),
+                                  np.stack([a for a, _ in r2]).view(np.uint8))
+    np.testing.assert_array_equal(layer.w13_weight_scale.cpu().numpy(), np.stack([b for _, b in r13]))
+    np.testing.assert_array_equal(layer.w2_weight_scale.cpu().numpy(), np.stack([b for _, b in r2]))
+    x = codecs.bf16_round(rng.standard_normal((T, H)).astype(np.float32))
+    logits = codecs.bf16_round(rng.standard_normal((T, E)).astype(np.float32))
+    got = method.apply_monolithic(layer, _t(x, dev, torch.bfloat16), _t(logits, dev, torch.bfloat16))
+    tw, ids = routing.select_experts(logits, k, True, "softmax")
+    ref, _, _ = omoe.fused_moe(x, omoe.ExpertWeights("fp8", np.stack([a for a, _ in r13]),
+                                                      np.stack([b for _, b in r13]), np.stack([a for a, _ in r2]),
+                                                      np.stack([b for _, b in r2])), tw, ids, act)
+    assert_close_rows(got.float().cpu().numpy(), ref, "fp8 moe chunked requant")

@@ -144,3 +144,24 @@ def test_grouped_layer_matches_per_token_loop():
                 a = codecs.bf16_round(moe.act_fn(gu[:I].astype(np.float32), gu[I:].astype(np.float32), "silu"))
                 want[t] += tw[t, j] * (w2[e].astype(np.float64) @ a)
     np.testing.assert_allclose(got, want, rtol=1e-2, atol=2e-2 * np.abs(want).max())
+
+
+def test_fp8_per_channel_expert_linear_is_the_w8a8_recipe():
+    """The "fp8" expert format's GEMM is the per-channel W8A8 matmul of
+    `kernels/quantized_matmul/util.py:80-124` (pinned by its own known
+    answers): after the bf16 cast the two agree bit for bit, and a
+    transposed scale or a dropped activation scale would not."""
+    from oracle import linear, quant
+
+    rng = np.random.default_rng(2)
+    E, N, K, R = 3, 48, 64, 5
+    w = (rng.standard_normal((E, N, K)) * 0.05).astype(np.float32)
+    q = [quant.quantize_tensor(w[e], "fp8") for e in range(E)]
+    wq, ws = np.stack([a for a, _ in q]), np.stack([b for _, b in q])
+    ew = moe.ExpertWeights("fp8", wq, ws, wq, ws)
+    x = codecs.bf16_round(rng.standard_normal((R, K)).astype(np.float32) * 3)
+    for e in range(E):
+        ref, _, _ = linear.w8a8_per_channel(x, wq[e], ws[e], "fp8")
+        np.testing.assert_array_equal(codecs.bf16_round(ew.linear(13, e, x)), ref)
+    assert not np.array_equal(codecs.bf16_round(ew.linear(13, 1, x)),
+                              linear.w8a8_per_channel(x, wq[1], ws[0], "fp8")[0])

@@ -39,6 +39,10 @@ FP8 = torch.float8_e4m3fn
 _REQUANT_DTYPES = {"float8_e4m3fn": FP8, "int8": torch.int8}
 
 
+# f32 bytes of one chunk of experts dequantized at load time
+REQUANT_CHUNK_BYTES = 1 << 30
+
+
 def _device():
     return torch.device("cuda", torch.cuda.current_device())
 
@@ -274,13 +278,24 @@ class Fp8MoEMethod:
             layer.w2_weight_scale = _param(layer.w2_weight_scale_inv.data.to(dev, torch.float32).contiguous())
             layer._qmoe_format = "fp8_block"
         else:
-            w13f = self._dequant_experts(layer, "w13", w13)
-            w2f = self._dequant_experts(layer, "w2", w2)
-            if interleaved:  # `fp8.py:364-367`: [g0, u0, g1, u1, ...] -> [g | u]
-                w13f = torch.cat([w13f[:, 0::2], w13f[:, 1::2]], dim=1)
             block = 128 if (self.block_quant and H % 128 == 0 and I % 128 == 0) else None
-            q13, s13 = requantize(w13f, "float8_e4m3fn", block)
-            q2, s2 = requantize(w2f, "float8_e4m3fn", block)
+            # dequantize -> (de-interleave) -> requantize on the device, a
+            # chunk of experts at a time so the f32 copy stays under ~1 GiB
+            # (the reference's chunked loop, `fp8.py:414-453`)
+            q13 = torch.empty((E, N13, H), dtype=FP8, device=dev)
+            q2 = torch.empty((E, H, I), dtype=FP8, device=dev)
+            s13 = torch.empty((E, N13) if block is None else (E, N13, H // block), dtype=torch.float32, device=dev)
+            s2 = torch.empty((E, H) if block is None else (E, H, I // block), dtype=torch.float32, device=dev)
+            chunk = max(1, REQUANT_CHUNK_BYTES // (4 * N13 * H))
+            for e0 in range(0, E, chunk):
+                e1 = min(E, e0 + chunk)
+                w13f = self._dequant_experts(layer, "w13", w13[e0:e1], e0)
+                if interleaved:  # `fp8.py:364-367`: [g0, u0, g1, u1, ...] -> [g | u]
+                    w13f = torch.cat([w13f[:, 0::2], w13f[:, 1::2]], dim=1)
+                q13[e0:e1], s13[e0:e1] = requantize(w13f, "float8_e4m3fn", block)
+                del w13f
+                q2[e0:e1], s2[e0:e1] = requantize(self._dequant_experts(layer, "w2", w2[e0:e1], e0),
+                                                  "float8_e4m3fn", block)
             layer.w13_weight, layer.w2_weight = _param(q13), _param(q2)
             layer.w13_weight_scale, layer.w2_weight_scale = _param(s13), _param(s2)
             layer._qmoe_format = "fp8_block_rows" if block else "fp8"
@@ -290,15 +305,19 @@ class Fp8MoEMethod:
         layer._qmoe_activation = act
         layer._qmoe_processed = True
 
-    def _dequant_experts(self, layer, which, w):
+    def _dequant_experts(self, layer, which, w, e0=0):
+        """f32 copy of experts [e0, e0 + len(w)) of `which` (w13 / w2)."""
         if w.dtype != FP8:
             return w.to(torch.float32)
+        n = w.shape[0]
         if self.block_quant:
-            s = getattr(layer, f"{which}_weight_scale_inv").data.to(w.device)
+            s = getattr(layer, f"{which}_weight_scale_inv").data[e0:e0 + n].to(w.device)
             return torch.stack([dequantize_fp8_weight(w[e], weight_scale_inv=s[e],
                                                       block=tuple(self.weight_block_size))
-                                for e in range(w.shape[0])])
+                                for e in range(n)])
         s = getattr(layer, f"{which}_weight_scale").data.to(w.device, torch.float32)
+        if s.numel() > 1:
+            s = s[e0:e0 + n]
         if which == "w13" and s.dim() == 2 and s.shape[1] == 2:  # one scale per w1 / w3 shard
             half = w.shape[1] // 2
             s = s.repeat_interleave(half, dim=1)[:, :, None]
