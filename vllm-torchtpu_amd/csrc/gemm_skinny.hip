@@ -11,10 +11,11 @@
 //    W wavefronts, and further across `ksplit` workgroups (grid.y) when
 //    the grid is small;
 //  * a wavefront issues the loads of U steps back to back, unconditionally
-//    (weight rows past N and activation rows past the group are clamped to
-//    valid rows -- they only feed outputs that are never stored), and only
-//    then waits and issues the MFMAs, so U steps of weights are in flight
-//    per wavefront. Only a K tail (K % 128 != 0) uses masked loads;
+//    (weight rows past N are clamped to valid rows, activation rows past the
+//    group read zeros from an out-of-range offset -- both only feed outputs
+//    that are never stored), and only then waits and issues the MFMAs, so U
+//    steps of weights are in flight per wavefront. Only a K tail
+//    (K % 128 != 0) uses masked loads;
 //  * weight loads are coalesced: 4 adjacent lanes read the 4 x 16 B of one
 //    row's 64 B segment (16 rows per load instruction; measured on MI355X,
 //    17% more bandwidth than one row per lane), and ds_bpermute then moves
@@ -90,6 +91,13 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void* base, int64_t bytes) {
   const int n = bytes >= 0x7fffffff ? 0x7fffffff : (int)bytes;
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
 }
+
+// A lane offset with this bit set is past every buffer's extent (the host
+// keeps operands below 2 GiB, and lane offsets below 2 GiB have the bit
+// clear): the load returns zeros and makes no memory request. The bit goes in
+// the per-lane offset, which the range check always covers; the scalar step
+// offset stays a valid one.
+constexpr uint32_t kOob = 0x80000000u;
 
 // cache-policy bits of the weight stream's loads (read once per launch)
 constexpr int kWeightAux = 0;
@@ -410,6 +418,9 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p)
 
   // Rows are taken 16*MS at a time (one pass when the host's row bound
   // holds; more passes re-read this workgroup's weight slice from cache).
+  // Lanes of rows past the group load with kOob set in their offset: zeros,
+  // and no memory request (at M = 1, 15 of the 16 copies of the activation
+  // row a 16-row tile would otherwise read).
   for (int mp = 0; mp < rows; mp += 16 * MS) {
     uint32_t aoff[MS];
     uint32_t soffa[MS][4];  // scale offsets of the 4 accumulator rows (block scales)
@@ -418,13 +429,13 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p)
       const int r = mp + ms * 16 + col;
       const int R = row0 + (r < rows ? r : 0);
       const int ar = p.a_rows ? p.a_rows[R] : R;
-      aoff[ms] = (uint32_t)(ar * lda_b + kg * Tr::kAOffBase);
+      aoff[ms] = r < rows ? (uint32_t)(ar * lda_b + kg * Tr::kAOffBase) : kOob;
       if constexpr (KIND == QK_W8A8_BLK) {
 #pragma unroll
         for (int r4 = 0; r4 < 4; ++r4) {
           const int rr = mp + ms * 16 + kg * 4 + r4;
           const int R2 = row0 + (rr < rows ? rr : 0);
-          soffa[ms][r4] = (uint32_t)((p.a_rows ? p.a_rows[R2] : R2) * p.lds_a * 4);
+          soffa[ms][r4] = rr < rows ? (uint32_t)((p.a_rows ? p.a_rows[R2] : R2) * p.lds_a * 4) : kOob;
         }
       }
     }
@@ -437,13 +448,13 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p)
 
     auto load_scales = [&](int ks, bool live, StepScales<MS, NS>& sc) {
       if constexpr (KIND == QK_W8A8_BLK) {
-        const uint32_t o = live ? (uint32_t)ks * 4 : 0x80000000u;
+        const uint32_t oob = live ? 0u : kOob;
 #pragma unroll
-        for (int s = 0; s < NS; ++s) sc.sb[s] = ldb_f32(sres, soffw[s], o);
+        for (int s = 0; s < NS; ++s) sc.sb[s] = ldb_f32(sres, soffw[s] | oob, (uint32_t)ks * 4);
 #pragma unroll
         for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
-          for (int r4 = 0; r4 < 4; ++r4) sc.sa[ms][r4] = ldb_f32(ares, soffa[ms][r4], o);
+          for (int r4 = 0; r4 < 4; ++r4) sc.sa[ms][r4] = ldb_f32(ares, soffa[ms][r4] | oob, (uint32_t)ks * 4);
       } else if constexpr (KIND == QK_W4A16_MX) {
 #pragma unroll
         for (int s = 0; s < NS; ++s) sc.eb[s] = s_eb[(s * 16 + col) * KB32 + ks * 4 + kg];
@@ -459,21 +470,20 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p)
       Frag fa[U][MS];
       StepScales<MS, NS> sc[U];
     };
-    // steps past the run are issued with an offset past every buffer's
-    // extent: the load instructions still count in vmcnt (so every path
-    // waits alike) but return zeros without a memory request
-    constexpr uint32_t kOob = 0x80000000u;
+    // steps past the run are issued with kOob set in the lane offsets: the
+    // load instructions still count in vmcnt (so every path waits alike) but
+    // return zeros without a memory request
     auto issue_mem = [&](int j, Chunk& c) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const bool live = j + u < nj;
-        const uint32_t kk = (uint32_t)(sbase + j + u);
-        const uint32_t ow = live ? kk * (4 * Tr::kWBytes) : kOob;
-        const uint32_t oa = live ? kk * (4 * Tr::kABytes) : kOob;
+        const uint32_t kk = live ? (uint32_t)(sbase + j + u) : 0u;
+        const uint32_t oob = live ? 0u : kOob;
 #pragma unroll
-        for (int s = 0; s < NS; ++s) ldw_seg<Tr::kWBytes, kWeightAux>(c.bw[u][s], wres, woff[s], ow);
+        for (int s = 0; s < NS; ++s)
+          ldw_seg<Tr::kWBytes, kWeightAux>(c.bw[u][s], wres, woff[s] | oob, kk * (4 * Tr::kWBytes));
 #pragma unroll
-        for (int ms = 0; ms < MS; ++ms) lda_chunks<Tr>(c.fa[u][ms], xres, aoff[ms], oa);
+        for (int ms = 0; ms < MS; ++ms) lda_chunks<Tr>(c.fa[u][ms], xres, aoff[ms] | oob, kk * (4 * Tr::kABytes));
       }
     };
     auto issue_sc = [&](int j, Chunk& c) {
@@ -519,8 +529,7 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p)
       }
     }
     // K tail (t = K % 128 valid k, a multiple of 32): a chunk whose k values
-    // start past K is loaded from the step's first chunk instead (always in
-    // range, so no load leaves the row) and fed as zeros
+    // start past K is loaded with kOob (zeros) and fed as zeros
     if (tail_mine) {
       const int kk = KSF;
       const int t = p.K - KSF * 128;
@@ -532,7 +541,7 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p)
       for (int s = 0; s < NS; ++s) {
 #pragma unroll
         for (int j = 0; j < Tr::kWBytes / 16; ++j) {
-          const uint32_t o = Tr::w_k0(j, lc) < t ? woff[s] + j * 64 : woff[s] - lc * 16;
+          const uint32_t o = Tr::w_k0(j, lc) < t ? woff[s] + j * 64 : kOob;
           const auto v = __builtin_amdgcn_raw_buffer_load_b128(wres, o, (uint32_t)kk * (4 * Tr::kWBytes), 0);
           bw[s].v[j] = make_uint4(v[0], v[1], v[2], v[3]);
         }
@@ -546,7 +555,7 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p)
 #pragma unroll
         for (int i = 0; i < Tr::kABytes / 16; ++i) {
           const bool ok = Tr::a_k0(i, kg) < t;
-          const uint32_t o = ok ? aoff[ms] + Tr::a_off(i) : aoff[ms] - kg * Tr::kAOffBase;
+          const uint32_t o = ok ? aoff[ms] + Tr::a_off(i) : kOob;
           const auto v = __builtin_amdgcn_raw_buffer_load_b128(xres, o, (uint32_t)kk * (4 * Tr::kABytes), 0);
           fa[ms].v[i] = ok ? make_uint4(v[0], v[1], v[2], v[3]) : make_uint4(0, 0, 0, 0);
         }
