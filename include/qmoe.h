@@ -10,7 +10,7 @@
  *   weights      [G][N][K]            N-major: each output channel's K contiguous
  *                                     (e2m1: [G][N][K/2], low nibble = even k)
  *   scales       per-channel f32 [G][N]; block f32 [G][N/bn][K/128];
- *                MX e8m0 bytes [G][N][K/32]
+ *                MX e8m0 bytes [G][N][K/32]; NVFP4 bf16 [G][N][K/16]
  * Reference paths below are relative to the reference plugin's
  * src/vllm_torchtpu/.
  */
@@ -31,7 +31,11 @@ enum {
   QMOE_W8A8_BLK = 1, /* A e4m3 + per-(row,128) scale; W e4m3 + per-(n/bn, 128) scale */
   QMOE_W8A16_PC = 2, /* A bf16; W e4m3 + per-channel scale */
   QMOE_W4A16_MX = 3, /* A bf16; W e2m1 + e8m0 scale per 32 k */
-  QMOE_W16A16 = 4    /* A bf16; W bf16 */
+  QMOE_W16A16 = 4,   /* A bf16; W bf16 */
+  QMOE_W4A16_NV = 5  /* A bf16; W e2m1 + bf16 scale per 16 k (NVFP4: the checkpoint's e4m3
+                        block scale times its f32 global scale, rounded to bf16 as the
+                        reference's `kernels/megablox/gmm_v2.py:452-462` dequantization
+                        does; each weight is bf16(code * scale)) */
 };
 
 /* Fused gate/up activations (qmoe_gemm_desc.act) */

@@ -143,3 +143,44 @@ def dequant_mxfp4(packed, scales_u8) -> np.ndarray:
     blk = k // s.shape[-1]
     out = vals.reshape(*vals.shape[:-1], s.shape[-1], blk) * s[..., None]
     return out.reshape(*vals.shape[:-2], n, k).astype(np.float32)
+
+
+# ---------------------------------------------------------------- NVFP4
+
+
+def nvfp4_fuse_scales(block_scale, global_scale, halves=False):
+    """ModelOpt NVFP4 block scales -> float32 fused scales.
+
+    ``block_scale``: e4m3fn codes (uint8) or their float32 values, [..., N, K/16];
+    ``global_scale``: the per-tensor float32 ``weight_scale_2`` -- a scalar for a
+    linear (`layers/adapter/quantization/nvfp4.py:700-714`), [E] for MoE w2, or
+    [E, 2] for MoE w13 with ``halves`` (gate rows take column 0, up rows column
+    1, `nvfp4.py:398-409`). One float32 product per scale.
+    """
+    b = np.asarray(block_scale)
+    b = e4m3_decode(b) if b.dtype == np.uint8 else b.astype(np.float32)
+    g = np.asarray(global_scale, np.float32)
+    if halves:
+        n = b.shape[-2] // 2
+        gate = (b[..., :n, :] * g[..., 0, None, None]).astype(np.float32)
+        up = (b[..., n:, :] * g[..., 1, None, None]).astype(np.float32)
+        return np.concatenate([gate, up], axis=-2)
+    if g.ndim == 0:
+        return (b * g).astype(np.float32)
+    return (b * g.reshape(g.shape + (1,) * (b.ndim - g.ndim))).astype(np.float32)
+
+
+def dequant_nvfp4(packed, scales_f32) -> np.ndarray:
+    """NVFP4 [..., N, K/2] codes + float32 [..., N, K/16] scales -> the bf16
+    weights (as float32) the reference multiplies with.
+
+    Block 16 is below the MXU width, so `kernels/megablox/gmm_v2.py:452-462`
+    dequantizes in the activation dtype: the scale is cast to bf16, the codes
+    to bf16 (exact), and their bf16 product is rounded once to bf16.
+    """
+    vals = fp4_decode(unpack_fp4(packed))
+    s = bf16_round(np.asarray(scales_f32, np.float32))
+    n, k = vals.shape[-2], vals.shape[-1]
+    blk = k // s.shape[-1]
+    prod = vals.reshape(*vals.shape[:-1], s.shape[-1], blk) * s[..., None]
+    return bf16_round(prod.reshape(*vals.shape[:-2], n, k).astype(np.float32))

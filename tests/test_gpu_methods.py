@@ -216,3 +216,72 @@ def test_fp8_moe_requantized_in_expert_chunks(dev, monkeypatch, interleaved):
                                                       np.stack([b for _, b in r13]), np.stack([a for a, _ in r2]),
                                                       np.stack([b for _, b in r2])), tw, ids, act)
     assert_close_rows(got.float().cpu().numpy(), ref, "fp8 moe chunked requant")
+
+
+def test_nvfp4_linear_from_checkpoint(dev):
+    """ModelOpt NVFP4 dense linear: e2m1 codes + e4m3 block scales + a shared
+    f32 global (`nvfp4.py:700-761`) -> fused bf16 block scales; apply() is the
+    W4A16 matmul plus bias. The stored scales equal the oracle's fused scales
+    rounded to bf16, bit for bit."""
+    from qmoe.layers import quantization as q
+
+    print("nvfp4 linear method", flush=True)
+    rng = np.random.default_rng(21)
+    N, K, M = 384, 1024, 5
+    method = q.Nvfp4Config().get_quant_method(torch.nn.Linear(1, 1), prefix="model.layers.0.mlp")
+    layer = torch.nn.Module()
+    method.create_weights(layer, K, [256, 128], K, N, torch.bfloat16)
+    codes = rng.integers(0, 256, (N, K // 2), dtype=np.uint8)
+    blk = rng.integers(0x20, 0x48, (N, K // 16)).astype(np.uint8)
+    g = np.float32(0.0123456789)
+    layer.weight.data = _t(codes, dev)
+    layer.weight_scale.data = _fp8(blk, dev)
+    layer.weight_scale_2.data = _t(np.full(2, g, np.float32), dev)
+    layer.input_scale.data = _t(np.ones(2, np.float32), dev)
+    method.process_weights_after_loading(layer)
+    assert not hasattr(layer, "weight_scale_2") and not hasattr(layer, "input_scale")
+    fused = codecs.nvfp4_fuse_scales(blk, g)
+    np.testing.assert_array_equal(layer.weight_scale.float().cpu().numpy(), codecs.bf16_round(fused))
+    x = codecs.bf16_round(rng.standard_normal((M, K)).astype(np.float32))
+    bias = codecs.bf16_round(rng.standard_normal(N).astype(np.float32))
+    got = method.apply(layer, _t(x, dev, torch.bfloat16), _t(bias, dev, torch.bfloat16))
+    ref = codecs.bf16_round(linear.w4a16_nvfp4(x, codes, fused) + bias)
+    assert_close_rows(got.float().cpu().numpy(), ref, "nvfp4 linear method")
+
+
+@pytest.mark.parametrize("T", [3, 150])
+def test_nvfp4_moe_from_checkpoint(dev, T):
+    """ModelOpt NVFP4 MoE: per-expert [gate, up] globals on w13 and a
+    per-expert global on w2 (`nvfp4.py:384-509`), silu; T = 3 takes the fused
+    routing + streaming path, T = 150 the tiled kernels."""
+    from qmoe.layers import quantization as q
+
+    print(f"nvfp4 moe method T={T}", flush=True)
+    rng = np.random.default_rng(23 + T)
+    E, H, I, k = 8, 256, 192, 2
+    layer = _moe_layer(k, "silu")
+    layer.moe_config.has_bias = False
+    method = q.Nvfp4MoEMethod(q.Nvfp4Config(), layer.moe_config)
+    method.create_weights(layer, E, H, I, torch.bfloat16)
+    c13 = rng.integers(0, 256, (E, 2 * I, H // 2), dtype=np.uint8)
+    c2 = rng.integers(0, 256, (E, H, I // 2), dtype=np.uint8)
+    b13 = rng.integers(0x20, 0x40, (E, 2 * I, H // 16)).astype(np.uint8)
+    b2 = rng.integers(0x20, 0x40, (E, H, I // 16)).astype(np.uint8)
+    g13 = (rng.random((E, 2)) * 0.01 + 0.003).astype(np.float32)
+    g2 = (rng.random(E) * 0.01 + 0.003).astype(np.float32)
+    layer.w13_weight.data = _t(c13, dev)
+    layer.w2_weight.data = _t(c2, dev)
+    layer.w13_weight_scale.data = _fp8(b13, dev)
+    layer.w2_weight_scale.data = _fp8(b2, dev)
+    layer.w13_weight_scale_2.data = _t(g13, dev)
+    layer.w2_weight_scale_2.data = _t(g2, dev)
+    method.process_weights_after_loading(layer)
+    s13 = codecs.nvfp4_fuse_scales(b13, g13, halves=True)
+    s2 = codecs.nvfp4_fuse_scales(b2, g2)
+    np.testing.assert_array_equal(layer.w13_weight_scale.float().cpu().numpy(), codecs.bf16_round(s13))
+    x = codecs.bf16_round(rng.standard_normal((T, H)).astype(np.float32))
+    logits = codecs.bf16_round(rng.standard_normal((T, E)).astype(np.float32))
+    got = method.apply_monolithic(layer, _t(x, dev, torch.bfloat16), _t(logits, dev, torch.bfloat16))
+    tw, ids = routing.select_experts(logits, k, True, "softmax")
+    ref, _, _ = omoe.fused_moe(x, omoe.ExpertWeights("nvfp4", c13, s13, c2, s2), tw, ids, "silu")
+    assert_close_rows(got.float().cpu().numpy(), ref, "nvfp4 moe method")

@@ -115,6 +115,14 @@ def _moe_case(fmt, E, k, H, I, T, seed, bias=False):
         s13 = (127 + rng.integers(-8, 1, (E, 2 * I, H // 32))).astype(np.uint8)
         w2 = rng.integers(0, 256, (E, H, I // 2), dtype=np.uint8)
         s2 = (127 + rng.integers(-8, 1, (E, H, I // 32))).astype(np.uint8)
+    elif fmt == "nvfp4":
+        # fused block scales: e4m3 block scale x a float32 global per expert (gate / up halves)
+        w13 = rng.integers(0, 256, (E, 2 * I, H // 2), dtype=np.uint8)
+        w2 = rng.integers(0, 256, (E, H, I // 2), dtype=np.uint8)
+        b13s = rng.integers(0x20, 0x40, (E, 2 * I, H // 16)).astype(np.uint8)
+        b2s = rng.integers(0x20, 0x40, (E, H, I // 16)).astype(np.uint8)
+        s13 = codecs.nvfp4_fuse_scales(b13s, (rng.random((E, 2)) * 0.01 + 0.003).astype(np.float32), halves=True)
+        s2 = codecs.nvfp4_fuse_scales(b2s, (rng.random(E) * 0.01 + 0.003).astype(np.float32))
     elif fmt == "fp8_block":
         w13f = (rng.standard_normal((E, 2 * I, H)) * 0.02).astype(np.float32)
         w2f = (rng.standard_normal((E, H, I)) * 0.02).astype(np.float32)
@@ -139,6 +147,10 @@ def _moe_case(fmt, E, k, H, I, T, seed, bias=False):
     ("mxfp4", "swigluoai", 16, 4, 512, 384, 40, True),
     ("mxfp4", "swigluoai", 16, 4, 512, 256, 300, True),   # tiled path (T > 64)
     ("mxfp4", "swigluoai", 8, 2, 288, 160, 6, False),     # K % 256 != 0 in both GEMMs
+    ("nvfp4", "silu", 8, 2, 256, 256, 1, False),
+    ("nvfp4", "silu", 16, 4, 512, 384, 40, False),
+    ("nvfp4", "gelu_tanh", 16, 4, 512, 256, 300, False),  # tiled path
+    ("nvfp4", "silu", 8, 2, 288, 160, 6, False),          # K % 64 == 32 in both GEMMs
     ("fp8_block", "silu", 8, 2, 512, 256, 5, False),
     ("fp8_block", "silu", 16, 4, 512, 256, 200, False),   # tiled path
     ("bf16", "silu", 8, 2, 256, 128, 9, False),
@@ -159,9 +171,10 @@ def test_fused_moe_layer(dev, fmt, act, E, k, H, I, T, bias):
             return t.view(torch.float8_e4m3fn)
         return t.to(wdt) if wdt is not None else t
 
+    sdt = torch.bfloat16 if fmt == "nvfp4" else None  # NVFP4 runtime scales are bf16
     got = fused_moe_gmm(
         _t(hid, dev, torch.bfloat16), wt(w13), wt(w2),
-        _t(s13, dev) if s13 is not None else None, _t(s2, dev) if s2 is not None else None,
+        _t(s13, dev, sdt) if s13 is not None else None, _t(s2, dev, sdt) if s2 is not None else None,
         _t(b13, dev) if b13 is not None else None, _t(b2, dev) if b2 is not None else None,
         _t(tw, dev, torch.bfloat16), _t(ids, dev), None, k, act,
         weight_format=fmt,

@@ -213,6 +213,57 @@ def test_w8a8_fp8_block(dev, M, K, N, tile_scales):
     assert_close_rows(y.float().cpu().numpy(), ref, f"fp8 blk {M}x{K}x{N}")
 
 
+def _nv_scales(rng, n, k):
+    """Fused NVFP4 block scales as a checkpoint makes them: e4m3 block scale
+    times a float32 global with a full mantissa (so the bf16 rounding of the
+    product matters), [n, k/16] float32."""
+    blk = codecs.e4m3_decode(rng.integers(0x20, 0x48, (n, k // 16)).astype(np.uint8))
+    return codecs.nvfp4_fuse_scales(blk, np.float32(0.0123456789))
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 2880, 5760), (16, 2880, 5760), (5, 512, 200), (33, 1024, 96),
+                                   # K % 128 != 0 (streaming kernel's tail step), small K
+                                   (3, 2848, 200), (1, 416, 70), (7, 96, 130),
+                                   # tiled kernel: 64/128-token tiles, K splits, ragged tiles
+                                   (300, 2880, 768), (520, 1024, 512), (200, 4096, 4096),
+                                   # K % 64 == 32 above the streaming bound: 64-row streaming passes
+                                   (70, 2848, 300)])
+def test_w4a16_nvfp4(dev, M, K, N):
+    from qmoe import _capi, ops
+
+    print(f"w4a16 nv M={M} K={K} N={N}", flush=True)
+    rng = np.random.default_rng(M + 2 * K + N)
+    packed = rng.integers(0, 256, (N, K // 2), dtype=np.uint8)
+    sc = _nv_scales(rng, N, K)
+    x = _bf16(rng, (M, K))
+    bias = (rng.standard_normal(N) * 0.1).astype(np.float32)
+    ref = linear.w4a16_nvfp4(x, packed, sc, bias)
+    y = ops.gemm(_capi.W4A16_NV, _t(x, dev, torch.bfloat16), _t(packed, dev),
+                 w_scale=_t(sc, dev, torch.bfloat16), bias=_t(bias, dev))
+    assert_close_rows(y.float().cpu().numpy(), ref, f"nvfp4 {M}x{K}x{N}")
+
+
+@pytest.mark.parametrize("M,K,N", [(16, 2880, 320), (256, 4096, 512)])
+def test_w4a16_nvfp4_dequant_bit_exact(dev, M, K, N):
+    """One-hot activation rows read single dequantized weights back: output
+    row i is column k_i of bf16(code * bf16(scale)), exactly (one nonzero
+    product, f32 accumulation, a bf16 value rounded to bf16). M = 16 runs the
+    streaming kernel, M = 256 the tiled one; the k_i cover every 16-k block
+    position of a row."""
+    from qmoe import _capi, ops
+
+    print(f"w4a16 nv one-hot M={M} K={K} N={N}", flush=True)
+    rng = np.random.default_rng(K + N)
+    packed = rng.integers(0, 256, (N, K // 2), dtype=np.uint8)
+    sc = _nv_scales(rng, N, K)
+    ks = (np.arange(M) * (K // M) + np.arange(M) % 16) % K
+    x = np.zeros((M, K), np.float32)
+    x[np.arange(M), ks] = 1.0
+    y = ops.gemm(_capi.W4A16_NV, _t(x, dev, torch.bfloat16), _t(packed, dev), w_scale=_t(sc, dev, torch.bfloat16))
+    want = codecs.dequant_nvfp4(packed, sc)[:, ks].T
+    np.testing.assert_array_equal(y.float().cpu().numpy(), want)
+
+
 @pytest.mark.parametrize("M,K,N", [(1, 2880, 5760), (16, 2880, 5760), (128, 2880, 1440),
                                    (5, 512, 200), (90, 1024, 96),
                                    # K % 256 = 32, 160 and K < 256: every partial last step pair

@@ -87,3 +87,60 @@ def test_activation_codes():
     assert ops.act_code("situ:2.0:none")[2] < 0
     with pytest.raises(NotImplementedError):
         ops.act_code("relu")
+
+
+def test_nvfp4_config_dispatch_and_shapes():
+    """ModelOpt NVFP4 (`nvfp4.py:236-297`): linear and MoE methods, excluded
+    modules run unquantized; the checkpoint parameters upstream registers."""
+    cfg = q.Nvfp4Config.from_config({"quantization": {"quant_algo": "NVFP4", "group_size": 16,
+                                                      "exclude_modules": ["lm_head"]}})
+    assert q.get_quantization_config("modelopt_fp4") is q.Nvfp4Config and cfg.get_name() == "modelopt_fp4"
+    assert isinstance(cfg.get_quant_method(torch.nn.Module(), "model.layers.0.mlp"), q.Nvfp4LinearMethod)
+    assert isinstance(cfg.get_quant_method(_moe_layer(), "model.layers.0.mlp.experts"), q.Nvfp4MoEMethod)
+    assert isinstance(cfg.get_quant_method(torch.nn.Module(), "lm_head"), q.UnquantizedLinearMethod)
+    assert isinstance(cfg.get_quant_method(_moe_layer(), "lm_head"), q.UnquantizedFusedMoEMethod)
+    with pytest.raises(ValueError):
+        q.Nvfp4Config(group_size=32)
+    layer = torch.nn.Module()
+    q.Nvfp4LinearMethod(cfg).create_weights(layer, 1024, [256, 128], 1024, 384, torch.bfloat16)
+    assert layer.weight.shape == (384, 512) and layer.weight.dtype == torch.uint8
+    assert layer.weight_scale.shape == (384, 64) and layer.weight_scale.dtype == torch.float8_e4m3fn
+    assert layer.weight_scale_2.shape == (2,) and layer.input_scale.shape == (2,)
+    moe = _moe_layer()
+    q.Nvfp4MoEMethod(cfg, moe.moe_config).create_weights(moe, 4, 256, 384, torch.bfloat16)
+    assert moe.w13_weight.shape == (4, 768, 128) and moe.w13_weight_scale.shape == (4, 768, 16)
+    assert moe.w2_weight.shape == (4, 256, 192) and moe.w2_weight_scale.shape == (4, 256, 24)
+    assert moe.w13_weight_scale_2.shape == (4, 2) and moe.w2_weight_scale_2.shape == (4,)
+
+
+def test_nvfp4_load_time_guards(monkeypatch):
+    """The reference's NVFP4 load-time errors (`nvfp4.py:378-392, 695-699`),
+    raised before any device work."""
+    cfg = q.Nvfp4Config()
+    lin = q.Nvfp4LinearMethod(cfg)
+    layer = torch.nn.Module()
+    lin.create_weights(layer, 64, [32, 32], 64, 64, torch.bfloat16)
+    layer.weight_scale_2.data = torch.tensor([1.0, 2.0])
+    with pytest.raises(AssertionError, match="Fused NVFP4 projections must share one global scale"):
+        lin.process_weights_after_loading(layer)
+
+    def moe_method(act="silu", has_bias=False, gated=True):
+        moe = _moe_layer()
+        moe.moe_config.has_bias = has_bias
+        moe.moe_config.is_act_and_mul = gated
+        moe.activation = act
+        return q.Nvfp4MoEMethod(cfg, moe.moe_config), moe
+
+    m, moe = moe_method(has_bias=True)
+    with pytest.raises(AssertionError, match="does not support bias"):
+        m.process_weights_after_loading(moe)
+    m, moe = moe_method(gated=False)
+    with pytest.raises(AssertionError, match="act_and_mul"):
+        m.process_weights_after_loading(moe)
+    m, moe = moe_method(act="swigluoai")
+    with pytest.raises(NotImplementedError, match="swigluoai"):
+        m.process_weights_after_loading(moe)
+    monkeypatch.setenv("MOE_REQUANTIZE_BLOCK_SIZE", "32")
+    m, moe = moe_method()
+    with pytest.raises(NotImplementedError, match="MOE_REQUANTIZE_BLOCK_SIZE"):
+        m.process_weights_after_loading(moe)

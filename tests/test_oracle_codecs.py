@@ -108,3 +108,60 @@ def test_bf16_round_matches_torch():
     x = x[np.isfinite(x)]
     ref = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
     np.testing.assert_array_equal(codecs.bf16_round(x), ref)
+
+
+# ---------------------------------------------------------------- NVFP4
+
+
+def test_nvfp4_fused_scale_known_answers():
+    """`tests/layers/adapter/quantization/test_nvfp4.py:255-284`: unit block
+    scales times a 2.5 global give 2.5; MoE w13 takes the gate global on the
+    first half of the rows and the up global on the second
+    (`nvfp4.py:398-409`), w2 its per-expert global."""
+    ones = np.ones((32, 4), np.float32)
+    np.testing.assert_array_equal(codecs.nvfp4_fuse_scales(ones, np.float32(2.5)), ones * 2.5)
+    s13 = codecs.nvfp4_fuse_scales(np.ones((2, 32, 4), np.float32), np.array([[2, 3], [4, 5]], np.float32),
+                                   halves=True)
+    np.testing.assert_array_equal(s13[:, :16], np.array([2, 4], np.float32)[:, None, None] * np.ones((2, 16, 4)))
+    np.testing.assert_array_equal(s13[:, 16:], np.array([3, 5], np.float32)[:, None, None] * np.ones((2, 16, 4)))
+    s2 = codecs.nvfp4_fuse_scales(np.ones((2, 8, 2), np.float32), np.array([2, 4], np.float32))
+    np.testing.assert_array_equal(s2, np.array([2, 4], np.float32)[:, None, None] * np.ones((2, 8, 2)))
+    # e4m3 codes decode first: 0x38 = 1.0, 0x3c = 1.5, 0x30 = 0.5
+    codes = np.array([[0x38, 0x3C, 0x30, 0xB8]], np.uint8)
+    np.testing.assert_array_equal(codecs.nvfp4_fuse_scales(codes, np.float32(2.0)),
+                                  np.array([[2.0, 3.0, 1.0, -2.0]], np.float32))
+
+
+def test_nvfp4_dequant_rounds_scale_then_product_to_bf16():
+    """Block 16 is dequantized in bf16 (`kernels/megablox/gmm_v2.py:452-462`):
+    bf16(code * bf16(scale)). Hand-computed cases: 1.5 x 1.0078125 =
+    1.51171875 sits halfway between bf16 neighbours 1.5078125 and 1.515625
+    and rounds to the even one (1.515625); 1.5 x 1.0234375 = 1.53515625 ties
+    down to 1.53125; scale 1.005859375 rounds up to 1.0078125 first (without
+    that step the product would round to 1.5078125)."""
+    def one(code, scale):
+        packed = np.array([[code | (code << 4)] * 8], np.uint8)  # one row, K = 16
+        return codecs.dequant_nvfp4(packed, np.array([[scale]], np.float32))[0, 0]
+
+    assert one(3, 1.0078125) == np.float32(1.515625)     # e2m1 code 3 = 1.5
+    assert one(3, 1.0234375) == np.float32(1.53125)
+    assert one(3, 1.005859375) == np.float32(1.515625)
+    assert one(11, 1.0078125) == np.float32(-1.515625)  # code 11 = -1.5
+    assert one(2, 1.005859375) == np.float32(1.0078125)  # code 2 = 1.0: just the rounded scale
+    assert one(7, 3.0) == np.float32(18.0)               # code 7 = 6.0, exact
+
+
+def test_nvfp4_dequant_with_power_of_two_scales_is_the_mxfp4_dequant():
+    """With power-of-two scales every product is exact, so NVFP4 and MXFP4
+    dequantization (pinned by the reference's e8m0 / e2m1 known answers)
+    agree; the 16-wide blocks each take their own scale."""
+    rng = np.random.default_rng(4)
+    packed = rng.integers(0, 256, (8, 32), dtype=np.uint8)  # K = 64
+    e = rng.integers(120, 134, (8, 2)).astype(np.uint8)     # e8m0 per 32 k
+    mx = codecs.dequant_mxfp4(packed, e)
+    s16 = np.repeat(codecs.e8m0_decode(e), 2, axis=1)       # the same scale on both 16-k halves
+    np.testing.assert_array_equal(codecs.dequant_nvfp4(packed, s16), mx)
+    s16[:, 1] *= 2  # second 16-k block of each row doubles
+    nv = codecs.dequant_nvfp4(packed, s16)
+    np.testing.assert_array_equal(nv[:, 16:32], mx[:, 16:32] * 2)
+    np.testing.assert_array_equal(nv[:, :16], mx[:, :16])

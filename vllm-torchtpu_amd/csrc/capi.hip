@@ -15,8 +15,8 @@ int qmoe_skinny_launch(int kind, GemmParams p, int max_rows, int slots, void* wo
 int qmoe_tiled_launch(int kind, GemmParams p, hipStream_t st);
 bool qmoe_f8_plan(const GemmParams& p, bool blk, int* bm_out, int* ksplit_out, int64_t* ws_bytes);
 int qmoe_f8_launch(GemmParams p, bool blk, void* workspace, int64_t ws_bytes, hipStream_t st);
-bool qmoe_w4_plan(const GemmParams& p, int* bm_out, int* ksplit_out, int64_t* ws_bytes);
-int qmoe_w4_launch(GemmParams p, void* workspace, int64_t ws_bytes, hipStream_t st);
+bool qmoe_w4_plan(const GemmParams& p, bool nv, int* bm_out, int* ksplit_out, int64_t* ws_bytes);
+int qmoe_w4_launch(GemmParams p, bool nv, void* workspace, int64_t ws_bytes, hipStream_t st);
 
 namespace {
 
@@ -26,7 +26,7 @@ constexpr int kSkinnyMaxRowsW8A8 = 32;
 
 int to_params(const qmoe_gemm_desc* d, GemmParams* p) {
   if (!d) return QMOE_ERR_ARG;
-  if (d->kind < QMOE_W8A8_PC || d->kind > QMOE_W16A16) return QMOE_ERR_ARG;
+  if (d->kind < QMOE_W8A8_PC || d->kind > QMOE_W4A16_NV) return QMOE_ERR_ARG;
   if (d->kind == QMOE_W8A8_PC && d->wfmt != 0 && d->wfmt != 1) return QMOE_ERR_ARG;
   if (d->act < QMOE_ACT_NONE || d->act > QMOE_ACT_SITU) return QMOE_ERR_ARG;
   if (d->M < 0 || d->N <= 0 || d->K <= 0 || d->slots <= 0) return QMOE_ERR_ARG;
@@ -38,9 +38,13 @@ int to_params(const qmoe_gemm_desc* d, GemmParams* p) {
   if (d->active && (!d->num_active || !d->group_offs)) return QMOE_ERR_ARG;
   if (!d->group_offs && d->slots != 1) return QMOE_ERR_ARG;
   // 16-byte loads along K
-  const int wbytes = d->kind == QMOE_W4A16_MX ? d->K / 2 : (d->kind == QMOE_W16A16 ? 2 * d->K : d->K);
+  const int wbytes = kind_fp4(d->kind) ? d->K / 2 : (d->kind == QMOE_W16A16 ? 2 * d->K : d->K);
   if (d->ldw < wbytes || (d->ldw % 16) != 0 || (d->K % 32) != 0) return QMOE_ERR_ARG;
-  const bool abf16 = d->kind == QMOE_W8A16_PC || d->kind == QMOE_W4A16_MX || d->kind == QMOE_W16A16;
+  // NVFP4 scales: bf16 [N][ldws >= K/16], 4-byte aligned pairs
+  if (d->kind == QMOE_W4A16_NV && (d->ldws < d->K / 16 || (d->ldws % 2) != 0 || (d->ws_gstride % 2) != 0 ||
+                                   (reinterpret_cast<uintptr_t>(d->w_scale) & 3)))
+    return QMOE_ERR_ARG;
+  const bool abf16 = kind_abf16(d->kind);
   if (d->lda < d->K || ((d->lda * (abf16 ? 2 : 1)) % 16) != 0) return QMOE_ERR_ARG;
   const int nout = d->act != QMOE_ACT_NONE ? d->N / 2 : d->N;
   if (d->ldy < nout) return QMOE_ERR_ARG;
@@ -107,6 +111,7 @@ bool use_skinny(const qmoe_gemm_desc* d) {
 }
 
 bool use_w4(const qmoe_gemm_desc* d) {
+  if (d->kind == QMOE_W4A16_NV) return true;  // the generic kernel has no NVFP4 form
   return d->kind == QMOE_W4A16_MX && !getenv("QMOE_W4_OFF");  // tuning knob: generic kernel only
 }
 
@@ -131,7 +136,7 @@ extern "C" int qmoe_gemm_workspace_size(const qmoe_gemm_desc* d, int64_t* bytes)
     p.active = nullptr;
     p.num_active = nullptr;
     int bm = 0, ks = 1;
-    const bool ok = use_w4(d) ? qmoe_w4_plan(p, &bm, &ks, bytes)
+    const bool ok = use_w4(d) ? qmoe_w4_plan(p, d->kind == QMOE_W4A16_NV, &bm, &ks, bytes)
                               : qmoe_f8_plan(p, d->kind == QMOE_W8A8_BLK, &bm, &ks, bytes);
     if (!ok) *bytes = 0;
   }
@@ -164,7 +169,7 @@ extern "C" int qmoe_gemm(const qmoe_gemm_desc* d, void* workspace, int64_t ws_by
     const int rc = qmoe_f8_launch(p, d->kind == QMOE_W8A8_BLK, workspace, ws_bytes, stream);
     if (rc != QMOE_ERR_ARG) return rc;
   } else if (use_w4(d)) {
-    const int rc = qmoe_w4_launch(p, workspace, ws_bytes, stream);
+    const int rc = qmoe_w4_launch(p, d->kind == QMOE_W4A16_NV, workspace, ws_bytes, stream);
     if (rc != QMOE_ERR_ARG) return rc;
   }
   const int rc = qmoe_tiled_launch(d->kind, p, stream);

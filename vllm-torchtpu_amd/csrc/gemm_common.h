@@ -19,7 +19,40 @@ enum QmoeKind {
   QK_W8A16_PC = 2,  // A bf16; W e4m3 + per-channel f32 scale
   QK_W4A16_MX = 3,  // A bf16; W e2m1 (2 per byte, low nibble = even k) + e8m0 per 32 k
   QK_W16A16 = 4,    // A bf16; W bf16
+  QK_W4A16_NV = 5,  // A bf16; W e2m1 (as QK_W4A16_MX) + bf16 scale per 16 k
 };
+
+// bf16 activations (the other kinds take 1-byte activation codes)
+QMOE_HD constexpr bool kind_abf16(int kind) {
+  return kind == QK_W8A16_PC || kind == QK_W4A16_MX || kind == QK_W16A16 || kind == QK_W4A16_NV;
+}
+
+// e2m1 weights (two codes per byte)
+QMOE_HD constexpr bool kind_fp4(int kind) { return kind == QK_W4A16_MX || kind == QK_W4A16_NV; }
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// 8 e2m1 codes (one dword, low nibble first) times a bf16-valued scale ->
+// 8 bf16, each the round-to-nearest-even of code * scale: the product of a
+// 2-bit and an 8-bit significand is exact in float32, so this is the one
+// rounding of the reference's bf16 multiply (`kernels/megablox/gmm_v2.py:
+// 452-462`). The scaled conversion instructions apply only the exponent of
+// their scale operand, so the codes are converted unscaled and multiplied.
+__device__ __forceinline__ uint4 nvfp4x8_to_bf16(uint32_t d, float s) {
+  const f32x2 f0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d, 1.0f, 0);
+  const f32x2 f1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d, 1.0f, 1);
+  const f32x2 f2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d, 1.0f, 2);
+  const f32x2 f3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d, 1.0f, 3);
+  union {
+    bf16x2 h[4];
+    uint4 u;
+  } r;
+  r.h[0] = __builtin_convertvector(f32x2{f0[0] * s, f0[1] * s}, bf16x2);
+  r.h[1] = __builtin_convertvector(f32x2{f1[0] * s, f1[1] * s}, bf16x2);
+  r.h[2] = __builtin_convertvector(f32x2{f2[0] * s, f2[1] * s}, bf16x2);
+  r.h[3] = __builtin_convertvector(f32x2{f3[0] * s, f3[1] * s}, bf16x2);
+  return r.u;
+}
 
 enum QmoeAct {
   QA_NONE = 0,
@@ -41,7 +74,7 @@ struct GemmParams {
   const uint8_t* w;
   int64_t ldw;             // bytes per weight row
   int64_t w_gstride;
-  const void* w_scale;     // f32 [N] | f32 [N/bn, ldws] | u8 [N, ldws]
+  const void* w_scale;     // f32 [N] | f32 [N/bn, ldws] | u8 [N, ldws] | bf16 [N, ldws]
   int64_t ldws;            // row stride of w_scale (elements)
   int64_t ws_gstride;      // group stride of w_scale (elements)
   int32_t ws_bn;           // rows of W sharing one block-scale row (1 or 128)

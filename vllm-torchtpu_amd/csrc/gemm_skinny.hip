@@ -51,10 +51,11 @@ struct Frag {
 
 template <int KIND, int WF>
 struct Traits {
-  static constexpr bool kAbf16 = KIND == QK_W8A16_PC || KIND == QK_W4A16_MX || KIND == QK_W16A16;
+  static constexpr bool kAbf16 = kind_abf16(KIND);
+  static constexpr bool kFp4 = kind_fp4(KIND);
   static constexpr bool kInt = KIND == QK_W8A8_PC && WF == 1;
   // bytes per lane per 128-k step (32 k values)
-  static constexpr int kWBytes = KIND == QK_W4A16_MX ? 16 : (KIND == QK_W16A16 ? 64 : 32);
+  static constexpr int kWBytes = kFp4 ? 16 : (KIND == QK_W16A16 ? 64 : 32);
   static constexpr int kABytes = kAbf16 ? 64 : 32;
   // Weight chunk j (16 B) of lane (column c, k-group kg) sits at byte
   // j*64 + kg*16 of the row's step (4 lanes x 16 B = one 64 B segment per
@@ -63,13 +64,13 @@ struct Traits {
   //   1-byte A (e4m3/int8) and bf16 A with bf16 W: byte kg*16 + i*64
   //   bf16 A with e4m3 W: byte kg*32 + (i/2)*128 + (i%2)*16
   //   bf16 A with e2m1 W: byte kg*64 + i*16
-  static constexpr int kAOffBase = KIND == QK_W4A16_MX ? 64 : (KIND == QK_W8A16_PC ? 32 : 16);
+  static constexpr int kAOffBase = kFp4 ? 64 : (KIND == QK_W8A16_PC ? 32 : 16);
   static __device__ __forceinline__ constexpr int a_off(int i) {
-    return KIND == QK_W4A16_MX ? i * 16 : (KIND == QK_W8A16_PC ? (i >> 1) * 128 + (i & 1) * 16 : i * 64);
+    return kFp4 ? i * 16 : (KIND == QK_W8A16_PC ? (i >> 1) * 128 + (i & 1) * 16 : i * 64);
   }
   // first k (within the step) of weight chunk (j, kg) / activation chunk (i, kg)
   static __device__ __forceinline__ constexpr int w_k0(int j, int kg) {
-    return KIND == QK_W4A16_MX ? kg * 32 : (KIND == QK_W16A16 ? j * 32 + kg * 8 : j * 64 + kg * 16);
+    return kFp4 ? kg * 32 : (KIND == QK_W16A16 ? j * 32 + kg * 8 : j * 64 + kg * 16);
   }
   static __device__ __forceinline__ constexpr int a_k0(int i, int kg) {
     return (kg * kAOffBase + a_off(i)) / (kAbf16 ? 2 : 1);
@@ -190,12 +191,13 @@ struct Acc {
 };
 
 // Per-step side data: per-(row, block) and per-(n, block) scales (W8A8_BLK),
-// e8m0 block scale of the lane's weight row (W4A16_MX).
+// e8m0 block scale of the lane's weight row (W4A16_MX), the two bf16 block
+// scales of the lane's 32 k (W4A16_NV, low half first).
 template <int MS, int NS>
 struct StepScales {
   float sa[MS][4];
   float sb[NS];
-  uint32_t eb[NS];  // raw e8m0 bytes, decoded where they are used
+  uint32_t eb[NS];  // raw e8m0 bytes / bf16 pairs, decoded where they are used
 };
 
 // One 128-k step of MFMAs for all (M tile, weight tile) pairs.
@@ -248,11 +250,16 @@ __device__ __forceinline__ void mma_step(Acc<KIND, WF, MS, NS>& acc, const Frag 
           const uint2 hi = fp8x4_to_bf16(d[2 * q + 1]);
           wb[q] = make_uint4(lo.x, lo.y, hi.x, hi.y);
         }
-      } else {  // QK_W4A16_MX
+      } else if constexpr (KIND == QK_W4A16_MX) {
         const uint32_t d[4] = {bw[s].v[0].x, bw[s].v[0].y, bw[s].v[0].z, bw[s].v[0].w};
         const float scale = e8m0_to_f32(sc.eb[s]);
 #pragma unroll
         for (int q = 0; q < 4; ++q) wb[q] = fp4x8_to_bf16(d[q], scale);
+      } else {  // QK_W4A16_NV: dwords 0-1 are the first 16-k block, 2-3 the second
+        const uint32_t d[4] = {bw[s].v[0].x, bw[s].v[0].y, bw[s].v[0].z, bw[s].v[0].w};
+        const float s0 = bits_f32(sc.eb[s] << 16), s1 = bits_f32(sc.eb[s] & 0xffff0000u);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) wb[q] = nvfp4x8_to_bf16(d[q], q < 2 ? s0 : s1);
       }
 #pragma unroll
       for (int ms = 0; ms < MS; ++ms)
@@ -360,12 +367,18 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p)
     woff[s] = (uint32_t)(row_of(s, lane >> 2) * p.ldw + (lane & 3) * 16);
   }
   const int perm_src = (4 * col + kg) * 4;
-  // scale streams: e8m0 bytes [N][K/32] (W4A16, staged below), per-step f32
-  // [N/bn][K/128] weight blocks and [rows][K/128] activation blocks (W8A8_BLK)
+  // scale streams: e8m0 bytes [N][K/32] (W4A16_MX, staged below), bf16
+  // [N][K/16] (W4A16_NV: one 4-byte pair per lane and step, for the lane's
+  // row and 32 k), per-step f32 [N/bn][K/128] weight blocks and [rows][K/128]
+  // activation blocks (W8A8_BLK)
   rsrc_t sres = wres, ares = wres;  // placeholders for kinds without scale streams
   uint32_t soffw[NS];
   if constexpr (KIND == QK_W4A16_MX) {
     sres = make_rsrc(static_cast<const uint8_t*>(p.w_scale) + (int64_t)g * p.ws_gstride, (int64_t)p.N * p.ldws);
+  } else if constexpr (KIND == QK_W4A16_NV) {
+    sres = make_rsrc(static_cast<const uint16_t*>(p.w_scale) + (int64_t)g * p.ws_gstride, (int64_t)p.N * p.ldws * 2);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) soffw[s] = (uint32_t)(nclamp[s] * p.ldws * 2 + kg * 4);
   } else if constexpr (KIND == QK_W8A8_BLK) {
     sres = make_rsrc(static_cast<const float*>(p.w_scale) + (int64_t)g * p.ws_gstride,
                      (int64_t)cdiv(p.N, p.ws_bn) * p.ldws * 4);
@@ -458,6 +471,11 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p)
       } else if constexpr (KIND == QK_W4A16_MX) {
 #pragma unroll
         for (int s = 0; s < NS; ++s) sc.eb[s] = s_eb[(s * 16 + col) * KB32 + ks * 4 + kg];
+      } else if constexpr (KIND == QK_W4A16_NV) {
+        const uint32_t oob = live ? 0u : kOob;
+#pragma unroll
+        for (int s = 0; s < NS; ++s)
+          sc.eb[s] = __builtin_amdgcn_raw_buffer_load_b32(sres, soffw[s] | oob, (uint32_t)ks * 16, 0);
       }
     };
 
@@ -567,6 +585,12 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p)
           const uint32_t b = s_eb[(s * 16 + col) * KB32 + kk * 4 + (ok ? kg : 0)];
           sc.eb[s] = ok ? b : 127u;
         }
+      } else if constexpr (KIND == QK_W4A16_NV) {
+        // blocks past K read zeros (the weights there are zero as well)
+        const uint32_t oob = kg * 32 < t ? 0u : kOob;
+#pragma unroll
+        for (int s = 0; s < NS; ++s)
+          sc.eb[s] = __builtin_amdgcn_raw_buffer_load_b32(sres, soffw[s] | oob, (uint32_t)kk * 16, 0);
       }
       mma_step<KIND, WF, MS, NS>(acc, fa, bw, sc);
     }
@@ -802,10 +826,13 @@ int qmoe_skinny_launch(int kind, GemmParams p, int max_rows, int slots, void* wo
   if (p.act != QA_NONE && (p.N % 2) != 0) return QMOE_ERR_ARG;
   if (kind == QK_W8A8_BLK && (p.K % 128) != 0) return QMOE_ERR_ARG;
   // 32-bit buffer offsets: every operand stream stays below 2 GiB
-  const bool abf16 = kind == QK_W8A16_PC || kind == QK_W4A16_MX || kind == QK_W16A16;
+  const bool abf16 = kind_abf16(kind);
   constexpr int64_t kLim = 0x7fffffff;
   if ((int64_t)p.N * p.ldw > kLim || p.M * p.lda * (abf16 ? 2 : 1) > kLim) return QMOE_ERR_ARG;
   if (kind == QK_W4A16_MX && ((int64_t)p.N * p.ldws > kLim || p.K > 16384)) return QMOE_ERR_ARG;
+  if (kind == QK_W4A16_NV && ((int64_t)p.N * p.ldws * 2 > kLim || (p.ldws % 2) != 0 ||
+                              (reinterpret_cast<uintptr_t>(p.w_scale) & 3) || (p.ws_gstride % 2) != 0))
+    return QMOE_ERR_ARG;
   if (kind == QK_W8A8_BLK &&
       ((int64_t)cdiv(p.N, p.ws_bn) * p.ldws * 4 > kLim || p.M * p.lds_a * 4 > kLim))
     return QMOE_ERR_ARG;
@@ -828,6 +855,7 @@ int qmoe_skinny_launch(int kind, GemmParams p, int max_rows, int slots, void* wo
     case QK_W8A8_BLK: launch_act<QK_W8A8_BLK, 0>(p, ms, ns, waves, grid, st); break;
     case QK_W8A16_PC: launch_act<QK_W8A16_PC, 0>(p, ms, ns, waves, grid, st); break;
     case QK_W4A16_MX: launch_act<QK_W4A16_MX, 0>(p, ms, ns, waves, grid, st); break;
+    case QK_W4A16_NV: launch_act<QK_W4A16_NV, 0>(p, ms, ns, waves, grid, st); break;
     case QK_W16A16: launch_act<QK_W16A16, 0>(p, ms, ns, waves, grid, st); break;
     default: return QMOE_ERR_ARG;
   }

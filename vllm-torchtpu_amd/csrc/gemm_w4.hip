@@ -1,12 +1,13 @@
-// Tiled (prefill) GEMM for bf16 activations x MXFP4 weights (W4A16: e2m1
-// codes, two per byte with the even k in the low nibble, one e8m0 scale per
-// 32 k), dense or grouped.
+// Tiled (prefill) GEMM for bf16 activations x FP4 weights (W4A16: e2m1
+// codes, two per byte with the even k in the low nibble; MXFP4: one e8m0
+// scale per 32 k; NVFP4: one bf16 scale per 16 k), dense or grouped.
 //
 // Restates the reference's W4A16 path (`layers/adapter/linear_common.py:
-// 188-209` -> `kernels/megablox/gmm_v2.py:452-462`: the block-32 weights are
-// dequantized to the activation dtype and multiplied in bf16 with f32
-// accumulation). The dequantization is exact in bf16, so expanding the codes
-// on the fly gives the same products as dequantizing the whole matrix first.
+// 188-209` -> `kernels/megablox/gmm_v2.py:452-462`: block-32 / block-16
+// weights are dequantized to the activation dtype and multiplied in bf16 with
+// f32 accumulation). Expanding the codes on the fly gives the same bf16
+// weights as dequantizing the whole matrix first: exact for e8m0 scales, one
+// round-to-nearest-even of code * scale for the bf16 NVFP4 scales.
 //
 // Design for gfx950 (one workgroup of 4 wavefronts per CU), on the machinery
 // of the 1-byte tiled kernel (gemm_tile.h):
@@ -17,11 +18,13 @@
 //    arrays) four stages ahead; each lane loads the scale bytes it needs
 //    with the copies (bounded buffer loads into a 4-deep register ring);
 //  * in a stage, lane l (row l % 32, half h = l / 32) feeds k in
-//    [32h, 32h + 32): that is one e8m0 block, 16 contiguous code bytes (one
-//    LDS read for all four 16-k MFMA steps) and one scale byte. Each 16-k
-//    step expands 8 codes to bf16 with the block scale applied
-//    (v_cvt_scalef32_pk_bf16_fp4); activation and weight use the same lane
-//    -> k assignment, so the products pair up whatever order the MFMA sums;
+//    [32h, 32h + 32): that is one e8m0 block (two NVFP4 blocks), 16
+//    contiguous code bytes (one LDS read for all four 16-k MFMA steps) and
+//    one scale byte (one 4-byte bf16 pair). Each 16-k step expands 8 codes
+//    to bf16 with the block scale applied (v_cvt_scalef32_pk_bf16_fp4 for
+//    e8m0; unscaled conversion, f32 product and bf16 rounding for NVFP4);
+//    activation and weight use the same lane -> k assignment, so the
+//    products pair up whatever order the MFMA sums;
 //  * every operand of stage s+1 is read into the second register set during
 //    the MFMAs of stage s; the activation rows are stored with the 16-byte
 //    chunk c of row r at slot c ^ ((r & 7) ^ ((r >> 3) & 1)) so that the
@@ -76,7 +79,7 @@ __device__ __forceinline__ bf16x8 as_bf16x8_u4(const uint4& x) {
   return c.v;
 }
 
-template <int BM, bool ACT>
+template <int BM, bool ACT, bool NV>
 __global__ __launch_bounds__(kThreads) void w4_gemm_kernel(const GemmParams p, int m_tiles, int n_tiles) {
   using S = W4Shape<BM>;
   constexpr int BN = kW4BN;
@@ -129,16 +132,17 @@ __global__ __launch_bounds__(kThreads) void w4_gemm_kernel(const GemmParams p, i
   // ---- LDS copies (16 bytes per lane) ----
   // activations: one instruction = 8 rows x 128 bytes (lane -> row l >> 3,
   // slot l & 7, fetching the chunk that the row's swizzle stores there);
-  // codes: 32 rows x 32 bytes (lane -> row l >> 1, half l & 1). Scale bytes:
-  // lane (row l % 32, half h) of weight block i needs byte 2*stage + h of
-  // its row.
+  // codes: 32 rows x 32 bytes (lane -> row l >> 1, half l & 1). Scales:
+  // lane (row l % 32, half h) of weight block i needs e8m0 byte 2*stage + h
+  // of its row (NVFP4: bf16 scales 4*stage + 2h and + 1, one 4-byte load).
+  constexpr int kSB = NV ? 2 : 1;  // bytes per scale
   constexpr int XI = BM / 32;  // activation copies per wavefront
   constexpr int WI = 2;        // code copies per wavefront
   const uint8_t* xbase = static_cast<const uint8_t*>(p.a);
   const uint8_t* wbase = p.w + (int64_t)g * p.w_gstride;
   const rsrc_t eres = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<void*>(static_cast<const void*>(static_cast<const uint8_t*>(p.w_scale) + (int64_t)g * p.ws_gstride)),
-      (short)0, (int)std::min<int64_t>((int64_t)p.N * p.ldws, 0x7fffffff), 0x00020000);
+      const_cast<void*>(static_cast<const void*>(static_cast<const uint8_t*>(p.w_scale) + (int64_t)g * p.ws_gstride * kSB)),
+      (short)0, (int)std::min<int64_t>((int64_t)p.N * p.ldws * kSB, 0x7fffffff), 0x00020000);
   const uint64_t lda_b = (uint64_t)p.lda * 2;
   uint32_t xrow[XI], woff[WI];
   int xcx[XI];
@@ -164,8 +168,9 @@ __global__ __launch_bounds__(kThreads) void w4_gemm_kernel(const GemmParams p, i
   auto wrow = [&](int i) { return tile_wrow<BN, TN, NI, ACT>(wn, i); };
   uint32_t eoff[NI];
 #pragma unroll
-  for (int i = 0; i < NI; ++i) eoff[i] = (uint32_t)wrow_global(wrow(i) + rl) * (uint32_t)p.ldws + kh;
-  uint32_t we[4][NI];  // e8m0 bytes of the stages in flight (stage s in set s % 4)
+  for (int i = 0; i < NI; ++i)
+    eoff[i] = (uint32_t)wrow_global(wrow(i) + rl) * (uint32_t)(p.ldws * kSB) + (NV ? kh * 4 : kh);
+  uint32_t we[4][NI];  // scales of the stages in flight (stage s in set s % 4)
   auto copy_stage = [&](uint8_t* dA, uint8_t* dW, int e, int ks) {
     const uint32_t st = (uint32_t)(u0 + ks);
 #pragma unroll
@@ -182,7 +187,10 @@ __global__ __launch_bounds__(kThreads) void w4_gemm_kernel(const GemmParams p, i
       __builtin_amdgcn_global_load_lds(src, QMOE_LDS(dA + (wave + 4 * j) * 1024), 16, 0, 0);
     }
 #pragma unroll
-    for (int i = 0; i < NI; ++i) we[e][i] = __builtin_amdgcn_raw_buffer_load_b8(eres, eoff[i], st * 2u, 0);
+    for (int i = 0; i < NI; ++i) {
+      if constexpr (NV) we[e][i] = __builtin_amdgcn_raw_buffer_load_b32(eres, eoff[i], st * 8u, 0);
+      else we[e][i] = __builtin_amdgcn_raw_buffer_load_b8(eres, eoff[i], st * 2u, 0);
+    }
   };
 
   // ---- operands of one stage into register set t ----
@@ -215,16 +223,24 @@ __global__ __launch_bounds__(kThreads) void w4_gemm_kernel(const GemmParams p, i
   // k-step outer, blocks inner: consecutive MFMAs go to different
   // accumulators, and a step's expansions overlap the previous step's MFMAs
   auto mma_stage = [&](int t, const uint32_t (&eb)[NI]) {
-    float scale[NI];
+    float scale[NI], scale1[NI];  // NVFP4: scale for 16-k steps 0-1, scale1 for 2-3
 #pragma unroll
-    for (int i = 0; i < NI; ++i) scale[i] = e8m0_to_f32(eb[i]);
+    for (int i = 0; i < NI; ++i) {
+      if constexpr (NV) {
+        scale[i] = bits_f32(eb[i] << 16);
+        scale1[i] = bits_f32(eb[i] & 0xffff0000u);
+      } else {
+        scale[i] = e8m0_to_f32(eb[i]);
+      }
+    }
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       bf16x8 wv[NI];
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
         const uint32_t d = q == 0 ? wc[t][i].x : (q == 1 ? wc[t][i].y : (q == 2 ? wc[t][i].z : wc[t][i].w));
-        wv[i] = w4_expand(d, scale[i]);
+        if constexpr (NV) wv[i] = as_bf16x8_u4(nvfp4x8_to_bf16(d, q < 2 ? scale[i] : scale1[i]));
+        else wv[i] = w4_expand(d, scale[i]);
       }
 #pragma unroll
       for (int i = 0; i < NI; ++i)
@@ -303,26 +319,33 @@ __global__ __launch_bounds__(kThreads) void w4_gemm_kernel(const GemmParams p, i
                                         n0, nlim, rows, wn, wm, lane);
 }
 
-template <int BM, bool ACT>
+template <int BM, bool ACT, bool NV>
 void w4_launch_shape(const GemmParams& p, hipStream_t st) {
   const int nout = ACT ? p.N / 2 : p.N;
   const int n_tiles = cdiv(nout, ACT ? kW4BN / 2 : kW4BN);
   const unsigned ks = (unsigned)std::max(1, p.ksplit);
   if (p.group_offs) {
     const int m_tiles = cdiv(p.M, BM) + std::min(p.slots, p.M);
-    hipLaunchKernelGGL((w4_gemm_kernel<BM, ACT>), dim3(n_tiles, m_tiles, ks), dim3(kThreads), 0, st, p, m_tiles,
-                       n_tiles);
+    hipLaunchKernelGGL((w4_gemm_kernel<BM, ACT, NV>), dim3(n_tiles, m_tiles, ks), dim3(kThreads), 0, st, p,
+                       m_tiles, n_tiles);
   } else {
     const int m_tiles = cdiv(p.M, BM);
     const int grid = cdiv(m_tiles * n_tiles, kXcds) * kXcds;
-    hipLaunchKernelGGL((w4_gemm_kernel<BM, ACT>), dim3(grid, 1, ks), dim3(kThreads), 0, st, p, m_tiles, n_tiles);
+    hipLaunchKernelGGL((w4_gemm_kernel<BM, ACT, NV>), dim3(grid, 1, ks), dim3(kThreads), 0, st, p, m_tiles,
+                       n_tiles);
   }
 }
 
-template <int BM>
+template <int BM, bool NV>
 void w4_launch_act(const GemmParams& p, hipStream_t st) {
-  if (p.act != QA_NONE) w4_launch_shape<BM, true>(p, st);
-  else w4_launch_shape<BM, false>(p, st);
+  if (p.act != QA_NONE) w4_launch_shape<BM, true, NV>(p, st);
+  else w4_launch_shape<BM, false, NV>(p, st);
+}
+
+template <int BM>
+void w4_launch_fmt(const GemmParams& p, bool nv, hipStream_t st) {
+  if (nv) w4_launch_act<BM, true>(p, st);
+  else w4_launch_act<BM, false>(p, st);
 }
 
 }  // namespace
@@ -331,15 +354,18 @@ void w4_launch_act(const GemmParams& p, hipStream_t st) {
 // rows, even scale rows, codes < 4 GiB per group), and its plan: token-tile
 // height (the largest of 128 / 64 / 32 that still fills the CUs, or that fits
 // the average group), K split (dense problems with few tiles) and the f32
-// workspace the split needs ([ksplit][M][N]).
-bool qmoe_w4_plan(const GemmParams& p, int* bm_out, int* ksplit_out, int64_t* ws_bytes) {
+// workspace the split needs ([ksplit][M][N]). `nv`: NVFP4 (bf16 scales per
+// 16 k) instead of MXFP4 (e8m0 per 32 k).
+bool qmoe_w4_plan(const GemmParams& p, bool nv, int* bm_out, int* ksplit_out, int64_t* ws_bytes) {
   if (p.M <= 0 || p.K <= 0 || (p.K % 64) != 0 || p.N <= 0) return false;
   if (p.act != QA_NONE && (p.N % 2) != 0) return false;
   if ((p.lda % 8) != 0 || (p.ldw % 16) != 0 || (p.ldws % 2) != 0) return false;
+  const int sal = nv ? 3 : 1;  // scale alignment mask: 4-byte bf16 pairs, 2-byte e8m0 pairs
   if ((reinterpret_cast<uintptr_t>(p.a) & 15) || (reinterpret_cast<uintptr_t>(p.w) & 15) ||
-      (p.w_gstride % 16) != 0 || (reinterpret_cast<uintptr_t>(p.w_scale) & 1) || (p.ws_gstride % 2) != 0)
+      (p.w_gstride % 16) != 0 || (reinterpret_cast<uintptr_t>(p.w_scale) & sal) || (p.ws_gstride % 2) != 0)
     return false;
-  if ((int64_t)p.ldw * p.N >= ((int64_t)1 << 32) || (int64_t)p.ldws * p.N >= ((int64_t)1 << 32)) return false;
+  if ((int64_t)p.ldw * p.N >= ((int64_t)1 << 32) || (int64_t)p.ldws * (nv ? 2 : 1) * p.N >= ((int64_t)1 << 31))
+    return false;
   const int nout = p.act != QA_NONE ? p.N / 2 : p.N;
   const int n_tiles = cdiv(nout, p.act != QA_NONE ? kW4BN / 2 : kW4BN);
   int bm = 32;
@@ -376,19 +402,19 @@ bool qmoe_w4_plan(const GemmParams& p, int* bm_out, int* ksplit_out, int64_t* ws
 
 // Launch per the plan (the caller sized the workspace); with a K split the
 // finishing kernel runs the epilogue.
-int qmoe_w4_launch(GemmParams p, void* workspace, int64_t ws_bytes, hipStream_t st) {
+int qmoe_w4_launch(GemmParams p, bool nv, void* workspace, int64_t ws_bytes, hipStream_t st) {
   int bm = 0, ksplit = 1;
   int64_t need = 0;
-  if (!qmoe_w4_plan(p, &bm, &ksplit, &need)) return QMOE_ERR_ARG;
+  if (!qmoe_w4_plan(p, nv, &bm, &ksplit, &need)) return QMOE_ERR_ARG;
   p.ksplit = ksplit;
   if (ksplit > 1) {
     if (!workspace || ws_bytes < need) return QMOE_ERR_WORKSPACE;
     p.partial = static_cast<float*>(workspace);
   }
   switch (bm) {
-    case 128: w4_launch_act<128>(p, st); break;
-    case 64: w4_launch_act<64>(p, st); break;
-    default: w4_launch_act<32>(p, st); break;
+    case 128: w4_launch_fmt<128>(p, nv, st); break;
+    case 64: w4_launch_fmt<64>(p, nv, st); break;
+    default: w4_launch_fmt<32>(p, nv, st); break;
   }
   if (ksplit > 1) {
     const int nout = p.act != QA_NONE ? p.N / 2 : p.N;

@@ -19,7 +19,7 @@ STATUS_TEXT = {
 }
 
 # GEMM kinds / activations (include/qmoe.h)
-W8A8_PC, W8A8_BLK, W8A16_PC, W4A16_MX, W16A16 = range(5)
+W8A8_PC, W8A8_BLK, W8A16_PC, W4A16_MX, W16A16, W4A16_NV = range(6)
 ACT_NONE, ACT_SILU, ACT_SWIGLUOAI, ACT_GELU_TANH, ACT_SILU_CLAMP, ACT_SITU = range(6)
 
 _vp = ctypes.c_void_p

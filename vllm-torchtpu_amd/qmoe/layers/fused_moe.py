@@ -13,6 +13,7 @@ Weight formats (this package's runtime layouts, produced by the MoE methods'
 format                w1 [E, 2I, H...] / w2        scales
 ====================  ==========================  ====================================
 ``mxfp4``             uint8 packed e2m1 [., ., K/2]  e8m0 uint8 [E, N, K/32]
+``nvfp4``             uint8 packed e2m1 [., ., K/2]  bf16 [E, N, K/16] (fused e4m3 x global)
 ``fp8_block``         float8_e4m3fn [E, N, K]      f32 tile scales [E, N/128, K/128]
 ``fp8_block_rows``    float8_e4m3fn [E, N, K]      f32 per-(row, 128) scales [E, N, K/128]
 ``fp8`` / ``int8``    float8_e4m3fn / int8         f32 per-channel [E, N]
@@ -45,7 +46,7 @@ def infer_weight_format(w1: torch.Tensor, w1_scale) -> str:
             return "fp8_block_rows" if w1_scale.shape[1] == w1.shape[1] else "fp8_block"
         return "fp8"
     if w1.dtype == torch.uint8 or "float4" in str(w1.dtype):
-        return "mxfp4"
+        return "nvfp4" if w1_scale is not None and w1_scale.dtype == torch.bfloat16 else "mxfp4"
     raise ValueError(f"unsupported MoE weight dtype {w1.dtype}")
 
 
@@ -63,7 +64,7 @@ def fused_moe_gmm(hidden_states, w1, w2, w1_scale, w2_scale, w1_bias, w2_bias, t
     if rhs_quant_dtype is not None:
         raise NotImplementedError("packed int4 rhs_quant_dtype is not supported")
     fmt = weight_format or infer_weight_format(w1, w1_scale)
-    if fmt not in ("mxfp4", "bf16", "fp8_block", "fp8_block_rows", "fp8", "int8"):
+    if fmt not in ("mxfp4", "nvfp4", "bf16", "fp8_block", "fp8_block_rows", "fp8", "int8"):
         raise ValueError(f"unknown MoE weight format {fmt!r}")
     ops.act_code(activation)  # NotImplementedError for an unknown activation string
     T, H = hidden_states.shape
@@ -152,11 +153,13 @@ def _moe_body(x, w1, w2, w1_scale, w2_scale, w1_bias, w2_bias, tw, topk_ids, top
     b2 = w2_bias.float().reshape(E, -1).contiguous() if w2_bias is not None else None
     u8 = lambda t: t.view(torch.uint8)  # noqa: E731
 
-    if fmt == "mxfp4":
-        inter = ops.gemm(_capi.W4A16_MX, x, u8(w1), w_scale=u8(w1_scale), bias=b1,
+    if fmt in ("mxfp4", "nvfp4"):
+        kind = _capi.W4A16_MX if fmt == "mxfp4" else _capi.W4A16_NV
+        sc = u8 if fmt == "mxfp4" else (lambda t: t)  # noqa: E731
+        inter = ops.gemm(kind, x, u8(w1), w_scale=sc(w1_scale), bias=b1,
                          a_rows=meta["token_sorted"], activation=activation, **common)
-        a2, a2_scale, kind, wf, bn = inter, None, _capi.W4A16_MX, 0, 1
-        w2k, w2s = u8(w2), u8(w2_scale)
+        a2, a2_scale, wf, bn = inter, None, 0, 1
+        w2k, w2s = u8(w2), sc(w2_scale)
     elif fmt == "bf16":
         inter = ops.gemm(_capi.W16A16, x, w1, bias=b1, a_rows=meta["token_sorted"],
                          activation=activation, **common)

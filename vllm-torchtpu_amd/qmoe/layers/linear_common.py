@@ -151,32 +151,41 @@ def _(x2, w_nk, w_s, w8a16_max_rows):
 
 def quantized_matmul_fp4(x: torch.Tensor, w_q: torch.Tensor, w_s: torch.Tensor,
                          bias: torch.Tensor | None = None) -> torch.Tensor:
-    """MXFP4 W4A16 dense linear, `linear_common.py:188-209, 242-255`.
+    """FP4 W4A16 dense linear, `linear_common.py:188-209, 242-255`.
 
     ``w_q``: packed e2m1 codes, N-major ``[n_out, n_in/2]`` uint8 (the
-    checkpoint layout; low nibble = even k); ``w_s``: e8m0 bytes
-    ``[n_out, n_in/32]``. bf16 activations stay unquantized (block 32 is
-    below the reference's dequantize-after-matmul threshold), f32 accumulate.
+    checkpoint layout; low nibble = even k). ``w_s`` picks the format:
+    e8m0 bytes ``[n_out, n_in/32]`` (MXFP4), or bf16 / f32 block scales
+    ``[n_out, n_in/16]`` (NVFP4: the fused e4m3 x global scale; f32 values are
+    rounded to bf16, which is what the reference's in-kernel dequantization
+    does with them, `kernels/megablox/gmm_v2.py:452-462`). bf16 activations
+    stay unquantized (both blocks are below the reference's
+    dequantize-after-matmul threshold), f32 accumulate.
     """
+    nv = w_s.dtype in (torch.bfloat16, torch.float32)
+    blk = 16 if nv else 32
     if w_q.dim() != 2 or w_s.dim() != 2:
-        raise ValueError("quantized_matmul_fp4 expects w_q [n_out, n_in/2] and w_s [n_out, n_in/32]")
+        raise ValueError(f"quantized_matmul_fp4 expects w_q [n_out, n_in/2] and w_s [n_out, n_in/{blk}]")
     n_out = w_s.shape[0]
     k_dim = x.shape[-1]
-    if w_q.shape != (n_out, k_dim // 2) or w_s.shape[1] * 32 != k_dim:
+    if w_q.shape != (n_out, k_dim // 2) or w_s.shape[1] * blk != k_dim:
         raise ValueError(
-            f"MXFP4 weight {tuple(w_q.shape)} / scale {tuple(w_s.shape)} do not match input dim {k_dim}"
+            f"{'NVFP4' if nv else 'MXFP4'} weight {tuple(w_q.shape)} / scale {tuple(w_s.shape)} "
+            f"do not match input dim {k_dim}"
         )
     x2 = x.reshape(-1, k_dim)
     if x2.dtype != torch.bfloat16:
         x2 = x2.to(torch.bfloat16)
-    out = torch.ops.qmoe.quantized_matmul_fp4(x2, w_q.view(torch.uint8), w_s.view(torch.uint8), bias)
+    w_s = w_s.to(torch.bfloat16) if nv else w_s.view(torch.uint8)
+    out = torch.ops.qmoe.quantized_matmul_fp4(x2, w_q.view(torch.uint8), w_s, bias)
     return out.reshape(*x.shape[:-1], n_out)
 
 
 @torch.library.custom_op("qmoe::quantized_matmul_fp4", mutates_args=())
 def _quantized_matmul_fp4_op(x2: torch.Tensor, w_q: torch.Tensor, w_s: torch.Tensor,
                              bias: Optional[torch.Tensor]) -> torch.Tensor:
-    return ops.gemm(_capi.W4A16_MX, x2, w_q.contiguous(), w_scale=w_s.contiguous(), bias=bias)
+    kind = _capi.W4A16_NV if w_s.dtype == torch.bfloat16 else _capi.W4A16_MX
+    return ops.gemm(kind, x2, w_q.contiguous(), w_scale=w_s.contiguous(), bias=bias)
 
 
 @_quantized_matmul_fp4_op.register_fake

@@ -4,11 +4,13 @@ maps a checkpoint's ``quantization`` method name to the config class."""
 
 from qmoe.layers.quantization.fp8 import Fp8Config, Fp8LinearMethod, Fp8MoEMethod
 from qmoe.layers.quantization.mxfp4 import Mxfp4Config, Mxfp4LinearMethod, Mxfp4MoEMethod
+from qmoe.layers.quantization.nvfp4 import Nvfp4Config, Nvfp4LinearMethod, Nvfp4MoEMethod
 from qmoe.layers.quantization.unquantized import UnquantizedFusedMoEMethod, UnquantizedLinearMethod
 
 _CONFIGS = {
     "fp8": Fp8Config,
     "mxfp4": Mxfp4Config,
+    "modelopt_fp4": Nvfp4Config,
 }
 
 
@@ -24,6 +26,6 @@ def get_quantization_config(method: str):
 
 __all__ = [
     "Fp8Config", "Fp8LinearMethod", "Fp8MoEMethod", "Mxfp4Config", "Mxfp4LinearMethod",
-    "Mxfp4MoEMethod", "UnquantizedFusedMoEMethod", "UnquantizedLinearMethod",
+    "Mxfp4MoEMethod", "Nvfp4Config", "Nvfp4LinearMethod", "Nvfp4MoEMethod", "UnquantizedFusedMoEMethod", "UnquantizedLinearMethod",
     "get_quantization_config",
 ]
