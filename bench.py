@@ -47,7 +47,7 @@ def parse():
     ap.add_argument("--m", type=int, default=4096, help="tokens of the headline step")
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="", help="comma list of sweep configs to run (0-4)")
+    ap.add_argument("--only", default="", help="comma list of sweep configs to run (0-4; 5 = NVFP4)")
     ap.add_argument("--profile", nargs="?", const="headline", default=None,
                     choices=["headline", "decode", "moe"],
                     help="rocprofv3 targets: the headline kernel + a copy calibration (default), "
@@ -254,6 +254,62 @@ def moe_layer_cfg(topk, scoring, activation, bias=None, rsf=1.0, groups=None):
                            use_grouped_topk=groups is not None, num_expert_group=groups[0] if groups else 1,
                            topk_group=groups[1] if groups else 1, custom_routing_function=None,
                            _qmoe_activation=activation)
+
+
+def nvfp4_weights(shape, gen):
+    """NVFP4 codes + fused bf16 block scales (e4m3 block scale x a float32
+    global, as a ModelOpt checkpoint's load makes them)."""
+    import torch
+
+    *lead, N, K = shape
+    codes = torch.randint(0, 256, (*lead, N, K // 2), device="cuda", dtype=torch.uint8, generator=gen)
+    blk = torch.randint(0x20, 0x48, (*lead, N, K // 16), device="cuda", generator=gen).to(torch.uint8)
+    sc = (blk.view(torch.float8_e4m3fn).float() * 0.0123456789).to(torch.bfloat16)
+    return codes, sc
+
+
+def sweep_nvfp4(only):
+    """NVFP4 W4A16 (the reference's ModelOpt FP4 path) on the config-0 dense
+    and config-3 MoE shapes (silu: the reference's NVFP4 MoE takes no
+    swigluoai). Algorithmic scale bytes are the checkpoint's e4m3 bytes."""
+    import torch
+
+    from qmoe import ops
+    from qmoe.layers.fused_moe import moe_forward
+    from qmoe.layers.linear_common import quantized_matmul_fp4
+
+    out = []
+    if only and "5" not in only:
+        return out
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    K, N = 2880, 5760
+    codes, sc = nvfp4_weights((N, K), gen)
+    for M in (1, 16, 128, 4096):
+        x = torch.randn((M, K), device="cuda", generator=gen).to(torch.bfloat16)
+        us = graph_time_us(lambda: quantized_matmul_fp4(x, codes, sc))[0]
+        nbytes = N * K // 2 + N * K // 16 + 2 * M * K + 2 * M * N
+        out.append(dict(cfg=5, kind="nvfp4_w4a16", M=M, K=K, N=N, **roof(2.0 * M * N * K, nbytes, us, "bf16")))
+        log(out[-1])
+    E, k, H, I = 128, 4, 2880, 2880
+    w13, s13 = nvfp4_weights((E, 2 * I, H), gen)
+    w2, s2 = nvfp4_weights((E, H, I), gen)
+    per_expert = 3 * I * H // 2 + 3 * I * H // 16
+    lcfg = moe_layer_cfg(k, "softmax", "silu")
+    for T in (1, 16, 1024):
+        x = torch.randn((T, H), device="cuda", generator=gen).to(torch.bfloat16)
+        logits = torch.randn((T, E), device="cuda", generator=gen).to(torch.bfloat16)
+
+        def layer():
+            return moe_forward(lcfg, x, logits, w13, w2, s13, s2, None, None, "nvfp4")
+
+        us = graph_time_us(layer, iters=20)[0]
+        _, ids = ops.moe_route(logits, k, "softmax", True)
+        touched = int(torch.unique(ids).numel())
+        nbytes = touched * per_expert + 2 * T * H * 2 + 2 * T * E
+        out.append(dict(cfg=5, kind="moe_nvfp4", T=T, experts_touched=touched,
+                        **roof(T * k * 6.0 * H * I, nbytes, us, "bf16")))
+        log(out[-1])
+    return out
 
 
 def sweep_moe(only):
@@ -528,7 +584,7 @@ def main():
     }
     only = [c for c in args.only.split(",") if c]
     if not args.no_sweep:
-        res["sweep"] = sweep_linear(only) + sweep_moe(only)
+        res["sweep"] = sweep_linear(only) + sweep_moe(only) + sweep_nvfp4(only)
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline()
     print(json.dumps(res))
