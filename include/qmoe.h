@@ -10,7 +10,8 @@
  *   weights      [G][N][K]            N-major: each output channel's K contiguous
  *                                     (e2m1: [G][N][K/2], low nibble = even k)
  *   scales       per-channel f32 [G][N]; block f32 [G][N/bn][K/128];
- *                MX e8m0 bytes [G][N][K/32]; NVFP4 bf16 [G][N][K/16]
+ *                MX e8m0 bytes [G][N][K/32]; NVFP4 bf16 [G][N][K/16];
+ *                INT4 bf16 [G][N][K/wq_group]
  * Reference paths below are relative to the reference plugin's
  * src/vllm_torchtpu/.
  */
@@ -32,10 +33,15 @@ enum {
   QMOE_W8A16_PC = 2, /* A bf16; W e4m3 + per-channel scale */
   QMOE_W4A16_MX = 3, /* A bf16; W e2m1 + e8m0 scale per 32 k */
   QMOE_W16A16 = 4,   /* A bf16; W bf16 */
-  QMOE_W4A16_NV = 5  /* A bf16; W e2m1 + bf16 scale per 16 k (NVFP4: the checkpoint's e4m3
+  QMOE_W4A16_NV = 5, /* A bf16; W e2m1 + bf16 scale per 16 k (NVFP4: the checkpoint's e4m3
                         block scale times its f32 global scale, rounded to bf16 as the
                         reference's `kernels/megablox/gmm_v2.py:452-462` dequantization
                         does; each weight is bf16(code * scale)) */
+  QMOE_W4A16_I4 = 6  /* A bf16; W symmetric 4-bit integers in the compressed-tensors
+                        encoding (nibble = value + 8, two per byte, even k in the low
+                        nibble: the int32 carriers of `compressed_tensors_moe_w4a16.py`
+                        read as bytes) + bf16 scale per wq_group k; each weight is
+                        bf16(value * scale), `kernels/megablox/gmm_v2.py:452-462` */
 };
 
 /* Fused gate/up activations (qmoe_gemm_desc.act) */
@@ -87,6 +93,7 @@ typedef struct qmoe_gemm_desc {
   void* y;                /* bf16 output */
   int64_t ldy;
   const int32_t* y_rows;  /* optional scatter map [M] */
+  int32_t wq_group;       /* QMOE_W4A16_I4: k values per scale (32, 64 or 128) */
 } qmoe_gemm_desc;
 
 /* ABI revision of this header (bumped on any layout change). */

@@ -184,3 +184,42 @@ def dequant_nvfp4(packed, scales_f32) -> np.ndarray:
     blk = k // s.shape[-1]
     prod = vals.reshape(*vals.shape[:-1], s.shape[-1], blk) * s[..., None]
     return bf16_round(prod.reshape(*vals.shape[:-2], n, k).astype(np.float32))
+
+
+# ---------------------------------------------------------------- INT4 (compressed-tensors)
+
+
+def int4_pack(values) -> np.ndarray:
+    """Symmetric int4 values [..., K] (-8..7) -> int32 carriers [..., K/8] in
+    the compressed-tensors encoding the reference's test builds
+    (`tests/kernels/test_gmm_v2.py:445-452`): nibble = (v + 8) & 15, value
+    8j + i of a row in bits 4i..4i+3 of carrier j."""
+    v = np.asarray(values, np.int64)
+    u = (v + 8) & 0xF
+    u = u.reshape(*u.shape[:-1], u.shape[-1] // 8, 8)
+    words = np.sum(u << (4 * np.arange(8, dtype=np.int64)), axis=-1)
+    return words.astype(np.uint32).view(np.int32)
+
+
+def int4_unpack(carriers) -> np.ndarray:
+    """int32 carriers [..., K/8] (or their bytes, uint8 [..., K/2]) -> int4
+    values [..., K] as float32 (nibble - 8)."""
+    c = np.ascontiguousarray(carriers)
+    b = c.view(np.uint8) if c.dtype != np.uint8 else c  # little-endian: carrier j = bytes 4j..4j+3
+    lo, hi = b & 0xF, b >> 4
+    nib = np.stack([lo, hi], axis=-1).reshape(*b.shape[:-1], b.shape[-1] * 2)
+    return nib.astype(np.float32) - 8.0
+
+
+def dequant_int4(carriers, scales) -> np.ndarray:
+    """INT4 weights + bf16-valued scales [..., N, K/group] -> the bf16 weights
+    (as float32) the reference multiplies with: groups below 256 k are
+    dequantized in the bf16 activation dtype, `int4.astype(bf16) * scale`
+    (`kernels/megablox/gmm_v2.py:452-462`, the expected value of
+    `tests/kernels/test_gmm_v2.py:434`), one bf16 rounding of the product."""
+    vals = int4_unpack(carriers)
+    s = bf16_round(np.asarray(scales, np.float32))
+    n, k = vals.shape[-2], vals.shape[-1]
+    grp = k // s.shape[-1]
+    prod = vals.reshape(*vals.shape[:-1], s.shape[-1], grp) * s[..., None]
+    return bf16_round(prod.reshape(*vals.shape[:-2], n, k).astype(np.float32))

@@ -7,7 +7,7 @@ same sums. Test infrastructure only.
 
 import numpy as np
 
-from oracle.codecs import bf16_round, dequant_mxfp4, dequant_nvfp4, e4m3_decode
+from oracle.codecs import bf16_round, dequant_int4, dequant_mxfp4, dequant_nvfp4, e4m3_decode
 from oracle.quant import dequant_codes, quantize_act
 
 
@@ -94,6 +94,16 @@ def w4a16_nvfp4(x, packed, scales_f32, bias=None):
     -> `quantized_matmul_fp4` -> gmm_v2 with block 16: the rhs is dequantized
     to bf16 as ``dequant_nvfp4`` states, bf16 x, f32 accumulation, bf16 out)."""
     out = _mm(x, dequant_nvfp4(packed, scales_f32))
+    if bias is not None:
+        out = out + np.asarray(bias, np.float32)[None, :]
+    return bf16_round(out)
+
+
+def w4a16_int4(x, carriers, scales, bias=None):
+    """Packed-int4 weight x bf16 activation (gmm_v2 with ``rhs_quant_dtype``
+    int4 and a group below 256: ``dequant_int4`` weights, bf16 x, f32
+    accumulation, bf16 out)."""
+    out = _mm(x, dequant_int4(carriers, scales))
     if bias is not None:
         out = out + np.asarray(bias, np.float32)[None, :]
     return bf16_round(out)

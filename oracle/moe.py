@@ -5,7 +5,7 @@ Test infrastructure only.
 
 import numpy as np
 
-from oracle.codecs import bf16_round, dequant_mxfp4, dequant_nvfp4, e4m3_decode
+from oracle.codecs import bf16_round, dequant_int4, dequant_mxfp4, dequant_nvfp4, e4m3_decode
 from oracle.linear import _mm
 from oracle.quant import quantize_act
 
@@ -87,10 +87,11 @@ class ExpertWeights:
     fmt:
       "mxfp4": w13 packed u8 [E, 2I, H/2] + e8m0 [E, 2I, H/32]; w2 [E, H, I/2] + [E, H, I/32]
       "nvfp4": w13 packed u8 [E, 2I, H/2] + f32 fused scales [E, 2I, H/16]; w2 likewise
+      "int4": w13 int32 carriers [E, 2I, H/8] + bf16-valued scales [E, 2I, H/group]; w2 likewise
       "fp8_block": w13 e4m3 [E, 2I, H] + tile scale_inv [E, 2I/128, H/128]; w2 likewise
       "fp8": w13 e4m3 [E, 2I, H] + per-channel scale [E, 2I]; w2 [E, H, I] + [E, H]
       "bf16": w13 [E, 2I, H] f32 (bf16 values); w2 [E, H, I]
-    Activations: bf16 for mxfp4/nvfp4/bf16 (W4A16 / W16A16); per-(row, 128) e4m3 for
+    Activations: bf16 for mxfp4/nvfp4/int4/bf16 (W4A16 / W16A16); per-(row, 128) e4m3 for
     fp8_block (the blockwise W8A8 recipe of config 4); per-row e4m3 for fp8
     (each expert GEMM is `kernels/quantized_matmul/util.py:80-124`, the
     per-channel W8A8 recipe, restated in ``linear.w8a8_per_channel``).
@@ -112,6 +113,8 @@ class ExpertWeights:
                 d = dequant_mxfp4(w, s)
             elif self.fmt == "nvfp4":
                 d = dequant_nvfp4(w, s)
+            elif self.fmt == "int4":
+                d = dequant_int4(w, s)
             elif self.fmt in ("fp8_block", "fp8"):
                 d = e4m3_decode(w)
             else:

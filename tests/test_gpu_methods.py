@@ -285,3 +285,37 @@ def test_nvfp4_moe_from_checkpoint(dev, T):
     tw, ids = routing.select_experts(logits, k, True, "softmax")
     ref, _, _ = omoe.fused_moe(x, omoe.ExpertWeights("nvfp4", c13, s13, c2, s2), tw, ids, "silu")
     assert_close_rows(got.float().cpu().numpy(), ref, "nvfp4 moe method")
+
+
+@pytest.mark.parametrize("T,group", [(4, 32), (150, 128)])
+def test_compressed_tensors_int4_moe_from_checkpoint(dev, T, group):
+    """Compressed-tensors packed-INT4 W4A16 MoE (`compressed_tensors_moe_w4a16.py`):
+    int32 carriers + bf16 group scales as loaded, silu; T = 4 takes the fused
+    routing + streaming path, T = 150 the tiled kernels."""
+    from qmoe.layers import quantization as q
+
+    print(f"ct int4 moe method T={T} group={group}", flush=True)
+    rng = np.random.default_rng(31 + T)
+    E, H, I, k = 8, 512, 256, 2
+    layer = _moe_layer(k, "silu")
+    cfg = q.CompressedTensorsConfig.from_config({"config_groups": {"group_0": {
+        "weights": {"num_bits": 4, "type": "int", "symmetric": True, "strategy": "group", "group_size": group},
+        "input_activations": None, "targets": ["Linear"]}}, "ignore": ["lm_head"]})
+    method = cfg.get_quant_method(layer, prefix="model.layers.0.mlp.experts")
+    method.create_weights(layer, E, H, I, torch.bfloat16)
+    v13 = rng.integers(-8, 8, (E, 2 * I, H))
+    v2 = rng.integers(-8, 8, (E, H, I))
+    s13 = codecs.bf16_round((rng.random((E, 2 * I, H // group)) * 0.004 + 0.001).astype(np.float32))
+    s2 = codecs.bf16_round((rng.random((E, H, I // group)) * 0.004 + 0.001).astype(np.float32))
+    layer.w13_weight_packed.data = _t(codecs.int4_pack(v13), dev)
+    layer.w2_weight_packed.data = _t(codecs.int4_pack(v2), dev)
+    layer.w13_weight_scale.data = _t(s13, dev, torch.bfloat16)
+    layer.w2_weight_scale.data = _t(s2, dev, torch.bfloat16)
+    method.process_weights_after_loading(layer)
+    x = codecs.bf16_round(rng.standard_normal((T, H)).astype(np.float32))
+    logits = codecs.bf16_round(rng.standard_normal((T, E)).astype(np.float32))
+    got = method.apply_monolithic(layer, _t(x, dev, torch.bfloat16), _t(logits, dev, torch.bfloat16))
+    tw, ids = routing.select_experts(logits, k, True, "softmax")
+    ref, _, _ = omoe.fused_moe(x, omoe.ExpertWeights("int4", codecs.int4_pack(v13), s13, codecs.int4_pack(v2), s2),
+                               tw, ids, "silu")
+    assert_close_rows(got.float().cpu().numpy(), ref, "ct int4 moe method")

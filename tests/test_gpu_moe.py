@@ -123,6 +123,12 @@ def _moe_case(fmt, E, k, H, I, T, seed, bias=False):
         b2s = rng.integers(0x20, 0x40, (E, H, I // 16)).astype(np.uint8)
         s13 = codecs.nvfp4_fuse_scales(b13s, (rng.random((E, 2)) * 0.01 + 0.003).astype(np.float32), halves=True)
         s2 = codecs.nvfp4_fuse_scales(b2s, (rng.random(E) * 0.01 + 0.003).astype(np.float32))
+    elif fmt.startswith("int4"):  # "int4-<group>": int32 carriers + bf16-valued group scales
+        g = int(fmt.split("-")[1])
+        w13 = codecs.int4_pack(rng.integers(-8, 8, (E, 2 * I, H)))
+        w2 = codecs.int4_pack(rng.integers(-8, 8, (E, H, I)))
+        s13 = codecs.bf16_round((rng.random((E, 2 * I, H // g)) * 0.004 + 0.001).astype(np.float32))
+        s2 = codecs.bf16_round((rng.random((E, H, I // g)) * 0.004 + 0.001).astype(np.float32))
     elif fmt == "fp8_block":
         w13f = (rng.standard_normal((E, 2 * I, H)) * 0.02).astype(np.float32)
         w2f = (rng.standard_normal((E, H, I)) * 0.02).astype(np.float32)
@@ -151,6 +157,10 @@ def _moe_case(fmt, E, k, H, I, T, seed, bias=False):
     ("nvfp4", "silu", 16, 4, 512, 384, 40, False),
     ("nvfp4", "gelu_tanh", 16, 4, 512, 256, 300, False),  # tiled path
     ("nvfp4", "silu", 8, 2, 288, 160, 6, False),          # K % 64 == 32 in both GEMMs
+    ("int4-32", "silu", 8, 2, 256, 256, 1, False),
+    ("int4-128", "silu", 16, 4, 512, 384, 40, False),
+    ("int4-64", "silu", 16, 4, 512, 256, 300, False),      # tiled path
+    ("int4-32", "silu", 8, 2, 288, 160, 6, False),         # K % 64 == 32 in both GEMMs
     ("fp8_block", "silu", 8, 2, 512, 256, 5, False),
     ("fp8_block", "silu", 16, 4, 512, 256, 200, False),   # tiled path
     ("bf16", "silu", 8, 2, 256, 128, 9, False),
@@ -161,8 +171,8 @@ def test_fused_moe_layer(dev, fmt, act, E, k, H, I, T, bias):
 
     print(f"fused moe {fmt} {act} E={E} k={k} H={H} I={I} T={T} bias={bias}", flush=True)
     w13, s13, w2, s2, b13, b2, hid, ids, tw = _moe_case(fmt, E, k, H, I, T, seed=E + T + H)
-    ref, _, _ = omoe.fused_moe(hid, omoe.ExpertWeights(fmt if fmt != "bf16" else "bf16", w13, s13, w2, s2,
-                                                      b13, b2), tw, ids, act)
+    ofmt = "int4" if fmt.startswith("int4") else fmt
+    ref, _, _ = omoe.fused_moe(hid, omoe.ExpertWeights(ofmt, w13, s13, w2, s2, b13, b2), tw, ids, act)
     wdt = torch.float8_e4m3fn if fmt == "fp8_block" else (torch.bfloat16 if fmt == "bf16" else None)
 
     def wt(a):
@@ -171,13 +181,13 @@ def test_fused_moe_layer(dev, fmt, act, E, k, H, I, T, bias):
             return t.view(torch.float8_e4m3fn)
         return t.to(wdt) if wdt is not None else t
 
-    sdt = torch.bfloat16 if fmt == "nvfp4" else None  # NVFP4 runtime scales are bf16
+    sdt = torch.bfloat16 if fmt == "nvfp4" or ofmt == "int4" else None  # NVFP4 / INT4 runtime scales: bf16
     got = fused_moe_gmm(
         _t(hid, dev, torch.bfloat16), wt(w13), wt(w2),
         _t(s13, dev, sdt) if s13 is not None else None, _t(s2, dev, sdt) if s2 is not None else None,
         _t(b13, dev) if b13 is not None else None, _t(b2, dev) if b2 is not None else None,
         _t(tw, dev, torch.bfloat16), _t(ids, dev), None, k, act,
-        weight_format=fmt,
+        weight_format=ofmt,
     )
     assert_close_rows(got.float().cpu().numpy(), ref, f"moe {fmt}")
 

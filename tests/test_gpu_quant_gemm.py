@@ -264,6 +264,56 @@ def test_w4a16_nvfp4_dequant_bit_exact(dev, M, K, N):
     np.testing.assert_array_equal(y.float().cpu().numpy(), want)
 
 
+def _int4_case(rng, n, k, group):
+    """Packed-int4 weights (int32 carriers, compressed-tensors encoding) and
+    bf16-valued group scales."""
+    carriers = codecs.int4_pack(rng.integers(-8, 8, (n, k)))
+    sc = codecs.bf16_round((rng.random((n, k // group)) * 0.02 + 0.002).astype(np.float32))
+    return carriers, sc
+
+
+@pytest.mark.parametrize("M,K,N,group", [(1, 2880, 5760, 32), (16, 4096, 1024, 128), (5, 512, 200, 64),
+                                         # K % 128 != 0: the streaming kernel's tail step
+                                         (3, 2848, 200, 32), (7, 96, 130, 32), (2, 320, 64, 64),
+                                         # tiled kernel (groups straddle and fill 64-k stages)
+                                         (300, 2880, 768, 32), (520, 1024, 512, 128), (200, 4096, 1024, 64),
+                                         # K % 64 == 32 above the streaming bound: 64-row streaming passes
+                                         (70, 2848, 300, 32)])
+def test_w4a16_int4(dev, M, K, N, group):
+    from qmoe import _capi, ops
+
+    print(f"w4a16 int4 M={M} K={K} N={N} group={group}", flush=True)
+    rng = np.random.default_rng(M + K + N + group)
+    carriers, sc = _int4_case(rng, N, K, group)
+    x = _bf16(rng, (M, K))
+    bias = (rng.standard_normal(N) * 0.1).astype(np.float32)
+    ref = linear.w4a16_int4(x, carriers, sc, bias)
+    y = ops.gemm(_capi.W4A16_I4, _t(x, dev, torch.bfloat16), _t(carriers, dev).view(torch.uint8),
+                 w_scale=_t(sc, dev, torch.bfloat16), bias=_t(bias, dev))
+    assert_close_rows(y.float().cpu().numpy(), ref, f"int4 {M}x{K}x{N} g{group}")
+
+
+@pytest.mark.parametrize("M,K,N,group", [(16, 2048, 320, 32), (16, 4096, 256, 128), (256, 4096, 512, 64),
+                                         (256, 2048, 256, 128)])
+def test_w4a16_int4_dequant_bit_exact(dev, M, K, N, group):
+    """One-hot activation rows read single dequantized weights back (as for
+    NVFP4): bf16(value * scale) exactly, through the streaming (M = 16) and
+    the tiled (M = 256) kernel."""
+    from qmoe import _capi, ops
+
+    print(f"w4a16 int4 one-hot M={M} K={K} N={N} group={group}", flush=True)
+    rng = np.random.default_rng(K + N + group)
+    carriers, sc = _int4_case(rng, N, K, group)
+    sc = codecs.bf16_round(sc * np.float32(1.0 + 3.0 / 512))  # mantissas that make products round
+    ks = (np.arange(M) * (K // M) + np.arange(M) * 7) % K
+    x = np.zeros((M, K), np.float32)
+    x[np.arange(M), ks] = 1.0
+    y = ops.gemm(_capi.W4A16_I4, _t(x, dev, torch.bfloat16), _t(carriers, dev).view(torch.uint8),
+                 w_scale=_t(sc, dev, torch.bfloat16))
+    want = codecs.dequant_int4(carriers, sc)[:, ks].T
+    np.testing.assert_array_equal(y.float().cpu().numpy(), want)
+
+
 @pytest.mark.parametrize("M,K,N", [(1, 2880, 5760), (16, 2880, 5760), (128, 2880, 1440),
                                    (5, 512, 200), (90, 1024, 96),
                                    # K % 256 = 32, 160 and K < 256: every partial last step pair

@@ -144,3 +144,44 @@ def test_nvfp4_load_time_guards(monkeypatch):
     m, moe = moe_method()
     with pytest.raises(NotImplementedError, match="MOE_REQUANTIZE_BLOCK_SIZE"):
         m.process_weights_after_loading(moe)
+
+
+def test_compressed_tensors_int4_dispatch_shapes_and_guards(monkeypatch):
+    """Compressed-tensors packed-INT4 W4A16 MoE: checkpoint parameter shapes
+    (`compressed_tensors_moe_w4a16.py:172-260`) and the reference's scheme
+    errors (`:142-170`), raised before any device work."""
+    def cfg(**w):
+        args = {"num_bits": 4, "type": "int", "symmetric": True, "strategy": "group", "group_size": 32}
+        args.update(w)
+        return q.CompressedTensorsConfig.from_config({"config_groups": {"g": {"weights": args}},
+                                                      "ignore": ["lm_head"]})
+
+    assert q.get_quantization_config("compressed-tensors") is q.CompressedTensorsConfig
+    m = cfg().get_quant_method(_moe_layer(), "model.layers.0.mlp.experts")
+    assert isinstance(m, q.CompressedTensorsW4A16MoEMethod) and m.packed_factor == 8
+    assert isinstance(cfg().get_quant_method(torch.nn.Module(), "lm_head"), q.UnquantizedLinearMethod)
+    with pytest.raises(NotImplementedError):
+        cfg().get_quant_method(torch.nn.Module(), "model.layers.0.self_attn.q_proj")
+    moe = _moe_layer()
+    m.create_weights(moe, 4, 256, 128, torch.bfloat16)
+    assert moe.w13_weight_packed.shape == (4, 256, 32) and moe.w13_weight_packed.dtype == torch.int32
+    assert moe.w2_weight_packed.shape == (4, 256, 16)
+    assert moe.w13_weight_scale.shape == (4, 256, 8) and moe.w2_weight_scale.shape == (4, 256, 4)
+    with pytest.raises(NotImplementedError, match="integer INT4 weights only"):
+        cfg(type="float").get_quant_method(_moe_layer()).create_weights(_moe_layer(), 4, 256, 128, torch.bfloat16)
+    with pytest.raises(NotImplementedError, match="symmetric INT4 only"):
+        cfg(symmetric=False).get_quant_method(_moe_layer()).create_weights(_moe_layer(), 4, 256, 128,
+                                                                           torch.bfloat16)
+    with pytest.raises(ValueError, match="must be divisible by group_size"):
+        cfg().get_quant_method(_moe_layer()).create_weights(_moe_layer(), 4, 256, 144, torch.bfloat16)
+    with pytest.raises(NotImplementedError, match="channel"):
+        cfg(strategy="channel").get_quant_method(_moe_layer()).create_weights(_moe_layer(), 4, 256, 128,
+                                                                              torch.bfloat16)
+    bad = _moe_layer()
+    m.create_weights(bad, 4, 256, 128, torch.bfloat16)
+    bad.w13_weight_packed = torch.nn.Parameter(torch.empty(4, 256, 128, dtype=torch.uint8), requires_grad=False)
+    with pytest.raises(NotImplementedError, match="packed in INT32"):
+        m.process_weights_after_loading(bad)
+    monkeypatch.setenv("MOE_REQUANTIZE_WEIGHT_DTYPE", "fp4")
+    with pytest.raises(NotImplementedError, match="MOE_REQUANTIZE"):
+        m.process_weights_after_loading(moe)

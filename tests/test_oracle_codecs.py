@@ -165,3 +165,38 @@ def test_nvfp4_dequant_with_power_of_two_scales_is_the_mxfp4_dequant():
     nv = codecs.dequant_nvfp4(packed, s16)
     np.testing.assert_array_equal(nv[:, 16:32], mx[:, 16:32] * 2)
     np.testing.assert_array_equal(nv[:, :16], mx[:, :16])
+
+
+# ---------------------------------------------------------------- INT4
+
+
+def test_int4_packing_is_the_reference_tests_encoding():
+    """`tests/kernels/test_gmm_v2.py:445-455`: nibble = (v + 8) & 15 at bits
+    4i of carrier j for value 8j + i; XOR 0x88888888 turns the carriers into
+    two's complement nibbles (what the reference's load hands to jnp.int4)."""
+    vals = np.array([[-8, -1, 0, 1, 7, 3, -5, 2, 6, -7, 5, -2, 4, -3, -4, -6]], np.int64)
+    c = codecs.int4_pack(vals)
+    assert c.dtype == np.int32 and c.shape == (1, 2)
+    # carrier 0: nibbles 0, 7, 8, 9, 15, 11, 3, 10 (low first)
+    assert int(c[0, 0]) & 0xFFFFFFFF == 0xA3BF9870
+    np.testing.assert_array_equal(codecs.int4_unpack(c), vals.astype(np.float32))
+    np.testing.assert_array_equal(codecs.int4_unpack(c.view(np.uint8)), vals.astype(np.float32))
+    x = (c.view(np.uint32) ^ np.uint32(0x88888888))
+    nib = np.stack([(x >> (4 * i)) & 0xF for i in range(8)], axis=-1).reshape(1, 16).astype(np.int64)
+    np.testing.assert_array_equal(np.where(nib >= 8, nib - 16, nib), vals)
+
+
+def test_int4_dequant_rounds_the_bf16_product():
+    """int4.astype(bf16) * bf16 scale (`tests/kernels/test_gmm_v2.py:434`):
+    7 x 1.0078125 = 7.0546875 rounds up to 7.0625; -3 x 1.0078125 =
+    -3.0234375 is a tie that goes to the even neighbour -3.03125; a scale that
+    is not bf16 rounds first (1.005859375 -> 1.0078125)."""
+    def one(v, scale):
+        c = codecs.int4_pack(np.array([[v] * 32], np.int64))
+        return codecs.dequant_int4(c, np.array([[scale]], np.float32))[0, 0]
+
+    assert one(7, 1.0078125) == np.float32(7.0625)
+    assert one(-3, 1.0078125) == np.float32(-3.03125)
+    assert one(1, 1.005859375) == np.float32(1.0078125)
+    assert one(-8, 0.5) == np.float32(-4.0)
+    assert one(0, 3.0) == np.float32(0.0)

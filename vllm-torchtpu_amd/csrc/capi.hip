@@ -15,8 +15,8 @@ int qmoe_skinny_launch(int kind, GemmParams p, int max_rows, int slots, void* wo
 int qmoe_tiled_launch(int kind, GemmParams p, hipStream_t st);
 bool qmoe_f8_plan(const GemmParams& p, bool blk, int* bm_out, int* ksplit_out, int64_t* ws_bytes);
 int qmoe_f8_launch(GemmParams p, bool blk, void* workspace, int64_t ws_bytes, hipStream_t st);
-bool qmoe_w4_plan(const GemmParams& p, bool nv, int* bm_out, int* ksplit_out, int64_t* ws_bytes);
-int qmoe_w4_launch(GemmParams p, bool nv, void* workspace, int64_t ws_bytes, hipStream_t st);
+bool qmoe_w4_plan(const GemmParams& p, int fmt, int* bm_out, int* ksplit_out, int64_t* ws_bytes);
+int qmoe_w4_launch(GemmParams p, int fmt, void* workspace, int64_t ws_bytes, hipStream_t st);
 
 namespace {
 
@@ -26,7 +26,7 @@ constexpr int kSkinnyMaxRowsW8A8 = 32;
 
 int to_params(const qmoe_gemm_desc* d, GemmParams* p) {
   if (!d) return QMOE_ERR_ARG;
-  if (d->kind < QMOE_W8A8_PC || d->kind > QMOE_W4A16_NV) return QMOE_ERR_ARG;
+  if (d->kind < QMOE_W8A8_PC || d->kind > QMOE_W4A16_I4) return QMOE_ERR_ARG;
   if (d->kind == QMOE_W8A8_PC && d->wfmt != 0 && d->wfmt != 1) return QMOE_ERR_ARG;
   if (d->act < QMOE_ACT_NONE || d->act > QMOE_ACT_SITU) return QMOE_ERR_ARG;
   if (d->M < 0 || d->N <= 0 || d->K <= 0 || d->slots <= 0) return QMOE_ERR_ARG;
@@ -38,11 +38,16 @@ int to_params(const qmoe_gemm_desc* d, GemmParams* p) {
   if (d->active && (!d->num_active || !d->group_offs)) return QMOE_ERR_ARG;
   if (!d->group_offs && d->slots != 1) return QMOE_ERR_ARG;
   // 16-byte loads along K
-  const int wbytes = kind_fp4(d->kind) ? d->K / 2 : (d->kind == QMOE_W16A16 ? 2 * d->K : d->K);
+  const int wbytes = kind_w4(d->kind) ? d->K / 2 : (d->kind == QMOE_W16A16 ? 2 * d->K : d->K);
   if (d->ldw < wbytes || (d->ldw % 16) != 0 || (d->K % 32) != 0) return QMOE_ERR_ARG;
   // NVFP4 scales: bf16 [N][ldws >= K/16], 4-byte aligned pairs
   if (d->kind == QMOE_W4A16_NV && (d->ldws < d->K / 16 || (d->ldws % 2) != 0 || (d->ws_gstride % 2) != 0 ||
                                    (reinterpret_cast<uintptr_t>(d->w_scale) & 3)))
+    return QMOE_ERR_ARG;
+  // INT4 scales: bf16 [N][ldws >= K/group], group 32, 64 or 128
+  if (d->kind == QMOE_W4A16_I4 &&
+      ((d->wq_group != 32 && d->wq_group != 64 && d->wq_group != 128) || (d->K % d->wq_group) != 0 ||
+       d->ldws < d->K / d->wq_group || (reinterpret_cast<uintptr_t>(d->w_scale) & 1)))
     return QMOE_ERR_ARG;
   const bool abf16 = kind_abf16(d->kind);
   if (d->lda < d->K || ((d->lda * (abf16 ? 2 : 1)) % 16) != 0) return QMOE_ERR_ARG;
@@ -61,6 +66,7 @@ int to_params(const qmoe_gemm_desc* d, GemmParams* p) {
   p->ldws = d->ldws;
   p->ws_gstride = d->ws_gstride;
   p->ws_bn = d->ws_bn > 0 ? d->ws_bn : 1;
+  p->wq_group = d->wq_group;
   p->bias = d->bias;
   p->bias_gstride = d->bias_gstride;
   p->group_offs = d->group_offs;
@@ -110,8 +116,14 @@ bool use_skinny(const qmoe_gemm_desc* d) {
   return skinny_rows(d) <= lim;
 }
 
+// the W4A16 tiled kernel's format code: 0 MXFP4, 1 NVFP4, 2 INT4
+int w4_fmt(const qmoe_gemm_desc* d) {
+  return d->kind == QMOE_W4A16_NV ? 1 : (d->kind == QMOE_W4A16_I4 ? 2 : 0);
+}
+
 bool use_w4(const qmoe_gemm_desc* d) {
-  if (d->kind == QMOE_W4A16_NV) return true;  // the generic kernel has no NVFP4 form
+  // the generic kernel has no NVFP4 / INT4 form
+  if (d->kind == QMOE_W4A16_NV || d->kind == QMOE_W4A16_I4) return true;
   return d->kind == QMOE_W4A16_MX && !getenv("QMOE_W4_OFF");  // tuning knob: generic kernel only
 }
 
@@ -122,7 +134,7 @@ bool use_f8(const qmoe_gemm_desc* d) {
 
 }  // namespace
 
-extern "C" int qmoe_abi_version(void) { return 1; }
+extern "C" int qmoe_abi_version(void) { return 2; }
 
 extern "C" int qmoe_gemm_workspace_size(const qmoe_gemm_desc* d, int64_t* bytes) {
   GemmParams p;
@@ -136,7 +148,7 @@ extern "C" int qmoe_gemm_workspace_size(const qmoe_gemm_desc* d, int64_t* bytes)
     p.active = nullptr;
     p.num_active = nullptr;
     int bm = 0, ks = 1;
-    const bool ok = use_w4(d) ? qmoe_w4_plan(p, d->kind == QMOE_W4A16_NV, &bm, &ks, bytes)
+    const bool ok = use_w4(d) ? qmoe_w4_plan(p, w4_fmt(d), &bm, &ks, bytes)
                               : qmoe_f8_plan(p, d->kind == QMOE_W8A8_BLK, &bm, &ks, bytes);
     if (!ok) *bytes = 0;
   }
@@ -169,7 +181,7 @@ extern "C" int qmoe_gemm(const qmoe_gemm_desc* d, void* workspace, int64_t ws_by
     const int rc = qmoe_f8_launch(p, d->kind == QMOE_W8A8_BLK, workspace, ws_bytes, stream);
     if (rc != QMOE_ERR_ARG) return rc;
   } else if (use_w4(d)) {
-    const int rc = qmoe_w4_launch(p, d->kind == QMOE_W4A16_NV, workspace, ws_bytes, stream);
+    const int rc = qmoe_w4_launch(p, w4_fmt(d), workspace, ws_bytes, stream);
     if (rc != QMOE_ERR_ARG) return rc;
   }
   const int rc = qmoe_tiled_launch(d->kind, p, stream);

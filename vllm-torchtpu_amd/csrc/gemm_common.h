@@ -20,15 +20,20 @@ enum QmoeKind {
   QK_W4A16_MX = 3,  // A bf16; W e2m1 (2 per byte, low nibble = even k) + e8m0 per 32 k
   QK_W16A16 = 4,    // A bf16; W bf16
   QK_W4A16_NV = 5,  // A bf16; W e2m1 (as QK_W4A16_MX) + bf16 scale per 16 k
+  QK_W4A16_I4 = 6,  // A bf16; W 4-bit integers, offset binary (nibble = v + 8), packed as
+                    // QK_W4A16_MX, + bf16 scale per wq_group k (32, 64 or 128)
 };
 
 // bf16 activations (the other kinds take 1-byte activation codes)
 QMOE_HD constexpr bool kind_abf16(int kind) {
-  return kind == QK_W8A16_PC || kind == QK_W4A16_MX || kind == QK_W16A16 || kind == QK_W4A16_NV;
+  return kind == QK_W8A16_PC || kind == QK_W4A16_MX || kind == QK_W16A16 || kind == QK_W4A16_NV ||
+         kind == QK_W4A16_I4;
 }
 
-// e2m1 weights (two codes per byte)
-QMOE_HD constexpr bool kind_fp4(int kind) { return kind == QK_W4A16_MX || kind == QK_W4A16_NV; }
+// 4-bit weights (two codes per byte, the even k in the low nibble)
+QMOE_HD constexpr bool kind_w4(int kind) {
+  return kind == QK_W4A16_MX || kind == QK_W4A16_NV || kind == QK_W4A16_I4;
+}
 
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
@@ -54,6 +59,29 @@ __device__ __forceinline__ uint4 nvfp4x8_to_bf16(uint32_t d, float s) {
   return r.u;
 }
 
+// 8 offset-binary 4-bit integers (one dword, low nibble first; value =
+// nibble - 8) times a bf16-valued scale -> 8 bf16, each the
+// round-to-nearest-even of value * scale (the reference's bf16 multiply of
+// the int4 weight by its bf16 scale). nibble * s + (-8 s) is computed by one
+// fma whose exact result (a 4-bit by 8-bit significand product) is
+// representable, so the only rounding is the final bf16 one.
+__device__ __forceinline__ uint4 int4x8_to_bf16(uint32_t d, float s) {
+  const uint32_t lo = d & 0x0f0f0f0fu;         // nibbles 0, 2, 4, 6 in bytes 0..3
+  const uint32_t hi = (d >> 4) & 0x0f0f0f0fu;  // nibbles 1, 3, 5, 7
+  const float ns = -8.0f * s;
+  union {
+    bf16x2 h[4];
+    uint4 u;
+  } r;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float a = fmaf((float)((lo >> (8 * j)) & 0xffu), s, ns);
+    const float b = fmaf((float)((hi >> (8 * j)) & 0xffu), s, ns);
+    r.h[j] = __builtin_convertvector(f32x2{a, b}, bf16x2);
+  }
+  return r.u;
+}
+
 enum QmoeAct {
   QA_NONE = 0,
   QA_SILU = 1,
@@ -74,10 +102,11 @@ struct GemmParams {
   const uint8_t* w;
   int64_t ldw;             // bytes per weight row
   int64_t w_gstride;
-  const void* w_scale;     // f32 [N] | f32 [N/bn, ldws] | u8 [N, ldws] | bf16 [N, ldws]
+  const void* w_scale;     // f32 [N] | f32 [N/bn, ldws] | u8 [N, ldws] | bf16 [N, ldws] (NVFP4, INT4)
   int64_t ldws;            // row stride of w_scale (elements)
   int64_t ws_gstride;      // group stride of w_scale (elements)
   int32_t ws_bn;           // rows of W sharing one block-scale row (1 or 128)
+  int32_t wq_group;        // QK_W4A16_I4: k values per scale (32, 64 or 128)
   const float* bias;       // optional f32 [G, N]
   int64_t bias_gstride;
   // rows / groups

@@ -52,10 +52,10 @@ struct Frag {
 template <int KIND, int WF>
 struct Traits {
   static constexpr bool kAbf16 = kind_abf16(KIND);
-  static constexpr bool kFp4 = kind_fp4(KIND);
+  static constexpr bool kW4 = kind_w4(KIND);
   static constexpr bool kInt = KIND == QK_W8A8_PC && WF == 1;
   // bytes per lane per 128-k step (32 k values)
-  static constexpr int kWBytes = kFp4 ? 16 : (KIND == QK_W16A16 ? 64 : 32);
+  static constexpr int kWBytes = kW4 ? 16 : (KIND == QK_W16A16 ? 64 : 32);
   static constexpr int kABytes = kAbf16 ? 64 : 32;
   // Weight chunk j (16 B) of lane (column c, k-group kg) sits at byte
   // j*64 + kg*16 of the row's step (4 lanes x 16 B = one 64 B segment per
@@ -64,13 +64,13 @@ struct Traits {
   //   1-byte A (e4m3/int8) and bf16 A with bf16 W: byte kg*16 + i*64
   //   bf16 A with e4m3 W: byte kg*32 + (i/2)*128 + (i%2)*16
   //   bf16 A with e2m1 W: byte kg*64 + i*16
-  static constexpr int kAOffBase = kFp4 ? 64 : (KIND == QK_W8A16_PC ? 32 : 16);
+  static constexpr int kAOffBase = kW4 ? 64 : (KIND == QK_W8A16_PC ? 32 : 16);
   static __device__ __forceinline__ constexpr int a_off(int i) {
-    return kFp4 ? i * 16 : (KIND == QK_W8A16_PC ? (i >> 1) * 128 + (i & 1) * 16 : i * 64);
+    return kW4 ? i * 16 : (KIND == QK_W8A16_PC ? (i >> 1) * 128 + (i & 1) * 16 : i * 64);
   }
   // first k (within the step) of weight chunk (j, kg) / activation chunk (i, kg)
   static __device__ __forceinline__ constexpr int w_k0(int j, int kg) {
-    return kFp4 ? kg * 32 : (KIND == QK_W16A16 ? j * 32 + kg * 8 : j * 64 + kg * 16);
+    return kW4 ? kg * 32 : (KIND == QK_W16A16 ? j * 32 + kg * 8 : j * 64 + kg * 16);
   }
   static __device__ __forceinline__ constexpr int a_k0(int i, int kg) {
     return (kg * kAOffBase + a_off(i)) / (kAbf16 ? 2 : 1);
@@ -192,7 +192,8 @@ struct Acc {
 
 // Per-step side data: per-(row, block) and per-(n, block) scales (W8A8_BLK),
 // e8m0 block scale of the lane's weight row (W4A16_MX), the two bf16 block
-// scales of the lane's 32 k (W4A16_NV, low half first).
+// scales of the lane's 32 k (W4A16_NV, low half first), the bf16 group
+// scale of the lane's 32 k (W4A16_I4).
 template <int MS, int NS>
 struct StepScales {
   float sa[MS][4];
@@ -255,6 +256,11 @@ __device__ __forceinline__ void mma_step(Acc<KIND, WF, MS, NS>& acc, const Frag 
         const float scale = e8m0_to_f32(sc.eb[s]);
 #pragma unroll
         for (int q = 0; q < 4; ++q) wb[q] = fp4x8_to_bf16(d[q], scale);
+      } else if constexpr (KIND == QK_W4A16_I4) {  // one group scale for the lane's 32 k
+        const uint32_t d[4] = {bw[s].v[0].x, bw[s].v[0].y, bw[s].v[0].z, bw[s].v[0].w};
+        const float sc1 = bits_f32(sc.eb[s] << 16);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) wb[q] = int4x8_to_bf16(d[q], sc1);
       } else {  // QK_W4A16_NV: dwords 0-1 are the first 16-k block, 2-3 the second
         const uint32_t d[4] = {bw[s].v[0].x, bw[s].v[0].y, bw[s].v[0].z, bw[s].v[0].w};
         const float s0 = bits_f32(sc.eb[s] << 16), s1 = bits_f32(sc.eb[s] & 0xffff0000u);
@@ -379,6 +385,11 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p)
     sres = make_rsrc(static_cast<const uint16_t*>(p.w_scale) + (int64_t)g * p.ws_gstride, (int64_t)p.N * p.ldws * 2);
 #pragma unroll
     for (int s = 0; s < NS; ++s) soffw[s] = (uint32_t)(nclamp[s] * p.ldws * 2 + kg * 4);
+  } else if constexpr (KIND == QK_W4A16_I4) {
+    // bf16 [N][K/group]: the lane's 32 k sit in group (128 step + 32 kg) / group
+    sres = make_rsrc(static_cast<const uint16_t*>(p.w_scale) + (int64_t)g * p.ws_gstride, (int64_t)p.N * p.ldws * 2);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) soffw[s] = (uint32_t)(nclamp[s] * p.ldws * 2 + (kg * 32 / p.wq_group) * 2);
   } else if constexpr (KIND == QK_W8A8_BLK) {
     sres = make_rsrc(static_cast<const float*>(p.w_scale) + (int64_t)g * p.ws_gstride,
                      (int64_t)cdiv(p.N, p.ws_bn) * p.ldws * 4);
@@ -386,6 +397,7 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p)
 #pragma unroll
     for (int s = 0; s < NS; ++s) soffw[s] = (uint32_t)((nclamp[s] / p.ws_bn) * p.ldws * 4);
   }
+  const uint32_t i4_step = KIND == QK_W4A16_I4 ? (uint32_t)(256 / p.wq_group) : 0u;  // INT4 scale bytes per step
   // e2m1: the workgroup's NS*16 scale rows (K/32 bytes each; the host keeps
   // K <= 16384) are staged in LDS once, so the K loop reads a step's byte
   // from LDS instead of issuing a scattered byte load per tile per step
@@ -476,6 +488,11 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p)
 #pragma unroll
         for (int s = 0; s < NS; ++s)
           sc.eb[s] = __builtin_amdgcn_raw_buffer_load_b32(sres, soffw[s] | oob, (uint32_t)ks * 16, 0);
+      } else if constexpr (KIND == QK_W4A16_I4) {
+        const uint32_t oob = live ? 0u : kOob;
+#pragma unroll
+        for (int s = 0; s < NS; ++s)
+          sc.eb[s] = __builtin_amdgcn_raw_buffer_load_b16(sres, soffw[s] | oob, (uint32_t)ks * i4_step, 0);
       }
     };
 
@@ -591,6 +608,12 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p)
 #pragma unroll
         for (int s = 0; s < NS; ++s)
           sc.eb[s] = __builtin_amdgcn_raw_buffer_load_b32(sres, soffw[s] | oob, (uint32_t)kk * 16, 0);
+      } else if constexpr (KIND == QK_W4A16_I4) {
+        // zero weights past K: their scale is read as zero too (0 * 0 + -8 * 0)
+        const uint32_t oob = kg * 32 < t ? 0u : kOob;
+#pragma unroll
+        for (int s = 0; s < NS; ++s)
+          sc.eb[s] = __builtin_amdgcn_raw_buffer_load_b16(sres, soffw[s] | oob, (uint32_t)kk * i4_step, 0);
       }
       mma_step<KIND, WF, MS, NS>(acc, fa, bw, sc);
     }
@@ -833,6 +856,10 @@ int qmoe_skinny_launch(int kind, GemmParams p, int max_rows, int slots, void* wo
   if (kind == QK_W4A16_NV && ((int64_t)p.N * p.ldws * 2 > kLim || (p.ldws % 2) != 0 ||
                               (reinterpret_cast<uintptr_t>(p.w_scale) & 3) || (p.ws_gstride % 2) != 0))
     return QMOE_ERR_ARG;
+  if (kind == QK_W4A16_I4 && ((int64_t)p.N * p.ldws * 2 > kLim || (reinterpret_cast<uintptr_t>(p.w_scale) & 1) ||
+                              (p.wq_group != 32 && p.wq_group != 64 && p.wq_group != 128) ||
+                              (p.K % p.wq_group) != 0))
+    return QMOE_ERR_ARG;
   if (kind == QK_W8A8_BLK &&
       ((int64_t)cdiv(p.N, p.ws_bn) * p.ldws * 4 > kLim || p.M * p.lds_a * 4 > kLim))
     return QMOE_ERR_ARG;
@@ -856,6 +883,7 @@ int qmoe_skinny_launch(int kind, GemmParams p, int max_rows, int slots, void* wo
     case QK_W8A16_PC: launch_act<QK_W8A16_PC, 0>(p, ms, ns, waves, grid, st); break;
     case QK_W4A16_MX: launch_act<QK_W4A16_MX, 0>(p, ms, ns, waves, grid, st); break;
     case QK_W4A16_NV: launch_act<QK_W4A16_NV, 0>(p, ms, ns, waves, grid, st); break;
+    case QK_W4A16_I4: launch_act<QK_W4A16_I4, 0>(p, ms, ns, waves, grid, st); break;
     case QK_W16A16: launch_act<QK_W16A16, 0>(p, ms, ns, waves, grid, st); break;
     default: return QMOE_ERR_ARG;
   }

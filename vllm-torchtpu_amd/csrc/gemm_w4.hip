@@ -1,13 +1,14 @@
-// Tiled (prefill) GEMM for bf16 activations x FP4 weights (W4A16: e2m1
-// codes, two per byte with the even k in the low nibble; MXFP4: one e8m0
-// scale per 32 k; NVFP4: one bf16 scale per 16 k), dense or grouped.
+// Tiled (prefill) GEMM for bf16 activations x 4-bit weights (W4A16: codes
+// two per byte with the even k in the low nibble; MXFP4: e2m1 + one e8m0
+// scale per 32 k; NVFP4: e2m1 + one bf16 scale per 16 k; INT4: offset-binary
+// integers + one bf16 scale per 32 / 64 / 128 k), dense or grouped.
 //
 // Restates the reference's W4A16 path (`layers/adapter/linear_common.py:
-// 188-209` -> `kernels/megablox/gmm_v2.py:452-462`: block-32 / block-16
-// weights are dequantized to the activation dtype and multiplied in bf16 with
-// f32 accumulation). Expanding the codes on the fly gives the same bf16
-// weights as dequantizing the whole matrix first: exact for e8m0 scales, one
-// round-to-nearest-even of code * scale for the bf16 NVFP4 scales.
+// 188-209` -> `kernels/megablox/gmm_v2.py:452-462`: blocks below 256 k are
+// dequantized to the activation dtype and multiplied in bf16 with f32
+// accumulation). Expanding the codes on the fly gives the same bf16 weights
+// as dequantizing the whole matrix first: exact for e8m0 scales, one
+// round-to-nearest-even of value * scale for the bf16 NVFP4 / INT4 scales.
 //
 // Design for gfx950 (one workgroup of 4 wavefronts per CU), on the machinery
 // of the 1-byte tiled kernel (gemm_tile.h):
@@ -20,9 +21,10 @@
 //  * in a stage, lane l (row l % 32, half h = l / 32) feeds k in
 //    [32h, 32h + 32): that is one e8m0 block (two NVFP4 blocks), 16
 //    contiguous code bytes (one LDS read for all four 16-k MFMA steps) and
-//    one scale byte (one 4-byte bf16 pair). Each 16-k step expands 8 codes
-//    to bf16 with the block scale applied (v_cvt_scalef32_pk_bf16_fp4 for
-//    e8m0; unscaled conversion, f32 product and bf16 rounding for NVFP4);
+//    one scale byte (NVFP4: one 4-byte bf16 pair; INT4: one bf16 group
+//    scale). Each 16-k step expands 8 codes to bf16 with the scale applied
+//    (v_cvt_scalef32_pk_bf16_fp4 for e8m0; unscaled conversion, f32 product
+//    and bf16 rounding for NVFP4 and INT4);
 //    activation and weight use the same lane -> k assignment, so the
 //    products pair up whatever order the MFMA sums;
 //  * every operand of stage s+1 is read into the second register set during
@@ -79,8 +81,10 @@ __device__ __forceinline__ bf16x8 as_bf16x8_u4(const uint4& x) {
   return c.v;
 }
 
-template <int BM, bool ACT, bool NV>
+// FMT: 0 MXFP4, 1 NVFP4, 2 INT4
+template <int BM, bool ACT, int FMT>
 __global__ __launch_bounds__(kThreads) void w4_gemm_kernel(const GemmParams p, int m_tiles, int n_tiles) {
+  constexpr bool NV = FMT == 1, I4 = FMT == 2;
   using S = W4Shape<BM>;
   constexpr int BN = kW4BN;
   constexpr int NI = S::NI, MJ = S::MJ, TN = S::TN, TM = S::TM;
@@ -134,8 +138,9 @@ __global__ __launch_bounds__(kThreads) void w4_gemm_kernel(const GemmParams p, i
   // slot l & 7, fetching the chunk that the row's swizzle stores there);
   // codes: 32 rows x 32 bytes (lane -> row l >> 1, half l & 1). Scales:
   // lane (row l % 32, half h) of weight block i needs e8m0 byte 2*stage + h
-  // of its row (NVFP4: bf16 scales 4*stage + 2h and + 1, one 4-byte load).
-  constexpr int kSB = NV ? 2 : 1;  // bytes per scale
+  // of its row (NVFP4: bf16 scales 4*stage + 2h and + 1, one 4-byte load;
+  // INT4: bf16 scale (64*stage + 32h) / group).
+  constexpr int kSB = NV || I4 ? 2 : 1;  // bytes per scale
   constexpr int XI = BM / 32;  // activation copies per wavefront
   constexpr int WI = 2;        // code copies per wavefront
   const uint8_t* xbase = static_cast<const uint8_t*>(p.a);
@@ -169,7 +174,8 @@ __global__ __launch_bounds__(kThreads) void w4_gemm_kernel(const GemmParams p, i
   uint32_t eoff[NI];
 #pragma unroll
   for (int i = 0; i < NI; ++i)
-    eoff[i] = (uint32_t)wrow_global(wrow(i) + rl) * (uint32_t)(p.ldws * kSB) + (NV ? kh * 4 : kh);
+    eoff[i] = (uint32_t)wrow_global(wrow(i) + rl) * (uint32_t)(p.ldws * kSB) + (NV ? kh * 4 : (I4 ? 0 : kh));
+  const int lg = I4 ? (p.wq_group == 32 ? 5 : (p.wq_group == 64 ? 6 : 7)) : 0;  // log2(group)
   uint32_t we[4][NI];  // scales of the stages in flight (stage s in set s % 4)
   auto copy_stage = [&](uint8_t* dA, uint8_t* dW, int e, int ks) {
     const uint32_t st = (uint32_t)(u0 + ks);
@@ -188,8 +194,14 @@ __global__ __launch_bounds__(kThreads) void w4_gemm_kernel(const GemmParams p, i
     }
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
-      if constexpr (NV) we[e][i] = __builtin_amdgcn_raw_buffer_load_b32(eres, eoff[i], st * 8u, 0);
-      else we[e][i] = __builtin_amdgcn_raw_buffer_load_b8(eres, eoff[i], st * 2u, 0);
+      if constexpr (NV) {
+        we[e][i] = __builtin_amdgcn_raw_buffer_load_b32(eres, eoff[i], st * 8u, 0);
+      } else if constexpr (I4) {
+        const uint32_t gi = (st * 64u + (uint32_t)kh * 32u) >> lg;  // group of the lane's 32 k
+        we[e][i] = __builtin_amdgcn_raw_buffer_load_b16(eres, eoff[i] + gi * 2u, 0, 0);
+      } else {
+        we[e][i] = __builtin_amdgcn_raw_buffer_load_b8(eres, eoff[i], st * 2u, 0);
+      }
     }
   };
 
@@ -229,6 +241,8 @@ __global__ __launch_bounds__(kThreads) void w4_gemm_kernel(const GemmParams p, i
       if constexpr (NV) {
         scale[i] = bits_f32(eb[i] << 16);
         scale1[i] = bits_f32(eb[i] & 0xffff0000u);
+      } else if constexpr (I4) {
+        scale[i] = bits_f32(eb[i] << 16);
       } else {
         scale[i] = e8m0_to_f32(eb[i]);
       }
@@ -240,6 +254,7 @@ __global__ __launch_bounds__(kThreads) void w4_gemm_kernel(const GemmParams p, i
       for (int i = 0; i < NI; ++i) {
         const uint32_t d = q == 0 ? wc[t][i].x : (q == 1 ? wc[t][i].y : (q == 2 ? wc[t][i].z : wc[t][i].w));
         if constexpr (NV) wv[i] = as_bf16x8_u4(nvfp4x8_to_bf16(d, q < 2 ? scale[i] : scale1[i]));
+        else if constexpr (I4) wv[i] = as_bf16x8_u4(int4x8_to_bf16(d, scale[i]));
         else wv[i] = w4_expand(d, scale[i]);
       }
 #pragma unroll
@@ -319,33 +334,34 @@ __global__ __launch_bounds__(kThreads) void w4_gemm_kernel(const GemmParams p, i
                                         n0, nlim, rows, wn, wm, lane);
 }
 
-template <int BM, bool ACT, bool NV>
+template <int BM, bool ACT, int FMT>
 void w4_launch_shape(const GemmParams& p, hipStream_t st) {
   const int nout = ACT ? p.N / 2 : p.N;
   const int n_tiles = cdiv(nout, ACT ? kW4BN / 2 : kW4BN);
   const unsigned ks = (unsigned)std::max(1, p.ksplit);
   if (p.group_offs) {
     const int m_tiles = cdiv(p.M, BM) + std::min(p.slots, p.M);
-    hipLaunchKernelGGL((w4_gemm_kernel<BM, ACT, NV>), dim3(n_tiles, m_tiles, ks), dim3(kThreads), 0, st, p,
+    hipLaunchKernelGGL((w4_gemm_kernel<BM, ACT, FMT>), dim3(n_tiles, m_tiles, ks), dim3(kThreads), 0, st, p,
                        m_tiles, n_tiles);
   } else {
     const int m_tiles = cdiv(p.M, BM);
     const int grid = cdiv(m_tiles * n_tiles, kXcds) * kXcds;
-    hipLaunchKernelGGL((w4_gemm_kernel<BM, ACT, NV>), dim3(grid, 1, ks), dim3(kThreads), 0, st, p, m_tiles,
+    hipLaunchKernelGGL((w4_gemm_kernel<BM, ACT, FMT>), dim3(grid, 1, ks), dim3(kThreads), 0, st, p, m_tiles,
                        n_tiles);
   }
 }
 
-template <int BM, bool NV>
+template <int BM, int FMT>
 void w4_launch_act(const GemmParams& p, hipStream_t st) {
-  if (p.act != QA_NONE) w4_launch_shape<BM, true, NV>(p, st);
-  else w4_launch_shape<BM, false, NV>(p, st);
+  if (p.act != QA_NONE) w4_launch_shape<BM, true, FMT>(p, st);
+  else w4_launch_shape<BM, false, FMT>(p, st);
 }
 
 template <int BM>
-void w4_launch_fmt(const GemmParams& p, bool nv, hipStream_t st) {
-  if (nv) w4_launch_act<BM, true>(p, st);
-  else w4_launch_act<BM, false>(p, st);
+void w4_launch_fmt(const GemmParams& p, int fmt, hipStream_t st) {
+  if (fmt == 1) w4_launch_act<BM, 1>(p, st);
+  else if (fmt == 2) w4_launch_act<BM, 2>(p, st);
+  else w4_launch_act<BM, 0>(p, st);
 }
 
 }  // namespace
@@ -354,17 +370,21 @@ void w4_launch_fmt(const GemmParams& p, bool nv, hipStream_t st) {
 // rows, even scale rows, codes < 4 GiB per group), and its plan: token-tile
 // height (the largest of 128 / 64 / 32 that still fills the CUs, or that fits
 // the average group), K split (dense problems with few tiles) and the f32
-// workspace the split needs ([ksplit][M][N]). `nv`: NVFP4 (bf16 scales per
-// 16 k) instead of MXFP4 (e8m0 per 32 k).
-bool qmoe_w4_plan(const GemmParams& p, bool nv, int* bm_out, int* ksplit_out, int64_t* ws_bytes) {
+// workspace the split needs ([ksplit][M][N]). `fmt`: 0 MXFP4 (e8m0 per
+// 32 k), 1 NVFP4 (bf16 per 16 k), 2 INT4 (bf16 per wq_group k).
+bool qmoe_w4_plan(const GemmParams& p, int fmt, int* bm_out, int* ksplit_out, int64_t* ws_bytes) {
   if (p.M <= 0 || p.K <= 0 || (p.K % 64) != 0 || p.N <= 0) return false;
   if (p.act != QA_NONE && (p.N % 2) != 0) return false;
-  if ((p.lda % 8) != 0 || (p.ldw % 16) != 0 || (p.ldws % 2) != 0) return false;
-  const int sal = nv ? 3 : 1;  // scale alignment mask: 4-byte bf16 pairs, 2-byte e8m0 pairs
-  if ((reinterpret_cast<uintptr_t>(p.a) & 15) || (reinterpret_cast<uintptr_t>(p.w) & 15) ||
-      (p.w_gstride % 16) != 0 || (reinterpret_cast<uintptr_t>(p.w_scale) & sal) || (p.ws_gstride % 2) != 0)
+  if ((p.lda % 8) != 0 || (p.ldw % 16) != 0 || (fmt != 2 && (p.ldws % 2) != 0)) return false;
+  if (fmt == 2 && ((p.wq_group != 32 && p.wq_group != 64 && p.wq_group != 128) || (p.K % p.wq_group) != 0))
     return false;
-  if ((int64_t)p.ldw * p.N >= ((int64_t)1 << 32) || (int64_t)p.ldws * (nv ? 2 : 1) * p.N >= ((int64_t)1 << 31))
+  // scale alignment mask: 4-byte bf16 pairs (NVFP4), 2-byte e8m0 pairs (MXFP4), bf16 (INT4)
+  const int sal = fmt == 1 ? 3 : 1;
+  if ((reinterpret_cast<uintptr_t>(p.a) & 15) || (reinterpret_cast<uintptr_t>(p.w) & 15) ||
+      (p.w_gstride % 16) != 0 || (reinterpret_cast<uintptr_t>(p.w_scale) & sal) ||
+      (fmt != 2 && (p.ws_gstride % 2) != 0))
+    return false;
+  if ((int64_t)p.ldw * p.N >= ((int64_t)1 << 32) || (int64_t)p.ldws * (fmt ? 2 : 1) * p.N >= ((int64_t)1 << 31))
     return false;
   const int nout = p.act != QA_NONE ? p.N / 2 : p.N;
   const int n_tiles = cdiv(nout, p.act != QA_NONE ? kW4BN / 2 : kW4BN);
@@ -402,19 +422,19 @@ bool qmoe_w4_plan(const GemmParams& p, bool nv, int* bm_out, int* ksplit_out, in
 
 // Launch per the plan (the caller sized the workspace); with a K split the
 // finishing kernel runs the epilogue.
-int qmoe_w4_launch(GemmParams p, bool nv, void* workspace, int64_t ws_bytes, hipStream_t st) {
+int qmoe_w4_launch(GemmParams p, int fmt, void* workspace, int64_t ws_bytes, hipStream_t st) {
   int bm = 0, ksplit = 1;
   int64_t need = 0;
-  if (!qmoe_w4_plan(p, nv, &bm, &ksplit, &need)) return QMOE_ERR_ARG;
+  if (!qmoe_w4_plan(p, fmt, &bm, &ksplit, &need)) return QMOE_ERR_ARG;
   p.ksplit = ksplit;
   if (ksplit > 1) {
     if (!workspace || ws_bytes < need) return QMOE_ERR_WORKSPACE;
     p.partial = static_cast<float*>(workspace);
   }
   switch (bm) {
-    case 128: w4_launch_fmt<128>(p, nv, st); break;
-    case 64: w4_launch_fmt<64>(p, nv, st); break;
-    default: w4_launch_fmt<32>(p, nv, st); break;
+    case 128: w4_launch_fmt<128>(p, fmt, st); break;
+    case 64: w4_launch_fmt<64>(p, fmt, st); break;
+    default: w4_launch_fmt<32>(p, fmt, st); break;
   }
   if (ksplit > 1) {
     const int nout = p.act != QA_NONE ? p.N / 2 : p.N;

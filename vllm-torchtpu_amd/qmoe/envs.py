@@ -39,8 +39,10 @@ _READERS = {
     "REQUANTIZE_WEIGHT_DTYPE": lambda: os.getenv("REQUANTIZE_WEIGHT_DTYPE", "float8_e4m3fn"),
     # FP8 dense linears keep bf16 activations for steps of at most this many rows
     "TPU_FP8_LINEAR_W8A16_MAX_ROWS": lambda: _nonneg_int("TPU_FP8_LINEAR_W8A16_MAX_ROWS", 0),
-    # MoE: weight block size to requantize checkpoint experts to (NVFP4)
+    # MoE: weight block size to requantize checkpoint experts to (NVFP4, INT4)
     "MOE_REQUANTIZE_BLOCK_SIZE": lambda: _opt_int("MOE_REQUANTIZE_BLOCK_SIZE"),
+    # MoE: weight dtype to requantize packed-int4 experts to (e.g. "fp4")
+    "MOE_REQUANTIZE_WEIGHT_DTYPE": lambda: os.getenv("MOE_REQUANTIZE_WEIGHT_DTYPE"),
     # MoE: routes with a zero routing weight are padding and skipped
     "TPU_MOE_SKIP_PADDED_TOKENS": lambda: _bool("TPU_MOE_SKIP_PADDED_TOKENS"),
 }

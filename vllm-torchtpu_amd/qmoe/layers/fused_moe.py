@@ -14,6 +14,8 @@ format                w1 [E, 2I, H...] / w2        scales
 ====================  ==========================  ====================================
 ``mxfp4``             uint8 packed e2m1 [., ., K/2]  e8m0 uint8 [E, N, K/32]
 ``nvfp4``             uint8 packed e2m1 [., ., K/2]  bf16 [E, N, K/16] (fused e4m3 x global)
+``int4``              int32 carriers [., ., K/8]     bf16 [E, N, K/group], group 32 / 64 / 128
+                      (8 offset-binary nibbles per int32, the compressed-tensors checkpoint form)
 ``fp8_block``         float8_e4m3fn [E, N, K]      f32 tile scales [E, N/128, K/128]
 ``fp8_block_rows``    float8_e4m3fn [E, N, K]      f32 per-(row, 128) scales [E, N, K/128]
 ``fp8`` / ``int8``    float8_e4m3fn / int8         f32 per-channel [E, N]
@@ -45,6 +47,8 @@ def infer_weight_format(w1: torch.Tensor, w1_scale) -> str:
         if w1_scale is not None and w1_scale.dim() == 3 and w1_scale.shape[-1] * 128 == w1.shape[-1]:
             return "fp8_block_rows" if w1_scale.shape[1] == w1.shape[1] else "fp8_block"
         return "fp8"
+    if w1.dtype == torch.int32:
+        return "int4"
     if w1.dtype == torch.uint8 or "float4" in str(w1.dtype):
         return "nvfp4" if w1_scale is not None and w1_scale.dtype == torch.bfloat16 else "mxfp4"
     raise ValueError(f"unsupported MoE weight dtype {w1.dtype}")
@@ -57,14 +61,17 @@ def fused_moe_gmm(hidden_states, w1, w2, w1_scale, w2_scale, w1_bias, w2_bias, t
 
     ``experts_start`` is the reference's expert-parallel offset; this build
     runs the whole expert set on one GPU, so it must be None or 0.
-    ``rhs_quant_dtype`` (packed int4 carriers) is not supported.
+    ``rhs_quant_dtype``: ``int4`` (any dtype object or string naming int4) marks
+    packed-int4 int32 weights (`compressed_tensors_moe_w4a16.py:380-405`).
     """
     if experts_start is not None and not isinstance(experts_start, torch.Tensor) and int(experts_start) != 0:
         raise NotImplementedError("expert parallelism is out of scope: experts_start must be 0")
     if rhs_quant_dtype is not None:
-        raise NotImplementedError("packed int4 rhs_quant_dtype is not supported")
+        if "int4" not in str(rhs_quant_dtype):
+            raise NotImplementedError(f"rhs_quant_dtype {rhs_quant_dtype} is not supported (int4 only)")
+        weight_format = weight_format or "int4"
     fmt = weight_format or infer_weight_format(w1, w1_scale)
-    if fmt not in ("mxfp4", "nvfp4", "bf16", "fp8_block", "fp8_block_rows", "fp8", "int8"):
+    if fmt not in ("mxfp4", "nvfp4", "int4", "bf16", "fp8_block", "fp8_block_rows", "fp8", "int8"):
         raise ValueError(f"unknown MoE weight format {fmt!r}")
     ops.act_code(activation)  # NotImplementedError for an unknown activation string
     T, H = hidden_states.shape
@@ -153,8 +160,8 @@ def _moe_body(x, w1, w2, w1_scale, w2_scale, w1_bias, w2_bias, tw, topk_ids, top
     b2 = w2_bias.float().reshape(E, -1).contiguous() if w2_bias is not None else None
     u8 = lambda t: t.view(torch.uint8)  # noqa: E731
 
-    if fmt in ("mxfp4", "nvfp4"):
-        kind = _capi.W4A16_MX if fmt == "mxfp4" else _capi.W4A16_NV
+    if fmt in ("mxfp4", "nvfp4", "int4"):
+        kind = {"mxfp4": _capi.W4A16_MX, "nvfp4": _capi.W4A16_NV, "int4": _capi.W4A16_I4}[fmt]
         sc = u8 if fmt == "mxfp4" else (lambda t: t)  # noqa: E731
         inter = ops.gemm(kind, x, u8(w1), w_scale=sc(w1_scale), bias=b1,
                          a_rows=meta["token_sorted"], activation=activation, **common)

@@ -121,7 +121,7 @@ def gemm(kind, a, w, *, a_scale=None, w_scale=None, bias=None, wfmt=0, ws_bn=1,
     a        : [rows, K] activation codes (1 byte) or bf16
     w        : [G, N, K] / [N, K] weights (1 byte codes, packed e2m1 [.., K/2], bf16)
     w_scale  : per-channel f32 [G, N] | block f32 [G, N/bn, K/128] | e8m0 u8 [G, N, K/32]
-               | NVFP4 bf16 [G, N, K/16]
+               | NVFP4 bf16 [G, N, K/16] | INT4 bf16 [G, N, K/group] (group 32, 64 or 128)
     Returns ``out`` ([M, N or N/2] bf16 unless given).
     """
     _require_gpu(a, w)
@@ -131,9 +131,9 @@ def gemm(kind, a, w, *, a_scale=None, w_scale=None, bias=None, wfmt=0, ws_bn=1,
     G, N, wcols = w.shape
     if a.stride(-1) != 1 or w.stride(-1) != 1 or w.stride(1) != wcols:
         raise ValueError("qmoe gemm needs K-contiguous activations and N-major [G, N, K] weights")
-    abf16 = kind in (_capi.W8A16_PC, _capi.W4A16_MX, _capi.W16A16, _capi.W4A16_NV)
+    abf16 = kind in (_capi.W8A16_PC, _capi.W4A16_MX, _capi.W16A16, _capi.W4A16_NV, _capi.W4A16_I4)
     K = a.shape[1]
-    if kind in (_capi.W4A16_MX, _capi.W4A16_NV):
+    if kind in (_capi.W4A16_MX, _capi.W4A16_NV, _capi.W4A16_I4):
         if wcols * 2 != K:
             raise ValueError(f"packed e2m1 weight has {wcols} bytes per row, expected K/2 = {K // 2}")
     elif wcols != K:
@@ -168,6 +168,12 @@ def gemm(kind, a, w, *, a_scale=None, w_scale=None, bias=None, wfmt=0, ws_bn=1,
                 ws = ws.unsqueeze(0)
             if kind == _capi.W4A16_NV and (ws.dtype != torch.bfloat16 or ws.shape[-1] * 16 != K):
                 raise ValueError(f"NVFP4 weight scales are bf16 [G, N, K/16], got {ws.dtype} {tuple(ws.shape)}")
+            if kind == _capi.W4A16_I4:
+                grp = K // ws.shape[-1] if ws.shape[-1] else 0
+                if ws.dtype != torch.bfloat16 or grp not in (32, 64, 128) or grp * ws.shape[-1] != K:
+                    raise ValueError(f"INT4 weight scales are bf16 [G, N, K/group] with group 32, 64 or 128, "
+                                     f"got {ws.dtype} {tuple(ws.shape)} for K={K}")
+                d.wq_group = grp
             d.ldws, d.ws_gstride = ws.stride(1), ws.stride(0)
         d.w_scale = ws.data_ptr()
     d.ws_bn = ws_bn
