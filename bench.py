@@ -47,7 +47,7 @@ def parse():
     ap.add_argument("--m", type=int, default=4096, help="tokens of the headline step")
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="", help="comma list of sweep configs to run (0-4; 5 = NVFP4)")
+    ap.add_argument("--only", default="", help="comma list of sweep configs to run (0-4; 5 = NVFP4 / INT4)")
     ap.add_argument("--profile", nargs="?", const="headline", default=None,
                     choices=["headline", "decode", "moe"],
                     help="rocprofv3 targets: the headline kernel + a copy calibration (default), "
@@ -268,10 +268,22 @@ def nvfp4_weights(shape, gen):
     return codes, sc
 
 
+def int4_weights(shape, gen, group=128):
+    """Packed-int4 weights (int32 carriers read as bytes) + bf16 group scales."""
+    import torch
+
+    *lead, N, K = shape
+    carriers = torch.randint(0, 256, (*lead, N, K // 2), device="cuda", dtype=torch.uint8, generator=gen)
+    sc = (torch.rand((*lead, N, K // group), device="cuda", generator=gen) * 0.004 + 0.001).to(torch.bfloat16)
+    return carriers, sc
+
+
 def sweep_nvfp4(only):
-    """NVFP4 W4A16 (the reference's ModelOpt FP4 path) on the config-0 dense
-    and config-3 MoE shapes (silu: the reference's NVFP4 MoE takes no
-    swigluoai). Algorithmic scale bytes are the checkpoint's e4m3 bytes."""
+    """NVFP4 W4A16 (the reference's ModelOpt FP4 path) and packed-INT4 W4A16
+    (group 128, the compressed-tensors MoE recipe) on the config-0 dense and
+    config-3 MoE shapes (silu: the reference's NVFP4 MoE takes no swigluoai).
+    Algorithmic scale bytes are the checkpoint's (e4m3 for NVFP4, bf16 for
+    INT4)."""
     import torch
 
     from qmoe import ops
@@ -307,6 +319,35 @@ def sweep_nvfp4(only):
         touched = int(torch.unique(ids).numel())
         nbytes = touched * per_expert + 2 * T * H * 2 + 2 * T * E
         out.append(dict(cfg=5, kind="moe_nvfp4", T=T, experts_touched=touched,
+                        **roof(T * k * 6.0 * H * I, nbytes, us, "bf16")))
+        log(out[-1])
+    del w13, s13, w2, s2
+    from qmoe import _capi
+
+    K, N = 2880, 5760
+    codes, sc = int4_weights((N, K), gen, group=32 if K % 128 else 128)
+    grp = K // sc.shape[-1]
+    for M in (1, 16, 128, 4096):
+        x = torch.randn((M, K), device="cuda", generator=gen).to(torch.bfloat16)
+        us = graph_time_us(lambda: ops.gemm(_capi.W4A16_I4, x, codes, w_scale=sc))[0]
+        nbytes = N * K // 2 + 2 * N * K // grp + 2 * M * K + 2 * M * N
+        out.append(dict(cfg=5, kind=f"int4_w4a16_g{grp}", M=M, K=K, N=N, **roof(2.0 * M * N * K, nbytes, us, "bf16")))
+        log(out[-1])
+    w13, s13 = int4_weights((E, 2 * I, H), gen, group=grp)
+    w2, s2 = int4_weights((E, H, I), gen, group=grp)
+    per_expert = 3 * I * H // 2 + 2 * 3 * I * H // grp
+    for T in (1, 16, 1024):
+        x = torch.randn((T, H), device="cuda", generator=gen).to(torch.bfloat16)
+        logits = torch.randn((T, E), device="cuda", generator=gen).to(torch.bfloat16)
+
+        def layer():
+            return moe_forward(lcfg, x, logits, w13, w2, s13, s2, None, None, "int4")
+
+        us = graph_time_us(layer, iters=20)[0]
+        _, ids = ops.moe_route(logits, k, "softmax", True)
+        touched = int(torch.unique(ids).numel())
+        nbytes = touched * per_expert + 2 * T * H * 2 + 2 * T * E
+        out.append(dict(cfg=5, kind=f"moe_int4_g{grp}", T=T, experts_touched=touched,
                         **roof(T * k * 6.0 * H * I, nbytes, us, "bf16")))
         log(out[-1])
     return out
