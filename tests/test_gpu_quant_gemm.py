@@ -190,7 +190,10 @@ def test_w8a8_int8_per_channel_bit_exact(dev, M, K, N):
 @pytest.mark.parametrize("M,K,N", [(1, 1024, 512), (32, 2048, 768), (130, 1024, 640), (256, 2048, 1024),
                                    # tiled block-scaled kernel: ragged tiles, 32/64/128-token tiles,
                                    # a K split (tall K, few tokens)
-                                   (300, 2048, 1280), (70, 1536, 384), (400, 1024, 2304), (96, 8192, 512)])
+                                   (300, 2048, 1280), (70, 1536, 384), (400, 1024, 2304), (96, 8192, 512),
+                                   # wide N (>= 16384 channels): tiled from 17 rows, K split 2 up to
+                                   # 64 tokens, 64-token tiles to 128 and from 257 to 512 tokens
+                                   (17, 1024, 16384), (50, 768, 16384), (100, 512, 16512), (260, 512, 16384)])
 @pytest.mark.parametrize("tile_scales", [True, False])
 def test_w8a8_fp8_block(dev, M, K, N, tile_scales):
     from qmoe import _capi, ops

@@ -23,6 +23,7 @@ namespace {
 constexpr int kSkinnyMaxRows = 64;
 constexpr int kSkinnyMaxGroupRows = 8;
 constexpr int kSkinnyMaxRowsW8A8 = 32;
+constexpr int kSkinnyMaxRowsBlkWide = 16;
 
 int to_params(const qmoe_gemm_desc* d, GemmParams* p) {
   if (!d) return QMOE_ERR_ARG;
@@ -112,6 +113,10 @@ bool use_skinny(const qmoe_gemm_desc* d) {
   const char* env = getenv("QMOE_SKINNY_MAX_ROWS");  // tuning knob
   int lim = d->group_offs ? kSkinnyMaxGroupRows : kSkinnyMaxRows;
   if (!d->group_offs && d->kind == QMOE_W8A8_PC) lim = kSkinnyMaxRowsW8A8;
+  // wide dense block-scaled problems (>= 16384 output channels): the tiled
+  // kernel with a K split wins from 17 rows (measured on MI355X, K 7168)
+  const int nout = d->act != QMOE_ACT_NONE ? d->N / 2 : d->N;
+  if (!d->group_offs && d->kind == QMOE_W8A8_BLK && nout >= 16384) lim = kSkinnyMaxRowsBlkWide;
   if (env) lim = atoi(env);
   return skinny_rows(d) <= lim;
 }

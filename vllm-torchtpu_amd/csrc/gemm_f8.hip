@@ -509,10 +509,29 @@ bool qmoe_f8_plan(const GemmParams& p, bool blk, int* bm_out, int* ksplit_out, i
     return false;
   if ((int64_t)p.ldw * p.N >= ((int64_t)1 << 32)) return false;
   int bm = f8_pick_bm_any(p);
-  if (blk && !getenv("QMOE_F8_BM")) {
+  int ksplit = 1;
+  const bool env_bm = getenv("QMOE_F8_BM") != nullptr;
+  // dense block-scaled problems with at least 64 weight-row tiles (16384
+  // output channels: DeepSeek-V3's wide projections) take the tile height
+  // and K split measured best on MI355X (K 7168, N 18432 / 24576)
+  const int nout = p.act != QA_NONE ? p.N / 2 : p.N;
+  const bool blk_wide = blk && !p.group_offs && cdiv(nout, p.act != QA_NONE ? 128 : 256) >= 64;
+  if (blk && !env_bm) {
     // block-scaled tiles hold at most 128 tokens; measured on MI355X (K 7168,
     // N 18432): 128-token tiles up to 256 and from 2048 tokens, 64 between
     bm = p.group_offs ? std::min(bm, 128) : (p.M > 256 && p.M < 2048 ? 64 : 128);
+    if (blk_wide) {
+      // (tokens: tile, split) 32: 32/2 (27 vs 34 us streaming), 64: 64/2
+      // (33 vs 60 us), 128: 64/1 (49 vs 85 us), 256: 128/1, 512: 64/1,
+      // 1024: 128/1 (254 vs 296 us at N 24576)
+      if (p.M <= 32) { bm = 32; ksplit = 2; }
+      else if (p.M <= 64) { bm = 64; ksplit = 2; }
+      else if (p.M <= 128) bm = 64;
+      else if (p.M <= 256) bm = 128;
+      else if (p.M <= 512) bm = 64;
+      else bm = 128;
+      ksplit = std::min(ksplit, p.K / 256);
+    }
   }
   const int m_tiles = p.group_offs ? cdiv(p.M, bm) + std::min(p.slots, p.M) : cdiv(p.M, bm);
   if (p.group_offs && m_tiles > 65535) return false;
@@ -520,9 +539,7 @@ bool qmoe_f8_plan(const GemmParams& p, bool blk, int* bm_out, int* ksplit_out, i
   // tokens) are split over K, with the tile and split that measured best on
   // MI355X: (32 rows, 4 slices) up to 256 tokens, (128, 4) up to 512,
   // (128, 2) above.
-  int ksplit = 1;
-  const bool env_bm = getenv("QMOE_F8_BM") != nullptr;
-  if (!p.group_offs && bm <= 64 && p.K >= 8192 && !env_bm) {
+  if (!p.group_offs && !blk_wide && bm <= 64 && p.K >= 8192 && !env_bm) {
     if (p.M <= 256) { bm = 32; ksplit = 4; }
     else if (p.M <= 512) { bm = 128; ksplit = 4; }
     else { bm = 128; ksplit = 2; }
