@@ -149,7 +149,7 @@ def test_runtime_quant_division_stress(dev, qdtype):
 SHAPES_SKINNY = [(1, 512, 384), (8, 1024, 640), (16, 2048, 256), (33, 512, 4096), (64, 4096, 1024)]
 # the last two split K across workgroups (few tiles, long K)
 SHAPES_TILED = [(65, 512, 384), (200, 1024, 1000), (512, 2048, 2048), (300, 1536, 2304), (130, 8192, 512),
-                (96, 14336, 768)]
+                (96, 14336, 768), (200, 8192, 640)]
 
 
 @pytest.mark.parametrize("M,K,N", SHAPES_SKINNY + SHAPES_TILED)

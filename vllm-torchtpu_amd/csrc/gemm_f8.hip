@@ -537,10 +537,11 @@ bool qmoe_f8_plan(const GemmParams& p, bool blk, int* bm_out, int* ksplit_out, i
   if (p.group_offs && m_tiles > 65535) return false;
   // Dense problems whose largest CU-filling tile is small (tall-K, few
   // tokens) are split over K, with the tile and split that measured best on
-  // MI355X: (32 rows, 4 slices) up to 256 tokens, (128, 4) up to 512,
-  // (128, 2) above.
+  // MI355X: (32 rows, 4 slices) up to 128 tokens, (64, 4) up to 256 (K 14336,
+  // N 4096: 30 vs 39 us), (128, 4) up to 512, (128, 2) above.
   if (!p.group_offs && !blk_wide && bm <= 64 && p.K >= 8192 && !env_bm) {
-    if (p.M <= 256) { bm = 32; ksplit = 4; }
+    if (p.M <= 128) { bm = 32; ksplit = 4; }
+    else if (p.M <= 256) { bm = 64; ksplit = 4; }
     else if (p.M <= 512) { bm = 128; ksplit = 4; }
     else { bm = 128; ksplit = 2; }
   }
