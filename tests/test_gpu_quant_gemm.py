@@ -228,7 +228,7 @@ def _nv_scales(rng, n, k):
                                    # K % 128 != 0 (streaming kernel's tail step), small K
                                    (3, 2848, 200), (1, 416, 70), (7, 96, 130),
                                    # tiled kernel: 64/128-token tiles, K splits, ragged tiles
-                                   (300, 2880, 768), (520, 1024, 512), (200, 4096, 4096),
+                                   (300, 2880, 768), (520, 1024, 512), (200, 4096, 4096), (50, 2880, 1000),
                                    # K % 64 == 32 above the streaming bound: 64-row streaming passes
                                    (70, 2848, 300)])
 def test_w4a16_nvfp4(dev, M, K, N):
@@ -326,7 +326,9 @@ def test_w4a16_int4_dequant_bit_exact(dev, M, K, N, group):
                                    # tiled kernel: 32/64/128-token tiles, K splits, ragged tiles;
                                    # K % 64 != 0 takes the generic tiled kernel
                                    (300, 2880, 768), (520, 1024, 512), (600, 512, 9216), (1200, 512, 9216),
-                                   (70, 2848, 300)])
+                                   (70, 2848, 300),
+                                   # 33..64 rows: tiled 32-token tiles with a 4-way K split
+                                   (50, 2880, 1000)])
 def test_w4a16_mxfp4(dev, M, K, N):
     from qmoe import _capi, ops
 

@@ -22,7 +22,7 @@ namespace {
 
 constexpr int kSkinnyMaxRows = 64;
 constexpr int kSkinnyMaxGroupRows = 8;
-constexpr int kSkinnyMaxRowsW8A8 = 32;
+constexpr int kSkinnyMaxRowsW8A8 = 32;  // also dense e2m1
 constexpr int kSkinnyMaxRowsBlkWide = 16;
 
 int to_params(const qmoe_gemm_desc* d, GemmParams* p) {
@@ -117,6 +117,9 @@ bool use_skinny(const qmoe_gemm_desc* d) {
   // kernel with a K split wins from 17 rows (measured on MI355X, K 7168)
   const int nout = d->act != QMOE_ACT_NONE ? d->N / 2 : d->N;
   if (!d->group_offs && d->kind == QMOE_W8A8_BLK && nout >= 16384) lim = kSkinnyMaxRowsBlkWide;
+  // dense e2m1 (MXFP4 / NVFP4): the tiled kernel's 32-token tiles with a K
+  // split win from 33 rows (measured on MI355X, K 2880, N 5760)
+  if (!d->group_offs && (d->kind == QMOE_W4A16_MX || d->kind == QMOE_W4A16_NV)) lim = kSkinnyMaxRowsW8A8;
   if (env) lim = atoi(env);
   return skinny_rows(d) <= lim;
 }

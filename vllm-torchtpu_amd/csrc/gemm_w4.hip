@@ -403,14 +403,28 @@ bool qmoe_w4_plan(const GemmParams& p, int fmt, int* bm_out, int* ksplit_out, in
     // CUs, else 64 with a K split (32-token tiles are slower at every M)
     bm = (int64_t)cdiv(p.M, 128) * n_tiles >= 200 ? 128 : 64;
   }
-  const int m_tiles = p.group_offs ? cdiv(p.M, bm) + std::min(p.slots, p.M) : cdiv(p.M, bm);
-  if (p.group_offs && m_tiles > 65535) return false;
+  const int m_tiles0 = p.group_offs ? cdiv(p.M, bm) + std::min(p.slots, p.M) : cdiv(p.M, bm);
+  if (p.group_offs && m_tiles0 > 65535) return false;
   // dense problems with fewer than ~200 tiles split K (every slice keeps at
   // least 8 stages)
   int ksplit = 1;
   if (!p.group_offs) {
-    const int tiles = m_tiles * n_tiles;
+    const int tiles = m_tiles0 * n_tiles;
     if (tiles < 200) ksplit = std::min(cdiv(256, tiles), std::max(1, (p.K / 64) / 8));
+  }
+  // e2m1 (MXFP4 / NVFP4) dense problems too small for 200 128-token tiles:
+  // measured on MI355X (K 2880, N 5760), 32-token tiles with a K split that
+  // shrinks as the tokens grow (MXFP4 64 tokens: 15.5 vs 20.0 us; 256: 25.5
+  // vs 32.2 us). INT4's costlier expansion keeps the larger tiles.
+  if (!p.group_offs && fmt != 2 && !env && (int64_t)cdiv(p.M, 128) * n_tiles < 200 && p.M <= 512) {
+    if (p.M <= 256) {
+      bm = 32;
+      ksplit = p.M <= 64 ? 4 : (p.M <= 128 ? 2 : 1);
+    } else {
+      bm = 64;
+      ksplit = 1;
+    }
+    ksplit = std::max(1, std::min(ksplit, p.K / 64));
   }
   const char* ks_env = getenv("QMOE_W4_KSPLIT");  // tuning knob
   if (ks_env && atoi(ks_env) > 0) ksplit = std::max(1, std::min(atoi(ks_env), p.K / 64));
