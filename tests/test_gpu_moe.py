@@ -163,6 +163,7 @@ def _moe_case(fmt, E, k, H, I, T, seed, bias=False):
     ("int4-32", "silu", 8, 2, 288, 160, 6, False),         # K % 64 == 32 in both GEMMs
     ("fp8_block", "silu", 8, 2, 512, 256, 5, False),
     ("fp8_block", "silu", 16, 4, 512, 256, 200, False),   # tiled path
+    ("fp8_block", "silu", 16, 4, 512, 256, 24, False),    # 6 rows per expert: tiled, 32-token tiles
     ("bf16", "silu", 8, 2, 256, 128, 9, False),
     ("bf16", "gelu_tanh", 8, 3, 256, 128, 100, True),
 ])

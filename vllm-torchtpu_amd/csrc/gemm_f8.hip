@@ -520,6 +520,9 @@ bool qmoe_f8_plan(const GemmParams& p, bool blk, int* bm_out, int* ksplit_out, i
     // block-scaled tiles hold at most 128 tokens; measured on MI355X (K 7168,
     // N 18432): 128-token tiles up to 256 and from 2048 tokens, 64 between
     bm = p.group_offs ? std::min(bm, 128) : (p.M > 256 && p.M < 2048 ? 64 : 128);
+    // grouped: 32-token tiles up to 12 rows per routed expert (measured on
+    // MI355X, DeepSeek-V3 experts: 4-12 rows 3-16% faster than 64)
+    if (p.group_offs && p.M <= 12 * std::max(1, std::min(p.slots, p.M))) bm = 32;
     if (blk_wide) {
       // (tokens: tile, split) 32: 32/2 (27 vs 34 us streaming), 64: 64/2
       // (33 vs 60 us), 128: 64/1 (49 vs 85 us), 256: 128/1, 512: 64/1,
