@@ -76,3 +76,31 @@ def test_product_path_has_no_cpu_fallback():
 
     with pytest.raises(ValueError, match="device tensors"):
         ops.row_quant(torch.zeros(2, 16, dtype=torch.bfloat16))
+
+
+def test_four_bit_descriptors_are_validated_on_the_host():
+    """NVFP4 / INT4 descriptors: scale layout and group checks run in
+    `qmoe_gemm_workspace_size` before any launch (pointer values are only
+    checked for alignment, never dereferenced)."""
+    from qmoe import _capi
+
+    def desc(kind, K=1024, ldws=None, group=0, scale_ptr=0x1000):
+        d = _capi.GemmDesc()
+        d.kind, d.a, d.w, d.y, d.w_scale = kind, 0x1000, 0x1000, 0x1000, scale_ptr
+        d.lda, d.ldw, d.ldy = K, K // 2, 256
+        d.M, d.N, d.K, d.slots, d.max_rows = 4, 256, K, 1, 4
+        d.ldws = ldws if ldws is not None else (K // 16 if kind == _capi.W4A16_NV else K // max(group, 1))
+        d.wq_group = group
+        return d
+
+    n = ctypes.c_int64(0)
+    ws = lambda d: _capi.lib.qmoe_gemm_workspace_size(ctypes.byref(d), ctypes.byref(n))  # noqa: E731
+    assert ws(desc(_capi.W4A16_NV)) == 0
+    assert ws(desc(_capi.W4A16_NV, ldws=32)) == 1            # fewer than K/16 scales per row
+    assert ws(desc(_capi.W4A16_NV, scale_ptr=0x1002)) == 1   # bf16 pairs need 4-byte alignment
+    for g in (32, 64, 128):
+        assert ws(desc(_capi.W4A16_I4, group=g)) == 0
+    assert ws(desc(_capi.W4A16_I4, group=48)) == 1           # groups of 32, 64 or 128 only
+    assert ws(desc(_capi.W4A16_I4, group=0)) == 1
+    assert ws(desc(_capi.W4A16_I4, K=1056, group=64)) == 1   # K not a multiple of the group
+    assert ws(desc(_capi.W4A16_I4, group=32, scale_ptr=0x1001)) == 1
