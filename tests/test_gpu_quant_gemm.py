@@ -280,6 +280,7 @@ def _int4_case(rng, n, k, group):
                                          (3, 2848, 200, 32), (7, 96, 130, 32), (2, 320, 64, 64),
                                          # tiled kernel (groups straddle and fill 64-k stages)
                                          (300, 2880, 768, 32), (520, 1024, 512, 128), (200, 4096, 1024, 64),
+                                         (256, 2880, 1000, 32), (400, 2048, 768, 64),
                                          # K % 64 == 32 above the streaming bound: 64-row streaming passes
                                          (70, 2848, 300, 32)])
 def test_w4a16_int4(dev, M, K, N, group):
