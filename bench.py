@@ -591,7 +591,7 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (got --gpus {args.gpus}); "
-              "the multi-GPU sharding design is documented in DESIGN.md", file=sys.stderr)
+              "sharding across GPUs is a design only in this build, not a measured path", file=sys.stderr)
         sys.exit(2)
     import torch
 
