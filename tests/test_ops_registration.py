@@ -15,6 +15,16 @@ E, H, I, T, K_TOP = 16, 256, 128, 15, 4
 
 
 def _moe_weights(dev, fmt):
+    if fmt == "nvfp4":
+        return (torch.empty((E, 2 * I, H // 2), dtype=torch.uint8, device=dev),
+                torch.empty((E, H, I // 2), dtype=torch.uint8, device=dev),
+                torch.empty((E, 2 * I, H // 16), dtype=torch.bfloat16, device=dev),
+                torch.empty((E, H, I // 16), dtype=torch.bfloat16, device=dev))
+    if fmt == "int4":
+        return (torch.empty((E, 2 * I, H // 8), dtype=torch.int32, device=dev),
+                torch.empty((E, H, I // 8), dtype=torch.int32, device=dev),
+                torch.empty((E, 2 * I, H // 64), dtype=torch.bfloat16, device=dev),
+                torch.empty((E, H, I // 64), dtype=torch.bfloat16, device=dev))
     if fmt == "mxfp4":
         return (torch.empty((E, 2 * I, H // 2), dtype=torch.uint8, device=dev),
                 torch.empty((E, H, I // 2), dtype=torch.uint8, device=dev),
@@ -37,16 +47,29 @@ def test_fake_shapes_and_dtypes():
         y = quantized_matmul_fp4(x, torch.empty((384, 128), dtype=torch.uint8, device="cuda"),
                                  torch.empty((384, 8), dtype=torch.uint8, device="cuda"))
         assert y.shape == (3, 5, 384)
+        # NVFP4: bf16 (or f32) scales per 16 k
+        y = quantized_matmul_fp4(x, torch.empty((384, 128), dtype=torch.uint8, device="cuda"),
+                                 torch.empty((384, 16), dtype=torch.bfloat16, device="cuda"))
+        assert y.shape == (3, 5, 384) and y.dtype == torch.bfloat16
+        with pytest.raises(ValueError, match="NVFP4 weight"):
+            quantized_matmul_fp4(x, torch.empty((384, 128), dtype=torch.uint8, device="cuda"),
+                                 torch.empty((384, 8), dtype=torch.float32, device="cuda"))
         logits = torch.empty((T, E), dtype=torch.bfloat16, device="cuda")
         h = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
         tw, ids = select_experts(h, logits, topk=K_TOP, renormalize=True, scoring_fn="softmax")
         assert tw.shape == (T, K_TOP) and tw.dtype == torch.bfloat16 and ids.dtype == torch.int32
         v, i = rowmax_select(torch.empty((7, E), device="cuda"), 3)
         assert v.shape == (7, 3) and v.dtype == torch.float32 and i.dtype == torch.int32
-        for fmt in ("mxfp4", "fp8_block"):
+        for fmt in ("mxfp4", "fp8_block", "nvfp4", "int4"):
             w1, w2, s1, s2 = _moe_weights("cuda", fmt)
             out = fused_moe_gmm(h, w1, w2, s1, s2, None, None, tw, ids, None, K_TOP, "silu", weight_format=fmt)
             assert out.shape == (T, H) and out.dtype == torch.bfloat16
+        # the reference's int4 marker selects the packed-int4 format from int32 carriers
+        w1, w2, s1, s2 = _moe_weights("cuda", "int4")
+        out = fused_moe_gmm(h, w1, w2, s1, s2, None, None, tw, ids, None, K_TOP, "silu", rhs_quant_dtype="int4")
+        assert out.shape == (T, H)
+        with pytest.raises(NotImplementedError):
+            fused_moe_gmm(h, w1, w2, s1, s2, None, None, tw, ids, None, K_TOP, "silu", rhs_quant_dtype="int2")
 
 
 def test_layer_traces_as_one_graph_of_qmoe_ops():
