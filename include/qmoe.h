@@ -118,6 +118,18 @@ int qmoe_row_quant(const void* x, int64_t ldx, int in_f32, int64_t M, int64_t K,
 int qmoe_gemm_workspace_size(const qmoe_gemm_desc* d, int64_t* bytes);
 
 /*
+ * The kernel choice qmoe_gemm makes for this problem, computed on the host
+ * from the descriptor alone (no device memory is read): path 0 weight
+ * streaming, 1 1-byte x 1-byte tiles, 2 bf16 x 4-bit tiles, 3 generic
+ * tiles, 4 weight streaming in 64-row passes; tile_m = token rows per tile
+ * (or per streaming pass); ksplit = K slices. No counterpart in the
+ * reference (its tiling is chosen inside the Pallas call,
+ * `kernels/megablox/gmm_v2.py:922-1055`); it lets tests assert which kernel
+ * instances they exercise. Any output pointer may be NULL.
+ */
+int qmoe_gemm_plan(const qmoe_gemm_desc* d, int32_t* path, int32_t* tile_m, int32_t* ksplit);
+
+/*
  * Quantized (grouped) GEMM. One group replaces the dense runtime matmul of
  * `layers/adapter/linear_common.py:69-128` (_quantized_matmul_jax ->
  * `kernels/quantized_matmul/util.py:80-124` xla_quantized_matmul, and the
@@ -205,10 +217,12 @@ int qmoe_moe_route_dispatch(const void* logits, int logits_f32, int64_t T, int E
  * Weighted unpermute, replaces `layers/core/fused_moe_gmm.py:572-577`:
  * out[t] = bf16( sum over valid slots j of rows[t*k + j] ), where `rows`
  * holds the already weighted down-projection rows in flat route order
- * (written by qmoe_gemm with row_weight and y_rows = sorted_idx).
+ * (written by qmoe_gemm with row_weight and y_rows = sorted_idx). A slot is
+ * valid under the dispatch rule: 0 <= id < E (and weight != 0 with
+ * skip_padded); the rows of other slots were never written and are skipped.
  */
 int qmoe_moe_combine(const uint16_t* rows, const int32_t* topk_ids, const uint16_t* topk_weights,
-                     int64_t T, int topk, int64_t H, int skip_padded, uint16_t* out, int64_t ldo,
+                     int64_t T, int topk, int E, int64_t H, int skip_padded, uint16_t* out, int64_t ldo,
                      qmoe_stream_t stream);
 
 #ifdef __cplusplus

@@ -97,13 +97,16 @@ class ExpertWeights:
     per-channel W8A8 recipe, restated in ``linear.w8a8_per_channel``).
     """
 
-    def __init__(self, fmt, w13, w13_scale, w2, w2_scale, b13=None, b2=None):
+    def __init__(self, fmt, w13, w13_scale, w2, w2_scale, b13=None, b2=None, keep=True):
         self.fmt, self.w13, self.s13, self.w2, self.s2 = fmt, w13, w13_scale, w2, w2_scale
         self.b13, self.b2 = b13, b2
+        self.keep = keep  # keep dequantized experts (False: bounded memory for large expert sets)
         self._cache = {}
 
     def dense(self, which, e):
         key = (which, e)
+        if not self.keep:
+            self._cache.clear()
         if key not in self._cache:
             w = self.w13[e] if which == 13 else self.w2[e]
             s = None
@@ -194,3 +197,37 @@ def fused_moe(hidden, weights: ExpertWeights, topk_weights, topk_ids, activation
         if pos < n_valid and meta["valid"][r]:
             out[r // k] += flat_w[r] * y_sorted[pos]
     return bf16_round(out), meta, inter_rows
+
+
+def fused_moe_tokens(hidden_rows, weights: ExpertWeights, topk_weights, topk_ids, activation,
+                     num_experts, skip_padded_tokens=False):
+    """The layer for a subset of tokens, one token at a time: the per-token
+    loop of the reference's test oracle `_reference_fused_moe`
+    (`tests/layers/core/test_fused_moe_gmm.py:387-427`: for each valid slot,
+    gate_up, activation, down, times the routing weight, summed over slots
+    in f32), with the arithmetic of `fused_moe` above (per-format expert
+    linears, bf16 intermediate, bf16 routing weights, ids outside
+    [0, num_experts) skipped as the permutation does). Every quantity of a
+    token depends on that token's row only, so the rows equal `fused_moe`'s
+    rows for the same tokens; this form touches only the experts the given
+    tokens route to.
+
+    hidden_rows [R, H], topk_weights / topk_ids [R, k] -> bf16-valued f32 [R, H].
+    """
+    x = np.asarray(hidden_rows, np.float32)
+    ids = np.asarray(topk_ids)
+    w = bf16_round(np.asarray(topk_weights, np.float32))
+    r, h = x.shape
+    out = np.zeros((r, h), np.float32)
+    for t in range(r):
+        acc = np.zeros(h, np.float32)
+        for j in range(ids.shape[1]):
+            e = int(ids[t, j])
+            if e < 0 or e >= num_experts or (skip_padded_tokens and w[t, j] == 0):
+                continue
+            gu = weights.linear(13, e, x[t:t + 1])
+            i = gu.shape[1] // 2
+            a = bf16_round(act_fn(gu[:, :i], gu[:, i:], activation))
+            acc += w[t, j] * weights.linear(2, e, a)[0]
+        out[t] = acc
+    return bf16_round(out)

@@ -5,7 +5,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import assert_close_rows
+from conftest import assert_close_rows, assert_close_same_codes
 from oracle import codecs, linear, quant
 from oracle import moe as omoe
 
@@ -165,7 +165,7 @@ def test_w8a8_fp8_per_channel(dev, M, K, N):
     xq, xs = ops.row_quant(_t(x, dev, torch.bfloat16), "fp8")
     np.testing.assert_array_equal(xq.view(torch.uint8).cpu().numpy(), xq_ref)
     y = ops.gemm(_capi.W8A8_PC, xq.view(torch.uint8), _t(wq, dev), a_scale=xs, w_scale=_t(ws, dev))
-    assert_close_rows(y.float().cpu().numpy(), ref, f"fp8 pc {M}x{K}x{N}")
+    assert_close_same_codes(y.float().cpu().numpy(), ref, f"fp8 pc {M}x{K}x{N}")
 
 
 @pytest.mark.parametrize("M,K,N", SHAPES_SKINNY + SHAPES_TILED)
@@ -213,7 +213,7 @@ def test_w8a8_fp8_block(dev, M, K, N, tile_scales):
     np.testing.assert_array_equal(xq.view(torch.uint8).cpu().numpy(), xq_ref)
     y = ops.gemm(_capi.W8A8_BLK, xq.view(torch.uint8), _t(wq, dev), a_scale=xs,
                  w_scale=_t(s_dev, dev), ws_bn=bn)
-    assert_close_rows(y.float().cpu().numpy(), ref, f"fp8 blk {M}x{K}x{N}")
+    assert_close_same_codes(y.float().cpu().numpy(), ref, f"fp8 blk {M}x{K}x{N}")
 
 
 def _nv_scales(rng, n, k):
@@ -243,7 +243,7 @@ def test_w4a16_nvfp4(dev, M, K, N):
     ref = linear.w4a16_nvfp4(x, packed, sc, bias)
     y = ops.gemm(_capi.W4A16_NV, _t(x, dev, torch.bfloat16), _t(packed, dev),
                  w_scale=_t(sc, dev, torch.bfloat16), bias=_t(bias, dev))
-    assert_close_rows(y.float().cpu().numpy(), ref, f"nvfp4 {M}x{K}x{N}")
+    assert_close_same_codes(y.float().cpu().numpy(), ref, f"nvfp4 {M}x{K}x{N}")
 
 
 @pytest.mark.parametrize("M,K,N", [(16, 2880, 320), (256, 4096, 512)])
@@ -294,7 +294,7 @@ def test_w4a16_int4(dev, M, K, N, group):
     ref = linear.w4a16_int4(x, carriers, sc, bias)
     y = ops.gemm(_capi.W4A16_I4, _t(x, dev, torch.bfloat16), _t(carriers, dev).view(torch.uint8),
                  w_scale=_t(sc, dev, torch.bfloat16), bias=_t(bias, dev))
-    assert_close_rows(y.float().cpu().numpy(), ref, f"int4 {M}x{K}x{N} g{group}")
+    assert_close_same_codes(y.float().cpu().numpy(), ref, f"int4 {M}x{K}x{N} g{group}")
 
 
 @pytest.mark.parametrize("M,K,N,group", [(16, 2048, 320, 32), (16, 4096, 256, 128), (256, 4096, 512, 64),
@@ -342,7 +342,7 @@ def test_w4a16_mxfp4(dev, M, K, N):
     ref = linear.w4a16_mxfp4(x, packed, sc, bias)
     y = ops.gemm(_capi.W4A16_MX, _t(x, dev, torch.bfloat16), _t(packed, dev), w_scale=_t(sc, dev),
                  bias=_t(bias, dev))
-    assert_close_rows(y.float().cpu().numpy(), ref, f"mxfp4 {M}x{K}x{N}")
+    assert_close_same_codes(y.float().cpu().numpy(), ref, f"mxfp4 {M}x{K}x{N}")
 
 
 @pytest.mark.parametrize("M,K,N", [(1, 1024, 512), (48, 512, 384), (100, 1024, 512)])
@@ -357,11 +357,11 @@ def test_w8a16_and_w16a16(dev, M, K, N):
     xt = _t(x, dev, torch.bfloat16)
     ref = linear.w8a16_per_channel(x, wq, ws)
     y = ops.gemm(_capi.W8A16_PC, xt, _t(wq, dev), w_scale=_t(ws, dev))
-    assert_close_rows(y.float().cpu().numpy(), ref, "w8a16")
+    assert_close_same_codes(y.float().cpu().numpy(), ref, "w8a16")
     wb = codecs.bf16_round(w)
     ref = linear.w16a16(x, wb)
     y = ops.gemm(_capi.W16A16, xt, _t(wb, dev, torch.bfloat16))
-    assert_close_rows(y.float().cpu().numpy(), ref, "w16a16")
+    assert_close_same_codes(y.float().cpu().numpy(), ref, "w16a16")
 
 
 def test_split_k_deterministic_and_reusable(dev):
@@ -380,7 +380,7 @@ def test_split_k_deterministic_and_reusable(dev):
     outs = [ops.gemm(_capi.W8A8_PC, xq.view(torch.uint8), wt, a_scale=xs, w_scale=wst) for _ in range(3)]
     for o in outs[1:]:
         assert torch.equal(o, outs[0])
-    assert_close_rows(outs[0].float().cpu().numpy(), ref, "split-k")
+    assert_close_same_codes(outs[0].float().cpu().numpy(), ref, "split-k")
 
 
 @pytest.mark.parametrize("M,K,I", [(200, 1024, 384), (96, 8192, 256)])
@@ -402,7 +402,8 @@ def test_w8a8_fp8_block_fused_activation(dev, M, K, I):
     assert_close_rows(y.float().cpu().numpy(), ref, f"fp8 blk silu {M}x{K}x{I}")
 
 
-@pytest.mark.parametrize("act", ["silu", "swigluoai"])
+@pytest.mark.parametrize("act", ["silu", "swigluoai", "gelu", "gelu_tanh", "silu_and_mul_with_clamp",
+                                 "situ:2.0:none", "situ:1.5:3.0"])
 def test_tiled_split_k_fused_activation(dev, act):
     """Tiled FP8 GEMM with a K split and the gate/up activation applied by
     the split-K finishing kernel."""
@@ -423,3 +424,75 @@ def test_tiled_split_k_fused_activation(dev, act):
                  activation=act)
     assert_close_rows(y.float().cpu().numpy(), ref, f"split-k {act}")
 
+
+
+ACTS = ["silu", "swigluoai", "gelu", "gelu_tanh", "silu_and_mul_with_clamp", "situ:2.0:none", "situ:1.5:3.0"]
+
+
+@pytest.mark.parametrize("act", ACTS)
+@pytest.mark.parametrize("M", [8, 200])
+def test_fused_activation_strings(dev, act, M):
+    """Every activation string of `kernels/megablox/gmm_v2.py:101-122` fused
+    into the gate/up epilogue, through the streaming (M = 8) and the tiled
+    (M = 200) kernels, FP8 per-channel weights. Gate/up sums are scaled
+    up so that the clamps (7, 10) and the tanh saturations are reached."""
+    from qmoe import _capi, ops
+
+    print(f"fused act {act} M={M}", flush=True)
+    rng = np.random.default_rng(M + len(act))
+    K, I = 1024, 384
+    w = (rng.standard_normal((2 * I, K)) * 0.4).astype(np.float32)
+    wq, ws = quant.quantize_tensor(w, "fp8")
+    x = _bf16(rng, (M, K))
+    xq_ref, sx = quant.quantize_act(x, "fp8")
+    acc = codecs.e4m3_decode(xq_ref).astype(np.float64) @ codecs.e4m3_decode(wq).astype(np.float64).T
+    gu = ((acc.astype(np.float32) * sx[:, None]).astype(np.float32) * ws[None, :]).astype(np.float32)
+    assert np.abs(gu).max() > 12.0  # the clamps bind
+    ref = codecs.bf16_round(omoe.act_fn(gu[:, :I], gu[:, I:], act))
+    xq, xs = ops.row_quant(_t(x, dev, torch.bfloat16), "fp8")
+    y = ops.gemm(_capi.W8A8_PC, xq.view(torch.uint8), _t(wq, dev), a_scale=xs, w_scale=_t(ws, dev),
+                 activation=act)
+    assert_close_rows(y.float().cpu().numpy(), ref, f"act {act} M={M}")
+
+
+# e8m0 bytes with known answers in the reference's decoder tests
+# (`tests/layers/core/test_mxfp4_requantization.py:194-209`)
+E8M0_EDGE = [0, 1, 127, 128, 253, 254, 255]
+
+
+@pytest.mark.parametrize("M", [16, 256])
+def test_mxfp4_one_hot_dequant_e8m0_edges(dev, M):
+    """One-hot activation rows read single dequantized MXFP4 weights back
+    through the streaming (M = 16) and tiled (M = 256) kernels, with the e8m0
+    edge bytes 0 (2^-127, an f32 subnormal), 1, 127, 128, 253, 254 and 255
+    (+inf) among the block scales. Rows holding only finite weights must read
+    back LUT[code] * 2^(byte - 127) exactly (bf16 values; subnormals kept);
+    the oracle's own matmul defines the rows that hold an inf (0 * inf = NaN
+    there)."""
+    from qmoe import _capi, ops
+
+    print(f"mxfp4 one-hot e8m0 edges M={M}", flush=True)
+    K, N = 1024, 256
+    rng = np.random.default_rng(M)
+    packed = rng.integers(0, 256, (N, K // 2), dtype=np.uint8)
+    sc = np.full((N, K // 32), 127, np.uint8)
+    safe = np.array([0, 1, 127, 128], np.uint8)
+    # rows 0..N/2: every block scale from {0, 1, 127, 128} (finite weights)
+    sc[: N // 2] = safe[rng.integers(0, 4, (N // 2, K // 32))]
+    # rows N/2..: the large bytes too (weights up to 6 * 2^127: inf in f32)
+    sc[N // 2:] = np.array(E8M0_EDGE, np.uint8)[rng.integers(0, 7, (N - N // 2, K // 32))]
+    ks = (np.arange(M) * (K // M) + np.arange(M) * 5) % K
+    x = np.zeros((M, K), np.float32)
+    x[np.arange(M), ks] = 1.0
+    y = ops.gemm(_capi.W4A16_MX, _t(x, dev, torch.bfloat16), _t(packed, dev), w_scale=_t(sc, dev))
+    got = y.float().cpu().numpy()
+    deq = codecs.dequant_mxfp4(packed, sc)
+    want = deq[:, ks].T  # [M, N]
+    fin = np.isfinite(deq).all(axis=1)  # rows whose every weight is finite
+    assert fin[: N // 2].all() and not fin.all()
+    np.testing.assert_array_equal(got[:, fin], want[:, fin])
+    sub = (sc[: N // 2] == 0).any()
+    assert sub, "subnormal scales are exercised"
+    with np.errstate(invalid="ignore", over="ignore"):
+        ref = linear.w4a16_mxfp4(x, packed, sc)
+    np.testing.assert_array_equal(np.isnan(got[:, ~fin]), np.isnan(ref[:, ~fin]))

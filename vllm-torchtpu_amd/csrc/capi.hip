@@ -4,15 +4,17 @@
 #include <algorithm>
 #include <cstdlib>
 
-#include "../../include/qmoe.h"
-#include "gemm_common.h"
+#include "gemm_route.h"
 
 // defined in gemm_skinny.hip / gemm_tiled.hip / gemm_f8.hip
 void qmoe_skinny_plan(int kind, int64_t M, int64_t N, int64_t K, int act, int slots, int rows,
                       int ksplit_hint, int* ksplit_out, int64_t* ws_bytes);
 int qmoe_skinny_launch(int kind, GemmParams p, int max_rows, int slots, void* workspace,
                        int64_t ws_bytes, int ksplit_hint, hipStream_t st);
+int qmoe_skinny_check(int kind, const GemmParams& p);
+int qmoe_skinny_tile_rows(int max_rows);
 int qmoe_tiled_launch(int kind, GemmParams p, hipStream_t st);
+int qmoe_tiled_check(int kind, const GemmParams& p, int* tile);
 bool qmoe_f8_plan(const GemmParams& p, bool blk, int* bm_out, int* ksplit_out, int64_t* ws_bytes);
 int qmoe_f8_launch(GemmParams p, bool blk, void* workspace, int64_t ws_bytes, hipStream_t st);
 bool qmoe_w4_plan(const GemmParams& p, int fmt, int* bm_out, int* ksplit_out, int64_t* ws_bytes);
@@ -26,7 +28,9 @@ constexpr int kSkinnyMaxGroupRowsBlk = 3;
 constexpr int kSkinnyMaxRowsW8A8 = 32;  // also dense e2m1
 constexpr int kSkinnyMaxRowsBlkWide = 16;
 
-int to_params(const qmoe_gemm_desc* d, GemmParams* p) {
+}  // namespace
+
+int qmoe_to_params(const qmoe_gemm_desc* d, GemmParams* p) {
   if (!d) return QMOE_ERR_ARG;
   if (d->kind < QMOE_W8A8_PC || d->kind > QMOE_W4A16_I4) return QMOE_ERR_ARG;
   if (d->kind == QMOE_W8A8_PC && d->wfmt != 0 && d->wfmt != 1) return QMOE_ERR_ARG;
@@ -90,6 +94,8 @@ int to_params(const qmoe_gemm_desc* d, GemmParams* p) {
   return QMOE_OK;
 }
 
+namespace {
+
 // Grid depth of the skinny kernel: every group, or -- with an active list --
 // at most one slot per row (a listed group has at least one row).
 int skinny_slots(const qmoe_gemm_desc* d) {
@@ -145,63 +151,113 @@ bool use_f8(const qmoe_gemm_desc* d) {
   return d->kind == QMOE_W8A8_PC || (d->kind == QMOE_W8A8_BLK && !getenv("QMOE_F8_BLK_OFF"));
 }
 
+// Kernel paths of qmoe_gemm (reported by qmoe_gemm_plan).
+enum Path {
+  kPathSkinny = 0,      // weight streaming (decode)
+  kPathF8 = 1,          // 1-byte x 1-byte tiles
+  kPathW4 = 2,          // bf16 x 4-bit tiles
+  kPathTiled = 3,       // generic tiles
+  kPathSkinnyPass = 4,  // weight streaming in 64-row passes (K outside every tiled granule)
+};
+
+// The one place that decides which kernel runs a problem: the streaming
+// kernel within its row limits (unless it declines the operands), else the
+// format's tiled kernel, else the generic tiled kernel, else the streaming
+// kernel in 64-row passes. The tiled kernels enumerate m-tiles over all
+// groups; the active list is a streaming-path device (it bounds the grid by
+// the number of routed experts), so `p` has it cleared for them.
 }  // namespace
 
-extern "C" int qmoe_abi_version(void) { return 2; }
+int qmoe_route_of(const qmoe_gemm_desc* d, GemmParams& p, QmoeRoute* r) {
+  const int kind = d->kind;
+  if (use_skinny(d) && qmoe_skinny_check(kind, p) == QMOE_OK) {
+    r->path = kPathSkinny;
+    r->tile_m = qmoe_skinny_tile_rows(skinny_rows(d));
+    qmoe_skinny_plan(kind, d->M, d->N, d->K, d->act, skinny_slots(d), skinny_rows(d), 0, &r->ksplit,
+                     &r->ws_bytes);
+    return QMOE_OK;
+  }
+  const bool skinny_first = use_skinny(d);
+  p.active = nullptr;
+  p.num_active = nullptr;
+  if (!skinny_first) {
+    int bm = 0, ks = 1;
+    int64_t ws = 0;
+    if (use_f8(d) && qmoe_f8_plan(p, kind == QMOE_W8A8_BLK, &bm, &ks, &ws)) {
+      *r = QmoeRoute{kPathF8, bm, ks, ws};
+      return QMOE_OK;
+    }
+    if (!use_f8(d) && use_w4(d) && qmoe_w4_plan(p, w4_fmt(d), &bm, &ks, &ws)) {
+      *r = QmoeRoute{kPathW4, bm, ks, ws};
+      return QMOE_OK;
+    }
+  }
+  int tile = 128;
+  if (qmoe_tiled_check(kind, p, &tile) == QMOE_OK) {
+    *r = QmoeRoute{kPathTiled, tile, 1, 0};
+    return QMOE_OK;
+  }
+  // bf16 activations with K % 64 == 32 (no tiled granule): the streaming
+  // kernel takes any K % 32 == 0, in passes of 64 rows per group
+  if (!skinny_first && qmoe_skinny_check(kind, p) == QMOE_OK) {
+    *r = QmoeRoute{kPathSkinnyPass, qmoe_skinny_tile_rows(kSkinnyMaxRows), 1, 0};
+    return QMOE_OK;
+  }
+  return QMOE_ERR_ARG;
+}
+
+int qmoe_run_route(const qmoe_gemm_desc* d, const QmoeRoute& r, GemmParams p, void* workspace,
+                   int64_t ws_bytes, hipStream_t stream) {
+  switch (r.path) {
+    case kPathSkinny: {
+      GemmParams q;
+      qmoe_to_params(d, &q);  // keeps the active list
+      return qmoe_skinny_launch(d->kind, q, skinny_rows(d), skinny_slots(d), workspace, ws_bytes, 0, stream);
+    }
+    case kPathF8: return qmoe_f8_launch(p, d->kind == QMOE_W8A8_BLK, workspace, ws_bytes, stream);
+    case kPathW4: return qmoe_w4_launch(p, w4_fmt(d), workspace, ws_bytes, stream);
+    case kPathTiled: return qmoe_tiled_launch(d->kind, p, stream);
+    default: {
+      GemmParams q;
+      qmoe_to_params(d, &q);
+      return qmoe_skinny_launch(d->kind, q, kSkinnyMaxRows, skinny_slots(d), workspace, ws_bytes, 1, stream);
+    }
+  }
+}
+
+extern "C" int qmoe_abi_version(void) { return 3; }
 
 extern "C" int qmoe_gemm_workspace_size(const qmoe_gemm_desc* d, int64_t* bytes) {
   GemmParams p;
-  const int st = to_params(d, &p);
+  const int st = qmoe_to_params(d, &p);
   if (st != QMOE_OK) return st;
-  *bytes = 0;
-  if (use_skinny(d)) {
-    int ks = 1;
-    qmoe_skinny_plan(d->kind, d->M, d->N, d->K, d->act, skinny_slots(d), skinny_rows(d), 0, &ks, bytes);
-  } else if (use_f8(d) || use_w4(d)) {
-    p.active = nullptr;
-    p.num_active = nullptr;
-    int bm = 0, ks = 1;
-    const bool ok = use_w4(d) ? qmoe_w4_plan(p, w4_fmt(d), &bm, &ks, bytes)
-                              : qmoe_f8_plan(p, d->kind == QMOE_W8A8_BLK, &bm, &ks, bytes);
-    if (!ok) *bytes = 0;
-  }
+  QmoeRoute r;
+  *bytes = qmoe_route_of(d, p, &r) == QMOE_OK ? r.ws_bytes : 0;
+  return QMOE_OK;
+}
+
+extern "C" int qmoe_gemm_plan(const qmoe_gemm_desc* d, int32_t* path, int32_t* tile_m, int32_t* ksplit) {
+  GemmParams p;
+  const int st = qmoe_to_params(d, &p);
+  if (st != QMOE_OK) return st;
+  QmoeRoute r;
+  const int rc = qmoe_route_of(d, p, &r);
+  if (rc != QMOE_OK) return rc;
+  if (path) *path = r.path;
+  if (tile_m) *tile_m = r.tile_m;
+  if (ksplit) *ksplit = r.ksplit;
   return QMOE_OK;
 }
 
 extern "C" int qmoe_gemm(const qmoe_gemm_desc* d, void* workspace, int64_t ws_bytes,
                          hipStream_t stream) {
   GemmParams p;
-  const int st = to_params(d, &p);
+  const int st = qmoe_to_params(d, &p);
   if (st != QMOE_OK) return st;
   if (d->M == 0) return QMOE_OK;
-  if (use_skinny(d)) {
-    // the skinny kernel declines (QMOE_ERR_ARG) operands of 2 GiB or more,
-    // which the generic tiled kernel takes
-    const int rc = qmoe_skinny_launch(d->kind, p, skinny_rows(d), skinny_slots(d), workspace, ws_bytes, 0, stream);
-    if (rc != QMOE_ERR_ARG) return rc;
-    p.active = nullptr;
-    p.num_active = nullptr;
-    return qmoe_tiled_launch(d->kind, p, stream);
-  }
-  // the tiled kernel enumerates m-tiles over all groups; the active list is
-  // a skinny-path device (it bounds the grid by the number of routed experts)
-  p.active = nullptr;
-  p.num_active = nullptr;
-  // the 1-byte x 1-byte and the bf16 x e2m1 kernels decline (QMOE_ERR_ARG)
-  // problems outside their envelopes (K granule, alignment), which the
-  // generic kernel takes
-  if (use_f8(d)) {
-    const int rc = qmoe_f8_launch(p, d->kind == QMOE_W8A8_BLK, workspace, ws_bytes, stream);
-    if (rc != QMOE_ERR_ARG) return rc;
-  } else if (use_w4(d)) {
-    const int rc = qmoe_w4_launch(p, w4_fmt(d), workspace, ws_bytes, stream);
-    if (rc != QMOE_ERR_ARG) return rc;
-  }
-  const int rc = qmoe_tiled_launch(d->kind, p, stream);
-  if (rc != QMOE_ERR_ARG) return rc;
-  // K outside the tiled kernels' granule (bf16 activations: K % 64 == 32):
-  // the streaming kernel takes any K % 32 == 0, in passes of 64 rows per group
-  GemmParams q;
-  to_params(d, &q);
-  return qmoe_skinny_launch(d->kind, q, kSkinnyMaxRows, skinny_slots(d), workspace, ws_bytes, 1, stream);
+  QmoeRoute r;
+  const int rc = qmoe_route_of(d, p, &r);
+  if (rc != QMOE_OK) return rc;
+  return qmoe_run_route(d, r, p, workspace, ws_bytes, stream);
 }
+

@@ -837,14 +837,10 @@ void qmoe_skinny_plan(int kind, int64_t M, int64_t N, int64_t K, int act, int sl
   *ws_bytes = pl.ws_bytes;
 }
 
-// Host-side launcher shared by the dense and MoE entry points.
-//   max_rows : rows the M tile is sized for (groups with more rows are
-//              still correct, in more passes)
-//   slots    : gridDim.z (groups, or the capacity of the active list)
-// Returns a QMOE_* status.
-int qmoe_skinny_launch(int kind, GemmParams p, int max_rows, int slots, void* workspace,
-                       int64_t ws_bytes, int ksplit_hint, hipStream_t st) {
-  if (max_rows <= 0 || slots <= 0 || p.M <= 0) return QMOE_OK;
+// Whether the skinny kernel takes the problem: QMOE_OK, or QMOE_ERR_ARG for
+// shapes outside its envelope (K granule, operands of 2 GiB or more, scale
+// alignment), which the generic tiled kernel takes.
+int qmoe_skinny_check(int kind, const GemmParams& p) {
   if (p.K <= 0 || (p.K % 32) != 0 || p.N <= 0) return QMOE_ERR_ARG;
   if (p.act != QA_NONE && (p.N % 2) != 0) return QMOE_ERR_ARG;
   if (kind == QK_W8A8_BLK && (p.K % 128) != 0) return QMOE_ERR_ARG;
@@ -863,6 +859,22 @@ int qmoe_skinny_launch(int kind, GemmParams p, int max_rows, int slots, void* wo
   if (kind == QK_W8A8_BLK &&
       ((int64_t)cdiv(p.N, p.ws_bn) * p.ldws * 4 > kLim || p.M * p.lds_a * 4 > kLim))
     return QMOE_ERR_ARG;
+  return QMOE_OK;
+}
+
+// Token rows one pass of the skinny kernel covers (16, 32 or 64).
+int qmoe_skinny_tile_rows(int max_rows) { return 16 * skinny_ms(max_rows); }
+
+// Host-side launcher shared by the dense and MoE entry points.
+//   max_rows : rows the M tile is sized for (groups with more rows are
+//              still correct, in more passes)
+//   slots    : gridDim.z (groups, or the capacity of the active list)
+// Returns a QMOE_* status.
+int qmoe_skinny_launch(int kind, GemmParams p, int max_rows, int slots, void* workspace,
+                       int64_t ws_bytes, int ksplit_hint, hipStream_t st) {
+  if (max_rows <= 0 || slots <= 0 || p.M <= 0) return QMOE_OK;
+  const int chk = qmoe_skinny_check(kind, p);
+  if (chk != QMOE_OK) return chk;
   const int ms = skinny_ms(max_rows);
   const int ns = skinny_ns(kind, ms);
   const int n_tiles = skinny_tiles(p.N, p.act, ns);

@@ -527,16 +527,15 @@ void launch_shape(const GemmParams& p, bool big, hipStream_t st) {
 
 // Tile shape: 256 x 256 when the problem has enough such tiles to fill the
 // GPU (>= 2 per CU), else 128 x 128.
-int qmoe_tiled_launch(int kind, GemmParams p, hipStream_t st) {
-  if (p.M <= 0) return QMOE_OK;
+// Whether the generic tiled kernel takes the problem (QMOE_OK) and its
+// tile edge (128, or 256 with the QMOE_TILED_BIG knob).
+int qmoe_tiled_check(int kind, const GemmParams& p, int* tile) {
   const bool abf16 = kind == QK_W8A16_PC || kind == QK_W4A16_MX || kind == QK_W16A16;
   const int kstage = abf16 ? 64 : 128;
+  if (kind != QK_W8A8_PC && kind != QK_W8A8_BLK && !abf16) return QMOE_ERR_ARG;
   if (p.K <= 0 || (p.K % kstage) != 0 || p.N <= 0) return QMOE_ERR_ARG;
   if (p.act != QA_NONE && (p.N % 2) != 0) return QMOE_ERR_ARG;
-  const int nout = p.act != QA_NONE ? p.N / 2 : p.N;
-  const int64_t big_tiles = (int64_t)cdiv(p.M, 256) * cdiv(nout, p.act != QA_NONE ? 128 : 256);
   bool big = false;  // 128 x 128 measured faster or equal on every config shape
-  (void)big_tiles;
   const char* env = getenv("QMOE_TILED_BIG");  // tuning knob: force 1 / 0
   if (env) big = atoi(env) != 0;
   if (kind != QK_W8A8_PC && kind != QK_W8A16_PC) big = false;
@@ -544,6 +543,16 @@ int qmoe_tiled_launch(int kind, GemmParams p, hipStream_t st) {
     const int m_tiles = cdiv(p.M, big ? 256 : 128) + std::min(p.slots, p.M);
     if (m_tiles > 65535) return QMOE_ERR_ARG;
   }
+  *tile = big ? 256 : 128;
+  return QMOE_OK;
+}
+
+int qmoe_tiled_launch(int kind, GemmParams p, hipStream_t st) {
+  if (p.M <= 0) return QMOE_OK;
+  int tile = 128;
+  const int chk = qmoe_tiled_check(kind, p, &tile);
+  if (chk != QMOE_OK) return chk;
+  const bool big = tile == 256;
   switch (kind) {
     case QK_W8A8_PC:
       if (p.wfmt == 0) launch_shape<QK_W8A8_PC, 0>(p, big, st);

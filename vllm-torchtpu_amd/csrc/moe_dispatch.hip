@@ -144,7 +144,7 @@ __global__ __launch_bounds__(64) void dispatch_small_kernel(
 __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict__ rows,
                                                       const int32_t* __restrict__ ids,
                                                       const uint16_t* __restrict__ wts, int topk,
-                                                      int64_t H, int skip_padded,
+                                                      int E, int64_t H, int skip_padded,
                                                       uint16_t* __restrict__ out, int64_t ldo) {
   const int64_t t = blockIdx.x;
   const int64_t h = ((int64_t)blockIdx.y * 256 + threadIdx.x) * 8;
@@ -153,7 +153,9 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
   for (int j = 0; j < topk; ++j) {
     const int64_t f = t * topk + j;
     const int id = ids[f];
-    bool ok = id >= 0;
+    // the dispatch kernels' validity rule: ids outside [0, E) sort into the
+    // invalid bucket, so the down GEMM never wrote their rows
+    bool ok = id >= 0 && id < E;
     if (skip_padded && ok) ok = (wts[f] & 0x7fffu) != 0;
     if (!ok) continue;
     const uint4 v = *reinterpret_cast<const uint4*>(rows + f * H + h);
@@ -193,13 +195,13 @@ extern "C" int qmoe_moe_dispatch(const int32_t* topk_ids, const uint16_t* topk_w
 }
 
 extern "C" int qmoe_moe_combine(const uint16_t* rows, const int32_t* topk_ids,
-                                const uint16_t* topk_weights, int64_t T, int topk, int64_t H,
+                                const uint16_t* topk_weights, int64_t T, int topk, int E, int64_t H,
                                 int skip_padded, uint16_t* out, int64_t ldo, hipStream_t stream) {
-  if (T < 0 || topk <= 0 || H <= 0 || (H % 8) != 0 || ldo < H || (ldo % 8) != 0) return QMOE_ERR_ARG;
+  if (T < 0 || topk <= 0 || E <= 0 || H <= 0 || (H % 8) != 0 || ldo < H || (ldo % 8) != 0) return QMOE_ERR_ARG;
   if (T == 0) return QMOE_OK;
   if (cdiv<int64_t>(H, 256 * 8) > 65535) return QMOE_ERR_ARG;
   dim3 grid((unsigned)T, (unsigned)cdiv<int64_t>(H, 256 * 8));
   hipLaunchKernelGGL(combine_kernel, grid, dim3(256), 0, stream, rows, topk_ids, topk_weights, topk,
-                     H, skip_padded, out, ldo);
+                     E, H, skip_padded, out, ldo);
   return hipGetLastError() == hipSuccess ? QMOE_OK : QMOE_ERR_LAUNCH;
 }

@@ -117,4 +117,5 @@ enum {
   QMOE_ERR_ARG = 1,        // bad shape / unsupported combination
   QMOE_ERR_WORKSPACE = 2,  // workspace too small
   QMOE_ERR_LAUNCH = 3,     // hipGetLastError after launch
+  QMOE_ERR_SCRATCH = 4,    // qmoe_gemm_static: the problem's split-K partials exceed the static scratch
 };

@@ -9,7 +9,7 @@ import os
 
 _LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libqmoe.so")
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 QMOE_OK = 0
 STATUS_TEXT = {
@@ -81,6 +81,9 @@ def _load():
                                    ctypes.c_int, _vp, _i64, _vp, _i64, _vp]
     lib.qmoe_gemm_workspace_size.restype = ctypes.c_int
     lib.qmoe_gemm_workspace_size.argtypes = [ctypes.POINTER(GemmDesc), ctypes.POINTER(_i64)]
+    lib.qmoe_gemm_plan.restype = ctypes.c_int
+    lib.qmoe_gemm_plan.argtypes = [ctypes.POINTER(GemmDesc), ctypes.POINTER(_i32), ctypes.POINTER(_i32),
+                                   ctypes.POINTER(_i32)]
     lib.qmoe_gemm.restype = ctypes.c_int
     lib.qmoe_gemm.argtypes = [ctypes.POINTER(GemmDesc), _vp, _i64, _vp]
     lib.qmoe_moe_route.restype = ctypes.c_int
@@ -98,7 +101,7 @@ def _load():
     lib.qmoe_moe_route_hash.argtypes = [_vp, ctypes.c_int, _i64, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp,
                                         _i64, _vp, ctypes.c_int, ctypes.c_int, _f32, _vp, _vp, _vp]
     lib.qmoe_moe_combine.restype = ctypes.c_int
-    lib.qmoe_moe_combine.argtypes = [_vp, _vp, _vp, _i64, ctypes.c_int, _i64, ctypes.c_int, _vp,
+    lib.qmoe_moe_combine.argtypes = [_vp, _vp, _vp, _i64, ctypes.c_int, ctypes.c_int, _i64, ctypes.c_int, _vp,
                                      _i64, _vp]
     v = lib.qmoe_abi_version()
     if v != ABI_VERSION:
@@ -112,6 +115,7 @@ EXPORTED = (
     "qmoe_abi_version",
     "qmoe_row_quant",
     "qmoe_gemm_workspace_size",
+    "qmoe_gemm_plan",
     "qmoe_gemm",
     "qmoe_moe_route",
     "qmoe_moe_dispatch",

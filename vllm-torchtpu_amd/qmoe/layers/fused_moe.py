@@ -64,8 +64,12 @@ def fused_moe_gmm(hidden_states, w1, w2, w1_scale, w2_scale, w1_bias, w2_bias, t
     ``rhs_quant_dtype``: ``int4`` (any dtype object or string naming int4) marks
     packed-int4 int32 weights (`compressed_tensors_moe_w4a16.py:380-405`).
     """
-    if experts_start is not None and not isinstance(experts_start, torch.Tensor) and int(experts_start) != 0:
-        raise NotImplementedError("expert parallelism is out of scope: experts_start must be 0")
+    # The reference passes experts_start as a 0-d int32 tensor exactly when
+    # expert parallelism is on (`layers/adapter/fused_moe.py:241-293`); this
+    # build holds the whole expert set, so any tensor (whatever its value) and
+    # any non-zero offset is refused rather than silently ignored.
+    if experts_start is not None and (isinstance(experts_start, torch.Tensor) or int(experts_start) != 0):
+        raise NotImplementedError("expert parallelism is out of scope: experts_start must be None or 0")
     if rhs_quant_dtype is not None:
         if "int4" not in str(rhs_quant_dtype):
             raise NotImplementedError(f"rhs_quant_dtype {rhs_quant_dtype} is not supported (int4 only)")
@@ -196,7 +200,7 @@ def _moe_body(x, w1, w2, w1_scale, w2_scale, w1_bias, w2_bias, tw, topk_ids, top
     routed = torch.empty((M, H), dtype=torch.bfloat16, device=x.device)
     ops.gemm(kind, a2, w2k, a_scale=a2_scale, w_scale=w2s, wfmt=wf, ws_bn=bn, bias=b2,
              row_weight=meta["sorted_weight"], y_rows=meta["sorted_idx"], out=routed, **common)
-    return ops.moe_combine(routed, topk_ids, tw, skip)
+    return ops.moe_combine(routed, topk_ids, tw, E, skip)
 
 
 @_fused_moe_gmm_op.register_fake

@@ -113,16 +113,31 @@ def row_quant(x, qdtype="fp8", block=None, mode="runtime"):
 # ---------------------------------------------------------------- GEMM
 
 
-def gemm(kind, a, w, *, a_scale=None, w_scale=None, bias=None, wfmt=0, ws_bn=1,
-         group_offs=None, active=None, num_active=None, slots=1, max_rows=None, a_rows=None,
-         activation=None, row_weight=None, out=None, y_rows=None, M=None):
-    """Run one (grouped) quantized GEMM through `qmoe_gemm`.
+def gemm(kind, a, w, **kw):
+    """Run one (grouped) quantized GEMM through `qmoe_gemm` (arguments as
+    `gemm_desc`); the split-K workspace comes from a per-device buffer grown
+    on demand. Returns ``out`` ([M, N or N/2] bf16 unless given)."""
+    d, out = gemm_desc(kind, a, w, **kw)
+    dev = a.device
+    need = ctypes.c_int64(0)
+    check(lib.qmoe_gemm_workspace_size(ctypes.byref(d), ctypes.byref(need)), "gemm (plan)")
+    if _plan_log is not None:
+        _plan_log.append(plan_of_desc(d))
+    ws_t, ws_n = _workspace(dev, need.value)
+    check(lib.qmoe_gemm(ctypes.byref(d), _ptr(ws_t), ws_n, _stream(dev)), "gemm")
+    return out
+
+
+def gemm_desc(kind, a, w, *, a_scale=None, w_scale=None, bias=None, wfmt=0, ws_bn=1,
+              group_offs=None, active=None, num_active=None, slots=1, max_rows=None, a_rows=None,
+              activation=None, row_weight=None, out=None, y_rows=None, M=None):
+    """Checked `qmoe_gemm_desc` of one (grouped) quantized GEMM, and its
+    output tensor (allocated here unless ``out`` is given).
 
     a        : [rows, K] activation codes (1 byte) or bf16
     w        : [G, N, K] / [N, K] weights (1 byte codes, packed e2m1 [.., K/2], bf16)
     w_scale  : per-channel f32 [G, N] | block f32 [G, N/bn, K/128] | e8m0 u8 [G, N, K/32]
                | NVFP4 bf16 [G, N, K/16] | INT4 bf16 [G, N, K/group] (group 32, 64 or 128)
-    Returns ``out`` ([M, N or N/2] bf16 unless given).
     """
     _require_gpu(a, w)
     dev = a.device
@@ -193,11 +208,84 @@ def gemm(kind, a, w, *, a_scale=None, w_scale=None, bias=None, wfmt=0, ws_bn=1,
     d.y = out.data_ptr()
     d.ldy = out.stride(0)
     d.y_rows = y_rows.data_ptr() if y_rows is not None else None
-    need = ctypes.c_int64(0)
-    check(lib.qmoe_gemm_workspace_size(ctypes.byref(d), ctypes.byref(need)), "gemm (plan)")
-    ws_t, ws_n = _workspace(dev, need.value)
-    check(lib.qmoe_gemm(ctypes.byref(d), _ptr(ws_t), ws_n, _stream(dev)), "gemm")
-    return out
+    return d, out
+
+
+# ---------------------------------------------------------------- kernel plans
+
+PATH_NAMES = ("stream", "tiled_1b", "tiled_4b", "tiled_generic", "stream_passes")
+
+_plan_log = None
+
+
+def plan_of_desc(d):
+    """(kind, wfmt, fused activation, grouped, path name, token rows per
+    tile, K split) that `qmoe_gemm` picks for the descriptor (host-side
+    `qmoe_gemm_plan`)."""
+    path, tile, ks = ctypes.c_int32(0), ctypes.c_int32(0), ctypes.c_int32(0)
+    check(lib.qmoe_gemm_plan(ctypes.byref(d), ctypes.byref(path), ctypes.byref(tile), ctypes.byref(ks)),
+          "gemm_plan")
+    return (int(d.kind), int(d.wfmt), int(d.act != _capi.ACT_NONE), int(bool(d.group_offs)),
+            PATH_NAMES[path.value], int(tile.value), int(ks.value))
+
+
+class record_plans:
+    """Context manager collecting the plan of every `gemm` call made inside
+    it (a list of `plan_of_desc` tuples)."""
+
+    def __enter__(self):
+        global _plan_log
+        self._prev = _plan_log
+        _plan_log = self.plans = []
+        return self.plans
+
+    def __exit__(self, *exc):
+        global _plan_log
+        _plan_log = self._prev
+        if self._prev is not None:
+            self._prev.extend(self.plans)
+        return False
+
+
+def plan_for_shape(kind, M, N, K, *, wfmt=0, activation=None, experts=0, max_rows=None, ws_bn=1,
+                   wq_group=0, lda=None):
+    """The plan `qmoe_gemm` makes for a problem of this shape, from a
+    descriptor with placeholder (aligned, never dereferenced) addresses and
+    contiguous strides: dense when ``experts == 0``, else grouped over
+    ``experts`` groups with an active list, ``max_rows`` rows at most per
+    group (the MoE layer passes the token count). Needs no GPU."""
+    w4 = kind in (_capi.W4A16_MX, _capi.W4A16_NV, _capi.W4A16_I4)
+    act, p0, p1 = act_code(activation)
+    base = 1 << 24
+    d = GemmDesc()
+    d.kind, d.wfmt = kind, wfmt
+    d.a = d.w = d.y = d.w_scale = d.a_scale = base
+    d.lda = lda if lda is not None else K
+    d.lds_a = K // 128 if kind == _capi.W8A8_BLK else 1
+    ldw = K // 2 if w4 else (2 * K if kind == _capi.W16A16 else K)
+    d.ldw, d.w_gstride = ldw, ldw * N
+    if kind == _capi.W8A8_BLK:
+        d.ldws = K // 128
+    elif kind == _capi.W4A16_MX:
+        d.ldws = K // 32
+    elif kind == _capi.W4A16_NV:
+        d.ldws = K // 16
+    elif kind == _capi.W4A16_I4:
+        d.ldws = K // wq_group
+    else:
+        d.ldws = 1
+    d.ws_gstride = d.ldws * (N // ws_bn if kind == _capi.W8A8_BLK else N)
+    d.ws_bn, d.wq_group = ws_bn, wq_group
+    if experts:
+        d.group_offs = d.active = d.num_active = base
+        d.slots = experts
+    else:
+        d.slots = 1
+    d.max_rows = max_rows if max_rows is not None else M
+    d.M, d.N, d.K = M, N, K
+    d.act, d.act_p0, d.act_p1 = act, p0, p1
+    d.ldy = N // 2 if act != _capi.ACT_NONE else N
+    return plan_of_desc(d)
 
 
 # ---------------------------------------------------------------- MoE
@@ -329,8 +417,11 @@ def moe_dispatch(topk_ids, topk_weights, num_experts, skip_padded_tokens=False):
     return meta
 
 
-def moe_combine(rows, topk_ids, topk_weights, skip_padded_tokens=False, out=None):
-    """Sum each token's k weighted route rows ([T*k, H] bf16) -> [T, H] bf16."""
+def moe_combine(rows, topk_ids, topk_weights, num_experts, skip_padded_tokens=False, out=None):
+    """Sum each token's k weighted route rows ([T*k, H] bf16) -> [T, H] bf16.
+
+    Slots whose id lies outside [0, num_experts) are skipped, as the
+    dispatch sorts them into the invalid bucket."""
     _require_gpu(rows, topk_ids, topk_weights)
     T, k = topk_ids.shape
     H = rows.shape[1]
@@ -338,7 +429,7 @@ def moe_combine(rows, topk_ids, topk_weights, skip_padded_tokens=False, out=None
         out = torch.empty((T, H), dtype=torch.bfloat16, device=rows.device)
     ids = topk_ids.to(torch.int32).contiguous()
     wts = topk_weights.to(torch.bfloat16).contiguous()
-    check(lib.qmoe_moe_combine(_ptr(rows), _ptr(ids), _ptr(wts), T, k, H,
+    check(lib.qmoe_moe_combine(_ptr(rows), _ptr(ids), _ptr(wts), T, k, int(num_experts), H,
                                int(bool(skip_padded_tokens)), _ptr(out), out.stride(0),
                                _stream(rows.device)), "moe_combine")
     return out
