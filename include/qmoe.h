@@ -4,7 +4,8 @@
  * Every entry point takes raw device pointers, sizes and a hipStream_t, is
  * asynchronous on that stream, allocates nothing, and returns a status:
  *   0 QMOE_OK, 1 QMOE_ERR_ARG (bad shape / unsupported combination),
- *   2 QMOE_ERR_WORKSPACE (workspace too small), 3 QMOE_ERR_LAUNCH.
+ *   2 QMOE_ERR_WORKSPACE (workspace too small), 3 QMOE_ERR_LAUNCH,
+ *   4 QMOE_ERR_SCRATCH (qmoe_gemm_static: partial sums exceed its scratch).
  * Layouts (all row-major):
  *   activations  [rows, K]            bf16 (uint16 bit patterns) or 1-byte codes
  *   weights      [G][N][K]            N-major: each output channel's K contiguous
@@ -142,6 +143,20 @@ int qmoe_gemm_plan(const qmoe_gemm_desc* d, int32_t* path, int32_t* tile_m, int3
  * stream.
  */
 int qmoe_gemm(const qmoe_gemm_desc* d, void* workspace, int64_t ws_bytes, qmoe_stream_t stream);
+
+/*
+ * qmoe_gemm for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc). No
+ * counterpart in the reference. Same kernels and results as qmoe_gemm; the
+ * split-K partial sums go to a static device array of the library
+ * (qmoe_gemm_static_scratch_bytes(), 64 MiB, held per GPU until the process
+ * ends) instead of a caller workspace, and no call allocates or frees
+ * anything. A problem whose partials exceed it returns QMOE_ERR_SCRATCH
+ * before any launch. Every call on one GPU shares that GPU's array: calls
+ * that overlap on one GPU (other streams, other threads) race.
+ */
+int qmoe_gemm_static(const qmoe_gemm_desc* d, qmoe_stream_t stream);
+int64_t qmoe_gemm_static_scratch_bytes(void);
 
 /*
  * MoE routing for T tokens over E experts: scores, top-k, renormalize and

@@ -16,6 +16,7 @@ STATUS_TEXT = {
     1: "invalid argument (shape, layout or unsupported combination)",
     2: "workspace too small",
     3: "kernel launch failed",
+    4: "the problem's split-K partial sums exceed the static scratch of qmoe_gemm_static (64 MiB)",
 }
 
 # GEMM kinds / activations (include/qmoe.h)
@@ -84,6 +85,10 @@ def _load():
     lib.qmoe_gemm_plan.restype = ctypes.c_int
     lib.qmoe_gemm_plan.argtypes = [ctypes.POINTER(GemmDesc), ctypes.POINTER(_i32), ctypes.POINTER(_i32),
                                    ctypes.POINTER(_i32)]
+    lib.qmoe_gemm_static.restype = ctypes.c_int
+    lib.qmoe_gemm_static.argtypes = [ctypes.POINTER(GemmDesc), _vp]
+    lib.qmoe_gemm_static_scratch_bytes.restype = _i64
+    lib.qmoe_gemm_static_scratch_bytes.argtypes = []
     lib.qmoe_gemm.restype = ctypes.c_int
     lib.qmoe_gemm.argtypes = [ctypes.POINTER(GemmDesc), _vp, _i64, _vp]
     lib.qmoe_moe_route.restype = ctypes.c_int
@@ -116,6 +121,8 @@ EXPORTED = (
     "qmoe_row_quant",
     "qmoe_gemm_workspace_size",
     "qmoe_gemm_plan",
+    "qmoe_gemm_static",
+    "qmoe_gemm_static_scratch_bytes",
     "qmoe_gemm",
     "qmoe_moe_route",
     "qmoe_moe_dispatch",
