@@ -38,6 +38,17 @@ enum {
                         block scale times its f32 global scale, rounded to bf16 as the
                         reference's `kernels/megablox/gmm_v2.py:452-462` dequantization
                         does; each weight is bf16(code * scale)) */
+  QMOE_W8A8_GMM = 7, /* A e4m3|int8 (wfmt) codes + f32 scale per (row, 512 columns, the last
+                        block partial) from qmoe_row_quant mode 2; W same dtype + per-channel f32
+                        scale [G][N] (ldws <= 1) or one per (row, B columns) [G][N][K/B] with
+                        ldws = K/B, B a power-of-two multiple of 512. The quantized-lhs regime
+                        of the reference's grouped
+                        matmul, `kernels/megablox/gmm_v2.py:500-548, 1198-1237` (weights with
+                        quant blocks of 256 or more columns: per-channel experts) */
+  QMOE_W8A16_BLK = 8, /* A bf16; W e4m3 + f32 scale per (n / ws_bn, 128 k) [G][N/bn][K/128];
+                        each weight is bf16(code * bf16(scale)) before the product: the
+                        dequantize-before-matmul regime of `kernels/megablox/gmm_v2.py:452-462`
+                        (quant blocks below 256 columns) */
   QMOE_W4A16_I4 = 6  /* A bf16; W symmetric 4-bit integers in the compressed-tensors
                         encoding (nibble = value + 8, two per byte, even k in the low
                         nibble: the int32 carriers of `compressed_tensors_moe_w4a16.py`

@@ -8,7 +8,7 @@ same sums. Test infrastructure only.
 import numpy as np
 
 from oracle.codecs import bf16_round, dequant_int4, dequant_mxfp4, dequant_nvfp4, e4m3_decode
-from oracle.quant import dequant_codes, quantize_act
+from oracle.quant import GMM_LHS_BLOCK, dequant_codes, quantize_act, quantize_gmm_lhs
 
 
 def _mm(a, b_nk) -> np.ndarray:
@@ -112,6 +112,88 @@ def w4a16_int4(x, carriers, scales, bias=None):
 def w16a16(x, w, bias=None):
     """Unquantized bf16 linear with f32 accumulation."""
     out = _mm(x, w)
+    if bias is not None:
+        out = out + np.asarray(bias, np.float32)[None, :]
+    return bf16_round(out)
+
+
+def _block_dots(xq, wq, qdtype, block):
+    """Per-512-block dot products of codes: [blocks, M, N] float64 (exact:
+    int8 products summed in float64 are exact integers, e4m3 products have
+    8-bit significands)."""
+    xv = dequant_codes(xq, qdtype).astype(np.float64)
+    wv = dequant_codes(wq, qdtype).astype(np.float64)
+    k = xv.shape[1]
+    nb = (k + block - 1) // block
+    return np.stack([xv[:, b * block:(b + 1) * block] @ wv[:, b * block:(b + 1) * block].T for b in range(nb)])
+
+
+def w8a8_gmm(x, wq, ws, qdtype, bias=None, round_out=True):
+    """The grouped matmul's quantized-lhs regime with per-channel weights
+    (``ws`` [N]) or per-(row, B columns) weights (``ws`` [N, K/B], B a
+    multiple of 512; `kernels/megablox/gmm_v2.py:500-548`), accumulated in
+    float32: the
+    activation codes and scales of `quantize_gmm_lhs`, each 512-column block's
+    dot times its activation scale, summed over blocks, times the per-channel
+    weight scale. This is the fp32-accumulated form the kernel computes (same
+    codes, so only the summation differs); `w8a8_gmm_bf16acc` is the
+    reference's own bf16 accumulation.
+
+    Returns (y [M, N] bf16-valued f32, or f32 sums with round_out=False; xq; xs).
+    """
+    xq, xs = quantize_gmm_lhs(x, qdtype)
+    dots = _block_dots(xq, wq, qdtype, GMM_LHS_BLOCK)
+    ws = np.asarray(ws, np.float32)
+    acc = np.zeros(dots.shape[1:], np.float32)
+    if ws.ndim == 2:  # per (row, B columns): each 512-column block meets the weight block it lies in
+        bw = xq.shape[1] // ws.shape[1]
+        for b in range(dots.shape[0]):
+            acc += ((dots[b].astype(np.float32) * xs[:, b:b + 1]).astype(np.float32)
+                    * ws[None, :, b * GMM_LHS_BLOCK // bw])
+        out = acc
+    else:
+        for b in range(dots.shape[0]):
+            acc += (dots[b].astype(np.float32) * xs[:, b:b + 1]).astype(np.float32)
+        out = (acc * ws[None, :]).astype(np.float32)
+    if bias is not None:
+        out = out + np.asarray(bias, np.float32)[None, :]
+    return (bf16_round(out) if round_out else out), xq, xs
+
+
+def w8a8_gmm_bf16acc(x, wq, ws, qdtype, bias=None):
+    """`kernels/megablox/gmm_v2.py:508-560` as written: the accumulator is
+    bf16 (`acc_dtype` defaults to bf16 when the lhs is quantized,
+    `:1230-1237`): per 512-column block, ``bf16(dot)``, times the bf16
+    activation scale (rounded), times the weight scale cast to bf16
+    (rounded), added to the bf16 accumulator (rounded); the bias is added in
+    bf16. Parity tests hold the kernel's fp32 accumulation to this within the
+    north-star bar."""
+    xq, xs = quantize_gmm_lhs(x, qdtype)
+    dots = _block_dots(xq, wq, qdtype, GMM_LHS_BLOCK)
+    ws16 = bf16_round(np.asarray(ws, np.float32))[None, :]
+    acc = np.zeros(dots.shape[1:], np.float32)
+    for b in range(dots.shape[0]):
+        blk = bf16_round(dots[b].astype(np.float32))
+        blk = bf16_round(blk * xs[:, b:b + 1])
+        blk = bf16_round(blk * ws16)
+        acc = bf16_round(acc + blk)
+    if bias is not None:
+        acc = bf16_round(acc + bf16_round(np.asarray(bias, np.float32))[None, :])
+    return acc
+
+
+def w8a16_blockwise(x, wq, ws_blocks, block=128, bias=None):
+    """The grouped matmul's dequantize-before-matmul regime for FP8 weights
+    with quant blocks under 256 columns (`kernels/megablox/gmm_v2.py:452-462`;
+    the single-group call of `adapter/linear_common.py:88-114` with
+    ``REQUANTIZE_BLOCK_SIZE=128``): each weight is ``bf16(code *
+    bf16(scale))`` (the codes and scales cast to the bf16 activation dtype,
+    multiplied in bf16), bf16 activations unquantized, f32 accumulation,
+    bf16 out. ``ws_blocks`` is [N, K/block]."""
+    w = dequant_codes(wq, "fp8")
+    n, k = w.shape
+    s = np.repeat(bf16_round(np.asarray(ws_blocks, np.float32)), block, axis=1)[:, :k]
+    out = _mm(x, bf16_round((w * s).astype(np.float32)))
     if bias is not None:
         out = out + np.asarray(bias, np.float32)[None, :]
     return bf16_round(out)

@@ -6,7 +6,7 @@ Test infrastructure only.
 import numpy as np
 
 from oracle.codecs import bf16_round, dequant_int4, dequant_mxfp4, dequant_nvfp4, e4m3_decode
-from oracle.linear import _mm
+from oracle.linear import _mm, w8a8_gmm
 from oracle.quant import quantize_act
 
 
@@ -89,12 +89,17 @@ class ExpertWeights:
       "nvfp4": w13 packed u8 [E, 2I, H/2] + f32 fused scales [E, 2I, H/16]; w2 likewise
       "int4": w13 int32 carriers [E, 2I, H/8] + bf16-valued scales [E, 2I, H/group]; w2 likewise
       "fp8_block": w13 e4m3 [E, 2I, H] + tile scale_inv [E, 2I/128, H/128]; w2 likewise
-      "fp8": w13 e4m3 [E, 2I, H] + per-channel scale [E, 2I]; w2 [E, H, I] + [E, H]
+      "fp8" / "int8": w13 e4m3 / int8 [E, 2I, H] + per-channel scale [E, 2I] (or per (row, B
+          columns) [E, 2I, H/B]); w2 [E, H, I] + [E, H]
+      "fp8_w8a16": w13 e4m3 [E, 2I, H] + per-(row, 128) scale [E, 2I, H/128]; w2 likewise
+      "fp8_rowquant" / "int8_rowquant": as "fp8" / "int8" with per-channel scales
       "bf16": w13 [E, 2I, H] f32 (bf16 values); w2 [E, H, I]
-    Activations: bf16 for mxfp4/nvfp4/int4/bf16 (W4A16 / W16A16); per-(row, 128) e4m3 for
-    fp8_block (the blockwise W8A8 recipe of config 4); per-row e4m3 for fp8
-    (each expert GEMM is `kernels/quantized_matmul/util.py:80-124`, the
-    per-channel W8A8 recipe, restated in ``linear.w8a8_per_channel``).
+    Activations: bf16 for mxfp4/nvfp4/int4/bf16 (W4A16 / W16A16) and fp8_w8a16 (weights
+    dequantized to bf16(code * bf16(scale)), `kernels/megablox/gmm_v2.py:452-462`);
+    per-(row, 128) e4m3 for fp8_block (the blockwise W8A8 recipe of config 4); per-(row,
+    512) bf16-arithmetic codes for fp8 / int8 (the grouped matmul's quantized-lhs regime,
+    `gmm_v2.py:500-548`, restated in ``linear.w8a8_gmm``); per-row codes for the
+    rowquant formats (`kernels/quantized_matmul/util.py:80-124`).
     """
 
     def __init__(self, fmt, w13, w13_scale, w2, w2_scale, b13=None, b2=None, keep=True):
@@ -118,8 +123,10 @@ class ExpertWeights:
                 d = dequant_nvfp4(w, s)
             elif self.fmt == "int4":
                 d = dequant_int4(w, s)
-            elif self.fmt in ("fp8_block", "fp8"):
+            elif self.fmt in ("fp8_block", "fp8", "fp8_w8a16", "fp8_rowquant"):
                 d = e4m3_decode(w)
+            elif self.fmt in ("int8", "int8_rowquant"):
+                d = np.asarray(w, np.int8).astype(np.float32)
             else:
                 d = np.asarray(w, np.float32)
             self._cache[key] = d
@@ -127,15 +134,25 @@ class ExpertWeights:
 
     def linear(self, which, e, x):
         """x bf16-valued [R, K] -> f32 [R, N] for expert e."""
-        if self.fmt == "fp8":
-            s = self.s13[e] if which == 13 else self.s2[e]
-            xq, xs = quantize_act(x, "fp8")
-            out = (_mm(e4m3_decode(xq), self.dense(which, e)) * xs[:, None]).astype(np.float32)
+        s = None if self.fmt == "bf16" else (self.s13[e] if which == 13 else self.s2[e])
+        if self.fmt in ("fp8", "int8"):
+            w = self.w13[e] if which == 13 else self.w2[e]
+            out, _, _ = w8a8_gmm(x, w, s, self.fmt, round_out=False)
+        elif self.fmt == "fp8_w8a16":
+            wv = self.dense(which, e)
+            sb = np.repeat(bf16_round(np.asarray(s, np.float32)), 128, axis=1)[:, :wv.shape[1]]
+            out = _mm(x, bf16_round((wv * sb).astype(np.float32)))
+        elif self.fmt in ("fp8_rowquant", "int8_rowquant"):
+            qd = self.fmt.split("_")[0]
+            xq, xs = quantize_act(x, qd)
+            xv = e4m3_decode(xq) if qd == "fp8" else xq.astype(np.float32)
+            wv = self.dense(which, e)
+            out = (_mm(xv, wv) * xs[:, None]).astype(np.float32) if qd == "fp8" else \
+                (np.matmul(xq.astype(np.float64), wv.astype(np.float64).T).astype(np.float32) * xs[:, None]).astype(np.float32)
             out = (out * np.asarray(s, np.float32)[None, :]).astype(np.float32)
         elif self.fmt != "fp8_block":
             out = _mm(x, self.dense(which, e))
         else:
-            s = self.s13[e] if which == 13 else self.s2[e]
             wv = self.dense(which, e)
             n, k = wv.shape
             xq, xs = quantize_act(x, "fp8", block=128)

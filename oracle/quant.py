@@ -79,6 +79,50 @@ def quantize_act(x, qdtype, block=None):
     return q.reshape(m, k), s[..., 0]
 
 
+GMM_LHS_BLOCK = 512
+
+
+def quantize_gmm_lhs(x, qdtype, block=GMM_LHS_BLOCK):
+    """The grouped matmul's on-the-fly activation quant,
+    `kernels/megablox/gmm_v2.py:508-536` (taken when the weight's quant
+    block is 256 columns or more, per-channel included, `:1198-1218`;
+    `quant_block_size=512`, `:1222-1228`).
+
+    Per (row, 512-column block) from column 0 (the kernel's K tile is the
+    whole K, `:966-969`, so the last block is partial when K % 512 != 0),
+    in the activation's dtype, bf16 (``dtype_max`` is a Python float, so the
+    division stays bf16): ``scale = bf16(absmax / qmax)``; ``inv = 0`` where
+    the scale is 0 else ``bf16(1 / scale)``; ``q = (x * inv).astype(q)``:
+    e4m3 round-to-nearest-even of the bf16 product (no clip; |q| <= ~452 <
+    464, the e4m3 overflow threshold), int8 by truncation toward zero (the
+    float -> int cast). A f32 quotient rounded once to bf16 is the correctly
+    rounded bf16 quotient (24 >= 2*8 + 2 bits).
+
+    Returns (codes [M, K] uint8 e4m3 / int8, scales f32 [M, ceil(K/512)]
+    holding the bf16 values; a zero block keeps scale 0).
+    """
+    x = bf16_round(np.asarray(x, dtype=np.float32))
+    m, k = x.shape
+    nb = (k + block - 1) // block
+    qmax = np.float32(448.0 if qdtype == "fp8" else 127.0)
+    codes = np.zeros((m, k), np.uint8 if qdtype == "fp8" else np.int8)
+    scales = np.zeros((m, nb), np.float32)
+    for b in range(nb):
+        xb = x[:, b * block:(b + 1) * block]
+        amax = np.max(np.abs(xb), axis=1, keepdims=True)
+        scale = bf16_round((amax / qmax).astype(np.float32))
+        with np.errstate(divide="ignore"):
+            inv = np.where(scale == 0, np.float32(0.0), bf16_round((np.float32(1.0) / scale).astype(np.float32)))
+        v = bf16_round((xb * inv).astype(np.float32))
+        if qdtype == "fp8":
+            codes[:, b * block:(b + 1) * block] = e4m3_encode(v)
+        else:
+            t = np.where(np.isnan(v), 0, np.clip(np.trunc(v), -128, 127))
+            codes[:, b * block:(b + 1) * block] = t.astype(np.int8)
+        scales[:, b] = scale[:, 0]
+    return codes, scales
+
+
 def dequant_codes(q, qdtype) -> np.ndarray:
     if qdtype == "fp8":
         return e4m3_decode(q)

@@ -32,20 +32,33 @@ def _linear_layer(method, n, k, ckpt_codes, ckpt_scale_inv, dev):
     return layer
 
 
-@pytest.mark.parametrize("mode", ["per_channel", "native_tiles", "int8"])
-def test_fp8_linear_from_block_checkpoint(dev, monkeypatch, mode):
+@pytest.mark.parametrize("mode", ["per_channel", "block128", "block512", "block512_int8", "native_tiles", "int8"])
+@pytest.mark.parametrize("M", [6, 300])
+def test_fp8_linear_from_block_checkpoint(dev, monkeypatch, mode, M):
+    """Checkpoint 128x128 FP8 -> the reference's runtime form for each env
+    setting (`fp8.py:216-348`): per-channel requant (default), per (row, B)
+    requant with ENABLE_QUANTIZED_MATMUL_KERNEL=1 REQUANTIZE_BLOCK_SIZE=B (a
+    [1, K/B, 1, N] scale; B = 128 runs bf16-dequantized weights, B = 512 the
+    per-(token, 512) quantized activations), int8; native tiles only with
+    QMOE_FP8_NATIVE_BLOCKS=1."""
     from qmoe.layers import quantization as q
 
-    print(f"fp8 linear method {mode}", flush=True)
-    for v in ("ENABLE_QUANTIZED_MATMUL_KERNEL", "REQUANTIZE_BLOCK_SIZE", "REQUANTIZE_WEIGHT_DTYPE"):
+    print(f"fp8 linear method {mode} M={M}", flush=True)
+    for v in ("ENABLE_QUANTIZED_MATMUL_KERNEL", "REQUANTIZE_BLOCK_SIZE", "REQUANTIZE_WEIGHT_DTYPE",
+              "QMOE_FP8_NATIVE_BLOCKS"):
         monkeypatch.delenv(v, raising=False)
-    if mode == "native_tiles":
+    if mode in ("native_tiles", "block128"):
         monkeypatch.setenv("ENABLE_QUANTIZED_MATMUL_KERNEL", "1")
         monkeypatch.setenv("REQUANTIZE_BLOCK_SIZE", "128")
-    if mode == "int8":
+    if mode.startswith("block512"):
+        monkeypatch.setenv("ENABLE_QUANTIZED_MATMUL_KERNEL", "1")
+        monkeypatch.setenv("REQUANTIZE_BLOCK_SIZE", "512")
+    if mode == "native_tiles":
+        monkeypatch.setenv("QMOE_FP8_NATIVE_BLOCKS", "1")
+    if mode in ("int8", "block512_int8"):
         monkeypatch.setenv("REQUANTIZE_WEIGHT_DTYPE", "int8")
     rng = np.random.default_rng(3)
-    N, K, M = 384, 512, 6
+    N, K = 384, 1024
     w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
     codes, s_inv = quant.quantize_fp8_tiles(w)
     method = q.Fp8LinearMethod(q.Fp8Config(weight_block_size=[128, 128]))
@@ -57,6 +70,17 @@ def test_fp8_linear_from_block_checkpoint(dev, monkeypatch, mode):
     if mode == "native_tiles":
         np.testing.assert_array_equal(layer.weight.view(torch.uint8).cpu().numpy(), codes)
         ref, _, _ = linear.w8a8_blockwise(x, codes, linear.tile_scales_to_blocks(s_inv, N))
+    elif mode.startswith("block"):
+        B = 128 if mode == "block128" else 512
+        qd = "int8" if mode.endswith("int8") else "fp8"
+        wq, wsb = quant.quantize_tensor(w_deq, qd, block=B)
+        assert tuple(layer.weight_scale.shape) == (1, K // B, 1, N)  # `fp8.py:270-294`
+        np.testing.assert_array_equal(layer.weight.view(torch.uint8).cpu().numpy(), wq.view(np.uint8))
+        np.testing.assert_array_equal(layer.weight_scale[0, :, 0, :].t().cpu().numpy(), wsb)
+        if B == 128:
+            ref = linear.w8a16_blockwise(x, wq, wsb)
+        else:
+            ref, _, _ = linear.w8a8_gmm(x, wq, wsb, qd)
     else:
         qd = "int8" if mode == "int8" else "fp8"
         wq, ws = quant.quantize_tensor(w_deq, qd)  # `fp8.py:297-348`: dequant -> requant per channel
@@ -99,12 +123,20 @@ def _moe_layer(k, act, renormalize=True, scoring="softmax", bias=None, grouped=N
     return layer
 
 
-def test_fp8_moe_block_checkpoint_sigmoid_grouped(dev):
+@pytest.mark.parametrize("native", [False, True])
+def test_fp8_moe_block_checkpoint_sigmoid_grouped(dev, monkeypatch, native):
     """DeepSeek-V3-form layer: 128x128 FP8 experts, sigmoid + bias, grouped
-    top-k, routed_scaling_factor; native tiles stay resident."""
+    top-k, routed_scaling_factor. By default the experts are requantized per
+    channel and run the reference's per-(token, 512) recipe
+    (`fp8.py:486-617`); with QMOE_FP8_NATIVE_BLOCKS=1 the native tiles stay
+    resident (the blockwise W8A8 recipe of BASELINE config 4)."""
     from qmoe.layers import quantization as q
 
-    print("fp8 moe method", flush=True)
+    print(f"fp8 moe method native={native}", flush=True)
+    for v in ("MOE_REQUANTIZE_WEIGHT_DTYPE", "MOE_REQUANTIZE_BLOCK_SIZE", "QMOE_FP8_NATIVE_BLOCKS"):
+        monkeypatch.delenv(v, raising=False)
+    if native:
+        monkeypatch.setenv("QMOE_FP8_NATIVE_BLOCKS", "1")
     rng = np.random.default_rng(7)
     E, H, I, k, T = 16, 256, 256, 4, 9
     cfg = q.Fp8Config(weight_block_size=[128, 128])
@@ -127,8 +159,78 @@ def test_fp8_moe_block_checkpoint_sigmoid_grouped(dev):
     logits = codecs.bf16_round(rng.standard_normal((T, E)).astype(np.float32))
     got = method.apply_monolithic(layer, _t(x, dev, torch.bfloat16), _t(logits, dev, torch.bfloat16))
     tw, ids = routing.grouped_topk(logits, k, True, 4, 2, "sigmoid", bias, 2.5)
-    ref, _, _ = omoe.fused_moe(x, omoe.ExpertWeights("fp8_block", c13, s13, c2, s2), tw, ids, "silu")
+    if native:
+        assert layer._qmoe_format == "fp8_block"
+        ew = omoe.ExpertWeights("fp8_block", c13, s13, c2, s2)
+    else:
+        assert layer._qmoe_format == "fp8"
+        r13 = [quant.quantize_tensor(quant.dequant_tiles(c13[e], s13[e]), "fp8") for e in range(E)]
+        r2 = [quant.quantize_tensor(quant.dequant_tiles(c2[e], s2[e]), "fp8") for e in range(E)]
+        ew = omoe.ExpertWeights("fp8", np.stack([a for a, _ in r13]), np.stack([b for _, b in r13]),
+                                np.stack([a for a, _ in r2]), np.stack([b for _, b in r2]))
+    ref, _, _ = omoe.fused_moe(x, ew, tw, ids, "silu")
     assert_close_rows(got.float().cpu().numpy(), ref, "fp8 moe method")
+
+
+@pytest.mark.parametrize("dtype,block,I,unpadded", [("int8", None, 128, None), ("float8_e4m3fn", 128, 256, None),
+                                                     ("float8_e4m3fn", 512, 512, None),
+                                                     ("float8_e4m3fn", None, 192, None),
+                                                     ("float8_e4m3fn", None, 256, 200)])
+def test_fp8_moe_requant_switches(dev, monkeypatch, dtype, block, I, unpadded):
+    """MOE_REQUANTIZE_WEIGHT_DTYPE / MOE_REQUANTIZE_BLOCK_SIZE (`fp8.py:185-213`):
+    int8 per channel (int8 activations per (token, 512)), fp8 per (row, 128)
+    (bf16-dequantized weights) and per (row, 512); an intermediate size that
+    is not a multiple of 128 is zero-padded to one, and the padding of an
+    unpadded intermediate size is zeroed (`fp8.py:351-406, 515-522`)."""
+    from qmoe.layers import quantization as q
+
+    print(f"fp8 moe requant {dtype} block={block} I={I} unpadded={unpadded}", flush=True)
+    for v in ("MOE_REQUANTIZE_WEIGHT_DTYPE", "MOE_REQUANTIZE_BLOCK_SIZE", "QMOE_FP8_NATIVE_BLOCKS"):
+        monkeypatch.delenv(v, raising=False)
+    monkeypatch.setenv("MOE_REQUANTIZE_WEIGHT_DTYPE", dtype)
+    if block:
+        monkeypatch.setenv("MOE_REQUANTIZE_BLOCK_SIZE", str(block))
+    rng = np.random.default_rng(17 + I)
+    E, H, k, T = 8, 512, 2, 11
+    layer = _moe_layer(k, "silu")
+    if unpadded:
+        layer.moe_config.intermediate_size_per_partition_unpadded = unpadded
+    method = q.Fp8MoEMethod(q.Fp8Config(), layer.moe_config)
+    method.create_weights(layer, E, H, I, torch.bfloat16)
+    w13f = (rng.standard_normal((E, 2 * I, H)) * 0.02).astype(np.float32)
+    w2f = (rng.standard_normal((E, H, I)) * 0.02).astype(np.float32)
+    s13 = (rng.random((E, 2)) * 1e-3 + 1e-4).astype(np.float32)
+    s2 = (rng.random(E) * 1e-3 + 1e-4).astype(np.float32)
+    c13 = codecs.e4m3_encode(np.clip(w13f / np.repeat(s13, I, axis=1)[:, :, None], -448, 448))
+    c2 = codecs.e4m3_encode(np.clip(w2f / s2[:, None, None], -448, 448))
+    layer.w13_weight.data = _fp8(c13, dev)
+    layer.w2_weight.data = _fp8(c2, dev)
+    layer.w13_weight_scale.data = _t(s13, dev)
+    layer.w2_weight_scale.data = _t(s2, dev)
+    method.process_weights_after_loading(layer)
+    real = unpadded or I
+    Ip = (I + 127) // 128 * 128
+    d13 = codecs.e4m3_decode(c13) * np.repeat(s13, I, axis=1)[:, :, None]
+    d2 = codecs.e4m3_decode(c2) * s2[:, None, None]
+    p13 = np.zeros((E, 2 * Ip, H), np.float32)
+    p13[:, :real], p13[:, Ip:Ip + real] = d13[:, :real], d13[:, I:I + real]
+    p2 = np.zeros((E, H, Ip), np.float32)
+    p2[:, :, :real] = d2[:, :, :real]
+    qd = "int8" if dtype == "int8" else "fp8"
+    r13 = [quant.quantize_tensor(p13[e], qd, block=block) for e in range(E)]
+    r2 = [quant.quantize_tensor(p2[e], qd, block=block) for e in range(E)]
+    w13q, w13s = np.stack([a for a, _ in r13]), np.stack([b for _, b in r13])
+    w2q, w2s = np.stack([a for a, _ in r2]), np.stack([b for _, b in r2])
+    np.testing.assert_array_equal(layer.w13_weight.data.view(torch.uint8).cpu().numpy(), w13q.view(np.uint8))
+    np.testing.assert_array_equal(layer.w2_weight_scale.cpu().numpy().reshape(w2s.shape), w2s)
+    fmt = {None: qd, 128: "fp8_w8a16", 512: "fp8"}[block]
+    assert layer._qmoe_format == fmt
+    x = codecs.bf16_round(rng.standard_normal((T, H)).astype(np.float32))
+    logits = codecs.bf16_round(rng.standard_normal((T, E)).astype(np.float32))
+    got = method.apply_monolithic(layer, _t(x, dev, torch.bfloat16), _t(logits, dev, torch.bfloat16))
+    tw, ids = routing.select_experts(logits, k, True, "softmax")
+    ref, _, _ = omoe.fused_moe(x, omoe.ExpertWeights(fmt, w13q, w13s, w2q, w2s), tw, ids, "silu")
+    assert_close_rows(got.float().cpu().numpy(), ref, f"fp8 moe requant {dtype} {block}")
 
 
 def test_mxfp4_moe_interleaved_checkpoint_swigluoai(dev):

@@ -129,6 +129,15 @@ def _moe_case(fmt, E, k, H, I, T, seed, bias=False):
         w2 = codecs.int4_pack(rng.integers(-8, 8, (E, H, I)))
         s13 = codecs.bf16_round((rng.random((E, 2 * I, H // g)) * 0.004 + 0.001).astype(np.float32))
         s2 = codecs.bf16_round((rng.random((E, H, I // g)) * 0.004 + 0.001).astype(np.float32))
+    elif fmt in ("fp8", "int8", "fp8_rowquant", "int8_rowquant", "fp8_w8a16"):
+        qd = "int8" if fmt.startswith("int8") else "fp8"
+        blk = 128 if fmt == "fp8_w8a16" else None
+        r13 = [quant.quantize_tensor((rng.standard_normal((2 * I, H)) * 0.02).astype(np.float32), qd, block=blk)
+               for _ in range(E)]
+        r2 = [quant.quantize_tensor((rng.standard_normal((H, I)) * 0.02).astype(np.float32), qd, block=blk)
+              for _ in range(E)]
+        w13, s13 = np.stack([q[0] for q in r13]), np.stack([q[1] for q in r13])
+        w2, s2 = np.stack([q[0] for q in r2]), np.stack([q[1] for q in r2])
     elif fmt == "fp8_block":
         w13f = (rng.standard_normal((E, 2 * I, H)) * 0.02).astype(np.float32)
         w2f = (rng.standard_normal((E, H, I)) * 0.02).astype(np.float32)
@@ -166,6 +175,16 @@ def _moe_case(fmt, E, k, H, I, T, seed, bias=False):
     ("fp8_block", "silu", 16, 4, 512, 256, 24, False),    # 6 rows per expert: tiled, 32-token tiles
     ("bf16", "silu", 8, 2, 256, 128, 9, False),
     ("bf16", "gelu_tanh", 8, 3, 256, 128, 100, True),
+    # the grouped matmul's quantized-lhs recipe (per-channel experts)
+    ("fp8", "silu", 8, 2, 1024, 256, 5, False),
+    ("fp8", "silu", 16, 4, 1024, 384, 40, False),
+    ("fp8", "swigluoai", 16, 4, 1024, 256, 300, True),    # tiled path
+    ("int8", "silu", 8, 2, 1024, 256, 5, False),
+    ("int8", "silu", 16, 4, 1024, 256, 300, False),       # tiled (generic) path
+    ("fp8_w8a16", "silu", 8, 2, 512, 256, 5, False),
+    ("fp8_w8a16", "silu", 16, 4, 512, 256, 300, True),
+    ("fp8_rowquant", "silu", 16, 4, 512, 256, 40, False),
+    ("int8_rowquant", "silu", 16, 4, 512, 256, 200, False),
 ])
 def test_fused_moe_layer(dev, fmt, act, E, k, H, I, T, bias):
     from qmoe.layers.fused_moe import fused_moe_gmm
@@ -174,7 +193,8 @@ def test_fused_moe_layer(dev, fmt, act, E, k, H, I, T, bias):
     w13, s13, w2, s2, b13, b2, hid, ids, tw = _moe_case(fmt, E, k, H, I, T, seed=E + T + H)
     ofmt = "int4" if fmt.startswith("int4") else fmt
     ref, _, _ = omoe.fused_moe(hid, omoe.ExpertWeights(ofmt, w13, s13, w2, s2, b13, b2), tw, ids, act)
-    wdt = torch.float8_e4m3fn if fmt == "fp8_block" else (torch.bfloat16 if fmt == "bf16" else None)
+    fp8_fmts = ("fp8_block", "fp8", "fp8_rowquant", "fp8_w8a16")
+    wdt = torch.float8_e4m3fn if fmt in fp8_fmts else (torch.bfloat16 if fmt == "bf16" else None)
 
     def wt(a):
         t = _t(a, dev)

@@ -146,11 +146,11 @@ def test_grouped_layer_matches_per_token_loop():
     np.testing.assert_allclose(got, want, rtol=1e-2, atol=2e-2 * np.abs(want).max())
 
 
-def test_fp8_per_channel_expert_linear_is_the_w8a8_recipe():
-    """The "fp8" expert format's GEMM is the per-channel W8A8 matmul of
-    `kernels/quantized_matmul/util.py:80-124` (pinned by its own known
-    answers): after the bf16 cast the two agree bit for bit, and a
-    transposed scale or a dropped activation scale would not."""
+def test_fp8_rowquant_expert_linear_is_the_w8a8_recipe():
+    """The "fp8_rowquant" expert format's GEMM is the per-channel W8A8 matmul
+    of `kernels/quantized_matmul/util.py:80-124` (pinned by its own known
+    answers): after the bf16 cast the two agree bit for bit, and a transposed
+    scale would not."""
     from oracle import linear, quant
 
     rng = np.random.default_rng(2)
@@ -158,10 +158,35 @@ def test_fp8_per_channel_expert_linear_is_the_w8a8_recipe():
     w = (rng.standard_normal((E, N, K)) * 0.05).astype(np.float32)
     q = [quant.quantize_tensor(w[e], "fp8") for e in range(E)]
     wq, ws = np.stack([a for a, _ in q]), np.stack([b for _, b in q])
-    ew = moe.ExpertWeights("fp8", wq, ws, wq, ws)
+    ew = moe.ExpertWeights("fp8_rowquant", wq, ws, wq, ws)
     x = codecs.bf16_round(rng.standard_normal((R, K)).astype(np.float32) * 3)
     for e in range(E):
         ref, _, _ = linear.w8a8_per_channel(x, wq[e], ws[e], "fp8")
         np.testing.assert_array_equal(codecs.bf16_round(ew.linear(13, e, x)), ref)
     assert not np.array_equal(codecs.bf16_round(ew.linear(13, 1, x)),
                               linear.w8a8_per_channel(x, wq[1], ws[0], "fp8")[0])
+
+
+@pytest.mark.parametrize("fmt", ["fp8", "int8"])
+def test_gmm_expert_linear_is_dequantize_then_matmul(fmt):
+    """The "fp8" / "int8" expert formats (the grouped matmul's quantized-lhs
+    recipe) equal the float64 matmul of the dequantized operands -- the
+    activation codes of `quantize_gmm_lhs` (pinned by hand-worked values)
+    times their per-(row, 512) scales, the weight codes times their channel
+    scales -- to float32 rounding, for each expert."""
+    from oracle import quant
+
+    rng = np.random.default_rng(5)
+    E, N, K, R = 2, 40, 1536, 4
+    w = (rng.standard_normal((E, N, K)) * 0.05).astype(np.float32)
+    q = [quant.quantize_tensor(w[e], fmt) for e in range(E)]
+    wq, ws = np.stack([a for a, _ in q]), np.stack([b for _, b in q])
+    ew = moe.ExpertWeights(fmt, wq, ws, wq, ws)
+    x = codecs.bf16_round(rng.standard_normal((R, K)).astype(np.float32) * 3)
+    x[:, 512:1024] *= 50.0
+    xq, xs = quant.quantize_gmm_lhs(x, fmt)
+    xd = quant.dequant_codes(xq, fmt).astype(np.float64) * np.repeat(xs, 512, axis=1)
+    for e in range(E):
+        wd = quant.dequant_codes(wq[e], fmt).astype(np.float64) * ws[e][:, None]
+        ref = xd @ wd.T
+        np.testing.assert_allclose(ew.linear(13, e, x), ref, rtol=2e-6, atol=2e-6 * np.abs(ref).max())

@@ -12,7 +12,16 @@
 //    (quantize_tensor): scale = absmax * f32(1/qmax) (reciprocal multiply),
 //    inv = scale == 0 ? 0 : 1/scale, codes clamp(x * inv); int rounds half to
 //    even. A zero scale stays 0.
-// Granularity: one scale per row, or per (row, 128-column block).
+//  * GROUPED-GEMM activation quant, kernels/megablox/gmm_v2.py:508-536
+//    (the quantized-lhs regime of gmm_v2, taken for weight blocks of 256 or
+//    more columns, per-channel weights included): per (row, 512-column
+//    block) from column 0, the last block partial, in bf16 arithmetic (the
+//    block's dtype_max is a Python float): scale = bf16(absmax / qmax),
+//    inv = scale == 0 ? 0 : bf16(1 / scale), codes = e4m3 RNE of
+//    bf16(x * inv) (no clip), or for int8 that bf16 value truncated toward
+//    zero (`.astype(int8)`). A zero scale stays 0.
+// Granularity: one scale per row, or per (row, 128-column block); the
+// grouped-GEMM mode per (row, 512-column block).
 //
 // Launch: one 256-thread workgroup per row (per-row scale); thread t owns 8
 // consecutive columns per 2048-column stride, so a 128-column block is
@@ -235,6 +244,49 @@ __global__ __launch_bounds__(kNT) void row_quant_kernel(
   if (tid == 0) scales[row * lds] = s;
 }
 
+// Grouped-GEMM quant (mode 2): one wavefront per 512-column block, lane l
+// holding columns [8 l, 8 l + 8) of it; every lane takes part in the
+// reduction (lanes past K contribute 0), only lanes inside K store.
+template <int kQdt>
+__global__ __launch_bounds__(kThreads) void gmm_quant_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                             int64_t K, uint8_t* __restrict__ q, int64_t ldq,
+                                                             float* __restrict__ scales, int64_t lds) {
+  const int64_t row = blockIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int64_t blk = (int64_t)blockIdx.y * (kThreads / 64) + (threadIdx.x >> 6);
+  const int64_t c = blk * 512 + lane * 8;
+  if (blk * 512 >= K) return;  // the whole wavefront is past K
+  const bool live = c < K;
+  Row8 r;
+  if (live) r = load8<false>(x, row * ldx + c);
+  else
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r.v[i] = 0.0f;
+  float m = amax8(r);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) m = nanmax(m, __shfl_xor(m, o, 64));
+  const float qmax = kQdt == 0 ? 448.0f : 127.0f;
+  const float scale = bf16_round(m / qmax);
+  const float inv = scale == 0.0f ? 0.0f : bf16_round(1.0f / scale);
+  if (live) {
+    uint32_t w[2] = {0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float v = bf16_round(r.v[i] * inv);
+      uint32_t code;
+      if (kQdt == 0) {
+        code = f32_to_e4m3(v);
+      } else {
+        float t = v != v ? 0.0f : fminf(fmaxf(truncf(v), -128.0f), 127.0f);
+        code = (uint32_t)(int32_t)t & 0xffu;
+      }
+      w[i >> 2] |= code << (8 * (i & 3));
+    }
+    *reinterpret_cast<uint2*>(q + row * ldq + c) = make_uint2(w[0], w[1]);
+  }
+  if (lane == 0) scales[row * lds + blk] = scale;
+}
+
 template <int kQdt, int kMode, bool kInF32, bool kBlock>
 void launch_rq(const void* x, int64_t ldx, int64_t M, int64_t K, uint8_t* q, int64_t ldq,
                float* s, int64_t lds, hipStream_t st) {
@@ -262,6 +314,18 @@ extern "C" int qmoe_row_quant(const void* x, int64_t ldx, int in_f32, int64_t M,
                               float* scales, int64_t lds, hipStream_t stream) {
   if (M < 0 || K <= 0 || (K % 8) != 0) return QMOE_ERR_ARG;
   if (qdtype != 0 && qdtype != 1) return QMOE_ERR_ARG;
+  if (mode == 2) {  // grouped-GEMM activation quant: bf16 rows, 512-column blocks
+    if (block != 512 || in_f32 || lds < cdiv<int64_t>(K, 512)) return QMOE_ERR_ARG;
+    if (M == 0) return QMOE_OK;
+    const dim3 grid((unsigned)M, (unsigned)cdiv<int64_t>(K, 512 * (kThreads / 64)));
+    if (qdtype == 0)
+      hipLaunchKernelGGL(gmm_quant_kernel<0>, grid, dim3(kThreads), 0, stream, static_cast<const uint16_t*>(x),
+                         ldx, K, static_cast<uint8_t*>(q), ldq, scales, lds);
+    else
+      hipLaunchKernelGGL(gmm_quant_kernel<1>, grid, dim3(kThreads), 0, stream, static_cast<const uint16_t*>(x),
+                         ldx, K, static_cast<uint8_t*>(q), ldq, scales, lds);
+    return hipGetLastError() == hipSuccess ? QMOE_OK : QMOE_ERR_LAUNCH;
+  }
   if (mode != 0 && mode != 1) return QMOE_ERR_ARG;
   if (block != 0 && block != 128) return QMOE_ERR_ARG;
   if (block == 128 && (K % 128) != 0) return QMOE_ERR_ARG;

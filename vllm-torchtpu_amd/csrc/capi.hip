@@ -32,14 +32,19 @@ constexpr int kSkinnyMaxRowsBlkWide = 16;
 
 int qmoe_to_params(const qmoe_gemm_desc* d, GemmParams* p) {
   if (!d) return QMOE_ERR_ARG;
-  if (d->kind < QMOE_W8A8_PC || d->kind > QMOE_W4A16_I4) return QMOE_ERR_ARG;
-  if (d->kind == QMOE_W8A8_PC && d->wfmt != 0 && d->wfmt != 1) return QMOE_ERR_ARG;
+  if (d->kind < QMOE_W8A8_PC || d->kind > QMOE_W8A16_BLK) return QMOE_ERR_ARG;
+  if ((d->kind == QMOE_W8A8_PC || d->kind == QMOE_W8A8_GMM) && d->wfmt != 0 && d->wfmt != 1) return QMOE_ERR_ARG;
   if (d->act < QMOE_ACT_NONE || d->act > QMOE_ACT_SITU) return QMOE_ERR_ARG;
   if (d->M < 0 || d->N <= 0 || d->K <= 0 || d->slots <= 0) return QMOE_ERR_ARG;
   if (!d->a || !d->w || !d->y) return QMOE_ERR_ARG;
-  if ((d->kind == QMOE_W8A8_PC || d->kind == QMOE_W8A8_BLK) && !d->a_scale) return QMOE_ERR_ARG;
+  if ((d->kind == QMOE_W8A8_PC || d->kind == QMOE_W8A8_BLK || d->kind == QMOE_W8A8_GMM) && !d->a_scale)
+    return QMOE_ERR_ARG;
   if (d->kind != QMOE_W16A16 && !d->w_scale) return QMOE_ERR_ARG;
   if (d->kind == QMOE_W8A8_BLK && (d->ws_bn <= 0 || (d->K % 128) != 0)) return QMOE_ERR_ARG;
+  // grouped-matmul recipe: activation scales per 512 columns, per-channel weights
+  if (d->kind == QMOE_W8A8_GMM && ((d->K % 128) != 0 || d->lds_a < (d->K + 511) / 512)) return QMOE_ERR_ARG;
+  if (d->kind == QMOE_W8A16_BLK && (d->ws_bn <= 0 || (d->K % 128) != 0 || d->ldws < d->K / 128))
+    return QMOE_ERR_ARG;
   if (d->act != QMOE_ACT_NONE && (d->N % 2) != 0) return QMOE_ERR_ARG;
   if (d->active && (!d->num_active || !d->group_offs)) return QMOE_ERR_ARG;
   if (!d->group_offs && d->slots != 1) return QMOE_ERR_ARG;
@@ -72,6 +77,27 @@ int qmoe_to_params(const qmoe_gemm_desc* d, GemmParams* p) {
   p->ldws = d->ldws;
   p->ws_gstride = d->ws_gstride;
   p->ws_bn = d->ws_bn > 0 ? d->ws_bn : 1;
+  p->a_kshift = 0;
+  p->w_kshift = 0;
+  if (d->kind == QMOE_W8A8_GMM) {
+    // onto the block-scale kernels: 512-column activation blocks; one weight
+    // scale per row ([G][N], ldws <= 1) or per (row, B columns) with
+    // B = K / ldws a power-of-two multiple of 512 ([G][N][K/B])
+    p->a_kshift = 2;
+    p->ws_bn = 1;
+    if (d->ldws <= 1) {
+      p->w_kshift = 31;
+      p->ldws = 1;
+    } else {
+      if (d->K % d->ldws != 0) return QMOE_ERR_ARG;
+      const int B = d->K / (int)d->ldws;
+      int sh = -1;
+      for (int j = 2; j < 20; ++j)
+        if (B == (128 << j)) sh = j;
+      if (sh < 0) return QMOE_ERR_ARG;
+      p->w_kshift = sh;
+    }
+  }
   p->wq_group = d->wq_group;
   p->bias = d->bias;
   p->bias_gstride = d->bias_gstride;
@@ -96,6 +122,10 @@ int qmoe_to_params(const qmoe_gemm_desc* d, GemmParams* p) {
 
 namespace {
 
+// Kernel kind of a descriptor kind: the grouped-matmul recipe runs on the
+// block-scale kernels (its shifts are set in qmoe_to_params)
+int kernel_kind(const qmoe_gemm_desc* d) { return d->kind == QMOE_W8A8_GMM ? QK_W8A8_BLK : d->kind; }
+
 // Grid depth of the skinny kernel: every group, or -- with an active list --
 // at most one slot per row (a listed group has at least one row).
 int skinny_slots(const qmoe_gemm_desc* d) {
@@ -119,7 +149,7 @@ int skinny_rows(const qmoe_gemm_desc* d) {
 bool use_skinny(const qmoe_gemm_desc* d) {
   const char* env = getenv("QMOE_SKINNY_MAX_ROWS");  // tuning knob
   int lim = d->group_offs ? kSkinnyMaxGroupRows : kSkinnyMaxRows;
-  if (!d->group_offs && d->kind == QMOE_W8A8_PC) lim = kSkinnyMaxRowsW8A8;
+  if (!d->group_offs && (d->kind == QMOE_W8A8_PC || d->kind == QMOE_W8A8_GMM)) lim = kSkinnyMaxRowsW8A8;
   // wide dense block-scaled problems (>= 16384 output channels): the tiled
   // kernel with a K split wins from 17 rows (measured on MI355X, K 7168)
   const int nout = d->act != QMOE_ACT_NONE ? d->N / 2 : d->N;
@@ -127,7 +157,7 @@ bool use_skinny(const qmoe_gemm_desc* d) {
   // grouped block-scaled (DeepSeek-V3 experts): the tiled kernel's 32-token
   // tiles win from 4 rows per routed expert (measured on MI355X, 256 experts,
   // top 8: 192 tokens 1309 vs 1466 us, 256 tokens 1432 vs 1704 us)
-  if (d->group_offs && d->kind == QMOE_W8A8_BLK) lim = kSkinnyMaxGroupRowsBlk;
+  if (d->group_offs && (d->kind == QMOE_W8A8_BLK || d->kind == QMOE_W8A8_GMM)) lim = kSkinnyMaxGroupRowsBlk;
   // dense e2m1 (MXFP4 / NVFP4): the tiled kernel's 32-token tiles with a K
   // split win from 33 rows (measured on MI355X, K 2880, N 5760)
   if (!d->group_offs && (d->kind == QMOE_W4A16_MX || d->kind == QMOE_W4A16_NV)) lim = kSkinnyMaxRowsW8A8;
@@ -148,7 +178,8 @@ bool use_w4(const qmoe_gemm_desc* d) {
 
 bool use_f8(const qmoe_gemm_desc* d) {
   if (getenv("QMOE_F8_OFF")) return false;  // tuning knob: generic kernel only
-  return d->kind == QMOE_W8A8_PC || (d->kind == QMOE_W8A8_BLK && !getenv("QMOE_F8_BLK_OFF"));
+  const bool blk = d->kind == QMOE_W8A8_BLK || (d->kind == QMOE_W8A8_GMM && d->wfmt == 0);
+  return d->kind == QMOE_W8A8_PC || (blk && !getenv("QMOE_F8_BLK_OFF"));
 }
 
 // Kernel paths of qmoe_gemm (reported by qmoe_gemm_plan).
@@ -169,7 +200,7 @@ enum Path {
 }  // namespace
 
 int qmoe_route_of(const qmoe_gemm_desc* d, GemmParams& p, QmoeRoute* r) {
-  const int kind = d->kind;
+  const int kind = kernel_kind(d);
   if (use_skinny(d) && qmoe_skinny_check(kind, p) == QMOE_OK) {
     r->path = kPathSkinny;
     r->tile_m = qmoe_skinny_tile_rows(skinny_rows(d));
@@ -183,7 +214,7 @@ int qmoe_route_of(const qmoe_gemm_desc* d, GemmParams& p, QmoeRoute* r) {
   if (!skinny_first) {
     int bm = 0, ks = 1;
     int64_t ws = 0;
-    if (use_f8(d) && qmoe_f8_plan(p, kind == QMOE_W8A8_BLK, &bm, &ks, &ws)) {
+    if (use_f8(d) && qmoe_f8_plan(p, kind == QK_W8A8_BLK, &bm, &ks, &ws)) {
       *r = QmoeRoute{kPathF8, bm, ks, ws};
       return QMOE_OK;
     }
@@ -208,24 +239,25 @@ int qmoe_route_of(const qmoe_gemm_desc* d, GemmParams& p, QmoeRoute* r) {
 
 int qmoe_run_route(const qmoe_gemm_desc* d, const QmoeRoute& r, GemmParams p, void* workspace,
                    int64_t ws_bytes, hipStream_t stream) {
+  const int kind = kernel_kind(d);
   switch (r.path) {
     case kPathSkinny: {
       GemmParams q;
       qmoe_to_params(d, &q);  // keeps the active list
-      return qmoe_skinny_launch(d->kind, q, skinny_rows(d), skinny_slots(d), workspace, ws_bytes, 0, stream);
+      return qmoe_skinny_launch(kind, q, skinny_rows(d), skinny_slots(d), workspace, ws_bytes, 0, stream);
     }
-    case kPathF8: return qmoe_f8_launch(p, d->kind == QMOE_W8A8_BLK, workspace, ws_bytes, stream);
+    case kPathF8: return qmoe_f8_launch(p, kind == QK_W8A8_BLK, workspace, ws_bytes, stream);
     case kPathW4: return qmoe_w4_launch(p, w4_fmt(d), workspace, ws_bytes, stream);
-    case kPathTiled: return qmoe_tiled_launch(d->kind, p, stream);
+    case kPathTiled: return qmoe_tiled_launch(kind, p, stream);
     default: {
       GemmParams q;
       qmoe_to_params(d, &q);
-      return qmoe_skinny_launch(d->kind, q, kSkinnyMaxRows, skinny_slots(d), workspace, ws_bytes, 1, stream);
+      return qmoe_skinny_launch(kind, q, kSkinnyMaxRows, skinny_slots(d), workspace, ws_bytes, 1, stream);
     }
   }
 }
 
-extern "C" int qmoe_abi_version(void) { return 3; }
+extern "C" int qmoe_abi_version(void) { return 4; }
 
 extern "C" int qmoe_gemm_workspace_size(const qmoe_gemm_desc* d, int64_t* bytes) {
   GemmParams p;

@@ -22,12 +22,17 @@ enum QmoeKind {
   QK_W4A16_NV = 5,  // A bf16; W e2m1 (as QK_W4A16_MX) + bf16 scale per 16 k
   QK_W4A16_I4 = 6,  // A bf16; W 4-bit integers, offset binary (nibble = v + 8), packed as
                     // QK_W4A16_MX, + bf16 scale per wq_group k (32, 64 or 128)
+  QK_W8A16_BLK = 8,  // A bf16; W e4m3 + f32 scale per (n / bn, 128 k), dequantized in bf16:
+                     // each weight is bf16(code * bf16(scale))
 };
+// The host maps the descriptor kind QMOE_W8A8_GMM (7) onto QK_W8A8_BLK with
+// a_kshift = 2 (activation scales per 512 columns) and w_kshift = 31 (one
+// weight scale per row: per-channel); wfmt 1 runs it on int8 codes.
 
 // bf16 activations (the other kinds take 1-byte activation codes)
 QMOE_HD constexpr bool kind_abf16(int kind) {
   return kind == QK_W8A16_PC || kind == QK_W4A16_MX || kind == QK_W16A16 || kind == QK_W4A16_NV ||
-         kind == QK_W4A16_I4;
+         kind == QK_W4A16_I4 || kind == QK_W8A16_BLK;
 }
 
 // 4-bit weights (two codes per byte, the even k in the low nibble)
@@ -106,6 +111,11 @@ struct GemmParams {
   int64_t ldws;            // row stride of w_scale (elements)
   int64_t ws_gstride;      // group stride of w_scale (elements)
   int32_t ws_bn;           // rows of W sharing one block-scale row (1 or 128)
+  // QK_W8A8_BLK: the scale of 128-k step s is a_scale[row, s >> a_kshift]
+  // and w_scale[n / ws_bn, s >> w_kshift] (0: 128-column blocks; 2: 512;
+  // 31: one scale for the whole row)
+  int32_t a_kshift;
+  int32_t w_kshift;
   int32_t wq_group;        // QK_W4A16_I4: k values per scale (32, 64 or 128)
   const float* bias;       // optional f32 [G, N]
   int64_t bias_gstride;

@@ -70,11 +70,16 @@ __device__ __forceinline__ i32x8 lds_frag(const uint8_t* p0, const uint8_t* p1) 
 __device__ __forceinline__ i32x4 lo4(const i32x8& v) { return i32x4{v[0], v[1], v[2], v[3]}; }
 __device__ __forceinline__ i32x4 hi4(const i32x8& v) { return i32x4{v[4], v[5], v[6], v[7]}; }
 
-template <bool INT, int BM, int BN, bool ACT, int KB, bool BLK>
+template <bool INT, int BM, int BN, bool ACT, int KB, bool BLK, bool WPC = false>
 __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, int m_tiles, int n_tiles) {
   static_assert(KB == 64 || KB == 128, "K bytes per LDS stage");
-  // BLK: 128x128 block scales (W8A8_BLK): one 128-byte stage is one K block
+  // BLK: block scales (W8A8_BLK): one 128-byte stage is one 128-column K step;
+  // the token scale of step s is a_scale[row, s >> a_kshift]. Without WPC the
+  // weight scale is that of the tile's 128-row block and K block s >> w_kshift;
+  // WPC (per-channel weights, the grouped-matmul recipe) applies one scale per
+  // weight row in the epilogue instead.
   static_assert(!BLK || (KB == 128 && !INT && BN == 256), "block scales: FP8, 128-byte stages, 256-row tiles");
+  static_assert(!WPC || BLK, "per-channel weight scales with block activation scales");
   using S = F8Shape<BM, BN>;
   constexpr int NI = S::NI, MJ = S::MJ, TN = S::TN, TM = S::TM;
   constexpr int BNO = ACT ? BN / 2 : BN;  // output channels per tile
@@ -138,7 +143,7 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
     } else {
       n = min(n0 + tid, nlim - 1);
     }
-    e_ws = BLK ? 1.0f : static_cast<const float*>(p.w_scale)[(int64_t)g * p.ws_gstride + n];
+    e_ws = BLK && !WPC ? 1.0f : static_cast<const float*>(p.w_scale)[(int64_t)g * p.ws_gstride + n];
     if (p.bias) e_bs = p.bias[(int64_t)g * p.bias_gstride + n];
   }
 
@@ -185,9 +190,12 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
   // scale `slot` for slot < BM, the scale of LDS weight rows
   // [(slot-BM)*128, +128) for slot < BM + 2, a duplicate elsewhere
   const float* sc_src = p.a_scale;
+  int sc_shift = 0;  // K-block shift of this lane's scale stream
   if constexpr (BLK) {
     const int slot = wave * 64 + lane;
-    if (slot >= BM && slot < BM + 2) {
+    sc_shift = p.a_kshift;
+    if (!WPC && slot >= BM && slot < BM + 2) {
+      sc_shift = p.w_kshift;
       const int b = slot - BM;
       const int n = ACT ? (b == 0 ? 0 : p.N / 2) + min(n0, nlim - 1) : min(n0 + b * 128, nlim - 1);
       sc_src = static_cast<const float*>(p.w_scale) + (int64_t)g * p.ws_gstride + (int64_t)(n / 128) * p.ldws;
@@ -209,7 +217,7 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
   auto copy_stage = [&](uint8_t* dW, uint8_t* dX, float* dS, int ks) {
     const uint32_t kb = kbase + (uint32_t)ks * (uint32_t)KB;
     if constexpr (BLK)
-      __builtin_amdgcn_global_load_lds(sc_src + kb / 128, QMOE_LDS(dS + wave * 64), 4, 0, 0);
+      __builtin_amdgcn_global_load_lds(sc_src + ((kb / 128) >> sc_shift), QMOE_LDS(dS + wave * 64), 4, 0, 0);
 #pragma unroll
     for (int j = 0; j < WI; ++j) {
       uint32_t o = woff[j];
@@ -276,7 +284,7 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
       for (int j = 0; j < MJ; ++j) sx[j] = sS[wm * TM + j * 32 + rl];
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
-        const float sw = sS[BM + wrow(i) / 128];
+        const float sw = WPC ? 1.0f : sS[BM + wrow(i) / 128];
 #pragma unroll
         for (int j = 0; j < MJ; ++j) scl[i][j] = sx[j] * sw;
       }
@@ -424,12 +432,12 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
 
 }
 
-template <bool INT, int BM, int BN, bool ACT, bool BLK>
+template <bool INT, int BM, int BN, bool ACT, bool BLK, bool WPC = false>
 void f8_launch_shape(const GemmParams& p, hipStream_t st) {
   const char* env = getenv("QMOE_F8_KB");  // tuning knob: K bytes per LDS stage
   const int kb = BLK ? 128 : (env ? atoi(env) : 128);
-  auto kern = kb == 64 ? f8_gemm_kernel<INT, BM, BN, ACT, BLK ? 128 : 64, BLK>
-                       : f8_gemm_kernel<INT, BM, BN, ACT, 128, BLK>;
+  auto kern = kb == 64 ? f8_gemm_kernel<INT, BM, BN, ACT, BLK ? 128 : 64, BLK, WPC>
+                       : f8_gemm_kernel<INT, BM, BN, ACT, 128, BLK, WPC>;
   const int nout = ACT ? p.N / 2 : p.N;
   const int n_tiles = cdiv(nout, ACT ? BN / 2 : BN);
   const unsigned ks = (unsigned)std::max(1, p.ksplit);
@@ -443,10 +451,10 @@ void f8_launch_shape(const GemmParams& p, hipStream_t st) {
   }
 }
 
-template <bool INT, int BM, int BN, bool BLK>
+template <bool INT, int BM, int BN, bool BLK, bool WPC = false>
 void f8_launch_act(const GemmParams& p, hipStream_t st) {
-  if (p.act != QA_NONE) f8_launch_shape<INT, BM, BN, true, BLK>(p, st);
-  else f8_launch_shape<INT, BM, BN, false, BLK>(p, st);
+  if (p.act != QA_NONE) f8_launch_shape<INT, BM, BN, true, BLK, WPC>(p, st);
+  else f8_launch_shape<INT, BM, BN, false, BLK, WPC>(p, st);
 }
 
 template <bool INT>
@@ -461,13 +469,18 @@ void f8_launch_bm(const GemmParams& p, int bm, hipStream_t st) {
 
 // block-scaled FP8: tiles of at most 128 tokens (the per-block sums need a
 // second accumulator set)
+template <bool WPC>
 void f8_launch_bm_blk(const GemmParams& p, int bm, hipStream_t st) {
   switch (bm) {
-    case 128: f8_launch_act<false, 128, 256, true>(p, st); break;
-    case 64: f8_launch_act<false, 64, 256, true>(p, st); break;
-    default: f8_launch_act<false, 32, 256, true>(p, st); break;
+    case 128: f8_launch_act<false, 128, 256, true, WPC>(p, st); break;
+    case 64: f8_launch_act<false, 64, 256, true, WPC>(p, st); break;
+    default: f8_launch_act<false, 32, 256, true, WPC>(p, st); break;
   }
 }
+
+// per-channel weight scales with block activation scales (the grouped-matmul
+// recipe): one weight scale for the whole row
+bool f8_wpc(const GemmParams& p) { return p.w_kshift >= 31; }
 
 }  // namespace
 
@@ -502,7 +515,9 @@ bool qmoe_f8_plan(const GemmParams& p, bool blk, int* bm_out, int* ksplit_out, i
   if (p.M <= 0 || p.K <= 0 || (p.K % 256) != 0 || p.N <= 0) return false;
   if (p.act != QA_NONE && (p.N % 2) != 0) return false;
   // block scales: 128-row weight blocks aligned with the tile's halves
-  if (blk && (p.ws_bn != 128 || (p.act != QA_NONE && ((p.N / 2) % 128) != 0))) return false;
+  // (per-channel weight scales need no alignment); 1-byte FP8 codes only
+  if (blk && !f8_wpc(p) && (p.ws_bn != 128 || (p.act != QA_NONE && ((p.N / 2) % 128) != 0))) return false;
+  if (blk && p.wfmt != 0) return false;
   if ((p.lda % 16) != 0 || (p.ldw % 16) != 0) return false;
   if ((reinterpret_cast<uintptr_t>(p.a) & 15) || (reinterpret_cast<uintptr_t>(p.w) & 15) ||
       (p.w_gstride % 16) != 0)
@@ -567,22 +582,26 @@ int qmoe_f8_launch(GemmParams p, bool blk, void* workspace, int64_t ws_bytes, hi
     if (!workspace || ws_bytes < need) return QMOE_ERR_WORKSPACE;
     p.partial = static_cast<float*>(workspace);
   }
-  if (blk) f8_launch_bm_blk(p, bm, st);
+  if (blk && f8_wpc(p)) f8_launch_bm_blk<true>(p, bm, st);
+  else if (blk) f8_launch_bm_blk<false>(p, bm, st);
   else if (p.wfmt == 1) f8_launch_bm<true>(p, bm, st);
   else f8_launch_bm<false>(p, bm, st);
   if (ksplit > 1) {
     const int nout = p.act != QA_NONE ? p.N / 2 : p.N;
     const dim3 rg((unsigned)cdiv(nout, 512), (unsigned)cdiv(p.M, 4), 1);
     const bool act = p.act != QA_NONE;
-    if (blk) {
-      if (act) hipLaunchKernelGGL((tile_splitk_finish_kernel<false, true, true>), rg, dim3(kThreads), 0, st, p);
-      else hipLaunchKernelGGL((tile_splitk_finish_kernel<false, false, true>), rg, dim3(kThreads), 0, st, p);
+    if (blk && f8_wpc(p)) {
+      if (act) hipLaunchKernelGGL((tile_splitk_finish_kernel<false, true, kScWeight>), rg, dim3(kThreads), 0, st, p);
+      else hipLaunchKernelGGL((tile_splitk_finish_kernel<false, false, kScWeight>), rg, dim3(kThreads), 0, st, p);
+    } else if (blk) {
+      if (act) hipLaunchKernelGGL((tile_splitk_finish_kernel<false, true, kScNone>), rg, dim3(kThreads), 0, st, p);
+      else hipLaunchKernelGGL((tile_splitk_finish_kernel<false, false, kScNone>), rg, dim3(kThreads), 0, st, p);
     } else if (p.wfmt == 1) {
-      if (act) hipLaunchKernelGGL((tile_splitk_finish_kernel<true, true, false>), rg, dim3(kThreads), 0, st, p);
-      else hipLaunchKernelGGL((tile_splitk_finish_kernel<true, false, false>), rg, dim3(kThreads), 0, st, p);
+      if (act) hipLaunchKernelGGL((tile_splitk_finish_kernel<true, true, kScAll>), rg, dim3(kThreads), 0, st, p);
+      else hipLaunchKernelGGL((tile_splitk_finish_kernel<true, false, kScAll>), rg, dim3(kThreads), 0, st, p);
     } else {
-      if (act) hipLaunchKernelGGL((tile_splitk_finish_kernel<false, true, false>), rg, dim3(kThreads), 0, st, p);
-      else hipLaunchKernelGGL((tile_splitk_finish_kernel<false, false, false>), rg, dim3(kThreads), 0, st, p);
+      if (act) hipLaunchKernelGGL((tile_splitk_finish_kernel<false, true, kScAll>), rg, dim3(kThreads), 0, st, p);
+      else hipLaunchKernelGGL((tile_splitk_finish_kernel<false, false, kScAll>), rg, dim3(kThreads), 0, st, p);
     }
   }
   return hipGetLastError() == hipSuccess ? QMOE_OK : QMOE_ERR_LAUNCH;

@@ -64,9 +64,10 @@ struct Traits {
   //   1-byte A (e4m3/int8) and bf16 A with bf16 W: byte kg*16 + i*64
   //   bf16 A with e4m3 W: byte kg*32 + (i/2)*128 + (i%2)*16
   //   bf16 A with e2m1 W: byte kg*64 + i*16
-  static constexpr int kAOffBase = kW4 ? 64 : (KIND == QK_W8A16_PC ? 32 : 16);
+  static constexpr bool kW8A16 = KIND == QK_W8A16_PC || KIND == QK_W8A16_BLK;
+  static constexpr int kAOffBase = kW4 ? 64 : (kW8A16 ? 32 : 16);
   static __device__ __forceinline__ constexpr int a_off(int i) {
-    return kW4 ? i * 16 : (KIND == QK_W8A16_PC ? (i >> 1) * 128 + (i & 1) * 16 : i * 64);
+    return kW4 ? i * 16 : (kW8A16 ? (i >> 1) * 128 + (i & 1) * 16 : i * 64);
   }
   // first k (within the step) of weight chunk (j, kg) / activation chunk (i, kg)
   static __device__ __forceinline__ constexpr int w_k0(int j, int kg) {
@@ -173,6 +174,20 @@ __device__ __forceinline__ uint4 fp4x8_to_bf16(uint32_t d, float scale) {
   return make_uint4(c0.u, c1.u, c2.u, c3.u);
 }
 
+// 4 e4m3 codes (one dword) times a bf16-valued scale -> 4 bf16, each the
+// round-to-nearest-even of code * scale (a 4-bit by 8-bit significand
+// product, exact in f32): the reference's bf16 dequantization of a block-
+// scaled FP8 weight, `kernels/megablox/gmm_v2.py:452-462`.
+__device__ __forceinline__ uint2 fp8x4_to_bf16_scaled(uint32_t d, float s) {
+  typedef float v2f __attribute__((ext_vector_type(2)));
+  const v2f lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)d, false);
+  const v2f hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)d, true);
+  union { bf16x2 h; uint32_t u; } a, b;
+  a.h = __builtin_convertvector(f32x2{lo[0] * s, lo[1] * s}, bf16x2);
+  b.h = __builtin_convertvector(f32x2{hi[0] * s, hi[1] * s}, bf16x2);
+  return make_uint2(a.u, b.u);
+}
+
 // 4 e4m3 codes (one dword) -> 4 bf16 bit patterns packed in two dwords
 // (e4m3 values are exact in f32 and in bf16, so truncation is exact).
 __device__ __forceinline__ uint2 fp8x4_to_bf16(uint32_t d) {
@@ -223,13 +238,23 @@ __device__ __forceinline__ void mma_step(Acc<KIND, WF, MS, NS>& acc, const Frag 
                                                              acc.v[ms][s], 0, 0, 0);
       }
   } else if constexpr (KIND == QK_W8A8_BLK) {
-    // one 128-k step == one scale block: scale the block's dot, then add
+    // one 128-k step lies in one scale block: scale the step's dot, then add
+    // (int8 codes: the step's int32 dot is exact in f32, |dot| < 2^21)
 #pragma unroll
     for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
-        f32x4 d = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(as_i32x8(fa[ms]), as_i32x8(bw[s]),
-                                                                   f32x4{0, 0, 0, 0}, 0, 0, 0, 127, 0, 127);
+        f32x4 d;
+        if constexpr (WF == 1) {
+          i32x4 di = __builtin_amdgcn_mfma_i32_16x16x64_i8(as_i32x4(fa[ms].v[0]), as_i32x4(bw[s].v[0]),
+                                                           i32x4{0, 0, 0, 0}, 0, 0, 0);
+          di = __builtin_amdgcn_mfma_i32_16x16x64_i8(as_i32x4(fa[ms].v[1]), as_i32x4(bw[s].v[1]), di, 0, 0, 0);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) d[r] = (float)di[r];
+        } else {
+          d = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(as_i32x8(fa[ms]), as_i32x8(bw[s]),
+                                                               f32x4{0, 0, 0, 0}, 0, 0, 0, 127, 0, 127);
+        }
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc.v[ms][s][r] += d[r] * (sc.sa[ms][r] * sc.sb[s]);
       }
@@ -249,6 +274,16 @@ __device__ __forceinline__ void mma_step(Acc<KIND, WF, MS, NS>& acc, const Frag 
         for (int q = 0; q < 4; ++q) {
           const uint2 lo = fp8x4_to_bf16(d[2 * q]);
           const uint2 hi = fp8x4_to_bf16(d[2 * q + 1]);
+          wb[q] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+        }
+      } else if constexpr (KIND == QK_W8A16_BLK) {  // bf16(code * bf16(scale)), the step's block scale
+        const uint32_t d[8] = {bw[s].v[0].x, bw[s].v[0].y, bw[s].v[0].z, bw[s].v[0].w,
+                               bw[s].v[1].x, bw[s].v[1].y, bw[s].v[1].z, bw[s].v[1].w};
+        const float sc1 = bf16_round(sc.sb[s]);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint2 lo = fp8x4_to_bf16_scaled(d[2 * q], sc1);
+          const uint2 hi = fp8x4_to_bf16_scaled(d[2 * q + 1], sc1);
           wb[q] = make_uint4(lo.x, lo.y, hi.x, hi.y);
         }
       } else if constexpr (KIND == QK_W4A16_MX) {
@@ -390,13 +425,16 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p)
     sres = make_rsrc(static_cast<const uint16_t*>(p.w_scale) + (int64_t)g * p.ws_gstride, (int64_t)p.N * p.ldws * 2);
 #pragma unroll
     for (int s = 0; s < NS; ++s) soffw[s] = (uint32_t)(nclamp[s] * p.ldws * 2 + (kg * 32 / p.wq_group) * 2);
-  } else if constexpr (KIND == QK_W8A8_BLK) {
+  } else if constexpr (KIND == QK_W8A8_BLK || KIND == QK_W8A16_BLK) {
     sres = make_rsrc(static_cast<const float*>(p.w_scale) + (int64_t)g * p.ws_gstride,
                      (int64_t)cdiv(p.N, p.ws_bn) * p.ldws * 4);
-    ares = make_rsrc(p.a_scale, (int64_t)p.M * p.lds_a * 4);
+    if (KIND == QK_W8A8_BLK) ares = make_rsrc(p.a_scale, (int64_t)p.M * p.lds_a * 4);
 #pragma unroll
     for (int s = 0; s < NS; ++s) soffw[s] = (uint32_t)((nclamp[s] / p.ws_bn) * p.ldws * 4);
   }
+  // block index of 128-k step ks: ks >> shift (the activation's and the
+  // weight's; 31 for one scale per row)
+  const int a_kshift = p.a_kshift, w_kshift = p.w_kshift;
   const uint32_t i4_step = KIND == QK_W4A16_I4 ? (uint32_t)(256 / p.wq_group) : 0u;  // INT4 scale bytes per step
   // e2m1: the workgroup's NS*16 scale rows (K/32 bytes each; the host keeps
   // K <= 16384) are staged in LDS once, so the K loop reads a step's byte
@@ -475,11 +513,16 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p)
       if constexpr (KIND == QK_W8A8_BLK) {
         const uint32_t oob = live ? 0u : kOob;
 #pragma unroll
-        for (int s = 0; s < NS; ++s) sc.sb[s] = ldb_f32(sres, soffw[s] | oob, (uint32_t)ks * 4);
+        for (int s = 0; s < NS; ++s) sc.sb[s] = ldb_f32(sres, soffw[s] | oob, (uint32_t)(ks >> w_kshift) * 4);
 #pragma unroll
         for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
-          for (int r4 = 0; r4 < 4; ++r4) sc.sa[ms][r4] = ldb_f32(ares, soffa[ms][r4] | oob, (uint32_t)ks * 4);
+          for (int r4 = 0; r4 < 4; ++r4)
+            sc.sa[ms][r4] = ldb_f32(ares, soffa[ms][r4] | oob, (uint32_t)(ks >> a_kshift) * 4);
+      } else if constexpr (KIND == QK_W8A16_BLK) {
+        const uint32_t oob = live ? 0u : kOob;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) sc.sb[s] = ldb_f32(sres, soffw[s] | oob, (uint32_t)(ks >> w_kshift) * 4);
       } else if constexpr (KIND == QK_W4A16_MX) {
 #pragma unroll
         for (int s = 0; s < NS; ++s) sc.eb[s] = s_eb[(s * 16 + col) * KB32 + ks * 4 + kg];
@@ -843,7 +886,7 @@ void qmoe_skinny_plan(int kind, int64_t M, int64_t N, int64_t K, int act, int sl
 int qmoe_skinny_check(int kind, const GemmParams& p) {
   if (p.K <= 0 || (p.K % 32) != 0 || p.N <= 0) return QMOE_ERR_ARG;
   if (p.act != QA_NONE && (p.N % 2) != 0) return QMOE_ERR_ARG;
-  if (kind == QK_W8A8_BLK && (p.K % 128) != 0) return QMOE_ERR_ARG;
+  if ((kind == QK_W8A8_BLK || kind == QK_W8A16_BLK) && (p.K % 128) != 0) return QMOE_ERR_ARG;
   // 32-bit buffer offsets: every operand stream stays below 2 GiB
   const bool abf16 = kind_abf16(kind);
   constexpr int64_t kLim = 0x7fffffff;
@@ -859,6 +902,7 @@ int qmoe_skinny_check(int kind, const GemmParams& p) {
   if (kind == QK_W8A8_BLK &&
       ((int64_t)cdiv(p.N, p.ws_bn) * p.ldws * 4 > kLim || p.M * p.lds_a * 4 > kLim))
     return QMOE_ERR_ARG;
+  if (kind == QK_W8A16_BLK && (int64_t)cdiv(p.N, p.ws_bn) * p.ldws * 4 > kLim) return QMOE_ERR_ARG;
   return QMOE_OK;
 }
 
@@ -891,8 +935,12 @@ int qmoe_skinny_launch(int kind, GemmParams p, int max_rows, int slots, void* wo
       if (p.wfmt == 0) launch_act<QK_W8A8_PC, 0>(p, ms, ns, waves, grid, st);
       else launch_act<QK_W8A8_PC, 1>(p, ms, ns, waves, grid, st);
       break;
-    case QK_W8A8_BLK: launch_act<QK_W8A8_BLK, 0>(p, ms, ns, waves, grid, st); break;
+    case QK_W8A8_BLK:
+      if (p.wfmt == 0) launch_act<QK_W8A8_BLK, 0>(p, ms, ns, waves, grid, st);
+      else launch_act<QK_W8A8_BLK, 1>(p, ms, ns, waves, grid, st);
+      break;
     case QK_W8A16_PC: launch_act<QK_W8A16_PC, 0>(p, ms, ns, waves, grid, st); break;
+    case QK_W8A16_BLK: launch_act<QK_W8A16_BLK, 0>(p, ms, ns, waves, grid, st); break;
     case QK_W4A16_MX: launch_act<QK_W4A16_MX, 0>(p, ms, ns, waves, grid, st); break;
     case QK_W4A16_NV: launch_act<QK_W4A16_NV, 0>(p, ms, ns, waves, grid, st); break;
     case QK_W4A16_I4: launch_act<QK_W4A16_I4, 0>(p, ms, ns, waves, grid, st); break;

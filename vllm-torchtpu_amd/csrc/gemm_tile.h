@@ -283,9 +283,16 @@ __device__ __forceinline__ void tile_epilogue(const GemmParams& p, const AccT (&
 // then scales, bias, activation and routing weight are applied as in the
 // single-pass epilogue. A grouped problem finds the row's group by binary
 // search over group_offs.
-// SCALED: the partials already carry every scale (block-scaled FP8, e2m1).
-template <bool INT, bool ACT, bool SCALED>
+// SC: which scales the finish applies -- kScAll (per-row activation and
+// per-channel weight scales), kScNone (the partials carry every scale:
+// block-scaled FP8, e2m1) or kScWeight (block activation scales are in the
+// partials, the per-channel weight scale is not: the grouped-matmul recipe).
+enum { kScAll = 0, kScNone = 1, kScWeight = 2 };
+
+template <bool INT, bool ACT, int SC>
 __global__ __launch_bounds__(kThreads) void tile_splitk_finish_kernel(const GemmParams p) {
+  constexpr bool SCALED = SC == kScNone;
+  constexpr bool ASCALE = SC == kScAll;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int R = blockIdx.y * 4 + wave;
   if (R >= p.M) return;
@@ -303,7 +310,7 @@ __global__ __launch_bounds__(kThreads) void tile_splitk_finish_kernel(const Gemm
     g = lo;
   }
   const int ar = p.a_rows ? p.a_rows[R] : R;
-  const float sxa = SCALED ? 1.0f : p.a_scale[(int64_t)ar * p.lds_a];
+  const float sxa = ASCALE ? p.a_scale[(int64_t)ar * p.lds_a] : 1.0f;
   const float rwt = p.row_weight ? bf16_to_f32(p.row_weight[R]) : 1.0f;
   const float* wsc = static_cast<const float*>(p.w_scale) + (int64_t)g * p.ws_gstride;
   const float* bias = p.bias ? p.bias + (int64_t)g * p.bias_gstride : nullptr;

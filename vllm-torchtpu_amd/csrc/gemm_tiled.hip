@@ -49,11 +49,13 @@ constexpr int kXcds = 8;
 
 template <int KIND, int WF>
 struct TTraits {
-  static constexpr bool kAbf16 = KIND == QK_W8A16_PC || KIND == QK_W4A16_MX || KIND == QK_W16A16;
+  static constexpr bool kAbf16 = KIND == QK_W8A16_PC || KIND == QK_W4A16_MX || KIND == QK_W16A16 ||
+                                 KIND == QK_W8A16_BLK;
   static constexpr bool kInt = KIND == QK_W8A8_PC && WF == 1;
   static constexpr int kKPerStage = kAbf16 ? 64 : 128;
   // bytes of one weight row per stage in HBM
-  static constexpr int kWRowBytes = KIND == QK_W4A16_MX ? 32 : (KIND == QK_W8A16_PC ? 64 : 128);
+  static constexpr int kWRowBytes =
+      KIND == QK_W4A16_MX ? 32 : (KIND == QK_W8A16_PC || KIND == QK_W8A16_BLK ? 64 : 128);
 };
 
 template <int BM, int BN, bool ACT>
@@ -90,6 +92,18 @@ __device__ __forceinline__ uint4 fp4x8_bf16(uint32_t d, float scale) {
   union { bf16x2 b; uint32_t u; } c0, c1, c2, c3;
   c0.b = p0; c1.b = p1; c2.b = p2; c3.b = p3;
   return make_uint4(c0.u, c1.u, c2.u, c3.u);
+}
+
+// e4m3 codes times a bf16-valued scale, each product rounded to bf16 once
+// (exact in f32: a 4-bit by 8-bit significand product)
+__device__ __forceinline__ uint2 fp8x4_bf16_scaled(uint32_t d, float s) {
+  typedef float v2f __attribute__((ext_vector_type(2)));
+  const v2f lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)d, false);
+  const v2f hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)d, true);
+  union { bf16x2 h; uint32_t u; } a, b;
+  a.h = __builtin_convertvector(f32x2{lo[0] * s, lo[1] * s}, bf16x2);
+  b.h = __builtin_convertvector(f32x2{hi[0] * s, hi[1] * s}, bf16x2);
+  return make_uint2(a.u, b.u);
 }
 
 __device__ __forceinline__ uint2 fp8x4_bf16(uint32_t d) {
@@ -270,7 +284,7 @@ __global__ __launch_bounds__(kThreads) void tiled_gemm_kernel(const GemmParams p
         if (idx < BM) {
           const int R = row0 + (idx < rows ? idx : 0);
           const int ar = p.a_rows ? p.a_rows[R] : R;
-          rsc[h] = p.a_scale[(int64_t)ar * p.lds_a + ks];
+          rsc[h] = p.a_scale[(int64_t)ar * p.lds_a + (ks >> p.a_kshift)];
         } else if (idx < BM + BN) {
           const int tr = idx - BM;
           int n;
@@ -282,7 +296,7 @@ __global__ __launch_bounds__(kThreads) void tiled_gemm_kernel(const GemmParams p
             n = min(n0 + tr, nlim - 1);
           }
           rsc[h] = static_cast<const float*>(p.w_scale)[(int64_t)g * p.ws_gstride +
-                                                        (int64_t)(n / p.ws_bn) * p.ldws + ks];
+                                                        (int64_t)(n / p.ws_bn) * p.ldws + (ks >> p.w_kshift)];
         }
       }
     }
@@ -314,6 +328,15 @@ __global__ __launch_bounds__(kThreads) void tiled_gemm_kernel(const GemmParams p
         uint4* d = reinterpret_cast<uint4*>(dst + cc * 32);
         const uint2 a0 = fp8x4_bf16(rw[i].x), a1 = fp8x4_bf16(rw[i].y);
         const uint2 a2 = fp8x4_bf16(rw[i].z), a3 = fp8x4_bf16(rw[i].w);
+        d[0] = make_uint4(a0.x, a0.y, a1.x, a1.y);
+        d[1] = make_uint4(a2.x, a2.y, a3.x, a3.y);
+      } else if constexpr (KIND == QK_W8A16_BLK) {
+        // the stage's 64 k lie in 128-k block ks >> 1 (scale rounded to bf16)
+        const float scl = bf16_round(static_cast<const float*>(p.w_scale)[
+            (int64_t)g * p.ws_gstride + (int64_t)(w_row[i] / p.ws_bn) * p.ldws + ((ks >> 1) >> p.w_kshift)]);
+        uint4* d = reinterpret_cast<uint4*>(dst + cc * 32);
+        const uint2 a0 = fp8x4_bf16_scaled(rw[i].x, scl), a1 = fp8x4_bf16_scaled(rw[i].y, scl);
+        const uint2 a2 = fp8x4_bf16_scaled(rw[i].z, scl), a3 = fp8x4_bf16_scaled(rw[i].w, scl);
         d[0] = make_uint4(a0.x, a0.y, a1.x, a1.y);
         d[1] = make_uint4(a2.x, a2.y, a3.x, a3.y);
       } else {
@@ -394,8 +417,16 @@ __global__ __launch_bounds__(kThreads) void tiled_gemm_kernel(const GemmParams p
         for (int r = 0; r < 4; ++r) sa[r] = sc[ar + kg * 4 + r];
 #pragma unroll
         for (int j = 0; j < NF; ++j) {
-          f32x4 d = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-              av, pack8(bfr[j][0], bfr[j][1]), f32x4{0, 0, 0, 0}, 0, 0, 0, 127, 0, 127);
+          f32x4 d;
+          if constexpr (WF == 1) {  // int8 codes: the stage's int32 dot is exact in f32
+            i32x4 di = __builtin_amdgcn_mfma_i32_16x16x64_i8(as_i4(a0), as_i4(bfr[j][0]), i32x4{0, 0, 0, 0}, 0, 0, 0);
+            di = __builtin_amdgcn_mfma_i32_16x16x64_i8(as_i4(a1), as_i4(bfr[j][1]), di, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) d[r] = (float)di[r];
+          } else {
+            d = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, pack8(bfr[j][0], bfr[j][1]),
+                                                                 f32x4{0, 0, 0, 0}, 0, 0, 0, 127, 0, 127);
+          }
 #pragma unroll
           for (int r = 0; r < 4; ++r) acc[i][j][r] += d[r] * (sa[r] * sbv[j]);
         }
@@ -530,9 +561,10 @@ void launch_shape(const GemmParams& p, bool big, hipStream_t st) {
 // Whether the generic tiled kernel takes the problem (QMOE_OK) and its
 // tile edge (128, or 256 with the QMOE_TILED_BIG knob).
 int qmoe_tiled_check(int kind, const GemmParams& p, int* tile) {
-  const bool abf16 = kind == QK_W8A16_PC || kind == QK_W4A16_MX || kind == QK_W16A16;
+  const bool abf16 = kind == QK_W8A16_PC || kind == QK_W4A16_MX || kind == QK_W16A16 || kind == QK_W8A16_BLK;
   const int kstage = abf16 ? 64 : 128;
   if (kind != QK_W8A8_PC && kind != QK_W8A8_BLK && !abf16) return QMOE_ERR_ARG;
+  if (kind == QK_W8A16_BLK && (p.K % 128) != 0) return QMOE_ERR_ARG;
   if (p.K <= 0 || (p.K % kstage) != 0 || p.N <= 0) return QMOE_ERR_ARG;
   if (p.act != QA_NONE && (p.N % 2) != 0) return QMOE_ERR_ARG;
   bool big = false;  // 128 x 128 measured faster or equal on every config shape
@@ -558,7 +590,11 @@ int qmoe_tiled_launch(int kind, GemmParams p, hipStream_t st) {
       if (p.wfmt == 0) launch_shape<QK_W8A8_PC, 0>(p, big, st);
       else launch_shape<QK_W8A8_PC, 1>(p, big, st);
       break;
-    case QK_W8A8_BLK: launch_shape<QK_W8A8_BLK, 0>(p, big, st); break;
+    case QK_W8A8_BLK:
+      if (p.wfmt == 0) launch_shape<QK_W8A8_BLK, 0>(p, big, st);
+      else launch_shape<QK_W8A8_BLK, 1>(p, big, st);
+      break;
+    case QK_W8A16_BLK: launch_shape<QK_W8A16_BLK, 0>(p, big, st); break;
     case QK_W8A16_PC: launch_shape<QK_W8A16_PC, 0>(p, big, st); break;
     case QK_W4A16_MX: launch_shape<QK_W4A16_MX, 0>(p, big, st); break;
     case QK_W16A16: launch_shape<QK_W16A16, 0>(p, big, st); break;

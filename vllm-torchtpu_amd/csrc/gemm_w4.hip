@@ -461,9 +461,9 @@ int qmoe_w4_launch(GemmParams p, int fmt, void* workspace, int64_t ws_bytes, hip
     const int nout = p.act != QA_NONE ? p.N / 2 : p.N;
     const dim3 rg((unsigned)cdiv(nout, 512), (unsigned)cdiv(p.M, 4), 1);
     if (p.act != QA_NONE)
-      hipLaunchKernelGGL((tile_splitk_finish_kernel<false, true, true>), rg, dim3(kThreads), 0, st, p);
+      hipLaunchKernelGGL((tile_splitk_finish_kernel<false, true, kScNone>), rg, dim3(kThreads), 0, st, p);
     else
-      hipLaunchKernelGGL((tile_splitk_finish_kernel<false, false, true>), rg, dim3(kThreads), 0, st, p);
+      hipLaunchKernelGGL((tile_splitk_finish_kernel<false, false, kScNone>), rg, dim3(kThreads), 0, st, p);
   }
   return hipGetLastError() == hipSuccess ? QMOE_OK : QMOE_ERR_LAUNCH;
 }

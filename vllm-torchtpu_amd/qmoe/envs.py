@@ -45,6 +45,12 @@ _READERS = {
     "MOE_REQUANTIZE_WEIGHT_DTYPE": lambda: os.getenv("MOE_REQUANTIZE_WEIGHT_DTYPE"),
     # MoE: routes with a zero routing weight are padding and skipped
     "TPU_MOE_SKIP_PADDED_TOKENS": lambda: _bool("TPU_MOE_SKIP_PADDED_TOKENS"),
+    # this build only (no reference counterpart): 128x128-block FP8 checkpoints
+    # keep their tiles at run time with per-(token, 128) e4m3 activations
+    # (the blockwise W8A8 recipe of BASELINE configs 2 and 4) instead of the
+    # reference's requantization (per channel for the MoE and without
+    # REQUANTIZE_BLOCK_SIZE, per (row, block) otherwise)
+    "QMOE_FP8_NATIVE_BLOCKS": lambda: _bool("QMOE_FP8_NATIVE_BLOCKS"),
 }
 
 

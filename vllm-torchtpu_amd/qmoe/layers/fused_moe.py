@@ -16,11 +16,31 @@ format                w1 [E, 2I, H...] / w2        scales
 ``nvfp4``             uint8 packed e2m1 [., ., K/2]  bf16 [E, N, K/16] (fused e4m3 x global)
 ``int4``              int32 carriers [., ., K/8]     bf16 [E, N, K/group], group 32 / 64 / 128
                       (8 offset-binary nibbles per int32, the compressed-tensors checkpoint form)
+``fp8`` / ``int8``    float8_e4m3fn / int8         f32 per-channel [E, N], or per (row, B
+                                                   columns) [E, N, K/B] with B a power-of-two
+                                                   multiple of 512
+``fp8_w8a16``         float8_e4m3fn [E, N, K]      f32 per-(row, 128) scales [E, N, K/128]
 ``fp8_block``         float8_e4m3fn [E, N, K]      f32 tile scales [E, N/128, K/128]
 ``fp8_block_rows``    float8_e4m3fn [E, N, K]      f32 per-(row, 128) scales [E, N, K/128]
-``fp8`` / ``int8``    float8_e4m3fn / int8         f32 per-channel [E, N]
+``fp8_rowquant`` /    float8_e4m3fn / int8         f32 per-channel [E, N]
+``int8_rowquant``
 ``bf16``              bfloat16                      none
 ====================  ==========================  ====================================
+
+Numeric recipe of each 1-byte format:
+
+* ``fp8`` / ``int8`` -- the reference's: its grouped matmul quantizes the
+  activations per (row, 512 columns) in bf16 arithmetic for weights with
+  quant blocks of 256+ columns (`kernels/megablox/gmm_v2.py:500-548`), to
+  e4m3 for float weights and int8 for int8 weights; the block sums are
+  scaled and accumulated in f32 (the reference accumulates in bf16).
+* ``fp8_w8a16`` -- the reference's for 128-column weight blocks
+  (``MOE_REQUANTIZE_BLOCK_SIZE=128``): each weight is bf16(code *
+  bf16(scale)), bf16 activations (`gmm_v2.py:452-462`).
+* ``fp8_block`` / ``fp8_block_rows`` -- the blockwise W8A8 recipe (per
+  (token, 128) e4m3 activations; BASELINE config 4's native 128x128 tiles).
+* ``fp8_rowquant`` / ``int8_rowquant`` -- per-token activation quant (the
+  dense linear's `kernels/quantized_matmul/util.py:80-124` recipe).
 
 w1's N axis is ``[gate | up]`` (gate rows first), as in the reference
 (`kernels/megablox/gmm_v2.py:894-901`).
@@ -38,6 +58,10 @@ import torch
 from qmoe import _capi, ops
 
 
+MOE_FORMATS = ("mxfp4", "nvfp4", "int4", "bf16", "fp8", "int8", "fp8_w8a16", "fp8_block", "fp8_block_rows",
+               "fp8_rowquant", "int8_rowquant")
+
+
 def infer_weight_format(w1: torch.Tensor, w1_scale) -> str:
     if w1.dtype == torch.bfloat16:
         return "bf16"
@@ -45,7 +69,7 @@ def infer_weight_format(w1: torch.Tensor, w1_scale) -> str:
         return "int8"
     if w1.dtype == torch.float8_e4m3fn:
         if w1_scale is not None and w1_scale.dim() == 3 and w1_scale.shape[-1] * 128 == w1.shape[-1]:
-            return "fp8_block_rows" if w1_scale.shape[1] == w1.shape[1] else "fp8_block"
+            return "fp8_w8a16" if w1_scale.shape[1] == w1.shape[1] else "fp8_block"
         return "fp8"
     if w1.dtype == torch.int32:
         return "int4"
@@ -75,7 +99,7 @@ def fused_moe_gmm(hidden_states, w1, w2, w1_scale, w2_scale, w1_bias, w2_bias, t
             raise NotImplementedError(f"rhs_quant_dtype {rhs_quant_dtype} is not supported (int4 only)")
         weight_format = weight_format or "int4"
     fmt = weight_format or infer_weight_format(w1, w1_scale)
-    if fmt not in ("mxfp4", "nvfp4", "int4", "bf16", "fp8_block", "fp8_block_rows", "fp8", "int8"):
+    if fmt not in MOE_FORMATS:
         raise ValueError(f"unknown MoE weight format {fmt!r}")
     ops.act_code(activation)  # NotImplementedError for an unknown activation string
     T, H = hidden_states.shape
@@ -150,6 +174,15 @@ def moe_forward(layer, x, router_logits, w1, w2, w1_scale, w2_scale, w1_bias, w2
                                      int(tg), act or "", bool(skip_padded_tokens), weight_format)
 
 
+def _gmm_scale(s, E):
+    """Weight scales of the grouped-matmul recipe: per-channel [E, N] or per
+    (row, B columns) [E, N, K/B], f32, contiguous."""
+    s = s.float()
+    if s.dim() == 3 and s.shape[-1] == 1:
+        s = s[..., 0]
+    return s.reshape(E, *s.shape[1:]).contiguous()
+
+
 def _moe_body(x, w1, w2, w1_scale, w2_scale, w1_bias, w2_bias, tw, topk_ids, topk, activation, skip, fmt, meta):
     """The experts of a routed layer, given the dispatch metadata."""
     activation = activation or None
@@ -185,8 +218,22 @@ def _moe_body(x, w1, w2, w1_scale, w2_scale, w1_bias, w2_bias, tw, topk_ids, top
         a2, kind, wf = u8(a2q), _capi.W8A8_BLK, 0
         w2k, w2s = u8(w2), w2_scale
     elif fmt in ("fp8", "int8"):
-        qd = "fp8" if fmt == "fp8" else "int8"
-        wf = 0 if fmt == "fp8" else 1
+        # the reference's grouped-matmul recipe: per-(row, 512) bf16-arithmetic
+        # activation quant before each GEMM
+        qd, wf = ("fp8", 0) if fmt == "fp8" else ("int8", 1)
+        xq, xs = ops.row_quant(x, qd, mode="gmm")
+        inter = ops.gemm(_capi.W8A8_GMM, u8(xq), u8(w1), a_scale=xs, w_scale=_gmm_scale(w1_scale, E),
+                         wfmt=wf, bias=b1, a_rows=meta["token_sorted"], activation=activation, **common)
+        a2q, a2_scale = ops.row_quant(inter, qd, mode="gmm")
+        a2, kind, bn = u8(a2q), _capi.W8A8_GMM, 1
+        w2k, w2s = u8(w2), _gmm_scale(w2_scale, E)
+    elif fmt == "fp8_w8a16":
+        inter = ops.gemm(_capi.W8A16_BLK, x, u8(w1), w_scale=w1_scale.float().contiguous(), ws_bn=1, bias=b1,
+                         a_rows=meta["token_sorted"], activation=activation, **common)
+        a2, a2_scale, kind, wf, bn = inter, None, _capi.W8A16_BLK, 0, 1
+        w2k, w2s = u8(w2), w2_scale.float().contiguous()
+    elif fmt in ("fp8_rowquant", "int8_rowquant"):
+        qd, wf = ("fp8", 0) if fmt == "fp8_rowquant" else ("int8", 1)
         xq, xs = ops.row_quant(x, qd)
         inter = ops.gemm(_capi.W8A8_PC, u8(xq), u8(w1), a_scale=xs,
                          w_scale=w1_scale.float().reshape(E, -1).contiguous(), wfmt=wf, bias=b1,

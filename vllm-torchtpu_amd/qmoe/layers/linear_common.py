@@ -42,53 +42,72 @@ def _weight_nk(w_q: torch.Tensor) -> torch.Tensor:
     return w_nk
 
 
-def _scale_blocks(w_s: torch.Tensor, k_dim: int, n_out: int):
-    """Block scales -> (f32 [N/bn, K/128] tensor, bn).
+# numeric regimes of `quantized_matmul` (the custom op's `regime` argument)
+REGIME_PER_CHANNEL = 0  # `util.py:80-124`: per-token activation quant, per-channel weights
+REGIME_NATIVE_BLOCKS = 1  # this build's 128x128-tile form: per-(token, 128) activation quant
+REGIME_GMM_QUANT_LHS = 2  # gmm_v2, weight blocks >= 256: per-(token, 512) bf16-arithmetic quant
+REGIME_GMM_W8A16 = 3  # gmm_v2, weight blocks < 256: bf16(code * bf16(scale)) weights, bf16 x
 
-    Accepts the reference's rank-4 ``[1, K/B, 1, N]`` (B must be 128; per
-    (K-block, n)) or the native compact ``[N/bn, K/128]`` form (bn = 1 or a
-    128x128 tile scale with bn = 128).
-    """
-    if w_s.dim() == 4:
-        _, sharded_num_blocks, mid, scale_n_out = w_s.shape
-        if mid != 1:
-            raise ValueError(f"Blockwise weight scale axis 2 must be 1, got {w_s.shape=}")
-        if scale_n_out != n_out:
-            raise ValueError(
-                f"Blockwise weight scale output dim {scale_n_out} must match "
-                f"weight output dim {n_out}."
-            )
-        if sharded_num_blocks <= 0 or k_dim % sharded_num_blocks != 0:
-            raise ValueError(
-                f"Input hidden dim {k_dim} must be divisible by block scale "
-                f"count {sharded_num_blocks}."
-            )
-        if k_dim // sharded_num_blocks != 128:
-            raise ValueError("qmoe blockwise kernels take 128-wide K blocks")
-        return w_s[0, :, 0, :].t().contiguous().float(), 1
-    if w_s.dim() == 2:
-        if w_s.shape[1] * 128 != k_dim:
-            raise ValueError(f"block scale has {w_s.shape[1]} K blocks, expected {k_dim // 128}")
-        if w_s.shape[0] == n_out:
-            return w_s.float().contiguous(), 1
-        if w_s.shape[0] == (n_out + 127) // 128:
-            return w_s.float().contiguous(), 128
-        raise ValueError(f"block scale rows {w_s.shape[0]} match neither {n_out} nor {n_out // 128}")
-    raise ValueError(f"unsupported weight scale shape {tuple(w_s.shape)}")
+# quant blocks below this many columns are dequantized before the matmul
+# (the reference's MXU width, `kernels/megablox/gmm_v2.py:255-262`)
+GMM_DEQUANT_BEFORE_BELOW = 256
+
+
+def _rank4_blocks(w_s: torch.Tensor, k_dim: int, n_out: int):
+    """The reference's rank-4 ``[1, K/B, 1, N]`` scale (validated with its
+    messages, `linear_common.py:83-104`) -> (``[N, K/B]`` f32 view or copy,
+    B). A rank-4 view of an N-major ``[N, K/B]`` buffer (what this package's
+    `process_weights_after_loading` stores) needs no copy."""
+    _, sharded_num_blocks, mid, scale_n_out = w_s.shape
+    if mid != 1:
+        raise ValueError(f"Blockwise weight scale axis 2 must be 1, got {w_s.shape=}")
+    if scale_n_out != n_out:
+        raise ValueError(
+            f"Blockwise weight scale output dim {scale_n_out} must match "
+            f"weight output dim {n_out}."
+        )
+    if sharded_num_blocks <= 0 or k_dim % sharded_num_blocks != 0:
+        raise ValueError(
+            f"Input hidden dim {k_dim} must be divisible by block scale "
+            f"count {sharded_num_blocks}."
+        )
+    sc = w_s[0, :, 0, :].t()
+    if sc.dtype != torch.float32 or not sc.is_contiguous():
+        sc = sc.float().contiguous()
+    return sc, k_dim // sharded_num_blocks
+
+
+def _native_blocks(w_s: torch.Tensor, k_dim: int, n_out: int):
+    """This build's compact block-scale form -> (f32 [N/bn, K/128], bn):
+    per (channel, 128-column block) (bn = 1) or per 128x128 tile (bn = 128)."""
+    if w_s.shape[1] * 128 != k_dim:
+        raise ValueError(f"block scale has {w_s.shape[1]} K blocks, expected {k_dim // 128}")
+    if w_s.shape[0] == n_out:
+        return w_s.float().contiguous(), 1
+    if w_s.shape[0] == (n_out + 127) // 128:
+        return w_s.float().contiguous(), 128
+    raise ValueError(f"block scale rows {w_s.shape[0]} match neither {n_out} nor {n_out // 128}")
 
 
 def quantized_matmul(x: torch.Tensor, w_q: torch.Tensor, w_s: torch.Tensor,
                      w8a16_max_rows: int = 0) -> torch.Tensor:
     """Runtime quantized dense linear, `linear_common.py:162-185` + `:69-128`.
 
-    * ``w_s`` 1-D ``[n_out]``: per-channel. e4m3 weights with
-      ``0 < rows <= w8a16_max_rows`` keep bf16 activations (W8A16); otherwise
-      activations are quantized per token (e4m3 in f32 / int8 in bf16
-      arithmetic, `kernels/quantized_matmul/util.py:80-124`) -- W8A8.
-    * block scales (rank-4 reference form or compact 2-D): e4m3 weights with
-      128-wide K blocks; activations quantized per (token, 128 columns) in
-      f32 -- the blockwise W8A8 recipe
-      (`kernels/quantized_matmul/blockwise_kernel.py:197-247`).
+    * ``w_s`` 1-D ``[n_out]``: per-channel (`kernels/quantized_matmul/util.py:
+      80-124`). e4m3 weights with ``0 < rows <= w8a16_max_rows`` keep bf16
+      activations (W8A16); otherwise activations are quantized per token (e4m3
+      in f32 / int8 in bf16 arithmetic) -- W8A8.
+    * ``w_s`` rank-4 ``[1, K/B, 1, N]`` (the reference's blockwise runtime
+      layout): the single-group grouped matmul of `:88-114`, in its regime for
+      B (`kernels/megablox/gmm_v2.py:255-262, 452-548`): B < 256 (B = 128):
+      e4m3 weights dequantized to bf16(code * bf16(scale)), bf16 activations;
+      B >= 256 (B = K, or a power-of-two multiple of 512): activations
+      quantized per (token, 512 columns) in bf16 arithmetic to e4m3 (int8 for
+      int8 weights), f32 accumulation of the scaled block sums.
+    * ``w_s`` 2-D ``[N/bn, K/128]`` (this build's native 128x128-tile form,
+      bn = 128, or per-(channel, 128) with bn = 1): activations quantized per
+      (token, 128 columns) in f32, the blockwise W8A8 recipe of
+      `kernels/quantized_matmul/blockwise_kernel.py:197-247`.
     """
     if x.shape[-1] != w_q.shape[0]:
         raise ValueError(
@@ -101,51 +120,70 @@ def quantized_matmul(x: torch.Tensor, w_q: torch.Tensor, w_s: torch.Tensor,
         x2 = x2.to(torch.bfloat16)
     w_nk = _weight_nk(w_q)
     k_dim, n_out = w_q.shape
+    if w_nk.dtype not in (torch.int8, torch.float8_e4m3fn):
+        raise ValueError(f"Unsupported quantized dtype: {w_nk.dtype}")
     if w_s.dim() == 1:
         if w_s.shape[0] != n_out:
             raise ValueError(f"per-channel scale has {w_s.shape[0]} entries, expected {n_out}")
-        if w_nk.dtype not in (torch.int8, torch.float8_e4m3fn):
-            raise ValueError(f"Unsupported quantized dtype: {w_nk.dtype}")
-    else:
+        regime = REGIME_PER_CHANNEL
+    elif w_s.dim() == 4:
+        w_s, block = _rank4_blocks(w_s, k_dim, n_out)
+        if block < GMM_DEQUANT_BEFORE_BELOW:
+            if block != 128 or w_nk.dtype != torch.float8_e4m3fn:
+                raise NotImplementedError(
+                    f"qmoe dequantizes weight blocks under {GMM_DEQUANT_BEFORE_BELOW} columns for "
+                    f"float8_e4m3fn weights with 128-column blocks only, got {w_nk.dtype} blocks of {block}")
+            regime = REGIME_GMM_W8A16
+        else:
+            if block != k_dim and (block % 512 or (block // 512) & (block // 512 - 1)):
+                raise NotImplementedError(
+                    f"qmoe runs weight blocks of 256+ columns as per-channel (B = K) or power-of-two "
+                    f"multiples of 512 columns, got {block} for K={k_dim}")
+            if k_dim % 128:
+                raise NotImplementedError(f"the quantized-lhs regime needs K % 128 == 0, got {k_dim}")
+            regime = REGIME_GMM_QUANT_LHS
+    elif w_s.dim() == 2:
         if w_nk.dtype != torch.float8_e4m3fn:
             raise ValueError(f"blockwise kernels take float8_e4m3fn weights, got {w_nk.dtype}")
-        w_s, _ = _scale_blocks(w_s, k_dim, n_out)
-    out = torch.ops.qmoe.quantized_matmul(x2, w_nk, w_s, int(w8a16_max_rows))
+        w_s, _ = _native_blocks(w_s, k_dim, n_out)
+        regime = REGIME_NATIVE_BLOCKS
+    else:
+        raise ValueError(f"unsupported weight scale shape {tuple(w_s.shape)}")
+    out = torch.ops.qmoe.quantized_matmul(x2, w_nk, w_s, int(w8a16_max_rows), regime)
     return out.reshape(orig_out_shape)
 
 
 @torch.library.custom_op("qmoe::quantized_matmul", mutates_args=())
 def _quantized_matmul_op(x2: torch.Tensor, w_nk: torch.Tensor, w_s: torch.Tensor,
-                         w8a16_max_rows: int) -> torch.Tensor:
+                         w8a16_max_rows: int, regime: int) -> torch.Tensor:
     """Checked operands: x2 bf16 [rows, K]; w_nk N-major [N, K] codes; w_s
-    per-channel f32 [N] or compact block scales [N/bn, K/128]."""
+    per-channel f32 [N], [N, K/B] (the gmm_v2 regimes) or compact native
+    block scales [N/bn, K/128]."""
     n_out, k_dim = w_nk.shape
     rows = x2.shape[0]
-    if w_s.dim() == 1:
+    wq = w_nk.view(torch.uint8)
+    is_int = w_nk.dtype == torch.int8
+    if regime == REGIME_PER_CHANNEL:
         ws = w_s.float().contiguous()
-        if w_nk.dtype == torch.int8:
+        if is_int:
             xq, xs = ops.row_quant(x2, "int8")
-            out = ops.gemm(_capi.W8A8_PC, xq.view(torch.uint8), w_nk.view(torch.uint8),
-                           a_scale=xs, w_scale=ws, wfmt=1)
-        elif w_nk.dtype == torch.float8_e4m3fn:
-            if 0 < rows <= w8a16_max_rows:
-                out = ops.gemm(_capi.W8A16_PC, x2, w_nk.view(torch.uint8), w_scale=ws)
-            else:
-                xq, xs = ops.row_quant(x2, "fp8")
-                out = ops.gemm(_capi.W8A8_PC, xq.view(torch.uint8), w_nk.view(torch.uint8),
-                               a_scale=xs, w_scale=ws, wfmt=0)
-        else:
-            raise ValueError(f"Unsupported quantized dtype: {w_nk.dtype}")
-    else:
-        sb, bn = _scale_blocks(w_s, k_dim, n_out)
-        xq, xs = ops.row_quant(x2, "fp8", block=128)
-        out = ops.gemm(_capi.W8A8_BLK, xq.view(torch.uint8), w_nk.view(torch.uint8),
-                       a_scale=xs, w_scale=sb, ws_bn=bn)
-    return out
+            return ops.gemm(_capi.W8A8_PC, xq.view(torch.uint8), wq, a_scale=xs, w_scale=ws, wfmt=1)
+        if 0 < rows <= w8a16_max_rows:
+            return ops.gemm(_capi.W8A16_PC, x2, wq, w_scale=ws)
+        xq, xs = ops.row_quant(x2, "fp8")
+        return ops.gemm(_capi.W8A8_PC, xq.view(torch.uint8), wq, a_scale=xs, w_scale=ws, wfmt=0)
+    if regime == REGIME_GMM_W8A16:
+        return ops.gemm(_capi.W8A16_BLK, x2, wq, w_scale=w_s, ws_bn=1)
+    if regime == REGIME_GMM_QUANT_LHS:
+        xq, xs = ops.row_quant(x2, "int8" if is_int else "fp8", mode="gmm")
+        return ops.gemm(_capi.W8A8_GMM, xq.view(torch.uint8), wq, a_scale=xs, w_scale=w_s, wfmt=int(is_int))
+    sb, bn = _native_blocks(w_s, k_dim, n_out)
+    xq, xs = ops.row_quant(x2, "fp8", block=128)
+    return ops.gemm(_capi.W8A8_BLK, xq.view(torch.uint8), wq, a_scale=xs, w_scale=sb, ws_bn=bn)
 
 
 @_quantized_matmul_op.register_fake
-def _(x2, w_nk, w_s, w8a16_max_rows):
+def _(x2, w_nk, w_s, w8a16_max_rows, regime):
     return x2.new_empty((x2.shape[0], w_nk.shape[0]), dtype=torch.bfloat16)
 
 

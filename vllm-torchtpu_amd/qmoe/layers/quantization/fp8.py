@@ -37,6 +37,9 @@ from qmoe.layers.linear_common import quantized_matmul
 
 FP8 = torch.float8_e4m3fn
 _REQUANT_DTYPES = {"float8_e4m3fn": FP8, "int8": torch.int8}
+# accepted by the reference's env parsing (`fp8.py:122-127`); no kernel here
+# runs e5m2 codes, so selecting it raises NotImplementedError at load time
+_REQUANT_DTYPES_UNBUILT = ("float8_e5m2",)
 
 
 # f32 bytes of one chunk of experts dequantized at load time
@@ -68,12 +71,47 @@ def get_linear_quant_config():
             "quantized_matmul_kernel or unset the quantize block size to trigger per-channel "
             "quantization."
         )
+    if name in _REQUANT_DTYPES_UNBUILT:
+        raise NotImplementedError(f"REQUANTIZE_WEIGHT_DTYPE={name} is not built: qmoe kernels take "
+                                  "float8_e4m3fn and int8 weight codes")
     if name not in _REQUANT_DTYPES:
-        supported = ", ".join(sorted(_REQUANT_DTYPES))
+        supported = ", ".join(sorted(list(_REQUANT_DTYPES) + list(_REQUANT_DTYPES_UNBUILT)))
         raise ValueError(f"Unsupported REQUANTIZE_WEIGHT_DTYPE={name!r}. Supported values: {supported}.")
-    if block is not None and block != 128:
-        raise ValueError(f"qmoe blockwise kernels take REQUANTIZE_BLOCK_SIZE=128, got {block}")
+    if block is not None:
+        _check_block(block, "REQUANTIZE_BLOCK_SIZE")
+        if block == 128 and name != "float8_e4m3fn":
+            raise NotImplementedError("128-column blocks are dequantized to bf16 before the matmul; qmoe "
+                                      "runs that regime for float8_e4m3fn codes only")
     return name, _REQUANT_DTYPES[name], block, bool(enable)
+
+
+def _check_block(block, env_name):
+    """Requantization blocks the kernels run: 128 (dequantized to bf16 before
+    the matmul, the reference's regime for blocks under 256) or a
+    power-of-two multiple of 512 (the quantized-activation regime)."""
+    ok = block == 128 or (block >= 512 and block % 512 == 0 and ((block // 512) & (block // 512 - 1)) == 0)
+    if not ok:
+        raise NotImplementedError(f"qmoe runs {env_name}=128 or a power-of-two multiple of 512, got {block}")
+
+
+def get_moe_quant_config():
+    """(dtype name, torch dtype, block size or None) for FP8 MoE
+    requantization from MOE_REQUANTIZE_WEIGHT_DTYPE / MOE_REQUANTIZE_BLOCK_SIZE,
+    `fp8.py:185-213` (default: float8_e4m3fn per channel)."""
+    name = envs.MOE_REQUANTIZE_WEIGHT_DTYPE or "float8_e4m3fn"
+    block = envs.MOE_REQUANTIZE_BLOCK_SIZE or None
+    if name in _REQUANT_DTYPES_UNBUILT:
+        raise NotImplementedError(f"MOE_REQUANTIZE_WEIGHT_DTYPE={name} is not built: qmoe kernels take "
+                                  "float8_e4m3fn and int8 weight codes")
+    if name not in _REQUANT_DTYPES:
+        supported = ", ".join(sorted(list(_REQUANT_DTYPES) + list(_REQUANT_DTYPES_UNBUILT)))
+        raise ValueError(f"Unsupported MOE_REQUANTIZE_WEIGHT_DTYPE={name!r}. Supported values: {supported}.")
+    if block is not None:
+        _check_block(block, "MOE_REQUANTIZE_BLOCK_SIZE")
+        if block == 128 and name != "float8_e4m3fn":
+            raise NotImplementedError("128-column blocks are dequantized to bf16 before the matmul; qmoe "
+                                      "runs that regime for float8_e4m3fn codes only")
+    return name, _REQUANT_DTYPES[name], block
 
 
 def dequantize_fp8_weight(weight, weight_scale=None, weight_scale_inv=None, block=None,
@@ -98,12 +136,19 @@ def dequantize_fp8_weight(weight, weight_scale=None, weight_scale_inv=None, bloc
 
 
 def requantize(w_f32, qdtype_name, block=None):
-    """f32 [..., N, K] -> codes + scale with the load-time quantizer kernel:
-    per row ([.., N] scale) or per (row, 128-column block) ([.., N, K/128])."""
+    """f32 [..., N, K] -> codes + scale with the load-time quantizer kernel
+    (`layers/core/quantization.py:232-318`): per row ([.., N] scale) or per
+    (row, B-column block) ([.., N, K/B]; B = 128 in one launch, larger B as
+    rows of B columns)."""
     lead = w_f32.shape[:-1]
     k = w_f32.shape[-1]
-    q, s = ops.row_quant(w_f32.reshape(-1, k).contiguous(), "fp8" if qdtype_name == "float8_e4m3fn" else "int8",
-                         block=block, mode="load")
+    qd = "fp8" if qdtype_name == "float8_e4m3fn" else "int8"
+    if block is not None and k % block:
+        raise ValueError(f"Quantization expects the requested axis to be divisible by block_size {block}, got {k}")
+    if block is not None and block != 128:
+        q, s = ops.row_quant(w_f32.reshape(-1, block).contiguous(), qd, mode="load")
+        return q.reshape(*lead, k), s.reshape(*lead, k // block)
+    q, s = ops.row_quant(w_f32.reshape(-1, k).contiguous(), qd, block=block, mode="load")
     q = q.reshape(*lead, k)
     s = s.reshape(*lead) if block is None else s.reshape(*lead, k // block)
     return q, s
@@ -186,9 +231,11 @@ class Fp8LinearMethod:
         ckpt_block = None
         if self.quant_config.is_checkpoint_fp8_serialized and self.block_quant:
             ckpt_block = tuple(getattr(layer, "weight_block_size", None) or self.weight_block_size)
-        if (blockwise and name == "float8_e4m3fn" and ckpt_block == (128, 128)
-                and weight.dtype == FP8 and weight.shape[0] % 128 == 0 and weight.shape[1] % 128 == 0):
-            # native 128x128 tiles: codes and tile scales stay as loaded
+        if (blockwise and block == 128 and envs.QMOE_FP8_NATIVE_BLOCKS and name == "float8_e4m3fn"
+                and ckpt_block == (128, 128) and weight.dtype == FP8 and weight.shape[0] % 128 == 0
+                and weight.shape[1] % 128 == 0):
+            # opt-in: native 128x128 tiles, codes and tile scales as loaded
+            # (the blockwise W8A8 recipe, compact [N/128, K/128] scales)
             w_rt = weight.contiguous()
             s_rt = layer.weight_scale_inv.data.to(dev, torch.float32).contiguous()
         else:
@@ -205,6 +252,10 @@ class Fp8LinearMethod:
             if block is not None and w_f.shape[-1] < block:
                 block = None  # `fp8.py:332-337`: too narrow for the block
             w_rt, s_rt = requantize(w_f, name, block if blockwise else None)
+            if blockwise and block is not None:
+                # the reference's runtime layout [1, K/B, 1, N]
+                # (`fp8.py:270-294`), as a view of the N-major [N, K/B] buffer
+                s_rt = s_rt.t()[None, :, None, :]
         for attr in ("weight_scale_inv", "weight_scale"):
             if hasattr(layer, attr):
                 delattr(layer, attr)
@@ -257,11 +308,23 @@ class Fp8MoEMethod:
 
     def process_weights_after_loading(self, layer):
         """Checkpoint -> runtime (`fp8.py:982-1106`), once. The FP8 MoE
-        asserts no bias, as the reference does (`:994`)."""
+        asserts no bias, as the reference does (`:994`).
+
+        The reference's recipe (`fp8.py:486-617`): dequantize to f32 in
+        chunks of experts, de-interleave swigluoai gate/up rows, zero the
+        padding of an unpadded intermediate size and pad the intermediate
+        size to a multiple of 128 (`:351-406`), requantize to
+        MOE_REQUANTIZE_WEIGHT_DTYPE (float8_e4m3fn by default, or int8) per
+        channel, or per (row, MOE_REQUANTIZE_BLOCK_SIZE columns). At run time
+        per-channel and 512+ blocks take the quantized-activation recipe, 128
+        blocks the bf16-dequantized one. With QMOE_FP8_NATIVE_BLOCKS=1 a
+        128x128-block checkpoint keeps its tiles instead (the blockwise W8A8
+        recipe of BASELINE config 4)."""
         if getattr(layer, "_qmoe_processed", False):
             return
         if getattr(layer, "w13_bias", None) is not None or getattr(layer, "w2_bias", None) is not None:
             raise AssertionError("FP8 MoE does not support bias")
+        name, _, block = get_moe_quant_config()
         dev = _device()
         act = _activation(layer)
         interleaved = act == "swigluoai"
@@ -269,8 +332,16 @@ class Fp8MoEMethod:
         w2 = layer.w2_weight.data.to(dev)
         E, N13, H = w13.shape
         I = w2.shape[2]
-        native = (self.block_quant and tuple(self.weight_block_size) == (128, 128) and w13.dtype == FP8
-                  and not interleaved and N13 % 128 == 0 and H % 128 == 0 and I % 128 == 0)
+        if self.block_quant:
+            bh, bw = self.weight_block_size
+            for wname, t in (("w13_weight", w13), ("w2_weight", w2)):
+                if t.shape[1] % bh or t.shape[2] % bw:
+                    raise ValueError(
+                        "FP8 block quantized MoE weights must be divisible by the checkpoint block size, "
+                        f"got {wname}.shape={tuple(t.shape)} and block_size={tuple(self.weight_block_size)}.")
+        native = (envs.QMOE_FP8_NATIVE_BLOCKS and block is None and name == "float8_e4m3fn" and self.block_quant
+                  and tuple(self.weight_block_size) == (128, 128) and w13.dtype == FP8 and not interleaved
+                  and N13 % 128 == 0 and H % 128 == 0 and I % 128 == 0)
         if native:
             layer.w13_weight = _param(w13.contiguous())
             layer.w2_weight = _param(w2.contiguous())
@@ -278,27 +349,48 @@ class Fp8MoEMethod:
             layer.w2_weight_scale = _param(layer.w2_weight_scale_inv.data.to(dev, torch.float32).contiguous())
             layer._qmoe_format = "fp8_block"
         else:
-            block = 128 if (self.block_quant and H % 128 == 0 and I % 128 == 0) else None
-            # dequantize -> (de-interleave) -> requantize on the device, a
-            # chunk of experts at a time so the f32 copy stays under ~1 GiB
-            # (the reference's chunked loop, `fp8.py:414-453`)
-            q13 = torch.empty((E, N13, H), dtype=FP8, device=dev)
-            q2 = torch.empty((E, H, I), dtype=FP8, device=dev)
-            s13 = torch.empty((E, N13) if block is None else (E, N13, H // block), dtype=torch.float32, device=dev)
-            s2 = torch.empty((E, H) if block is None else (E, H, I // block), dtype=torch.float32, device=dev)
-            chunk = max(1, REQUANT_CHUNK_BYTES // (4 * N13 * H))
+            # the logical intermediate size (the rest of I is checkpoint
+            # padding, zeroed) and its 128-aligned runtime size
+            moe = getattr(layer, "moe_config", None) or self.moe
+            real = getattr(moe, "intermediate_size_per_partition_unpadded", None) or I
+            Ip = (I + 127) // 128 * 128
+            for wname, kk in (("w13", H), ("w2", Ip)):
+                if block is not None and kk % block:
+                    raise ValueError(f"Unsupported MoE quantization: {wname} contracting dimension {kk} is not "
+                                     f"divisible by block_size={block}.")
+            qdt = FP8 if name == "float8_e4m3fn" else torch.int8
+
+            def alloc(n, k):
+                return (torch.empty((E, n, k), dtype=qdt, device=dev),
+                        torch.empty((E, n) if block is None else (E, n, k // block), dtype=torch.float32,
+                                    device=dev))
+
+            q13, s13 = alloc(2 * Ip, H)
+            q2, s2 = alloc(H, Ip)
+            # dequantize -> (de-interleave) -> zero / pad -> requantize on the
+            # device, a chunk of experts at a time so the f32 copy stays under
+            # ~1 GiB (the reference's chunked loop, `fp8.py:414-453`)
+            chunk = max(1, REQUANT_CHUNK_BYTES // (4 * 2 * Ip * H))
             for e0 in range(0, E, chunk):
                 e1 = min(E, e0 + chunk)
-                w13f = self._dequant_experts(layer, "w13", w13[e0:e1], e0)
+                f = self._dequant_experts(layer, "w13", w13[e0:e1], e0)
                 if interleaved:  # `fp8.py:364-367`: [g0, u0, g1, u1, ...] -> [g | u]
-                    w13f = torch.cat([w13f[:, 0::2], w13f[:, 1::2]], dim=1)
-                q13[e0:e1], s13[e0:e1] = requantize(w13f, "float8_e4m3fn", block)
-                del w13f
-                q2[e0:e1], s2[e0:e1] = requantize(self._dequant_experts(layer, "w2", w2[e0:e1], e0),
-                                                  "float8_e4m3fn", block)
+                    f = torch.cat([f[:, 0::2], f[:, 1::2]], dim=1)
+                g, u = f[:, :I], f[:, I:]
+                f = torch.zeros((e1 - e0, 2 * Ip, H), dtype=torch.float32, device=dev)
+                f[:, :real], f[:, Ip:Ip + real] = g[:, :real], u[:, :real]
+                del g, u
+                q13[e0:e1], s13[e0:e1] = requantize(f, name, block)
+                f2 = torch.zeros((e1 - e0, H, Ip), dtype=torch.float32, device=dev)
+                f2[:, :, :real] = self._dequant_experts(layer, "w2", w2[e0:e1], e0)[:, :, :real]
+                q2[e0:e1], s2[e0:e1] = requantize(f2, name, block)
+                del f, f2
             layer.w13_weight, layer.w2_weight = _param(q13), _param(q2)
             layer.w13_weight_scale, layer.w2_weight_scale = _param(s13), _param(s2)
-            layer._qmoe_format = "fp8_block_rows" if block else "fp8"
+            if block == 128:
+                layer._qmoe_format = "fp8_w8a16"
+            else:
+                layer._qmoe_format = "fp8" if name == "float8_e4m3fn" else "int8"
         for attr in ("w13_weight_scale_inv", "w2_weight_scale_inv"):
             if hasattr(layer, attr):
                 delattr(layer, attr)
@@ -327,12 +419,8 @@ class Fp8MoEMethod:
 
     def apply_monolithic(self, layer, x, router_logits, input_ids=None):
         """`fp8.py:1108-1222` (single-GPU branch): route, then fused MoE."""
-        fmt = layer._qmoe_format
-        # fp8_block_rows: per-(row, 128) scales, the block kernels with one
-        # scale row per weight row
-        wf = fmt if fmt in ("fp8_block", "fp8_block_rows") else "fp8"
         return moe_forward(layer, x, router_logits, layer.w13_weight, layer.w2_weight, layer.w13_weight_scale,
-                           layer.w2_weight_scale, None, None, wf,
+                           layer.w2_weight_scale, None, None, layer._qmoe_format,
                            skip_padded_tokens=envs.TPU_MOE_SKIP_PADDED_TOKENS, input_ids=input_ids)
 
 

@@ -86,8 +86,11 @@ def row_quant(x, qdtype="fp8", block=None, mode="runtime"):
     mode "runtime": `kernels/quantized_matmul/util.py:294-318` semantics
     (scale = absmax / qmax; fp8 in f32, int8 in bf16 arithmetic; zero scale
     -> 1). mode "load": `layers/core/quantization.py:232-318` (reciprocal
-    multiply; zero rows keep scale 0). Returns (codes [M, K] float8_e4m3fn or
-    int8, scales f32 [M] or [M, K/128]).
+    multiply; zero rows keep scale 0). mode "gmm": the grouped matmul's
+    quantized-lhs regime, `kernels/megablox/gmm_v2.py:508-536` (per (row,
+    512 columns), bf16 arithmetic, fp8 RNE / int8 truncated codes; block is
+    always 512). Returns (codes [M, K] float8_e4m3fn or int8, scales f32
+    [M], [M, K/128] or [M, ceil(K/512)]).
     """
     _require_gpu(x)
     if x.dim() != 2:
@@ -99,10 +102,10 @@ def row_quant(x, qdtype="fp8", block=None, mode="runtime"):
     if not in_f32 and x.dtype != torch.bfloat16:
         raise ValueError(f"row_quant expects bf16 (or f32 at load time), got {x.dtype}")
     qd = {"fp8": 0, "int8": 1}[qdtype]
-    md = {"runtime": 0, "load": 1}[mode]
-    blk = 0 if block is None else int(block)
+    md = {"runtime": 0, "load": 1, "gmm": 2}[mode]
+    blk = 512 if md == 2 else (0 if block is None else int(block))
     q = torch.empty((M, K), dtype=FP8 if qd == 0 else torch.int8, device=x.device)
-    ns = 1 if blk == 0 else K // blk
+    ns = 1 if blk == 0 else (K + blk - 1) // blk
     s = torch.empty((M, ns), dtype=torch.float32, device=x.device)
     if M:
         check(lib.qmoe_row_quant(_ptr(x), x.stride(0), int(in_f32), M, K, qd, md, blk, _ptr(q), K,
@@ -146,7 +149,8 @@ def gemm_desc(kind, a, w, *, a_scale=None, w_scale=None, bias=None, wfmt=0, ws_b
     G, N, wcols = w.shape
     if a.stride(-1) != 1 or w.stride(-1) != 1 or w.stride(1) != wcols:
         raise ValueError("qmoe gemm needs K-contiguous activations and N-major [G, N, K] weights")
-    abf16 = kind in (_capi.W8A16_PC, _capi.W4A16_MX, _capi.W16A16, _capi.W4A16_NV, _capi.W4A16_I4)
+    abf16 = kind in (_capi.W8A16_PC, _capi.W4A16_MX, _capi.W16A16, _capi.W4A16_NV, _capi.W4A16_I4,
+                     _capi.W8A16_BLK)
     K = a.shape[1]
     if kind in (_capi.W4A16_MX, _capi.W4A16_NV, _capi.W4A16_I4):
         if wcols * 2 != K:
@@ -175,7 +179,7 @@ def gemm_desc(kind, a, w, *, a_scale=None, w_scale=None, bias=None, wfmt=0, ws_b
     d.w_gstride = w.stride(0) * w.element_size()
     if w_scale is not None:
         ws = w_scale
-        if kind in (_capi.W8A8_PC, _capi.W8A16_PC):
+        if kind in (_capi.W8A8_PC, _capi.W8A16_PC) or (kind == _capi.W8A8_GMM and ws.numel() == G * N):
             ws = ws.reshape(G, N)
             d.ldws, d.ws_gstride = 1, ws.stride(0)
         else:
@@ -261,10 +265,10 @@ def plan_for_shape(kind, M, N, K, *, wfmt=0, activation=None, experts=0, max_row
     d.kind, d.wfmt = kind, wfmt
     d.a = d.w = d.y = d.w_scale = d.a_scale = base
     d.lda = lda if lda is not None else K
-    d.lds_a = K // 128 if kind == _capi.W8A8_BLK else 1
+    d.lds_a = K // 128 if kind == _capi.W8A8_BLK else ((K + 511) // 512 if kind == _capi.W8A8_GMM else 1)
     ldw = K // 2 if w4 else (2 * K if kind == _capi.W16A16 else K)
     d.ldw, d.w_gstride = ldw, ldw * N
-    if kind == _capi.W8A8_BLK:
+    if kind in (_capi.W8A8_BLK, _capi.W8A16_BLK):
         d.ldws = K // 128
     elif kind == _capi.W4A16_MX:
         d.ldws = K // 32
@@ -274,7 +278,7 @@ def plan_for_shape(kind, M, N, K, *, wfmt=0, activation=None, experts=0, max_row
         d.ldws = K // wq_group
     else:
         d.ldws = 1
-    d.ws_gstride = d.ldws * (N // ws_bn if kind == _capi.W8A8_BLK else N)
+    d.ws_gstride = d.ldws * (N // ws_bn if kind in (_capi.W8A8_BLK, _capi.W8A16_BLK) else N)
     d.ws_bn, d.wq_group = ws_bn, wq_group
     if experts:
         d.group_offs = d.active = d.num_active = base
