@@ -291,6 +291,21 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
     }
   };
   auto mma = [&](int t) {
+    if constexpr (INT) {
+      // the two 32-k halves of the k-step go to every accumulator in turn:
+      // the second MFMA of an accumulator comes NI * MJ MFMAs after its first,
+      // so no MFMA waits on the result of the one before it
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+#pragma unroll
+          for (int j = 0; j < MJ; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(h ? hi4(wf[t][i]) : lo4(wf[t][i]),
+                                                              h ? hi4(xf[t][j]) : lo4(xf[t][j]), acc[i][j], 0, 0,
+                                                              0);
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < NI; ++i)
 #pragma unroll
@@ -298,9 +313,6 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
         if constexpr (BLK) {
           const f32x16 c = t == 0 ? f32x16{} : tmp[i][j];
           tmp[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[t][i], xf[t][j], c, 0, 0, 0, 127, 0, 127);
-        } else if constexpr (INT) {
-          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(lo4(wf[t][i]), lo4(xf[t][j]), acc[i][j], 0, 0, 0);
-          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(hi4(wf[t][i]), hi4(xf[t][j]), acc[i][j], 0, 0, 0);
         } else {
           acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[t][i], xf[t][j], acc[i][j], 0, 0, 0,
                                                                       127, 0, 127);
@@ -344,9 +356,13 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
     auto stage = [&](uint8_t* fW, uint8_t* fX, uint8_t* nW, uint8_t* nX, int s, int t) {
       wait_copies_upto<2 * CPS>();  // copies issued after stage s+1's: s+2, s+3
       stage_barrier();
+      // the operand reads of stage s+1 come before the copies in program
+      // order: the compiler treats an LDS copy as a write that may alias any
+      // LDS read after it, so reads placed after the copies could not be
+      // interleaved with this stage's MFMAs
+      read_frags(nW, nX, 0, t ^ 1);
       copy_stage(fW, fX, sS0, min(s + 4, KS - 1));
       mma(t);
-      read_frags(nW, nX, 0, t ^ 1);
       interleave<0, NM, NR, CPS>();
     };
     for (int s = 0; s < KS; s += 4) {
@@ -380,10 +396,13 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
       __builtin_amdgcn_sched_barrier(0);
       wait_copies_upto<(AHEAD - 2) * CPS>();  // stage s+1 has landed
       stage_barrier();
+      // k-step 0 of stage s+1 is read before the copies are issued (an LDS
+      // copy may alias any later LDS read for the compiler, which would keep
+      // the reads behind every copy and expose their latency)
+      read_frags(nW, nX, 0, 0);
       copy_stage(cW, cX, cS, min(s + AHEAD, KS - 1));
       mma(1);
       apply_scales();
-      read_frags(nW, nX, 0, 0);
       interleave<0, NM, NR, CPS>();
     };
     copy_stage(sW0, sX0, sS0, 0);

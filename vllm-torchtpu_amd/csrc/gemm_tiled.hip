@@ -404,11 +404,14 @@ __global__ __launch_bounds__(kThreads) void tiled_gemm_kernel(const GemmParams p
           acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, pack8(bfr[j][0], bfr[j][1]),
                                                                        acc[i][j], 0, 0, 0, 127, 0, 127);
       } else if constexpr (KIND == QK_W8A8_PC && WF == 1) {
+        // both 64-k halves of every fragment pair, the second NF MFMAs after
+        // the first (no MFMA waits on the one before it)
 #pragma unroll
-        for (int j = 0; j < NF; ++j) {
+        for (int j = 0; j < NF; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(as_i4(a0), as_i4(bfr[j][0]), acc[i][j], 0, 0, 0);
+#pragma unroll
+        for (int j = 0; j < NF; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(as_i4(a1), as_i4(bfr[j][1]), acc[i][j], 0, 0, 0);
-        }
       } else if constexpr (KIND == QK_W8A8_BLK) {
         const i32x8 av = pack8(a0, a1);
         const float* sc = sSc + buf * (BM + BN);
