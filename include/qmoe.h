@@ -251,6 +251,64 @@ int qmoe_moe_combine(const uint16_t* rows, const int32_t* topk_ids, const uint16
                      int64_t T, int topk, int E, int64_t H, int skip_padded, uint16_t* out, int64_t ldo,
                      qmoe_stream_t stream);
 
+/*
+ * Fused decode MoE layer: the shared expert plus the routed experts of a
+ * decode step, one call. Replaces the kernel call of
+ * `layers/adapter/fused_moe_decode.py:249-339` (`_build_op` -> `_layer`),
+ * i.e. `kernels/experimental/fused_moe_decode/fused_moe_decode_kernel.py:
+ * 552-740` (`fused_moe_decode`) on one rank: n_ranks = 1 (the all-reduce is
+ * the identity), expert_start = None, scatter_rows = False; the caller's
+ * router supplies topk_ids / topk_weights.
+ *
+ * Numerics (all float32, output bf16): hidden states quantized to e4m3 per
+ * (row, 512 columns) as scale = max|x| / 448, codes e4m3(x * (1 / scale));
+ * each block's code dot times its row scale, summed, times the per-channel
+ * w1 scale; mid = silu(gate) * up * coeff, coeff = bf16(route weight) *
+ * routed_scale summed over the token's routes to that expert, or for the
+ * shared expert sigmoid(x . shared_gate) (1 when shared_gate is NULL);
+ * mid quantized per (row, 512 columns) the same way; second dot per block
+ * times its row scale, summed, times the per-channel w2 scale; the shared
+ * expert and the active routed experts added into one float32 sum per
+ * token.
+ *
+ * weight_blocks = 128 (this build's variant, no reference counterpart):
+ * 128x128 weight tiles kept as checkpointed, activations quantized per
+ * (row, 128 columns), each block's dot times the activation block scale
+ * times the tile scale.
+ */
+typedef struct qmoe_moe_decode_desc {
+  const void* x;           /* bf16 [T][H] hidden states */
+  int64_t T;               /* tokens, 1..64 */
+  int64_t H;               /* hidden size, a multiple of 512 */
+  int64_t I;               /* routed intermediate size, a multiple of 128 */
+  int64_t I_shared;        /* shared intermediate size, a multiple of 128, <= I */
+  int E;                   /* routed experts, 1..512 */
+  int topk;                /* routes per token, 1..64 */
+  const int32_t* topk_ids; /* [T][topk]; ids outside [0, E) select nothing */
+  const void* topk_weights;/* [T][topk] bf16 (weights_f32 = 0) or f32 */
+  int weights_f32;
+  float routed_scale;      /* multiplies the routed experts only */
+  int weight_blocks;       /* 0: per-channel scales; 128: 128x128 tile scales */
+  const void* w1;          /* e4m3 [E][2I][H]: gate rows then up rows */
+  const void* w2;          /* e4m3 [E][H][I] */
+  const float* w1_scale;   /* [E][2I] | [E][2I/128][H/128] */
+  const float* w2_scale;   /* [E][H]  | [E][H/128][I/128] */
+  const void* shared_w1;   /* e4m3 [2 I_shared][H] */
+  const void* shared_w2;   /* e4m3 [H][I_shared] */
+  const float* shared_w1_scale; /* [2 I_shared] | [2 I_shared/128][H/128] */
+  const float* shared_w2_scale; /* [H] | [H/128][I_shared/128] */
+  const uint16_t* shared_gate;  /* bf16 [H], or NULL for an ungated shared expert */
+  uint16_t* out;           /* bf16 [T][ldo] */
+  int64_t ldo;
+} qmoe_moe_decode_desc;
+
+/* Workspace bytes of qmoe_moe_decode for this descriptor. */
+int qmoe_moe_decode_workspace_size(const qmoe_moe_decode_desc* d, int64_t* bytes);
+
+/* Four launches on `stream`; QMOE_ERR_ARG outside the envelope above,
+ * QMOE_ERR_WORKSPACE when ws_bytes is below qmoe_moe_decode_workspace_size. */
+int qmoe_moe_decode(const qmoe_moe_decode_desc* d, void* workspace, int64_t ws_bytes, qmoe_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -43,12 +43,9 @@ E4M3_MAX = 448.0
 E4M3_NAN = 0x7F
 
 
-def e4m3_decode(codes) -> np.ndarray:
-    """uint8 e4m3fn codes -> float32 values (exact).
-
-    Layout S.EEEE.MMM, bias 7, no infinities, S.1111.111 is NaN.
-    """
-    c = np.asarray(codes, dtype=np.uint8).astype(np.int64)
+def _e4m3_values(c) -> np.ndarray:
+    """Layout S.EEEE.MMM, bias 7, no infinities, S.1111.111 is NaN."""
+    c = np.asarray(c, dtype=np.int64)
     s = np.where((c >> 7) & 1, -1.0, 1.0)
     e = (c >> 3) & 0xF
     m = c & 0x7
@@ -56,6 +53,15 @@ def e4m3_decode(codes) -> np.ndarray:
     val = s * val
     val = np.where((e == 0xF) & (m == 0x7), np.nan, val)
     return val.astype(np.float32)
+
+
+_E4M3_TABLE = _e4m3_values(np.arange(256))
+
+
+def e4m3_decode(codes) -> np.ndarray:
+    """uint8 e4m3fn codes -> float32 values (exact), through the table of
+    `_e4m3_values` over all 256 codes."""
+    return _E4M3_TABLE[np.asarray(codes, dtype=np.uint8)]
 
 
 def e4m3_encode(x) -> np.ndarray:

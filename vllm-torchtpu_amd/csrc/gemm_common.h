@@ -138,7 +138,35 @@ struct GemmParams {
   // split-K workspace (skinny kernel only)
   float* partial;
   int32_t ksplit;
+  // Fused decode MoE (skinny kernel only, ksplit 1, no bias). x0 != 0: group
+  // 0 is the layer's shared expert, with its own weights w_x / scales ws_x
+  // (same layout, n_x weight rows), and group g >= 1 is expert g - 1 of w /
+  // w_scale. y32 != nullptr: the epilogue multiplies by row_coeff[R] and
+  // stores float32 at y32[R * ldy + n], folding the absolute maximum of each
+  // (row, 2^bshift columns) block into bmax[R * ldb + n >> bshift] (float32
+  // bits, atomic max; the values are non-negative, so integer order is float
+  // order). The extra group needs no dispatch metadata: its workgroups start
+  // streaming without waiting for the active list.
+  int32_t x0;
+  int32_t n_x;
+  int32_t rows_x;  // rows of the extra group: compact rows [0, rows_x), always slot 0
+  const uint8_t* w_x;
+  const void* ws_x;
+  const float* row_coeff;
+  float* y32;
+  uint32_t* bmax;
+  int32_t bshift;
+  int32_t ldb;
 };
+
+// Group g's slice of a per-group array with group stride gs (elements); with
+// p.x0, group 0 is the extra group's own array and the others shift down.
+template <typename T>
+__device__ __forceinline__ const T* group_slice(const GemmParams& p, const T* base, const void* xbase, int64_t gs,
+                                                int g) {
+  if (p.x0) return g == 0 ? static_cast<const T*>(xbase) : base + (int64_t)(g - 1) * gs;
+  return base + (int64_t)g * gs;
+}
 
 __device__ __forceinline__ float qmoe_sigmoid(float x) { return 1.0f / (1.0f + __expf(-x)); }
 

@@ -39,15 +39,17 @@
 #include <type_traits>
 
 #include "gemm_common.h"
+#include "stream_load.h"
 
 namespace {
 
+using namespace qmoe_stream;
+
+// cache-policy bits of the weight stream's loads (read once per launch)
+constexpr int kWeightAux = 0;
+
 constexpr int kWaves = 4;  // wavefronts of the split-K finishing kernel
 constexpr int kThreads = kWaves * 64;
-
-struct Frag {
-  uint4 v[4];
-};
 
 template <int KIND, int WF>
 struct Traits {
@@ -83,38 +85,6 @@ struct Traits {
 // at the end of the short per-wavefront K slices and lose 5-30%)
 int default_unroll() { return 1; }
 
-// Operands are read with buffer loads: a wave-uniform resource (base and
-// extent in SGPRs), a 32-bit per-lane offset fixed for the whole K loop, and
-// the step's byte offset as a scalar. This keeps one VGPR per stream instead
-// of a 64-bit address per load; the host keeps every operand below 2 GiB.
-using rsrc_t = __amdgpu_buffer_rsrc_t;
-
-__device__ __forceinline__ rsrc_t make_rsrc(const void* base, int64_t bytes) {
-  const int n = bytes >= 0x7fffffff ? 0x7fffffff : (int)bytes;
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
-}
-
-// A lane offset with this bit set is past every buffer's extent (the host
-// keeps operands below 2 GiB, and lane offsets below 2 GiB have the bit
-// clear): the load returns zeros and makes no memory request. The bit goes in
-// the per-lane offset, which the range check always covers; the scalar step
-// offset stays a valid one.
-constexpr uint32_t kOob = 0x80000000u;
-
-// cache-policy bits of the weight stream's loads (read once per launch)
-constexpr int kWeightAux = 0;
-
-// NB/16 weight chunks of one step: 16 B at voff + j*64 (the lane's column of
-// 64 B segment j of its load row)
-template <int NB, int AUX = 0>
-__device__ __forceinline__ void ldw_seg(Frag& f, rsrc_t r, uint32_t voff, uint32_t soff) {
-#pragma unroll
-  for (int j = 0; j < NB / 16; ++j) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff + j * 64, soff, AUX);
-    f.v[j] = make_uint4(v[0], v[1], v[2], v[3]);
-  }
-}
-
 // activation chunks of one step at the offsets of Traits::a_off
 template <typename Tr>
 __device__ __forceinline__ void lda_chunks(Frag& f, rsrc_t r, uint32_t voff, uint32_t soff) {
@@ -123,32 +93,6 @@ __device__ __forceinline__ void lda_chunks(Frag& f, rsrc_t r, uint32_t voff, uin
     const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff + Tr::a_off(i), soff, 0);
     f.v[i] = make_uint4(v[0], v[1], v[2], v[3]);
   }
-}
-
-// Weight loads put row (l >> 2), column (l & 3) of a 64 B segment in lane l,
-// so the 4 lanes of each 64 B piece are adjacent (the load is coalesced);
-// the MFMA wants row (l & 15), k-group (l >> 4) in lane l. `src` is the
-// byte address of lane 4*(l & 15) + (l >> 4).
-template <int NB>
-__device__ __forceinline__ void permute_w(Frag& f, int src) {
-#pragma unroll
-  for (int j = 0; j < NB / 16; ++j) {
-    f.v[j].x = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)f.v[j].x);
-    f.v[j].y = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)f.v[j].y);
-    f.v[j].z = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)f.v[j].z);
-    f.v[j].w = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)f.v[j].w);
-  }
-}
-
-__device__ __forceinline__ float ldb_f32(rsrc_t r, uint32_t voff, uint32_t soff) {
-  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
-}
-
-__device__ __forceinline__ i32x8 as_i32x8(const Frag& f) {
-  i32x8 r;
-  r[0] = f.v[0].x; r[1] = f.v[0].y; r[2] = f.v[0].z; r[3] = f.v[0].w;
-  r[4] = f.v[1].x; r[5] = f.v[1].y; r[6] = f.v[1].z; r[7] = f.v[1].w;
-  return r;
 }
 
 __device__ __forceinline__ i32x4 as_i32x4(const uint4& u) {
@@ -318,9 +262,9 @@ __device__ __forceinline__ float finish_elem(const GemmParams& p, float acc, int
   float v = acc;
   if (KIND == QK_W8A8_PC) {
     v = v * p.a_scale[(int64_t)arow * p.lds_a];
-    v = v * static_cast<const float*>(p.w_scale)[(int64_t)g * p.ws_gstride + n];
+    v = v * group_slice(p, static_cast<const float*>(p.w_scale), p.ws_x, p.ws_gstride, g)[n];
   } else if (KIND == QK_W8A16_PC) {
-    v = v * static_cast<const float*>(p.w_scale)[(int64_t)g * p.ws_gstride + n];
+    v = v * group_slice(p, static_cast<const float*>(p.w_scale), p.ws_x, p.ws_gstride, g)[n];
   }
   if (p.bias) v += p.bias[(int64_t)g * p.bias_gstride + n];
   return v;
@@ -344,6 +288,12 @@ __device__ __forceinline__ void store_out(const GemmParams& p, int g, int R, int
 
 // group of this workgroup's slot; false if the slot is empty
 __device__ __forceinline__ bool slot_group(const GemmParams& p, int slot, int& g, int& row0, int& rows) {
+  if (p.x0 && slot == 0) {
+    g = 0;
+    row0 = 0;
+    rows = p.rows_x;
+    return rows > 0;
+  }
   g = slot;
   if (p.active) {
     if (slot >= *p.num_active) return false;
@@ -372,7 +322,11 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p)
   // matching up rows
   constexpr int NH = NS / 2;
   const int tile = blockIdx.x;
-  const int nlim = ACT ? (p.N >> 1) : p.N;
+  // weight rows of this group (the extra group of a fused decode layer may
+  // have fewer; its surplus tiles have no work)
+  const int NG = (p.x0 && g == 0) ? p.n_x : p.N;
+  const int nlim = ACT ? (NG >> 1) : NG;
+  if (tile * (ACT ? 16 * NH : 16 * NS) >= nlim) return;
   int nw[NS];
   bool nok[NS];
   if (ACT) {
@@ -381,7 +335,7 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p)
       const int c = tile * (16 * NH) + s * 16 + col;
       nok[s] = nok[s + NH] = c < nlim;
       nw[s] = c;
-      nw[s + NH] = (p.N >> 1) + c;
+      nw[s + NH] = (NG >> 1) + c;
     }
   } else {
 #pragma unroll
@@ -391,20 +345,20 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p)
     }
   }
   g = __builtin_amdgcn_readfirstlane(g);
-  const rsrc_t wres = make_rsrc(p.w + (int64_t)g * p.w_gstride, (int64_t)p.N * p.ldw);
+  const rsrc_t wres = make_rsrc(group_slice(p, p.w, p.w_x, p.w_gstride, g), (int64_t)NG * p.ldw);
   auto row_of = [&](int s, int c) {  // clamped global row of tile s, column c
     if (ACT) {
       const int r = min(tile * (16 * NH) + (s % NH) * 16 + c, nlim - 1);
-      return s < NH ? r : (p.N >> 1) + r;
+      return s < NH ? r : (NG >> 1) + r;
     }
-    return min(tile * (16 * NS) + s * 16 + c, p.N - 1);
+    return min(tile * (16 * NS) + s * 16 + c, NG - 1);
   };
   // weight loads: lane l reads row (l >> 2) of each tile, 16 B column (l & 3)
   uint32_t woff[NS];
   int nclamp[NS];
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
-    nclamp[s] = nok[s] ? nw[s] : (ACT ? (s < NH ? nlim - 1 : p.N - 1) : p.N - 1);
+    nclamp[s] = nok[s] ? nw[s] : (ACT ? (s < NH ? nlim - 1 : NG - 1) : NG - 1);
     woff[s] = (uint32_t)(row_of(s, lane >> 2) * p.ldw + (lane & 3) * 16);
   }
   const int perm_src = (4 * col + kg) * 4;
@@ -415,19 +369,21 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p)
   rsrc_t sres = wres, ares = wres;  // placeholders for kinds without scale streams
   uint32_t soffw[NS];
   if constexpr (KIND == QK_W4A16_MX) {
-    sres = make_rsrc(static_cast<const uint8_t*>(p.w_scale) + (int64_t)g * p.ws_gstride, (int64_t)p.N * p.ldws);
+    sres = make_rsrc(group_slice(p, static_cast<const uint8_t*>(p.w_scale), p.ws_x, p.ws_gstride, g), (int64_t)NG * p.ldws);
   } else if constexpr (KIND == QK_W4A16_NV) {
-    sres = make_rsrc(static_cast<const uint16_t*>(p.w_scale) + (int64_t)g * p.ws_gstride, (int64_t)p.N * p.ldws * 2);
+    sres = make_rsrc(group_slice(p, static_cast<const uint16_t*>(p.w_scale), p.ws_x, p.ws_gstride, g),
+                     (int64_t)NG * p.ldws * 2);
 #pragma unroll
     for (int s = 0; s < NS; ++s) soffw[s] = (uint32_t)(nclamp[s] * p.ldws * 2 + kg * 4);
   } else if constexpr (KIND == QK_W4A16_I4) {
     // bf16 [N][K/group]: the lane's 32 k sit in group (128 step + 32 kg) / group
-    sres = make_rsrc(static_cast<const uint16_t*>(p.w_scale) + (int64_t)g * p.ws_gstride, (int64_t)p.N * p.ldws * 2);
+    sres = make_rsrc(group_slice(p, static_cast<const uint16_t*>(p.w_scale), p.ws_x, p.ws_gstride, g),
+                     (int64_t)NG * p.ldws * 2);
 #pragma unroll
     for (int s = 0; s < NS; ++s) soffw[s] = (uint32_t)(nclamp[s] * p.ldws * 2 + (kg * 32 / p.wq_group) * 2);
   } else if constexpr (KIND == QK_W8A8_BLK || KIND == QK_W8A16_BLK) {
-    sres = make_rsrc(static_cast<const float*>(p.w_scale) + (int64_t)g * p.ws_gstride,
-                     (int64_t)cdiv(p.N, p.ws_bn) * p.ldws * 4);
+    sres = make_rsrc(group_slice(p, static_cast<const float*>(p.w_scale), p.ws_x, p.ws_gstride, g),
+                     (int64_t)cdiv(NG, p.ws_bn) * p.ldws * 4);
     if (KIND == QK_W8A8_BLK) ares = make_rsrc(p.a_scale, (int64_t)p.M * p.lds_a * 4);
 #pragma unroll
     for (int s = 0; s < NS; ++s) soffw[s] = (uint32_t)((nclamp[s] / p.ws_bn) * p.ldws * 4);
@@ -716,7 +672,33 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p)
           for (int s = 0; s < NS; ++s) v[s] = (float)acc.v[ms][s][r];
         }
         const int ar = p.a_rows ? p.a_rows[R] : R;
-        if (ACT) {
+        if (p.y32) {
+          // fused decode epilogue: float32 out times the row coefficient,
+          // and the row's absolute maximum over this workgroup's columns
+          // (one quantization block: 16 * NS columns from a multiple of 32)
+          // folded into the block maximum. The 16 lanes of a row share kg,
+          // so the row test above is uniform across them.
+          const float coef = p.row_coeff ? p.row_coeff[R] : 1.0f;
+          float mx = 0.0f;
+#pragma unroll
+          for (int s = 0; s < (ACT ? NH : NS); ++s) {
+            if (!nok[s]) continue;
+            float o;
+            if constexpr (ACT)
+              o = qmoe_act(p.act, finish_elem<KIND>(p, v[s], ar, g, nw[s]),
+                           finish_elem<KIND>(p, v[s + NH], ar, g, nw[s + NH]), p.act_p0, p.act_p1);
+            else
+              o = finish_elem<KIND>(p, v[s], ar, g, nw[s]);
+            o = o * coef;
+            p.y32[(int64_t)R * p.ldy + nw[s]] = o;
+            mx = fmaxf(mx, fabsf(o));
+          }
+#pragma unroll
+          for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 16));
+          if (col == 0)
+            atomicMax(p.bmax + (int64_t)R * p.ldb + ((tile * (ACT ? 16 * NH : 16 * NS)) >> p.bshift),
+                      __float_as_uint(mx));
+        } else if (ACT) {
 #pragma unroll
           for (int s = 0; s < NH; ++s)
             if (nok[s]) store_out<KIND, true>(p, g, R, ar, nw[s], nw[s], nw[s + NH], v[s], v[s + NH]);

@@ -9,7 +9,7 @@ import os
 
 _LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libqmoe.so")
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 QMOE_OK = 0
 STATUS_TEXT = {
@@ -68,6 +68,36 @@ class GemmDesc(ctypes.Structure):
     ]
 
 
+class DecodeDesc(ctypes.Structure):
+    """Mirror of `qmoe_moe_decode_desc` (field order and types must match)."""
+
+    _fields_ = [
+        ("x", _vp),
+        ("T", _i64),
+        ("H", _i64),
+        ("I", _i64),
+        ("I_shared", _i64),
+        ("E", _i32),
+        ("topk", _i32),
+        ("topk_ids", _vp),
+        ("topk_weights", _vp),
+        ("weights_f32", _i32),
+        ("routed_scale", _f32),
+        ("weight_blocks", _i32),
+        ("w1", _vp),
+        ("w2", _vp),
+        ("w1_scale", _vp),
+        ("w2_scale", _vp),
+        ("shared_w1", _vp),
+        ("shared_w2", _vp),
+        ("shared_w1_scale", _vp),
+        ("shared_w2_scale", _vp),
+        ("shared_gate", _vp),
+        ("out", _vp),
+        ("ldo", _i64),
+    ]
+
+
 def _load():
     if not os.path.exists(_LIB_PATH):
         raise ImportError(
@@ -108,6 +138,10 @@ def _load():
     lib.qmoe_moe_combine.restype = ctypes.c_int
     lib.qmoe_moe_combine.argtypes = [_vp, _vp, _vp, _i64, ctypes.c_int, ctypes.c_int, _i64, ctypes.c_int, _vp,
                                      _i64, _vp]
+    lib.qmoe_moe_decode_workspace_size.restype = ctypes.c_int
+    lib.qmoe_moe_decode_workspace_size.argtypes = [ctypes.POINTER(DecodeDesc), ctypes.POINTER(_i64)]
+    lib.qmoe_moe_decode.restype = ctypes.c_int
+    lib.qmoe_moe_decode.argtypes = [ctypes.POINTER(DecodeDesc), _vp, _i64, _vp]
     v = lib.qmoe_abi_version()
     if v != ABI_VERSION:
         raise ImportError(f"qmoe: libqmoe.so ABI {v} != expected {ABI_VERSION}; rebuild it")
@@ -129,6 +163,8 @@ EXPORTED = (
     "qmoe_moe_route_dispatch",
     "qmoe_moe_route_hash",
     "qmoe_moe_combine",
+    "qmoe_moe_decode_workspace_size",
+    "qmoe_moe_decode",
 )
 
 

@@ -45,6 +45,10 @@ _READERS = {
     "MOE_REQUANTIZE_WEIGHT_DTYPE": lambda: os.getenv("MOE_REQUANTIZE_WEIGHT_DTYPE"),
     # MoE: routes with a zero routing weight are padding and skipped
     "TPU_MOE_SKIP_PADDED_TOKENS": lambda: _bool("TPU_MOE_SKIP_PADDED_TOKENS"),
+    # MoE decode: serve armed layers' decode steps with the fused decode op
+    # (shared + routed experts), up to MAX_TOKENS tokens per step
+    "FUSED_MOE_DECODE_KERNEL": lambda: _bool("FUSED_MOE_DECODE_KERNEL"),
+    "FUSED_MOE_DECODE_KERNEL_MAX_TOKENS": lambda: int(os.getenv("FUSED_MOE_DECODE_KERNEL_MAX_TOKENS", "256")),
     # this build only (no reference counterpart): 128x128-block FP8 checkpoints
     # keep their tiles at run time with per-(token, 128) e4m3 activations
     # (the blockwise W8A8 recipe of BASELINE configs 2 and 4) instead of the

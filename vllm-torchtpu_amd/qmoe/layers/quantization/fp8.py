@@ -418,7 +418,18 @@ class Fp8MoEMethod:
         return w.to(torch.float32) * s
 
     def apply_monolithic(self, layer, x, router_logits, input_ids=None):
-        """`fp8.py:1108-1222` (single-GPU branch): route, then fused MoE."""
+        """`fp8.py:1108-1222` (single-GPU branch): route, then fused MoE; an
+        armed layer (`arm_fused_moe_decode`) returns shared + routed from the
+        fused decode op (`fp8.py:1203-1220`)."""
+        from qmoe.layers import fused_moe_decode as fmd
+
+        if fmd.fused_moe_decode_supported(self):
+            from qmoe.layers import moe_routing
+
+            # zero-weight (padding) routes add nothing to the op's sums, so
+            # TPU_MOE_SKIP_PADDED_TOKENS needs no mask here
+            topk_weights, topk_ids = moe_routing.route(layer, x, router_logits, input_ids=input_ids)
+            return fmd.fused_moe_decode(self, layer, x, topk_weights, topk_ids)
         return moe_forward(layer, x, router_logits, layer.w13_weight, layer.w2_weight, layer.w13_weight_scale,
                            layer.w2_weight_scale, None, None, layer._qmoe_format,
                            skip_padded_tokens=envs.TPU_MOE_SKIP_PADDED_TOKENS, input_ids=input_ids)

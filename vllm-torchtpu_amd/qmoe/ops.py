@@ -6,6 +6,7 @@ layouts on the host, and launches the HIP kernels on the current stream via
 """
 
 import ctypes
+import math
 import threading
 
 import torch
@@ -436,4 +437,95 @@ def moe_combine(rows, topk_ids, topk_weights, num_experts, skip_padded_tokens=Fa
     check(lib.qmoe_moe_combine(_ptr(rows), _ptr(ids), _ptr(wts), T, k, int(num_experts), H,
                                int(bool(skip_padded_tokens)), _ptr(out), out.stride(0),
                                _stream(rows.device)), "moe_combine")
+    return out
+
+
+# ---------------------------------------------------------------- fused decode MoE
+
+DECODE_MAX_TOKENS = 64
+
+
+def _f32c(t, shape, what):
+    """float32 contiguous scales of `shape` (unit axes may differ)."""
+    if t.numel() != math.prod(shape):
+        raise ValueError(f"{what}: expected {tuple(shape)} float32 scales, got {tuple(t.shape)}")
+    return t.float().reshape(shape).contiguous()
+
+
+def moe_decode(hidden, w1, w2, w1_scale, w2_scale, shared_w1, shared_w1_scale, shared_w2, shared_w2_scale,
+               shared_gate_weight, topk_weights, topk_ids, routed_scale=1.0, weight_blocks=None, out=None):
+    """Fused decode MoE layer -- shared expert + routed experts -> bf16 [T, H]
+    (`kernels/experimental/fused_moe_decode/fused_moe_decode_kernel.py:
+    552-740` on one rank; the numerics are stated at `qmoe_moe_decode` in
+    include/qmoe.h).
+
+    Layouts (N-major, the layout the MoE methods keep): ``w1`` e4m3 [E, 2I, H]
+    (gate rows then up rows), ``w2`` [E, H, I]; scales per channel ([E, 2I] /
+    [E, H], trailing unit axes allowed) or, with ``weight_blocks=128``,
+    128x128 tile scales ([E, 2I/128, H/128] / [E, H/128, I/128]). The shared
+    expert's tensors drop the E axis ([2 I_s, H], [H, I_s]); ``I_s <= I``.
+    ``shared_gate_weight``: [H] bf16 (any shape of H elements) or None for an
+    ungated shared expert. ``routed_scale`` multiplies the routed experts
+    only. 1..64 tokens."""
+    _require_gpu(hidden, w1, w2, topk_ids, topk_weights)
+    T, H = hidden.shape
+    E, N1, H1 = w1.shape
+    I = N1 // 2
+    Is = shared_w2.shape[1]
+    k = topk_ids.shape[1]
+    if not 1 <= T <= DECODE_MAX_TOKENS:
+        raise ValueError(f"moe_decode takes 1..{DECODE_MAX_TOKENS} tokens, got {T}")
+    if H1 != H or tuple(w2.shape) != (E, H, I) or tuple(shared_w1.shape) != (2 * Is, H) or \
+            tuple(shared_w2.shape) != (H, Is) or tuple(topk_weights.shape) != (T, k):
+        raise ValueError("moe_decode: inconsistent weight / routing shapes")
+    for t, name in ((w1, "w1"), (w2, "w2"), (shared_w1, "shared_w1"), (shared_w2, "shared_w2")):
+        if t.dtype != FP8 or not t.is_contiguous():
+            raise ValueError(f"moe_decode: {name} must be a contiguous float8_e4m3fn tensor")
+    tiles = bool(weight_blocks)
+    if tiles and weight_blocks != 128:
+        raise ValueError("moe_decode: weight_blocks must be None or 128")
+    if tiles:
+        s1 = _f32c(w1_scale, (E, N1 // 128, H // 128), "w1_scale")
+        s2 = _f32c(w2_scale, (E, H // 128, I // 128), "w2_scale")
+        ss1 = _f32c(shared_w1_scale, (2 * Is // 128, H // 128), "shared_w1_scale")
+        ss2 = _f32c(shared_w2_scale, (H // 128, Is // 128), "shared_w2_scale")
+    else:
+        s1 = _f32c(w1_scale, (E, N1), "w1_scale")
+        s2 = _f32c(w2_scale, (E, H), "w2_scale")
+        ss1 = _f32c(shared_w1_scale, (2 * Is,), "shared_w1_scale")
+        ss2 = _f32c(shared_w2_scale, (H,), "shared_w2_scale")
+    x = hidden.to(torch.bfloat16).contiguous()
+    if x.data_ptr() % 16:
+        x = x.clone()  # the kernel reads 16-byte chunks
+    ids = topk_ids.to(torch.int32).contiguous()
+    f32w = topk_weights.dtype == torch.float32
+    tw = topk_weights.contiguous() if f32w else topk_weights.to(torch.bfloat16).contiguous()
+    gate = None
+    if shared_gate_weight is not None:
+        if shared_gate_weight.numel() != H:
+            raise ValueError("moe_decode: shared_gate_weight must hold H values")
+        gate = shared_gate_weight.reshape(H).to(torch.bfloat16).contiguous()
+        if gate.data_ptr() % 16:
+            gate = gate.clone()
+    if out is None:
+        out = torch.empty((T, H), dtype=torch.bfloat16, device=hidden.device)
+    d = _capi.DecodeDesc()
+    d.x = _ptr(x).value
+    d.T, d.H, d.I, d.I_shared, d.E, d.topk = T, H, I, Is, E, k
+    d.topk_ids = _ptr(ids).value
+    d.topk_weights = _ptr(tw).value
+    d.weights_f32 = int(f32w)
+    d.routed_scale = float(routed_scale)
+    d.weight_blocks = 128 if tiles else 0
+    d.w1, d.w2 = _ptr(w1).value, _ptr(w2).value
+    d.w1_scale, d.w2_scale = _ptr(s1).value, _ptr(s2).value
+    d.shared_w1, d.shared_w2 = _ptr(shared_w1).value, _ptr(shared_w2).value
+    d.shared_w1_scale, d.shared_w2_scale = _ptr(ss1).value, _ptr(ss2).value
+    d.shared_gate = _ptr(gate).value if gate is not None else None
+    d.out = _ptr(out).value
+    d.ldo = out.stride(0)
+    nbytes = ctypes.c_int64(0)
+    check(lib.qmoe_moe_decode_workspace_size(ctypes.byref(d), ctypes.byref(nbytes)), "moe_decode (shape)")
+    ws, ws_n = _workspace(hidden.device, nbytes.value)
+    check(lib.qmoe_moe_decode(ctypes.byref(d), _ptr(ws), ws_n, _stream(hidden.device)), "moe_decode")
     return out
