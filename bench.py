@@ -47,11 +47,14 @@ def parse():
     ap.add_argument("--m", type=int, default=4096, help="tokens of the headline step")
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="", help="comma list of sweep configs to run (0-4; 5 = NVFP4 / INT4)")
+    ap.add_argument("--only", default="", help="comma list of sweep configs to run (0-4; 5 = NVFP4 / INT4; "
+                                                "v = hipBLASLt reference points)")
     ap.add_argument("--profile", nargs="?", const="headline", default=None,
-                    choices=["headline", "decode", "moe"],
+                    choices=["headline", "decode", "moe", "vendor", "floor"],
                     help="rocprofv3 targets: the headline kernel + a copy calibration (default), "
-                         "the decode GEMMs (cfg 0/1/2 at M=1), or the MoE layers at T=1 (cfg 3/4)")
+                         "the decode GEMMs (cfg 0/1/2 at M=1), the MoE layers at T=1 (cfg 3/4), "
+                         "this build's FP8 GEMM beside hipBLASLt's (torch._scaled_mm) on both cfg 1 "
+                         "shapes at M=4096, or the plain-read floor (time vs size)")
     return ap.parse_args()
 
 
@@ -180,14 +183,22 @@ def headline(args):
     gemm = lambda: ops.gemm(_capi.W8A8_PC, xqu, wu, a_scale=xs, w_scale=s_up)  # noqa: E731
     k_us, _, _ = event_time_us(gemm, iters=max(10, args.steps))
     k_flops = 2.0 * M * 4096 * 14336
-    k_bytes = 14336 * 4096 + 14336 * 4 + M * 4096 + 4 * M + 2 * M * 14336
+    # weight codes + per-channel scales + bf16 x + bf16 y (the activation
+    # quantization is not counted as algorithmic traffic)
+    k_bytes = 14336 * 4096 + 14336 * 4 + 2 * M * 4096 + 2 * M * 14336
     return dict(dt=dt, flops=flops, k_us=k_us, k_flops=k_flops, k_bytes=k_bytes)
 
 
 # ------------------------------------------------------------------ sweep
 
 
+FLOOR = []  # plain-read floor curve of this run (read_floor), when measured
+
+
 def roof(flops, nbytes, us, peak_key):
+    """Throughput of one point against its bound. HBM-bound points also carry
+    `floor_frac`: the plain read of the same bytes (this run's floor curve,
+    launch included) over the point's time."""
     t = us * 1e-6
     tf = flops / t / 1e12
     gbs = nbytes / t / 1e9
@@ -195,8 +206,11 @@ def roof(flops, nbytes, us, peak_key):
     t_mfma = flops / PEAK[peak_key]
     bound = "hbm" if t_mem >= t_mfma else "mfma"
     frac = (t_mem if bound == "hbm" else t_mfma) / t
-    return dict(us=round(us, 2), tflops=round(tf, 2), gbs=round(gbs, 1), bound=bound,
-                roofline_frac=round(frac, 3), t_roof_us=round(max(t_mem, t_mfma) * 1e6, 2))
+    r = dict(us=round(us, 2), tflops=round(tf, 2), gbs=round(gbs, 1), bound=bound,
+             roofline_frac=round(frac, 3), t_roof_us=round(max(t_mem, t_mfma) * 1e6, 2))
+    if bound == "hbm" and FLOOR:
+        r["floor_frac"] = round(floor_us(FLOOR, nbytes) / us, 3)
+    return r
 
 
 def sweep_linear(only):
@@ -210,12 +224,15 @@ def sweep_linear(only):
     if not only or "0" in only:
         K, N = 2880, 5760
         codes, sc = mxfp4_weights((N, K), gen)
+        host = (codes.cpu().numpy(), sc.cpu().numpy()) if PAR.on else None
         for M in (1, 16, 128):
             x = torch.randn((M, K), device="cuda", generator=gen).to(torch.bfloat16)
             us = graph_time_us(lambda: quantized_matmul_fp4(x, codes, sc))[0]
             nbytes = N * K // 2 + N * K // 32 + 2 * M * K + 2 * M * N
+            par = PAR.linear(quantized_matmul_fp4(x, codes, sc), x, M,
+                             lambda xr: oracle_mod("linear").w4a16_mxfp4(xr, *host)) if PAR.on else {}
             out.append(dict(cfg=0, kind="mxfp4_w4a16", M=M, K=K, N=N,
-                            **roof(2.0 * M * N * K, nbytes, us, "bf16")))
+                            **roof(2.0 * M * N * K, nbytes, us, "bf16"), **par))
             log(out[-1])
     if not only or "1" in only:
         for qd in ("fp8", "int8"):
@@ -223,23 +240,36 @@ def sweep_linear(only):
                 w = torch.randn((N, K), device="cuda", generator=gen) * 0.02
                 q, s = ops.row_quant(w, qd, mode="load")
                 del w
+                if PAR.on:
+                    wq_h, ws_h = q.view(torch.uint8).cpu().numpy(), s.cpu().numpy()
+                    if qd == "int8":
+                        wq_h = wq_h.view(np.int8)
                 for M in (1, 8, 64, 512, 4096):
                     x = torch.randn((M, K), device="cuda", generator=gen).to(torch.bfloat16)
                     us = graph_time_us(lambda: quantized_matmul(x, q.t(), s), iters=30)[0]
                     nbytes = N * K + 4 * N + 2 * M * K + 2 * M * N
+                    par = PAR.linear(quantized_matmul(x, q.t(), s), x, M,
+                                     lambda xr: oracle_mod("linear").w8a8_per_channel(xr, wq_h, ws_h, qd)[0],
+                                     exact=qd == "int8") if PAR.on else {}
                     out.append(dict(cfg=1, kind=f"{qd}_w8a8_pc", M=M, K=K, N=N,
-                                    **roof(2.0 * M * N * K, nbytes, us, qd)))
+                                    **roof(2.0 * M * N * K, nbytes, us, qd), **par))
                     log(out[-1])
     if not only or "2" in only:
         K = 7168
         for N in (18432, 24576):
             q, s = fp8_weights(N, K, gen, tiles=True)
+            if PAR.on:
+                wq_h = q.view(torch.uint8).cpu().numpy()
+                wsb_h = oracle_mod("linear").tile_scales_to_blocks(s.cpu().numpy(), N)
             for M in (1, 32, 256, 2048, 8192):
                 x = torch.randn((M, K), device="cuda", generator=gen).to(torch.bfloat16)
                 us = graph_time_us(lambda: quantized_matmul(x, q.t(), s), iters=20)[0]
                 nbytes = N * K + 4 * (N // 128) * (K // 128) + 2 * M * K + 2 * M * N
+                par = PAR.linear(quantized_matmul(x, q.t(), s), x, M,
+                                 lambda xr: oracle_mod("linear").w8a8_blockwise(xr, wq_h, wsb_h)[0],
+                                 n=2) if PAR.on else {}
                 out.append(dict(cfg=2, kind="fp8_w8a8_blk128", M=M, K=K, N=N,
-                                **roof(2.0 * M * N * K, nbytes, us, "fp8")))
+                                **roof(2.0 * M * N * K, nbytes, us, "fp8"), **par))
                 log(out[-1])
     return out
 
@@ -375,11 +405,19 @@ def sweep_moe(only):
                 return moe_forward(lcfg, x, logits, w13, w2, s13, s2, None, None, "mxfp4")
 
             us = graph_time_us(layer, iters=20)[0]
-            _, ids = ops.moe_route(logits, k, "softmax", True)
+            tw, ids = ops.moe_route(logits, k, "softmax", True)
             touched = int(torch.unique(ids).numel())
             nbytes = touched * per_expert + 2 * T * H * 2 + 2 * T * E
+            par = {}
+            if PAR.on:
+                omoe, orouting = oracle_mod("moe"), oracle_mod("routing")
+                _, ids_ref = orouting.select_experts(PAR._np(logits), k, True, "softmax")
+                ew = omoe.ExpertWeights("mxfp4", _DevRows(w13), _DevRows(s13), _DevRows(w2), _DevRows(s2), keep=False)
+                par = PAR.moe(layer(), T, lambda tk: omoe.fused_moe_tokens(
+                    PAR._np(x[tk]), ew, PAR._np(tw[tk]), ids_ref[tk], "swigluoai", E),
+                    np.array_equal(ids.cpu().numpy(), ids_ref))
             out.append(dict(cfg=3, kind="moe_mxfp4_gptoss", T=T, experts_touched=touched,
-                            **roof(T * k * 6.0 * H * I, nbytes, us, "bf16")))
+                            **roof(T * k * 6.0 * H * I, nbytes, us, "bf16"), **par))
             log(out[-1])
         del w13, s13, w2, s2
         torch.cuda.empty_cache()
@@ -431,13 +469,80 @@ def sweep_moe(only):
                     return routed_part() + shared()
 
                 us = graph_time_us(full, iters=15)[0]
-                _, ids = ops.moe_route(logits, k, "sigmoid", True, bias=bias, routed_scaling_factor=2.5,
-                                       num_expert_group=8, topk_group=4)
+                tw, ids = ops.moe_route(logits, k, "sigmoid", True, bias=bias, routed_scaling_factor=2.5,
+                                        num_expert_group=8, topk_group=4)
                 touched = int(torch.unique(ids).numel()) + 1
                 nbytes = touched * per_expert + 2 * T * H * 2 + 2 * T * E
+                par, ids_ok = {}, None
+                if PAR.on:
+                    omoe, orouting = oracle_mod("moe"), oracle_mod("routing")
+                    _, ids_ref = orouting.grouped_topk(PAR._np(logits), k, True, 8, 4, "sigmoid", PAR._np(bias), 2.5)
+                    ids_ok = np.array_equal(ids.cpu().numpy(), ids_ref)
+                    # routed part only (the shared expert's GEMMs are
+                    # checked at these shapes by the parity tests)
+                    ew = omoe.ExpertWeights("fp8_block", _DevRows(w13.view(torch.uint8)), _DevRows(s13),
+                                            _DevRows(w2.view(torch.uint8)), _DevRows(s2), keep=False)
+                    par = PAR.moe(routed_part(), T, lambda tk: omoe.fused_moe_tokens(
+                        PAR._np(x[tk]), ew, PAR._np(tw[tk]), ids_ref[tk], "silu", E), ids_ok, n=1)
                 out.append(dict(cfg=4, kind="moe_fp8blk_dsv3" + ("_skewed" if skew else ""), T=T,
-                                experts_touched=touched, **roof(T * (k + 1) * 6.0 * H * I, nbytes, us, "fp8")))
+                                experts_touched=touched, **roof(T * (k + 1) * 6.0 * H * I, nbytes, us, "fp8"),
+                                **par))
                 log(out[-1])
+                if T > ops.DECODE_MAX_TOKENS:
+                    continue
+
+                def decode_layer():
+                    # the fused decode op (shared + routed experts): routing
+                    # launch, then the op; routed_scaling_factor moves into it
+                    tw, ti = ops.moe_route(logits, k, "sigmoid", True, bias=bias, routed_scaling_factor=1.0,
+                                           num_expert_group=8, topk_group=4)
+                    return ops.moe_decode(x, w13, w2, s13, s2, sh13, ss13, sh2, ss2, None, tw, ti,
+                                          routed_scale=2.5, weight_blocks=128)
+
+                us = graph_time_us(decode_layer, iters=15)[0]
+                par = {}
+                if PAR.on:
+                    odec = oracle_mod("decode")
+                    tw1, ti1 = ops.moe_route(logits, k, "sigmoid", True, bias=bias, routed_scaling_factor=1.0,
+                                             num_expert_group=8, topk_group=4)
+                    sh = tuple(PAR._np(t.view(torch.uint8) if t.dtype == torch.float8_e4m3fn else t)
+                               for t in (sh13, ss13, sh2, ss2))
+                    par = PAR.moe(decode_layer(), T, lambda tk: odec.fused_moe_decode(
+                        PAR._np(x[tk]), _DevRows(w13.view(torch.uint8)), _DevRows(s13), _DevRows(w2.view(torch.uint8)),
+                        _DevRows(s2), *sh, None, PAR._np(tw1[tk]), PAR._np(ti1[tk]), routed_scale=2.5,
+                        weight_blocks=128), ids_ok, n=1)
+                out.append(dict(cfg=4, kind="moe_fp8blk_dsv3_decode_op" + ("_skewed" if skew else ""), T=T,
+                                experts_touched=touched, **roof(T * (k + 1) * 6.0 * H * I, nbytes, us, "fp8"),
+                                **par))
+                log(out[-1])
+    return out
+
+
+def sweep_vendor():
+    """Vendor reference points on the same box: hipBLASLt's FP8 GEMM
+    (torch._scaled_mm) on the cfg 1 shapes at M 512 and 4096, same codes as
+    this build's tiled GEMM, GEMM alone (no activation quantization), beside
+    this build's GEMM alone."""
+    import torch
+
+    from qmoe import _capi, ops
+
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    out = []
+    for K, N in ((4096, 14336), (14336, 4096)):
+        w, s = fp8_weights(N, K, gen)
+        for M in (512, 4096):
+            x = torch.randn((M, K), device="cuda", generator=gen).to(torch.bfloat16)
+            xq, xs = ops.row_quant(x, "fp8")
+            ours = lambda: ops.gemm(_capi.W8A8_PC, xq.view(torch.uint8), w.view(torch.uint8),  # noqa: E731
+                                    a_scale=xs, w_scale=s)
+            vend, scaling = vendor_scaled_mm(xq, w, xs, s)
+            nbytes = N * K + 4 * N + 2 * M * K + 2 * M * N
+            for name, fn in (("qmoe_gemm_fp8_pc", ours), (f"hipblaslt_scaled_mm_{scaling.split()[0]}", vend)):
+                us = graph_time_us(fn, iters=30)[0]
+                out.append(dict(cfg=1, kind=name, M=M, K=K, N=N, **roof(2.0 * M * N * K, nbytes, us, "fp8")))
+                log(out[-1])
+        del w, s
     return out
 
 
@@ -461,31 +566,149 @@ def profiled_traffic(m):
     return int(rd + wr)
 
 
+# ------------------------------------------------------------------ CPU leg: per-point parity
+
+
+class ParityLeg:
+    """Per-point parity and CPU time, part of the CPU-baseline leg (the oracle
+    is the checker here, never the thing timed on the GPU). For each sweep
+    point a few output rows (tokens) are recomputed by the CPU oracle from
+    the same device inputs:
+
+    * `parity`: rows checked, max |err| / row max, cosine, and `pass` for the
+      north-star bar (max |err| <= 2e-2 * row max, cosine >= 0.9995); INT8
+      GEMMs also carry `exact` (integer accumulation is bit-exact); MoE points
+      carry `ids_exact` (every token's routing ids against the oracle's);
+    * `cpu_ms_est`: the oracle's time for the whole point, from its times on
+      n and 2n sampled rows (fixed part + per-row part, linear in rows), or
+      for MoE points the per-token time times T (the oracle loops over
+      tokens); `cpu_ms_sample` is the measured time of the larger sample.
+
+    Disabled (empty dicts) with --no-cpu."""
+
+    def __init__(self, on):
+        self.on = on
+        self.threads = None
+        if on:
+            sys.path.insert(0, ROOT)
+
+    @staticmethod
+    def _np(t):
+        return t.detach().float().cpu().numpy() if t.dtype in (_torch().bfloat16, _torch().float16) \
+            else t.detach().cpu().numpy()
+
+    @staticmethod
+    def _rows(M, n):
+        if M <= n:
+            return np.arange(M)
+        return np.unique(np.linspace(0, M - 1, n).round().astype(np.int64))
+
+    @staticmethod
+    def _stats(got, ref):
+        got = np.asarray(got, np.float64).reshape(-1, np.asarray(got).shape[-1])
+        ref = np.asarray(ref, np.float64).reshape(got.shape)
+        err = np.abs(got - ref).max(axis=-1) / np.maximum(np.abs(ref).max(axis=-1), 1e-30)
+        den = np.linalg.norm(got) * np.linalg.norm(ref)
+        cos = float((got * ref).sum() / den) if den > 0 else 1.0
+        ok = bool(np.isfinite(got).all() and err.max() <= 2e-2 and cos >= 0.9995)
+        return dict(rows=int(got.shape[0]), max_err_rowmax=float(f"{err.max():.3g}"), cos=round(cos, 7), ok=ok)
+
+    def linear(self, y, x, M, oracle_fn, n=4, exact=False):
+        """oracle_fn(x_rows_f32) -> reference rows; y the device output."""
+        if not self.on:
+            return {}
+        r1, r2 = self._rows(M, n), self._rows(M, 2 * n)
+        t0 = time.perf_counter()
+        oracle_fn(self._np(x[r1]))
+        t1 = time.perf_counter()
+        ref = oracle_fn(self._np(x[r2]))
+        t2 = time.perf_counter()
+        got = self._np(y[r2])
+        st = self._stats(got, ref)
+        if exact:
+            st["exact"] = bool(np.array_equal(got, ref))
+        ta, tb = t1 - t0, t2 - t1
+        per_row = max(tb - ta, 0.0) / max(len(r2) - len(r1), 1)
+        est = max(ta - len(r1) * per_row, 0.0) + M * per_row if len(r2) > len(r1) else tb
+        return dict(parity=st, cpu_ms_sample=round(tb * 1e3, 1), cpu_ms_est=round(est * 1e3, 1))
+
+    def moe(self, y, T, oracle_tokens, ids_exact, n=2):
+        """oracle_tokens(token_idx) -> reference rows for those tokens."""
+        if not self.on:
+            return {}
+        toks = self._rows(T, n)
+        t0 = time.perf_counter()
+        ref = oracle_tokens(toks)
+        dt = time.perf_counter() - t0
+        st = self._stats(self._np(y[toks]), ref)
+        st["ids_exact"] = bool(ids_exact)
+        return dict(parity=st, cpu_ms_sample=round(dt * 1e3, 1), cpu_ms_est=round(dt / len(toks) * T * 1e3, 1))
+
+
+def _torch():
+    import torch
+
+    return torch
+
+
+PAR = ParityLeg(False)
+
+
+def oracle_mod(name):
+    """An oracle module (the CPU leg's checker)."""
+    import importlib
+
+    if ROOT not in sys.path:
+        sys.path.insert(0, ROOT)
+    return importlib.import_module(f"oracle.{name}")
+
+
+class _DevRows:
+    """[E, ...] device tensor read one expert at a time (the oracle indexes
+    w[e])."""
+
+    def __init__(self, t):
+        self.t, self.shape = t, tuple(t.shape)
+
+    def __getitem__(self, e):
+        return self.t[int(e)].cpu().numpy()
+
+
 # ------------------------------------------------------------------ CPU baseline
 
 
 def cpu_baseline():
     """The CPU oracle on a bounded sample of the headline workload: FP8 W8A8
     per-channel, K=4096, N=14336, M=256 (dynamic per-token quant + fp32
-    dequantize-then-matmul), repeated for about 10-20 s."""
+    dequantize-then-matmul), at least 5 repetitions and up to about 10 s;
+    the median repetition gives `value`. `cores` is the BLAS thread count
+    numpy ran with (threadpoolctl), beside os.cpu_count() and
+    torch.get_num_threads()."""
+    import torch
+
     sys.path.insert(0, ROOT)
     from oracle import codecs, linear, quant
 
-    threads = os.cpu_count() or 1
     rng = np.random.default_rng(0)
     K, N, M = 4096, 14336, 256
     w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
     wq, ws = quant.quantize_tensor(w, "fp8")
     x = codecs.bf16_round(rng.standard_normal((M, K)).astype(np.float32))
     linear.w8a8_per_channel(x, wq, ws, "fp8")  # warm-up
-    reps, t0 = 0, time.perf_counter()
-    while True:
+    times, t_start = [], time.perf_counter()
+    while len(times) < 5 or (time.perf_counter() - t_start < 10.0 and len(times) < 60):
+        t0 = time.perf_counter()
         linear.w8a8_per_channel(x, wq, ws, "fp8")
-        reps += 1
-        el = time.perf_counter() - t0
-        if el > 10.0 or reps >= 30:
-            break
-    dt = el / reps
+        times.append(time.perf_counter() - t0)
+    dt = float(np.median(times))
+    blas_threads = None
+    try:
+        from threadpoolctl import threadpool_info
+
+        blas = [i["num_threads"] for i in threadpool_info() if i.get("user_api") == "blas"]
+        blas_threads = max(blas) if blas else None
+    except Exception:  # threadpoolctl absent or unreadable: report os.cpu_count()
+        blas_threads = None
     cpu_model = ""
     try:
         for line in open("/proc/cpuinfo"):
@@ -494,9 +717,12 @@ def cpu_baseline():
                 break
     except OSError:
         pass
-    return dict(value=round(2.0 * M * N * K / dt / 1e12, 4), unit="TFLOP/s", cores=threads,
-                kind="port", sample=f"fp8 w8a8 per-channel M={M} K={K} N={N}, {reps} reps, "
-                f"{dt * 1e3:.1f} ms each, numpy fp32 BLAS, {cpu_model}")
+    cores = blas_threads or os.cpu_count() or 1
+    return dict(value=round(2.0 * M * N * K / dt / 1e12, 4), unit="TFLOP/s", cores=cores,
+                kind="port", sample=f"fp8 w8a8 per-channel M={M} K={K} N={N}: median of {len(times)} reps, "
+                f"{dt * 1e3:.1f} ms each (p10 {np.percentile(times, 10) * 1e3:.1f}, p90 "
+                f"{np.percentile(times, 90) * 1e3:.1f}), numpy fp32 BLAS with {cores} threads; "
+                f"os.cpu_count() {os.cpu_count()}, torch.get_num_threads() {torch.get_num_threads()}; {cpu_model}")
 
 
 def profile_target(args):
@@ -584,10 +810,109 @@ def profile_moe(args):
     log("profile target done: cfg3 / cfg4 MoE T=1 x23 each")
 
 
+def vendor_scaled_mm(xq, wq, xs, ws):
+    """hipBLASLt's FP8 GEMM through torch._scaled_mm on the same codes: row-wise
+    scales ([M,1] x [1,N]) when this torch build takes them, else unit tensor
+    scales. Returns (callable, scaling)."""
+    import torch
+
+    b = wq.t()  # [K, N] column-major view of the N-major weight
+    out = torch.empty((xq.shape[0], wq.shape[0]), dtype=torch.bfloat16, device=xq.device)
+    try:
+        sa, sb = xs.reshape(-1, 1).float().contiguous(), ws.reshape(1, -1).float().contiguous()
+        torch._scaled_mm(xq, b, sa, sb, out_dtype=torch.bfloat16)
+        torch.cuda.synchronize()
+        return (lambda: torch._scaled_mm(xq, b, sa, sb, out_dtype=torch.bfloat16)), "rowwise"
+    except (RuntimeError, ValueError):
+        one = torch.ones((), dtype=torch.float32, device=xq.device)
+        torch._scaled_mm(xq, b, one, one, out_dtype=torch.bfloat16)
+        torch.cuda.synchronize()
+        return (lambda: torch._scaled_mm(xq, b, one, one, out_dtype=torch.bfloat16)), "tensorwise (unit)"
+    finally:
+        del out
+
+
+def profile_vendor(args):
+    """rocprofv3 target: 10 launches each of this build's tiled FP8 GEMM and
+    of hipBLASLt's FP8 GEMM (torch._scaled_mm) on the two cfg 1 shapes at
+    M=args.m (up K4096 N14336, down K14336 N4096), same codes, after 3
+    warm-up calls; then a plain 256 MiB copy (10 launches) for the
+    FETCH_SIZE / WRITE_SIZE calibration."""
+    import torch
+
+    from qmoe import _capi, ops
+
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    M = args.m
+    for K, N in ((4096, 14336), (14336, 4096)):
+        w, s = fp8_weights(N, K, gen)
+        x = torch.randn((M, K), device="cuda", generator=gen).to(torch.bfloat16)
+        xq, xs = ops.row_quant(x, "fp8")
+        ours = lambda: ops.gemm(_capi.W8A8_PC, xq.view(torch.uint8), w.view(torch.uint8),  # noqa: E731
+                                a_scale=xs, w_scale=s)
+        vend, scaling = vendor_scaled_mm(xq, w, xs, s)
+        for fn in (ours, vend):
+            for _ in range(13):
+                fn()
+            torch.cuda.synchronize()
+        log(f"profile target: K={K} N={N} M={M}: qmoe tiled FP8 x13, torch._scaled_mm ({scaling}) x13")
+    src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log("profile target done: copy 256MiB x10")
+
+
+FLOOR_MB = (1, 2, 4, 8.8, 16, 32, 58.7, 128, 176, 352, 1024)
+
+
+def read_floor():
+    """Plain-read floor: `qmoe_stream_read` over buffers of FLOOR_MB
+    megabytes, each timed like the sweep points (graph replays, so the
+    launch gap inside a graph is included). Returns [{mb, us, gbs}]."""
+    import torch
+
+    from qmoe import ops
+
+    big = torch.empty(int(max(FLOOR_MB) * 1e6) // 16 * 16, dtype=torch.uint8, device="cuda")
+    big.random_(0, 255)
+    sink = torch.empty(2048, dtype=torch.int32, device="cuda")
+    out = []
+    for mb in FLOOR_MB:
+        n = int(mb * 1e6) // 16 * 16
+        view = big[:n]
+        us = graph_time_us(lambda: ops.stream_read(view, sink=sink), iters=30)[0]
+        out.append(dict(mb=mb, us=round(us, 2), gbs=round(n / us / 1e3, 1)))
+        log("read floor", out[-1])
+    del big
+    return out
+
+
+def floor_us(floor, nbytes):
+    """Plain-read time of `nbytes` interpolated (linear in bytes) on the
+    measured floor curve."""
+    pts = [(p["mb"] * 1e6, p["us"]) for p in floor]
+    if nbytes <= pts[0][0]:
+        return pts[0][1]
+    for (b0, t0), (b1, t1) in zip(pts, pts[1:]):
+        if nbytes <= b1:
+            return t0 + (t1 - t0) * (nbytes - b0) / (b1 - b0)
+    (b0, t0), (b1, t1) = pts[-2], pts[-1]
+    return t1 + (t1 - t0) * (nbytes - b1) / (b1 - b0)
+
+
+def profile_floor(args):
+    """rocprofv3 target: the plain-read floor curve (qmoe_stream_read over
+    FLOOR_MB sizes), printed as one JSON line."""
+    print(json.dumps({"read_floor": read_floor()}))
+
+
 def main():
     args = parse()
     if args.profile:
-        {"headline": profile_target, "decode": profile_decode, "moe": profile_moe}[args.profile](args)
+        {"headline": profile_target, "decode": profile_decode, "moe": profile_moe, "vendor": profile_vendor,
+         "floor": profile_floor}[args.profile](args)
         return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (got --gpus {args.gpus}); "
@@ -624,8 +949,13 @@ def main():
                      "algorithmic_bytes": h["k_bytes"]},
     }
     only = [c for c in args.only.split(",") if c]
+    PAR.on = not args.no_cpu
     if not args.no_sweep:
+        FLOOR.extend(read_floor())
+        res["read_floor"] = FLOOR
         res["sweep"] = sweep_linear(only) + sweep_moe(only) + sweep_nvfp4(only)
+        if not only or "v" in only:
+            res["sweep"] += sweep_vendor()
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline()
     print(json.dumps(res))

@@ -309,6 +309,15 @@ int qmoe_moe_decode_workspace_size(const qmoe_moe_decode_desc* d, int64_t* bytes
  * QMOE_ERR_WORKSPACE when ws_bytes is below qmoe_moe_decode_workspace_size. */
 int qmoe_moe_decode(const qmoe_moe_decode_desc* d, void* workspace, int64_t ws_bytes, qmoe_stream_t stream);
 
+/*
+ * Plain read of `bytes` (a multiple of 16, 16-byte aligned) at `src` by at
+ * most `workgroups` 256-thread workgroups; `sink` receives at most one dword
+ * per workgroup ([workgroups] uint32, normally untouched). No counterpart in
+ * the reference: a measurement helper giving the HBM read floor (time vs
+ * size, launch included) that the weight-streaming GEMMs are compared with.
+ */
+int qmoe_stream_read(const void* src, int64_t bytes, int32_t workgroups, void* sink, qmoe_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -48,7 +48,7 @@ using namespace qmoe_stream;
 // cache-policy bits of the weight stream's loads (read once per launch)
 constexpr int kWeightAux = 0;
 
-constexpr int kWaves = 4;  // wavefronts of the split-K finishing kernel
+constexpr int kWaves = 4;  // wavefronts per workgroup (streaming and split-K finishing kernels)
 constexpr int kThreads = kWaves * 64;
 
 template <int KIND, int WF>
@@ -80,10 +80,11 @@ struct Traits {
   }
 };
 
-// 128-k steps per pipeline chunk (two chunks are in flight per wavefront);
-// measured on MI355X: one step (deeper chunks add clamped duplicate loads
-// at the end of the short per-wavefront K slices and lose 5-30%)
-int default_unroll() { return 1; }
+// 128-k steps per pipeline chunk (two chunks are in flight per wavefront):
+// one. Measured on MI355X: deeper chunks (2 or 4 steps) add clamped duplicate
+// loads at the end of the short per-wavefront K slices and lose 5-30%, so
+// only the one-step form is instantiated.
+constexpr int kUnroll = 1;
 
 // activation chunks of one step at the offsets of Traits::a_off
 template <typename Tr>
@@ -362,7 +363,9 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p)
     woff[s] = (uint32_t)(row_of(s, lane >> 2) * p.ldw + (lane & 3) * 16);
   }
   const int perm_src = (4 * col + kg) * 4;
-  // scale streams: e8m0 bytes [N][K/32] (W4A16_MX, staged below), bf16
+  // scale streams: e8m0 bytes [N][K/32] (W4A16_MX: one byte per lane, tile
+  // and step, for the lane's row and 32 k, loaded with the step's weights;
+  // measured on MI355X, faster than staging the rows in LDS first), bf16
   // [N][K/16] (W4A16_NV: one 4-byte pair per lane and step, for the lane's
   // row and 32 k), per-step f32 [N/bn][K/128] weight blocks and [rows][K/128]
   // activation blocks (W8A8_BLK)
@@ -370,6 +373,8 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p)
   uint32_t soffw[NS];
   if constexpr (KIND == QK_W4A16_MX) {
     sres = make_rsrc(group_slice(p, static_cast<const uint8_t*>(p.w_scale), p.ws_x, p.ws_gstride, g), (int64_t)NG * p.ldws);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) soffw[s] = (uint32_t)(nclamp[s] * p.ldws + kg);
   } else if constexpr (KIND == QK_W4A16_NV) {
     sres = make_rsrc(group_slice(p, static_cast<const uint16_t*>(p.w_scale), p.ws_x, p.ws_gstride, g),
                      (int64_t)NG * p.ldws * 2);
@@ -392,40 +397,18 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p)
   // weight's; 31 for one scale per row)
   const int a_kshift = p.a_kshift, w_kshift = p.w_kshift;
   const uint32_t i4_step = KIND == QK_W4A16_I4 ? (uint32_t)(256 / p.wq_group) : 0u;  // INT4 scale bytes per step
-  // e2m1: the workgroup's NS*16 scale rows (K/32 bytes each; the host keeps
-  // K <= 16384) are staged in LDS once, so the K loop reads a step's byte
-  // from LDS instead of issuing a scattered byte load per tile per step
-  constexpr int kMaxEB = 512;
-  __shared__ uint8_t s_eb[KIND == QK_W4A16_MX ? NS * 16 * kMaxEB : 1];
-  const int KB32 = p.K >> 5;
-  auto stage_scales = [&]() {  // 16 byte loads in flight per thread per batch
-    const int total = NS * 16 * KB32;
-    for (int b0 = 0; b0 < total; b0 += 16 * NT) {
-      uint32_t v[16];
-#pragma unroll
-      for (int u = 0; u < 16; ++u) {
-        const int idx = min(b0 + u * NT + (int)threadIdx.x, total - 1);
-        const int rr = idx / KB32, b = idx - rr * KB32;
-        v[u] = __builtin_amdgcn_raw_buffer_load_b8(sres, (uint32_t)(row_of(rr >> 4, rr & 15) * p.ldws + b), 0, 0);
-      }
-#pragma unroll
-      for (int u = 0; u < 16; ++u) {
-        const int idx = b0 + u * NT + (int)threadIdx.x;
-        if (idx < total) s_eb[idx] = (uint8_t)v[u];
-      }
-    }
-  };
-
   // K steps: KSF full 128-wide steps, plus a tail step when K % 128 != 0
   const int KSF = p.K >> 7;
   const bool tail = (p.K & 127) != 0;
   const int KS = KSF + (tail ? 1 : 0);
   // this wavefront's full steps are sbase + j, j < nj (a contiguous run of
   // the workgroup's K slice); the wavefront whose run ends at K takes the tail
+  // (q or q + 1 steps per slice: the first KS % nsl slices take one more)
   const int nsl = p.ksplit * W;
   const int sl = blockIdx.y * W + wave;
-  const int sbase = (int)((int64_t)KS * sl / nsl);
-  const int send = (int)((int64_t)KS * (sl + 1) / nsl);
+  const int q = (int)((uint32_t)KS / (uint32_t)nsl), rem = KS - q * nsl;
+  const int sbase = sl * q + min(sl, rem);
+  const int send = sbase + q + (sl < rem ? 1 : 0);
   const int nj = max(0, min(send, KSF) - sbase);
   const bool tail_mine = tail && send == KS && sbase < send;
 
@@ -480,8 +463,10 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p)
 #pragma unroll
         for (int s = 0; s < NS; ++s) sc.sb[s] = ldb_f32(sres, soffw[s] | oob, (uint32_t)(ks >> w_kshift) * 4);
       } else if constexpr (KIND == QK_W4A16_MX) {
+        const uint32_t oob = live ? 0u : kOob;
 #pragma unroll
-        for (int s = 0; s < NS; ++s) sc.eb[s] = s_eb[(s * 16 + col) * KB32 + ks * 4 + kg];
+        for (int s = 0; s < NS; ++s)
+          sc.eb[s] = __builtin_amdgcn_raw_buffer_load_b8(sres, soffw[s] | oob, (uint32_t)ks * 4, 0);
       } else if constexpr (KIND == QK_W4A16_NV) {
         const uint32_t oob = live ? 0u : kOob;
 #pragma unroll
@@ -544,11 +529,6 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p)
     Chunk ca, cb;
     const bool run = nj > 0;
     if (run) issue_mem(0, ca);
-    if (KIND == QK_W4A16_MX && mp == 0) {
-      // the scale rows are staged while the first chunk is in flight
-      stage_scales();
-      __syncthreads();
-    }
     if (run) {
       issue_sc(0, ca);
       for (int j = 0; j < nj; j += 2 * U) {
@@ -598,7 +578,7 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p)
         const bool ok = kg * 32 < t;
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
-          const uint32_t b = s_eb[(s * 16 + col) * KB32 + kk * 4 + (ok ? kg : 0)];
+          const uint32_t b = __builtin_amdgcn_raw_buffer_load_b8(sres, ok ? soffw[s] : kOob, (uint32_t)kk * 4, 0);
           sc.eb[s] = ok ? b : 127u;
         }
       } else if constexpr (KIND == QK_W4A16_NV) {
@@ -749,23 +729,10 @@ __global__ __launch_bounds__(kThreads) void skinny_reduce_kernel(const GemmParam
   }
 }
 
-template <int KIND, int WF, int MS, bool ACT, int NS, int W>
-void launch_skinny_w(const GemmParams& p, dim3 grid, hipStream_t st) {
-  const char* env_s = getenv("QMOE_SKINNY_U");  // tuning knob: 1, 2 or 4
-  const int env_u = env_s ? atoi(env_s) : 0;
-  const int u = env_u > 0 ? env_u : default_unroll();
-  if (u >= 4)
-    hipLaunchKernelGGL((skinny_gemm_kernel<KIND, WF, MS, ACT, 4, NS, W>), grid, dim3(W * 64), 0, st, p);
-  else if (u >= 2)
-    hipLaunchKernelGGL((skinny_gemm_kernel<KIND, WF, MS, ACT, 2, NS, W>), grid, dim3(W * 64), 0, st, p);
-  else
-    hipLaunchKernelGGL((skinny_gemm_kernel<KIND, WF, MS, ACT, 1, NS, W>), grid, dim3(W * 64), 0, st, p);
-}
-
 template <int KIND, int WF, int MS, bool ACT, int NS>
-void launch_skinny(const GemmParams& p, int waves, dim3 grid, hipStream_t st) {
-  if (MS <= 2 && waves >= 8) launch_skinny_w<KIND, WF, MS, ACT, NS, (MS <= 2 ? 8 : 4)>(p, grid, st);
-  else launch_skinny_w<KIND, WF, MS, ACT, NS, 4>(p, grid, st);
+void launch_skinny(const GemmParams& p, dim3 grid, hipStream_t st) {
+  hipLaunchKernelGGL((skinny_gemm_kernel<KIND, WF, MS, ACT, kUnroll, NS, kWaves>), grid, dim3(kWaves * 64), 0,
+                     st, p);
   if (p.ksplit > 1) {
     const int nout = ACT ? p.N / 2 : p.N;
     dim3 rg((unsigned)cdiv(nout, 64), 1, grid.z);
@@ -774,26 +741,26 @@ void launch_skinny(const GemmParams& p, int waves, dim3 grid, hipStream_t st) {
 }
 
 template <int KIND, int WF, bool ACT>
-void launch_ms(const GemmParams& p, int ms, int ns, int waves, dim3 grid, hipStream_t st) {
+void launch_ms(const GemmParams& p, int ms, int ns, dim3 grid, hipStream_t st) {
   if (ms == 1) {
     if constexpr (KIND == QK_W4A16_MX) {
       if (ns == 4) {
-        launch_skinny<KIND, WF, 1, ACT, 4>(p, waves, grid, st);
+        launch_skinny<KIND, WF, 1, ACT, 4>(p, grid, st);
         return;
       }
     }
-    launch_skinny<KIND, WF, 1, ACT, 2>(p, waves, grid, st);
+    launch_skinny<KIND, WF, 1, ACT, 2>(p, grid, st);
   } else if (ms == 2) {
-    launch_skinny<KIND, WF, 2, ACT, 2>(p, waves, grid, st);
+    launch_skinny<KIND, WF, 2, ACT, 2>(p, grid, st);
   } else {
-    launch_skinny<KIND, WF, 4, ACT, 2>(p, waves, grid, st);
+    launch_skinny<KIND, WF, 4, ACT, 2>(p, grid, st);
   }
 }
 
 template <int KIND, int WF>
-void launch_act(const GemmParams& p, int ms, int ns, int waves, dim3 grid, hipStream_t st) {
-  if (p.act != QA_NONE) launch_ms<KIND, WF, true>(p, ms, ns, waves, grid, st);
-  else launch_ms<KIND, WF, false>(p, ms, ns, waves, grid, st);
+void launch_act(const GemmParams& p, int ms, int ns, dim3 grid, hipStream_t st) {
+  if (p.act != QA_NONE) launch_ms<KIND, WF, true>(p, ms, ns, grid, st);
+  else launch_ms<KIND, WF, false>(p, ms, ns, grid, st);
 }
 
 // 16-row M tiles per pass for a problem whose groups hold `rows` rows
@@ -822,7 +789,6 @@ int skinny_tiles(int64_t N, int act, int ns) {
 namespace {
 
 struct SkinnyPlan {
-  int waves;   // wavefronts per workgroup (4 or 8)
   int ksplit;  // K slices over grid.y
   int64_t ws_bytes;
 };
@@ -834,7 +800,7 @@ int env_int(const char* name, int dflt) {
 
 // Launch shape of the skinny kernel. Measured on MI355X: 4 wavefronts per
 // workgroup stream best (8 or 16, i.e. shorter K runs per wavefront, lose
-// 10-60%; 8 stays as a tuning option); K is split across workgroups only when there are fewer than ~160
+// 10-60%, so only 4 is instantiated); K is split across workgroups only when there are fewer than ~160
 // workgroups (one per 32 weight rows), which costs a second launch and the
 // [ksplit][M][N] float32 partial sums in the workspace; every wavefront keeps
 // at least two 128-k steps.
@@ -843,13 +809,13 @@ SkinnyPlan skinny_plan(int kind, int64_t M, int64_t N, int64_t K, int act, int s
   const int ms = skinny_ms(rows);
   const int n_wg = skinny_tiles(N, act, skinny_ns(kind, ms)) * std::max(slots, 1);
   const int KS = (int)cdiv<int64_t>(K, 128);
-  // tuning knobs (read per call): wavefronts per workgroup, forced K split,
-  // workgroup count the split planner aims for
-  const int w = ms <= 2 && env_int("QMOE_SKINNY_WAVES", 4) == 8 ? 8 : 4;
+  // tuning knobs (read per call): forced K split, workgroup count the split
+  // planner aims for
+  const int w = kWaves;
   int ksplit = ksplit_hint > 0 ? ksplit_hint : env_int("QMOE_SKINNY_KSPLIT", 0);
   if (ksplit <= 0) ksplit = (int)cdiv<int64_t>(env_int("QMOE_SKINNY_TARGET_WG", 160), n_wg);
   ksplit = std::max(1, std::min(ksplit, std::max(1, KS / (2 * w))));
-  return SkinnyPlan{w, ksplit, ksplit <= 1 ? 0 : (int64_t)ksplit * M * N * 4};
+  return SkinnyPlan{ksplit, ksplit <= 1 ? 0 : (int64_t)ksplit * M * N * 4};
 }
 
 }  // namespace
@@ -873,7 +839,7 @@ int qmoe_skinny_check(int kind, const GemmParams& p) {
   const bool abf16 = kind_abf16(kind);
   constexpr int64_t kLim = 0x7fffffff;
   if ((int64_t)p.N * p.ldw > kLim || p.M * p.lda * (abf16 ? 2 : 1) > kLim) return QMOE_ERR_ARG;
-  if (kind == QK_W4A16_MX && ((int64_t)p.N * p.ldws > kLim || p.K > 16384)) return QMOE_ERR_ARG;
+  if (kind == QK_W4A16_MX && (int64_t)p.N * p.ldws > kLim) return QMOE_ERR_ARG;
   if (kind == QK_W4A16_NV && ((int64_t)p.N * p.ldws * 2 > kLim || (p.ldws % 2) != 0 ||
                               (reinterpret_cast<uintptr_t>(p.w_scale) & 3) || (p.ws_gstride % 2) != 0))
     return QMOE_ERR_ARG;
@@ -905,7 +871,6 @@ int qmoe_skinny_launch(int kind, GemmParams p, int max_rows, int slots, void* wo
   const int ns = skinny_ns(kind, ms);
   const int n_tiles = skinny_tiles(p.N, p.act, ns);
   const SkinnyPlan pl = skinny_plan(kind, p.M, p.N, p.K, p.act, slots, max_rows, ksplit_hint);
-  const int waves = pl.waves;
   p.ksplit = pl.ksplit;
   if (pl.ksplit > 1) {
     if (!workspace || ws_bytes < pl.ws_bytes) return QMOE_ERR_WORKSPACE;
@@ -914,19 +879,19 @@ int qmoe_skinny_launch(int kind, GemmParams p, int max_rows, int slots, void* wo
   dim3 grid(n_tiles, pl.ksplit, slots);
   switch (kind) {
     case QK_W8A8_PC:
-      if (p.wfmt == 0) launch_act<QK_W8A8_PC, 0>(p, ms, ns, waves, grid, st);
-      else launch_act<QK_W8A8_PC, 1>(p, ms, ns, waves, grid, st);
+      if (p.wfmt == 0) launch_act<QK_W8A8_PC, 0>(p, ms, ns, grid, st);
+      else launch_act<QK_W8A8_PC, 1>(p, ms, ns, grid, st);
       break;
     case QK_W8A8_BLK:
-      if (p.wfmt == 0) launch_act<QK_W8A8_BLK, 0>(p, ms, ns, waves, grid, st);
-      else launch_act<QK_W8A8_BLK, 1>(p, ms, ns, waves, grid, st);
+      if (p.wfmt == 0) launch_act<QK_W8A8_BLK, 0>(p, ms, ns, grid, st);
+      else launch_act<QK_W8A8_BLK, 1>(p, ms, ns, grid, st);
       break;
-    case QK_W8A16_PC: launch_act<QK_W8A16_PC, 0>(p, ms, ns, waves, grid, st); break;
-    case QK_W8A16_BLK: launch_act<QK_W8A16_BLK, 0>(p, ms, ns, waves, grid, st); break;
-    case QK_W4A16_MX: launch_act<QK_W4A16_MX, 0>(p, ms, ns, waves, grid, st); break;
-    case QK_W4A16_NV: launch_act<QK_W4A16_NV, 0>(p, ms, ns, waves, grid, st); break;
-    case QK_W4A16_I4: launch_act<QK_W4A16_I4, 0>(p, ms, ns, waves, grid, st); break;
-    case QK_W16A16: launch_act<QK_W16A16, 0>(p, ms, ns, waves, grid, st); break;
+    case QK_W8A16_PC: launch_act<QK_W8A16_PC, 0>(p, ms, ns, grid, st); break;
+    case QK_W8A16_BLK: launch_act<QK_W8A16_BLK, 0>(p, ms, ns, grid, st); break;
+    case QK_W4A16_MX: launch_act<QK_W4A16_MX, 0>(p, ms, ns, grid, st); break;
+    case QK_W4A16_NV: launch_act<QK_W4A16_NV, 0>(p, ms, ns, grid, st); break;
+    case QK_W4A16_I4: launch_act<QK_W4A16_I4, 0>(p, ms, ns, grid, st); break;
+    case QK_W16A16: launch_act<QK_W16A16, 0>(p, ms, ns, grid, st); break;
     default: return QMOE_ERR_ARG;
   }
   return hipGetLastError() == hipSuccess ? QMOE_OK : QMOE_ERR_LAUNCH;

@@ -142,6 +142,8 @@ def _load():
     lib.qmoe_moe_decode_workspace_size.argtypes = [ctypes.POINTER(DecodeDesc), ctypes.POINTER(_i64)]
     lib.qmoe_moe_decode.restype = ctypes.c_int
     lib.qmoe_moe_decode.argtypes = [ctypes.POINTER(DecodeDesc), _vp, _i64, _vp]
+    lib.qmoe_stream_read.restype = ctypes.c_int
+    lib.qmoe_stream_read.argtypes = [_vp, _i64, _i32, _vp, _vp]
     v = lib.qmoe_abi_version()
     if v != ABI_VERSION:
         raise ImportError(f"qmoe: libqmoe.so ABI {v} != expected {ABI_VERSION}; rebuild it")
@@ -152,6 +154,7 @@ lib = _load()
 
 EXPORTED = (
     "qmoe_abi_version",
+    "qmoe_stream_read",
     "qmoe_row_quant",
     "qmoe_gemm_workspace_size",
     "qmoe_gemm_plan",

@@ -529,3 +529,17 @@ def moe_decode(hidden, w1, w2, w1_scale, w2_scale, shared_w1, shared_w1_scale, s
     ws, ws_n = _workspace(hidden.device, nbytes.value)
     check(lib.qmoe_moe_decode(ctypes.byref(d), _ptr(ws), ws_n, _stream(hidden.device)), "moe_decode")
     return out
+
+
+def stream_read(buf, workgroups=2048, sink=None):
+    """Plain read of a device buffer (`qmoe_stream_read`): the HBM read floor
+    the weight-streaming GEMMs are measured against. ``buf``'s byte size must
+    be a multiple of 16; ``sink`` (int32 [workgroups]) is allocated when not
+    given."""
+    _require_gpu(buf)
+    nbytes = buf.numel() * buf.element_size()
+    if sink is None:
+        sink = torch.empty(workgroups, dtype=torch.int32, device=buf.device)
+    check(lib.qmoe_stream_read(_ptr(buf), nbytes, workgroups, _ptr(sink), _stream(buf.device)), "stream_read")
+    return sink
+
