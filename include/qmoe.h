@@ -133,7 +133,8 @@ int qmoe_gemm_workspace_size(const qmoe_gemm_desc* d, int64_t* bytes);
  * The kernel choice qmoe_gemm makes for this problem, computed on the host
  * from the descriptor alone (no device memory is read): path 0 weight
  * streaming, 1 1-byte x 1-byte tiles, 2 bf16 x 4-bit tiles, 3 generic
- * tiles, 4 weight streaming in 64-row passes; tile_m = token rows per tile
+ * tiles, 4 weight streaming in 64-row passes, 5 1-byte x 1-byte 256 x 256
+ * tiles on persistent workgroups (one per CU of the current device); tile_m = token rows per tile
  * (or per streaming pass); ksplit = K slices. No counterpart in the
  * reference (its tiling is chosen inside the Pallas call,
  * `kernels/megablox/gmm_v2.py:922-1055`); it lets tests assert which kernel

@@ -187,6 +187,40 @@ def test_w8a8_int8_per_channel_bit_exact(dev, M, K, N):
     np.testing.assert_array_equal(y.float().cpu().numpy(), ref)
 
 
+# more 256 x 256 tiles than CUs: persistent workgroups (ragged last token
+# and channel tiles, the shortest K of the path, a tile count that leaves
+# workgroups with different numbers of tiles)
+SHAPES_PERSISTENT = [(2000, 1024, 8200), (4096, 512, 4352), (1300, 2048, 14336)]
+
+
+@pytest.mark.parametrize("M,K,N", SHAPES_PERSISTENT)
+@pytest.mark.parametrize("qdtype", ["fp8", "int8"])
+def test_w8a8_persistent_tiles(dev, M, K, N, qdtype):
+    """The persistent 256 x 256 kernel against the oracle (FP8 within one
+    bf16 ulp of the same-code oracle, INT8 bit-exact), and the plan reports
+    it."""
+    from qmoe import _capi, ops
+
+    wf = int(qdtype == "int8")
+    plan = ops.plan_for_shape(_capi.W8A8_PC, M, N, K, wfmt=wf)
+    print(f"w8a8 persistent {qdtype} M={M} K={K} N={N} plan={plan}", flush=True)
+    assert plan[4:] == ("tiled_1b_persistent", 256, 1), plan
+    rng = np.random.default_rng(M + 5 * K + N + wf)
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    wq, ws = quant.quantize_tensor(w, qdtype)
+    x = _bf16(rng, (M, K))
+    ref, xq_ref, _ = linear.w8a8_per_channel(x, wq, ws, qdtype)
+    xq, xs = ops.row_quant(_t(x, dev, torch.bfloat16), qdtype)
+    np.testing.assert_array_equal(xq.view(torch.uint8).cpu().numpy(), xq_ref.view(np.uint8))
+    y = ops.gemm(_capi.W8A8_PC, xq.view(torch.uint8), _t(wq.view(np.uint8), dev), a_scale=xs,
+                 w_scale=_t(ws, dev), wfmt=wf)
+    got = y.float().cpu().numpy()
+    if qdtype == "int8":
+        np.testing.assert_array_equal(got, ref)
+    else:
+        assert_close_same_codes(got, ref, f"fp8 persistent {M}x{K}x{N}")
+
+
 @pytest.mark.parametrize("M,K,N", [(1, 1024, 512), (32, 2048, 768), (130, 1024, 640), (256, 2048, 1024),
                                    # tiled block-scaled kernel: ragged tiles, 32/64/128-token tiles,
                                    # a K split (tall K, few tokens)

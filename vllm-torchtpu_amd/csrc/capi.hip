@@ -17,6 +17,7 @@ int qmoe_tiled_launch(int kind, GemmParams p, hipStream_t st);
 int qmoe_tiled_check(int kind, const GemmParams& p, int* tile);
 bool qmoe_f8_plan(const GemmParams& p, bool blk, int* bm_out, int* ksplit_out, int64_t* ws_bytes);
 int qmoe_f8_launch(GemmParams p, bool blk, void* workspace, int64_t ws_bytes, hipStream_t st);
+bool qmoe_f8_persistent(const GemmParams& p, bool blk);
 bool qmoe_w4_plan(const GemmParams& p, int fmt, int* bm_out, int* ksplit_out, int64_t* ws_bytes);
 int qmoe_w4_launch(GemmParams p, int fmt, void* workspace, int64_t ws_bytes, hipStream_t st);
 
@@ -189,6 +190,7 @@ enum Path {
   kPathW4 = 2,          // bf16 x 4-bit tiles
   kPathTiled = 3,       // generic tiles
   kPathSkinnyPass = 4,  // weight streaming in 64-row passes (K outside every tiled granule)
+  kPathF8Persistent = 5,  // 1-byte x 1-byte 256 x 256 tiles, persistent workgroups
 };
 
 // The one place that decides which kernel runs a problem: the streaming
@@ -215,7 +217,7 @@ int qmoe_route_of(const qmoe_gemm_desc* d, GemmParams& p, QmoeRoute* r) {
     int bm = 0, ks = 1;
     int64_t ws = 0;
     if (use_f8(d) && qmoe_f8_plan(p, kind == QK_W8A8_BLK, &bm, &ks, &ws)) {
-      *r = QmoeRoute{kPathF8, bm, ks, ws};
+      *r = QmoeRoute{qmoe_f8_persistent(p, kind == QK_W8A8_BLK) ? kPathF8Persistent : kPathF8, bm, ks, ws};
       return QMOE_OK;
     }
     if (!use_f8(d) && use_w4(d) && qmoe_w4_plan(p, w4_fmt(d), &bm, &ks, &ws)) {
@@ -246,7 +248,8 @@ int qmoe_run_route(const qmoe_gemm_desc* d, const QmoeRoute& r, GemmParams p, vo
       qmoe_to_params(d, &q);  // keeps the active list
       return qmoe_skinny_launch(kind, q, skinny_rows(d), skinny_slots(d), workspace, ws_bytes, 0, stream);
     }
-    case kPathF8: return qmoe_f8_launch(p, kind == QK_W8A8_BLK, workspace, ws_bytes, stream);
+    case kPathF8:
+    case kPathF8Persistent: return qmoe_f8_launch(p, kind == QK_W8A8_BLK, workspace, ws_bytes, stream);
     case kPathW4: return qmoe_w4_launch(p, w4_fmt(d), workspace, ws_bytes, stream);
     case kPathTiled: return qmoe_tiled_launch(kind, p, stream);
     default: {

@@ -35,6 +35,7 @@
 #include <type_traits>
 
 #include "gemm_tile.h"
+#include "stream_load.h"
 
 
 namespace {
@@ -451,6 +452,309 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
 
 }
 
+// Persistent dense form of the 256 x 256 tile (128-byte K stages in two LDS
+// buffers, per-token x per-channel scales, no K split, bias or row maps).
+// Measured on MI355X: the one-tile-per-workgroup kernel spends ~14 us per
+// tile outside its K loop (launch, the first stages' copy latency, the
+// LDS-staged epilogue), which on the up projection of Llama-3-8B (896 tiles
+// of 32 stages) is a fifth of the time. Here each workgroup walks tiles b,
+// b + G, b + 2G, ... (G the grid, a multiple of the 8 XCDs, so a workgroup
+// stays on its XCD's tile range) and the stage pipeline runs on across
+// tiles: the copies of the next tile's first two stages are issued during
+// the current tile's last two stages, so they are in flight while this
+// tile's epilogue runs. The epilogue therefore cannot stage through the
+// stage buffers: it stores from registers, with the tile's token and
+// channel scales in small double-buffered LDS arrays of their own.
+template <bool INT>
+__global__ __launch_bounds__(kThreads) void f8_persistent_kernel(const GemmParams p, int m_tiles, int n_tiles,
+                                                                 int tile_slots) {
+  constexpr bool ACT = false;  // fused activations take the one-tile kernel
+  constexpr int BM = 256, BN = 256, KB = 128;
+  using S = F8Shape<BM, BN>;
+  constexpr int NI = S::NI, MJ = S::MJ, TN = S::TN, TM = S::TM;
+  __shared__ __align__(1024) uint8_t sW0[BN * KB], sW1[BN * KB];
+  __shared__ __align__(1024) uint8_t sX0[BM * KB], sX1[BM * KB];
+  // per-tile epilogue vectors, double-buffered by tile parity: written after
+  // the tile's first stage, read by its epilogue while the next tile's are
+  // written to the other set
+  __shared__ __align__(16) float s_sx[2][BM], s_ws[2][BN];
+
+  const int tid = threadIdx.x;
+  // the wavefront index in an SGPR: the LDS destinations of the copies are
+  // then scalar (M0) values instead of VGPRs held across the K loop
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wn = wave % S::WN, wm = wave / S::WN;
+  const int nlim = ACT ? p.N / 2 : p.N;
+  constexpr int BNO = ACT ? BN / 2 : BN;
+  constexpr int RPI = 8;                   // rows per copy instruction (128-byte rows)
+  constexpr int WI = BN / (4 * RPI);       // weight copies per wavefront per stage
+  constexpr int XI = BM / (4 * RPI);       // activation copies per wavefront per stage
+  constexpr int CPS = WI + XI;
+  const int KS = p.K / KB;                 // stages per tile (the host keeps K % 256 == 0, K >= 512)
+  const uint8_t* xbase = static_cast<const uint8_t*>(p.a);
+  const uint8_t* wbase = p.w;
+
+  // A tile's copies: this lane moves row r_j = rbase + 32 j of the weight
+  // and activation stages (j < 8), 16-byte chunk `chunk` of the row's 128
+  // bytes (the chunk its slot holds under the row swizzle, the same for
+  // every j); the row offsets are formed at each copy from the tile's
+  // (uniform) origin, so no per-tile offsets stay live across the K loop.
+  struct Src {
+    int row0, rows, n0;
+  };
+  const int rbase = wave * RPI + (lane >> 3);
+  const int chunk = ((lane & 7) ^ (lane >> 3) ^ (wave & 1)) * 16;
+  auto make_src = [&](int row0, int rows, int n0, Src& sc) {
+    sc.row0 = row0;
+    sc.rows = rows;
+    sc.n0 = n0;
+  };
+  auto copy_stage = [&](uint8_t* dW, uint8_t* dX, const Src& sc, int ks) {
+    const uint32_t kb = (uint32_t)ks * (uint32_t)KB;
+#pragma unroll
+    for (int j = 0; j < WI; ++j) {
+      const int n = min(sc.n0 + rbase + 32 * j, nlim - 1);
+      uint32_t o = (uint32_t)n * (uint32_t)p.ldw + (uint32_t)chunk;
+      asm volatile("" : "+v"(o));
+      __builtin_amdgcn_global_load_lds(wbase + (o + kb), QMOE_LDS(dW + (wave + 4 * j) * 1024), 16, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < XI; ++j) {
+      uint32_t r = (uint32_t)(sc.row0 + min(rbase + 32 * j, sc.rows - 1));
+      asm volatile("" : "+v"(r));
+      const uint8_t* src = xbase + (uint64_t)r * (uint64_t)p.lda + (kb + (uint32_t)chunk);
+      __builtin_amdgcn_global_load_lds(src, QMOE_LDS(dX + (wave + 4 * j) * 1024), 16, 0, 0);
+    }
+  };
+
+  // operand reads: lane -> row (l & 31), 32 bytes of k-step t of the stage
+  const int rl = lane & 31, kh = lane >> 5;
+  int po[2][2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) po[t][h] = rl * 128 + (((4 * t + 2 * kh + h) ^ ((rl & 7) ^ ((rl >> 3) & 1))) * 16);
+  auto wrow = [&](int i) { return tile_wrow<BN, TN, NI, ACT>(wn, i); };
+  i32x8 wf[2][NI], xf[2][MJ];
+  auto read_frags = [&](const uint8_t* sW, const uint8_t* sX, int ks, int t) {
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const uint8_t* b = sW + wrow(i) * KB;
+      wf[t][i] = lds_frag(b + po[ks][0], b + po[ks][1]);
+    }
+#pragma unroll
+    for (int j = 0; j < MJ; ++j) {
+      const uint8_t* b = sX + (wm * TM + j * 32) * KB;
+      xf[t][j] = lds_frag(b + po[ks][0], b + po[ks][1]);
+    }
+  };
+  using Acc = typename std::conditional<INT, i32x16, f32x16>::type;
+  Acc acc[NI][MJ];
+  auto mma = [&](int t) {
+    if constexpr (INT) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+#pragma unroll
+          for (int j = 0; j < MJ; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(h ? hi4(wf[t][i]) : lo4(wf[t][i]),
+                                                              h ? hi4(xf[t][j]) : lo4(xf[t][j]), acc[i][j], 0, 0,
+                                                              0);
+    } else {
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+#pragma unroll
+        for (int j = 0; j < MJ; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[t][i], xf[t][j], acc[i][j], 0, 0, 0, 127,
+                                                                      0, 127);
+    }
+  };
+  constexpr int NM = NI * MJ * (INT ? 2 : 1);
+  constexpr int NR = 2 * (NI + MJ);
+
+  // tiles of this workgroup: b = blockIdx.x + i * gridDim.x over the
+  // XCD-ordered slots [0, tile_slots)
+  int b = blockIdx.x;
+  int mt, nt;
+  if (!tile_dense(b, m_tiles, n_tiles, mt, nt)) return;
+  Src cur;
+  int row0 = mt * BM, rows = min(BM, p.M - row0), n0 = nt * BNO;
+  make_src(row0, rows, n0, cur);
+  copy_stage(sW0, sX0, cur, 0);
+  copy_stage(sW1, sX1, cur, 1);
+  wait_copies_upto<CPS>();
+  __syncthreads();
+
+  for (int par = 0;; par ^= 1) {
+    // the next tile (or none: the last copies then refetch this tile's last
+    // stage into buffers that are never read again)
+    int mt2 = 0, nt2 = 0;
+    const bool has_next = b + (int)gridDim.x < tile_slots && tile_dense(b + gridDim.x, m_tiles, n_tiles, mt2, nt2);
+    const int row0n = mt2 * BM, rowsn = has_next ? min(BM, p.M - row0n) : 0, n0n = nt2 * BNO;
+
+    // stage 0 has landed everywhere (prologue / end of the previous tile)
+    read_frags(sW0, sX0, 0, 0);
+    // epilogue inputs of this tile (token tid's activation scale, weight row
+    // tid's scale), loaded now and stored to LDS after stage 0
+    const float e_sx = p.a_scale[(int64_t)(row0 + min(tid, rows - 1)) * p.lds_a];
+    const float e_ws = static_cast<const float*>(p.w_scale)[min(n0 + tid, nlim - 1)];
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+#pragma unroll
+      for (int j = 0; j < MJ; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+    // Stage s lives in LDS buffer s % 2 (as in f8_gemm_kernel with 128-byte
+    // stages) and copies stage kc of the tile in `cur`: s + 2 of this tile,
+    // and in the last two stages the next tile's stages 0 and 1 (`cur` is
+    // switched to the next tile before them), or this tile's last stage
+    // again when there is no next tile (into a buffer never read again).
+    // The last stage reads no operands ahead and does not wait for the
+    // copies: the next tile's first stage lands while the epilogue runs.
+    auto stage = [&](uint8_t* cW, uint8_t* cX, uint8_t* nW, uint8_t* nX, int kc, bool last) {
+      mma(0);
+      read_frags(cW, cX, 1, 1);
+      interleave<0, NM, NR, 0>();
+      __builtin_amdgcn_sched_barrier(0);
+      if (!last) wait_copies_upto<0>();  // stage s + 1 has landed
+      stage_barrier();
+      if (!last) read_frags(nW, nX, 0, 0);
+      copy_stage(cW, cX, cur, kc);
+      mma(1);
+      interleave<0, NM, NR, CPS>();
+    };
+    stage(sW0, sX0, sW1, sX1, 2, false);
+    // the epilogue vectors have landed (the wait in stage 0 covers every
+    // earlier load); the stage barriers ahead make them visible
+    s_sx[par][tid] = e_sx;
+    s_ws[par][tid] = e_ws;
+    stage(sW1, sX1, sW0, sX0, 3, false);
+    for (int s = 2; s < KS - 2; s += 2) {
+      stage(sW0, sX0, sW1, sX1, s + 2, false);
+      stage(sW1, sX1, sW0, sX0, s + 3, false);
+    }
+    if (has_next) make_src(row0n, rowsn, n0n, cur);
+    stage(sW0, sX0, sW1, sX1, has_next ? 0 : KS - 1, false);
+    stage(sW1, sX1, sW0, sX0, has_next ? 1 : KS - 1, true);
+    // the epilogue starts after the last MFMAs: the empty asm takes every
+    // accumulator, so no MFMA can be sunk into the epilogue (interleaving
+    // the two keeps the last stage's operands alive across it)
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+#pragma unroll
+      for (int j = 0; j < MJ; ++j) asm volatile("" : "+a"(acc[i][j]));
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- epilogue (the next tile's first two stages are in flight) ----
+    // A register quad holds 4 consecutive output channels of one token; the
+    // lane 32 apart holds the next 4 (kh = 1). The two exchange one quad of
+    // each pair (q even, q odd), so lane kh = 0 stores the 8 channels of the
+    // even quad and lane kh = 1 those of the odd one: one 16-byte bf16 store
+    // per lane per pair (the host guarantees N % 8 == 0 and 16-byte aligned
+    // output rows), bf16 by the hardware round-to-nearest-even conversion.
+    const qmoe_stream::rsrc_t yres = qmoe_stream::make_rsrc(p.y, (int64_t)p.M * p.ldy * 2);
+    float sxa[MJ];
+    bool tok_ok[MJ];
+#pragma unroll
+    for (int j = 0; j < MJ; ++j) {
+      const int tr = wm * TM + j * 32 + rl;
+      tok_ok[j] = tr < rows;
+      sxa[j] = s_sx[par][min(tr, rows - 1)];
+    }
+    // Stores in token-major order: the four stores (i, qp) of blocks i = 2c,
+    // 2c + 1 cover 128 contiguous bytes of a token's row back to back, so
+    // the L2 assembles whole lines before writing them out.
+#pragma unroll
+    for (int j = 0; j < MJ; ++j)
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+#pragma unroll
+        for (int qp = 0; qp < 2; ++qp) {
+          const int lr_out = wrow(i) + (2 * qp + kh) * 8;  // first tile row of this lane's 8 channels
+          const bool ch_ok = n0 + lr_out < nlim;
+          uint32_t pk[2][2];  // [quad of the pair][dword]
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int q = 2 * qp + h;
+            const float4 cs = *reinterpret_cast<const float4*>(s_ws[par] + wrow(i) + q * 8 + kh * 4);
+            const float csv[4] = {cs.x, cs.y, cs.z, cs.w};
+            float o[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) o[t] = ((float)acc[i][j][q * 4 + t] * sxa[j]) * csv[t];
+            union { bf16x2 b; uint32_t u; } lo, hi;
+            lo.b = __builtin_convertvector(f32x2{o[0], o[1]}, bf16x2);
+            hi.b = __builtin_convertvector(f32x2{o[2], o[3]}, bf16x2);
+            pk[h][0] = lo.u;
+            pk[h][1] = hi.u;
+          }
+          // kh = 0 sends its odd quad and keeps the even one; kh = 1 the reverse
+          const uint32_t s0 = kh ? pk[0][0] : pk[1][0], s1 = kh ? pk[0][1] : pk[1][1];
+          const uint32_t r0 = (uint32_t)__shfl_xor((int)s0, 32, 64), r1 = (uint32_t)__shfl_xor((int)s1, 32, 64);
+          i32x4 out;
+          out[0] = (int)(kh ? r0 : pk[0][0]);
+          out[1] = (int)(kh ? r1 : pk[0][1]);
+          out[2] = (int)(kh ? pk[1][0] : r0);
+          out[3] = (int)(kh ? pk[1][1] : r1);
+          // outputs past the tile's tokens or channels store at an offset
+          // past the buffer: the store is dropped, with no branch
+          const uint32_t yoff = tok_ok[j] && ch_ok
+                                    ? (uint32_t)((row0 + wm * TM + j * 32 + rl) * (uint32_t)p.ldy + n0 + lr_out) * 2u
+                                    : qmoe_stream::kOob;
+          __builtin_amdgcn_raw_buffer_store_b128(out, yres, yoff, 0, 0);
+        }
+    if (!has_next) {
+      // no LDS copy may still be landing when the workgroup's LDS is freed
+      wait_copies_upto<0>();
+      break;
+    }
+    // the next tile's stage 0 has landed everywhere (its copies are older
+    // than stage 1's and than the stores: at most CPS operations newer)
+    wait_copies_upto<CPS>();
+    stage_barrier();
+    b += gridDim.x;
+    row0 = row0n;
+    rows = rowsn;
+    n0 = n0n;
+  }
+}
+
+// Workgroups of the persistent 256 x 256 tile kernel for `tiles` tiles: as
+// few tile rounds as the CUs of the current device allow, spread evenly
+// (896 tiles on 256 CUs: 4 rounds on 224 workgroups, not 3.5 on 256;
+// measured on MI355X, 216 vs 222 us for Llama-3-8B's up projection at 4096
+// tokens), rounded up to a multiple of the 8 XCDs. 0 when the tiles fit one
+// round (the one-tile kernel then runs) or the tuning knob QMOE_F8_PERSIST=0
+// turns the kernel off; another value of the knob caps the workgroups.
+int f8_persistent_grid(int tiles) {
+  const char* env = getenv("QMOE_F8_PERSIST");  // tuning knob
+  if (env && atoi(env) == 0) return 0;
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                               hipSuccess)
+    return 0;
+  if (env && atoi(env) >= kXcds) cus = std::min(cus, atoi(env));
+  cus = cus / kXcds * kXcds;
+  if (cus <= 0 || tiles <= cus / 2) return 0;
+  const int rounds = cdiv(tiles, cus);
+  return std::min(cus, cdiv(cdiv(tiles, rounds), kXcds) * kXcds);
+}
+
+// Whether a dense problem with this plan runs the persistent kernel: 256 x
+// 256 tiles of per-channel W8A8 without a fused activation or K split,
+// 128-byte stages (the default of the QMOE_F8_KB knob), K >= 512, plain
+// row-major output with N % 8 == 0 and 16-byte aligned rows below 2 GiB, no
+// bias, row gather / scatter or routing weights, and more tiles than CUs.
+bool f8_persistent_ok(const GemmParams& p, bool blk, int bm, int ksplit) {
+  if (blk || bm != 256 || ksplit != 1 || p.group_offs || p.act != QA_NONE || p.K < 512) return false;
+  const char* env = getenv("QMOE_F8_KB");
+  if (env && atoi(env) == 64) return false;
+  if ((p.N % 8) != 0 || (p.ldy % 8) != 0 || (reinterpret_cast<uintptr_t>(p.y) & 15) != 0) return false;
+  if (p.a_rows || p.y_rows || p.row_weight || p.bias || (int64_t)p.M * p.ldy * 2 >= 0x7fffffffLL) return false;
+  return f8_persistent_grid(cdiv(p.M, 256) * cdiv(p.N, 256)) > 0;
+}
+
 template <bool INT, int BM, int BN, bool ACT, bool BLK, bool WPC = false>
 void f8_launch_shape(const GemmParams& p, hipStream_t st) {
   const char* env = getenv("QMOE_F8_KB");  // tuning knob: K bytes per LDS stage
@@ -466,6 +770,13 @@ void f8_launch_shape(const GemmParams& p, hipStream_t st) {
   } else {
     const int m_tiles = cdiv(p.M, BM);
     const int grid = cdiv(m_tiles * n_tiles, kXcds) * kXcds;
+    if constexpr (BM == 256 && BN == 256 && !BLK && !ACT) {
+      if (kb == 128 && f8_persistent_ok(p, BLK, BM, (int)ks)) {
+        hipLaunchKernelGGL((f8_persistent_kernel<INT>), dim3(f8_persistent_grid(m_tiles * n_tiles)), dim3(kThreads),
+                           0, st, p, m_tiles, n_tiles, grid);
+        return;
+      }
+    }
     hipLaunchKernelGGL(kern, dim3(grid, 1, ks), dim3(kThreads), 0, st, p, m_tiles, n_tiles);
   }
 }
@@ -588,6 +899,13 @@ bool qmoe_f8_plan(const GemmParams& p, bool blk, int* bm_out, int* ksplit_out, i
   *ksplit_out = ksplit;
   *ws_bytes = ksplit > 1 ? (int64_t)ksplit * p.M * p.N * 4 : 0;
   return true;
+}
+
+// Whether the planned problem runs the persistent 256 x 256 kernel.
+bool qmoe_f8_persistent(const GemmParams& p, bool blk) {
+  int bm = 0, ksplit = 1;
+  int64_t ws = 0;
+  return qmoe_f8_plan(p, blk, &bm, &ksplit, &ws) && f8_persistent_ok(p, blk, bm, ksplit);
 }
 
 // Launch per the plan (the caller checked qmoe_f8_plan and sized the

@@ -7,7 +7,8 @@
 #include "gemm_common.h"
 
 struct QmoeRoute {
-  int path = 0;    // 0 streaming, 1 1-byte tiles, 2 4-bit tiles, 3 generic tiles, 4 streaming passes
+  int path = 0;    // 0 streaming, 1 1-byte tiles, 2 4-bit tiles, 3 generic tiles, 4 streaming passes,
+                   // 5 1-byte tiles on persistent workgroups
   int tile_m = 0;  // token rows per tile (tiled) or per pass (streaming)
   int ksplit = 1;
   int64_t ws_bytes = 0;  // split-K partials the launch needs

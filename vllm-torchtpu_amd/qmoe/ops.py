@@ -218,7 +218,7 @@ def gemm_desc(kind, a, w, *, a_scale=None, w_scale=None, bias=None, wfmt=0, ws_b
 
 # ---------------------------------------------------------------- kernel plans
 
-PATH_NAMES = ("stream", "tiled_1b", "tiled_4b", "tiled_generic", "stream_passes")
+PATH_NAMES = ("stream", "tiled_1b", "tiled_4b", "tiled_generic", "stream_passes", "tiled_1b_persistent")
 
 _plan_log = None
 
