@@ -168,7 +168,11 @@ def test_compressed_tensors_int4_dispatch_shapes_and_guards(monkeypatch):
     assert moe.w2_weight_packed.shape == (4, 256, 16)
     assert moe.w13_weight_scale.shape == (4, 256, 8) and moe.w2_weight_scale.shape == (4, 256, 4)
     with pytest.raises(NotImplementedError, match="integer INT4 weights only"):
-        cfg(type="float").get_quant_method(_moe_layer()).create_weights(_moe_layer(), 4, 256, 128, torch.bfloat16)
+        q.CompressedTensorsW4A16MoEMethod({"num_bits": 4, "type": "float", "symmetric": True, "strategy": "group",
+                                           "group_size": 32}).create_weights(_moe_layer(), 4, 256, 128,
+                                                                             torch.bfloat16)
+    # a float 4-bit group-32 scheme is MXFP4 and dispatches to its own method
+    assert isinstance(cfg(type="float").get_quant_method(_moe_layer()), q.CompressedTensorsW4ANMxfp4MoEMethod)
     with pytest.raises(NotImplementedError, match="symmetric INT4 only"):
         cfg(symmetric=False).get_quant_method(_moe_layer()).create_weights(_moe_layer(), 4, 256, 128,
                                                                            torch.bfloat16)
@@ -185,3 +189,50 @@ def test_compressed_tensors_int4_dispatch_shapes_and_guards(monkeypatch):
     monkeypatch.setenv("MOE_REQUANTIZE_WEIGHT_DTYPE", "fp4")
     with pytest.raises(NotImplementedError, match="MOE_REQUANTIZE"):
         m.process_weights_after_loading(moe)
+
+
+def _ct_cfg(weights, input_activations=None):
+    return q.CompressedTensorsConfig.from_config({"config_groups": {"group_0": {
+        "weights": weights, "input_activations": input_activations, "targets": ["Linear"]}}, "ignore": ["lm_head"]})
+
+
+def test_compressed_tensors_dispatch():
+    """`compressed_tensors.py:200-254`, `compressed_tensors_moe.py:80-116`:
+    FP8 linears through the FP8 method (block / channel strategies), MoE by
+    weight scheme, ignored layers unquantized, other schemes refused."""
+    fp8_block = _ct_cfg({"num_bits": 8, "type": "float", "strategy": "block", "block_structure": [128, 128],
+                         "dynamic": False}, {"num_bits": 8, "type": "float", "strategy": "token", "dynamic": True})
+    m = fp8_block.get_quant_method(torch.nn.Module(), prefix="model.layers.0.mlp.down_proj")
+    assert isinstance(m, q.Fp8LinearMethod) and m.weight_block_size == [128, 128]
+    assert isinstance(fp8_block.get_quant_method(_moe_layer(), prefix="model.layers.0.mlp.experts"), q.Fp8MoEMethod)
+    assert isinstance(fp8_block.get_quant_method(torch.nn.Module(), prefix="lm_head"), q.UnquantizedLinearMethod)
+    fp8_ch = _ct_cfg({"num_bits": 8, "type": "float", "strategy": "channel", "dynamic": False})
+    m = fp8_ch.get_quant_method(torch.nn.Module(), prefix="x")
+    assert isinstance(m, q.Fp8LinearMethod) and m.quant_config.is_channel_quant and m.weight_block_size is None
+    layer = torch.nn.Module()
+    m.create_weights(layer, 64, [32, 32], 64, 64, torch.bfloat16)
+    assert tuple(layer.weight_scale.shape) == (64, 1)
+    mx = _ct_cfg({"num_bits": 4, "type": "float", "strategy": "group", "group_size": 32})
+    assert isinstance(mx.get_quant_method(_moe_layer(), prefix="e"), q.CompressedTensorsW4ANMxfp4MoEMethod)
+    i4 = _ct_cfg({"num_bits": 4, "type": "int", "strategy": "group", "group_size": 128})
+    assert isinstance(i4.get_quant_method(_moe_layer(), prefix="e"), q.CompressedTensorsW4A16MoEMethod)
+    with pytest.raises(NotImplementedError):
+        i4.get_quant_method(torch.nn.Module(), prefix="x")  # dense INT4: not ported (as in the reference)
+    with pytest.raises(RuntimeError, match="Unsupported TPU FusedMoe scheme"):
+        _ct_cfg({"num_bits": 8, "type": "int", "strategy": "channel"}).get_quant_method(_moe_layer(), prefix="e")
+
+
+def test_compressed_tensors_mxfp4_moe_weight_shapes():
+    layer = _moe_layer()
+    m = q.CompressedTensorsW4ANMxfp4MoEMethod(layer.moe_config)
+    m.create_weights(layer, 4, 256, 128, torch.bfloat16)
+    assert tuple(layer.w13_weight_packed.shape) == (4, 256, 128) and layer.w13_weight_packed.dtype == torch.uint8
+    assert tuple(layer.w13_weight_scale.shape) == (4, 256, 8)
+    assert tuple(layer.w2_weight_packed.shape) == (4, 256, 64) and tuple(layer.w2_weight_scale.shape) == (4, 256, 4)
+
+
+def test_layout_markers():
+    from qmoe.layers import linear_common as lc
+
+    assert lc.KEEP_VLLM_LAYOUT_ATTR == "_tpu_keep_vllm_weight_layout"
+    assert lc.WEIGHT_FLIPPED_ATTR == "_tpu_weight_flipped"

@@ -56,6 +56,7 @@ from typing import Optional
 import torch
 
 from qmoe import _capi, ops
+from qmoe.layers import ref_layout
 
 
 MOE_FORMATS = ("mxfp4", "nvfp4", "int4", "bf16", "fp8", "int8", "fp8_w8a16", "fp8_block", "fp8_block_rows",
@@ -87,6 +88,12 @@ def fused_moe_gmm(hidden_states, w1, w2, w1_scale, w2_scale, w1_bias, w2_bias, t
     runs the whole expert set on one GPU, so it must be None or 0.
     ``rhs_quant_dtype``: ``int4`` (any dtype object or string naming int4) marks
     packed-int4 int32 weights (`compressed_tensors_moe_w4a16.py:380-405`).
+
+    Weights come in this package's layouts (table above; what the MoE
+    methods hold) or in the reference's runtime layout -- ``w1 [E, H, 2I]``,
+    ``w2 [E, I, H]``, scales ``[E, K/B, 1, N]`` or ``[E, K/B, N]``, biases
+    ``[E, 1, N]`` -- which is recognized from the shapes and repacked once
+    per weight tensor (`qmoe/layers/ref_layout.py`).
     """
     # The reference passes experts_start as a 0-d int32 tensor exactly when
     # expert parallelism is on (`layers/adapter/fused_moe.py:241-293`); this
@@ -98,6 +105,11 @@ def fused_moe_gmm(hidden_states, w1, w2, w1_scale, w2_scale, w1_bias, w2_bias, t
         if "int4" not in str(rhs_quant_dtype):
             raise NotImplementedError(f"rhs_quant_dtype {rhs_quant_dtype} is not supported (int4 only)")
         weight_format = weight_format or "int4"
+    if weight_format is None and ref_layout.is_reference_moe_layout(hidden_states.shape[-1], w1, w2, w1_scale):
+        # the reference's runtime layout (K-major, [E, K/B, 1, N] scales),
+        # repacked once per weight tensor
+        w1, w2, w1_scale, w2_scale, w1_bias, w2_bias, weight_format = ref_layout.moe_weights(
+            hidden_states.shape[-1], w1, w2, w1_scale, w2_scale, w1_bias, w2_bias)
     fmt = weight_format or infer_weight_format(w1, w1_scale)
     if fmt not in MOE_FORMATS:
         raise ValueError(f"unknown MoE weight format {fmt!r}")

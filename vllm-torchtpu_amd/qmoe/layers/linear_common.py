@@ -27,18 +27,30 @@ from typing import Optional
 import torch
 
 from qmoe import _capi, ops
+from qmoe.layers import ref_layout
+
+# Markers of the reference's linear layers (`linear_common.py:30-53`). A
+# module that reads a linear layer's ``.weight`` raw sets KEEP_VLLM_LAYOUT on
+# it so the weight keeps vLLM's ``[n_out, n_in]`` layout; the reference
+# flips every other weight to ``[n_in, n_out]`` once and records that with
+# WEIGHT_FLIPPED. This package keeps every weight in ``[n_out, n_in]`` (the
+# kernels read N-major weights), so both hold trivially: raw readers always
+# see vLLM's layout and no flip can be repeated.
+KEEP_VLLM_LAYOUT_ATTR = "_tpu_keep_vllm_weight_layout"
+WEIGHT_FLIPPED_ATTR = "_tpu_weight_flipped"
 
 
 def _weight_nk(w_q: torch.Tensor) -> torch.Tensor:
-    """[K, N] logical weight -> the N-major [N, K] buffer it views."""
+    """[K, N] logical weight -> the N-major [N, K] buffer it views (this
+    package's layout: ``weight.t()`` of the ``[n_out, n_in]`` parameter). A
+    contiguous K-major ``[n_in, n_out]`` weight (the reference's runtime
+    layout after its load-time flip, `fp8.py:1598-1617`) is transposed into
+    an N-major copy once per weight tensor (`qmoe/layers/ref_layout.py`)."""
     if w_q.dim() != 2:
         raise ValueError(f"weight must be 2-D [n_in, n_out], got {tuple(w_q.shape)}")
     w_nk = w_q.t()
     if not w_nk.is_contiguous():
-        raise ValueError(
-            "qmoe expects w_q as the [n_in, n_out] view of an N-major [n_out, n_in] "
-            "buffer (stride (1, n_in)); keep the checkpoint layout and pass weight.t()"
-        )
+        w_nk = ref_layout.nmajor_copy(w_q)
     return w_nk
 
 
@@ -192,7 +204,10 @@ def quantized_matmul_fp4(x: torch.Tensor, w_q: torch.Tensor, w_s: torch.Tensor,
     """FP4 W4A16 dense linear, `linear_common.py:188-209, 242-255`.
 
     ``w_q``: packed e2m1 codes, N-major ``[n_out, n_in/2]`` uint8 (the
-    checkpoint layout; low nibble = even k). ``w_s`` picks the format:
+    checkpoint layout; low nibble = even k), or the reference's runtime form
+    (K-major ``float4_e2m1fn_x2`` / uint8 ``[n_in, n_out/2]`` with a rank-4
+    ``[1, n_in/B, 1, n_out]`` float32 scale, B = 16 or 32), repacked once per
+    weight tensor (`qmoe/layers/ref_layout.py`). ``w_s`` picks the format:
     e8m0 bytes ``[n_out, n_in/32]`` (MXFP4), or bf16 / f32 block scales
     ``[n_out, n_in/16]`` (NVFP4: the fused e4m3 x global scale; f32 values are
     rounded to bf16, which is what the reference's in-kernel dequantization
@@ -200,6 +215,10 @@ def quantized_matmul_fp4(x: torch.Tensor, w_q: torch.Tensor, w_s: torch.Tensor,
     stay unquantized (both blocks are below the reference's
     dequantize-after-matmul threshold), f32 accumulate.
     """
+    if w_s.dim() == 4:
+        # the reference's runtime layout: K-major fp4 [n_in, n_out] (bytes
+        # [n_in, n_out / 2]) + [1, n_in / B, 1, n_out] float32, repacked once
+        w_q, w_s = ref_layout.fp4_linear(w_q, w_s, x.shape[-1])
     nv = w_s.dtype in (torch.bfloat16, torch.float32)
     blk = 16 if nv else 32
     if w_q.dim() != 2 or w_s.dim() != 2:

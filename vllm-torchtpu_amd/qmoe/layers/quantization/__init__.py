@@ -2,7 +2,8 @@
 `layers/adapter/quantization/__init__.py:51-101`, `get_tpu_quantization_config`):
 maps a checkpoint's ``quantization`` method name to the config class."""
 
-from qmoe.layers.quantization.compressed_tensors import CompressedTensorsConfig, CompressedTensorsW4A16MoEMethod
+from qmoe.layers.quantization.compressed_tensors import (CompressedTensorsConfig, CompressedTensorsW4A16MoEMethod,
+                                                        CompressedTensorsW4ANMxfp4MoEMethod)
 from qmoe.layers.quantization.fp8 import Fp8Config, Fp8LinearMethod, Fp8MoEMethod
 from qmoe.layers.quantization.mxfp4 import Mxfp4Config, Mxfp4LinearMethod, Mxfp4MoEMethod
 from qmoe.layers.quantization.nvfp4 import Nvfp4Config, Nvfp4LinearMethod, Nvfp4MoEMethod
@@ -27,7 +28,7 @@ def get_quantization_config(method: str):
 
 
 __all__ = [
-    "CompressedTensorsConfig", "CompressedTensorsW4A16MoEMethod", "Fp8Config", "Fp8LinearMethod", "Fp8MoEMethod", "Mxfp4Config", "Mxfp4LinearMethod",
+    "CompressedTensorsConfig", "CompressedTensorsW4A16MoEMethod", "CompressedTensorsW4ANMxfp4MoEMethod", "Fp8Config", "Fp8LinearMethod", "Fp8MoEMethod", "Mxfp4Config", "Mxfp4LinearMethod",
     "Mxfp4MoEMethod", "Nvfp4Config", "Nvfp4LinearMethod", "Nvfp4MoEMethod", "UnquantizedFusedMoEMethod", "UnquantizedLinearMethod",
     "get_quantization_config",
 ]

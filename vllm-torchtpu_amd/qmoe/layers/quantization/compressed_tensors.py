@@ -32,13 +32,55 @@ def _args(d):
         return d
     return SimpleNamespace(num_bits=d.get("num_bits", 4), type=d.get("type", "int"),
                            symmetric=d.get("symmetric", True), strategy=d.get("strategy", "group"),
-                           group_size=d.get("group_size"), actorder=d.get("actorder"))
+                           group_size=d.get("group_size"), actorder=d.get("actorder"),
+                           dynamic=d.get("dynamic", False), block_structure=d.get("block_structure"))
+
+
+def _kind(v) -> str:
+    """The lower-case name of an enum or string field ("float", "group", ...)."""
+    return str(getattr(v, "value", v)).lower()
+
+
+def _is_weight_fp8(q) -> bool:
+    """`compressed_tensors.py:63-68`."""
+    return q is not None and _kind(q.type) == "float" and int(q.num_bits) == 8
+
+
+def _is_int4_w4aN(q) -> bool:
+    """`compressed_tensors.py:71-83`: static INT4 weights, group or channel
+    strategy."""
+    return (q is not None and int(q.num_bits) == 4 and _kind(q.type) == "int"
+            and _kind(q.strategy) in ("group", "channel") and not bool(getattr(q, "dynamic", False)))
+
+
+def _is_mxfp4(q) -> bool:
+    """MXFP4 weights (upstream compressed-tensors' MXFP4 scheme: 4-bit floats,
+    group strategy, 32 values per e8m0 scale)."""
+    return (q is not None and int(q.num_bits) == 4 and _kind(q.type) == "float"
+            and _kind(q.strategy) == "group" and int(getattr(q, "group_size", 0) or 0) == 32)
+
+
+def _build_fp8_config(weight_quant, input_quant):
+    """`compressed_tensors.py:86-109`: an FP8 compressed-tensors scheme as an
+    Fp8Config (block size from the block strategy, per-channel flag from the
+    channel strategy; dynamic activations unless the scheme says static)."""
+    from qmoe.layers.quantization.fp8 import Fp8Config
+
+    block = weight_quant.block_structure if _kind(weight_quant.strategy) == "block" else None
+    scheme = "dynamic" if (input_quant is None or bool(getattr(input_quant, "dynamic", True))) else "static"
+    cfg = Fp8Config(is_checkpoint_fp8_serialized=True, activation_scheme=scheme, weight_block_size=block)
+    cfg.is_channel_quant = _kind(weight_quant.strategy) == "channel"
+    return cfg
 
 
 class CompressedTensorsConfig:
-    """The compressed-tensors schemes on this hot path: packed-INT4 W4A16 MoE
-    experts (`compressed_tensors_moe.py:80-110` dispatch); the reference's
-    other compressed-tensors schemes run through upstream vLLM layers."""
+    """The compressed-tensors schemes on this hot path
+    (`compressed_tensors.py:200-254`, `compressed_tensors_moe.py:80-116`):
+    FP8 linears through the FP8 linear method (the reference's bypass), and
+    MoE experts dispatched by weight scheme -- packed INT4 (W4A16), MXFP4
+    (W4A16, `compressed_tensors_moe_w4an_mxfp4.py`) or FP8 (the FP8 MoE
+    method). The scheme of the checkpoint's first config group applies to
+    every layer not in ``ignore``."""
 
     def __init__(self, weight_quant=None, input_quant=None, ignore=None):
         self.weight_quant = _args(weight_quant)
@@ -56,15 +98,25 @@ class CompressedTensorsConfig:
         return cls(first.get("weights"), first.get("input_activations"), config.get("ignore"))
 
     def get_quant_method(self, layer, prefix=""):
+        from qmoe.layers.quantization.fp8 import Fp8LinearMethod, Fp8MoEMethod
         from qmoe.layers.quantization.unquantized import UnquantizedFusedMoEMethod, UnquantizedLinearMethod
 
         moe = hasattr(layer, "moe_config")
-        if any(prefix.startswith(p) for p in self.ignore):
+        if any(prefix.startswith(p) for p in self.ignore) or self.weight_quant is None:
             return UnquantizedFusedMoEMethod(layer.moe_config) if moe else UnquantizedLinearMethod()
+        wq, iq = self.weight_quant, self.input_quant
         if not moe:
-            raise NotImplementedError("qmoe runs compressed-tensors MoE experts only; dense compressed-tensors "
-                                      "schemes are not on this path")
-        return CompressedTensorsW4A16MoEMethod(self.weight_quant, self.input_quant, layer.moe_config)
+            if _is_weight_fp8(wq):  # `compressed_tensors.py:227-231`
+                return Fp8LinearMethod(_build_fp8_config(wq, iq))
+            raise NotImplementedError("Compressed-tensors linear schemes other than FP8 are not implemented "
+                                      "(the reference raises for them too)")
+        if _is_int4_w4aN(wq):
+            return CompressedTensorsW4A16MoEMethod(wq, iq, layer.moe_config)
+        if _is_mxfp4(wq):
+            return CompressedTensorsW4ANMxfp4MoEMethod(layer.moe_config)
+        if _is_weight_fp8(wq):
+            return Fp8MoEMethod(_build_fp8_config(wq, iq), layer.moe_config)
+        raise RuntimeError(f"Unsupported TPU FusedMoe scheme: {wq}, {iq}")
 
 
 class CompressedTensorsW4A16MoEMethod:
@@ -156,3 +208,86 @@ class CompressedTensorsW4A16MoEMethod:
         return moe_forward(layer, x, router_logits, layer.w13_weight_packed, layer.w2_weight_packed,
                            layer.w13_weight_scale, layer.w2_weight_scale, None, None, "int4",
                            skip_padded_tokens=envs.TPU_MOE_SKIP_PADDED_TOKENS, input_ids=input_ids)
+
+
+class CompressedTensorsW4ANMxfp4MoEMethod:
+    """Compressed-tensors MXFP4 MoE (`compressed_tensors_moe_w4an_mxfp4.py:
+    49-342`), W4A16: bf16 activations against e2m1 experts expanded in
+    registers with their e8m0 block scales.
+
+    The checkpoint holds N-major e2m1 codes packed two per byte along K and
+    one e8m0 byte per 32 K values (``w13_weight_packed u8 [E, 2I, H/2]``,
+    ``w13_weight_scale u8 [E, 2I, H/32]``, ``w2_weight_packed u8 [E, H,
+    I/2]``, ``w2_weight_scale u8 [E, H, I/32]``), no biases. The reference
+    turns them into K-major native fp4 with float32 scales ``[E, K/32, 1,
+    N]`` (`:173-273`); here they stay as loaded -- the same values: codes
+    times 2^(byte - 127) -- and run as this package's ``mxfp4`` format. The
+    scales of an unloaded intermediate padding are zeroed first, as the
+    reference does (`:138-171`: an untouched 0xff byte would make a padded
+    zero weight NaN). Requantizing to W4A8 (``MOE_REQUANTIZE_BLOCK_SIZE``)
+    is not built and raises."""
+
+    is_monolithic = True
+    supports_internal_mk = False
+
+    def __init__(self, moe_config=None):
+        self.moe = moe_config
+        self.group_size = 32
+
+    def maybe_roundup_sizes(self, hidden_size, intermediate_size_per_partition, *args, **kwargs):
+        return hidden_size, intermediate_size_per_partition
+
+    def create_weights(self, layer, num_experts, hidden_size, intermediate_size_per_partition,
+                       params_dtype, **extra_weight_attrs):
+        E, H, I = num_experts, hidden_size, intermediate_size_per_partition
+        if H % 32 or I % 32:
+            raise ValueError(f"MXFP4 MoE sizes must be multiples of 32, got H={H}, I={I}")
+        u8 = torch.uint8
+        layer.register_parameter("w13_weight_packed", _param(torch.empty(E, 2 * I, H // 2, dtype=u8)))
+        layer.register_parameter("w13_weight_scale", _param(torch.empty(E, 2 * I, H // 32, dtype=u8)))
+        layer.register_parameter("w2_weight_packed", _param(torch.empty(E, H, I // 2, dtype=u8)))
+        layer.register_parameter("w2_weight_scale", _param(torch.empty(E, H, I // 32, dtype=u8)))
+
+    def _neutralize_padded_scales(self, layer, s13, s2):
+        """`compressed_tensors_moe_w4an_mxfp4.py:138-171`."""
+        moe = getattr(layer, "moe_config", None) or self.moe
+        unpadded = getattr(moe, "intermediate_size_per_partition_unpadded", None)
+        padded = s2.shape[-1] * self.group_size
+        if unpadded is None or unpadded >= padded:
+            return
+        if unpadded % self.group_size:
+            raise ValueError("MXFP4 unpadded intermediate size per partition must be divisible by "
+                             f"{self.group_size}, got {unpadded}.")
+        s13[:, unpadded:padded, :] = 0
+        s13[:, padded + unpadded:2 * padded, :] = 0
+        s2[:, :, unpadded // self.group_size:] = 0
+
+    def process_weights_after_loading(self, layer):
+        if getattr(layer, "_qmoe_processed", False):
+            return
+        if envs.MOE_REQUANTIZE_BLOCK_SIZE:
+            raise NotImplementedError("qmoe runs compressed-tensors MXFP4 experts as W4A16 at their 32-value "
+                                      "blocks; W4A8 requantization (MOE_REQUANTIZE_BLOCK_SIZE) is not built")
+        dev = _device()
+        w13 = layer.w13_weight_packed.data.to(dev).view(torch.uint8).contiguous()
+        w2 = layer.w2_weight_packed.data.to(dev).view(torch.uint8).contiguous()
+        s13 = layer.w13_weight_scale.data.to(dev).view(torch.uint8).contiguous()
+        s2 = layer.w2_weight_scale.data.to(dev).view(torch.uint8).contiguous()
+        self._neutralize_padded_scales(layer, s13, s2)
+        for name in ("w13_weight_packed", "w2_weight_packed"):
+            delattr(layer, name)
+        layer.w13_weight, layer.w2_weight = _param(w13), _param(w2)
+        layer.w13_weight_scale, layer.w2_weight_scale = _param(s13), _param(s2)
+        layer.w13_bias = None
+        layer.w2_bias = None
+        layer._qmoe_activation = _activation(layer)
+        layer._qmoe_processed = True
+
+    def apply_monolithic(self, layer, x, router_logits, input_ids=None):
+        """`compressed_tensors_moe_w4an_mxfp4.py:275-342`: route, then the
+        fused MoE with padded tokens skipped (the reference passes
+        ``skip_padded_tokens=True``)."""
+        return moe_forward(layer, x, router_logits, layer.w13_weight, layer.w2_weight, layer.w13_weight_scale,
+                           layer.w2_weight_scale, None, None, "mxfp4", skip_padded_tokens=True,
+                           input_ids=input_ids)
+

@@ -33,7 +33,7 @@ import torch
 
 from qmoe import envs, ops
 from qmoe.layers.fused_moe import moe_forward
-from qmoe.layers.linear_common import quantized_matmul
+from qmoe.layers.linear_common import KEEP_VLLM_LAYOUT_ATTR, quantized_matmul
 
 FP8 = torch.float8_e4m3fn
 _REQUANT_DTYPES = {"float8_e4m3fn": FP8, "int8": torch.int8}
@@ -165,6 +165,9 @@ class Fp8Config:
         self.activation_scheme = activation_scheme
         self.weight_block_size = list(weight_block_size) if weight_block_size else None
         self.ignored_layers = ignored_layers or []
+        # one scale per output channel in the checkpoint (compressed-tensors
+        # channel strategy, `compressed_tensors.py:86-109`)
+        self.is_channel_quant = False
 
     @classmethod
     def get_name(cls):
@@ -215,6 +218,8 @@ class Fp8LinearMethod:
                 bh, bw = self.weight_block_size
                 s = torch.empty((n + bh - 1) // bh, (k + bw - 1) // bw, dtype=torch.float32)
                 layer.register_parameter("weight_scale_inv", _param(s))
+            elif getattr(self.quant_config, "is_channel_quant", False):
+                layer.register_parameter("weight_scale", _param(torch.empty(n, 1, dtype=torch.float32)))
             else:
                 layer.register_parameter("weight_scale", _param(torch.empty(len(output_partition_sizes),
                                                                             dtype=torch.float32)))
@@ -226,6 +231,9 @@ class Fp8LinearMethod:
         if getattr(layer, "_qmoe_processed", False):
             return
         name, _, block, blockwise = self._linear_quant_config
+        if _is_embedding(layer):
+            # embedding tables are gathered by row: one scale per row
+            block, blockwise = None, False
         dev = _device()
         weight = layer.weight.data.to(dev)
         ckpt_block = None
@@ -264,12 +272,39 @@ class Fp8LinearMethod:
         layer._qmoe_processed = True
 
     def apply(self, layer, x, bias=None):
-        """`fp8.py:1669-1690`: quantized matmul, then the bias."""
-        out = quantized_matmul(x, layer.weight.t(), layer.weight_scale,
-                               w8a16_max_rows=self.w8a16_max_rows)
+        """`fp8.py:1669-1690`: quantized matmul, then the bias. The weight is
+        held in vLLM's ``[n_out, n_in]`` layout for every layer, so a layer
+        marked KEEP_VLLM_LAYOUT (read raw elsewhere) needs no flip here; the
+        matmul takes the ``[n_in, n_out]`` view. An embedding table used as
+        the output projection (VocabParallelEmbedding: tied lm_head) keeps
+        bf16 activations (W8A16, `:1679-1681`)."""
+        if _is_embedding(layer):
+            x2 = x.reshape(-1, x.shape[-1])
+            rows = max(1, x2.shape[0])
+            out = quantized_matmul(x2, layer.weight.t(), layer.weight_scale, w8a16_max_rows=rows)
+            out = out.reshape(*x.shape[:-1], out.shape[-1])
+        else:
+            out = quantized_matmul(x, layer.weight.t(), layer.weight_scale,
+                                   w8a16_max_rows=self.w8a16_max_rows)
         if bias is not None:
             out = out + bias
         return out
+
+    def embedding(self, layer, input_):
+        """`fp8.py:1692-1698`: gather the rows of the ``[vocab, H]`` codes and
+        their per-row scales, dequantize in the layer's dtype."""
+        flat = input_.reshape(-1)
+        out_dtype = getattr(layer, "params_dtype", None) or getattr(layer, "orig_dtype", None) or torch.bfloat16
+        w = torch.index_select(layer.weight, 0, flat).to(out_dtype)
+        s = torch.index_select(layer.weight_scale.reshape(-1), 0, flat).to(out_dtype).unsqueeze(-1)
+        return (w * s).reshape(*input_.shape, -1)
+
+    def tie_weights(self, layer, embed_tokens):
+        """`fp8.py:1700-1704`: share the embedding's codes and scales."""
+        layer.weight = embed_tokens.weight
+        layer.weight_scale = embed_tokens.weight_scale
+        setattr(layer, KEEP_VLLM_LAYOUT_ATTR, True)
+        return layer
 
 
 class Fp8MoEMethod:
@@ -302,6 +337,9 @@ class Fp8MoEMethod:
                     E, (2 * I + bh - 1) // bh, (H + bw - 1) // bw, dtype=torch.float32)))
                 layer.register_parameter("w2_weight_scale_inv", _param(torch.empty(
                     E, (H + bh - 1) // bh, (I + bw - 1) // bw, dtype=torch.float32)))
+            elif getattr(self.quant_config, "is_channel_quant", False):
+                layer.register_parameter("w13_weight_scale", _param(torch.ones(E, 2 * I, 1, dtype=torch.float32)))
+                layer.register_parameter("w2_weight_scale", _param(torch.ones(E, H, 1, dtype=torch.float32)))
             else:
                 layer.register_parameter("w13_weight_scale", _param(torch.ones(E, 2, dtype=torch.float32)))
                 layer.register_parameter("w2_weight_scale", _param(torch.ones(E, dtype=torch.float32)))
@@ -433,6 +471,13 @@ class Fp8MoEMethod:
         return moe_forward(layer, x, router_logits, layer.w13_weight, layer.w2_weight, layer.w13_weight_scale,
                            layer.w2_weight_scale, None, None, layer._qmoe_format,
                            skip_padded_tokens=envs.TPU_MOE_SKIP_PADDED_TOKENS, input_ids=input_ids)
+
+
+def _is_embedding(layer) -> bool:
+    """A vocab embedding table (vLLM's VocabParallelEmbedding or a subclass,
+    e.g. ParallelLMHead), `fp8.py:1612-1614, 1679`."""
+    return any(c.__name__ == "VocabParallelEmbedding" for c in type(layer).__mro__) or bool(
+        getattr(layer, "_qmoe_embedding", False))
 
 
 def _activation(layer):
