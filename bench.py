@@ -775,8 +775,9 @@ def profile_decode(args):
 
 def profile_moe(args):
     """rocprofv3 target: 20 MoE layers at T=1 each for cfg 3 (GPT-OSS,
-    MXFP4) and cfg 4 (DeepSeek-V3 routed experts, 128x128 FP8), after 3
-    warm-up layers."""
+    MXFP4) and cfg 4 (DeepSeek-V3 routed experts, 128x128 FP8), then 20 of
+    cfg 4's fused decode op (routing launch + shared and routed experts),
+    after 3 warm-up layers each."""
     import torch
 
     from qmoe.layers.fused_moe import moe_forward
@@ -807,7 +808,17 @@ def profile_moe(args):
     for _ in range(23):
         moe_forward(lcfg, x, logits, w13, w2, s13, s2, None, None, "fp8_block")
     torch.cuda.synchronize()
-    log("profile target done: cfg3 / cfg4 MoE T=1 x23 each")
+    # the fused decode op (shared expert + routed experts) on the same layer
+    from qmoe import ops
+
+    sh13, ss13 = fp8_weights(2 * I, H, gen, tiles=True)
+    sh2, ss2 = fp8_weights(H, I, gen, tiles=True)
+    for _ in range(23):
+        tw, ti = ops.moe_route(logits, k, "sigmoid", True, bias=bias, routed_scaling_factor=1.0,
+                               num_expert_group=8, topk_group=4)
+        ops.moe_decode(x, w13, w2, s13, s2, sh13, ss13, sh2, ss2, None, tw, ti, routed_scale=2.5, weight_blocks=128)
+    torch.cuda.synchronize()
+    log("profile target done: cfg3 / cfg4 MoE T=1 x23 each, cfg4 decode op T=1 x23")
 
 
 def vendor_scaled_mm(xq, wq, xs, ws):

@@ -59,6 +59,64 @@ def test_route_sigmoid_bias(dev, grouped, T):
     np.testing.assert_allclose(w.float().cpu().numpy(), w_ref, rtol=8e-3, atol=1e-6)
 
 
+@pytest.mark.parametrize("T,E,k,scoring,ng,tg,use_bias", [
+    (7, 512, 8, "sigmoid", 8, 3, True),        # groups of 64 (one slot each)
+    (9, 384, 8, "sigmoid", 6, 2, True),        # groups of 64, 6 of 8 slots hold experts
+    (1, 256, 8, "sigmoid", 32, 8, True),       # groups of 8
+    (5, 128, 8, "sigmoid", 64, 16, True),      # groups of 2
+    (6, 128, 4, "softmax", 32, 4, False),      # groups of 4, group score = max
+    (4, 64, 6, "softmax", 64, 20, False),      # groups of 1
+    (5, 160, 6, "softmax", 8, 3, False),       # groups of 20 (not a power of two)
+    (6, 96, 6, "sqrtsoftplus", 6, 3, True),    # groups of 16, half of slot 1 empty
+])
+@pytest.mark.parametrize("ties", [False, True])
+def test_route_grouped_group_sizes(dev, T, E, k, scoring, ng, tg, use_bias, ties):
+    """Grouped routing for every group-size regime of the kernel (DPP within a
+    row, row broadcasts for 32 / 64, the LDS loop otherwise), against the
+    oracle; `ties` draws logits and bias from a coarse grid so that choice and
+    group scores tie exactly (lowest expert / group wins)."""
+    from qmoe import ops
+
+    print(f"route grouped T={T} E={E} k={k} {scoring} groups=({ng},{tg}) bias={use_bias} ties={ties}", flush=True)
+    rng = np.random.default_rng(T * 7 + E + ng + ties)
+    if ties:
+        logits = (rng.integers(-4, 5, (T, E)) * 0.25).astype(np.float32)
+        bias = (rng.integers(-2, 3, E) * 0.125).astype(np.float32) if use_bias else None
+    else:
+        logits = codecs.bf16_round(rng.standard_normal((T, E)).astype(np.float32))
+        bias = (rng.standard_normal(E) * 0.1).astype(np.float32) if use_bias else None
+    rsf = 2.5 if use_bias else 1.0
+    w_ref, ids_ref = routing.grouped_topk(logits, k, True, ng, tg, scoring, bias, rsf)
+    w, ids = ops.moe_route(_t(logits, dev, torch.bfloat16), k, scoring, True,
+                           bias=_t(bias, dev) if bias is not None else None, routed_scaling_factor=rsf,
+                           num_expert_group=ng, topk_group=tg)
+    np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
+    np.testing.assert_allclose(w.float().cpu().numpy(), w_ref, rtol=8e-3, atol=1e-6)
+    if T * k <= 64 and T <= 16:
+        w2, ids2, _ = ops.moe_route_dispatch(_t(logits, dev, torch.bfloat16), k, scoring, True,
+                                             bias=_t(bias, dev) if bias is not None else None,
+                                             routed_scaling_factor=rsf, num_expert_group=ng, topk_group=tg)
+        np.testing.assert_array_equal(ids2.cpu().numpy(), ids_ref)
+        np.testing.assert_array_equal(w2.view(torch.int16).cpu().numpy(), w.view(torch.int16).cpu().numpy())
+
+
+@pytest.mark.parametrize("scoring,use_bias", [("sigmoid", True), ("softmax", False)])
+def test_route_plain_ties(dev, scoring, use_bias):
+    """Plain top-k with exact ties across and inside slots: lowest id first."""
+    from qmoe import ops
+
+    print(f"route plain ties {scoring}", flush=True)
+    rng = np.random.default_rng(11)
+    T, E, k = 12, 320, 8
+    logits = (rng.integers(-3, 4, (T, E)) * 0.5).astype(np.float32)
+    bias = (rng.integers(-1, 2, E) * 0.25).astype(np.float32) if use_bias else None
+    w_ref, ids_ref = routing.select_experts(logits, k, True, scoring, bias, 1.0)
+    w, ids = ops.moe_route(_t(logits, dev, torch.bfloat16), k, scoring, True,
+                           bias=_t(bias, dev) if bias is not None else None)
+    np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
+    np.testing.assert_allclose(w.float().cpu().numpy(), w_ref, rtol=8e-3, atol=1e-6)
+
+
 def test_rowmax_select_nan_and_sentinel_rows(dev):
     # tests/kernels/test_router_topk.py:101-135 (NaN, -inf, -FLT_MAX rows)
     from qmoe.layers.moe_routing import rowmax_select

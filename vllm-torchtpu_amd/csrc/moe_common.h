@@ -18,14 +18,20 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
 
+// Exclusive prefix sum over the wavefront (and the total), by DPP: row_shr
+// 1, 2, 4, 8 inside each 16-lane row (lanes whose source falls outside the
+// row add the `old` 0), then row_bcast:15 adds a row's last lane to the next
+// row (rows 1, 3) and row_bcast:31 adds lane 31 to rows 2 and 3.
 __device__ __forceinline__ int wave_excl_scan(int v, int lane, int& total) {
+  (void)lane;
   int x = v;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int y = __shfl_up(x, o, 64);
-    if (lane >= o) x += y;
-  }
-  total = __shfl(x, 63, 64);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, false);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, false);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, false);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);
+  total = __builtin_amdgcn_readlane(x, 63);
   return x - v;
 }
 

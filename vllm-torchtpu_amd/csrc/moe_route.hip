@@ -11,10 +11,11 @@
 // rounded score), so that a bias-corrected choice score -- compared exactly
 // -- is reproducible on any host that evaluates the same definition.
 //
-// The kernel is instantiated per (slots, scoring rule, grouped): a decode
-// step runs it on one CU with a cold instruction cache, so its time is
-// mostly instruction fetch, and each instantiation carries only the code of
-// its own rule.
+// The kernel is instantiated per (slots, scoring rule, grouped). A decode
+// step routes one token with one wavefront, so the time is the latency of a
+// dependent chain of cross-lane steps: those are DPP moves and readlanes (no
+// LDS shuffles), the expert holding a pass's max comes from ballots, and
+// lane-dependent choices are selects rather than divergent branches.
 
 #include "moe_common.h"
 
@@ -47,25 +48,64 @@ __device__ __forceinline__ void top2_merge(float& m1, float& m2, float o1, float
   m2 = lo;
 }
 
+// The selection compares order keys: the int whose signed order is the
+// float order (non-NaN input; -0.0 is taken as +0.0, so equal floats give
+// equal keys). Integer max / min need no NaN quieting, so a DPP move folds
+// into the max, and uniform keys reduce with scalar instructions.
+__device__ __forceinline__ int fkey(float f) {
+  const int b = __float_as_int(f + 0.0f);
+  return b >= 0 ? b : b ^ 0x7fffffff;
+}
+__device__ __forceinline__ float kfloat(int k) { return __int_as_float(k >= 0 ? k : k ^ 0x7fffffff); }
+constexpr int kMinKey = (int)0x80800000u;  // fkey(-FLT_MAX): taken, or no expert
+constexpr int kNoKey = (int)0x80000000u;   // below every key: the empty side of a top-2
+
+__device__ __forceinline__ void top2_merge_k(int& m1, int& m2, int o1, int o2) {
+  const int hi = max(m1, o1);
+  const int lo = max(min(m1, o1), max(m2, o2));
+  m1 = hi;
+  m2 = lo;
+}
+
 using qmoe_moe::wave_lds_sync;
 
-// Cross-lane reductions without LDS round trips: DPP moves inside each
-// 16-lane row (xor-1 and xor-2 inside quads, then the half-row and row
-// mirrors; each step pairs lanes holding disjoint partial results, so every
-// lane of a row ends with the row's result), then the four row results read
-// into scalars. The results are wave-uniform.
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+// Cross-lane steps are DPP moves (a VALU operand, no LDS round trip) and
+// v_readlane into scalars. DPP controls used here:
+//   0xB1 quad_perm [1,0,3,2] (lane ^ 1), 0x4E quad_perm [2,3,0,1] (lane ^ 2),
+//   0x141 row_half_mirror (i <-> 7 - i inside 8 lanes), 0x140 row_mirror
+//   (i <-> 15 - i inside a 16-lane row), 0x142 row_bcast:15 (lane 15 of a row
+//   to the whole next row), 0x143 row_bcast:31 (lane 31 to rows 2 and 3).
+// The first four pair lanes holding disjoint partial results, so after them
+// every lane of a row holds the row's result; rows disabled by the row mask
+// receive `old`.
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ float dpp_f(float v, float old = 0.0f) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL, ROWS, 0xF, false));
 }
 template <int CTRL>
-__device__ __forceinline__ int dpp_i(int v) {
-  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+__device__ __forceinline__ double dpp_d(double v) {
+  const uint64_t u = (uint64_t)__double_as_longlong(v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, 0xF, 0xF, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, 0xF, 0xF, false);
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ int dpp_i(int v, int old = 0) {
+  return __builtin_amdgcn_update_dpp(old, v, CTRL, ROWS, 0xF, false);
 }
 __device__ __forceinline__ float lane_f(float v, int l) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
+__device__ __forceinline__ double lane_d(double v, int l) {
+  const uint64_t u = (uint64_t)__double_as_longlong(v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, l);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), l);
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
 
+// Wave-uniform max / sum over all 64 lanes (row all-reduce by DPP, then the
+// four row results read into scalars).
 __device__ __forceinline__ float wave_max_u(float v) {
   v = fmaxf(v, dpp_f<0xB1>(v));
   v = fmaxf(v, dpp_f<0x4E>(v));
@@ -73,16 +113,14 @@ __device__ __forceinline__ float wave_max_u(float v) {
   v = fmaxf(v, dpp_f<0x140>(v));
   return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
 }
-
-__device__ __forceinline__ int wave_min_u(int v) {
-  v = min(v, dpp_i<0xB1>(v));
-  v = min(v, dpp_i<0x4E>(v));
-  v = min(v, dpp_i<0x141>(v));
-  v = min(v, dpp_i<0x140>(v));
-  return min(min(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
-             min(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+__device__ __forceinline__ int wave_max_k(int v) {
+  v = max(v, dpp_i<0xB1>(v));
+  v = max(v, dpp_i<0x4E>(v));
+  v = max(v, dpp_i<0x141>(v));
+  v = max(v, dpp_i<0x140>(v));
+  return max(max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+             max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
 }
-
 __device__ __forceinline__ float wave_sum_u(float v) {
   v = v + dpp_f<0xB1>(v);
   v = v + dpp_f<0x4E>(v);
@@ -90,45 +128,42 @@ __device__ __forceinline__ float wave_sum_u(float v) {
   v = v + dpp_f<0x140>(v);
   return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
 }
-
-// (value, index) argmax over the wavefront: largest value, lowest index
-// among the lanes holding it (values are never NaN here). Uniform result.
-__device__ __forceinline__ void wave_argmax(float& v, int& i) {
-  const float m = wave_max_u(v);
-  i = wave_min_u(v == m ? i : 0x7fffffff);
-  v = m;
+__device__ __forceinline__ double wave_sum_du(double v) {
+  v = v + dpp_d<0xB1>(v);
+  v = v + dpp_d<0x4E>(v);
+  v = v + dpp_d<0x141>(v);
+  v = v + dpp_d<0x140>(v);
+  return (lane_d(v, 0) + lane_d(v, 16)) + (lane_d(v, 32) + lane_d(v, 48));
 }
 
-// Top-2 all-reduce inside aligned groups of G = 2^n <= 64 lanes.
-__device__ __forceinline__ void group_top2(float& m1, float& m2, int G) {
-  if (G > 1) top2_merge(m1, m2, dpp_f<0xB1>(m1), dpp_f<0xB1>(m2));
-  if (G > 2) top2_merge(m1, m2, dpp_f<0x4E>(m1), dpp_f<0x4E>(m2));
-  if (G > 4) top2_merge(m1, m2, dpp_f<0x141>(m1), dpp_f<0x141>(m2));
-  if (G > 8) top2_merge(m1, m2, dpp_f<0x140>(m1), dpp_f<0x140>(m2));
-  if (G > 16) top2_merge(m1, m2, __shfl_xor(m1, 16, 64), __shfl_xor(m2, 16, 64));
-  if (G > 32) top2_merge(m1, m2, __shfl_xor(m1, 32, 64), __shfl_xor(m2, 32, 64));
-}
-
-// One rowmax pass over the lane's slots (values already clamped to >= kNeg,
-// masked entries hold -FLT_MAX). Returns the wave-wide max and its lowest id.
+// Per slot, the lanes that hold an expert (e = 64 * slot + lane < E).
 template <int S>
-__device__ __forceinline__ void rowmax_pass(const float (&cur)[kMaxSlots], int lane, int E, float& mv,
-                                            int& mi) {
-  float v = -3.402823466e38f;
-  int idx = 0x7fffffff;
+__device__ __forceinline__ void expert_lanes(int E, uint64_t (&vm)[kMaxSlots]) {
 #pragma unroll
   for (int j = 0; j < S; ++j) {
-    const int e = j * 64 + lane;
-    if (e < E && (cur[j] > v)) {
-      v = cur[j];
-      idx = e;
-    }
+    const int n = E - j * 64;
+    vm[j] = n >= 64 ? ~0ull : (n <= 0 ? 0ull : ((1ull << n) - 1ull));
   }
-  // lanes with no expert contribute (-FLT_MAX, INT_MAX); a real expert
-  // holding -FLT_MAX ties on value and wins on index
-  wave_argmax(v, idx);
-  mv = v;
-  mi = idx;
+}
+
+// One pass of the sort-free top-k over order keys: the row max m
+// (wave-uniform) and the lowest expert holding it, found from one ballot per
+// slot (the lowest slot with a hit, then its lowest lane). Lanes without an
+// expert hold the key of -FLT_MAX and are left out of the ballots, so a real
+// expert holding -FLT_MAX wins a tie with them.
+template <int S>
+__device__ __forceinline__ void top_pass(const int (&cur)[kMaxSlots], const uint64_t (&vm)[kMaxSlots], int& m,
+                                         int& mi) {
+  int v = cur[0];
+#pragma unroll
+  for (int j = 1; j < S; ++j) v = max(v, cur[j]);
+  m = wave_max_k(v);
+  mi = 0x7fffffff;
+#pragma unroll
+  for (int j = S - 1; j >= 0; --j) {
+    const uint64_t b = __ballot(cur[j] == m) & vm[j];
+    if (b) mi = j * 64 + (int)__builtin_ctzll(b);
+  }
 }
 
 // Scores of token t's row, expert e in lane e % 64, slot e / 64 (calling
@@ -138,17 +173,26 @@ template <int S, int SCORING>
 __device__ __forceinline__ void row_scores(const void* __restrict__ logits, int logits_f32, int64_t t, int E,
                                            float (&s)[kMaxSlots]) {
   const int lane = threadIdx.x & 63;
+  // every load of the row issued before the first use (the dtype branch is
+  // uniform and outside the slot loop); lanes past E load expert E - 1 and
+  // drop it
   float x[kMaxSlots];
+  if (logits_f32) {
 #pragma unroll
-  for (int j = 0; j < S; ++j) {
-    const int e = j * 64 + lane;
-    float v = 0.0f;
-    if (e < E) {
-      v = logits_f32 ? static_cast<const float*>(logits)[t * E + e]
-                     : bf16_to_f32(static_cast<const uint16_t*>(logits)[t * E + e]);
+    for (int j = 0; j < S; ++j) {
+      const int e = j * 64 + lane;
+      x[j] = static_cast<const float*>(logits)[t * E + (e < E ? e : E - 1)];
     }
-    x[j] = v;
+  } else {
+#pragma unroll
+    for (int j = 0; j < S; ++j) {
+      const int e = j * 64 + lane;
+      x[j] = bf16_to_f32(static_cast<const uint16_t*>(logits)[t * E + (e < E ? e : E - 1)]);
+    }
   }
+#pragma unroll
+  for (int j = 0; j < S; ++j)
+    if (j * 64 + lane >= E) x[j] = 0.0f;
   if constexpr (SCORING == 0) {  // softmax in float64
     float mx = -__builtin_inff();
     bool nan = false;
@@ -166,7 +210,7 @@ __device__ __forceinline__ void row_scores(const void* __restrict__ logits, int 
       ex[j] = (j * 64 + lane < E) ? exp((double)x[j] - (double)mx) : 0.0;
       sum += ex[j];
     }
-    for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+    sum = wave_sum_du(sum);
     const int anynan = __any(nan);
 #pragma unroll
     for (int j = 0; j < S; ++j) s[j] = anynan ? __builtin_nanf("") : (float)(ex[j] / sum);
@@ -174,13 +218,16 @@ __device__ __forceinline__ void row_scores(const void* __restrict__ logits, int 
 #pragma unroll
     for (int j = 0; j < S; ++j) s[j] = score_of<SCORING>(x[j]);
   }
-
 }
 
+constexpr int kChoiceLds = kMaxSlots * 64 + 64;  // floats of LDS scratch per wavefront
+
 // Routes token t with the calling wavefront (all 64 lanes). `ch` is this
-// wavefront's LDS scratch (kMaxSlots * 64 floats, grouped selection with
-// groups that are not a power of two <= 64). When lds_ids is given, the
-// token's ids and bf16 weights also go to lds_ids / lds_w [t * topk + j].
+// wavefront's LDS scratch of kChoiceLds floats (grouped selection: the
+// group scores, and the choice scores when groups are not a power of two).
+// When lds_ids is given, the token's ids and bf16 weights also go to
+// lds_ids / lds_w [t * topk + j]. The selection is branch-free per lane:
+// lane-dependent choices are selects, the remaining branches are uniform.
 template <int S, int SCORING, bool GROUPED>
 __device__ __forceinline__ void route_token(const void* __restrict__ logits, int logits_f32, int64_t t, int E,
                                             int topk, const float* __restrict__ bias, int renormalize, float rsf,
@@ -188,74 +235,91 @@ __device__ __forceinline__ void route_token(const void* __restrict__ logits, int
                                             int32_t* __restrict__ out_ids, float* ch, int32_t* lds_ids,
                                             uint16_t* lds_w) {
   const int lane = threadIdx.x & 63;
+  constexpr float kMin = -3.402823466e38f;  // -FLT_MAX
+  const int neg_key = fkey(kNeg);
 
+  uint64_t vm[kMaxSlots];
+  expert_lanes<S>(E, vm);
+  // bias loads issued with the row's loads
+  float bv[kMaxSlots];
+  if (bias) {
+#pragma unroll
+    for (int j = 0; j < S; ++j) bv[j] = bias[j * 64 + lane < E ? j * 64 + lane : E - 1];
+  }
   float s[kMaxSlots];
   row_scores<S, SCORING>(logits, logits_f32, t, E, s);
 
-  // choice scores
-  float c[kMaxSlots];
+  // keys of the choice scores, clamped to >= kNeg (NaN included)
+  int cur[kMaxSlots];
 #pragma unroll
   for (int j = 0; j < S; ++j) {
-    const int e = j * 64 + lane;
-    c[j] = (bias && e < E) ? s[j] + bias[e] : s[j];
+    const float c = bias ? s[j] + bv[j] : s[j];
+    cur[j] = j * 64 + lane < E ? fkey(c > kNeg ? c : kNeg) : kMinKey;
   }
-
-  float cur[kMaxSlots];
-#pragma unroll
-  for (int j = 0; j < S; ++j) cur[j] = c[j] > kNeg ? c[j] : kNeg;
 
   if constexpr (GROUPED) {
     const int gsize = E / num_group;
+    float* gsl = ch + kMaxSlots * 64;  // group scores
     // group score: the top choice score, or the sum of the top two when a
     // correction bias is given
-    float gs = -3.402823466e38f;
-    if (gsize <= 64 && (gsize & (gsize - 1)) == 0) {
-      // power-of-two groups inside a slot: top-2 by a butterfly over the
-      // group's lanes, then lane g fetches group g's result
-      float res[S];
+    const bool two = bias != nullptr && gsize >= 2;
+    const bool pow2 = gsize <= 64 && (gsize & (gsize - 1)) == 0;
+    int gl = 0;
+    if (pow2) {
+      gl = __builtin_ctz((unsigned)gsize);
+      // power-of-two groups are aligned inside a slot: top-2 all-reduce over
+      // the group's lanes by DPP (rows, then row_bcast into the later rows),
+      // leaving the group's result in its last lane
+      int m1[kMaxSlots], m2[kMaxSlots];
 #pragma unroll
       for (int j = 0; j < S; ++j) {
-        float m1 = j * 64 + lane < E ? cur[j] : -__builtin_inff();
-        float m2 = -__builtin_inff();
-        group_top2(m1, m2, gsize);
-        res[j] = bias ? (gsize >= 2 ? m1 + m2 : m1) : m1;
+        m1[j] = cur[j];
+        m2[j] = kNoKey;
       }
-      const int first = (lane < num_group ? lane : 0) * gsize;  // group's first expert
-      float v = 0.0f;
+#define QMOE_GROUP_STEP(CTRL, ROWS)                                                                  \
+  _Pragma("unroll") for (int j = 0; j < S; ++j) {                                                    \
+    const int o1 = dpp_i<CTRL, ROWS>(m1[j], kNoKey), o2 = dpp_i<CTRL, ROWS>(m2[j], kNoKey);          \
+    top2_merge_k(m1[j], m2[j], o1, o2);                                                              \
+  }
+      if (gsize > 1) { QMOE_GROUP_STEP(0xB1, 0xF) }
+      if (gsize > 2) { QMOE_GROUP_STEP(0x4E, 0xF) }
+      if (gsize > 4) { QMOE_GROUP_STEP(0x141, 0xF) }
+      if (gsize > 8) { QMOE_GROUP_STEP(0x140, 0xF) }
+      if (gsize > 16) { QMOE_GROUP_STEP(0x142, 0xA) }
+      if (gsize > 32) { QMOE_GROUP_STEP(0x143, 0x8) }
+#undef QMOE_GROUP_STEP
+      const bool last = ((lane + 1) & (gsize - 1)) == 0;
 #pragma unroll
       for (int j = 0; j < S; ++j) {
-        const float r = __shfl(res[j], first & 63, 64);
-        if (j == (first >> 6)) v = r;
+        const int g = (j * 64 + lane) >> gl;
+        if (last && g < num_group) gsl[g] = two ? kfloat(m1[j]) + kfloat(m2[j]) : kfloat(m1[j]);
       }
-      if (lane < num_group) gs = v;
     } else {
 #pragma unroll
       for (int j = 0; j < S; ++j)
-        if (j * 64 + lane < E) ch[j * 64 + lane] = cur[j];
+        if (j * 64 + lane < E) ch[j * 64 + lane] = kfloat(cur[j]);
       wave_lds_sync();
       if (lane < num_group) {
         float m1 = -__builtin_inff(), m2 = -__builtin_inff();
         for (int i = 0; i < gsize; ++i) top2_merge(m1, m2, ch[lane * gsize + i], -__builtin_inff());
-        gs = bias ? (gsize >= 2 ? m1 + m2 : m1) : m1;
+        gsl[lane] = two ? m1 + m2 : m1;
       }
     }
-    // top `topk_group` groups (rowmax order over group scores)
-    float gcur = lane < num_group ? (gs > kNeg ? gs : kNeg) : -3.402823466e38f;
-    bool keep = false;
-    for (int p = 0; p < topk_group; ++p) {
-      float v = gcur;
-      int i = lane < num_group ? lane : 0x7fffffff;
-      wave_argmax(v, i);
-      if (lane == i) {
-        keep = true;
-        gcur = -3.402823466e38f;
-      }
+    wave_lds_sync();
+    // the `topk_group` best groups: rank by (score desc, group asc), scores
+    // clamped to >= kNeg -- the set k row-max passes over the groups pick
+    const float mine = lane < num_group ? fmaxf(gsl[lane], kNeg) : kMin;
+    int rank = 0;
+    for (int h = 0; h < num_group; ++h) {
+      const float o = fmaxf(gsl[h], kNeg);
+      rank += (o > mine || (o == mine && h < lane)) ? 1 : 0;
     }
-    const uint64_t kept_groups = __ballot(keep);
+    const uint64_t kept = __ballot(lane < num_group && rank < topk_group);
 #pragma unroll
     for (int j = 0; j < S; ++j) {
       const int e = j * 64 + lane;
-      if (e < E && !((kept_groups >> (e / gsize)) & 1)) cur[j] = kNeg;
+      const int g = pow2 ? (e >> gl) : e / gsize;
+      if (e < E && !((kept >> g) & 1)) cur[j] = neg_key;
     }
   }
   const bool gather = bias != nullptr || GROUPED;
@@ -264,27 +328,25 @@ __device__ __forceinline__ void route_token(const void* __restrict__ logits, int
   float myw = 0.0f;
   int myid = 0;
   for (int p = 0; p < topk; ++p) {
-    float mv;
-    int mi;
-    rowmax_pass<S>(cur, lane, E, mv, mi);  // wave-uniform results
+    int mk, mi;
+    top_pass<S>(cur, vm, mk, mi);  // wave-uniform results
+    const float mv = kfloat(mk);
     if (p == 0) first = mv;
-    // weight: the pass value for plain top-k, the unbiased score otherwise
-    float w = mv;
-    if (gather) {
-      const int src_slot = mi >> 6;
-      float sv = 0.0f;
+    myid = lane == p ? mi : myid;
+    myw = lane == p ? mv : myw;
 #pragma unroll
-      for (int j = 0; j < S; ++j)
-        if (j == src_slot) sv = s[j];
-      w = lane_f(sv, mi & 63);
-    }
-    if (lane == p) {
-      myid = mi;
-      myw = w;
-    }
+    for (int j = 0; j < S; ++j) cur[j] = j * 64 + lane == mi ? kMinKey : cur[j];
+  }
+  // weight: the pass value for plain top-k, the unbiased score otherwise
+  // (lane p fetches its expert's score from the lane that holds it)
+  if (gather) {
+    float sv = 0.0f;
 #pragma unroll
-    for (int j = 0; j < S; ++j)
-      if (j * 64 + lane == mi) cur[j] = -3.402823466e38f;
+    for (int j = 0; j < S; ++j) {
+      const float v = __shfl(s[j], myid & 63, 64);
+      sv = (myid >> 6) == j ? v : sv;
+    }
+    myw = sv;
   }
   if (lane < topk) out_ids[t * topk + lane] = myid;
   // a plain top-k row with no score above the sentinel is poisoned (NaN)
@@ -313,7 +375,7 @@ __global__ __launch_bounds__(256) void route_kernel(const void* __restrict__ log
                                                     void* __restrict__ out_w, int w_f32,
                                                     int32_t* __restrict__ out_ids) {
   const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  __shared__ float choice_lds[GROUPED ? 4 : 1][GROUPED ? kMaxSlots * 64 : 1];
+  __shared__ float choice_lds[GROUPED ? 4 : 1][GROUPED ? kChoiceLds : 1];
   if (t >= T) return;
   route_token<S, SCORING, GROUPED>(logits, logits_f32, t, E, topk, bias, renormalize, rsf, num_group, topk_group,
                                    out_w, w_f32, out_ids, choice_lds[GROUPED ? threadIdx.x >> 6 : 0], nullptr,
@@ -331,7 +393,7 @@ __global__ __launch_bounds__(1024) void route_dispatch_kernel(
     int32_t* __restrict__ out_ids, int skip_padded, int32_t* __restrict__ sorted_idx, int32_t* __restrict__ revert,
     int32_t* __restrict__ token_sorted, int32_t* __restrict__ group_offs, int32_t* __restrict__ active,
     int32_t* __restrict__ num_active, uint16_t* __restrict__ sorted_weight) {
-  __shared__ float choice_lds[GROUPED ? 16 : 1][GROUPED ? kMaxSlots * 64 : 1];
+  __shared__ float choice_lds[GROUPED ? 16 : 1][GROUPED ? kChoiceLds : 1];
   __shared__ int32_t s_ids[64];
   __shared__ uint16_t s_w[64];
   __shared__ int cnt[64 * qmoe_moe::kPer];
