@@ -492,12 +492,12 @@ def sweep_moe(only):
                     continue
 
                 def decode_layer():
-                    # the fused decode op (shared + routed experts): routing
-                    # launch, then the op; routed_scaling_factor moves into it
-                    tw, ti = ops.moe_route(logits, k, "sigmoid", True, bias=bias, routed_scaling_factor=1.0,
-                                           num_expert_group=8, topk_group=4)
-                    return ops.moe_decode(x, w13, w2, s13, s2, sh13, ss13, sh2, ss2, None, tw, ti,
-                                          routed_scale=2.5, weight_blocks=128)
+                    # the fused decode op (shared + routed experts), routing
+                    # the tokens itself; routed_scaling_factor moves into it
+                    return ops.moe_decode_routed(x, logits, k, w13, w2, s13, s2, sh13, ss13, sh2, ss2, None,
+                                                 scoring_func="sigmoid", renormalize=True, bias=bias,
+                                                 routed_scaling_factor=1.0, num_expert_group=8, topk_group=4,
+                                                 routed_scale=2.5, weight_blocks=128)[0]
 
                 us = graph_time_us(decode_layer, iters=15)[0]
                 par = {}
@@ -776,8 +776,8 @@ def profile_decode(args):
 def profile_moe(args):
     """rocprofv3 target: 20 MoE layers at T=1 each for cfg 3 (GPT-OSS,
     MXFP4) and cfg 4 (DeepSeek-V3 routed experts, 128x128 FP8), then 20 of
-    cfg 4's fused decode op (routing launch + shared and routed experts),
-    after 3 warm-up layers each."""
+    cfg 4's fused decode op (routing inside its first launch, shared and
+    routed experts), after 3 warm-up layers each."""
     import torch
 
     from qmoe.layers.fused_moe import moe_forward
@@ -814,9 +814,9 @@ def profile_moe(args):
     sh13, ss13 = fp8_weights(2 * I, H, gen, tiles=True)
     sh2, ss2 = fp8_weights(H, I, gen, tiles=True)
     for _ in range(23):
-        tw, ti = ops.moe_route(logits, k, "sigmoid", True, bias=bias, routed_scaling_factor=1.0,
-                               num_expert_group=8, topk_group=4)
-        ops.moe_decode(x, w13, w2, s13, s2, sh13, ss13, sh2, ss2, None, tw, ti, routed_scale=2.5, weight_blocks=128)
+        ops.moe_decode_routed(x, logits, k, w13, w2, s13, s2, sh13, ss13, sh2, ss2, None, scoring_func="sigmoid",
+                              renormalize=True, bias=bias, routed_scaling_factor=1.0, num_expert_group=8,
+                              topk_group=4, routed_scale=2.5, weight_blocks=128)
     torch.cuda.synchronize()
     log("profile target done: cfg3 / cfg4 MoE T=1 x23 each, cfg4 decode op T=1 x23")
 

@@ -301,13 +301,28 @@ typedef struct qmoe_moe_decode_desc {
   const uint16_t* shared_gate;  /* bf16 [H], or NULL for an ungated shared expert */
   uint16_t* out;           /* bf16 [T][ldo] */
   int64_t ldo;
+  /* Routing by the call (optional; no counterpart in the reference, whose
+   * router runs before the decode kernel). With router_logits not NULL the
+   * call first routes the tokens -- qmoe_moe_route's rule and results for
+   * these arguments, bf16 weights -- and writes topk_ids / topk_weights,
+   * which are then outputs (weights_f32 must be 0). Up to 8 tokens are
+   * routed inside the first launch, more by a routing launch before it. */
+  const void* router_logits;     /* [T][E] bf16 (logits_f32 = 0) or f32 */
+  int logits_f32;
+  int scoring;                   /* as qmoe_moe_route */
+  const float* correction_bias;  /* [E] or NULL */
+  int renormalize;
+  float routed_scaling_factor;
+  int num_group;
+  int topk_group;
 } qmoe_moe_decode_desc;
 
 /* Workspace bytes of qmoe_moe_decode for this descriptor. */
 int qmoe_moe_decode_workspace_size(const qmoe_moe_decode_desc* d, int64_t* bytes);
 
-/* Four launches on `stream`; QMOE_ERR_ARG outside the envelope above,
- * QMOE_ERR_WORKSPACE when ws_bytes is below qmoe_moe_decode_workspace_size. */
+/* Four launches on `stream` (five when more than 8 tokens are routed by the
+ * call); QMOE_ERR_ARG outside the envelope above, QMOE_ERR_WORKSPACE when
+ * ws_bytes is below qmoe_moe_decode_workspace_size. */
 int qmoe_moe_decode(const qmoe_moe_decode_desc* d, void* workspace, int64_t ws_bytes, qmoe_stream_t stream);
 
 /*

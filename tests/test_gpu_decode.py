@@ -173,6 +173,49 @@ def test_repeat_calls_are_deterministic(dev):
         np.testing.assert_array_equal(_run(L, dev), a)
 
 
+# (T, E, k, scoring, groups, bias, tiles): T <= 8 routes inside the prep
+# launch (1, 2, 4 and 8 slots per row, group sizes 32, 16, 64 and 20), T > 8
+# through the router's own launch first
+ROUTED_CASES = [
+    (1, 256, 8, "sigmoid", (8, 4), True, True),
+    (3, 128, 4, "softmax", None, False, False),
+    (8, 64, 6, "sqrtsoftplus", None, True, True),
+    (5, 320, 6, "sigmoid", (5, 2), True, False),
+    (2, 160, 6, "softmax", (8, 3), False, True),
+    (6, 96, 4, "sigmoid", (6, 3), True, False),
+    (12, 96, 4, "softmax", (6, 3), False, True),
+]
+
+
+@pytest.mark.parametrize("T,E,k,scoring,groups,use_bias,tiles", ROUTED_CASES)
+def test_decode_routed_matches_route_then_decode(dev, T, E, k, scoring, groups, use_bias, tiles):
+    """`moe_decode_routed` (the op routes the tokens itself) gives bit for
+    bit the routes of `moe_route` and the output of `moe_decode` on them."""
+    from qmoe import ops
+
+    print(f"moe_decode_routed T={T} E={E} k={k} {scoring} groups={groups} bias={use_bias} tiles={tiles}",
+          flush=True)
+    H, I, Is = 1024, 256, 128
+    L = _layer(T * 13 + E, E, H, I, Is, T, k, tiles=tiles, gated=True)
+    rng = np.random.default_rng(E + T)
+    logits = _t(codecs.bf16_round(rng.standard_normal((T, E)).astype(np.float32)), dev, torch.bfloat16)
+    bias = _t((rng.standard_normal(E) * 0.1).astype(np.float32), dev) if use_bias else None
+    ng, tg = groups if groups else (1, 1)
+    rkw = dict(bias=bias, routed_scaling_factor=1.5 if use_bias else 1.0, num_expert_group=ng, topk_group=tg)
+    g = _t(L["shared_gate"], dev, torch.bfloat16)
+    wts = (_f8(L["w1q"], dev), _f8(L["w2q"], dev), _t(L["w1s"], dev), _t(L["w2s"], dev),
+           _f8(L["shared_w1q"], dev), _t(L["shared_w1s"], dev), _f8(L["shared_w2q"], dev),
+           _t(L["shared_w2s"], dev), g)
+    x = _t(L["hidden"], dev, torch.bfloat16)
+    wr, ir = ops.moe_route(logits, k, scoring, True, **rkw)
+    yr = ops.moe_decode(x, *wts, wr, ir, routed_scale=2.5, weight_blocks=L["weight_blocks"])
+    y, w, ids = ops.moe_decode_routed(x, logits, k, *wts, scoring_func=scoring, renormalize=True, **rkw,
+                                      routed_scale=2.5, weight_blocks=L["weight_blocks"])
+    np.testing.assert_array_equal(ids.cpu().numpy(), ir.cpu().numpy())
+    np.testing.assert_array_equal(w.view(torch.int16).cpu().numpy(), wr.view(torch.int16).cpu().numpy())
+    np.testing.assert_array_equal(y.view(torch.int16).cpu().numpy(), yr.view(torch.int16).cpu().numpy())
+
+
 @pytest.mark.parametrize("T,tiles", [(1, True), (1, False), (8, True), (16, False)])
 def test_decode_deepseek_v3_shapes(dev, T, tiles):
     """BASELINE config 4's layer (E 256, H 7168, I 2048, top-8, one shared
@@ -311,6 +354,14 @@ def test_armed_layer_serves_shared_plus_routed(dev, monkeypatch, gated, rsf):
         logits = codecs.bf16_round(rng.standard_normal((T, E)).astype(np.float32))
         got = method.apply_monolithic(layer, _t(x, dev, torch.bfloat16), _t(logits, dev, torch.bfloat16))
         ref, L = _layer_oracle(layer, mlp, x, logits, k, rsf, gated)
+        if T <= 8:
+            # the op routed the tokens itself: bit-equal to routing first
+            from qmoe.layers import moe_routing
+
+            xt, lt = _t(x, dev, torch.bfloat16), _t(logits, dev, torch.bfloat16)
+            tw, ti = moe_routing.route(layer, xt, lt)
+            two = fmd.fused_moe_decode(method, layer, xt, tw, ti)
+            np.testing.assert_array_equal(got.view(torch.int16).cpu().numpy(), two.view(torch.int16).cpu().numpy())
         got = got.float().cpu().numpy()
         if T <= 8:
             assert_close_rows(got, ref, f"armed T={T}", rel=1e-2)

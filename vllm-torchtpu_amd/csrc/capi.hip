@@ -260,7 +260,7 @@ int qmoe_run_route(const qmoe_gemm_desc* d, const QmoeRoute& r, GemmParams p, vo
   }
 }
 
-extern "C" int qmoe_abi_version(void) { return 5; }
+extern "C" int qmoe_abi_version(void) { return 6; }
 
 extern "C" int qmoe_gemm_workspace_size(const qmoe_gemm_desc* d, int64_t* bytes) {
   GemmParams p;

@@ -33,6 +33,7 @@
 #include <algorithm>
 
 #include "gemm_common.h"
+#include "moe_route.h"
 #include "stream_load.h"
 
 #include "qmoe.h"
@@ -47,6 +48,7 @@ using namespace qmoe_stream;
 constexpr int kPrep = 256;        // threads of the prep and quantization workgroups
 constexpr int kMaxTokens = 64;    // tokens of one fused decode call
 constexpr int kMaxExperts = 512;
+constexpr int kRouteInPrep = 8;   // tokens the prep launch routes itself (2 per wavefront)
 
 // Workspace carve-up (byte offsets, 256-aligned), shared by host and kernels.
 struct DecodeLayout {
@@ -110,14 +112,24 @@ struct PrepArgs {
   int32_t* map;
   uint32_t* bmax;
   int64_t bmax_words;
+  // in-launch routing (prep instantiations with S > 0 slots): the router's
+  // arguments, and where the ids and bf16 weights go
+  const void* logits;
+  int logits_f32, scoring, renormalize, num_group, topk_group;
+  const float* bias;
+  float rsf;
+  int32_t* ids_out;
+  uint16_t* w_out;
 };
 
 // The reference's route weight: rounded to the activation dtype (bf16), then
 // times routed_scale in float32 (`fused_moe_decode_kernel.py:639-641`).
+__device__ __forceinline__ float scaled_route_weight(const PrepArgs& a, float w_bf16) {
+  return a.routed_scale != 1.0f ? w_bf16 * a.routed_scale : w_bf16;
+}
 __device__ __forceinline__ float route_weight(const PrepArgs& a, int f) {
-  const float w = a.tw_f32 ? bf16_round(static_cast<const float*>(a.tw)[f])
-                           : bf16_to_f32(static_cast<const uint16_t*>(a.tw)[f]);
-  return a.routed_scale != 1.0f ? w * a.routed_scale : w;
+  return scaled_route_weight(a, a.tw_f32 ? bf16_round(static_cast<const float*>(a.tw)[f])
+                                         : bf16_to_f32(static_cast<const uint16_t*>(a.tw)[f]));
 }
 
 // Route f's row coefficient from the staged ids / weights, or 0 when it
@@ -138,27 +150,25 @@ __device__ __forceinline__ float route_coeff(const int* ids, const float* w, int
   return c;
 }
 
-// Exclusive scan of one int per thread over the workgroup (kPrep threads).
+// Exclusive scan of one int per thread over the workgroup (kPrep threads):
+// the wavefront scans by DPP, then the wavefront totals through LDS.
 __device__ __forceinline__ int prep_scan(int v, int* tmp, int& total) {
   constexpr int kW = kPrep / 64;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  int x = v;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int y = __shfl_up(x, o, 64);
-    if (lane >= o) x += y;
-  }
-  if (lane == 63) tmp[wave] = x;
+  int wtot = 0;
+  const int ex = qmoe_moe::wave_excl_scan(v, lane, wtot);
+  if (lane == 0) tmp[wave] = wtot;
   __syncthreads();
   int before = 0;
   total = 0;
 #pragma unroll
   for (int w = 0; w < kW; ++w) {
-    if (w < wave) before += tmp[w];
-    total += tmp[w];
+    const int c = tmp[w];
+    before += w < wave ? c : 0;
+    total += c;
   }
   __syncthreads();
-  return before + x - v;
+  return before + ex;
 }
 
 // Token t's hidden-state codes per (row, XB columns) in float32 (scale =
@@ -235,6 +245,10 @@ __device__ __forceinline__ void quant_token(const PrepArgs& a, int t) {
 
 constexpr int kMaxRoutes = kMaxTokens * 64;
 
+// S > 0: workgroup 0 first routes the step's tokens (S 64-expert slots per
+// row, at most kRouteInPrep tokens: wavefront w routes tokens w, w + 4), the
+// routes going to LDS for the dispatch and to ids_out / w_out.
+template <int S>
 __global__ __launch_bounds__(kPrep) void decode_prep_kernel(const PrepArgs a) {
   const int tid = threadIdx.x;
   // every workgroup clears its share of the block-maximum table
@@ -255,9 +269,22 @@ __global__ __launch_bounds__(kPrep) void decode_prep_kernel(const PrepArgs a) {
   __shared__ int slotpos[kMaxExperts];
   __shared__ int tmp[kPrep / 64];
   const int Nf = a.T * a.topk;
-  for (int f = tid; f < Nf; f += kPrep) {
-    s_ids[f] = a.ids[f];
-    s_w[f] = route_weight(a, f);
+  if constexpr (S > 0) {
+    __shared__ float route_lds[kPrep / 64][qmoe_route::kChoiceLds];
+    __shared__ uint16_t s_w16[kRouteInPrep * 64];
+    const int wave = tid >> 6;
+    const bool grouped = a.num_group > 1 && a.topk_group < a.num_group;
+    for (int t = wave; t < a.T; t += kPrep / 64)
+      qmoe_route::route_token_any<S>(a.scoring, grouped, a.logits, a.logits_f32, t, a.E, a.topk, a.bias,
+                                     a.renormalize, a.rsf, a.num_group, a.topk_group, a.w_out, a.ids_out,
+                                     route_lds[wave], s_ids, s_w16);
+    __syncthreads();
+    for (int f = tid; f < Nf; f += kPrep) s_w[f] = scaled_route_weight(a, bf16_to_f32(s_w16[f]));
+  } else {
+    for (int f = tid; f < Nf; f += kPrep) {
+      s_ids[f] = a.ids[f];
+      s_w[f] = route_weight(a, f);
+    }
   }
   for (int e = tid; e < a.E; e += kPrep) cnt[e] = 0;
   __syncthreads();
@@ -320,8 +347,12 @@ __global__ __launch_bounds__(kPrep) void decode_mid_quant_kernel(const float* __
                                                                  const int32_t* __restrict__ goffs, int E, int T,
                                                                  int I, int Is, int qb, int nbm,
                                                                  uint8_t* __restrict__ mq, float* __restrict__ msc) {
+  // every row bound R (no wait on the group offsets first): rows past the
+  // used count have block maxima 0 (cleared by prep) and their codes are
+  // never read
+  (void)goffs;
+  (void)E;
   const int R = blockIdx.x;
-  if (R >= goffs[E + 1]) return;
   const int width = R < T ? Is : I;
   const float* src = mid + (int64_t)R * I;
   uint8_t* dst = mq + (int64_t)R * I;
@@ -606,6 +637,10 @@ int decode_check(const qmoe_moe_decode_desc* d) {
   // 32-bit buffer offsets per expert slab and for the row buffers
   constexpr int64_t kLim = 0x7fffffff;
   if (2 * d->I * d->H > kLim || d->T * (d->topk + 1) * d->I * 4 > kLim) return QMOE_ERR_ARG;
+  // routing by the call: the router's envelope, bf16 weights written out
+  if (d->router_logits &&
+      (d->weights_f32 || !qmoe_route::route_args_ok(d->T, d->E, d->topk, d->scoring, d->num_group, d->topk_group)))
+    return QMOE_ERR_ARG;
   return QMOE_OK;
 }
 
@@ -650,7 +685,39 @@ extern "C" int qmoe_moe_decode(const qmoe_moe_decode_desc* d, void* workspace, i
   pa.map = reinterpret_cast<int32_t*>(ws + L.map);
   pa.bmax = reinterpret_cast<uint32_t*>(ws + L.bmax);
   pa.bmax_words = (int64_t)L.R * L.nbm;
-  hipLaunchKernelGGL(decode_prep_kernel, dim3((unsigned)(1 + T)), dim3(kPrep), 0, stream, pa);
+  // routing by the call: inside the prep launch for up to kRouteInPrep
+  // tokens, else the router's own launch first (same results either way)
+  int route_slots = 0;
+  if (d->router_logits) {
+    int32_t* ids = const_cast<int32_t*>(d->topk_ids);
+    uint16_t* tw = static_cast<uint16_t*>(const_cast<void*>(d->topk_weights));
+    if (T <= kRouteInPrep) {
+      route_slots = qmoe_route::route_slots(d->E);
+      pa.logits = d->router_logits;
+      pa.logits_f32 = d->logits_f32;
+      pa.scoring = d->scoring;
+      pa.renormalize = d->renormalize;
+      pa.num_group = d->num_group;
+      pa.topk_group = d->topk_group;
+      pa.bias = d->correction_bias;
+      pa.rsf = d->routed_scaling_factor;
+      pa.ids_out = ids;
+      pa.w_out = tw;
+    } else {
+      const int rc = qmoe_moe_route(d->router_logits, d->logits_f32, T, d->E, d->topk, d->scoring,
+                                    d->correction_bias, d->renormalize, d->routed_scaling_factor, d->num_group,
+                                    d->topk_group, tw, 0, ids, stream);
+      if (rc != QMOE_OK) return rc;
+    }
+  }
+  const dim3 pgrid((unsigned)(1 + T));
+  switch (route_slots) {
+    case 1: hipLaunchKernelGGL(decode_prep_kernel<1>, pgrid, dim3(kPrep), 0, stream, pa); break;
+    case 2: hipLaunchKernelGGL(decode_prep_kernel<2>, pgrid, dim3(kPrep), 0, stream, pa); break;
+    case 4: hipLaunchKernelGGL(decode_prep_kernel<4>, pgrid, dim3(kPrep), 0, stream, pa); break;
+    case 8: hipLaunchKernelGGL(decode_prep_kernel<8>, pgrid, dim3(kPrep), 0, stream, pa); break;
+    default: hipLaunchKernelGGL(decode_prep_kernel<0>, pgrid, dim3(kPrep), 0, stream, pa); break;
+  }
   if (hipGetLastError() != hipSuccess) return QMOE_ERR_LAUNCH;
 
   // gate_up: silu(gate) * up * coefficient, float32 rows + block maxima

@@ -9,7 +9,7 @@ import os
 
 _LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libqmoe.so")
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 QMOE_OK = 0
 STATUS_TEXT = {
@@ -95,6 +95,14 @@ class DecodeDesc(ctypes.Structure):
         ("shared_gate", _vp),
         ("out", _vp),
         ("ldo", _i64),
+        ("router_logits", _vp),
+        ("logits_f32", _i32),
+        ("scoring", _i32),
+        ("correction_bias", _vp),
+        ("renormalize", _i32),
+        ("routed_scaling_factor", _f32),
+        ("num_group", _i32),
+        ("topk_group", _i32),
     ]
 
 

@@ -14,7 +14,9 @@ has no shared expert, and its ``routed_scaling_factor`` moves into the op
 
 An armed layer's forward (`fused_moe_decode`) runs `ops.moe_decode` for
 steps of up to ``FUSED_MOE_DECODE_KERNEL_MAX_TOKENS`` tokens (capped at the
-kernel's 64) and above that what the runner would compute with the op off:
+kernel's 64) -- `fused_moe_decode_routed` with the routing folded into the
+op when the layer uses the plain or grouped rule -- and above that what the
+runner would compute with the op off:
 the GMM MoE path, the shared expert's linears and their sum
 (`fused_moe_decode.py:105-164`, `_gmm_layer`). One GPU: there is no
 all-reduce and no expert parallelism.
@@ -172,6 +174,31 @@ def _shared_expert(x, w1s, s1s, w2s, s2s, wg):
     out = quantized_matmul(mid, w2s.t(), s2s).float()
     if wg is not None:
         out = torch.sigmoid(x.float() @ wg.reshape(-1, 1).to(x.dtype).float()) * out
+    return out
+
+
+def fused_moe_decode_routed(quant_method, layer, x, router_logits, input_ids=None):
+    """Forward of an armed layer that routes inside the op: the same routes
+    as `moe_routing.route` (the layer's plain or grouped rule) and the same
+    output as `fused_moe_decode` on them, with the routing folded into the
+    op's first launch. None when the step is not served that way (a
+    model-supplied routing function, hash routing, non-bf16 hidden states,
+    or more tokens than the op takes)."""
+    from qmoe.layers import moe_routing
+
+    cfg = getattr(quant_method, FUSED_MOE_DECODE_OP_ATTR)
+    if (x.shape[0] > cfg["max_tokens"] or x.dtype != torch.bfloat16
+            or getattr(layer, "custom_routing_function", None) is not None
+            or (getattr(layer, "hash_indices_table", None) is not None and input_ids is not None)):
+        return None
+    bias, rsf, ng, tg = moe_routing.routing_params(layer)
+    w1s, s1s, w2s, s2s, wg = (getattr(layer, name) for name in _SHARED_BUFFERS)
+    out, _, _ = ops.moe_decode_routed(x, router_logits, layer.moe_config.experts_per_token, layer.w13_weight,
+                                      layer.w2_weight, layer.w13_weight_scale, layer.w2_weight_scale, w1s, s1s,
+                                      w2s, s2s, wg, scoring_func=layer.scoring_func,
+                                      renormalize=layer.renormalize, bias=bias, routed_scaling_factor=rsf,
+                                      num_expert_group=ng, topk_group=tg, routed_scale=cfg["routed_scale"],
+                                      weight_blocks=cfg["weight_blocks"])
     return out
 
 

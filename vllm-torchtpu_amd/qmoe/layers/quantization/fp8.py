@@ -466,6 +466,9 @@ class Fp8MoEMethod:
 
             # zero-weight (padding) routes add nothing to the op's sums, so
             # TPU_MOE_SKIP_PADDED_TOKENS needs no mask here
+            out = fmd.fused_moe_decode_routed(self, layer, x, router_logits, input_ids=input_ids)
+            if out is not None:
+                return out
             topk_weights, topk_ids = moe_routing.route(layer, x, router_logits, input_ids=input_ids)
             return fmd.fused_moe_decode(self, layer, x, topk_weights, topk_ids)
         return moe_forward(layer, x, router_logits, layer.w13_weight, layer.w2_weight, layer.w13_weight_scale,

@@ -468,15 +468,61 @@ def moe_decode(hidden, w1, w2, w1_scale, w2_scale, shared_w1, shared_w1_scale, s
     ungated shared expert. ``routed_scale`` multiplies the routed experts
     only. 1..64 tokens."""
     _require_gpu(hidden, w1, w2, topk_ids, topk_weights)
+    if tuple(topk_weights.shape) != tuple(topk_ids.shape):
+        raise ValueError("moe_decode: inconsistent weight / routing shapes")
+    ids = topk_ids.to(torch.int32).contiguous()
+    f32w = topk_weights.dtype == torch.float32
+    tw = topk_weights.contiguous() if f32w else topk_weights.to(torch.bfloat16).contiguous()
+    return _moe_decode_call(hidden, w1, w2, w1_scale, w2_scale, shared_w1, shared_w1_scale, shared_w2,
+                            shared_w2_scale, shared_gate_weight, tw, ids, routed_scale, weight_blocks, out, None)
+
+
+def moe_decode_routed(hidden, router_logits, top_k, w1, w2, w1_scale, w2_scale, shared_w1, shared_w1_scale,
+                      shared_w2, shared_w2_scale, shared_gate_weight, scoring_func="softmax", renormalize=True,
+                      bias=None, routed_scaling_factor=1.0, num_expert_group=1, topk_group=1, routed_scale=1.0,
+                      weight_blocks=None, out=None):
+    """`moe_route` + `moe_decode` in one call: the op routes the tokens
+    itself (for up to 8 tokens inside its first launch) with `moe_route`'s
+    rule and arguments, then runs the fused decode layer. Returns (out bf16
+    [T, H], topk_weights bf16 [T, k], topk_ids int32 [T, k]) -- the same
+    values as the two calls. No counterpart in the reference, whose router
+    runs before its decode kernel."""
+    _require_gpu(hidden, router_logits, bias)
+    if scoring_func not in _SCORING:
+        raise NotImplementedError(f"FusedMoE does not support {scoring_func} scoring function for TPU.")
+    x = router_logits.reshape(-1, router_logits.shape[-1])
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        x = x.float()
+    x = x.contiguous()
+    T, E = x.shape
+    if top_k > E:
+        raise ValueError(f"topk k={top_k} exceeds the expert count {E}")
+    if T != hidden.shape[0] or E != w1.shape[0]:
+        raise ValueError("moe_decode_routed: router logits must be [T, E]")
+    tw = torch.empty((T, top_k), dtype=torch.bfloat16, device=x.device)
+    ids = torch.empty((T, top_k), dtype=torch.int32, device=x.device)
+    b = bias.float().contiguous() if bias is not None else None
+    route = (x, b, _SCORING[scoring_func], renormalize, routed_scaling_factor, num_expert_group, topk_group)
+    out = _moe_decode_call(hidden, w1, w2, w1_scale, w2_scale, shared_w1, shared_w1_scale, shared_w2,
+                           shared_w2_scale, shared_gate_weight, tw, ids, routed_scale, weight_blocks, out, route)
+    return out, tw, ids
+
+
+def _moe_decode_call(hidden, w1, w2, w1_scale, w2_scale, shared_w1, shared_w1_scale, shared_w2, shared_w2_scale,
+                     shared_gate_weight, tw, ids, routed_scale, weight_blocks, out, route):
+    """Checks, the `qmoe_moe_decode_desc` and the call; `route` = (logits,
+    bias, scoring, renormalize, rsf, num_group, topk_group) when the op
+    routes (then `tw` / `ids` are its outputs)."""
+    _require_gpu(hidden, w1, w2, ids, tw)
     T, H = hidden.shape
     E, N1, H1 = w1.shape
     I = N1 // 2
     Is = shared_w2.shape[1]
-    k = topk_ids.shape[1]
+    k = ids.shape[1]
     if not 1 <= T <= DECODE_MAX_TOKENS:
         raise ValueError(f"moe_decode takes 1..{DECODE_MAX_TOKENS} tokens, got {T}")
     if H1 != H or tuple(w2.shape) != (E, H, I) or tuple(shared_w1.shape) != (2 * Is, H) or \
-            tuple(shared_w2.shape) != (H, Is) or tuple(topk_weights.shape) != (T, k):
+            tuple(shared_w2.shape) != (H, Is) or tuple(tw.shape) != (T, k):
         raise ValueError("moe_decode: inconsistent weight / routing shapes")
     for t, name in ((w1, "w1"), (w2, "w2"), (shared_w1, "shared_w1"), (shared_w2, "shared_w2")):
         if t.dtype != FP8 or not t.is_contiguous():
@@ -497,9 +543,6 @@ def moe_decode(hidden, w1, w2, w1_scale, w2_scale, shared_w1, shared_w1_scale, s
     x = hidden.to(torch.bfloat16).contiguous()
     if x.data_ptr() % 16:
         x = x.clone()  # the kernel reads 16-byte chunks
-    ids = topk_ids.to(torch.int32).contiguous()
-    f32w = topk_weights.dtype == torch.float32
-    tw = topk_weights.contiguous() if f32w else topk_weights.to(torch.bfloat16).contiguous()
     gate = None
     if shared_gate_weight is not None:
         if shared_gate_weight.numel() != H:
@@ -514,7 +557,7 @@ def moe_decode(hidden, w1, w2, w1_scale, w2_scale, shared_w1, shared_w1_scale, s
     d.T, d.H, d.I, d.I_shared, d.E, d.topk = T, H, I, Is, E, k
     d.topk_ids = _ptr(ids).value
     d.topk_weights = _ptr(tw).value
-    d.weights_f32 = int(f32w)
+    d.weights_f32 = int(tw.dtype == torch.float32)
     d.routed_scale = float(routed_scale)
     d.weight_blocks = 128 if tiles else 0
     d.w1, d.w2 = _ptr(w1).value, _ptr(w2).value
@@ -524,6 +567,16 @@ def moe_decode(hidden, w1, w2, w1_scale, w2_scale, shared_w1, shared_w1_scale, s
     d.shared_gate = _ptr(gate).value if gate is not None else None
     d.out = _ptr(out).value
     d.ldo = out.stride(0)
+    if route is not None:
+        lg, b, scoring, renorm, rsf, ng, tg = route
+        d.router_logits = _ptr(lg).value
+        d.logits_f32 = int(lg.dtype == torch.float32)
+        d.scoring = scoring
+        d.correction_bias = _ptr(b).value if b is not None else None
+        d.renormalize = int(bool(renorm))
+        d.routed_scaling_factor = float(rsf)
+        d.num_group = int(ng or 1)
+        d.topk_group = int(tg or 1)
     nbytes = ctypes.c_int64(0)
     check(lib.qmoe_moe_decode_workspace_size(ctypes.byref(d), ctypes.byref(nbytes)), "moe_decode (shape)")
     ws, ws_n = _workspace(hidden.device, nbytes.value)
