@@ -173,6 +173,28 @@ def test_repeat_calls_are_deterministic(dev):
         np.testing.assert_array_equal(_run(L, dev), a)
 
 
+@pytest.mark.parametrize("T,tiles", [(40, False), (64, True)])
+def test_split_down_ranges(dev, T, tiles):
+    """Above 16 tokens the down kernel cuts the active list into ranges
+    whose partial sums a last launch adds in range order: repeated calls
+    agree bit for bit, tokens with no valid route (and a step whose routes
+    are all invalid: one active slot, the shared expert) get the shared
+    expert alone, and the result meets the oracle bar."""
+    print(f"moe_decode split down T={T} tiles={tiles}", flush=True)
+    L = _layer(T + 5, 48, 1024, 256, 128, T, 6, tiles=tiles)
+    L["topk_ids"][3, :] = -1
+    L["topk_ids"][T - 1, :] = 48
+    a = _run(L, dev)
+    for _ in range(2):
+        np.testing.assert_array_equal(_run(L, dev), a)
+    assert_close_rows(a, decode.fused_moe_decode(**L), f"split down T={T}", rel=1e-2)
+    # shared expert alone (I_s = 128): a row of small values, where one
+    # intermediate code on the other side of a rounding boundary is a few
+    # bf16 ulps -- the north-star row bar
+    none = {**L, "topk_ids": np.full_like(L["topk_ids"], -1)}
+    assert_close_rows(_run(none, dev), decode.fused_moe_decode(**none), "no routed expert")
+
+
 # (T, E, k, scoring, groups, bias, tiles): T <= 8 routes inside the prep
 # launch (1, 2, 4 and 8 slots per row, group sizes 32, 16, 64 and 20), T > 8
 # through the router's own launch first

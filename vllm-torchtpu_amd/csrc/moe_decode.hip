@@ -31,6 +31,7 @@
 // tensors have the same layouts without the E axis and I_s <= I.
 
 #include <algorithm>
+#include <cstdlib>
 
 #include "gemm_common.h"
 #include "moe_route.h"
@@ -52,16 +53,28 @@ constexpr int kRouteInPrep = 8;   // tokens the prep launch routes itself (2 per
 
 // Workspace carve-up (byte offsets, 256-aligned), shared by host and kernels.
 struct DecodeLayout {
-  int64_t xq, xs, goffs, active, nact, arows, coeff, map, mid, bmax, mq, msc, total;
+  int64_t xq, xs, goffs, active, nact, arows, coeff, map, mid, bmax, mq, msc, part, total;
   int R;      // rows: T shared + T * topk routed (upper bound)
   int slots;  // 1 + min(E, T * topk)
   int xb;     // hidden-state quantization block (512 or 128)
   int qb;     // intermediate quantization block: 512 (the last one partial when
               // I % 512 != 0, the reference's min(512, I) blocks) or 128
   int nbx, nbm;
+  int splits;  // down: contiguous ranges of the active list over grid.y
 };
 
 int64_t align256(int64_t v) { return (v + 255) & ~(int64_t)255; }
+
+// Workgroups of the down kernel per column block: above 16 tokens a step
+// touches ~100-250 experts, and one workgroup walking all of them in turn
+// (two in flight) is latency bound, so the active list is cut into
+// contiguous ranges whose float32 partial sums are added in range order by
+// a last launch.
+int down_splits(int64_t T) {
+  const char* env = std::getenv("QMOE_DECODE_DOWN_SPLITS");  // tuning knob: 1..16
+  if (env && std::atoi(env) >= 1 && std::atoi(env) <= 16) return T > 16 ? std::atoi(env) : 1;
+  return T > 16 ? 4 : 1;
+}
 
 DecodeLayout decode_layout(const qmoe_moe_decode_desc* d) {
   DecodeLayout L{};
@@ -89,6 +102,8 @@ DecodeLayout decode_layout(const qmoe_moe_decode_desc* d) {
   L.bmax = take((int64_t)L.R * L.nbm * 4);
   L.mq = take((int64_t)L.R * d->I);
   L.msc = take((int64_t)L.R * L.nbm * 4);
+  L.splits = down_splits(d->T);
+  L.part = take(L.splits > 1 ? (int64_t)L.splits * d->T * d->H * 4 : 0);
   L.total = o;
   return L;
 }
@@ -392,6 +407,8 @@ struct DownArgs {
   const float* ws2x;  // [H] or [H/128][Is/128]
   uint16_t* out;
   int64_t ldo;
+  int splits;      // grid.y: contiguous ranges of the active list
+  float* partial;  // splits > 1: float32 [splits][T][H] partial sums
 };
 
 // One workgroup: output columns [n0, n0 + 16 * NS) for every token (MT
@@ -552,18 +569,26 @@ __global__ __launch_bounds__(W * 64) void decode_down_kernel(const DownArgs a) {
 
   Slot sa, sb;
   Item ia, ib;
-  setup_issue(0, sa, ia);
+  // range y of the active list: the shared slot 0, then the routed slots
+  // 1..nact-1 cut into `splits` contiguous pieces, [1 + (nact-1) y / splits,
+  // 1 + (nact-1) (y+1) / splits), range 0 also taking slot 0 -- so range 0
+  // is never empty and the shared slot's loads go out first
+  const int ys = blockIdx.y;
+  if (ys == 0) setup_issue(0, sa, ia);
   const int nact = min(*a.nact, a.slots);
   for (int i = threadIdx.x; i < nact; i += W * 64) s_active[i] = a.active[i];
   for (int i = threadIdx.x; i < nact * a.T; i += W * 64) s_map[i] = (int16_t)a.map[i];
   __syncthreads();
-  for (int s = 0; s < nact; s += 2) {
-    if (s + 1 < nact) setup_issue(s + 1, sb, ib);
+  const int sb0 = ys == 0 ? 0 : 1 + (int)((int64_t)(nact - 1) * ys / a.splits);
+  const int se = 1 + (int)((int64_t)(nact - 1) * (ys + 1) / a.splits);
+  if (ys != 0 && sb0 < se) setup_issue(sb0, sa, ia);
+  for (int s = sb0; s < se; s += 2) {
+    if (s + 1 < se) setup_issue(s + 1, sb, ib);
     __builtin_amdgcn_sched_barrier(0);
     consume(sa, ia);
     __builtin_amdgcn_sched_barrier(0);
-    if (s + 1 >= nact) break;
-    if (s + 2 < nact) setup_issue(s + 2, sa, ia);
+    if (s + 1 >= se) break;
+    if (s + 2 < se) setup_issue(s + 2, sa, ia);
     __builtin_amdgcn_sched_barrier(0);
     consume(sb, ib);
     __builtin_amdgcn_sched_barrier(0);
@@ -596,13 +621,29 @@ __global__ __launch_bounds__(W * 64) void decode_down_kernel(const DownArgs a) {
       const int tok = mt * 16 + 4 * kg + q;
       if (tok >= a.T) continue;
 #pragma unroll
-      for (int ns = 0; ns < NS; ++ns) a.out[(int64_t)tok * a.ldo + n0 + ns * 16 + col] = f32_to_bf16(acc[mt][ns][q]);
+      for (int ns = 0; ns < NS; ++ns) {
+        if (a.splits > 1)
+          a.partial[((int64_t)ys * a.T + tok) * a.H + n0 + ns * 16 + col] = acc[mt][ns][q];
+        else
+          a.out[(int64_t)tok * a.ldo + n0 + ns * 16 + col] = f32_to_bf16(acc[mt][ns][q]);
+      }
     }
+}
+
+// The down kernel's range partial sums added in range order, bf16 out.
+__global__ __launch_bounds__(256) void decode_down_sum_kernel(const float* __restrict__ partial, int splits, int T,
+                                                              int H, uint16_t* __restrict__ out, int64_t ldo) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)T * H) return;
+  const int tok = (int)(i / H), n = (int)(i - (int64_t)tok * H);
+  float v = partial[i];
+  for (int y = 1; y < splits; ++y) v += partial[(int64_t)y * T * H + i];
+  out[(int64_t)tok * ldo + n] = f32_to_bf16(v);
 }
 
 template <int MT, int NS, int CH, int W>
 void launch_down(const DownArgs& a, bool tiles, hipStream_t st) {
-  const dim3 grid((unsigned)(a.H / (16 * NS)));
+  const dim3 grid((unsigned)(a.H / (16 * NS)), (unsigned)a.splits);
   const size_t lds = (size_t)a.slots * a.T * sizeof(int16_t);  // s_map
   if (tiles)
     hipLaunchKernelGGL((decode_down_kernel<MT, NS, CH, W, true>), grid, dim3(W * 64), lds, st, a);
@@ -755,7 +796,10 @@ extern "C" int qmoe_moe_decode(const qmoe_moe_decode_desc* d, void* workspace, i
   g.bmax = pa.bmax;
   g.bshift = L.qb == 512 ? 9 : 7;
   g.ldb = L.nbm;
-  int rc = qmoe_skinny_launch(QK_W8A8_BLK, g, T, L.slots, nullptr, 0, 1, stream);
+  // the M tile sized for 16 rows whatever T is: routed experts hold about
+  // T * topk / E rows, and a 64-row tile's activation loads and MFMAs cost
+  // more than the shared expert's extra passes over its weights
+  int rc = qmoe_skinny_launch(QK_W8A8_BLK, g, std::min(T, 16), L.slots, nullptr, 0, 1, stream);
   if (rc != QMOE_OK) return rc;
 
   hipLaunchKernelGGL(decode_mid_quant_kernel, dim3((unsigned)L.R), dim3(kPrep), 0, stream, g.y32, pa.bmax,
@@ -782,11 +826,19 @@ extern "C" int qmoe_moe_decode(const qmoe_moe_decode_desc* d, void* workspace, i
   da.ws2x = d->shared_w2_scale;
   da.out = d->out;
   da.ldo = d->ldo;
+  da.splits = L.splits;
+  da.partial = L.splits > 1 ? reinterpret_cast<float*>(ws + L.part) : nullptr;
   if (T <= 16) {
     if (I <= 2048) launch_down<1, 1, 4, 4>(da, tiles, stream);
     else launch_down<1, 1, 8, 4>(da, tiles, stream);
   } else {
     launch_down<4, 1, 2, 8>(da, tiles, stream);
+  }
+  if (hipGetLastError() != hipSuccess) return QMOE_ERR_LAUNCH;
+  if (L.splits > 1) {
+    const int64_t n = (int64_t)T * H;
+    hipLaunchKernelGGL(decode_down_sum_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
+                       da.partial, L.splits, T, H, d->out, d->ldo);
   }
   return hipGetLastError() == hipSuccess ? QMOE_OK : QMOE_ERR_LAUNCH;
 }
