@@ -50,11 +50,12 @@ def parse():
     ap.add_argument("--only", default="", help="comma list of sweep configs to run (0-4; 5 = NVFP4 / INT4; "
                                                 "v = hipBLASLt reference points)")
     ap.add_argument("--profile", nargs="?", const="headline", default=None,
-                    choices=["headline", "decode", "moe", "vendor", "floor"],
+                    choices=["headline", "decode", "moe", "vendor", "floor", "w4"],
                     help="rocprofv3 targets: the headline kernel + a copy calibration (default), "
                          "the decode GEMMs (cfg 0/1/2 at M=1), the MoE layers at T=1 (cfg 3/4), "
                          "this build's FP8 GEMM beside hipBLASLt's (torch._scaled_mm) on both cfg 1 "
-                         "shapes at M=4096, or the plain-read floor (time vs size)")
+                         "shapes at M=4096, the plain-read floor (time vs size), or the large-M MXFP4 "
+                         "path (cfg 0 at M=8192, cfg 3 at T=8192)")
     return ap.parse_args()
 
 
@@ -225,14 +226,17 @@ def sweep_linear(only):
         K, N = 2880, 5760
         codes, sc = mxfp4_weights((N, K), gen)
         host = (codes.cpu().numpy(), sc.cpu().numpy()) if PAR.on else None
-        for M in (1, 16, 128):
+        for M in (1, 16, 128, 2048, 8192):
             x = torch.randn((M, K), device="cuda", generator=gen).to(torch.bfloat16)
             us = graph_time_us(lambda: quantized_matmul_fp4(x, codes, sc))[0]
             nbytes = N * K // 2 + N * K // 32 + 2 * M * K + 2 * M * N
             par = PAR.linear(quantized_matmul_fp4(x, codes, sc), x, M,
                              lambda xr: oracle_mod("linear").w4a16_mxfp4(xr, *host)) if PAR.on else {}
-            out.append(dict(cfg=0, kind="mxfp4_w4a16", M=M, K=K, N=N,
-                            **roof(2.0 * M * N * K, nbytes, us, "bf16"), **par))
+            pt = dict(cfg=0, kind="mxfp4_w4a16", M=M, K=K, N=N, **roof(2.0 * M * N * K, nbytes, us, "bf16"), **par)
+            if M >= 2048:
+                # the W4A16 recipe runs bf16 MFMA; against the dense FP4 peak too
+                pt["fp4_peak_frac"] = round(2.0 * M * N * K / (us * 1e-6) / PEAK["fp4"], 4)
+            out.append(pt)
             log(out[-1])
     if not only or "1" in only:
         for qd in ("fp8", "int8"):
@@ -416,8 +420,11 @@ def sweep_moe(only):
                 par = PAR.moe(layer(), T, lambda tk: omoe.fused_moe_tokens(
                     PAR._np(x[tk]), ew, PAR._np(tw[tk]), ids_ref[tk], "swigluoai", E),
                     np.array_equal(ids.cpu().numpy(), ids_ref))
-            out.append(dict(cfg=3, kind="moe_mxfp4_gptoss", T=T, experts_touched=touched,
-                            **roof(T * k * 6.0 * H * I, nbytes, us, "bf16"), **par))
+            pt = dict(cfg=3, kind="moe_mxfp4_gptoss", T=T, experts_touched=touched,
+                      **roof(T * k * 6.0 * H * I, nbytes, us, "bf16"), **par)
+            if T >= 1024:
+                pt["fp4_peak_frac"] = round(T * k * 6.0 * H * I / (us * 1e-6) / PEAK["fp4"], 4)
+            out.append(pt)
             log(out[-1])
         del w13, s13, w2, s2
         torch.cuda.empty_cache()
@@ -913,6 +920,43 @@ def floor_us(floor, nbytes):
     return t1 + (t1 - t0) * (nbytes - b1) / (b1 - b0)
 
 
+def profile_w4(args):
+    """rocprofv3 target: the large-M MXFP4 (W4A16) path -- 8 launches of the
+    dense cfg 0 linear at M=8192 (K 2880, N 5760) and 8 cfg 3 GPT-OSS MoE
+    layers at T=8192 (128 experts, top-4, swigluoai), after 2 warm-up calls
+    each; then a plain 256 MiB copy (10 launches) for the FETCH_SIZE /
+    WRITE_SIZE calibration."""
+    import torch
+
+    from qmoe.layers.fused_moe import moe_forward
+    from qmoe.layers.linear_common import quantized_matmul_fp4
+
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    K, N, M = 2880, 5760, 8192
+    codes, sc = mxfp4_weights((N, K), gen)
+    x = torch.randn((M, K), device="cuda", generator=gen).to(torch.bfloat16)
+    for _ in range(10):
+        quantized_matmul_fp4(x, codes, sc)
+    torch.cuda.synchronize()
+    log("profile target: cfg0 MXFP4 M=8192 x10")
+    E, k, H, I, T = 128, 4, 2880, 2880, 8192
+    w13, s13 = mxfp4_weights((E, 2 * I, H), gen)
+    w2, s2 = mxfp4_weights((E, H, I), gen)
+    x = torch.randn((T, H), device="cuda", generator=gen).to(torch.bfloat16)
+    logits = torch.randn((T, E), device="cuda", generator=gen).to(torch.bfloat16)
+    lcfg = moe_layer_cfg(k, "softmax", "swigluoai")
+    for _ in range(10):
+        moe_forward(lcfg, x, logits, w13, w2, s13, s2, None, None, "mxfp4")
+    torch.cuda.synchronize()
+    log("profile target: cfg3 MoE T=8192 x10")
+    src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log("profile target done: copy 256MiB x10")
+
+
 def profile_floor(args):
     """rocprofv3 target: the plain-read floor curve (qmoe_stream_read over
     FLOOR_MB sizes), printed as one JSON line."""
@@ -923,7 +967,7 @@ def main():
     args = parse()
     if args.profile:
         {"headline": profile_target, "decode": profile_decode, "moe": profile_moe, "vendor": profile_vendor,
-         "floor": profile_floor}[args.profile](args)
+         "floor": profile_floor, "w4": profile_w4}[args.profile](args)
         return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (got --gpus {args.gpus}); "
