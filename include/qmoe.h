@@ -49,11 +49,18 @@ enum {
                         each weight is bf16(code * bf16(scale)) before the product: the
                         dequantize-before-matmul regime of `kernels/megablox/gmm_v2.py:452-462`
                         (quant blocks below 256 columns) */
-  QMOE_W4A16_I4 = 6  /* A bf16; W symmetric 4-bit integers in the compressed-tensors
+  QMOE_W4A16_I4 = 6, /* A bf16; W symmetric 4-bit integers in the compressed-tensors
                         encoding (nibble = value + 8, two per byte, even k in the low
                         nibble: the int32 carriers of `compressed_tensors_moe_w4a16.py`
                         read as bytes) + bf16 scale per wq_group k; each weight is
                         bf16(value * scale), `kernels/megablox/gmm_v2.py:452-462` */
+  QMOE_W4A4_MX = 9   /* A e2m1 codes packed as W (lda in bytes >= K/2) + e8m0 bytes per
+                        (row, 32 k) in a_scale [M, lds_a >= K/32] (qmoe_mx_quant); W as
+                        QMOE_W4A16_MX. Both scales go to the MFMA. Opt-in MX activations
+                        (no counterpart in the reference, whose W4A4 method runs W4A16,
+                        `compressed_tensors_moe_w4an_mxfp4.py:49-55`). Dense only, no
+                        fused activation or row maps; K % 512 == 0 and K >= 1024 (pad
+                        with zero codes); optional bias */
 };
 
 /* Fused gate/up activations (qmoe_gemm_desc.act) */
@@ -125,6 +132,22 @@ int qmoe_abi_version(void);
 int qmoe_row_quant(const void* x, int64_t ldx, int in_f32, int64_t M, int64_t K, int qdtype,
                    int mode, int block, void* q, int64_t ldq, float* scales, int64_t lds,
                    qmoe_stream_t stream);
+
+/*
+ * MX activation quantizer: bf16 rows x [M, K] (K % 32 == 0) -> e2m1 codes
+ * packed two per byte (low nibble = even column) q [M, ldq >= Kp/2] and e8m0
+ * bytes scales [M, lds >= Kp/32], columns K..Kp-1 (Kp % 32 == 0) as zero
+ * blocks (codes 0, byte 0); and/or (xq != NULL) the dequantized values as
+ * bf16 [M, ldxq >= K], exact. Per 32-column block: the reference's ue8m0
+ * block rule, `layers/core/quantization.py:232-318` (`quantize_tensor` with
+ * use_ue8m0, scale = amax * f32(1/6) snapped up to a power of two) and its
+ * e2m1 encoder `compressed_tensors_moe/utils.py:167-183`
+ * (`quantize_to_fp4_e2m1_nibbles`). The reference's W4A4 MXFP4 method runs
+ * its activations unquantized; this is the activation side of the opt-in
+ * QMOE_W4A4_MX GEMM. At least one of q, xq.
+ */
+int qmoe_mx_quant(const void* x, int64_t ldx, int64_t M, int64_t K, int64_t Kp, void* q, int64_t ldq,
+                  void* scales, int64_t lds, void* xq, int64_t ldxq, qmoe_stream_t stream);
 
 /* Workspace bytes qmoe_gemm needs for this problem (split-K partials). */
 int qmoe_gemm_workspace_size(const qmoe_gemm_desc* d, int64_t* bytes);

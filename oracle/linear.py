@@ -197,3 +197,17 @@ def w8a16_blockwise(x, wq, ws_blocks, block=128, bias=None):
     if bias is not None:
         out = out + np.asarray(bias, np.float32)[None, :]
     return bf16_round(out)
+
+
+def w4a4_mxfp4(a_packed, a_scales, w_packed, w_scales, bias=None):
+    """MXFP4 activation x MXFP4 weight (the opt-in W4A4 regime): both
+    operands dequantized exactly (`dequant_mxfp4`, `layers/core/
+    quantization.py:321-345`), f64 sums of the exact products, bias in f32,
+    bf16 out. Equal to `w4a16_mxfp4` of the dequantized activations (they
+    are exact in bf16) up to the summation order."""
+    a = dequant_mxfp4(a_packed, a_scales).astype(np.float64)
+    w = dequant_mxfp4(w_packed, w_scales).astype(np.float64)
+    out = (a @ w.T).astype(np.float32)
+    if bias is not None:
+        out = out + np.asarray(bias, np.float32)[None, :]
+    return bf16_round(out)

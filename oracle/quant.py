@@ -185,3 +185,75 @@ def dequant_tiles(codes, scale_inv, tile=128) -> np.ndarray:
     n, k = codes.shape
     v = e4m3_decode(codes).reshape(n // tile, tile, k // tile, tile)
     return (v * scale_inv[:, None, :, None]).reshape(n, k).astype(np.float32)
+
+
+# ---------------------------------------------------------------- MX (e2m1 + e8m0) activations
+
+MX_BLOCK = 32
+FP4_MAX = np.float32(6.0)
+# bucket edges of the reference's e2m1 encoder: magnitude code = number of
+# edges strictly below |v| (torch.bucketize, right=False), so a value on an
+# edge takes the lower code
+FP4_EDGES = np.array([0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0], dtype=np.float32)
+
+
+def e8m0_exponent_ceil(scale) -> np.ndarray:
+    """Smallest e in [-127, 127] with 2**e >= scale (f32 scale >= 0).
+
+    `layers/core/quantization.py:285-298`: ``ceil(log2(scale))``, raised by
+    one where ``exp2`` of it is still below the scale, clamped to [-127,
+    127]; a zero scale gives -inf and the clamp pins it to -127. Computed
+    here exactly from the binary exponent (frexp: scale = f * 2**E with f in
+    [0.5, 1), so the answer is E - 1 when f == 0.5, else E), which is the
+    value that rule repairs ``log2`` to.
+    """
+    s = np.asarray(scale, dtype=np.float32)
+    f, e = np.frexp(s)
+    out = np.where(f == 0.5, e - 1, e).astype(np.int64)
+    out = np.where(s == 0, -127, out)
+    out = np.where(np.isinf(s), 127, out)
+    return np.clip(out, -127, 127)
+
+
+def fp4_encode_bucket(v) -> np.ndarray:
+    """Scaled f32 values -> e2m1 nibbles, the reference's encoder
+    `compressed_tensors_moe/utils.py:167-183` (`quantize_to_fp4_e2m1_nibbles`):
+    magnitude by the bucket edges above (values past 5.0, including those
+    beyond 6, saturate to code 7 = 6.0), sign bit 8 for v < 0 (so -0.0
+    keeps sign 0)."""
+    v = np.asarray(v, dtype=np.float32)
+    mag = np.searchsorted(FP4_EDGES, np.abs(v), side="left").astype(np.uint8)
+    return (mag | np.where(v < 0, np.uint8(8), np.uint8(0))).astype(np.uint8)
+
+
+def quantize_mx_fp4(x, k_pad=None):
+    """bf16 / f32 activations [M, K] -> MXFP4 (packed e2m1 codes [M, Kp/2],
+    low nibble = even k; e8m0 bytes [M, Kp/32]).
+
+    The reference's ue8m0 block quantizer, `layers/core/quantization.py:
+    232-318` (`quantize_tensor(..., block_size=32, use_ue8m0=True)`) with
+    e2m1 as the target (qmax 6): per 32-value block ``scale = amax * f32(1/6)``
+    in f32, snapped UP to a power of two 2**e (`e8m0_exponent_ceil`), byte
+    e + 127; values ``x * (1 / 2**e)`` clamped to +-6 and encoded by the
+    reference's e2m1 encoder (`fp4_encode_bucket`). The reference has no
+    activation quantizer for its W4A4 method (it runs W4A16); this is its
+    weight-side rule applied to activations. Columns K..Kp-1 (``k_pad``, a
+    multiple of 32 >= K) are zero blocks: codes 0, byte 0 (the rule's answer
+    for an all-zero block).
+    """
+    x = np.asarray(x, dtype=np.float32)
+    m, k = x.shape
+    kp = k if k_pad is None else int(k_pad)
+    if k % MX_BLOCK or kp % MX_BLOCK or kp < k:
+        raise ValueError("MX quantization needs K and the padded K to be multiples of 32")
+    xp = np.zeros((m, kp), np.float32)
+    xp[:, :k] = x
+    blocks = xp.reshape(m, kp // MX_BLOCK, MX_BLOCK)
+    amax = np.max(np.abs(blocks), axis=-1)
+    scale = (amax * np.float32(1.0 / 6.0)).astype(np.float32)
+    e = e8m0_exponent_ceil(scale)
+    inv = np.ldexp(np.float32(1.0), -e).astype(np.float32)
+    v = np.clip((blocks * inv[..., None]).astype(np.float32), -FP4_MAX, FP4_MAX)
+    codes = fp4_encode_bucket(v).reshape(m, kp)
+    packed = (codes[:, 0::2] | (codes[:, 1::2] << 4)).astype(np.uint8)
+    return packed, (e + 127).astype(np.uint8)

@@ -253,3 +253,32 @@ def test_output_columns_follow_weight_rows(fn):
     x2 = x.copy()
     x2[1:] *= 7.0
     np.testing.assert_array_equal(run(x2, wq, ws)[0], y[0])
+
+
+def test_w4a4_mxfp4_known_answers_and_w4a16_identity():
+    from oracle.quant import quantize_mx_fp4
+
+    k, n = 128, 8
+    # all ones (code 2, scale byte 127) on both sides: every output is K
+    ones = np.full((3, k // 2), 0x22, np.uint8)
+    s1 = np.full((3, k // 32), 127, np.uint8)
+    wq = np.full((n, k // 2), 0x22, np.uint8)
+    ws = np.full((n, k // 32), 127, np.uint8)
+    np.testing.assert_array_equal(linear.w4a4_mxfp4(ones, s1, wq, ws), np.full((3, n), float(k), np.float32))
+    # one-hot activation (1.0 at column c) reads back column c of the weight
+    rng = np.random.default_rng(2)
+    wq = rng.integers(0, 256, (n, k // 2), dtype=np.uint8)
+    ws = rng.integers(120, 130, (n, k // 32), dtype=np.uint8)
+    wd = codecs.dequant_mxfp4(wq, ws)
+    for c in (0, 1, 37, 127):
+        x = np.zeros((1, k), np.float32)
+        x[0, c] = 1.0
+        aq, as_ = quantize_mx_fp4(x)
+        np.testing.assert_array_equal(linear.w4a4_mxfp4(aq, as_, wq, ws)[0], codecs.bf16_round(wd[:, c]))
+    # equal to the W4A16 recipe on the dequantized (bf16-exact) activations
+    x = rng.standard_normal((5, k)).astype(np.float32)
+    aq, as_ = quantize_mx_fp4(x)
+    ad = codecs.dequant_mxfp4(aq, as_)
+    assert np.array_equal(codecs.bf16_round(ad), ad)
+    np.testing.assert_allclose(linear.w4a4_mxfp4(aq, as_, wq, ws), linear.w4a16_mxfp4(ad, wq, ws), rtol=2 ** -7,
+                               atol=1e-6)

@@ -111,3 +111,85 @@ def test_tile_quant_roundtrip_error_bound():
     d = quant.dequant_tiles(c, s)
     rel = np.abs(d - w) / np.repeat(np.repeat(s, 128, 0), 128, 1)
     assert rel.max() <= 16.0 + 1e-3  # half an ulp of 448's binade in scale units
+
+
+# ---------------------------------------------------------------- MX activations
+
+
+def _torch_ue8m0_exponent(scale):
+    """The reference's exponent rule executed literally in torch f32
+    (`layers/core/quantization.py:285-298`: ceil(log2), repair, clamp)."""
+    s = torch.from_numpy(np.asarray(scale, np.float32))
+    e = torch.ceil(torch.log2(s))
+    e = torch.where(torch.exp2(e) < s, e + 1, e).clamp(-127, 127)
+    return e.to(torch.int64).numpy()
+
+
+def test_mx_exponent_matches_log2_rule_and_is_minimal():
+    rng = np.random.default_rng(3)
+    amax = np.concatenate([
+        np.abs(rng.standard_normal(4000)).astype(np.float32) * np.float32(2.0) ** rng.integers(-40, 40, 4000),
+        (6.0 * np.float32(2.0) ** np.arange(-60, 60)).astype(np.float32),           # exact powers after /6
+        np.nextafter((6.0 * np.float32(2.0) ** np.arange(-60, 60)).astype(np.float32), np.float32(np.inf)),
+        np.float32([0.0, 1e-45, 1e-40, 3e38]),
+    ]).astype(np.float32)
+    scale = (amax * np.float32(1.0 / 6.0)).astype(np.float32)
+    e = quant.e8m0_exponent_ceil(scale)
+    np.testing.assert_array_equal(e, _torch_ue8m0_exponent(scale))
+    # 2**e covers the scale and 2**(e-1) does not (inside the clamp range)
+    p = np.ldexp(1.0, e)
+    assert (p >= scale).all()
+    inner = e > -127
+    assert (np.ldexp(1.0, e[inner] - 1) < scale[inner]).all()
+
+
+def test_mx_known_answers():
+    # amax 6 -> scale 1 -> byte 127; edge values take the lower code
+    x = np.zeros((1, 32), np.float32)
+    x[0, :8] = [6.0, 3.0, -1.25, 0.3, 0.75, -5.0, 5.01, -0.0]
+    q, s = quant.quantize_mx_fp4(x)
+    assert s.tolist() == [[127]]
+    nib = codecs.unpack_fp4(q)[0, :8]
+    # 6 -> 7, 3 -> 5, -1.25 -> -(1.0), 0.3 -> 0.5, 0.75 -> 0.5, -5 -> -(4.0), 5.01 -> 6, -0 -> +0
+    assert nib.tolist() == [7, 5, 8 | 2, 1, 1, 8 | 6, 7, 0]
+    # amax 12 -> scale 2 -> byte 128; amax 6.5 -> scale > 1 -> byte 128 as well
+    for amax, byte in ((12.0, 128), (6.5, 128), (3.0, 126), (0.0, 0)):
+        x = np.zeros((1, 32), np.float32)
+        x[0, 5] = amax
+        q, s = quant.quantize_mx_fp4(x)
+        assert s[0, 0] == byte, (amax, s)
+    # zero padding to the requested width
+    q, s = quant.quantize_mx_fp4(np.ones((2, 32), np.float32), k_pad=96)
+    assert q.shape == (2, 48) and s.shape == (2, 3)
+    assert (q[:, 16:] == 0).all() and (s[:, 1:] == 0).all()
+
+
+def test_mx_encoder_is_nearest_with_ties_down_and_matches_bucketize():
+    v = np.concatenate([np.linspace(-7, 7, 20001), quant.FP4_EDGES, -quant.FP4_EDGES]).astype(np.float32)
+    c = quant.fp4_encode_bucket(v)
+    mags = np.float32([0, 0.5, 1, 1.5, 2, 3, 4, 6])
+    dist = np.abs(np.abs(v)[:, None] - mags[None, :])
+    got = np.abs(codecs.fp4_decode(c))
+    best = dist.min(axis=1)
+    assert np.allclose(np.abs(np.abs(v) - got), best, rtol=0, atol=0)
+    lower = mags[np.argmin(dist, axis=1)]  # argmin takes the first (lower) of two equal distances
+    np.testing.assert_array_equal(got, lower)
+    # the reference's own call, torch.bucketize(|v|, edges) | sign
+    t = torch.from_numpy(v)
+    ref = torch.bucketize(t.abs(), torch.from_numpy(quant.FP4_EDGES)).to(torch.uint8)
+    ref = ref | torch.where(t < 0, 8, 0).to(torch.uint8)
+    np.testing.assert_array_equal(c, ref.numpy())
+
+
+def test_mx_reproduces_representable_values_and_error_bound():
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal((16, 256)) * np.float32(2.0) ** rng.integers(-6, 6, (16, 1))).astype(np.float32)
+    q, s = quant.quantize_mx_fp4(x)
+    d = codecs.dequant_mxfp4(q, s)
+    # error within half the widest e2m1 gap (1.0 at the top) times the block scale
+    blk = np.repeat(codecs.e8m0_decode(s), 32, axis=1)
+    assert (np.abs(d - x) <= blk).all()
+    # MX values quantize to themselves (a block whose top code is 3.0 moves
+    # one octave down and doubles its codes: same values)
+    q2, s2 = quant.quantize_mx_fp4(d)
+    np.testing.assert_array_equal(codecs.dequant_mxfp4(q2, s2), d)

@@ -287,6 +287,74 @@ __global__ __launch_bounds__(kThreads) void gmm_quant_kernel(const uint16_t* __r
   if (lane == 0) scales[row * lds + blk] = scale;
 }
 
+// ---- MX activation quant (e2m1 codes + e8m0 byte per 32 columns) ----
+// The reference's ue8m0 block quantizer, layers/core/quantization.py:232-318
+// (quantize_tensor with use_ue8m0) with e2m1 as the target: per 32-column
+// block scale = amax * f32(1/6), snapped up to the smallest power of two 2^e
+// >= scale (the value its ceil(log2) + repair step computes; e clamped to
+// [-127, 127], byte e + 127); values x * 2^-e clamped to +-6 and encoded by
+// the reference's e2m1 encoder, compressed_tensors_moe/utils.py:167-183
+// (magnitude = number of the edges 0.25 0.75 1.25 1.75 2.5 3.5 5 strictly
+// below |v|, sign 8 for v < 0). Thread t owns 8 consecutive columns per
+// 2048-column span (grid.y), so a block is 4 adjacent lanes; columns K..Kp-1
+// are zero blocks (codes 0, byte 0). Outputs: packed codes (low nibble = even
+// column, one dword per lane) + scale bytes, and/or the dequantized values
+// as bf16 (exact: an e2m1 value times a power of two), for callers that run
+// the 4-bit activations through a bf16-activation kernel.
+__device__ __forceinline__ int mx_exponent_ceil(float scale) {
+  const uint32_t b = f32_bits(scale);
+  const int be = (int)((b >> 23) & 0xffu);
+  const uint32_t mant = b & 0x7fffffu;
+  if (be == 255) return 127;
+  // subnormal scales: 2^-127 = 2^22 ulps; at or below it the clamp gives -127
+  if (be == 0) return mant > (1u << 22) ? -126 : -127;
+  const int e = be - 127 + (mant != 0u ? 1 : 0);
+  return e < -127 ? -127 : (e > 127 ? 127 : e);
+}
+
+template <bool kCodes, bool kFake>
+__global__ __launch_bounds__(kThreads) void mx_quant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int64_t K,
+                                                            int64_t Kp, uint8_t* __restrict__ q, int64_t ldq,
+                                                            uint8_t* __restrict__ scales, int64_t lds,
+                                                            uint16_t* __restrict__ xq, int64_t ldxq) {
+  const int64_t row = blockIdx.x;
+  const int64_t c = ((int64_t)blockIdx.y * kThreads + threadIdx.x) * 8;
+  Row8 r;
+  if (c < K) r = load8<false>(x, row * ldx + c);
+  else
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r.v[i] = 0.0f;
+  // the 4 lanes of a block are all below K or all past it (K % 32 == 0)
+  float m = amax8(r);
+  m = nanmax(m, __shfl_xor(m, 1, 64));
+  m = nanmax(m, __shfl_xor(m, 2, 64));
+  const int e = mx_exponent_ceil(m * (1.0f / 6.0f));
+  const float inv = __builtin_amdgcn_ldexpf(1.0f, -e);
+  if (c >= Kp) return;
+  uint32_t w = 0;
+  uint32_t d[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float v = fminf(fmaxf(r.v[i] * inv, -6.0f), 6.0f);
+    const float a = fabsf(v);
+    const uint32_t mag = (uint32_t)(a > 0.25f) + (uint32_t)(a > 0.75f) + (uint32_t)(a > 1.25f) +
+                         (uint32_t)(a > 1.75f) + (uint32_t)(a > 2.5f) + (uint32_t)(a > 3.5f) + (uint32_t)(a > 5.0f);
+    const uint32_t code = mag | (v < 0.0f ? 8u : 0u);
+    w |= code << (4 * i);
+    if (kFake) {
+      // e2m1 magnitude of the code, times 2^e: exact in bf16 (3 significant bits)
+      const float mv = mag < 4u ? 0.5f * (float)mag : (mag < 6u ? (float)(mag - 2u) : (mag == 6u ? 4.0f : 6.0f));
+      const float dv = __builtin_amdgcn_ldexpf(v < 0.0f ? -mv : mv, e);
+      d[i >> 1] |= (f32_bits(dv) >> 16) << (16 * (i & 1));
+    }
+  }
+  if (kCodes) {
+    *reinterpret_cast<uint32_t*>(q + row * ldq + c / 2) = w;
+    if ((threadIdx.x & 3) == 0) scales[row * lds + c / 32] = (uint8_t)(e + 127);
+  }
+  if (kFake && c < K) *reinterpret_cast<uint4*>(xq + row * ldxq + c) = make_uint4(d[0], d[1], d[2], d[3]);
+}
+
 template <int kQdt, int kMode, bool kInF32, bool kBlock>
 void launch_rq(const void* x, int64_t ldx, int64_t M, int64_t K, uint8_t* q, int64_t ldq,
                float* s, int64_t lds, hipStream_t st) {
@@ -345,5 +413,34 @@ extern "C" int qmoe_row_quant(const void* x, int64_t ldx, int in_f32, int64_t M,
     else { if (blk) QMOE_RQ(1, 1, false, true); else QMOE_RQ(1, 1, false, false); }
   }
 #undef QMOE_RQ
+  return hipGetLastError() == hipSuccess ? QMOE_OK : QMOE_ERR_LAUNCH;
+}
+
+// See include/qmoe.h for the contract.
+extern "C" int qmoe_mx_quant(const void* x, int64_t ldx, int64_t M, int64_t K, int64_t Kp, void* q, int64_t ldq,
+                             void* scales, int64_t lds, void* xq, int64_t ldxq, hipStream_t stream) {
+  if (!x || M < 0 || K <= 0 || (K % 32) != 0 || Kp < K || (Kp % 32) != 0) return QMOE_ERR_ARG;
+  if (ldx < K || (ldx % 8) != 0 || (reinterpret_cast<uintptr_t>(x) & 15)) return QMOE_ERR_ARG;
+  const bool codes = q != nullptr;
+  if (!codes && !xq) return QMOE_ERR_ARG;
+  if (codes && (!scales || ldq < Kp / 2 || (ldq % 4) != 0 || lds < Kp / 32 || (reinterpret_cast<uintptr_t>(q) & 3)))
+    return QMOE_ERR_ARG;
+  if (xq && (ldxq < K || (ldxq % 8) != 0 || (reinterpret_cast<uintptr_t>(xq) & 15))) return QMOE_ERR_ARG;
+  if (M == 0) return QMOE_OK;
+  if (M > 0x7fffffff || cdiv<int64_t>(Kp, kThreads * 8) > 65535) return QMOE_ERR_ARG;
+  const dim3 grid((unsigned)M, (unsigned)cdiv<int64_t>(Kp, kThreads * 8));
+  const uint16_t* xb = static_cast<const uint16_t*>(x);
+  uint8_t* qb = static_cast<uint8_t*>(q);
+  uint8_t* sb = static_cast<uint8_t*>(scales);
+  uint16_t* fb = static_cast<uint16_t*>(xq);
+  if (codes && xq)
+    hipLaunchKernelGGL((mx_quant_kernel<true, true>), grid, dim3(kThreads), 0, stream, xb, ldx, K, Kp, qb, ldq, sb,
+                       lds, fb, ldxq);
+  else if (codes)
+    hipLaunchKernelGGL((mx_quant_kernel<true, false>), grid, dim3(kThreads), 0, stream, xb, ldx, K, Kp, qb, ldq, sb,
+                       lds, fb, ldxq);
+  else
+    hipLaunchKernelGGL((mx_quant_kernel<false, true>), grid, dim3(kThreads), 0, stream, xb, ldx, K, Kp, qb, ldq, sb,
+                       lds, fb, ldxq);
   return hipGetLastError() == hipSuccess ? QMOE_OK : QMOE_ERR_LAUNCH;
 }

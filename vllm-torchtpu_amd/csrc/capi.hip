@@ -17,6 +17,8 @@ int qmoe_tiled_launch(int kind, GemmParams p, hipStream_t st);
 int qmoe_tiled_check(int kind, const GemmParams& p, int* tile);
 bool qmoe_f8_plan(const GemmParams& p, bool blk, int* bm_out, int* ksplit_out, int64_t* ws_bytes);
 int qmoe_f8_launch(GemmParams p, bool blk, void* workspace, int64_t ws_bytes, hipStream_t st);
+bool qmoe_mx_plan(const GemmParams& p);
+int qmoe_mx_launch(const GemmParams& p, hipStream_t st);
 bool qmoe_f8_persistent(const GemmParams& p, bool blk);
 bool qmoe_w4_plan(const GemmParams& p, int fmt, int* bm_out, int* ksplit_out, int64_t* ws_bytes);
 int qmoe_w4_launch(GemmParams p, int fmt, void* workspace, int64_t ws_bytes, hipStream_t st);
@@ -33,13 +35,16 @@ constexpr int kSkinnyMaxRowsBlkWide = 16;
 
 int qmoe_to_params(const qmoe_gemm_desc* d, GemmParams* p) {
   if (!d) return QMOE_ERR_ARG;
-  if (d->kind < QMOE_W8A8_PC || d->kind > QMOE_W8A16_BLK) return QMOE_ERR_ARG;
+  if (d->kind < QMOE_W8A8_PC || d->kind > QMOE_W4A4_MX) return QMOE_ERR_ARG;
   if ((d->kind == QMOE_W8A8_PC || d->kind == QMOE_W8A8_GMM) && d->wfmt != 0 && d->wfmt != 1) return QMOE_ERR_ARG;
   if (d->act < QMOE_ACT_NONE || d->act > QMOE_ACT_SITU) return QMOE_ERR_ARG;
   if (d->M < 0 || d->N <= 0 || d->K <= 0 || d->slots <= 0) return QMOE_ERR_ARG;
   if (!d->a || !d->w || !d->y) return QMOE_ERR_ARG;
-  if ((d->kind == QMOE_W8A8_PC || d->kind == QMOE_W8A8_BLK || d->kind == QMOE_W8A8_GMM) && !d->a_scale)
+  if ((d->kind == QMOE_W8A8_PC || d->kind == QMOE_W8A8_BLK || d->kind == QMOE_W8A8_GMM ||
+       d->kind == QMOE_W4A4_MX) && !d->a_scale)
     return QMOE_ERR_ARG;
+  // MX activations: e8m0 bytes per (row, 32 k) on both operands
+  if (d->kind == QMOE_W4A4_MX && (d->lds_a < d->K / 32 || d->ldws < d->K / 32)) return QMOE_ERR_ARG;
   if (d->kind != QMOE_W16A16 && !d->w_scale) return QMOE_ERR_ARG;
   if (d->kind == QMOE_W8A8_BLK && (d->ws_bn <= 0 || (d->K % 128) != 0)) return QMOE_ERR_ARG;
   // grouped-matmul recipe: activation scales per 512 columns, per-channel weights
@@ -50,7 +55,8 @@ int qmoe_to_params(const qmoe_gemm_desc* d, GemmParams* p) {
   if (d->active && (!d->num_active || !d->group_offs)) return QMOE_ERR_ARG;
   if (!d->group_offs && d->slots != 1) return QMOE_ERR_ARG;
   // 16-byte loads along K
-  const int wbytes = kind_w4(d->kind) ? d->K / 2 : (d->kind == QMOE_W16A16 ? 2 * d->K : d->K);
+  const bool w4 = kind_w4(d->kind) || d->kind == QMOE_W4A4_MX;
+  const int wbytes = w4 ? d->K / 2 : (d->kind == QMOE_W16A16 ? 2 * d->K : d->K);
   if (d->ldw < wbytes || (d->ldw % 16) != 0 || (d->K % 32) != 0) return QMOE_ERR_ARG;
   // NVFP4 scales: bf16 [N][ldws >= K/16], 4-byte aligned pairs
   if (d->kind == QMOE_W4A16_NV && (d->ldws < d->K / 16 || (d->ldws % 2) != 0 || (d->ws_gstride % 2) != 0 ||
@@ -62,7 +68,9 @@ int qmoe_to_params(const qmoe_gemm_desc* d, GemmParams* p) {
        d->ldws < d->K / d->wq_group || (reinterpret_cast<uintptr_t>(d->w_scale) & 1)))
     return QMOE_ERR_ARG;
   const bool abf16 = kind_abf16(d->kind);
-  if (d->lda < d->K || ((d->lda * (abf16 ? 2 : 1)) % 16) != 0) return QMOE_ERR_ARG;
+  // packed e2m1 activations: lda counts bytes (two codes each)
+  const int abytes = d->kind == QMOE_W4A4_MX ? d->K / 2 : d->K;
+  if (d->lda < abytes || ((d->lda * (abf16 ? 2 : 1)) % 16) != 0) return QMOE_ERR_ARG;
   const int nout = d->act != QMOE_ACT_NONE ? d->N / 2 : d->N;
   if (d->ldy < nout) return QMOE_ERR_ARG;
   *p = GemmParams{};
@@ -191,6 +199,7 @@ enum Path {
   kPathTiled = 3,       // generic tiles
   kPathSkinnyPass = 4,  // weight streaming in 64-row passes (K outside every tiled granule)
   kPathF8Persistent = 5,  // 1-byte x 1-byte 256 x 256 tiles, persistent workgroups
+  kPathMx = 6,            // e2m1 x e2m1 with e8m0 scales on both, 256 x 256 persistent tiles
 };
 
 // The one place that decides which kernel runs a problem: the streaming
@@ -203,6 +212,11 @@ enum Path {
 
 int qmoe_route_of(const qmoe_gemm_desc* d, GemmParams& p, QmoeRoute* r) {
   const int kind = kernel_kind(d);
+  if (kind == QK_W4A4_MX) {  // one kernel takes MX activations
+    if (!qmoe_mx_plan(p)) return QMOE_ERR_ARG;
+    *r = QmoeRoute{kPathMx, 256, 1, 0};
+    return QMOE_OK;
+  }
   if (use_skinny(d) && qmoe_skinny_check(kind, p) == QMOE_OK) {
     r->path = kPathSkinny;
     r->tile_m = qmoe_skinny_tile_rows(skinny_rows(d));
@@ -252,6 +266,7 @@ int qmoe_run_route(const qmoe_gemm_desc* d, const QmoeRoute& r, GemmParams p, vo
     case kPathF8Persistent: return qmoe_f8_launch(p, kind == QK_W8A8_BLK, workspace, ws_bytes, stream);
     case kPathW4: return qmoe_w4_launch(p, w4_fmt(d), workspace, ws_bytes, stream);
     case kPathTiled: return qmoe_tiled_launch(kind, p, stream);
+    case kPathMx: return qmoe_mx_launch(p, stream);
     default: {
       GemmParams q;
       qmoe_to_params(d, &q);
@@ -260,7 +275,7 @@ int qmoe_run_route(const qmoe_gemm_desc* d, const QmoeRoute& r, GemmParams p, vo
   }
 }
 
-extern "C" int qmoe_abi_version(void) { return 6; }
+extern "C" int qmoe_abi_version(void) { return 7; }
 
 extern "C" int qmoe_gemm_workspace_size(const qmoe_gemm_desc* d, int64_t* bytes) {
   GemmParams p;

@@ -24,6 +24,8 @@ enum QmoeKind {
                     // QK_W4A16_MX, + bf16 scale per wq_group k (32, 64 or 128)
   QK_W8A16_BLK = 8,  // A bf16; W e4m3 + f32 scale per (n / bn, 128 k), dequantized in bf16:
                      // each weight is bf16(code * bf16(scale))
+  QK_W4A4_MX = 9,    // A e2m1 (packed as W) + e8m0 byte per (row, 32 k) in a_scale; W as
+                     // QK_W4A16_MX; both scales applied by the MFMA (dense tiles only)
 };
 // The host maps the descriptor kind QMOE_W8A8_GMM (7) onto QK_W8A8_BLK with
 // a_kshift = 2 (activation scales per 512 columns) and w_kshift = 31 (one
@@ -100,8 +102,9 @@ struct GemmParams {
   // A operand
   const void* a;           // codes (1 byte) or bf16, row-major
   int64_t lda;             // row stride in elements
-  const float* a_scale;    // W8A8: per-row [rows] or per-(row,kb) [rows, lds_a]
-  int64_t lds_a;           // row stride of a_scale (1 for per-row)
+  const float* a_scale;    // W8A8: per-row [rows] or per-(row,kb) [rows, lds_a];
+                           // QK_W4A4_MX: e8m0 bytes [rows, lds_a]
+  int64_t lds_a;           // row stride of a_scale (1 for per-row; bytes for QK_W4A4_MX)
   const int32_t* a_rows;   // optional gather: physical A row of compact row R
   // W operand, group g at w + g * w_gstride (bytes); row n at + n * ldw
   const uint8_t* w;

@@ -70,6 +70,11 @@ __device__ __forceinline__ i32x8 lds_frag(const uint8_t* p0, const uint8_t* p1) 
 
 __device__ __forceinline__ i32x4 lo4(const i32x8& v) { return i32x4{v[0], v[1], v[2], v[3]}; }
 __device__ __forceinline__ i32x4 hi4(const i32x8& v) { return i32x4{v[4], v[5], v[6], v[7]}; }
+// e2m1 MFMA operand: 4 registers (32 codes) in the low half of the 8-register
+// operand; the undefined upper half lets the compiler pass a 4-register tuple
+__device__ __forceinline__ i32x8 fp4_op(const i32x4& v) {
+  return __builtin_shufflevector(v, v, 0, 1, 2, 3, -1, -1, -1, -1);
+}
 
 template <bool INT, int BM, int BN, bool ACT, int KB, bool BLK, bool WPC = false>
 __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, int m_tiles, int n_tiles) {
@@ -465,18 +470,32 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
 // tile's epilogue runs. The epilogue therefore cannot stage through the
 // stage buffers: it stores from registers, with the tile's token and
 // channel scales in small double-buffered LDS arrays of their own.
-template <bool INT>
+//
+// MODE 0: FP8 e4m3 codes; 1: INT8 codes; 2: MX (QK_W4A4_MX): e2m1 codes of
+// both operands with their e8m0 bytes. An MX stage is the same 128 bytes per
+// row (256 k values, 8 scale bytes); its MFMAs are
+// v_mfma_scale_f32_32x32x64_f8f6f4 with e2m1 operands (16 bytes per lane:
+// row l & 31, k values 32 (l >> 5) .. + 31 of the 64-k step) and the scale
+// bytes of the lane's row and 32-k block selected by opsel from a dword, so
+// the sums come out scaled and the epilogue adds only the bias. The stage's
+// scale bytes ([256 rows][8 bytes] per operand) ride in the stage's copies
+// (dword LDS copies) into LDS arrays beside the code buffers.
+template <int MODE>
 __global__ __launch_bounds__(kThreads) void f8_persistent_kernel(const GemmParams p, int m_tiles, int n_tiles,
                                                                  int tile_slots) {
+  constexpr bool INT = MODE == 1, MX = MODE == 2;
   constexpr bool ACT = false;  // fused activations take the one-tile kernel
   constexpr int BM = 256, BN = 256, KB = 128;
   using S = F8Shape<BM, BN>;
   constexpr int NI = S::NI, MJ = S::MJ, TN = S::TN, TM = S::TM;
   __shared__ __align__(1024) uint8_t sW0[BN * KB], sW1[BN * KB];
   __shared__ __align__(1024) uint8_t sX0[BM * KB], sX1[BM * KB];
+  // MX scale bytes of the two stage buffers ([row][8], 32 k per byte)
+  constexpr int QB = MX ? BN * 8 : 16;
+  __shared__ __align__(16) uint8_t sQW0[QB], sQW1[QB], sQX0[QB], sQX1[QB];
   // per-tile epilogue vectors, double-buffered by tile parity: written after
   // the tile's first stage, read by its epilogue while the next tile's are
-  // written to the other set
+  // written to the other set (MX: s_ws holds the bias, s_sx is unused)
   __shared__ __align__(16) float s_sx[2][BM], s_ws[2][BN];
 
   const int tid = threadIdx.x;
@@ -489,10 +508,14 @@ __global__ __launch_bounds__(kThreads) void f8_persistent_kernel(const GemmParam
   constexpr int RPI = 8;                   // rows per copy instruction (128-byte rows)
   constexpr int WI = BN / (4 * RPI);       // weight copies per wavefront per stage
   constexpr int XI = BM / (4 * RPI);       // activation copies per wavefront per stage
-  constexpr int CPS = WI + XI;
-  const int KS = p.K / KB;                 // stages per tile (the host keeps K % 256 == 0, K >= 512)
+  constexpr int QI = MX ? BN / (4 * 32) : 0;  // MX scale copies per operand (32 rows of 8 bytes each)
+  constexpr int CPS = WI + XI + 2 * QI;
+  // stages per tile (the host keeps the row bytes a multiple of 256, >= 512)
+  const int KS = (MX ? p.K / 2 : p.K) / KB;
   const uint8_t* xbase = static_cast<const uint8_t*>(p.a);
   const uint8_t* wbase = p.w;
+  const uint8_t* xqbase = reinterpret_cast<const uint8_t*>(p.a_scale);
+  const uint8_t* wqbase = static_cast<const uint8_t*>(p.w_scale);
 
   // A tile's copies: this lane moves row r_j = rbase + 32 j of the weight
   // and activation stages (j < 8), 16-byte chunk `chunk` of the row's 128
@@ -509,7 +532,7 @@ __global__ __launch_bounds__(kThreads) void f8_persistent_kernel(const GemmParam
     sc.rows = rows;
     sc.n0 = n0;
   };
-  auto copy_stage = [&](uint8_t* dW, uint8_t* dX, const Src& sc, int ks) {
+  auto copy_stage = [&](uint8_t* dW, uint8_t* dX, uint8_t* dQW, uint8_t* dQX, const Src& sc, int ks) {
     const uint32_t kb = (uint32_t)ks * (uint32_t)KB;
 #pragma unroll
     for (int j = 0; j < WI; ++j) {
@@ -525,18 +548,43 @@ __global__ __launch_bounds__(kThreads) void f8_persistent_kernel(const GemmParam
       const uint8_t* src = xbase + (uint64_t)r * (uint64_t)p.lda + (kb + (uint32_t)chunk);
       __builtin_amdgcn_global_load_lds(src, QMOE_LDS(dX + (wave + 4 * j) * 1024), 16, 0, 0);
     }
+    if constexpr (MX) {
+      // scale rows (wave * QI + j) * 32 + lane / 2, dword lane & 1 of the
+      // stage's 8 bytes: each copy fills 256 contiguous LDS bytes
+      const uint32_t kq = (uint32_t)ks * 8u + (uint32_t)(lane & 1) * 4u;
+#pragma unroll
+      for (int j = 0; j < QI; ++j) {
+        const int rr = (wave * QI + j) * 32 + (lane >> 1);
+        const int n = min(sc.n0 + rr, nlim - 1);
+        uint32_t o = (uint32_t)n * (uint32_t)p.ldws + kq;
+        asm volatile("" : "+v"(o));
+        __builtin_amdgcn_global_load_lds(wqbase + o, QMOE_LDS(dQW + (wave * QI + j) * 256), 4, 0, 0);
+        uint32_t r = (uint32_t)(sc.row0 + min(rr, sc.rows - 1));
+        asm volatile("" : "+v"(r));
+        const uint8_t* src = xqbase + (uint64_t)r * (uint64_t)p.lds_a + kq;
+        __builtin_amdgcn_global_load_lds(src, QMOE_LDS(dQX + (wave * QI + j) * 256), 4, 0, 0);
+      }
+    }
   };
 
-  // operand reads: lane -> row (l & 31), 32 bytes of k-step t of the stage
+  // operand reads: lane -> row (l & 31), 32 bytes of half t of the stage:
+  // 1-byte codes: bytes 32 (l >> 5) .. + 31 of the 64-byte k-step t (chunks
+  // 4t + 2 kh + h); MX: the 16 bytes of 64-k step h of the half (chunks
+  // 4t + 2h + kh), one MFMA each
   const int rl = lane & 31, kh = lane >> 5;
   int po[2][2];
 #pragma unroll
   for (int t = 0; t < 2; ++t)
 #pragma unroll
-    for (int h = 0; h < 2; ++h) po[t][h] = rl * 128 + (((4 * t + 2 * kh + h) ^ ((rl & 7) ^ ((rl >> 3) & 1))) * 16);
+    for (int h = 0; h < 2; ++h)
+      po[t][h] = rl * 128 + (((MX ? 4 * t + 2 * h + kh : 4 * t + 2 * kh + h) ^ ((rl & 7) ^ ((rl >> 3) & 1))) * 16);
   auto wrow = [&](int i) { return tile_wrow<BN, TN, NI, ACT>(wn, i); };
   i32x8 wf[2][NI], xf[2][MJ];
-  auto read_frags = [&](const uint8_t* sW, const uint8_t* sX, int ks, int t) {
+  // MX: scale dword of half t (bytes 4t .. 4t + 3 of the row: 32-k blocks
+  // 4t + 2h + kh), shifted so that byte 2h is the lane's block of step h
+  uint32_t wsc[2][MX ? NI : 1], xsc[2][MX ? MJ : 1];
+  auto read_frags = [&](const uint8_t* sW, const uint8_t* sX, const uint8_t* sQW, const uint8_t* sQX, int ks,
+                        int t) {
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       const uint8_t* b = sW + wrow(i) * KB;
@@ -547,11 +595,36 @@ __global__ __launch_bounds__(kThreads) void f8_persistent_kernel(const GemmParam
       const uint8_t* b = sX + (wm * TM + j * 32) * KB;
       xf[t][j] = lds_frag(b + po[ks][0], b + po[ks][1]);
     }
+    if constexpr (MX) {
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+        wsc[t][i] = *reinterpret_cast<const uint32_t*>(sQW + (wrow(i) + rl) * 8 + ks * 4) >> (8 * kh);
+#pragma unroll
+      for (int j = 0; j < MJ; ++j)
+        xsc[t][j] = *reinterpret_cast<const uint32_t*>(sQX + (wm * TM + j * 32 + rl) * 8 + ks * 4) >> (8 * kh);
+    }
   };
   using Acc = typename std::conditional<INT, i32x16, f32x16>::type;
   Acc acc[NI][MJ];
   auto mma = [&](int t) {
-    if constexpr (INT) {
+    if constexpr (MX) {
+      // opsel 0 / 2 picks byte 0 / 2 of the shifted scale dword: the lane's
+      // 32-k block of 64-k step 0 / 1 of the half
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+#pragma unroll
+        for (int j = 0; j < MJ; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fp4_op(lo4(wf[t][i])), fp4_op(lo4(xf[t][j])),
+                                                                      acc[i][j], 4, 4, 0, (int)wsc[t][i], 0,
+                                                                      (int)xsc[t][j]);
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+#pragma unroll
+        for (int j = 0; j < MJ; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fp4_op(hi4(wf[t][i])), fp4_op(hi4(xf[t][j])),
+                                                                      acc[i][j], 4, 4, 2, (int)wsc[t][i], 2,
+                                                                      (int)xsc[t][j]);
+    } else if constexpr (INT) {
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
@@ -570,8 +643,8 @@ __global__ __launch_bounds__(kThreads) void f8_persistent_kernel(const GemmParam
                                                                       0, 127);
     }
   };
-  constexpr int NM = NI * MJ * (INT ? 2 : 1);
-  constexpr int NR = 2 * (NI + MJ);
+  constexpr int NM = NI * MJ * (INT || MX ? 2 : 1);
+  constexpr int NR = (MX ? 3 : 2) * (NI + MJ);
 
   // tiles of this workgroup: b = blockIdx.x + i * gridDim.x over the
   // XCD-ordered slots [0, tile_slots)
@@ -581,8 +654,8 @@ __global__ __launch_bounds__(kThreads) void f8_persistent_kernel(const GemmParam
   Src cur;
   int row0 = mt * BM, rows = min(BM, p.M - row0), n0 = nt * BNO;
   make_src(row0, rows, n0, cur);
-  copy_stage(sW0, sX0, cur, 0);
-  copy_stage(sW1, sX1, cur, 1);
+  copy_stage(sW0, sX0, sQW0, sQX0, cur, 0);
+  copy_stage(sW1, sX1, sQW1, sQX1, cur, 1);
   wait_copies_upto<CPS>();
   __syncthreads();
 
@@ -594,11 +667,17 @@ __global__ __launch_bounds__(kThreads) void f8_persistent_kernel(const GemmParam
     const int row0n = mt2 * BM, rowsn = has_next ? min(BM, p.M - row0n) : 0, n0n = nt2 * BNO;
 
     // stage 0 has landed everywhere (prologue / end of the previous tile)
-    read_frags(sW0, sX0, 0, 0);
+    read_frags(sW0, sX0, sQW0, sQX0, 0, 0);
     // epilogue inputs of this tile (token tid's activation scale, weight row
-    // tid's scale), loaded now and stored to LDS after stage 0
-    const float e_sx = p.a_scale[(int64_t)(row0 + min(tid, rows - 1)) * p.lds_a];
-    const float e_ws = static_cast<const float*>(p.w_scale)[min(n0 + tid, nlim - 1)];
+    // tid's scale; MX: weight row tid's bias), loaded now and stored to LDS
+    // after stage 0
+    float e_sx = 0.0f, e_ws = 0.0f;
+    if constexpr (MX) {
+      if (p.bias) e_ws = p.bias[min(n0 + tid, nlim - 1)];
+    } else {
+      e_sx = p.a_scale[(int64_t)(row0 + min(tid, rows - 1)) * p.lds_a];
+      e_ws = static_cast<const float*>(p.w_scale)[min(n0 + tid, nlim - 1)];
+    }
 #pragma unroll
     for (int i = 0; i < NI; ++i)
 #pragma unroll
@@ -613,31 +692,32 @@ __global__ __launch_bounds__(kThreads) void f8_persistent_kernel(const GemmParam
     // again when there is no next tile (into a buffer never read again).
     // The last stage reads no operands ahead and does not wait for the
     // copies: the next tile's first stage lands while the epilogue runs.
-    auto stage = [&](uint8_t* cW, uint8_t* cX, uint8_t* nW, uint8_t* nX, int kc, bool last) {
+    auto stage = [&](uint8_t* cW, uint8_t* cX, uint8_t* cQW, uint8_t* cQX, uint8_t* nW, uint8_t* nX,
+                     uint8_t* nQW, uint8_t* nQX, int kc, bool last) {
       mma(0);
-      read_frags(cW, cX, 1, 1);
+      read_frags(cW, cX, cQW, cQX, 1, 1);
       interleave<0, NM, NR, 0>();
       __builtin_amdgcn_sched_barrier(0);
       if (!last) wait_copies_upto<0>();  // stage s + 1 has landed
       stage_barrier();
-      if (!last) read_frags(nW, nX, 0, 0);
-      copy_stage(cW, cX, cur, kc);
+      if (!last) read_frags(nW, nX, nQW, nQX, 0, 0);
+      copy_stage(cW, cX, cQW, cQX, cur, kc);
       mma(1);
       interleave<0, NM, NR, CPS>();
     };
-    stage(sW0, sX0, sW1, sX1, 2, false);
+    stage(sW0, sX0, sQW0, sQX0, sW1, sX1, sQW1, sQX1, 2, false);
     // the epilogue vectors have landed (the wait in stage 0 covers every
     // earlier load); the stage barriers ahead make them visible
     s_sx[par][tid] = e_sx;
     s_ws[par][tid] = e_ws;
-    stage(sW1, sX1, sW0, sX0, 3, false);
+    stage(sW1, sX1, sQW1, sQX1, sW0, sX0, sQW0, sQX0, 3, false);
     for (int s = 2; s < KS - 2; s += 2) {
-      stage(sW0, sX0, sW1, sX1, s + 2, false);
-      stage(sW1, sX1, sW0, sX0, s + 3, false);
+      stage(sW0, sX0, sQW0, sQX0, sW1, sX1, sQW1, sQX1, s + 2, false);
+      stage(sW1, sX1, sQW1, sQX1, sW0, sX0, sQW0, sQX0, s + 3, false);
     }
     if (has_next) make_src(row0n, rowsn, n0n, cur);
-    stage(sW0, sX0, sW1, sX1, has_next ? 0 : KS - 1, false);
-    stage(sW1, sX1, sW0, sX0, has_next ? 1 : KS - 1, true);
+    stage(sW0, sX0, sQW0, sQX0, sW1, sX1, sQW1, sQX1, has_next ? 0 : KS - 1, false);
+    stage(sW1, sX1, sQW1, sQX1, sW0, sX0, sQW0, sQX0, has_next ? 1 : KS - 1, true);
     // the epilogue starts after the last MFMAs: the empty asm takes every
     // accumulator, so no MFMA can be sunk into the epilogue (interleaving
     // the two keeps the last stage's operands alive across it)
@@ -682,7 +762,8 @@ __global__ __launch_bounds__(kThreads) void f8_persistent_kernel(const GemmParam
             const float csv[4] = {cs.x, cs.y, cs.z, cs.w};
             float o[4];
 #pragma unroll
-            for (int t = 0; t < 4; ++t) o[t] = ((float)acc[i][j][q * 4 + t] * sxa[j]) * csv[t];
+            for (int t = 0; t < 4; ++t)
+              o[t] = MX ? (float)acc[i][j][q * 4 + t] + csv[t] : ((float)acc[i][j][q * 4 + t] * sxa[j]) * csv[t];
             union { bf16x2 b; uint32_t u; } lo, hi;
             lo.b = __builtin_convertvector(f32x2{o[0], o[1]}, bf16x2);
             hi.b = __builtin_convertvector(f32x2{o[2], o[3]}, bf16x2);
@@ -772,8 +853,8 @@ void f8_launch_shape(const GemmParams& p, hipStream_t st) {
     const int grid = cdiv(m_tiles * n_tiles, kXcds) * kXcds;
     if constexpr (BM == 256 && BN == 256 && !BLK && !ACT) {
       if (kb == 128 && f8_persistent_ok(p, BLK, BM, (int)ks)) {
-        hipLaunchKernelGGL((f8_persistent_kernel<INT>), dim3(f8_persistent_grid(m_tiles * n_tiles)), dim3(kThreads),
-                           0, st, p, m_tiles, n_tiles, grid);
+        hipLaunchKernelGGL((f8_persistent_kernel<INT ? 1 : 0>), dim3(f8_persistent_grid(m_tiles * n_tiles)),
+                           dim3(kThreads), 0, st, p, m_tiles, n_tiles, grid);
         return;
       }
     }
@@ -941,5 +1022,42 @@ int qmoe_f8_launch(GemmParams p, bool blk, void* workspace, int64_t ws_bytes, hi
       else hipLaunchKernelGGL((tile_splitk_finish_kernel<false, false, kScAll>), rg, dim3(kThreads), 0, st, p);
     }
   }
+  return hipGetLastError() == hipSuccess ? QMOE_OK : QMOE_ERR_LAUNCH;
+}
+
+// ---- MX (QK_W4A4_MX): the persistent 256 x 256 kernel in mode 2 ----
+// Whether the kernel takes the problem: dense, no fused activation or row
+// maps, K % 512 == 0 and K >= 1024 (128-byte stages of packed codes, an even
+// count of at least 4), 16-byte aligned code rows and operands, 4-byte
+// aligned scale rows, N % 8 == 0 with 16-byte aligned output rows, weights
+// and outputs within the kernel's 32-bit offsets.
+bool qmoe_mx_plan(const GemmParams& p) {
+  if (p.M <= 0 || p.N <= 0 || (p.K % 512) != 0 || p.K < 1024) return false;
+  if (p.group_offs || p.act != QA_NONE || p.a_rows || p.y_rows || p.row_weight || !p.a_scale || !p.w_scale)
+    return false;
+  if ((p.lda % 16) != 0 || (p.ldw % 16) != 0 || (p.lds_a % 4) != 0 || (p.ldws % 4) != 0) return false;
+  if ((reinterpret_cast<uintptr_t>(p.a) & 15) || (reinterpret_cast<uintptr_t>(p.w) & 15) ||
+      (reinterpret_cast<uintptr_t>(p.a_scale) & 3) || (reinterpret_cast<uintptr_t>(p.w_scale) & 3))
+    return false;
+  if ((p.N % 8) != 0 || (p.ldy % 8) != 0 || (reinterpret_cast<uintptr_t>(p.y) & 15) != 0) return false;
+  if ((int64_t)p.ldw * p.N >= ((int64_t)1 << 32) || (int64_t)p.ldws * p.N >= ((int64_t)1 << 32)) return false;
+  return (int64_t)p.M * p.ldy * 2 < 0x7fffffffLL;
+}
+
+// Launch: as few tile rounds as the CUs allow, spread evenly over a
+// multiple of the 8 XCDs (also for fewer tiles than CUs: one tile each).
+int qmoe_mx_launch(const GemmParams& p, hipStream_t st) {
+  if (!qmoe_mx_plan(p)) return QMOE_ERR_ARG;
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return QMOE_ERR_LAUNCH;
+  cus = std::max(kXcds, cus / kXcds * kXcds);
+  const int m_tiles = cdiv(p.M, 256), n_tiles = cdiv(p.N, 256);
+  const int tiles = m_tiles * n_tiles;
+  const int rounds = cdiv(tiles, cus);
+  const int grid = std::min(cus, cdiv(cdiv(tiles, rounds), kXcds) * kXcds);
+  hipLaunchKernelGGL((f8_persistent_kernel<2>), dim3(grid), dim3(kThreads), 0, st, p, m_tiles, n_tiles,
+                     cdiv(tiles, kXcds) * kXcds);
   return hipGetLastError() == hipSuccess ? QMOE_OK : QMOE_ERR_LAUNCH;
 }

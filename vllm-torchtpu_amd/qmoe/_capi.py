@@ -9,7 +9,7 @@ import os
 
 _LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libqmoe.so")
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 QMOE_OK = 0
 STATUS_TEXT = {
@@ -20,7 +20,7 @@ STATUS_TEXT = {
 }
 
 # GEMM kinds / activations (include/qmoe.h)
-W8A8_PC, W8A8_BLK, W8A16_PC, W4A16_MX, W16A16, W4A16_NV, W4A16_I4, W8A8_GMM, W8A16_BLK = range(9)
+W8A8_PC, W8A8_BLK, W8A16_PC, W4A16_MX, W16A16, W4A16_NV, W4A16_I4, W8A8_GMM, W8A16_BLK, W4A4_MX = range(10)
 ACT_NONE, ACT_SILU, ACT_SWIGLUOAI, ACT_GELU_TANH, ACT_SILU_CLAMP, ACT_SITU = range(6)
 
 _vp = ctypes.c_void_p
@@ -118,6 +118,8 @@ def _load():
     lib.qmoe_row_quant.restype = ctypes.c_int
     lib.qmoe_row_quant.argtypes = [_vp, _i64, ctypes.c_int, _i64, _i64, ctypes.c_int, ctypes.c_int,
                                    ctypes.c_int, _vp, _i64, _vp, _i64, _vp]
+    lib.qmoe_mx_quant.restype = ctypes.c_int
+    lib.qmoe_mx_quant.argtypes = [_vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp]
     lib.qmoe_gemm_workspace_size.restype = ctypes.c_int
     lib.qmoe_gemm_workspace_size.argtypes = [ctypes.POINTER(GemmDesc), ctypes.POINTER(_i64)]
     lib.qmoe_gemm_plan.restype = ctypes.c_int
@@ -164,6 +166,7 @@ EXPORTED = (
     "qmoe_abi_version",
     "qmoe_stream_read",
     "qmoe_row_quant",
+    "qmoe_mx_quant",
     "qmoe_gemm_workspace_size",
     "qmoe_gemm_plan",
     "qmoe_gemm_static",

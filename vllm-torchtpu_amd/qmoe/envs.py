@@ -55,6 +55,10 @@ _READERS = {
     # reference's requantization (per channel for the MoE and without
     # REQUANTIZE_BLOCK_SIZE, per (row, block) otherwise)
     "QMOE_FP8_NATIVE_BLOCKS": lambda: _bool("QMOE_FP8_NATIVE_BLOCKS"),
+    # this build only (no reference counterpart): dense MXFP4 linears quantize
+    # their activations to MXFP4 too (W4A4, e2m1 + e8m0 per 32 columns) and
+    # run the MX MFMA kernel; off: bf16 activations (W4A16) as the reference
+    "QMOE_MXFP4_MX_ACTIVATIONS": lambda: _bool("QMOE_MXFP4_MX_ACTIVATIONS"),
 }
 
 

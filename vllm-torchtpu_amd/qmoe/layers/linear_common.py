@@ -248,3 +248,78 @@ def _quantized_matmul_fp4_op(x2: torch.Tensor, w_q: torch.Tensor, w_s: torch.Ten
 @_quantized_matmul_fp4_op.register_fake
 def _(x2, w_q, w_s, bias):
     return x2.new_empty((x2.shape[0], w_s.shape[0]), dtype=torch.bfloat16)
+
+
+# ---------------------------------------------------------------- opt-in MX activations (W4A4)
+#
+# No counterpart in the reference (its W4A4 MXFP4 method runs bf16
+# activations, `compressed_tensors_moe_w4an_mxfp4.py:49-55`): MXFP4 weights
+# with activations quantized per 32 columns to e2m1 + e8m0 (`ops.mx_quant`,
+# the reference's ue8m0 block rule and e2m1 encoder), both scales applied by
+# the MFMA. The MX kernel takes K in multiples of 512 (at least 1024), so
+# the weight is zero-padded along K once at load (`pad_mxfp4_for_mx`).
+# Problems too small to fill the CUs with 256 x 256 tiles run the same
+# numbers on the bf16-activation kernels: the MX-quantized activations are
+# exact in bf16 and the products of the two formats are exact in f32, so
+# only the f32 summation order differs.
+
+MX_K_ALIGN = 512
+# 256 x 256 tiles below which the bf16-activation kernels take the problem
+MX_MIN_TILES = 128
+
+
+def mx_padded_k(k: int) -> int:
+    """K of the MX kernel for a layer of input size ``k``: a multiple of 512,
+    at least 1024."""
+    return max(2 * MX_K_ALIGN, -(-int(k) // MX_K_ALIGN) * MX_K_ALIGN)
+
+
+def pad_mxfp4_for_mx(w_q: torch.Tensor, w_s: torch.Tensor):
+    """Zero-pad MXFP4 weights ``[n_out, k/2]`` codes + ``[n_out, k/32]`` e8m0
+    along K to ``mx_padded_k(k)``: codes 0 (and scale byte 127, 1.0) in the
+    padding, so the extra products are zero."""
+    n, kb = w_q.shape
+    k = 2 * kb
+    if w_s.shape != (n, k // 32):
+        raise ValueError(f"MXFP4 scale {tuple(w_s.shape)} does not match codes {tuple(w_q.shape)}")
+    kp = mx_padded_k(k)
+    wq = torch.zeros((n, kp // 2), dtype=torch.uint8, device=w_q.device)
+    ws = torch.full((n, kp // 32), 127, dtype=torch.uint8, device=w_s.device)
+    wq[:, :kb] = w_q.view(torch.uint8)
+    ws[:, : k // 32] = w_s.view(torch.uint8)
+    return wq, ws
+
+
+def quantized_matmul_mxfp4_a4(x: torch.Tensor, w_pad: torch.Tensor, ws_pad: torch.Tensor, k: int,
+                              bias: torch.Tensor | None = None) -> torch.Tensor:
+    """MXFP4 weight x MX-quantized activation linear: ``x`` [..., k] (bf16 or
+    castable), ``w_pad`` / ``ws_pad`` from `pad_mxfp4_for_mx`, optional bias
+    [n_out] added in f32 before the bf16 rounding. bf16 out."""
+    n_out = w_pad.shape[0]
+    kp = w_pad.shape[1] * 2
+    if x.shape[-1] != k or k % 32 or kp != mx_padded_k(k) or ws_pad.shape != (n_out, kp // 32):
+        raise ValueError(f"MX linear: input dim {x.shape[-1]}, k {k}, padded weight {tuple(w_pad.shape)} / "
+                         f"{tuple(ws_pad.shape)} do not match")
+    x2 = x.reshape(-1, k)
+    if x2.dtype != torch.bfloat16:
+        x2 = x2.to(torch.bfloat16)
+    b = None if bias is None else bias.reshape(n_out).to(torch.float32)
+    out = torch.ops.qmoe.quantized_matmul_mxfp4_a4(x2, w_pad, ws_pad, b)
+    return out.reshape(*x.shape[:-1], n_out)
+
+
+@torch.library.custom_op("qmoe::quantized_matmul_mxfp4_a4", mutates_args=())
+def _quantized_matmul_mxfp4_a4_op(x2: torch.Tensor, w_pad: torch.Tensor, ws_pad: torch.Tensor,
+                                  bias: Optional[torch.Tensor]) -> torch.Tensor:
+    M, k = x2.shape
+    n_out, kp = w_pad.shape[0], w_pad.shape[1] * 2
+    if -(-M // 256) * -(-n_out // 256) >= MX_MIN_TILES:
+        q, sc = ops.mx_quant(x2, k_pad=kp)
+        return ops.gemm(_capi.W4A4_MX, q, w_pad, a_scale=sc, w_scale=ws_pad, bias=bias)
+    xq = ops.mx_quant(x2, codes=False, dequantized=True)
+    return ops.gemm(_capi.W4A16_MX, xq, w_pad[:, : k // 2], w_scale=ws_pad[:, : k // 32], bias=bias)
+
+
+@_quantized_matmul_mxfp4_a4_op.register_fake
+def _(x2, w_pad, ws_pad, bias):
+    return x2.new_empty((x2.shape[0], w_pad.shape[0]), dtype=torch.bfloat16)

@@ -27,7 +27,7 @@ import torch
 
 from qmoe import envs
 from qmoe.layers.fused_moe import moe_forward
-from qmoe.layers.linear_common import quantized_matmul_fp4
+from qmoe.layers.linear_common import pad_mxfp4_for_mx, quantized_matmul_fp4, quantized_matmul_mxfp4_a4
 from qmoe.layers.quantization.fp8 import _activation, _device, _param
 
 
@@ -54,7 +54,17 @@ class Mxfp4Config:
 
 
 class Mxfp4LinearMethod:
-    """Dense MXFP4 weight x bf16 activation linear."""
+    """Dense MXFP4 weight x bf16 activation linear.
+
+    ``mx_activations`` (default: the QMOE_MXFP4_MX_ACTIVATIONS flag) opts
+    into MX-quantized activations (W4A4; no counterpart in the reference):
+    the weight is zero-padded along K at load to the MX kernel's multiple of
+    512 (``layer.weight`` / ``layer.weight_scale`` stay views of the
+    checkpoint shape) and `quantized_matmul_mxfp4_a4` runs the forward.
+    """
+
+    def __init__(self, mx_activations=None):
+        self.mx_activations = envs.QMOE_MXFP4_MX_ACTIVATIONS if mx_activations is None else bool(mx_activations)
 
     def create_weights(self, layer, input_size_per_partition, output_partition_sizes, input_size,
                        output_size, params_dtype, **extra_weight_attrs):
@@ -69,8 +79,17 @@ class Mxfp4LinearMethod:
         dev = _device()
         layer.weight = _param(layer.weight.data.to(dev).view(torch.uint8).contiguous())
         layer.weight_scale = _param(layer.weight_scale.data.to(dev).view(torch.uint8).contiguous())
+        if self.mx_activations:
+            kb, ks = layer.weight.shape[1], layer.weight_scale.shape[1]
+            wq, ws = pad_mxfp4_for_mx(layer.weight.data, layer.weight_scale.data)
+            layer.qmoe_mx_weight, layer.qmoe_mx_weight_scale, layer.qmoe_mx_k = wq, ws, 2 * kb
+            layer.weight = _param(wq[:, :kb])
+            layer.weight_scale = _param(ws[:, :ks])
 
     def apply(self, layer, x, bias=None):
+        if getattr(layer, "qmoe_mx_k", None):
+            return quantized_matmul_mxfp4_a4(x, layer.qmoe_mx_weight, layer.qmoe_mx_weight_scale, layer.qmoe_mx_k,
+                                             bias)
         out = quantized_matmul_fp4(x, layer.weight, layer.weight_scale)
         if bias is not None:
             out = out + bias

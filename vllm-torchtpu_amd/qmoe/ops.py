@@ -114,6 +114,41 @@ def row_quant(x, qdtype="fp8", block=None, mode="runtime"):
     return q, (s[:, 0] if blk == 0 else s)
 
 
+def mx_quant(x, k_pad=None, codes=True, dequantized=False):
+    """MX activation quantization of bf16 rows ``x`` [M, K] (K % 32 == 0):
+    the reference's ue8m0 block rule (`layers/core/quantization.py:232-318`,
+    scale = amax * f32(1/6) snapped up to a power of two) with its e2m1
+    encoder (`compressed_tensors_moe/utils.py:167-183`), per 32 columns.
+
+    ``codes``: returns e2m1 codes packed two per byte (low nibble = even
+    column) ``[M, Kp/2]`` uint8 and e8m0 bytes ``[M, Kp/32]`` uint8, columns
+    K..Kp-1 zero (``k_pad`` = Kp, a multiple of 32, default K).
+    ``dequantized``: also (or only, with ``codes=False``) the quantized values
+    as bf16 ``[M, K]`` (exact). Returns the requested tensors in that order.
+    """
+    _require_gpu(x)
+    if x.dim() != 2 or x.dtype != torch.bfloat16:
+        raise ValueError(f"mx_quant expects bf16 [M, K], got {x.dtype} {tuple(x.shape)}")
+    if x.stride(-1) != 1 or x.stride(0) % 8 or x.data_ptr() % 16:
+        x = x.contiguous()
+    M, K = x.shape
+    kp = K if k_pad is None else int(k_pad)
+    if K % 32 or kp % 32 or kp < K:
+        raise ValueError(f"mx_quant needs K ({K}) and the padded K ({kp}) to be multiples of 32, K <= padded K")
+    if not codes and not dequantized:
+        raise ValueError("mx_quant: nothing requested")
+    dev = x.device
+    q = torch.empty((M, kp // 2), dtype=torch.uint8, device=dev) if codes else None
+    sc = torch.empty((M, kp // 32), dtype=torch.uint8, device=dev) if codes else None
+    xq = torch.empty((M, K), dtype=torch.bfloat16, device=dev) if dequantized else None
+    if M:
+        check(lib.qmoe_mx_quant(_ptr(x), x.stride(0), M, K, kp, _ptr(q) if codes else None, kp // 2,
+                                _ptr(sc) if codes else None, kp // 32, _ptr(xq) if dequantized else None, K,
+                                _stream(dev)), "mx_quant")
+    out = ((q, sc) if codes else ()) + ((xq,) if dequantized else ())
+    return out if len(out) > 1 else out[0]
+
+
 # ---------------------------------------------------------------- GEMM
 
 
@@ -138,7 +173,8 @@ def gemm_desc(kind, a, w, *, a_scale=None, w_scale=None, bias=None, wfmt=0, ws_b
     """Checked `qmoe_gemm_desc` of one (grouped) quantized GEMM, and its
     output tensor (allocated here unless ``out`` is given).
 
-    a        : [rows, K] activation codes (1 byte) or bf16
+    a        : [rows, K] activation codes (1 byte) or bf16; W4A4_MX: packed e2m1 [rows, K/2]
+               with e8m0 bytes [rows, K/32] in ``a_scale``
     w        : [G, N, K] / [N, K] weights (1 byte codes, packed e2m1 [.., K/2], bf16)
     w_scale  : per-channel f32 [G, N] | block f32 [G, N/bn, K/128] | e8m0 u8 [G, N, K/32]
                | NVFP4 bf16 [G, N, K/16] | INT4 bf16 [G, N, K/group] (group 32, 64 or 128)
@@ -148,12 +184,16 @@ def gemm_desc(kind, a, w, *, a_scale=None, w_scale=None, bias=None, wfmt=0, ws_b
     if w.dim() == 2:
         w = w.unsqueeze(0)
     G, N, wcols = w.shape
-    if a.stride(-1) != 1 or w.stride(-1) != 1 or w.stride(1) != wcols:
+    # rows may be padded (a row stride above the row length, 16-byte multiples)
+    if a.stride(-1) != 1 or w.stride(-1) != 1 or w.stride(1) < wcols or w.stride(0) < N * w.stride(1):
         raise ValueError("qmoe gemm needs K-contiguous activations and N-major [G, N, K] weights")
     abf16 = kind in (_capi.W8A16_PC, _capi.W4A16_MX, _capi.W16A16, _capi.W4A16_NV, _capi.W4A16_I4,
                      _capi.W8A16_BLK)
-    K = a.shape[1]
-    if kind in (_capi.W4A16_MX, _capi.W4A16_NV, _capi.W4A16_I4):
+    K = a.shape[1] * (2 if kind == _capi.W4A4_MX else 1)
+    if kind == _capi.W4A4_MX and (a.dtype != torch.uint8 or a_scale is None or a_scale.dtype != torch.uint8
+                                  or a_scale.dim() != 2 or a_scale.shape[1] * 32 < K):
+        raise ValueError("W4A4_MX takes packed e2m1 activations [M, K/2] uint8 with e8m0 bytes [M, K/32]")
+    if kind in (_capi.W4A16_MX, _capi.W4A16_NV, _capi.W4A16_I4, _capi.W4A4_MX):
         if wcols * 2 != K:
             raise ValueError(f"packed e2m1 weight has {wcols} bytes per row, expected K/2 = {K // 2}")
     elif wcols != K:
@@ -218,7 +258,8 @@ def gemm_desc(kind, a, w, *, a_scale=None, w_scale=None, bias=None, wfmt=0, ws_b
 
 # ---------------------------------------------------------------- kernel plans
 
-PATH_NAMES = ("stream", "tiled_1b", "tiled_4b", "tiled_generic", "stream_passes", "tiled_1b_persistent")
+PATH_NAMES = ("stream", "tiled_1b", "tiled_4b", "tiled_generic", "stream_passes", "tiled_1b_persistent",
+              "tiled_mx_persistent")
 
 _plan_log = None
 
@@ -259,19 +300,21 @@ def plan_for_shape(kind, M, N, K, *, wfmt=0, activation=None, experts=0, max_row
     contiguous strides: dense when ``experts == 0``, else grouped over
     ``experts`` groups with an active list, ``max_rows`` rows at most per
     group (the MoE layer passes the token count). Needs no GPU."""
-    w4 = kind in (_capi.W4A16_MX, _capi.W4A16_NV, _capi.W4A16_I4)
+    w4 = kind in (_capi.W4A16_MX, _capi.W4A16_NV, _capi.W4A16_I4, _capi.W4A4_MX)
     act, p0, p1 = act_code(activation)
     base = 1 << 24
     d = GemmDesc()
     d.kind, d.wfmt = kind, wfmt
     d.a = d.w = d.y = d.w_scale = d.a_scale = base
-    d.lda = lda if lda is not None else K
+    d.lda = lda if lda is not None else (K // 2 if kind == _capi.W4A4_MX else K)
     d.lds_a = K // 128 if kind == _capi.W8A8_BLK else ((K + 511) // 512 if kind == _capi.W8A8_GMM else 1)
+    if kind == _capi.W4A4_MX:
+        d.lds_a = K // 32
     ldw = K // 2 if w4 else (2 * K if kind == _capi.W16A16 else K)
     d.ldw, d.w_gstride = ldw, ldw * N
     if kind in (_capi.W8A8_BLK, _capi.W8A16_BLK):
         d.ldws = K // 128
-    elif kind == _capi.W4A16_MX:
+    elif kind in (_capi.W4A16_MX, _capi.W4A4_MX):
         d.ldws = K // 32
     elif kind == _capi.W4A16_NV:
         d.ldws = K // 16
