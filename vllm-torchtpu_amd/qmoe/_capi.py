@@ -2,10 +2,19 @@
 
 The library is required: if it is missing or does not load, importing this
 module raises, so no call can silently run anything but the HIP kernels.
+
+torch is imported before the library is loaded: the PyTorch wheel carries
+its own HIP runtime (``torch/lib/libamdhip64.so``, the same soname as
+ROCm's), and libqmoe.so must bind to that one. Loaded first, it would bind
+to ROCm's copy and torch would then load its own: two runtimes in one
+process, whose streams and allocations the other does not know (kernel
+launches on torch's streams then fail).
 """
 
 import ctypes
 import os
+
+import torch  # noqa: F401  (its HIP runtime first; see above)
 
 _LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libqmoe.so")
 
