@@ -50,12 +50,13 @@ def parse():
     ap.add_argument("--only", default="", help="comma list of sweep configs to run (0-4; 5 = NVFP4 / INT4; "
                                                 "v = hipBLASLt reference points)")
     ap.add_argument("--profile", nargs="?", const="headline", default=None,
-                    choices=["headline", "decode", "moe", "vendor", "floor", "w4"],
+                    choices=["headline", "decode", "moe", "vendor", "floor", "w4", "mx"],
                     help="rocprofv3 targets: the headline kernel + a copy calibration (default), "
                          "the decode GEMMs (cfg 0/1/2 at M=1), the MoE layers at T=1 (cfg 3/4), "
                          "this build's FP8 GEMM beside hipBLASLt's (torch._scaled_mm) on both cfg 1 "
-                         "shapes at M=4096, the plain-read floor (time vs size), or the large-M MXFP4 "
-                         "path (cfg 0 at M=8192, cfg 3 at T=8192)")
+                         "shapes at M=4096, the plain-read floor (time vs size), the large-M MXFP4 "
+                         "path (cfg 0 at M=8192, cfg 3 at T=8192), or the opt-in MX activation path "
+                         "(cfg 0 at M=8192)")
     return ap.parse_args()
 
 
@@ -214,6 +215,44 @@ def roof(flops, nbytes, us, peak_key):
     return r
 
 
+def sweep_mx(codes, sc, host, gen):
+    """Config 0 shape with the opt-in MX activations (W4A4: e2m1 + e8m0 per
+    32 columns on both operands, K zero-padded 2880 -> 3072 for the MX
+    kernel) at the large-M points: the whole linear (activation quant +
+    GEMM) and the GEMM alone, against the dense FP4 peak. Flops count the
+    layer's K (2880); the padded columns are overhead."""
+    import torch
+
+    from qmoe import _capi, ops
+    from qmoe.layers.linear_common import pad_mxfp4_for_mx, quantized_matmul_mxfp4_a4
+
+    N, K = codes.shape[0], codes.shape[1] * 2
+    wp, wsp = pad_mxfp4_for_mx(codes, sc)
+    kp = wp.shape[1] * 2
+    hostp = (wp.cpu().numpy(), wsp.cpu().numpy()) if PAR.on else None
+    out = []
+    for M in (2048, 8192):
+        x = torch.randn((M, K), device="cuda", generator=gen).to(torch.bfloat16)
+        us = graph_time_us(lambda: quantized_matmul_mxfp4_a4(x, wp, wsp, K))[0]
+        q, s = ops.mx_quant(x, k_pad=kp)
+        us_gemm = graph_time_us(lambda: ops.gemm(_capi.W4A4_MX, q, wp, a_scale=s, w_scale=wsp))[0]
+        nbytes = N * kp // 2 + N * kp // 32 + 2 * M * K + 2 * M * N
+        if PAR.on:
+            olin, oq = oracle_mod("linear"), oracle_mod("quant")
+            par = PAR.linear(quantized_matmul_mxfp4_a4(x, wp, wsp, K), x, M,
+                             lambda xr: olin.w4a4_mxfp4(*oq.quantize_mx_fp4(xr, k_pad=kp), *hostp))
+        else:
+            par = {}
+        flops = 2.0 * M * N * K
+        pt = dict(cfg=0, kind="mxfp4_w4a4_mx", M=M, K=K, K_padded=kp, N=N, **roof(flops, nbytes, us, "fp4"),
+                  fp4_peak_frac=round(flops / (us * 1e-6) / PEAK["fp4"], 4), gemm_us=round(us_gemm, 2),
+                  gemm_fp4_peak_frac=round(flops / (us_gemm * 1e-6) / PEAK["fp4"], 4),
+                  gemm_fp4_peak_frac_padded_k=round(2.0 * M * N * kp / (us_gemm * 1e-6) / PEAK["fp4"], 4), **par)
+        out.append(pt)
+        log(pt)
+    return out
+
+
 def sweep_linear(only):
     import torch
 
@@ -238,6 +277,7 @@ def sweep_linear(only):
                 pt["fp4_peak_frac"] = round(2.0 * M * N * K / (us * 1e-6) / PEAK["fp4"], 4)
             out.append(pt)
             log(out[-1])
+        out.extend(sweep_mx(codes, sc, host, gen))
     if not only or "1" in only:
         for qd in ("fp8", "int8"):
             for K, N in ((4096, 14336), (14336, 4096)):
@@ -957,6 +997,36 @@ def profile_w4(args):
     log("profile target done: copy 256MiB x10")
 
 
+def profile_mx(args):
+    """rocprofv3 target: the opt-in MX activation path at config 0's shape,
+    M=8192 (K 2880 padded to 3072, N 5760): 10 activation quantizations
+    and 10 MX GEMMs after 2 warm-up calls each; then a plain 256 MiB copy
+    (10 launches) for the FETCH_SIZE / WRITE_SIZE calibration."""
+    import torch
+
+    from qmoe import _capi, ops
+    from qmoe.layers.linear_common import pad_mxfp4_for_mx
+
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    K, N, M = 2880, 5760, 8192
+    codes, sc = mxfp4_weights((N, K), gen)
+    wp, wsp = pad_mxfp4_for_mx(codes, sc)
+    kp = wp.shape[1] * 2
+    x = torch.randn((M, K), device="cuda", generator=gen).to(torch.bfloat16)
+    for _ in range(12):
+        q, s = ops.mx_quant(x, k_pad=kp)
+    for _ in range(12):
+        ops.gemm(_capi.W4A4_MX, q, wp, a_scale=s, w_scale=wsp)
+    torch.cuda.synchronize()
+    log("profile target: cfg0 MX W4A4 M=8192 quant x12, gemm x12")
+    src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log("profile target done: copy 256MiB x10")
+
+
 def profile_floor(args):
     """rocprofv3 target: the plain-read floor curve (qmoe_stream_read over
     FLOOR_MB sizes), printed as one JSON line."""
@@ -967,7 +1037,7 @@ def main():
     args = parse()
     if args.profile:
         {"headline": profile_target, "decode": profile_decode, "moe": profile_moe, "vendor": profile_vendor,
-         "floor": profile_floor, "w4": profile_w4}[args.profile](args)
+         "floor": profile_floor, "w4": profile_w4, "mx": profile_mx}[args.profile](args)
         return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (got --gpus {args.gpus}); "

@@ -34,6 +34,8 @@
 // own span, so the per-element division and encode run on S CUs instead of
 // one.
 
+#include <algorithm>
+
 #include "qmoe_common.h"
 
 namespace {
@@ -312,47 +314,91 @@ __device__ __forceinline__ int mx_exponent_ceil(float scale) {
   return e < -127 ? -127 : (e > 127 ? 127 : e);
 }
 
+// Work split: the (row, 8-column group) pairs in row-major order, one group
+// per lane per step, kMxIter groups kThreads apart per loop trip (several
+// 16-byte loads in flight), a grid-stride loop over all of them: rows of any
+// length keep every lane busy (a per-row grid would leave most of a row's
+// last 2048-column span idle at K = 2880). Kp % 32 == 0 keeps the 4 groups
+// of a 32-column block in one row and in 4 adjacent lanes, which are live or
+// past the end together.
+constexpr int kMxIter = 4;
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+// e2m1 magnitude code (0..7) of |v| <= 6 by the reference encoder's edges
+// (ties to the lower magnitude), from the f32 bits ab = bits(|v|): at 1.0 and
+// above, the f32 rounded to one mantissa bit with ties toward zero (add
+// 2^21 - 1, drop 22 bits; the carry moves 1.75+ to 2.0, 5.0 stays 4.0) is
+// 254 + 2 (exponent) + mantissa bit = code + 252. Below 1.0 the same rounding
+// of |v| + 1 (exact for the codes that matter: |v| > 2^-8) gives 254, 255
+// and 256 for codes 0, 1 and 2 (edges 0.25 and 0.75).
+__device__ __forceinline__ uint32_t e2m1_mag(uint32_t ab) {
+  const bool small = ab < 0x3f800000u;
+  const float t = small ? bits_f32(ab) + 1.0f : bits_f32(ab);
+  return ((f32_bits(t) + 0x1fffffu) >> 22) - (small ? 254u : 252u);
+}
+
 template <bool kCodes, bool kFake>
-__global__ __launch_bounds__(kThreads) void mx_quant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int64_t K,
-                                                            int64_t Kp, uint8_t* __restrict__ q, int64_t ldq,
+__global__ __launch_bounds__(kThreads) void mx_quant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int K,
+                                                            int Kp, int total, uint8_t* __restrict__ q, int64_t ldq,
                                                             uint8_t* __restrict__ scales, int64_t lds,
                                                             uint16_t* __restrict__ xq, int64_t ldxq) {
-  const int64_t row = blockIdx.x;
-  const int64_t c = ((int64_t)blockIdx.y * kThreads + threadIdx.x) * 8;
-  Row8 r;
-  if (c < K) r = load8<false>(x, row * ldx + c);
-  else
+  const uint32_t gpr = (uint32_t)Kp / 8u;  // groups per row
+  const int step = (int)gridDim.x * kThreads * kMxIter;
+  for (int g0 = (int)blockIdx.x * kThreads * kMxIter + (int)threadIdx.x; g0 < total; g0 += step) {
+    uint4 raw[kMxIter];  // 8 bf16 values
+    int64_t row[kMxIter];
+    int c[kMxIter];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) r.v[i] = 0.0f;
-  // the 4 lanes of a block are all below K or all past it (K % 32 == 0)
-  float m = amax8(r);
-  m = nanmax(m, __shfl_xor(m, 1, 64));
-  m = nanmax(m, __shfl_xor(m, 2, 64));
-  const int e = mx_exponent_ceil(m * (1.0f / 6.0f));
-  const float inv = __builtin_amdgcn_ldexpf(1.0f, -e);
-  if (c >= Kp) return;
-  uint32_t w = 0;
-  uint32_t d[4] = {0u, 0u, 0u, 0u};
+    for (int it = 0; it < kMxIter; ++it) {
+      const int g = g0 + it * kThreads;
+      const uint32_t rr = (uint32_t)g / gpr;
+      row[it] = rr;
+      c[it] = (int)(((uint32_t)g - rr * gpr) * 8u);
+      raw[it] = g < total && c[it] < K ? *reinterpret_cast<const uint4*>(x + row[it] * ldx + c[it])
+                                       : make_uint4(0u, 0u, 0u, 0u);
+    }
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float v = fminf(fmaxf(r.v[i] * inv, -6.0f), 6.0f);
-    const float a = fabsf(v);
-    const uint32_t mag = (uint32_t)(a > 0.25f) + (uint32_t)(a > 0.75f) + (uint32_t)(a > 1.25f) +
-                         (uint32_t)(a > 1.75f) + (uint32_t)(a > 2.5f) + (uint32_t)(a > 3.5f) + (uint32_t)(a > 5.0f);
-    const uint32_t code = mag | (v < 0.0f ? 8u : 0u);
-    w |= code << (4 * i);
-    if (kFake) {
-      // e2m1 magnitude of the code, times 2^e: exact in bf16 (3 significant bits)
-      const float mv = mag < 4u ? 0.5f * (float)mag : (mag < 6u ? (float)(mag - 2u) : (mag == 6u ? 4.0f : 6.0f));
-      const float dv = __builtin_amdgcn_ldexpf(v < 0.0f ? -mv : mv, e);
-      d[i >> 1] |= (f32_bits(dv) >> 16) << (16 * (i & 1));
+    for (int it = 0; it < kMxIter; ++it) {
+      const uint32_t wd[4] = {raw[it].x, raw[it].y, raw[it].z, raw[it].w};
+      // block amax on the absolute-value bits of the bf16 pairs (ordered
+      // like the values; inputs are finite): packed 16-bit maxima
+      u16x2 m2 = __builtin_bit_cast(u16x2, wd[0] & 0x7fff7fffu);
+#pragma unroll
+      for (int i = 1; i < 4; ++i) m2 = __builtin_elementwise_max(m2, __builtin_bit_cast(u16x2, wd[i] & 0x7fff7fffu));
+      uint32_t mb = (uint32_t)max(m2.x, m2.y) << 16;
+      mb = max(mb, (uint32_t)__shfl_xor((int)mb, 1, 64));
+      mb = max(mb, (uint32_t)__shfl_xor((int)mb, 2, 64));
+      const int e = mx_exponent_ceil(bits_f32(mb) * (1.0f / 6.0f));
+      const float inv = __builtin_amdgcn_ldexpf(1.0f, -e);
+      if (g0 + it * kThreads >= total) continue;
+      uint32_t w = 0;
+      uint32_t d[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float xv = bits_f32(i & 1 ? wd[i >> 1] & 0xffff0000u : wd[i >> 1] << 16);
+        // |x| 2^-e <= amax 2^-e <= 6: the reference's clamp to +-6 never
+        // binds; + 0.0f turns -0 into +0 (the encoder's sign is v < 0)
+        const uint32_t vb = f32_bits(xv * inv + 0.0f);
+        const uint32_t mag = e2m1_mag(vb & 0x7fffffffu);
+        const uint32_t code = mag | ((vb >> 28) & 8u);
+        const float v = bits_f32(vb);
+        w |= code << (4 * i);
+        if (kFake) {
+          // e2m1 magnitude of the code, times 2^e: exact in bf16 (3 significant bits)
+          const float mv =
+              mag < 4u ? 0.5f * (float)mag : (mag < 6u ? (float)(mag - 2u) : (mag == 6u ? 4.0f : 6.0f));
+          const float dv = __builtin_amdgcn_ldexpf(v < 0.0f ? -mv : mv, e);
+          d[i >> 1] |= (f32_bits(dv) >> 16) << (16 * (i & 1));
+        }
+      }
+      if (kCodes) {
+        *reinterpret_cast<uint32_t*>(q + row[it] * ldq + c[it] / 2) = w;
+        if ((threadIdx.x & 3) == 0) scales[row[it] * lds + c[it] / 32] = (uint8_t)(e + 127);
+      }
+      if (kFake && c[it] < K)
+        *reinterpret_cast<uint4*>(xq + row[it] * ldxq + c[it]) = make_uint4(d[0], d[1], d[2], d[3]);
     }
   }
-  if (kCodes) {
-    *reinterpret_cast<uint32_t*>(q + row * ldq + c / 2) = w;
-    if ((threadIdx.x & 3) == 0) scales[row * lds + c / 32] = (uint8_t)(e + 127);
-  }
-  if (kFake && c < K) *reinterpret_cast<uint4*>(xq + row * ldxq + c) = make_uint4(d[0], d[1], d[2], d[3]);
 }
 
 template <int kQdt, int kMode, bool kInF32, bool kBlock>
@@ -427,20 +473,24 @@ extern "C" int qmoe_mx_quant(const void* x, int64_t ldx, int64_t M, int64_t K, i
     return QMOE_ERR_ARG;
   if (xq && (ldxq < K || (ldxq % 8) != 0 || (reinterpret_cast<uintptr_t>(xq) & 15))) return QMOE_ERR_ARG;
   if (M == 0) return QMOE_OK;
-  if (M > 0x7fffffff || cdiv<int64_t>(Kp, kThreads * 8) > 65535) return QMOE_ERR_ARG;
-  const dim3 grid((unsigned)M, (unsigned)cdiv<int64_t>(Kp, kThreads * 8));
+  // group indices in 32 bits, including the last loop trip's overshoot
+  const int64_t total = M * (Kp / 8);
+  if (total + (int64_t)kThreads * kMxIter * 4096 > 0x7fffffffLL) return QMOE_ERR_ARG;
+  // enough workgroups for every CU several times over, at most one loop trip
+  // of groups each when that is fewer
+  const dim3 grid((unsigned)std::min<int64_t>(cdiv<int64_t>(total, kThreads * kMxIter), 4096));
   const uint16_t* xb = static_cast<const uint16_t*>(x);
   uint8_t* qb = static_cast<uint8_t*>(q);
   uint8_t* sb = static_cast<uint8_t*>(scales);
   uint16_t* fb = static_cast<uint16_t*>(xq);
   if (codes && xq)
-    hipLaunchKernelGGL((mx_quant_kernel<true, true>), grid, dim3(kThreads), 0, stream, xb, ldx, K, Kp, qb, ldq, sb,
-                       lds, fb, ldxq);
+    hipLaunchKernelGGL((mx_quant_kernel<true, true>), grid, dim3(kThreads), 0, stream, xb, ldx, (int)K, (int)Kp,
+                       (int)total, qb, ldq, sb, lds, fb, ldxq);
   else if (codes)
-    hipLaunchKernelGGL((mx_quant_kernel<true, false>), grid, dim3(kThreads), 0, stream, xb, ldx, K, Kp, qb, ldq, sb,
-                       lds, fb, ldxq);
+    hipLaunchKernelGGL((mx_quant_kernel<true, false>), grid, dim3(kThreads), 0, stream, xb, ldx, (int)K, (int)Kp,
+                       (int)total, qb, ldq, sb, lds, fb, ldxq);
   else
-    hipLaunchKernelGGL((mx_quant_kernel<false, true>), grid, dim3(kThreads), 0, stream, xb, ldx, K, Kp, qb, ldq, sb,
-                       lds, fb, ldxq);
+    hipLaunchKernelGGL((mx_quant_kernel<false, true>), grid, dim3(kThreads), 0, stream, xb, ldx, (int)K, (int)Kp,
+                       (int)total, qb, ldq, sb, lds, fb, ldxq);
   return hipGetLastError() == hipSuccess ? QMOE_OK : QMOE_ERR_LAUNCH;
 }
