@@ -236,3 +236,43 @@ def test_layout_markers():
 
     assert lc.KEEP_VLLM_LAYOUT_ATTR == "_tpu_keep_vllm_weight_layout"
     assert lc.WEIGHT_FLIPPED_ATTR == "_tpu_weight_flipped"
+
+
+@pytest.mark.parametrize("experts_start", [torch.tensor(0, dtype=torch.int32), torch.tensor(8, dtype=torch.int32), 8])
+def test_fused_moe_gmm_refuses_expert_parallel_offsets(experts_start):
+    """The reference passes experts_start as a 0-d int32 tensor exactly when
+    expert parallelism is on (`layers/adapter/fused_moe.py:241-293`); this
+    build holds the whole expert set, so any tensor and any non-zero offset
+    raises before anything runs (CPU tensors: no kernel is reached)."""
+    from qmoe.layers.fused_moe import fused_moe_gmm
+
+    E, H, I, T = 4, 256, 128, 3
+    x = torch.zeros((T, H), dtype=torch.bfloat16)
+    w1 = torch.zeros((E, 2 * I, H), dtype=torch.bfloat16)
+    w2 = torch.zeros((E, H, I), dtype=torch.bfloat16)
+    tw = torch.ones((T, 2), dtype=torch.float32)
+    ti = torch.zeros((T, 2), dtype=torch.int32)
+    with pytest.raises(NotImplementedError, match="expert parallelism"):
+        fused_moe_gmm(x, w1, w2, None, None, None, None, tw, ti, experts_start, 2, "silu")
+
+
+def test_mx_activation_host_logic():
+    """Host side of the opt-in MX activations: the K the MX kernel takes, the
+    zero padding of the weight, and the kernel route (no GPU needed)."""
+    from qmoe import _capi, ops
+    from qmoe.layers.linear_common import mx_padded_k, pad_mxfp4_for_mx
+
+    assert [mx_padded_k(k) for k in (32, 1024, 2880, 3072, 4096, 7168)] == [1024, 1024, 3072, 3072, 4096, 7168]
+    wq = torch.randint(0, 256, (8, 1440), dtype=torch.uint8)
+    ws = torch.randint(100, 140, (8, 90), dtype=torch.uint8)
+    wp, wsp = pad_mxfp4_for_mx(wq, ws)
+    assert wp.shape == (8, 1536) and wsp.shape == (8, 96)
+    assert torch.equal(wp[:, :1440], wq) and (wp[:, 1440:] == 0).all()
+    assert torch.equal(wsp[:, :90], ws) and (wsp[:, 90:] == 127).all()
+    assert ops.plan_for_shape(_capi.W4A4_MX, 8192, 5760, 3072)[4] == "tiled_mx_persistent"
+    assert ops.plan_for_shape(_capi.W4A4_MX, 1, 256, 1024)[4] == "tiled_mx_persistent"
+    for k in (2880, 512):  # not a multiple of 512 / fewer than 4 stages
+        with pytest.raises(RuntimeError):
+            ops.plan_for_shape(_capi.W4A4_MX, 256, 256, k)
+    with pytest.raises(RuntimeError):  # no fused activation on the MX kernel
+        ops.plan_for_shape(_capi.W4A4_MX, 256, 512, 1024, activation="silu")
