@@ -7,7 +7,7 @@ import numpy as np
 
 from oracle.codecs import bf16_round, dequant_int4, dequant_mxfp4, dequant_nvfp4, e4m3_decode
 from oracle.linear import _mm, w8a8_gmm
-from oracle.quant import quantize_act
+from oracle.quant import quantize_act, quantize_mx_fp4
 
 
 def prepare_routed(topk_ids, topk_weights=None, num_experts=None, skip_padded_tokens=False):
@@ -94,6 +94,9 @@ class ExpertWeights:
       "fp8_w8a16": w13 e4m3 [E, 2I, H] + per-(row, 128) scale [E, 2I, H/128]; w2 likewise
       "fp8_rowquant" / "int8_rowquant": as "fp8" / "int8" with per-channel scales
       "bf16": w13 [E, 2I, H] f32 (bf16 values); w2 [E, H, I]
+      "mxfp4_mx": weights as "mxfp4" (unpadded); each expert linear's input rows (the
+          gathered tokens, the bf16 intermediate) MX-quantized per 32 columns
+          (``quant.quantize_mx_fp4``) and dequantized exactly: the opt-in W4A4 regime
     Activations: bf16 for mxfp4/nvfp4/int4/bf16 (W4A16 / W16A16) and fp8_w8a16 (weights
     dequantized to bf16(code * bf16(scale)), `kernels/megablox/gmm_v2.py:452-462`);
     per-(row, 128) e4m3 for fp8_block (the blockwise W8A8 recipe of config 4); per-(row,
@@ -117,7 +120,7 @@ class ExpertWeights:
             s = None
             if self.fmt != "bf16":
                 s = self.s13[e] if which == 13 else self.s2[e]
-            if self.fmt == "mxfp4":
+            if self.fmt in ("mxfp4", "mxfp4_mx"):
                 d = dequant_mxfp4(w, s)
             elif self.fmt == "nvfp4":
                 d = dequant_nvfp4(w, s)
@@ -150,6 +153,9 @@ class ExpertWeights:
             out = (_mm(xv, wv) * xs[:, None]).astype(np.float32) if qd == "fp8" else \
                 (np.matmul(xq.astype(np.float64), wv.astype(np.float64).T).astype(np.float32) * xs[:, None]).astype(np.float32)
             out = (out * np.asarray(s, np.float32)[None, :]).astype(np.float32)
+        elif self.fmt == "mxfp4_mx":
+            xq, xs = quantize_mx_fp4(x)
+            out = _mm(dequant_mxfp4(xq, xs), self.dense(which, e))
         elif self.fmt != "fp8_block":
             out = _mm(x, self.dense(which, e))
         else:

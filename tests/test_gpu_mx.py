@@ -151,3 +151,60 @@ def test_mxfp4_linear_mx_activations(dev, M):
     # to 0.16 of the row max at M = 64), so only a loose agreement is asserted
     ref16 = linear.w4a16_mxfp4(x, wq, ws, b)
     assert_close_rows(got, ref16, "mx vs w4a16", rel=0.3, cos_min=0.99)
+
+
+@pytest.mark.parametrize("T", [8, 1024])
+def test_mxfp4_moe_mx_activations(dev, T):
+    """GPT-OSS-form MXFP4 MoE layer (interleaved gate/up rows, biases,
+    softmax top 4, swigluoai; H = I = 2880 padded to 3072) with MX
+    activations: at T = 1024 (512 rows per routed expert) both expert GEMMs
+    run the grouped MX tiles, at T = 8 the bf16-activation kernels on the
+    dequantized MX activations. Sampled tokens against the oracle's
+    "mxfp4_mx" recipe (MX quantization of the gathered tokens and of the bf16
+    intermediate)."""
+    from qmoe import ops
+    from qmoe.layers import quantization as q
+    from oracle import moe as omoe
+    from oracle import routing
+
+    print(f"mxfp4 moe mx activations T={T}", flush=True)
+    rng = np.random.default_rng(T)
+    E, H, I, k = 8, 2880, 2880, 4
+    layer = torch.nn.Module()
+    import types
+
+    layer.moe_config = types.SimpleNamespace(experts_per_token=k, has_bias=True)
+    layer.renormalize, layer.scoring_func, layer.e_score_correction_bias = True, "softmax", None
+    layer.use_grouped_topk, layer.num_expert_group, layer.topk_group = False, None, None
+    layer.routed_scaling_factor, layer.custom_routing_function, layer.activation = 1.0, None, "swigluoai"
+    method = q.Mxfp4MoEMethod(layer.moe_config, mx_activations=True)
+    method.create_weights(layer, E, H, I, torch.bfloat16)
+    c13 = rng.integers(0, 256, (E, 2 * I, H // 2), dtype=np.uint8)
+    s13 = (127 - rng.integers(0, 9, (E, 2 * I, H // 32))).astype(np.uint8)
+    c2 = rng.integers(0, 256, (E, H, I // 2), dtype=np.uint8)
+    s2 = (127 - rng.integers(0, 9, (E, H, I // 32))).astype(np.uint8)
+    b13 = codecs.bf16_round((rng.standard_normal((E, 2 * I)) * 0.1).astype(np.float32))
+    b2 = codecs.bf16_round((rng.standard_normal((E, H)) * 0.1).astype(np.float32))
+    layer.w13_weight.data = _t(c13, dev)
+    layer.w13_weight_scale.data = _t(s13, dev)
+    layer.w2_weight.data = _t(c2, dev)
+    layer.w2_weight_scale.data = _t(s2, dev)
+    layer.w13_bias.data = _t(b13, dev, torch.bfloat16)
+    layer.w2_bias.data = _t(b2, dev, torch.bfloat16)
+    method.process_weights_after_loading(layer)
+    assert layer.w13_weight.shape == (E, 2 * I, 1536) and layer.w2_weight_scale.shape == (E, H, 96)
+    x = codecs.bf16_round(rng.standard_normal((T, H)).astype(np.float32))
+    logits = codecs.bf16_round(rng.standard_normal((T, E)).astype(np.float32))
+    with ops.record_plans() as plans:
+        got = method.apply_monolithic(layer, _t(x, dev, torch.bfloat16), _t(logits, dev, torch.bfloat16))
+    paths = [pl[4] for pl in plans]
+    if T == 1024:
+        assert paths == ["tiled_mx", "tiled_mx"], paths
+    else:
+        assert "tiled_mx" not in paths and paths, paths
+    tw, ids = routing.select_experts(logits, k, True, "softmax")
+    dei = lambda a: np.concatenate([a[:, 0::2], a[:, 1::2]], axis=1)  # noqa: E731
+    weights = omoe.ExpertWeights("mxfp4_mx", dei(c13), dei(s13), c2, s2, dei(b13), b2)
+    rows = np.unique(np.linspace(0, T - 1, min(T, 24)).astype(int))
+    ref = omoe.fused_moe_tokens(x[rows], weights, tw[rows], ids[rows], "swigluoai", E)
+    assert_close_rows(got.float().cpu().numpy()[rows], ref, f"mxfp4 moe mx T={T}")

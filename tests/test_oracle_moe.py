@@ -190,3 +190,29 @@ def test_gmm_expert_linear_is_dequantize_then_matmul(fmt):
         wd = quant.dequant_codes(wq[e], fmt).astype(np.float64) * ws[e][:, None]
         ref = xd @ wd.T
         np.testing.assert_allclose(ew.linear(13, e, x), ref, rtol=2e-6, atol=2e-6 * np.abs(ref).max())
+
+
+def test_mx_activation_format_is_two_w4a4_linears():
+    """The "mxfp4_mx" expert format on one expert, top 1, routing weight 1:
+    the layer is the pinned W4A4 linear of the MX-quantized tokens, the
+    activation, a bf16 round, then the W4A4 linear of the MX-quantized
+    intermediate (`oracle.linear.w4a4_mxfp4`, `oracle.quant.quantize_mx_fp4`)."""
+    from oracle import linear, quant
+
+    rng = np.random.default_rng(4)
+    T, H, I = 5, 64, 64
+    w13 = rng.integers(0, 256, (1, 2 * I, H // 2), dtype=np.uint8)
+    s13 = rng.integers(120, 128, (1, 2 * I, H // 32), dtype=np.uint8)
+    w2 = rng.integers(0, 256, (1, H, I // 2), dtype=np.uint8)
+    s2 = rng.integers(120, 128, (1, H, I // 32), dtype=np.uint8)
+    x = codecs.bf16_round(rng.standard_normal((T, H)).astype(np.float32))
+    out, _, _ = moe.fused_moe(x, moe.ExpertWeights("mxfp4_mx", w13, s13, w2, s2), np.ones((T, 1), np.float32),
+                              np.zeros((T, 1), np.int32), "swigluoai")
+    gu = linear.w4a4_mxfp4(*quant.quantize_mx_fp4(x), w13[0], s13[0])
+    a = codecs.bf16_round(moe.act_fn(gu[:, :I], gu[:, I:], "swigluoai"))
+    y = linear.w4a4_mxfp4(*quant.quantize_mx_fp4(a), w2[0], s2[0])
+    # the layer keeps gate_up in f32 up to the activation; the composition rounds it to bf16 first
+    np.testing.assert_allclose(out, y, rtol=2e-2, atol=2e-2 * np.abs(y).max())
+    assert not np.array_equal(out, moe.fused_moe(x, moe.ExpertWeights("mxfp4", w13, s13, w2, s2),
+                                                 np.ones((T, 1), np.float32), np.zeros((T, 1), np.int32),
+                                                 "swigluoai")[0])

@@ -17,8 +17,8 @@ int qmoe_tiled_launch(int kind, GemmParams p, hipStream_t st);
 int qmoe_tiled_check(int kind, const GemmParams& p, int* tile);
 bool qmoe_f8_plan(const GemmParams& p, bool blk, int* bm_out, int* ksplit_out, int64_t* ws_bytes);
 int qmoe_f8_launch(GemmParams p, bool blk, void* workspace, int64_t ws_bytes, hipStream_t st);
-bool qmoe_mx_plan(const GemmParams& p);
-int qmoe_mx_launch(const GemmParams& p, hipStream_t st);
+int qmoe_mx_plan(const GemmParams& p);
+int qmoe_mx_launch(GemmParams p, hipStream_t st);
 bool qmoe_f8_persistent(const GemmParams& p, bool blk);
 bool qmoe_w4_plan(const GemmParams& p, int fmt, int* bm_out, int* ksplit_out, int64_t* ws_bytes);
 int qmoe_w4_launch(GemmParams p, int fmt, void* workspace, int64_t ws_bytes, hipStream_t st);
@@ -200,6 +200,7 @@ enum Path {
   kPathSkinnyPass = 4,  // weight streaming in 64-row passes (K outside every tiled granule)
   kPathF8Persistent = 5,  // 1-byte x 1-byte 256 x 256 tiles, persistent workgroups
   kPathMx = 6,            // e2m1 x e2m1 with e8m0 scales on both, 256 x 256 persistent tiles
+  kPathMxTiles = 7,       // the same operands, grouped tiles (one tile per workgroup)
 };
 
 // The one place that decides which kernel runs a problem: the streaming
@@ -212,9 +213,10 @@ enum Path {
 
 int qmoe_route_of(const qmoe_gemm_desc* d, GemmParams& p, QmoeRoute* r) {
   const int kind = kernel_kind(d);
-  if (kind == QK_W4A4_MX) {  // one kernel takes MX activations
-    if (!qmoe_mx_plan(p)) return QMOE_ERR_ARG;
-    *r = QmoeRoute{kPathMx, 256, 1, 0};
+  if (kind == QK_W4A4_MX) {  // the MX kernels take MX activations, nothing else does
+    const int bm = qmoe_mx_plan(p);
+    if (!bm) return QMOE_ERR_ARG;
+    *r = QmoeRoute{p.group_offs ? kPathMxTiles : kPathMx, bm, 1, 0};
     return QMOE_OK;
   }
   if (use_skinny(d) && qmoe_skinny_check(kind, p) == QMOE_OK) {
@@ -266,7 +268,8 @@ int qmoe_run_route(const qmoe_gemm_desc* d, const QmoeRoute& r, GemmParams p, vo
     case kPathF8Persistent: return qmoe_f8_launch(p, kind == QK_W8A8_BLK, workspace, ws_bytes, stream);
     case kPathW4: return qmoe_w4_launch(p, w4_fmt(d), workspace, ws_bytes, stream);
     case kPathTiled: return qmoe_tiled_launch(kind, p, stream);
-    case kPathMx: return qmoe_mx_launch(p, stream);
+    case kPathMx:
+    case kPathMxTiles: return qmoe_mx_launch(p, stream);
     default: {
       GemmParams q;
       qmoe_to_params(d, &q);

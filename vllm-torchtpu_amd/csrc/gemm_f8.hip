@@ -76,9 +76,14 @@ __device__ __forceinline__ i32x8 fp4_op(const i32x4& v) {
   return __builtin_shufflevector(v, v, 0, 1, 2, 3, -1, -1, -1, -1);
 }
 
-template <bool INT, int BM, int BN, bool ACT, int KB, bool BLK, bool WPC = false>
+template <bool INT, int BM, int BN, bool ACT, int KB, bool BLK, bool WPC = false, bool MX = false>
 __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, int m_tiles, int n_tiles) {
   static_assert(KB == 64 || KB == 128, "K bytes per LDS stage");
+  // MX (QK_W4A4_MX): e2m1 codes of both operands in the 128-byte stages (256
+  // k), their e8m0 bytes ([row][8] per stage) copied beside them; the MFMA
+  // applies both scales, so the epilogue's token and weight scales are 1
+  // (the persistent kernel's mode 2 describes the operand layout)
+  static_assert(!MX || (KB == 128 && !INT && !BLK && BM >= 128), "MX: 128-byte stages, tiles of >= 128 tokens");
   // BLK: block scales (W8A8_BLK): one 128-byte stage is one 128-column K step;
   // the token scale of step s is a_scale[row, s >> a_kshift]. Without WPC the
   // weight scale is that of the tile's 128-row block and K block s >> w_kshift;
@@ -102,6 +107,10 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
   constexpr int B3 = KB == 64 ? 64 : 0;                // and of array 3
   __shared__ __align__(1024) uint8_t sW0[BN * KB], sW1[BN * KB], sW2[B2 ? BN * B2 : 16], sW3[B3 ? BN * B3 : 16];
   __shared__ __align__(1024) uint8_t sX0[XRS * KB], sX1[XRS * KB], sX2[B2 ? XRS * B2 : 16], sX3[B3 ? XRS * B3 : 16];
+  // MX scale bytes of stage buffers 0..2
+  constexpr int QWB = MX ? BN * 8 : 16, QXB = MX ? BM * 8 : 16, QB2 = MX && TRI;
+  __shared__ __align__(16) uint8_t sQW0[QWB], sQW1[QWB], sQW2[QB2 ? QWB : 16];
+  __shared__ __align__(16) uint8_t sQX0[QXB], sQX1[QXB], sQX2[QB2 ? QXB : 16];
   __shared__ int s_info[4];
   __shared__ float s_sx[BM], s_rw[BM], s_ws[BN], s_bs[BN];
   // BLK: per-stage scales, one 64-float slot per wavefront: [0, BM) token
@@ -137,7 +146,7 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
   if (tid < BM) {
     const int R = row0 + min(tid, rows - 1);
     const int ar = p.a_rows ? p.a_rows[R] : R;
-    e_sx = BLK ? 1.0f : p.a_scale[(int64_t)ar * p.lds_a];
+    e_sx = BLK || MX ? 1.0f : p.a_scale[(int64_t)ar * p.lds_a];
     if (p.row_weight) e_rw = bf16_to_f32(p.row_weight[R]);
     e_yr = p.y_rows ? p.y_rows[R] : R;
   }
@@ -149,7 +158,7 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
     } else {
       n = min(n0 + tid, nlim - 1);
     }
-    e_ws = BLK && !WPC ? 1.0f : static_cast<const float*>(p.w_scale)[(int64_t)g * p.ws_gstride + n];
+    e_ws = (BLK && !WPC) || MX ? 1.0f : static_cast<const float*>(p.w_scale)[(int64_t)g * p.ws_gstride + n];
     if (p.bias) e_bs = p.bias[(int64_t)g * p.bias_gstride + n];
   }
 
@@ -191,6 +200,32 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
     }
     woff[j] = (uint32_t)n * (uint32_t)p.ldw + chunk_of(r);
   }
+  // MX scale copies: 32 rows x 8 bytes per instruction (lane -> row lane / 2,
+  // dword lane & 1), QW weight and QX activation instructions per wavefront
+  constexpr int QW = MX ? BN / 128 : 0, QX = MX ? BM / 128 : 0;
+  const uint8_t* wqbase = static_cast<const uint8_t*>(p.w_scale) + (int64_t)g * p.ws_gstride;
+  const uint8_t* xqbase = reinterpret_cast<const uint8_t*>(p.a_scale);
+  uint32_t qwoff[QW ? QW : 1], qxrow[QX ? QX : 1];
+  if constexpr (MX) {
+#pragma unroll
+    for (int j = 0; j < QW; ++j) {
+      const int r = (wave * QW + j) * 32 + (lane >> 1);
+      int n;
+      if (ACT) {
+        const int cidx = min(n0 + (r % (BN / 2)), nlim - 1);
+        n = (r < BN / 2 ? 0 : p.N / 2) + cidx;
+      } else {
+        n = min(n0 + r, nlim - 1);
+      }
+      qwoff[j] = (uint32_t)n * (uint32_t)p.ldws + (uint32_t)(lane & 1) * 4u;
+    }
+#pragma unroll
+    for (int j = 0; j < QX; ++j) {
+      const int r = (wave * QX + j) * 32 + (lane >> 1);
+      const int R = row0 + min(r, rows - 1);
+      qxrow[j] = (uint32_t)(p.a_rows ? p.a_rows[R] : R);
+    }
+  }
   // BLK: this lane's source for the per-stage scale copy (4 bytes; the K
   // block index is added per stage): LDS slot wave*64 + lane holds token
   // scale `slot` for slot < BM, the scale of LDS weight rows
@@ -216,14 +251,30 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
   // MFMA loop.
   // split-K: this workgroup's K range, in units of 256 bytes (two 128-byte
   // or four 64-byte stages, so every pipeline below runs whole loops)
-  const int NU = p.K / 256;
+  const int NU = (MX ? p.K / 2 : p.K) / 256;
   const int u0 = (int)((int64_t)NU * blockIdx.z / p.ksplit);
   const int u1 = (int)((int64_t)NU * (blockIdx.z + 1) / p.ksplit);
   const uint32_t kbase = (uint32_t)u0 * 256u;
-  auto copy_stage = [&](uint8_t* dW, uint8_t* dX, float* dS, int ks) {
+  auto copy_stage = [&](uint8_t* dW, uint8_t* dX, float* dS, uint8_t* dQW, uint8_t* dQX, int ks) {
     const uint32_t kb = kbase + (uint32_t)ks * (uint32_t)KB;
     if constexpr (BLK)
       __builtin_amdgcn_global_load_lds(sc_src + ((kb / 128) >> sc_shift), QMOE_LDS(dS + wave * 64), 4, 0, 0);
+    if constexpr (MX) {
+      const uint32_t kq = kb / 16;  // one scale byte per 16 code bytes
+#pragma unroll
+      for (int j = 0; j < QW; ++j) {
+        uint32_t o = qwoff[j];
+        asm volatile("" : "+v"(o));
+        __builtin_amdgcn_global_load_lds(wqbase + (o + kq), QMOE_LDS(dQW + (wave * QW + j) * 256), 4, 0, 0);
+      }
+#pragma unroll
+      for (int j = 0; j < QX; ++j) {
+        uint32_t r = qxrow[j];
+        asm volatile("" : "+v"(r));
+        const uint8_t* src = xqbase + (uint64_t)r * (uint64_t)p.lds_a + (kq + (uint32_t)(lane & 1) * 4u);
+        __builtin_amdgcn_global_load_lds(src, QMOE_LDS(dQX + (wave * QX + j) * 256), 4, 0, 0);
+      }
+    }
 #pragma unroll
     for (int j = 0; j < WI; ++j) {
       uint32_t o = woff[j];
@@ -249,15 +300,28 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       if (KB == 64) po[t][h] = rl * 64 + (((2 * kh + h) ^ ((rl >> 2) & 3)) * 16);
-      else po[t][h] = rl * 128 + (((4 * t + 2 * kh + h) ^ ((rl & 7) ^ ((rl >> 3) & 1))) * 16);
+      else  // MX: 16 bytes of 64-k step h of the half (chunk 4t + 2h + kh)
+        po[t][h] = rl * 128 + (((MX ? 4 * t + 2 * h + kh : 4 * t + 2 * kh + h) ^ ((rl & 7) ^ ((rl >> 3) & 1))) * 16);
     }
   auto wrow = [&](int i) {  // LDS row of this wavefront's weight block i
     if (ACT) return (i < NI / 2 ? 0 : BN / 2) + wn * (TN / 2) + (i % (NI / 2)) * 32;
     return wn * TN + i * 32;
   };
   i32x8 wf[2][NI], xf[2][MJ];
+  // MX: scale dword of half t (32-k blocks 4t + 2h + kh), shifted so that
+  // byte 2h is the lane's block of step h
+  uint32_t wsc[2][MX ? NI : 1], xsc[2][MX ? MJ : 1];
   // operands of k-step `ks` of the stage in (sW, sX) into register set t
-  auto read_frags = [&](const uint8_t* sW, const uint8_t* sX, int ks, int t) {
+  auto read_frags = [&](const uint8_t* sW, const uint8_t* sX, const uint8_t* sQW, const uint8_t* sQX, int ks,
+                        int t) {
+    if constexpr (MX) {
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+        wsc[t][i] = *reinterpret_cast<const uint32_t*>(sQW + (wrow(i) + rl) * 8 + ks * 4) >> (8 * kh);
+#pragma unroll
+      for (int j = 0; j < MJ; ++j)
+        xsc[t][j] = *reinterpret_cast<const uint32_t*>(sQX + (wm * TM + j * 32 + rl) * 8 + ks * 4) >> (8 * kh);
+    }
     const int h0 = KB == 64 ? po[0][0] : po[ks][0], h1 = KB == 64 ? po[0][1] : po[ks][1];
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
@@ -297,6 +361,23 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
     }
   };
   auto mma = [&](int t) {
+    if constexpr (MX) {
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+#pragma unroll
+        for (int j = 0; j < MJ; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fp4_op(lo4(wf[t][i])), fp4_op(lo4(xf[t][j])),
+                                                                      acc[i][j], 4, 4, 0, (int)wsc[t][i], 0,
+                                                                      (int)xsc[t][j]);
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+#pragma unroll
+        for (int j = 0; j < MJ; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fp4_op(hi4(wf[t][i])), fp4_op(hi4(xf[t][j])),
+                                                                      acc[i][j], 4, 4, 2, (int)wsc[t][i], 2,
+                                                                      (int)xsc[t][j]);
+      return;
+    }
     if constexpr (INT) {
       // the two 32-k halves of the k-step go to every accumulator in turn:
       // the second MFMA of an accumulator comes NI * MJ MFMAs after its first,
@@ -337,9 +418,9 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
     }
   };
 
-  constexpr int CPS = WI + XI + (BLK ? 1 : 0);  // copy instructions per wavefront per stage
-  constexpr int NM = NI * MJ * (INT ? 2 : 1);  // MFMAs per k-step
-  constexpr int NR = 2 * (NI + MJ);            // LDS operand reads per k-step
+  constexpr int CPS = WI + XI + (BLK ? 1 : 0) + QW + QX;  // copy instructions per wavefront per stage
+  constexpr int NM = NI * MJ * (INT || MX ? 2 : 1);       // MFMAs per k-step
+  constexpr int NR = (MX ? 3 : 2) * (NI + MJ);            // LDS operand reads per k-step
   if constexpr (KB == 64) {
     // ---- four stages of one k-step (KS % 4 == 0) ----
     // Stage s lives in LDS buffer s % 4 and is copied four stages ahead.
@@ -352,13 +433,13 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
     // the last stage into a consumed buffer, which is never read again), so
     // the loop body has no branch.
     const int KS = (u1 - u0) * 4;
-    copy_stage(sW0, sX0, sS0, 0);
-    copy_stage(sW1, sX1, sS0, 1);
-    copy_stage(sW2, sX2, sS0, 2);
-    copy_stage(sW3, sX3, sS0, 3);
+    copy_stage(sW0, sX0, sS0, sQW0, sQX0, 0);
+    copy_stage(sW1, sX1, sS0, sQW0, sQX0, 1);
+    copy_stage(sW2, sX2, sS0, sQW0, sQX0, 2);
+    copy_stage(sW3, sX3, sS0, sQW0, sQX0, 3);
     wait_copies_upto<3 * CPS>();
     __syncthreads();
-    read_frags(sW0, sX0, 0, 0);
+    read_frags(sW0, sX0, sQW0, sQX0, 0, 0);
     auto stage = [&](uint8_t* fW, uint8_t* fX, uint8_t* nW, uint8_t* nX, int s, int t) {
       wait_copies_upto<2 * CPS>();  // copies issued after stage s+1's: s+2, s+3
       stage_barrier();
@@ -366,8 +447,8 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
       // order: the compiler treats an LDS copy as a write that may alias any
       // LDS read after it, so reads placed after the copies could not be
       // interleaved with this stage's MFMAs
-      read_frags(nW, nX, 0, t ^ 1);
-      copy_stage(fW, fX, sS0, min(s + 4, KS - 1));
+      read_frags(nW, nX, sQW0, sQX0, 0, t ^ 1);
+      copy_stage(fW, fX, sS0, sQW0, sQX0, min(s + 4, KS - 1));
       mma(t);
       interleave<0, NM, NR, CPS>();
     };
@@ -391,9 +472,10 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
     // stage s+3, so a copy has two stages to land.
     const int KS = (u1 - u0) * 2;
     constexpr int AHEAD = TRI ? 3 : 2;
-    auto stage = [&](uint8_t* cW, uint8_t* cX, float* cS, uint8_t* nW, uint8_t* nX, int s) {
+    auto stage = [&](uint8_t* cW, uint8_t* cX, float* cS, uint8_t* cQW, uint8_t* cQX, uint8_t* nW, uint8_t* nX,
+                     uint8_t* nQW, uint8_t* nQX, int s) {
       mma(0);
-      read_frags(cW, cX, 1, 1);
+      read_frags(cW, cX, cQW, cQX, 1, 1);
       read_scales(cS);
       interleave<0, NM, NR + (BLK ? MJ + NI : 0), 0>();
       // every MFMA of k-step 0 is issued before the wait (the wait has no
@@ -405,31 +487,31 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
       // k-step 0 of stage s+1 is read before the copies are issued (an LDS
       // copy may alias any later LDS read for the compiler, which would keep
       // the reads behind every copy and expose their latency)
-      read_frags(nW, nX, 0, 0);
-      copy_stage(cW, cX, cS, min(s + AHEAD, KS - 1));
+      read_frags(nW, nX, nQW, nQX, 0, 0);
+      copy_stage(cW, cX, cS, cQW, cQX, min(s + AHEAD, KS - 1));
       mma(1);
       apply_scales();
       interleave<0, NM, NR, CPS>();
     };
-    copy_stage(sW0, sX0, sS0, 0);
-    copy_stage(sW1, sX1, sS1, 1);
-    if constexpr (TRI) copy_stage(sW2, sX2, sS2, min(2, KS - 1));
+    copy_stage(sW0, sX0, sS0, sQW0, sQX0, 0);
+    copy_stage(sW1, sX1, sS1, sQW1, sQX1, 1);
+    if constexpr (TRI) copy_stage(sW2, sX2, sS2, sQW2, sQX2, min(2, KS - 1));
     wait_copies_upto<(AHEAD - 1) * CPS>();
     __syncthreads();
-    read_frags(sW0, sX0, 0, 0);
+    read_frags(sW0, sX0, sQW0, sQX0, 0, 0);
     if constexpr (TRI) {
       int s = 0;
       for (; s + 3 <= KS; s += 3) {
-        stage(sW0, sX0, sS0, sW1, sX1, s);
-        stage(sW1, sX1, sS1, sW2, sX2, s + 1);
-        stage(sW2, sX2, sS2, sW0, sX0, s + 2);
+        stage(sW0, sX0, sS0, sQW0, sQX0, sW1, sX1, sQW1, sQX1, s);
+        stage(sW1, sX1, sS1, sQW1, sQX1, sW2, sX2, sQW2, sQX2, s + 1);
+        stage(sW2, sX2, sS2, sQW2, sQX2, sW0, sX0, sQW0, sQX0, s + 2);
       }
-      if (s < KS) stage(sW0, sX0, sS0, sW1, sX1, s);
-      if (s + 1 < KS) stage(sW1, sX1, sS1, sW2, sX2, s + 1);
+      if (s < KS) stage(sW0, sX0, sS0, sQW0, sQX0, sW1, sX1, sQW1, sQX1, s);
+      if (s + 1 < KS) stage(sW1, sX1, sS1, sQW1, sQX1, sW2, sX2, sQW2, sQX2, s + 1);
     } else {
       for (int s = 0; s < KS; s += 2) {
-        stage(sW0, sX0, sS0, sW1, sX1, s);
-        stage(sW1, sX1, sS1, sW0, sX0, s + 1);
+        stage(sW0, sX0, sS0, sQW0, sQX0, sW1, sX1, sQW1, sQX1, s);
+        stage(sW1, sX1, sS1, sQW1, sQX1, sW0, sX0, sQW0, sQX0, s + 1);
       }
     }
   }
@@ -1025,29 +1107,62 @@ int qmoe_f8_launch(GemmParams p, bool blk, void* workspace, int64_t ws_bytes, hi
   return hipGetLastError() == hipSuccess ? QMOE_OK : QMOE_ERR_LAUNCH;
 }
 
-// ---- MX (QK_W4A4_MX): the persistent 256 x 256 kernel in mode 2 ----
-// Whether the kernel takes the problem: dense, no fused activation or row
-// maps, K % 512 == 0 and K >= 1024 (128-byte stages of packed codes, an even
-// count of at least 4), 16-byte aligned code rows and operands, 4-byte
-// aligned scale rows, N % 8 == 0 with 16-byte aligned output rows, weights
-// and outputs within the kernel's 32-bit offsets.
-bool qmoe_mx_plan(const GemmParams& p) {
-  if (p.M <= 0 || p.N <= 0 || (p.K % 512) != 0 || p.K < 1024) return false;
-  if (p.group_offs || p.act != QA_NONE || p.a_rows || p.y_rows || p.row_weight || !p.a_scale || !p.w_scale)
-    return false;
-  if ((p.lda % 16) != 0 || (p.ldw % 16) != 0 || (p.lds_a % 4) != 0 || (p.ldws % 4) != 0) return false;
+// ---- MX (QK_W4A4_MX) ----
+// Dense problems: the persistent 256 x 256 kernel in mode 2 (no fused
+// activation, bias only). Grouped problems (MoE): the one-tile kernel in MX
+// mode with 256- or 128-token tiles (the average rows per routed group above
+// or below 192), fused activation, bias, routing weight and row maps, no K
+// split. Both: K % 512 == 0 and K >= 1024 (128-byte stages of packed codes,
+// an even count of at least 4), 16-byte aligned code rows and operands,
+// 4-byte aligned scale rows, weights within the kernels' 32-bit offsets.
+// Returns the token-tile height, 0 when no MX kernel takes the problem.
+int qmoe_mx_plan(const GemmParams& p) {
+  if (p.M <= 0 || p.N <= 0 || (p.K % 512) != 0 || p.K < 1024 || !p.a_scale || !p.w_scale) return 0;
+  if (p.act != QA_NONE && (p.N % 2) != 0) return 0;
+  if ((p.lda % 16) != 0 || (p.ldw % 16) != 0 || (p.lds_a % 4) != 0 || (p.ldws % 4) != 0) return 0;
   if ((reinterpret_cast<uintptr_t>(p.a) & 15) || (reinterpret_cast<uintptr_t>(p.w) & 15) ||
-      (reinterpret_cast<uintptr_t>(p.a_scale) & 3) || (reinterpret_cast<uintptr_t>(p.w_scale) & 3))
-    return false;
-  if ((p.N % 8) != 0 || (p.ldy % 8) != 0 || (reinterpret_cast<uintptr_t>(p.y) & 15) != 0) return false;
-  if ((int64_t)p.ldw * p.N >= ((int64_t)1 << 32) || (int64_t)p.ldws * p.N >= ((int64_t)1 << 32)) return false;
-  return (int64_t)p.M * p.ldy * 2 < 0x7fffffffLL;
+      (reinterpret_cast<uintptr_t>(p.a_scale) & 3) || (reinterpret_cast<uintptr_t>(p.w_scale) & 3) ||
+      (p.w_gstride % 16) != 0 || (p.ws_gstride % 4) != 0)
+    return 0;
+  if ((int64_t)p.ldw * p.N >= ((int64_t)1 << 32) || (int64_t)p.ldws * p.N >= ((int64_t)1 << 32)) return 0;
+  if (p.group_offs) {
+    const int avg = std::max(1, p.M / std::max(1, std::min(p.slots, p.M)));
+    const int bm = avg > 192 ? 256 : 128;
+    return cdiv(p.M, bm) + std::min(p.slots, p.M) > 65535 ? 0 : bm;
+  }
+  if (p.act != QA_NONE || p.a_rows || p.y_rows || p.row_weight) return 0;
+  if ((p.N % 8) != 0 || (p.ldy % 8) != 0 || (reinterpret_cast<uintptr_t>(p.y) & 15) != 0) return 0;
+  return (int64_t)p.M * p.ldy * 2 < 0x7fffffffLL ? 256 : 0;
 }
 
-// Launch: as few tile rounds as the CUs allow, spread evenly over a
-// multiple of the 8 XCDs (also for fewer tiles than CUs: one tile each).
-int qmoe_mx_launch(const GemmParams& p, hipStream_t st) {
-  if (!qmoe_mx_plan(p)) return QMOE_ERR_ARG;
+namespace {
+
+template <int BM, bool ACT>
+void mx_launch_grouped(const GemmParams& p, hipStream_t st) {
+  const int nout = ACT ? p.N / 2 : p.N;
+  const int n_tiles = cdiv(nout, ACT ? 128 : 256);
+  const int m_tiles = cdiv(p.M, BM) + std::min(p.slots, p.M);
+  hipLaunchKernelGGL((f8_gemm_kernel<false, BM, 256, ACT, 128, false, false, true>), dim3(n_tiles, m_tiles, 1),
+                     dim3(kThreads), 0, st, p, m_tiles, n_tiles);
+}
+
+}  // namespace
+
+// Dense: as few tile rounds as the CUs allow, spread evenly over a multiple
+// of the 8 XCDs (also for fewer tiles than CUs: one tile each). Grouped: one
+// workgroup per (weight tile, token tile of a group), as the FP8 tiles.
+int qmoe_mx_launch(GemmParams p, hipStream_t st) {
+  const int bm = qmoe_mx_plan(p);
+  if (!bm) return QMOE_ERR_ARG;
+  p.ksplit = 1;
+  if (p.group_offs) {
+    p.active = nullptr;  // the tiles enumerate every group
+    p.num_active = nullptr;
+    const bool act = p.act != QA_NONE;
+    if (bm == 256) act ? mx_launch_grouped<256, true>(p, st) : mx_launch_grouped<256, false>(p, st);
+    else act ? mx_launch_grouped<128, true>(p, st) : mx_launch_grouped<128, false>(p, st);
+    return hipGetLastError() == hipSuccess ? QMOE_OK : QMOE_ERR_LAUNCH;
+  }
   int dev = 0, cus = 0;
   if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)

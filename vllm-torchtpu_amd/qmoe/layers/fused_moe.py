@@ -60,7 +60,17 @@ from qmoe.layers import ref_layout
 
 
 MOE_FORMATS = ("mxfp4", "nvfp4", "int4", "bf16", "fp8", "int8", "fp8_w8a16", "fp8_block", "fp8_block_rows",
-               "fp8_rowquant", "int8_rowquant")
+               "fp8_rowquant", "int8_rowquant", "mxfp4_mx")
+
+# "mxfp4_mx" (opt-in, no reference counterpart): MXFP4 experts with MX
+# activations -- the tokens and the intermediate quantized per 32 columns to
+# e2m1 + e8m0 (`ops.mx_quant`), both GEMMs on the scaled FP4 MFMA. The
+# weights are zero-padded along K at load to the MX kernel's multiple of 512
+# (`linear_common.pad_mxfp4_for_mx`): w13 [E, 2I, Hp/2] + [E, 2I, Hp/32], w2
+# [E, H, Ip/2] + [E, H, Ip/32]. Below MX_MOE_MIN_ROWS rows per routed expert
+# (decode steps, small batches) the same numbers run on the W4A16 kernels: the
+# MX activations dequantized to bf16 (exact), the unpadded weight views.
+MX_MOE_MIN_ROWS = 64
 
 
 def infer_weight_format(w1: torch.Tensor, w1_scale) -> str:
@@ -209,7 +219,24 @@ def _moe_body(x, w1, w2, w1_scale, w2_scale, w1_bias, w2_bias, tw, topk_ids, top
     b2 = w2_bias.float().reshape(E, -1).contiguous() if w2_bias is not None else None
     u8 = lambda t: t.view(torch.uint8)  # noqa: E731
 
-    if fmt in ("mxfp4", "nvfp4", "int4"):
+    if fmt == "mxfp4_mx":
+        Hp, Ip = w1.shape[-1] * 2, w2.shape[-1] * 2
+        I = w1.shape[1] // 2 if activation else w1.shape[1]
+        if M >= MX_MOE_MIN_ROWS * min(E, M):
+            xq, xs = ops.mx_quant(x, k_pad=Hp)
+            inter = ops.gemm(_capi.W4A4_MX, xq, u8(w1), a_scale=xs, w_scale=u8(w1_scale), bias=b1,
+                             a_rows=meta["token_sorted"], activation=activation, **common)
+            a2, a2_scale = ops.mx_quant(inter, k_pad=Ip)
+            kind, wf, bn = _capi.W4A4_MX, 0, 1
+            w2k, w2s = u8(w2), u8(w2_scale)
+        else:
+            xd = ops.mx_quant(x, codes=False, dequantized=True)
+            inter = ops.gemm(_capi.W4A16_MX, xd, u8(w1)[..., : H // 2], w_scale=u8(w1_scale)[..., : H // 32],
+                             bias=b1, a_rows=meta["token_sorted"], activation=activation, **common)
+            a2 = ops.mx_quant(inter, codes=False, dequantized=True)
+            a2_scale, kind, wf, bn = None, _capi.W4A16_MX, 0, 1
+            w2k, w2s = u8(w2)[..., : I // 2], u8(w2_scale)[..., : I // 32]
+    elif fmt in ("mxfp4", "nvfp4", "int4"):
         kind = {"mxfp4": _capi.W4A16_MX, "nvfp4": _capi.W4A16_NV, "int4": _capi.W4A16_I4}[fmt]
         sc = u8 if fmt == "mxfp4" else (lambda t: t)  # noqa: E731
         inter = ops.gemm(kind, x, u8(w1), w_scale=sc(w1_scale), bias=b1,

@@ -97,13 +97,20 @@ class Mxfp4LinearMethod:
 
 
 class Mxfp4MoEMethod:
-    """MXFP4 fused MoE (`mxfp4.py:207-364`), experts resident as MXFP4."""
+    """MXFP4 fused MoE (`mxfp4.py:207-364`), experts resident as MXFP4.
+
+    ``mx_activations`` (default: the QMOE_MXFP4_MX_ACTIVATIONS flag) opts
+    into MX-quantized activations for both expert GEMMs (no counterpart in
+    the reference; weight format "mxfp4_mx" of `fused_moe`): the experts are
+    zero-padded along K at load to the MX kernel's multiple of 512.
+    """
 
     is_monolithic = True
     supports_internal_mk = False
 
-    def __init__(self, moe_config=None):
+    def __init__(self, moe_config=None, mx_activations=None):
         self.moe = moe_config
+        self.mx_activations = envs.QMOE_MXFP4_MX_ACTIVATIONS if mx_activations is None else bool(mx_activations)
 
     def maybe_roundup_sizes(self, hidden_size, intermediate_size_per_partition, *args, **kwargs):
         return hidden_size, intermediate_size_per_partition
@@ -137,10 +144,15 @@ class Mxfp4MoEMethod:
             s13 = torch.cat([s13[:, 0::2], s13[:, 1::2]], dim=1)
             if b13 is not None:
                 b13 = torch.cat([b13[:, 0::2], b13[:, 1::2]], dim=1)
+        w2 = layer.w2_weight.data.to(dev).view(torch.uint8)
+        s2 = layer.w2_weight_scale.data.to(dev).view(torch.uint8)
+        if self.mx_activations:
+            w13, s13 = _pad_experts_for_mx(w13, s13)
+            w2, s2 = _pad_experts_for_mx(w2, s2)
         layer.w13_weight = _param(w13.contiguous())
         layer.w13_weight_scale = _param(s13.contiguous())
-        layer.w2_weight = _param(layer.w2_weight.data.to(dev).view(torch.uint8).contiguous())
-        layer.w2_weight_scale = _param(layer.w2_weight_scale.data.to(dev).view(torch.uint8).contiguous())
+        layer.w2_weight = _param(w2.contiguous())
+        layer.w2_weight_scale = _param(s2.contiguous())
         layer.w13_bias = _param(b13.to(torch.float32).contiguous()) if b13 is not None else None
         if getattr(layer, "w2_bias", None) is not None:
             layer.w2_bias = _param(layer.w2_bias.data.to(dev, torch.float32).contiguous())
@@ -151,4 +163,18 @@ class Mxfp4MoEMethod:
         """`mxfp4.py:322-364`: route, then the fused MoE on MXFP4 experts."""
         return moe_forward(layer, x, router_logits, layer.w13_weight, layer.w2_weight, layer.w13_weight_scale,
                            layer.w2_weight_scale, getattr(layer, "w13_bias", None), getattr(layer, "w2_bias", None),
-                           "mxfp4", skip_padded_tokens=envs.TPU_MOE_SKIP_PADDED_TOKENS, input_ids=input_ids)
+                           "mxfp4_mx" if self.mx_activations else "mxfp4",
+                           skip_padded_tokens=envs.TPU_MOE_SKIP_PADDED_TOKENS, input_ids=input_ids)
+
+
+def _pad_experts_for_mx(w, s):
+    """[E, N, K/2] codes + [E, N, K/32] e8m0 -> zero-padded along K to the MX
+    kernel's multiple of 512 (one expert at a time)."""
+    E, N, kb = w.shape
+    wp, sp = pad_mxfp4_for_mx(w[0], s[0])
+    out_w = torch.empty((E, N, wp.shape[1]), dtype=torch.uint8, device=w.device)
+    out_s = torch.empty((E, N, sp.shape[1]), dtype=torch.uint8, device=w.device)
+    out_w[0], out_s[0] = wp, sp
+    for e in range(1, E):
+        out_w[e], out_s[e] = pad_mxfp4_for_mx(w[e], s[e])
+    return out_w, out_s
