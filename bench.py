@@ -56,7 +56,7 @@ def parse():
                          "this build's FP8 GEMM beside hipBLASLt's (torch._scaled_mm) on both cfg 1 "
                          "shapes at M=4096, the plain-read floor (time vs size), the large-M MXFP4 "
                          "path (cfg 0 at M=8192, cfg 3 at T=8192), or the opt-in MX activation path "
-                         "(cfg 0 at M=8192)")
+                         "(cfg 0 at M=8192, cfg 3 at T=8192)")
     return ap.parse_args()
 
 
@@ -466,7 +466,40 @@ def sweep_moe(only):
                 pt["fp4_peak_frac"] = round(T * k * 6.0 * H * I / (us * 1e-6) / PEAK["fp4"], 4)
             out.append(pt)
             log(out[-1])
-        del w13, s13, w2, s2
+        # the opt-in MX activations (weight format mxfp4_mx: experts padded
+        # along K 2880 -> 3072, tokens and intermediate MX-quantized) at the
+        # large-T points; flops count the layer's K
+        from qmoe.layers.quantization.mxfp4 import _pad_experts_for_mx
+
+        w13p, s13p = _pad_experts_for_mx(w13, s13)
+        w2p, s2p = _pad_experts_for_mx(w2, s2)
+        for T in (1024, 8192):
+            x = torch.randn((T, H), device="cuda", generator=gen).to(torch.bfloat16)
+            logits = torch.randn((T, E), device="cuda", generator=gen).to(torch.bfloat16)
+
+            def layer_mx():
+                return moe_forward(lcfg, x, logits, w13p, w2p, s13p, s2p, None, None, "mxfp4_mx")
+
+            us = graph_time_us(layer_mx, iters=20)[0]
+            tw, ids = ops.moe_route(logits, k, "softmax", True)
+            touched = int(torch.unique(ids).numel())
+            nbytes = touched * per_expert * 3072 // 2880 + 2 * T * H * 2 + 2 * T * E
+            par = {}
+            if PAR.on:
+                omoe, orouting = oracle_mod("moe"), oracle_mod("routing")
+                _, ids_ref = orouting.select_experts(PAR._np(logits), k, True, "softmax")
+                ew = omoe.ExpertWeights("mxfp4_mx", _DevRows(w13), _DevRows(s13), _DevRows(w2), _DevRows(s2),
+                                        keep=False)
+                par = PAR.moe(layer_mx(), T, lambda tk: omoe.fused_moe_tokens(
+                    PAR._np(x[tk]), ew, PAR._np(tw[tk]), ids_ref[tk], "swigluoai", E),
+                    np.array_equal(ids.cpu().numpy(), ids_ref))
+            flops = T * k * 6.0 * H * I
+            pt = dict(cfg=3, kind="moe_mxfp4_gptoss_mx_act", T=T, experts_touched=touched,
+                      **roof(flops, nbytes, us, "fp4"), fp4_peak_frac=round(flops / (us * 1e-6) / PEAK["fp4"], 4),
+                      **par)
+            out.append(pt)
+            log(out[-1])
+        del w13, s13, w2, s2, w13p, s13p, w2p, s2p
         torch.cuda.empty_cache()
     if not only or "4" in only:
         E, k, H, I = 256, 8, 7168, 2048
@@ -1000,8 +1033,10 @@ def profile_w4(args):
 def profile_mx(args):
     """rocprofv3 target: the opt-in MX activation path at config 0's shape,
     M=8192 (K 2880 padded to 3072, N 5760): 10 activation quantizations
-    and 10 MX GEMMs after 2 warm-up calls each; then a plain 256 MiB copy
-    (10 launches) for the FETCH_SIZE / WRITE_SIZE calibration."""
+    and 10 MX GEMMs after 2 warm-up calls each; 10 config 3 GPT-OSS MoE
+    layers at T=8192 with MX activations (experts padded to K 3072); then a
+    plain 256 MiB copy (10 launches) for the FETCH_SIZE / WRITE_SIZE
+    calibration."""
     import torch
 
     from qmoe import _capi, ops
@@ -1019,6 +1054,19 @@ def profile_mx(args):
         ops.gemm(_capi.W4A4_MX, q, wp, a_scale=s, w_scale=wsp)
     torch.cuda.synchronize()
     log("profile target: cfg0 MX W4A4 M=8192 quant x12, gemm x12")
+    from qmoe.layers.fused_moe import moe_forward
+    from qmoe.layers.quantization.mxfp4 import _pad_experts_for_mx
+
+    E, k, H, I, T = 128, 4, 2880, 2880, 8192
+    w13, s13 = _pad_experts_for_mx(*mxfp4_weights((E, 2 * I, H), gen))
+    w2, s2 = _pad_experts_for_mx(*mxfp4_weights((E, H, I), gen))
+    x = torch.randn((T, H), device="cuda", generator=gen).to(torch.bfloat16)
+    logits = torch.randn((T, E), device="cuda", generator=gen).to(torch.bfloat16)
+    lcfg = moe_layer_cfg(k, "softmax", "swigluoai")
+    for _ in range(10):
+        moe_forward(lcfg, x, logits, w13, w2, s13, s2, None, None, "mxfp4_mx")
+    torch.cuda.synchronize()
+    log("profile target: cfg3 MoE T=8192 with MX activations x10")
     src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
     dst = torch.empty_like(src)
     for _ in range(10):

@@ -137,8 +137,12 @@ def test_rowmax_select_nan_and_sentinel_rows(dev):
     np.testing.assert_array_equal(v.cpu().numpy(), ref_v)
 
 
+# from 8192 routes the chunked three-launch form runs: (2048, 4, 512) is
+# exactly 8 chunks at the widest bucket row, (3001, 4, 128) has a ragged last
+# chunk of 1764 routes, (2047, 4, 16) stays on the one-workgroup kernel
 @pytest.mark.parametrize("T,k,E", [(3, 2, 2), (1, 8, 256), (64, 8, 256), (4096, 8, 256),
-                                   (8192, 4, 128), (100, 10, 512)])
+                                   (8192, 4, 128), (100, 10, 512), (2048, 4, 512), (3001, 4, 128),
+                                   (2047, 4, 16)])
 @pytest.mark.parametrize("skip_padded", [False, True])
 def test_dispatch_bit_exact(dev, T, k, E, skip_padded):
     from qmoe import ops
