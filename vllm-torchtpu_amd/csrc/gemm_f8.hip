@@ -1127,7 +1127,9 @@ int qmoe_mx_plan(const GemmParams& p) {
   if ((int64_t)p.ldw * p.N >= ((int64_t)1 << 32) || (int64_t)p.ldws * p.N >= ((int64_t)1 << 32)) return 0;
   if (p.group_offs) {
     const int avg = std::max(1, p.M / std::max(1, std::min(p.slots, p.M)));
-    const int bm = avg > 192 ? 256 : 128;
+    int bm = avg > 192 ? 256 : 128;
+    const char* env = getenv("QMOE_MX_BM");  // tuning knob: 128 or 256
+    if (env && (atoi(env) == 128 || atoi(env) == 256)) bm = atoi(env);
     return cdiv(p.M, bm) + std::min(p.slots, p.M) > 65535 ? 0 : bm;
   }
   if (p.act != QA_NONE || p.a_rows || p.y_rows || p.row_weight) return 0;
