@@ -200,8 +200,10 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
     }
     woff[j] = (uint32_t)n * (uint32_t)p.ldw + chunk_of(r);
   }
-  // MX scale copies: 32 rows x 8 bytes per instruction (lane -> row lane / 2,
-  // dword lane & 1), QW weight and QX activation instructions per wavefront
+  // MX scale copies: 32 rows x 8 bytes per instruction, lane -> row lane & 31,
+  // dword lane >> 5, so that the instruction's 256 LDS bytes are [dword][row]
+  // and the reads (32 consecutive rows, one dword) hit 32 consecutive banks;
+  // QW weight and QX activation instructions per wavefront
   constexpr int QW = MX ? BN / 128 : 0, QX = MX ? BM / 128 : 0;
   const uint8_t* wqbase = static_cast<const uint8_t*>(p.w_scale) + (int64_t)g * p.ws_gstride;
   const uint8_t* xqbase = reinterpret_cast<const uint8_t*>(p.a_scale);
@@ -209,7 +211,7 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
   if constexpr (MX) {
 #pragma unroll
     for (int j = 0; j < QW; ++j) {
-      const int r = (wave * QW + j) * 32 + (lane >> 1);
+      const int r = (wave * QW + j) * 32 + (lane & 31);
       int n;
       if (ACT) {
         const int cidx = min(n0 + (r % (BN / 2)), nlim - 1);
@@ -217,11 +219,11 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
       } else {
         n = min(n0 + r, nlim - 1);
       }
-      qwoff[j] = (uint32_t)n * (uint32_t)p.ldws + (uint32_t)(lane & 1) * 4u;
+      qwoff[j] = (uint32_t)n * (uint32_t)p.ldws + (uint32_t)(lane >> 5) * 4u;
     }
 #pragma unroll
     for (int j = 0; j < QX; ++j) {
-      const int r = (wave * QX + j) * 32 + (lane >> 1);
+      const int r = (wave * QX + j) * 32 + (lane & 31);
       const int R = row0 + min(r, rows - 1);
       qxrow[j] = (uint32_t)(p.a_rows ? p.a_rows[R] : R);
     }
@@ -271,7 +273,7 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
       for (int j = 0; j < QX; ++j) {
         uint32_t r = qxrow[j];
         asm volatile("" : "+v"(r));
-        const uint8_t* src = xqbase + (uint64_t)r * (uint64_t)p.lds_a + (kq + (uint32_t)(lane & 1) * 4u);
+        const uint8_t* src = xqbase + (uint64_t)r * (uint64_t)p.lds_a + (kq + (uint32_t)(lane >> 5) * 4u);
         __builtin_amdgcn_global_load_lds(src, QMOE_LDS(dQX + (wave * QX + j) * 256), 4, 0, 0);
       }
     }
@@ -315,12 +317,14 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
   auto read_frags = [&](const uint8_t* sW, const uint8_t* sX, const uint8_t* sQW, const uint8_t* sQX, int ks,
                         int t) {
     if constexpr (MX) {
+      // block of 32 rows at 8 (first row) bytes, dword plane ks, row rl
 #pragma unroll
       for (int i = 0; i < NI; ++i)
-        wsc[t][i] = *reinterpret_cast<const uint32_t*>(sQW + (wrow(i) + rl) * 8 + ks * 4) >> (8 * kh);
+        wsc[t][i] = *reinterpret_cast<const uint32_t*>(sQW + wrow(i) * 8 + ks * 128 + rl * 4) >> (8 * kh);
 #pragma unroll
       for (int j = 0; j < MJ; ++j)
-        xsc[t][j] = *reinterpret_cast<const uint32_t*>(sQX + (wm * TM + j * 32 + rl) * 8 + ks * 4) >> (8 * kh);
+        xsc[t][j] =
+            *reinterpret_cast<const uint32_t*>(sQX + (wm * TM + j * 32) * 8 + ks * 128 + rl * 4) >> (8 * kh);
     }
     const int h0 = KB == 64 ? po[0][0] : po[ks][0], h1 = KB == 64 ? po[0][1] : po[ks][1];
 #pragma unroll
@@ -631,12 +635,14 @@ __global__ __launch_bounds__(kThreads) void f8_persistent_kernel(const GemmParam
       __builtin_amdgcn_global_load_lds(src, QMOE_LDS(dX + (wave + 4 * j) * 1024), 16, 0, 0);
     }
     if constexpr (MX) {
-      // scale rows (wave * QI + j) * 32 + lane / 2, dword lane & 1 of the
-      // stage's 8 bytes: each copy fills 256 contiguous LDS bytes
-      const uint32_t kq = (uint32_t)ks * 8u + (uint32_t)(lane & 1) * 4u;
+      // copy q moves scale rows 32q .. 32q + 31 of the stage (lane -> row
+      // lane & 31, dword lane >> 5 of the row's 8 bytes) into 256 LDS bytes
+      // laid out [dword][row]: the reads (32 consecutive rows, one dword)
+      // then hit 32 consecutive banks
+      const uint32_t kq = (uint32_t)ks * 8u + (uint32_t)(lane >> 5) * 4u;
 #pragma unroll
       for (int j = 0; j < QI; ++j) {
-        const int rr = (wave * QI + j) * 32 + (lane >> 1);
+        const int rr = (wave * QI + j) * 32 + (lane & 31);
         const int n = min(sc.n0 + rr, nlim - 1);
         uint32_t o = (uint32_t)n * (uint32_t)p.ldws + kq;
         asm volatile("" : "+v"(o));
@@ -678,12 +684,14 @@ __global__ __launch_bounds__(kThreads) void f8_persistent_kernel(const GemmParam
       xf[t][j] = lds_frag(b + po[ks][0], b + po[ks][1]);
     }
     if constexpr (MX) {
+      // block of 32 rows at 8 (first row) bytes, dword plane ks, row rl
 #pragma unroll
       for (int i = 0; i < NI; ++i)
-        wsc[t][i] = *reinterpret_cast<const uint32_t*>(sQW + (wrow(i) + rl) * 8 + ks * 4) >> (8 * kh);
+        wsc[t][i] = *reinterpret_cast<const uint32_t*>(sQW + wrow(i) * 8 + ks * 128 + rl * 4) >> (8 * kh);
 #pragma unroll
       for (int j = 0; j < MJ; ++j)
-        xsc[t][j] = *reinterpret_cast<const uint32_t*>(sQX + (wm * TM + j * 32 + rl) * 8 + ks * 4) >> (8 * kh);
+        xsc[t][j] =
+            *reinterpret_cast<const uint32_t*>(sQX + (wm * TM + j * 32) * 8 + ks * 128 + rl * 4) >> (8 * kh);
     }
   };
   using Acc = typename std::conditional<INT, i32x16, f32x16>::type;
