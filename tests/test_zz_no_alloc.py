@@ -86,3 +86,27 @@ def test_gemm_static_refuses_oversized_partials(dev):
     ws = torch.ones(N, dtype=torch.float32, device=dev)
     st, _, _ = _static_gemm(lib, a, s, w, ws)
     assert st == 4
+
+
+def test_gemm_static_mx_activations(dev):
+    """The opt-in MX kind (QMOE_W4A4_MX, no K split, no scratch) through the
+    allocation-free entry: bit-identical to `qmoe_gemm` on two calls in a
+    row, the second smaller."""
+    from qmoe import _capi, ops
+
+    lib = _lib()
+    for i, (M, N, K) in enumerate(((512, 1024, 2048), (200, 520, 1024))):
+        print(f"gemm_static mx M={M} N={N} K={K}", flush=True)
+        rng = np.random.default_rng(M + N)
+        x = torch.from_numpy(codecs.bf16_round(rng.standard_normal((M, K)).astype(np.float32))).to(dev)
+        q, s = ops.mx_quant(x.to(torch.bfloat16))
+        wq = torch.from_numpy(rng.integers(0, 256, (N, K // 2), dtype=np.uint8)).to(dev)
+        ws = torch.from_numpy(rng.integers(118, 130, (N, K // 32), dtype=np.uint8)).to(dev)
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+        d, out = ops.gemm_desc(_capi.W4A4_MX, q, wq, a_scale=s, w_scale=ws, out=out)
+        st = lib.qmoe_gemm_static(ctypes.byref(d), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        assert st == 0, _capi.STATUS_TEXT.get(st, st)
+        assert ops.plan_of_desc(d)[4] == "tiled_mx_persistent"
+        ref = ops.gemm(_capi.W4A4_MX, q, wq, a_scale=s, w_scale=ws)
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"call {i}: static output differs"
