@@ -69,6 +69,27 @@ __device__ __forceinline__ i32x8 lds_frag(const uint8_t* p0, const uint8_t* p1) 
 }
 
 __device__ __forceinline__ i32x4 lo4(const i32x8& v) { return i32x4{v[0], v[1], v[2], v[3]}; }
+
+// `interleave` (gemm_tile.h) with NV vector-ALU instructions after every MFMA
+// but the first, and NV after the last: the block-scaled tiles' scaling of
+// the previous block pair runs while the next MFMA executes
+template <int K, int NM, int NR, int NC, int NV>
+__device__ __forceinline__ void interleave_v() {
+  if constexpr (NV == 0) {
+    interleave<K, NM, NR, NC>();
+  } else if constexpr (K < NM) {
+    constexpr int H = NM / 2 > 0 ? NM / 2 : 1;
+    constexpr int r0 = K < H ? K * NR / H : NR, r1 = K < H ? (K + 1) * NR / H : NR;
+    constexpr int c0 = K < H ? 0 : (K - H) * NC / (NM - H), c1 = K < H ? 0 : (K - H + 1) * NC / (NM - H);
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+    if constexpr (K > 0) __builtin_amdgcn_sched_group_barrier(0x002, NV, 0);  // VALU
+    if constexpr (r1 > r0) __builtin_amdgcn_sched_group_barrier(0x100, r1 - r0, 0);  // DS read
+    if constexpr (c1 > c0) __builtin_amdgcn_sched_group_barrier(0x020, c1 - c0, 0);  // VMEM read
+    interleave_v<K + 1, NM, NR, NC, NV>();
+  } else {
+    __builtin_amdgcn_sched_group_barrier(0x002, NV, 0);  // VALU
+  }
+}
 __device__ __forceinline__ i32x4 hi4(const i32x8& v) { return i32x4{v[4], v[5], v[6], v[7]}; }
 // e2m1 MFMA operand: 4 registers (32 codes) in the low half of the 8-register
 // operand; the undefined upper half lets the compiler pass a 4-register tuple
@@ -397,13 +418,36 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
                                                               0);
       return;
     }
+    if constexpr (BLK) {
+      if (t == 1) {
+        // the stage's last k-step: block pair p's MFMA, then the scaling
+        // acc += tmp * (sx * sw) of pair p - 1, whose MFMA has completed by
+        // then, so the FMAs run on the vector ALU while the matrix core runs
+        // the next MFMA (each accumulator still sees the same operations in
+        // the same order)
+#pragma unroll
+        for (int q = 0; q <= NI * MJ; ++q) {
+          if (q < NI * MJ) {
+            const int i = q / MJ, j = q % MJ;
+            tmp[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[1][i], xf[1][j], tmp[i][j], 0, 0, 0,
+                                                                        127, 0, 127);
+          }
+          if (q > 0) {
+            const int i = (q - 1) / MJ, j = (q - 1) % MJ;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] += tmp[i][j][r] * scl[i][j];
+          }
+        }
+        return;
+      }
+    }
 #pragma unroll
     for (int i = 0; i < NI; ++i)
 #pragma unroll
       for (int j = 0; j < MJ; ++j) {
         if constexpr (BLK) {
-          const f32x16 c = t == 0 ? f32x16{} : tmp[i][j];
-          tmp[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[t][i], xf[t][j], c, 0, 0, 0, 127, 0, 127);
+          tmp[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[t][i], xf[t][j], f32x16{}, 0, 0, 0, 127,
+                                                                      0, 127);
         } else {
           acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[t][i], xf[t][j], acc[i][j], 0, 0, 0,
                                                                       127, 0, 127);
@@ -411,16 +455,6 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
       }
   };
 
-  auto apply_scales = [&]() {
-    if constexpr (BLK) {
-#pragma unroll
-      for (int i = 0; i < NI; ++i)
-#pragma unroll
-        for (int j = 0; j < MJ; ++j)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) acc[i][j][r] += tmp[i][j][r] * scl[i][j];
-    }
-  };
 
   constexpr int CPS = WI + XI + (BLK ? 1 : 0) + QW + QX;  // copy instructions per wavefront per stage
   constexpr int NM = NI * MJ * (INT || MX ? 2 : 1);       // MFMAs per k-step
@@ -494,8 +528,8 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
       read_frags(nW, nX, nQW, nQX, 0, 0);
       copy_stage(cW, cX, cS, cQW, cQX, min(s + AHEAD, KS - 1));
       mma(1);
-      apply_scales();
-      interleave<0, NM, NR, CPS>();
+      // BLK: each MFMA followed by the previous block pair's 16 scaling FMAs
+      interleave_v<0, NM, NR, CPS, BLK ? 16 : 0>();
     };
     copy_stage(sW0, sX0, sS0, sQW0, sQX0, 0);
     copy_stage(sW1, sX1, sS1, sQW1, sQX1, 1);
