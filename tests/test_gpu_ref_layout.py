@@ -158,13 +158,17 @@ def _moe_layer(k, act):
     return layer
 
 
-@pytest.mark.parametrize("T", [3, 150])
-def test_compressed_tensors_mxfp4_moe(dev, T):
+@pytest.mark.parametrize("T,mx", [(3, False), (150, False), (150, True), (2048, True)])
+def test_compressed_tensors_mxfp4_moe(dev, T, mx):
     """Compressed-tensors MXFP4 MoE (`compressed_tensors_moe_w4an_mxfp4.py`):
-    packed codes + e8m0 scales as loaded, silu, padded tokens skipped."""
+    packed codes + e8m0 scales as loaded, silu, padded tokens skipped. With
+    the opt-in MX activations (H 256 / I 192 padded to 1024): T = 150 runs
+    the bf16-activation kernels on the dequantized MX activations over the
+    padded weights' views, T = 2048 (512 rows per expert) the grouped MX
+    tiles; against the oracle's "mxfp4_mx" recipe."""
     from qmoe.layers import quantization as q
 
-    print(f"ct mxfp4 moe T={T}", flush=True)
+    print(f"ct mxfp4 moe T={T} mx={mx}", flush=True)
     rng = np.random.default_rng(41 + T)
     E, H, I, k = 8, 256, 192, 2
     layer = _moe_layer(k, "silu")
@@ -172,6 +176,7 @@ def test_compressed_tensors_mxfp4_moe(dev, T):
         "weights": {"num_bits": 4, "type": "float", "strategy": "group", "group_size": 32}}}})
     method = cfg.get_quant_method(layer, prefix="model.layers.0.mlp.experts")
     assert isinstance(method, q.CompressedTensorsW4ANMxfp4MoEMethod)
+    method.mx_activations = mx
     method.create_weights(layer, E, H, I, torch.bfloat16)
     c13 = rng.integers(0, 256, (E, 2 * I, H // 2), dtype=np.uint8)
     s13 = (127 + rng.integers(-8, 1, (E, 2 * I, H // 32))).astype(np.uint8)
@@ -186,8 +191,9 @@ def test_compressed_tensors_mxfp4_moe(dev, T):
     logits = codecs.bf16_round(rng.standard_normal((T, E)).astype(np.float32))
     got = method.apply_monolithic(layer, _t(x, dev, torch.bfloat16), _t(logits, dev, torch.bfloat16))
     tw, ids = routing.select_experts(logits, k, True, "softmax")
-    ref, _, _ = omoe.fused_moe(x, omoe.ExpertWeights("mxfp4", c13, s13, c2, s2), tw, ids, "silu")
-    assert_close_rows(got.float().cpu().numpy(), ref, "ct mxfp4 moe")
+    ref, _, _ = omoe.fused_moe(x, omoe.ExpertWeights("mxfp4_mx" if mx else "mxfp4", c13, s13, c2, s2), tw, ids,
+                               "silu")
+    assert_close_rows(got.float().cpu().numpy(), ref, f"ct mxfp4 moe mx={mx}")
 
 
 def test_compressed_tensors_fp8_channel_moe(dev):

@@ -225,14 +225,20 @@ class CompressedTensorsW4ANMxfp4MoEMethod:
     scales of an unloaded intermediate padding are zeroed first, as the
     reference does (`:138-171`: an untouched 0xff byte would make a padded
     zero weight NaN). Requantizing to W4A8 (``MOE_REQUANTIZE_BLOCK_SIZE``)
-    is not built and raises."""
+    is not built and raises.
+
+    ``mx_activations`` (default: the QMOE_MXFP4_MX_ACTIVATIONS flag) opts
+    into MX-quantized activations (the W4A4 the method's name promises; no
+    counterpart in the reference, which runs W4A16): experts zero-padded
+    along K at load, weight format "mxfp4_mx" of `fused_moe`."""
 
     is_monolithic = True
     supports_internal_mk = False
 
-    def __init__(self, moe_config=None):
+    def __init__(self, moe_config=None, mx_activations=None):
         self.moe = moe_config
         self.group_size = 32
+        self.mx_activations = envs.QMOE_MXFP4_MX_ACTIVATIONS if mx_activations is None else bool(mx_activations)
 
     def maybe_roundup_sizes(self, hidden_size, intermediate_size_per_partition, *args, **kwargs):
         return hidden_size, intermediate_size_per_partition
@@ -274,6 +280,11 @@ class CompressedTensorsW4ANMxfp4MoEMethod:
         s13 = layer.w13_weight_scale.data.to(dev).view(torch.uint8).contiguous()
         s2 = layer.w2_weight_scale.data.to(dev).view(torch.uint8).contiguous()
         self._neutralize_padded_scales(layer, s13, s2)
+        if self.mx_activations:
+            from qmoe.layers.quantization.mxfp4 import _pad_experts_for_mx
+
+            w13, s13 = _pad_experts_for_mx(w13, s13)
+            w2, s2 = _pad_experts_for_mx(w2, s2)
         for name in ("w13_weight_packed", "w2_weight_packed"):
             delattr(layer, name)
         layer.w13_weight, layer.w2_weight = _param(w13), _param(w2)
@@ -288,6 +299,6 @@ class CompressedTensorsW4ANMxfp4MoEMethod:
         fused MoE with padded tokens skipped (the reference passes
         ``skip_padded_tokens=True``)."""
         return moe_forward(layer, x, router_logits, layer.w13_weight, layer.w2_weight, layer.w13_weight_scale,
-                           layer.w2_weight_scale, None, None, "mxfp4", skip_padded_tokens=True,
-                           input_ids=input_ids)
+                           layer.w2_weight_scale, None, None, "mxfp4_mx" if self.mx_activations else "mxfp4",
+                           skip_padded_tokens=True, input_ids=input_ids)
 
