@@ -58,9 +58,10 @@ enum {
                         (row, 32 k) in a_scale [M, lds_a >= K/32] (qmoe_mx_quant); W as
                         QMOE_W4A16_MX. Both scales go to the MFMA. Opt-in MX activations
                         (no counterpart in the reference, whose W4A4 method runs W4A16,
-                        `compressed_tensors_moe_w4an_mxfp4.py:49-55`). Dense only, no
-                        fused activation or row maps; K % 512 == 0 and K >= 1024 (pad
-                        with zero codes); optional bias */
+                        `compressed_tensors_moe_w4an_mxfp4.py:49-55`). Dense: bias only;
+                        grouped: fused activation, bias, row maps and routing weight as
+                        the other kinds (a_rows also gathers the scale rows); no K split;
+                        K % 512 == 0 and K >= 1024 (pad with zero codes) */
 };
 
 /* Fused gate/up activations (qmoe_gemm_desc.act) */

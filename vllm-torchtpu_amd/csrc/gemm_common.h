@@ -25,7 +25,8 @@ enum QmoeKind {
   QK_W8A16_BLK = 8,  // A bf16; W e4m3 + f32 scale per (n / bn, 128 k), dequantized in bf16:
                      // each weight is bf16(code * bf16(scale))
   QK_W4A4_MX = 9,    // A e2m1 (packed as W) + e8m0 byte per (row, 32 k) in a_scale; W as
-                     // QK_W4A16_MX; both scales applied by the MFMA (dense tiles only)
+                     // QK_W4A16_MX; both scales applied by the MFMA (the 1-byte tile kernels' MX
+                     // modes, dense and grouped)
 };
 // The host maps the descriptor kind QMOE_W8A8_GMM (7) onto QK_W8A8_BLK with
 // a_kshift = 2 (activation scales per 512 columns) and w_kshift = 31 (one
