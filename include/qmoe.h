@@ -86,8 +86,8 @@ typedef struct qmoe_gemm_desc {
   int32_t kind;           /* QMOE_W8A8_PC ... */
   int32_t wfmt;           /* QMOE_W8A8_PC only: 0 e4m3, 1 int8 */
   const void* a;          /* activation codes or bf16 */
-  int64_t lda;            /* elements */
-  const float* a_scale;   /* W8A8: [rows] or [rows, lds_a] */
+  int64_t lda;            /* elements (W4A4_MX: bytes of packed codes) */
+  const float* a_scale;   /* W8A8: [rows] or [rows, lds_a]; W4A4_MX: e8m0 bytes [rows, lds_a] */
   int64_t lds_a;
   const int32_t* a_rows;  /* optional gather map [M] */
   const void* w;
