@@ -6,7 +6,7 @@ Test infrastructure only.
 import numpy as np
 
 from oracle.codecs import bf16_round, dequant_int4, dequant_mxfp4, dequant_nvfp4, e4m3_decode
-from oracle.linear import _mm, w8a8_gmm
+from oracle.linear import _mm, w8a8_gmm, w8a8_gmm_bf16acc
 from oracle.quant import quantize_act, quantize_mx_fp4
 
 
@@ -91,6 +91,9 @@ class ExpertWeights:
       "fp8_block": w13 e4m3 [E, 2I, H] + tile scale_inv [E, 2I/128, H/128]; w2 likewise
       "fp8" / "int8": w13 e4m3 / int8 [E, 2I, H] + per-channel scale [E, 2I] (or per (row, B
           columns) [E, 2I, H/B]); w2 [E, H, I] + [E, H]
+      "fp8_bf16acc": as "fp8" (per-channel), each expert linear with the grouped matmul's own
+          bf16 accumulator (``linear.w8a8_gmm_bf16acc``, `gmm_v2.py:508-560` as written) and
+          silu applied in bf16 (``silu_mul_bf16``)
       "fp8_w8a16": w13 e4m3 [E, 2I, H] + per-(row, 128) scale [E, 2I, H/128]; w2 likewise
       "fp8_rowquant" / "int8_rowquant": as "fp8" / "int8" with per-channel scales
       "bf16": w13 [E, 2I, H] f32 (bf16 values); w2 [E, H, I]
@@ -126,7 +129,7 @@ class ExpertWeights:
                 d = dequant_nvfp4(w, s)
             elif self.fmt == "int4":
                 d = dequant_int4(w, s)
-            elif self.fmt in ("fp8_block", "fp8", "fp8_w8a16", "fp8_rowquant"):
+            elif self.fmt in ("fp8_block", "fp8", "fp8_bf16acc", "fp8_w8a16", "fp8_rowquant"):
                 d = e4m3_decode(w)
             elif self.fmt in ("int8", "int8_rowquant"):
                 d = np.asarray(w, np.int8).astype(np.float32)
@@ -141,6 +144,9 @@ class ExpertWeights:
         if self.fmt in ("fp8", "int8"):
             w = self.w13[e] if which == 13 else self.w2[e]
             out, _, _ = w8a8_gmm(x, w, s, self.fmt, round_out=False)
+        elif self.fmt == "fp8_bf16acc":
+            w = self.w13[e] if which == 13 else self.w2[e]
+            out = w8a8_gmm_bf16acc(x, w, s, "fp8")
         elif self.fmt == "fp8_w8a16":
             wv = self.dense(which, e)
             sb = np.repeat(bf16_round(np.asarray(s, np.float32)), 128, axis=1)[:, :wv.shape[1]]
@@ -208,7 +214,10 @@ def fused_moe(hidden, weights: ExpertWeights, topk_weights, topk_ids, activation
         rows = x[meta["token_sorted"][lo:hi]]
         gu = weights.linear(13, e, rows)
         i = gu.shape[1] // 2
-        a = bf16_round(act_fn(gu[:, :i], gu[:, i:], activation))
+        if weights.fmt == "fp8_bf16acc" and activation == "silu":
+            a = silu_mul_bf16(gu[:, :i], gu[:, i:])
+        else:
+            a = bf16_round(act_fn(gu[:, :i], gu[:, i:], activation))
         if inter_rows is None:
             inter_rows = np.zeros((t * k, i), np.float32)
         inter_rows[lo:hi] = a
@@ -254,3 +263,64 @@ def fused_moe_tokens(hidden_rows, weights: ExpertWeights, topk_weights, topk_ids
             acc += w[t, j] * weights.linear(2, e, a)[0]
         out[t] = acc
     return bf16_round(out)
+
+
+def silu_mul_bf16(g, u):
+    """``jax.nn.silu(g) * u`` on bf16 arrays, as the grouped matmul applies it
+    to its bf16 accumulator (`kernels/megablox/gmm_v2.py:575`) and the
+    dense-expert kernel to its own (`moe_dense_expert.py:152`): ``sigmoid``,
+    ``g * sigmoid`` and ``* u`` each rounded to bf16."""
+    g = bf16_round(np.asarray(g, np.float32))
+    return bf16_round(bf16_round(g * bf16_round(_sigmoid(g))) * bf16_round(np.asarray(u, np.float32)))
+
+
+def dense_expert_moe(hidden, w13, s13, w2, s2, topk_weights, topk_ids):
+    """The dense-expert decode branch, `kernels/experimental/moe_dense_expert.py:
+    112-190, 249-270` (taken by `layers/core/fused_moe_gmm.py:669-686`), in
+    this package's expert layout: w13 e4m3 codes [E, 2I, H] ([gate | up]
+    rows), w2 [E, H, I], per-channel f32 scales s13 [E, 2I], s2 [E, H].
+
+    * Routing coefficients ``coeff[t, e] = sum over routes of f32(bf16(w))``
+      for the routes of token t to expert e (repeated ids merge; ids outside
+      [0, E) add nothing), `:256-262`; an expert is active when any of its
+      coefficients is non-zero.
+    * Per active expert, ascending id: gate_up as the grouped matmul's
+      quantized-lhs regime with its bf16 accumulator (`:131-151`:
+      per (row, 512) e4m3 codes with bf16 scales, bf16 block dot, times the
+      activation scale, times bf16(weight scale), bf16 sums; this is
+      ``linear.w8a8_gmm_bf16acc``); ``silu(gate) * up`` with jax's bf16
+      elementwise rounding (``sigmoid``, ``gate * sigmoid``, ``* up`` each
+      rounded to bf16, `:152`); the same recipe for down (`:153-168`).
+    * ``owner[t] += coeff[t, e] * f32(down)`` where ``coeff != 0``, else 0
+      (the mask keeps a non-finite expert output out of tokens that do not
+      route to it, `:169-172`); the result is bf16(owner) (`:246`).
+
+    Every token's rows depend on that token only, so the expert linears run
+    on the tokens with a non-zero coefficient; the others are masked anyway.
+
+    hidden [T, H] bf16-valued; topk_weights / topk_ids [T, k] -> [T, H]
+    bf16-valued f32.
+    """
+    x = bf16_round(np.asarray(hidden, np.float32))
+    t, h = x.shape
+    ids = np.asarray(topk_ids)
+    w = bf16_round(np.asarray(topk_weights, np.float32))
+    num_experts = np.asarray(w13).shape[0]
+    coeff = np.zeros((t, num_experts), np.float32)
+    for r in range(ids.shape[1]):
+        for tok in range(t):
+            e = int(ids[tok, r])
+            if 0 <= e < num_experts:
+                coeff[tok, e] = np.float32(coeff[tok, e] + w[tok, r])
+    owner = np.zeros((t, h), np.float32)
+    for e in range(num_experts):
+        rows = np.nonzero(coeff[:, e] != 0)[0]
+        if rows.size == 0:
+            continue
+        gu = w8a8_gmm_bf16acc(x[rows], w13[e], s13[e], "fp8")
+        i = gu.shape[1] // 2
+        a = silu_mul_bf16(gu[:, :i], gu[:, i:])
+        y = w8a8_gmm_bf16acc(a, w2[e], s2[e], "fp8")
+        owner[rows] = (owner[rows] + (y * coeff[rows, e][:, None]).astype(np.float32)).astype(np.float32)
+    return bf16_round(owner)
+

@@ -276,3 +276,60 @@ def test_mx_activation_host_logic():
             ops.plan_for_shape(_capi.W4A4_MX, 256, 256, k)
     with pytest.raises(RuntimeError):  # no fused activation on the MX kernel
         ops.plan_for_shape(_capi.W4A4_MX, 256, 512, 1024, activation="silu")
+
+
+def _dense_expert_args(m=16, h=512, i=512, e=4):
+    x = torch.zeros((m, h), dtype=torch.bfloat16)
+    w1 = torch.zeros((e, 2 * i, h), dtype=torch.float8_e4m3fn)
+    w2 = torch.zeros((e, h, i), dtype=torch.float8_e4m3fn)
+    s1 = torch.ones((e, 2 * i), dtype=torch.float32)
+    s2 = torch.ones((e, h), dtype=torch.float32)
+    return x, w1, w2, s1, s2
+
+
+@pytest.mark.parametrize("unsupported", ["none", "unaligned_tokens", "bias", "activation", "scale",
+                                         "bf16_weights", "unaligned_hidden", "unaligned_inter", "block_scale"])
+def test_dense_expert_admission(unsupported):
+    """`tests/kernels/experimental/test_moe_dense_expert.py:122-149`: the
+    unsupported inputs keep the grouped path (the admission rule of
+    `moe_dense_expert.py:50-90`)."""
+    from qmoe.layers.fused_moe import can_use_dense_expert
+
+    x, w1, w2, s1, s2 = _dense_expert_args()
+    b1, act, fmt = None, "silu", "fp8"
+    if unsupported == "unaligned_tokens":
+        x = x[:15]
+    elif unsupported == "bias":
+        b1 = torch.zeros((w1.shape[0], 1, w1.shape[1]))
+    elif unsupported == "activation":
+        act = "gelu"
+    elif unsupported == "scale":
+        s1 = None
+    elif unsupported == "bf16_weights":
+        w1, fmt = w1.to(torch.bfloat16), "bf16"
+    elif unsupported == "unaligned_hidden":
+        x, w1, w2, s1, s2 = _dense_expert_args(h=384)
+    elif unsupported == "unaligned_inter":
+        x, w1, w2, s1, s2 = _dense_expert_args(i=320)
+    elif unsupported == "block_scale":
+        s1, fmt = torch.ones((4, 1024, 4)), "fp8_w8a16"
+    assert can_use_dense_expert(x, w1, w2, s1, s2, b1, None, act, fmt) == (unsupported == "none")
+
+
+def test_dense_expert_threshold_env(monkeypatch):
+    """`TPU_MOE_DENSE_EXPERT_THRESHOLD` (`envs.py:642`, non-negative, 0 =
+    off) counts tokens: admitted exactly when 0 < T <= threshold."""
+    from qmoe import envs
+    from qmoe.layers.fused_moe import _dense_expert_admitted
+
+    x, w1, w2, s1, s2 = _dense_expert_args(m=32)
+    monkeypatch.delenv("TPU_MOE_DENSE_EXPERT_THRESHOLD", raising=False)
+    assert envs.TPU_MOE_DENSE_EXPERT_THRESHOLD == 0
+    assert not _dense_expert_admitted(x, w1, w2, s1, s2, None, None, "silu", "fp8")
+    monkeypatch.setenv("TPU_MOE_DENSE_EXPERT_THRESHOLD", "31")
+    assert not _dense_expert_admitted(x, w1, w2, s1, s2, None, None, "silu", "fp8")
+    monkeypatch.setenv("TPU_MOE_DENSE_EXPERT_THRESHOLD", "32")
+    assert _dense_expert_admitted(x, w1, w2, s1, s2, None, None, "silu", "fp8")
+    monkeypatch.setenv("TPU_MOE_DENSE_EXPERT_THRESHOLD", "-1")
+    with pytest.raises(ValueError):
+        envs.TPU_MOE_DENSE_EXPERT_THRESHOLD

@@ -216,3 +216,127 @@ def test_mx_activation_format_is_two_w4a4_linears():
     assert not np.array_equal(out, moe.fused_moe(x, moe.ExpertWeights("mxfp4", w13, s13, w2, s2),
                                                  np.ones((T, 1), np.float32), np.zeros((T, 1), np.int32),
                                                  "swigluoai")[0])
+
+
+def _dense_expert_fixture(i=512, seed=27):
+    """The reference's dense-expert fixture (`tests/kernels/experimental/
+    test_moe_dense_expert.py:27-37`: m 16, h 512, e 4, randn tokens, integer
+    codes in [-8, 8], scales U(0.006, 0.012)) in this package's N-major layout."""
+    rng = np.random.default_rng(seed)
+    m, h, e = 16, 512, 4
+    x = codecs.bf16_round(rng.normal(size=(m, h)).astype(np.float32))
+    w13 = codecs.e4m3_encode(rng.integers(-8, 9, size=(e, 2 * i, h)).astype(np.float32))
+    w2 = codecs.e4m3_encode(rng.integers(-8, 9, size=(e, h, i)).astype(np.float32))
+    s13 = rng.uniform(0.006, 0.012, size=(e, 2 * i)).astype(np.float32)
+    s2 = rng.uniform(0.006, 0.012, size=(e, h)).astype(np.float32)
+    return x, w13, s13, w2, s2
+
+
+def dense_expert_case(case):
+    """The reference test's routing cases (`test_moe_dense_expert.py:56-70`)
+    with its expert-parallel offset 64 removed: ids 64..67 are local experts
+    0..3, ids outside them (63, 68, 0..3 before the shift) are -1."""
+    ids = np.tile(np.array([[0, 1, -1, -1]], np.int32), (16, 1))
+    ids[8:, :2] = [2, 3]
+    w = np.tile(np.array([[0.125, 0.25, 0.375, 0.25]], np.float32), (16, 1))
+    if case == "single":
+        ids[:, :] = [3, -1, -1, -1]
+    elif case == "three":
+        ids[:, :] = [0, 1, 2, -1]
+    elif case == "empty":
+        ids[:, :] = -1
+    elif case == "zero":
+        w[:] = 0
+    elif case == "duplicate":
+        ids[:, :] = [0, 0, 1, 1]
+    return ids, w
+
+
+@pytest.mark.parametrize("case", ["empty", "zero"])
+def test_dense_expert_no_local_work_is_zero(case):
+    """Known answer of `test_moe_dense_expert.py:99-101`: no active route
+    gives exactly 0."""
+    x, w13, s13, w2, s2 = _dense_expert_fixture()
+    ids, w = dense_expert_case(case)
+    out = moe.dense_expert_moe(x, w13, s13, w2, s2, w, ids)
+    assert np.array_equal(out, np.zeros_like(out))
+
+
+@pytest.mark.parametrize("i", [512, 640])
+@pytest.mark.parametrize("case", ["mixed", "single", "three", "duplicate"])
+def test_dense_expert_within_the_reference_bar_of_the_grouped_path(case, i):
+    """The reference holds the dense-expert branch to a relative L2 error
+    under 0.008 against its grouped path (`test_moe_dense_expert.py:102-104`),
+    both with the grouped matmul's bf16 accumulator: here the same bar
+    against the grouped oracle with that accumulator (format
+    ``fp8_bf16acc``), on the reference's fixture and cases. A dropped
+    coefficient, a swapped gate / up half or a transposed weight fails by far.
+
+    Against the f32-accumulated grouped recipe (format ``fp8``, what the
+    kernels compute and the north star's fp32-accumulated reference) the gap
+    is larger, about 2 % relative L2: the intermediate differs by about 0.5 %
+    and its per-(row, 512) e4m3 requantization turns that into fresh rounding
+    noise; the north star's cosine bar still holds."""
+    x, w13, s13, w2, s2 = _dense_expert_fixture(i)
+    ids, w = dense_expert_case(case)
+    dense = moe.dense_expert_moe(x, w13, s13, w2, s2, w, ids)
+    grouped, _, _ = moe.fused_moe(x, moe.ExpertWeights("fp8_bf16acc", w13, s13, w2, s2), w, ids, "silu")
+    rel = np.linalg.norm(dense - grouped) / np.linalg.norm(grouped)
+    assert rel < 0.008, rel  # exactly 0 here: the coefficients' products are exact
+    f32acc, _, _ = moe.fused_moe(x, moe.ExpertWeights("fp8", w13, s13, w2, s2), w, ids, "silu")
+    cos = np.sum(dense * f32acc) / (np.linalg.norm(dense) * np.linalg.norm(f32acc))
+    assert cos >= 0.9995 and np.linalg.norm(dense - f32acc) / np.linalg.norm(f32acc) < 0.05
+
+
+def test_dense_expert_hand_computed_value():
+    """One token, one route, every rounding exact: a 448 in the token's block
+    gives scale 1 (codes = values); gate code 1 x 16 at scale 1 and up code
+    -2 x 14 ... : gate 16, up -28, silu(16) * -28 = -448 in bf16 (sigmoid(16)
+    rounds to 1); its block scale is 1 again, the down code 1 at scale 2^-4
+    gives -28, times the coefficient 0.5: -14. Gate and up swapped would give
+    silu(-28) * 16 ~ 0."""
+    h, i, e = 512, 128, 1
+    x = np.zeros((1, h), np.float32)
+    x[0, 0], x[0, 5] = 448.0, 16.0
+    w13 = np.zeros((e, 2 * i, h), np.float32)
+    w13[0, 3, 5] = 1.0        # gate channel 3 reads column 5: 16
+    w13[0, i + 3, 5] = -1.75  # up channel 3: 16 * -1.75 = -28
+    w2 = np.zeros((e, h, i), np.float32)
+    w2[0, 7, 3] = 1.0
+    s13 = np.ones((e, 2 * i), np.float32)
+    s2 = np.full((e, h), 2.0 ** -4, np.float32)
+    ids, w = np.array([[0]], np.int32), np.array([[0.5]], np.float32)
+    out = moe.dense_expert_moe(x, codecs.e4m3_encode(w13), s13, codecs.e4m3_encode(w2), s2, w, ids)
+    expect = np.zeros((1, h), np.float32)
+    expect[0, 7] = -14.0
+    assert np.array_equal(out, expect)
+
+
+def test_dense_expert_duplicate_ids_merge_coefficients():
+    """Routes of one token to one expert add their coefficients
+    (`moe_dense_expert.py:256-262`): ids [0, 0] with weights [a, b] equal
+    id 0 with weight a + b when the sum is exact in bf16."""
+    x, w13, s13, w2, s2 = _dense_expert_fixture()
+    ids2 = np.tile(np.array([[0, 0]], np.int32), (16, 1))
+    w2r = np.tile(np.array([[0.25, 0.5]], np.float32), (16, 1))
+    one = moe.dense_expert_moe(x, w13, s13, w2, s2, np.full((16, 1), 0.75, np.float32), ids2[:, :1])
+    two = moe.dense_expert_moe(x, w13, s13, w2, s2, w2r, ids2)
+    assert np.array_equal(one, two)
+
+
+def test_dense_expert_nonfinite_expert_stays_with_its_tokens():
+    """`test_moe_dense_expert.py:281-304`: with expert 3's gate_up codes NaN,
+    tokens routed to expert 0 stay finite, tokens routed to 3 are NaN; a
+    zero-coefficient route to expert 3 contributes exactly 0 (the mask)."""
+    x, w13, s13, w2, s2 = _dense_expert_fixture()
+    w13 = w13.copy()
+    w13[3] = 0x7F  # e4m3fn NaN
+    ids = np.where(np.arange(16)[:, None] < 8, 0, 3).astype(np.int32)
+    with np.errstate(invalid="ignore"):  # the NaN rows' requantization casts NaN
+        out = moe.dense_expert_moe(x, w13, s13, w2, s2, np.ones((16, 1), np.float32), ids)
+    assert np.isfinite(out[:8]).all() and np.isnan(out[8:]).all()
+    ids2 = np.tile(np.array([[0, 3]], np.int32), (16, 1))
+    w_zero = np.tile(np.array([[1.0, 0.0]], np.float32), (16, 1))
+    masked = moe.dense_expert_moe(x, w13, s13, w2, s2, w_zero, ids2)
+    only0 = moe.dense_expert_moe(x, w13, s13, w2, s2, np.ones((16, 1), np.float32), ids2[:, :1])
+    assert np.array_equal(masked, only0)

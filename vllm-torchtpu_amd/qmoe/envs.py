@@ -45,6 +45,9 @@ _READERS = {
     "MOE_REQUANTIZE_WEIGHT_DTYPE": lambda: os.getenv("MOE_REQUANTIZE_WEIGHT_DTYPE"),
     # MoE: routes with a zero routing weight are padding and skipped
     "TPU_MOE_SKIP_PADDED_TOKENS": lambda: _bool("TPU_MOE_SKIP_PADDED_TOKENS"),
+    # MoE: steps of at most this many tokens (0: off) with per-channel FP8
+    # experts, silu and no biases take the dense-expert decode semantics
+    "TPU_MOE_DENSE_EXPERT_THRESHOLD": lambda: _nonneg_int("TPU_MOE_DENSE_EXPERT_THRESHOLD", 0),
     # MoE decode: serve armed layers' decode steps with the fused decode op
     # (shared + routed experts), up to MAX_TOKENS tokens per step
     "FUSED_MOE_DECODE_KERNEL": lambda: _bool("FUSED_MOE_DECODE_KERNEL"),

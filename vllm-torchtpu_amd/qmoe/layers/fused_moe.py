@@ -89,6 +89,44 @@ def infer_weight_format(w1: torch.Tensor, w1_scale) -> str:
     raise ValueError(f"unsupported MoE weight dtype {w1.dtype}")
 
 
+def _per_channel(s, E, N) -> bool:
+    return (s is not None and s.dtype == torch.float32 and s.shape[0] == E and s.shape[1] == N
+            and (s.dim() == 2 or (s.dim() == 3 and s.shape[2] == 1)))
+
+
+def can_use_dense_expert(hidden_states, w1, w2, w1_scale, w2_scale, w1_bias, w2_bias, activation, fmt) -> bool:
+    """Admission of the dense-expert decode branch
+    (`kernels/experimental/moe_dense_expert.py:50-90`, ``can_use_dense_expert``),
+    on this package's expert layout: silu; per-channel e4m3 experts (format
+    ``fp8``: w1 [E, 2I, H], w2 [E, H, I], f32 scales [E, 2I] / [E, H], or
+    [E, N, 1]); no biases; bf16 tokens; T % 16 == 0, H % 512 == 0, I % 128 == 0.
+    The reference's hardware clause (native FP8 and a 512-column activation
+    block at least one matrix-unit column wide) always holds here: per-channel
+    experts always quantize their activations per (row, 512)."""
+    if activation != "silu" or fmt != "fp8" or w1_bias is not None or w2_bias is not None:
+        return False
+    if hidden_states.dim() != 2 or w1.dim() != 3 or w2.dim() != 3 or hidden_states.dtype != torch.bfloat16:
+        return False
+    if w1.dtype != torch.float8_e4m3fn or w2.dtype != torch.float8_e4m3fn:
+        return False
+    m, h = hidden_states.shape
+    e, out, i = w2.shape
+    if min(m, h, i, e) <= 0 or m % 16 or h % 512 or i % 128:
+        return False
+    if out != h or tuple(w1.shape) != (e, 2 * i, h):
+        return False
+    return _per_channel(w1_scale, e, 2 * i) and _per_channel(w2_scale, e, h)
+
+
+def _dense_expert_admitted(x, w1, w2, w1_scale, w2_scale, w1_bias, w2_bias, activation, fmt) -> bool:
+    """``0 < T <= TPU_MOE_DENSE_EXPERT_THRESHOLD`` and the admission rule, the
+    token threshold first (`layers/core/fused_moe_gmm.py:669-686`)."""
+    from qmoe import envs
+
+    return (0 < x.shape[0] <= envs.TPU_MOE_DENSE_EXPERT_THRESHOLD
+            and can_use_dense_expert(x, w1, w2, w1_scale, w2_scale, w1_bias, w2_bias, activation, fmt))
+
+
 def fused_moe_gmm(hidden_states, w1, w2, w1_scale, w2_scale, w1_bias, w2_bias, topk_weights,
                   topk_ids, experts_start, topk, activation, rhs_quant_dtype=None,
                   skip_padded_tokens=None, weight_format=None):
@@ -127,6 +165,16 @@ def fused_moe_gmm(hidden_states, w1, w2, w1_scale, w2_scale, w1_bias, w2_bias, t
     T, H = hidden_states.shape
     if topk_weights.shape != (T, topk) or topk_ids.shape != (T, topk):
         raise ValueError(f"topk tensors must be [{T}, {topk}]")
+    # The dense-expert decode branch (`fused_moe_gmm.py:669-686`) weighs each
+    # active expert's output by the token's summed routing coefficient and
+    # masks zero coefficients before accumulating (`moe_dense_expert.py:
+    # 175-181`), so a zero-weight route contributes exactly 0 even when its
+    # expert's output is not finite. Its activation recipe is already this
+    # format's (per (row, 512) bf16-arithmetic e4m3 codes), and the grouped
+    # path visits each active expert's weights once, as it does; what it
+    # adds is the mask, which is the skipping of zero-weight routes.
+    if _dense_expert_admitted(hidden_states, w1, w2, w1_scale, w2_scale, w1_bias, w2_bias, activation, fmt):
+        skip_padded_tokens = True
     x = hidden_states if hidden_states.dtype == torch.bfloat16 else hidden_states.to(torch.bfloat16)
     # `fused_moe_gmm.py:653`: routing weights take the hidden dtype
     tw = topk_weights.to(torch.bfloat16)
@@ -190,6 +238,8 @@ def moe_forward(layer, x, router_logits, w1, w2, w1_scale, w2_scale, w1_bias, w2
         return fused_moe_gmm(x, w1, w2, w1_scale, w2_scale, w1_bias, w2_bias, topk_weights, topk_ids, None, topk,
                              act, skip_padded_tokens=skip_padded_tokens, weight_format=weight_format)
     ops.act_code(act)
+    if _dense_expert_admitted(x, w1, w2, w1_scale, w2_scale, w1_bias, w2_bias, act, weight_format):
+        skip_padded_tokens = True  # the dense-expert branch's coefficient mask, as in fused_moe_gmm
     bias, rsf, ng, tg = moe_routing.routing_params(layer)
     return torch.ops.qmoe.routed_moe(x, router_logits, w1, w2, w1_scale, w2_scale, w1_bias, w2_bias, int(topk),
                                      layer.scoring_func, bool(layer.renormalize), bias, float(rsf), int(ng),
