@@ -172,16 +172,22 @@ def test_fp8_moe_block_checkpoint_sigmoid_grouped(dev, monkeypatch, native):
     assert_close_rows(got.float().cpu().numpy(), ref, "fp8 moe method")
 
 
-@pytest.mark.parametrize("dtype,block,I,unpadded", [("int8", None, 128, None), ("float8_e4m3fn", 128, 256, None),
-                                                     ("float8_e4m3fn", 512, 512, None),
-                                                     ("float8_e4m3fn", None, 192, None),
-                                                     ("float8_e4m3fn", None, 256, 200)])
-def test_fp8_moe_requant_switches(dev, monkeypatch, dtype, block, I, unpadded):
+@pytest.mark.parametrize("dtype,block,I,unpadded,dense", [("int8", None, 128, None, False),
+                                                           ("float8_e4m3fn", 128, 256, None, False),
+                                                           ("float8_e4m3fn", 512, 512, None, False),
+                                                           ("float8_e4m3fn", None, 192, None, False),
+                                                           ("float8_e4m3fn", None, 256, 200, False),
+                                                           ("float8_e4m3fn", None, 128, None, True)])
+def test_fp8_moe_requant_switches(dev, monkeypatch, dtype, block, I, unpadded, dense):
     """MOE_REQUANTIZE_WEIGHT_DTYPE / MOE_REQUANTIZE_BLOCK_SIZE (`fp8.py:185-213`):
     int8 per channel (int8 activations per (token, 512)), fp8 per (row, 128)
     (bf16-dequantized weights) and per (row, 512); an intermediate size that
     is not a multiple of 128 is zero-padded to one, and the padding of an
-    unpadded intermediate size is zeroed (`fp8.py:351-406, 515-522`)."""
+    unpadded intermediate size is zeroed (`fp8.py:351-406, 515-522`). With
+    ``dense``, a 16-token step under TPU_MOE_DENSE_EXPERT_THRESHOLD: the
+    method's per-channel runtime layout is admitted to the dense-expert
+    branch (`layers/core/fused_moe_gmm.py:669-686`), here on the fused
+    route + dispatch route of `moe_forward`."""
     from qmoe.layers import quantization as q
 
     print(f"fp8 moe requant {dtype} block={block} I={I} unpadded={unpadded}", flush=True)
@@ -191,7 +197,8 @@ def test_fp8_moe_requant_switches(dev, monkeypatch, dtype, block, I, unpadded):
     if block:
         monkeypatch.setenv("MOE_REQUANTIZE_BLOCK_SIZE", str(block))
     rng = np.random.default_rng(17 + I)
-    E, H, k, T = 8, 512, 2, 11
+    E, H, k, T = 8, 512, 2, (16 if dense else 11)
+    monkeypatch.setenv("TPU_MOE_DENSE_EXPERT_THRESHOLD", "16" if dense else "0")
     layer = _moe_layer(k, "silu")
     if unpadded:
         layer.moe_config.intermediate_size_per_partition_unpadded = unpadded
@@ -227,10 +234,19 @@ def test_fp8_moe_requant_switches(dev, monkeypatch, dtype, block, I, unpadded):
     assert layer._qmoe_format == fmt
     x = codecs.bf16_round(rng.standard_normal((T, H)).astype(np.float32))
     logits = codecs.bf16_round(rng.standard_normal((T, E)).astype(np.float32))
+    if dense:
+        from qmoe.layers.fused_moe import _dense_expert_admitted
+
+        assert _dense_expert_admitted(_t(x, dev, torch.bfloat16), layer.w13_weight, layer.w2_weight,
+                                      layer.w13_weight_scale, layer.w2_weight_scale, None, None, "silu", fmt)
     got = method.apply_monolithic(layer, _t(x, dev, torch.bfloat16), _t(logits, dev, torch.bfloat16))
     tw, ids = routing.select_experts(logits, k, True, "softmax")
     ref, _, _ = omoe.fused_moe(x, omoe.ExpertWeights(fmt, w13q, w13s, w2q, w2s), tw, ids, "silu")
     assert_close_rows(got.float().cpu().numpy(), ref, f"fp8 moe requant {dtype} {block}")
+    if dense:
+        d = omoe.dense_expert_moe(x, w13q, w13s.reshape(E, -1), w2q, w2s.reshape(E, -1), tw, ids)
+        g = got.float().cpu().numpy().astype(np.float64)
+        assert np.sum(g * d) / (np.linalg.norm(g) * np.linalg.norm(d)) >= 0.9995
 
 
 def test_mxfp4_moe_interleaved_checkpoint_swigluoai(dev):
