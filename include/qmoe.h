@@ -145,7 +145,10 @@ int qmoe_row_quant(const void* x, int64_t ldx, int in_f32, int64_t M, int64_t K,
  * e2m1 encoder `compressed_tensors_moe/utils.py:167-183`
  * (`quantize_to_fp4_e2m1_nibbles`). The reference's W4A4 MXFP4 method runs
  * its activations unquantized; this is the activation side of the opt-in
- * QMOE_W4A4_MX GEMM. At least one of q, xq.
+ * QMOE_W4A4_MX GEMM. At least one of q, xq. A block holding an inf or NaN
+ * (the reference's rule has no answer for it) gets codes 0 and byte 255,
+ * the e8m0 NaN encoding: it reads back as NaN (xq: bf16 NaN) and the row's
+ * other blocks keep their own codes.
  */
 int qmoe_mx_quant(const void* x, int64_t ldx, int64_t M, int64_t K, int64_t Kp, void* q, int64_t ldq,
                   void* scales, int64_t lds, void* xq, int64_t ldxq, qmoe_stream_t stream);

@@ -240,6 +240,12 @@ def quantize_mx_fp4(x, k_pad=None):
     weight-side rule applied to activations. Columns K..Kp-1 (``k_pad``, a
     multiple of 32 >= K) are zero blocks: codes 0, byte 0 (the rule's answer
     for an all-zero block).
+
+    A block holding an inf or NaN (the reference's rule has no answer: its
+    scale would be non-finite) gets this build's definition: codes 0 and
+    byte 255, the e8m0 NaN encoding, so the block dequantizes to NaN and the
+    row's other blocks are untouched. Parity of that case is the build's own
+    definition (no reference counterpart).
     """
     x = np.asarray(x, dtype=np.float32)
     m, k = x.shape
@@ -249,6 +255,8 @@ def quantize_mx_fp4(x, k_pad=None):
     xp = np.zeros((m, kp), np.float32)
     xp[:, :k] = x
     blocks = xp.reshape(m, kp // MX_BLOCK, MX_BLOCK)
+    bad = ~np.isfinite(blocks).all(axis=-1)
+    blocks = np.where(bad[..., None], np.float32(0.0), blocks)
     amax = np.max(np.abs(blocks), axis=-1)
     scale = (amax * np.float32(1.0 / 6.0)).astype(np.float32)
     e = e8m0_exponent_ceil(scale)
@@ -256,4 +264,4 @@ def quantize_mx_fp4(x, k_pad=None):
     v = np.clip((blocks * inv[..., None]).astype(np.float32), -FP4_MAX, FP4_MAX)
     codes = fp4_encode_bucket(v).reshape(m, kp)
     packed = (codes[:, 0::2] | (codes[:, 1::2] << 4)).astype(np.uint8)
-    return packed, (e + 127).astype(np.uint8)
+    return packed, np.where(bad, 255, e + 127).astype(np.uint8)

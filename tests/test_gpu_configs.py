@@ -358,6 +358,138 @@ def test_cfg4_shared_expert(dev, T):
     assert_close_same_codes(_np(y[toks].float()), ref, f"cfg4 shared down T={T}")
 
 
+_E4D = {}
+
+
+def _cfg4_default_layer(qd):
+    """Config 4's checkpoint through the FP8 MoE method's default load path
+    (`fp8.py:486-617`: 128 x 128 tiles dequantized in float32 on the
+    device, requantized per output channel to e4m3, or to int8 with
+    MOE_REQUANTIZE_WEIGHT_DTYPE=int8); one processed layer kept at a time."""
+    import types
+
+    from qmoe.layers import quantization as q
+
+    if _E4D.get("qd") != qd:
+        _E4D.clear()
+        import os
+
+        w13, s13, w2, s2, _, _, _, _, bias = _cfg4_experts()
+        E, H, I = 256, 7168, 2048
+        layer = torch.nn.Module()
+        layer.moe_config = types.SimpleNamespace(experts_per_token=8, has_bias=False)
+        layer.renormalize, layer.scoring_func, layer.e_score_correction_bias = True, "sigmoid", bias
+        layer.use_grouped_topk, layer.num_expert_group, layer.topk_group = True, 8, 4
+        layer.routed_scaling_factor, layer.custom_routing_function, layer.activation = 2.5, None, "silu"
+        saved = {v: os.environ.pop(v, None) for v in ("MOE_REQUANTIZE_WEIGHT_DTYPE", "MOE_REQUANTIZE_BLOCK_SIZE",
+                                                      "QMOE_FP8_NATIVE_BLOCKS")}
+        try:
+            if qd == "int8":
+                os.environ["MOE_REQUANTIZE_WEIGHT_DTYPE"] = "int8"
+            method = q.Fp8MoEMethod(q.Fp8Config(weight_block_size=[128, 128]), layer.moe_config)
+            method.create_weights(layer, E, H, I, torch.bfloat16)
+            layer.w13_weight.data, layer.w2_weight.data = w13, w2
+            layer.w13_weight_scale_inv.data, layer.w2_weight_scale_inv.data = s13, s2
+            method.process_weights_after_loading(layer)
+        finally:
+            for v, val in saved.items():
+                os.environ.pop(v, None)
+                if val is not None:
+                    os.environ[v] = val
+        assert layer._qmoe_format == qd
+        # the requantized codes and scales of a few experts, bit-exact
+        for e in (0, 131, 255):
+            for wt, st, c, sc in ((w13, s13, layer.w13_weight, layer.w13_weight_scale),
+                                  (w2, s2, layer.w2_weight, layer.w2_weight_scale)):
+                rq, rs = quant.quantize_tensor(quant.dequant_tiles(_np(wt[e].view(torch.uint8)), _np(st[e])), qd)
+                np.testing.assert_array_equal(_np(c[e].view(torch.uint8)), rq.view(np.uint8))
+                np.testing.assert_array_equal(_np(sc[e]).reshape(rs.shape), rs)
+        # the shared expert as a default dense FP8 linear: the same tiles
+        # dequantized and requantized per channel (`fp8.py:297-348`)
+        from qmoe import ops
+        from qmoe.layers.quantization.fp8 import dequantize_fp8_weight
+
+        _, _, _, _, sh13, ss13, sh2, ss2, _ = _cfg4_experts()
+        shared = []
+        for wt, st in ((sh13, ss13), (sh2, ss2)):
+            qc, sc = ops.row_quant(dequantize_fp8_weight(wt, weight_scale_inv=st, block=(128, 128)), qd, mode="load")
+            rq, rs = quant.quantize_tensor(quant.dequant_tiles(_np(wt.view(torch.uint8)), _np(st)), qd)
+            np.testing.assert_array_equal(_np(qc.view(torch.uint8)), rq.view(np.uint8))
+            np.testing.assert_array_equal(_np(sc), rs)
+            shared += [qc, sc]
+        _E4D.update(qd=qd, layer=layer, method=method, shared=shared)
+    return _E4D["method"], _E4D["layer"]
+
+
+@pytest.mark.parametrize("T", [1, 8, 64, 512, 4096])
+@pytest.mark.parametrize("qd", ["fp8", "int8"])
+def test_cfg4_default_recipe(dev, qd, T):
+    """Config 4 through the method's DEFAULT recipe -- what a DeepSeek-V3
+    checkpoint loaded by `Fp8MoEMethod` runs without this build's opt-in
+    native tiles: per-channel e4m3 (or int8) experts and per-(token, 512)
+    bf16-arithmetic activation codes before each grouped GEMM
+    (`kernels/megablox/gmm_v2.py:500-548, 1198-1237`). Ids of every token
+    bit-exact; the layer output on a token sample against the oracle's
+    grouped-matmul recipe."""
+    from qmoe import ops
+
+    E, k, H = 256, 8, 7168
+    print(f"cfg4 default recipe {qd} T={T}", flush=True)
+    method, layer = _cfg4_default_layer(qd)
+    bias = layer.e_score_correction_bias
+    g = _gen(530 + T)
+    x = torch.randn((T, H), device="cuda", generator=g).to(torch.bfloat16)
+    logits = _cfg4_logits(T, False, g)
+    y = _run(lambda: method.apply_monolithic(layer, x, logits))
+    tw, ids = ops.moe_route(logits, k, "sigmoid", True, bias=bias, routed_scaling_factor=2.5,
+                            num_expert_group=8, topk_group=4)
+    _, ids_ref = routing.grouped_topk(_np(logits.float()), k, True, 8, 4, "sigmoid", _np(bias), 2.5)
+    np.testing.assert_array_equal(_np(ids), ids_ref)
+    toks = _rows_sample(T, 3)
+    codes = (lambda t: t.view(torch.uint8)) if qd == "fp8" else (lambda t: t)
+    ew = omoe.ExpertWeights(qd, _DeviceExperts(codes(layer.w13_weight)),
+                            _DeviceExperts(layer.w13_weight_scale.reshape(E, -1)),
+                            _DeviceExperts(codes(layer.w2_weight)),
+                            _DeviceExperts(layer.w2_weight_scale.reshape(E, -1)), keep=False)
+    ref = omoe.fused_moe_tokens(_np(x[toks].float()), ew, _np(tw[toks].float()), ids_ref[toks], "silu", E)
+    assert_close_rows(_np(y[toks].float()), ref, f"cfg4 default {qd} T={T}")
+
+    # the shared expert beside it: per-token activation codes, silu fused
+    # into the gate_up GEMM, the intermediate re-quantized per token
+    from qmoe import _capi
+
+    qs13, cs13, qs2, cs2 = _E4D["shared"]
+    wf, I = (0 if qd == "fp8" else 1), 2048
+
+    def shared():
+        xq, xs = ops.row_quant(x, qd)
+        a = ops.gemm(_capi.W8A8_PC, xq.view(torch.uint8), qs13.view(torch.uint8), a_scale=xs, w_scale=cs13,
+                     wfmt=wf, activation="silu")
+        aq, as_ = ops.row_quant(a, qd)
+        return a, ops.gemm(_capi.W8A8_PC, aq.view(torch.uint8), qs2.view(torch.uint8), a_scale=as_, w_scale=cs2,
+                           wfmt=wf)
+
+    a, ys = _run(shared)
+    toks = _rows_sample(T, 8)
+    q13n = _np(qs13.view(torch.uint8)) if qd == "fp8" else _np(qs13)
+    gu, _, _ = linear.w8a8_per_channel(_np(x[toks].float()), q13n, _np(cs13), qd)
+    assert_close_rows(_np(a[toks].float()), codecs.bf16_round(omoe.act_fn(gu[:, :I], gu[:, I:], "silu")),
+                      f"cfg4 default shared gate_up {qd} T={T}")
+    q2n = _np(qs2.view(torch.uint8)) if qd == "fp8" else _np(qs2)
+    ref2, _, _ = linear.w8a8_per_channel(_np(a[toks].float()), q2n, _np(cs2), qd)
+    if qd == "int8":
+        np.testing.assert_array_equal(_np(ys[toks].float()), ref2)
+    else:
+        assert_close_same_codes(_np(ys[toks].float()), ref2, f"cfg4 default shared down {qd} T={T}")
+
+
+def test_cfg4_default_recipe_release():
+    """Frees the processed default-recipe layer (11.3 GB) before the
+    module's later tests."""
+    _E4D.clear()
+    torch.cuda.empty_cache()
+
+
 # ------------------------------------------------------------------ coverage
 
 
@@ -387,6 +519,14 @@ def _bench_plans():
             ops.plan_for_shape(_capi.W8A8_BLK, 8 * T, 7168, 2048, experts=256, max_rows=T, ws_bn=128),
             ops.plan_for_shape(_capi.W8A8_BLK, T, 4096, 7168, activation="silu", ws_bn=128),
             ops.plan_for_shape(_capi.W8A8_BLK, T, 7168, 2048, ws_bn=128)]
+    for wf in (0, 1):
+        for T in (1, 8, 64, 512, 4096):
+            plans[f"cfg4 default wfmt={wf} T={T}"] = [
+                ops.plan_for_shape(_capi.W8A8_GMM, 8 * T, 4096, 7168, wfmt=wf, activation="silu", experts=256,
+                                   max_rows=T),
+                ops.plan_for_shape(_capi.W8A8_GMM, 8 * T, 7168, 2048, wfmt=wf, experts=256, max_rows=T),
+                ops.plan_for_shape(_capi.W8A8_PC, T, 4096, 7168, wfmt=wf, activation="silu"),
+                ops.plan_for_shape(_capi.W8A8_PC, T, 7168, 2048, wfmt=wf)]
     return plans
 
 

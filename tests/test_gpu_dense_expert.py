@@ -114,3 +114,24 @@ def test_dense_expert_nonfinite_expert_stays_with_its_tokens(dev, monkeypatch):
     masked = _run(dev, monkeypatch, 1024, x, np.tile(np.array([[1.0, 0.0]], np.float32), (16, 1)), ids2, wts)
     alone = _run(dev, monkeypatch, 1024, x, np.ones((16, 1), np.float32), ids2[:, :1], wts)
     assert np.isfinite(masked).all() and np.array_equal(masked, alone)
+
+
+def test_dense_expert_opposite_routes_cancel(dev, monkeypatch):
+    """`moe_dense_expert.py:258-262`: a token's routes to one expert merge
+    into one coefficient before the mask, so weights +w and -w on the NaN
+    expert 3 beside a route to expert 0 give exactly the route to 0 alone
+    (the grouped sum w*y + (-w)*y would be NaN)."""
+    print("dense expert +w/-w on a NaN expert", flush=True)
+    x, w13, s13, w2, s2 = _dense_expert_fixture()
+    w13 = w13.copy()
+    w13[3] = 0x7F  # e4m3fn NaN
+    wts = _weights(dev, w13, s13, w2, s2)
+    ids3 = np.tile(np.array([[0, 3, 3]], np.int32), (16, 1))
+    w3 = np.tile(np.array([[1.0, 0.375, -0.375]], np.float32), (16, 1))
+    merged = _run(dev, monkeypatch, 1024, x, w3, ids3, wts)
+    alone = _run(dev, monkeypatch, 1024, x, np.ones((16, 1), np.float32), ids3[:, :1], wts)
+    assert np.isfinite(merged).all() and np.array_equal(merged, alone)
+    # two routes to expert 0 (0.25 + 0.75) are the single route of weight 1
+    ids0 = np.tile(np.array([[0, 0]], np.int32), (16, 1))
+    w0 = np.tile(np.array([[0.25, 0.75]], np.float32), (16, 1))
+    assert np.array_equal(_run(dev, monkeypatch, 1024, x, w0, ids0, wts), alone)

@@ -208,3 +208,33 @@ def test_mxfp4_moe_mx_activations(dev, T):
     rows = np.unique(np.linspace(0, T - 1, min(T, 24)).astype(int))
     ref = omoe.fused_moe_tokens(x[rows], weights, tw[rows], ids[rows], "swigluoai", E)
     assert_close_rows(got.float().cpu().numpy()[rows], ref, f"mxfp4 moe mx T={T}")
+
+
+def test_mx_quant_non_finite_blocks(dev):
+    """Blocks holding inf or NaN: codes 0 and scale byte 255 (the e8m0 NaN
+    encoding), the dequantized block NaN, and every other block of the row
+    exactly as without them (no code spills into a neighbour)."""
+    from qmoe import ops
+
+    print("mx_quant non-finite blocks", flush=True)
+    rng = np.random.default_rng(77)
+    M, K = 4, 256
+    x = _acts(rng, M, K)
+    x[0, 5] = np.inf
+    x[0, 70] = -np.inf
+    x[2, 33] = np.nan
+    x[3, 255] = np.nan
+    x[3, 0] = np.inf
+    q_ref, s_ref = quant.quantize_mx_fp4(x)
+    q, s, xq = ops.mx_quant(_t(x, dev, torch.bfloat16), dequantized=True)
+    np.testing.assert_array_equal(s.cpu().numpy(), s_ref)
+    np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
+    bad = {(0, 0), (0, 2), (2, 1), (3, 7), (3, 0)}
+    d = xq.float().cpu().numpy()
+    for r in range(M):
+        for b in range(K // 32):
+            blk = d[r, b * 32:(b + 1) * 32]
+            if (r, b) in bad:
+                assert s_ref[r, b] == 255 and np.isnan(blk).all()
+            else:
+                assert np.isfinite(blk).all()

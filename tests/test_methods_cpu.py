@@ -333,3 +333,20 @@ def test_dense_expert_threshold_env(monkeypatch):
     monkeypatch.setenv("TPU_MOE_DENSE_EXPERT_THRESHOLD", "-1")
     with pytest.raises(ValueError):
         envs.TPU_MOE_DENSE_EXPERT_THRESHOLD
+
+
+def test_merge_repeated_routes():
+    """The dense-expert coefficient table in route form: repeated ids on a
+    token sum their weights (f32, route order) into the first route; later
+    repeats become id -1 with weight 0; +w / -w cancel to exactly 0."""
+    from qmoe.layers.fused_moe import merge_repeated_routes
+
+    ids = torch.tensor([[0, 3, 3, 1], [2, 2, 2, -1], [5, 6, 7, 8]], dtype=torch.int32)
+    w = torch.tensor([[1.0, 0.375, -0.375, 0.5], [0.25, 0.25, 0.5, 0.0], [0.1, 0.2, 0.3, 0.4]],
+                     dtype=torch.bfloat16)
+    mw, mi = merge_repeated_routes(w, ids)
+    assert mi.tolist() == [[0, 3, -1, 1], [2, -1, -1, -1], [5, 6, 7, 8]]
+    assert mw.dtype == torch.bfloat16
+    assert mw[0].float().tolist() == [1.0, 0.0, 0.0, 0.5]
+    assert mw[1].float().tolist() == [1.0, 0.0, 0.0, 0.0]
+    assert torch.equal(mw[2], w[2])

@@ -193,3 +193,32 @@ def test_mx_reproduces_representable_values_and_error_bound():
     # one octave down and doubles its codes: same values)
     q2, s2 = quant.quantize_mx_fp4(d)
     np.testing.assert_array_equal(codecs.dequant_mxfp4(q2, s2), d)
+
+
+def test_mx_quant_non_finite_blocks_are_nan_blocks():
+    """The build's definition for inf / NaN inside a 32-value block (the
+    reference's rule has none): codes 0, byte 255 (e8m0 NaN), so the block
+    decodes to NaN; the row's finite blocks quantize exactly as they do with
+    the bad block replaced by zeros."""
+    from oracle import codecs
+
+    rng = np.random.default_rng(3)
+    x = codecs.bf16_round(rng.standard_normal((2, 128)).astype(np.float32))
+    y = x.copy()
+    y[0, 40] = np.inf
+    y[1, 127] = np.nan
+    q, s = quant.quantize_mx_fp4(y)
+    z = x.copy()
+    z[0, 32:64] = 0.0
+    z[1, 96:128] = 0.0
+    qz, sz = quant.quantize_mx_fp4(z)
+    assert s[0, 1] == 255 and s[1, 3] == 255
+    assert (q[0, 16:32] == 0).all() and (q[1, 48:64] == 0).all()
+    keep = np.ones_like(s, bool)
+    keep[0, 1] = keep[1, 3] = False
+    np.testing.assert_array_equal(s[keep], sz[keep])
+    np.testing.assert_array_equal(q[:, :16], qz[:, :16])
+    with np.errstate(invalid="ignore"):
+        d = codecs.dequant_mxfp4(q, s)
+    assert np.isnan(d[0, 32:64]).all() and np.isnan(d[1, 96:]).all()
+    assert np.isfinite(d[0, :32]).all() and np.isfinite(d[1, :96]).all()

@@ -104,3 +104,41 @@ def test_repack_is_cached_per_weight_tensor():
     w.add_(1)  # an in-place change invalidates the copy
     b = rl.nmajor_copy(w)
     assert b is not a and torch.equal(b, w.t())
+
+
+def test_repack_cache_under_inference_mode():
+    """vLLM runs the forward under torch.inference_mode(): weights created
+    there keep no version counter. The repack cache keys them on identity
+    (nmajor_copy, fp4_linear, moe_weights), returns the same copy on the
+    second call, and still follows in-place changes of ordinary tensors."""
+    rng = np.random.default_rng(5)
+    k, n = 64, 32
+    with torch.inference_mode():
+        w = torch.from_numpy(rng.integers(-100, 100, (k, n), dtype=np.int8))
+        a = rl.nmajor_copy(w)
+        assert a is rl.nmajor_copy(w)
+        torch.testing.assert_close(a, w.t())
+        codes = rng.integers(0, 16, (n, k), dtype=np.uint8)
+        wq = torch.from_numpy(codecs.pack_fp4(codes.T.copy()))  # [K, N/2]
+        ws = torch.full((1, k // 32, 1, n), 0.5, dtype=torch.float32)
+        c, s = rl.fp4_linear(wq, ws, k)
+        c2, s2 = rl.fp4_linear(wq, ws, k)
+        assert c is c2 and s is s2
+        np.testing.assert_array_equal(codecs.unpack_fp4(c.numpy()), codes)
+        assert bool((s == 126).all())
+        E, H, I = 2, 64, 32
+        w1 = torch.from_numpy(rng.integers(-100, 100, (E, H, 2 * I), dtype=np.int8))
+        w2 = torch.from_numpy(rng.integers(-100, 100, (E, I, H), dtype=np.int8))
+        s1 = torch.ones((E, 1, 1, 2 * I), dtype=torch.float32)
+        s2 = torch.ones((E, 1, 1, H), dtype=torch.float32)
+        r1 = rl.moe_weights(H, w1, w2, s1, s2, None, None)
+        r2 = rl.moe_weights(H, w1, w2, s1, s2, None, None)
+        assert r1[0] is r2[0] and r1[1] is r2[1] and r1[-1] == "int8"
+        torch.testing.assert_close(r1[0], w1.transpose(1, 2))
+    # an ordinary tensor changed in place is repacked again
+    v = torch.from_numpy(rng.integers(-100, 100, (k, n), dtype=np.int8))
+    b = rl.nmajor_copy(v)
+    v.add_(1)
+    b2 = rl.nmajor_copy(v)
+    assert b2 is not b
+    torch.testing.assert_close(b2, v.t())

@@ -361,14 +361,19 @@ __global__ __launch_bounds__(kThreads) void mx_quant_kernel(const uint16_t* __re
     for (int it = 0; it < kMxIter; ++it) {
       const uint32_t wd[4] = {raw[it].x, raw[it].y, raw[it].z, raw[it].w};
       // block amax on the absolute-value bits of the bf16 pairs (ordered
-      // like the values; inputs are finite): packed 16-bit maxima
+      // like the values, inf and NaN above every finite value): packed
+      // 16-bit maxima
       u16x2 m2 = __builtin_bit_cast(u16x2, wd[0] & 0x7fff7fffu);
 #pragma unroll
       for (int i = 1; i < 4; ++i) m2 = __builtin_elementwise_max(m2, __builtin_bit_cast(u16x2, wd[i] & 0x7fff7fffu));
       uint32_t mb = (uint32_t)max(m2.x, m2.y) << 16;
       mb = max(mb, (uint32_t)__shfl_xor((int)mb, 1, 64));
       mb = max(mb, (uint32_t)__shfl_xor((int)mb, 2, 64));
-      const int e = mx_exponent_ceil(bits_f32(mb) * (1.0f / 6.0f));
+      // a block holding an inf or NaN: codes 0 and scale byte 255 (the e8m0
+      // NaN encoding), so the block reads back as NaN and its neighbours
+      // keep their own codes
+      const bool bad = mb >= 0x7f800000u;
+      const int e = mx_exponent_ceil(bits_f32(bad ? 0u : mb) * (1.0f / 6.0f));
       const float inv = __builtin_amdgcn_ldexpf(1.0f, -e);
       if (g0 + it * kThreads >= total) continue;
       uint32_t w = 0;
@@ -379,8 +384,8 @@ __global__ __launch_bounds__(kThreads) void mx_quant_kernel(const uint16_t* __re
         // |x| 2^-e <= amax 2^-e <= 6: the reference's clamp to +-6 never
         // binds; + 0.0f turns -0 into +0 (the encoder's sign is v < 0)
         const uint32_t vb = f32_bits(xv * inv + 0.0f);
-        const uint32_t mag = e2m1_mag(vb & 0x7fffffffu);
-        const uint32_t code = mag | ((vb >> 28) & 8u);
+        const uint32_t mag = bad ? 0u : e2m1_mag(vb & 0x7fffffffu);
+        const uint32_t code = bad ? 0u : mag | ((vb >> 28) & 8u);
         const float v = bits_f32(vb);
         w |= code << (4 * i);
         if (kFake) {
@@ -388,12 +393,12 @@ __global__ __launch_bounds__(kThreads) void mx_quant_kernel(const uint16_t* __re
           const float mv =
               mag < 4u ? 0.5f * (float)mag : (mag < 6u ? (float)(mag - 2u) : (mag == 6u ? 4.0f : 6.0f));
           const float dv = __builtin_amdgcn_ldexpf(v < 0.0f ? -mv : mv, e);
-          d[i >> 1] |= (f32_bits(dv) >> 16) << (16 * (i & 1));
+          d[i >> 1] |= (bad ? 0x7fc0u : f32_bits(dv) >> 16) << (16 * (i & 1));
         }
       }
       if (kCodes) {
         *reinterpret_cast<uint32_t*>(q + row[it] * ldq + c[it] / 2) = w;
-        if ((threadIdx.x & 3) == 0) scales[row[it] * lds + c[it] / 32] = (uint8_t)(e + 127);
+        if ((threadIdx.x & 3) == 0) scales[row[it] * lds + c[it] / 32] = bad ? (uint8_t)255 : (uint8_t)(e + 127);
       }
       if (kFake && c[it] < K)
         *reinterpret_cast<uint4*>(xq + row[it] * ldxq + c[it]) = make_uint4(d[0], d[1], d[2], d[3]);

@@ -118,6 +118,30 @@ def can_use_dense_expert(hidden_states, w1, w2, w1_scale, w2_scale, w1_bias, w2_
     return _per_channel(w1_scale, e, 2 * i) and _per_channel(w2_scale, e, h)
 
 
+def merge_repeated_routes(topk_weights: torch.Tensor, topk_ids: torch.Tensor):
+    """The dense-expert branch's coefficient table in route form
+    (`kernels/experimental/moe_dense_expert.py:258-262`): a token's
+    coefficient for an expert is the float32 sum, in route order, of the
+    weights of its routes to that expert. The first of those routes carries
+    the sum (rounded to the routing weights' bf16, the grouped path's
+    coefficient dtype) and the later ones become invalid (id -1), so weights
+    +w and -w on one expert cancel to exactly 0 and the zero-coefficient
+    mask drops the expert even when its output is not finite. Returns
+    (weights, ids) of the same shapes."""
+    ids = topk_ids.to(torch.int32)
+    w = topk_weights.float()
+    k = ids.shape[1]
+    same = ids[:, :, None] == ids[:, None, :]  # [T, k, k]: route i and route j name one expert
+    coeff = torch.zeros_like(w)
+    for j in range(k):  # the reference's accumulation order
+        coeff = coeff + torch.where(same[:, :, j], w[:, j:j + 1], torch.zeros_like(w))
+    earlier = torch.ones((k, k), dtype=torch.bool, device=ids.device).tril(-1)  # [i, j]: j < i
+    repeat = (same & earlier).any(-1)
+    merged_ids = torch.where(repeat, torch.full_like(ids, -1), ids)
+    merged_w = torch.where(repeat, torch.zeros_like(coeff), coeff).to(torch.bfloat16)
+    return merged_w, merged_ids
+
+
 def _dense_expert_admitted(x, w1, w2, w1_scale, w2_scale, w1_bias, w2_bias, activation, fmt) -> bool:
     """``0 < T <= TPU_MOE_DENSE_EXPERT_THRESHOLD`` and the admission rule, the
     token threshold first (`layers/core/fused_moe_gmm.py:669-686`)."""
@@ -172,9 +196,12 @@ def fused_moe_gmm(hidden_states, w1, w2, w1_scale, w2_scale, w1_bias, w2_bias, t
     # expert's output is not finite. Its activation recipe is already this
     # format's (per (row, 512) bf16-arithmetic e4m3 codes), and the grouped
     # path visits each active expert's weights once, as it does; what it
-    # adds is the mask, which is the skipping of zero-weight routes.
+    # adds is the coefficient table (a token's repeated routes to one expert
+    # merged into one coefficient) and the mask, which is the skipping of
+    # zero-coefficient routes.
     if _dense_expert_admitted(hidden_states, w1, w2, w1_scale, w2_scale, w1_bias, w2_bias, activation, fmt):
         skip_padded_tokens = True
+        topk_weights, topk_ids = merge_repeated_routes(topk_weights, topk_ids)
     x = hidden_states if hidden_states.dtype == torch.bfloat16 else hidden_states.to(torch.bfloat16)
     # `fused_moe_gmm.py:653`: routing weights take the hidden dtype
     tw = topk_weights.to(torch.bfloat16)

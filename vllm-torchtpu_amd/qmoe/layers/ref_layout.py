@@ -43,6 +43,14 @@ FP4X2 = getattr(torch, "float4_e2m1fn_x2", None)
 _CACHE = {}
 
 
+def _version_of(t: torch.Tensor):
+    """The in-place version counter of `t`, or None for an inference tensor
+    (created under ``torch.inference_mode()``, as vLLM's forward runs): such
+    tensors keep no counter, so their cache entry is keyed on identity
+    alone."""
+    return None if t.is_inference() else t._version
+
+
 def _cached(t: torch.Tensor, key, make):
     """`make()` once per (weight tensor, key, in-place version)."""
     tid = id(t)
@@ -52,10 +60,11 @@ def _cached(t: torch.Tensor, key, make):
         _CACHE[tid] = ent
     slot = ent[1]
     hit = slot.get(key)
-    if hit is not None and hit[0] == t._version:
+    ver = _version_of(t)
+    if hit is not None and hit[0] == ver:
         return hit[1]
     out = make()
-    slot[key] = (t._version, out)
+    slot[key] = (ver, out)
     return out
 
 

@@ -7,7 +7,6 @@ layouts on the host, and launches the HIP kernels on the current stream via
 
 import ctypes
 import math
-import threading
 
 import torch
 
@@ -59,23 +58,19 @@ def _bytes_view(t):
 
 # ---------------------------------------------------------------- workspace
 
-_ws_lock = threading.Lock()
-_ws = {}
-
 
 def _workspace(dev, nbytes):
-    """Per-device workspace for split-K partial sums, grown on demand. The
-    kernels write every partial before reading it, so it needs no clearing;
-    calls are ordered by the current stream."""
+    """Scratch for one call (split-K partial sums, the fused decode op's
+    dispatch and intermediates), taken from torch's caching allocator on the
+    current stream. The allocator keeps a block on the stream it was made
+    on until the work queued there has used it, and a HIP graph captured
+    around the call owns its block for the graph's lifetime, so concurrent
+    streams never share bytes and a replay never reaches freed memory. The
+    kernels write every byte they read (the decode op clears its own
+    block-maximum table in its first launch), so nothing is cleared here."""
     if nbytes <= 0:
         return None, 0
-    key = (dev.type, dev.index)
-    with _ws_lock:
-        cur = _ws.get(key)
-        if cur is None or cur.numel() < nbytes:
-            cur = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
-            _ws[key] = cur
-    return cur, cur.numel()
+    return torch.empty(nbytes, dtype=torch.uint8, device=dev), nbytes
 
 
 # ---------------------------------------------------------------- row quant
@@ -154,8 +149,8 @@ def mx_quant(x, k_pad=None, codes=True, dequantized=False):
 
 def gemm(kind, a, w, **kw):
     """Run one (grouped) quantized GEMM through `qmoe_gemm` (arguments as
-    `gemm_desc`); the split-K workspace comes from a per-device buffer grown
-    on demand. Returns ``out`` ([M, N or N/2] bf16 unless given)."""
+    `gemm_desc`); the split-K workspace is allocated for the call on the
+    current stream. Returns ``out`` ([M, N or N/2] bf16 unless given)."""
     d, out = gemm_desc(kind, a, w, **kw)
     dev = a.device
     need = ctypes.c_int64(0)
