@@ -57,13 +57,14 @@ def parse():
     ap.add_argument("--only", default="", help="comma list of sweep configs to run (0-4; 5 = NVFP4 / INT4; "
                                                 "v = hipBLASLt reference points)")
     ap.add_argument("--profile", nargs="?", const="headline", default=None,
-                    choices=["headline", "decode", "moe", "vendor", "floor", "w4", "mx"],
+                    choices=["headline", "decode", "moe", "vendor", "floor", "w4", "mx", "midm"],
                     help="rocprofv3 targets: the headline kernel + a copy calibration (default), "
                          "the decode GEMMs (cfg 0/1/2 at M=1), the MoE layers at T=1 (cfg 3/4), "
                          "this build's FP8 GEMM beside hipBLASLt's (torch._scaled_mm) on both cfg 1 "
                          "shapes at M=4096, the plain-read floor (time vs size), the large-M MXFP4 "
                          "path (cfg 0 at M=8192, cfg 3 at T=8192), or the opt-in MX activation path "
-                         "(cfg 0 at M=8192, cfg 3 at T=8192)")
+                         "(cfg 0 at M=8192, cfg 3 at T=8192), or the mid-M linears (cfg 0 M=128, cfg 1 "
+                         "M=64 / 512, cfg 2 M=256)")
     return ap.parse_args()
 
 
@@ -1186,6 +1187,35 @@ def profile_mx(args):
     log("profile target done: copy 256MiB x10")
 
 
+def profile_midm(args):
+    """rocprofv3 target: the mid-M linears, 20 launches each after 3
+    warm-up calls -- cfg 0 MXFP4 at M=128, cfg 1 FP8 W8A8 up / down at M=64
+    and 512 (activation quant included), cfg 2 block FP8 (N 18432) at
+    M=256."""
+    import torch
+
+    from qmoe.layers.linear_common import quantized_matmul, quantized_matmul_fp4
+
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    codes, sc = mxfp4_weights((5760, 2880), gen)
+    x0 = torch.randn((128, 2880), device="cuda", generator=gen).to(torch.bfloat16)
+    calls = [("cfg0 M=128", lambda: quantized_matmul_fp4(x0, codes, sc))]
+    for K, N in ((4096, 14336), (14336, 4096)):
+        w, s = fp8_weights(N, K, gen)
+        for M in (64, 512):
+            x = torch.randn((M, K), device="cuda", generator=gen).to(torch.bfloat16)
+            calls.append((f"cfg1 K={K} M={M}", lambda x=x, w=w, s=s: quantized_matmul(x, w.t(), s)))
+    w2, s2 = fp8_weights(18432, 7168, gen, tiles=True)
+    x2 = torch.randn((256, 7168), device="cuda", generator=gen).to(torch.bfloat16)
+    calls.append(("cfg2 M=256", lambda: quantized_matmul(x2, w2.t(), s2)))
+    for name, fn in calls:
+        for _ in range(23):
+            fn()
+        torch.cuda.synchronize()
+        log(f"profile target: {name} x23")
+    log("profile target done")
+
+
 def profile_floor(args):
     """rocprofv3 target: the plain-read floor curve (qmoe_stream_read over
     FLOOR_MB sizes), printed as one JSON line."""
@@ -1196,7 +1226,7 @@ def main():
     args = parse()
     if args.profile:
         {"headline": profile_target, "decode": profile_decode, "moe": profile_moe, "vendor": profile_vendor,
-         "floor": profile_floor, "w4": profile_w4, "mx": profile_mx}[args.profile](args)
+         "floor": profile_floor, "w4": profile_w4, "mx": profile_mx, "midm": profile_midm}[args.profile](args)
         return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (got --gpus {args.gpus}); "

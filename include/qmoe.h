@@ -54,7 +54,7 @@ enum {
                         nibble: the int32 carriers of `compressed_tensors_moe_w4a16.py`
                         read as bytes) + bf16 scale per wq_group k; each weight is
                         bf16(value * scale), `kernels/megablox/gmm_v2.py:452-462` */
-  QMOE_W4A4_MX = 9   /* A e2m1 codes packed as W (lda in bytes >= K/2) + e8m0 bytes per
+  QMOE_W4A4_MX = 9,  /* A e2m1 codes packed as W (lda in bytes >= K/2) + e8m0 bytes per
                         (row, 32 k) in a_scale [M, lds_a >= K/32] (qmoe_mx_quant); W as
                         QMOE_W4A16_MX. Both scales go to the MFMA. Opt-in MX activations
                         (no counterpart in the reference, whose W4A4 method runs W4A16,
@@ -62,6 +62,18 @@ enum {
                         grouped: fused activation, bias, row maps and routing weight as
                         the other kinds (a_rows also gathers the scale rows); no K split;
                         K % 512 == 0 and K >= 1024 (pad with zero codes) */
+  QMOE_W8A8_PC_DYN = 10 /* A bf16 rows (lda in elements, a multiple of 8), quantized per row
+                        inside the call with the runtime recipe of
+                        `kernels/quantized_matmul/util.py:294-318` (quantize_block: scale =
+                        absmax / qmax, e4m3 in f32 or int8 in bf16 arithmetic per wfmt;
+                        qmoe_row_quant mode 0 computes the same codes); W and w_scale as
+                        QMOE_W8A8_PC; a_scale unused. The whole xla_quantized_matmul of
+                        `:80-124` in one call. Dense only (no group_offs). Decode-size
+                        problems quantize inside the weight-streaming kernel (one launch: each
+                        workgroup reads its rows' absmax from L2 while its first weight loads
+                        are in flight); the rest quantize into the workspace first. The
+                        workspace also holds the row scales, so it is needed whatever the
+                        plan (qmoe_gemm_workspace_size) */
 };
 
 /* Fused gate/up activations (qmoe_gemm_desc.act) */
@@ -84,7 +96,7 @@ enum {
  */
 typedef struct qmoe_gemm_desc {
   int32_t kind;           /* QMOE_W8A8_PC ... */
-  int32_t wfmt;           /* QMOE_W8A8_PC only: 0 e4m3, 1 int8 */
+  int32_t wfmt;           /* QMOE_W8A8_PC, _GMM, _PC_DYN: 0 e4m3, 1 int8 */
   const void* a;          /* activation codes or bf16 */
   int64_t lda;            /* elements (W4A4_MX: bytes of packed codes) */
   const float* a_scale;   /* W8A8: [rows] or [rows, lds_a]; W4A4_MX: e8m0 bytes [rows, lds_a] */
@@ -161,7 +173,11 @@ int qmoe_gemm_workspace_size(const qmoe_gemm_desc* d, int64_t* bytes);
  * from the descriptor alone (no device memory is read): path 0 weight
  * streaming, 1 1-byte x 1-byte tiles, 2 bf16 x 4-bit tiles, 3 generic
  * tiles, 4 weight streaming in 64-row passes, 5 1-byte x 1-byte 256 x 256
- * tiles on persistent workgroups (one per CU of the current device); tile_m = token rows per tile
+ * tiles on persistent workgroups (one per CU of the current device), 6 MX
+ * 256 x 256 persistent tiles, 7 MX grouped tiles, 8 weight streaming with
+ * the per-row activation quantization inside (QMOE_W8A8_PC_DYN; for the
+ * kind's other problems the path of the GEMM after its separate
+ * quantization); tile_m = token rows per tile
  * (or per streaming pass); ksplit = K slices. No counterpart in the
  * reference (its tiling is chosen inside the Pallas call,
  * `kernels/megablox/gmm_v2.py:922-1055`); it lets tests assert which kernel

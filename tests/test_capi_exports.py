@@ -104,3 +104,28 @@ def test_four_bit_descriptors_are_validated_on_the_host():
     assert ws(desc(_capi.W4A16_I4, group=0)) == 1
     assert ws(desc(_capi.W4A16_I4, K=1056, group=64)) == 1   # K not a multiple of the group
     assert ws(desc(_capi.W4A16_I4, group=32, scale_ptr=0x1001)) == 1
+
+
+def test_dynamic_quant_kind_plans_on_the_host():
+    """QMOE_W8A8_PC_DYN (bf16 rows quantized inside the call): one row runs
+    the streaming kernel with the quantization inside; larger problems the
+    plan of the per-channel GEMM after a separate quantization, whose codes
+    and scales the workspace holds; grouped descriptors are refused."""
+    from qmoe import _capi, ops
+
+    for K, N in ((4096, 14336), (14336, 4096)):
+        assert ops.plan_for_shape(_capi.W8A8_PC_DYN, 1, N, K)[4] == "stream_dyn"
+        for M in (8, 64, 4096):
+            assert ops.plan_for_shape(_capi.W8A8_PC_DYN, M, N, K)[4:] == ops.plan_for_shape(_capi.W8A8_PC, M, N, K)[4:]
+    d = _capi.GemmDesc()
+    d.kind, d.a, d.w, d.y, d.w_scale = _capi.W8A8_PC_DYN, 1 << 24, 1 << 24, 1 << 24, 1 << 24
+    d.lda, d.ldw, d.ldy, d.ldws = 4096, 4096, 1024, 1
+    d.M, d.N, d.K, d.slots, d.max_rows = 64, 1024, 4096, 1, 64
+    n = ctypes.c_int64(0)
+    assert _capi.lib.qmoe_gemm_workspace_size(ctypes.byref(d), ctypes.byref(n)) == 0
+    assert n.value >= 64 * 4096 + 64 * 4  # the codes and scales of the separate quantization
+    d.M = d.max_rows = 1
+    assert _capi.lib.qmoe_gemm_workspace_size(ctypes.byref(d), ctypes.byref(n)) == 0
+    assert n.value >= 4  # the row scale
+    d.group_offs, d.slots = 1 << 24, 2
+    assert _capi.lib.qmoe_gemm_workspace_size(ctypes.byref(d), ctypes.byref(n)) == 1

@@ -504,7 +504,7 @@ def _bench_plans():
     for wf in (0, 1):
         for K, N in ((4096, 14336), (14336, 4096)):
             for M in (1, 8, 64, 512, 4096):
-                plans[f"cfg1 wfmt={wf} M={M} K={K}"] = [ops.plan_for_shape(_capi.W8A8_PC, M, N, K, wfmt=wf)]
+                plans[f"cfg1 wfmt={wf} M={M} K={K}"] = [ops.plan_for_shape(_capi.W8A8_PC_DYN, M, N, K, wfmt=wf)]
     for N in (18432, 24576):
         for M in (1, 32, 256, 2048, 8192):
             plans[f"cfg2 M={M} N={N}"] = [ops.plan_for_shape(_capi.W8A8_BLK, M, N, 7168, ws_bn=128)]

@@ -13,6 +13,7 @@ int qmoe_skinny_launch(int kind, GemmParams p, int max_rows, int slots, void* wo
                        int64_t ws_bytes, int ksplit_hint, hipStream_t st);
 int qmoe_skinny_check(int kind, const GemmParams& p);
 int qmoe_skinny_tile_rows(int max_rows);
+bool qmoe_skinny_qa_fits(int64_t M, int64_t K, int ksplit);
 int qmoe_tiled_launch(int kind, GemmParams p, hipStream_t st);
 int qmoe_tiled_check(int kind, const GemmParams& p, int* tile);
 bool qmoe_f8_plan(const GemmParams& p, bool blk, int* bm_out, int* ksplit_out, int64_t* ws_bytes);
@@ -35,8 +36,12 @@ constexpr int kSkinnyMaxRowsBlkWide = 16;
 
 int qmoe_to_params(const qmoe_gemm_desc* d, GemmParams* p) {
   if (!d) return QMOE_ERR_ARG;
-  if (d->kind < QMOE_W8A8_PC || d->kind > QMOE_W4A4_MX) return QMOE_ERR_ARG;
-  if ((d->kind == QMOE_W8A8_PC || d->kind == QMOE_W8A8_GMM) && d->wfmt != 0 && d->wfmt != 1) return QMOE_ERR_ARG;
+  if (d->kind < QMOE_W8A8_PC || d->kind > QMOE_W8A8_PC_DYN) return QMOE_ERR_ARG;
+  if ((d->kind == QMOE_W8A8_PC || d->kind == QMOE_W8A8_GMM || d->kind == QMOE_W8A8_PC_DYN) && d->wfmt != 0 &&
+      d->wfmt != 1)
+    return QMOE_ERR_ARG;
+  // bf16 rows quantized inside: dense problems only
+  if (d->kind == QMOE_W8A8_PC_DYN && (d->group_offs || d->a_rows)) return QMOE_ERR_ARG;
   if (d->act < QMOE_ACT_NONE || d->act > QMOE_ACT_SITU) return QMOE_ERR_ARG;
   if (d->M < 0 || d->N <= 0 || d->K <= 0 || d->slots <= 0) return QMOE_ERR_ARG;
   if (!d->a || !d->w || !d->y) return QMOE_ERR_ARG;
@@ -67,7 +72,7 @@ int qmoe_to_params(const qmoe_gemm_desc* d, GemmParams* p) {
       ((d->wq_group != 32 && d->wq_group != 64 && d->wq_group != 128) || (d->K % d->wq_group) != 0 ||
        d->ldws < d->K / d->wq_group || (reinterpret_cast<uintptr_t>(d->w_scale) & 1)))
     return QMOE_ERR_ARG;
-  const bool abf16 = kind_abf16(d->kind);
+  const bool abf16 = kind_abf16(d->kind) || d->kind == QMOE_W8A8_PC_DYN;
   // packed e2m1 activations: lda counts bytes (two codes each)
   const int abytes = d->kind == QMOE_W4A4_MX ? d->K / 2 : d->K;
   if (d->lda < abytes || ((d->lda * (abf16 ? 2 : 1)) % 16) != 0) return QMOE_ERR_ARG;
@@ -132,8 +137,12 @@ int qmoe_to_params(const qmoe_gemm_desc* d, GemmParams* p) {
 namespace {
 
 // Kernel kind of a descriptor kind: the grouped-matmul recipe runs on the
-// block-scale kernels (its shifts are set in qmoe_to_params)
-int kernel_kind(const qmoe_gemm_desc* d) { return d->kind == QMOE_W8A8_GMM ? QK_W8A8_BLK : d->kind; }
+// block-scale kernels (its shifts are set in qmoe_to_params); bf16 rows
+// quantized inside run on the per-channel kernels
+int kernel_kind(const qmoe_gemm_desc* d) {
+  if (d->kind == QMOE_W8A8_PC_DYN) return QK_W8A8_PC;
+  return d->kind == QMOE_W8A8_GMM ? QK_W8A8_BLK : d->kind;
+}
 
 // Grid depth of the skinny kernel: every group, or -- with an active list --
 // at most one slot per row (a listed group has at least one row).
@@ -201,7 +210,41 @@ enum Path {
   kPathF8Persistent = 5,  // 1-byte x 1-byte 256 x 256 tiles, persistent workgroups
   kPathMx = 6,            // e2m1 x e2m1 with e8m0 scales on both, 256 x 256 persistent tiles
   kPathMxTiles = 7,       // the same operands, grouped tiles (one tile per workgroup)
+  kPathSkinnyDyn = 8,     // weight streaming with the per-row activation quantization inside
 };
+
+int64_t align256(int64_t b) { return (b + 255) / 256 * 256; }
+
+// QMOE_W8A8_PC_DYN: whether the streaming kernel quantizes the activations
+// itself. Each of its workgroups reads every row for the absmax and then
+// its K range again for the codes (two dependent L2 round trips before its
+// first MFMA) instead of a separate quantizer launch; measured on MI355X
+// (Llama-3-8B MLP shapes, FP8 and INT8) that pays for one row (up / down
+// projection 14.4 -> 12.8 us / 18.8 -> 16.5 us) and for two rows without a
+// K split, and loses from four rows on.
+bool dyn_fused(const qmoe_gemm_desc* d, const GemmParams& p, int ksplit) {
+  const char* env = getenv("QMOE_DYN_FUSE_ROWS");  // tuning knob: row limit
+  const int lim = env ? std::min(atoi(env), 32) : (ksplit == 1 ? 2 : 1);
+  return d->M <= lim && d->act == QMOE_ACT_NONE && (d->K % 128) == 0 &&
+         qmoe_skinny_check(QK_W8A8_PC, p) == QMOE_OK;
+}
+
+// The two-step form of a QMOE_W8A8_PC_DYN problem: codes [M][K] and scales
+// [M] at the start of the workspace (qmoe_row_quant mode 0), then the
+// QMOE_W8A8_PC problem over them with the rest of the workspace.
+int64_t dyn_prefix(const qmoe_gemm_desc* d) {
+  return align256((int64_t)d->M * d->K) + align256(4 * (int64_t)std::max(d->M, 1));
+}
+
+qmoe_gemm_desc dyn_inner(const qmoe_gemm_desc* d, uint8_t* ws) {
+  qmoe_gemm_desc e = *d;
+  e.kind = QMOE_W8A8_PC;
+  e.a = ws;
+  e.lda = d->K;
+  e.a_scale = reinterpret_cast<const float*>(ws + align256((int64_t)d->M * d->K));
+  e.lds_a = 1;
+  return e;
+}
 
 // The one place that decides which kernel runs a problem: the streaming
 // kernel within its row limits (unless it declines the operands), else the
@@ -213,6 +256,25 @@ enum Path {
 
 int qmoe_route_of(const qmoe_gemm_desc* d, GemmParams& p, QmoeRoute* r) {
   const int kind = kernel_kind(d);
+  if (d->kind == QMOE_W8A8_PC_DYN) {
+    int ks = 1;
+    int64_t ws = 0;
+    qmoe_skinny_plan(QK_W8A8_PC, d->M, d->N, d->K, d->act, 1, d->M, 0, &ks, &ws);
+    if (dyn_fused(d, p, ks)) {  // one launch; the row scales first in the workspace
+      if (qmoe_skinny_qa_fits(d->M, d->K, ks)) {
+        *r = QmoeRoute{kPathSkinnyDyn, qmoe_skinny_tile_rows(d->M), ks, ws + align256(4 * (int64_t)d->M)};
+        return QMOE_OK;
+      }
+    }
+    // placeholder workspace address (256-aligned, as device allocations
+    // are): the plan reads no memory; the launch plans again with the real one
+    const qmoe_gemm_desc e = dyn_inner(d, reinterpret_cast<uint8_t*>((uintptr_t)1 << 24));
+    GemmParams pe;
+    int st = qmoe_to_params(&e, &pe);
+    if (st == QMOE_OK) st = qmoe_route_of(&e, pe, r);
+    if (st == QMOE_OK) r->ws_bytes += dyn_prefix(d);
+    return st;
+  }
   if (kind == QK_W4A4_MX) {  // the MX kernels take MX activations, nothing else does
     const int bm = qmoe_mx_plan(p);
     if (!bm) return QMOE_ERR_ARG;
@@ -258,6 +320,28 @@ int qmoe_route_of(const qmoe_gemm_desc* d, GemmParams& p, QmoeRoute* r) {
 int qmoe_run_route(const qmoe_gemm_desc* d, const QmoeRoute& r, GemmParams p, void* workspace,
                    int64_t ws_bytes, hipStream_t stream) {
   const int kind = kernel_kind(d);
+  if (d->kind == QMOE_W8A8_PC_DYN) {
+    uint8_t* w8 = static_cast<uint8_t*>(workspace);
+    if (!w8 || ws_bytes < r.ws_bytes) return QMOE_ERR_WORKSPACE;
+    if (r.path == kPathSkinnyDyn) {
+      const int64_t sc = align256(4 * (int64_t)d->M);
+      p.a_quant = 1;
+      p.a_scale = reinterpret_cast<const float*>(w8);
+      p.lds_a = 1;
+      return qmoe_skinny_launch(QK_W8A8_PC, p, d->M, 1, w8 + sc, ws_bytes - sc, 0, stream);
+    }
+    const qmoe_gemm_desc e = dyn_inner(d, w8);
+    int st = qmoe_row_quant(d->a, d->lda, 0, d->M, d->K, d->wfmt, 0, 0, w8, d->K, const_cast<float*>(e.a_scale), 1,
+                            stream);
+    if (st != QMOE_OK) return st;
+    GemmParams pe;
+    QmoeRoute re;
+    st = qmoe_to_params(&e, &pe);
+    if (st == QMOE_OK) st = qmoe_route_of(&e, pe, &re);
+    if (st != QMOE_OK) return st;
+    const int64_t pre = dyn_prefix(d);
+    return qmoe_run_route(&e, re, pe, w8 + pre, ws_bytes - pre, stream);
+  }
   switch (r.path) {
     case kPathSkinny: {
       GemmParams q;
@@ -278,7 +362,7 @@ int qmoe_run_route(const qmoe_gemm_desc* d, const QmoeRoute& r, GemmParams p, vo
   }
 }
 
-extern "C" int qmoe_abi_version(void) { return 7; }
+extern "C" int qmoe_abi_version(void) { return 8; }
 
 extern "C" int qmoe_gemm_workspace_size(const qmoe_gemm_desc* d, int64_t* bytes) {
   GemmParams p;

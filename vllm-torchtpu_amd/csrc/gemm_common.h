@@ -132,6 +132,9 @@ struct GemmParams {
   int32_t N;                  // weight rows (2*I when an activation is fused)
   int32_t K;
   int32_t wfmt;               // QK_W8A8_PC only: 0 e4m3, 1 int8
+  int32_t a_quant;            // QK_W8A8_PC, streaming kernel: A holds bf16 rows that the kernel
+                              // quantizes per row (runtime recipe, wfmt's codes) before the MFMAs;
+                              // a_scale then receives the row scales (for the split-K finish)
   // epilogue
   int32_t act;
   float act_p0, act_p1;

@@ -39,6 +39,7 @@
 #include <type_traits>
 
 #include "gemm_common.h"
+#include "row_quant.h"
 #include "stream_load.h"
 
 namespace {
@@ -52,11 +53,17 @@ using namespace qmoe_stream;
 constexpr int kWeightAux = 0;
 
 constexpr int kWaves = 4;  // wavefronts per workgroup (streaming and split-K finishing kernels)
+// QA: the most dynamic LDS a workgroup's activation codes may take (two
+// workgroups still fit one CU's 160 KB)
+constexpr int64_t kQaMaxLds = 64 << 10;
 constexpr int kThreads = kWaves * 64;
 
-template <int KIND, int WF>
+// QA: the kernel reads bf16 activation rows and quantizes them per row
+// itself (QK_W8A8_PC only); its A fragments then come from the codes it
+// wrote to LDS, not from global memory.
+template <int KIND, int WF, bool QA = false>
 struct Traits {
-  static constexpr bool kAbf16 = kind_abf16(KIND);
+  static constexpr bool kAbf16 = kind_abf16(KIND) || QA;
   static constexpr bool kW4 = kind_w4(KIND);
   static constexpr bool kInt = KIND == QK_W8A8_PC && WF == 1;
   // bytes per lane per 128-k step (32 k values)
@@ -69,7 +76,7 @@ struct Traits {
   //   1-byte A (e4m3/int8) and bf16 A with bf16 W: byte kg*16 + i*64
   //   bf16 A with e4m3 W: byte kg*32 + (i/2)*128 + (i%2)*16
   //   bf16 A with e2m1 W: byte kg*64 + i*16
-  static constexpr bool kW8A16 = KIND == QK_W8A16_PC || KIND == QK_W8A16_BLK;
+  static constexpr bool kW8A16 = KIND == QK_W8A16_PC || KIND == QK_W8A16_BLK || QA;
   static constexpr int kAOffBase = kW4 ? 64 : (kW8A16 ? 32 : 16);
   static __device__ __forceinline__ constexpr int a_off(int i) {
     return kW4 ? i * 16 : (kW8A16 ? (i >> 1) * 128 + (i & 1) * 16 : i * 64);
@@ -261,11 +268,13 @@ __device__ __forceinline__ void mma_step(Acc<KIND, WF, MS, NS>& acc, const Frag 
 }
 
 // Per-format scale + bias for one accumulator element (before activation).
-template <int KIND>
-__device__ __forceinline__ float finish_elem(const GemmParams& p, float acc, int arow, int g, int n) {
+// QA: the activation row's scale is `asc` (computed in the kernel).
+template <int KIND, bool QA = false>
+__device__ __forceinline__ float finish_elem(const GemmParams& p, float acc, int arow, int g, int n,
+                                             float asc = 0.0f) {
   float v = acc;
   if (KIND == QK_W8A8_PC) {
-    v = v * p.a_scale[(int64_t)arow * p.lds_a];
+    v = v * (QA ? asc : p.a_scale[(int64_t)arow * p.lds_a]);
     v = v * group_slice(p, static_cast<const float*>(p.w_scale), p.ws_x, p.ws_gstride, g)[n];
   } else if (KIND == QK_W8A16_PC) {
     v = v * group_slice(p, static_cast<const float*>(p.w_scale), p.ws_x, p.ws_gstride, g)[n];
@@ -274,16 +283,16 @@ __device__ __forceinline__ float finish_elem(const GemmParams& p, float acc, int
   return v;
 }
 
-template <int KIND, bool ACT>
+template <int KIND, bool ACT, bool QA = false>
 __device__ __forceinline__ void store_out(const GemmParams& p, int g, int R, int arow, int ncol_out,
-                                          int n0, int n1, float v0, float v1) {
+                                          int n0, int n1, float v0, float v1, float asc = 0.0f) {
   float out;
   if (ACT) {
-    const float gte = finish_elem<KIND>(p, v0, arow, g, n0);
-    const float up = finish_elem<KIND>(p, v1, arow, g, n1);
+    const float gte = finish_elem<KIND, QA>(p, v0, arow, g, n0, asc);
+    const float up = finish_elem<KIND, QA>(p, v1, arow, g, n1, asc);
     out = qmoe_act(p.act, gte, up, p.act_p0, p.act_p1);
   } else {
-    out = finish_elem<KIND>(p, v0, arow, g, n0);
+    out = finish_elem<KIND, QA>(p, v0, arow, g, n0, asc);
   }
   if (p.row_weight) out *= bf16_to_f32(p.row_weight[R]);
   const int64_t yr = p.y_rows ? p.y_rows[R] : R;
@@ -308,9 +317,10 @@ __device__ __forceinline__ bool slot_group(const GemmParams& p, int slot, int& g
   return rows > 0;
 }
 
-template <int KIND, int WF, int MS, bool ACT, int U, int NS, int W>
+template <int KIND, int WF, int MS, bool ACT, int U, int NS, int W, bool QA = false>
 __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p) {
-  using Tr = Traits<KIND, WF>;
+  using Tr = Traits<KIND, WF, QA>;
+  static_assert(!QA || KIND == QK_W8A8_PC, "in-kernel activation quantization is per-channel W8A8 only");
   constexpr int NT = W * 64;
   const int lane = threadIdx.x & 63;
   // wave-uniform in an SGPR, so K-slice bounds and loop tests are scalar
@@ -419,6 +429,12 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p)
   const rsrc_t xres = make_rsrc(p.a, (int64_t)p.M * lda_b);
   constexpr int NV = MS * NS * 4;
   __shared__ float red[W - 1][NV][64];
+  // QA: the rows' absolute maxima (as integer bits), the row scales, and
+  // the rows' codes over this workgroup's K range (dynamic LDS: rows x
+  // (range bytes + 16), the pad spreading rows over the banks)
+  __shared__ float s_amax[1][QA ? 16 * MS : 1];
+  __shared__ float s_sx[QA ? 16 * MS : 1];
+  extern __shared__ __align__(16) uint8_t s_codes[];
   const int64_t plane = (int64_t)p.M * p.N;
 
   // Rows are taken 16*MS at a time (one pass when the host's row bound
@@ -450,6 +466,8 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p)
     for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
       for (int s = 0; s < NS; ++s) acc.v[ms][s] = {0, 0, 0, 0};
+    // QA: rows of the codes in LDS, their first step and row stride (bytes)
+    int qa_rows = 0, qa_s0 = 0, qa_stride = 0;
 
     auto load_scales = [&](int ks, bool live, StepScales<MS, NS>& sc) {
       if constexpr (KIND == QK_W8A8_BLK) {
@@ -504,8 +522,10 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p)
 #pragma unroll
         for (int s = 0; s < NS; ++s)
           ldw_seg<Tr::kWBytes, kWeightAux>(c.bw[u][s], wres, woff[s] | oob, kk * (4 * Tr::kWBytes));
+        if constexpr (!QA) {
 #pragma unroll
-        for (int ms = 0; ms < MS; ++ms) lda_chunks<Tr>(c.fa[u][ms], xres, aoff[ms] | oob, kk * (4 * Tr::kABytes));
+          for (int ms = 0; ms < MS; ++ms) lda_chunks<Tr>(c.fa[u][ms], xres, aoff[ms] | oob, kk * (4 * Tr::kABytes));
+        }
       }
     };
     auto issue_sc = [&](int j, Chunk& c) {
@@ -521,7 +541,24 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p)
       for (int u = 0; u < U; ++u) {
 #pragma unroll
         for (int s = 0; s < NS; ++s) permute_w<Tr::kWBytes>(c.bw[u][s], perm_src);
-        if (j + u < nj) mma_step<KIND, WF, MS, NS>(acc, c.fa[u], c.bw[u], c.sc[u]);
+        if (j + u < nj) {
+          if constexpr (QA) {
+            // the step's codes of the lane's row: k kg*16 .. +16 and 64 +
+            // kg*16 .. +16 of the step, from LDS (rows past the group: 0)
+            const int off = (sbase + j + u - qa_s0) * 128 + kg * 16;
+#pragma unroll
+            for (int ms = 0; ms < MS; ++ms) {
+              const int r = ms * 16 + col;
+              const bool live = r < qa_rows;
+              const uint8_t* src = s_codes + (live ? r : 0) * qa_stride + off;
+              const uint4 c0 = *reinterpret_cast<const uint4*>(src);
+              const uint4 c1 = *reinterpret_cast<const uint4*>(src + 64);
+              c.fa[u][ms].v[0] = live ? c0 : make_uint4(0, 0, 0, 0);
+              c.fa[u][ms].v[1] = live ? c1 : make_uint4(0, 0, 0, 0);
+            }
+          }
+          mma_step<KIND, WF, MS, NS>(acc, c.fa[u], c.bw[u], c.sc[u]);
+        }
       }
     };
     // Issues are unconditional (clamped step indices): a load issued only on
@@ -532,6 +569,84 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p)
     Chunk ca, cb;
     const bool run = nj > 0;
     if (run) issue_mem(0, ca);
+    if constexpr (QA) {
+      // Phase 1, while the first weight chunk is in flight: each row's
+      // absolute maximum over the whole K. The rows' 16-byte chunks are
+      // dealt to all threads (from L2 after the first workgroup's read),
+      // eight independent loads per batch; each chunk's maximum is folded
+      // into its row's LDS slot by an integer atomic max (|x| bit patterns
+      // order like the values, NaN above inf: NaN-sticky).
+      const int np = min(16 * MS, rows - mp);
+      const int cpr = p.K >> 3;  // 16-byte chunks per row
+      unsigned* s_amax_u = reinterpret_cast<unsigned*>(&s_amax[0][0]);
+      if ((int)threadIdx.x < 16 * MS) s_amax_u[threadIdx.x] = 0u;
+      __syncthreads();
+      {
+        constexpr int kIt = 8;
+        const int items = np * cpr;
+        for (int i0 = (int)threadIdx.x; i0 < items; i0 += NT * kIt) {
+          uint4 v[kIt];
+          int rr[kIt];
+#pragma unroll
+          for (int it = 0; it < kIt; ++it) {
+            const int i = i0 + it * NT;
+            const int r = i / cpr;
+            rr[it] = i < items ? r : -1;
+            const uint32_t o = i < items ? (uint32_t)((row0 + mp + r) * lda_b) + (uint32_t)(i - r * cpr) * 16u : kOob;
+            const auto t = __builtin_amdgcn_raw_buffer_load_b128(xres, o, 0, 0);
+            v[it] = make_uint4(t[0], t[1], t[2], t[3]);
+          }
+#pragma unroll
+          for (int it = 0; it < kIt; ++it)
+            if (rr[it] >= 0) atomicMax(&s_amax_u[rr[it]], __float_as_uint(qmoe_rq::amax8(qmoe_rq::row8_bf16(v[it]))));
+        }
+      }
+      __syncthreads();
+      if ((int)threadIdx.x < 16 * MS) {
+        const float m = (int)threadIdx.x < np ? __uint_as_float(s_amax_u[threadIdx.x]) : 0.0f;
+        s_sx[threadIdx.x] = qmoe_rq::make_scale<WF, 0>(m);
+      }
+      __syncthreads();
+      // the row scales for the split-K finishing kernel's epilogue
+      if (p.a_scale && blockIdx.x == 0 && blockIdx.y == 0 && (int)threadIdx.x < np)
+        const_cast<float*>(p.a_scale)[(int64_t)(row0 + mp + (int)threadIdx.x) * p.lds_a] = s_sx[threadIdx.x];
+      // Phase 2: the codes of this workgroup's K range (the union of its
+      // wavefronts' step runs) into LDS, 16 codes per thread per trip,
+      // with the arithmetic of qmoe_row_quant mode 0 (row_quant.h)
+      const int sl0 = blockIdx.y * W, sl1 = sl0 + W - 1;
+      qa_s0 = sl0 * q + min(sl0, rem);
+      const int qa_s1 = sl1 * q + min(sl1, rem) + q + (sl1 < rem ? 1 : 0);
+      const int nc = (qa_s1 - qa_s0) * 8;  // 16-code chunks per row
+      qa_rows = np;
+      qa_stride = (qa_s1 - qa_s0) * 128 + 16;
+      constexpr int kJt = 4;  // 16-code chunks per batch (eight loads)
+      for (int i0 = (int)threadIdx.x; i0 < np * nc; i0 += NT * kJt) {
+        uint4 v[kJt][2];
+#pragma unroll
+        for (int jt = 0; jt < kJt; ++jt) {
+          const int i = i0 + jt * NT;
+          const int rr = i / nc;
+          const uint32_t o = i < np * nc ? (uint32_t)((row0 + mp + rr) * lda_b) +
+                                               (uint32_t)(qa_s0 * 128 + (i - rr * nc) * 16) * 2u
+                                         : kOob;
+          const auto t0 = __builtin_amdgcn_raw_buffer_load_b128(xres, o, 0, 0);
+          const auto t1 = __builtin_amdgcn_raw_buffer_load_b128(xres, o + 16u, 0, 0);
+          v[jt][0] = make_uint4(t0[0], t0[1], t0[2], t0[3]);
+          v[jt][1] = make_uint4(t1[0], t1[1], t1[2], t1[3]);
+        }
+#pragma unroll
+        for (int jt = 0; jt < kJt; ++jt) {
+          const int i = i0 + jt * NT;
+          if (i >= np * nc) continue;
+          const int rr = i / nc, c16 = i - rr * nc;
+          const float sc = s_sx[rr];
+          const uint2 a0 = qmoe_rq::codes8<WF, 0>(qmoe_rq::row8_bf16(v[jt][0]), sc);
+          const uint2 a1 = qmoe_rq::codes8<WF, 0>(qmoe_rq::row8_bf16(v[jt][1]), sc);
+          *reinterpret_cast<uint4*>(s_codes + rr * qa_stride + c16 * 16) = make_uint4(a0.x, a0.y, a1.x, a1.y);
+        }
+      }
+      __syncthreads();
+    }
     if (run) {
       issue_sc(0, ca);
       for (int j = 0; j < nj; j += 2 * U) {
@@ -547,7 +662,7 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p)
     }
     // K tail (t = K % 128 valid k, a multiple of 32): a chunk whose k values
     // start past K is loaded with kOob (zeros) and fed as zeros
-    if (tail_mine) {
+    if constexpr (!QA) if (tail_mine) {
       const int kk = KSF;
       const int t = p.K - KSF * 128;
       Frag bw[NS];
@@ -655,6 +770,7 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p)
           for (int s = 0; s < NS; ++s) v[s] = (float)acc.v[ms][s][r];
         }
         const int ar = p.a_rows ? p.a_rows[R] : R;
+        const float asc = QA ? s_sx[ms * 16 + kg * 4 + r] : 0.0f;
         if (p.y32) {
           // fused decode epilogue: float32 out times the row coefficient,
           // and the row's absolute maximum over this workgroup's columns
@@ -668,10 +784,10 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p)
             if (!nok[s]) continue;
             float o;
             if constexpr (ACT)
-              o = qmoe_act(p.act, finish_elem<KIND>(p, v[s], ar, g, nw[s]),
-                           finish_elem<KIND>(p, v[s + NH], ar, g, nw[s + NH]), p.act_p0, p.act_p1);
+              o = qmoe_act(p.act, finish_elem<KIND, QA>(p, v[s], ar, g, nw[s], asc),
+                           finish_elem<KIND, QA>(p, v[s + NH], ar, g, nw[s + NH], asc), p.act_p0, p.act_p1);
             else
-              o = finish_elem<KIND>(p, v[s], ar, g, nw[s]);
+              o = finish_elem<KIND, QA>(p, v[s], ar, g, nw[s], asc);
             o = o * coef;
             p.y32[(int64_t)R * p.ldy + nw[s]] = o;
             mx = fmaxf(mx, fabsf(o));
@@ -684,11 +800,11 @@ __global__ __launch_bounds__(W * 64) void skinny_gemm_kernel(const GemmParams p)
         } else if (ACT) {
 #pragma unroll
           for (int s = 0; s < NH; ++s)
-            if (nok[s]) store_out<KIND, true>(p, g, R, ar, nw[s], nw[s], nw[s + NH], v[s], v[s + NH]);
+            if (nok[s]) store_out<KIND, true, QA>(p, g, R, ar, nw[s], nw[s], nw[s + NH], v[s], v[s + NH], asc);
         } else {
 #pragma unroll
           for (int s = 0; s < NS; ++s)
-            if (nok[s]) store_out<KIND, false>(p, g, R, ar, nw[s], nw[s], 0, v[s], 0.0f);
+            if (nok[s]) store_out<KIND, false, QA>(p, g, R, ar, nw[s], nw[s], 0, v[s], 0.0f, asc);
         }
       }
   }
@@ -732,9 +848,9 @@ __global__ __launch_bounds__(kThreads) void skinny_reduce_kernel(const GemmParam
   }
 }
 
-template <int KIND, int WF, int MS, bool ACT, int NS>
-void launch_skinny(const GemmParams& p, dim3 grid, hipStream_t st) {
-  hipLaunchKernelGGL((skinny_gemm_kernel<KIND, WF, MS, ACT, kUnroll, NS, kWaves>), grid, dim3(kWaves * 64), 0,
+template <int KIND, int WF, int MS, bool ACT, int NS, bool QA = false>
+void launch_skinny(const GemmParams& p, dim3 grid, hipStream_t st, unsigned lds = 0) {
+  hipLaunchKernelGGL((skinny_gemm_kernel<KIND, WF, MS, ACT, kUnroll, NS, kWaves, QA>), grid, dim3(kWaves * 64), lds,
                      st, p);
   if (p.ksplit > 1) {
     const int nout = ACT ? p.N / 2 : p.N;
@@ -758,6 +874,14 @@ void launch_ms(const GemmParams& p, int ms, int ns, dim3 grid, hipStream_t st) {
   } else {
     launch_skinny<KIND, WF, 4, ACT, 2>(p, grid, st);
   }
+}
+
+// QA (per-channel W8A8 with the activation quantization inside): no fused
+// activation, 16 or 32 rows per pass (the host's row limit is below that)
+template <int WF>
+void launch_qa(const GemmParams& p, int ms, dim3 grid, hipStream_t st, unsigned lds) {
+  if (ms == 1) launch_skinny<QK_W8A8_PC, WF, 1, false, 2, true>(p, grid, st, lds);
+  else launch_skinny<QK_W8A8_PC, WF, 2, false, 2, true>(p, grid, st, lds);
 }
 
 template <int KIND, int WF>
@@ -839,7 +963,7 @@ int qmoe_skinny_check(int kind, const GemmParams& p) {
   if (p.act != QA_NONE && (p.N % 2) != 0) return QMOE_ERR_ARG;
   if ((kind == QK_W8A8_BLK || kind == QK_W8A16_BLK) && (p.K % 128) != 0) return QMOE_ERR_ARG;
   // 32-bit buffer offsets: every operand stream stays below 2 GiB
-  const bool abf16 = kind_abf16(kind);
+  const bool abf16 = kind_abf16(kind) || p.a_quant;
   constexpr int64_t kLim = 0x7fffffff;
   if ((int64_t)p.N * p.ldw > kLim || p.M * p.lda * (abf16 ? 2 : 1) > kLim) return QMOE_ERR_ARG;
   if (kind == QK_W4A16_MX && (int64_t)p.N * p.ldws > kLim) return QMOE_ERR_ARG;
@@ -855,6 +979,21 @@ int qmoe_skinny_check(int kind, const GemmParams& p) {
     return QMOE_ERR_ARG;
   if (kind == QK_W8A16_BLK && (int64_t)cdiv(p.N, p.ws_bn) * p.ldws * 4 > kLim) return QMOE_ERR_ARG;
   return QMOE_OK;
+}
+
+// QA: dynamic LDS of a workgroup's codes, rows x (its K range + 16 bytes);
+// a workgroup's range is W wavefront runs of at most ceil(steps / slices)
+// 128-k steps each.
+int64_t qmoe_skinny_qa_lds(int64_t M, int64_t K, int ksplit) {
+  const int64_t ks = cdiv<int64_t>(K, 128);
+  const int64_t nsl = (int64_t)std::max(1, ksplit) * kWaves;
+  return M * (kWaves * cdiv<int64_t>(ks, nsl) * 128 + 16);
+}
+
+// Whether the in-kernel activation quantization takes an M x K problem
+// split `ksplit` ways over K (its codes fit the workgroup's LDS).
+bool qmoe_skinny_qa_fits(int64_t M, int64_t K, int ksplit) {
+  return qmoe_skinny_qa_lds(M, K, ksplit) <= kQaMaxLds;
 }
 
 // Token rows one pass of the skinny kernel covers (16, 32 or 64).
@@ -882,8 +1021,16 @@ int qmoe_skinny_launch(int kind, GemmParams p, int max_rows, int slots, void* wo
   dim3 grid(n_tiles, pl.ksplit, slots);
   switch (kind) {
     case QK_W8A8_PC:
-      if (p.wfmt == 0) launch_act<QK_W8A8_PC, 0>(p, ms, ns, grid, st);
-      else launch_act<QK_W8A8_PC, 1>(p, ms, ns, grid, st);
+      if (p.a_quant) {
+        const int64_t lds = qmoe_skinny_qa_lds(p.M, p.K, pl.ksplit);
+        if (p.act != QA_NONE || ms > 2 || (p.K % 128) != 0 || p.group_offs || lds > kQaMaxLds) return QMOE_ERR_ARG;
+        if (p.wfmt == 0) launch_qa<0>(p, ms, grid, st, (unsigned)lds);
+        else launch_qa<1>(p, ms, grid, st, (unsigned)lds);
+      } else if (p.wfmt == 0) {
+        launch_act<QK_W8A8_PC, 0>(p, ms, ns, grid, st);
+      } else {
+        launch_act<QK_W8A8_PC, 1>(p, ms, ns, grid, st);
+      }
       break;
     case QK_W8A8_BLK:
       if (p.wfmt == 0) launch_act<QK_W8A8_BLK, 0>(p, ms, ns, grid, st);

@@ -18,7 +18,7 @@ import torch  # noqa: F401  (its HIP runtime first; see above)
 
 _LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libqmoe.so")
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 QMOE_OK = 0
 STATUS_TEXT = {
@@ -29,7 +29,8 @@ STATUS_TEXT = {
 }
 
 # GEMM kinds / activations (include/qmoe.h)
-W8A8_PC, W8A8_BLK, W8A16_PC, W4A16_MX, W16A16, W4A16_NV, W4A16_I4, W8A8_GMM, W8A16_BLK, W4A4_MX = range(10)
+(W8A8_PC, W8A8_BLK, W8A16_PC, W4A16_MX, W16A16, W4A16_NV, W4A16_I4, W8A8_GMM, W8A16_BLK, W4A4_MX,
+ W8A8_PC_DYN) = range(11)
 ACT_NONE, ACT_SILU, ACT_SWIGLUOAI, ACT_GELU_TANH, ACT_SILU_CLAMP, ACT_SITU = range(6)
 
 _vp = ctypes.c_void_p

@@ -177,13 +177,14 @@ def _quantized_matmul_op(x2: torch.Tensor, w_nk: torch.Tensor, w_s: torch.Tensor
     is_int = w_nk.dtype == torch.int8
     if regime == REGIME_PER_CHANNEL:
         ws = w_s.float().contiguous()
-        if is_int:
-            xq, xs = ops.row_quant(x2, "int8")
-            return ops.gemm(_capi.W8A8_PC, xq.view(torch.uint8), wq, a_scale=xs, w_scale=ws, wfmt=1)
-        if 0 < rows <= w8a16_max_rows:
+        if not is_int and 0 < rows <= w8a16_max_rows:
             return ops.gemm(_capi.W8A16_PC, x2, wq, w_scale=ws)
-        xq, xs = ops.row_quant(x2, "fp8")
-        return ops.gemm(_capi.W8A8_PC, xq.view(torch.uint8), wq, a_scale=xs, w_scale=ws, wfmt=0)
+        # per-token activation quant + W8A8 in one call (decode sizes quantize
+        # inside the streaming kernel; larger ones quantize first)
+        x2 = x2.contiguous()
+        if x2.data_ptr() % 16:
+            x2 = x2.clone()
+        return ops.gemm(_capi.W8A8_PC_DYN, x2, wq, w_scale=ws, wfmt=int(is_int))
     if regime == REGIME_GMM_W8A16:
         return ops.gemm(_capi.W8A16_BLK, x2, wq, w_scale=w_s, ws_bn=1)
     if regime == REGIME_GMM_QUANT_LHS:

@@ -183,7 +183,7 @@ def gemm_desc(kind, a, w, *, a_scale=None, w_scale=None, bias=None, wfmt=0, ws_b
     if a.stride(-1) != 1 or w.stride(-1) != 1 or w.stride(1) < wcols or w.stride(0) < N * w.stride(1):
         raise ValueError("qmoe gemm needs K-contiguous activations and N-major [G, N, K] weights")
     abf16 = kind in (_capi.W8A16_PC, _capi.W4A16_MX, _capi.W16A16, _capi.W4A16_NV, _capi.W4A16_I4,
-                     _capi.W8A16_BLK)
+                     _capi.W8A16_BLK, _capi.W8A8_PC_DYN)
     K = a.shape[1] * (2 if kind == _capi.W4A4_MX else 1)
     if kind == _capi.W4A4_MX and (a.dtype != torch.uint8 or a_scale is None or a_scale.dtype != torch.uint8
                                   or a_scale.dim() != 2 or a_scale.shape[1] * 32 < K):
@@ -215,7 +215,8 @@ def gemm_desc(kind, a, w, *, a_scale=None, w_scale=None, bias=None, wfmt=0, ws_b
     d.w_gstride = w.stride(0) * w.element_size()
     if w_scale is not None:
         ws = w_scale
-        if kind in (_capi.W8A8_PC, _capi.W8A16_PC) or (kind == _capi.W8A8_GMM and ws.numel() == G * N):
+        if kind in (_capi.W8A8_PC, _capi.W8A16_PC, _capi.W8A8_PC_DYN) or (kind == _capi.W8A8_GMM and
+                                                                           ws.numel() == G * N):
             ws = ws.reshape(G, N)
             d.ldws, d.ws_gstride = 1, ws.stride(0)
         else:
@@ -254,7 +255,7 @@ def gemm_desc(kind, a, w, *, a_scale=None, w_scale=None, bias=None, wfmt=0, ws_b
 # ---------------------------------------------------------------- kernel plans
 
 PATH_NAMES = ("stream", "tiled_1b", "tiled_4b", "tiled_generic", "stream_passes", "tiled_1b_persistent",
-              "tiled_mx_persistent", "tiled_mx")
+              "tiled_mx_persistent", "tiled_mx", "stream_dyn")
 
 _plan_log = None
 
