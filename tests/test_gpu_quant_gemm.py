@@ -187,6 +187,44 @@ def test_w8a8_int8_per_channel_bit_exact(dev, M, K, N):
     np.testing.assert_array_equal(y.float().cpu().numpy(), ref)
 
 
+# 128-row weight tiles (dense per-channel problems whose 256-row tiles leave
+# CUs idle): ragged token and channel tiles, the tall-K forms with and
+# without a K split
+SHAPES_NARROW = [(64, 4096, 14336), (100, 4096, 2048), (256, 2048, 1000), (300, 14336, 1024), (700, 8192, 1152)]
+
+
+@pytest.mark.parametrize("M,K,N", SHAPES_NARROW)
+@pytest.mark.parametrize("qdtype", ["fp8", "int8"])
+def test_w8a8_narrow_weight_tiles(dev, M, K, N, qdtype):
+    """The 1-byte tile kernel with 128-row weight tiles against the oracle
+    (FP8 within one bf16 ulp of the same-code oracle, INT8 bit-exact), with
+    a bias on the FP8 runs; the plan reports the narrow tiles."""
+    from qmoe import _capi, ops
+
+    wf = int(qdtype == "int8")
+    plan = ops.plan_for_shape(_capi.W8A8_PC, M, N, K, wfmt=wf)
+    print(f"w8a8 narrow {qdtype} M={M} K={K} N={N} plan={plan}", flush=True)
+    assert plan[4] == "tiled_1b_n128", plan
+    rng = np.random.default_rng(M + 3 * K + N + wf)
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    wq, ws = quant.quantize_tensor(w, qdtype)
+    x = _bf16(rng, (M, K))
+    bias = None if wf else codecs.bf16_round(rng.standard_normal(N).astype(np.float32))
+    ref, _, _ = linear.w8a8_per_channel(x, wq, ws, qdtype)
+    xq, xs = ops.row_quant(_t(x, dev, torch.bfloat16), qdtype)
+    y = ops.gemm(_capi.W8A8_PC, xq.view(torch.uint8), _t(wq.view(np.uint8), dev), a_scale=xs,
+                 w_scale=_t(ws, dev), wfmt=wf, bias=None if bias is None else _t(bias, dev))
+    got = y.float().cpu().numpy()
+    if wf:
+        np.testing.assert_array_equal(got, ref)
+    else:
+        # the bias is added to the f32 result before the bf16 rounding
+        xq_r, xs_r = quant.quantize_act(x, "fp8")
+        dot = np.matmul(codecs.e4m3_decode(xq_r), codecs.e4m3_decode(wq).T).astype(np.float32)
+        full = ((dot * xs_r[:, None]).astype(np.float32) * ws[None, :]).astype(np.float32) + bias[None, :]
+        assert_close_same_codes(got, codecs.bf16_round(full.astype(np.float32)), f"narrow fp8 {M}x{K}x{N}")
+
+
 # more 256 x 256 tiles than CUs: persistent workgroups (ragged last token
 # and channel tiles, the shortest K of the path, a tile count that leaves
 # workgroups with different numbers of tiles)

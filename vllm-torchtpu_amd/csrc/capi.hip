@@ -16,7 +16,7 @@ int qmoe_skinny_tile_rows(int max_rows);
 bool qmoe_skinny_qa_fits(int64_t M, int64_t K, int ksplit);
 int qmoe_tiled_launch(int kind, GemmParams p, hipStream_t st);
 int qmoe_tiled_check(int kind, const GemmParams& p, int* tile);
-bool qmoe_f8_plan(const GemmParams& p, bool blk, int* bm_out, int* ksplit_out, int64_t* ws_bytes);
+bool qmoe_f8_plan(const GemmParams& p, bool blk, int* bm_out, int* ksplit_out, int64_t* ws_bytes, int* bn_out);
 int qmoe_f8_launch(GemmParams p, bool blk, void* workspace, int64_t ws_bytes, hipStream_t st);
 int qmoe_mx_plan(const GemmParams& p);
 int qmoe_mx_launch(GemmParams p, hipStream_t st);
@@ -211,6 +211,7 @@ enum Path {
   kPathMx = 6,            // e2m1 x e2m1 with e8m0 scales on both, 256 x 256 persistent tiles
   kPathMxTiles = 7,       // the same operands, grouped tiles (one tile per workgroup)
   kPathSkinnyDyn = 8,     // weight streaming with the per-row activation quantization inside
+  kPathF8Narrow = 9,      // 1-byte x 1-byte tiles of 128 weight rows
 };
 
 int64_t align256(int64_t b) { return (b + 255) / 256 * 256; }
@@ -294,8 +295,11 @@ int qmoe_route_of(const qmoe_gemm_desc* d, GemmParams& p, QmoeRoute* r) {
   if (!skinny_first) {
     int bm = 0, ks = 1;
     int64_t ws = 0;
-    if (use_f8(d) && qmoe_f8_plan(p, kind == QK_W8A8_BLK, &bm, &ks, &ws)) {
-      *r = QmoeRoute{qmoe_f8_persistent(p, kind == QK_W8A8_BLK) ? kPathF8Persistent : kPathF8, bm, ks, ws};
+    int bn = 256;
+    if (use_f8(d) && qmoe_f8_plan(p, kind == QK_W8A8_BLK, &bm, &ks, &ws, &bn)) {
+      const int path = bn == 128 ? kPathF8Narrow
+                                 : (qmoe_f8_persistent(p, kind == QK_W8A8_BLK) ? kPathF8Persistent : kPathF8);
+      *r = QmoeRoute{path, bm, ks, ws};
       return QMOE_OK;
     }
     if (!use_f8(d) && use_w4(d) && qmoe_w4_plan(p, w4_fmt(d), &bm, &ks, &ws)) {
@@ -349,6 +353,7 @@ int qmoe_run_route(const qmoe_gemm_desc* d, const QmoeRoute& r, GemmParams p, vo
       return qmoe_skinny_launch(kind, q, skinny_rows(d), skinny_slots(d), workspace, ws_bytes, 0, stream);
     }
     case kPathF8:
+    case kPathF8Narrow:
     case kPathF8Persistent: return qmoe_f8_launch(p, kind == QK_W8A8_BLK, workspace, ws_bytes, stream);
     case kPathW4: return qmoe_w4_launch(p, w4_fmt(d), workspace, ws_bytes, stream);
     case kPathTiled: return qmoe_tiled_launch(kind, p, stream);

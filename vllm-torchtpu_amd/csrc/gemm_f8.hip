@@ -993,7 +993,16 @@ void f8_launch_act(const GemmParams& p, hipStream_t st) {
 }
 
 template <bool INT>
-void f8_launch_bm(const GemmParams& p, int bm, hipStream_t st) {
+void f8_launch_bm(const GemmParams& p, int bm, int bn, hipStream_t st) {
+  if (bn == 128 && p.act == QA_NONE) {  // narrow weight tiles (twice the workgroups)
+    switch (bm) {
+      case 256: f8_launch_shape<INT, 256, 128, false, false>(p, st); break;
+      case 128: f8_launch_shape<INT, 128, 128, false, false>(p, st); break;
+      case 64: f8_launch_shape<INT, 64, 128, false, false>(p, st); break;
+      default: f8_launch_shape<INT, 32, 128, false, false>(p, st); break;
+    }
+    return;
+  }
   switch (bm) {
     case 256: f8_launch_act<INT, 256, 256, false>(p, st); break;
     case 128: f8_launch_act<INT, 128, 256, false>(p, st); break;
@@ -1046,7 +1055,7 @@ static int f8_pick_bm_any(const GemmParams& p) {
 // Whether this kernel takes the problem (K % 256, 16-byte alignment,
 // weights < 4 GiB per group), and its plan: token-tile height, K split and
 // the f32 workspace the split needs ([ksplit][M][N]).
-bool qmoe_f8_plan(const GemmParams& p, bool blk, int* bm_out, int* ksplit_out, int64_t* ws_bytes) {
+bool qmoe_f8_plan(const GemmParams& p, bool blk, int* bm_out, int* ksplit_out, int64_t* ws_bytes, int* bn_out) {
   if (p.M <= 0 || p.K <= 0 || (p.K % 256) != 0 || p.N <= 0) return false;
   if (p.act != QA_NONE && (p.N % 2) != 0) return false;
   // block scales: 128-row weight blocks aligned with the tile's halves
@@ -1098,8 +1107,30 @@ bool qmoe_f8_plan(const GemmParams& p, bool blk, int* bm_out, int* ksplit_out, i
     else if (p.M <= 512) { bm = 128; ksplit = 4; }
     else { bm = 128; ksplit = 2; }
   }
+  // Dense per-channel problems (no fused activation) whose 256-row weight
+  // tiles leave CUs idle take 128-row weight tiles (twice the workgroups),
+  // with the token tile and split measured best on MI355X (Llama-3-8B MLP
+  // shapes): K 4096, N 14336: 64 tokens 32 / 1 (14.9 vs 18.5 us), 128
+  // tokens 64 / 1 (17.1 vs 19.1), 256 tokens 128 / 1 (22.9 vs 24.2); K
+  // 14336, N 4096: 512 tokens 128 / 2 (42.2 vs 44.9), 1024 tokens 128 / 1
+  // (59.6 vs 70.0).
+  int bn = 256;
+  if (!blk && !p.group_offs && p.act == QA_NONE && !env_bm) {
+    const int n256 = cdiv(p.N, 256);
+    if (p.K < 8192 && p.M <= 256) {
+      const int b = p.M <= 64 ? 32 : (p.M <= 128 ? 64 : 128);
+      if (cdiv(p.M, b) * n256 < 256) { bm = b; bn = 128; ksplit = 1; }
+    } else if (p.K >= 8192 && p.M > 256 && p.M <= 1024 && cdiv(p.M, 128) * n256 < 256) {
+      bm = 128;
+      bn = 128;
+      ksplit = p.M <= 512 ? 2 : 1;
+    }
+  }
+  const char* env_bn = getenv("QMOE_F8_BN");  // tuning knob: 128 or 256
+  if (env_bn && !blk && p.act == QA_NONE) bn = atoi(env_bn) == 128 ? 128 : 256;
   const char* env = getenv("QMOE_F8_KSPLIT");  // tuning knob
   if (env && atoi(env) > 0) ksplit = std::max(1, std::min(atoi(env), p.K / 256));
+  if (bn_out) *bn_out = bn;
   *bm_out = bm;
   *ksplit_out = ksplit;
   *ws_bytes = ksplit > 1 ? (int64_t)ksplit * p.M * p.N * 4 : 0;
@@ -1108,9 +1139,9 @@ bool qmoe_f8_plan(const GemmParams& p, bool blk, int* bm_out, int* ksplit_out, i
 
 // Whether the planned problem runs the persistent 256 x 256 kernel.
 bool qmoe_f8_persistent(const GemmParams& p, bool blk) {
-  int bm = 0, ksplit = 1;
+  int bm = 0, ksplit = 1, bn = 256;
   int64_t ws = 0;
-  return qmoe_f8_plan(p, blk, &bm, &ksplit, &ws) && f8_persistent_ok(p, blk, bm, ksplit);
+  return qmoe_f8_plan(p, blk, &bm, &ksplit, &ws, &bn) && bn == 256 && f8_persistent_ok(p, blk, bm, ksplit);
 }
 
 // Launch per the plan (the caller checked qmoe_f8_plan and sized the
@@ -1118,7 +1149,8 @@ bool qmoe_f8_persistent(const GemmParams& p, bool blk) {
 int qmoe_f8_launch(GemmParams p, bool blk, void* workspace, int64_t ws_bytes, hipStream_t st) {
   int bm = 0, ksplit = 1;
   int64_t need = 0;
-  if (!qmoe_f8_plan(p, blk, &bm, &ksplit, &need)) return QMOE_ERR_ARG;
+  int bn = 256;
+  if (!qmoe_f8_plan(p, blk, &bm, &ksplit, &need, &bn)) return QMOE_ERR_ARG;
   p.ksplit = ksplit;
   if (ksplit > 1) {
     if (!workspace || ws_bytes < need) return QMOE_ERR_WORKSPACE;
@@ -1126,8 +1158,8 @@ int qmoe_f8_launch(GemmParams p, bool blk, void* workspace, int64_t ws_bytes, hi
   }
   if (blk && f8_wpc(p)) f8_launch_bm_blk<true>(p, bm, st);
   else if (blk) f8_launch_bm_blk<false>(p, bm, st);
-  else if (p.wfmt == 1) f8_launch_bm<true>(p, bm, st);
-  else f8_launch_bm<false>(p, bm, st);
+  else if (p.wfmt == 1) f8_launch_bm<true>(p, bm, bn, st);
+  else f8_launch_bm<false>(p, bm, bn, st);
   if (ksplit > 1) {
     const int nout = p.act != QA_NONE ? p.N / 2 : p.N;
     const dim3 rg((unsigned)cdiv(nout, 512), (unsigned)cdiv(p.M, 4), 1);
