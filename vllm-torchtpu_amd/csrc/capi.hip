@@ -221,11 +221,11 @@ int64_t align256(int64_t b) { return (b + 255) / 256 * 256; }
 // its K range again for the codes (two dependent L2 round trips before its
 // first MFMA) instead of a separate quantizer launch; measured on MI355X
 // (Llama-3-8B MLP shapes, FP8 and INT8) that pays for one row (up / down
-// projection 14.4 -> 12.8 us / 18.8 -> 16.5 us) and for two rows without a
-// K split, and loses from four rows on.
+// projection 14.3 -> 12.8 us / 16.5 -> 15.4 us) and for two rows of K 4096
+// (15.0 -> 14.2 us), and loses for two rows of K 14336 and from four rows.
 bool dyn_fused(const qmoe_gemm_desc* d, const GemmParams& p, int ksplit) {
   const char* env = getenv("QMOE_DYN_FUSE_ROWS");  // tuning knob: row limit
-  const int lim = env ? std::min(atoi(env), 32) : (ksplit == 1 ? 2 : 1);
+  const int lim = env ? std::min(atoi(env), 32) : (ksplit == 1 && d->K < 8192 ? 2 : 1);
   return d->M <= lim && d->act == QMOE_ACT_NONE && (d->K % 128) == 0 &&
          qmoe_skinny_check(QK_W8A8_PC, p) == QMOE_OK;
 }

@@ -868,6 +868,12 @@ void launch_ms(const GemmParams& p, int ms, int ns, dim3 grid, hipStream_t st) {
         return;
       }
     }
+    if constexpr (!ACT) {
+      if (ns == 1) {
+        launch_skinny<KIND, WF, 1, false, 1>(p, grid, st);
+        return;
+      }
+    }
     launch_skinny<KIND, WF, 1, ACT, 2>(p, grid, st);
   } else if (ms == 2) {
     launch_skinny<KIND, WF, 2, ACT, 2>(p, grid, st);
@@ -879,8 +885,9 @@ void launch_ms(const GemmParams& p, int ms, int ns, dim3 grid, hipStream_t st) {
 // QA (per-channel W8A8 with the activation quantization inside): no fused
 // activation, 16 or 32 rows per pass (the host's row limit is below that)
 template <int WF>
-void launch_qa(const GemmParams& p, int ms, dim3 grid, hipStream_t st, unsigned lds) {
-  if (ms == 1) launch_skinny<QK_W8A8_PC, WF, 1, false, 2, true>(p, grid, st, lds);
+void launch_qa(const GemmParams& p, int ms, int ns, dim3 grid, hipStream_t st, unsigned lds) {
+  if (ms == 1 && ns == 1) launch_skinny<QK_W8A8_PC, WF, 1, false, 1, true>(p, grid, st, lds);
+  else if (ms == 1) launch_skinny<QK_W8A8_PC, WF, 1, false, 2, true>(p, grid, st, lds);
   else launch_skinny<QK_W8A8_PC, WF, 2, false, 2, true>(p, grid, st, lds);
 }
 
@@ -901,10 +908,12 @@ int skinny_ms(int rows) {
 // 16-row weight tiles per workgroup: 2 (measured on MI355X: 4 tiles for
 // e2m1 weights gain a few percent on grouped decode and lose a third on
 // dense decode, where the workgroup count halves)
-int skinny_ns(int kind, int ms) {
+int skinny_ns(int kind, int ms, int act) {
+  const char* env = getenv("QMOE_SKINNY_NS");  // tuning knob: 1 (no fused activation), 2 or 4 (e2m1)
+  const int v = env ? atoi(env) : 2;
+  if (ms == 1 && act == QA_NONE && v == 1) return 1;
   if (kind != QK_W4A16_MX || ms != 1) return 2;
-  const char* env = getenv("QMOE_SKINNY_NS");  // tuning knob: 2 or 4
-  return env && atoi(env) == 4 ? 4 : 2;
+  return v == 4 ? 4 : 2;
 }
 
 int skinny_tiles(int64_t N, int act, int ns) {
@@ -918,6 +927,7 @@ namespace {
 struct SkinnyPlan {
   int ksplit;  // K slices over grid.y
   int64_t ws_bytes;
+  int ns;      // 16-row weight tiles per workgroup
 };
 
 int env_int(const char* name, int dflt) {
@@ -931,18 +941,34 @@ int env_int(const char* name, int dflt) {
 // workgroups (one per 32 weight rows), which costs a second launch and the
 // [ksplit][M][N] float32 partial sums in the workspace; every wavefront keeps
 // at least two 128-k steps.
+//
+// Weight tiles per workgroup: two 16-row tiles, or one for dense 1-byte
+// weights without a fused activation when there is a single row or when
+// two-tile workgroups would split K (measured on MI355X: the FP8 down
+// projection K 14336, N 4096 at 1 / 8 / 16 rows 13.0 / 14.8 / 16.7 -> 11.0 /
+// 12.3 / 12.6 us with one tile, which needs no split and so no second
+// launch; 128x128 block FP8 N 18432 at one row 25.2 -> 23.5 us; e2m1
+// weights are slower with one tile).
 SkinnyPlan skinny_plan(int kind, int64_t M, int64_t N, int64_t K, int act, int slots, int rows,
                        int ksplit_hint) {
   const int ms = skinny_ms(rows);
-  const int n_wg = skinny_tiles(N, act, skinny_ns(kind, ms)) * std::max(slots, 1);
   const int KS = (int)cdiv<int64_t>(K, 128);
   // tuning knobs (read per call): forced K split, workgroup count the split
   // planner aims for
   const int w = kWaves;
-  int ksplit = ksplit_hint > 0 ? ksplit_hint : env_int("QMOE_SKINNY_KSPLIT", 0);
-  if (ksplit <= 0) ksplit = (int)cdiv<int64_t>(env_int("QMOE_SKINNY_TARGET_WG", 160), n_wg);
-  ksplit = std::max(1, std::min(ksplit, std::max(1, KS / (2 * w))));
-  return SkinnyPlan{ksplit, ksplit <= 1 ? 0 : (int64_t)ksplit * M * N * 4};
+  const int target = env_int("QMOE_SKINNY_TARGET_WG", 160);
+  const int ks_env = ksplit_hint > 0 ? ksplit_hint : env_int("QMOE_SKINNY_KSPLIT", 0);
+  auto split_for = [&](int ns) {
+    int ks = ks_env > 0 ? ks_env : (int)cdiv<int64_t>(target, skinny_tiles(N, act, ns) * std::max(slots, 1));
+    return std::max(1, std::min(ks, std::max(1, KS / (2 * w))));
+  };
+  int ns = skinny_ns(kind, ms, act);
+  const bool one_byte_w = kind == QK_W8A8_PC || kind == QK_W8A8_BLK;
+  if (!getenv("QMOE_SKINNY_NS") && one_byte_w && ms == 1 && act == QA_NONE && slots == 1 && ns == 2 &&
+      (M == 1 || split_for(2) > 1))
+    ns = 1;
+  const int ksplit = split_for(ns);
+  return SkinnyPlan{ksplit, ksplit <= 1 ? 0 : (int64_t)ksplit * M * N * 4, ns};
 }
 
 }  // namespace
@@ -1010,9 +1036,9 @@ int qmoe_skinny_launch(int kind, GemmParams p, int max_rows, int slots, void* wo
   const int chk = qmoe_skinny_check(kind, p);
   if (chk != QMOE_OK) return chk;
   const int ms = skinny_ms(max_rows);
-  const int ns = skinny_ns(kind, ms);
-  const int n_tiles = skinny_tiles(p.N, p.act, ns);
   const SkinnyPlan pl = skinny_plan(kind, p.M, p.N, p.K, p.act, slots, max_rows, ksplit_hint);
+  const int ns = pl.ns;
+  const int n_tiles = skinny_tiles(p.N, p.act, ns);
   p.ksplit = pl.ksplit;
   if (pl.ksplit > 1) {
     if (!workspace || ws_bytes < pl.ws_bytes) return QMOE_ERR_WORKSPACE;
@@ -1024,8 +1050,8 @@ int qmoe_skinny_launch(int kind, GemmParams p, int max_rows, int slots, void* wo
       if (p.a_quant) {
         const int64_t lds = qmoe_skinny_qa_lds(p.M, p.K, pl.ksplit);
         if (p.act != QA_NONE || ms > 2 || (p.K % 128) != 0 || p.group_offs || lds > kQaMaxLds) return QMOE_ERR_ARG;
-        if (p.wfmt == 0) launch_qa<0>(p, ms, grid, st, (unsigned)lds);
-        else launch_qa<1>(p, ms, grid, st, (unsigned)lds);
+        if (p.wfmt == 0) launch_qa<0>(p, ms, ns, grid, st, (unsigned)lds);
+        else launch_qa<1>(p, ms, ns, grid, st, (unsigned)lds);
       } else if (p.wfmt == 0) {
         launch_act<QK_W8A8_PC, 0>(p, ms, ns, grid, st);
       } else {
