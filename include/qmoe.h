@@ -29,7 +29,8 @@ typedef struct ihipStream_t* qmoe_stream_t; /* == hipStream_t */
 
 /* GEMM kinds (qmoe_gemm_desc.kind) */
 enum {
-  QMOE_W8A8_PC = 0,  /* A e4m3|int8 + per-row f32 scale; W same dtype + per-channel f32 scale */
+  QMOE_W8A8_PC = 0,  /* A e4m3|int8|e5m2 (wfmt) + per-row f32 scale; W same dtype + per-channel
+                        f32 scale */
   QMOE_W8A8_BLK = 1, /* A e4m3 + per-(row,128) scale; W e4m3 + per-(n/bn, 128) scale */
   QMOE_W8A16_PC = 2, /* A bf16; W e4m3 + per-channel scale */
   QMOE_W4A16_MX = 3, /* A bf16; W e2m1 + e8m0 scale per 32 k */
@@ -38,8 +39,9 @@ enum {
                         block scale times its f32 global scale, rounded to bf16 as the
                         reference's `kernels/megablox/gmm_v2.py:452-462` dequantization
                         does; each weight is bf16(code * scale)) */
-  QMOE_W8A8_GMM = 7, /* A e4m3|int8 (wfmt) codes + f32 scale per (row, 512 columns, the last
-                        block partial) from qmoe_row_quant mode 2; W same dtype + per-channel f32
+  QMOE_W8A8_GMM = 7, /* A e4m3|int8 codes + f32 scale per (row, 512 columns, the last
+                        block partial) from qmoe_row_quant mode 2; W e4m3|int8|e5m2 (wfmt; A is
+                        int8 for int8 W, e4m3 for float W) + per-channel f32
                         scale [G][N] (ldws <= 1) or one per (row, B columns) [G][N][K/B] with
                         ldws = K/B, B a power-of-two multiple of 512. The quantized-lhs regime
                         of the reference's grouped
@@ -65,7 +67,7 @@ enum {
   QMOE_W8A8_PC_DYN = 10 /* A bf16 rows (lda in elements, a multiple of 8), quantized per row
                         inside the call with the runtime recipe of
                         `kernels/quantized_matmul/util.py:294-318` (quantize_block: scale =
-                        absmax / qmax, e4m3 in f32 or int8 in bf16 arithmetic per wfmt;
+                        absmax / qmax, e4m3 / e5m2 in f32 or int8 in bf16 arithmetic per wfmt;
                         qmoe_row_quant mode 0 computes the same codes); W and w_scale as
                         QMOE_W8A8_PC; a_scale unused. The whole xla_quantized_matmul of
                         `:80-124` in one call. Dense only (no group_offs). Decode-size
@@ -96,7 +98,7 @@ enum {
  */
 typedef struct qmoe_gemm_desc {
   int32_t kind;           /* QMOE_W8A8_PC ... */
-  int32_t wfmt;           /* QMOE_W8A8_PC, _GMM, _PC_DYN: 0 e4m3, 1 int8 */
+  int32_t wfmt;           /* QMOE_W8A8_PC, _GMM, _PC_DYN: 0 e4m3, 1 int8, 2 e5m2; other kinds 0 */
   const void* a;          /* activation codes or bf16 */
   int64_t lda;            /* elements (W4A4_MX: bytes of packed codes) */
   const float* a_scale;   /* W8A8: [rows] or [rows, lds_a]; W4A4_MX: e8m0 bytes [rows, lds_a] */
@@ -134,7 +136,8 @@ int qmoe_abi_version(void);
 /*
  * Row quantizer: rows of x (bf16, or f32 when in_f32) -> 1-byte codes q and
  * f32 scales (one per row, or per (row, 128 columns) when block == 128).
- *   qdtype 0 e4m3fn, 1 int8.
+ *   qdtype 0 e4m3fn, 1 int8, 2 e5m2 (per-row scales only; not mode 2, whose codes are
+ *   e4m3 for any float weight: `kernels/megablox/gmm_v2.py:1198-1218`).
  *   mode 0: runtime activation quant, replaces the reference's
  *           `kernels/quantized_matmul/util.py:47-64` quantize_tensor /
  *           `:294-318` quantize_block (fp8 in f32, int8 in bf16 arithmetic);

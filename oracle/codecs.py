@@ -1,7 +1,8 @@
-"""Bit-level codecs: bf16 rounding, OCP e4m3fn, e2m1 (fp4), e8m0.
+"""Bit-level codecs: bf16 rounding, OCP e4m3fn and e5m2, e2m1 (fp4), e8m0.
 
 Written from the format definitions (OCP 8-bit floating point spec v1.0 for
-E4M3 "fn"; OCP MX spec v1.0 for E2M1 and E8M0). Test infrastructure only.
+E4M3 "fn" and E5M2; OCP MX spec v1.0 for E2M1 and E8M0). Test
+infrastructure only.
 """
 
 import numpy as np
@@ -90,6 +91,58 @@ def e4m3_encode(x) -> np.ndarray:
     mant = np.rint(v / np.exp2((ev - 3).astype(np.float64))).astype(np.int64) - 8
     code = np.where(norm, ((ev + 7) << 3) | mant, code)
     code = np.where(np.isnan(x) | (v > E4M3_MAX), E4M3_NAN, code)
+    return (code | sign).astype(np.uint8)
+
+
+# ---------------------------------------------------------------- e5m2
+
+E5M2_MAX = 57344.0
+E5M2_INF = 0x7C
+E5M2_NAN = 0x7F
+
+
+def _e5m2_values(c) -> np.ndarray:
+    """Layout S.EEEEE.MM, bias 15, IEEE-like: E == 31 is inf (M == 0) or NaN."""
+    c = np.asarray(c, dtype=np.int64)
+    s = np.where((c >> 7) & 1, -1.0, 1.0)
+    e = (c >> 2) & 0x1F
+    m = c & 0x3
+    with np.errstate(over="ignore"):
+        val = np.where(e == 0, m * 2.0 ** -16, (1.0 + m / 4.0) * np.exp2(e - 15.0))
+    val = np.where(e == 0x1F, np.where(m == 0, np.inf, np.nan), val)
+    return (s * val).astype(np.float32)
+
+
+_E5M2_TABLE = _e5m2_values(np.arange(256))
+
+
+def e5m2_decode(codes) -> np.ndarray:
+    """uint8 e5m2 codes -> float32 values (exact)."""
+    return _E5M2_TABLE[np.asarray(codes, dtype=np.uint8)]
+
+
+def e5m2_encode(x) -> np.ndarray:
+    """float32 -> uint8 e5m2 codes, round-to-nearest-even; magnitudes that
+    round above 57344 become inf, NaN becomes 0x7F with its sign (torch's
+    float8_e5m2 cast). The reference clips to +-57344 first."""
+    x = np.asarray(x, dtype=np.float32)
+    a = np.abs(x).astype(np.float64)
+    sign = np.signbit(x).astype(np.int64) << 7
+    _, ex = np.frexp(a)
+    e = np.maximum(ex.astype(np.int64) - 1, -14)  # subnormal binade: quantum 2**-16
+    q = np.exp2((e - 2).astype(np.float64))
+    v = np.rint(a / q) * q  # RNE, exact
+    code = np.zeros(a.shape, dtype=np.int64)
+    nz = v > 0
+    _, ev = np.frexp(np.where(nz, v, 1.0))
+    ev = ev.astype(np.int64) - 1
+    sub = nz & (ev < -14)
+    code = np.where(sub, np.rint(v / 2.0 ** -16).astype(np.int64), code)
+    norm = nz & ~sub
+    mant = np.rint(v / np.exp2((ev - 2).astype(np.float64))).astype(np.int64) - 4
+    code = np.where(norm, ((ev + 15) << 2) | mant, code)
+    code = np.where(v > E5M2_MAX, E5M2_INF, code)
+    code = np.where(np.isnan(x), E5M2_NAN, code)
     return (code | sign).astype(np.uint8)
 
 

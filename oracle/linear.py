@@ -31,8 +31,8 @@ def w8a8_per_channel(x, wq, ws, qdtype):
     if qdtype == "int8":
         acc = np.matmul(xq.astype(np.float64), np.asarray(wq, np.int8).astype(np.float64).T)
         out = acc.astype(np.float32)
-    else:
-        out = _mm(e4m3_decode(xq), e4m3_decode(wq))
+    else:  # e4m3 or e5m2 on both operands (the activation takes the weight's dtype)
+        out = _mm(dequant_codes(xq, qdtype), dequant_codes(wq, qdtype))
     out = (out * sx[:, None]).astype(np.float32)
     out = (out * np.asarray(ws, np.float32)[None, :]).astype(np.float32)
     return bf16_round(out), xq, sx
@@ -117,18 +117,18 @@ def w16a16(x, w, bias=None):
     return bf16_round(out)
 
 
-def _block_dots(xq, wq, qdtype, block):
+def _block_dots(xq, wq, qdtype, block, wdtype=None):
     """Per-512-block dot products of codes: [blocks, M, N] float64 (exact:
-    int8 products summed in float64 are exact integers, e4m3 products have
-    8-bit significands)."""
+    int8 products summed in float64 are exact integers, e4m3 / e5m2
+    products have at most 8-bit significands)."""
     xv = dequant_codes(xq, qdtype).astype(np.float64)
-    wv = dequant_codes(wq, qdtype).astype(np.float64)
+    wv = dequant_codes(wq, wdtype or qdtype).astype(np.float64)
     k = xv.shape[1]
     nb = (k + block - 1) // block
     return np.stack([xv[:, b * block:(b + 1) * block] @ wv[:, b * block:(b + 1) * block].T for b in range(nb)])
 
 
-def w8a8_gmm(x, wq, ws, qdtype, bias=None, round_out=True):
+def w8a8_gmm(x, wq, ws, qdtype, bias=None, round_out=True, wdtype=None):
     """The grouped matmul's quantized-lhs regime with per-channel weights
     (``ws`` [N]) or per-(row, B columns) weights (``ws`` [N, K/B], B a
     multiple of 512; `kernels/megablox/gmm_v2.py:500-548`), accumulated in
@@ -139,10 +139,14 @@ def w8a8_gmm(x, wq, ws, qdtype, bias=None, round_out=True):
     codes, so only the summation differs); `w8a8_gmm_bf16acc` is the
     reference's own bf16 accumulation.
 
+    ``qdtype`` is the activation codes' dtype ("fp8" for any float weight,
+    e5m2 included: `gmm_v2.py:1198-1218`; "int8" for int8 weights) and
+    ``wdtype`` the weight codes' (default the same).
+
     Returns (y [M, N] bf16-valued f32, or f32 sums with round_out=False; xq; xs).
     """
     xq, xs = quantize_gmm_lhs(x, qdtype)
-    dots = _block_dots(xq, wq, qdtype, GMM_LHS_BLOCK)
+    dots = _block_dots(xq, wq, qdtype, GMM_LHS_BLOCK, wdtype)
     ws = np.asarray(ws, np.float32)
     acc = np.zeros(dots.shape[1:], np.float32)
     if ws.ndim == 2:  # per (row, B columns): each 512-column block meets the weight block it lies in

@@ -5,7 +5,7 @@ Test infrastructure only.
 
 import numpy as np
 
-from oracle.codecs import bf16_round, dequant_int4, dequant_mxfp4, dequant_nvfp4, e4m3_decode
+from oracle.codecs import bf16_round, dequant_int4, dequant_mxfp4, dequant_nvfp4, e4m3_decode, e5m2_decode
 from oracle.linear import _mm, w8a8_gmm, w8a8_gmm_bf16acc
 from oracle.quant import quantize_act, quantize_mx_fp4
 
@@ -131,6 +131,8 @@ class ExpertWeights:
                 d = dequant_int4(w, s)
             elif self.fmt in ("fp8_block", "fp8", "fp8_bf16acc", "fp8_w8a16", "fp8_rowquant"):
                 d = e4m3_decode(w)
+            elif self.fmt == "e5m2":
+                d = e5m2_decode(w)
             elif self.fmt in ("int8", "int8_rowquant"):
                 d = np.asarray(w, np.int8).astype(np.float32)
             else:
@@ -141,9 +143,10 @@ class ExpertWeights:
     def linear(self, which, e, x):
         """x bf16-valued [R, K] -> f32 [R, N] for expert e."""
         s = None if self.fmt == "bf16" else (self.s13[e] if which == 13 else self.s2[e])
-        if self.fmt in ("fp8", "int8"):
+        if self.fmt in ("fp8", "int8", "e5m2"):
             w = self.w13[e] if which == 13 else self.w2[e]
-            out, _, _ = w8a8_gmm(x, w, s, self.fmt, round_out=False)
+            qd = "fp8" if self.fmt == "e5m2" else self.fmt  # float weights meet e4m3 activations
+            out, _, _ = w8a8_gmm(x, w, s, qd, round_out=False, wdtype=self.fmt)
         elif self.fmt == "fp8_bf16acc":
             w = self.w13[e] if which == 13 else self.w2[e]
             out = w8a8_gmm_bf16acc(x, w, s, "fp8")

@@ -19,9 +19,10 @@ Test infrastructure only.
 
 import numpy as np
 
-from oracle.codecs import bf16_round, e4m3_decode, e4m3_encode
+from oracle.codecs import bf16_round, e4m3_decode, e4m3_encode, e5m2_decode, e5m2_encode
 
 FP8_MAX = np.float32(448.0)
+E5M2_MAX = np.float32(57344.0)
 
 
 def _absmax(x, axis):
@@ -63,15 +64,26 @@ def quantize_block_int8(x, axis=-1):
     return q, scale
 
 
+def quantize_block_e5m2(x, axis=-1):
+    """`util.py:303-318` with a float8_e5m2 target: as the e4m3 form (the
+    finfo maximum is a NumPy float32 scalar, so float32 arithmetic) with
+    qmax = 57344, the e5m2 maximum."""
+    x = np.asarray(x, dtype=np.float32)
+    scale = (_absmax(x, axis) / E5M2_MAX).astype(np.float32)
+    scale = np.where(scale == 0, np.float32(1.0), scale).astype(np.float32)
+    q = np.clip((x / scale).astype(np.float32), -E5M2_MAX, E5M2_MAX)
+    return e5m2_encode(q), scale
+
+
 def quantize_act(x, qdtype, block=None):
     """Per-token (``block=None``) or per-(token, block) activation quant.
 
-    ``qdtype`` is "fp8" or "int8". Returns codes [M, K] and scales [M] or
-    [M, K/block] (float32).
+    ``qdtype`` is "fp8", "e5m2" or "int8". Returns codes [M, K] and scales
+    [M] or [M, K/block] (float32).
     """
     x = np.asarray(x, dtype=np.float32)
     m, k = x.shape
-    fn = quantize_block_fp8 if qdtype == "fp8" else quantize_block_int8
+    fn = {"fp8": quantize_block_fp8, "e5m2": quantize_block_e5m2, "int8": quantize_block_int8}[qdtype]
     if block is None:
         q, s = fn(x, axis=-1)
         return q, s[:, 0]
@@ -126,13 +138,16 @@ def quantize_gmm_lhs(x, qdtype, block=GMM_LHS_BLOCK):
 def dequant_codes(q, qdtype) -> np.ndarray:
     if qdtype == "fp8":
         return e4m3_decode(q)
+    if qdtype == "e5m2":
+        return e5m2_decode(q)
     return np.asarray(q, dtype=np.int8).astype(np.float32)
 
 
 def quantize_tensor(w, qdtype, block=None):
     """Load-time quantizer, `layers/core/quantization.py:232-318` (no ue8m0).
 
-    Quantizes along the last axis; ``block=None`` means the whole axis.
+    ``qdtype``: "fp8" (e4m3fn), "e5m2" or "int8" (qmax the dtype's finfo /
+    iinfo maximum). Quantizes along the last axis; ``block=None`` means the whole axis.
     Returns (codes, scale) with scale shaped [..., K/block] (squeezed to [...]
     for the whole-axis case, as the reference's ``squeeze(-1)`` does).
     """
@@ -141,8 +156,8 @@ def quantize_tensor(w, qdtype, block=None):
     block = block or k
     if k % block:
         raise ValueError("Quantization expects the requested axis to be divisible by block_size")
-    qmax = 448.0 if qdtype == "fp8" else 127.0
-    qmin = -448.0 if qdtype == "fp8" else -128.0
+    qmax = {"fp8": 448.0, "e5m2": 57344.0, "int8": 127.0}[qdtype]
+    qmin = -128.0 if qdtype == "int8" else -qmax
     blocked = w.reshape(*w.shape[:-1], k // block, block)
     recip = np.float32(1.0 / qmax)
     scale = (_absmax(blocked, -1) * recip).astype(np.float32)
@@ -151,6 +166,8 @@ def quantize_tensor(w, qdtype, block=None):
     q = np.clip((blocked * inv).astype(np.float32), qmin, qmax)
     if qdtype == "fp8":
         codes = e4m3_encode(q)
+    elif qdtype == "e5m2":
+        codes = e5m2_encode(q)
     else:
         codes = np.where(np.isnan(q), 0, np.rint(q)).astype(np.int8)
     codes = codes.reshape(w.shape)

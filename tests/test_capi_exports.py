@@ -129,3 +129,26 @@ def test_dynamic_quant_kind_plans_on_the_host():
     assert n.value >= 4  # the row scale
     d.group_offs, d.slots = 1 << 24, 2
     assert _capi.lib.qmoe_gemm_workspace_size(ctypes.byref(d), ctypes.byref(n)) == 1
+
+
+def test_weight_code_formats_are_validated_on_the_host():
+    """wfmt 0 e4m3, 1 int8, 2 e5m2 for the per-channel, grouped-matmul and
+    in-call-quantization W8A8 kinds; any other value, and a nonzero wfmt on
+    the other kinds, is refused before a launch. e5m2 plans the same kernels
+    as e4m3 (the 1-byte tiles and the streaming kernel take both formats)."""
+    from qmoe import _capi, ops
+
+    for kind in (_capi.W8A8_PC, _capi.W8A8_GMM, _capi.W8A8_PC_DYN):
+        for M in (1, 64, 4096):
+            e4 = ops.plan_for_shape(kind, M, 4096, 4096, wfmt=0)
+            assert ops.plan_for_shape(kind, M, 4096, 4096, wfmt=2)[2:] == e4[2:]
+    d = _capi.GemmDesc()
+    d.kind, d.a, d.w, d.y, d.w_scale, d.a_scale = _capi.W8A8_PC, 1 << 24, 1 << 24, 1 << 24, 1 << 24, 1 << 24
+    d.lda, d.ldw, d.ldy, d.ldws, d.lds_a = 4096, 4096, 1024, 1, 1
+    d.M, d.N, d.K, d.slots, d.max_rows = 64, 1024, 4096, 1, 64
+    n = ctypes.c_int64(0)
+    for wfmt, rc in ((0, 0), (1, 0), (2, 0), (3, 1), (-1, 1)):
+        d.wfmt = wfmt
+        assert _capi.lib.qmoe_gemm_workspace_size(ctypes.byref(d), ctypes.byref(n)) == rc, wfmt
+    d.kind, d.wfmt = _capi.W8A16_PC, 2
+    assert _capi.lib.qmoe_gemm_workspace_size(ctypes.byref(d), ctypes.byref(n)) == 1

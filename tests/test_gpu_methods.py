@@ -32,15 +32,17 @@ def _linear_layer(method, n, k, ckpt_codes, ckpt_scale_inv, dev):
     return layer
 
 
-@pytest.mark.parametrize("mode", ["per_channel", "block128", "block512", "block512_int8", "native_tiles", "int8"])
+@pytest.mark.parametrize("mode", ["per_channel", "block128", "block512", "block512_int8", "native_tiles", "int8",
+                                  "e5m2", "block512_e5m2"])
 @pytest.mark.parametrize("M", [6, 300])
 def test_fp8_linear_from_block_checkpoint(dev, monkeypatch, mode, M):
     """Checkpoint 128x128 FP8 -> the reference's runtime form for each env
     setting (`fp8.py:216-348`): per-channel requant (default), per (row, B)
     requant with ENABLE_QUANTIZED_MATMUL_KERNEL=1 REQUANTIZE_BLOCK_SIZE=B (a
     [1, K/B, 1, N] scale; B = 128 runs bf16-dequantized weights, B = 512 the
-    per-(token, 512) quantized activations), int8; native tiles only with
-    QMOE_FP8_NATIVE_BLOCKS=1."""
+    per-(token, 512) quantized activations), int8 and float8_e5m2 codes (per
+    channel: e5m2 activations; B = 512: e4m3 activations); native tiles only
+    with QMOE_FP8_NATIVE_BLOCKS=1."""
     from qmoe.layers import quantization as q
 
     print(f"fp8 linear method {mode} M={M}", flush=True)
@@ -57,6 +59,8 @@ def test_fp8_linear_from_block_checkpoint(dev, monkeypatch, mode, M):
         monkeypatch.setenv("QMOE_FP8_NATIVE_BLOCKS", "1")
     if mode in ("int8", "block512_int8"):
         monkeypatch.setenv("REQUANTIZE_WEIGHT_DTYPE", "int8")
+    if mode in ("e5m2", "block512_e5m2"):
+        monkeypatch.setenv("REQUANTIZE_WEIGHT_DTYPE", "float8_e5m2")
     rng = np.random.default_rng(3)
     N, K = 384, 1024
     w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
@@ -73,16 +77,17 @@ def test_fp8_linear_from_block_checkpoint(dev, monkeypatch, mode, M):
     elif mode.startswith("block"):
         B = 128 if mode == "block128" else 512
         qd = "int8" if mode.endswith("int8") else "fp8"
-        wq, wsb = quant.quantize_tensor(w_deq, qd, block=B)
+        wd = "e5m2" if mode.endswith("e5m2") else qd
+        wq, wsb = quant.quantize_tensor(w_deq, wd, block=B)
         assert tuple(layer.weight_scale.shape) == (1, K // B, 1, N)  # `fp8.py:270-294`
         np.testing.assert_array_equal(layer.weight.view(torch.uint8).cpu().numpy(), wq.view(np.uint8))
         np.testing.assert_array_equal(layer.weight_scale[0, :, 0, :].t().cpu().numpy(), wsb)
         if B == 128:
             ref = linear.w8a16_blockwise(x, wq, wsb)
         else:
-            ref, _, _ = linear.w8a8_gmm(x, wq, wsb, qd)
+            ref, _, _ = linear.w8a8_gmm(x, wq, wsb, qd, wdtype=wd)
     else:
-        qd = "int8" if mode == "int8" else "fp8"
+        qd = {"int8": "int8", "e5m2": "e5m2"}.get(mode, "fp8")
         wq, ws = quant.quantize_tensor(w_deq, qd)  # `fp8.py:297-348`: dequant -> requant per channel
         np.testing.assert_array_equal(layer.weight.view(torch.uint8).cpu().numpy(), wq.view(np.uint8))
         np.testing.assert_array_equal(layer.weight_scale.cpu().numpy(), ws)
@@ -177,11 +182,14 @@ def test_fp8_moe_block_checkpoint_sigmoid_grouped(dev, monkeypatch, native):
                                                            ("float8_e4m3fn", 512, 512, None, False),
                                                            ("float8_e4m3fn", None, 192, None, False),
                                                            ("float8_e4m3fn", None, 256, 200, False),
-                                                           ("float8_e4m3fn", None, 128, None, True)])
+                                                           ("float8_e4m3fn", None, 128, None, True),
+                                                           ("float8_e5m2", None, 256, None, False),
+                                                           ("float8_e5m2", 512, 512, None, False)])
 def test_fp8_moe_requant_switches(dev, monkeypatch, dtype, block, I, unpadded, dense):
     """MOE_REQUANTIZE_WEIGHT_DTYPE / MOE_REQUANTIZE_BLOCK_SIZE (`fp8.py:185-213`):
     int8 per channel (int8 activations per (token, 512)), fp8 per (row, 128)
-    (bf16-dequantized weights) and per (row, 512); an intermediate size that
+    (bf16-dequantized weights) and per (row, 512), e5m2 per channel and per
+    (row, 512) (e4m3 activations per (token, 512)); an intermediate size that
     is not a multiple of 128 is zero-padded to one, and the padding of an
     unpadded intermediate size is zeroed (`fp8.py:351-406, 515-522`). With
     ``dense``, a 16-token step under TPU_MOE_DENSE_EXPERT_THRESHOLD: the
@@ -223,14 +231,14 @@ def test_fp8_moe_requant_switches(dev, monkeypatch, dtype, block, I, unpadded, d
     p13[:, :real], p13[:, Ip:Ip + real] = d13[:, :real], d13[:, I:I + real]
     p2 = np.zeros((E, H, Ip), np.float32)
     p2[:, :, :real] = d2[:, :, :real]
-    qd = "int8" if dtype == "int8" else "fp8"
+    qd = {"int8": "int8", "float8_e5m2": "e5m2"}.get(dtype, "fp8")
     r13 = [quant.quantize_tensor(p13[e], qd, block=block) for e in range(E)]
     r2 = [quant.quantize_tensor(p2[e], qd, block=block) for e in range(E)]
     w13q, w13s = np.stack([a for a, _ in r13]), np.stack([b for _, b in r13])
     w2q, w2s = np.stack([a for a, _ in r2]), np.stack([b for _, b in r2])
     np.testing.assert_array_equal(layer.w13_weight.data.view(torch.uint8).cpu().numpy(), w13q.view(np.uint8))
     np.testing.assert_array_equal(layer.w2_weight_scale.cpu().numpy().reshape(w2s.shape), w2s)
-    fmt = {None: qd, 128: "fp8_w8a16", 512: "fp8"}[block]
+    fmt = "fp8_w8a16" if block == 128 else qd
     assert layer._qmoe_format == fmt
     x = codecs.bf16_round(rng.standard_normal((T, H)).astype(np.float32))
     logits = codecs.bf16_round(rng.standard_normal((T, E)).astype(np.float32))

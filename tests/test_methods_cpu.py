@@ -36,6 +36,31 @@ def test_unsupported_requant_dtype(monkeypatch):
         q.Fp8LinearMethod(q.Fp8Config())
 
 
+def test_e5m2_requant_dtype(monkeypatch):
+    """float8_e5m2 is a requantization target of both env gates
+    (`fp8.py:122-127`); the 128-column block regime stays e4m3-only."""
+    from qmoe.layers.fused_moe import infer_weight_format
+    from qmoe.layers.quantization import fp8
+
+    for v in ("ENABLE_QUANTIZED_MATMUL_KERNEL", "REQUANTIZE_BLOCK_SIZE", "MOE_REQUANTIZE_BLOCK_SIZE"):
+        monkeypatch.delenv(v, raising=False)
+    monkeypatch.setenv("REQUANTIZE_WEIGHT_DTYPE", "float8_e5m2")
+    monkeypatch.setenv("MOE_REQUANTIZE_WEIGHT_DTYPE", "float8_e5m2")
+    assert fp8.get_linear_quant_config()[:3] == ("float8_e5m2", torch.float8_e5m2, None)
+    assert fp8.get_moe_quant_config() == ("float8_e5m2", torch.float8_e5m2, None)
+    monkeypatch.setenv("ENABLE_QUANTIZED_MATMUL_KERNEL", "1")
+    monkeypatch.setenv("REQUANTIZE_BLOCK_SIZE", "512")
+    assert fp8.get_linear_quant_config()[2] == 512
+    monkeypatch.setenv("REQUANTIZE_BLOCK_SIZE", "128")
+    with pytest.raises(NotImplementedError, match="float8_e4m3fn"):
+        fp8.get_linear_quant_config()
+    monkeypatch.setenv("MOE_REQUANTIZE_BLOCK_SIZE", "128")
+    with pytest.raises(NotImplementedError, match="float8_e4m3fn"):
+        fp8.get_moe_quant_config()
+    w = torch.zeros((2, 4, 8), dtype=torch.float8_e5m2)
+    assert infer_weight_format(w, torch.ones((2, 4))) == "e5m2"
+
+
 def test_negative_w8a16_rows_rejected(monkeypatch):
     monkeypatch.setenv("TPU_FP8_LINEAR_W8A16_MAX_ROWS", "-1")
     with pytest.raises(ValueError):

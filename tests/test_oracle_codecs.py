@@ -200,3 +200,30 @@ def test_int4_dequant_rounds_the_bf16_product():
     assert one(1, 1.005859375) == np.float32(1.0078125)
     assert one(-8, 0.5) == np.float32(-4.0)
     assert one(0, 3.0) == np.float32(0.0)
+
+
+def test_e5m2_decode_every_code_matches_torch():
+    codes = np.arange(256, dtype=np.uint8)
+    ref = torch.from_numpy(codes).view(torch.float8_e5m2).float().numpy()
+    got = codecs.e5m2_decode(codes)
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(ref))
+    ok = ~np.isnan(ref)
+    np.testing.assert_array_equal(got[ok], ref[ok])
+    assert (np.signbit(got[ok]) == np.signbit(ref[ok])).all()
+
+
+def test_e5m2_encode_matches_torch_cast():
+    """RNE over random magnitudes across the whole range, the subnormals,
+    every halfway point between adjacent codes, the overflow edge (61440
+    rounds to inf), signed zeros, inf and NaN: the codes torch's
+    float8_e5m2 cast gives."""
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal(100000) * np.exp2(rng.integers(-20, 17, 100000))).astype(np.float32)
+    vals = codecs.e5m2_decode(np.arange(256, dtype=np.uint8)).astype(np.float64)
+    fin = np.sort(vals[np.isfinite(vals) & (vals >= 0)])
+    mids = ((fin[1:] + fin[:-1]) / 2).astype(np.float32)
+    edge = np.float32([57344.0, 61439.996, 61440.0, 65536.0, 2.0 ** -17, 3 * 2.0 ** -18, 0.0, -0.0,
+                       np.inf, -np.inf, np.nan, -np.nan])
+    x = np.concatenate([x, mids, -mids, np.nextafter(mids, np.float32(0)), np.nextafter(mids, np.float32(1e9)), edge])
+    ref = torch.from_numpy(x).to(torch.float8_e5m2).view(torch.uint8).numpy()
+    np.testing.assert_array_equal(codecs.e5m2_encode(x), ref)

@@ -222,3 +222,27 @@ def test_mx_quant_non_finite_blocks_are_nan_blocks():
         d = codecs.dequant_mxfp4(q, s)
     assert np.isnan(d[0, 32:64]).all() and np.isnan(d[1, 96:]).all()
     assert np.isfinite(d[0, :32]).all() and np.isfinite(d[1, :96]).all()
+
+
+def test_e5m2_quantizers():
+    """float8_e5m2 targets: the load-time quantizer's codes are torch's
+    e5m2 cast of the clipped reciprocal-scaled values (scale = amax *
+    f32(1/57344)); the runtime quantizer divides by amax / 57344 in f32;
+    both read back within the e5m2 quantum (2 mantissa bits: 12.5 % of the
+    binade)."""
+    rng = np.random.default_rng(9)
+    w = (rng.standard_normal((6, 256)) * 0.02).astype(np.float32)
+    q, s = quant.quantize_tensor(w, "e5m2")
+    scale = (np.abs(w).max(axis=-1) * np.float32(1.0 / 57344.0)).astype(np.float32)
+    np.testing.assert_array_equal(s, scale)
+    t = np.clip(w * (np.float32(1.0) / scale)[:, None], -57344, 57344).astype(np.float32)
+    np.testing.assert_array_equal(q, torch.from_numpy(t).to(torch.float8_e5m2).view(torch.uint8).numpy())
+    back = codecs.e5m2_decode(q) * s[:, None]
+    assert np.all(np.abs(back - w) <= 0.125 * np.abs(w) + 1e-30 + 2.0 ** -16 * s[:, None])
+    x = codecs.bf16_round(rng.standard_normal((3, 128)).astype(np.float32))
+    xq, xs = quant.quantize_act(x, "e5m2")
+    sx = (np.abs(x).max(axis=-1) / np.float32(57344.0)).astype(np.float32)
+    np.testing.assert_array_equal(xs, sx)
+    ref = torch.from_numpy(np.clip(x / sx[:, None], -57344, 57344).astype(np.float32)).to(torch.float8_e5m2)
+    np.testing.assert_array_equal(xq, ref.view(torch.uint8).numpy())
+    assert codecs.e5m2_decode(xq).max() == 57344.0  # the row maximum maps to the e5m2 maximum

@@ -45,7 +45,7 @@ def _static_gemm(lib, xq, xs, wq, ws, activation=None):
 
 @pytest.mark.parametrize("shapes,act", [
     # streaming kernel with a K split (decode rows, tall K), then fewer rows
-    (((4, 14336, 4096), (2, 14336, 4096)), None),
+    (((4, 14336, 1024), (2, 14336, 1024)), None),
     # 1-byte tiled kernel with a 4-way K split, then a smaller M
     (((96, 14336, 1024), (40, 14336, 1024)), None),
     # tiled split-K finishing kernel with a fused activation, then smaller
@@ -75,9 +75,9 @@ def test_gemm_static_refuses_oversized_partials(dev):
     lib = _lib()
     cap = lib.qmoe_gemm_static_scratch_bytes()
     assert cap == 64 << 20
-    # 512 tokens, K 14336, N 12288: tiled 128-token tiles with a 4-way split,
-    # 4 * 512 * 12288 * 4 bytes = 96 MiB of partials
-    M, K, N = 512, 14336, 12288
+    # 256 tokens, K 14336, N 24576: 1-byte tiles with a 4-way split,
+    # 4 * 256 * 24576 * 4 bytes = 96 MiB of partials
+    M, K, N = 256, 14336, 24576
     plan = ops.plan_for_shape(_capi.W8A8_PC, M, N, K)
     assert plan[6] * M * N * 4 > cap, plan
     a = torch.zeros((M, K), dtype=torch.uint8, device=dev)

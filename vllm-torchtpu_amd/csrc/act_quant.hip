@@ -305,8 +305,9 @@ extern "C" int qmoe_row_quant(const void* x, int64_t ldx, int in_f32, int64_t M,
                               int qdtype, int mode, int block, void* q, int64_t ldq,
                               float* scales, int64_t lds, hipStream_t stream) {
   if (M < 0 || K <= 0 || (K % 8) != 0) return QMOE_ERR_ARG;
-  if (qdtype != 0 && qdtype != 1) return QMOE_ERR_ARG;
+  if (qdtype < 0 || qdtype > 2) return QMOE_ERR_ARG;
   if (mode == 2) {  // grouped-GEMM activation quant: bf16 rows, 512-column blocks
+    if (qdtype == 2) return QMOE_ERR_ARG;  // float weights meet e4m3 activations there
     if (block != 512 || in_f32 || lds < cdiv<int64_t>(K, 512)) return QMOE_ERR_ARG;
     if (M == 0) return QMOE_OK;
     const dim3 grid((unsigned)M, (unsigned)cdiv<int64_t>(K, 512 * (kThreads / 64)));
@@ -326,7 +327,12 @@ extern "C" int qmoe_row_quant(const void* x, int64_t ldx, int in_f32, int64_t M,
   uint8_t* qq = static_cast<uint8_t*>(q);
   const bool blk = block == 128;
 #define QMOE_RQ(QD, MD, F32, BLK) launch_rq<QD, MD, F32, BLK>(x, ldx, M, K, qq, ldq, scales, lds, stream)
-  if (mode == 0) {
+  if (qdtype == 2) {  // e5m2: per-row scales (runtime, or load time from f32 / bf16)
+    if (blk) return QMOE_ERR_ARG;
+    if (mode == 0) QMOE_RQ(2, 0, false, false);
+    else if (in_f32) QMOE_RQ(2, 1, true, false);
+    else QMOE_RQ(2, 1, false, false);
+  } else if (mode == 0) {
     if (qdtype == 0) { if (blk) QMOE_RQ(0, 0, false, true); else QMOE_RQ(0, 0, false, false); }
     else { if (blk) QMOE_RQ(1, 0, false, true); else QMOE_RQ(1, 0, false, false); }
   } else if (in_f32) {

@@ -37,9 +37,13 @@ constexpr int kSkinnyMaxRowsBlkWide = 16;
 int qmoe_to_params(const qmoe_gemm_desc* d, GemmParams* p) {
   if (!d) return QMOE_ERR_ARG;
   if (d->kind < QMOE_W8A8_PC || d->kind > QMOE_W8A8_PC_DYN) return QMOE_ERR_ARG;
-  if ((d->kind == QMOE_W8A8_PC || d->kind == QMOE_W8A8_GMM || d->kind == QMOE_W8A8_PC_DYN) && d->wfmt != 0 &&
-      d->wfmt != 1)
+  // weight codes: 0 e4m3, 1 int8, 2 e5m2 (the per-channel and grouped-matmul
+  // W8A8 kinds); the other kinds name their formats themselves
+  if (d->kind == QMOE_W8A8_PC || d->kind == QMOE_W8A8_GMM || d->kind == QMOE_W8A8_PC_DYN) {
+    if (d->wfmt < 0 || d->wfmt > 2) return QMOE_ERR_ARG;
+  } else if (d->wfmt != 0) {
     return QMOE_ERR_ARG;
+  }
   // bf16 rows quantized inside: dense problems only
   if (d->kind == QMOE_W8A8_PC_DYN && (d->group_offs || d->a_rows)) return QMOE_ERR_ARG;
   if (d->act < QMOE_ACT_NONE || d->act > QMOE_ACT_SITU) return QMOE_ERR_ARG;
@@ -196,7 +200,7 @@ bool use_w4(const qmoe_gemm_desc* d) {
 
 bool use_f8(const qmoe_gemm_desc* d) {
   if (getenv("QMOE_F8_OFF")) return false;  // tuning knob: generic kernel only
-  const bool blk = d->kind == QMOE_W8A8_BLK || (d->kind == QMOE_W8A8_GMM && d->wfmt == 0);
+  const bool blk = d->kind == QMOE_W8A8_BLK || (d->kind == QMOE_W8A8_GMM && d->wfmt != 1);
   return d->kind == QMOE_W8A8_PC || (blk && !getenv("QMOE_F8_BLK_OFF"));
 }
 

@@ -97,8 +97,12 @@ __device__ __forceinline__ i32x8 fp4_op(const i32x4& v) {
   return __builtin_shufflevector(v, v, 0, 1, 2, 3, -1, -1, -1, -1);
 }
 
-template <bool INT, int BM, int BN, bool ACT, int KB, bool BLK, bool WPC = false, bool MX = false>
+// E5: e5m2 operands (bit 0 the weights, bit 1 the activations; the others
+// e4m3): the MFMA's operand format codes
+template <bool INT, int BM, int BN, bool ACT, int KB, bool BLK, bool WPC = false, bool MX = false, int E5 = 0>
 __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, int m_tiles, int n_tiles) {
+  static_assert(E5 == 0 || (!INT && !MX), "e5m2 operands: float codes only");
+  constexpr int kFw = E5 & 1, kFx = (E5 >> 1) & 1;  // weight (A) / activation (B) format codes
   static_assert(KB == 64 || KB == 128, "K bytes per LDS stage");
   // MX (QK_W4A4_MX): e2m1 codes of both operands in the 128-byte stages (256
   // k), their e8m0 bytes ([row][8] per stage) copied beside them; the MFMA
@@ -429,7 +433,7 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
         for (int q = 0; q <= NI * MJ; ++q) {
           if (q < NI * MJ) {
             const int i = q / MJ, j = q % MJ;
-            tmp[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[1][i], xf[1][j], tmp[i][j], 0, 0, 0,
+            tmp[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[1][i], xf[1][j], tmp[i][j], kFw, kFx, 0,
                                                                         127, 0, 127);
           }
           if (q > 0) {
@@ -446,10 +450,10 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
 #pragma unroll
       for (int j = 0; j < MJ; ++j) {
         if constexpr (BLK) {
-          tmp[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[t][i], xf[t][j], f32x16{}, 0, 0, 0, 127,
-                                                                      0, 127);
+          tmp[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[t][i], xf[t][j], f32x16{}, kFw, kFx, 0,
+                                                                      127, 0, 127);
         } else {
-          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[t][i], xf[t][j], acc[i][j], 0, 0, 0,
+          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[t][i], xf[t][j], acc[i][j], kFw, kFx, 0,
                                                                       127, 0, 127);
         }
       }
@@ -952,7 +956,7 @@ int f8_persistent_grid(int tiles) {
 // row-major output with N % 8 == 0 and 16-byte aligned rows below 2 GiB, no
 // bias, row gather / scatter or routing weights, and more tiles than CUs.
 bool f8_persistent_ok(const GemmParams& p, bool blk, int bm, int ksplit) {
-  if (blk || bm != 256 || ksplit != 1 || p.group_offs || p.act != QA_NONE || p.K < 512) return false;
+  if (blk || bm != 256 || ksplit != 1 || p.group_offs || p.act != QA_NONE || p.K < 512 || p.wfmt > 1) return false;
   const char* env = getenv("QMOE_F8_KB");
   if (env && atoi(env) == 64) return false;
   if ((p.N % 8) != 0 || (p.ldy % 8) != 0 || (reinterpret_cast<uintptr_t>(p.y) & 15) != 0) return false;
@@ -960,12 +964,12 @@ bool f8_persistent_ok(const GemmParams& p, bool blk, int bm, int ksplit) {
   return f8_persistent_grid(cdiv(p.M, 256) * cdiv(p.N, 256)) > 0;
 }
 
-template <bool INT, int BM, int BN, bool ACT, bool BLK, bool WPC = false>
+template <bool INT, int BM, int BN, bool ACT, bool BLK, bool WPC = false, int E5 = 0>
 void f8_launch_shape(const GemmParams& p, hipStream_t st) {
   const char* env = getenv("QMOE_F8_KB");  // tuning knob: K bytes per LDS stage
   const int kb = BLK ? 128 : (env ? atoi(env) : 128);
-  auto kern = kb == 64 ? f8_gemm_kernel<INT, BM, BN, ACT, BLK ? 128 : 64, BLK, WPC>
-                       : f8_gemm_kernel<INT, BM, BN, ACT, 128, BLK, WPC>;
+  auto kern = kb == 64 ? f8_gemm_kernel<INT, BM, BN, ACT, BLK ? 128 : 64, BLK, WPC, false, E5>
+                       : f8_gemm_kernel<INT, BM, BN, ACT, 128, BLK, WPC, false, E5>;
   const int nout = ACT ? p.N / 2 : p.N;
   const int n_tiles = cdiv(nout, ACT ? BN / 2 : BN);
   const unsigned ks = (unsigned)std::max(1, p.ksplit);
@@ -975,7 +979,7 @@ void f8_launch_shape(const GemmParams& p, hipStream_t st) {
   } else {
     const int m_tiles = cdiv(p.M, BM);
     const int grid = cdiv(m_tiles * n_tiles, kXcds) * kXcds;
-    if constexpr (BM == 256 && BN == 256 && !BLK && !ACT) {
+    if constexpr (BM == 256 && BN == 256 && !BLK && !ACT && E5 == 0) {
       if (kb == 128 && f8_persistent_ok(p, BLK, BM, (int)ks)) {
         hipLaunchKernelGGL((f8_persistent_kernel<INT ? 1 : 0>), dim3(f8_persistent_grid(m_tiles * n_tiles)),
                            dim3(kThreads), 0, st, p, m_tiles, n_tiles, grid);
@@ -986,39 +990,39 @@ void f8_launch_shape(const GemmParams& p, hipStream_t st) {
   }
 }
 
-template <bool INT, int BM, int BN, bool BLK, bool WPC = false>
+template <bool INT, int BM, int BN, bool BLK, bool WPC = false, int E5 = 0>
 void f8_launch_act(const GemmParams& p, hipStream_t st) {
-  if (p.act != QA_NONE) f8_launch_shape<INT, BM, BN, true, BLK, WPC>(p, st);
-  else f8_launch_shape<INT, BM, BN, false, BLK, WPC>(p, st);
+  if (p.act != QA_NONE) f8_launch_shape<INT, BM, BN, true, BLK, WPC, E5>(p, st);
+  else f8_launch_shape<INT, BM, BN, false, BLK, WPC, E5>(p, st);
 }
 
-template <bool INT>
+template <bool INT, int E5 = 0>
 void f8_launch_bm(const GemmParams& p, int bm, int bn, hipStream_t st) {
   if (bn == 128 && p.act == QA_NONE) {  // narrow weight tiles (twice the workgroups)
     switch (bm) {
-      case 256: f8_launch_shape<INT, 256, 128, false, false>(p, st); break;
-      case 128: f8_launch_shape<INT, 128, 128, false, false>(p, st); break;
-      case 64: f8_launch_shape<INT, 64, 128, false, false>(p, st); break;
-      default: f8_launch_shape<INT, 32, 128, false, false>(p, st); break;
+      case 256: f8_launch_shape<INT, 256, 128, false, false, false, E5>(p, st); break;
+      case 128: f8_launch_shape<INT, 128, 128, false, false, false, E5>(p, st); break;
+      case 64: f8_launch_shape<INT, 64, 128, false, false, false, E5>(p, st); break;
+      default: f8_launch_shape<INT, 32, 128, false, false, false, E5>(p, st); break;
     }
     return;
   }
   switch (bm) {
-    case 256: f8_launch_act<INT, 256, 256, false>(p, st); break;
-    case 128: f8_launch_act<INT, 128, 256, false>(p, st); break;
-    case 64: f8_launch_act<INT, 64, 256, false>(p, st); break;
-    default: f8_launch_act<INT, 32, 256, false>(p, st); break;
+    case 256: f8_launch_act<INT, 256, 256, false, false, E5>(p, st); break;
+    case 128: f8_launch_act<INT, 128, 256, false, false, E5>(p, st); break;
+    case 64: f8_launch_act<INT, 64, 256, false, false, E5>(p, st); break;
+    default: f8_launch_act<INT, 32, 256, false, false, E5>(p, st); break;
   }
 }
 
 // block-scaled FP8: tiles of at most 128 tokens (the per-block sums need a
-// second accumulator set)
-template <bool WPC>
+// second accumulator set); E5 1: e5m2 weights against e4m3 activations
+template <bool WPC, int E5 = 0>
 void f8_launch_bm_blk(const GemmParams& p, int bm, hipStream_t st) {
   switch (bm) {
-    case 128: f8_launch_act<false, 128, 256, true, WPC>(p, st); break;
-    case 64: f8_launch_act<false, 64, 256, true, WPC>(p, st); break;
-    default: f8_launch_act<false, 32, 256, true, WPC>(p, st); break;
+    case 128: f8_launch_act<false, 128, 256, true, WPC, E5>(p, st); break;
+    case 64: f8_launch_act<false, 64, 256, true, WPC, E5>(p, st); break;
+    default: f8_launch_act<false, 32, 256, true, WPC, E5>(p, st); break;
   }
 }
 
@@ -1061,7 +1065,9 @@ bool qmoe_f8_plan(const GemmParams& p, bool blk, int* bm_out, int* ksplit_out, i
   // block scales: 128-row weight blocks aligned with the tile's halves
   // (per-channel weight scales need no alignment); 1-byte FP8 codes only
   if (blk && !f8_wpc(p) && (p.ws_bn != 128 || (p.act != QA_NONE && ((p.N / 2) % 128) != 0))) return false;
-  if (blk && p.wfmt != 0) return false;
+  // block scales take float codes: e4m3, or e5m2 weights (the grouped-matmul
+  // recipe; its activations stay e4m3)
+  if (blk && p.wfmt == 1) return false;
   if ((p.lda % 16) != 0 || (p.ldw % 16) != 0) return false;
   if ((reinterpret_cast<uintptr_t>(p.a) & 15) || (reinterpret_cast<uintptr_t>(p.w) & 15) ||
       (p.w_gstride % 16) != 0)
@@ -1156,9 +1162,14 @@ int qmoe_f8_launch(GemmParams p, bool blk, void* workspace, int64_t ws_bytes, hi
     if (!workspace || ws_bytes < need) return QMOE_ERR_WORKSPACE;
     p.partial = static_cast<float*>(workspace);
   }
-  if (blk && f8_wpc(p)) f8_launch_bm_blk<true>(p, bm, st);
+  // e5m2 weights (wfmt 2): against e5m2 activations for per-channel W8A8,
+  // e4m3 ones for the grouped-matmul recipe (per-channel weight scales)
+  if (blk && f8_wpc(p) && p.wfmt == 2) f8_launch_bm_blk<true, 1>(p, bm, st);
+  else if (blk && f8_wpc(p)) f8_launch_bm_blk<true>(p, bm, st);
+  else if (blk && p.wfmt == 2) f8_launch_bm_blk<false, 1>(p, bm, st);
   else if (blk) f8_launch_bm_blk<false>(p, bm, st);
   else if (p.wfmt == 1) f8_launch_bm<true>(p, bm, bn, st);
+  else if (p.wfmt == 2) f8_launch_bm<false, 3>(p, bm, bn, st);
   else f8_launch_bm<false>(p, bm, bn, st);
   if (ksplit > 1) {
     const int nout = p.act != QA_NONE ? p.N / 2 : p.N;

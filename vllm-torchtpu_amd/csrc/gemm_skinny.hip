@@ -175,13 +175,15 @@ struct StepScales {
 template <int KIND, int WF, int MS, int NS>
 __device__ __forceinline__ void mma_step(Acc<KIND, WF, MS, NS>& acc, const Frag (&fa)[MS],
                                          const Frag (&bw)[NS], const StepScales<MS, NS>& sc) {
-  if constexpr (KIND == QK_W8A8_PC && WF == 0) {
+  if constexpr (KIND == QK_W8A8_PC && WF != 1) {
+    // e4m3 (WF 0) or e5m2 (WF 2) on both operands (format codes 0 / 1)
+    constexpr int kF = WF == 2 ? 1 : 0;
 #pragma unroll
     for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
       for (int s = 0; s < NS; ++s)
         acc.v[ms][s] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-            as_i32x8(fa[ms]), as_i32x8(bw[s]), acc.v[ms][s], 0, 0, 0, 127, 0, 127);
+            as_i32x8(fa[ms]), as_i32x8(bw[s]), acc.v[ms][s], kF, kF, 0, 127, 0, 127);
   } else if constexpr (KIND == QK_W8A8_PC && WF == 1) {
 #pragma unroll
     for (int ms = 0; ms < MS; ++ms)
@@ -207,8 +209,10 @@ __device__ __forceinline__ void mma_step(Acc<KIND, WF, MS, NS>& acc, const Frag 
 #pragma unroll
           for (int r = 0; r < 4; ++r) d[r] = (float)di[r];
         } else {
+          // e4m3 activations; e4m3 (WF 0) or e5m2 (WF 2) weights
           d = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(as_i32x8(fa[ms]), as_i32x8(bw[s]),
-                                                               f32x4{0, 0, 0, 0}, 0, 0, 0, 127, 0, 127);
+                                                               f32x4{0, 0, 0, 0}, 0, WF == 2 ? 1 : 0, 0, 127, 0,
+                                                               127);
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc.v[ms][s][r] += d[r] * (sc.sa[ms][r] * sc.sb[s]);
@@ -309,8 +313,12 @@ __device__ __forceinline__ bool slot_group(const GemmParams& p, int slot, int& g
   }
   g = slot;
   if (p.active) {
-    if (slot >= *p.num_active) return false;
-    g = p.active[slot];
+    // both loads at once (the list has an entry for every slot of the grid:
+    // its capacity), then the count decides
+    const int na = *p.num_active;
+    const int ga = p.active[slot];
+    if (slot >= na) return false;
+    g = ga;
   }
   row0 = p.group_offs ? p.group_offs[g] : 0;
   rows = p.group_offs ? p.group_offs[g + 1] - row0 : p.M;
@@ -1051,16 +1059,20 @@ int qmoe_skinny_launch(int kind, GemmParams p, int max_rows, int slots, void* wo
         const int64_t lds = qmoe_skinny_qa_lds(p.M, p.K, pl.ksplit);
         if (p.act != QA_NONE || ms > 2 || (p.K % 128) != 0 || p.group_offs || lds > kQaMaxLds) return QMOE_ERR_ARG;
         if (p.wfmt == 0) launch_qa<0>(p, ms, ns, grid, st, (unsigned)lds);
-        else launch_qa<1>(p, ms, ns, grid, st, (unsigned)lds);
+        else if (p.wfmt == 1) launch_qa<1>(p, ms, ns, grid, st, (unsigned)lds);
+        else launch_qa<2>(p, ms, ns, grid, st, (unsigned)lds);
       } else if (p.wfmt == 0) {
         launch_act<QK_W8A8_PC, 0>(p, ms, ns, grid, st);
-      } else {
+      } else if (p.wfmt == 1) {
         launch_act<QK_W8A8_PC, 1>(p, ms, ns, grid, st);
+      } else {
+        launch_act<QK_W8A8_PC, 2>(p, ms, ns, grid, st);
       }
       break;
     case QK_W8A8_BLK:
       if (p.wfmt == 0) launch_act<QK_W8A8_BLK, 0>(p, ms, ns, grid, st);
-      else launch_act<QK_W8A8_BLK, 1>(p, ms, ns, grid, st);
+      else if (p.wfmt == 1) launch_act<QK_W8A8_BLK, 1>(p, ms, ns, grid, st);
+      else launch_act<QK_W8A8_BLK, 2>(p, ms, ns, grid, st);
       break;
     case QK_W8A16_PC: launch_act<QK_W8A16_PC, 0>(p, ms, ns, grid, st); break;
     case QK_W8A16_BLK: launch_act<QK_W8A16_BLK, 0>(p, ms, ns, grid, st); break;

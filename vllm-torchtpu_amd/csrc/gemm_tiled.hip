@@ -567,6 +567,7 @@ int qmoe_tiled_check(int kind, const GemmParams& p, int* tile) {
   const bool abf16 = kind == QK_W8A16_PC || kind == QK_W4A16_MX || kind == QK_W16A16 || kind == QK_W8A16_BLK;
   const int kstage = abf16 ? 64 : 128;
   if (kind != QK_W8A8_PC && kind != QK_W8A8_BLK && !abf16) return QMOE_ERR_ARG;
+  if (p.wfmt != 0 && p.wfmt != 1) return QMOE_ERR_ARG;  // no e5m2 form
   if (kind == QK_W8A16_BLK && (p.K % 128) != 0) return QMOE_ERR_ARG;
   if (p.K <= 0 || (p.K % kstage) != 0 || p.N <= 0) return QMOE_ERR_ARG;
   if (p.act != QA_NONE && (p.N % 2) != 0) return QMOE_ERR_ARG;

@@ -83,6 +83,38 @@ QMOE_HD float e4m3_to_f32(uint32_t c) {
   return bits_f32(s | ((e + 120u) << 23) | (m << 20));
 }
 
+// ----------------------------------------------------------------- e5m2
+
+// float32 -> OCP e5m2 code, round-to-nearest-even (bias 15, two mantissa
+// bits; magnitudes rounding above 57344 give inf; NaN -> 0x7f with the
+// input's sign). Callers clip to +-57344 first, as the reference does.
+QMOE_HD uint32_t f32_to_e5m2(float f) {
+  uint32_t u = f32_bits(f);
+  uint32_t sign = (u >> 24) & 0x80u;
+  uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return sign | 0x7fu;
+  if (a >= (113u << 23)) {  // |f| >= 2^-14: normal e5m2 binade
+    uint32_t r = (a + 0xfffffu + ((a >> 21) & 1u)) >> 21;
+    r -= 112u << 2;  // rebias 127 -> 15
+    if (r > 0x7bu) r = 0x7cu;  // inf
+    return sign | r;
+  }
+  // subnormal quantum 2^-16: a * 65536 is exact and < 4; rint is RNE, and
+  // 4 is the code of 2^-14
+  float v = bits_f32(a) * 65536.0f;
+  return sign | (uint32_t)rintf(v);
+}
+
+// OCP e5m2 code -> float32 (exact).
+QMOE_HD float e5m2_to_f32(uint32_t c) {
+  uint32_t s = (c & 0x80u) << 24;
+  uint32_t e = (c >> 2) & 0x1fu;
+  uint32_t m = c & 0x3u;
+  if (e == 0x1fu) return bits_f32(s | (m ? 0x7fc00000u : 0x7f800000u));
+  if (e == 0) return bits_f32(s | f32_bits((float)m * 1.52587890625e-05f));
+  return bits_f32(s | ((e + 112u) << 23) | (m << 21));
+}
+
 // ----------------------------------------------------------------- e8m0
 
 // e8m0 byte -> float32 2^(b-127). b == 0 is the f32 subnormal 2^-127 and

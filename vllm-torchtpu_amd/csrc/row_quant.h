@@ -39,18 +39,29 @@ __device__ __forceinline__ Row8 load8(const void* base, int64_t idx) {
 }
 
 // mode: 0 runtime (division), 1 load-time (reciprocal multiply)
-// qdt : 0 e4m3fn, 1 int8
+// qdt : 0 e4m3fn, 1 int8, 2 e5m2 (float targets run in f32, qmax 448 /
+// 57344; int8 in bf16 arithmetic at runtime)
+template <int kQdt>
+__device__ __forceinline__ constexpr float qmax_of() {
+  return kQdt == 0 ? 448.0f : (kQdt == 2 ? 57344.0f : 127.0f);
+}
+
+template <int kQdt>
+__device__ __forceinline__ uint32_t float_code(float q) {
+  return kQdt == 2 ? f32_to_e5m2(q) : f32_to_e4m3(q);
+}
+
 template <int kQdt, int kMode>
 __device__ __forceinline__ float make_scale(float amax) {
   if (kMode == 0) {
-    if (kQdt == 0) {
-      float s = amax / 448.0f;
+    if (kQdt != 1) {
+      float s = amax / qmax_of<kQdt>();
       return s == 0.0f ? 1.0f : s;
     }
     float s = bf16_round(amax / 127.0f);
     return s == 0.0f ? 1.0f : s;
   }
-  const float recip = kQdt == 0 ? (float)(1.0 / 448.0) : (float)(1.0 / 127.0);
+  const float recip = kQdt == 0 ? (float)(1.0 / 448.0) : (kQdt == 2 ? (float)(1.0 / 57344.0) : (float)(1.0 / 127.0));
   return amax * recip;
 }
 
@@ -69,20 +80,22 @@ __device__ __forceinline__ float div_rn(float x, float scale, float inv) {
 template <int kQdt, int kMode>
 __device__ __forceinline__ uint32_t quant1(float x, float scale, float inv) {
   if (kMode == 0) {
-    if (kQdt == 0) {
+    if (kQdt != 1) {
+      constexpr float mx = qmax_of<kQdt>();
       float d = x / scale;
-      float q = d != d ? d : fminf(fmaxf(d, -448.0f), 448.0f);  // clip keeps NaN
-      return f32_to_e4m3(q);
+      float q = d != d ? d : fminf(fmaxf(d, -mx), mx);  // clip keeps NaN
+      return float_code<kQdt>(q);
     }
     float q = rintf(bf16_round(x / scale));
     q = q != q ? 0.0f : fminf(fmaxf(q, -128.0f), 127.0f);  // NaN -> 0, saturate
     return (uint32_t)(int32_t)q & 0xffu;
   }
   float q = x * inv;
-  if (kQdt == 0) {
-    float c = fminf(fmaxf(q, -448.0f), 448.0f);
+  if (kQdt != 1) {
+    constexpr float mx = qmax_of<kQdt>();
+    float c = fminf(fmaxf(q, -mx), mx);
     if (q != q) c = q;
-    return f32_to_e4m3(c);
+    return float_code<kQdt>(c);
   }
   float c = q != q ? 0.0f : fminf(fmaxf(q, -128.0f), 127.0f);
   return (uint32_t)(int32_t)rintf(c) & 0xffu;
@@ -90,18 +103,27 @@ __device__ __forceinline__ uint32_t quant1(float x, float scale, float inv) {
 
 // Runtime codes of 8 values of a row whose scale is finite (so are the
 // values: the absmax is NaN- and inf-sticky): division as div_rn, clip,
-// then the hardware RNE conversion (e4m3 pairs) or rint (int8). Returns the
-// 8 code bytes, the first value in the low byte.
+// then the hardware RNE conversion (e4m3 / e5m2 pairs) or rint (int8).
+// Returns the 8 code bytes, the first value in the low byte.
 template <int kQdt>
 __device__ __forceinline__ uint2 codes8_fast(const Row8& r, float scale, float inv) {
-  if (kQdt == 0) {
+  if (kQdt != 1) {
+    constexpr float mx = qmax_of<kQdt>();
     float d[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) d[i] = fminf(fmaxf(div_rn(r.v[i], scale, inv), -448.0f), 448.0f);
-    int lo = __builtin_amdgcn_cvt_pk_fp8_f32(d[0], d[1], 0, false);
-    lo = __builtin_amdgcn_cvt_pk_fp8_f32(d[2], d[3], lo, true);
-    int hi = __builtin_amdgcn_cvt_pk_fp8_f32(d[4], d[5], 0, false);
-    hi = __builtin_amdgcn_cvt_pk_fp8_f32(d[6], d[7], hi, true);
+    for (int i = 0; i < 8; ++i) d[i] = fminf(fmaxf(div_rn(r.v[i], scale, inv), -mx), mx);
+    int lo, hi;
+    if (kQdt == 0) {
+      lo = __builtin_amdgcn_cvt_pk_fp8_f32(d[0], d[1], 0, false);
+      lo = __builtin_amdgcn_cvt_pk_fp8_f32(d[2], d[3], lo, true);
+      hi = __builtin_amdgcn_cvt_pk_fp8_f32(d[4], d[5], 0, false);
+      hi = __builtin_amdgcn_cvt_pk_fp8_f32(d[6], d[7], hi, true);
+    } else {
+      lo = __builtin_amdgcn_cvt_pk_bf8_f32(d[0], d[1], 0, false);
+      lo = __builtin_amdgcn_cvt_pk_bf8_f32(d[2], d[3], lo, true);
+      hi = __builtin_amdgcn_cvt_pk_bf8_f32(d[4], d[5], 0, false);
+      hi = __builtin_amdgcn_cvt_pk_bf8_f32(d[6], d[7], hi, true);
+    }
     return make_uint2((uint32_t)lo, (uint32_t)hi);
   }
   uint32_t lo = 0, hi = 0;

@@ -16,8 +16,8 @@ format                w1 [E, 2I, H...] / w2        scales
 ``nvfp4``             uint8 packed e2m1 [., ., K/2]  bf16 [E, N, K/16] (fused e4m3 x global)
 ``int4``              int32 carriers [., ., K/8]     bf16 [E, N, K/group], group 32 / 64 / 128
                       (8 offset-binary nibbles per int32, the compressed-tensors checkpoint form)
-``fp8`` / ``int8``    float8_e4m3fn / int8         f32 per-channel [E, N], or per (row, B
-                                                   columns) [E, N, K/B] with B a power-of-two
+``fp8`` / ``int8`` /  float8_e4m3fn / int8 /      f32 per-channel [E, N], or per (row, B
+``e5m2``              float8_e5m2                  columns) [E, N, K/B] with B a power-of-two
                                                    multiple of 512
 ``fp8_w8a16``         float8_e4m3fn [E, N, K]      f32 per-(row, 128) scales [E, N, K/128]
 ``fp8_block``         float8_e4m3fn [E, N, K]      f32 tile scales [E, N/128, K/128]
@@ -29,10 +29,11 @@ format                w1 [E, 2I, H...] / w2        scales
 
 Numeric recipe of each 1-byte format:
 
-* ``fp8`` / ``int8`` -- the reference's: its grouped matmul quantizes the
-  activations per (row, 512 columns) in bf16 arithmetic for weights with
-  quant blocks of 256+ columns (`kernels/megablox/gmm_v2.py:500-548`), to
-  e4m3 for float weights and int8 for int8 weights; the block sums are
+* ``fp8`` / ``int8`` / ``e5m2`` -- the reference's: its grouped matmul
+  quantizes the activations per (row, 512 columns) in bf16 arithmetic for
+  weights with quant blocks of 256+ columns (`kernels/megablox/gmm_v2.py:
+  500-548`), to e4m3 for float weights (e4m3 and e5m2) and int8 for int8
+  weights; the block sums are
   scaled and accumulated in f32 (the reference accumulates in bf16).
 * ``fp8_w8a16`` -- the reference's for 128-column weight blocks
   (``MOE_REQUANTIZE_BLOCK_SIZE=128``): each weight is bf16(code *
@@ -59,8 +60,8 @@ from qmoe import _capi, ops
 from qmoe.layers import ref_layout
 
 
-MOE_FORMATS = ("mxfp4", "nvfp4", "int4", "bf16", "fp8", "int8", "fp8_w8a16", "fp8_block", "fp8_block_rows",
-               "fp8_rowquant", "int8_rowquant", "mxfp4_mx")
+MOE_FORMATS = ("mxfp4", "nvfp4", "int4", "bf16", "fp8", "int8", "e5m2", "fp8_w8a16", "fp8_block",
+               "fp8_block_rows", "fp8_rowquant", "int8_rowquant", "mxfp4_mx")
 
 # "mxfp4_mx" (opt-in, no reference counterpart): MXFP4 experts with MX
 # activations -- the tokens and the intermediate quantized per 32 columns to
@@ -78,6 +79,8 @@ def infer_weight_format(w1: torch.Tensor, w1_scale) -> str:
         return "bf16"
     if w1.dtype == torch.int8:
         return "int8"
+    if w1.dtype == torch.float8_e5m2:
+        return "e5m2"
     if w1.dtype == torch.float8_e4m3fn:
         if w1_scale is not None and w1_scale.dim() == 3 and w1_scale.shape[-1] * 128 == w1.shape[-1]:
             return "fp8_w8a16" if w1_scale.shape[1] == w1.shape[1] else "fp8_block"
@@ -333,10 +336,11 @@ def _moe_body(x, w1, w2, w1_scale, w2_scale, w1_bias, w2_bias, tw, topk_ids, top
         a2q, a2_scale = ops.row_quant(inter, "fp8", block=128)
         a2, kind, wf = u8(a2q), _capi.W8A8_BLK, 0
         w2k, w2s = u8(w2), w2_scale
-    elif fmt in ("fp8", "int8"):
+    elif fmt in ("fp8", "int8", "e5m2"):
         # the reference's grouped-matmul recipe: per-(row, 512) bf16-arithmetic
-        # activation quant before each GEMM
-        qd, wf = ("fp8", 0) if fmt == "fp8" else ("int8", 1)
+        # activation quant before each GEMM (e4m3 for float experts, e5m2
+        # included: `kernels/megablox/gmm_v2.py:1199-1215`)
+        qd, wf = {"fp8": ("fp8", 0), "int8": ("int8", 1), "e5m2": ("fp8", 2)}[fmt]
         xq, xs = ops.row_quant(x, qd, mode="gmm")
         inter = ops.gemm(_capi.W8A8_GMM, u8(xq), u8(w1), a_scale=xs, w_scale=_gmm_scale(w1_scale, E),
                          wfmt=wf, bias=b1, a_rows=meta["token_sorted"], activation=activation, **common)

@@ -132,7 +132,7 @@ def quantized_matmul(x: torch.Tensor, w_q: torch.Tensor, w_s: torch.Tensor,
         x2 = x2.to(torch.bfloat16)
     w_nk = _weight_nk(w_q)
     k_dim, n_out = w_q.shape
-    if w_nk.dtype not in (torch.int8, torch.float8_e4m3fn):
+    if w_nk.dtype not in (torch.int8, torch.float8_e4m3fn, torch.float8_e5m2):
         raise ValueError(f"Unsupported quantized dtype: {w_nk.dtype}")
     if w_s.dim() == 1:
         if w_s.shape[0] != n_out:
@@ -175,21 +175,27 @@ def _quantized_matmul_op(x2: torch.Tensor, w_nk: torch.Tensor, w_s: torch.Tensor
     rows = x2.shape[0]
     wq = w_nk.view(torch.uint8)
     is_int = w_nk.dtype == torch.int8
+    # weight code format of the W8A8 kinds: 0 e4m3, 1 int8, 2 e5m2
+    wfmt = 1 if is_int else (2 if w_nk.dtype == torch.float8_e5m2 else 0)
     if regime == REGIME_PER_CHANNEL:
         ws = w_s.float().contiguous()
         if not is_int and 0 < rows <= w8a16_max_rows:
+            if wfmt == 2:
+                raise NotImplementedError("qmoe runs W8A16 (w8a16_max_rows) for float8_e4m3fn weights only")
             return ops.gemm(_capi.W8A16_PC, x2, wq, w_scale=ws)
-        # per-token activation quant + W8A8 in one call (decode sizes quantize
-        # inside the streaming kernel; larger ones quantize first)
+        # per-token activation quant (to the weight dtype, `util.py:113`) +
+        # W8A8 in one call (decode sizes quantize inside the streaming
+        # kernel; larger ones quantize first)
         x2 = x2.contiguous()
         if x2.data_ptr() % 16:
             x2 = x2.clone()
-        return ops.gemm(_capi.W8A8_PC_DYN, x2, wq, w_scale=ws, wfmt=int(is_int))
+        return ops.gemm(_capi.W8A8_PC_DYN, x2, wq, w_scale=ws, wfmt=wfmt)
     if regime == REGIME_GMM_W8A16:
         return ops.gemm(_capi.W8A16_BLK, x2, wq, w_scale=w_s, ws_bn=1)
     if regime == REGIME_GMM_QUANT_LHS:
+        # e4m3 activations for any float weights (`kernels/megablox/gmm_v2.py:1199-1215`)
         xq, xs = ops.row_quant(x2, "int8" if is_int else "fp8", mode="gmm")
-        return ops.gemm(_capi.W8A8_GMM, xq.view(torch.uint8), wq, a_scale=xs, w_scale=w_s, wfmt=int(is_int))
+        return ops.gemm(_capi.W8A8_GMM, xq.view(torch.uint8), wq, a_scale=xs, w_scale=w_s, wfmt=wfmt)
     sb, bn = _native_blocks(w_s, k_dim, n_out)
     xq, xs = ops.row_quant(x2, "fp8", block=128)
     return ops.gemm(_capi.W8A8_BLK, xq.view(torch.uint8), wq, a_scale=xs, w_scale=sb, ws_bn=bn)

@@ -19,7 +19,10 @@ weights to K-major instead):
     ``[n_out/128, n_in/128]`` (no requantization); any other checkpoint is
     requantized per (output channel, 128-wide K block) -> ``[n_out, n_in/128]``.
   ``REQUANTIZE_WEIGHT_DTYPE=int8`` requantizes per channel to int8 (W8A8 with
-  int8 activations, bit-exact int32 accumulation).
+  int8 activations, bit-exact int32 accumulation); ``float8_e5m2`` to e5m2
+  codes (per channel: e5m2 activations as well, `util.py:80-124` quantizes
+  them to the weight dtype; blocks of 512+: e4m3 activations, the grouped
+  matmul's rule).
 * MoE weights ``w13 [E, 2I, H]`` / ``w2 [E, H, I]``; a 128x128-block
   checkpoint keeps native codes + tile scales (the DeepSeek-V3 form), other
   checkpoints are requantized per channel.
@@ -36,10 +39,10 @@ from qmoe.layers.fused_moe import moe_forward
 from qmoe.layers.linear_common import KEEP_VLLM_LAYOUT_ATTR, quantized_matmul
 
 FP8 = torch.float8_e4m3fn
-_REQUANT_DTYPES = {"float8_e4m3fn": FP8, "int8": torch.int8}
-# accepted by the reference's env parsing (`fp8.py:122-127`); no kernel here
-# runs e5m2 codes, so selecting it raises NotImplementedError at load time
-_REQUANT_DTYPES_UNBUILT = ("float8_e5m2",)
+# requantization targets (`fp8.py:122-127`); the short names are the ones
+# `ops.row_quant` takes
+_REQUANT_DTYPES = {"float8_e4m3fn": FP8, "int8": torch.int8, "float8_e5m2": torch.float8_e5m2}
+_QDTYPE_SHORT = {"float8_e4m3fn": "fp8", "int8": "int8", "float8_e5m2": "e5m2"}
 
 
 # f32 bytes of one chunk of experts dequantized at load time
@@ -71,11 +74,8 @@ def get_linear_quant_config():
             "quantized_matmul_kernel or unset the quantize block size to trigger per-channel "
             "quantization."
         )
-    if name in _REQUANT_DTYPES_UNBUILT:
-        raise NotImplementedError(f"REQUANTIZE_WEIGHT_DTYPE={name} is not built: qmoe kernels take "
-                                  "float8_e4m3fn and int8 weight codes")
     if name not in _REQUANT_DTYPES:
-        supported = ", ".join(sorted(list(_REQUANT_DTYPES) + list(_REQUANT_DTYPES_UNBUILT)))
+        supported = ", ".join(sorted(_REQUANT_DTYPES))
         raise ValueError(f"Unsupported REQUANTIZE_WEIGHT_DTYPE={name!r}. Supported values: {supported}.")
     if block is not None:
         _check_block(block, "REQUANTIZE_BLOCK_SIZE")
@@ -100,11 +100,8 @@ def get_moe_quant_config():
     `fp8.py:185-213` (default: float8_e4m3fn per channel)."""
     name = envs.MOE_REQUANTIZE_WEIGHT_DTYPE or "float8_e4m3fn"
     block = envs.MOE_REQUANTIZE_BLOCK_SIZE or None
-    if name in _REQUANT_DTYPES_UNBUILT:
-        raise NotImplementedError(f"MOE_REQUANTIZE_WEIGHT_DTYPE={name} is not built: qmoe kernels take "
-                                  "float8_e4m3fn and int8 weight codes")
     if name not in _REQUANT_DTYPES:
-        supported = ", ".join(sorted(list(_REQUANT_DTYPES) + list(_REQUANT_DTYPES_UNBUILT)))
+        supported = ", ".join(sorted(_REQUANT_DTYPES))
         raise ValueError(f"Unsupported MOE_REQUANTIZE_WEIGHT_DTYPE={name!r}. Supported values: {supported}.")
     if block is not None:
         _check_block(block, "MOE_REQUANTIZE_BLOCK_SIZE")
@@ -142,7 +139,7 @@ def requantize(w_f32, qdtype_name, block=None):
     rows of B columns)."""
     lead = w_f32.shape[:-1]
     k = w_f32.shape[-1]
-    qd = "fp8" if qdtype_name == "float8_e4m3fn" else "int8"
+    qd = _QDTYPE_SHORT[qdtype_name]
     if block is not None and k % block:
         raise ValueError(f"Quantization expects the requested axis to be divisible by block_size {block}, got {k}")
     if block is not None and block != 128:
@@ -352,7 +349,7 @@ class Fp8MoEMethod:
         chunks of experts, de-interleave swigluoai gate/up rows, zero the
         padding of an unpadded intermediate size and pad the intermediate
         size to a multiple of 128 (`:351-406`), requantize to
-        MOE_REQUANTIZE_WEIGHT_DTYPE (float8_e4m3fn by default, or int8) per
+        MOE_REQUANTIZE_WEIGHT_DTYPE (float8_e4m3fn by default, int8 or float8_e5m2) per
         channel, or per (row, MOE_REQUANTIZE_BLOCK_SIZE columns). At run time
         per-channel and 512+ blocks take the quantized-activation recipe, 128
         blocks the bf16-dequantized one. With QMOE_FP8_NATIVE_BLOCKS=1 a
@@ -396,7 +393,7 @@ class Fp8MoEMethod:
                 if block is not None and kk % block:
                     raise ValueError(f"Unsupported MoE quantization: {wname} contracting dimension {kk} is not "
                                      f"divisible by block_size={block}.")
-            qdt = FP8 if name == "float8_e4m3fn" else torch.int8
+            qdt = _REQUANT_DTYPES[name]
 
             def alloc(n, k):
                 return (torch.empty((E, n, k), dtype=qdt, device=dev),
@@ -428,7 +425,7 @@ class Fp8MoEMethod:
             if block == 128:
                 layer._qmoe_format = "fp8_w8a16"
             else:
-                layer._qmoe_format = "fp8" if name == "float8_e4m3fn" else "int8"
+                layer._qmoe_format = {"float8_e4m3fn": "fp8", "int8": "int8", "float8_e5m2": "e5m2"}[name]
         for attr in ("w13_weight_scale_inv", "w2_weight_scale_inv"):
             if hasattr(layer, attr):
                 delattr(layer, attr)

@@ -191,11 +191,11 @@ def moe_weights(hidden: int, w1, w2, w1_scale, w2_scale, w1_bias, w2_bias):
                 raise ValueError("fused_moe_gmm: bf16 weights take no scales")
             s1 = s2 = None
             fmt = "bf16"
-        elif w1.dtype in (torch.float8_e4m3fn, torch.int8):
+        elif w1.dtype in (torch.float8_e4m3fn, torch.int8, torch.float8_e5m2):
             if w1_scale is None or w2_scale is None:
                 raise ValueError("fused_moe_gmm: 1-byte weights need scales [E, K/B, 1, N]")
             b1, b2 = block_of(w1_scale, k1), block_of(w2_scale, k2)
-            q = "int8" if w1.dtype == torch.int8 else "fp8"
+            q = {torch.int8: "int8", torch.float8_e5m2: "e5m2"}.get(w1.dtype, "fp8")
             s1n = _cached(w1_scale, "nmajor", lambda: scale_nmajor(w1_scale))  # [E, N, K/B]
             s2n = _cached(w2_scale, "nmajor", lambda: scale_nmajor(w2_scale))
             if b1 == k1 and b2 == k2:  # one block: per channel

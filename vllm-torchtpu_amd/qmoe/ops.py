@@ -85,8 +85,9 @@ def row_quant(x, qdtype="fp8", block=None, mode="runtime"):
     multiply; zero rows keep scale 0). mode "gmm": the grouped matmul's
     quantized-lhs regime, `kernels/megablox/gmm_v2.py:508-536` (per (row,
     512 columns), bf16 arithmetic, fp8 RNE / int8 truncated codes; block is
-    always 512). Returns (codes [M, K] float8_e4m3fn or int8, scales f32
-    [M], [M, K/128] or [M, ceil(K/512)]).
+    always 512). qdtype "fp8" (e4m3fn), "int8" or "e5m2" (one scale per row,
+    modes "runtime" and "load"). Returns (codes [M, K] float8_e4m3fn, int8 or
+    float8_e5m2, scales f32 [M], [M, K/128] or [M, ceil(K/512)]).
     """
     _require_gpu(x)
     if x.dim() != 2:
@@ -97,10 +98,12 @@ def row_quant(x, qdtype="fp8", block=None, mode="runtime"):
     in_f32 = x.dtype == torch.float32
     if not in_f32 and x.dtype != torch.bfloat16:
         raise ValueError(f"row_quant expects bf16 (or f32 at load time), got {x.dtype}")
-    qd = {"fp8": 0, "int8": 1}[qdtype]
+    qd = {"fp8": 0, "int8": 1, "e5m2": 2}[qdtype]
     md = {"runtime": 0, "load": 1, "gmm": 2}[mode]
     blk = 512 if md == 2 else (0 if block is None else int(block))
-    q = torch.empty((M, K), dtype=FP8 if qd == 0 else torch.int8, device=x.device)
+    if qd == 2 and blk:
+        raise ValueError("row_quant: e5m2 codes take one scale per row (no blocks, no gmm mode)")
+    q = torch.empty((M, K), dtype=(FP8, torch.int8, torch.float8_e5m2)[qd], device=x.device)
     ns = 1 if blk == 0 else (K + blk - 1) // blk
     s = torch.empty((M, ns), dtype=torch.float32, device=x.device)
     if M:
