@@ -576,7 +576,8 @@ def sweep_moe(only):
                                 experts_touched=touched, **roof(T * (k + 1) * 6.0 * H * I, nbytes, us, "fp8"),
                                 **par))
                 log(out[-1])
-                if T > ops.DECODE_MAX_TOKENS:
+                # an armed layer serves larger steps with the GMM path above
+                if T > min(ops.DECODE_MAX_TOKENS, decode_op_tokens()):
                     continue
 
                 def decode_layer():
@@ -605,6 +606,14 @@ def sweep_moe(only):
                 log(out[-1])
         out.extend(sweep_moe_default(lcfg, w13, s13, w2, s2, sh13, ss13, sh2, ss2, bias, gen))
     return out
+
+
+def decode_op_tokens():
+    """The most tokens an armed MoE layer serves with the fused decode op
+    (the measured crossover to the GMM path)."""
+    from qmoe import envs
+
+    return envs.QMOE_DECODE_OP_MAX_TOKENS or 1 << 30
 
 
 def sweep_moe_default(lcfg, w13, s13, w2, s2, sh13, ss13, sh2, ss2, bias, gen):
@@ -682,7 +691,7 @@ def sweep_moe_default(lcfg, w13, s13, w2, s2, sh13, ss13, sh2, ss2, bias, gen):
             out.append(dict(cfg=4, kind=f"moe_{qd}_pc_dsv3_default", T=T, experts_touched=touched,
                             **roof(T * (k + 1) * 6.0 * H * I, nbytes, us, qd), **par))
             log(out[-1])
-            if qd != "fp8" or T > ops.DECODE_MAX_TOKENS:
+            if qd != "fp8" or T > min(ops.DECODE_MAX_TOKENS, decode_op_tokens()):
                 continue
 
             def decode_layer():
@@ -1188,18 +1197,19 @@ def profile_mx(args):
 
 
 def profile_midm(args):
-    """rocprofv3 target: the mid-M linears, 20 launches each after 3
-    warm-up calls -- cfg 0 MXFP4 at M=128, cfg 1 FP8 W8A8 up / down at M=64
-    and 512 (activation quant included), cfg 2 block FP8 (N 18432) at
-    M=256."""
+    """rocprofv3 target: the small- and mid-M linears, 23 launches each --
+    cfg 0 MXFP4 at M=1, 16 and 128, cfg 1 FP8 W8A8 up / down at M=64 and 512
+    (activation quant included), cfg 2 block FP8 (N 18432) at M=256."""
     import torch
 
     from qmoe.layers.linear_common import quantized_matmul, quantized_matmul_fp4
 
     gen = torch.Generator(device="cuda").manual_seed(1)
     codes, sc = mxfp4_weights((5760, 2880), gen)
-    x0 = torch.randn((128, 2880), device="cuda", generator=gen).to(torch.bfloat16)
-    calls = [("cfg0 M=128", lambda: quantized_matmul_fp4(x0, codes, sc))]
+    calls = []
+    for M in (1, 16, 128):
+        x0 = torch.randn((M, 2880), device="cuda", generator=gen).to(torch.bfloat16)
+        calls.append((f"cfg0 M={M}", lambda x0=x0: quantized_matmul_fp4(x0, codes, sc)))
     for K, N in ((4096, 14336), (14336, 4096)):
         w, s = fp8_weights(N, K, gen)
         for M in (64, 512):

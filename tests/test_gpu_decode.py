@@ -391,3 +391,23 @@ def test_armed_layer_serves_shared_plus_routed(dev, monkeypatch, gated, rsf):
             # a different recipe (the GMM MoE's and the dense linears'):
             # the reference test's bar against the decomposed layer
             assert _max_rel(got, decode.decomposed_layer_f32(**L, routed_scale=rsf)) < 0.08
+
+
+def test_arming_caps_the_op_at_the_measured_crossover(dev, monkeypatch):
+    """Above QMOE_DECODE_OP_MAX_TOKENS (16: the fused op's measured
+    crossover with the GMM path) an armed layer's steps take the GMM path
+    even under a larger FUSED_MOE_DECODE_KERNEL_MAX_TOKENS; 0 leaves the
+    reference's cap alone."""
+    from qmoe.layers import fused_moe_decode as fmd
+
+    print("decode op crossover cap", flush=True)
+    monkeypatch.setenv("FUSED_MOE_DECODE_KERNEL", "1")
+    monkeypatch.setenv("FUSED_MOE_DECODE_KERNEL_MAX_TOKENS", "64")
+    for env, cap in ((None, 16), ("0", 64), ("4", 4)):
+        if env is None:
+            monkeypatch.delenv("QMOE_DECODE_OP_MAX_TOKENS", raising=False)
+        else:
+            monkeypatch.setenv("QMOE_DECODE_OP_MAX_TOKENS", env)
+        model, _, _, method, _ = _armed_runner(dev, monkeypatch, 8, 512, 128, 128, 2, False, 1.0, seed=5)
+        assert fmd.arm_fused_moe_decode(model) == 1
+        assert getattr(method, fmd.FUSED_MOE_DECODE_OP_ATTR)["max_tokens"] == cap

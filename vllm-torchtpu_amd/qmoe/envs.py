@@ -52,6 +52,11 @@ _READERS = {
     # (shared + routed experts), up to MAX_TOKENS tokens per step
     "FUSED_MOE_DECODE_KERNEL": lambda: _bool("FUSED_MOE_DECODE_KERNEL"),
     "FUSED_MOE_DECODE_KERNEL_MAX_TOKENS": lambda: int(os.getenv("FUSED_MOE_DECODE_KERNEL_MAX_TOKENS", "256")),
+    # this build only: the most tokens an armed layer's step serves with the
+    # fused decode op before the GMM path (faster above it on MI355X; see
+    # `qmoe/layers/fused_moe_decode.py`), whatever the cap above allows (0:
+    # the cap alone)
+    "QMOE_DECODE_OP_MAX_TOKENS": lambda: _nonneg_int("QMOE_DECODE_OP_MAX_TOKENS", 16),
     # this build only (no reference counterpart): 128x128-block FP8 checkpoints
     # keep their tiles at run time with per-(token, 128) e4m3 activations
     # (the blockwise W8A8 recipe of BASELINE configs 2 and 4) instead of the

@@ -138,6 +138,13 @@ def arm_fused_moe_decode(model, what="model") -> int:
         logger.warning("FUSED_MOE_DECODE_KERNEL_MAX_TOKENS=%d: the fused decode op serves at most %d tokens; "
                        "larger steps take the GMM path", max_tokens, ops.DECODE_MAX_TOKENS)
         max_tokens = ops.DECODE_MAX_TOKENS
+    # Measured on MI355X (DeepSeek-V3 layer: 256 experts, top 8, 128x128 FP8
+    # tiles, shared expert included, graph-replayed): the op matches the GMM
+    # path plus the shared linears up to 16 tokens (T = 8 / 16: 386 / 552 vs
+    # 385 / 556 us) and is 20-25% slower above (T = 24 / 64: 797 / 1217 vs
+    # 647 / 989 us), where its down kernel walks 150-250 experts per column
+    # block; larger steps take the GMM path (QMOE_DECODE_OP_MAX_TOKENS)
+    max_tokens = max(1, min(max_tokens, envs.QMOE_DECODE_OP_MAX_TOKENS or max_tokens))
     runners = [m for m in model.modules() if hasattr(m, "routed_experts") and hasattr(m, "_quant_method")]
     armed = 0
     for runner in runners:
