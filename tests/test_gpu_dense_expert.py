@@ -117,7 +117,7 @@ def test_dense_expert_nonfinite_expert_stays_with_its_tokens(dev, monkeypatch):
 
 
 def test_dense_expert_opposite_routes_cancel(dev, monkeypatch):
-    """`moe_dense_expert.py:258-262`: a token's routes to one expert merge
+    """`moe_dense_expert.py:258-268`: a token's routes to one expert merge
     into one coefficient before the mask, so weights +w and -w on the NaN
     expert 3 beside a route to expert 0 give exactly the route to 0 alone
     (the grouped sum w*y + (-w)*y would be NaN)."""

@@ -123,7 +123,7 @@ def can_use_dense_expert(hidden_states, w1, w2, w1_scale, w2_scale, w1_bias, w2_
 
 def merge_repeated_routes(topk_weights: torch.Tensor, topk_ids: torch.Tensor):
     """The dense-expert branch's coefficient table in route form
-    (`kernels/experimental/moe_dense_expert.py:258-262`): a token's
+    (`kernels/experimental/moe_dense_expert.py:258-268`): a token's
     coefficient for an expert is the float32 sum, in route order, of the
     weights of its routes to that expert. The first of those routes carries
     the sum (rounded to the routing weights' bf16, the grouped path's

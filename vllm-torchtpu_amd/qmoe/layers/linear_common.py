@@ -183,7 +183,7 @@ def _quantized_matmul_op(x2: torch.Tensor, w_nk: torch.Tensor, w_s: torch.Tensor
             if wfmt == 2:
                 raise NotImplementedError("qmoe runs W8A16 (w8a16_max_rows) for float8_e4m3fn weights only")
             return ops.gemm(_capi.W8A16_PC, x2, wq, w_scale=ws)
-        # per-token activation quant (to the weight dtype, `util.py:113`) +
+        # per-token activation quant (to the weight dtype, `util.py:108`) +
         # W8A8 in one call (decode sizes quantize inside the streaming
         # kernel; larger ones quantize first)
         x2 = x2.contiguous()
