@@ -180,8 +180,10 @@ int qmoe_gemm_workspace_size(const qmoe_gemm_desc* d, int64_t* bytes);
  * 256 x 256 persistent tiles, 7 MX grouped tiles, 8 weight streaming with
  * the per-row activation quantization inside (QMOE_W8A8_PC_DYN; for the
  * kind's other problems the path of the GEMM after its separate
- * quantization), 9 1-byte x 1-byte tiles of 128 weight rows; tile_m = token rows per tile
- * (or per streaming pass); ksplit = K slices. No counterpart in the
+ * quantization), 9 1-byte x 1-byte tiles of 128 weight rows, 10 weight
+ * streaming in slices of tile_m rows of a dense problem (one slice per
+ * grid.z index, each streaming the whole weight matrix); tile_m = token rows
+ * per tile (or per streaming pass or slice); ksplit = K slices. No counterpart in the
  * reference (its tiling is chosen inside the Pallas call,
  * `kernels/megablox/gmm_v2.py:922-1055`); it lets tests assert which kernel
  * instances they exercise. Any output pointer may be NULL.

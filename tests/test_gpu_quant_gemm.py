@@ -400,7 +400,7 @@ def test_w4a16_int4_dequant_bit_exact(dev, M, K, N, group):
                                    # K % 64 != 0 takes the generic tiled kernel
                                    (300, 2880, 768), (520, 1024, 512), (600, 512, 9216), (1200, 512, 9216),
                                    (70, 2848, 300),
-                                   # 33..64 rows: tiled 32-token tiles with a 4-way K split
+                                   # 33..64 rows: the streaming kernel in 16-row slices
                                    (50, 2880, 1000)])
 def test_w4a16_mxfp4(dev, M, K, N):
     from qmoe import _capi, ops

@@ -216,7 +216,35 @@ enum Path {
   kPathMxTiles = 7,       // the same operands, grouped tiles (one tile per workgroup)
   kPathSkinnyDyn = 8,     // weight streaming with the per-row activation quantization inside
   kPathF8Narrow = 9,      // 1-byte x 1-byte tiles of 128 weight rows
+  kPathSkinnyRows = 10,   // weight streaming, one slice of rows per grid.z index
 };
+
+// Dense problems of a few dozen rows can stream the weights once per slice
+// of 16 rows: one slice per grid.z index, every slice's workgroups
+// streaming the whole weight matrix (the slices of one weight tile meet its
+// bytes in one XCD's L2). Measured on MI355X: e2m1 weights (K 2880, N 5760)
+// at 17 / 32 / 64 rows 8.4 / 11.0 / 15.8 -> 8.0 / 10.5 / 13.8 us (slower
+// from 128 rows); 1-byte weights only while the slices keep the grid near
+// one workgroup per CU -- the FP8 down projection (K 14336, N 4096, 128
+// tiles per slice) at 32 rows 21.2 -> 14.8 us with no K split, while the up
+// projection (448 tiles per slice) loses 17.1 -> 20.3 us. 0: not this route.
+int dense_row_split(const qmoe_gemm_desc* d) {
+  if (d->group_offs || d->active || d->M <= 16) return 0;
+  const char* env = getenv("QMOE_SKINNY_ROW_SPLIT");  // tuning knob: 0 off, 16 / 32 / 64 forced up to 256 rows
+  if (env) {
+    const int rs = atoi(env);
+    const bool ok = (rs == 16 || rs == 32 || rs == 64) && d->M > rs && d->M <= 256 && d->kind != QMOE_W4A4_MX &&
+                    d->kind != QMOE_W8A8_PC_DYN;
+    return ok ? rs : 0;
+  }
+  if (d->kind == QMOE_W4A16_MX || d->kind == QMOE_W4A16_NV) return d->M <= 64 ? 16 : 0;
+  if (d->kind == QMOE_W8A8_PC && d->M <= 32) {
+    const int64_t nout = d->act != QMOE_ACT_NONE ? d->N / 2 : d->N;
+    const int64_t tiles = d->act != QMOE_ACT_NONE ? cdiv<int64_t>(nout, 16) : cdiv<int64_t>(nout, 32);
+    return tiles * cdiv<int64_t>(d->M, 16) <= 320 ? 16 : 0;
+  }
+  return 0;
+}
 
 int64_t align256(int64_t b) { return (b + 255) / 256 * 256; }
 
@@ -286,6 +314,12 @@ int qmoe_route_of(const qmoe_gemm_desc* d, GemmParams& p, QmoeRoute* r) {
     *r = QmoeRoute{p.group_offs ? kPathMxTiles : kPathMx, bm, 1, 0};
     return QMOE_OK;
   }
+  if (const int rs = dense_row_split(d)) {
+    if (qmoe_skinny_check(kind, p) == QMOE_OK) {
+      *r = QmoeRoute{kPathSkinnyRows, rs, 1, 0};
+      return QMOE_OK;
+    }
+  }
   if (use_skinny(d) && qmoe_skinny_check(kind, p) == QMOE_OK) {
     r->path = kPathSkinny;
     r->tile_m = qmoe_skinny_tile_rows(skinny_rows(d));
@@ -351,6 +385,12 @@ int qmoe_run_route(const qmoe_gemm_desc* d, const QmoeRoute& r, GemmParams p, vo
     return qmoe_run_route(&e, re, pe, w8 + pre, ws_bytes - pre, stream);
   }
   switch (r.path) {
+    case kPathSkinnyRows: {
+      GemmParams q;
+      qmoe_to_params(d, &q);
+      q.row_split = r.tile_m;
+      return qmoe_skinny_launch(kind, q, r.tile_m, (int)cdiv<int64_t>(d->M, r.tile_m), workspace, ws_bytes, 1, stream);
+    }
     case kPathSkinny: {
       GemmParams q;
       qmoe_to_params(d, &q);  // keeps the active list

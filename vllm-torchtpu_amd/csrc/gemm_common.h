@@ -145,6 +145,10 @@ struct GemmParams {
   // split-K workspace (skinny kernel only)
   float* partial;
   int32_t ksplit;
+  // dense streaming kernel only: gridDim.z slices of row_split rows each
+  // (slice z: rows [z * row_split, +row_split)), all reading the one weight
+  // matrix; 0: the grid's z dimension is the groups
+  int32_t row_split;
   // Fused decode MoE (skinny kernel only, ksplit 1, no bias). x0 != 0: group
   // 0 is the layer's shared expert, with its own weights w_x / scales ws_x
   // (same layout, n_x weight rows), and group g >= 1 is expert g - 1 of w /

@@ -10,7 +10,7 @@ struct QmoeRoute {
   int path = 0;    // 0 streaming, 1 1-byte tiles, 2 4-bit tiles, 3 generic tiles, 4 streaming passes,
                    // 5 1-byte tiles on persistent workgroups, 6 MX (e2m1 x e2m1) persistent tiles,
                    // 7 MX grouped tiles, 8 streaming with the activation quantization inside,
-                   // 9 1-byte tiles of 128 weight rows
+                   // 9 1-byte tiles of 128 weight rows, 10 streaming in row slices (one per grid.z)
   int tile_m = 0;  // token rows per tile (tiled) or per pass (streaming)
   int ksplit = 1;
   int64_t ws_bytes = 0;  // split-K partials the launch needs

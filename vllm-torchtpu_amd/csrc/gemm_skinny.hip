@@ -305,6 +305,12 @@ __device__ __forceinline__ void store_out(const GemmParams& p, int g, int R, int
 
 // group of this workgroup's slot; false if the slot is empty
 __device__ __forceinline__ bool slot_group(const GemmParams& p, int slot, int& g, int& row0, int& rows) {
+  if (p.row_split) {  // dense: slice `slot` of the rows
+    g = 0;
+    row0 = slot * p.row_split;
+    rows = min(p.row_split, p.M - row0);
+    return rows > 0;
+  }
   if (p.x0 && slot == 0) {
     g = 0;
     row0 = 0;
@@ -1053,6 +1059,16 @@ int qmoe_skinny_launch(int kind, GemmParams p, int max_rows, int slots, void* wo
     p.partial = static_cast<float*>(workspace);
   }
   dim3 grid(n_tiles, pl.ksplit, slots);
+  if (p.row_split) {
+    // row slices: one pass each, no K split, and the weight-tile dimension a
+    // multiple of the 8 XCDs so that every slice's workgroup of a tile runs
+    // on the same XCD (workgroups are dealt to XCDs round robin) and finds
+    // the tile's bytes in that XCD's L2
+    if (p.group_offs || p.active || p.x0 || p.a_quant || pl.ksplit != 1 || p.row_split > 16 * ms ||
+        cdiv(p.M, p.row_split) != slots)
+      return QMOE_ERR_ARG;
+    grid.x = (unsigned)cdiv(n_tiles, 8) * 8;
+  }
   switch (kind) {
     case QK_W8A8_PC:
       if (p.a_quant) {

@@ -258,7 +258,7 @@ def gemm_desc(kind, a, w, *, a_scale=None, w_scale=None, bias=None, wfmt=0, ws_b
 # ---------------------------------------------------------------- kernel plans
 
 PATH_NAMES = ("stream", "tiled_1b", "tiled_4b", "tiled_generic", "stream_passes", "tiled_1b_persistent",
-              "tiled_mx_persistent", "tiled_mx", "stream_dyn", "tiled_1b_n128")
+              "tiled_mx_persistent", "tiled_mx", "stream_dyn", "tiled_1b_n128", "stream_rows")
 
 _plan_log = None
 
