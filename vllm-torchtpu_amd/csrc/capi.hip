@@ -200,7 +200,7 @@ bool use_w4(const qmoe_gemm_desc* d) {
 
 bool use_f8(const qmoe_gemm_desc* d) {
   if (getenv("QMOE_F8_OFF")) return false;  // tuning knob: generic kernel only
-  const bool blk = d->kind == QMOE_W8A8_BLK || (d->kind == QMOE_W8A8_GMM && d->wfmt != 1);
+  const bool blk = d->kind == QMOE_W8A8_BLK || d->kind == QMOE_W8A8_GMM;
   return d->kind == QMOE_W8A8_PC || (blk && !getenv("QMOE_F8_BLK_OFF"));
 }
 

@@ -114,7 +114,7 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
   // weight scale is that of the tile's 128-row block and K block s >> w_kshift;
   // WPC (per-channel weights, the grouped-matmul recipe) applies one scale per
   // weight row in the epilogue instead.
-  static_assert(!BLK || (KB == 128 && !INT && BN == 256), "block scales: FP8, 128-byte stages, 256-row tiles");
+  static_assert(!BLK || (KB == 128 && BN == 256), "block scales: 128-byte stages, 256-row tiles");
   static_assert(!WPC || BLK, "per-channel weight scales with block activation scales");
   using S = F8Shape<BM, BN>;
   constexpr int NI = S::NI, MJ = S::MJ, TN = S::TN, TM = S::TM;
@@ -364,7 +364,8 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
     }
   };
 
-  using Acc = typename std::conditional<INT, i32x16, f32x16>::type;
+  // BLK: the scaled block sums accumulate in f32 for INT8 codes too
+  using Acc = typename std::conditional<INT && !BLK, i32x16, f32x16>::type;
   Acc acc[NI][MJ];
 #pragma unroll
   for (int i = 0; i < NI; ++i)
@@ -374,7 +375,9 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
 
   // BLK: the stage's block sums go to tmp, then acc += tmp * (sx * sw)
-  f32x16 tmp[BLK ? NI : 1][BLK ? MJ : 1];
+  // (INT8 codes: an exact int32 block sum, |sum| < 2^21, converted to f32)
+  using Tmp = typename std::conditional<INT, i32x16, f32x16>::type;
+  Tmp tmp[BLK ? NI : 1][BLK ? MJ : 1];
   float scl[BLK ? NI : 1][BLK ? MJ : 1];
   auto read_scales = [&](const float* sS) {
     if constexpr (BLK) {
@@ -407,7 +410,7 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
                                                                       (int)xsc[t][j]);
       return;
     }
-    if constexpr (INT) {
+    if constexpr (INT && !BLK) {
       // the two 32-k halves of the k-step go to every accumulator in turn:
       // the second MFMA of an accumulator comes NI * MJ MFMAs after its first,
       // so no MFMA waits on the result of the one before it
@@ -428,20 +431,44 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
         // acc += tmp * (sx * sw) of pair p - 1, whose MFMA has completed by
         // then, so the FMAs run on the vector ALU while the matrix core runs
         // the next MFMA (each accumulator still sees the same operations in
-        // the same order)
+        // the same order). INT8: every pair's first 32-k half first, then
+        // the second halves with the scaling behind them.
+        if constexpr (INT) {
+#pragma unroll
+          for (int i = 0; i < NI; ++i)
+#pragma unroll
+            for (int j = 0; j < MJ; ++j)
+              tmp[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(lo4(wf[1][i]), lo4(xf[1][j]), tmp[i][j], 0, 0, 0);
+        }
 #pragma unroll
         for (int q = 0; q <= NI * MJ; ++q) {
           if (q < NI * MJ) {
             const int i = q / MJ, j = q % MJ;
-            tmp[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[1][i], xf[1][j], tmp[i][j], kFw, kFx, 0,
-                                                                        127, 0, 127);
+            if constexpr (INT)
+              tmp[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(hi4(wf[1][i]), hi4(xf[1][j]), tmp[i][j], 0, 0, 0);
+            else
+              tmp[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[1][i], xf[1][j], tmp[i][j], kFw, kFx,
+                                                                          0, 127, 0, 127);
           }
           if (q > 0) {
             const int i = (q - 1) / MJ, j = (q - 1) % MJ;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] += tmp[i][j][r] * scl[i][j];
+            for (int r = 0; r < 16; ++r) acc[i][j][r] += (float)tmp[i][j][r] * scl[i][j];
           }
         }
+        return;
+      }
+      if constexpr (INT) {
+        // the stage's first k-step: fresh block sums, halves as above
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int i = 0; i < NI; ++i)
+#pragma unroll
+            for (int j = 0; j < MJ; ++j)
+              tmp[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(h ? hi4(wf[0][i]) : lo4(wf[0][i]),
+                                                                h ? hi4(xf[0][j]) : lo4(xf[0][j]),
+                                                                h ? tmp[i][j] : i32x16{}, 0, 0, 0);
         return;
       }
     }
@@ -559,7 +586,7 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
   }
 
   if (p.ksplit > 1) {
-    tile_store_partials<BN, TN, TM, NI, MJ, ACT, INT>(p, acc, row0, rows, n0, nlim, wn, wm, lane);
+    tile_store_partials<BN, TN, TM, NI, MJ, ACT, INT && !BLK>(p, acc, row0, rows, n0, nlim, wn, wm, lane);
     return;
   }
   wait_copies_upto<0>();
@@ -1015,14 +1042,15 @@ void f8_launch_bm(const GemmParams& p, int bm, int bn, hipStream_t st) {
   }
 }
 
-// block-scaled FP8: tiles of at most 128 tokens (the per-block sums need a
-// second accumulator set); E5 1: e5m2 weights against e4m3 activations
-template <bool WPC, int E5 = 0>
+// block-scaled tiles: at most 128 tokens (the per-block sums need a second
+// accumulator set); E5 1: e5m2 weights against e4m3 activations; INT: int8
+// codes (the grouped-matmul recipe for int8 weights)
+template <bool INT, bool WPC, int E5 = 0>
 void f8_launch_bm_blk(const GemmParams& p, int bm, hipStream_t st) {
   switch (bm) {
-    case 128: f8_launch_act<false, 128, 256, true, WPC, E5>(p, st); break;
-    case 64: f8_launch_act<false, 64, 256, true, WPC, E5>(p, st); break;
-    default: f8_launch_act<false, 32, 256, true, WPC, E5>(p, st); break;
+    case 128: f8_launch_act<INT, 128, 256, true, WPC, E5>(p, st); break;
+    case 64: f8_launch_act<INT, 64, 256, true, WPC, E5>(p, st); break;
+    default: f8_launch_act<INT, 32, 256, true, WPC, E5>(p, st); break;
   }
 }
 
@@ -1065,9 +1093,8 @@ bool qmoe_f8_plan(const GemmParams& p, bool blk, int* bm_out, int* ksplit_out, i
   // block scales: 128-row weight blocks aligned with the tile's halves
   // (per-channel weight scales need no alignment); 1-byte FP8 codes only
   if (blk && !f8_wpc(p) && (p.ws_bn != 128 || (p.act != QA_NONE && ((p.N / 2) % 128) != 0))) return false;
-  // block scales take float codes: e4m3, or e5m2 weights (the grouped-matmul
-  // recipe; its activations stay e4m3)
-  if (blk && p.wfmt == 1) return false;
+  // block scales take e4m3 codes, e5m2 weights against e4m3 activations or
+  // int8 codes on both operands (the last two: the grouped-matmul recipe)
   if ((p.lda % 16) != 0 || (p.ldw % 16) != 0) return false;
   if ((reinterpret_cast<uintptr_t>(p.a) & 15) || (reinterpret_cast<uintptr_t>(p.w) & 15) ||
       (p.w_gstride % 16) != 0)
@@ -1163,11 +1190,14 @@ int qmoe_f8_launch(GemmParams p, bool blk, void* workspace, int64_t ws_bytes, hi
     p.partial = static_cast<float*>(workspace);
   }
   // e5m2 weights (wfmt 2): against e5m2 activations for per-channel W8A8,
-  // e4m3 ones for the grouped-matmul recipe (per-channel weight scales)
-  if (blk && f8_wpc(p) && p.wfmt == 2) f8_launch_bm_blk<true, 1>(p, bm, st);
-  else if (blk && f8_wpc(p)) f8_launch_bm_blk<true>(p, bm, st);
-  else if (blk && p.wfmt == 2) f8_launch_bm_blk<false, 1>(p, bm, st);
-  else if (blk) f8_launch_bm_blk<false>(p, bm, st);
+  // e4m3 ones for the grouped-matmul recipe; int8 (wfmt 1) block-scaled
+  // tiles: the grouped-matmul recipe for int8 weights
+  if (blk && f8_wpc(p) && p.wfmt == 2) f8_launch_bm_blk<false, true, 1>(p, bm, st);
+  else if (blk && f8_wpc(p) && p.wfmt == 1) f8_launch_bm_blk<true, true>(p, bm, st);
+  else if (blk && f8_wpc(p)) f8_launch_bm_blk<false, true>(p, bm, st);
+  else if (blk && p.wfmt == 2) f8_launch_bm_blk<false, false, 1>(p, bm, st);
+  else if (blk && p.wfmt == 1) f8_launch_bm_blk<true, false>(p, bm, st);
+  else if (blk) f8_launch_bm_blk<false, false>(p, bm, st);
   else if (p.wfmt == 1) f8_launch_bm<true>(p, bm, bn, st);
   else if (p.wfmt == 2) f8_launch_bm<false, 3>(p, bm, bn, st);
   else f8_launch_bm<false>(p, bm, bn, st);
