@@ -264,7 +264,8 @@ def test_w8a8_persistent_tiles(dev, M, K, N, qdtype):
                                    # a K split (tall K, few tokens)
                                    (300, 2048, 1280), (70, 1536, 384), (400, 1024, 2304), (96, 8192, 512),
                                    # wide N (>= 16384 channels): tiled from 17 rows, K split 2 up to
-                                   # 64 tokens, 64-token tiles to 128 and from 257 to 512 tokens
+                                   # 32 tokens, 128-row weight tiles from 33 to 128 and from 257 to
+                                   # 512 tokens (tile scales)
                                    (17, 1024, 16384), (50, 768, 16384), (100, 512, 16512), (260, 512, 16384)])
 @pytest.mark.parametrize("tile_scales", [True, False])
 def test_w8a8_fp8_block(dev, M, K, N, tile_scales):

@@ -114,7 +114,8 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
   // weight scale is that of the tile's 128-row block and K block s >> w_kshift;
   // WPC (per-channel weights, the grouped-matmul recipe) applies one scale per
   // weight row in the epilogue instead.
-  static_assert(!BLK || (KB == 128 && BN == 256), "block scales: 128-byte stages, 256-row tiles");
+  static_assert(!BLK || (KB == 128 && (BN == 256 || (BN == 128 && BM <= 128))),
+                "block scales: 128-byte stages, 256-row tiles or 128-row tiles of <= 128 tokens");
   static_assert(!WPC || BLK, "per-channel weight scales with block activation scales");
   using S = F8Shape<BM, BN>;
   constexpr int NI = S::NI, MJ = S::MJ, TN = S::TN, TM = S::TM;
@@ -386,7 +387,10 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
       for (int j = 0; j < MJ; ++j) sx[j] = sS[wm * TM + j * 32 + rl];
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
-        const float sw = WPC ? 1.0f : sS[BM + wrow(i) / 128];
+        // the tile's 128-row weight blocks: LDS rows 0..127 and 128..255 of a
+        // 256-row tile; with an activation the gate and the up half
+        const int wb = ACT ? (wrow(i) >= BN / 2 ? 1 : 0) : wrow(i) / 128;
+        const float sw = WPC ? 1.0f : sS[BM + wb];
 #pragma unroll
         for (int j = 0; j < MJ; ++j) scl[i][j] = sx[j] * sw;
       }
@@ -1046,7 +1050,15 @@ void f8_launch_bm(const GemmParams& p, int bm, int bn, hipStream_t st) {
 // accumulator set); E5 1: e5m2 weights against e4m3 activations; INT: int8
 // codes (the grouped-matmul recipe for int8 weights)
 template <bool INT, bool WPC, int E5 = 0>
-void f8_launch_bm_blk(const GemmParams& p, int bm, hipStream_t st) {
+void f8_launch_bm_blk(const GemmParams& p, int bm, int bn, hipStream_t st) {
+  if (bn == 128) {
+    // 128-row weight tiles: a fused activation (gate and up halves of 64
+    // rows) needs two weight blocks per wavefront, so 128-token tiles
+    if (bm == 128) f8_launch_act<INT, 128, 128, true, WPC, E5>(p, st);
+    else if (bm == 64) f8_launch_shape<INT, 64, 128, false, true, WPC, E5>(p, st);
+    else f8_launch_shape<INT, 32, 128, false, true, WPC, E5>(p, st);
+    return;
+  }
   switch (bm) {
     case 128: f8_launch_act<INT, 128, 256, true, WPC, E5>(p, st); break;
     case 64: f8_launch_act<INT, 64, 256, true, WPC, E5>(p, st); break;
@@ -1159,8 +1171,19 @@ bool qmoe_f8_plan(const GemmParams& p, bool blk, int* bm_out, int* ksplit_out, i
       ksplit = p.M <= 512 ? 2 : 1;
     }
   }
+  // Dense wide block-scaled problems (the blk_wide rule above) take 128-row
+  // weight tiles where they measured faster on MI355X (K 7168, N 18432 /
+  // 24576): 64 tokens 64 / 1 (35.5 / 39.6 -> 32.6 / 33.7 us), 128 tokens
+  // 128 / 1 (48.8 / 49.5 -> 44.5 / 47.3), 257-512 tokens 64 / 1 (142.0 /
+  // 158.1 -> 121.0 / 147.0); 256 and 1024 tokens keep 256-row tiles
+  if (blk_wide && !env_bm && p.act == QA_NONE && ((p.M > 32 && p.M <= 128) || (p.M > 256 && p.M <= 512))) {
+    bm = p.M <= 64 || p.M > 256 ? 64 : 128;
+    bn = 128;
+    ksplit = 1;
+  }
   const char* env_bn = getenv("QMOE_F8_BN");  // tuning knob: 128 or 256
-  if (env_bn && !blk && p.act == QA_NONE) bn = atoi(env_bn) == 128 ? 128 : 256;
+  if (env_bn && (p.act == QA_NONE || (blk && bm == 128))) bn = atoi(env_bn) == 128 ? 128 : 256;
+  if (blk && bn == 128 && bm > 128) bn = 256;
   const char* env = getenv("QMOE_F8_KSPLIT");  // tuning knob
   if (env && atoi(env) > 0) ksplit = std::max(1, std::min(atoi(env), p.K / 256));
   if (bn_out) *bn_out = bn;
@@ -1192,12 +1215,12 @@ int qmoe_f8_launch(GemmParams p, bool blk, void* workspace, int64_t ws_bytes, hi
   // e5m2 weights (wfmt 2): against e5m2 activations for per-channel W8A8,
   // e4m3 ones for the grouped-matmul recipe; int8 (wfmt 1) block-scaled
   // tiles: the grouped-matmul recipe for int8 weights
-  if (blk && f8_wpc(p) && p.wfmt == 2) f8_launch_bm_blk<false, true, 1>(p, bm, st);
-  else if (blk && f8_wpc(p) && p.wfmt == 1) f8_launch_bm_blk<true, true>(p, bm, st);
-  else if (blk && f8_wpc(p)) f8_launch_bm_blk<false, true>(p, bm, st);
-  else if (blk && p.wfmt == 2) f8_launch_bm_blk<false, false, 1>(p, bm, st);
-  else if (blk && p.wfmt == 1) f8_launch_bm_blk<true, false>(p, bm, st);
-  else if (blk) f8_launch_bm_blk<false, false>(p, bm, st);
+  if (blk && f8_wpc(p) && p.wfmt == 2) f8_launch_bm_blk<false, true, 1>(p, bm, bn, st);
+  else if (blk && f8_wpc(p) && p.wfmt == 1) f8_launch_bm_blk<true, true>(p, bm, bn, st);
+  else if (blk && f8_wpc(p)) f8_launch_bm_blk<false, true>(p, bm, bn, st);
+  else if (blk && p.wfmt == 2) f8_launch_bm_blk<false, false, 1>(p, bm, bn, st);
+  else if (blk && p.wfmt == 1) f8_launch_bm_blk<true, false>(p, bm, bn, st);
+  else if (blk) f8_launch_bm_blk<false, false>(p, bm, bn, st);
   else if (p.wfmt == 1) f8_launch_bm<true>(p, bm, bn, st);
   else if (p.wfmt == 2) f8_launch_bm<false, 3>(p, bm, bn, st);
   else f8_launch_bm<false>(p, bm, bn, st);
