@@ -1181,6 +1181,11 @@ bool qmoe_f8_plan(const GemmParams& p, bool blk, int* bm_out, int* ksplit_out, i
     bn = 128;
     ksplit = 1;
   }
+  // Grouped 128 x 128-tile problems without an activation (the MoE down
+  // projection) in 32- or 64-token tiles: 128-row weight tiles, measured on
+  // MI355X (DeepSeek-V3 layer, native tiles) T = 256 / 512 1373.6 / 1566.8
+  // -> 1319.1 / 1517.9 us; 128-token tiles (T = 4096) lose with them
+  if (blk && p.group_offs && !f8_wpc(p) && p.act == QA_NONE && !env_bm && bm <= 64) bn = 128;
   const char* env_bn = getenv("QMOE_F8_BN");  // tuning knob: 128 or 256
   if (env_bn && (p.act == QA_NONE || (blk && bm == 128))) bn = atoi(env_bn) == 128 ? 128 : 256;
   if (blk && bn == 128 && bm > 128) bn = 256;
