@@ -57,7 +57,7 @@ def test_graph_replays_after_a_larger_call(dev):
 
     print("workspace: graph capture of split-K gemm + moe_decode, larger eager calls between replays", flush=True)
     small, _, need_small = _splitk_problem(dev, 1, 4, 1024, 14336)
-    big, big_ref, need_big = _splitk_problem(dev, 2, 32, 4096, 14336)
+    big, big_ref, need_big = _splitk_problem(dev, 2, 48, 4096, 14336)
     assert need_big > need_small
     L = _layer(11, 32, 1024, 512, 256, 5, 6)
     x = _td(L["hidden"], dev, torch.bfloat16)
