@@ -233,15 +233,18 @@ SHAPES_PERSISTENT = [(2000, 1024, 8200), (4096, 512, 4352), (1300, 2048, 14336)]
 
 @pytest.mark.parametrize("M,K,N", SHAPES_PERSISTENT)
 @pytest.mark.parametrize("qdtype", ["fp8", "int8"])
-def test_w8a8_persistent_tiles(dev, M, K, N, qdtype):
-    """The persistent 256 x 256 kernel against the oracle (FP8 within one
-    bf16 ulp of the same-code oracle, INT8 bit-exact), and the plan reports
-    it."""
+@pytest.mark.parametrize("pbn", ["256", "224"])
+def test_w8a8_persistent_tiles(dev, monkeypatch, M, K, N, qdtype, pbn):
+    """The persistent kernel in both tile heights (256 x 256, and 256
+    tokens x 224 weight rows: ragged channel tiles at N 8200 and 4352)
+    against the oracle (FP8 within one bf16 ulp of the same-code oracle, INT8
+    bit-exact), and the plan reports it."""
     from qmoe import _capi, ops
 
+    monkeypatch.setenv("QMOE_F8_PERSIST_BN", pbn)
     wf = int(qdtype == "int8")
     plan = ops.plan_for_shape(_capi.W8A8_PC, M, N, K, wfmt=wf)
-    print(f"w8a8 persistent {qdtype} M={M} K={K} N={N} plan={plan}", flush=True)
+    print(f"w8a8 persistent {qdtype} M={M} K={K} N={N} rows={pbn} plan={plan}", flush=True)
     assert plan[4:] == ("tiled_1b_persistent", 256, 1), plan
     rng = np.random.default_rng(M + 5 * K + N + wf)
     w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)

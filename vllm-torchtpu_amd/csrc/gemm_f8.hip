@@ -635,14 +635,23 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
 // the sums come out scaled and the epilogue adds only the bias. The stage's
 // scale bytes ([256 rows][8 bytes] per operand) ride in the stage's copies
 // (dword LDS copies) into LDS arrays beside the code buffers.
-template <int MODE>
+//
+// BN (weight rows per tile) is 256, or 224 for 1-byte codes: the wavefronts
+// then form a 1 x 4 grid of 224 weight rows x 64 tokens each (7 x 2 blocks).
+// Measured on MI355X (FP8, 4096 tokens): a 256-wide tile's MFMA loop alone
+// (no copies, no operand reads, no barriers) runs at ~3.6 PFLOP/s, so the
+// tile count per round matters as much as the loop: N = 14336 makes 896
+// tiles of 256 x 256 -- 4 rounds on 224 of the 256 CUs -- but 1024 tiles of
+// 256 x 224, 4 rounds on all 256.
+template <int MODE, int BN = 256>
 __global__ __launch_bounds__(kThreads) void f8_persistent_kernel(const GemmParams p, int m_tiles, int n_tiles,
                                                                  int tile_slots) {
   constexpr bool INT = MODE == 1, MX = MODE == 2;
   constexpr bool ACT = false;  // fused activations take the one-tile kernel
-  constexpr int BM = 256, BN = 256, KB = 128;
-  using S = F8Shape<BM, BN>;
-  constexpr int NI = S::NI, MJ = S::MJ, TN = S::TN, TM = S::TM;
+  constexpr int BM = 256, KB = 128;
+  static_assert(BN == 256 || (BN == 224 && !MX), "weight tile height");
+  constexpr int WN = BN == 256 ? 2 : 1, WM = 4 / WN;  // wavefront grid (weight rows x tokens)
+  constexpr int TN = BN / WN, TM = BM / WM, NI = TN / 32, MJ = TM / 32;
   __shared__ __align__(1024) uint8_t sW0[BN * KB], sW1[BN * KB];
   __shared__ __align__(1024) uint8_t sX0[BM * KB], sX1[BM * KB];
   // MX scale bytes of the two stage buffers ([row][8], 32 k per byte)
@@ -657,7 +666,7 @@ __global__ __launch_bounds__(kThreads) void f8_persistent_kernel(const GemmParam
   // the wavefront index in an SGPR: the LDS destinations of the copies are
   // then scalar (M0) values instead of VGPRs held across the K loop
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wn = wave % S::WN, wm = wave / S::WN;
+  const int wn = wave % WN, wm = wave / WN;
   const int nlim = ACT ? p.N / 2 : p.N;
   constexpr int BNO = ACT ? BN / 2 : BN;
   constexpr int RPI = 8;                   // rows per copy instruction (128-byte rows)
@@ -868,7 +877,7 @@ __global__ __launch_bounds__(kThreads) void f8_persistent_kernel(const GemmParam
     // the epilogue vectors have landed (the wait in stage 0 covers every
     // earlier load); the stage barriers ahead make them visible
     s_sx[par][tid] = e_sx;
-    s_ws[par][tid] = e_ws;
+    if (BN == 256 || tid < BN) s_ws[par][tid] = e_ws;
     stage(sW1, sX1, sQW1, sQX1, sW0, sX0, sQW0, sQX0, 3, false);
     for (int s = 2; s < KS - 2; s += 2) {
       stage(sW0, sX0, sQW0, sQX0, sW1, sX1, sQW1, sQX1, s + 2, false);
@@ -960,14 +969,10 @@ __global__ __launch_bounds__(kThreads) void f8_persistent_kernel(const GemmParam
   }
 }
 
-// Workgroups of the persistent 256 x 256 tile kernel for `tiles` tiles: as
-// few tile rounds as the CUs of the current device allow, spread evenly
-// (896 tiles on 256 CUs: 4 rounds on 224 workgroups, not 3.5 on 256;
-// measured on MI355X, 216 vs 222 us for Llama-3-8B's up projection at 4096
-// tokens), rounded up to a multiple of the 8 XCDs. 0 when the tiles fit one
-// round (the one-tile kernel then runs) or the tuning knob QMOE_F8_PERSIST=0
-// turns the kernel off; another value of the knob caps the workgroups.
-int f8_persistent_grid(int tiles) {
+// CUs the persistent kernel may use, a multiple of the 8 XCDs: 0 when the
+// tuning knob QMOE_F8_PERSIST=0 turns the kernel off; another value of the
+// knob caps them.
+int f8_persistent_cus() {
   const char* env = getenv("QMOE_F8_PERSIST");  // tuning knob
   if (env && atoi(env) == 0) return 0;
   int dev = 0, cus = 0;
@@ -975,10 +980,40 @@ int f8_persistent_grid(int tiles) {
                                                hipSuccess)
     return 0;
   if (env && atoi(env) >= kXcds) cus = std::min(cus, atoi(env));
-  cus = cus / kXcds * kXcds;
+  return cus / kXcds * kXcds;
+}
+
+// Workgroups of the persistent tile kernel for `tiles` tiles: as few tile
+// rounds as the CUs allow, spread evenly (896 tiles on 256 CUs: 4 rounds on
+// 224 workgroups, not 3.5 on 256; measured on MI355X, 216 vs 222 us for
+// Llama-3-8B's up projection at 4096 tokens), rounded up to a multiple of
+// the 8 XCDs. 0 when the tiles fit one round (the one-tile kernel then runs)
+// or the kernel is off.
+int f8_persistent_grid(int tiles) {
+  const int cus = f8_persistent_cus();
   if (cus <= 0 || tiles <= cus / 2) return 0;
   const int rounds = cdiv(tiles, cus);
   return std::min(cus, cdiv(cdiv(tiles, rounds), kXcds) * kXcds);
+}
+
+// Weight rows per persistent tile: 224 where its tile rounds times rows,
+// weighted by 17/16, are fewer than 256's on this device's CUs, else 256. A
+// round's time follows the tile height, and a 224-row tile does ~6 % less
+// per row than a 256-row one (7 x 2 blocks per wavefront instead of 4 x 4:
+// more operand reads per MFMA). Measured on MI355X, Llama-3-8B's up
+// projection (N 14336) at 4096 tokens, 1024 tiles in 4 rounds of 224 rows
+// instead of 896 in 4 rounds of 256: 222.0 -> 207.8 us (FP8), 233.6 ->
+// 216.7 us (INT8); at 8192 tokens (7 rounds of 256 against 8 of 224) 394 vs
+// 418 us. The tuning knob QMOE_F8_PERSIST_BN (224 or 256) forces one.
+int f8_persistent_bn(const GemmParams& p) {
+  const char* env = getenv("QMOE_F8_PERSIST_BN");  // tuning knob
+  if (env && (atoi(env) == 224 || atoi(env) == 256)) return atoi(env);
+  const int cus = f8_persistent_cus();
+  if (cus <= 0) return 256;
+  const int mt = cdiv(p.M, 256);
+  const int64_t c256 = (int64_t)cdiv(mt * cdiv(p.N, 256), cus) * 256;
+  const int64_t c224 = (int64_t)cdiv(mt * cdiv(p.N, 224), cus) * 224;
+  return c224 * 17 < c256 * 16 ? 224 : 256;
 }
 
 // Whether a dense problem with this plan runs the persistent kernel: 256 x
@@ -1012,8 +1047,14 @@ void f8_launch_shape(const GemmParams& p, hipStream_t st) {
     const int grid = cdiv(m_tiles * n_tiles, kXcds) * kXcds;
     if constexpr (BM == 256 && BN == 256 && !BLK && !ACT && E5 == 0) {
       if (kb == 128 && f8_persistent_ok(p, BLK, BM, (int)ks)) {
-        hipLaunchKernelGGL((f8_persistent_kernel<INT ? 1 : 0>), dim3(f8_persistent_grid(m_tiles * n_tiles)),
-                           dim3(kThreads), 0, st, p, m_tiles, n_tiles, grid);
+        const int pbn = f8_persistent_bn(p);
+        const int pn = cdiv(p.N, pbn), tiles = m_tiles * pn, slots = cdiv(tiles, kXcds) * kXcds;
+        if (pbn == 224)
+          hipLaunchKernelGGL((f8_persistent_kernel<INT ? 1 : 0, 224>), dim3(f8_persistent_grid(tiles)),
+                             dim3(kThreads), 0, st, p, m_tiles, pn, slots);
+        else
+          hipLaunchKernelGGL((f8_persistent_kernel<INT ? 1 : 0>), dim3(f8_persistent_grid(tiles)), dim3(kThreads),
+                             0, st, p, m_tiles, pn, slots);
         return;
       }
     }
