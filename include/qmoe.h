@@ -176,8 +176,8 @@ int qmoe_gemm_workspace_size(const qmoe_gemm_desc* d, int64_t* bytes);
  * from the descriptor alone (no device memory is read): path 0 weight
  * streaming, 1 1-byte x 1-byte tiles, 2 bf16 x 4-bit tiles, 3 generic
  * tiles, 4 weight streaming in 64-row passes, 5 1-byte x 1-byte tiles of
- * 256 tokens x 256 or 224 weight rows on persistent workgroups (at most one
- * per CU of the current device), 6 MX
+ * 256 tokens x 256 or 224 weight rows, or 128 tokens x 224 rows, on
+ * persistent workgroups (at most one per CU of the current device), 6 MX
  * 256 x 256 persistent tiles, 7 MX grouped tiles, 8 weight streaming with
  * the per-row activation quantization inside (QMOE_W8A8_PC_DYN; for the
  * kind's other problems the path of the GEMM after its separate

@@ -262,6 +262,41 @@ def test_w8a8_persistent_tiles(dev, monkeypatch, M, K, N, qdtype, pbn):
         assert_close_same_codes(got, ref, f"fp8 persistent {M}x{K}x{N}")
 
 
+@pytest.mark.parametrize("M,K,N", [(1000, 2048, 7000), (512, 4096, 14336), (300, 1024, 14336)])
+@pytest.mark.parametrize("qdtype", ["fp8", "int8"])
+def test_w8a8_persistent_mid_tiles(dev, monkeypatch, M, K, N, qdtype):
+    """Mid-size problems whose 64- or 128-token one-tile grid takes more
+    tile rounds x area run the persistent kernel in 128-token x 224-row tiles
+    (ragged last token and channel tiles at 1000 x 7000 and 300 tokens; 300
+    tokens would take 64-token one-tile tiles): against the oracle, and
+    bit-identical to the one-tile kernel (the same MFMA sequence per
+    output)."""
+    from qmoe import _capi, ops
+
+    wf = int(qdtype == "int8")
+    plan = ops.plan_for_shape(_capi.W8A8_PC, M, N, K, wfmt=wf)
+    print(f"w8a8 persistent mid {qdtype} M={M} K={K} N={N} plan={plan}", flush=True)
+    assert plan[4:] == ("tiled_1b_persistent", 128, 1), plan
+    rng = np.random.default_rng(M + 3 * K + N + wf)
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    wq, ws = quant.quantize_tensor(w, qdtype)
+    x = _bf16(rng, (M, K))
+    xq, xs = ops.row_quant(_t(x, dev, torch.bfloat16), qdtype)
+    wt, wst = _t(wq.view(np.uint8), dev), _t(ws, dev)
+    y = ops.gemm(_capi.W8A8_PC, xq.view(torch.uint8), wt, a_scale=xs, w_scale=wst, wfmt=wf)
+    monkeypatch.setenv("QMOE_F8_PERSIST_BN", "256")  # the one-tile 128 x 256 kernel
+    y1 = ops.gemm(_capi.W8A8_PC, xq.view(torch.uint8), wt, a_scale=xs, w_scale=wst, wfmt=wf)
+    assert ops.plan_for_shape(_capi.W8A8_PC, M, N, K, wfmt=wf)[4] == "tiled_1b"
+    assert torch.equal(y.view(torch.int16), y1.view(torch.int16))
+    r = np.unique(np.linspace(0, M - 1, 6).round().astype(np.int64))
+    ref, _, _ = linear.w8a8_per_channel(x[r], wq, ws, qdtype)
+    got = y[torch.from_numpy(r).to(dev)].float().cpu().numpy()
+    if qdtype == "int8":
+        np.testing.assert_array_equal(got, ref)
+    else:
+        assert_close_same_codes(got, ref, f"fp8 persistent mid {M}x{K}x{N}")
+
+
 @pytest.mark.parametrize("M,K,N", [(1, 1024, 512), (32, 2048, 768), (130, 1024, 640), (256, 2048, 1024),
                                    # tiled block-scaled kernel: ragged tiles, 32/64/128-token tiles,
                                    # a K split (tall K, few tokens)

@@ -211,7 +211,7 @@ enum Path {
   kPathW4 = 2,          // bf16 x 4-bit tiles
   kPathTiled = 3,       // generic tiles
   kPathSkinnyPass = 4,  // weight streaming in 64-row passes (K outside every tiled granule)
-  kPathF8Persistent = 5,  // 1-byte x 1-byte 256 x 256 tiles, persistent workgroups
+  kPathF8Persistent = 5,  // 1-byte x 1-byte tiles (256 or 128 tokens), persistent workgroups
   kPathMx = 6,            // e2m1 x e2m1 with e8m0 scales on both, 256 x 256 persistent tiles
   kPathMxTiles = 7,       // the same operands, grouped tiles (one tile per workgroup)
   kPathSkinnyDyn = 8,     // weight streaming with the per-row activation quantization inside
@@ -337,7 +337,8 @@ int qmoe_route_of(const qmoe_gemm_desc* d, GemmParams& p, QmoeRoute* r) {
     if (use_f8(d) && qmoe_f8_plan(p, kind == QK_W8A8_BLK, &bm, &ks, &ws, &bn)) {
       const int path = bn == 128 ? kPathF8Narrow
                                  : (qmoe_f8_persistent(p, kind == QK_W8A8_BLK) ? kPathF8Persistent : kPathF8);
-      *r = QmoeRoute{path, bm, ks, ws};
+      // persistent tiles hold 128 or 256 tokens (a 64-token plan runs 128)
+      *r = QmoeRoute{path, path == kPathF8Persistent ? std::max(bm, 128) : bm, ks, ws};
       return QMOE_OK;
     }
     if (!use_f8(d) && use_w4(d) && qmoe_w4_plan(p, w4_fmt(d), &bm, &ks, &ws)) {

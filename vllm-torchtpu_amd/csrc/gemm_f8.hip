@@ -643,13 +643,18 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
 // tile count per round matters as much as the loop: N = 14336 makes 896
 // tiles of 256 x 256 -- 4 rounds on 224 of the 256 CUs -- but 1024 tiles of
 // 256 x 224, 4 rounds on all 256.
-template <int MODE, int BN = 256>
+//
+// BM (tokens per tile) is 256, or 128 for 1-byte codes (mid-size problems
+// whose 128 x 256 tiles leave CUs idle: 512 tokens of Llama-3-8B's up
+// projection make 224 such tiles, but 256 of 128 x 224).
+template <int MODE, int BN = 256, int BM = 256>
 __global__ __launch_bounds__(kThreads) void f8_persistent_kernel(const GemmParams p, int m_tiles, int n_tiles,
                                                                  int tile_slots) {
   constexpr bool INT = MODE == 1, MX = MODE == 2;
   constexpr bool ACT = false;  // fused activations take the one-tile kernel
-  constexpr int BM = 256, KB = 128;
+  constexpr int KB = 128;
   static_assert(BN == 256 || (BN == 224 && !MX), "weight tile height");
+  static_assert(BM == 256 || (BM == 128 && !MX), "token tile height");
   constexpr int WN = BN == 256 ? 2 : 1, WM = 4 / WN;  // wavefront grid (weight rows x tokens)
   constexpr int TN = BN / WN, TM = BM / WM, NI = TN / 32, MJ = TM / 32;
   __shared__ __align__(1024) uint8_t sW0[BN * KB], sW1[BN * KB];
@@ -876,7 +881,7 @@ __global__ __launch_bounds__(kThreads) void f8_persistent_kernel(const GemmParam
     stage(sW0, sX0, sQW0, sQX0, sW1, sX1, sQW1, sQX1, 2, false);
     // the epilogue vectors have landed (the wait in stage 0 covers every
     // earlier load); the stage barriers ahead make them visible
-    s_sx[par][tid] = e_sx;
+    if (BM == 256 || tid < BM) s_sx[par][tid] = e_sx;
     if (BN == 256 || tid < BN) s_ws[par][tid] = e_ws;
     stage(sW1, sX1, sQW1, sQX1, sW0, sX0, sQW0, sQX0, 3, false);
     for (int s = 2; s < KS - 2; s += 2) {
@@ -1021,13 +1026,43 @@ int f8_persistent_bn(const GemmParams& p) {
 // 128-byte stages (the default of the QMOE_F8_KB knob), K >= 512, plain
 // row-major output with N % 8 == 0 and 16-byte aligned rows below 2 GiB, no
 // bias, row gather / scatter or routing weights, and more tiles than CUs.
-bool f8_persistent_ok(const GemmParams& p, bool blk, int bm, int ksplit) {
-  if (blk || bm != 256 || ksplit != 1 || p.group_offs || p.act != QA_NONE || p.K < 512 || p.wfmt > 1) return false;
+bool f8_persistent_form_ok(const GemmParams& p, bool blk, int ksplit) {
+  if (blk || ksplit != 1 || p.group_offs || p.act != QA_NONE || p.K < 512 || p.wfmt > 1) return false;
   const char* env = getenv("QMOE_F8_KB");
   if (env && atoi(env) == 64) return false;
   if ((p.N % 8) != 0 || (p.ldy % 8) != 0 || (reinterpret_cast<uintptr_t>(p.y) & 15) != 0) return false;
-  if (p.a_rows || p.y_rows || p.row_weight || p.bias || (int64_t)p.M * p.ldy * 2 >= 0x7fffffffLL) return false;
-  return f8_persistent_grid(cdiv(p.M, 256) * cdiv(p.N, 256)) > 0;
+  return !(p.a_rows || p.y_rows || p.row_weight || p.bias || (int64_t)p.M * p.ldy * 2 >= 0x7fffffffLL);
+}
+
+bool f8_persistent_ok(const GemmParams& p, bool blk, int bm, int ksplit) {
+  return bm == 256 && f8_persistent_form_ok(p, blk, ksplit) && f8_persistent_grid(cdiv(p.M, 256) * cdiv(p.N, 256)) > 0;
+}
+
+// Whether a problem planned on one-tile 64- or 128-token x 256-row tiles
+// runs the persistent kernel in tiles of 128 tokens x 224 weight rows
+// instead: the same form, and fewer tile rounds times tile area (the 224-row
+// tile weighted as in f8_persistent_bn). Measured on MI355X, Llama-3-8B's up
+// projection (K 4096, N 14336): 512 tokens 39.7 -> 36.0 us (256 tiles on 256
+// CUs instead of 224 one-tile workgroups), 640 67.1 -> 58.5, 768 67.4 ->
+// 59.7; 1000 x 7000 (K 2048) 25.4 -> 20.7 us.
+bool f8_persistent_mid_ok(const GemmParams& p, bool blk, int bm, int bn, int ksplit) {
+  if ((bm != 128 && bm != 64) || bn != 256 || !f8_persistent_form_ok(p, blk, ksplit)) return false;
+  const char* env = getenv("QMOE_F8_PERSIST_BN");  // tuning knob: 256 keeps the one-tile kernel
+  if (env && atoi(env) == 256) return false;
+  const int cus = f8_persistent_cus();
+  if (cus <= 0) return false;
+  const int mid = cdiv(p.M, 128) * cdiv(p.N, 224);
+  const int64_t c_cur = (int64_t)cdiv(cdiv(p.M, bm) * cdiv(p.N, 256), cus) * bm * 256 * 16;
+  const int64_t c_mid = (int64_t)cdiv(mid, cus) * 128 * 224 * 17;
+  return c_mid < c_cur && f8_persistent_grid(mid) > 0;
+}
+
+// The persistent kernel in 128 x 224 tiles (f8_persistent_mid_ok holds).
+template <bool INT>
+void f8_launch_mid(const GemmParams& p, hipStream_t st) {
+  const int mt = cdiv(p.M, 128), pn = cdiv(p.N, 224), tiles = mt * pn;
+  hipLaunchKernelGGL((f8_persistent_kernel<INT ? 1 : 0, 224, 128>), dim3(f8_persistent_grid(tiles)), dim3(kThreads),
+                     0, st, p, mt, pn, cdiv(tiles, kXcds) * kXcds);
 }
 
 template <bool INT, int BM, int BN, bool ACT, bool BLK, bool WPC = false, int E5 = 0>
@@ -1243,7 +1278,8 @@ bool qmoe_f8_plan(const GemmParams& p, bool blk, int* bm_out, int* ksplit_out, i
 bool qmoe_f8_persistent(const GemmParams& p, bool blk) {
   int bm = 0, ksplit = 1, bn = 256;
   int64_t ws = 0;
-  return qmoe_f8_plan(p, blk, &bm, &ksplit, &ws, &bn) && bn == 256 && f8_persistent_ok(p, blk, bm, ksplit);
+  return qmoe_f8_plan(p, blk, &bm, &ksplit, &ws, &bn) && bn == 256 &&
+         (f8_persistent_ok(p, blk, bm, ksplit) || f8_persistent_mid_ok(p, blk, bm, bn, ksplit));
 }
 
 // Launch per the plan (the caller checked qmoe_f8_plan and sized the
@@ -1267,6 +1303,7 @@ int qmoe_f8_launch(GemmParams p, bool blk, void* workspace, int64_t ws_bytes, hi
   else if (blk && p.wfmt == 2) f8_launch_bm_blk<false, false, 1>(p, bm, bn, st);
   else if (blk && p.wfmt == 1) f8_launch_bm_blk<true, false>(p, bm, bn, st);
   else if (blk) f8_launch_bm_blk<false, false>(p, bm, bn, st);
+  else if (f8_persistent_mid_ok(p, blk, bm, bn, ksplit)) p.wfmt == 1 ? f8_launch_mid<true>(p, st) : f8_launch_mid<false>(p, st);
   else if (p.wfmt == 1) f8_launch_bm<true>(p, bm, bn, st);
   else if (p.wfmt == 2) f8_launch_bm<false, 3>(p, bm, bn, st);
   else f8_launch_bm<false>(p, bm, bn, st);
