@@ -57,14 +57,14 @@ def parse():
     ap.add_argument("--only", default="", help="comma list of sweep configs to run (0-4; 5 = NVFP4 / INT4; "
                                                 "v = hipBLASLt reference points)")
     ap.add_argument("--profile", nargs="?", const="headline", default=None,
-                    choices=["headline", "decode", "moe", "vendor", "floor", "w4", "mx", "midm"],
+                    choices=["headline", "decode", "moe", "vendor", "floor", "w4", "mx", "midm", "moet"],
                     help="rocprofv3 targets: the headline kernel + a copy calibration (default), "
                          "the decode GEMMs (cfg 0/1/2 at M=1), the MoE layers at T=1 (cfg 3/4), "
                          "this build's FP8 GEMM beside hipBLASLt's (torch._scaled_mm) on both cfg 1 "
                          "shapes at M=4096, the plain-read floor (time vs size), the large-M MXFP4 "
                          "path (cfg 0 at M=8192, cfg 3 at T=8192), or the opt-in MX activation path "
-                         "(cfg 0 at M=8192, cfg 3 at T=8192), or the mid-M linears (cfg 0 M=128, cfg 1 "
-                         "M=64 / 512, cfg 2 M=256)")
+                         "(cfg 0 at M=8192, cfg 3 at T=8192), the mid-M linears (cfg 0 M=128, cfg 1 "
+                         "M=64 / 512, cfg 2 M=256), or the cfg 4 MoE layers at T=512 / 4096")
     return ap.parse_args()
 
 
@@ -1226,6 +1226,65 @@ def profile_midm(args):
     log("profile target done")
 
 
+def profile_moet(args):
+    """rocprofv3 target: config 4 (DeepSeek-V3, 256 experts, top-8 grouped)
+    routed MoE layers at T = 512 and 4096 -- 6 layers each with the native
+    128 x 128 FP8 tiles (format fp8_block), then 6 each through the method's
+    default recipe (per-channel e4m3 experts, per-(token, 512) activation
+    codes, format fp8) -- after 2 warm-up layers each; then a plain 256 MiB
+    copy (10 launches) for the FETCH_SIZE / WRITE_SIZE calibration."""
+    import torch
+
+    from qmoe.layers.fused_moe import moe_forward
+    from qmoe.layers.quantization.fp8 import dequantize_fp8_weight, requantize
+
+    gen = torch.Generator(device="cuda").manual_seed(4)
+    E, k, H, I = 256, 8, 7168, 2048
+    w13 = torch.empty((E, 2 * I, H), device="cuda", dtype=torch.float8_e4m3fn)
+    s13 = torch.empty((E, 2 * I // 128, H // 128), device="cuda", dtype=torch.float32)
+    w2 = torch.empty((E, H, I), device="cuda", dtype=torch.float8_e4m3fn)
+    s2 = torch.empty((E, H // 128, I // 128), device="cuda", dtype=torch.float32)
+    for e in range(E):
+        w13[e], s13[e] = fp8_weights(2 * I, H, gen, tiles=True)
+        w2[e], s2[e] = fp8_weights(H, I, gen, tiles=True)
+    bias = torch.randn(E, device="cuda", generator=gen) * 0.1
+    lcfg = moe_layer_cfg(k, "sigmoid", "silu", bias=bias, rsf=2.5, groups=(8, 4))
+    inputs = {}
+    for T in (512, 4096):
+        inputs[T] = (torch.randn((T, H), device="cuda", generator=gen).to(torch.bfloat16),
+                     torch.randn((T, E), device="cuda", generator=gen).to(torch.bfloat16))
+    for T, (x, logits) in inputs.items():
+        for _ in range(8):
+            moe_forward(lcfg, x, logits, w13, w2, s13, s2, None, None, "fp8_block")
+        torch.cuda.synchronize()
+        log(f"profile target: cfg4 fp8_block T={T} x8")
+
+    def per_channel(w, s):
+        q = torch.empty(w.shape, dtype=torch.float8_e4m3fn, device=w.device)
+        sc = torch.empty(w.shape[:-1], dtype=torch.float32, device=w.device)
+        for e in range(w.shape[0]):
+            q[e], sc[e] = requantize(dequantize_fp8_weight(w[e], weight_scale_inv=s[e], block=(128, 128)),
+                                     "float8_e4m3fn")
+        return q, sc
+
+    q13, c13 = per_channel(w13, s13)
+    del w13, s13
+    q2, c2 = per_channel(w2, s2)
+    del w2, s2
+    for T, (x, logits) in inputs.items():
+        for _ in range(8):
+            moe_forward(lcfg, x, logits, q13, q2, c13, c2, None, None, "fp8")
+        torch.cuda.synchronize()
+        log(f"profile target: cfg4 fp8 default recipe T={T} x8")
+    del q13, q2
+    src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log("profile target done: copy 256MiB x10")
+
+
 def profile_floor(args):
     """rocprofv3 target: the plain-read floor curve (qmoe_stream_read over
     FLOOR_MB sizes), printed as one JSON line."""
@@ -1236,7 +1295,8 @@ def main():
     args = parse()
     if args.profile:
         {"headline": profile_target, "decode": profile_decode, "moe": profile_moe, "vendor": profile_vendor,
-         "floor": profile_floor, "w4": profile_w4, "mx": profile_mx, "midm": profile_midm}[args.profile](args)
+         "floor": profile_floor, "w4": profile_w4, "mx": profile_mx, "midm": profile_midm,
+         "moet": profile_moet}[args.profile](args)
         return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (got --gpus {args.gpus}); "
