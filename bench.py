@@ -1253,11 +1253,15 @@ def profile_moet(args):
     for T in (512, 4096):
         inputs[T] = (torch.randn((T, H), device="cuda", generator=gen).to(torch.bfloat16),
                      torch.randn((T, E), device="cuda", generator=gen).to(torch.bfloat16))
+    from qmoe import ops
+
     for T, (x, logits) in inputs.items():
         for _ in range(8):
             moe_forward(lcfg, x, logits, w13, w2, s13, s2, None, None, "fp8_block")
         torch.cuda.synchronize()
-        log(f"profile target: cfg4 fp8_block T={T} x8")
+        _, ids = ops.moe_route(logits, k, "sigmoid", True, bias=bias, routed_scaling_factor=2.5, num_expert_group=8,
+                               topk_group=4)
+        log(f"profile target: cfg4 fp8_block T={T} x8, {int(torch.unique(ids).numel())} experts routed")
 
     def per_channel(w, s):
         q = torch.empty(w.shape, dtype=torch.float8_e4m3fn, device=w.device)

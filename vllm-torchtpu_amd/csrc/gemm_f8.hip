@@ -339,32 +339,6 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
   // MX: scale dword of half t (32-k blocks 4t + 2h + kh), shifted so that
   // byte 2h is the lane's block of step h
   uint32_t wsc[2][MX ? NI : 1], xsc[2][MX ? MJ : 1];
-  // operands of k-step `ks` of the stage in (sW, sX) into register set t
-  auto read_frags = [&](const uint8_t* sW, const uint8_t* sX, const uint8_t* sQW, const uint8_t* sQX, int ks,
-                        int t) {
-    if constexpr (MX) {
-      // block of 32 rows at 8 (first row) bytes, dword plane ks, row rl
-#pragma unroll
-      for (int i = 0; i < NI; ++i)
-        wsc[t][i] = *reinterpret_cast<const uint32_t*>(sQW + wrow(i) * 8 + ks * 128 + rl * 4) >> (8 * kh);
-#pragma unroll
-      for (int j = 0; j < MJ; ++j)
-        xsc[t][j] =
-            *reinterpret_cast<const uint32_t*>(sQX + (wm * TM + j * 32) * 8 + ks * 128 + rl * 4) >> (8 * kh);
-    }
-    const int h0 = KB == 64 ? po[0][0] : po[ks][0], h1 = KB == 64 ? po[0][1] : po[ks][1];
-#pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const uint8_t* b = sW + wrow(i) * KB;
-      wf[t][i] = lds_frag(b + h0, b + h1);
-    }
-#pragma unroll
-    for (int j = 0; j < MJ; ++j) {
-      const uint8_t* b = sX + (wm * TM + j * 32) * KB;
-      xf[t][j] = lds_frag(b + h0, b + h1);
-    }
-  };
-
   // BLK: the scaled block sums accumulate in f32 for INT8 codes too
   using Acc = typename std::conditional<INT && !BLK, i32x16, f32x16>::type;
   Acc acc[NI][MJ];
@@ -380,215 +354,258 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
   using Tmp = typename std::conditional<INT, i32x16, f32x16>::type;
   Tmp tmp[BLK ? NI : 1][BLK ? MJ : 1];
   float scl[BLK ? NI : 1][BLK ? MJ : 1];
-  auto read_scales = [&](const float* sS) {
-    if constexpr (BLK) {
-      float sx[MJ];
+  // The K pipeline over the wavefront's first MJE 32-token blocks (MJ: all
+  // of them); the accumulators of the others keep their zeros.
+  auto pipeline = [&](auto mje_c) {
+    constexpr int MJE = decltype(mje_c)::value;
+    // operands of k-step `ks` of the stage in (sW, sX) into register set t
+    auto read_frags = [&](const uint8_t* sW, const uint8_t* sX, const uint8_t* sQW, const uint8_t* sQX, int ks,
+                          int t) {
+      if constexpr (MX) {
+        // block of 32 rows at 8 (first row) bytes, dword plane ks, row rl
 #pragma unroll
-      for (int j = 0; j < MJ; ++j) sx[j] = sS[wm * TM + j * 32 + rl];
+        for (int i = 0; i < NI; ++i)
+          wsc[t][i] = *reinterpret_cast<const uint32_t*>(sQW + wrow(i) * 8 + ks * 128 + rl * 4) >> (8 * kh);
+#pragma unroll
+        for (int j = 0; j < MJE; ++j)
+          xsc[t][j] =
+              *reinterpret_cast<const uint32_t*>(sQX + (wm * TM + j * 32) * 8 + ks * 128 + rl * 4) >> (8 * kh);
+      }
+      const int h0 = KB == 64 ? po[0][0] : po[ks][0], h1 = KB == 64 ? po[0][1] : po[ks][1];
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
-        // the tile's 128-row weight blocks: LDS rows 0..127 and 128..255 of a
-        // 256-row tile; with an activation the gate and the up half
-        const int wb = ACT ? (wrow(i) >= BN / 2 ? 1 : 0) : wrow(i) / 128;
-        const float sw = WPC ? 1.0f : sS[BM + wb];
-#pragma unroll
-        for (int j = 0; j < MJ; ++j) scl[i][j] = sx[j] * sw;
+        const uint8_t* b = sW + wrow(i) * KB;
+        wf[t][i] = lds_frag(b + h0, b + h1);
       }
-    }
-  };
-  auto mma = [&](int t) {
-    if constexpr (MX) {
 #pragma unroll
-      for (int i = 0; i < NI; ++i)
+      for (int j = 0; j < MJE; ++j) {
+        const uint8_t* b = sX + (wm * TM + j * 32) * KB;
+        xf[t][j] = lds_frag(b + h0, b + h1);
+      }
+    };
+
+    auto read_scales = [&](const float* sS) {
+      if constexpr (BLK) {
+        float sx[MJE];
 #pragma unroll
-        for (int j = 0; j < MJ; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fp4_op(lo4(wf[t][i])), fp4_op(lo4(xf[t][j])),
-                                                                      acc[i][j], 4, 4, 0, (int)wsc[t][i], 0,
-                                                                      (int)xsc[t][j]);
+        for (int j = 0; j < MJE; ++j) sx[j] = sS[wm * TM + j * 32 + rl];
 #pragma unroll
-      for (int i = 0; i < NI; ++i)
+        for (int i = 0; i < NI; ++i) {
+          // the tile's 128-row weight blocks: LDS rows 0..127 and 128..255 of a
+          // 256-row tile; with an activation the gate and the up half
+          const int wb = ACT ? (wrow(i) >= BN / 2 ? 1 : 0) : wrow(i) / 128;
+          const float sw = WPC ? 1.0f : sS[BM + wb];
 #pragma unroll
-        for (int j = 0; j < MJ; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fp4_op(hi4(wf[t][i])), fp4_op(hi4(xf[t][j])),
-                                                                      acc[i][j], 4, 4, 2, (int)wsc[t][i], 2,
-                                                                      (int)xsc[t][j]);
-      return;
-    }
-    if constexpr (INT && !BLK) {
-      // the two 32-k halves of the k-step go to every accumulator in turn:
-      // the second MFMA of an accumulator comes NI * MJ MFMAs after its first,
-      // so no MFMA waits on the result of the one before it
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
+          for (int j = 0; j < MJE; ++j) scl[i][j] = sx[j] * sw;
+        }
+      }
+    };
+    auto mma = [&](int t) {
+      if constexpr (MX) {
 #pragma unroll
         for (int i = 0; i < NI; ++i)
 #pragma unroll
-          for (int j = 0; j < MJ; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(h ? hi4(wf[t][i]) : lo4(wf[t][i]),
-                                                              h ? hi4(xf[t][j]) : lo4(xf[t][j]), acc[i][j], 0, 0,
-                                                              0);
-      return;
-    }
-    if constexpr (BLK) {
-      if (t == 1) {
-        // the stage's last k-step: block pair p's MFMA, then the scaling
-        // acc += tmp * (sx * sw) of pair p - 1, whose MFMA has completed by
-        // then, so the FMAs run on the vector ALU while the matrix core runs
-        // the next MFMA (each accumulator still sees the same operations in
-        // the same order). INT8: every pair's first 32-k half first, then
-        // the second halves with the scaling behind them.
-        if constexpr (INT) {
+          for (int j = 0; j < MJE; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fp4_op(lo4(wf[t][i])), fp4_op(lo4(xf[t][j])),
+                                                                        acc[i][j], 4, 4, 0, (int)wsc[t][i], 0,
+                                                                        (int)xsc[t][j]);
 #pragma unroll
-          for (int i = 0; i < NI; ++i)
+        for (int i = 0; i < NI; ++i)
 #pragma unroll
-            for (int j = 0; j < MJ; ++j)
-              tmp[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(lo4(wf[1][i]), lo4(xf[1][j]), tmp[i][j], 0, 0, 0);
-        }
-#pragma unroll
-        for (int q = 0; q <= NI * MJ; ++q) {
-          if (q < NI * MJ) {
-            const int i = q / MJ, j = q % MJ;
-            if constexpr (INT)
-              tmp[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(hi4(wf[1][i]), hi4(xf[1][j]), tmp[i][j], 0, 0, 0);
-            else
-              tmp[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[1][i], xf[1][j], tmp[i][j], kFw, kFx,
-                                                                          0, 127, 0, 127);
-          }
-          if (q > 0) {
-            const int i = (q - 1) / MJ, j = (q - 1) % MJ;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] += (float)tmp[i][j][r] * scl[i][j];
-          }
-        }
+          for (int j = 0; j < MJE; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fp4_op(hi4(wf[t][i])), fp4_op(hi4(xf[t][j])),
+                                                                        acc[i][j], 4, 4, 2, (int)wsc[t][i], 2,
+                                                                        (int)xsc[t][j]);
         return;
       }
-      if constexpr (INT) {
-        // the stage's first k-step: fresh block sums, halves as above
+      if constexpr (INT && !BLK) {
+        // the two 32-k halves of the k-step go to every accumulator in turn:
+        // the second MFMA of an accumulator comes NI * MJE MFMAs after its first,
+        // so no MFMA waits on the result of the one before it
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
           for (int i = 0; i < NI; ++i)
 #pragma unroll
-            for (int j = 0; j < MJ; ++j)
-              tmp[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(h ? hi4(wf[0][i]) : lo4(wf[0][i]),
-                                                                h ? hi4(xf[0][j]) : lo4(xf[0][j]),
-                                                                h ? tmp[i][j] : i32x16{}, 0, 0, 0);
+            for (int j = 0; j < MJE; ++j)
+              acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(h ? hi4(wf[t][i]) : lo4(wf[t][i]),
+                                                                h ? hi4(xf[t][j]) : lo4(xf[t][j]), acc[i][j], 0, 0,
+                                                                0);
         return;
       }
-    }
+      if constexpr (BLK) {
+        if (t == 1) {
+          // the stage's last k-step: block pair p's MFMA, then the scaling
+          // acc += tmp * (sx * sw) of pair p - 1, whose MFMA has completed by
+          // then, so the FMAs run on the vector ALU while the matrix core runs
+          // the next MFMA (each accumulator still sees the same operations in
+          // the same order). INT8: every pair's first 32-k half first, then
+          // the second halves with the scaling behind them.
+          if constexpr (INT) {
 #pragma unroll
-    for (int i = 0; i < NI; ++i)
+            for (int i = 0; i < NI; ++i)
 #pragma unroll
-      for (int j = 0; j < MJ; ++j) {
-        if constexpr (BLK) {
-          tmp[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[t][i], xf[t][j], f32x16{}, kFw, kFx, 0,
-                                                                      127, 0, 127);
-        } else {
-          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[t][i], xf[t][j], acc[i][j], kFw, kFx, 0,
-                                                                      127, 0, 127);
+              for (int j = 0; j < MJE; ++j)
+                tmp[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(lo4(wf[1][i]), lo4(xf[1][j]), tmp[i][j], 0, 0, 0);
+          }
+#pragma unroll
+          for (int q = 0; q <= NI * MJE; ++q) {
+            if (q < NI * MJE) {
+              const int i = q / MJE, j = q % MJE;
+              if constexpr (INT)
+                tmp[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(hi4(wf[1][i]), hi4(xf[1][j]), tmp[i][j], 0, 0, 0);
+              else
+                tmp[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[1][i], xf[1][j], tmp[i][j], kFw, kFx,
+                                                                            0, 127, 0, 127);
+            }
+            if (q > 0) {
+              const int i = (q - 1) / MJE, j = (q - 1) % MJE;
+#pragma unroll
+              for (int r = 0; r < 16; ++r) acc[i][j][r] += (float)tmp[i][j][r] * scl[i][j];
+            }
+          }
+          return;
+        }
+        if constexpr (INT) {
+          // the stage's first k-step: fresh block sums, halves as above
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int i = 0; i < NI; ++i)
+#pragma unroll
+              for (int j = 0; j < MJE; ++j)
+                tmp[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(h ? hi4(wf[0][i]) : lo4(wf[0][i]),
+                                                                  h ? hi4(xf[0][j]) : lo4(xf[0][j]),
+                                                                  h ? tmp[i][j] : i32x16{}, 0, 0, 0);
+          return;
         }
       }
-  };
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+#pragma unroll
+        for (int j = 0; j < MJE; ++j) {
+          if constexpr (BLK) {
+            tmp[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[t][i], xf[t][j], f32x16{}, kFw, kFx, 0,
+                                                                        127, 0, 127);
+          } else {
+            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[t][i], xf[t][j], acc[i][j], kFw, kFx, 0,
+                                                                        127, 0, 127);
+          }
+        }
+    };
 
 
-  constexpr int CPS = WI + XI + (BLK ? 1 : 0) + QW + QX;  // copy instructions per wavefront per stage
-  constexpr int NM = NI * MJ * (INT || MX ? 2 : 1);       // MFMAs per k-step
-  constexpr int NR = (MX ? 3 : 2) * (NI + MJ);            // LDS operand reads per k-step
-  if constexpr (KB == 64) {
-    // ---- four stages of one k-step (KS % 4 == 0) ----
-    // Stage s lives in LDS buffer s % 4 and is copied four stages ahead.
-    // Stage s: wait for the own copy of stage s+1 -> barrier (every copy of
-    // stage s+1 has landed, and every wavefront holds the operands of stage
-    // s in registers, so buffer s % 4 is free) -> copy stage s+4 into it ->
-    // MFMAs of stage s, with the operand reads of stage s+1 issued among the
-    // first MFMAs (so they have landed by the next barrier) and the copies
-    // among the rest. The copy is unconditional (past the end it refetches
-    // the last stage into a consumed buffer, which is never read again), so
-    // the loop body has no branch.
-    const int KS = (u1 - u0) * 4;
-    copy_stage(sW0, sX0, sS0, sQW0, sQX0, 0);
-    copy_stage(sW1, sX1, sS0, sQW0, sQX0, 1);
-    copy_stage(sW2, sX2, sS0, sQW0, sQX0, 2);
-    copy_stage(sW3, sX3, sS0, sQW0, sQX0, 3);
-    wait_copies_upto<3 * CPS>();
-    __syncthreads();
-    read_frags(sW0, sX0, sQW0, sQX0, 0, 0);
-    auto stage = [&](uint8_t* fW, uint8_t* fX, uint8_t* nW, uint8_t* nX, int s, int t) {
-      wait_copies_upto<2 * CPS>();  // copies issued after stage s+1's: s+2, s+3
-      stage_barrier();
-      // the operand reads of stage s+1 come before the copies in program
-      // order: the compiler treats an LDS copy as a write that may alias any
-      // LDS read after it, so reads placed after the copies could not be
-      // interleaved with this stage's MFMAs
-      read_frags(nW, nX, sQW0, sQX0, 0, t ^ 1);
-      copy_stage(fW, fX, sS0, sQW0, sQX0, min(s + 4, KS - 1));
-      mma(t);
-      interleave<0, NM, NR, CPS>();
-    };
-    for (int s = 0; s < KS; s += 4) {
-      stage(sW0, sX0, sW1, sX1, s, 0);
-      stage(sW1, sX1, sW2, sX2, s + 1, 1);
-      stage(sW2, sX2, sW3, sX3, s + 2, 0);
-      stage(sW3, sX3, sW0, sX0, s + 3, 1);
-    }
-  } else {
-    // ---- two stages of two k-steps (KS % 2 == 0) ----
-    // Stage s lives in LDS buffer s % 2. Its first half runs the MFMAs of
-    // k-step 0 while k-step 1 is read; then: wait for the own copy of stage
-    // s+1 -> barrier (stage s+1 has landed everywhere, and stage s has been
-    // read everywhere, so its buffer is free) -> copy stage s+2 into it ->
-    // MFMAs of k-step 1 while k-step 0 of stage s+1 is read. A copy has one
-    // stage (two k-steps of MFMAs) to land.
-    // BLK: the stage's scales are read with its second k-step (before the
-    // barrier that frees its buffer) and applied after the k-step's MFMAs.
-    // With three buffers (TRI) the buffer freed at stage s's barrier takes
-    // stage s+3, so a copy has two stages to land.
-    const int KS = (u1 - u0) * 2;
-    constexpr int AHEAD = TRI ? 3 : 2;
-    auto stage = [&](uint8_t* cW, uint8_t* cX, float* cS, uint8_t* cQW, uint8_t* cQX, uint8_t* nW, uint8_t* nX,
-                     uint8_t* nQW, uint8_t* nQX, int s) {
-      mma(0);
-      read_frags(cW, cX, cQW, cQX, 1, 1);
-      read_scales(cS);
-      interleave<0, NM, NR + (BLK ? MJ + NI : 0), 0>();
-      // every MFMA of k-step 0 is issued before the wait (the wait has no
-      // data dependence on them, so the scheduler would otherwise hoist it
-      // above half of them and cut the copies' latency slack)
-      __builtin_amdgcn_sched_barrier(0);
-      wait_copies_upto<(AHEAD - 2) * CPS>();  // stage s+1 has landed
-      stage_barrier();
-      // k-step 0 of stage s+1 is read before the copies are issued (an LDS
-      // copy may alias any later LDS read for the compiler, which would keep
-      // the reads behind every copy and expose their latency)
-      read_frags(nW, nX, nQW, nQX, 0, 0);
-      copy_stage(cW, cX, cS, cQW, cQX, min(s + AHEAD, KS - 1));
-      mma(1);
-      // BLK: each MFMA followed by the previous block pair's 16 scaling FMAs
-      interleave_v<0, NM, NR, CPS, BLK ? 16 : 0>();
-    };
-    copy_stage(sW0, sX0, sS0, sQW0, sQX0, 0);
-    copy_stage(sW1, sX1, sS1, sQW1, sQX1, 1);
-    if constexpr (TRI) copy_stage(sW2, sX2, sS2, sQW2, sQX2, min(2, KS - 1));
-    wait_copies_upto<(AHEAD - 1) * CPS>();
-    __syncthreads();
-    read_frags(sW0, sX0, sQW0, sQX0, 0, 0);
-    if constexpr (TRI) {
-      int s = 0;
-      for (; s + 3 <= KS; s += 3) {
-        stage(sW0, sX0, sS0, sQW0, sQX0, sW1, sX1, sQW1, sQX1, s);
-        stage(sW1, sX1, sS1, sQW1, sQX1, sW2, sX2, sQW2, sQX2, s + 1);
-        stage(sW2, sX2, sS2, sQW2, sQX2, sW0, sX0, sQW0, sQX0, s + 2);
+    constexpr int CPS = WI + XI + (BLK ? 1 : 0) + QW + QX;  // copy instructions per wavefront per stage
+    constexpr int NM = NI * MJE * (INT || MX ? 2 : 1);       // MFMAs per k-step
+    constexpr int NR = (MX ? 3 : 2) * (NI + MJE);            // LDS operand reads per k-step
+    if constexpr (KB == 64) {
+      // ---- four stages of one k-step (KS % 4 == 0) ----
+      // Stage s lives in LDS buffer s % 4 and is copied four stages ahead.
+      // Stage s: wait for the own copy of stage s+1 -> barrier (every copy of
+      // stage s+1 has landed, and every wavefront holds the operands of stage
+      // s in registers, so buffer s % 4 is free) -> copy stage s+4 into it ->
+      // MFMAs of stage s, with the operand reads of stage s+1 issued among the
+      // first MFMAs (so they have landed by the next barrier) and the copies
+      // among the rest. The copy is unconditional (past the end it refetches
+      // the last stage into a consumed buffer, which is never read again), so
+      // the loop body has no branch.
+      const int KS = (u1 - u0) * 4;
+      copy_stage(sW0, sX0, sS0, sQW0, sQX0, 0);
+      copy_stage(sW1, sX1, sS0, sQW0, sQX0, 1);
+      copy_stage(sW2, sX2, sS0, sQW0, sQX0, 2);
+      copy_stage(sW3, sX3, sS0, sQW0, sQX0, 3);
+      wait_copies_upto<3 * CPS>();
+      __syncthreads();
+      read_frags(sW0, sX0, sQW0, sQX0, 0, 0);
+      auto stage = [&](uint8_t* fW, uint8_t* fX, uint8_t* nW, uint8_t* nX, int s, int t) {
+        wait_copies_upto<2 * CPS>();  // copies issued after stage s+1's: s+2, s+3
+        stage_barrier();
+        // the operand reads of stage s+1 come before the copies in program
+        // order: the compiler treats an LDS copy as a write that may alias any
+        // LDS read after it, so reads placed after the copies could not be
+        // interleaved with this stage's MFMAs
+        read_frags(nW, nX, sQW0, sQX0, 0, t ^ 1);
+        copy_stage(fW, fX, sS0, sQW0, sQX0, min(s + 4, KS - 1));
+        mma(t);
+        interleave<0, NM, NR, CPS>();
+      };
+      for (int s = 0; s < KS; s += 4) {
+        stage(sW0, sX0, sW1, sX1, s, 0);
+        stage(sW1, sX1, sW2, sX2, s + 1, 1);
+        stage(sW2, sX2, sW3, sX3, s + 2, 0);
+        stage(sW3, sX3, sW0, sX0, s + 3, 1);
       }
-      if (s < KS) stage(sW0, sX0, sS0, sQW0, sQX0, sW1, sX1, sQW1, sQX1, s);
-      if (s + 1 < KS) stage(sW1, sX1, sS1, sQW1, sQX1, sW2, sX2, sQW2, sQX2, s + 1);
     } else {
-      for (int s = 0; s < KS; s += 2) {
-        stage(sW0, sX0, sS0, sQW0, sQX0, sW1, sX1, sQW1, sQX1, s);
-        stage(sW1, sX1, sS1, sQW1, sQX1, sW0, sX0, sQW0, sQX0, s + 1);
+      // ---- two stages of two k-steps (KS % 2 == 0) ----
+      // Stage s lives in LDS buffer s % 2. Its first half runs the MFMAs of
+      // k-step 0 while k-step 1 is read; then: wait for the own copy of stage
+      // s+1 -> barrier (stage s+1 has landed everywhere, and stage s has been
+      // read everywhere, so its buffer is free) -> copy stage s+2 into it ->
+      // MFMAs of k-step 1 while k-step 0 of stage s+1 is read. A copy has one
+      // stage (two k-steps of MFMAs) to land.
+      // BLK: the stage's scales are read with its second k-step (before the
+      // barrier that frees its buffer) and applied after the k-step's MFMAs.
+      // With three buffers (TRI) the buffer freed at stage s's barrier takes
+      // stage s+3, so a copy has two stages to land.
+      const int KS = (u1 - u0) * 2;
+      constexpr int AHEAD = TRI ? 3 : 2;
+      auto stage = [&](uint8_t* cW, uint8_t* cX, float* cS, uint8_t* cQW, uint8_t* cQX, uint8_t* nW, uint8_t* nX,
+                       uint8_t* nQW, uint8_t* nQX, int s) {
+        mma(0);
+        read_frags(cW, cX, cQW, cQX, 1, 1);
+        read_scales(cS);
+        interleave<0, NM, NR + (BLK ? MJE + NI : 0), 0>();
+        // every MFMA of k-step 0 is issued before the wait (the wait has no
+        // data dependence on them, so the scheduler would otherwise hoist it
+        // above half of them and cut the copies' latency slack)
+        __builtin_amdgcn_sched_barrier(0);
+        wait_copies_upto<(AHEAD - 2) * CPS>();  // stage s+1 has landed
+        stage_barrier();
+        // k-step 0 of stage s+1 is read before the copies are issued (an LDS
+        // copy may alias any later LDS read for the compiler, which would keep
+        // the reads behind every copy and expose their latency)
+        read_frags(nW, nX, nQW, nQX, 0, 0);
+        copy_stage(cW, cX, cS, cQW, cQX, min(s + AHEAD, KS - 1));
+        mma(1);
+        // BLK: each MFMA followed by the previous block pair's 16 scaling FMAs
+        interleave_v<0, NM, NR, CPS, BLK ? 16 : 0>();
+      };
+      copy_stage(sW0, sX0, sS0, sQW0, sQX0, 0);
+      copy_stage(sW1, sX1, sS1, sQW1, sQX1, 1);
+      if constexpr (TRI) copy_stage(sW2, sX2, sS2, sQW2, sQX2, min(2, KS - 1));
+      wait_copies_upto<(AHEAD - 1) * CPS>();
+      __syncthreads();
+      read_frags(sW0, sX0, sQW0, sQX0, 0, 0);
+      if constexpr (TRI) {
+        int s = 0;
+        for (; s + 3 <= KS; s += 3) {
+          stage(sW0, sX0, sS0, sQW0, sQX0, sW1, sX1, sQW1, sQX1, s);
+          stage(sW1, sX1, sS1, sQW1, sQX1, sW2, sX2, sQW2, sQX2, s + 1);
+          stage(sW2, sX2, sS2, sQW2, sQX2, sW0, sX0, sQW0, sQX0, s + 2);
+        }
+        if (s < KS) stage(sW0, sX0, sS0, sQW0, sQX0, sW1, sX1, sQW1, sQX1, s);
+        if (s + 1 < KS) stage(sW1, sX1, sS1, sQW1, sQX1, sW2, sX2, sQW2, sQX2, s + 1);
+      } else {
+        for (int s = 0; s < KS; s += 2) {
+          stage(sW0, sX0, sS0, sQW0, sQX0, sW1, sX1, sQW1, sQX1, s);
+          stage(sW1, sX1, sS1, sQW1, sQX1, sW0, sX0, sQW0, sQX0, s + 1);
+        }
       }
     }
-  }
 
+  };
+  // A block-scaled tile whose wavefront holds at most 32 of its tokens (the
+  // last tile of a routed expert, a ragged last token tile) runs the MFMAs
+  // and block scaling of its first 32-token block only: the other block's
+  // sums belong to no token. Every wavefront still makes the same copies
+  // and reaches the same barriers.
+  if constexpr (BLK && MJ == 2) {
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+    if (rows - (wave_u / S::WN) * TM <= 32) pipeline(std::integral_constant<int, 1>{});
+    else pipeline(std::integral_constant<int, MJ>{});
+  } else {
+    pipeline(std::integral_constant<int, MJ>{});
+  }
   if (p.ksplit > 1) {
     tile_store_partials<BN, TN, TM, NI, MJ, ACT, INT && !BLK>(p, acc, row0, rows, n0, nlim, wn, wm, lane);
     return;
@@ -1303,7 +1320,8 @@ int qmoe_f8_launch(GemmParams p, bool blk, void* workspace, int64_t ws_bytes, hi
   else if (blk && p.wfmt == 2) f8_launch_bm_blk<false, false, 1>(p, bm, bn, st);
   else if (blk && p.wfmt == 1) f8_launch_bm_blk<true, false>(p, bm, bn, st);
   else if (blk) f8_launch_bm_blk<false, false>(p, bm, bn, st);
-  else if (f8_persistent_mid_ok(p, blk, bm, bn, ksplit)) p.wfmt == 1 ? f8_launch_mid<true>(p, st) : f8_launch_mid<false>(p, st);
+  else if (f8_persistent_mid_ok(p, blk, bm, bn, ksplit) && p.wfmt == 1) f8_launch_mid<true>(p, st);
+  else if (f8_persistent_mid_ok(p, blk, bm, bn, ksplit)) f8_launch_mid<false>(p, st);
   else if (p.wfmt == 1) f8_launch_bm<true>(p, bm, bn, st);
   else if (p.wfmt == 2) f8_launch_bm<false, 3>(p, bm, bn, st);
   else f8_launch_bm<false>(p, bm, bn, st);
