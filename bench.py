@@ -47,8 +47,11 @@ def log(*a):
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=50)
+    # untimed steps before the timed ones: on a fresh MI355X the headline step
+    # takes ~60 steps to reach its steady time (measured: 489, 469, then
+    # 455-460 us per step over blocks of 20 steps)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--m", type=int, default=4096, help="tokens of the headline step")
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
