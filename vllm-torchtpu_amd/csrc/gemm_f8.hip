@@ -629,8 +629,9 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
 
 }
 
-// Persistent dense form of the 256 x 256 tile (128-byte K stages in two LDS
-// buffers, per-token x per-channel scales, no K split, bias or row maps).
+// Persistent dense form of the 1-byte tiles (256 x 256 and the shapes below;
+// 128-byte K stages in two LDS buffers, per-token x per-channel scales, no K
+// split, bias or row maps).
 // Measured on MI355X: the one-tile-per-workgroup kernel spends ~14 us per
 // tile outside its K loop (launch, the first stages' copy latency, the
 // LDS-staged epilogue), which on the up projection of Llama-3-8B (896 tiles
@@ -1291,7 +1292,8 @@ bool qmoe_f8_plan(const GemmParams& p, bool blk, int* bm_out, int* ksplit_out, i
   return true;
 }
 
-// Whether the planned problem runs the persistent 256 x 256 kernel.
+// Whether the planned problem runs the persistent kernel (256 x 256 / 256 x 224
+// tiles, or 128 x 224 for mid-size problems).
 bool qmoe_f8_persistent(const GemmParams& p, bool blk) {
   int bm = 0, ksplit = 1, bn = 256;
   int64_t ws = 0;
