@@ -205,25 +205,8 @@ __global__ __launch_bounds__(kThreads) void w4_gemm_kernel(const GemmParams p, i
     }
   };
 
-  // ---- operands of one stage into register set t ----
   uint4 wc[2][NI];  // codes: dword q feeds 16-k step q
   uint4 xa[2][MJ][4];  // activations: [block][16-k step]
-  auto read_stage = [&](const uint8_t* sA, const uint8_t* sW, int t) {
-#pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const int r = wrow(i) + rl;
-      wc[t][i] = *reinterpret_cast<const uint4*>(sW + r * 32 + kh * 16);
-    }
-#pragma unroll
-    for (int j = 0; j < MJ; ++j) {
-      const int r = wm * TM + j * 32 + rl;
-      const uint8_t* row = sA + r * 128;
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        xa[t][j][q] = *reinterpret_cast<const uint4*>(row + (((kh * 4 + q) ^ w4_swz(r)) * 16));
-    }
-  };
-
   f32x16 acc[NI][MJ];
 #pragma unroll
   for (int i = 0; i < NI; ++i)
@@ -232,82 +215,119 @@ __global__ __launch_bounds__(kThreads) void w4_gemm_kernel(const GemmParams p, i
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  // k-step outer, blocks inner: consecutive MFMAs go to different
-  // accumulators, and a step's expansions overlap the previous step's MFMAs
-  auto mma_stage = [&](int t, const uint32_t (&eb)[NI]) {
-    float scale[NI], scale1[NI];  // NVFP4: scale for 16-k steps 0-1, scale1 for 2-3
-#pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      if constexpr (NV) {
-        scale[i] = bits_f32(eb[i] << 16);
-        scale1[i] = bits_f32(eb[i] & 0xffff0000u);
-      } else if constexpr (I4) {
-        scale[i] = bits_f32(eb[i] << 16);
-      } else {
-        scale[i] = e8m0_to_f32(eb[i]);
-      }
-    }
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      bf16x8 wv[NI];
+  // The K pipeline over the first MJE 32-token blocks of the tile (MJ: all
+  // of them); the accumulators of the others keep their zeros.
+  auto pipeline = [&](auto mje_c) {
+    constexpr int MJE = decltype(mje_c)::value;
+    // ---- operands of one stage into register set t ----
+    auto read_stage = [&](const uint8_t* sA, const uint8_t* sW, int t) {
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
-        const uint32_t d = q == 0 ? wc[t][i].x : (q == 1 ? wc[t][i].y : (q == 2 ? wc[t][i].z : wc[t][i].w));
-        if constexpr (NV) wv[i] = as_bf16x8_u4(nvfp4x8_to_bf16(d, q < 2 ? scale[i] : scale1[i]));
-        else if constexpr (I4) wv[i] = as_bf16x8_u4(int4x8_to_bf16(d, scale[i]));
-        else wv[i] = w4_expand(d, scale[i]);
+        const int r = wrow(i) + rl;
+        wc[t][i] = *reinterpret_cast<const uint4*>(sW + r * 32 + kh * 16);
       }
 #pragma unroll
-      for (int i = 0; i < NI; ++i)
+      for (int j = 0; j < MJE; ++j) {
+        const int r = wm * TM + j * 32 + rl;
+        const uint8_t* row = sA + r * 128;
 #pragma unroll
-        for (int j = 0; j < MJ; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wv[i], as_bf16x8_u4(xa[t][j][q]), acc[i][j], 0, 0, 0);
-    }
-  };
+        for (int q = 0; q < 4; ++q)
+          xa[t][j][q] = *reinterpret_cast<const uint4*>(row + (((kh * 4 + q) ^ w4_swz(r)) * 16));
+      }
+    };
 
-  constexpr int CPS = WI + XI + NI;        // vector-memory loads per wavefront per stage
-  constexpr int NM = NI * MJ * 4;          // MFMAs per stage
-  constexpr int NR = NI + MJ * 4;          // LDS operand reads per stage
-  // Stage s lives in buffer s % 4 and is copied four stages ahead. Stage s:
-  // wait for the own copy of stage s+1 -> barrier (stage s+1 has landed
-  // everywhere, and every wavefront holds stage s in registers, so buffer
-  // s % 4 is free) -> copy stage s+4 into it -> MFMAs of stage s with the
-  // operand reads of stage s+1 among the first half and the copies among
-  // the second. Copies past the end refetch the last stage into a consumed
-  // buffer (never read again).
-  // (stage s's scale bytes are register set s % 4; they are taken before
-  // the set is reloaded with stage s+4)
-  auto stage = [&](uint8_t* fA, uint8_t* fW, const uint8_t* nA, const uint8_t* nW, int e, int s, int t) {
-    wait_copies_upto<2 * CPS>();
-    stage_barrier();
-    uint32_t eb[NI];
+    // k-step outer, blocks inner: consecutive MFMAs go to different
+    // accumulators, and a step's expansions overlap the previous step's MFMAs
+    auto mma_stage = [&](int t, const uint32_t (&eb)[NI]) {
+      float scale[NI], scale1[NI];  // NVFP4: scale for 16-k steps 0-1, scale1 for 2-3
 #pragma unroll
-    for (int i = 0; i < NI; ++i) eb[i] = we[e][i];
-    copy_stage(fA, fW, e, min(s + 4, KS - 1));
-    mma_stage(t, eb);
-    read_stage(nA, nW, t ^ 1);
-    interleave<0, NM, NR, CPS>();
-  };
-  if (KS > 0) {
-    copy_stage(sA0, sW0, 0, 0);
-    copy_stage(sA1, sW1, 1, min(1, KS - 1));
-    copy_stage(sA2, sW2, 2, min(2, KS - 1));
-    copy_stage(sA3, sW3, 3, min(3, KS - 1));
-    wait_copies_upto<3 * CPS>();
-    __syncthreads();
-    read_stage(sA0, sW0, 0);
-    int s = 0;
-    for (; s + 4 <= KS; s += 4) {
-      stage(sA0, sW0, sA1, sW1, 0, s, 0);
-      stage(sA1, sW1, sA2, sW2, 1, s + 1, 1);
-      stage(sA2, sW2, sA3, sW3, 2, s + 2, 0);
-      stage(sA3, sW3, sA0, sW0, 3, s + 3, 1);
+      for (int i = 0; i < NI; ++i) {
+        if constexpr (NV) {
+          scale[i] = bits_f32(eb[i] << 16);
+          scale1[i] = bits_f32(eb[i] & 0xffff0000u);
+        } else if constexpr (I4) {
+          scale[i] = bits_f32(eb[i] << 16);
+        } else {
+          scale[i] = e8m0_to_f32(eb[i]);
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        bf16x8 wv[NI];
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+          const uint32_t d = q == 0 ? wc[t][i].x : (q == 1 ? wc[t][i].y : (q == 2 ? wc[t][i].z : wc[t][i].w));
+          if constexpr (NV) wv[i] = as_bf16x8_u4(nvfp4x8_to_bf16(d, q < 2 ? scale[i] : scale1[i]));
+          else if constexpr (I4) wv[i] = as_bf16x8_u4(int4x8_to_bf16(d, scale[i]));
+          else wv[i] = w4_expand(d, scale[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+#pragma unroll
+          for (int j = 0; j < MJE; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wv[i], as_bf16x8_u4(xa[t][j][q]), acc[i][j], 0, 0, 0);
+      }
+    };
+
+    constexpr int CPS = WI + XI + NI;        // vector-memory loads per wavefront per stage
+    constexpr int NM = NI * MJE * 4;         // MFMAs per stage
+    constexpr int NR = NI + MJE * 4;         // LDS operand reads per stage
+    // Stage s lives in buffer s % 4 and is copied four stages ahead. Stage s:
+    // wait for the own copy of stage s+1 -> barrier (stage s+1 has landed
+    // everywhere, and every wavefront holds stage s in registers, so buffer
+    // s % 4 is free) -> copy stage s+4 into it -> MFMAs of stage s with the
+    // operand reads of stage s+1 among the first half and the copies among
+    // the second. Copies past the end refetch the last stage into a consumed
+    // buffer (never read again).
+    // (stage s's scale bytes are register set s % 4; they are taken before
+    // the set is reloaded with stage s+4)
+    auto stage = [&](uint8_t* fA, uint8_t* fW, const uint8_t* nA, const uint8_t* nW, int e, int s, int t) {
+      wait_copies_upto<2 * CPS>();
+      stage_barrier();
+      uint32_t eb[NI];
+#pragma unroll
+      for (int i = 0; i < NI; ++i) eb[i] = we[e][i];
+      copy_stage(fA, fW, e, min(s + 4, KS - 1));
+      mma_stage(t, eb);
+      read_stage(nA, nW, t ^ 1);
+      interleave<0, NM, NR, CPS>();
+    };
+    if (KS > 0) {
+      copy_stage(sA0, sW0, 0, 0);
+      copy_stage(sA1, sW1, 1, min(1, KS - 1));
+      copy_stage(sA2, sW2, 2, min(2, KS - 1));
+      copy_stage(sA3, sW3, 3, min(3, KS - 1));
+      wait_copies_upto<3 * CPS>();
+      __syncthreads();
+      read_stage(sA0, sW0, 0);
+      int s = 0;
+      for (; s + 4 <= KS; s += 4) {
+        stage(sA0, sW0, sA1, sW1, 0, s, 0);
+        stage(sA1, sW1, sA2, sW2, 1, s + 1, 1);
+        stage(sA2, sW2, sA3, sW3, 2, s + 2, 0);
+        stage(sA3, sW3, sA0, sW0, 3, s + 3, 1);
+      }
+      if (s < KS) stage(sA0, sW0, sA1, sW1, 0, s, 0);
+      if (s + 1 < KS) stage(sA1, sW1, sA2, sW2, 1, s + 1, 1);
+      if (s + 2 < KS) stage(sA2, sW2, sA3, sW3, 2, s + 2, 0);
     }
-    if (s < KS) stage(sA0, sW0, sA1, sW1, 0, s, 0);
-    if (s + 1 < KS) stage(sA1, sW1, sA2, sW2, 1, s + 1, 1);
-    if (s + 2 < KS) stage(sA2, sW2, sA3, sW3, 2, s + 2, 0);
+
+  };
+  // A tile with at most 32 (64) valid tokens -- a routed expert's last tile
+  // -- runs the MFMAs of its first one (two) 32-token blocks only: the
+  // others' sums belong to no token. The expansion of the weight codes, the
+  // copies and the barriers are the same.
+  const int rows_u = __builtin_amdgcn_readfirstlane(rows);
+  if constexpr (MJ == 4) {
+    if (rows_u <= 32) pipeline(std::integral_constant<int, 1>{});
+    else if (rows_u <= 64) pipeline(std::integral_constant<int, 2>{});
+    else pipeline(std::integral_constant<int, 4>{});
+  } else if constexpr (MJ == 2) {
+    if (rows_u <= 32) pipeline(std::integral_constant<int, 1>{});
+    else pipeline(std::integral_constant<int, 2>{});
+  } else {
+    pipeline(std::integral_constant<int, MJ>{});
   }
-
   if (p.ksplit > 1) {
     tile_store_partials<BN, TN, TM, NI, MJ, ACT, false>(p, acc, row0, rows, n0, nlim, wn, wm, lane);
     return;
