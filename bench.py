@@ -58,6 +58,7 @@ def parse():
     ap.add_argument("--sweep-out", default="gpurun_out/bench_sweep.json",
                     help="where the full sweep (every point, read floor, parity objects) is written")
     ap.add_argument("--only", default="", help="comma list of sweep configs to run (0-4; 5 = NVFP4 / INT4; "
+                                                "6 = the decoder layers' other linears; "
                                                 "v = hipBLASLt reference points)")
     ap.add_argument("--profile", nargs="?", const="headline", default=None,
                     choices=["headline", "decode", "moe", "vendor", "floor", "w4", "mx", "midm", "moet"],
@@ -434,6 +435,58 @@ def sweep_nvfp4(only):
         nbytes = touched * per_expert + 2 * T * H * 2 + 2 * T * E
         out.append(dict(cfg=5, kind=f"moe_int4_g{grp}", T=T, experts_touched=touched,
                         **roof(T * k * 6.0 * H * I, nbytes, us, "bf16")))
+        log(out[-1])
+    return out
+
+
+def sweep_decoder(only):
+    """Config "6": the other linears of the decoder layers the MoE configs
+    come from, through the same entry points at their real shapes --
+    DeepSeek-V3's attention projections (q_a, kv_a with the rope part, q_b,
+    kv_b, o) as the FP8 method's default recipe (per-channel e4m3 weights,
+    per-token activation codes, `layers/adapter/quantization/fp8.py:1669-1690`),
+    Llama-3-8B's qkv and o, and DeepSeek-V3's bf16 router gate
+    (`UnquantizedLinearMethod`, the W16A16 kind) -- at decode (1 token) and
+    prefill (4096 tokens)."""
+    import torch
+
+    from qmoe import _capi, ops
+    from qmoe.layers.linear_common import quantized_matmul
+
+    if only and "6" not in only:
+        return []
+    gen = torch.Generator(device="cuda").manual_seed(6)
+    out = []
+    shapes = [("dsv3_q_a", 1536, 7168), ("dsv3_kv_a", 576, 7168), ("dsv3_q_b", 24576, 1536),
+              ("dsv3_kv_b", 32768, 512), ("dsv3_o", 7168, 16384), ("llama3_qkv", 6144, 4096),
+              ("llama3_o", 4096, 4096)]
+    for name, N, K in shapes:
+        w = torch.randn((N, K), device="cuda", generator=gen) * 0.02
+        q, s = ops.row_quant(w, "fp8", mode="load")
+        del w
+        if PAR.on:
+            wq_h, ws_h = q.view(torch.uint8).cpu().numpy(), s.cpu().numpy()
+        for M in (1, 4096):
+            x = torch.randn((M, K), device="cuda", generator=gen).to(torch.bfloat16)
+            us = graph_time_us(lambda: quantized_matmul(x, q.t(), s), iters=20)[0]
+            nbytes = N * K + 4 * N + 2 * M * K + 2 * M * N
+            par = PAR.linear(quantized_matmul(x, q.t(), s), x, M,
+                             lambda xr: oracle_mod("linear").w8a8_per_channel(xr, wq_h, ws_h, "fp8")[0],
+                             n=2) if PAR.on else {}
+            out.append(dict(cfg=6, kind=f"fp8_pc_{name}", M=M, K=K, N=N, **roof(2.0 * M * N * K, nbytes, us, "fp8"),
+                            **par))
+            log(out[-1])
+    N, K = 256, 7168
+    wg = (torch.randn((N, K), device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
+    wg_h = wg.float().cpu().numpy() if PAR.on else None
+    for M in (1, 4096):
+        x = torch.randn((M, K), device="cuda", generator=gen).to(torch.bfloat16)
+        us = graph_time_us(lambda: ops.gemm(_capi.W16A16, x, wg), iters=20)[0]
+        nbytes = 2 * N * K + 2 * M * K + 2 * M * N
+        par = PAR.linear(ops.gemm(_capi.W16A16, x, wg), x, M,
+                         lambda xr: oracle_mod("linear").w16a16(xr, wg_h), n=2) if PAR.on else {}
+        out.append(dict(cfg=6, kind="bf16_dsv3_router_gate", M=M, K=K, N=N,
+                        **roof(2.0 * M * N * K, nbytes, us, "bf16"), **par))
         log(out[-1])
     return out
 
@@ -1345,7 +1398,7 @@ def main():
     if not args.no_sweep:
         FLOOR.extend(read_floor())
         full["read_floor"] = FLOOR
-        full["sweep"] = sweep_linear(only) + sweep_moe(only) + sweep_nvfp4(only)
+        full["sweep"] = sweep_linear(only) + sweep_moe(only) + sweep_nvfp4(only) + sweep_decoder(only)
         if not only or "v" in only:
             full["sweep"] += sweep_vendor()
         res["sweep_summary"] = compact_sweep(full["sweep"])

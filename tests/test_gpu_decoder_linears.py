@@ -73,7 +73,7 @@ DSV3 = [("q_a", 1536, 7168), ("kv_a", 576, 7168), ("q_b", 24576, 1536), ("kv_b",
         ("o", 7168, 16384), ("shared_gate_up", 4096, 7168), ("shared_down", 7168, 2048)]
 
 
-@pytest.mark.parametrize("M", [1, 64, 512])
+@pytest.mark.parametrize("M", [1, 64, 512, 4096])
 @pytest.mark.parametrize("name,N,K", DSV3)
 def test_dsv3_projection_default_recipe(dev, monkeypatch, name, N, K, M):
     """Default recipe: checkpoint tiles dequantized in float32, requantized
@@ -130,7 +130,7 @@ def test_dsv3_projection_native_tiles(dev, monkeypatch, name, N, K, M):
     assert_close_rows(y[torch.from_numpy(r).to(dev)].float().cpu().numpy(), ref, f"dsv3 {name} native M={M}")
 
 
-@pytest.mark.parametrize("M", [1, 16, 512])
+@pytest.mark.parametrize("M", [1, 16, 512, 4096])
 @pytest.mark.parametrize("name,widths,K", [("qkv", [4096, 1024, 1024], 4096), ("o", [4096], 4096)])
 def test_llama_attention_per_tensor_shards(dev, monkeypatch, name, widths, K, M):
     """Llama-3-8B FP8 checkpoints with one tensor scale per merged shard
