@@ -262,6 +262,39 @@ def test_w8a8_persistent_tiles(dev, monkeypatch, M, K, N, qdtype, pbn):
         assert_close_same_codes(got, ref, f"fp8 persistent {M}x{K}x{N}")
 
 
+@pytest.mark.parametrize("seed", range(4))
+def test_w8a8_persistent_matches_one_tile(dev, monkeypatch, seed):
+    """Seeded shapes of 300-5000 tokens, 1000-20000 output channels (N % 8 ==
+    0) and K of 512-4096: whatever persistent tile shape the planner picks
+    (256 x 256, 256 x 224, 128 x 224), the outputs equal the one-tile
+    kernel's bit for bit (both run the same MFMA sequence per output)."""
+    from qmoe import _capi, ops
+
+    rng = np.random.default_rng(1000 + seed)
+    for _ in range(4):
+        M = int(rng.integers(300, 5000))
+        N = int(rng.integers(125, 2500)) * 8
+        K = int(rng.integers(2, 17)) * 256
+        wf = int(rng.integers(0, 2))
+        monkeypatch.delenv("QMOE_F8_PERSIST", raising=False)
+        plan = ops.plan_for_shape(_capi.W8A8_PC, M, N, K, wfmt=wf)
+        print(f"w8a8 persistent vs one-tile M={M} K={K} N={N} wfmt={wf} plan={plan}", flush=True)
+        g = torch.Generator(device=dev).manual_seed(seed * 7 + M)
+        q = torch.randint(0, 120, (N, K), device=dev, dtype=torch.uint8, generator=g)
+        if wf:
+            q = torch.randint(-127, 128, (N, K), device=dev, dtype=torch.int8, generator=g).view(torch.uint8)
+        xq = torch.randint(0, 120, (M, K), device=dev, dtype=torch.uint8, generator=g)
+        if wf:
+            xq = torch.randint(-127, 128, (M, K), device=dev, dtype=torch.int8, generator=g).view(torch.uint8)
+        s = torch.rand(N, device=dev, generator=g) * 1e-3
+        xs = torch.rand(M, device=dev, generator=g)
+        y = ops.gemm(_capi.W8A8_PC, xq, q, a_scale=xs, w_scale=s, wfmt=wf)
+        monkeypatch.setenv("QMOE_F8_PERSIST", "0")
+        assert ops.plan_for_shape(_capi.W8A8_PC, M, N, K, wfmt=wf)[4] != "tiled_1b_persistent"
+        y1 = ops.gemm(_capi.W8A8_PC, xq, q, a_scale=xs, w_scale=s, wfmt=wf)
+        assert torch.equal(y.view(torch.int16), y1.view(torch.int16)), (M, K, N, wf, plan)
+
+
 @pytest.mark.parametrize("M,K,N", [(1000, 2048, 7000), (512, 4096, 14336), (300, 1024, 14336)])
 @pytest.mark.parametrize("qdtype", ["fp8", "int8"])
 def test_w8a8_persistent_mid_tiles(dev, monkeypatch, M, K, N, qdtype):
