@@ -190,7 +190,9 @@ def test_w8a8_int8_per_channel_bit_exact(dev, M, K, N):
 # 128-row weight tiles (dense per-channel problems whose 256-row tiles leave
 # CUs idle): ragged token and channel tiles, the tall-K forms with and
 # without a K split
-SHAPES_NARROW = [(64, 4096, 14336), (100, 4096, 2048), (256, 2048, 1000), (300, 14336, 1024), (700, 8192, 1152)]
+SHAPES_NARROW = [(64, 4096, 14336), (100, 4096, 2048), (256, 2048, 1000), (300, 14336, 1024), (700, 8192, 1152),
+                 # at most 1024 channels, over 256 tokens: 64- and 128-token tiles
+                 (2000, 7168, 576), (4096, 4096, 1000)]
 
 
 @pytest.mark.parametrize("M,K,N", SHAPES_NARROW)
@@ -506,6 +508,49 @@ def test_w8a16_and_w16a16(dev, M, K, N):
     ref = linear.w16a16(x, wb)
     y = ops.gemm(_capi.W16A16, xt, _t(wb, dev, torch.bfloat16))
     assert_close_same_codes(y.float().cpu().numpy(), ref, "w16a16")
+
+
+@pytest.mark.parametrize("kind", ["w16a16", "w8a16_pc", "w8a16_blk"])
+@pytest.mark.parametrize("M,K,N,ks", [(4096, 7168, 256, 8), (8192, 7168, 256, 4), (300, 4096, 512, 8),
+                                      (1000, 2048, 384, 4), (2000, 4096, 200, 8), (129, 7168, 256, 8)])
+def test_tiled_generic_k_split(dev, monkeypatch, kind, M, K, N, ks):
+    """The generic tiled kernel split over K (dense bf16 activations in
+    under 256 tiles of 128 x 128; each slice's f32 sums summed in
+    slice order by the finishing kernel, which applies the weight scale, bias
+    and row weight): the planned split, oracle rows to the same-codes bar, and
+    the unsplit kernel (QMOE_TILED_KSPLIT=1) with bias and row weights."""
+    from qmoe import _capi, ops
+
+    print(f"tiled generic K split {kind} M={M} K={K} N={N}", flush=True)
+    rng = np.random.default_rng(M + 3 * K + 7 * N)
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    x = _bf16(rng, (M, K))
+    bias = (rng.standard_normal(N) * 0.1).astype(np.float32)
+    r = np.unique(np.linspace(0, M - 1, 6).round().astype(np.int64))
+    if kind == "w16a16":
+        wb = codecs.bf16_round(w)
+        kc, wt, kw = _capi.W16A16, _t(wb, dev, torch.bfloat16), {}
+        ref = linear.w16a16(x[r], wb, bias=bias)
+    elif kind == "w8a16_pc":
+        wq, ws = quant.quantize_tensor(w, "fp8")
+        kc, wt, kw = _capi.W8A16_PC, _t(wq, dev), dict(w_scale=_t(ws, dev))
+        ref = linear.w8a16_per_channel(x[r], wq, ws)  # no bias term in this oracle
+    else:
+        wq, sblk = quant.quantize_tensor(w, "fp8", block=128)
+        kc, wt, kw = _capi.W8A16_BLK, _t(wq, dev), dict(w_scale=_t(sblk, dev), ws_bn=1)
+        ref = linear.w8a16_blockwise(x[r], wq, sblk, bias=bias)
+    xt, bt = _t(x, dev, torch.bfloat16), _t(bias, dev)
+    with ops.record_plans() as plans:
+        y = ops.gemm(kc, xt, wt, bias=None if kind == "w8a16_pc" else bt, **kw)
+    assert plans[0][4:] == ("tiled_generic", 128, ks), plans
+    assert_close_same_codes(y[torch.from_numpy(r).to(dev)].float().cpu().numpy(), ref, f"{kind} split M={M}")
+    rw = _t(rng.uniform(0.25, 2.0, M).astype(np.float32), dev, torch.bfloat16)
+    y2 = ops.gemm(kc, xt, wt, bias=bt, row_weight=rw, **kw)
+    monkeypatch.setenv("QMOE_TILED_KSPLIT", "1")
+    with ops.record_plans() as plans:
+        y1 = ops.gemm(kc, xt, wt, bias=bt, row_weight=rw, **kw)
+    assert plans[0][4:] == ("tiled_generic", 128, 1), plans
+    assert_close_same_codes(y2.float().cpu().numpy(), y1.float().cpu().numpy(), f"{kind} split vs one pass M={M}")
 
 
 def test_split_k_deterministic_and_reusable(dev):

@@ -14,8 +14,8 @@ int qmoe_skinny_launch(int kind, GemmParams p, int max_rows, int slots, void* wo
 int qmoe_skinny_check(int kind, const GemmParams& p);
 int qmoe_skinny_tile_rows(int max_rows);
 bool qmoe_skinny_qa_fits(int64_t M, int64_t K, int ksplit);
-int qmoe_tiled_launch(int kind, GemmParams p, hipStream_t st);
-int qmoe_tiled_check(int kind, const GemmParams& p, int* tile);
+int qmoe_tiled_launch(int kind, GemmParams p, void* workspace, int64_t ws_bytes, hipStream_t st);
+int qmoe_tiled_plan(int kind, const GemmParams& p, int* tile, int* ksplit, int64_t* ws_bytes);
 bool qmoe_f8_plan(const GemmParams& p, bool blk, int* bm_out, int* ksplit_out, int64_t* ws_bytes, int* bn_out);
 int qmoe_f8_launch(GemmParams p, bool blk, void* workspace, int64_t ws_bytes, hipStream_t st);
 int qmoe_mx_plan(const GemmParams& p);
@@ -346,9 +346,10 @@ int qmoe_route_of(const qmoe_gemm_desc* d, GemmParams& p, QmoeRoute* r) {
       return QMOE_OK;
     }
   }
-  int tile = 128;
-  if (qmoe_tiled_check(kind, p, &tile) == QMOE_OK) {
-    *r = QmoeRoute{kPathTiled, tile, 1, 0};
+  int tile = 128, tks = 1;
+  int64_t tws = 0;
+  if (qmoe_tiled_plan(kind, p, &tile, &tks, &tws) == QMOE_OK) {
+    *r = QmoeRoute{kPathTiled, tile, tks, tws};
     return QMOE_OK;
   }
   // bf16 activations with K % 64 == 32 (no tiled granule): the streaming
@@ -401,7 +402,7 @@ int qmoe_run_route(const qmoe_gemm_desc* d, const QmoeRoute& r, GemmParams p, vo
     case kPathF8Narrow:
     case kPathF8Persistent: return qmoe_f8_launch(p, kind == QK_W8A8_BLK, workspace, ws_bytes, stream);
     case kPathW4: return qmoe_w4_launch(p, w4_fmt(d), workspace, ws_bytes, stream);
-    case kPathTiled: return qmoe_tiled_launch(kind, p, stream);
+    case kPathTiled: return qmoe_tiled_launch(kind, p, workspace, ws_bytes, stream);
     case kPathMx:
     case kPathMxTiles: return qmoe_mx_launch(p, stream);
     default: {

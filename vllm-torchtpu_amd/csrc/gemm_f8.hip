@@ -1263,6 +1263,16 @@ bool qmoe_f8_plan(const GemmParams& p, bool blk, int* bm_out, int* ksplit_out, i
       bm = 128;
       bn = 128;
       ksplit = p.M <= 512 ? 2 : 1;
+    } else if (p.K < 8192 && p.M > 256 && n256 <= 4 && cdiv(p.M, 128) * cdiv(p.N, 128) <= 256) {
+      // at most 1024 channels (DeepSeek-V3's kv_a projection, 576): 64- or
+      // 128-token tiles of 128 rows, the larger once the smaller would make
+      // over 256 tiles. Measured on MI355X: K 7168, N 576, 512 / 1024 / 2048
+      // / 4096 tokens 26.3 / 25.3 / 26.6 / 48.4 -> 20.9 / 21.7 / 21.6 / 28.6
+      // us; N 512, 4096 / 8192 tokens 28.6 / 37.2 -> 24.1 / 34.2; K 4096,
+      // N 1024, 2048 / 4096 tokens 19.1 / 25.0 -> 15.3 / 23.6
+      bm = cdiv(p.M, 64) * cdiv(p.N, 128) <= 256 ? 64 : 128;
+      bn = 128;
+      ksplit = 1;
     }
   }
   // Dense wide block-scaled problems (the blk_wide rule above) take 128-row
@@ -1299,6 +1309,17 @@ bool qmoe_f8_persistent(const GemmParams& p, bool blk) {
   int64_t ws = 0;
   return qmoe_f8_plan(p, blk, &bm, &ksplit, &ws, &bn) && bn == 256 &&
          (f8_persistent_ok(p, blk, bm, ksplit) || f8_persistent_mid_ok(p, blk, bm, bn, ksplit));
+}
+
+// K-split finish of the generic tiled kernel's f32 partials (no fused
+// activation): the partials carry every scale, or all but the per-channel
+// weight scale (weight_scale: bf16 activations against e4m3 weights).
+int qmoe_tile_splitk_finish(const GemmParams& p, bool weight_scale, hipStream_t st) {
+  if (p.act != QA_NONE || p.ksplit < 2 || !p.partial) return QMOE_ERR_ARG;
+  const dim3 rg((unsigned)cdiv(p.N, 512), (unsigned)cdiv(p.M, 4), 1);
+  if (weight_scale) hipLaunchKernelGGL((tile_splitk_finish_kernel<false, false, kScWeight>), rg, dim3(kThreads), 0, st, p);
+  else hipLaunchKernelGGL((tile_splitk_finish_kernel<false, false, kScNone>), rg, dim3(kThreads), 0, st, p);
+  return hipGetLastError() == hipSuccess ? QMOE_OK : QMOE_ERR_LAUNCH;
 }
 
 // Launch per the plan (the caller checked qmoe_f8_plan and sized the

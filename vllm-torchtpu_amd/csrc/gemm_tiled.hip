@@ -260,7 +260,11 @@ __global__ __launch_bounds__(kThreads) void tiled_gemm_kernel(const GemmParams p
     w_row[i] = ok ? n : 0;
   }
 
-  const int KS = p.K / Tr::kKPerStage;
+  // K stages [ks0, ks1): all of them, or slice blockIdx.z of a K split
+  // (dense, no fused activation: the slices' f32 sums go to the partials)
+  const int ks_all = p.K / Tr::kKPerStage;
+  const int ks0 = (int)((int64_t)blockIdx.z * ks_all / gridDim.z);
+  const int ks1 = (int)((int64_t)(blockIdx.z + 1) * ks_all / gridDim.z);
 
   uint4 ra[A_CH];
   uint4 rw[W_CH];
@@ -367,15 +371,15 @@ __global__ __launch_bounds__(kThreads) void tiled_gemm_kernel(const GemmParams p
 #pragma unroll
     for (int j = 0; j < NF; ++j) acc[i][j] = AccT{0, 0, 0, 0};
 
-  if (KS > 0) {
-    gload(0);
-    sstore(0, 0);
+  if (ks1 > ks0) {
+    gload(ks0);
+    sstore(0, ks0);
   }
   __syncthreads();
 
-  for (int ks = 0; ks < KS; ++ks) {
-    const int buf = ks & 1;
-    if (ks + 1 < KS) gload(ks + 1);
+  for (int ks = ks0; ks < ks1; ++ks) {
+    const int buf = (ks - ks0) & 1;
+    if (ks + 1 < ks1) gload(ks + 1);
 
     const uint8_t* A = sA(buf);
     const uint8_t* Bt = sB(buf);
@@ -443,8 +447,28 @@ __global__ __launch_bounds__(kThreads) void tiled_gemm_kernel(const GemmParams p
     }
     // buf ^ 1 was last read in the previous stage, which every wavefront
     // finished before the previous barrier
-    if (ks + 1 < KS) sstore(buf ^ 1, ks + 1);
+    if (ks + 1 < ks1) sstore(buf ^ 1, ks + 1);
     __syncthreads();
+  }
+
+  if constexpr (!Tr::kInt && !ACT && BM == 128) {
+    if (gridDim.z > 1) {  // K split: this slice's sums, [slice][M][N] f32
+      float* dst = p.partial + (int64_t)blockIdx.z * p.M * p.N;
+#pragma unroll
+      for (int i = 0; i < MF; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int rr = wm * (BM / 2) + i * 16 + kg * 4 + r;
+          if (rr >= rows) continue;
+          float* drow = dst + (int64_t)(row0 + rr) * p.N;
+#pragma unroll
+          for (int j = 0; j < NF; ++j) {
+            const int n = n0 + wn * (BN / 2) + j * 16 + col;
+            if (n < nlim) drow[n] = acc[i][j][r];
+          }
+        }
+      return;
+    }
   }
 
   // ---- epilogue: finish in registers, stage bf16 in LDS, 16-byte stores ----
@@ -510,7 +534,7 @@ __global__ __launch_bounds__(kThreads) void tiled_gemm_kernel(const GemmParams p
 }
 
 template <int KIND, int WF, int BM, int BN, bool ACT>
-void launch_tiled(const GemmParams& p, hipStream_t st) {
+void launch_tiled(const GemmParams& p, int ksplit, hipStream_t st) {
   constexpr size_t smem = tiled_smem_bytes<BM, BN, ACT>();
   auto kern = tiled_gemm_kernel<KIND, WF, BM, BN, ACT>;
   static bool attr_set = false;  // once per instantiation (process-wide)
@@ -528,14 +552,15 @@ void launch_tiled(const GemmParams& p, hipStream_t st) {
     const int m_tiles = cdiv(p.M, BM);
     const int total = m_tiles * n_tiles;
     const int grid = cdiv(total, kXcds) * kXcds;
-    hipLaunchKernelGGL(kern, dim3(grid, 1, 1), dim3(kThreads), smem, st, p, m_tiles, n_tiles);
+    hipLaunchKernelGGL(kern, dim3(grid, 1, ksplit), dim3(kThreads), smem, st, p, m_tiles, n_tiles);
   }
 }
 
 template <int KIND, int WF, int BM, int BN>
-void launch_tiled_act(const GemmParams& p, hipStream_t st) {
-  if (p.act != QA_NONE) launch_tiled<KIND, WF, BM, BN, true>(p, st);
-  else launch_tiled<KIND, WF, BM, BN, false>(p, st);
+void launch_tiled_act(const GemmParams& p, int ksplit, hipStream_t st) {
+  // K splits: 128 x 128 tiles without a fused activation only
+  if (p.act != QA_NONE) launch_tiled<KIND, WF, BM, BN, true>(p, 1, st);
+  else launch_tiled<KIND, WF, BM, BN, false>(p, BM == 128 ? ksplit : 1, st);
 }
 
 // 256 x 256 tiles only for the kinds whose 128 x 128 wavefront tile fits the
@@ -547,23 +572,32 @@ constexpr bool has_big_tile() {
 }
 
 template <int KIND, int WF>
-void launch_shape(const GemmParams& p, bool big, hipStream_t st) {
+void launch_shape(const GemmParams& p, bool big, int ksplit, hipStream_t st) {
   if constexpr (has_big_tile<KIND>()) {
     if (big) {
-      launch_tiled_act<KIND, WF, 256, 256>(p, st);
+      launch_tiled_act<KIND, WF, 256, 256>(p, ksplit, st);
       return;
     }
   }
-  launch_tiled_act<KIND, WF, 128, 128>(p, st);
+  launch_tiled_act<KIND, WF, 128, 128>(p, ksplit, st);
 }
 
 }  // namespace
 
-// Tile shape: 256 x 256 when the problem has enough such tiles to fill the
-// GPU (>= 2 per CU), else 128 x 128.
-// Whether the generic tiled kernel takes the problem (QMOE_OK) and its
-// tile edge (128, or 256 with the QMOE_TILED_BIG knob).
-int qmoe_tiled_check(int kind, const GemmParams& p, int* tile) {
+// K-split finish for this kernel's partials (defined with the other tiled
+// kernels' finish): sums the slices in order, then the per-channel weight
+// scale (weight_scale), bias and routing weight, bf16 out.
+int qmoe_tile_splitk_finish(const GemmParams& p, bool weight_scale, hipStream_t st);
+
+// Whether the generic tiled kernel takes the problem (QMOE_OK) and its plan:
+// tile edge (128, or 256 with the QMOE_TILED_BIG knob), K split and the f32
+// workspace the split needs ([ksplit][M][N]). Dense bf16-activation problems
+// without a fused activation and under 256 tiles of 128 x 128 are split over
+// K into about 512 workgroups (at most 8 slices of at least 8 stages).
+// Measured on MI355X, DeepSeek-V3's router gate (K 7168, N 256): 128 / 1024
+// / 4096 / 8192 tokens 94.3 / 98.6 / 98.3 / 98.6 us in one pass, 22.2 / 23.9
+// / 35.0 / 49.8 in 8 / 8 / 8 / 4 slices.
+int qmoe_tiled_plan(int kind, const GemmParams& p, int* tile, int* ksplit, int64_t* ws_bytes) {
   const bool abf16 = kind == QK_W8A16_PC || kind == QK_W4A16_MX || kind == QK_W16A16 || kind == QK_W8A16_BLK;
   const int kstage = abf16 ? 64 : 128;
   if (kind != QK_W8A8_PC && kind != QK_W8A8_BLK && !abf16) return QMOE_ERR_ARG;
@@ -579,30 +613,50 @@ int qmoe_tiled_check(int kind, const GemmParams& p, int* tile) {
     const int m_tiles = cdiv(p.M, big ? 256 : 128) + std::min(p.slots, p.M);
     if (m_tiles > 65535) return QMOE_ERR_ARG;
   }
+  int ks = 1;
+  if (abf16 && !big && !p.group_offs && p.act == QA_NONE && p.M > 0) {
+    const int64_t tiles = (int64_t)cdiv(p.M, 128) * cdiv(p.N, 128);
+    if (tiles < 256) ks = (int)std::min<int64_t>(std::min<int64_t>(8, 512 / tiles), p.K / kstage / 8);
+    const char* ks_env = getenv("QMOE_TILED_KSPLIT");  // tuning knob
+    if (ks_env && atoi(ks_env) > 0) ks = std::min(atoi(ks_env), p.K / kstage);
+    ks = std::max(ks, 1);
+  }
   *tile = big ? 256 : 128;
+  if (ksplit) *ksplit = ks;
+  if (ws_bytes) *ws_bytes = ks > 1 ? (int64_t)ks * p.M * p.N * 4 : 0;
   return QMOE_OK;
 }
 
-int qmoe_tiled_launch(int kind, GemmParams p, hipStream_t st) {
+int qmoe_tiled_launch(int kind, GemmParams p, void* workspace, int64_t ws_bytes, hipStream_t st) {
   if (p.M <= 0) return QMOE_OK;
-  int tile = 128;
-  const int chk = qmoe_tiled_check(kind, p, &tile);
+  int tile = 128, ks = 1;
+  int64_t need = 0;
+  const int chk = qmoe_tiled_plan(kind, p, &tile, &ks, &need);
   if (chk != QMOE_OK) return chk;
+  p.ksplit = ks;
+  if (ks > 1) {
+    if (!workspace || ws_bytes < need) return QMOE_ERR_WORKSPACE;
+    p.partial = static_cast<float*>(workspace);
+  }
   const bool big = tile == 256;
   switch (kind) {
     case QK_W8A8_PC:
-      if (p.wfmt == 0) launch_shape<QK_W8A8_PC, 0>(p, big, st);
-      else launch_shape<QK_W8A8_PC, 1>(p, big, st);
+      if (p.wfmt == 0) launch_shape<QK_W8A8_PC, 0>(p, big, 1, st);
+      else launch_shape<QK_W8A8_PC, 1>(p, big, 1, st);
       break;
     case QK_W8A8_BLK:
-      if (p.wfmt == 0) launch_shape<QK_W8A8_BLK, 0>(p, big, st);
-      else launch_shape<QK_W8A8_BLK, 1>(p, big, st);
+      if (p.wfmt == 0) launch_shape<QK_W8A8_BLK, 0>(p, big, 1, st);
+      else launch_shape<QK_W8A8_BLK, 1>(p, big, 1, st);
       break;
-    case QK_W8A16_BLK: launch_shape<QK_W8A16_BLK, 0>(p, big, st); break;
-    case QK_W8A16_PC: launch_shape<QK_W8A16_PC, 0>(p, big, st); break;
-    case QK_W4A16_MX: launch_shape<QK_W4A16_MX, 0>(p, big, st); break;
-    case QK_W16A16: launch_shape<QK_W16A16, 0>(p, big, st); break;
+    case QK_W8A16_BLK: launch_shape<QK_W8A16_BLK, 0>(p, big, ks, st); break;
+    case QK_W8A16_PC: launch_shape<QK_W8A16_PC, 0>(p, big, ks, st); break;
+    case QK_W4A16_MX: launch_shape<QK_W4A16_MX, 0>(p, big, ks, st); break;
+    case QK_W16A16: launch_shape<QK_W16A16, 0>(p, big, ks, st); break;
     default: return QMOE_ERR_ARG;
+  }
+  if (ks > 1) {
+    const int fin = qmoe_tile_splitk_finish(p, kind == QK_W8A16_PC, st);
+    if (fin != QMOE_OK) return fin;
   }
   return hipGetLastError() == hipSuccess ? QMOE_OK : QMOE_ERR_LAUNCH;
 }
