@@ -78,7 +78,8 @@ def test_e5m2_runtime_boundaries(dev):
     np.testing.assert_array_equal(q.view(torch.uint8).cpu().numpy(), q_ref.view(np.uint8))
 
 
-@pytest.mark.parametrize("M,K", [(1, 4096), (7, 2048), (64, 7168), (3, 14336), (2, 40960)])
+@pytest.mark.parametrize("M,K", [(1, 4096), (7, 2048), (64, 7168), (3, 14336), (2, 40960), (600, 7168),
+                                 (300, 14336)])
 def test_e5m2_runtime_rows(dev, M, K):
     """Random rows across exponents, a zero row (scale 1), an outlier, and
     rows with inf / NaN (the software encoder's slow path): codes and scales

@@ -25,7 +25,9 @@ def _bf16(rng, shape, scale=1.0):
 @pytest.mark.parametrize("block", [None, 128])
 @pytest.mark.parametrize("M,K", [(1, 4096), (7, 2048), (64, 7168), (300, 1024),
                                  # decode rows on 1024 threads: held in registers, and streamed
-                                 (3, 14336), (2, 40960)])
+                                 (3, 14336), (2, 40960),
+                                 # prefill rows: held in registers up to 16384 columns, streamed beyond
+                                 (4096, 4096), (600, 7168), (1000, 14336), (257, 16384), (300, 20480)])
 def test_row_quant_runtime_bit_exact(dev, qdtype, block, M, K):
     if qdtype == "int8" and block is not None:
         pytest.skip("int8 activations are quantized per token only")
@@ -42,6 +44,34 @@ def test_row_quant_runtime_bit_exact(dev, qdtype, block, M, K):
     q, s = ops.row_quant(_t(x, dev, torch.bfloat16), qdtype, block=block)
     np.testing.assert_array_equal(q.view(torch.uint8).cpu().numpy(), q_ref.view(np.uint8))
     np.testing.assert_array_equal(s.cpu().numpy(), s_ref)
+
+
+@pytest.mark.parametrize("qdtype", ["fp8", "int8"])
+@pytest.mark.parametrize("M,K", [(600, 7168), (513, 14336)])
+def test_row_quant_prefill_rows_non_finite(dev, qdtype, M, K):
+    """Prefill rows with inf / NaN entries (and a row of zeros): the finite
+    rows' codes and scales bit-exact against the oracle, the others' scales
+    not finite (a row's inf or NaN does not leak into its neighbours)."""
+    from qmoe import ops
+
+    print(f"row_quant prefill rows non-finite {qdtype} M={M} K={K}", flush=True)
+    rng = np.random.default_rng(M + K)
+    x = _bf16(rng, (M, K), 2.0)
+    x[0, :] = 0.0
+    x[3, 17] = np.inf
+    x[5, K - 1] = -np.inf
+    x[7, 4000] = np.nan
+    x[M - 1, 9] = np.nan
+    x[M - 1, K - 9] = -np.inf
+    x = codecs.bf16_round(x)
+    fin = np.isfinite(x).all(axis=1)
+    assert fin.sum() == M - 4
+    q_ref, s_ref = quant.quantize_act(x[fin], qdtype)
+    q, s = ops.row_quant(_t(x, dev, torch.bfloat16), qdtype)
+    sc = s.cpu().numpy()
+    np.testing.assert_array_equal(sc[fin], s_ref)
+    np.testing.assert_array_equal(q.view(torch.uint8).cpu().numpy()[fin], q_ref.view(np.uint8))
+    assert not np.isfinite(sc[~fin]).any()
 
 
 @pytest.mark.parametrize("qdtype", ["fp8", "int8"])
