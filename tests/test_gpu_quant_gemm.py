@@ -294,6 +294,39 @@ def test_w8a8_persistent_tiles(dev, monkeypatch, M, K, N, qdtype, pbn):
         assert_close_same_codes(got, ref, f"fp8 persistent {M}x{K}x{N}")
 
 
+# output rows of a multiple of 32 KB with short K: the persistent tiles in
+# plain order (the in-flight stores then spread over the whole row width)
+@pytest.mark.parametrize("M,K,N", [(1024, 512, 16384), (600, 1024, 32768)])
+@pytest.mark.parametrize("qdtype", ["fp8", "int8"])
+def test_w8a8_persistent_wide_rows(dev, monkeypatch, M, K, N, qdtype):
+    """Plain tile order against the oracle (sampled rows: FP8 within one bf16
+    ulp of the same-code oracle, INT8 bit-exact) and bit-identical to the
+    XCD-run order (QMOE_F8_PERSIST_ORDER=0)."""
+    from qmoe import _capi, ops
+
+    wf = int(qdtype == "int8")
+    rng = np.random.default_rng(M + K + N + wf)
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    wq, ws = quant.quantize_tensor(w, qdtype)
+    x = _bf16(rng, (M, K))
+    xq, xs = ops.row_quant(_t(x, dev, torch.bfloat16), qdtype)
+    wt, wst = _t(wq.view(np.uint8), dev), _t(ws, dev)
+    with ops.record_plans() as plans:
+        y = ops.gemm(_capi.W8A8_PC, xq.view(torch.uint8), wt, a_scale=xs, w_scale=wst, wfmt=wf)
+    print(f"w8a8 persistent wide rows {qdtype} M={M} K={K} N={N} plan={plans[0]}", flush=True)
+    assert plans[0][4] == "tiled_1b_persistent", plans
+    monkeypatch.setenv("QMOE_F8_PERSIST_ORDER", "0")
+    y0 = ops.gemm(_capi.W8A8_PC, xq.view(torch.uint8), wt, a_scale=xs, w_scale=wst, wfmt=wf)
+    assert torch.equal(y.view(torch.int16), y0.view(torch.int16))
+    r = np.unique(np.linspace(0, M - 1, 6).round().astype(np.int64))
+    ref, _, _ = linear.w8a8_per_channel(x[r], wq, ws, qdtype)
+    got = y[torch.from_numpy(r).to(dev)].float().cpu().numpy()
+    if wf:
+        np.testing.assert_array_equal(got, ref)
+    else:
+        assert_close_same_codes(got, ref, f"persistent wide rows {M}x{K}x{N}")
+
+
 @pytest.mark.parametrize("seed", range(4))
 def test_w8a8_persistent_matches_one_tile(dev, monkeypatch, seed):
     """Seeded shapes of 300-5000 tokens, 1000-20000 output channels (N % 8 ==

@@ -667,7 +667,7 @@ __global__ __launch_bounds__(kThreads) void f8_gemm_kernel(const GemmParams p, i
 // projection make 224 such tiles, but 256 of 128 x 224).
 template <int MODE, int BN = 256, int BM = 256>
 __global__ __launch_bounds__(kThreads) void f8_persistent_kernel(const GemmParams p, int m_tiles, int n_tiles,
-                                                                 int tile_slots) {
+                                                                 int tile_slots, int wide) {
   constexpr bool INT = MODE == 1, MX = MODE == 2;
   constexpr bool ACT = false;  // fused activations take the one-tile kernel
   constexpr int KB = 128;
@@ -838,10 +838,14 @@ __global__ __launch_bounds__(kThreads) void f8_persistent_kernel(const GemmParam
   constexpr int NR = (MX ? 3 : 2) * (NI + MJ);
 
   // tiles of this workgroup: b = blockIdx.x + i * gridDim.x over the
-  // XCD-ordered slots [0, tile_slots)
+  // XCD-ordered slots [0, tile_slots), or in plain order (wide: rows of a
+  // multiple of 32 KB)
+  auto tile_of = [&](int bb, int& m, int& n) {
+    return wide ? tile_wide(bb, m_tiles, n_tiles, m, n) : tile_dense(bb, m_tiles, n_tiles, m, n);
+  };
   int b = blockIdx.x;
   int mt, nt;
-  if (!tile_dense(b, m_tiles, n_tiles, mt, nt)) return;
+  if (!tile_of(b, mt, nt)) return;
   Src cur;
   int row0 = mt * BM, rows = min(BM, p.M - row0), n0 = nt * BNO;
   make_src(row0, rows, n0, cur);
@@ -854,7 +858,7 @@ __global__ __launch_bounds__(kThreads) void f8_persistent_kernel(const GemmParam
     // the next tile (or none: the last copies then refetch this tile's last
     // stage into buffers that are never read again)
     int mt2 = 0, nt2 = 0;
-    const bool has_next = b + (int)gridDim.x < tile_slots && tile_dense(b + gridDim.x, m_tiles, n_tiles, mt2, nt2);
+    const bool has_next = b + (int)gridDim.x < tile_slots && tile_of(b + gridDim.x, mt2, nt2);
     const int row0n = mt2 * BM, rowsn = has_next ? min(BM, p.M - row0n) : 0, n0n = nt2 * BNO;
 
     // stage 0 has landed everywhere (prologue / end of the previous tile)
@@ -1075,12 +1079,22 @@ bool f8_persistent_mid_ok(const GemmParams& p, bool blk, int bm, int bn, int ksp
   return c_mid < c_cur && f8_persistent_grid(mid) > 0;
 }
 
+// Whether the persistent kernel walks its tiles in plain order (tile_wide):
+// output rows of a multiple of 32 KB and K up to 1024, where it was
+// measured (the QMOE_F8_PERSIST_ORDER knob forces 0: XCD runs, 1: plain
+// order).
+int f8_persistent_wide(const GemmParams& p) {
+  const char* env = getenv("QMOE_F8_PERSIST_ORDER");  // tuning knob
+  if (env && (atoi(env) == 0 || atoi(env) == 1)) return atoi(env);
+  return ((int64_t)p.ldy * 2) % 32768 == 0 && p.K <= 1024 ? 1 : 0;
+}
+
 // The persistent kernel in 128 x 224 tiles (f8_persistent_mid_ok holds).
 template <bool INT>
 void f8_launch_mid(const GemmParams& p, hipStream_t st) {
   const int mt = cdiv(p.M, 128), pn = cdiv(p.N, 224), tiles = mt * pn;
   hipLaunchKernelGGL((f8_persistent_kernel<INT ? 1 : 0, 224, 128>), dim3(f8_persistent_grid(tiles)), dim3(kThreads),
-                     0, st, p, mt, pn, cdiv(tiles, kXcds) * kXcds);
+                     0, st, p, mt, pn, cdiv(tiles, kXcds) * kXcds, f8_persistent_wide(p));
 }
 
 template <bool INT, int BM, int BN, bool ACT, bool BLK, bool WPC = false, int E5 = 0>
@@ -1102,12 +1116,13 @@ void f8_launch_shape(const GemmParams& p, hipStream_t st) {
       if (kb == 128 && f8_persistent_ok(p, BLK, BM, (int)ks)) {
         const int pbn = f8_persistent_bn(p);
         const int pn = cdiv(p.N, pbn), tiles = m_tiles * pn, slots = cdiv(tiles, kXcds) * kXcds;
+        const int wide = f8_persistent_wide(p);
         if (pbn == 224)
           hipLaunchKernelGGL((f8_persistent_kernel<INT ? 1 : 0, 224>), dim3(f8_persistent_grid(tiles)),
-                             dim3(kThreads), 0, st, p, m_tiles, pn, slots);
+                             dim3(kThreads), 0, st, p, m_tiles, pn, slots, wide);
         else
           hipLaunchKernelGGL((f8_persistent_kernel<INT ? 1 : 0>), dim3(f8_persistent_grid(tiles)), dim3(kThreads),
-                             0, st, p, m_tiles, pn, slots);
+                             0, st, p, m_tiles, pn, slots, wide);
         return;
       }
     }
@@ -1437,6 +1452,6 @@ int qmoe_mx_launch(GemmParams p, hipStream_t st) {
   const int rounds = cdiv(tiles, cus);
   const int grid = std::min(cus, cdiv(cdiv(tiles, rounds), kXcds) * kXcds);
   hipLaunchKernelGGL((f8_persistent_kernel<2>), dim3(grid), dim3(kThreads), 0, st, p, m_tiles, n_tiles,
-                     cdiv(tiles, kXcds) * kXcds);
+                     cdiv(tiles, kXcds) * kXcds, 0);
   return hipGetLastError() == hipSuccess ? QMOE_OK : QMOE_ERR_LAUNCH;
 }
