@@ -115,6 +115,13 @@ def test_dynamic_quant_kind_plans_on_the_host():
 
     for K, N in ((4096, 14336), (14336, 4096)):
         assert ops.plan_for_shape(_capi.W8A8_PC_DYN, 1, N, K)[4] == "stream_dyn"
+    # one row: one K slice (few weight tiles would otherwise split K); rows
+    # under 1024 columns quantize in a launch of their own
+    for K, N in ((7168, 1536), (7168, 576)):
+        assert ops.plan_for_shape(_capi.W8A8_PC_DYN, 1, N, K)[4:] == ("stream_dyn", 16, 1)
+        assert ops.plan_for_shape(_capi.W8A8_PC, 1, N, K)[6] > 1
+    assert ops.plan_for_shape(_capi.W8A8_PC_DYN, 1, 32768, 512)[4] == "stream"
+    for K, N in ((4096, 14336), (14336, 4096)):
         for M in (8, 64, 4096):
             assert ops.plan_for_shape(_capi.W8A8_PC_DYN, M, N, K)[4:] == ops.plan_for_shape(_capi.W8A8_PC, M, N, K)[4:]
     d = _capi.GemmDesc()

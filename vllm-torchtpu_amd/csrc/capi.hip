@@ -255,12 +255,22 @@ int64_t align256(int64_t b) { return (b + 255) / 256 * 256; }
 // (Llama-3-8B MLP shapes, FP8 and INT8) that pays for one row (up / down
 // projection 14.3 -> 12.8 us / 16.5 -> 15.4 us) and for two rows of K 4096
 // (15.0 -> 14.2 us), and loses for two rows of K 14336 and from four rows.
+// Short rows over many channels lose too: DeepSeek-V3's kv_b projection (K
+// 512, N 32768: 2048 workgroups each quantizing the row) 10.3 -> 8.3 us in
+// two launches, so K of at least 1024 is required.
 bool dyn_fused(const qmoe_gemm_desc* d, const GemmParams& p, int ksplit) {
   const char* env = getenv("QMOE_DYN_FUSE_ROWS");  // tuning knob: row limit
   const int lim = env ? std::min(atoi(env), 32) : (ksplit == 1 && d->K < 8192 ? 2 : 1);
-  return d->M <= lim && d->act == QMOE_ACT_NONE && (d->K % 128) == 0 &&
+  return d->M <= lim && d->act == QMOE_ACT_NONE && (d->K % 128) == 0 && d->K >= 1024 &&
          qmoe_skinny_check(QK_W8A8_PC, p) == QMOE_OK;
 }
+
+// K slices of the in-kernel form: one for a single row (measured on MI355X,
+// DeepSeek-V3's q_a / kv_a projections, K 7168, N 1536 / 576: the 2 / 5
+// slices the streaming planner picks for their few weight tiles, and the
+// finishing launch they need, 8.7 / 8.5 -> 7.6 / 7.5 us), else the
+// streaming planner's choice (0).
+int dyn_split_hint(const qmoe_gemm_desc* d) { return d->M == 1 ? 1 : 0; }
 
 // The two-step form of a QMOE_W8A8_PC_DYN problem: codes [M][K] and scales
 // [M] at the start of the workspace (qmoe_row_quant mode 0), then the
@@ -292,7 +302,7 @@ int qmoe_route_of(const qmoe_gemm_desc* d, GemmParams& p, QmoeRoute* r) {
   if (d->kind == QMOE_W8A8_PC_DYN) {
     int ks = 1;
     int64_t ws = 0;
-    qmoe_skinny_plan(QK_W8A8_PC, d->M, d->N, d->K, d->act, 1, d->M, 0, &ks, &ws);
+    qmoe_skinny_plan(QK_W8A8_PC, d->M, d->N, d->K, d->act, 1, d->M, dyn_split_hint(d), &ks, &ws);
     if (dyn_fused(d, p, ks)) {  // one launch; the row scales first in the workspace
       if (qmoe_skinny_qa_fits(d->M, d->K, ks)) {
         *r = QmoeRoute{kPathSkinnyDyn, qmoe_skinny_tile_rows(d->M), ks, ws + align256(4 * (int64_t)d->M)};
@@ -372,7 +382,7 @@ int qmoe_run_route(const qmoe_gemm_desc* d, const QmoeRoute& r, GemmParams p, vo
       p.a_quant = 1;
       p.a_scale = reinterpret_cast<const float*>(w8);
       p.lds_a = 1;
-      return qmoe_skinny_launch(QK_W8A8_PC, p, d->M, 1, w8 + sc, ws_bytes - sc, 0, stream);
+      return qmoe_skinny_launch(QK_W8A8_PC, p, d->M, 1, w8 + sc, ws_bytes - sc, dyn_split_hint(d), stream);
     }
     const qmoe_gemm_desc e = dyn_inner(d, w8);
     int st = qmoe_row_quant(d->a, d->lda, 0, d->M, d->K, d->wfmt, 0, 0, w8, d->K, const_cast<float*>(e.a_scale), 1,
