@@ -61,14 +61,15 @@ def parse():
                                                 "6 = the decoder layers' other linears; "
                                                 "v = hipBLASLt reference points)")
     ap.add_argument("--profile", nargs="?", const="headline", default=None,
-                    choices=["headline", "decode", "moe", "vendor", "floor", "w4", "mx", "midm", "moet"],
+                    choices=["headline", "decode", "moe", "vendor", "floor", "w4", "mx", "midm", "moet", "dec6"],
                     help="rocprofv3 targets: the headline kernel + a copy calibration (default), "
                          "the decode GEMMs (cfg 0/1/2 at M=1), the MoE layers at T=1 (cfg 3/4), "
                          "this build's FP8 GEMM beside hipBLASLt's (torch._scaled_mm) on both cfg 1 "
                          "shapes at M=4096, the plain-read floor (time vs size), the large-M MXFP4 "
                          "path (cfg 0 at M=8192, cfg 3 at T=8192), or the opt-in MX activation path "
                          "(cfg 0 at M=8192, cfg 3 at T=8192), the mid-M linears (cfg 0 M=128, cfg 1 "
-                         "M=64 / 512, cfg 2 M=256), or the cfg 4 MoE layers at T=512 / 4096")
+                         "M=64 / 512, cfg 2 M=256), the cfg 4 MoE layers at T=512 / 4096, or config "
+                         "6's linears at 4096 tokens")
     return ap.parse_args()
 
 
@@ -1282,6 +1283,50 @@ def profile_midm(args):
     log("profile target done")
 
 
+def profile_dec6(args):
+    """rocprofv3 target: config 6's linears at 4096 tokens, 13 launches each
+    after 3 warm-up calls -- DeepSeek-V3 q_a / kv_a / q_b / kv_b / o and
+    Llama-3-8B qkv / o through `quantized_matmul` (activation quant
+    included), and the bf16 router gate; then a plain 256 MiB copy (10
+    launches) for the FETCH_SIZE / WRITE_SIZE calibration."""
+    import torch
+
+    from qmoe import _capi, ops
+    from qmoe.layers.linear_common import quantized_matmul
+
+    gen = torch.Generator(device="cuda").manual_seed(6)
+    M = 4096
+    for name, N, K in (("dsv3_q_a", 1536, 7168), ("dsv3_kv_a", 576, 7168), ("dsv3_q_b", 24576, 1536),
+                       ("dsv3_kv_b", 32768, 512), ("dsv3_o", 7168, 16384), ("llama3_qkv", 6144, 4096),
+                       ("llama3_o", 4096, 4096)):
+        w, s = fp8_weights(N, K, gen)
+        x = torch.randn((M, K), device="cuda", generator=gen).to(torch.bfloat16)
+        for _ in range(3):
+            quantized_matmul(x, w.t(), s)
+        torch.cuda.synchronize()
+        log(f"profile target: {name} warm-up x3")
+        for _ in range(13):
+            quantized_matmul(x, w.t(), s)
+        torch.cuda.synchronize()
+        log(f"profile target: {name} M={M} K={K} N={N} x13")
+        del w, s, x
+    wg = (torch.randn((256, 7168), device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
+    x = torch.randn((M, 7168), device="cuda", generator=gen).to(torch.bfloat16)
+    for _ in range(3):
+        ops.gemm(_capi.W16A16, x, wg)
+    torch.cuda.synchronize()
+    for _ in range(13):
+        ops.gemm(_capi.W16A16, x, wg)
+    torch.cuda.synchronize()
+    log(f"profile target: bf16 router gate M={M} K=7168 N=256 x13 (after 3 warm-up)")
+    src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log("profile target done: copy 256MiB x10")
+
+
 def profile_moet(args):
     """rocprofv3 target: config 4 (DeepSeek-V3, 256 experts, top-8 grouped)
     routed MoE layers at T = 512 and 4096 -- 6 layers each with the native
@@ -1355,7 +1400,7 @@ def main():
     args = parse()
     if args.profile:
         {"headline": profile_target, "decode": profile_decode, "moe": profile_moe, "vendor": profile_vendor,
-         "floor": profile_floor, "w4": profile_w4, "mx": profile_mx, "midm": profile_midm,
+         "floor": profile_floor, "w4": profile_w4, "mx": profile_mx, "midm": profile_midm, "dec6": profile_dec6,
          "moet": profile_moet}[args.profile](args)
         return
     if args.gpus != 1:
