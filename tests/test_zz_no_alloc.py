@@ -67,6 +67,33 @@ def test_gemm_static_matches_gemm(dev, shapes, act):
         assert torch.equal(got, ref), f"call {i}: static-scratch output differs"
 
 
+def test_gemm_static_generic_k_split(dev):
+    """The generic tiled kernel's K split (bf16 activations x bf16 weights,
+    DeepSeek-V3's router gate shape) with its f32 slices in the static
+    scratch: identical to qmoe_gemm on two calls in a row, the second
+    smaller."""
+    from qmoe import _capi, ops
+
+    lib = _lib()
+    K, N = 7168, 256
+    rng = np.random.default_rng(7)
+    w = torch.from_numpy(codecs.bf16_round((rng.standard_normal((N, K)) * 0.02).astype(np.float32))).to(dev)
+    w = w.to(torch.bfloat16)
+    for M in (4096, 1000):
+        print(f"gemm_static generic K split M={M} K={K} N={N}", flush=True)
+        x = torch.from_numpy(codecs.bf16_round(rng.standard_normal((M, K)).astype(np.float32))).to(dev)
+        x = x.to(torch.bfloat16)
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+        d, out = ops.gemm_desc(_capi.W16A16, x, w, out=out)
+        plan = ops.plan_of_desc(d)
+        assert plan[4] == "tiled_generic" and plan[6] > 1, plan
+        st = lib.qmoe_gemm_static(ctypes.byref(d), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        assert st == 0, _capi.STATUS_TEXT.get(st, st)
+        ref = ops.gemm(_capi.W16A16, x, w)
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"M={M}: static-scratch output differs"
+
+
 def test_gemm_static_refuses_oversized_partials(dev):
     """A problem whose split-K partials exceed the scratch is refused before
     any launch (status QMOE_ERR_SCRATCH = 4)."""
