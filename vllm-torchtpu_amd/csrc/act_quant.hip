@@ -23,8 +23,9 @@
 // Granularity: one scale per row, or per (row, 128-column block); the
 // grouped-GEMM mode per (row, 512-column block).
 //
-// Launch: one 256-thread workgroup per row (per-row scale); thread t owns 8
-// consecutive columns per 2048-column stride, so a 128-column block is
+// Launch: one 256-thread workgroup per row (per-row scale; 128 threads for
+// many rows of 2049-8192 columns); thread t owns 8 consecutive columns per
+// 8 x (threads)-column stride, so a 128-column block is
 // exactly 16 adjacent lanes of one wavefront (reduced with shuffles, no LDS).
 // Per-block scales need no row-wide reduction, so a row's 2048-column spans
 // go to separate workgroups (grid.y): a decode row is quantized in one
@@ -293,6 +294,14 @@ void launch_rq(const void* x, int64_t ldx, int64_t M, int64_t K, uint8_t* q, int
   else if (!kBlock && M <= 64 && K > kThreads * 8)
     hipLaunchKernelGGL((row_quant_kernel<kQdt, kMode, kInF32, kBlock, 1024>), dim3((unsigned)M), dim3(1024), 0,
                        st, x, ldx, K, q, ldq, s, lds);
+  else if (!kBlock && M > 256 && K > 2048 && K <= 128 * 8 * 8)
+    // many rows of 2049-8192 columns: 128 threads per row, the row still held
+    // in registers (measured on MI355X, 4096 rows of 4096 / 7168 columns,
+    // FP8: 14.7 / 19.5 -> 12.6 / 18.6 us; 8192 rows of 4096: 24.5 -> 20.7 us;
+    // 512 threads and more are slower, and rows of 14336 columns, which 128
+    // threads would stream twice, stay on 256)
+    hipLaunchKernelGGL((row_quant_kernel<kQdt, kMode, kInF32, kBlock, 128>), dim3((unsigned)M), dim3(128), 0, st, x,
+                       ldx, K, q, ldq, s, lds);
   else
     hipLaunchKernelGGL((row_quant_kernel<kQdt, kMode, kInF32, kBlock, kThreads>), dim3((unsigned)M, spans),
                        dim3(kThreads), 0, st, x, ldx, K, q, ldq, s, lds);
