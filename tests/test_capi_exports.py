@@ -159,3 +159,33 @@ def test_weight_code_formats_are_validated_on_the_host():
         assert _capi.lib.qmoe_gemm_workspace_size(ctypes.byref(d), ctypes.byref(n)) == rc, wfmt
     d.kind, d.wfmt = _capi.W8A16_PC, 2
     assert _capi.lib.qmoe_gemm_workspace_size(ctypes.byref(d), ctypes.byref(n)) == 1
+
+
+def test_under_filled_prefill_plans_on_the_host():
+    """Prefill problems that one tile per workgroup would leave under-filled:
+    dense bf16-activation problems under 256 tiles of 128 x 128 split K into
+    about 512 workgroups (at most 8 slices of at least 8 stages), with the
+    f32 slices sized in the workspace; per-channel 1-byte problems of at
+    most 1024 channels over 256 tokens take 128-row weight tiles of 64 or
+    128 tokens (the larger once the smaller would make over 256 tiles)."""
+    from qmoe import _capi, ops
+
+    # DeepSeek-V3's bf16 router gate (K 7168, N 256)
+    for M, ks in ((65, 8), (4096, 8), (8192, 4), (16384, 1)):
+        assert ops.plan_for_shape(_capi.W16A16, M, 256, 7168)[4:] == ("tiled_generic", 128, ks), M
+    assert ops.plan_for_shape(_capi.W8A16_PC, 4096, 256, 7168)[4:] == ("tiled_generic", 128, 8)
+    # a short K keeps one slice; a fused activation never splits
+    assert ops.plan_for_shape(_capi.W16A16, 1000, 256, 512)[6] == 1
+    assert ops.plan_for_shape(_capi.W16A16, 4096, 512, 7168, activation="silu")[6] == 1
+    d = _capi.GemmDesc()
+    d.kind, d.a, d.w, d.y = _capi.W16A16, 1 << 24, 1 << 24, 1 << 24
+    d.lda, d.ldw, d.ldy = 7168, 2 * 7168, 256
+    d.M, d.N, d.K, d.slots, d.max_rows = 4096, 256, 7168, 1, 4096
+    n = ctypes.c_int64(0)
+    assert _capi.lib.qmoe_gemm_workspace_size(ctypes.byref(d), ctypes.byref(n)) == 0
+    assert n.value == 8 * 4096 * 256 * 4
+    # DeepSeek-V3's kv_a projection (576 channels) and a ragged 1000-channel problem
+    for wf in (0, 1):
+        assert ops.plan_for_shape(_capi.W8A8_PC, 2000, 576, 7168, wfmt=wf)[4:] == ("tiled_1b_n128", 64, 1)
+        assert ops.plan_for_shape(_capi.W8A8_PC, 4096, 576, 7168, wfmt=wf)[4:] == ("tiled_1b_n128", 128, 1)
+        assert ops.plan_for_shape(_capi.W8A8_PC, 4096, 1000, 4096, wfmt=wf)[4:] == ("tiled_1b_n128", 128, 1)
