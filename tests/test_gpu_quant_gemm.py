@@ -296,7 +296,9 @@ def test_w8a8_persistent_tiles(dev, monkeypatch, M, K, N, qdtype, pbn):
 
 # output rows of a multiple of 32 KB with short K: the persistent tiles in
 # plain order (the in-flight stores then spread over the whole row width)
-@pytest.mark.parametrize("M,K,N", [(1024, 512, 16384), (600, 1024, 32768)])
+@pytest.mark.parametrize("M,K,N", [(1024, 512, 16384), (600, 1024, 32768),
+                                   # 128 x 224 tiles (mid-size problem)
+                                   (300, 1024, 16384)])
 @pytest.mark.parametrize("qdtype", ["fp8", "int8"])
 def test_w8a8_persistent_wide_rows(dev, monkeypatch, M, K, N, qdtype):
     """Plain tile order against the oracle (sampled rows: FP8 within one bf16
